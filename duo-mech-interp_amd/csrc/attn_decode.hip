@@ -1,0 +1,274 @@
+// Gated GQA attention decode: one new query token per row over a bf16 KV cache, split-K over the context.
+//
+// Semantics (HF:656-698 with a cache, eager_attention_forward HF:604-626; WGSL engine/kernels_qwen35.js:73-123):
+//   q_h   <- partial RoPE at position cache_len[b] - 1 (pairs (i, i + rot/2) on the first rot dims, HF:554-589)
+//   o_h    = softmax(q_h . K^T * scale) V      over keys 0 .. cache_len[b]-1 of kv head h / (Hq / Hkv)
+//   out_h  = o_h * sigmoid(gate_h)             (HF:698)
+//
+// Pass 1 (attn_decode_partial_kernel): one block of 4 waves per (split, kv head, row). The G = Hq / Hkv query heads
+// that share a kv head are the M rows of one 16x16x32 MFMA tile, so each K row is read from HBM once for all G
+// heads. Each wave walks 16-key tiles of the block's span: scores via 8 MFMAs whose B operand is loaded straight
+// from the cache (16 contiguous bytes per lane), an online softmax on the 16 columns, then P.V on the vector ALU with
+// fully coalesced 16-byte V-row loads (32 lanes cover one 512-byte row). The four waves' (max, sum, acc) are merged
+// in LDS and written as one partial per (row, kv head, split).
+// Pass 2 (attn_decode_merge_kernel): log-sum-exp merge over splits, sigmoid gate, bf16 store.
+// HBM traffic is the K and V spans once (AI ~ 4 flop/byte): the kernel is bandwidth bound by design.
+#include "q35_common.h"
+#include "q35hip.h"
+
+namespace q35 {
+
+constexpr int kDecD = 256;  // head dim
+constexpr int kDecTile = 16;
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_decode_partial_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ kc, const __bf16* __restrict__ vc,
+    const int32_t* __restrict__ cache_len, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int rot,
+    float* __restrict__ part, int Hq, int Hkv, int max_len, int S, int L, float scale) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8, "heads per kv head");
+  constexpr int NG = (G + 3) / 4;  // lane groups of the MFMA D tile that hold real heads
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // cache_len lives on the device, so it is clamped here rather than trusted: 0 <= len <= max_len
+  const int len = min(max(cache_len[b], 0), max_len);
+  const int k_begin = s * L;
+  const int k_end = min(k_begin + L, len);
+  const int pos = max(len - 1, 0);
+
+  __shared__ float qf[G][kDecD];
+  __shared__ float pl[4][kDecTile][G];
+  __shared__ float comb_o[4][G][kDecD];
+  __shared__ float comb_ml[4][G][2];
+
+  // 1. the G query heads of this kv head, rotated at position pos, in fp32
+  const __bf16* qb = q + ((size_t)b * Hq + (size_t)kvh * G) * kDecD;
+  const int half = rot >> 1;
+  for (int i = tid; i < G * kDecD; i += 256) {
+    const int hh = i / kDecD, d = i % kDecD;
+    float x = (float)qb[hh * kDecD + d];
+    if (d < rot) {
+      const int j = d < half ? d : d - half;
+      const float c = cos_t[(size_t)pos * half + j], sn = sin_t[(size_t)pos * half + j];
+      const float pr = (float)qb[hh * kDecD + (d < half ? d + half : d - half)];
+      x = d < half ? x * c - pr * sn : x * c + pr * sn;
+    }
+    qf[hh][d] = x;
+  }
+  __syncthreads();
+
+  // 2. A operand: row = head (l % 16 < G), k = dims 32 ks + 8 (l / 16) + j
+  bf16x8 qa[8];
+  {
+    const int hr = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qa[ks][j] = (__bf16)(hr < G ? qf[hr][32 * ks + 8 * kg + j] : 0.f);
+  }
+
+  // 3. online softmax over this wave's tiles
+  const size_t kvbase = ((size_t)b * Hkv + kvh) * (size_t)max_len * kDecD;
+  const __bf16* kb = kc + kvbase;
+  const __bf16* vb = vc + kvbase;
+  float m_run[4], l_run[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) { m_run[r] = -INFINITY; l_run[r] = 0.f; }
+  float acc[G][8];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[hh][e] = 0.f;
+
+  const int kn = lane & 15, kg = lane >> 4;  // score-tile coordinates: key column, lane group
+  const int d0 = 8 * (lane & 31), kp = lane >> 5;  // PV coordinates: 8 dims, key parity
+  for (int key0 = k_begin + kDecTile * wave; key0 < k_end; key0 += 4 * kDecTile) {
+    // scores S[head][key] for 16 keys
+    const int key = key0 + kn;
+    const bool kvalid = key < k_end;
+    const __bf16* krow = kb + (size_t)(kvalid ? key : k_begin) * kDecD + 8 * kg;
+    f32x4 sc = zero4();
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const bf16x8 kv8 = *reinterpret_cast<const bf16x8*>(krow + 32 * ks);
+      sc = mfma16(qa[ks], kv8, sc);
+    }
+    // lane group kg holds heads 4 kg + r
+    float p[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = kvalid ? sc[r] * scale : -INFINITY;
+      float tm = x;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) tm = fmaxf(tm, __shfl_xor(tm, off, 64));
+      const float mn = fmaxf(m_run[r], tm);
+      const float corr = __expf(m_run[r] - mn);
+      p[r] = __expf(x - mn);
+      float ps = p[r];
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off, 64);
+      l_run[r] = l_run[r] * corr + ps;
+      m_run[r] = mn;
+      if (kg < NG && 4 * kg + r < G) pl[wave][kn][4 * kg + r] = p[r];
+      // stash corr in the score lane group's registers for the broadcast
+      sc[r] = corr;
+    }
+    __builtin_amdgcn_wave_barrier();
+    float corr_h[G];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+      corr_h[hh] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sc[hh & 3]), 16 * (hh >> 2)));
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[hh][e] *= corr_h[hh];
+    // P.V: lane takes keys key0 + 2 i + kp
+#pragma unroll
+    for (int i = 0; i < kDecTile / 2; ++i) {
+      const int n = 2 * i + kp;
+      const int vkey = key0 + n;
+      if (vkey < k_end) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(vb + (size_t)vkey * kDecD + d0);
+        float vv[8] = {bf16lo(raw.x), bf16hi(raw.x), bf16lo(raw.y), bf16hi(raw.y),
+                       bf16lo(raw.z), bf16hi(raw.z), bf16lo(raw.w), bf16hi(raw.w)};
+#pragma unroll
+        for (int hh = 0; hh < G; ++hh) {
+          const float ph = pl[wave][n][hh];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[hh][e] += ph * vv[e];
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // 4. fold the two key-parity halves, then merge the four waves in LDS
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[hh][e] += __shfl_xor(acc[hh][e], 32, 64);
+  if (lane < 32) {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) comb_o[wave][hh][d0 + e] = acc[hh][e];
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int hh = 4 * kg + r;
+    if (kn == 0 && kg < NG && hh < G) {
+      comb_ml[wave][hh][0] = m_run[r];
+      comb_ml[wave][hh][1] = l_run[r];
+    }
+  }
+  __syncthreads();
+  float* pb = part + (((size_t)b * Hkv + kvh) * S + s) * (size_t)G * (kDecD + 2);
+  for (int i = tid; i < G * kDecD; i += 256) {
+    const int hh = i / kDecD, d = i % kDecD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, comb_ml[w][hh][0]);
+    float Lsum = 0.f, O = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = __expf(comb_ml[w][hh][0] - M);
+        Lsum += comb_ml[w][hh][1] * f;
+        O += comb_o[w][hh][d] * f;
+      }
+    }
+    pb[(size_t)hh * (kDecD + 2) + d] = O;
+    if (d == 0) {
+      pb[(size_t)hh * (kDecD + 2) + kDecD] = M;
+      pb[(size_t)hh * (kDecD + 2) + kDecD + 1] = Lsum;
+    }
+  }
+}
+
+// Merge over splits, gate, store. One block per (query head, row), one thread per output dim.
+__global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __restrict__ part,
+                                                                const __bf16* __restrict__ gate,
+                                                                __bf16* __restrict__ out, int Hq, int Hkv, int S) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int G = Hq / Hkv, kvh = h / G, hh = h % G;
+  const float* pb = part + ((size_t)b * Hkv + kvh) * S * (size_t)G * (kDecD + 2) + (size_t)hh * (kDecD + 2);
+  const size_t sstride = (size_t)G * (kDecD + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < S; ++s) M = fmaxf(M, pb[s * sstride + kDecD]);
+  float Lsum = 0.f, O = 0.f;
+  if (M != -INFINITY) {
+    for (int s = 0; s < S; ++s) {
+      const float ms = pb[s * sstride + kDecD];
+      if (ms == -INFINITY) continue;
+      const float f = __expf(ms - M);
+      Lsum += pb[s * sstride + kDecD + 1] * f;
+      O += pb[s * sstride + d] * f;
+    }
+  }
+  const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + d;
+  const float res = Lsum > 0.f ? O / Lsum : 0.f;
+  out[oi] = (__bf16)(res * sigmoidf_((float)gate[oi]));
+}
+
+static int decode_splits(int64_t B, int64_t Hkv, int64_t max_len, int64_t splits, int* L_out) {
+  int64_t S = splits;
+  if (S <= 0) {
+    const int64_t target = 1024;  // blocks: about four per CU
+    S = (target + B * Hkv - 1) / (B * Hkv);
+  }
+  const int64_t max_s = (max_len + 63) / 64;
+  if (S > max_s) S = max_s;
+  if (S < 1) S = 1;
+  int64_t L = (max_len + S - 1) / S;
+  L = (L + 63) / 64 * 64;
+  S = (max_len + L - 1) / L;
+  *L_out = (int)L;
+  return (int)S;
+}
+
+}  // namespace q35
+
+extern "C" size_t q35_gated_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                                        int64_t max_len, int64_t splits) {
+  using namespace q35;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0) return 0;
+  int L;
+  const int S = decode_splits(B, Hkv, max_len, splits, &L);
+  return (size_t)B * Hq * S * (size_t)(D + 2) * sizeof(float);
+}
+
+extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* gate,
+                                     const int32_t* cache_len, const float* cos, const float* sin, void* out,
+                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
+                                     float scale, int64_t splits, void* workspace, size_t workspace_bytes,
+                                     q35_stream_t stream) {
+  using namespace q35;
+  if (!q || !k_cache || !v_cache || !gate || !cache_len || !out) return Q35_EINVAL;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D || (rot & 1))
+    return Q35_EINVAL;
+  if (rot > 0 && (!cos || !sin)) return Q35_EINVAL;
+  if (D != kDecD || B > 65535 || Hkv > 65535) return Q35_EUNSUPPORTED;
+  const int64_t G = Hq / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return Q35_EUNSUPPORTED;
+  int L;
+  const int S = decode_splits(B, Hkv, max_len, splits, &L);
+  const size_t need = q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits);
+  if (!workspace || workspace_bytes < need) return Q35_EWORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  float* part = (float*)workspace;
+  dim3 grid(S, (unsigned)Hkv, (unsigned)B), block(256);
+#define Q35_DEC_LAUNCH(GG)                                                                                     \
+  hipLaunchKernelGGL(attn_decode_partial_kernel<GG>, grid, block, 0, st, (const __bf16*)q,                     \
+                     (const __bf16*)k_cache, (const __bf16*)v_cache, cache_len, cos, sin, (int)rot, part, (int)Hq, \
+                     (int)Hkv, (int)max_len, S, L, scale)
+  switch (G) {
+    case 1: Q35_DEC_LAUNCH(1); break;
+    case 2: Q35_DEC_LAUNCH(2); break;
+    case 4: Q35_DEC_LAUNCH(4); break;
+    default: Q35_DEC_LAUNCH(8); break;
+  }
+#undef Q35_DEC_LAUNCH
+  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3((unsigned)Hq, (unsigned)B), dim3(kDecD), 0, st, part,
+                     (const __bf16*)gate, (__bf16*)out, (int)Hq, (int)Hkv, S);
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}

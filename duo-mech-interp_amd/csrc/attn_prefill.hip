@@ -1,0 +1,287 @@
+// Gated causal GQA attention prefill with partial RoPE and the sigmoid output gate fused (flash-style, MFMA bf16).
+//
+// Semantics (HF:656-698, eager_attention_forward HF:604-626, apply_rotary_pos_emb HF:554-589; WGSL
+// engine/kernels_qwen35.js:50-59 and :73-123):
+//   q, k  <- partial RoPE on dims [0, rot): x * cos + rotate_half(x) * sin, pairs (i, i + rot/2), position pos0 + t
+//   o_h    = softmax(q_h K^T * scale + causal mask) V     (fp32 softmax; kv head h / (Hq / Hkv))
+//   out    = o * sigmoid(gate)
+//
+// Decomposition: one block per (32-query block, group of up to 4 query heads sharing a kv head, batch row); wave w
+// of the block owns query head w of the group, so every K/V tile staged in LDS serves up to 4 heads. Query blocks
+// are issued longest (latest) first to shorten the causal tail.
+// Per 32-key tile each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (K from LDS, Q^T resident in
+// registers as the B operand), so a query's 16 scores sit in one lane (row max / sum need one cross-half exchange),
+// then O^T += V^T P^T where P^T's accumulator layout is used directly as the B operand (k permutation of the keys;
+// the V^T operand in LDS is read with the same permutation). K tiles are rotated while staged; V tiles are
+// transposed while staged (4 keys x 8 dims per thread). Two LDS stages, one barrier per tile.
+#include "q35_common.h"
+#include "q35hip.h"
+
+namespace q35 {
+
+constexpr int kPD = 256;            // head dim
+constexpr int kBQ = 32;             // queries per wave
+constexpr int kBK = 32;             // keys per tile
+constexpr int kKS = kPD + 8;        // K tile row stride (elements): 528 B, conflict-free 16-byte reads
+constexpr int kVS = kBK + 4;        // V^T row stride (elements): 72 B, conflict-free 8-byte reads
+
+template <int GW>
+__global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+    const __bf16* __restrict__ gate, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos0,
+    __bf16* __restrict__ out, int T, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb, int B) {
+  constexpr int NT = 64 * GW;
+  __shared__ __attribute__((aligned(16))) __bf16 ks_lds[2][kBK * kKS];
+  __shared__ __attribute__((aligned(16))) __bf16 vt_lds[2][kPD * kVS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n_other = B * Hkv * ngroups;
+  const int qb = nqb - 1 - (int)(blockIdx.x / n_other);
+  const int rem = blockIdx.x % n_other;
+  const int b = rem / (Hkv * ngroups);
+  const int kvh = (rem / ngroups) % Hkv;
+  const int hg = rem % ngroups;
+  const int G = Hq / Hkv;
+  const int h = kvh * G + hg * GW + wave;
+  const int q0 = qb * kBQ;
+  const int half = rot >> 1;
+
+  const int ln = lane & 31, hh = lane >> 5;
+
+  // ---- Q^T operand (B of S^T = K Q^T): lane holds query q0 + ln, dims 16 ks + 8 hh + j ----
+  bf16x8 qop[16];
+  {
+    const int t = q0 + ln;
+    const bool tv = t < T;
+    const __bf16* qrow = q + (((size_t)b * T + (tv ? t : 0)) * Hq + h) * kPD;
+    const int pos = pos0 + t;
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      const int d = 16 * ks + 8 * hh;
+      const uint4 raw = *reinterpret_cast<const uint4*>(qrow + d);
+      float x[8] = {bf16lo(raw.x), bf16hi(raw.x), bf16lo(raw.y), bf16hi(raw.y),
+                    bf16lo(raw.z), bf16hi(raw.z), bf16lo(raw.w), bf16hi(raw.w)};
+      if (tv && d < rot) {
+        const int pd = d < half ? d + half : d - half;
+        const uint4 pr = *reinterpret_cast<const uint4*>(qrow + pd);
+        const float y[8] = {bf16lo(pr.x), bf16hi(pr.x), bf16lo(pr.y), bf16hi(pr.y),
+                            bf16lo(pr.z), bf16hi(pr.z), bf16lo(pr.w), bf16hi(pr.w)};
+        const int j0 = d < half ? d : d - half;
+        const float sg = d < half ? -1.f : 1.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float c = cos_t[(size_t)pos * half + j0 + j], sn = sin_t[(size_t)pos * half + j0 + j];
+          x[j] = x[j] * c + sg * y[j] * sn;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qop[ks][j] = (__bf16)(tv ? x[j] : 0.f);
+    }
+  }
+
+  // ---- staging of one K/V tile: global -> registers -> (rotate / transpose) -> LDS ----
+  constexpr int KCH = kBK * (kPD / 8) / NT;  // 16-byte K chunks per thread
+  constexpr int VUN = (kBK / 4) * (kPD / 8) / NT;  // (4 keys x 8 dims) V units per thread
+  uint4 kreg[KCH], kpar[KCH], vreg[VUN][4];
+  const __bf16* kbase = k + ((size_t)b * T * Hkv + kvh) * kPD;  // + (key * Hkv) * kPD
+  const __bf16* vbase = v + ((size_t)b * T * Hkv + kvh) * kPD;
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + i * NT, row = c >> 5, cc = c & 31;
+      const int key = kt * kBK + row;
+      uint4 z = {0u, 0u, 0u, 0u};
+      kreg[i] = z;
+      kpar[i] = z;
+      if (key < T) {
+        const __bf16* kr = kbase + (size_t)key * Hkv * kPD;
+        kreg[i] = *reinterpret_cast<const uint4*>(kr + 8 * cc);
+        if (8 * cc < rot) {
+          const int pd = 8 * cc < half ? 8 * cc + half : 8 * cc - half;
+          kpar[i] = *reinterpret_cast<const uint4*>(kr + pd);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VUN; ++i) {
+      const int u = tid + i * NT, dc = u >> 3, kq = u & 7;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kt * kBK + 4 * kq + r;
+        uint4 z = {0u, 0u, 0u, 0u};
+        vreg[i][r] = key < T ? *reinterpret_cast<const uint4*>(vbase + (size_t)key * Hkv * kPD + 8 * dc) : z;
+      }
+    }
+  };
+  auto store_tile = [&](int kt, int buf) {
+    __bf16* kl = ks_lds[buf];
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + i * NT, row = c >> 5, cc = c & 31;
+      uint4 w = kreg[i];
+      const int d = 8 * cc;
+      if (d < rot && kt * kBK + row < T) {
+        const int pos = pos0 + kt * kBK + row;
+        const int j0 = d < half ? d : d - half;
+        const float sg = d < half ? -1.f : 1.f;
+        const uint4 p = kpar[i];
+        float x[8] = {bf16lo(w.x), bf16hi(w.x), bf16lo(w.y), bf16hi(w.y),
+                      bf16lo(w.z), bf16hi(w.z), bf16lo(w.w), bf16hi(w.w)};
+        const float y[8] = {bf16lo(p.x), bf16hi(p.x), bf16lo(p.y), bf16hi(p.y),
+                            bf16lo(p.z), bf16hi(p.z), bf16lo(p.w), bf16hi(p.w)};
+        bf16x8 o8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float c0 = cos_t[(size_t)pos * half + j0 + j], s0 = sin_t[(size_t)pos * half + j0 + j];
+          o8[j] = (__bf16)(x[j] * c0 + sg * y[j] * s0);
+        }
+        w = *reinterpret_cast<const uint4*>(&o8);
+      }
+      *reinterpret_cast<uint4*>(kl + row * kKS + 8 * cc) = w;
+    }
+    __bf16* vl = vt_lds[buf];
+#pragma unroll
+    for (int i = 0; i < VUN; ++i) {
+      const int u = tid + i * NT, dc = u >> 3, kq = u & 7;
+      // transpose 4 keys x 8 dims -> 8 dims x 4 keys
+      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&vreg[i][0]);
+      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&vreg[i][1]);
+      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&vreg[i][2]);
+      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&vreg[i][3]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int wi = e >> 1, sh = (e & 1) * 16;
+        const uint32_t a0 = (w0[wi] >> sh) & 0xffffu, a1 = (w1[wi] >> sh) & 0xffffu;
+        const uint32_t a2 = (w2[wi] >> sh) & 0xffffu, a3 = (w3[wi] >> sh) & 0xffffu;
+        uint2 pk;
+        pk.x = a0 | (a1 << 16);
+        pk.y = a2 | (a3 << 16);
+        *reinterpret_cast<uint2*>(vl + (8 * dc + e) * kVS + 4 * kq) = pk;
+      }
+    }
+  };
+
+  const int nkt_all = (T + kBK - 1) / kBK;
+  const int nkt = min(nkt_all, (q0 + kBQ - 1) / kBK + 1);
+
+  f32x16 o[8];
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) o[mt] = zero16();
+  float m_run = -INFINITY, l_run = 0.f;
+  const int tq = q0 + ln;  // this lane's query
+
+  load_tile(0);
+  store_tile(0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nkt) load_tile(kt + 1);
+    // S^T = K Q^T: rows = 32 keys, cols = 32 queries
+    const __bf16* kl = ks_lds[buf];
+    f32x16 s = zero16();
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(kl + ln * kKS + 16 * ks + 8 * hh);
+      s = mfma32(a, qop[ks], s);
+    }
+    // online softmax along the keys of this lane's query
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kt * kBK + 8 * (r >> 2) + 4 * hh + (r & 3);
+      const float x = (key <= tq && key < T) ? s[r] * scale : -INFINITY;
+      s[r] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m_run, mx);
+    const float corr = __expf(m_run - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = __expf(s[r] - mn);
+      ps += s[r];
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    l_run = l_run * corr + ps;
+    m_run = mn;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[mt][r] *= corr;
+    bf16x8 pb[2];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      pb[0][j] = (__bf16)s[j];
+      pb[1][j] = (__bf16)s[8 + j];
+    }
+    // O^T += V^T P^T: rows = 256 dims (8 tiles), k = 32 keys (2 steps)
+    const __bf16* vl = vt_lds[buf];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const __bf16* vr = vl + (32 * mt + ln) * kVS + 16 * kk + 4 * hh;
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
+        uint4 w;
+        w.x = lo.x; w.y = lo.y; w.z = hi.x; w.w = hi.y;
+        o[mt] = mfma32(*reinterpret_cast<const bf16x8*>(&w), pb[kk], o[mt]);
+      }
+    }
+    if (kt + 1 < nkt) store_tile(kt + 1, buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: normalise, gate, store ----
+  if (tq < T) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    const size_t rowo = ((size_t)b * T + tq) * (size_t)Hq * kPD + (size_t)h * kPD;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int d = 32 * mt + 8 * c + 4 * hh;
+        const uint2 gr = *reinterpret_cast<const uint2*>(gate + rowo + d);
+        const float gv[4] = {bf16lo(gr.x), bf16hi(gr.x), bf16lo(gr.y), bf16hi(gr.y)};
+        bf16x4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = (__bf16)(o[mt][4 * c + e] * inv * sigmoidf_(gv[e]));
+        *reinterpret_cast<bf16x4*>(out + rowo + d) = ov;
+      }
+    }
+  }
+}
+
+}  // namespace q35
+
+extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const void* gate,
+                                      const float* cos, const float* sin, int64_t pos0, void* out, int64_t B,
+                                      int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t rot, float scale,
+                                      q35_stream_t stream) {
+  using namespace q35;
+  if (!q || !k || !v || !gate || !out) return Q35_EINVAL;
+  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D || pos0 < 0)
+    return Q35_EINVAL;
+  if (rot > 0 && (!cos || !sin)) return Q35_EINVAL;
+  if (D != kPD || (rot % 16) != 0) return Q35_EUNSUPPORTED;
+  const int64_t G = Hq / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return Q35_EUNSUPPORTED;
+  const int GW = G > 4 ? 4 : (int)G;
+  const int ngroups = (int)(G / GW);
+  const int64_t nqb = (T + kBQ - 1) / kBQ;
+  const int64_t nblocks = nqb * B * Hkv * ngroups;
+  if (nblocks > 0x7fffffff || T * Hq * D > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define Q35_PF_LAUNCH(GG)                                                                                      \
+  hipLaunchKernelGGL(attn_prefill_kernel<GG>, dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q, \
+                     (const __bf16*)k, (const __bf16*)v, (const __bf16*)gate, cos, sin, (int)pos0, (__bf16*)out,  \
+                     (int)T, (int)Hq, (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B)
+  switch (GW) {
+    case 1: Q35_PF_LAUNCH(1); break;
+    case 2: Q35_PF_LAUNCH(2); break;
+    default: Q35_PF_LAUNCH(4); break;
+  }
+#undef Q35_PF_LAUNCH
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}

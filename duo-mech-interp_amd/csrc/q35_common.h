@@ -1,0 +1,70 @@
+// Shared device helpers for the Qwen3.5 hybrid-attention kernels (gfx950 / CDNA4, wave64).
+//
+// MFMA operand layouts used throughout (v_mfma_f32_16x16x32_bf16 and v_mfma_f32_32x32x16_bf16, gfx950):
+//   16x16x32:  A[16x32]  lane l holds row l%16, k = 8*(l/16) + j (j = 0..7)
+//              B[32x16]  lane l holds col l%16, k = 8*(l/16) + j
+//              D[16x16]  lane l holds col l%16, rows 4*(l/16) + r (r = 0..3)
+//   32x32x16:  A[32x16]  lane l holds row l%32, k = 8*(l/32) + j
+//              B[16x32]  lane l holds col l%32, k = 8*(l/32) + j
+//              D[32x32]  lane l holds col l%32, rows 8*(r/4) + 4*(l/32) + r%4 (r = 0..15)
+// A sum over k does not depend on the order of k, so a kernel may feed any fixed permutation of the k index as long
+// as the A and B operands of one instruction use the same one. The kernels use this to feed accumulator tiles
+// (D layout) straight back in as B operands without a trip through LDS.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+
+namespace q35 {
+
+// Element types the kernels accept for activations (q, k, v, o, gate).
+enum DType : int { kF32 = 0, kBF16 = 1 };
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
+
+// bf16 bit patterns -> fp32 (exact).
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Pack two 4-row accumulator fragments into one 8-element bf16 operand (k permutation described above).
+__device__ __forceinline__ bf16x8 pack8(const f32x4& lo, const f32x4& hi) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { r[i] = (__bf16)lo[i]; r[4 + i] = (__bf16)hi[i]; }
+  return r;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+
+// Sum / max over the 64 lanes of a wave (butterfly; every lane ends with the result).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace q35

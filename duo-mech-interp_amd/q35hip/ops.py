@@ -1,0 +1,255 @@
+"""torch.library registration (namespace q35) of the HIP kernels, plus Python entry points whose signatures follow the
+reference's replaceable functions.
+
+Reference interfaces mirrored (HF: transformers 5.15.0 models/qwen3_5/modeling_qwen3_5.py, run by the reference's
+tests/engine_ref.py):
+  chunk_gated_delta_rule      <- torch_chunk_gated_delta_rule (HF:248-327, hub-kernel name "chunk_gated_delta_rule")
+  recurrent_gated_delta_rule  <- torch_recurrent_gated_delta_rule (HF:330-380, "recurrent_gated_delta_rule")
+  gated_attention_prefill     <- apply_rotary_pos_emb + eager_attention_forward + sigmoid gate (HF:656-698)
+  gated_attention_decode      <- the same for one token over a KV cache (WGSL engine/kernels_qwen35.js:73-123)
+  residual_steer_add_         <- layers[12] forward hook (tests/engine_ref.py:49-53), WGSL resAdd
+                                 (engine/kernels.js:190-203)
+Every op runs on the current HIP stream of its inputs' device; inputs are validated here (device, dtype, layout,
+shape) and a bad call raises RuntimeError. CPU tensors raise: there is no CPU path in the product.
+"""
+import math
+
+import torch
+
+from . import _lib
+from ._lib import Q35_BF16, Q35_F32, Q35Error, check
+
+_DT = {torch.float32: Q35_F32, torch.bfloat16: Q35_BF16}
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require(cond, msg):
+    if not cond:
+        raise Q35Error("q35hip: " + msg)
+
+
+def _on_gpu(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        _require(t.is_cuda, "inputs must be HIP device tensors (there is no CPU fallback)")
+        _require(t.is_contiguous(), "inputs must be contiguous")
+        dev = t.device if dev is None else dev
+        _require(t.device == dev, "inputs must be on one device")
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------- schema
+_LIB = torch.library.Library("q35", "DEF")
+_LIB.define("gdn_recurrent(Tensor q, Tensor k, Tensor v, Tensor g, Tensor beta, Tensor? initial_state, "
+            "float scale, bool use_qk_l2norm) -> (Tensor, Tensor)")
+_LIB.define("gdn_decode_step_(Tensor q, Tensor k, Tensor v, Tensor g, Tensor beta, Tensor(a!) state, "
+            "float scale, bool use_qk_l2norm) -> Tensor")
+_LIB.define("gdn_chunk_prefill(Tensor q, Tensor k, Tensor v, Tensor g, Tensor beta, Tensor? initial_state, "
+            "int chunk_size, float scale, bool use_qk_l2norm) -> (Tensor, Tensor)")
+_LIB.define("gated_attn_prefill(Tensor q, Tensor k, Tensor v, Tensor gate, Tensor cos, Tensor sin, int pos0, "
+            "float scale) -> Tensor")
+_LIB.define("gated_attn_decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor gate, Tensor cache_len, "
+            "Tensor cos, Tensor sin, float scale, int splits) -> Tensor")
+_LIB.define("resid_add_rows_(Tensor(a!) x, Tensor vecs, Tensor? vec_of_row) -> ()")
+
+
+# ---------------------------------------------------------------- gated delta rule
+def _gdn_check(q, k, v, g, beta, state):
+    _on_gpu(q, k, v, g, beta, state)
+    _require(q.dtype in _DT and k.dtype == q.dtype and v.dtype == q.dtype, "q, k, v must share dtype fp32 or bf16")
+    _require(g.dtype == torch.float32 and beta.dtype == torch.float32, "g and beta must be fp32")
+    _require(q.dim() == 4 and k.shape == q.shape and v.dim() == 4, "q, k: [B, T, Hk, Dk]; v: [B, T, H, Dv]")
+    B, T, Hk, Dk = q.shape
+    H, Dv = v.shape[2], v.shape[3]
+    _require(v.shape[0] == B and v.shape[1] == T, "v must match q in batch and time")
+    _require(H % Hk == 0, "value heads must be a multiple of q/k heads")
+    _require(tuple(g.shape) == (B, T, H) and tuple(beta.shape) == (B, T, H), "g, beta: [B, T, H]")
+    if state is not None:
+        _require(state.dtype == torch.float32 and tuple(state.shape) == (B, H, Dk, Dv), "state: [B, H, Dk, Dv] fp32")
+    return B, T, Hk, H, Dk, Dv
+
+
+def _gdn_recurrent_impl(q, k, v, g, beta, initial_state, scale, use_qk_l2norm):
+    B, T, Hk, H, Dk, Dv = _gdn_check(q, k, v, g, beta, initial_state)
+    o = torch.empty_like(v)
+    S = torch.empty(B, H, Dk, Dv, dtype=torch.float32, device=q.device)
+    st = _lib.lib().q35_gdn_recurrent(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(initial_state), _ptr(S),
+                                      _ptr(o), B, T, Hk, H, Dk, Dv, _DT[q.dtype], float(scale), int(use_qk_l2norm),
+                                      _stream(q))
+    check(st, "q35_gdn_recurrent")
+    return o, S
+
+
+def _gdn_decode_step_impl(q, k, v, g, beta, state, scale, use_qk_l2norm):
+    B, T, Hk, H, Dk, Dv = _gdn_check(q, k, v, g, beta, state)
+    o = torch.empty_like(v)
+    st = _lib.lib().q35_gdn_recurrent(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(state), _ptr(state),
+                                      _ptr(o), B, T, Hk, H, Dk, Dv, _DT[q.dtype], float(scale), int(use_qk_l2norm),
+                                      _stream(q))
+    check(st, "q35_gdn_recurrent")
+    return o
+
+
+def _gdn_chunk_impl(q, k, v, g, beta, initial_state, chunk_size, scale, use_qk_l2norm):
+    B, T, Hk, H, Dk, Dv = _gdn_check(q, k, v, g, beta, initial_state)
+    L = _lib.lib()
+    nbytes = L.q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, chunk_size)
+    _require(nbytes > 0, f"unsupported chunk prefill shape (Dk={Dk}, Dv={Dv}, chunk={chunk_size})")
+    ws = _workspace(nbytes, q.device)
+    o = torch.empty_like(v)
+    S = torch.empty(B, H, Dk, Dv, dtype=torch.float32, device=q.device)
+    st = L.q35_gdn_chunk_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(initial_state), _ptr(S),
+                                 _ptr(o), B, T, Hk, H, Dk, Dv, _DT[q.dtype], float(scale), int(use_qk_l2norm),
+                                 chunk_size, _ptr(ws), ws.numel(), _stream(q))
+    check(st, "q35_gdn_chunk_prefill")
+    return o, S
+
+
+# ---------------------------------------------------------------- gated attention
+def _tables_check(cos, sin, rows_needed):
+    _require(cos.dtype == torch.float32 and sin.dtype == torch.float32, "cos/sin tables must be fp32")
+    _require(cos.dim() == 2 and sin.shape == cos.shape, "cos/sin tables: [P, rot/2]")
+    _require(cos.shape[0] >= rows_needed or cos.shape[1] == 0, f"cos/sin tables need {rows_needed} rows")
+    return 2 * cos.shape[1]
+
+
+def _attn_prefill_impl(q, k, v, gate, cos, sin, pos0, scale):
+    _on_gpu(q, k, v, gate, cos, sin)
+    _require(q.dtype == torch.bfloat16 and k.dtype == q.dtype and v.dtype == q.dtype and gate.dtype == q.dtype,
+             "q, k, v, gate must be bf16")
+    _require(q.dim() == 4 and k.dim() == 4 and v.shape == k.shape, "q: [B, T, Hq, D]; k, v: [B, T, Hkv, D]")
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    _require(k.shape[0] == B and k.shape[1] == T and k.shape[3] == D, "k/v must match q in batch, time, head dim")
+    _require(tuple(gate.shape) == (B, T, Hq * D), "gate: [B, T, Hq * D]")
+    rot = _tables_check(cos, sin, pos0 + T)
+    out = torch.empty(B, T, Hq * D, dtype=q.dtype, device=q.device)
+    st = _lib.lib().q35_gated_attn_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(cos), _ptr(sin), int(pos0),
+                                           _ptr(out), B, T, Hq, Hkv, D, rot, float(scale), _stream(q))
+    check(st, "q35_gated_attn_prefill")
+    return out
+
+
+def _attn_decode_impl(q, k_cache, v_cache, gate, cache_len, cos, sin, scale, splits):
+    _on_gpu(q, k_cache, v_cache, gate, cache_len, cos, sin)
+    _require(q.dtype == torch.bfloat16 and k_cache.dtype == q.dtype and v_cache.dtype == q.dtype
+             and gate.dtype == q.dtype, "q, caches, gate must be bf16")
+    _require(cache_len.dtype == torch.int32, "cache_len must be int32")
+    _require(q.dim() == 3 and k_cache.dim() == 4 and v_cache.shape == k_cache.shape,
+             "q: [B, Hq, D]; caches: [B, Hkv, max_len, D]")
+    B, Hq, D = q.shape
+    Hkv, max_len = k_cache.shape[1], k_cache.shape[2]
+    _require(k_cache.shape[0] == B and k_cache.shape[3] == D, "caches must match q in batch and head dim")
+    _require(tuple(gate.shape) == (B, Hq * D) and tuple(cache_len.shape) == (B,), "gate: [B, Hq*D]; cache_len: [B]")
+    rot = _tables_check(cos, sin, max_len)
+    L = _lib.lib()
+    nbytes = L.q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits)
+    ws = _workspace(nbytes, q.device)
+    out = torch.empty(B, Hq * D, dtype=q.dtype, device=q.device)
+    st = L.q35_gated_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(gate), _ptr(cache_len), _ptr(cos),
+                                 _ptr(sin), _ptr(out), B, Hq, Hkv, D, max_len, rot, float(scale), int(splits),
+                                 _ptr(ws), ws.numel(), _stream(q))
+    check(st, "q35_gated_attn_decode")
+    return out
+
+
+def _resid_add_impl(x, vecs, vec_of_row):
+    _on_gpu(x, vecs, vec_of_row)
+    _require(x.dtype in _DT and vecs.dtype == torch.float32, "x fp32/bf16, vecs fp32")
+    _require(x.dim() == 3 and vecs.dim() == 2 and vecs.shape[1] == x.shape[2], "x: [rows, T, H]; vecs: [nvec, H]")
+    if vec_of_row is not None:
+        _require(vec_of_row.dtype == torch.int32 and tuple(vec_of_row.shape) == (x.shape[0],),
+                 "vec_of_row: [rows] int32")
+    rows, T, H = x.shape
+    st = _lib.lib().q35_resid_add_rows(_ptr(x), _ptr(vecs), _ptr(vec_of_row), rows, T, H, vecs.shape[0],
+                                       _DT[x.dtype], _stream(x))
+    check(st, "q35_resid_add_rows")
+
+
+def _no_cpu(name):
+    def f(*args, **kwargs):
+        raise Q35Error(f"q35hip: q35::{name} needs HIP device tensors; the product has no CPU path")
+    return f
+
+
+for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_", _gdn_decode_step_impl),
+                     ("gdn_chunk_prefill", _gdn_chunk_impl), ("gated_attn_prefill", _attn_prefill_impl),
+                     ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl)]:
+    _LIB.impl(_name, _impl, "CUDA")
+    _LIB.impl(_name, _no_cpu(_name), "CPU")
+
+
+# Meta (shape-only) kernels
+def _meta_gdn(q, k, v, g, beta, initial_state, *rest):
+    B, T, Hk, Dk = q.shape
+    H, Dv = v.shape[2], v.shape[3]
+    return torch.empty_like(v), v.new_empty(B, H, Dk, Dv, dtype=torch.float32)
+
+
+_LIB.impl("gdn_recurrent", _meta_gdn, "Meta")
+_LIB.impl("gdn_chunk_prefill", _meta_gdn, "Meta")
+_LIB.impl("gdn_decode_step_", lambda q, k, v, g, beta, state, scale, l2: torch.empty_like(v), "Meta")
+_LIB.impl("gated_attn_prefill",
+          lambda q, k, v, gate, cos, sin, pos0, scale: q.new_empty(q.shape[0], q.shape[1], q.shape[2] * q.shape[3]),
+          "Meta")
+_LIB.impl("gated_attn_decode",
+          lambda q, kc, vc, gate, cl, cos, sin, scale, splits: q.new_empty(q.shape[0], q.shape[1] * q.shape[2]),
+          "Meta")
+_LIB.impl("resid_add_rows_", lambda x, vecs, vor: None, "Meta")
+
+
+# ---------------------------------------------------------------- Python entry points (reference signatures)
+def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, output_final_state=False,
+                               use_qk_l2norm_in_kernel=False, scale=None, **kwargs):
+    """Drop-in for torch_recurrent_gated_delta_rule (HF:331-380): [B, T, H, D] layouts, returns
+    (o in the input dtype, final fp32 state or None)."""
+    scale = 1.0 / math.sqrt(key.shape[-1]) if scale is None else scale
+    o, S = torch.ops.q35.gdn_recurrent(query, key, value, g.float().contiguous(), beta.float().contiguous(),
+                                       initial_state, scale, bool(use_qk_l2norm_in_kernel))
+    return o, (S if output_final_state else None)
+
+
+def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_state=None, output_final_state=False,
+                           use_qk_l2norm_in_kernel=False, scale=None, **kwargs):
+    """Drop-in for torch_chunk_gated_delta_rule (HF:249-327); chunk_size must be 64."""
+    scale = 1.0 / math.sqrt(key.shape[-1]) if scale is None else scale
+    o, S = torch.ops.q35.gdn_chunk_prefill(query, key, value, g.float().contiguous(), beta.float().contiguous(),
+                                           initial_state, int(chunk_size), scale, bool(use_qk_l2norm_in_kernel))
+    return o, (S if output_final_state else None)
+
+
+def gdn_decode_step_(query, key, value, g, beta, state, use_qk_l2norm_in_kernel=True, scale=None):
+    """One (or more) token(s) of the recurrence with the fp32 state updated in place; returns o."""
+    scale = 1.0 / math.sqrt(key.shape[-1]) if scale is None else scale
+    return torch.ops.q35.gdn_decode_step_(query, key, value, g, beta, state, scale, bool(use_qk_l2norm_in_kernel))
+
+
+def gated_attention_prefill(q, k, v, gate, cos, sin, pos0=0, scale=None):
+    """Causal gated GQA attention with partial RoPE (q: [B, T, Hq, D]; k, v: [B, T, Hkv, D]; gate: [B, T, Hq*D];
+    cos/sin: [P, rot/2] fp32 by position). Returns [B, T, Hq*D] bf16."""
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    return torch.ops.q35.gated_attn_prefill(q, k, v, gate, cos, sin, int(pos0), float(scale))
+
+
+def gated_attention_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, scale=None, splits=0):
+    """One new token per row over a bf16 KV cache [B, Hkv, max_len, D]; q rotated at position cache_len - 1."""
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    return torch.ops.q35.gated_attn_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, float(scale), int(splits))
+
+
+def residual_steer_add_(x, vecs, vec_of_row=None):
+    """x[r, t, :] += vecs[vec_of_row[r]] in place (negative index: no vector; None: min(r, nvec - 1))."""
+    torch.ops.q35.resid_add_rows_(x, vecs, vec_of_row)
+    return x

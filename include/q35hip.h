@@ -1,0 +1,124 @@
+/*
+ * q35hip: C ABI of the MI355X (gfx950) kernels for the Qwen3.5 hybrid-attention hot path.
+ *
+ * Every entry point takes raw device pointers, explicit int64 sizes and a HIP stream, enqueues its kernels on that
+ * stream and returns a status code (Q35_OK or one of the Q35_E* values below). No entry point allocates device
+ * memory, synchronises the host, or throws: scratch memory comes from a caller-provided workspace whose size the
+ * matching *_workspace_bytes function reports. Tensors are dense and row-major in the layouts stated per function.
+ *
+ * Reference interfaces replaced (paths relative to the scasella/duo-mech-interp checkout; HF: is
+ * transformers 5.15.0 models/qwen3_5/modeling_qwen3_5.py, which the reference's PyTorch mirror
+ * tests/engine_ref.py runs):
+ *   q35_gdn_recurrent        HF:331-380 torch_recurrent_gated_delta_rule; engine/kernels_qwen35.js:183-247 `delta`
+ *   q35_gdn_chunk_prefill    HF:249-327 torch_chunk_gated_delta_rule (chunk_size 64)
+ *   q35_gated_attn_prefill   HF:554-589 apply_rotary_pos_emb (partial) + HF:604-626 eager_attention_forward (causal)
+ *                            + HF:698 sigmoid gate; engine/kernels_qwen35.js:73-123 `attention`
+ *   q35_gated_attn_decode    same as above for one new token per row over a KV cache (engine/kernels_qwen35.js:73-123
+ *                            with T = 1; HF decode through DynamicCache)
+ *   q35_resid_add_rows       tests/engine_ref.py:49-53 residual vector hook; engine/kernels.js:190-203 `resAdd`
+ */
+#ifndef Q35HIP_H
+#define Q35HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t without pulling in the HIP headers (identical type). */
+typedef struct ihipStream_t* q35_stream_t;
+
+enum q35_status {
+  Q35_OK = 0,
+  Q35_EINVAL = 1,       /* null pointer, non-positive size, or inconsistent sizes */
+  Q35_EUNSUPPORTED = 2, /* a size or dtype this build has no kernel for (e.g. head dim other than 128 / 256) */
+  Q35_EWORKSPACE = 3,   /* workspace pointer null or smaller than *_workspace_bytes */
+  Q35_ELAUNCH = 4       /* the HIP runtime refused a kernel launch */
+};
+
+enum q35_dtype { Q35_F32 = 0, Q35_BF16 = 1 };
+
+/* Human-readable name of a status code (static storage). */
+const char* q35_status_string(int status);
+/* ABI version of this library: bumped when a signature changes. */
+int q35_abi_version(void);
+
+/*
+ * Gated delta rule, token-serial form (decode, or any T).
+ * Replaces torch_recurrent_gated_delta_rule(query, key, value, g, beta, initial_state, output_final_state,
+ * use_qk_l2norm_in_kernel) at HF:331-380, and the recurrence inside the WGSL `delta` kernel
+ * (engine/kernels_qwen35.js:229-236).
+ *   q, k:  [B, T, Hk, Dk]   dtype           v, out: [B, T, H, Dv]   dtype
+ *   g, beta: [B, T, H] fp32 (g is the log decay, alpha = exp(g))
+ *   initial_state: [B, H, Dk, Dv] fp32 or NULL (zeros); final_state: [B, H, Dk, Dv] fp32 (may alias initial_state)
+ *   H must be a multiple of Hk (q/k head h / (H / Hk) serves value head h, as repeat_interleave at HF:500-502).
+ *   Dk = Dv = 128 (the reference engine requires it: engine/model.js:52).
+ *   scale multiplies q after the optional l2 normalisation (HF uses 1/sqrt(Dk)).
+ */
+int q35_gdn_recurrent(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                      const float* initial_state, float* final_state, void* out,
+                      int64_t B, int64_t T, int64_t Hk, int64_t H, int64_t Dk, int64_t Dv,
+                      int dtype, float scale, int use_qk_l2norm, q35_stream_t stream);
+
+/*
+ * Gated delta rule, chunked form (prefill). Replaces torch_chunk_gated_delta_rule at HF:249-327: the same
+ * arguments and layouts as q35_gdn_recurrent, chunk_size 64 (the only size this build supports). T need not be a
+ * multiple of 64 (the tail chunk is zero-padded as HF:271-277 does). Needs a workspace of
+ * q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, 64) bytes (256-byte aligned).
+ */
+size_t q35_gdn_chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t Dk, int64_t Dv, int64_t chunk_size);
+int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                          const float* initial_state, float* final_state, void* out,
+                          int64_t B, int64_t T, int64_t Hk, int64_t H, int64_t Dk, int64_t Dv,
+                          int dtype, float scale, int use_qk_l2norm, int64_t chunk_size,
+                          void* workspace, size_t workspace_bytes, q35_stream_t stream);
+
+/*
+ * Gated causal GQA softmax attention over one call's tokens, with partial rotary embedding and the sigmoid output
+ * gate fused. Replaces, at HF:656-698, apply_rotary_pos_emb -> attention_interface (eager_attention_forward,
+ * HF:604-626, causal mask, softmax in fp32) -> reshape -> * sigmoid(gate); and the WGSL `attention` kernel
+ * (engine/kernels_qwen35.js:73-123) plus the rotary part of `attnPrep` (engine/kernels_qwen35.js:50-59).
+ *   q: [B, T, Hq, D] bf16   k, v: [B, T, Hkv, D] bf16   gate: [B, T, Hq * D] bf16   out: [B, T, Hq * D] bf16
+ *   cos, sin: [P, rot / 2] fp32 tables by absolute position (position of token t is pos0 + t, P > pos0 + T - 1);
+ *   rotary pairs (i, i + rot/2) on the first rot dims (rotate_half, HF:546-551). rot = 0 disables the rotation.
+ *   scale is the softmax scale (HF: head_dim ** -0.5). D = 256, Hq / Hkv in {1, 2, 4, 8}.
+ */
+int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const void* gate,
+                           const float* cos, const float* sin, int64_t pos0, void* out,
+                           int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t rot,
+                           float scale, q35_stream_t stream);
+
+/*
+ * Gated GQA attention for one new token per row over a bf16 KV cache (split-K over the context, then a merge).
+ *   q: [B, Hq, D] bf16 (not yet rotated; rotated here at position cache_len[b] - 1)
+ *   k_cache, v_cache: [B, Hkv, max_len, D] bf16, keys already rotated; row b uses keys 0 .. cache_len[b] - 1
+ *   cache_len: [B] int32 on the device (1 <= cache_len[b] <= max_len)
+ *   gate: [B, Hq * D] bf16    out: [B, Hq * D] bf16
+ *   splits <= 0 lets the library choose the split count. Needs
+ *   q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits) bytes of workspace.
+ */
+size_t q35_gated_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
+                                             int64_t splits);
+int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* gate,
+                          const int32_t* cache_len, const float* cos, const float* sin, void* out,
+                          int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
+                          float scale, int64_t splits, void* workspace, size_t workspace_bytes,
+                          q35_stream_t stream);
+
+/*
+ * Residual steering add: x[r, t, :] += vecs[vec_of_row[r], :] for every row r and position t; rows whose index is
+ * negative are left alone. Replaces the layer-12 forward hook of tests/engine_ref.py:49-53 (out + s * vec at every
+ * position) and the WGSL `resAdd` (engine/kernels.js:190-203, vector row = min(row, 3)).
+ *   x: [rows, T, H] dtype (fp32 or bf16)   vecs: [nvec, H] fp32   vec_of_row: [rows] int32 on the device, or NULL
+ *   for min(r, nvec - 1) as the WGSL kernel does.
+ */
+int q35_resid_add_rows(void* x, const float* vecs, const int32_t* vec_of_row, int64_t rows, int64_t T, int64_t H,
+                       int64_t nvec, int dtype, q35_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q35HIP_H */

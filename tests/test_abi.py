@@ -1,0 +1,89 @@
+"""The C ABI library loads and exports every entry point include/q35hip.h declares; argument validation rejects
+bad calls before anything is launched (no GPU needed)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import q35hip
+from q35hip import _lib
+from q35hip.build import LIB_PATH
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "q35hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(q35_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for n in ["q35_gdn_recurrent", "q35_gdn_chunk_prefill", "q35_gated_attn_prefill", "q35_gated_attn_decode",
+              "q35_resid_add_rows"]:
+        assert n in names
+
+
+def test_library_built_and_exports_every_declared_symbol():
+    assert os.path.exists(LIB_PATH), "libq35hip.so not built (run __graft_entry__.build())"
+    raw = ctypes.CDLL(LIB_PATH)
+    for n in declared_functions():
+        assert hasattr(raw, n), f"{n} declared in q35hip.h but not exported"
+    assert sorted(_lib.EXPORTS) == declared_functions()
+
+
+def test_status_strings_and_version():
+    L = q35hip.lib()
+    assert L.q35_abi_version() == 1
+    assert L.q35_status_string(0) == b"ok"
+    assert b"invalid" in L.q35_status_string(1)
+
+
+def test_validation_rejects_without_launching():
+    L = q35hip.lib()
+    # null pointers
+    assert L.q35_gdn_recurrent(None, None, None, None, None, None, None, None, 1, 1, 1, 1, 128, 128, 1, 1.0, 1,
+                               None) == 1
+    fake = 0x1000
+    # unsupported head dim
+    assert L.q35_gdn_recurrent(fake, fake, fake, fake, fake, None, fake, fake, 1, 1, 1, 1, 64, 64, 1, 1.0, 1,
+                               None) == 2
+    # value heads not a multiple of q/k heads
+    assert L.q35_gdn_recurrent(fake, fake, fake, fake, fake, None, fake, fake, 1, 1, 3, 4, 128, 128, 1, 1.0, 1,
+                               None) == 1
+    # chunk size other than 64
+    assert L.q35_gdn_chunk_workspace_bytes(1, 128, 16, 128, 128, 32) == 0
+    assert L.q35_gdn_chunk_prefill(fake, fake, fake, fake, fake, None, fake, fake, 1, 128, 16, 16, 128, 128, 1, 1.0,
+                                   1, 32, fake, 1 << 30, None) == 2
+    # workspace too small
+    assert L.q35_gdn_chunk_prefill(fake, fake, fake, fake, fake, None, fake, fake, 1, 128, 16, 16, 128, 128, 1, 1.0,
+                                   1, 64, fake, 16, None) == 3
+    # attention: head dim 128 unsupported, GQA ratio 3 unsupported, odd rot invalid
+    assert L.q35_gated_attn_prefill(fake, fake, fake, fake, fake, fake, 0, fake, 1, 16, 8, 2, 128, 64, 0.1,
+                                    None) == 2
+    assert L.q35_gated_attn_prefill(fake, fake, fake, fake, fake, fake, 0, fake, 1, 16, 6, 2, 256, 64, 0.1,
+                                    None) == 2
+    assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 8, 2, 256, 128, 63, 0.1, 0,
+                                   fake, 1 << 20, None) == 1
+    assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 8, 2, 256, 128, 64, 0.1, 0,
+                                   fake, 8, None) == 3
+    assert L.q35_resid_add_rows(None, fake, None, 1, 1, 8, 1, 0, None) == 1
+
+
+def test_decode_workspace_scales_with_splits():
+    L = q35hip.lib()
+    a = L.q35_gated_attn_decode_workspace_bytes(3, 8, 2, 256, 8192, 4)
+    b = L.q35_gated_attn_decode_workspace_bytes(3, 8, 2, 256, 8192, 8)
+    assert a > 0 and b == 2 * a
+
+
+def test_ops_refuse_cpu_tensors():
+    x = torch.zeros(1, 4, 16, 128)
+    g = torch.zeros(1, 4, 16)
+    with pytest.raises(Exception, match="no CPU|HIP device"):
+        q35hip.chunk_gated_delta_rule(x, x, x, g, g)
+    with pytest.raises(Exception, match="no CPU|HIP device"):
+        q35hip.recurrent_gated_delta_rule(x, x, x, g, g, None, True)

@@ -1,0 +1,94 @@
+"""Gated attention parity on the GPU: HIP prefill / decode kernels against the CPU oracle in fp32 on the same
+bf16-rounded inputs (relative error <= 2e-2, the bf16-activation tolerance)."""
+import pytest
+import torch
+
+import oracle
+import q35hip
+from q35hip import workloads
+from gpu_util import announce, device
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _tables(n):
+    return workloads.rope_tables(n)
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,pos0", [(1, 1, 8, 2, 0), (2, 100, 8, 2, 0), (1, 257, 8, 2, 5),
+                                             (1, 96, 4, 4, 0), (1, 70, 8, 1, 3), (1, 64, 16, 2, 0)])
+def test_prefill_small(B, T, Hq, Hkv, pos0):
+    dev = device()
+    inp = workloads.attn_prefill_inputs(B=B, T=T, Hq=Hq, Hkv=Hkv, seed=T)
+    cos, sin = _tables(pos0 + T)
+    ref = oracle.gated_attention(inp["q"], inp["k"], inp["v"], inp["gate"], cos, sin, pos0=pos0)
+    d = workloads.to_device(inp, dev)
+    announce(f"attn prefill B{B} T{T} Hq{Hq} Hkv{Hkv} pos0 {pos0}")
+    out = q35hip.gated_attention_prefill(d["q"], d["k"], d["v"], d["gate"], cos.to(dev), sin.to(dev), pos0=pos0)
+    assert oracle.rel_err(out.float().cpu(), ref) <= TOL
+
+
+def test_prefill_full_size():
+    """B = 1, T = 4096, causal, 8 q / 2 kv heads, head dim 256, RoPE theta 1e7 on dims 0..63, sigmoid gate."""
+    dev = device()
+    inp = workloads.attn_prefill_inputs(B=1, T=4096, seed=0)
+    cos, sin = _tables(4096)
+    ref = oracle.gated_attention(inp["q"], inp["k"], inp["v"], inp["gate"], cos, sin)
+    d = workloads.to_device(inp, dev)
+    announce("attn prefill T4096 (full size)")
+    out = q35hip.gated_attention_prefill(d["q"], d["k"], d["v"], d["gate"], cos.to(dev), sin.to(dev))
+    e = oracle.rel_err(out.float().cpu(), ref)
+    print(f"attn prefill T4096 rel err {e:.3e}")
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("B", [3, 32])
+def test_decode_full_size(B):
+    """Batch 3 and 32, context 8192, 8 q / 2 kv heads, head dim 256, bf16 KV cache, split-K."""
+    dev = device()
+    inp = workloads.attn_decode_inputs(B=B, N=8192, seed=B)
+    cos, sin = _tables(8192)
+    ref = oracle.gated_attention_decode(inp["q"], inp["k_cache"], inp["v_cache"], inp["gate"], inp["cache_len"],
+                                        cos, sin)
+    d = workloads.to_device(inp, dev)
+    announce(f"attn decode B{B} N8192")
+    out = q35hip.gated_attention_decode(d["q"], d["k_cache"], d["v_cache"], d["gate"], d["cache_len"],
+                                        cos.to(dev), sin.to(dev))
+    e = oracle.rel_err(out.float().cpu(), ref)
+    print(f"attn decode B{B} rel err {e:.3e}")
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("splits", [1, 2, 7, 0, 64])
+def test_decode_ragged_lengths_and_split_invariance(splits):
+    dev = device()
+    lens = [1, 17, 300, 1000]
+    inp = workloads.attn_decode_inputs(B=4, N=1000, max_len=1024, seed=4, lens=lens)
+    cos, sin = _tables(1024)
+    ref = oracle.gated_attention_decode(inp["q"], inp["k_cache"], inp["v_cache"], inp["gate"], inp["cache_len"],
+                                        cos, sin)
+    d = workloads.to_device(inp, dev)
+    announce(f"attn decode ragged splits {splits}")
+    out = q35hip.gated_attention_decode(d["q"], d["k_cache"], d["v_cache"], d["gate"], d["cache_len"],
+                                        cos.to(dev), sin.to(dev), splits=splits)
+    assert oracle.rel_err(out.float().cpu(), ref) <= TOL
+
+
+def test_decode_matches_last_prefill_row():
+    """Decode of token T-1 over the rotated K cache of a prefill equals the prefill's last output row."""
+    dev = device()
+    T = 300
+    inp = workloads.attn_prefill_inputs(B=1, T=T, seed=12)
+    cos, sin = _tables(T)
+    d = workloads.to_device(inp, dev)
+    announce("attn decode vs prefill last row")
+    full = q35hip.gated_attention_prefill(d["q"], d["k"], d["v"], d["gate"], cos.to(dev), sin.to(dev))
+    k_rot = oracle.apply_partial_rope(inp["k"].float(), cos, sin).to(torch.bfloat16)  # [1, T, Hkv, D]
+    k_cache = k_rot.transpose(1, 2).contiguous().to(dev)
+    v_cache = inp["v"].transpose(1, 2).contiguous().to(dev)
+    q_last = d["q"][:, T - 1].contiguous()
+    gate_last = d["gate"][:, T - 1].contiguous()
+    cl = torch.tensor([T], dtype=torch.int32, device=dev)
+    dec = q35hip.gated_attention_decode(q_last, k_cache, v_cache, gate_last, cl, cos.to(dev), sin.to(dev))
+    assert oracle.rel_err(dec.float().cpu(), full[:, T - 1].float().cpu()) <= TOL

@@ -1,0 +1,136 @@
+"""Gated DeltaNet parity on the GPU: HIP kernels against the CPU oracle (fp32 recurrence) on seeded inputs.
+
+Tolerances (relative error sqrt(sum (a-b)^2 / sum b^2), the reference's metric, tests/engine.mjs:17):
+  fp32 state with fp32 activations: <= 1e-3;  bf16 activations: <= 2e-2.
+"""
+import pytest
+import torch
+
+import oracle
+import q35hip
+from q35hip import workloads
+from gpu_util import announce, device
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_BF16 = 2e-2
+
+
+def _oracle_rec(inp, state=None, dtype=torch.float32):
+    return oracle.recurrent_gated_delta_rule(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"],
+                                             initial_state=state, output_final_state=True,
+                                             use_qk_l2norm_in_kernel=True, dtype=dtype)
+
+
+def test_decode_64_sequential_steps_fp32():
+    """64 sequential single-token decode steps, batch 1, 16 heads, d 128, fp32 state from 0, seed 0."""
+    dev = device()
+    inp = workloads.gdn_inputs(B=1, T=64, H=16, D=128, seed=0)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    state = torch.zeros(1, 16, 128, 128, device=dev)
+    outs = []
+    announce("gdn decode 64 steps B1 H16 fp32")
+    for t in range(64):
+        sl = slice(t, t + 1)
+        o = q35hip.gdn_decode_step_(d["q"][:, sl].contiguous(), d["k"][:, sl].contiguous(),
+                                    d["v"][:, sl].contiguous(), d["g"][:, sl].contiguous(),
+                                    d["beta"][:, sl].contiguous(), state)
+        outs.append(o)
+    o = torch.cat(outs, dim=1).cpu()
+    torch.cuda.synchronize()
+    assert oracle.rel_err(o, o_ref) <= TOL_F32
+    assert oracle.rel_err(state.cpu(), s_ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_recurrent_multi_token_gqa_initial_state(dtype):
+    """T = 37 in one launch, B = 2, 8 value heads over 4 q/k heads, a non-zero initial state."""
+    dev = device()
+    inp = workloads.gdn_inputs(B=2, T=37, H=8, Hk=4, D=128, seed=1, dtype=dtype, normalize=False)
+    s0 = 0.1 * torch.randn(2, 8, 128, 128, generator=torch.Generator().manual_seed(5))
+    o_ref, s_ref = _oracle_rec(inp, s0)
+    d = workloads.to_device(inp, dev)
+    announce(f"gdn recurrent T37 B2 H8/4 {dtype}")
+    o, S = q35hip.recurrent_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=s0.to(dev),
+                                             output_final_state=True, use_qk_l2norm_in_kernel=True)
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    assert oracle.rel_err(o.float().cpu(), o_ref) <= tol
+    assert oracle.rel_err(S.cpu(), s_ref) <= tol
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65, 200])
+def test_chunk_prefill_ragged_lengths(T):
+    """Chunked prefill against the fp32 recurrence for T not a multiple of 64 (zero-padded tail), bf16 inputs."""
+    dev = device()
+    inp = workloads.gdn_inputs(B=2, T=T, H=4, D=128, seed=T, dtype=torch.bfloat16)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    announce(f"gdn chunk T{T} B2 H4 bf16")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], output_final_state=True,
+                                         use_qk_l2norm_in_kernel=True)
+    assert oracle.rel_err(o.float().cpu(), o_ref) <= TOL_BF16
+    assert oracle.rel_err(S.cpu(), s_ref) <= TOL_BF16
+
+
+def test_chunk_prefill_initial_state_and_gqa():
+    dev = device()
+    inp = workloads.gdn_inputs(B=1, T=256, H=8, Hk=2, D=128, seed=7, dtype=torch.bfloat16, normalize=False)
+    s0 = 0.2 * torch.randn(1, 8, 128, 128, generator=torch.Generator().manual_seed(9))
+    o_ref, s_ref = _oracle_rec(inp, s0)
+    d = workloads.to_device(inp, dev)
+    announce("gdn chunk T256 H8/2 initial state")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=s0.to(dev),
+                                         output_final_state=True, use_qk_l2norm_in_kernel=True)
+    assert oracle.rel_err(o.float().cpu(), o_ref) <= TOL_BF16
+    assert oracle.rel_err(S.cpu(), s_ref) <= TOL_BF16
+
+
+def test_chunk_prefill_fp32_inputs():
+    dev = device()
+    inp = workloads.gdn_inputs(B=1, T=300, H=4, D=128, seed=11, dtype=torch.float32)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    announce("gdn chunk T300 fp32 inputs")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], output_final_state=True,
+                                         use_qk_l2norm_in_kernel=True)
+    assert o.dtype == torch.float32
+    assert oracle.rel_err(o.cpu(), o_ref) <= TOL_BF16
+    assert oracle.rel_err(S.cpu(), s_ref) <= TOL_BF16
+
+
+def test_chunk_prefill_full_size():
+    """B = 1, T = 4096, 16 heads, d 128, bf16 q/k/v, chunk 64, fp32 state; against the fp32 CPU recurrence."""
+    dev = device()
+    inp = workloads.gdn_inputs(B=1, T=4096, H=16, D=128, seed=0, dtype=torch.bfloat16)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    announce("gdn chunk T4096 H16 bf16 (full size)")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], output_final_state=True,
+                                         use_qk_l2norm_in_kernel=True)
+    eo, es = oracle.rel_err(o.float().cpu(), o_ref), oracle.rel_err(S.cpu(), s_ref)
+    print(f"T4096 rel err o {eo:.3e} S {es:.3e}")
+    assert eo <= TOL_BF16 and es <= TOL_BF16
+
+
+def test_chunk_then_decode_handoff():
+    """Prefill 128 tokens with the chunk kernel, continue 16 tokens with the decode kernel on the carried state:
+    equals one 144-token recurrence."""
+    dev = device()
+    inp = workloads.gdn_inputs(B=1, T=144, H=4, D=128, seed=3, dtype=torch.bfloat16)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    announce("gdn chunk->decode handoff")
+    pre = {k: v[:, :128].contiguous() for k, v in d.items()}
+    o1, S = q35hip.chunk_gated_delta_rule(pre["q"], pre["k"], pre["v"], pre["g"], pre["beta"], output_final_state=True,
+                                          use_qk_l2norm_in_kernel=True)
+    outs = [o1]
+    for t in range(128, 144):
+        sl = slice(t, t + 1)
+        outs.append(q35hip.gdn_decode_step_(d["q"][:, sl].contiguous(), d["k"][:, sl].contiguous(),
+                                            d["v"][:, sl].contiguous(), d["g"][:, sl].contiguous(),
+                                            d["beta"][:, sl].contiguous(), S))
+    o = torch.cat(outs, dim=1).float().cpu()
+    assert oracle.rel_err(o, o_ref) <= TOL_BF16
+    assert oracle.rel_err(S.cpu(), s_ref) <= TOL_BF16
