@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Benchmark of the Qwen3.5 hybrid-attention hot path on one MI355X.
+
+Headline (the JSON `value`): Gated DeltaNet chunked prefill, B = 1, T = 4096, 16 heads, d_k = d_v = 128, bf16
+q/k/v, chunk 64, fp32 state -> tokens per second. The same line carries a breakdown of the other workloads (GDN
+decode step, gated-attention prefill T = 4096, gated-attention decode B = 3 and 32 over an 8192 context), each as
+tok/s and as a fraction of its roofline, plus the CPU oracle timed on the host cores.
+
+Method: every step is one call of the op on fresh device-resident inputs. Steps are captured once per input set in a
+HIP graph and replayed; HIP events recorded on the launch stream around each replay give the per-step GPU time.
+Input sets rotate so that the bytes touched between two uses of one set exceed the 256 MB Infinity Cache: the GB/s
+figures are HBM figures, not cache figures.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--only gdn_prefill,...] [--no-cpu]
+"""
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "duo-mech-interp_amd"))
+
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+PEAK_BF16_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
+ROTATE_BYTES = 640 << 20     # distinct bytes cycled through between two uses of one input set
+
+# Algorithmic work per unit (minimum HBM bytes / nominal FLOPs)
+GDN_PREFILL_BYTES = 68_681_728      # q,k,v bf16 + g,beta fp32 + o bf16 + final S fp32 (T 4096, H 16, d 128)
+GDN_PREFILL_FLOPS = 1.190e10
+GDN_DECODE_STEP_BYTES = 2_130_048   # S read + write fp32 + q,k,v,o,g,beta (B 1, H 16, d 128)
+ATTN_PREFILL_FLOPS = 6.874e10       # 4 * D * Hq * T (T + 1) / 2, T 4096, Hq 8, D 256
+ATTN_PREFILL_BYTES = 58_720_256
+ATTN_DECODE_ROW_BYTES = 16_789_504  # K + V span 16,777,216 + q, gate, out 12,288
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="", help="comma list of workloads to run")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
+    return ap.parse_args()
+
+
+class Timer:
+    """Graph-captured steps over rotating input sets, timed with events on the capture/launch stream."""
+
+    def __init__(self, torch, make_call, n_sets, reps=1):
+        """reps calls are captured per graph (one per input set, cycling), so that a replay costs one graph launch
+        for `reps` steps: per-step times of microsecond kernels are then not graph-launch bound."""
+        self.torch = torch
+        self.graphs = []
+        self.keep = []
+        self.reps = reps
+        stream = torch.cuda.Stream()
+        calls = [make_call(i) for i in range(n_sets)]
+        with torch.cuda.stream(stream):  # warm the allocator outside the graphs
+            for c in calls:
+                c()
+        torch.cuda.synchronize()
+        n_graphs = max(1, n_sets // reps) if reps > 1 else n_sets
+        for gi in range(n_graphs):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                outs = [calls[(gi * reps + r) % n_sets]() for r in range(reps)]
+            self.graphs.append(g)
+            self.keep.append(outs)
+        torch.cuda.synchronize()
+
+    def run(self, steps, warmup):
+        torch = self.torch
+        n = len(self.graphs)
+        for i in range(warmup):
+            self.graphs[i % n].replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        t0 = time.perf_counter()
+        for i in range(steps):
+            ev[i][0].record(stream)
+            self.graphs[i % n].replay()
+            ev[i][1].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per = [a.elapsed_time(b) * 1e-3 / self.reps for a, b in ev]  # seconds per call
+        return {"wall_s": wall / self.reps, "step_s": sum(per) / len(per), "min_step_s": min(per)}
+
+
+def n_sets_for(bytes_per_set, cap=24):
+    return max(2, min(cap, math.ceil(ROTATE_BYTES / max(bytes_per_set, 1)) + 1))
+
+
+def bench_gdn_prefill(torch, q35hip, workloads, steps, warmup, dev):
+    B, T, H, D = 1, 4096, 16, 128
+    per_set = GDN_PREFILL_BYTES + 88 * 1024 * 1024  # inputs/outputs + the op's workspace
+    n = n_sets_for(per_set, cap=8)
+    sets = []
+    for i in range(n):
+        sets.append(workloads.to_device(workloads.gdn_inputs(B=B, T=T, H=H, D=D, seed=i, dtype=torch.bfloat16), dev))
+
+    def make_call(i):
+        d = sets[i]
+        return lambda: q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"],
+                                                     output_final_state=True, use_qk_l2norm_in_kernel=True)
+    r = Timer(torch, make_call, n).run(steps, warmup)
+    t = r["step_s"]
+    gbs = GDN_PREFILL_BYTES / t / 1e9
+    return {"tok_s": T * B / t, "ms": t * 1e3, "achieved_gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
+            "tflops": GDN_PREFILL_FLOPS / t / 1e12, "wall_ms_per_step": r["wall_s"] / steps * 1e3, "sets": n}
+
+
+def bench_gdn_decode(torch, q35hip, workloads, steps, warmup, dev):
+    """One decode step (T = 1). Two shapes: the latency-bound B = 1 step (state 1 MiB, as in a model where the layer's
+    state stays resident between steps) and a bandwidth shape, B = 16 over 20 distinct layer states (320 MB cycled)."""
+    out = {}
+    for name, B, nstate in (("b1", 1, 64), ("b16", 16, 20)):
+        H, D = 16, 128
+        inp = workloads.to_device(workloads.gdn_inputs(B=B, T=1, H=H, D=D, seed=0, dtype=torch.float32), dev)
+        states = [torch.zeros(B, H, D, D, device=dev) for _ in range(nstate)]
+
+        def make_call(i, inp=inp, states=states):
+            return lambda: q35hip.gdn_decode_step_(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], states[i])
+        r = Timer(torch, make_call, nstate, reps=nstate).run(steps, warmup)
+        t = r["step_s"]
+        by = B * GDN_DECODE_STEP_BYTES
+        out[name] = {"tok_s": B / t, "us": t * 1e6, "achieved_gbs": by / t / 1e9, "frac": by / t / 1e9 / PEAK_HBM_GBS,
+                     "state_mb_cycled": nstate * B * H * D * D * 4 / 1e6}
+    return out
+
+
+def bench_attn_prefill(torch, q35hip, workloads, steps, warmup, dev):
+    B, T = 1, 4096
+    n = n_sets_for(ATTN_PREFILL_BYTES, cap=8)
+    cos, sin = [x.to(dev) for x in workloads.rope_tables(T)]
+    sets = [workloads.to_device(workloads.attn_prefill_inputs(B=B, T=T, seed=i), dev) for i in range(n)]
+
+    def make_call(i):
+        d = sets[i]
+        return lambda: q35hip.gated_attention_prefill(d["q"], d["k"], d["v"], d["gate"], cos, sin)
+    r = Timer(torch, make_call, n).run(steps, warmup)
+    t = r["step_s"]
+    tf = ATTN_PREFILL_FLOPS / t / 1e12
+    return {"tok_s": T / t, "ms": t * 1e3, "achieved_tflops": tf, "frac": tf / PEAK_BF16_TFLOPS, "sets": n}
+
+
+def bench_attn_decode(torch, q35hip, workloads, steps, warmup, dev):
+    out = {}
+    N = 8192
+    cos, sin = [x.to(dev) for x in workloads.rope_tables(N)]
+    for B in (3, 32):
+        by = B * ATTN_DECODE_ROW_BYTES
+        n = n_sets_for(by, cap=16)
+        sets = [workloads.to_device(workloads.attn_decode_inputs(B=B, N=N, seed=i), dev) for i in range(n)]
+
+        def make_call(i, sets=sets):
+            d = sets[i]
+            return lambda: q35hip.gated_attention_decode(d["q"], d["k_cache"], d["v_cache"], d["gate"],
+                                                         d["cache_len"], cos, sin)
+        r = Timer(torch, make_call, n, reps=n).run(steps, warmup)
+        t = r["step_s"]
+        out[f"b{B}"] = {"tok_s": B / t, "us": t * 1e6, "achieved_gbs": by / t / 1e9,
+                        "frac": by / t / 1e9 / PEAK_HBM_GBS, "sets": n}
+        del sets
+        torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(budget_s):
+    """The CPU oracle (a PyTorch-CPU restatement of the reference's fp32 path) timed on this host: the chunked gated
+    delta rule over the same T = 4096, 16-head workload, fp32, all threads torch uses."""
+    import torch
+    sys.path.insert(0, REPO)
+    import oracle
+    from q35hip import workloads
+    inp = workloads.gdn_inputs(B=1, T=4096, H=16, D=128, seed=0, dtype=torch.bfloat16)
+    threads = torch.get_num_threads()
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        oracle.chunk_gated_delta_rule(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"],
+                                      use_qk_l2norm_in_kernel=True)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s * 0.5 or len(times) >= 5:
+            break
+    t = min(times)
+    return {"value": 4096 / t, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle chunk_gated_delta_rule fp32 on the full T=4096 H=16 workload, best of {len(times)} "
+                      f"({t:.2f} s each); host {platform.processor() or platform.machine()}, "
+                      f"{os.cpu_count()} logical CPUs visible"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the hot path's "
+              "multi-GPU sharding is a design note only)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import q35hip
+    from q35hip import workloads
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    dev = torch.device("cuda:0")
+    q35hip.lib()
+    only = set(filter(None, args.only.split(",")))
+    want = lambda name: not only or name in only  # noqa: E731
+
+    res = {}
+    if want("gdn_prefill"):
+        res["gdn_prefill"] = bench_gdn_prefill(torch, q35hip, workloads, args.steps, args.warmup, dev)
+        print(f"# gdn_prefill {res['gdn_prefill']}", file=sys.stderr, flush=True)
+    if want("attn_decode"):
+        res["attn_decode"] = bench_attn_decode(torch, q35hip, workloads, args.steps, args.warmup, dev)
+        print(f"# attn_decode {res['attn_decode']}", file=sys.stderr, flush=True)
+    if want("attn_prefill"):
+        res["attn_prefill"] = bench_attn_prefill(torch, q35hip, workloads, args.steps, args.warmup, dev)
+        print(f"# attn_prefill {res['attn_prefill']}", file=sys.stderr, flush=True)
+    if want("gdn_decode"):
+        res["gdn_decode"] = bench_gdn_decode(torch, q35hip, workloads, args.steps, args.warmup, dev)
+        print(f"# gdn_decode {res['gdn_decode']}", file=sys.stderr, flush=True)
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    gp = res.get("gdn_prefill")
+    line = {
+        "metric": "GDN prefill tok/s + gated-attn decode tok/s @1 GPU; % of HBM/MFMA roofline",
+        "value": round(gp["tok_s"], 1) if gp else None,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gp["ms"], 4) if gp else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "gdn_chunked_prefill", "batch": 1, "seq_len": 4096, "heads": 16, "d_k": 128,
+                   "d_v": 128, "chunk": 64, "state": "fp32", "activations": "bf16", "parallelism": "none (1 GPU)"},
+        "roofline": ({"bound": "hbm", "achieved": round(gp["achieved_gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                      "frac": round(gp["frac"], 4), "traffic": None} if gp else None),
+        "cpu_baseline": cpu,
+        "breakdown": res,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -83,18 +83,25 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   const int kn = lane & 15, kg = lane >> 4;  // score-tile coordinates: key column, lane group
   const int d0 = 8 * (lane & 31), kp = lane >> 5;  // PV coordinates: 8 dims, key parity
   for (int key0 = k_begin + kDecTile * wave; key0 < k_end; key0 += 4 * kDecTile) {
-    // scores S[head][key] for 16 keys
+    // issue the tile's K and V loads together: V does not depend on the scores
     const int key = key0 + kn;
     const bool kvalid = key < k_end;
     const __bf16* krow = kb + (size_t)(kvalid ? key : k_begin) * kDecD + 8 * kg;
+    bf16x8 kv8[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) kv8[ks] = *reinterpret_cast<const bf16x8*>(krow + 32 * ks);
+    uint4 vraw[kDecTile / 2];
+#pragma unroll
+    for (int i = 0; i < kDecTile / 2; ++i) {
+      const int vkey = key0 + 2 * i + kp;
+      const uint4 z = {0u, 0u, 0u, 0u};
+      vraw[i] = vkey < k_end ? *reinterpret_cast<const uint4*>(vb + (size_t)vkey * kDecD + d0) : z;
+    }
+    // scores S[head][key] for 16 keys
     f32x4 sc = zero4();
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-      const bf16x8 kv8 = *reinterpret_cast<const bf16x8*>(krow + 32 * ks);
-      sc = mfma16(qa[ks], kv8, sc);
-    }
+    for (int ks = 0; ks < 8; ++ks) sc = mfma16(qa[ks], kv8[ks], sc);
     // lane group kg holds heads 4 kg + r
-    float p[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float x = kvalid ? sc[r] * scale : -INFINITY;
@@ -103,15 +110,14 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
       for (int off = 1; off < 16; off <<= 1) tm = fmaxf(tm, __shfl_xor(tm, off, 64));
       const float mn = fmaxf(m_run[r], tm);
       const float corr = __expf(m_run[r] - mn);
-      p[r] = __expf(x - mn);
-      float ps = p[r];
+      const float p = __expf(x - mn);
+      float ps = p;
 #pragma unroll
       for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off, 64);
       l_run[r] = l_run[r] * corr + ps;
       m_run[r] = mn;
-      if (kg < NG && 4 * kg + r < G) pl[wave][kn][4 * kg + r] = p[r];
-      // stash corr in the score lane group's registers for the broadcast
-      sc[r] = corr;
+      if (kg < NG && 4 * kg + r < G) pl[wave][kn][4 * kg + r] = p;
+      sc[r] = corr;  // broadcast source for the accumulator rescale below
     }
     __builtin_amdgcn_wave_barrier();
     float corr_h[G];
@@ -122,21 +128,18 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     for (int hh = 0; hh < G; ++hh)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[hh][e] *= corr_h[hh];
-    // P.V: lane takes keys key0 + 2 i + kp
+    // P.V: lane takes keys key0 + 2 i + kp (masked keys were loaded as zeros and carry p = 0)
 #pragma unroll
     for (int i = 0; i < kDecTile / 2; ++i) {
       const int n = 2 * i + kp;
-      const int vkey = key0 + n;
-      if (vkey < k_end) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(vb + (size_t)vkey * kDecD + d0);
-        float vv[8] = {bf16lo(raw.x), bf16hi(raw.x), bf16lo(raw.y), bf16hi(raw.y),
-                       bf16lo(raw.z), bf16hi(raw.z), bf16lo(raw.w), bf16hi(raw.w)};
+      const uint4 raw = vraw[i];
+      const float vv[8] = {bf16lo(raw.x), bf16hi(raw.x), bf16lo(raw.y), bf16hi(raw.y),
+                           bf16lo(raw.z), bf16hi(raw.z), bf16lo(raw.w), bf16hi(raw.w)};
 #pragma unroll
-        for (int hh = 0; hh < G; ++hh) {
-          const float ph = pl[wave][n][hh];
+      for (int hh = 0; hh < G; ++hh) {
+        const float ph = pl[wave][n][hh];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[hh][e] += ph * vv[e];
-        }
+        for (int e = 0; e < 8; ++e) acc[hh][e] += ph * vv[e];
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -185,38 +188,64 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   }
 }
 
-// Merge over splits, gate, store. One block per (query head, row), one thread per output dim.
+// Merge over splits, gate, store. One block per (query head, row): the split weights exp(m_s - M) / L are formed
+// once in LDS, then four groups of 64 threads each fold a quarter of the splits for 4 dims per thread (16-byte
+// loads, all independent), and the four groups are summed in LDS.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __restrict__ part,
                                                                 const __bf16* __restrict__ gate,
                                                                 __bf16* __restrict__ out, int Hq, int Hkv, int S) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int G = Hq / Hkv, kvh = h / G, hh = h % G;
-  const float* pb = part + ((size_t)b * Hkv + kvh) * S * (size_t)G * (kDecD + 2) + (size_t)hh * (kDecD + 2);
   const size_t sstride = (size_t)G * (kDecD + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < S; ++s) M = fmaxf(M, pb[s * sstride + kDecD]);
-  float Lsum = 0.f, O = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < S; ++s) {
-      const float ms = pb[s * sstride + kDecD];
-      if (ms == -INFINITY) continue;
-      const float f = __expf(ms - M);
-      Lsum += pb[s * sstride + kDecD + 1] * f;
-      O += pb[s * sstride + d] * f;
-    }
+  const float* pb = part + ((size_t)b * Hkv + kvh) * S * sstride + (size_t)hh * (kDecD + 2);
+  extern __shared__ float wsh[];  // [S] weights, then [4][kDecD] partial sums
+  __shared__ float red[2][4];
+  // global max over splits
+  float mx = -INFINITY;
+  for (int s = tid; s < S; s += 256) mx = fmaxf(mx, pb[s * sstride + kDecD]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if ((tid & 63) == 0) red[0][tid >> 6] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  float ls = 0.f;
+  for (int s = tid; s < S; s += 256) {
+    const float ms = pb[s * sstride + kDecD];
+    const float w = (ms == -INFINITY || M == -INFINITY) ? 0.f : __expf(ms - M);
+    wsh[s] = w;
+    ls += w * pb[s * sstride + kDecD + 1];
   }
-  const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + d;
-  const float res = Lsum > 0.f ? O / Lsum : 0.f;
-  out[oi] = (__bf16)(res * sigmoidf_((float)gate[oi]));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ls += __shfl_xor(ls, o, 64);
+  if ((tid & 63) == 0) red[1][tid >> 6] = ls;
+  __syncthreads();
+  const float Lsum = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  const int grp = tid >> 6, d4 = 4 * (tid & 63);
+  f32x4 acc = zero4();
+  for (int s = grp; s < S; s += 4) {
+    const float w = wsh[s];
+    const f32x4 o4 = *reinterpret_cast<const f32x4*>(pb + s * sstride + d4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += w * o4[e];
+  }
+  float* accs = wsh + S;
+  *reinterpret_cast<f32x4*>(accs + grp * kDecD + d4) = acc;
+  __syncthreads();
+  if (tid < kDecD) {
+    const float O = accs[tid] + accs[kDecD + tid] + accs[2 * kDecD + tid] + accs[3 * kDecD + tid];
+    const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + tid;
+    const float res = Lsum > 0.f ? O / Lsum : 0.f;
+    out[oi] = (__bf16)(res * sigmoidf_((float)gate[oi]));
+  }
 }
 
 static int decode_splits(int64_t B, int64_t Hkv, int64_t max_len, int64_t splits, int* L_out) {
   int64_t S = splits;
   if (S <= 0) {
-    const int64_t target = 1024;  // blocks: about four per CU
+    const int64_t target = 512;  // blocks: two per CU
     S = (target + B * Hkv - 1) / (B * Hkv);
   }
-  const int64_t max_s = (max_len + 63) / 64;
+  const int64_t max_s = (max_len + 127) / 128;  // at least two 16-key tiles per wave
   if (S > max_s) S = max_s;
   if (S < 1) S = 1;
   int64_t L = (max_len + S - 1) / S;
@@ -268,7 +297,8 @@ extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const v
     default: Q35_DEC_LAUNCH(8); break;
   }
 #undef Q35_DEC_LAUNCH
-  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3((unsigned)Hq, (unsigned)B), dim3(kDecD), 0, st, part,
+  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3((unsigned)Hq, (unsigned)B), dim3(256),
+                     (size_t)(S + 4 * kDecD) * sizeof(float), st, part,
                      (const __bf16*)gate, (__bf16*)out, (int)Hq, (int)Hkv, S);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }

@@ -24,6 +24,8 @@ constexpr int kBQ = 32;             // queries per wave
 constexpr int kBK = 32;             // keys per tile
 constexpr int kKS = kPD + 8;        // K tile row stride (elements): 528 B, conflict-free 16-byte reads
 constexpr int kVS = kBK + 4;        // V^T row stride (elements): 72 B, conflict-free 8-byte reads
+constexpr int kRotMax = 64;         // rotary dims supported by the fused rotation (Qwen3.5: 64)
+constexpr int kHM = kRotMax / 2;    // cos / sin entries per position
 
 template <int GW>
 __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
@@ -33,6 +35,7 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
   constexpr int NT = 64 * GW;
   __shared__ __attribute__((aligned(16))) __bf16 ks_lds[2][kBK * kKS];
   __shared__ __attribute__((aligned(16))) __bf16 vt_lds[2][kPD * kVS];
+  __shared__ __attribute__((aligned(16))) float rope_lds[2][kBK][2 * kHM];  // cos | sin of the staged tile's keys
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n_other = B * Hkv * ngroups;
@@ -80,26 +83,57 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
   }
 
   // ---- staging of one K/V tile: global -> registers -> (rotate / transpose) -> LDS ----
+  // K chunks are numbered rotary chunks first (32 rows x RC chunks of 8 dims, RC = rot / 8), then the rest, so the
+  // rotary work spreads over the threads. The cos/sin rows of the tile's 32 keys are loaded with the tile and
+  // passed through LDS (one float4 of the table slice per thread per array).
   constexpr int KCH = kBK * (kPD / 8) / NT;  // 16-byte K chunks per thread
   constexpr int VUN = (kBK / 4) * (kPD / 8) / NT;  // (4 keys x 8 dims) V units per thread
+  constexpr int RQ = (kBK * kHM / 4 + NT - 1) / NT;  // float4s of each rope table slice per thread
+  const int RC = rot / 8;
   uint4 kreg[KCH], kpar[KCH], vreg[VUN][4];
+  f32x4 creg[RQ > 0 ? RQ : 1], sreg[RQ > 0 ? RQ : 1];
   const __bf16* kbase = k + ((size_t)b * T * Hkv + kvh) * kPD;  // + (key * Hkv) * kPD
   const __bf16* vbase = v + ((size_t)b * T * Hkv + kvh) * kPD;
+  auto kchunk = [&](int c, int& row, int& cc) {
+    if (c < kBK * RC) {
+      row = c / RC;
+      cc = c % RC;
+    } else {
+      const int c2 = c - kBK * RC;
+      row = c2 / (32 - RC);
+      cc = RC + c2 % (32 - RC);
+    }
+  };
   auto load_tile = [&](int kt) {
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
-      const int c = tid + i * NT, row = c >> 5, cc = c & 31;
+      int row, cc;
+      kchunk(tid + i * NT, row, cc);
       const int key = kt * kBK + row;
-      uint4 z = {0u, 0u, 0u, 0u};
+      const uint4 z = {0u, 0u, 0u, 0u};
       kreg[i] = z;
       kpar[i] = z;
       if (key < T) {
         const __bf16* kr = kbase + (size_t)key * Hkv * kPD;
         kreg[i] = *reinterpret_cast<const uint4*>(kr + 8 * cc);
-        if (8 * cc < rot) {
+        if (cc < RC) {
           const int pd = 8 * cc < half ? 8 * cc + half : 8 * cc - half;
           kpar[i] = *reinterpret_cast<const uint4*>(kr + pd);
         }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RQ; ++i) {
+      // table slice [32 keys][half] of cos and sin, as float4s
+      const int e4 = tid + i * NT;  // float4 index within the slice
+      const int row = e4 / (kHM / 4), j4 = e4 % (kHM / 4);
+      const int key = kt * kBK + row;
+      const f32x4 z = zero4();
+      creg[i] = z;
+      sreg[i] = z;
+      if (e4 < kBK * kHM / 4 && key < T && 4 * j4 < half) {
+        creg[i] = *reinterpret_cast<const f32x4*>(cos_t + (size_t)(pos0 + key) * half + 4 * j4);
+        sreg[i] = *reinterpret_cast<const f32x4*>(sin_t + (size_t)(pos0 + key) * half + 4 * j4);
       }
     }
 #pragma unroll
@@ -108,33 +142,45 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = kt * kBK + 4 * kq + r;
-        uint4 z = {0u, 0u, 0u, 0u};
+        const uint4 z = {0u, 0u, 0u, 0u};
         vreg[i][r] = key < T ? *reinterpret_cast<const uint4*>(vbase + (size_t)key * Hkv * kPD + 8 * dc) : z;
       }
     }
   };
   auto store_tile = [&](int kt, int buf) {
+    if (rot > 0) {
+      float* rl = &rope_lds[buf][0][0];
+#pragma unroll
+      for (int i = 0; i < RQ; ++i) {
+        const int e4 = tid + i * NT;
+        const int row = e4 / (kHM / 4), j4 = e4 % (kHM / 4);
+        if (e4 < kBK * kHM / 4) {
+          *reinterpret_cast<f32x4*>(rl + row * (2 * kHM) + 4 * j4) = creg[i];
+          *reinterpret_cast<f32x4*>(rl + row * (2 * kHM) + kHM + 4 * j4) = sreg[i];
+        }
+      }
+      __syncthreads();
+    }
     __bf16* kl = ks_lds[buf];
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
-      const int c = tid + i * NT, row = c >> 5, cc = c & 31;
+      int row, cc;
+      kchunk(tid + i * NT, row, cc);
       uint4 w = kreg[i];
       const int d = 8 * cc;
-      if (d < rot && kt * kBK + row < T) {
-        const int pos = pos0 + kt * kBK + row;
+      if (cc < RC && kt * kBK + row < T) {
+        const float* cr = &rope_lds[buf][row][0];
+        const float* sr = cr + kHM;
         const int j0 = d < half ? d : d - half;
         const float sg = d < half ? -1.f : 1.f;
         const uint4 p = kpar[i];
-        float x[8] = {bf16lo(w.x), bf16hi(w.x), bf16lo(w.y), bf16hi(w.y),
-                      bf16lo(w.z), bf16hi(w.z), bf16lo(w.w), bf16hi(w.w)};
+        const float x[8] = {bf16lo(w.x), bf16hi(w.x), bf16lo(w.y), bf16hi(w.y),
+                            bf16lo(w.z), bf16hi(w.z), bf16lo(w.w), bf16hi(w.w)};
         const float y[8] = {bf16lo(p.x), bf16hi(p.x), bf16lo(p.y), bf16hi(p.y),
                             bf16lo(p.z), bf16hi(p.z), bf16lo(p.w), bf16hi(p.w)};
         bf16x8 o8;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float c0 = cos_t[(size_t)pos * half + j0 + j], s0 = sin_t[(size_t)pos * half + j0 + j];
-          o8[j] = (__bf16)(x[j] * c0 + sg * y[j] * s0);
-        }
+        for (int j = 0; j < 8; ++j) o8[j] = (__bf16)(x[j] * cr[j0 + j] + sg * y[j] * sr[j0 + j]);
         w = *reinterpret_cast<const uint4*>(&o8);
       }
       *reinterpret_cast<uint4*>(kl + row * kKS + 8 * cc) = w;
@@ -184,7 +230,9 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
       const bf16x8 a = *reinterpret_cast<const bf16x8*>(kl + ln * kKS + 16 * ks + 8 * hh);
       s = mfma32(a, qop[ks], s);
     }
-    // online softmax along the keys of this lane's query
+    // online softmax along the keys of this lane's query. The running max is only moved (and O, l rescaled) when
+    // a row max exceeds it by more than 8 (natural log units): p = exp(s - m) then stays <= e^8, exact enough in
+    // fp32 and in the bf16 P operand, and most tiles skip the 128-register rescale.
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -194,21 +242,24 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
       mx = fmaxf(mx, x);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mn = fmaxf(m_run, mx);
-    const float corr = __expf(m_run - mn);
+    if (__any(mx > m_run + 8.f)) {
+      const float mn = fmaxf(m_run, mx);
+      const float corr = __expf(m_run - mn);
+      l_run *= corr;
+      m_run = mn;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[mt][r] *= corr;
+    }
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      s[r] = __expf(s[r] - mn);
+      s[r] = __expf(s[r] - m_run);
       ps += s[r];
     }
     ps += __shfl_xor(ps, 32, 64);
-    l_run = l_run * corr + ps;
-    m_run = mn;
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[mt][r] *= corr;
+    l_run += ps;
     bf16x8 pb[2];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -264,7 +315,7 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
   if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D || pos0 < 0)
     return Q35_EINVAL;
   if (rot > 0 && (!cos || !sin)) return Q35_EINVAL;
-  if (D != kPD || (rot % 16) != 0) return Q35_EUNSUPPORTED;
+  if (D != kPD || (rot % 16) != 0 || rot > kRotMax) return Q35_EUNSUPPORTED;
   const int64_t G = Hq / Hkv;
   if (G != 1 && G != 2 && G != 4 && G != 8) return Q35_EUNSUPPORTED;
   const int GW = G > 4 ? 4 : (int)G;

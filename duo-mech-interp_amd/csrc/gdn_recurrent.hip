@@ -55,6 +55,13 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(const Tin* __restric
   for (int t = 0; t < T; ++t) {
     const int par = t & 1;
     const size_t tok = (size_t)b * T + t;
+    // per-token scalars and this thread's value columns, issued first so they overlap the reductions
+    const float alpha = expf(g[tok * H + h]);
+    const float be = beta[tok * H + h];
+    const Tin* vrow = v + (tok * H + h) * kGdnD + j0;
+    float vv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vv[e] = to_f32(vrow[e]);
     float qv = 0.f, kv = 0.f;
     if (tid < kGdnD) {
       qv = to_f32(q[(tok * Hk + kh) * kGdnD + tid]);
@@ -110,13 +117,10 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(const Tin* __restric
 #pragma unroll
       for (int e = 0; e < 4; ++e) { A[e] += a2[e]; C[e] += c2[e]; }
     }
-    const float alpha = expf(g[tok * H + h]);
-    const float be = beta[tok * H + h];
-    const Tin* vrow = v + (tok * H + h) * kGdnD + j0;
     f32x4 out;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float d = be * (to_f32(vrow[e]) - alpha * A[e]);
+      const float d = be * (vv[e] - alpha * A[e]);
       out[e] = alpha * C[e] + qk * d;
       s[0][e] = alpha * s[0][e] + kk0 * d;
       s[1][e] = alpha * s[1][e] + kk1 * d;
