@@ -60,6 +60,12 @@ __device__ __forceinline__ bf16x8 pack8(const f32x4& lo, const f32x4& hi) {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
 
+// Block barrier that orders LDS traffic only. __syncthreads() also waits for every outstanding global load of the
+// calling wave (its fence has release semantics), which would drain register prefetches issued for the next
+// iteration; this waits for LDS operations (lgkmcnt) and meets the other waves, leaving global loads in flight.
+// The "memory" clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Sum / max over the 64 lanes of a wave (butterfly; every lane ends with the result).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
