@@ -90,12 +90,13 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     bf16x8 kv8[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) kv8[ks] = *reinterpret_cast<const bf16x8*>(krow + 32 * ks);
-    uint4 vraw[kDecTile / 2];
+    u32x4 vraw[kDecTile / 2];  // rows past the span: loaded from a clamped row, zeroed by select (no branch)
 #pragma unroll
     for (int i = 0; i < kDecTile / 2; ++i) {
       const int vkey = key0 + 2 * i + kp;
-      const uint4 z = {0u, 0u, 0u, 0u};
-      vraw[i] = vkey < k_end ? *reinterpret_cast<const uint4*>(vb + (size_t)vkey * kDecD + d0) : z;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      const u32x4 ld = *reinterpret_cast<const u32x4*>(vb + (size_t)min(vkey, k_end - 1) * kDecD + d0);
+      vraw[i] = vkey < k_end ? ld : z;
     }
     // scores S[head][key] for 16 keys
     f32x4 sc = zero4();
@@ -132,9 +133,9 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
 #pragma unroll
     for (int i = 0; i < kDecTile / 2; ++i) {
       const int n = 2 * i + kp;
-      const uint4 raw = vraw[i];
-      const float vv[8] = {bf16lo(raw.x), bf16hi(raw.x), bf16lo(raw.y), bf16hi(raw.y),
-                           bf16lo(raw.z), bf16hi(raw.z), bf16lo(raw.w), bf16hi(raw.w)};
+      const u32x4 raw = vraw[i];
+      const float vv[8] = {bf16lo(raw[0]), bf16hi(raw[0]), bf16lo(raw[1]), bf16hi(raw[1]),
+                           bf16lo(raw[2]), bf16hi(raw[2]), bf16lo(raw[3]), bf16hi(raw[3])};
 #pragma unroll
       for (int hh = 0; hh < G; ++hh) {
         const float ph = pl[wave][n][hh];

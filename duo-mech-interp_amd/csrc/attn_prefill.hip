@@ -90,7 +90,9 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
   constexpr int VUN = (kBK / 4) * (kPD / 8) / NT;  // (4 keys x 8 dims) V units per thread
   constexpr int RQ = (kBK * kHM / 4 + NT - 1) / NT;  // float4s of each rope table slice per thread
   const int RC = rot / 8;
-  uint4 kreg[KCH], kpar[KCH], vreg[VUN][4];
+  // rotary chunks come first, so with rot <= 64 only the first KPAR chunks of a thread can need a partner chunk
+  constexpr int KPAR = (kBK * (kRotMax / 8) + NT - 1) / NT;
+  u32x4 kreg[KCH], kpar[KPAR], vreg[VUN][4];
   f32x4 creg[RQ > 0 ? RQ : 1], sreg[RQ > 0 ? RQ : 1];
   const __bf16* kbase = k + ((size_t)b * T * Hkv + kvh) * kPD;  // + (key * Hkv) * kPD
   const __bf16* vbase = v + ((size_t)b * T * Hkv + kvh) * kPD;
@@ -109,17 +111,14 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
     for (int i = 0; i < KCH; ++i) {
       int row, cc;
       kchunk(tid + i * NT, row, cc);
-      const int key = kt * kBK + row;
-      const uint4 z = {0u, 0u, 0u, 0u};
-      kreg[i] = z;
-      kpar[i] = z;
-      if (key < T) {
-        const __bf16* kr = kbase + (size_t)key * Hkv * kPD;
-        kreg[i] = *reinterpret_cast<const uint4*>(kr + 8 * cc);
-        if (cc < RC) {
-          const int pd = 8 * cc < half ? 8 * cc + half : 8 * cc - half;
-          kpar[i] = *reinterpret_cast<const uint4*>(kr + pd);
-        }
+      // loads are unconditional from clamped rows (a load whose use sits in a branch is waited for in place);
+      // rows past T are zeroed when the tile is written to LDS
+      const int key = min(kt * kBK + row, T - 1);
+      const __bf16* kr = kbase + (size_t)key * Hkv * kPD;
+      kreg[i] = *reinterpret_cast<const u32x4*>(kr + 8 * cc);
+      if (i < KPAR) {
+        const int pd = cc < RC ? (8 * cc < half ? 8 * cc + half : 8 * cc - half) : 8 * cc;
+        kpar[i < KPAR ? i : 0] = *reinterpret_cast<const u32x4*>(kr + pd);
       }
     }
 #pragma unroll
@@ -127,23 +126,18 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
       // table slice [32 keys][half] of cos and sin, as float4s
       const int e4 = tid + i * NT;  // float4 index within the slice
       const int row = e4 / (kHM / 4), j4 = e4 % (kHM / 4);
-      const int key = kt * kBK + row;
-      const f32x4 z = zero4();
-      creg[i] = z;
-      sreg[i] = z;
-      if (e4 < kBK * kHM / 4 && key < T && 4 * j4 < half) {
-        creg[i] = *reinterpret_cast<const f32x4*>(cos_t + (size_t)(pos0 + key) * half + 4 * j4);
-        sreg[i] = *reinterpret_cast<const f32x4*>(sin_t + (size_t)(pos0 + key) * half + 4 * j4);
-      }
+      const int key = min(kt * kBK + min(row, kBK - 1), T - 1);
+      const int jc = min(4 * j4, half - 4);  // entries past rot/2 are never read back
+      creg[i] = *reinterpret_cast<const f32x4*>(cos_t + (size_t)(pos0 + key) * half + jc);
+      sreg[i] = *reinterpret_cast<const f32x4*>(sin_t + (size_t)(pos0 + key) * half + jc);
     }
 #pragma unroll
     for (int i = 0; i < VUN; ++i) {
       const int u = tid + i * NT, dc = u >> 3, kq = u & 7;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int key = kt * kBK + 4 * kq + r;
-        const uint4 z = {0u, 0u, 0u, 0u};
-        vreg[i][r] = key < T ? *reinterpret_cast<const uint4*>(vbase + (size_t)key * Hkv * kPD + 8 * dc) : z;
+        const int key = min(kt * kBK + 4 * kq + r, T - 1);
+        vreg[i][r] = *reinterpret_cast<const u32x4*>(vbase + (size_t)key * Hkv * kPD + 8 * dc);
       }
     }
   };
@@ -166,43 +160,46 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
     for (int i = 0; i < KCH; ++i) {
       int row, cc;
       kchunk(tid + i * NT, row, cc);
-      uint4 w = kreg[i];
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      const bool kvalid = kt * kBK + row < T;
+      u32x4 w = kvalid ? kreg[i] : z;
       const int d = 8 * cc;
-      if (cc < RC && kt * kBK + row < T) {
+      if (i < KPAR && cc < RC && kvalid) {
         const float* cr = &rope_lds[buf][row][0];
         const float* sr = cr + kHM;
         const int j0 = d < half ? d : d - half;
         const float sg = d < half ? -1.f : 1.f;
-        const uint4 p = kpar[i];
-        const float x[8] = {bf16lo(w.x), bf16hi(w.x), bf16lo(w.y), bf16hi(w.y),
-                            bf16lo(w.z), bf16hi(w.z), bf16lo(w.w), bf16hi(w.w)};
-        const float y[8] = {bf16lo(p.x), bf16hi(p.x), bf16lo(p.y), bf16hi(p.y),
-                            bf16lo(p.z), bf16hi(p.z), bf16lo(p.w), bf16hi(p.w)};
+        const u32x4 p = kpar[i < KPAR ? i : 0];
+        const float x[8] = {bf16lo(w[0]), bf16hi(w[0]), bf16lo(w[1]), bf16hi(w[1]),
+                            bf16lo(w[2]), bf16hi(w[2]), bf16lo(w[3]), bf16hi(w[3])};
+        const float y[8] = {bf16lo(p[0]), bf16hi(p[0]), bf16lo(p[1]), bf16hi(p[1]),
+                            bf16lo(p[2]), bf16hi(p[2]), bf16lo(p[3]), bf16hi(p[3])};
         bf16x8 o8;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o8[j] = (__bf16)(x[j] * cr[j0 + j] + sg * y[j] * sr[j0 + j]);
-        w = *reinterpret_cast<const uint4*>(&o8);
+        w = __builtin_bit_cast(u32x4, o8);
       }
-      *reinterpret_cast<uint4*>(kl + row * kKS + 8 * cc) = w;
+      *reinterpret_cast<u32x4*>(kl + row * kKS + 8 * cc) = w;
     }
     __bf16* vl = vt_lds[buf];
 #pragma unroll
     for (int i = 0; i < VUN; ++i) {
       const int u = tid + i * NT, dc = u >> 3, kq = u & 7;
-      // transpose 4 keys x 8 dims -> 8 dims x 4 keys
-      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&vreg[i][0]);
-      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&vreg[i][1]);
-      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&vreg[i][2]);
-      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&vreg[i][3]);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vreg[i][r] = kt * kBK + 4 * kq + r < T ? vreg[i][r] : z;
+      // transpose 4 keys x 8 dims -> 8 dims x 4 keys (component selects: taking the address of a register array
+      // would move it to scratch)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int wi = e >> 1, sh = (e & 1) * 16;
-        const uint32_t a0 = (w0[wi] >> sh) & 0xffffu, a1 = (w1[wi] >> sh) & 0xffffu;
-        const uint32_t a2 = (w2[wi] >> sh) & 0xffffu, a3 = (w3[wi] >> sh) & 0xffffu;
-        uint2 pk;
-        pk.x = a0 | (a1 << 16);
-        pk.y = a2 | (a3 << 16);
-        *reinterpret_cast<uint2*>(vl + (8 * dc + e) * kVS + 4 * kq) = pk;
+        auto h16 = [&](const u32x4& r) -> uint32_t {
+          const uint32_t w = r[e >> 1];
+          return (e & 1) ? (w >> 16) : (w & 0xffffu);
+        };
+        u32x2 pk;
+        pk[0] = h16(vreg[i][0]) | (h16(vreg[i][1]) << 16);
+        pk[1] = h16(vreg[i][2]) | (h16(vreg[i][3]) << 16);
+        *reinterpret_cast<u32x2*>(vl + (8 * dc + e) * kVS + 4 * kq) = pk;
       }
     }
   };
@@ -224,12 +221,16 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
     if (kt + 1 < nkt) load_tile(kt + 1);
     // S^T = K Q^T: rows = 32 keys, cols = 32 queries
     const __bf16* kl = ks_lds[buf];
-    f32x16 s = zero16();
+    f32x16 s = zero16(), s2 = zero16();  // two independent chains over the 16 K steps
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {
-      const bf16x8 a = *reinterpret_cast<const bf16x8*>(kl + ln * kKS + 16 * ks + 8 * hh);
-      s = mfma32(a, qop[ks], s);
+    for (int ks = 0; ks < 16; ks += 2) {
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kl + ln * kKS + 16 * ks + 8 * hh);
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kl + ln * kKS + 16 * (ks + 1) + 8 * hh);
+      s = mfma32(a0, qop[ks], s);
+      s2 = mfma32(a1, qop[ks + 1], s2);
     }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] += s2[r];
     // online softmax along the keys of this lane's query. The running max is only moved (and O, l rescaled) when
     // a row max exceeds it by more than 8 (natural log units): p = exp(s - m) then stays <= e^8, exact enough in
     // fp32 and in the bf16 P operand, and most tiles skip the 128-register rescale.
@@ -273,11 +274,10 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const __bf16* vr = vl + (32 * mt + ln) * kVS + 16 * kk + 4 * hh;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 8);
-        uint4 w;
-        w.x = lo.x; w.y = lo.y; w.z = hi.x; w.w = hi.y;
-        o[mt] = mfma32(*reinterpret_cast<const bf16x8*>(&w), pb[kk], o[mt]);
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 8);
+        const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
+        o[mt] = mfma32(__builtin_bit_cast(bf16x8, w), pb[kk], o[mt]);
       }
     }
     if (kt + 1 < nkt) store_tile(kt + 1, buf ^ 1);
