@@ -5,8 +5,11 @@
   attn_prefill:    B = 1, T = 4096, causal, 8 query / 2 kv heads, head dim 256, RoPE theta 1e7 on dims 0..63,
                    gate [T, 8 * 256].
   attn_decode:     B in {3, 32}, context 8192, same heads, bf16 KV cache, one query per row, split-K.
+  hybrid stack:    Qwen3.5-0.8B shape (Q35Config), seeded random weights (init_weights), int8 per-output-channel MLP.
 q and k are L2-normalised per head, beta = sigmoid(randn), g = -softplus(randn) (log decay, alpha = exp(g)).
 """
+from dataclasses import dataclass
+
 import torch
 import torch.nn.functional as F
 
@@ -60,3 +63,84 @@ def rope_tables(n_pos, head_dim=256, partial_rotary_factor=0.25, theta=1e7):
 
 def to_device(d, device):
     return {k: (v.to(device) if torch.is_tensor(v) else v) for k, v in d.items()}
+
+
+@dataclass
+class Q35Config:
+    vocab: int = 151936
+    hidden: int = 1024
+    inter: int = 3584
+    layers: int = 24
+    n_heads: int = 8
+    n_kv: int = 2
+    head_dim: int = 256
+    lin_k_heads: int = 16
+    lin_v_heads: int = 16
+    lin_dk: int = 128
+    lin_dv: int = 128
+    conv_k: int = 4
+    rope_theta: float = 1e7
+    partial_rotary: float = 0.25
+    eps: float = 1e-6
+    full_attention_interval: int = 4
+    init_std: float = 0.02
+
+    def is_attention(self, layer):
+        """Layer pattern of HFcfg:113-115: every full_attention_interval-th layer is full attention."""
+        return (layer + 1) % self.full_attention_interval == 0
+
+    @property
+    def conv_dim(self):
+        return 2 * self.lin_k_heads * self.lin_dk + self.lin_v_heads * self.lin_dv
+
+    @property
+    def rot(self):
+        return int(self.head_dim * self.partial_rotary)
+
+
+def quantize_rows_int8(w):
+    """Per-output-channel symmetric int8: q = round(w / s), s = max|w_row| / 127 (rows = output channels)."""
+    s = w.abs().amax(dim=1, keepdim=True).clamp_min(1e-12) / 127.0
+    q = torch.round(w / s).clamp(-127, 127).to(torch.int8)
+    return q, s.squeeze(1).float()
+
+
+def init_weights(cfg: Q35Config, seed=0):
+    """Deterministic random init (seeded): normal(0, init_std) for every linear, the conv and the tied embedding;
+    decoder / q / k RMSNorm weights 0 (gain 1 + w = 1) and the gated norm weight 1 (HF:171, HF:813-820);
+    dt_bias = 1; A_log = log U(0, 16). MLP weights are stored int8 per output channel with fp32 scales."""
+    g = torch.Generator().manual_seed(seed)
+    std = cfg.init_std
+
+    def lin(o, i):
+        return torch.randn(o, i, generator=g) * std
+
+    H = cfg.hidden
+    W = {"embed": torch.randn(cfg.vocab, H, generator=g) * std, "norm": torch.zeros(H)}
+    for l in range(cfg.layers):
+        p = f"layers.{l}."
+        W[p + "input_layernorm"] = torch.zeros(H)
+        W[p + "post_attention_layernorm"] = torch.zeros(H)
+        if cfg.is_attention(l):
+            W[p + "q_proj"] = lin(cfg.n_heads * cfg.head_dim * 2, H)
+            W[p + "k_proj"] = lin(cfg.n_kv * cfg.head_dim, H)
+            W[p + "v_proj"] = lin(cfg.n_kv * cfg.head_dim, H)
+            W[p + "o_proj"] = lin(H, cfg.n_heads * cfg.head_dim)
+            W[p + "q_norm"] = torch.zeros(cfg.head_dim)
+            W[p + "k_norm"] = torch.zeros(cfg.head_dim)
+        else:
+            vd = cfg.lin_v_heads * cfg.lin_dv
+            W[p + "in_proj_qkv"] = lin(cfg.conv_dim, H)
+            W[p + "in_proj_z"] = lin(vd, H)
+            W[p + "in_proj_b"] = lin(cfg.lin_v_heads, H)
+            W[p + "in_proj_a"] = lin(cfg.lin_v_heads, H)
+            W[p + "conv1d"] = torch.randn(cfg.conv_dim, cfg.conv_k, generator=g) * std
+            W[p + "dt_bias"] = torch.ones(cfg.lin_v_heads)
+            W[p + "A_log"] = torch.empty(cfg.lin_v_heads).uniform_(0, 16, generator=g).log()
+            W[p + "norm"] = torch.ones(cfg.lin_dv)
+            W[p + "out_proj"] = lin(H, vd)
+        for name, (o, i) in (("gate_proj", (cfg.inter, H)), ("up_proj", (cfg.inter, H)), ("down_proj", (H, cfg.inter))):
+            q, s = quantize_rows_int8(lin(o, i))
+            W[p + name + ".q"] = q
+            W[p + name + ".s"] = s
+    return W
