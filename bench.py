@@ -31,6 +31,9 @@ ROTATE_BYTES = 640 << 20     # distinct bytes cycled through between two uses of
 # Algorithmic work per unit (minimum HBM bytes / nominal FLOPs)
 GDN_PREFILL_BYTES = 68_681_728      # q,k,v bf16 + g,beta fp32 + o bf16 + final S fp32 (T 4096, H 16, d 128)
 GDN_PREFILL_FLOPS = 1.190e10
+# HBM bytes one GDN prefill launch (prep + scan kernels) actually moves: rocprofv3 FETCH_SIZE / WRITE_SIZE per
+# dispatch, each scaled by what the counter reads for a 256 MiB device copy (profiles/gdn_prefill_b1_t4096_h16_traffic.md)
+GDN_PREFILL_TRAFFIC_BYTES = 272_700_000
 GDN_DECODE_STEP_BYTES = 2_130_048   # S read + write fp32 + q,k,v,o,g,beta (B 1, H 16, d 128)
 ATTN_PREFILL_FLOPS = 6.874e10       # 4 * D * Hq * T (T + 1) / 2, T 4096, Hq 8, D 256
 ATTN_PREFILL_BYTES = 58_720_256
@@ -171,6 +174,56 @@ def bench_attn_decode(torch, q35hip, workloads, steps, warmup, dev):
     return out
 
 
+def bench_copy(torch, dev, mb=256, reps=5):
+    """A plain device copy of known size (mb MiB read + mb MiB written per launch): the calibration point for the
+    FETCH_SIZE / WRITE_SIZE counters of a profiler run."""
+    src = torch.ones(mb << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    return {"bytes_per_launch": 2 * (mb << 20), "us": t * 1e6, "gbs": 2 * (mb << 20) / t / 1e9}
+
+
+def bench_stack(torch, q35hip, workloads, dev, steps=256):
+    """The Qwen3.5-0.8B-shaped hybrid stack (24 layers, int8 SwiGLU, tied 151,936 embedding), batch 3 steered rows:
+    2048-token prefill, then `steps` greedy decode steps, host-driven (no graph capture). Reported end to end."""
+    from q35hip import model as gm
+    cfg = workloads.Q35Config()
+    W = workloads.init_weights(cfg, seed=0)
+    g = gm.HybridModel(cfg, W, dev, max_len=2048 + steps + 8, rows=3)
+    del W
+    prompt = torch.randint(0, cfg.vocab, (1, 2048), generator=torch.Generator().manual_seed(0)).repeat(3, 1)
+    v = torch.randn(cfg.hidden, generator=torch.Generator().manual_seed(0))
+    g.set_vectors(torch.stack([v, -v]) * 0.1, [0, -1, 1])
+    for _ in range(2):  # warm: allocator, library handles
+        g.reset()
+        g.forward(prompt[:, :256])
+        g.forward(torch.zeros(3, 1, dtype=torch.long))
+    torch.cuda.synchronize()
+    g.reset()
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    e0.record()
+    logits, _ = g.forward(prompt)
+    e1.record()
+    for _ in range(steps):
+        nxt = logits.argmax(-1, keepdim=True)
+        logits, _ = g.forward(nxt)
+    e2.record()
+    torch.cuda.synchronize()
+    tp = e0.elapsed_time(e1) * 1e-3
+    td = e1.elapsed_time(e2) * 1e-3
+    return {"prefill_tok_s": 3 * 2048 / tp, "prefill_ms": tp * 1e3, "decode_tok_s": 3 * steps / td,
+            "decode_ms_per_step": td / steps * 1e3, "rows": 3, "prompt": 2048, "steps": steps,
+            "note": "host-driven decode loop (torch glue between the HIP ops), no graph capture"}
+
+
 def cpu_baseline(budget_s):
     """The CPU oracle (a PyTorch-CPU restatement of the reference's fp32 path) timed on this host: the chunked gated
     delta rule over the same T = 4096, 16-head workload, fp32, all threads torch uses."""
@@ -225,6 +278,13 @@ def main():
         res["gdn_decode"] = bench_gdn_decode(torch, q35hip, workloads, args.steps, args.warmup, dev)
         print(f"# gdn_decode {res['gdn_decode']}", file=sys.stderr, flush=True)
 
+    if only and "copy" in only:
+        res["copy"] = bench_copy(torch, dev)
+        print(f"# copy {res['copy']}", file=sys.stderr, flush=True)
+    if want("stack"):
+        res["stack"] = bench_stack(torch, q35hip, workloads, dev)
+        print(f"# stack {res['stack']}", file=sys.stderr, flush=True)
+
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     gp = res.get("gdn_prefill")
     line = {
@@ -243,7 +303,7 @@ def main():
         "config": {"workload": "gdn_chunked_prefill", "batch": 1, "seq_len": 4096, "heads": 16, "d_k": 128,
                    "d_v": 128, "chunk": 64, "state": "fp32", "activations": "bf16", "parallelism": "none (1 GPU)"},
         "roofline": ({"bound": "hbm", "achieved": round(gp["achieved_gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                      "frac": round(gp["frac"], 4), "traffic": None} if gp else None),
+                      "frac": round(gp["frac"], 4), "traffic": GDN_PREFILL_TRAFFIC_BYTES} if gp else None),
         "cpu_baseline": cpu,
         "breakdown": res,
     }
