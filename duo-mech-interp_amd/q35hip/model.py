@@ -1,18 +1,17 @@
 """Qwen3.5-shaped hybrid decoder stack on one MI355X: the hot path runs on the q35hip HIP ops, the glue around it
 (projections, causal conv, norms, int8-dequantised SwiGLU, embedding, lm head) on torch.
 
-Per-layer functions keep the reference's boundary: gated_deltanet_layer and gated_attention_layer are the mixers of
-one decoder layer (HF: transformers 5.15.0 models/qwen3_5/modeling_qwen3_5.py, Qwen3_5GatedDeltaNet.forward HF:432-543
-and Qwen3_5Attention.forward HF:656-701; engine/model.js:426-461 dispatches them per layer), and the residual
-steering add after one layer mirrors the layers[12] forward hook of tests/engine_ref.py:49-53 and the WGSL resAdd
-(engine/kernels.js:190-203). States are caller-owned tensors mutated in place (engine/model.js:333-336).
+The layer loop follows Model._forward (engine/model.js:404-466) and Qwen3_5DecoderLayer.forward (HF: transformers
+5.15.0 models/qwen3_5/modeling_qwen3_5.py, HF:753-793): RMSNorm(1 + w) -> mixer -> + residual -> RMSNorm(1 + w) ->
+SwiGLU MLP -> + residual -> [steering add]. The mixers and the steering add are the per-layer functions of
+q35hip.layers; the model owns their states (GDN conv / recurrent states, bf16 KV caches) and mutates them in place
+(engine/model.js:308-342).
 """
-import math
-
 import torch
 import torch.nn.functional as F
 
-from . import ops
+from . import layers
+from .layers import rmsnorm_1p
 
 
 class Q35Weights:
@@ -33,89 +32,9 @@ class Q35Weights:
         return self.t[k]
 
 
-def rmsnorm_1p(x, w, eps):
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * (1.0 + w.float())).to(x.dtype)
-
-
-def rope_rows(x, cos_rows, sin_rows):
-    """Rotate dims [0, rot) of x [B, T, H, D] with rotate_half pairs (glue for the KV-cache writer)."""
-    half = cos_rows.shape[-1]
-    rot = 2 * half
-    c = cos_rows[None, :, None, :]
-    s = sin_rows[None, :, None, :]
-    x1, x2 = x[..., :half].float(), x[..., half:rot].float()
-    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s, x[..., rot:].float()], dim=-1)
-
-
-def gated_deltanet_layer(cfg, W, l, h, state, decode):
-    """Gated DeltaNet mixer of layer l (HF:432-543). h: [B, T, H] fp32. state: dict with 'conv' [B, K-1, C] and
-    'rec' [B, Hv, dk, dv] fp32 (mutated in place on decode), or None on a fresh prefill. Returns (y, state)."""
-    p = f"layers.{l}."
-    B, T, _ = h.shape
-    mixed = h @ W[p + "in_proj_qkv"].T
-    z = h @ W[p + "in_proj_z"].T
-    b = h @ W[p + "in_proj_b"].T
-    a = h @ W[p + "in_proj_a"].T
-    w = W[p + "conv1d"]
-    K = w.shape[1]
-    prev = torch.zeros(B, K - 1, mixed.shape[-1], device=h.device) if state is None else state["conv"]
-    full = torch.cat([prev, mixed], dim=1)
-    conv = full[:, 0:T] * w[:, 0]
-    for i in range(1, K):
-        conv = conv + full[:, i:i + T] * w[:, i]
-    conv = F.silu(conv)
-    new_conv = full[:, -(K - 1):].contiguous()
-    kd = cfg.lin_k_heads * cfg.lin_dk
-    q = conv[..., :kd].reshape(B, T, cfg.lin_k_heads, cfg.lin_dk).contiguous()
-    k = conv[..., kd:2 * kd].reshape(B, T, cfg.lin_k_heads, cfg.lin_dk).contiguous()
-    v = conv[..., 2 * kd:].reshape(B, T, cfg.lin_v_heads, cfg.lin_dv).contiguous()
-    beta = torch.sigmoid(b).contiguous()
-    g = (-W[p + "A_log"].exp() * F.softplus(a + W[p + "dt_bias"])).contiguous()
-    if decode:
-        rec = state["rec"]
-        o = ops.gdn_decode_step_(q, k, v, g, beta, rec, use_qk_l2norm_in_kernel=True)
-    else:
-        rec0 = None if state is None else state["rec"]
-        o, rec = ops.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=rec0, output_final_state=True,
-                                            use_qk_l2norm_in_kernel=True)
-    o = o.reshape(-1, cfg.lin_dv)
-    on = o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + cfg.eps)
-    o = (W[p + "norm"] * on) * F.silu(z.reshape(-1, cfg.lin_dv))
-    return o.reshape(B, T, -1) @ W[p + "out_proj"].T, {"conv": new_conv, "rec": rec}
-
-
-def gated_attention_layer(cfg, W, l, h, cache, pos, cos, sin):
-    """Gated attention mixer of layer l (HF:656-701). cache: dict 'k', 'v' bf16 [B, Hkv, max_len, D] (rotated keys),
-    filled here for positions pos..pos+T-1. Prefill (pos == 0) runs the fused RoPE + causal flash kernel; decode
-    (T == 1) the split-K kernel over the cache."""
-    p = f"layers.{l}."
-    B, T, _ = h.shape
-    D = cfg.head_dim
-    qg = (h @ W[p + "q_proj"].T).view(B, T, cfg.n_heads, 2 * D)
-    q = rmsnorm_1p(qg[..., :D], W[p + "q_norm"], cfg.eps)
-    gate = qg[..., D:].reshape(B, T, cfg.n_heads * D)
-    k = rmsnorm_1p((h @ W[p + "k_proj"].T).view(B, T, cfg.n_kv, D), W[p + "k_norm"], cfg.eps)
-    v = (h @ W[p + "v_proj"].T).view(B, T, cfg.n_kv, D)
-    k_rot = rope_rows(k, cos[pos:pos + T], sin[pos:pos + T])
-    cache["k"][:, :, pos:pos + T] = k_rot.transpose(1, 2).to(torch.bfloat16)
-    cache["v"][:, :, pos:pos + T] = v.transpose(1, 2).to(torch.bfloat16)
-    if T > 1:
-        if pos != 0:
-            raise ValueError("gated_attention_layer: multi-token calls continue from position 0 only")
-        o = ops.gated_attention_prefill(q.to(torch.bfloat16).contiguous(), k.to(torch.bfloat16).contiguous(),
-                                        v.to(torch.bfloat16).contiguous(), gate.to(torch.bfloat16).contiguous(),
-                                        cos, sin, pos0=pos)
-    else:
-        cl = torch.full((B,), pos + 1, dtype=torch.int32, device=h.device)
-        o = ops.gated_attention_decode(q[:, 0].to(torch.bfloat16).contiguous(), cache["k"], cache["v"],
-                                       gate[:, 0].to(torch.bfloat16).contiguous(), cl, cos, sin).view(B, 1, -1)
-    return o.float() @ W[p + "o_proj"].T
-
-
-def mlp(W, l, h):
-    p = f"layers.{l}."
-    return (F.silu(h @ W[p + "gate_proj"].T) * (h @ W[p + "up_proj"].T)) @ W[p + "down_proj"].T
+def mlp(p, h):
+    """SwiGLU MLP (HF:704-717) with the int8 per-output-channel weights dequantised once at load."""
+    return (F.silu(h @ p["gate_proj"].T) * (h @ p["up_proj"].T)) @ p["down_proj"].T
 
 
 class HybridModel:
@@ -125,23 +44,29 @@ class HybridModel:
     def __init__(self, cfg, W, device, max_len=4096, rows=3, steer_layer=12):
         self.cfg, self.device, self.steer_layer = cfg, device, steer_layer
         self.W = W if isinstance(W, Q35Weights) else Q35Weights(W, device)
-        rot = int(cfg.head_dim * cfg.partial_rotary)
-        inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, rot, 2, dtype=torch.int64).to(torch.float) / rot))
-        ang = torch.arange(max_len, dtype=torch.float32)[:, None] * inv_freq[None, :]
-        self.cos, self.sin = ang.cos().contiguous().to(device), ang.sin().contiguous().to(device)
         self.max_len, self.rows = max_len, rows
         self.vecs = None
         self.vec_rows = None
-        self.caches = {}
+        self.params = [{n[len(f"layers.{l}."):]: t for n, t in self.W.t.items() if n.startswith(f"layers.{l}.")}
+                       for l in range(cfg.layers)]
+        self.states = []
         for l in range(cfg.layers):
             if cfg.is_attention(l):
                 shape = (rows, cfg.n_kv, max_len, cfg.head_dim)
-                self.caches[l] = {"k": torch.zeros(shape, dtype=torch.bfloat16, device=device),
-                                  "v": torch.zeros(shape, dtype=torch.bfloat16, device=device)}
+                self.states.append({"k": torch.zeros(shape, dtype=torch.bfloat16, device=device),
+                                    "v": torch.zeros(shape, dtype=torch.bfloat16, device=device)})
+            else:
+                self.states.append({
+                    "conv": torch.zeros(rows, cfg.conv_k - 1, cfg.conv_dim, device=device),
+                    "rec": torch.zeros(rows, cfg.lin_v_heads, cfg.lin_dk, cfg.lin_dv, device=device)})
         self.reset()
 
     def reset(self):
-        self.states = [None] * self.cfg.layers
+        """Start a new sequence: zero the recurrent and conv states (KV caches are overwritten by position)."""
+        for st in self.states:
+            if "rec" in st:
+                st["rec"].zero_()
+                st["conv"].zero_()
         self.pos = 0
 
     def set_vectors(self, vecs, vec_of_row):
@@ -156,21 +81,22 @@ class HybridModel:
         if self.pos + T > self.max_len:
             raise ValueError("context exceeds the KV cache")
         x = W["embed"][ids.to(self.device)]
-        decode = self.pos > 0 and T == 1
         collected = None
         last = cfg.layers - 1 if stop_after is None else stop_after
         for l in range(last + 1):
-            p = f"layers.{l}."
-            h = rmsnorm_1p(x, W[p + "input_layernorm"], cfg.eps)
+            p, st = self.params[l], self.states[l]
+            h = rmsnorm_1p(x, p["input_layernorm"], cfg.eps)
             if cfg.is_attention(l):
-                y = gated_attention_layer(cfg, W, l, h, self.caches[l], self.pos, self.cos, self.sin)
+                y = layers.gated_attention_layer(h, p, st["k"], st["v"], self.pos, rope_theta=cfg.rope_theta,
+                                                 partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps)
             else:
-                y, self.states[l] = gated_deltanet_layer(cfg, W, l, h, self.states[l], decode)
+                y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
+                                                head_k_dim=cfg.lin_dk, eps=cfg.eps)
             x = x + y
-            x = x + mlp(W, l, rmsnorm_1p(x, W[p + "post_attention_layernorm"], cfg.eps))
+            x = x + mlp(p, rmsnorm_1p(x, p["post_attention_layernorm"], cfg.eps))
             if l == self.steer_layer and self.vecs is not None:
                 x = x.contiguous()
-                ops.residual_steer_add_(x, self.vecs, self.vec_rows)
+                layers.residual_steer_add(x, self.vecs, self.vec_rows)
             if l == collect_layer:
                 collected = x.clone()
         self.pos += T

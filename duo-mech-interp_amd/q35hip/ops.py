@@ -211,13 +211,26 @@ _LIB.impl("resid_add_rows_", lambda x, vecs, vor: None, "Meta")
 
 
 # ---------------------------------------------------------------- Python entry points (reference signatures)
+def _hf_args(query, key, value, g, beta, initial_state):
+    """HF passes q / k / v as strided views of the conv output (HF:482-502) and beta in the model dtype: make them
+    dense, with g, beta and the state in fp32."""
+    query, key, value = query.contiguous(), key.contiguous(), value.contiguous()
+    if value.dtype != query.dtype:
+        value = value.to(query.dtype)
+    g, beta = g.float().contiguous(), beta.float().contiguous()
+    if initial_state is not None:
+        initial_state = initial_state.float().contiguous()
+    return query, key, value, g, beta, initial_state
+
+
 def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, output_final_state=False,
                                use_qk_l2norm_in_kernel=False, scale=None, **kwargs):
     """Drop-in for torch_recurrent_gated_delta_rule (HF:331-380): [B, T, H, D] layouts, returns
     (o in the input dtype, final fp32 state or None)."""
     scale = 1.0 / math.sqrt(key.shape[-1]) if scale is None else scale
-    o, S = torch.ops.q35.gdn_recurrent(query, key, value, g.float().contiguous(), beta.float().contiguous(),
-                                       initial_state, scale, bool(use_qk_l2norm_in_kernel))
+    query, key, value, g, beta, initial_state = _hf_args(query, key, value, g, beta, initial_state)
+    o, S = torch.ops.q35.gdn_recurrent(query, key, value, g, beta, initial_state, scale,
+                                       bool(use_qk_l2norm_in_kernel))
     return o, (S if output_final_state else None)
 
 
@@ -225,8 +238,9 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, initial_st
                            use_qk_l2norm_in_kernel=False, scale=None, **kwargs):
     """Drop-in for torch_chunk_gated_delta_rule (HF:249-327); chunk_size must be 64."""
     scale = 1.0 / math.sqrt(key.shape[-1]) if scale is None else scale
-    o, S = torch.ops.q35.gdn_chunk_prefill(query, key, value, g.float().contiguous(), beta.float().contiguous(),
-                                           initial_state, int(chunk_size), scale, bool(use_qk_l2norm_in_kernel))
+    query, key, value, g, beta, initial_state = _hf_args(query, key, value, g, beta, initial_state)
+    o, S = torch.ops.q35.gdn_chunk_prefill(query, key, value, g, beta, initial_state, int(chunk_size), scale,
+                                           bool(use_qk_l2norm_in_kernel))
     return o, (S if output_final_state else None)
 
 

@@ -70,10 +70,11 @@ def test_zero_state_closed_form():
 
 def test_linear_in_v_at_zero_state():
     inp = workloads.gdn_inputs(B=1, T=7, H=2, D=16, seed=7)
-    v2 = torch.randn_like(inp["v"])
-    a, _ = oracle.recurrent_gated_delta_rule(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], dtype=torch.float64)
+    v1 = inp["v"].double()
+    v2 = torch.randn(v1.shape, generator=torch.Generator().manual_seed(70), dtype=torch.float64)
+    a, _ = oracle.recurrent_gated_delta_rule(inp["q"], inp["k"], v1, inp["g"], inp["beta"], dtype=torch.float64)
     b, _ = oracle.recurrent_gated_delta_rule(inp["q"], inp["k"], v2, inp["g"], inp["beta"], dtype=torch.float64)
-    c, _ = oracle.recurrent_gated_delta_rule(inp["q"], inp["k"], 2 * inp["v"] - 3 * v2, inp["g"], inp["beta"],
+    c, _ = oracle.recurrent_gated_delta_rule(inp["q"], inp["k"], 2 * v1 - 3 * v2, inp["g"], inp["beta"],
                                              dtype=torch.float64)
     assert torch.allclose(c, 2 * a - 3 * b, atol=1e-10)
 
