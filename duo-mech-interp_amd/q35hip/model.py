@@ -136,7 +136,8 @@ def steered_greedy(model, prompt_ids, steps, steer_layer=12, dose=0.8, seed=0):
     cfg = model.cfg
     model.reset()
     model.vecs = None
-    _, resid = model.forward(prompt_ids[:1], stop_after=steer_layer, collect_layer=steer_layer)
+    # the states are sized for every row, so the unsteered calibration pass runs the whole batch and reads row 0
+    _, resid = model.forward(prompt_ids, stop_after=steer_layer, collect_layer=steer_layer)
     med = median_resid_norm(resid[0])
     v = torch.randn(cfg.hidden, generator=torch.Generator().manual_seed(seed))
     v = v / v.norm() * (dose * med)
