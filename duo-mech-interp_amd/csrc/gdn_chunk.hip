@@ -1,80 +1,67 @@
-// Gated DeltaNet, chunked form (prefill): chunk 64, UT/WY intra-chunk transform, fp32 state carried across chunks.
+// Gated DeltaNet, chunked form (prefill): chunk-64 UT/WY transform, fp32 state carried across the sequence.
 //
-// Math (HF:249-327 torch_chunk_gated_delta_rule; the decay masks and the 63-row forward substitution at HF:288-298).
-// Per (b, h) and chunk c of 64 positions, with gamma = cumsum(g) inside the chunk, q^ = l2norm(q) * scale,
-// k^ = l2norm(k), and L[t][s] = -beta_t (k^_t . k^_s) exp(gamma_t - gamma_s) for s < t (0 otherwise):
-//   T      = (I - L)^-1                                  (HF's substitution loop + eye)
-//   U      = T diag(beta) V                              (HF `value`)
-//   W      = T diag(beta exp(gamma)) K^                  (HF `k_cumdecay`)
-//   P[t][s]= (q^_t . k^_s) exp(gamma_t - gamma_s), s <= t  (HF intra-chunk `attn`)
-//   per chunk, in order:  Vn = U - W S ;  O = (Q^ exp(gamma)) S + P Vn ;  S <- exp(gamma_last) S + K~^T Vn
-//   with K~[s] = k^_s exp(gamma_last - gamma_s). Every exponent is <= 0 (g <= 0), so nothing overflows.
-// The l2 normalisation is applied as fp32 row / column scales of the products (q, k stay exact bf16 MFMA operands).
+// Math (HF:249-327 torch_chunk_gated_delta_rule; decay masks and the 63-row forward substitution at HF:288-298).
+// Per (b, h), with q^ = l2norm(q) * scale, k^ = l2norm(k) and, inside a span of positions, gamma = cumsum(g):
+//   L[t][s] = -beta_t (k^_t . k^_s) exp(gamma_t - gamma_s)  (s < t),     T = (I - L)^-1
+//   U = T diag(beta) V,   W = T diag(beta exp(gamma)) K^,   P[t][s] = (q^_t . k^_s) exp(gamma_t - gamma_s)  (s <= t)
+//   per span:  O = (Q^ exp(gamma)) S + P (U - W S),   S <- exp(gamma_last) S + K~^T (U - W S),
+//              K~[s] = k^_s exp(gamma_last - gamma_s).
+// Every exponent is <= 0 (g <= 0), so nothing overflows. HF applies this per chunk of 64; two consecutive chunks are
+// one span of 128 here: T of the pair is block lower-triangular with the two chunk-64 inverses T00, T11 on its
+// diagonal and T10 = T11 L10 T00 below, so W and U of the pair are the chunk-64 ones with the second chunk's
+// corrected by the first's:  W1 = T11 (K'1 + L10 W0),  U1 = T11 (V'1 + L10 U0).
 //
-// Kernel 1, gdn_chunk_prep_kernel: one block (4 waves, 64 KB LDS, two blocks per CU) per (chunk, head, row), all
-// chunks in parallel. 16-byte loads; K and V are transposed 8x8 in registers into XOR-swizzled LDS tiles (bank-
-// conflict-free writes and MFMA-operand reads); K K^T and Q K^T on bf16 MFMA with operands read straight from L2;
-// the 64x64 unit-lower-triangular inverse in fp32 (16x16 diagonal blocks by forward substitution in registers, then
-// one independent chain per block column for the off-diagonal blocks on fp32 MFMA); U and W on bf16 MFMA. Every
-// operand of kernel 2 is written pre-swizzled into MFMA lane order (16 contiguous bytes per lane).
-// Kernel 2, gdn_chunk_scan_kernel: one block of 2 waves per (16-column slice of the value dim, head, row).
-// Wave 0 carries the 128x16 fp32 state slice in MFMA accumulators through the chunks and does only the serial work
-// (Vn = U - W S, S <- e^g S + K~^T Vn), with the next chunk's records copied global -> LDS by global_load_lds one
-// chunk ahead (no registers held, explicit vmcnt waits). It hands the packed
-// state and Vn of each chunk to wave 1 through a double-buffered LDS slot (one barrier per chunk); wave 1 forms the
-// outputs O = Q~ S + P Vn off the serial path. The 8 slices of a head are placed on one XCD to share its L2.
+// The serial part is regrouped so that one scan step (one pair) is a single matrix product on the state:
+//   S <- exp(G) S + M S + Bm,    O = Q' S + R,   with  M = -K~^T W,  Bm = K~^T U,  Q' = Q^ exp(gamma) - P W,  R = P U
+// (exact algebra: U - W S substituted into both lines). M, Bm, Q', R depend on the inputs only, so all of them come
+// out of one fully parallel kernel, and the sequential kernel streams 128 x 128 bf16 matrices per 128 positions.
+//
+// Kernel 1, gdn_pair_prep_kernel: one block of 8 waves per (pair, head, row), all pairs in parallel. k, q, v rows
+// are staged in XOR-swizzled LDS tiles (row-major for the K K^T / Q K^T products, transposed for the products that
+// contract over positions); the two 64 x 64 inverses run in fp32 (16 x 16 diagonal blocks by forward substitution,
+// off-diagonal blocks by per-column chains on fp32 MFMA); every other product is bf16 MFMA with fp32 accumulation.
+// The products are oriented so that their accumulator tiles pack straight into the scan kernel's MFMA operand order,
+// and the records are written with 16- or 8-byte coalesced stores.
+// Kernel 2, gdn_pair_scan_kernel: 16 blocks per (row, head): 8 slices of 16 value columns x 2 halves of the output
+// rows. Each block carries its 128 x 16 fp32 state slice in registers (4 waves x 32 rows) and, per pair, does
+// 8 + 4 MFMAs per wave; the bf16 state is exchanged through LDS once per pair. Operands stream straight from L2 into
+// registers three pairs ahead; a fifth wave touches the records several pairs further ahead so that the first of the
+// 16 blocks to need a line finds it in L2. The 16 blocks of a head are placed on one XCD (they share its L2).
 #include "q35_common.h"
 #include "q35hip.h"
 
 namespace q35 {
 
-constexpr int kC = 64;          // chunk
-constexpr int kD = 128;         // Dk = Dv
-constexpr int kFS = kC + 4;     // row stride of the [64][64] fp32 LDS array
-constexpr int kPS = kC + 8;     // row stride of the [64][64] bf16 P array
-constexpr int kWS = kD + 8;     // row stride of the [64][128] bf16 W staging array (aliases the fp32 array)
+constexpr int kC = 64;        // chunk of the UT transform
+constexpr int kP = 128;       // positions per scan step (two chunks)
+constexpr int kD = 128;       // Dk = Dv
+constexpr int kFS = kC + 4;   // row stride (floats) of the fp32 64 x 64 inversion arrays
 
-// Per-(b, h, chunk) workspace records.
-constexpr size_t kWElems = 4 * 4 * 64 * 8;   // W   [mt 4][ks 4][lane][8] bf16
-constexpr size_t kQElems = 4 * 4 * 64 * 8;   // Q~  [mt 4][ks 4][lane][8] bf16: q rq_t scale exp(gamma_t)
-constexpr size_t kKTElems = 8 * 2 * 64 * 8;  // K~^T[mt 8][ks 2][lane][8] bf16
-constexpr size_t kPElems = 4 * 2 * 64 * 8;   // P   [mt 4][ks 2][lane][8] bf16
-constexpr size_t kUElems = 8 * 4 * 64 * 4;   // U   [slice 8][mt 4][lane][4] fp32
-constexpr size_t kEGElems = 64 * 4;          // exp(gamma_last) replicated [lane][4] fp32 (one 1 KB record)
+// Record of one (b, h, pair), bytes. Fragment order: [row tile][k step][lane][8] bf16, lane l holding row
+// 16 rt + l % 16 and columns 32 ks + kmap(l / 16, j) (kmap below); D order: [row tile][slice][lane][4] bf16, lane l
+// holding rows 16 rt + 4 (l / 16) + r of column 16 slice + l % 16 (the MFMA accumulator layout).
+constexpr size_t kRecM = 0;           // M  = -K~^T W   [128 d][128 d]   fragment order
+constexpr size_t kRecQ = 32768;       // Q'             [128 pos][128 d] fragment order
+constexpr size_t kRecB = 65536;       // Bm = K~^T U    [128 d][128 dv]  D order
+constexpr size_t kRecR = 98304;       // R  = P U       [128 pos][128 dv] D order
+constexpr size_t kRecE = 131072;      // exp(gamma_last) fp32
+constexpr size_t kRecBytes = 131328;  // 256-byte aligned
 
-struct ChunkWs {
-  __bf16* W;
-  __bf16* Q;
-  __bf16* KT;
-  __bf16* P;
-  float* U;
-  float* EG;
-};
+constexpr int kScanAhead = 3;    // pairs whose operands are held in registers ahead of use
+constexpr int kTouchAhead = 8;   // pairs ahead of use that the L2 warm-up wave touches
 
-static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+// k index of position j (0..7) of lane group g in a 32-wide K step fed from two 16-row accumulator tiles
+__device__ __forceinline__ int kmap(int g, int j) { return j < 4 ? 4 * g + j : 12 + 4 * g + j; }
 
-static ChunkWs chunk_ws_layout(void* base, size_t nbhc, size_t* total) {
-  ChunkWs w;
-  char* p = (char*)base;
-  size_t off = 0;
-  w.W = (__bf16*)(p + off);  off = align256(off + nbhc * kWElems * 2);
-  w.Q = (__bf16*)(p + off);  off = align256(off + nbhc * kQElems * 2);
-  w.KT = (__bf16*)(p + off); off = align256(off + nbhc * kKTElems * 2);
-  w.P = (__bf16*)(p + off);  off = align256(off + nbhc * kPElems * 2);
-  w.U = (float*)(p + off);   off = align256(off + nbhc * kUElems * 4);
-  w.EG = (float*)(p + off);  off = align256(off + nbhc * kEGElems * 4);
-  *total = off;
-  return w;
+// [128][128] bf16 LDS tiles, 256-byte rows of 16 segments of 16 bytes; segment s of row r lives at s ^ swz(r).
+// Both access patterns used (16 lanes reading one segment of 16 consecutive rows; 16 lanes writing one segment of
+// rows 8 c + e, c = 0..15) touch 16 distinct segments: conflict-free.
+__device__ __forceinline__ int swz16(int r) { return (r ^ (r >> 3)) & 15; }
+__device__ __forceinline__ int t128(int r, int c) { return r * 256 + ((((c >> 3) ^ swz16(r)) << 4) | ((c & 7) << 1)); }
+__device__ __forceinline__ bf16x8 frag(const char* tile, int r, int c) {
+  return *reinterpret_cast<const bf16x8*>(tile + t128(r, c));
 }
 
-// k index of position p (0..7) of lane group g in a 32-wide K step fed from two 16-row accumulator tiles
-__device__ __forceinline__ int kmap(int g, int p) { return p < 4 ? 4 * g + p : 12 + 4 * g + p; }
-
-// Transposed [128][64] bf16 tiles: 16-byte block b (8 positions) of row d lives at block b ^ swz(d).
-__device__ __forceinline__ int swz(int d) { return (d ^ (d >> 3)) & 7; }
-__device__ __forceinline__ int tofs(int d, int pos) { return d * kC + 8 * ((pos >> 3) ^ swz(d)) + (pos & 7); }
-
-__device__ __forceinline__ bf16x8 load8b(const __bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ bf16x8 load8b(const float* p) {
   const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
   bf16x8 r;
@@ -82,34 +69,24 @@ __device__ __forceinline__ bf16x8 load8b(const float* p) {
   for (int e = 0; e < 4; ++e) { r[e] = (__bf16)a[e]; r[4 + e] = (__bf16)b[e]; }
   return r;
 }
+// Raw loads as packed bf16 bits (fp32 input rounded to bf16), issued unconditionally from clamped addresses; rows
+// outside the sequence are zeroed afterwards with a select.
+__device__ __forceinline__ u32x4 raw8(const __bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x4 raw8(const float* p) {
+  const bf16x8 r = load8b(p);
+  return __builtin_bit_cast(u32x4, r);
+}
 __device__ __forceinline__ f32x4 load4f(const __bf16* p) {
-  const uint2 r = *reinterpret_cast<const uint2*>(p);
+  const u32x2 r = *reinterpret_cast<const u32x2*>(p);
   f32x4 o = {bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y)};
   return o;
 }
 __device__ __forceinline__ f32x4 load4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
-
-// Raw loads as packed bf16 bits (fp32 input rounded to bf16), issued unconditionally from clamped addresses so that
-// many loads stay in flight; rows outside the sequence are zeroed afterwards with a select, not a branch (a load
-// inside a branch whose result is used in the branch makes the compiler wait for it right there).
-__device__ __forceinline__ uint4 raw8(const __bf16* p) { return *reinterpret_cast<const uint4*>(p); }
-__device__ __forceinline__ uint4 raw8(const float* p) {
-  const bf16x8 r = load8b(p);
-  return *reinterpret_cast<const uint4*>(&r);
-}
-__device__ __forceinline__ uint2 raw4(const __bf16* p) { return *reinterpret_cast<const uint2*>(p); }
-__device__ __forceinline__ uint2 raw4(const float* p) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-  bf16x4 r;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = (__bf16)a[e];
-  return *reinterpret_cast<const uint2*>(&r);
-}
-__device__ __forceinline__ uint4 mask8(uint4 r, bool keep) {
-  const uint4 z = {0u, 0u, 0u, 0u};
+__device__ __forceinline__ u32x4 mask8(u32x4 r, bool keep) {
+  const u32x4 z = {0u, 0u, 0u, 0u};
   return keep ? r : z;
 }
-__device__ __forceinline__ float sumsq8(const uint4& r) {
+__device__ __forceinline__ float sumsq8(const u32x4& r) {
   const float x[8] = {bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y),
                       bf16lo(r.z), bf16hi(r.z), bf16lo(r.w), bf16hi(r.w)};
   float ss = 0.f;
@@ -118,18 +95,34 @@ __device__ __forceinline__ float sumsq8(const uint4& r) {
   return ss;
 }
 // sum of squares in the input precision (fp32 input: of the unrounded values)
-__device__ __forceinline__ float sumsq8_in(const __bf16* p, const uint4& r) { return sumsq8(r); }
-__device__ __forceinline__ float sumsq8_in(const float* p, const uint4&) {
+__device__ __forceinline__ float sumsq8_in(const __bf16*, const u32x4& r) { return sumsq8(r); }
+__device__ __forceinline__ float sumsq8_in(const float* p, const u32x4&) {
   const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 4; ++e) ss += a[e] * a[e] + b[e] * b[e];
   return ss;
 }
-
-__device__ __forceinline__ uint32_t half16(const uint4& r, int e) {
+__device__ __forceinline__ uint32_t half16(const u32x4& r, int e) {
   const uint32_t w = e < 2 ? r.x : e < 4 ? r.y : e < 6 ? r.z : r.w;
   return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+// 8x8 bf16 transpose: column e of 8 rows (one 16-byte row segment each) as one 16-byte segment
+__device__ __forceinline__ u32x4 column8(const u32x4 (&raw)[8], int e) {
+  u32x4 w;
+  w.x = half16(raw[0], e) | (half16(raw[1], e) << 16);
+  w.y = half16(raw[2], e) | (half16(raw[3], e) << 16);
+  w.z = half16(raw[4], e) | (half16(raw[5], e) << 16);
+  w.w = half16(raw[6], e) | (half16(raw[7], e) << 16);
+  return w;
+}
+__device__ __forceinline__ u32x2 pack4(float a, float b, float c, float d) {
+  bf16x4 r = {(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
+  return __builtin_bit_cast(u32x2, r);
+}
+__device__ __forceinline__ f32x4 unpack4(const u32x2& r) {
+  f32x4 o = {bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y)};
+  return o;
 }
 
 __device__ __forceinline__ f32x4 mfma_f32_16x16x4(float a, float b, const f32x4& c) {
@@ -147,146 +140,20 @@ __device__ __forceinline__ f32x4 mm16_f32(const float* X, int xs, const float* Y
   return acc;
 }
 
-template <typename Tin>
-__global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
-                                                                const Tin* __restrict__ v, const float* __restrict__ g,
-                                                                const float* __restrict__ beta, ChunkWs ws, int T,
-                                                                int NC, int Hk, int H, float scale, int l2norm) {
-  __shared__ __attribute__((aligned(16))) __bf16 kt[kD * kC];     // raw k, transposed + swizzled
-  __shared__ __attribute__((aligned(16))) __bf16 vt[kD * kC];     // raw v, transposed + swizzled
-  __shared__ __attribute__((aligned(16))) float Am[kC * kFS];     // L; T' diag blocks; T_ij (i > j) at block (j, i)
-  __shared__ __attribute__((aligned(16))) __bf16 pl[kC * kPS];    // P (bf16), lower triangle
-  __shared__ __attribute__((aligned(16))) float scr[4][16 * 17];  // per-wave 16x16 scratch
-  __shared__ float gam[kC], bet[kC], rkn[kC], rqn[kC];
+// First fragment of row tile rt in the packed lower-triangular P store (row tile rt has rt / 2 + 1 k steps).
+__device__ __forceinline__ int pbase(int rt) { return (rt >> 1) * ((rt >> 1) + 1) + (rt & 1) * ((rt >> 1) + 1); }
+constexpr int kPFrags = 20;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Unit lower-triangular 64 x 64 inverse in place (fp32, row stride kFS): on entry the strictly-lower part of `Am`
+// holds L (zeros on and above the diagonal of the diagonal blocks); on exit block (i, i) holds the strictly-lower
+// part of its diagonal inverse and, for i > j, T_ij is stored transposed in the unused upper block (j, i). Four
+// waves: wave bb inverts diagonal block bb, then runs block column bb. `bar` is a barrier of all waves of the block.
+template <typename Bar>
+__device__ __forceinline__ void invert64(float* Am, int bb, int lane, float* sc, Bar bar) {
   const int li = lane & 15, lg = lane >> 4;
-  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int kh = h / (H / Hk);
-  const int t0 = c * kC;
-  const int nvalid = min(kC, T - t0);
-  const size_t bhc = ((size_t)b * H + h) * NC + c;
-  auto krow = [&](int row) { return k + (((size_t)b * T + t0 + row) * Hk + kh) * kD; };
-  auto qrow = [&](int row) { return q + (((size_t)b * T + t0 + row) * Hk + kh) * kD; };
-
-  // 1. stage: threads 0-127 transpose k (and take |k| per row), threads 128-255 transpose v and take |q| per row;
-  //    unit = 8 rows x 8 dims. The last wave also forms the gates.
   {
-    const int u = tid & 127, rg = u >> 4, cc = u & 15;
-    const bool isK = tid < 128;
-    uint4 raw[8], rq[8];
-    const Tin* src[8];
-    const Tin* qsrc[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = min(8 * rg + i, nvalid - 1);
-      const size_t tok = (size_t)b * T + t0 + row;
-      src[i] = isK ? k + (tok * Hk + kh) * kD + 8 * cc : v + (tok * H + h) * kD + 8 * cc;
-      qsrc[i] = q + (tok * Hk + kh) * kD + 8 * cc;
-      raw[i] = raw8(src[i]);
-    }
-    if (!isK) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) rq[i] = raw8(qsrc[i]);
-    }
-    float ss[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool valid = 8 * rg + i < nvalid;
-      ss[i] = valid ? (isK ? sumsq8_in(src[i], raw[i]) : sumsq8_in(qsrc[i], rq[i])) : 0.f;
-      raw[i] = mask8(raw[i], valid);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) ss[i] += __shfl_xor(ss[i], off, 64);
-    }
-    if (cc == 0) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) (isK ? rkn : rqn)[8 * rg + i] = l2norm ? rsqrtf(ss[i] + 1e-6f) : 1.f;
-    }
-    __bf16* dst = isK ? kt : vt;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = 8 * cc + e;
-      uint4 w;
-      w.x = half16(raw[0], e) | (half16(raw[1], e) << 16);
-      w.y = half16(raw[2], e) | (half16(raw[3], e) << 16);
-      w.z = half16(raw[4], e) | (half16(raw[5], e) << 16);
-      w.w = half16(raw[6], e) | (half16(raw[7], e) << 16);
-      *reinterpret_cast<uint4*>(dst + d * kC + 8 * (rg ^ swz(d))) = w;
-    }
-    if (wave == 3) {  // gates: gamma = cumsum(g), beta (zero in the padded tail, as HF pads g and beta with 0)
-      float gv = 0.f, bv = 0.f;
-      if (lane < nvalid) {
-        const size_t idx = ((size_t)b * T + t0 + lane) * H + h;
-        gv = g[idx];
-        bv = beta[idx];
-      }
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float y = __shfl_up(gv, off, 64);
-        if (lane >= off) gv += y;
-      }
-      gam[lane] = gv;
-      bet[lane] = bv;
-    }
-  }
-  __syncthreads();
-
-  // 2. lower 16x16 tiles (mt >= nt) of K K^T and Q K^T from raw bf16 rows in L2 (all of the wave's operand loads
-  //    issued before the first MFMA); l2norm / scale / decay applied in fp32.
-  {
-    const int np = wave < 2 ? 3 : 2;  // tiles p = wave, wave + 4, wave + 8 (< 10)
-    bf16x8 opk[3][4], opq[3][4], opb[3][4];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const int p = wave + 4 * i;
-      const int mt = (p >= 1) + (p >= 3) + (p >= 6);
-      const int nt = p - mt * (mt + 1) / 2;
-      const int ra = 16 * mt + li, rb = 16 * nt + li;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int d0 = 32 * ks + 8 * lg;
-        const int rac = min(ra, nvalid - 1), rbc = min(rb, nvalid - 1);
-        const uint4 ka = mask8(raw8(krow(rac) + d0), ra < nvalid), qa = mask8(raw8(qrow(rac) + d0), ra < nvalid);
-        const uint4 kb = mask8(raw8(krow(rbc) + d0), rb < nvalid);
-        opk[i][ks] = *reinterpret_cast<const bf16x8*>(&ka);
-        opq[i][ks] = *reinterpret_cast<const bf16x8*>(&qa);
-        opb[i][ks] = *reinterpret_cast<const bf16x8*>(&kb);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      if (i < np) {
-        const int p = wave + 4 * i;
-        const int mt = (p >= 1) + (p >= 3) + (p >= 6);
-        const int nt = p - mt * (mt + 1) / 2;
-        f32x4 ak = zero4(), aq = zero4();
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          ak = mfma16(opk[i][ks], opb[i][ks], ak);
-          aq = mfma16(opq[i][ks], opb[i][ks], aq);
-        }
-        const int s = 16 * nt + li;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * mt + 4 * lg + r;
-          const float dec = s <= t ? __expf(gam[t] - gam[s]) : 0.f;
-          const float kk = ak[r] * rkn[t] * rkn[s];
-          const float qk = aq[r] * rqn[t] * scale * rkn[s];
-          Am[t * kFS + s] = s < t ? -bet[t] * kk * dec : 0.f;
-          pl[t * kPS + s] = (__bf16)(qk * dec);
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  // 3. diagonal 16x16 blocks: T' = strictly-lower part of (I - L_bb)^-1 by forward substitution in registers.
-  //    Lane j keeps column j; row i's original entries are broadcast with readlane before row i is overwritten.
-  {
-    const int bb = wave;
+    // forward substitution: lane j keeps column j; row i's original entries are broadcast with readlane before row i
+    // is overwritten
     float tc[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) tc[i] = Am[(16 * bb + i) * kFS + 16 * bb + li];
@@ -305,204 +172,467 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(const Tin* __res
       for (int i = 0; i < 16; ++i) Am[(16 * bb + i) * kFS + 16 * bb + lane] = tc[i];
     }
   }
-  __syncthreads();
-
-  // 4. off-diagonal blocks T_ij = (I + T'_ii) sum_{k=j}^{i-1} L_ik T_kj with T_jj = I + T'_jj. Block column j depends
-  //    only on its own earlier blocks, so wave j runs column j as an independent chain (no block barriers);
-  //    T_ij is stored transposed in the unused upper block (j, i).
-  {
-    auto blk = [&](int bi, int bj) { return Am + (16 * bi) * kFS + 16 * bj; };
-    const int j = wave;
-    float* sc = scr[wave];
-    for (int i = j + 1; i < 4; ++i) {
-      f32x4 acc;
-      const float* Lij = blk(i, j);
+  bar();
+  // T_ij = (I + T'_ii) sum_{k=j}^{i-1} L_ik T_kj with T_jj = I + T'_jj: column j is an independent chain
+  auto blk = [&](int bi, int bj) { return Am + (16 * bi) * kFS + 16 * bj; };
+  const int j = bb;
+  for (int i = j + 1; i < 4; ++i) {
+    f32x4 acc;
+    const float* Lij = blk(i, j);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = Lij[(4 * lg + r) * kFS + li];
-      acc = mm16_f32(Lij, kFS, blk(j, j), kFS, false, acc, lane);
-      for (int kk = j + 1; kk < i; ++kk) acc = mm16_f32(blk(i, kk), kFS, blk(j, kk), kFS, true, acc, lane);
+    for (int r = 0; r < 4; ++r) acc[r] = Lij[(4 * lg + r) * kFS + li];
+    acc = mm16_f32(Lij, kFS, blk(j, j), kFS, false, acc, lane);
+    for (int kk = j + 1; kk < i; ++kk) acc = mm16_f32(blk(i, kk), kFS, blk(j, kk), kFS, true, acc, lane);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[(4 * lg + r) * 17 + li] = acc[r];
-      __builtin_amdgcn_wave_barrier();
-      acc = mm16_f32(blk(i, i), kFS, sc, 17, false, acc, lane);
-      // store transposed: element (row 4 lg + r, col li) of T_ij at block (j, i) [li][4 lg + r]
-      *reinterpret_cast<f32x4*>(blk(j, i) + li * kFS + 4 * lg) = acc;
-      __builtin_amdgcn_wave_barrier();
-    }
-  }
-  __syncthreads();
-
-  // 5a. outputs independent of T: K~^T, Q~, P, exp(gamma_last)
-  const float gl = gam[kC - 1];
-  {
-    __bf16* KTo = ws.KT + bhc * kKTElems;
-    // K~^T [mt 8][ks 2][lane][p] = k[s][d] rk_s exp(gl - gamma_s), s = 32 ks + kmap(lg, p), d = 16 mt + li
-#pragma unroll
-    for (int m2 = 0; m2 < 2; ++m2) {
-      const int mt = 2 * wave + m2, d = 16 * mt + li;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int s0 = 32 * ks + 4 * lg, s1 = s0 + 16;
-        const uint2 lo = *reinterpret_cast<const uint2*>(kt + tofs(d, s0));
-        const uint2 hi = *reinterpret_cast<const uint2*>(kt + tofs(d, s1));
-        const float x[8] = {bf16lo(lo.x), bf16hi(lo.x), bf16lo(lo.y), bf16hi(lo.y),
-                            bf16lo(hi.x), bf16hi(hi.x), bf16lo(hi.y), bf16hi(hi.y)};
-        bf16x8 o8;
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-          const int s = p < 4 ? s0 + p : s1 + p - 4;
-          o8[p] = (__bf16)(x[p] * rkn[s] * __expf(gl - gam[s]));
-        }
-        *reinterpret_cast<bf16x8*>(KTo + ((mt * 2 + ks) * 64 + lane) * 8) = o8;
-      }
-    }
-    // Q~ [mt 4][ks 4][lane][p] = q[t][32 ks + kmap(lg, p)] rq_t scale exp(gamma_t), t = 16 mt + li
-    {
-      __bf16* Qo = ws.Q + bhc * kQElems;
-      const int mt = wave, t = 16 * mt + li;
-      const float f = rqn[t] * scale * __expf(gam[t]);
-      const Tin* qr = qrow(min(t, nvalid - 1));
-      f32x4 lo[4], hi[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        lo[ks] = load4f(qr + 32 * ks + 4 * lg);
-        hi[ks] = load4f(qr + 32 * ks + 16 + 4 * lg);
-      }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        bf16x8 o8;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          o8[e] = (__bf16)(t < nvalid ? lo[ks][e] * f : 0.f);
-          o8[4 + e] = (__bf16)(t < nvalid ? hi[ks][e] * f : 0.f);
-        }
-        *reinterpret_cast<bf16x8*>(Qo + ((mt * 4 + ks) * 64 + lane) * 8) = o8;
-      }
-    }
-    // P [mt 4][ks 2][lane][p] = P[16 mt + li][32 ks + kmap(lg, p)] (zero above the diagonal)
-    {
-      __bf16* Po = ws.P + bhc * kPElems;
-      const int mt = wave, t = 16 * mt + li;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        bf16x8 o8;
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-          const int s = 32 * ks + kmap(lg, p);
-          o8[p] = s <= t ? pl[t * kPS + s] : (__bf16)0.f;
-        }
-        *reinterpret_cast<bf16x8*>(Po + ((mt * 2 + ks) * 64 + lane) * 8) = o8;
-      }
-    }
-    if (tid < 64) {
-      const float e = __expf(gl);
-      const f32x4 e4 = {e, e, e, e};
-      *reinterpret_cast<f32x4*>(ws.EG + bhc * kEGElems + 4 * tid) = e4;
-    }
-  }
-
-  // 5b. A operands of U = T diag(beta) V and W = T diag(beta exp(gamma) rk) K from the assembled T
-  const int mt = wave, t = 16 * mt + li;
-  bf16x8 au[2], aw[2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      const int s = 32 * ks + 8 * lg + jj;
-      const int bs = s >> 4;
-      float tv;
-      if (bs == mt) tv = (t == s ? 1.f : 0.f) + (s < t ? Am[t * kFS + s] : 0.f);
-      else if (bs < mt) tv = Am[s * kFS + t];  // T_{mt, bs} stored transposed at block (bs, mt)
-      else tv = 0.f;
-      tv *= bet[s];
-      au[ks][jj] = (__bf16)tv;
-      aw[ks][jj] = (__bf16)(tv * __expf(gam[s]) * rkn[s]);
-    }
-  }
-  __syncthreads();  // every wave has read Am; it becomes the W staging array
-
-  // 5c. U (fp32, scan-kernel accumulator order) and W (bf16, staged for the swizzled store)
-  {
-    float* Uo = ws.U + bhc * kUElems;
-    __bf16* wl = reinterpret_cast<__bf16*>(Am);
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const int d = 16 * nt + li;
-      f32x4 accu = zero4(), accw = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int pos = 32 * ks + 8 * lg;
-        const bf16x8 bv = *reinterpret_cast<const bf16x8*>(vt + tofs(d, pos));
-        const bf16x8 bk = *reinterpret_cast<const bf16x8*>(kt + tofs(d, pos));
-        accu = mfma16(au[ks], bv, accu);
-        accw = mfma16(aw[ks], bk, accw);
-      }
-      *reinterpret_cast<f32x4*>(Uo + ((nt * 4 + mt) * 64 + lane) * 4) = accu;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) wl[(16 * mt + 4 * lg + r) * kWS + d] = (__bf16)accw[r];
-    }
-  }
-  __syncthreads();
-  {
-    __bf16* Wo = ws.W + bhc * kWElems;
-    const __bf16* wl = reinterpret_cast<const __bf16*>(Am);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const uint2 lo = *reinterpret_cast<const uint2*>(wl + t * kWS + 32 * ks + 4 * lg);
-      const uint2 hi = *reinterpret_cast<const uint2*>(wl + t * kWS + 32 * ks + 16 + 4 * lg);
-      uint4 o;
-      o.x = lo.x; o.y = lo.y; o.z = hi.x; o.w = hi.y;
-      *reinterpret_cast<uint4*>(Wo + ((mt * 4 + ks) * 64 + lane) * 8) = o;
-    }
+    for (int r = 0; r < 4; ++r) sc[(4 * lg + r) * 17 + li] = acc[r];
+    __builtin_amdgcn_wave_barrier();
+    acc = mm16_f32(blk(i, i), kFS, sc, 17, false, acc, lane);
+    *reinterpret_cast<f32x4*>(blk(j, i) + li * kFS + 4 * lg) = acc;
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
-// Hand-over slot from the recurrence wave to the output wave: packed state (4 B operands) and packed Vn (2).
-struct ScanSlot {
-  bf16x8 sb[4][64];
-  bf16x8 vb[2][64];
-};
-// LDS prefetch stages, filled by global_load_lds_dwordx4 (lane i's 16 bytes land at +16 i of each 1 KB record):
-// the recurrence wave's W, K~^T and own U slice; the output wave's Q~ and P.
-struct RecStage {
-  bf16x8 w[16][64];
-  bf16x8 kt[16][64];
-  f32x4 u[4][64];
-  f32x4 eg[64];
-};
-struct OutStage {
-  bf16x8 q[16][64];
-  bf16x8 p[8][64];
-};
+// T[t][s] of a 64 x 64 inverse stored by invert64 (t, s in 0..63)
+__device__ __forceinline__ float tinv(const float* Am, int t, int s) {
+  const int bt = t >> 4, bs = s >> 4;
+  if (bs == bt) return (t == s ? 1.f : 0.f) + (s < t ? Am[t * kFS + s] : 0.f);
+  if (bs < bt) return Am[s * kFS + t];
+  return 0.f;
+}
 
-// Copy n consecutive 1 KB records (src, 64 lanes x 16 B each) into LDS records (dst) without touching registers:
-// one global_load_lds_dwordx4 per record, M0 = LDS destination. The instructions are issued from inline asm so that
-// the compiler does not track them as LDS writes (its tracking would make every later LDS read wait for all of
-// them); the kernels order them with explicit vmcnt waits instead.
+template <typename Tin>
+__global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
+                                                               const Tin* __restrict__ v, const float* __restrict__ g,
+                                                               const float* __restrict__ beta, char* __restrict__ ws,
+                                                               int T, int NP, int Hk, int H, float scale, int l2norm) {
+  __shared__ __attribute__((aligned(16))) char R1[32768];           // k row-major -> k transposed
+  __shared__ __attribute__((aligned(16))) char R2[32768];           // q row-major -> v transposed -> U transposed
+  __shared__ __attribute__((aligned(16))) float R3[2 * 64 * kFS];   // L00, L11 -> T00, T11 (fp32) -> W transposed
+  __shared__ __attribute__((aligned(16))) bf16x8 L10f[8][64];       // L10 A fragments [rt 4][ks 2], natural k order
+  __shared__ __attribute__((aligned(16))) bf16x8 Pf[kPFrags][64];   // P A fragments (lower), natural k order
+  __shared__ float scr[8][16 * 17];
+  __shared__ float gam[kP], bet[kP], rkn[kP], rqn[kP];
+  // per position t: {gamma_t, -beta_t rk_t, rk_t, rq_t scale} and {beta_t e^gamma_t rk_t, beta_t,
+  // rk_t e^(gamma_last - gamma_t), rq_t scale e^gamma_t}
+  __shared__ f32x4 pa[kP], pb[kP];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  // grid (H, NP, B): the heads of one pair are dispatched together, so concurrently running blocks read whole
+  // [H, D] rows of q, k, v
+  const int h = blockIdx.x, p = blockIdx.y, b = blockIdx.z;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int kh = h / (H / Hk);
+  const int t0 = p * kP;
+  const int nvalid = min(kP, T - t0);
+  char* rec = ws + (((size_t)b * H + h) * NP + p) * kRecBytes;
+  char* WT = reinterpret_cast<char*>(R3);
+
+  // ---- 0. stage. Threads 0-255 hold an 8 x 8 unit of k (rows 8 rg.., dims 8 cc..), threads 256-511 one of v; the
+  //         units stay in registers for the transposed copies written after the K K^T phase. q goes row-major.
+  const int u = tid & 255, rg = u >> 4, cc = u & 15;
+  const bool isK = tid < 256;
+  u32x4 raw[8];
+  {
+    const Tin* src[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const size_t tok = (size_t)b * T + t0 + min(8 * rg + i, nvalid - 1);
+      src[i] = isK ? k + (tok * Hk + kh) * kD + 8 * cc : v + (tok * H + h) * kD + 8 * cc;
+      raw[i] = raw8(src[i]);
+    }
+    float ss[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool valid = 8 * rg + i < nvalid;
+      ss[i] = valid && isK ? sumsq8_in(src[i], raw[i]) : 0.f;
+      raw[i] = mask8(raw[i], valid);
+    }
+    if (isK) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) ss[i] += __shfl_xor(ss[i], off, 64);
+      }
+      if (cc == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rkn[8 * rg + i] = l2norm ? rsqrtf(ss[i] + 1e-6f) : 1.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(R1 + t128(8 * rg + i, 8 * cc)) = raw[i];
+    }
+  }
+  {
+    const int row = tid >> 2, s0 = 4 * (tid & 3);
+    const Tin* qs = q + (((size_t)b * T + t0 + min(row, nvalid - 1)) * Hk + kh) * kD;
+    u32x4 rq[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      rq[j] = raw8(qs + 8 * (s0 + j));
+      ss += sumsq8_in(qs + 8 * (s0 + j), rq[j]);
+    }
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    if ((tid & 3) == 0) rqn[row] = l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(R2 + t128(row, 8 * (s0 + j))) = mask8(rq[j], row < nvalid);
+  }
+  if (wave == 0) {  // gates: gamma = cumsum(g) over the pair, beta; zero past the sequence end (HF pads with 0)
+    float g0 = 0.f, g1 = 0.f, b0 = 0.f, b1 = 0.f;
+    const size_t base = ((size_t)b * T + t0) * H + h;
+    if (lane < nvalid) { g0 = g[base + (size_t)lane * H]; b0 = beta[base + (size_t)lane * H]; }
+    if (64 + lane < nvalid) { g1 = g[base + (size_t)(64 + lane) * H]; b1 = beta[base + (size_t)(64 + lane) * H]; }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y0 = __shfl_up(g0, off, 64), y1 = __shfl_up(g1, off, 64);
+      if (lane >= off) { g0 += y0; g1 += y1; }
+    }
+    const float tot0 = __shfl(g0, 63, 64);
+    gam[lane] = g0;
+    gam[64 + lane] = tot0 + g1;
+    bet[lane] = b0;
+    bet[64 + lane] = b1;
+  }
+  for (int i = tid; i < kPFrags * 64; i += 512) {
+    const bf16x8 z = {};
+    Pf[i >> 6][i & 63] = z;
+  }
+  __syncthreads();
+  if (tid < kP) {
+    const float gt = gam[tid], gl = gam[kP - 1];
+    const f32x4 a = {gt, -bet[tid] * rkn[tid], rkn[tid], rqn[tid] * scale};
+    const f32x4 c = {bet[tid] * __expf(gt) * rkn[tid], bet[tid], rkn[tid] * __expf(gl - gt),
+                     tid < nvalid ? rqn[tid] * scale * __expf(gt) : 0.f};
+    pa[tid] = a;
+    pb[tid] = c;
+  }
+  __syncthreads();
+
+  // ---- 1. K K^T over the 8 row tiles of the pair (the 36 tiles x >= y: L00, L11 and the cross block L10) and
+  //         Q K^T (P, the 36 tiles s-tile <= t-tile). Wave w takes the K K^T row x = w (w + 1 tiles) and the
+  //         P row 7 - w (8 - w tiles), so that one operand of each row is loaded once and the waves stay balanced.
+  //         Cross and P tiles are computed transposed (positions s down each lane's 4 rows) so that every lane's 4
+  //         results are 4 consecutive k indices of a natural-order A fragment (one 8-byte store).
+  {
+    auto kk_epilogue = [&](int x, int y, const f32x4& acc) {
+      if (x >= 4 && y < 4) {  // cross: rows s of tile y, column t of tile x
+        const int t = 16 * x + li, s0 = 16 * y + 4 * lg;
+        const f32x4 ic = pa[t];
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const f32x4 ir = pa[s0 + r];
+          v[r] = ic[1] * ir[2] * acc[r] * __expf(ic[0] - ir[0]);
+        }
+        bf16x8* dst = &L10f[(x - 4) * 2 + (s0 >> 5)][(t & 15) + 16 * ((s0 & 31) >> 3)];
+        *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(dst) + 2 * (s0 & 7)) = pack4(v[0], v[1], v[2], v[3]);
+      } else {  // diagonal chunk block: rows t of tile x, column s of tile y
+        const int cb = x >= 4, s = 16 * y + li;
+        const f32x4 ic = pa[s];
+        float* Am = R3 + cb * 64 * kFS;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * x + 4 * lg + r;
+          const f32x4 ir = pa[t];
+          Am[(t - 64 * cb) * kFS + (s - 64 * cb)] = s < t ? ir[1] * ic[2] * acc[r] * __expf(ir[0] - ic[0]) : 0.f;
+        }
+      }
+    };
+    auto p_epilogue = [&](int a, int bt, const f32x4& acc) {  // rows s of tile a, column t of tile bt
+      const int t = 16 * bt + li, s0 = 16 * a + 4 * lg;
+      const f32x4 ic = pa[t];
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const f32x4 ir = pa[s0 + r];
+        v[r] = s0 + r <= t ? ic[3] * ir[2] * acc[r] * __expf(ic[0] - ir[0]) : 0.f;
+      }
+      bf16x8* dst = &Pf[pbase(bt) + (s0 >> 5)][(t & 15) + 16 * ((s0 & 31) >> 3)];
+      *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(dst) + 2 * (s0 & 7)) = pack4(v[0], v[1], v[2], v[3]);
+    };
+    const int x = wv, bt = 7 - wv;
+    bf16x8 fx[4], fq[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      fx[ks] = frag(R1, 16 * x + li, 32 * ks + 8 * lg);
+      fq[ks] = frag(R2, 16 * bt + li, 32 * ks + 8 * lg);
+    }
+#pragma unroll
+    for (int y0 = 0; y0 < 8; y0 += 2) {
+      if (y0 > x) break;
+      bf16x8 fy[2][4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) fy[j][ks] = frag(R1, 16 * min(y0 + j, x) + li, 32 * ks + 8 * lg);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int y = y0 + j;
+        if (y > x) break;
+        f32x4 acc = zero4();
+        if (x >= 4 && y < 4) {
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) acc = mfma16(fy[j][ks], fx[ks], acc);
+        } else {
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) acc = mfma16(fx[ks], fy[j][ks], acc);
+        }
+        kk_epilogue(x, y, acc);
+      }
+    }
+#pragma unroll
+    for (int a0 = 0; a0 < 8; a0 += 2) {
+      if (a0 > bt) break;
+      bf16x8 fa[2][4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) fa[j][ks] = frag(R1, 16 * min(a0 + j, bt) + li, 32 * ks + 8 * lg);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (a0 + j > bt) break;
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc = mfma16(fa[j][ks], fq[ks], acc);
+        p_epilogue(a0 + j, bt, acc);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 2. transposed k and v from the registers; the two chunk inverses T00, T11 (waves 0-3, 4-7)
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    *reinterpret_cast<u32x4*>((isK ? R1 : R2) + t128(8 * cc + e, 8 * rg)) = column8(raw, e);
+  {
+    float* Am = R3 + (wave >> 2) * 64 * kFS;
+    invert64(Am, wave & 3, lane, scr[wave], [] { __syncthreads(); });
+  }
+  __syncthreads();
+  // A operands held in registers: rows 16 rt .. of T00 scaled for W0 (waves 0-3) or U0 (waves 4-7), and of T11.
+  // T[t][s] (layout of invert64): diagonal block row-major with an implicit unit diagonal, the block below it stored
+  // transposed; both candidates are read and the right one selected (no divergent loads).
+  const int rt = wv & 3;
+  const bool isW = wv < 4;
+  bf16x8 a0[2], a1[2];
+  {
+    const int t = 16 * rt + li;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int s0 = 32 * ks + 8 * lg, bs = s0 >> 4;
+      float d0[8], d1[8], x0[8], x1[8];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const f32x4 u0 = *reinterpret_cast<const f32x4*>(R3 + t * kFS + s0 + 4 * h2);
+        const f32x4 u1 = *reinterpret_cast<const f32x4*>(R3 + 64 * kFS + t * kFS + s0 + 4 * h2);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { d0[4 * h2 + e] = u0[e]; d1[4 * h2 + e] = u1[e]; }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        x0[j] = R3[(s0 + j) * kFS + t];
+        x1[j] = R3[64 * kFS + (s0 + j) * kFS + t];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int sj = s0 + j;
+        const float dg0 = (sj == t ? 1.f : 0.f) + (sj < t ? d0[j] : 0.f);
+        const float dg1 = (sj == t ? 1.f : 0.f) + (sj < t ? d1[j] : 0.f);
+        const float v0 = bs == rt ? dg0 : (bs < rt ? x0[j] : 0.f);
+        const float v1 = bs == rt ? dg1 : (bs < rt ? x1[j] : 0.f);
+        a0[ks][j] = (__bf16)(v0 * (isW ? pb[sj][0] : pb[sj][1]));
+        a1[ks][j] = (__bf16)v1;
+      }
+    }
+  }
+  __syncthreads();  // R3 (fp32 T) is free: it becomes W^T
+
+  // ---- 3. W0 = T00 diag(beta e^gamma rk) K0, U0 = T00 diag(beta) V0   (wave: row tile rt; W or U; 8 col tiles)
+  char* XT = isW ? WT : R2;  // this wave's destination (W^T or U^T, [d][pos])
+  {
+    const char* src = isW ? R1 : R2;
+    f32x4 acc[8];
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) {
+      acc[ct] = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) acc[ct] = mfma16(a0[ks], frag(src, 16 * ct + li, 32 * ks + 8 * lg), acc[ct]);
+    }
+    __syncthreads();  // every wave has read chunk 0 of V^T before U0 replaces it
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct)
+      *reinterpret_cast<u32x2*>(XT + t128(16 * ct + li, 16 * rt + 4 * lg)) =
+          pack4(acc[ct][0], acc[ct][1], acc[ct][2], acc[ct][3]);
+  }
+  __syncthreads();
+
+  // ---- 4. Z = L10 [W0 | U0] + [K'1 | V'1]   (chunk-1 columns of W^T / U^T; U^T overwrites V^T in place)
+  {
+    f32x4 acc[8];
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) {
+      acc[ct] = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        acc[ct] = mfma16(L10f[rt * 2 + ks][lane], frag(XT, 16 * ct + li, 32 * ks + 8 * lg), acc[ct]);
+    }
+    const char* raw_src = isW ? R1 : R2;
+    const int t = 64 + 16 * rt + 4 * lg;
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = isW ? pb[t + r][0] : pb[t + r][1];
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) {
+      const int d = 16 * ct + li;
+      const f32x4 x = unpack4(*reinterpret_cast<const u32x2*>(raw_src + t128(d, t)));
+      *reinterpret_cast<u32x2*>(XT + t128(d, t)) =
+          pack4(acc[ct][0] + x[0] * sc[0], acc[ct][1] + x[1] * sc[1], acc[ct][2] + x[2] * sc[2],
+                acc[ct][3] + x[3] * sc[3]);
+    }
+  }
+  __syncthreads();
+
+  // ---- 5. W1 = T11 Z_W, U1 = T11 Z_U
+  {
+    f32x4 acc[8];
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) {
+      acc[ct] = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) acc[ct] = mfma16(a1[ks], frag(XT, 16 * ct + li, 64 + 32 * ks + 8 * lg), acc[ct]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct)
+      *reinterpret_cast<u32x2*>(XT + t128(16 * ct + li, 64 + 16 * rt + 4 * lg)) =
+          pack4(acc[ct][0], acc[ct][1], acc[ct][2], acc[ct][3]);
+  }
+  __syncthreads();
+
+  // ---- 6. M = -K~^T W (computed as its transpose M^T = -W^T K~, whose 16 x 16 tiles pack straight into M's A
+  //         fragments) and Bm = K~^T U. Wave w: d tiles 4 (w / 4) .. + 3 of K~ (shared by both products), the d' tile
+  //         pair of k step w % 4 for M^T, the value-slice pair 2 (w % 4) .. + 1 for Bm.
+  const float gl = gam[kP - 1];
+  const int dq = 4 * (wv >> 2), kq = wv & 3;
+  {
+    bf16x8 F[4][4];  // K~ [positions 32 ks + 8 lg + j][d 16 (dq + i) + li]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) F[i][ks] = frag(R1, 16 * (dq + i) + li, 32 * ks + 8 * lg);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      float sc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sc[j] = pb[32 * ks + 8 * lg + j][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) F[i][ks][j] = (__bf16)((float)F[i][ks][j] * sc[j]);
+    }
+    bf16x8 wf[2][4], uf[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        wf[a][ks] = frag(WT, 16 * (2 * kq + a) + li, 32 * ks + 8 * lg);
+        uf[a][ks] = frag(R2, 16 * (2 * kq + a) + li, 32 * ks + 8 * lg);
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 lo = zero4(), hi = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        lo = mfma16(wf[0][ks], F[i][ks], lo);
+        hi = mfma16(wf[1][ks], F[i][ks], hi);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) { lo[r] = -lo[r]; hi[r] = -hi[r]; }
+      *reinterpret_cast<bf16x8*>(rec + kRecM + ((size_t)((dq + i) * 4 + kq) * 64 + lane) * 16) = pack8(lo, hi);
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc = mfma16(F[i][ks], uf[a][ks], acc);
+        *reinterpret_cast<u32x2*>(rec + kRecB + ((size_t)((dq + i) * 8 + 2 * kq + a) * 64 + lane) * 8) =
+            pack4(acc[0], acc[1], acc[2], acc[3]);
+      }
+    }
+  }
+
+  // ---- 7. Q' = Q^ e^gamma - P W (as its transpose) and R = P U. Wave w: position tiles 4 (w / 4) .. + 3 (P is zero
+  //         above the diagonal: row tile b has b / 2 + 1 k steps), the d' tile pair 2 (w % 4) .. + 1 for Q'^T, the
+  //         value-slice pair 2 (w % 4) .. + 1 for R.
+  {
+    bf16x8 wf[2][4], uf[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        wf[a][ks] = frag(WT, 16 * (2 * kq + a) + li, 32 * ks + 8 * lg);
+        uf[a][ks] = frag(R2, 16 * (2 * kq + a) + li, 32 * ks + 8 * lg);
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int bt = dq + i, nks = (bt >> 1) + 1;
+      const int t = 16 * bt + li;
+      const Tin* qr = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
+      f32x4 qt[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) qt[a] = load4f(qr + 16 * (2 * kq + a) + 4 * lg);
+      bf16x8 pf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) pf[ks] = Pf[pbase(bt) + min(ks, nks - 1)][lane];
+      f32x4 qp[2], rr[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) { qp[a] = zero4(); rr[a] = zero4(); }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks < nks) {
+#pragma unroll
+          for (int a = 0; a < 2; ++a) {
+            qp[a] = mfma16(wf[a][ks], pf[ks], qp[a]);
+            rr[a] = mfma16(pf[ks], uf[a][ks], rr[a]);
+          }
+        }
+      }
+      const float fq = pb[t][3];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qp[a][r] = qt[a][r] * fq - qp[a][r];
+      *reinterpret_cast<bf16x8*>(rec + kRecQ + ((size_t)(bt * 4 + kq) * 64 + lane) * 16) = pack8(qp[0], qp[1]);
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+        *reinterpret_cast<u32x2*>(rec + kRecR + ((size_t)(bt * 8 + 2 * kq + a) * 64 + lane) * 8) =
+            pack4(rr[a][0], rr[a][1], rr[a][2], rr[a][3]);
+    }
+  }
+  if (tid == 0) *reinterpret_cast<float*>(rec + kRecE) = __expf(gl);
+}
+
+// L2 warm-up: one global_load_lds_dword of one dword per 128-byte line into a dummy LDS area (no registers held);
+// the instruction is issued from inline asm so that the compiler does not order later LDS accesses behind it.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
-__device__ __forceinline__ void dma_records(const void* src, void* dst, int n, int lane) {
-  const char* s = reinterpret_cast<const char*>(src) + lane * 16;
-  const uint32_t d = lds_addr(dst);
-#pragma unroll
-  for (int i = 0; i < n; ++i)
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(d + i * 1024), "v"(s + i * 1024)
-                 : "memory", "m0");
+__device__ __forceinline__ void touch_line(const char* p, uint32_t lds_dummy) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_dummy), "v"(p) : "memory", "m0");
 }
 
-// Blocks are dispatched round-robin over the 8 XCDs (block i runs on XCD i % 8). The 8 column slices of one
-// (row, head) read the same W / K~^T / Q~ / P records, so they are mapped onto one XCD to share its L2: block L
-// serves XCD x = L % 8, and the j-th block of that XCD (j = L / 8) is slice j % 8 of head-row unit 8 (j / 8) + x.
-// When the number of (row, head) units is not a multiple of 8 the plain slice-fastest mapping is used.
-__device__ __forceinline__ void scan_block_coords(int L, int nunits, int& sl, int& unit) {
+// Blocks are dispatched round-robin over the 8 XCDs (block i runs on XCD i % 8). The 16 blocks of one (row, head)
+// read the same records, so they are mapped onto one XCD to share its L2: block L serves XCD x = L % 8, and the j-th
+// block of that XCD (j = L / 8) is block j % 16 of unit 8 (j / 16) + x. When the number of (row, head) units is not
+// a multiple of 8 the plain mapping is used.
+__device__ __forceinline__ void scan_coords(int L, int nunits, int& idx, int& unit) {
   if ((nunits & 7) == 0) {
     const int x = L & 7, j = L >> 3;
-    sl = j & 7;
-    unit = 8 * (j >> 3) + x;
+    idx = j & 15;
+    unit = 8 * (j >> 4) + x;
   } else {
-    sl = L & 7;
-    unit = L >> 3;
+    idx = L & 15;
+    unit = L >> 4;
   }
 }
 
@@ -513,126 +643,121 @@ __device__ __forceinline__ void store_out(__amdgpu_buffer_rsrc_t rc, int off_ele
   __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, x), rc, off_elems * 4, 0, 0);
 }
 
-// Number of vector-memory operations the output wave issues per chunk besides its prefetch: one store per output.
-constexpr int kOutStores = 16;
+// Operands of one pair for one wave of the scan kernel.
+struct PairOps {
+  bf16x8 m[2][4];  // M fragments of the wave's two state row tiles
+  bf16x8 qf[4];    // Q' fragments of the wave's output row tile
+  u32x2 bv[2];     // Bm (D order) of the two state row tiles
+  u32x2 rv;        // R (D order) of the output row tile
+  float eg;
+};
 
-template <typename Tin>
-__global__ __launch_bounds__(128) void gdn_chunk_scan_kernel(ChunkWs ws, const float* s_in, float* s_out,
-                                                             Tin* __restrict__ o, int T, int NC, int H, int B) {
-  __shared__ ScanSlot slot[2];
-  __shared__ RecStage rst[2];
-  __shared__ OutStage ost[2];
+template <typename Tout>
+__global__ __launch_bounds__(320, 1) void gdn_pair_scan_kernel(const char* __restrict__ ws, const float* s_in,
+                                                               float* s_out, Tout* __restrict__ o, int T, int NP,
+                                                               int H, int B) {
+  __shared__ bf16x8 slot[2][4][64];
+  __shared__ int dummy[64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int sl, unit;
-  scan_block_coords(blockIdx.x, H * B, sl, unit);
+  int idx, unit;
+  scan_coords(blockIdx.x, H * B, idx, unit);
+  const int sl = idx & 7, half = idx >> 3;
   const int h = unit % H, b = unit / H;
   const int li = lane & 15, lg = lane >> 4;
-  const int col = 16 * sl + li;
-  const size_t bh = (size_t)b * H + h;
+  const char* rec0 = ws + (size_t)unit * NP * kRecBytes;
 
-  if (wave == 0) {
-    // ---------------- recurrence wave ----------------
-    const size_t sbase = bh * kD * kD;
-    f32x4 S[8];
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) S[mt][r] = s_in ? s_in[sbase + (size_t)(16 * mt + 4 * lg + r) * kD + col] : 0.f;
-    auto prefetch = [&](int c, RecStage& st) {
-      const size_t bhc = bh * NC + c;
-      dma_records(ws.W + bhc * kWElems, &st.w[0][0], 16, lane);
-      dma_records(ws.KT + bhc * kKTElems, &st.kt[0][0], 16, lane);
-      dma_records(ws.U + bhc * kUElems + (size_t)sl * 4 * 64 * 4, &st.u[0][0], 4, lane);
-      dma_records(ws.EG + bhc * kEGElems, &st.eg[0], 1, lane);
-    };
-    prefetch(0, rst[0]);
-    for (int c = 0; c < NC; ++c) {
-      // issue the next chunk's 37 records (the last chunk re-reads itself: no branch), then wait for this chunk's,
-      // which were issued one iteration earlier
-      const int cn = c + 1 < NC ? c + 1 : c;
-      prefetch(cn, rst[(c + 1) & 1]);
-      asm volatile("s_waitcnt vmcnt(37)" ::: "memory");
-      const RecStage& st = rst[c & 1];
-      const float eg = st.eg[lane][0];
-      ScanSlot& sd = slot[c & 1];
-      bf16x8 sb[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        sb[ks] = pack8(S[2 * ks], S[2 * ks + 1]);
-        sd.sb[ks][lane] = sb[ks];
-      }
-      f32x4 vn[4];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc = mfma16(st.w[mt * 4 + ks][lane], sb[ks], acc);
-        const f32x4 u = st.u[mt][lane];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) vn[mt][r] = u[r] - acc[r];
-      }
-      bf16x8 vb[2];
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        vb[k2] = pack8(vn[2 * k2], vn[2 * k2 + 1]);
-        sd.vb[k2][lane] = vb[k2];
-      }
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) S[mt][r] *= eg;
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) S[mt] = mfma16(st.kt[mt * 2 + k2][lane], vb[k2], S[mt]);
-      }
-      lds_barrier();  // slot c & 1 is complete (the next chunk's records stay in flight)
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // drain the last (redundant) prefetch before LDS goes away
-    if (s_out) {
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s_out[sbase + (size_t)(16 * mt + 4 * lg + r) * kD + col] = S[mt][r];
-    }
-  } else {
-    // ---------------- output wave ----------------
-    // Outputs go through a buffer resource spanning row b's [T, H, 128] block: stores past the sequence end fall
-    // outside it and are dropped by the hardware, so the store path has no branch.
-    const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
-        o + (size_t)b * T * H * kD, 0, (int)((size_t)T * H * kD * sizeof(Tin)), 0x00020000);
-    auto prefetch = [&](int c, OutStage& st) {
-      const size_t bhc = bh * NC + c;
-      dma_records(ws.Q + bhc * kQElems, &st.q[0][0], 16, lane);
-      dma_records(ws.P + bhc * kPElems, &st.p[0][0], 8, lane);
-    };
-    prefetch(0, ost[0]);
-    for (int c = 0; c < NC; ++c) {
-      const int cn = c + 1 < NC ? c + 1 : c;
-      prefetch(cn, ost[(c + 1) & 1]);
-      // this chunk's 24 records are older than the 24 just issued and the previous chunk's stores
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(24 + kOutStores) : "memory");
-      lds_barrier();  // the recurrence wave has filled slot c & 1
-      const OutStage& st = ost[c & 1];
-      const ScanSlot& sd = slot[c & 1];
-      bf16x8 sb[4], vb[2];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) sb[ks] = sd.sb[ks][lane];
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) vb[k2] = sd.vb[k2][lane];
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc = mfma16(st.q[mt * 4 + ks][lane], sb[ks], acc);
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) acc = mfma16(st.p[mt * 2 + k2][lane], vb[k2], acc);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = c * kC + 16 * mt + 4 * lg + r;
-          store_out(orc, (t * H + h) * kD + col, acc[r], (Tin*)nullptr);
-        }
-      }
+  if (wave == 4) {
+    // ---------------- L2 warm-up wave: 64 of the 1024 record lines per pair, kTouchAhead pairs ahead ------------
+    const uint32_t d = lds_addr(dummy);
+    const size_t line = (size_t)(64 * idx + lane) * 128;
+    for (int pt = kScanAhead; pt < kTouchAhead && pt < NP; ++pt) touch_line(rec0 + (size_t)pt * kRecBytes + line, d);
+    for (int pp = 0; pp < NP; ++pp) {
+      const int pt = pp + kTouchAhead;
+      if (pt < NP) touch_line(rec0 + (size_t)pt * kRecBytes + line, d);
+      lds_barrier();
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+
+  const int w = wave;
+  const int col = 16 * sl + li;
+  const size_t sbase = (size_t)unit * kD * kD;
+  f32x4 S[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[i][r] = s_in ? s_in[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col] : 0.f;
+
+  auto load = [&](int pp, PairOps& op) {
+    const char* rec = rec0 + (size_t)min(pp, NP - 1) * kRecBytes;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        op.m[i][ks] = *reinterpret_cast<const bf16x8*>(rec + kRecM + ((size_t)((2 * w + i) * 4 + ks) * 64 + lane) * 16);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      op.qf[ks] = *reinterpret_cast<const bf16x8*>(rec + kRecQ + ((size_t)((4 * half + w) * 4 + ks) * 64 + lane) * 16);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      op.bv[i] = *reinterpret_cast<const u32x2*>(rec + kRecB + ((size_t)((2 * w + i) * 8 + sl) * 64 + lane) * 8);
+    op.rv = *reinterpret_cast<const u32x2*>(rec + kRecR + ((size_t)((4 * half + w) * 8 + sl) * 64 + lane) * 8);
+    op.eg = *reinterpret_cast<const float*>(rec + kRecE);
+  };
+
+  // Outputs go through a buffer resource spanning row b's [T, H, 128] block: stores past the sequence end fall
+  // outside it and are dropped by the hardware.
+  const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
+      o + (size_t)b * T * H * kD, 0, (int)((size_t)T * H * kD * sizeof(Tout)), 0x00020000);
+
+  auto step = [&](int pp, const PairOps& op) {
+    const bf16x8 own = pack8(S[0], S[1]);
+    slot[pp & 1][w][lane] = own;
+    lds_barrier();
+    bf16x8 sb[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sb[ks] = ks == w ? own : slot[pp & 1][ks][lane];
+    // outputs of this pair's half: O = Q' S + R
+    f32x4 acc = unpack4(op.rv);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = mfma16(op.qf[ks], sb[ks], acc);
+    const int tb = kP * pp + 64 * half + 16 * w + 4 * lg;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) store_out(orc, ((tb + r) * H + h) * kD + col, acc[r], (Tout*)nullptr);
+    // state: S <- e^G S + Bm + M S
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const f32x4 bm = unpack4(op.bv[i]);
+      f32x4 s;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = op.eg * S[i][r] + bm[r];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) s = mfma16(op.m[i][ks], sb[ks], s);
+      S[i] = s;
+    }
+  };
+
+  static_assert(kScanAhead == 3, "the pair loop below is unrolled by three");
+  PairOps o0, o1, o2;
+  load(0, o0);
+  load(1, o1);
+  load(2, o2);
+  for (int pp = 0; pp < NP; pp += 3) {
+    step(pp, o0);
+    load(pp + 3, o0);
+    if (pp + 1 < NP) step(pp + 1, o1);
+    load(pp + 4, o1);
+    if (pp + 2 < NP) step(pp + 2, o2);
+    load(pp + 5, o2);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (s_out && half == 0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_out[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col] = S[i][r];
   }
 }
 
@@ -642,10 +767,8 @@ extern "C" size_t q35_gdn_chunk_workspace_bytes(int64_t B, int64_t T, int64_t H,
                                                 int64_t chunk_size) {
   using namespace q35;
   if (B <= 0 || T <= 0 || H <= 0 || Dk != kD || Dv != kD || chunk_size != kC) return 0;
-  const size_t NC = (size_t)((T + kC - 1) / kC);
-  size_t total = 0;
-  chunk_ws_layout(nullptr, (size_t)B * H * NC, &total);
-  return total;
+  const size_t NP = (size_t)((T + kP - 1) / kP);
+  return (size_t)B * H * NP * kRecBytes;
 }
 
 extern "C" int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v, const float* g, const float* beta,
@@ -658,28 +781,28 @@ extern "C" int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v
   if (B <= 0 || T <= 0 || Hk <= 0 || H <= 0 || Dk <= 0 || Dv <= 0 || H % Hk != 0 || chunk_size <= 0)
     return Q35_EINVAL;
   if (Dk != kD || Dv != kD || chunk_size != kC) return Q35_EUNSUPPORTED;
-  if (B > 65535 || H > 65535 || H * B > (1 << 27) || T > ((int64_t)1 << 30) / (H > Hk ? H : Hk))
+  if (B > 65535 || H > 65535 || H * B > (1 << 26) || T > ((int64_t)1 << 30) / (H > Hk ? H : Hk))
     return Q35_EUNSUPPORTED;
   // the output buffer resource spans one row's [T, H, 128] block and is addressed with 32-bit byte offsets
   if (T * H * kD * (dtype == Q35_F32 ? 4 : 2) >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
   if (dtype != Q35_F32 && dtype != Q35_BF16) return Q35_EUNSUPPORTED;
-  const int64_t NC = (T + kC - 1) / kC;
-  if (NC > 0x7fffffff) return Q35_EUNSUPPORTED;
-  size_t need = 0;
-  ChunkWs ws = chunk_ws_layout(workspace, (size_t)B * H * NC, &need);
+  const int64_t NP = (T + kP - 1) / kP;
+  if (NP > 65535) return Q35_EUNSUPPORTED;
+  const size_t need = q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, chunk_size);
   if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  dim3 g1((unsigned)NC, (unsigned)H, (unsigned)B), g2((unsigned)(kD / 16 * H * B));
+  char* ws = static_cast<char*>(workspace);
+  dim3 g1((unsigned)H, (unsigned)NP, (unsigned)B), g2((unsigned)(16 * H * B));
   if (dtype == Q35_F32) {
-    hipLaunchKernelGGL(gdn_chunk_prep_kernel<float>, g1, dim3(256), 0, st, (const float*)q, (const float*)k,
-                       (const float*)v, g, beta, ws, (int)T, (int)NC, (int)Hk, (int)H, scale, use_qk_l2norm);
-    hipLaunchKernelGGL(gdn_chunk_scan_kernel<float>, g2, dim3(128), 0, st, ws, initial_state, final_state,
-                       (float*)out, (int)T, (int)NC, (int)H, (int)B);
+    hipLaunchKernelGGL(gdn_pair_prep_kernel<float>, g1, dim3(512), 0, st, (const float*)q, (const float*)k,
+                       (const float*)v, g, beta, ws, (int)T, (int)NP, (int)Hk, (int)H, scale, use_qk_l2norm);
+    hipLaunchKernelGGL(gdn_pair_scan_kernel<float>, g2, dim3(320), 0, st, ws, initial_state, final_state,
+                       (float*)out, (int)T, (int)NP, (int)H, (int)B);
   } else {
-    hipLaunchKernelGGL(gdn_chunk_prep_kernel<__bf16>, g1, dim3(256), 0, st, (const __bf16*)q, (const __bf16*)k,
-                       (const __bf16*)v, g, beta, ws, (int)T, (int)NC, (int)Hk, (int)H, scale, use_qk_l2norm);
-    hipLaunchKernelGGL(gdn_chunk_scan_kernel<__bf16>, g2, dim3(128), 0, st, ws, initial_state, final_state,
-                       (__bf16*)out, (int)T, (int)NC, (int)H, (int)B);
+    hipLaunchKernelGGL(gdn_pair_prep_kernel<__bf16>, g1, dim3(512), 0, st, (const __bf16*)q, (const __bf16*)k,
+                       (const __bf16*)v, g, beta, ws, (int)T, (int)NP, (int)Hk, (int)H, scale, use_qk_l2norm);
+    hipLaunchKernelGGL(gdn_pair_scan_kernel<__bf16>, g2, dim3(320), 0, st, ws, initial_state, final_state,
+                       (__bf16*)out, (int)T, (int)NP, (int)H, (int)B);
   }
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
