@@ -41,33 +41,8 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   __shared__ float comb_o[4][G][kDecD];
   __shared__ float comb_ml[4][G][2];
 
-  // 1. the G query heads of this kv head, rotated at position pos, in fp32
-  const __bf16* qb = q + ((size_t)b * Hq + (size_t)kvh * G) * kDecD;
-  const int half = rot >> 1;
-  for (int i = tid; i < G * kDecD; i += 256) {
-    const int hh = i / kDecD, d = i % kDecD;
-    float x = (float)qb[hh * kDecD + d];
-    if (d < rot) {
-      const int j = d < half ? d : d - half;
-      const float c = cos_t[(size_t)pos * half + j], sn = sin_t[(size_t)pos * half + j];
-      const float pr = (float)qb[hh * kDecD + (d < half ? d + half : d - half)];
-      x = d < half ? x * c - pr * sn : x * c + pr * sn;
-    }
-    qf[hh][d] = x;
-  }
-  __syncthreads();
-
-  // 2. A operand: row = head (l % 16 < G), k = dims 32 ks + 8 (l / 16) + j
+  // Online-softmax state and the per-tile helpers (qa, the query A operand, is filled in step 2 below)
   bf16x8 qa[8];
-  {
-    const int hr = lane & 15, kg = lane >> 4;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) qa[ks][j] = (__bf16)(hr < G ? qf[hr][32 * ks + 8 * kg + j] : 0.f);
-  }
-
-  // 3. online softmax over this wave's tiles
   const size_t kvbase = ((size_t)b * Hkv + kvh) * (size_t)max_len * kDecD;
   const __bf16* kb = kc + kvbase;
   const __bf16* vb = vc + kvbase;
@@ -82,15 +57,12 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
 
   const int kn = lane & 15, kg = lane >> 4;  // score-tile coordinates: key column, lane group
   const int d0 = 8 * (lane & 31), kp = lane >> 5;  // PV coordinates: 8 dims, key parity
-  for (int key0 = k_begin + kDecTile * wave; key0 < k_end; key0 += 4 * kDecTile) {
-    // issue the tile's K and V loads together: V does not depend on the scores
+  // K and V of one 16-key tile: keys past the span are loaded from a clamped row and masked (no branch)
+  auto tile_load = [&](int key0, bf16x8 (&kv8)[8], u32x4 (&vraw)[kDecTile / 2]) {
     const int key = key0 + kn;
-    const bool kvalid = key < k_end;
-    const __bf16* krow = kb + (size_t)(kvalid ? key : k_begin) * kDecD + 8 * kg;
-    bf16x8 kv8[8];
+    const __bf16* krow = kb + (size_t)(key < k_end ? key : k_begin) * kDecD + 8 * kg;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) kv8[ks] = *reinterpret_cast<const bf16x8*>(krow + 32 * ks);
-    u32x4 vraw[kDecTile / 2];  // rows past the span: loaded from a clamped row, zeroed by select (no branch)
 #pragma unroll
     for (int i = 0; i < kDecTile / 2; ++i) {
       const int vkey = key0 + 2 * i + kp;
@@ -98,6 +70,9 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
       const u32x4 ld = *reinterpret_cast<const u32x4*>(vb + (size_t)min(vkey, k_end - 1) * kDecD + d0);
       vraw[i] = vkey < k_end ? ld : z;
     }
+  };
+  auto tile_compute = [&](int key0, const bf16x8 (&kv8)[8], const u32x4 (&vraw)[kDecTile / 2]) {
+    const bool kvalid = key0 + kn < k_end;
     // scores S[head][key] for 16 keys
     f32x4 sc = zero4();
 #pragma unroll
@@ -144,6 +119,61 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
       }
     }
     __builtin_amdgcn_wave_barrier();
+  };
+  // first tile pair's K and V loads go out before the q prologue (they do not depend on q)
+  int key0 = k_begin + kDecTile * wave;
+  bf16x8 ka[8], kb2[8];
+  u32x4 va[kDecTile / 2], vb2[kDecTile / 2];
+  bool two = key0 + 4 * kDecTile < k_end;
+  if (key0 < k_end) {
+    tile_load(key0, ka, va);
+    if (two) tile_load(key0 + 4 * kDecTile, kb2, vb2);
+  }
+
+  // 1. the G query heads of this kv head, rotated at position pos, in fp32 (all loads of a thread issued together)
+  {
+    const __bf16* qb = q + ((size_t)b * Hq + (size_t)kvh * G) * kDecD;
+    const int half = rot >> 1;
+    constexpr int NQ = G * kDecD / 256;
+    float x[NQ], pr[NQ], c[NQ], sn[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int i = tid + 256 * u, hh = i / kDecD, d = i % kDecD;
+      const bool rotd = d < rot;
+      const int j = d < half ? d : d - half;
+      x[u] = (float)qb[hh * kDecD + d];
+      pr[u] = (float)qb[hh * kDecD + (rotd ? (d < half ? d + half : d - half) : d)];
+      c[u] = rotd ? cos_t[(size_t)pos * half + j] : 1.f;
+      sn[u] = rotd ? sin_t[(size_t)pos * half + j] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int i = tid + 256 * u, hh = i / kDecD, d = i % kDecD;
+      qf[hh][d] = d < half ? x[u] * c[u] - pr[u] * sn[u] : x[u] * c[u] + pr[u] * sn[u];
+    }
+  }
+  __syncthreads();
+
+  // 2. A operand: row = head (l % 16 < G), k = dims 32 ks + 8 (l / 16) + j
+  {
+    const int hr = lane & 15, kgq = lane >> 4;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qa[ks][j] = (__bf16)(hr < G ? qf[hr][32 * ks + 8 * kgq + j] : 0.f);
+  }
+
+  // 3. tiles key0 = k_begin + 16 wave + 64 i, two per iteration: both tiles' loads are in flight before the first
+  // tile's math (the second only when the wave has it); the first pair is issued before the q prologue above
+  for (; key0 < k_end;) {
+    tile_compute(key0, ka, va);
+    if (two) tile_compute(key0 + 4 * kDecTile, kb2, vb2);
+    key0 += 8 * kDecTile;
+    if (key0 < k_end) {
+      two = key0 + 4 * kDecTile < k_end;
+      tile_load(key0, ka, va);
+      if (two) tile_load(key0 + 4 * kDecTile, kb2, vb2);
+    }
   }
 
   // 4. fold the two key-parity halves, then merge the four waves in LDS
@@ -189,18 +219,19 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   }
 }
 
-// Merge over splits, gate, store. One block per (query head, row): the split weights exp(m_s - M) / L are formed
-// once in LDS, then four groups of 64 threads each fold a quarter of the splits for 4 dims per thread (16-byte
-// loads, all independent), and the four groups are summed in LDS.
+// Merge over splits, gate, store. One block per (query head, row, quarter of the head dims): the split weights
+// exp(m_s - M) are formed once in LDS, then four groups of 64 threads each fold a quarter of the splits for one dim
+// per thread (256-byte coalesced loads), and the four groups are summed in LDS.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __restrict__ part,
                                                                 const __bf16* __restrict__ gate,
                                                                 __bf16* __restrict__ out, int Hq, int Hkv, int S) {
-  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int h = blockIdx.x, b = blockIdx.y, dq = blockIdx.z, tid = threadIdx.x;
   const int G = Hq / Hkv, kvh = h / G, hh = h % G;
   const size_t sstride = (size_t)G * (kDecD + 2);
   const float* pb = part + ((size_t)b * Hkv + kvh) * S * sstride + (size_t)hh * (kDecD + 2);
-  extern __shared__ float wsh[];  // [S] weights, then [4][kDecD] partial sums
+  extern __shared__ float wsh[];  // [S] weights
   __shared__ float red[2][4];
+  __shared__ float accs[4][64];
   // global max over splits
   float mx = -INFINITY;
   for (int s = tid; s < S; s += 256) mx = fmaxf(mx, pb[s * sstride + kDecD]);
@@ -221,20 +252,22 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __r
   if ((tid & 63) == 0) red[1][tid >> 6] = ls;
   __syncthreads();
   const float Lsum = red[1][0] + red[1][1] + red[1][2] + red[1][3];
-  const int grp = tid >> 6, d4 = 4 * (tid & 63);
-  f32x4 acc = zero4();
-  for (int s = grp; s < S; s += 4) {
-    const float w = wsh[s];
-    const f32x4 o4 = *reinterpret_cast<const f32x4*>(pb + s * sstride + d4);
+  const int grp = tid >> 6, d = 64 * dq + (tid & 63);
+  float acc = 0.f;
+  int s = grp;
+  for (; s + 28 < S; s += 32) {  // eight independent loads in flight per thread
+    float x[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] += w * o4[e];
+    for (int u = 0; u < 8; ++u) x[u] = pb[(size_t)(s + 4 * u) * sstride + d];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += wsh[s + 4 * u] * x[u];
   }
-  float* accs = wsh + S;
-  *reinterpret_cast<f32x4*>(accs + grp * kDecD + d4) = acc;
+  for (; s < S; s += 4) acc += wsh[s] * pb[(size_t)s * sstride + d];
+  accs[grp][tid & 63] = acc;
   __syncthreads();
-  if (tid < kDecD) {
-    const float O = accs[tid] + accs[kDecD + tid] + accs[2 * kDecD + tid] + accs[3 * kDecD + tid];
-    const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + tid;
+  if (tid < 64) {
+    const float O = accs[0][tid] + accs[1][tid] + accs[2][tid] + accs[3][tid];
+    const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + d;
     const float res = Lsum > 0.f ? O / Lsum : 0.f;
     out[oi] = (__bf16)(res * sigmoidf_((float)gate[oi]));
   }
@@ -298,8 +331,8 @@ extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const v
     default: Q35_DEC_LAUNCH(8); break;
   }
 #undef Q35_DEC_LAUNCH
-  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3((unsigned)Hq, (unsigned)B), dim3(256),
-                     (size_t)(S + 4 * kDecD) * sizeof(float), st, part,
+  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3((unsigned)Hq, (unsigned)B, kDecD / 64), dim3(256),
+                     (size_t)S * sizeof(float), st, part,
                      (const __bf16*)gate, (__bf16*)out, (int)Hq, (int)Hkv, S);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
