@@ -6,38 +6,149 @@
 //   o_h    = softmax(q_h K^T * scale + causal mask) V     (fp32 softmax; kv head h / (Hq / Hkv))
 //   out    = o * sigmoid(gate)
 //
-// Decomposition: one block per (32-query block, group of up to 4 query heads sharing a kv head, batch row); wave w
-// of the block owns query head w of the group, so every K/V tile staged in LDS serves up to 4 heads. Query blocks
-// are issued longest (latest) first to shorten the causal tail.
-// Per 32-key tile each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (K from LDS, Q^T resident in
-// registers as the B operand), so a query's 16 scores sit in one lane (row max / sum need one cross-half exchange),
-// then O^T += V^T P^T where P^T's accumulator layout is used directly as the B operand (k permutation of the keys;
-// the V^T operand in LDS is read with the same permutation). K tiles are rotated while staged; V tiles are
-// transposed while staged (4 keys x 8 dims per thread). Two LDS stages, one barrier per tile.
+// Kernel 1, attn_kv_prep_kernel: K rotated once ([B, Hkv, Tp, D] bf16, keys padded to a multiple of 64 with zeros)
+// and V transposed once ([B, Hkv, D, Tp] bf16) into the workspace, so that the main loop stages its tiles with
+// plain global -> LDS copies. Inside each group of 16 keys, V^T stores keys in the order 0-3, 8-11, 4-7, 12-15
+// (bits 2 and 3 of the key index swapped): that is the key order in which an MFMA accumulator tile of scores is fed
+// back as a B operand, so every A fragment of V^T is one 16-byte read.
+// Kernel 2, attn_prefill_kernel: one block of 4 waves per (32-query block, group of up to 4 query heads sharing a kv
+// head, batch row); wave w owns query head w of the group, so every K/V tile in LDS serves up to 4 heads. Query
+// blocks are issued longest (latest) first. Per 64-key tile each wave computes S^T = K Q^T with 32 x 32 x 16 bf16
+// MFMAs (K from LDS, Q^T resident in registers as the B operand: a query's 32 scores sit in one lane pair), the
+// online softmax in registers, then O^T += V^T P^T with P^T's accumulator tiles used directly as B operands. Tiles
+// arrive by global_load_lds DMA into XOR-swizzled LDS (conflict-free 16-byte operand reads), two stages and one
+// barrier per tile (tile kt + 1 is copied while tile kt is computed), each wave copying a quarter of every tile.
 #include "q35_common.h"
 #include "q35hip.h"
 
 namespace q35 {
 
-constexpr int kPD = 256;            // head dim
-constexpr int kBQ = 32;             // queries per wave
-constexpr int kBK = 32;             // keys per tile
-constexpr int kKS = kPD + 8;        // K tile row stride (elements): 528 B, conflict-free 16-byte reads
-constexpr int kVS = kBK + 4;        // V^T row stride (elements): 72 B, conflict-free 8-byte reads
-constexpr int kRotMax = 64;         // rotary dims supported by the fused rotation (Qwen3.5: 64)
-constexpr int kHM = kRotMax / 2;    // cos / sin entries per position
+constexpr int kPD = 256;           // head dim
+constexpr int kBQ = 32;            // queries per wave
+constexpr int kBN = 64;            // keys per tile
+constexpr int kRotMax = 64;        // rotary dims supported (Qwen3.5: 64)
+
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// 16 bytes per lane from global to LDS (lane i's bytes land at M0 + 16 i); no registers are involved. Issued from
+// inline asm so the compiler does not order LDS reads behind it; completion is awaited with explicit vmcnt counts.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds_dst) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
+}
+
+// key order inside a group of 16 keys in V^T (an involution: swaps bits 2 and 3)
+__device__ __forceinline__ int vperm(int p) { return (p & 3) | ((p & 4) << 1) | ((p & 8) >> 1); }
+
+// ---------------------------------------------------------------------------------------------------------------
+// Kernel 1: one block of 256 threads per (64 keys, kv head, row). ROT (rotary dims) is a template parameter so that
+// the rotation pairs are compile-time register indices.
+template <int ROT>
+__global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+                                                           const float* __restrict__ cos_t,
+                                                           const float* __restrict__ sin_t, int pos0,
+                                                           __bf16* __restrict__ kr, __bf16* __restrict__ vt, int T,
+                                                           int Tp, int Hkv) {
+  static_assert(ROT % 16 == 0 && ROT <= kRotMax, "rotary dims");
+  constexpr int half = ROT / 2;
+  const int tid = threadIdx.x;
+  const int key0 = blockIdx.x * kBN, kvh = blockIdx.y, b = blockIdx.z;
+  const size_t head = (size_t)b * Hkv + kvh;
+  // K: thread = (row r, quarter cq of the dims); the rotary dims [0, rot) all sit in quarter 0
+  {
+    const int r = tid >> 2, cq = tid & 3;
+    const int key = key0 + r;
+    const bool valid = key < T;
+    const __bf16* src = k + (((size_t)b * T + min(key, T - 1)) * Hkv + kvh) * kPD + 64 * cq;
+    u32x4 w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = *reinterpret_cast<const u32x4*>(src + 8 * i);
+    if (ROT > 0 && cq == 0 && valid) {
+      float x[64];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[8 * i + 2 * e] = bf16lo(w[i][e]);
+          x[8 * i + 2 * e + 1] = bf16hi(w[i][e]);
+        }
+      const float* cr = cos_t + (size_t)(pos0 + key) * half;
+      const float* sr = sin_t + (size_t)(pos0 + key) * half;
+      float y[64];
+#pragma unroll
+      for (int d = 0; d < 64; ++d) {
+        if (d < ROT) {
+          const int j = d < half ? d : d - half;
+          const float pr = d < half ? -x[(d + half) & 63] : x[(d + 64 - half) & 63];
+          y[d] = x[d] * cr[j] + pr * sr[j];
+        } else {
+          y[d] = x[d];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        bf16x8 o8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o8[e] = (__bf16)y[8 * i + e];
+        w[i] = __builtin_bit_cast(u32x4, o8);
+      }
+    }
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    __bf16* dst = kr + (head * Tp + key) * kPD + 64 * cq;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(dst + 8 * i) = valid ? w[i] : z;
+  }
+  // V^T: thread = (8 keys kg, 8 dims dg); an 8 x 8 transpose in registers, each dim row written as two 8-byte
+  // pieces (keys kg*8 .. +3 and +4 .. +7 land 8 positions apart after the in-group permutation)
+  {
+    const int kg = tid >> 5, dg = tid & 31;
+    u32x4 w[8];
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int key = key0 + 8 * kg + i;
+      const u32x4 ld = *reinterpret_cast<const u32x4*>(v + (((size_t)b * T + min(key, T - 1)) * Hkv + kvh) * kPD +
+                                                      8 * dg);
+      w[i] = key < T ? ld : z;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      auto h16 = [&](const u32x4& r) -> uint32_t {
+        const uint32_t x = r[e >> 1];
+        return (e & 1) ? (x >> 16) : (x & 0xffffu);
+      };
+      u32x2 lo, hi;
+      lo[0] = h16(w[0]) | (h16(w[1]) << 16);
+      lo[1] = h16(w[2]) | (h16(w[3]) << 16);
+      hi[0] = h16(w[4]) | (h16(w[5]) << 16);
+      hi[1] = h16(w[6]) | (h16(w[7]) << 16);
+      const int d = 8 * dg + e;
+      const int p0 = 8 * kg;  // first key of this unit inside the tile
+      __bf16* row = vt + (head * kPD + d) * Tp + key0 + (p0 & ~15);
+      *reinterpret_cast<u32x2*>(row + vperm(p0 & 15)) = lo;
+      *reinterpret_cast<u32x2*>(row + vperm((p0 & 15) + 4)) = hi;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Kernel 2. LDS tiles: K [64 keys][512 B], 16-byte segment s of row r at s ^ (r & 15); V^T [256 dims][128 B],
+// segment s of row d at s ^ ((d >> 1) & 7). The copies apply the swizzle on the global side (lane i of a copy
+// fetches the segment that belongs at LDS position i).
+struct PfStage {
+  __bf16 k[kBN * kPD];
+  __bf16 v[kPD * kBN];
+};
 
 template <int GW>
-__global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ k, const __bf16* __restrict__ v,
+__global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
+    const __bf16* __restrict__ q, const __bf16* __restrict__ kr, const __bf16* __restrict__ vt,
     const __bf16* __restrict__ gate, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos0,
-    __bf16* __restrict__ out, int T, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb, int B) {
-  constexpr int NT = 64 * GW;
-  __shared__ __attribute__((aligned(16))) __bf16 ks_lds[2][kBK * kKS];
-  __shared__ __attribute__((aligned(16))) __bf16 vt_lds[2][kPD * kVS];
-  __shared__ __attribute__((aligned(16))) float rope_lds[2][kBK][2 * kHM];  // cos | sin of the staged tile's keys
+    __bf16* __restrict__ out, int T, int Tp, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb, int B) {
+  __shared__ PfStage stage[2];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_other = B * Hkv * ngroups;
   const int qb = nqb - 1 - (int)(blockIdx.x / n_other);
   const int rem = blockIdx.x % n_other;
@@ -48,10 +159,38 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
   const int h = kvh * G + hg * GW + wave;
   const int q0 = qb * kBQ;
   const int half = rot >> 1;
-
   const int ln = lane & 31, hh = lane >> 5;
+  const size_t head = (size_t)b * Hkv + kvh;
+  const char* kbase = reinterpret_cast<const char*>(kr + head * Tp * kPD);
+  const char* vbase = reinterpret_cast<const char*>(vt + head * kPD * Tp);
 
-  // ---- Q^T operand (B of S^T = K Q^T): lane holds query q0 + ln, dims 16 ks + 8 hh + j ----
+  // this wave's share of the copies of tile kt into stage s: CPW of the 32 K copies (2 rows each) and CPW of the
+  // 32 V^T copies (8 rows each)
+  constexpr int CPW = 32 / GW;
+  auto copy_tile = [&](int kt, int s) {
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));  // keep the per-lane source offsets out of registers between tiles
+    const int key0 = kt * kBN;
+    const uint32_t kl = lds_u32(&stage[s].k[0]), vl = lds_u32(&stage[s].v[0]);
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      const int c = CPW * wave + i;  // copy index 0..31
+      const int r = 2 * c + (lane >> 5), ps = lane & 31;
+      const int ls = ps ^ (r & 15);
+      dma16(kbase + (size_t)(key0 + r) * (kPD * 2) + 16 * ls, __builtin_amdgcn_readfirstlane(kl + 1024 * c));
+    }
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      const int c = CPW * wave + i;
+      const int d = 8 * c + (lane >> 3), ps = lane & 7;
+      const int ls = ps ^ ((d >> 1) & 7);
+      dma16(vbase + (size_t)d * (Tp * 2) + (size_t)key0 * 2 + 16 * ls, __builtin_amdgcn_readfirstlane(vl + 1024 * c));
+    }
+  };
+
+  const int nkt = (q0 + kBQ - 1) / kBN + 1;  // tiles holding keys 0 .. q0 + 31
+  copy_tile(0, 0);
+  // ---- Q^T operand (B of S^T = K Q^T): lane holds query q0 + ln, dims 16 ks + 8 hh + j, rotated ----
   bf16x8 qop[16];
   {
     const int t = q0 + ln;
@@ -61,14 +200,14 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
 #pragma unroll
     for (int ks = 0; ks < 16; ++ks) {
       const int d = 16 * ks + 8 * hh;
-      const uint4 raw = *reinterpret_cast<const uint4*>(qrow + d);
-      float x[8] = {bf16lo(raw.x), bf16hi(raw.x), bf16lo(raw.y), bf16hi(raw.y),
-                    bf16lo(raw.z), bf16hi(raw.z), bf16lo(raw.w), bf16hi(raw.w)};
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + d);
+      float x[8] = {bf16lo(raw[0]), bf16hi(raw[0]), bf16lo(raw[1]), bf16hi(raw[1]),
+                    bf16lo(raw[2]), bf16hi(raw[2]), bf16lo(raw[3]), bf16hi(raw[3])};
       if (tv && d < rot) {
         const int pd = d < half ? d + half : d - half;
-        const uint4 pr = *reinterpret_cast<const uint4*>(qrow + pd);
-        const float y[8] = {bf16lo(pr.x), bf16hi(pr.x), bf16lo(pr.y), bf16hi(pr.y),
-                            bf16lo(pr.z), bf16hi(pr.z), bf16lo(pr.w), bf16hi(pr.w)};
+        const u32x4 pr = *reinterpret_cast<const u32x4*>(qrow + pd);
+        const float y[8] = {bf16lo(pr[0]), bf16hi(pr[0]), bf16lo(pr[1]), bf16hi(pr[1]),
+                            bf16lo(pr[2]), bf16hi(pr[2]), bf16lo(pr[3]), bf16hi(pr[3])};
         const int j0 = d < half ? d : d - half;
         const float sg = d < half ? -1.f : 1.f;
 #pragma unroll
@@ -82,166 +221,72 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
     }
   }
 
-  // ---- staging of one K/V tile: global -> registers -> (rotate / transpose) -> LDS ----
-  // K chunks are numbered rotary chunks first (32 rows x RC chunks of 8 dims, RC = rot / 8), then the rest, so the
-  // rotary work spreads over the threads. The cos/sin rows of the tile's 32 keys are loaded with the tile and
-  // passed through LDS (one float4 of the table slice per thread per array).
-  constexpr int KCH = kBK * (kPD / 8) / NT;  // 16-byte K chunks per thread
-  constexpr int VUN = (kBK / 4) * (kPD / 8) / NT;  // (4 keys x 8 dims) V units per thread
-  constexpr int RQ = (kBK * kHM / 4 + NT - 1) / NT;  // float4s of each rope table slice per thread
-  const int RC = rot / 8;
-  // rotary chunks come first, so with rot <= 64 only the first KPAR chunks of a thread can need a partner chunk
-  constexpr int KPAR = (kBK * (kRotMax / 8) + NT - 1) / NT;
-  u32x4 kreg[KCH], kpar[KPAR], vreg[VUN][4];
-  f32x4 creg[RQ > 0 ? RQ : 1], sreg[RQ > 0 ? RQ : 1];
-  const __bf16* kbase = k + ((size_t)b * T * Hkv + kvh) * kPD;  // + (key * Hkv) * kPD
-  const __bf16* vbase = v + ((size_t)b * T * Hkv + kvh) * kPD;
-  auto kchunk = [&](int c, int& row, int& cc) {
-    if (c < kBK * RC) {
-      row = c / RC;
-      cc = c % RC;
-    } else {
-      const int c2 = c - kBK * RC;
-      row = c2 / (32 - RC);
-      cc = RC + c2 % (32 - RC);
-    }
-  };
-  auto load_tile = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      int row, cc;
-      kchunk(tid + i * NT, row, cc);
-      // loads are unconditional from clamped rows (a load whose use sits in a branch is waited for in place);
-      // rows past T are zeroed when the tile is written to LDS
-      const int key = min(kt * kBK + row, T - 1);
-      const __bf16* kr = kbase + (size_t)key * Hkv * kPD;
-      kreg[i] = *reinterpret_cast<const u32x4*>(kr + 8 * cc);
-      if (i < KPAR) {
-        const int pd = cc < RC ? (8 * cc < half ? 8 * cc + half : 8 * cc - half) : 8 * cc;
-        kpar[i < KPAR ? i : 0] = *reinterpret_cast<const u32x4*>(kr + pd);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < RQ; ++i) {
-      // table slice [32 keys][half] of cos and sin, as float4s
-      const int e4 = tid + i * NT;  // float4 index within the slice
-      const int row = e4 / (kHM / 4), j4 = e4 % (kHM / 4);
-      const int key = min(kt * kBK + min(row, kBK - 1), T - 1);
-      const int jc = min(4 * j4, half - 4);  // entries past rot/2 are never read back
-      creg[i] = *reinterpret_cast<const f32x4*>(cos_t + (size_t)(pos0 + key) * half + jc);
-      sreg[i] = *reinterpret_cast<const f32x4*>(sin_t + (size_t)(pos0 + key) * half + jc);
-    }
-#pragma unroll
-    for (int i = 0; i < VUN; ++i) {
-      const int u = tid + i * NT, dc = u >> 3, kq = u & 7;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = min(kt * kBK + 4 * kq + r, T - 1);
-        vreg[i][r] = *reinterpret_cast<const u32x4*>(vbase + (size_t)key * Hkv * kPD + 8 * dc);
-      }
-    }
-  };
-  auto store_tile = [&](int kt, int buf) {
-    if (rot > 0) {
-      float* rl = &rope_lds[buf][0][0];
-#pragma unroll
-      for (int i = 0; i < RQ; ++i) {
-        const int e4 = tid + i * NT;
-        const int row = e4 / (kHM / 4), j4 = e4 % (kHM / 4);
-        if (e4 < kBK * kHM / 4) {
-          *reinterpret_cast<f32x4*>(rl + row * (2 * kHM) + 4 * j4) = creg[i];
-          *reinterpret_cast<f32x4*>(rl + row * (2 * kHM) + kHM + 4 * j4) = sreg[i];
-        }
-      }
-      __syncthreads();
-    }
-    __bf16* kl = ks_lds[buf];
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      int row, cc;
-      kchunk(tid + i * NT, row, cc);
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      const bool kvalid = kt * kBK + row < T;
-      u32x4 w = kvalid ? kreg[i] : z;
-      const int d = 8 * cc;
-      if (i < KPAR && cc < RC && kvalid) {
-        const float* cr = &rope_lds[buf][row][0];
-        const float* sr = cr + kHM;
-        const int j0 = d < half ? d : d - half;
-        const float sg = d < half ? -1.f : 1.f;
-        const u32x4 p = kpar[i < KPAR ? i : 0];
-        const float x[8] = {bf16lo(w[0]), bf16hi(w[0]), bf16lo(w[1]), bf16hi(w[1]),
-                            bf16lo(w[2]), bf16hi(w[2]), bf16lo(w[3]), bf16hi(w[3])};
-        const float y[8] = {bf16lo(p[0]), bf16hi(p[0]), bf16lo(p[1]), bf16hi(p[1]),
-                            bf16lo(p[2]), bf16hi(p[2]), bf16lo(p[3]), bf16hi(p[3])};
-        bf16x8 o8;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o8[j] = (__bf16)(x[j] * cr[j0 + j] + sg * y[j] * sr[j0 + j]);
-        w = __builtin_bit_cast(u32x4, o8);
-      }
-      *reinterpret_cast<u32x4*>(kl + row * kKS + 8 * cc) = w;
-    }
-    __bf16* vl = vt_lds[buf];
-#pragma unroll
-    for (int i = 0; i < VUN; ++i) {
-      const int u = tid + i * NT, dc = u >> 3, kq = u & 7;
-      const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int r = 0; r < 4; ++r) vreg[i][r] = kt * kBK + 4 * kq + r < T ? vreg[i][r] : z;
-      // transpose 4 keys x 8 dims -> 8 dims x 4 keys (component selects: taking the address of a register array
-      // would move it to scratch)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        auto h16 = [&](const u32x4& r) -> uint32_t {
-          const uint32_t w = r[e >> 1];
-          return (e & 1) ? (w >> 16) : (w & 0xffffu);
-        };
-        u32x2 pk;
-        pk[0] = h16(vreg[i][0]) | (h16(vreg[i][1]) << 16);
-        pk[1] = h16(vreg[i][2]) | (h16(vreg[i][3]) << 16);
-        *reinterpret_cast<u32x2*>(vl + (8 * dc + e) * kVS + 4 * kq) = pk;
-      }
-    }
-  };
-
-  const int nkt_all = (T + kBK - 1) / kBK;
-  const int nkt = min(nkt_all, (q0 + kBQ - 1) / kBK + 1);
-
   f32x16 o[8];
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) o[mt] = zero16();
   float m_run = -INFINITY, l_run = 0.f;
   const int tq = q0 + ln;  // this lane's query
+  const int full_tiles = q0 / kBN;  // tiles entirely below this block's first query: no mask
 
-  load_tile(0);
-  store_tile(0, 0);
-  __syncthreads();
   for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nkt) load_tile(kt + 1);
-    // S^T = K Q^T: rows = 32 keys, cols = 32 queries
-    const __bf16* kl = ks_lds[buf];
-    f32x16 s = zero16(), s2 = zero16();  // two independent chains over the 16 K steps
+    const int s = kt & 1;
+    // this wave's copies of tile kt are its only ones in flight; after the barrier every wave's have landed and
+    // every wave is done with tile kt - 1, whose stage then receives tile kt + 1
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (kt + 1 < nkt) copy_tile(kt + 1, s ^ 1);
+    const char* kl = reinterpret_cast<const char*>(&stage[s].k[0]);
+    const char* vl = reinterpret_cast<const char*>(&stage[s].v[0]);
+    // the operand addresses below are recomputed every tile from an opaque copy of the lane id: hoisted out of the
+    // loop they would occupy some 60 registers, and the kernel is register-bound
+    int lo_ = threadIdx.x & 63;
+    asm volatile("" : "+v"(lo_));
+    const int ln = lo_ & 31, hh = lo_ >> 5;
+    // S^T = K Q^T for the two 32-key halves of the tile (rows = keys, cols = this wave's 32 queries): four
+    // independent accumulation chains, K fragments read four K steps at a time
+    f32x16 sc[2];
+    {
+      f32x16 acc[2][2];
 #pragma unroll
-    for (int ks = 0; ks < 16; ks += 2) {
-      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(kl + ln * kKS + 16 * ks + 8 * hh);
-      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(kl + ln * kKS + 16 * (ks + 1) + 8 * hh);
-      s = mfma32(a0, qop[ks], s);
-      s2 = mfma32(a1, qop[ks + 1], s2);
+      for (int ksub = 0; ksub < 2; ++ksub) { acc[ksub][0] = zero16(); acc[ksub][1] = zero16(); }
+#pragma unroll
+      for (int ks0 = 0; ks0 < 16; ks0 += 4) {
+        bf16x8 kf[2][4];
+#pragma unroll
+        for (int ksub = 0; ksub < 2; ++ksub) {
+          const int r = 32 * ksub + ln;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            kf[ksub][j] = *reinterpret_cast<const bf16x8*>(kl + r * 512 + 16 * ((2 * (ks0 + j) + hh) ^ (r & 15)));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int ksub = 0; ksub < 2; ++ksub) acc[ksub][j & 1] = mfma32(kf[ksub][j], qop[ks0 + j], acc[ksub][j & 1]);
+        // all eight reads first, then the eight MFMAs (the default schedule waits on each read pair in turn)
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      }
+#pragma unroll
+      for (int ksub = 0; ksub < 2; ++ksub)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc[ksub][i] = acc[ksub][0][i] + acc[ksub][1][i];
     }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] += s2[r];
-    // online softmax along the keys of this lane's query. The running max is only moved (and O, l rescaled) when
-    // a row max exceeds it by more than 8 (natural log units): p = exp(s - m) then stays <= e^8, exact enough in
-    // fp32 and in the bf16 P operand, and most tiles skip the 128-register rescale.
+    // online softmax along the keys of this lane's query (lane pair l, l ^ 32 holds all 64 keys). The running max
+    // only moves (and O, l are rescaled) when a tile max exceeds it by more than 8: p = exp(s - m) <= e^8 stays
+    // exact enough in fp32 and in the bf16 P operand, and most tiles skip the 128-register rescale.
     float mx = -INFINITY;
+    const bool masked = kt >= full_tiles;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kt * kBK + 8 * (r >> 2) + 4 * hh + (r & 3);
-      const float x = (key <= tq && key < T) ? s[r] * scale : -INFINITY;
-      s[r] = x;
-      mx = fmaxf(mx, x);
-    }
+    for (int ksub = 0; ksub < 2; ++ksub)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kt * kBN + 32 * ksub + 8 * (i >> 2) + 4 * hh + (i & 3);
+        float x = sc[ksub][i] * scale;
+        if (masked) x = (key <= tq && key < T) ? x : -INFINITY;
+        sc[ksub][i] = x;
+        mx = fmaxf(mx, x);
+      }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     if (__any(mx > m_run + 8.f)) {
       const float mn = fmaxf(m_run, mx);
@@ -251,37 +296,39 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[mt][r] *= corr;
+        for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
     }
     float ps = 0.f;
+    bf16x8 pb[4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = __expf(s[r] - m_run);
-      ps += s[r];
-    }
+    for (int ksub = 0; ksub < 2; ++ksub)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float p = __expf(sc[ksub][i] - m_run);
+        ps += p;
+        pb[2 * ksub + (i >> 3)][i & 7] = (__bf16)p;
+      }
     ps += __shfl_xor(ps, 32, 64);
     l_run += ps;
-    bf16x8 pb[2];
+    // O^T += V^T P^T: rows = 256 dims (8 tiles of 32), k = 64 keys (4 steps of 16); V^T fragments read two dim
+    // tiles at a time
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      pb[0][j] = (__bf16)s[j];
-      pb[1][j] = (__bf16)s[8 + j];
-    }
-    // O^T += V^T P^T: rows = 256 dims (8 tiles), k = 32 keys (2 steps)
-    const __bf16* vl = vt_lds[buf];
+    for (int mt0 = 0; mt0 < 8; mt0 += 2) {
+      bf16x8 vf[2][4];
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
+      for (int u = 0; u < 2; ++u) {
+        const int d = 32 * (mt0 + u) + ln;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const __bf16* vr = vl + (32 * mt + ln) * kVS + 16 * kk + 4 * hh;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 8);
-        const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
-        o[mt] = mfma32(__builtin_bit_cast(bf16x8, w), pb[kk], o[mt]);
+        for (int kk = 0; kk < 4; ++kk)
+          vf[u][kk] = *reinterpret_cast<const bf16x8*>(vl + d * 128 + 16 * ((2 * kk + hh) ^ ((d >> 1) & 7)));
       }
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) o[mt0 + u] = mfma32(vf[u][kk], pb[kk], o[mt0 + u]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     }
-    if (kt + 1 < nkt) store_tile(kt + 1, buf ^ 1);
-    __syncthreads();
   }
 
   // ---- epilogue: normalise, gate, store ----
@@ -293,8 +340,8 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int d = 32 * mt + 8 * c + 4 * hh;
-        const uint2 gr = *reinterpret_cast<const uint2*>(gate + rowo + d);
-        const float gv[4] = {bf16lo(gr.x), bf16hi(gr.x), bf16lo(gr.y), bf16hi(gr.y)};
+        const u32x2 gr = *reinterpret_cast<const u32x2*>(gate + rowo + d);
+        const float gv[4] = {bf16lo(gr[0]), bf16hi(gr[0]), bf16lo(gr[1]), bf16hi(gr[1])};
         bf16x4 ov;
 #pragma unroll
         for (int e = 0; e < 4; ++e) ov[e] = (__bf16)(o[mt][4 * c + e] * inv * sigmoidf_(gv[e]));
@@ -304,12 +351,20 @@ __global__ __launch_bounds__(64 * GW) void attn_prefill_kernel(
   }
 }
 
+static int64_t padded_T(int64_t T) { return (T + kBN - 1) / kBN * kBN; }
+
 }  // namespace q35
+
+extern "C" size_t q35_gated_attn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t Hkv, int64_t D) {
+  using namespace q35;
+  if (B <= 0 || T <= 0 || Hkv <= 0 || D != kPD) return 0;
+  return (size_t)2 * B * Hkv * padded_T(T) * kPD * sizeof(__bf16);
+}
 
 extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const void* gate,
                                       const float* cos, const float* sin, int64_t pos0, void* out, int64_t B,
                                       int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t rot, float scale,
-                                      q35_stream_t stream) {
+                                      void* workspace, size_t workspace_bytes, q35_stream_t stream) {
   using namespace q35;
   if (!q || !k || !v || !gate || !out) return Q35_EINVAL;
   if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D || pos0 < 0)
@@ -322,12 +377,32 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
   const int ngroups = (int)(G / GW);
   const int64_t nqb = (T + kBQ - 1) / kBQ;
   const int64_t nblocks = nqb * B * Hkv * ngroups;
-  if (nblocks > 0x7fffffff || T * Hq * D > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
+  const int64_t Tp = padded_T(T);
+  if (nblocks > 0x7fffffff || B > 65535 || Hkv > 65535 || Tp / kBN > 0x7fffffff || T * Hq * D > ((int64_t)1 << 40))
+    return Q35_EUNSUPPORTED;
+  // V^T rows are addressed with 32-bit byte offsets inside a head's [D, Tp] block
+  if (Tp * kPD * 2 >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
+  const size_t need = q35_gated_attn_prefill_workspace_bytes(B, T, Hkv, D);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define Q35_PF_LAUNCH(GG)                                                                                      \
-  hipLaunchKernelGGL(attn_prefill_kernel<GG>, dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q, \
-                     (const __bf16*)k, (const __bf16*)v, (const __bf16*)gate, cos, sin, (int)pos0, (__bf16*)out,  \
-                     (int)T, (int)Hq, (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B)
+  __bf16* kr = static_cast<__bf16*>(workspace);
+  __bf16* vt = kr + (size_t)B * Hkv * Tp * kPD;
+  const dim3 gp((unsigned)(Tp / kBN), (unsigned)Hkv, (unsigned)B);
+#define Q35_KV_LAUNCH(R)                                                                                         \
+  hipLaunchKernelGGL(attn_kv_prep_kernel<R>, gp, dim3(256), 0, st, (const __bf16*)k, (const __bf16*)v, cos, sin, \
+                     (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv)
+  switch (rot) {
+    case 0: Q35_KV_LAUNCH(0); break;
+    case 16: Q35_KV_LAUNCH(16); break;
+    case 32: Q35_KV_LAUNCH(32); break;
+    case 48: Q35_KV_LAUNCH(48); break;
+    default: Q35_KV_LAUNCH(64); break;
+  }
+#undef Q35_KV_LAUNCH
+#define Q35_PF_LAUNCH(GG)                                                                                         \
+  hipLaunchKernelGGL(attn_prefill_kernel<GG>, dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q,    \
+                     kr, vt, (const __bf16*)gate, cos, sin, (int)pos0, (__bf16*)out, (int)T, (int)Tp, (int)Hq,     \
+                     (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B)
   switch (GW) {
     case 1: Q35_PF_LAUNCH(1); break;
     case 2: Q35_PF_LAUNCH(2); break;

@@ -136,8 +136,12 @@ def _attn_prefill_impl(q, k, v, gate, cos, sin, pos0, scale):
     _require(tuple(gate.shape) == (B, T, Hq * D), "gate: [B, T, Hq * D]")
     rot = _tables_check(cos, sin, pos0 + T)
     out = torch.empty(B, T, Hq * D, dtype=q.dtype, device=q.device)
-    st = _lib.lib().q35_gated_attn_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(cos), _ptr(sin), int(pos0),
-                                           _ptr(out), B, T, Hq, Hkv, D, rot, float(scale), _stream(q))
+    L = _lib.lib()
+    nbytes = L.q35_gated_attn_prefill_workspace_bytes(B, T, Hkv, D)
+    _require(nbytes > 0, "unsupported attention shape")
+    ws = _workspace(nbytes, q.device)
+    st = L.q35_gated_attn_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(cos), _ptr(sin), int(pos0),
+                                  _ptr(out), B, T, Hq, Hkv, D, rot, float(scale), _ptr(ws), ws.numel(), _stream(q))
     check(st, "q35_gated_attn_prefill")
     return out
 

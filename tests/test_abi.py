@@ -37,7 +37,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 1
+    assert L.q35_abi_version() == 2
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -63,9 +63,14 @@ def test_validation_rejects_without_launching():
                                    1, 64, fake, 16, None) == 3
     # attention: head dim 128 unsupported, GQA ratio 3 unsupported, odd rot invalid
     assert L.q35_gated_attn_prefill(fake, fake, fake, fake, fake, fake, 0, fake, 1, 16, 8, 2, 128, 64, 0.1,
-                                    None) == 2
+                                    fake, 1 << 20, None) == 2
     assert L.q35_gated_attn_prefill(fake, fake, fake, fake, fake, fake, 0, fake, 1, 16, 6, 2, 256, 64, 0.1,
-                                    None) == 2
+                                    fake, 1 << 20, None) == 2
+    # prefill workspace: head dim other than 256 has none; too small a workspace is rejected
+    assert L.q35_gated_attn_prefill_workspace_bytes(1, 100, 2, 128) == 0
+    assert L.q35_gated_attn_prefill_workspace_bytes(1, 100, 2, 256) == 2 * 2 * 128 * 256 * 2
+    assert L.q35_gated_attn_prefill(fake, fake, fake, fake, fake, fake, 0, fake, 1, 100, 8, 2, 256, 64, 0.1,
+                                    fake, 16, None) == 3
     assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 8, 2, 256, 128, 63, 0.1, 0,
                                    fake, 1 << 20, None) == 1
     assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 8, 2, 256, 128, 64, 0.1, 0,
