@@ -48,10 +48,16 @@ __global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restr
                                                            const float* __restrict__ cos_t,
                                                            const float* __restrict__ sin_t, int pos0,
                                                            __bf16* __restrict__ kr, __bf16* __restrict__ vt, int T,
-                                                           int Tp, int Hkv) {
+                                                           int Tp, int Hkv, int* __restrict__ cnt, int ncnt) {
   static_assert(ROT % 16 == 0 && ROT <= kRotMax, "rotary dims");
   constexpr int half = ROT / 2;
   const int tid = threadIdx.x;
+  // the attention kernel's split-block arrival counters start every launch at zero
+  {
+    const int lb = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const int nb = gridDim.x * gridDim.y * gridDim.z;
+    for (int i = lb * 256 + tid; i < ncnt; i += nb * 256) cnt[i] = 0;
+  }
   const int key0 = blockIdx.x * kBN, kvh = blockIdx.y, b = blockIdx.z;
   const size_t head = (size_t)b * Hkv + kvh;
   // K: thread = (row r, quarter cq of the dims); the rotary dims [0, rot) all sit in quarter 0
@@ -140,17 +146,65 @@ struct PfStage {
   __bf16 v[kPD * kBN];
 };
 
+// Work items. Query block qb needs key tiles 0 .. nkt(qb) - 1, so the causal blocks range from 1 to ~T/64 tiles. With
+// a split length Ls > 0, every block with more than Ls tiles (qb >= 2 Ls) is run as two items, tiles [0, Ls) and
+// [Ls, nkt), whose (O, m, l) are merged by whichever finishes second; the others run whole. Items are numbered
+// longest first: all first halves (Ls tiles each), then second halves and whole blocks alternately, each in
+// decreasing length, so that the hardware's in-order dispatch to free CUs balances the CUs' total tiles.
+constexpr int kPartFloats = 8192 + 128;  // one wave's partial: O^T [32 x 256] fp32 in accumulator order, m[64], l[64]
+
+struct PfItem {
+  int qb, kt0, kt1, half;  // half: -1 for a whole block, else 0 / 1
+};
+
+__host__ __device__ inline int pf_tiles(int qb) { return (qb * kBQ + kBQ - 1) / kBN + 1; }
+
+__host__ __device__ inline PfItem pf_item(int idx, int nqb, int Ls) {
+  if (Ls == 0) {
+    const int qb = nqb - 1 - idx;
+    return {qb, 0, pf_tiles(qb), -1};
+  }
+  const int qs = 2 * Ls, nsq = nqb - qs;  // blocks qs .. nqb-1 are split
+  if (idx < nsq) return {nqb - 1 - idx, 0, Ls, 0};
+  const int j = idx - nsq, m2 = nsq < qs ? nsq : qs;
+  bool second;
+  int p;
+  if (j < 2 * m2) {
+    p = j >> 1;
+    second = (j & 1) == 0;
+  } else {
+    p = m2 + (j - 2 * m2);
+    second = nsq > qs;
+  }
+  if (second) {
+    const int qb = nqb - 1 - p;
+    return {qb, Ls, pf_tiles(qb), 1};
+  }
+  const int qb = qs - 1 - p;
+  return {qb, 0, pf_tiles(qb), -1};
+}
+
+// split length for a launch: none for short sequences, else half of the longest block's tiles
+inline int pf_split_len(int nqb) {
+  const int nmax = pf_tiles(nqb - 1);
+  return nmax >= 8 ? (nmax + 1) / 2 : 0;
+}
+inline int pf_items(int nqb, int Ls) { return Ls == 0 ? nqb : 2 * (nqb - 2 * Ls) + 2 * Ls; }
+
 template <int GW>
 __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ kr, const __bf16* __restrict__ vt,
     const __bf16* __restrict__ gate, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos0,
-    __bf16* __restrict__ out, int T, int Tp, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb, int B) {
+    __bf16* __restrict__ out, int T, int Tp, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb, int B,
+    int Ls, float* __restrict__ part, int* __restrict__ cnt) {
   __shared__ PfStage stage[2];
+  __shared__ int merge_here;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_other = B * Hkv * ngroups;
-  const int qb = nqb - 1 - (int)(blockIdx.x / n_other);
+  const PfItem it = pf_item((int)(blockIdx.x / n_other), nqb, Ls);
+  const int qb = it.qb;
   const int rem = blockIdx.x % n_other;
   const int b = rem / (Hkv * ngroups);
   const int kvh = (rem / ngroups) % Hkv;
@@ -188,8 +242,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     }
   };
 
-  const int nkt = (q0 + kBQ - 1) / kBN + 1;  // tiles holding keys 0 .. q0 + 31
-  copy_tile(0, 0);
+  copy_tile(it.kt0, it.kt0 & 1);
   // ---- Q^T operand (B of S^T = K Q^T): lane holds query q0 + ln, dims 16 ks + 8 hh + j, rotated ----
   bf16x8 qop[16];
   {
@@ -228,15 +281,15 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
   const int tq = q0 + ln;  // this lane's query
   const int full_tiles = q0 / kBN;  // tiles entirely below this block's first query: no mask
 
-  for (int kt = 0; kt < nkt; ++kt) {
+  // Scores of tile kt (scaled and causally masked) into sc; returns this lane's query's max over the tile's keys.
+  auto tile_scores = [&](int kt, f32x16 (&sc)[2]) -> float {
     const int s = kt & 1;
     // this wave's copies of tile kt are its only ones in flight; after the barrier every wave's have landed and
     // every wave is done with tile kt - 1, whose stage then receives tile kt + 1
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (kt + 1 < nkt) copy_tile(kt + 1, s ^ 1);
+    if (kt + 1 < it.kt1) copy_tile(kt + 1, s ^ 1);
     const char* kl = reinterpret_cast<const char*>(&stage[s].k[0]);
-    const char* vl = reinterpret_cast<const char*>(&stage[s].v[0]);
     // the operand addresses below are recomputed every tile from an opaque copy of the lane id: hoisted out of the
     // loop they would occupy some 60 registers, and the kernel is register-bound
     int lo_ = threadIdx.x & 63;
@@ -244,37 +297,27 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     const int ln = lo_ & 31, hh = lo_ >> 5;
     // S^T = K Q^T for the two 32-key halves of the tile (rows = keys, cols = this wave's 32 queries): four
     // independent accumulation chains, K fragments read four K steps at a time
-    f32x16 sc[2];
-    {
-      f32x16 acc[2][2];
+    f32x16 acc[2][2];
 #pragma unroll
-      for (int ksub = 0; ksub < 2; ++ksub) { acc[ksub][0] = zero16(); acc[ksub][1] = zero16(); }
+    for (int ksub = 0; ksub < 2; ++ksub) { acc[ksub][0] = zero16(); acc[ksub][1] = zero16(); }
 #pragma unroll
-      for (int ks0 = 0; ks0 < 16; ks0 += 4) {
-        bf16x8 kf[2][4];
+    for (int ks0 = 0; ks0 < 16; ks0 += 4) {
+      bf16x8 kf[2][4];
 #pragma unroll
-        for (int ksub = 0; ksub < 2; ++ksub) {
-          const int r = 32 * ksub + ln;
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            kf[ksub][j] = *reinterpret_cast<const bf16x8*>(kl + r * 512 + 16 * ((2 * (ks0 + j) + hh) ^ (r & 15)));
-        }
+      for (int ksub = 0; ksub < 2; ++ksub) {
+        const int r = 32 * ksub + ln;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int ksub = 0; ksub < 2; ++ksub) acc[ksub][j & 1] = mfma32(kf[ksub][j], qop[ks0 + j], acc[ksub][j & 1]);
-        // all eight reads first, then the eight MFMAs (the default schedule waits on each read pair in turn)
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+          kf[ksub][j] = *reinterpret_cast<const bf16x8*>(kl + r * 512 + 16 * ((2 * (ks0 + j) + hh) ^ (r & 15)));
       }
 #pragma unroll
-      for (int ksub = 0; ksub < 2; ++ksub)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) sc[ksub][i] = acc[ksub][0][i] + acc[ksub][1][i];
+        for (int ksub = 0; ksub < 2; ++ksub) acc[ksub][j & 1] = mfma32(kf[ksub][j], qop[ks0 + j], acc[ksub][j & 1]);
+      // all eight reads first, then the eight MFMAs (the default schedule waits on each read pair in turn)
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     }
-    // online softmax along the keys of this lane's query (lane pair l, l ^ 32 holds all 64 keys). The running max
-    // only moves (and O, l are rescaled) when a tile max exceeds it by more than 8: p = exp(s - m) <= e^8 stays
-    // exact enough in fp32 and in the bf16 P operand, and most tiles skip the 128-register rescale.
     float mx = -INFINITY;
     const bool masked = kt >= full_tiles;
 #pragma unroll
@@ -282,22 +325,20 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int key = kt * kBN + 32 * ksub + 8 * (i >> 2) + 4 * hh + (i & 3);
-        float x = sc[ksub][i] * scale;
+        float x = (acc[ksub][0][i] + acc[ksub][1][i]) * scale;
         if (masked) x = (key <= tq && key < T) ? x : -INFINITY;
         sc[ksub][i] = x;
         mx = fmaxf(mx, x);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    if (__any(mx > m_run + 8.f)) {
-      const float mn = fmaxf(m_run, mx);
-      const float corr = __expf(m_run - mn);
-      l_run *= corr;
-      m_run = mn;
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
-    }
+    return fmaxf(mx, __shfl_xor(mx, 32, 64));
+  };
+  // P = exp(S - m_run) of tile kt into the row sum, then O^T += V^T P^T: rows = 256 dims (8 tiles of 32),
+  // k = 64 keys (4 steps of 16); V^T fragments read two dim tiles at a time
+  auto tile_accumulate = [&](int kt, const f32x16 (&sc)[2]) {
+    const char* vl = reinterpret_cast<const char*>(&stage[kt & 1].v[0]);
+    int lo_ = threadIdx.x & 63;
+    asm volatile("" : "+v"(lo_));
+    const int ln = lo_ & 31, hh = lo_ >> 5;
     float ps = 0.f;
     bf16x8 pb[4];
 #pragma unroll
@@ -310,8 +351,6 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
       }
     ps += __shfl_xor(ps, 32, 64);
     l_run += ps;
-    // O^T += V^T P^T: rows = 256 dims (8 tiles of 32), k = 64 keys (4 steps of 16); V^T fragments read two dim
-    // tiles at a time
 #pragma unroll
     for (int mt0 = 0; mt0 < 8; mt0 += 2) {
       bf16x8 vf[2][4];
@@ -329,6 +368,76 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     }
+  };
+
+  // Online softmax along the keys of each lane's query (lane pair l, l ^ 32 holds all 64 keys of a tile). The
+  // running max only moves (and O, l are rescaled) when a tile max exceeds it by more than 8: p = exp(s - m) <= e^8
+  // stays exact enough in fp32 and in the bf16 P operand. The inner loop runs the tiles that need no rescale, so O
+  // never leaves the MFMA accumulators there; the rescale (a read, multiply and write-back of all 128 accumulator
+  // registers) sits outside it and runs a few times per block (always at tile 0).
+  int kt = it.kt0;
+  while (kt < it.kt1) {
+    f32x16 sc[2];
+    float mx = tile_scores(kt, sc);
+    while (!__any(mx > m_run + 8.f)) {
+      tile_accumulate(kt, sc);
+      if (++kt == it.kt1) break;
+      mx = tile_scores(kt, sc);
+    }
+    if (kt == it.kt1) break;
+    const float mn = fmaxf(m_run, mx);
+    const float corr = __expf(m_run - mn);
+    l_run *= corr;
+    m_run = mn;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
+    tile_accumulate(kt, sc);
+    ++kt;
+  }
+
+  // ---- a split query block: both halves publish (O, m, l); the second to finish merges and stores ----
+  if (it.half >= 0) {
+    const int pair = (qb - 2 * Ls) * n_other + rem;
+    float* mine = part + ((size_t)(2 * pair + it.half) * GW + wave) * kPartFloats;
+    const float* other = part + ((size_t)(2 * pair + (it.half ^ 1)) * GW + wave) * kPartFloats;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 w = {o[mt][4 * c], o[mt][4 * c + 1], o[mt][4 * c + 2], o[mt][4 * c + 3]};
+        *reinterpret_cast<f32x4*>(mine + ((mt * 4 + c) * 64 + lane) * 4) = w;
+      }
+    mine[8192 + lane] = m_run;
+    mine[8192 + 64 + lane] = l_run;
+    // release: this block's partial is visible device-wide before its arrival is counted
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) merge_here = atomicAdd(cnt + pair, 1);
+    __syncthreads();
+    if (merge_here == 0) return;  // the other half is still running and will merge
+    __threadfence();              // acquire: the other half's partial was published before its count
+    // O = O0 e^(m0 - m) + O1 e^(m1 - m), l likewise, always in half order so that the result does not depend on
+    // which half finished last. Neither half has a fully masked query: the second half starts at key 64 Ls and every
+    // query of a split block is at or past it.
+    const float m_o = other[8192 + lane], l_o = other[8192 + 64 + lane];
+    const float m0 = it.half ? m_o : m_run, m1 = it.half ? m_run : m_o;
+    const float l0 = it.half ? l_o : l_run, l1 = it.half ? l_run : l_o;
+    const float mm = fmaxf(m0, m1);
+    const float c0 = __expf(m0 - mm), c1 = __expf(m1 - mm);
+    l_run = fmaf(l0, c0, l1 * c1);
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f32x4 w = *reinterpret_cast<const f32x4*>(other + ((mt * 4 + c) * 64 + lane) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = o[mt][4 * c + e];
+          o[mt][4 * c + e] = it.half ? fmaf(w[e], c0, a * c1) : fmaf(a, c0, w[e] * c1);
+        }
+      }
   }
 
   // ---- epilogue: normalise, gate, store ----
@@ -353,12 +462,36 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
 
 static int64_t padded_T(int64_t T) { return (T + kBN - 1) / kBN * kBN; }
 
+// Workspace: K rotated and V transposed ([B, Hkv, Tp, D] bf16 each), then the split blocks' partials
+// ([pairs][2 halves][wave] x kPartFloats fp32), then one int arrival counter per pair.
+struct PfLayout {
+  size_t part_off, cnt_off, total;
+  int64_t ncnt;
+};
+static PfLayout pf_layout(int64_t B, int64_t T, int64_t Hq, int64_t Hkv) {
+  const int64_t Tp = padded_T(T);
+  const int64_t G = Hq / Hkv;
+  const int64_t GW = G > 4 ? 4 : G;
+  const int64_t nqb = (T + kBQ - 1) / kBQ;
+  const int Ls = pf_split_len((int)nqb);
+  const int64_t nsq = Ls ? nqb - 2 * Ls : 0;
+  PfLayout l;
+  l.ncnt = nsq * B * Hkv * (G / GW);
+  l.part_off = (size_t)2 * B * Hkv * Tp * kPD * sizeof(__bf16);
+  l.cnt_off = l.part_off + (size_t)2 * l.ncnt * GW * kPartFloats * sizeof(float);
+  l.total = (l.cnt_off + (size_t)l.ncnt * sizeof(int) + 255) / 256 * 256;
+  return l;
+}
+
 }  // namespace q35
 
-extern "C" size_t q35_gated_attn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t Hkv, int64_t D) {
+extern "C" size_t q35_gated_attn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D) {
   using namespace q35;
-  if (B <= 0 || T <= 0 || Hkv <= 0 || D != kPD) return 0;
-  return (size_t)2 * B * Hkv * padded_T(T) * kPD * sizeof(__bf16);
+  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D != kPD) return 0;
+  const int64_t G = Hq / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return 0;
+  if (T > ((int64_t)1 << 30) || B * Hq > ((int64_t)1 << 30)) return 0;
+  return pf_layout(B, T, Hq, Hkv).total;
 }
 
 extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const void* gate,
@@ -375,22 +508,27 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
   if (G != 1 && G != 2 && G != 4 && G != 8) return Q35_EUNSUPPORTED;
   const int GW = G > 4 ? 4 : (int)G;
   const int ngroups = (int)(G / GW);
-  const int64_t nqb = (T + kBQ - 1) / kBQ;
-  const int64_t nblocks = nqb * B * Hkv * ngroups;
   const int64_t Tp = padded_T(T);
-  if (nblocks > 0x7fffffff || B > 65535 || Hkv > 65535 || Tp / kBN > 0x7fffffff || T * Hq * D > ((int64_t)1 << 40))
-    return Q35_EUNSUPPORTED;
+  if (T > ((int64_t)1 << 30) || B > 65535 || Hkv > 65535 || T * Hq * D > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
+  const int64_t nqb = (T + kBQ - 1) / kBQ;
+  const int Ls = pf_split_len((int)nqb);
+  const int64_t nblocks = (int64_t)pf_items((int)nqb, Ls) * B * Hkv * ngroups;
+  if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
   // V^T rows are addressed with 32-bit byte offsets inside a head's [D, Tp] block
   if (Tp * kPD * 2 >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
-  const size_t need = q35_gated_attn_prefill_workspace_bytes(B, T, Hkv, D);
-  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
+  const PfLayout lay = pf_layout(B, T, Hq, Hkv);
+  if (lay.ncnt > 0x7fffffff) return Q35_EUNSUPPORTED;
+  if (!workspace || workspace_bytes < lay.total || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  __bf16* kr = static_cast<__bf16*>(workspace);
+  char* ws = static_cast<char*>(workspace);
+  __bf16* kr = reinterpret_cast<__bf16*>(ws);
   __bf16* vt = kr + (size_t)B * Hkv * Tp * kPD;
+  float* part = reinterpret_cast<float*>(ws + lay.part_off);
+  int* cnt = reinterpret_cast<int*>(ws + lay.cnt_off);
   const dim3 gp((unsigned)(Tp / kBN), (unsigned)Hkv, (unsigned)B);
 #define Q35_KV_LAUNCH(R)                                                                                         \
   hipLaunchKernelGGL(attn_kv_prep_kernel<R>, gp, dim3(256), 0, st, (const __bf16*)k, (const __bf16*)v, cos, sin, \
-                     (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv)
+                     (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv, cnt, (int)lay.ncnt)
   switch (rot) {
     case 0: Q35_KV_LAUNCH(0); break;
     case 16: Q35_KV_LAUNCH(16); break;
@@ -402,7 +540,7 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
 #define Q35_PF_LAUNCH(GG)                                                                                         \
   hipLaunchKernelGGL(attn_prefill_kernel<GG>, dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q,    \
                      kr, vt, (const __bf16*)gate, cos, sin, (int)pos0, (__bf16*)out, (int)T, (int)Tp, (int)Hq,     \
-                     (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B)
+                     (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B, Ls, part, cnt)
   switch (GW) {
     case 1: Q35_PF_LAUNCH(1); break;
     case 2: Q35_PF_LAUNCH(2); break;

@@ -36,7 +36,7 @@ _SIGS = {
     "q35_gdn_chunk_workspace_bytes": ([I64, I64, I64, I64, I64, I64], SZ),
     "q35_gdn_chunk_prefill": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I32, F32, I32, I64, P, SZ, P],
                               I32),
-    "q35_gated_attn_prefill_workspace_bytes": ([I64, I64, I64, I64], SZ),
+    "q35_gated_attn_prefill_workspace_bytes": ([I64, I64, I64, I64, I64], SZ),
     "q35_gated_attn_prefill": ([P, P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, F32, P, SZ, P], I32),
     "q35_gated_attn_decode_workspace_bytes": ([I64, I64, I64, I64, I64, I64], SZ),
     "q35_gated_attn_decode": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, F32, I64, P, SZ, P], I32),

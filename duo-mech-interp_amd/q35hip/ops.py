@@ -137,7 +137,7 @@ def _attn_prefill_impl(q, k, v, gate, cos, sin, pos0, scale):
     rot = _tables_check(cos, sin, pos0 + T)
     out = torch.empty(B, T, Hq * D, dtype=q.dtype, device=q.device)
     L = _lib.lib()
-    nbytes = L.q35_gated_attn_prefill_workspace_bytes(B, T, Hkv, D)
+    nbytes = L.q35_gated_attn_prefill_workspace_bytes(B, T, Hq, Hkv, D)
     _require(nbytes > 0, "unsupported attention shape")
     ws = _workspace(nbytes, q.device)
     st = L.q35_gated_attn_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(cos), _ptr(sin), int(pos0),

@@ -37,7 +37,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 2
+    assert L.q35_abi_version() == 3
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -67,8 +67,15 @@ def test_validation_rejects_without_launching():
     assert L.q35_gated_attn_prefill(fake, fake, fake, fake, fake, fake, 0, fake, 1, 16, 6, 2, 256, 64, 0.1,
                                     fake, 1 << 20, None) == 2
     # prefill workspace: head dim other than 256 has none; too small a workspace is rejected
-    assert L.q35_gated_attn_prefill_workspace_bytes(1, 100, 2, 128) == 0
-    assert L.q35_gated_attn_prefill_workspace_bytes(1, 100, 2, 256) == 2 * 2 * 128 * 256 * 2
+    assert L.q35_gated_attn_prefill_workspace_bytes(1, 100, 8, 2, 128) == 0
+    assert L.q35_gated_attn_prefill_workspace_bytes(1, 100, 6, 2, 256) == 0
+    # short sequence: rotated keys and transposed values only
+    assert L.q35_gated_attn_prefill_workspace_bytes(1, 100, 8, 2, 256) == 2 * 2 * 128 * 256 * 2
+    # T 4096: 128 query blocks, those with more than 32 key tiles (64 of them) split in two; per split block and
+    # kv head, 2 halves x 4 waves x (32 x 256 + 128) fp32 partials and one counter
+    kv = 2 * 2 * 4096 * 256 * 2
+    parts = 64 * 2 * 2 * 4 * (8192 + 128) * 4
+    assert L.q35_gated_attn_prefill_workspace_bytes(1, 4096, 8, 2, 256) == kv + parts + 64 * 2 * 4
     assert L.q35_gated_attn_prefill(fake, fake, fake, fake, fake, fake, 0, fake, 1, 100, 8, 2, 256, 64, 0.1,
                                     fake, 16, None) == 3
     assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 8, 2, 256, 128, 63, 0.1, 0,
