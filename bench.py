@@ -193,7 +193,8 @@ def bench_copy(torch, dev, mb=256, reps=5):
 
 def bench_stack(torch, q35hip, workloads, dev, steps=256):
     """The Qwen3.5-0.8B-shaped hybrid stack (24 layers, int8 SwiGLU, tied 151,936 embedding), batch 3 steered rows:
-    2048-token prefill, then `steps` greedy decode steps, host-driven (no graph capture). Reported end to end."""
+    2048-token prefill, then `steps` greedy decode steps, host-driven (no graph capture). Reported end to end. The
+    prefill is timed with each Gated DeltaNet prefill kernel (the fp32 token-serial default and the chunked one)."""
     from q35hip import model as gm
     cfg = workloads.Q35Config()
     W = workloads.init_weights(cfg, seed=0)
@@ -202,26 +203,34 @@ def bench_stack(torch, q35hip, workloads, dev, steps=256):
     prompt = torch.randint(0, cfg.vocab, (1, 2048), generator=torch.Generator().manual_seed(0)).repeat(3, 1)
     v = torch.randn(cfg.hidden, generator=torch.Generator().manual_seed(0))
     g.set_vectors(torch.stack([v, -v]) * 0.1, [0, -1, 1])
-    for _ in range(2):  # warm: allocator, library handles
+    out = {"rows": 3, "prompt": 2048, "steps": steps}
+    for mode in ("chunk", "recurrent"):  # the default ("recurrent") last: its states feed the decode loop
+        g.gdn_prefill = mode
+        for _ in range(2):  # warm: allocator, library handles
+            g.reset()
+            g.forward(prompt[:, :256])
+            g.forward(torch.zeros(3, 1, dtype=torch.long))
+        torch.cuda.synchronize()
         g.reset()
-        g.forward(prompt[:, :256])
-        g.forward(torch.zeros(3, 1, dtype=torch.long))
-    torch.cuda.synchronize()
-    g.reset()
-    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-    e0.record()
-    logits, _ = g.forward(prompt)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        logits, _ = g.forward(prompt)
+        e1.record()
+        torch.cuda.synchronize()
+        tp = e0.elapsed_time(e1) * 1e-3
+        out[f"prefill_{mode}_tok_s"] = 3 * 2048 / tp
+        out[f"prefill_{mode}_ms"] = tp * 1e3
+    e1, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e1.record()
     for _ in range(steps):
         nxt = logits.argmax(-1, keepdim=True)
         logits, _ = g.forward(nxt)
     e2.record()
     torch.cuda.synchronize()
-    tp = e0.elapsed_time(e1) * 1e-3
     td = e1.elapsed_time(e2) * 1e-3
-    return {"prefill_tok_s": 3 * 2048 / tp, "prefill_ms": tp * 1e3, "decode_tok_s": 3 * steps / td,
-            "decode_ms_per_step": td / steps * 1e3, "rows": 3, "prompt": 2048, "steps": steps,
-            "note": "host-driven decode loop (torch glue between the HIP ops), no graph capture"}
+    out.update({"decode_tok_s": 3 * steps / td, "decode_ms_per_step": td / steps * 1e3,
+                "note": "host-driven decode loop (torch glue between the HIP ops), no graph capture"})
+    return out
 
 
 def cpu_baseline(budget_s):

@@ -10,19 +10,56 @@
 //   o_j    = sum_i S[i][j] q_i
 // The kernel reads S once and writes it once per launch: with a = S^T k and c = S^T q taken on the undecayed S,
 //   u = alpha a,  o = alpha c + (q . k) d,  S' = alpha S + k d^T,
-// which is the same arithmetic regrouped (both dot products come from one pass over the state tile).
+// which is the same arithmetic regrouped (both dot products come from one pass over the state tile). The norms are
+// folded in as scalars: a and c are taken with the raw k and q and scaled by rsqrt(|k|^2 + eps) and
+// rsqrt(|q|^2 + eps) * scale afterwards.
 //
-// Decomposition: one block per (slice of 16 value columns, head, batch row) -> Dv/16 * H * B blocks of 256 threads.
-// Thread t owns a float4 of columns (t % 4) in rows t/4 and t/4 + 64, so every wave reads 16 full 64-byte row
-// segments per load. The column reductions run as xor-shuffles over lanes with equal t % 4, then across the four
-// waves through LDS. Memory per launch: S read + written once (2 * 4 * Dk * Dv bytes per (b, h)).
+// Decomposition: value columns are independent given k and q, so one block of 256 threads takes a slice of 32 value
+// columns (128 bytes of every state row, one full cache line) of one (head, row): grid (Dv / 32, H, B). Thread t
+// owns the float4 of columns 4 (t % 8) .. + 3 in the four rows t / 8 + 32 i, so one wave load covers eight whole
+// 128-byte lines. Column sums run as three xor-shuffles over the lanes of a wave with equal t % 8, then across the
+// four waves through LDS (double-buffered by token parity: one barrier per token). Every wave forms |q|^2, |k|^2
+// and q . k itself from two elements per lane, and the next token's inputs are loaded while the current token is
+// reduced, so a token costs one barrier and no exposed global-load latency after the first.
 #include "q35_common.h"
 #include "q35hip.h"
 
 namespace q35 {
 
 constexpr int kGdnD = 128;   // Dk = Dv
-constexpr int kGdnJS = 16;   // value columns per block
+constexpr int kGdnJS = 32;   // value columns per block
+
+// Per-token inputs of one thread (loaded one token ahead).
+struct RecIn {
+  float kr[4], qr[4];  // k and q at this thread's four state rows
+  float k2[2], q2[2];  // two elements per lane for the norms
+  float vv[4];         // v at this thread's four value columns
+  float g, beta;
+};
+
+template <typename Tin>
+__device__ __forceinline__ void rec_load(RecIn& in, const Tin* __restrict__ q, const Tin* __restrict__ k,
+                                         const Tin* __restrict__ v, const float* __restrict__ g,
+                                         const float* __restrict__ beta, size_t tok, int Hk, int kh, int H, int h,
+                                         int rg, int j0, int lane) {
+  const Tin* qrow = q + (tok * Hk + kh) * kGdnD;
+  const Tin* krow = k + (tok * Hk + kh) * kGdnD;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    in.kr[i] = to_f32(krow[rg + 32 * i]);
+    in.qr[i] = to_f32(qrow[rg + 32 * i]);
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    in.k2[e] = to_f32(krow[2 * lane + e]);
+    in.q2[e] = to_f32(qrow[2 * lane + e]);
+  }
+  const Tin* vrow = v + (tok * H + h) * kGdnD + j0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) in.vv[e] = to_f32(vrow[e]);
+  in.g = g[tok * H + h];
+  in.beta = beta[tok * H + h];
+}
 
 template <typename Tin>
 __global__ __launch_bounds__(256) void gdn_recurrent_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
@@ -32,108 +69,85 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(const Tin* __restric
                                                             float scale, int l2norm) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int cq = tid & 3;   // column quad of this thread
-  const int r0 = tid >> 2;  // rows r0 and r0 + 64
+  const int cq = tid & 7;   // column quad of this thread
+  const int rg = tid >> 3;  // rows rg + 32 i
   const int j0 = blockIdx.x * kGdnJS + cq * 4;
   const int h = blockIdx.y, b = blockIdx.z;
   const int kh = h / (H / Hk);
 
-  __shared__ float qs[2][kGdnD], ks[2][kGdnD];
-  __shared__ float red1[2][4][4];   // [parity][wave][sum q^2, sum k^2, sum q k, pad]
-  __shared__ f32x4 red2[2][4][4][2];  // [parity][wave][column quad][S^T k | S^T q]
+  __shared__ f32x4 red[2][4][8][2];  // [token parity][wave][column quad][S^T k | S^T q]
 
   const size_t sbase = ((size_t)b * H + h) * kGdnD * kGdnD;
-  f32x4 s[2];
+  f32x4 s[4];
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    if (s_in)
-      s[p] = *reinterpret_cast<const f32x4*>(s_in + sbase + (size_t)(r0 + 64 * p) * kGdnD + j0);
-    else
-      s[p] = zero4();
-  }
+  for (int i = 0; i < 4; ++i)
+    s[i] = s_in ? *reinterpret_cast<const f32x4*>(s_in + sbase + (size_t)(rg + 32 * i) * kGdnD + j0) : zero4();
 
+  RecIn cur, nxt;
+  rec_load(cur, q, k, v, g, beta, (size_t)b * T, Hk, kh, H, h, rg, j0, lane);
   for (int t = 0; t < T; ++t) {
     const int par = t & 1;
     const size_t tok = (size_t)b * T + t;
-    // per-token scalars and this thread's value columns, issued first so they overlap the reductions
-    const float alpha = expf(g[tok * H + h]);
-    const float be = beta[tok * H + h];
-    const Tin* vrow = v + (tok * H + h) * kGdnD + j0;
-    float vv[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) vv[e] = to_f32(vrow[e]);
-    float qv = 0.f, kv = 0.f;
-    if (tid < kGdnD) {
-      qv = to_f32(q[(tok * Hk + kh) * kGdnD + tid]);
-      kv = to_f32(k[(tok * Hk + kh) * kGdnD + tid]);
-      qs[par][tid] = qv;
-      ks[par][tid] = kv;
-    }
-    float sq = qv * qv, sk = kv * kv, sqk = qv * kv;
-    if (wave < 2) {  // waves 2 and 3 hold no q/k elements
-      sq = wave_sum(sq);
-      sk = wave_sum(sk);
-      sqk = wave_sum(sqk);
-      if (lane == 0) {
-        red1[par][wave][0] = sq;
-        red1[par][wave][1] = sk;
-        red1[par][wave][2] = sqk;
-      }
-    }
-    __syncthreads();
-    const float Sq = red1[par][0][0] + red1[par][1][0];
-    const float Sk = red1[par][0][1] + red1[par][1][1];
-    const float Sqk = red1[par][0][2] + red1[par][1][2];
-    const float rq = l2norm ? rsqrtf(Sq + 1e-6f) : 1.f;
-    const float rk = l2norm ? rsqrtf(Sk + 1e-6f) : 1.f;
-    const float qsc = rq * scale;
-    const float qk = Sqk * rq * rk * scale;
-    const float kk0 = ks[par][r0] * rk, kk1 = ks[par][r0 + 64] * rk;
-    const float qq0 = qs[par][r0] * qsc, qq1 = qs[par][r0 + 64] * qsc;
-
+    if (t + 1 < T) rec_load(nxt, q, k, v, g, beta, tok + 1, Hk, kh, H, h, rg, j0, lane);
+    // partial column sums over this thread's rows, then over the 8 row groups of the wave
     f32x4 a, c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      a[e] = s[0][e] * kk0 + s[1][e] * kk1;
-      c[e] = s[0][e] * qq0 + s[1][e] * qq1;
+      a[e] = s[0][e] * cur.kr[0] + s[1][e] * cur.kr[1] + s[2][e] * cur.kr[2] + s[3][e] * cur.kr[3];
+      c[e] = s[0][e] * cur.qr[0] + s[1][e] * cur.qr[1] + s[2][e] * cur.qr[2] + s[3][e] * cur.qr[3];
     }
 #pragma unroll
-    for (int off = 4; off < 64; off <<= 1) {
+    for (int off = 8; off < 64; off <<= 1) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         a[e] += __shfl_xor(a[e], off, 64);
         c[e] += __shfl_xor(c[e], off, 64);
       }
     }
-    if (lane < 4) {
-      red2[par][wave][lane][0] = a;
-      red2[par][wave][lane][1] = c;
+    if (lane < 8) {
+      red[par][wave][lane][0] = a;
+      red[par][wave][lane][1] = c;
     }
-    __syncthreads();
-    f32x4 A = red2[par][0][cq][0], C = red2[par][0][cq][1];
+    // norms of this token's q and k (every wave forms them itself)
+    float sq = cur.q2[0] * cur.q2[0] + cur.q2[1] * cur.q2[1];
+    float sk = cur.k2[0] * cur.k2[0] + cur.k2[1] * cur.k2[1];
+    float sqk = cur.q2[0] * cur.k2[0] + cur.q2[1] * cur.k2[1];
+    sq = wave_sum(sq);
+    sk = wave_sum(sk);
+    sqk = wave_sum(sqk);
+    lds_barrier();
+    f32x4 A = red[par][0][cq][0], C = red[par][0][cq][1];
 #pragma unroll
     for (int w = 1; w < 4; ++w) {
-      const f32x4 a2 = red2[par][w][cq][0], c2 = red2[par][w][cq][1];
+      const f32x4 a2 = red[par][w][cq][0], c2 = red[par][w][cq][1];
 #pragma unroll
       for (int e = 0; e < 4; ++e) { A[e] += a2[e]; C[e] += c2[e]; }
     }
+    const float rk = l2norm ? rsqrtf(sk + 1e-6f) : 1.f;
+    const float rqs = (l2norm ? rsqrtf(sq + 1e-6f) : 1.f) * scale;
+    const float qk = sqk * rqs * rk;
+    const float alpha = expf(cur.g);
+    float kk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kk[i] = cur.kr[i] * rk;
     f32x4 out;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float d = be * (vv[e] - alpha * A[e]);
-      out[e] = alpha * C[e] + qk * d;
-      s[0][e] = alpha * s[0][e] + kk0 * d;
-      s[1][e] = alpha * s[1][e] + kk1 * d;
+      const float d = cur.beta * (cur.vv[e] - alpha * rk * A[e]);
+      out[e] = alpha * rqs * C[e] + qk * d;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i][e] = alpha * s[i][e] + kk[i] * d;
     }
-    if (r0 == 0) {
+    if (rg == 0) {
       Tin* orow = o + (tok * H + h) * kGdnD + j0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) orow[e] = from_f32<Tin>(out[e]);
     }
+    if (t + 1 < T) cur = nxt;
   }
 #pragma unroll
-  for (int p = 0; p < 2; ++p)
-    *reinterpret_cast<f32x4*>(s_out + sbase + (size_t)(r0 + 64 * p) * kGdnD + j0) = s[p];
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<f32x4*>(s_out + sbase + (size_t)(rg + 32 * i) * kGdnD + j0) = s[i];
 }
 
 }  // namespace q35

@@ -58,13 +58,17 @@ def _rotate_rows(x, cos_rows, sin_rows):
 
 
 def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_heads=None, head_k_dim=None,
-                         eps=1e-6):
+                         eps=1e-6, prefill="chunk"):
     """Gated DeltaNet mixer of one decoder layer (Qwen3_5GatedDeltaNet.forward, HF:432-543; the WGSL conv + delta
     kernels, engine/kernels_qwen35.js:127-247). x: [B, T, H] fp32 (the input-normed residual). A call with T == 1
-    is one recurrent decode step (HF:505-517); T > 1 runs the chunked prefill from rec_state (HF:518-530). Both
-    states are updated in place. head_scale: optional [Hv] per-head output scale applied after the gated norm
-    (engine/kernels_qwen35.js:243). num_k_heads / head_k_dim default to the value heads / value head dim (the
-    Qwen3.5 text models use Hk = Hv and dk = dv). Returns y [B, T, H]."""
+    is one recurrent decode step (HF:505-517). T > 1 runs from rec_state either the chunked prefill (HF:518-530;
+    prefill="chunk": bf16 MFMA products, relative error a few 1e-3) or the token-serial fp32 recurrence
+    (prefill="recurrent": fp32 throughout, as the WGSL engine runs prefill token by token,
+    engine/kernels_qwen35.js:183-247). Both states are updated in place. head_scale: optional [Hv] per-head output
+    scale applied after the gated norm (engine/kernels_qwen35.js:243). num_k_heads / head_k_dim default to the
+    value heads / value head dim (the Qwen3.5 text models use Hk = Hv and dk = dv). Returns y [B, T, H]."""
+    if prefill not in ("chunk", "recurrent"):
+        raise ValueError(f"gated_deltanet_layer: prefill must be 'chunk' or 'recurrent', not {prefill!r}")
     B, T, _ = x.shape
     Hv = p["A_log"].numel()
     dv = p["norm"].numel()
@@ -90,7 +94,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     v = conv[..., 2 * kd:].reshape(B, T, Hv, dv).contiguous()
     beta = torch.sigmoid(b).contiguous()
     g = (-p["A_log"].float().exp() * F.softplus(a.float() + p["dt_bias"].float())).contiguous()
-    if T == 1:
+    if T == 1 or prefill == "recurrent":
         o = ops.gdn_decode_step_(q, k, v, g, beta, rec_state, use_qk_l2norm_in_kernel=True)
     else:
         o, S = ops.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=rec_state, output_final_state=True,

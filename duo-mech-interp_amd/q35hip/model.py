@@ -39,10 +39,18 @@ def mlp(p, h):
 
 class HybridModel:
     """B independent rows decoded together (the boosted / as-is / suppressed rows of the reference's steer loop,
-    engine/analysis.js:117-145). fp32 residual stream; vectors added after steer_layer at every position."""
+    engine/analysis.js:117-145). fp32 residual stream; vectors added after steer_layer at every position.
 
-    def __init__(self, cfg, W, device, max_len=4096, rows=3, steer_layer=12):
+    gdn_prefill selects the Gated DeltaNet prefill kernel: "recurrent" (default) runs the fp32 token-serial kernel,
+    whose outputs agree with the fp32 CPU recurrence to about 1e-6, so greedy tokens follow the fp32 reference even
+    through near ties of a few 1e-3 in the logits; "chunk" runs the chunked bf16-MFMA kernel (faster prefill,
+    relative error a few 1e-3 per layer)."""
+
+    def __init__(self, cfg, W, device, max_len=4096, rows=3, steer_layer=12, gdn_prefill="recurrent"):
+        if gdn_prefill not in ("chunk", "recurrent"):
+            raise ValueError(f"HybridModel: gdn_prefill must be 'chunk' or 'recurrent', not {gdn_prefill!r}")
         self.cfg, self.device, self.steer_layer = cfg, device, steer_layer
+        self.gdn_prefill = gdn_prefill
         self.W = W if isinstance(W, Q35Weights) else Q35Weights(W, device)
         self.max_len, self.rows = max_len, rows
         self.vecs = None
@@ -91,7 +99,7 @@ class HybridModel:
                                                  partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps)
             else:
                 y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
-                                                head_k_dim=cfg.lin_dk, eps=cfg.eps)
+                                                head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill)
             x = x + y
             x = x + mlp(p, rmsnorm_1p(x, p["post_attention_layernorm"], cfg.eps))
             if l == self.steer_layer and self.vecs is not None:

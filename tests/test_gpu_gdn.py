@@ -44,6 +44,22 @@ def test_decode_64_sequential_steps_fp32():
     assert oracle.rel_err(state.cpu(), s_ref) <= TOL_F32
 
 
+def test_recurrent_long_prefill_fp32():
+    """The token-serial kernel as a prefill: T = 2048 in one launch, B = 3, 16 heads, fp32 from a non-zero state
+    (the hybrid stack's fp32 GDN prefill shape); fp32 tolerance."""
+    dev = device()
+    inp = workloads.gdn_inputs(B=3, T=2048, H=16, D=128, seed=3, dtype=torch.float32, normalize=False)
+    s0 = 0.1 * torch.randn(3, 16, 128, 128, generator=torch.Generator().manual_seed(6))
+    o_ref, s_ref = _oracle_rec(inp, s0)
+    d = workloads.to_device(inp, dev)
+    announce("gdn recurrent T2048 B3 H16 fp32")
+    state = s0.to(dev)
+    o = q35hip.gdn_decode_step_(d["q"], d["k"], d["v"], d["g"], d["beta"], state)
+    torch.cuda.synchronize()
+    assert oracle.rel_err(o.cpu(), o_ref) <= TOL_F32
+    assert oracle.rel_err(state.cpu(), s_ref) <= TOL_F32
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_recurrent_multi_token_gqa_initial_state(dtype):
     """T = 37 in one launch, B = 2, 8 value heads over 4 q/k heads, a non-zero initial state."""

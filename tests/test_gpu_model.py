@@ -18,15 +18,16 @@ from tiny_weights import STEER_LAYER, tiny_config, tiny_inputs, tiny_weights  # 
 pytestmark = pytest.mark.gpu
 
 
-def test_tiny_stack_prefill_decode_and_steering():
+@pytest.mark.parametrize("gdn_prefill", ["recurrent", "chunk"])
+def test_tiny_stack_prefill_decode_and_steering(gdn_prefill):
     dev = device()
     cfg = tiny_config()
     W = tiny_weights(cfg)
     ids, vec = tiny_inputs(cfg)
-    announce("model tiny prefill/decode")
+    announce(f"model tiny prefill/decode, GDN prefill {gdn_prefill}")
     ref = om.OracleModel(cfg, W, steer_layer=STEER_LAYER)
     ref.set_vectors(torch.stack([vec, -vec]))
-    g = gm.HybridModel(cfg, W, dev, max_len=256, rows=2, steer_layer=STEER_LAYER)
+    g = gm.HybridModel(cfg, W, dev, max_len=256, rows=2, steer_layer=STEER_LAYER, gdn_prefill=gdn_prefill)
     g.set_vectors(torch.stack([vec, -vec]), [0, 1])
     lr, _ = ref.forward(ids)
     lg, _ = g.forward(ids)
@@ -49,8 +50,8 @@ def test_full_stack_steered_greedy_64_steps():
     W = workloads.init_weights(cfg, seed=0)
     prompt = torch.randint(0, cfg.vocab, (1, 2048), generator=torch.Generator().manual_seed(0)).repeat(3, 1)
     steps = 64
-    announce("model full stack: GPU")
-    g = gm.HybridModel(cfg, W, dev, max_len=2048 + steps + 8, rows=3)
+    announce("model full stack: GPU (fp32 token-serial GDN prefill)")
+    g = gm.HybridModel(cfg, W, dev, max_len=2048 + steps + 8, rows=3, gdn_prefill="recurrent")
     toks_g, marg_g, v = gm.steered_greedy(g, prompt, steps)
     announce("model full stack: CPU oracle")
     ref = om.OracleModel(cfg, W, steer_layer=12)
