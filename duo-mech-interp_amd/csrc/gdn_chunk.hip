@@ -76,12 +76,29 @@ __device__ __forceinline__ u32x4 raw8(const float* p) {
   const bf16x8 r = load8b(p);
   return __builtin_bit_cast(u32x4, r);
 }
+__device__ __forceinline__ f32x4 unpack_bf16x4(const u32x2& r) {
+  f32x4 o = {bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y)};
+  return o;
+}
 __device__ __forceinline__ f32x4 load4f(const __bf16* p) {
   const u32x2 r = *reinterpret_cast<const u32x2*>(p);
   f32x4 o = {bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y)};
   return o;
 }
 __device__ __forceinline__ f32x4 load4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+// Four consecutive inputs as loaded (bf16 bits or fp32), converted to fp32 only when used: a raw load can be issued
+// long before its use while holding half the registers for bf16.
+template <typename Tin> struct Raw4;
+template <> struct Raw4<__bf16> {
+  u32x2 r;
+  __device__ __forceinline__ void load(const __bf16* p) { r = *reinterpret_cast<const u32x2*>(p); }
+  __device__ __forceinline__ f32x4 f() const { return unpack_bf16x4(r); }
+};
+template <> struct Raw4<float> {
+  f32x4 r;
+  __device__ __forceinline__ void load(const float* p) { r = *reinterpret_cast<const f32x4*>(p); }
+  __device__ __forceinline__ f32x4 f() const { return r; }
+};
 __device__ __forceinline__ u32x4 mask8(u32x4 r, bool keep) {
   const u32x4 z = {0u, 0u, 0u, 0u};
   return keep ? r : z;
@@ -315,43 +332,43 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
   //         Cross and P tiles are computed transposed (positions s down each lane's 4 rows) so that every lane's 4
   //         results are 4 consecutive k indices of a natural-order A fragment (one 8-byte store).
   {
-    auto kk_epilogue = [&](int x, int y, const f32x4& acc) {
-      if (x >= 4 && y < 4) {  // cross: rows s of tile y, column t of tile x
+    // The epilogues scale each product by per-position terms held in pa (LDS). Every pa value a tile needs is read
+    // into registers together with the tile's operand fragments, before its MFMAs, so that no LDS read latency sits
+    // between a product and its store (the epilogue stores to LDS, which the compiler will not move reads across).
+    const int x = wv, bt = 7 - wv;
+    const f32x4 pcx = pa[16 * x + li];    // cross tiles: column t of tile x
+    const f32x4 pcb = pa[16 * bt + li];   // P tiles: column t of tile bt
+    f32x4 prx[4];                         // diagonal tiles: rows t of tile x
+#pragma unroll
+    for (int r = 0; r < 4; ++r) prx[r] = pa[16 * x + 4 * lg + r];
+    auto kk_epilogue = [&](int y, const f32x4& acc, const f32x4 (&py)[4], const f32x4& pcy) {
+      if (x >= 4 && y < 4) {  // cross: rows s of tile y (py), column t of tile x (pcx)
         const int t = 16 * x + li, s0 = 16 * y + 4 * lg;
-        const f32x4 ic = pa[t];
         float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const f32x4 ir = pa[s0 + r];
-          v[r] = ic[1] * ir[2] * acc[r] * __expf(ic[0] - ir[0]);
-        }
+        for (int r = 0; r < 4; ++r) v[r] = pcx[1] * py[r][2] * acc[r] * __expf(pcx[0] - py[r][0]);
         bf16x8* dst = &L10f[(x - 4) * 2 + (s0 >> 5)][(t & 15) + 16 * ((s0 & 31) >> 3)];
         *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(dst) + 2 * (s0 & 7)) = pack4(v[0], v[1], v[2], v[3]);
-      } else {  // diagonal chunk block: rows t of tile x, column s of tile y
+      } else {  // diagonal chunk block: rows t of tile x (prx), column s of tile y (pcy)
         const int cb = x >= 4, s = 16 * y + li;
-        const f32x4 ic = pa[s];
         float* Am = R3 + cb * 64 * kFS;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * x + 4 * lg + r;
-          const f32x4 ir = pa[t];
-          Am[(t - 64 * cb) * kFS + (s - 64 * cb)] = s < t ? ir[1] * ic[2] * acc[r] * __expf(ir[0] - ic[0]) : 0.f;
+          Am[(t - 64 * cb) * kFS + (s - 64 * cb)] =
+              s < t ? prx[r][1] * pcy[2] * acc[r] * __expf(prx[r][0] - pcy[0]) : 0.f;
         }
       }
     };
-    auto p_epilogue = [&](int a, int bt, const f32x4& acc) {  // rows s of tile a, column t of tile bt
+    auto p_epilogue = [&](int a, const f32x4& acc, const f32x4 (&pa4)[4]) {  // rows s of tile a, column t of bt
       const int t = 16 * bt + li, s0 = 16 * a + 4 * lg;
-      const f32x4 ic = pa[t];
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const f32x4 ir = pa[s0 + r];
-        v[r] = s0 + r <= t ? ic[3] * ir[2] * acc[r] * __expf(ic[0] - ir[0]) : 0.f;
-      }
+      for (int r = 0; r < 4; ++r)
+        v[r] = s0 + r <= t ? pcb[3] * pa4[r][2] * acc[r] * __expf(pcb[0] - pa4[r][0]) : 0.f;
       bf16x8* dst = &Pf[pbase(bt) + (s0 >> 5)][(t & 15) + 16 * ((s0 & 31) >> 3)];
       *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(dst) + 2 * (s0 & 7)) = pack4(v[0], v[1], v[2], v[3]);
     };
-    const int x = wv, bt = 7 - wv;
     bf16x8 fx[4], fq[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -362,41 +379,57 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
     for (int y0 = 0; y0 < 8; y0 += 2) {
       if (y0 > x) break;
       bf16x8 fy[2][4];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) fy[j][ks] = frag(R1, 16 * min(y0 + j, x) + li, 32 * ks + 8 * lg);
+      f32x4 py[2][4], pcy[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int y = y0 + j;
-        if (y > x) break;
-        f32x4 acc = zero4();
-        if (x >= 4 && y < 4) {
+        const int yy = min(y0 + j, x);
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) acc = mfma16(fy[j][ks], fx[ks], acc);
+        for (int ks = 0; ks < 4; ++ks) fy[j][ks] = frag(R1, 16 * yy + li, 32 * ks + 8 * lg);
+        pcy[j] = pa[16 * yy + li];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) py[j][r] = pa[16 * yy + 4 * lg + r];
+      }
+      f32x4 acc[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        acc[j] = zero4();
+        if (y0 + j > x) continue;
+        if (x >= 4 && y0 + j < 4) {
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) acc[j] = mfma16(fy[j][ks], fx[ks], acc[j]);
         } else {
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) acc = mfma16(fx[ks], fy[j][ks], acc);
+          for (int ks = 0; ks < 4; ++ks) acc[j] = mfma16(fx[ks], fy[j][ks], acc[j]);
         }
-        kk_epilogue(x, y, acc);
       }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (y0 + j <= x) kk_epilogue(y0 + j, acc[j], py[j], pcy[j]);
     }
 #pragma unroll
     for (int a0 = 0; a0 < 8; a0 += 2) {
       if (a0 > bt) break;
       bf16x8 fa[2][4];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) fa[j][ks] = frag(R1, 16 * min(a0 + j, bt) + li, 32 * ks + 8 * lg);
+      f32x4 pr[2][4];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        if (a0 + j > bt) break;
-        f32x4 acc = zero4();
+        const int aa = min(a0 + j, bt);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc = mfma16(fa[j][ks], fq[ks], acc);
-        p_epilogue(a0 + j, bt, acc);
+        for (int ks = 0; ks < 4; ++ks) fa[j][ks] = frag(R1, 16 * aa + li, 32 * ks + 8 * lg);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[j][r] = pa[16 * aa + 4 * lg + r];
       }
+      f32x4 acc[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        acc[j] = zero4();
+        if (a0 + j > bt) continue;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc[j] = mfma16(fa[j][ks], fq[ks], acc[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (a0 + j <= bt) p_epilogue(a0 + j, acc[j], pr[j]);
     }
   }
   __syncthreads();
@@ -515,6 +548,15 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
   //         pair of k step w % 4 for M^T, the value-slice pair 2 (w % 4) .. + 1 for Bm.
   const float gl = gam[kP - 1];
   const int dq = 4 * (wv >> 2), kq = wv & 3;
+  // q rows of the Q' products of step 7, loaded now so that their latency is covered by step 6
+  Raw4<Tin> qraw[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 16 * (dq + i) + li;
+    const Tin* qr = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) qraw[i][a].load(qr + 16 * (2 * kq + a) + 4 * lg);
+  }
   {
     bf16x8 F[4][4];  // K~ [positions 32 ks + 8 lg + j][d 16 (dq + i) + li]
 #pragma unroll
@@ -577,10 +619,9 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
     for (int i = 0; i < 4; ++i) {
       const int bt = dq + i, nks = (bt >> 1) + 1;
       const int t = 16 * bt + li;
-      const Tin* qr = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
       f32x4 qt[2];
 #pragma unroll
-      for (int a = 0; a < 2; ++a) qt[a] = load4f(qr + 16 * (2 * kq + a) + 4 * lg);
+      for (int a = 0; a < 2; ++a) qt[a] = qraw[i][a].f();
       bf16x8 pf[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) pf[ks] = Pf[pbase(bt) + min(ks, nks - 1)][lane];
