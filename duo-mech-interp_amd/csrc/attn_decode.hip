@@ -7,11 +7,13 @@
 //
 // Pass 1 (attn_decode_partial_kernel): one block of 4 waves per (split, kv head, row). The G = Hq / Hkv query heads
 // that share a kv head are the M rows of one 16x16x32 MFMA tile, so each K row is read from HBM once for all G
-// heads. Each wave walks 16-key tiles of the block's span: scores via 8 MFMAs whose B operand is loaded straight
-// from the cache (16 contiguous bytes per lane), an online softmax on the 16 columns, then P.V on the vector ALU with
-// fully coalesced 16-byte V-row loads (32 lanes cover one 512-byte row). The four waves' (max, sum, acc) are merged
-// in LDS and written as one partial per (row, kv head, split).
-// Pass 2 (attn_decode_merge_kernel): log-sum-exp merge over splits, sigmoid gate, bf16 store.
+// heads. Each wave walks 16-key tiles of the block's span with the next tile's K and V loads in flight while the
+// current tile is computed: scores via 8 MFMAs whose B operand is loaded straight from the cache (16 contiguous
+// bytes per lane), an online softmax on the 16 columns with DPP row reductions (no LDS round trips), then P.V on the
+// vector ALU with fully coalesced 16-byte V-row loads (32 lanes cover one 512-byte row). The four waves'
+// (max, sum, acc) are merged in LDS and written as one partial per (row, kv head, split).
+// Pass 2 (attn_decode_merge_kernel): log-sum-exp merge over splits, sigmoid gate, bf16 store; every load of a
+// thread is issued before the first is used (one memory round trip).
 // HBM traffic is the K and V spans once (AI ~ 4 flop/byte): the kernel is bandwidth bound by design.
 #include "q35_common.h"
 #include "q35hip.h"
@@ -21,28 +23,54 @@ namespace q35 {
 constexpr int kDecD = 256;  // head dim
 constexpr int kDecTile = 16;
 
-template <int G>
+__device__ __forceinline__ f32x4 unpack_bf16x4(const u32x2& r) {
+  f32x4 o = {bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y)};
+  return o;
+}
+
+// Max / sum over the 16 lanes of a DPP row (lanes 16 r .. 16 r + 15), result in every lane of the row: quad_perm
+// [1,0,3,2] and [2,3,0,1] combine the lanes of a quad, row_half_mirror (lane i <- 7 - i within 8) the two quads of
+// a half row, row_mirror (lane i <- 15 - i) the two halves.
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));
+  v = fmaxf(v, dpp_mov<0x4E>(v));
+  v = fmaxf(v, dpp_mov<0x141>(v));
+  return fmaxf(v, dpp_mov<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  return v + dpp_mov<0x140>(v);
+}
+
+template <int G, int NT>
 __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ kc, const __bf16* __restrict__ vc,
     const int32_t* __restrict__ cache_len, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int rot,
-    float* __restrict__ part, int Hq, int Hkv, int max_len, int S, int L, float scale) {
+    float* __restrict__ part, int Hq, int Hkv, int max_len, int S, float scale) {
   static_assert(G == 1 || G == 2 || G == 4 || G == 8, "heads per kv head");
   constexpr int NG = (G + 3) / 4;  // lane groups of the MFMA D tile that hold real heads
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   // cache_len lives on the device, so it is clamped here rather than trusted: 0 <= len <= max_len
   const int len = min(max(cache_len[b], 0), max_len);
+  constexpr int L = 4 * kDecTile * NT;  // keys of the block's span: NT tiles per wave
   const int k_begin = s * L;
   const int k_end = min(k_begin + L, len);
   const int pos = max(len - 1, 0);
 
-  __shared__ float qf[G][kDecD];
+  __shared__ __attribute__((aligned(16))) float qf[G][kDecD];
   __shared__ float pl[4][kDecTile][G];
   __shared__ float comb_o[4][G][kDecD];
   __shared__ float comb_ml[4][G][2];
 
-  // Online-softmax state and the per-tile helpers (qa, the query A operand, is filled in step 2 below)
-  bf16x8 qa[8];
+  // Online-softmax state and the per-tile helpers (qfrag, the query A operand in LDS, is filled in step 2 below;
+  // it is read per tile rather than held in registers, which keeps two tiles' K and V in flight within budget)
+  __shared__ bf16x8 qfrag[8][64];
   const size_t kvbase = ((size_t)b * Hkv + kvh) * (size_t)max_len * kDecD;
   const __bf16* kb = kc + kvbase;
   const __bf16* vb = vc + kvbase;
@@ -60,15 +88,15 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   // K and V of one 16-key tile: keys past the span are loaded from a clamped row and masked (no branch)
   auto tile_load = [&](int key0, bf16x8 (&kv8)[8], u32x4 (&vraw)[kDecTile / 2]) {
     const int key = key0 + kn;
-    const __bf16* krow = kb + (size_t)(key < k_end ? key : k_begin) * kDecD + 8 * kg;
+    const __bf16* krow = kb + (size_t)(key < k_end ? key : min(k_begin, max_len - 1)) * kDecD + 8 * kg;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) kv8[ks] = *reinterpret_cast<const bf16x8*>(krow + 32 * ks);
+    // keys past the span read the span's last row: their p is exactly 0, so the finite values they bring add
+    // nothing (no select on the loaded data, which would make the load's consumer wait for it here)
 #pragma unroll
     for (int i = 0; i < kDecTile / 2; ++i) {
       const int vkey = key0 + 2 * i + kp;
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      const u32x4 ld = *reinterpret_cast<const u32x4*>(vb + (size_t)min(vkey, k_end - 1) * kDecD + d0);
-      vraw[i] = vkey < k_end ? ld : z;
+      vraw[i] = *reinterpret_cast<const u32x4*>(vb + (size_t)max(min(vkey, k_end - 1), 0) * kDecD + d0);
     }
   };
   auto tile_compute = [&](int key0, const bf16x8 (&kv8)[8], const u32x4 (&vraw)[kDecTile / 2]) {
@@ -76,21 +104,15 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     // scores S[head][key] for 16 keys
     f32x4 sc = zero4();
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) sc = mfma16(qa[ks], kv8[ks], sc);
+    for (int ks = 0; ks < 8; ++ks) sc = mfma16(qfrag[ks][lane], kv8[ks], sc);
     // lane group kg holds heads 4 kg + r
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float x = kvalid ? sc[r] * scale : -INFINITY;
-      float tm = x;
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) tm = fmaxf(tm, __shfl_xor(tm, off, 64));
-      const float mn = fmaxf(m_run[r], tm);
+      const float mn = fmaxf(m_run[r], row16_max(x));
       const float corr = __expf(m_run[r] - mn);
       const float p = __expf(x - mn);
-      float ps = p;
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off, 64);
-      l_run[r] = l_run[r] * corr + ps;
+      l_run[r] = l_run[r] * corr + row16_sum(p);
       m_run[r] = mn;
       if (kg < NG && 4 * kg + r < G) pl[wave][kn][4 * kg + r] = p;
       sc[r] = corr;  // broadcast source for the accumulator rescale below
@@ -104,7 +126,7 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     for (int hh = 0; hh < G; ++hh)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[hh][e] *= corr_h[hh];
-    // P.V: lane takes keys key0 + 2 i + kp (masked keys were loaded as zeros and carry p = 0)
+    // P.V: lane takes keys key0 + 2 i + kp (masked keys carry p = 0)
 #pragma unroll
     for (int i = 0; i < kDecTile / 2; ++i) {
       const int n = 2 * i + kp;
@@ -120,60 +142,78 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     }
     __builtin_amdgcn_wave_barrier();
   };
-  // first tile pair's K and V loads go out before the q prologue (they do not depend on q)
-  int key0 = k_begin + kDecTile * wave;
-  bf16x8 ka[8], kb2[8];
-  u32x4 va[kDecTile / 2], vb2[kDecTile / 2];
-  bool two = key0 + 4 * kDecTile < k_end;
-  if (key0 < k_end) {
-    tile_load(key0, ka, va);
-    if (two) tile_load(key0 + 4 * kDecTile, kb2, vb2);
-  }
-
-  // 1. the G query heads of this kv head, rotated at position pos, in fp32 (all loads of a thread issued together)
+  // the first tile's K and V loads go out before the q prologue (they do not depend on q)
+  // 1. the G query heads of this kv head, rotated at position pos, in fp32. Thread t takes quads of 4 dims
+  // (qi = t, t + 256, ...); every load is unconditional (clamped indices, results selected afterwards) so that all
+  // of them are issued together. rot is a multiple of 8, so no quad straddles rot or rot / 2.
+  const int half = rot >> 1;
+  constexpr int NQ = (G * 64 + 255) / 256;
+  u32x2 xq[NQ], pq[NQ];
+  f32x4 cq[NQ], sq[NQ];
   {
     const __bf16* qb = q + ((size_t)b * Hq + (size_t)kvh * G) * kDecD;
-    const int half = rot >> 1;
-    constexpr int NQ = G * kDecD / 256;
-    float x[NQ], pr[NQ], c[NQ], sn[NQ];
 #pragma unroll
     for (int u = 0; u < NQ; ++u) {
-      const int i = tid + 256 * u, hh = i / kDecD, d = i % kDecD;
-      const bool rotd = d < rot;
-      const int j = d < half ? d : d - half;
-      x[u] = (float)qb[hh * kDecD + d];
-      pr[u] = (float)qb[hh * kDecD + (rotd ? (d < half ? d + half : d - half) : d)];
-      c[u] = rotd ? cos_t[(size_t)pos * half + j] : 1.f;
-      sn[u] = rotd ? sin_t[(size_t)pos * half + j] : 0.f;
+      const int qi = min(tid + 256 * u, G * 64 - 1), hh = qi >> 6, d0 = 4 * (qi & 63);
+      const bool rotd = d0 < rot;
+      const int pd0 = rotd ? (d0 < half ? d0 + half : d0 - half) : d0;
+      xq[u] = *reinterpret_cast<const u32x2*>(qb + hh * kDecD + d0);
+      pq[u] = *reinterpret_cast<const u32x2*>(qb + hh * kDecD + pd0);
+      if (rot > 0) {
+        const int j0 = rotd ? (d0 < half ? d0 : d0 - half) : 0;
+        cq[u] = *reinterpret_cast<const f32x4*>(cos_t + (size_t)pos * half + j0);
+        sq[u] = *reinterpret_cast<const f32x4*>(sin_t + (size_t)pos * half + j0);
+      }
     }
+  }
 #pragma unroll
-    for (int u = 0; u < NQ; ++u) {
-      const int i = tid + 256 * u, hh = i / kDecD, d = i % kDecD;
-      qf[hh][d] = d < half ? x[u] * c[u] - pr[u] * sn[u] : x[u] * c[u] + pr[u] * sn[u];
+  for (int u = 0; u < NQ; ++u) {
+    const int qi = tid + 256 * u, hh = qi >> 6, d0 = 4 * (qi & 63);
+    if (qi < G * 64) {
+      const f32x4 x = unpack_bf16x4(xq[u]), y = unpack_bf16x4(pq[u]);
+      f32x4 r;
+      if (d0 < rot) {
+        const float sg = d0 < half ? -1.f : 1.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = x[e] * cq[u][e] + sg * y[e] * sq[u][e];
+      } else {
+        r = x;
+      }
+      *reinterpret_cast<f32x4*>(&qf[hh][d0]) = r;
     }
   }
   __syncthreads();
 
-  // 2. A operand: row = head (l % 16 < G), k = dims 32 ks + 8 (l / 16) + j
+  // 2. A operand: row = head (l % 16 < G), k = dims 32 ks + 8 (l / 16) + j; wave w writes k steps 2 w, 2 w + 1
   {
     const int hr = lane & 15, kgq = lane >> 4;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
+    for (int u = 0; u < 2; ++u) {
+      const int ks = 2 * wave + u;
+      bf16x8 a;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qa[ks][j] = (__bf16)(hr < G ? qf[hr][32 * ks + 8 * kgq + j] : 0.f);
-  }
-
-  // 3. tiles key0 = k_begin + 16 wave + 64 i, two per iteration: both tiles' loads are in flight before the first
-  // tile's math (the second only when the wave has it); the first pair is issued before the q prologue above
-  for (; key0 < k_end;) {
-    tile_compute(key0, ka, va);
-    if (two) tile_compute(key0 + 4 * kDecTile, kb2, vb2);
-    key0 += 8 * kDecTile;
-    if (key0 < k_end) {
-      two = key0 + 4 * kDecTile < k_end;
-      tile_load(key0, ka, va);
-      if (two) tile_load(key0 + 4 * kDecTile, kb2, vb2);
+      for (int j = 0; j < 8; ++j) a[j] = (__bf16)(hr < G ? qf[hr][32 * ks + 8 * kgq + j] : 0.f);
+      qfrag[ks][lane] = a;
     }
+  }
+  __syncthreads();
+
+  // K / V tile registers, two sets used alternately (indices are compile-time after unrolling). Loads are issued
+  // for every tile of the span, with rows clamped into the cache, so that none sits behind a branch. The first
+  // tile's loads go out only once the query is in: issued earlier, they (and every other block's) would queue ahead
+  // of the query's loads at the memory controllers, and nothing can be computed before the query arrives.
+  const int key_w = k_begin + kDecTile * wave;
+  bf16x8 kt[2][8];
+  u32x4 vt[2][kDecTile / 2];
+  tile_load(key_w, kt[0], vt[0]);
+
+  // 3. tiles key_w + 64 t, t < NT, fully unrolled: tile t + 1's loads are issued before tile t is computed. A
+  // tile wholly past the span is loaded (clamped rows) but not computed: its keys carry no weight, and the rows it
+  // read may lie beyond the cached length.
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (t + 1 < NT) tile_load(key_w + 4 * kDecTile * (t + 1), kt[(t + 1) & 1], vt[(t + 1) & 1]);
+    if (key_w + 4 * kDecTile * t < k_end) tile_compute(key_w + 4 * kDecTile * t, kt[t & 1], vt[t & 1]);
   }
 
   // 4. fold the two key-parity halves, then merge the four waves in LDS
@@ -219,74 +259,78 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   }
 }
 
-// Merge over splits, gate, store. One block per (query head, row, quarter of the head dims): the split weights
-// exp(m_s - M) are formed once in LDS, then four groups of 64 threads each fold a quarter of the splits for one dim
-// per thread (256-byte coalesced loads), and the four groups are summed in LDS.
+// Merge over splits, gate, store. One block per (query head, row, slice of 32 head dims): thread (g, d) folds the
+// splits g, g + 8, ... of dim d with an online log-sum-exp, loading eight splits' (max, sum, acc) at a time before
+// using any of them; the eight groups are combined in LDS.
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __restrict__ part,
                                                                 const __bf16* __restrict__ gate,
                                                                 __bf16* __restrict__ out, int Hq, int Hkv, int S) {
-  const int h = blockIdx.x, b = blockIdx.y, dq = blockIdx.z, tid = threadIdx.x;
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int G = Hq / Hkv, kvh = h / G, hh = h % G;
+  const int grp = tid >> 5, d = 32 * blockIdx.z + (tid & 31);
   const size_t sstride = (size_t)G * (kDecD + 2);
   const float* pb = part + ((size_t)b * Hkv + kvh) * S * sstride + (size_t)hh * (kDecD + 2);
-  extern __shared__ float wsh[];  // [S] weights
-  __shared__ float red[2][4];
-  __shared__ float accs[4][64];
-  // global max over splits
-  float mx = -INFINITY;
-  for (int s = tid; s < S; s += 256) mx = fmaxf(mx, pb[s * sstride + kDecD]);
+  __shared__ float gm[8], gl[8], go[8][32];
+  float M = -INFINITY, Lsum = 0.f, O = 0.f;
+  for (int s0 = grp; s0 < S; s0 += 64) {
+    float m[8], l[8], a[8];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  if ((tid & 63) == 0) red[0][tid >> 6] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
-  float ls = 0.f;
-  for (int s = tid; s < S; s += 256) {
-    const float ms = pb[s * sstride + kDecD];
-    const float w = (ms == -INFINITY || M == -INFINITY) ? 0.f : __expf(ms - M);
-    wsh[s] = w;
-    ls += w * pb[s * sstride + kDecD + 1];
+    for (int u = 0; u < 8; ++u) {
+      const int s = min(s0 + 8 * u, S - 1);
+      m[u] = pb[(size_t)s * sstride + kDecD];
+      l[u] = pb[(size_t)s * sstride + kDecD + 1];
+      a[u] = pb[(size_t)s * sstride + d];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (s0 + 8 * u >= S || m[u] == -INFINITY) continue;
+      const float mn = fmaxf(M, m[u]);
+      const float c0 = __expf(M - mn), c1 = __expf(m[u] - mn);
+      Lsum = Lsum * c0 + l[u] * c1;
+      O = O * c0 + a[u] * c1;
+      M = mn;
+    }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ls += __shfl_xor(ls, o, 64);
-  if ((tid & 63) == 0) red[1][tid >> 6] = ls;
-  __syncthreads();
-  const float Lsum = red[1][0] + red[1][1] + red[1][2] + red[1][3];
-  const int grp = tid >> 6, d = 64 * dq + (tid & 63);
-  float acc = 0.f;
-  int s = grp;
-  for (; s + 28 < S; s += 32) {  // eight independent loads in flight per thread
-    float x[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = pb[(size_t)(s + 4 * u) * sstride + d];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) acc += wsh[s + 4 * u] * x[u];
+  if ((tid & 31) == 0) {
+    gm[grp] = M;
+    gl[grp] = Lsum;
   }
-  for (; s < S; s += 4) acc += wsh[s] * pb[(size_t)s * sstride + d];
-  accs[grp][tid & 63] = acc;
+  go[grp][tid & 31] = O;
   __syncthreads();
-  if (tid < 64) {
-    const float O = accs[0][tid] + accs[1][tid] + accs[2][tid] + accs[3][tid];
+  if (tid < 32) {
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) Mx = fmaxf(Mx, gm[g]);
+    float Lt = 0.f, Ot = 0.f;
+    if (Mx != -INFINITY) {
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        const float w = gm[g] == -INFINITY ? 0.f : __expf(gm[g] - Mx);
+        Lt += gl[g] * w;
+        Ot += go[g][tid] * w;
+      }
+    }
     const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + d;
-    const float res = Lsum > 0.f ? O / Lsum : 0.f;
+    const float res = Lt > 0.f ? Ot / Lt : 0.f;
     out[oi] = (__bf16)(res * sigmoidf_((float)gate[oi]));
   }
 }
 
-static int decode_splits(int64_t B, int64_t Hkv, int64_t max_len, int64_t splits, int* L_out) {
+// Split of the context: a block's span is 64 NT keys (NT 16-key tiles per wave), NT a power of two <= 16. By
+// default the spans are sized so that about 512 blocks (two per CU, all resident at once) cover B x Hkv contexts.
+constexpr int kMaxNT = 16;
+static int decode_splits(int64_t B, int64_t Hkv, int64_t max_len, int64_t splits, int* nt_out) {
   int64_t S = splits;
   if (S <= 0) {
-    const int64_t target = 512;  // blocks: two per CU
+    const int64_t target = 512;
     S = (target + B * Hkv - 1) / (B * Hkv);
   }
-  const int64_t max_s = (max_len + 127) / 128;  // at least two 16-key tiles per wave
-  if (S > max_s) S = max_s;
   if (S < 1) S = 1;
-  int64_t L = (max_len + S - 1) / S;
-  L = (L + 63) / 64 * 64;
-  S = (max_len + L - 1) / L;
-  *L_out = (int)L;
-  return (int)S;
+  const int64_t L0 = (max_len + S - 1) / S;
+  int nt = 1;
+  while (nt < kMaxNT && (int64_t)64 * nt < L0) nt <<= 1;
+  *nt_out = nt;
+  return (int)((max_len + 64 * nt - 1) / (64 * nt));
 }
 
 }  // namespace q35
@@ -295,8 +339,8 @@ extern "C" size_t q35_gated_attn_decode_workspace_bytes(int64_t B, int64_t Hq, i
                                                         int64_t max_len, int64_t splits) {
   using namespace q35;
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0) return 0;
-  int L;
-  const int S = decode_splits(B, Hkv, max_len, splits, &L);
+  int nt;
+  const int S = decode_splits(B, Hkv, max_len, splits, &nt);
   return (size_t)B * Hq * S * (size_t)(D + 2) * sizeof(float);
 }
 
@@ -309,30 +353,40 @@ extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const v
   if (!q || !k_cache || !v_cache || !gate || !cache_len || !out) return Q35_EINVAL;
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D || (rot & 1))
     return Q35_EINVAL;
+  if (rot % 8 != 0) return Q35_EUNSUPPORTED;
   if (rot > 0 && (!cos || !sin)) return Q35_EINVAL;
   if (D != kDecD || B > 65535 || Hkv > 65535) return Q35_EUNSUPPORTED;
   const int64_t G = Hq / Hkv;
   if (G != 1 && G != 2 && G != 4 && G != 8) return Q35_EUNSUPPORTED;
-  int L;
-  const int S = decode_splits(B, Hkv, max_len, splits, &L);
+  int nt;
+  const int S = decode_splits(B, Hkv, max_len, splits, &nt);
+  if ((int64_t)S * 64 * nt > ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
   const size_t need = q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits);
   if (!workspace || workspace_bytes < need) return Q35_EWORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   float* part = (float*)workspace;
   dim3 grid(S, (unsigned)Hkv, (unsigned)B), block(256);
-#define Q35_DEC_LAUNCH(GG)                                                                                     \
-  hipLaunchKernelGGL(attn_decode_partial_kernel<GG>, grid, block, 0, st, (const __bf16*)q,                     \
+#define Q35_DEC_LAUNCH(GG, NT)                                                                                   \
+  hipLaunchKernelGGL((attn_decode_partial_kernel<GG, NT>), grid, block, 0, st, (const __bf16*)q,                \
                      (const __bf16*)k_cache, (const __bf16*)v_cache, cache_len, cos, sin, (int)rot, part, (int)Hq, \
-                     (int)Hkv, (int)max_len, S, L, scale)
-  switch (G) {
-    case 1: Q35_DEC_LAUNCH(1); break;
-    case 2: Q35_DEC_LAUNCH(2); break;
-    case 4: Q35_DEC_LAUNCH(4); break;
-    default: Q35_DEC_LAUNCH(8); break;
+                     (int)Hkv, (int)max_len, S, scale)
+#define Q35_DEC_NT(GG)                        \
+  switch (nt) {                               \
+    case 1: Q35_DEC_LAUNCH(GG, 1); break;     \
+    case 2: Q35_DEC_LAUNCH(GG, 2); break;     \
+    case 4: Q35_DEC_LAUNCH(GG, 4); break;     \
+    case 8: Q35_DEC_LAUNCH(GG, 8); break;     \
+    default: Q35_DEC_LAUNCH(GG, 16); break;   \
   }
+  switch (G) {
+    case 1: Q35_DEC_NT(1); break;
+    case 2: Q35_DEC_NT(2); break;
+    case 4: Q35_DEC_NT(4); break;
+    default: Q35_DEC_NT(8); break;
+  }
+#undef Q35_DEC_NT
 #undef Q35_DEC_LAUNCH
-  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3((unsigned)Hq, (unsigned)B, kDecD / 64), dim3(256),
-                     (size_t)S * sizeof(float), st, part,
+  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3((unsigned)Hq, (unsigned)B, kDecD / 32), dim3(256), 0, st, part,
                      (const __bf16*)gate, (__bf16*)out, (int)Hq, (int)Hkv, S);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }

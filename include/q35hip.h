@@ -101,7 +101,9 @@ int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const vo
  *   k_cache, v_cache: [B, Hkv, max_len, D] bf16, keys already rotated; row b uses keys 0 .. cache_len[b] - 1
  *   cache_len: [B] int32 on the device (1 <= cache_len[b] <= max_len)
  *   gate: [B, Hq * D] bf16    out: [B, Hq * D] bf16
- *   splits <= 0 lets the library choose the split count. Needs
+ *   cos, sin: [P, rot / 2] fp32 by position (P >= max_len); rot a multiple of 8 (Q35_EUNSUPPORTED otherwise)
+ *   splits <= 0 lets the library choose the split count (a request is rounded to whole 64-key multiples of a
+ *   power-of-two span, so the count used may be lower). Needs
  *   q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits) bytes of workspace.
  */
 size_t q35_gated_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
