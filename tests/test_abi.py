@@ -86,10 +86,13 @@ def test_validation_rejects_without_launching():
 
 
 def test_decode_workspace_scales_with_splits():
+    """The workspace holds one partial per split; a split request is rounded to a power-of-two span of at most
+    1024 keys (64 keys x 16 tiles), so 8 and 16 splits of 8192 keys are honoured and 4 becomes 8."""
     L = q35hip.lib()
-    a = L.q35_gated_attn_decode_workspace_bytes(3, 8, 2, 256, 8192, 4)
-    b = L.q35_gated_attn_decode_workspace_bytes(3, 8, 2, 256, 8192, 8)
-    assert a > 0 and b == 2 * a
+    a = L.q35_gated_attn_decode_workspace_bytes(3, 8, 2, 256, 8192, 8)
+    b = L.q35_gated_attn_decode_workspace_bytes(3, 8, 2, 256, 8192, 16)
+    c = L.q35_gated_attn_decode_workspace_bytes(3, 8, 2, 256, 8192, 4)
+    assert a > 0 and b == 2 * a and c == a
 
 
 def test_ops_refuse_cpu_tensors():
