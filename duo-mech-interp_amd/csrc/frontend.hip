@@ -1,0 +1,280 @@
+// The per-layer work around the two mixers, as HBM-bound passes over the fused projection output y (one GEMM per
+// layer produces every projection of a token as one row of y):
+//
+//   gdn_conv_kernel        Gated DeltaNet front end (HF:454-499; WGSL conv / convState, engine/kernels_qwen35.js
+//                          :127-178, and the gate terms of `delta`, :226-229): causal depthwise conv (K taps, carried
+//                          state of the previous K-1 inputs) + SiLU over the q|k|v channels of y, split into dense
+//                          q, k [B, T, Hk, dk] and v [B, T, Hv, dv]; beta = sigmoid(b), g = -exp(A_log) *
+//                          softplus(a + dt_bias) (softplus threshold 20) from the b and a columns of y; the conv state
+//                          advanced by the call's T inputs.
+//   gated_rmsnorm_kernel   Qwen3_5RMSNormGated (HF:168-184; engine/kernels_qwen35.js:237-243): per (token, head)
+//                          o * rsqrt(mean o^2 + eps) * w * silu(z) * head_scale, with plain w.
+//   attn_prep_kernel       attention front end (HF:667-680; WGSL attnPrep, engine/kernels_qwen35.js:18-69): per
+//                          head RMSNorm with (1 + w) of q and k, the per-head [q | gate] halves of q_proj split apart,
+//                          dense bf16 q, gate, k, v for the prefill kernel, and the rotated keys and the values
+//                          written into the bf16 KV cache at positions pos[b] + t (pos read on the device, so that a
+//                          captured decode step replays at the right position).
+#include "q35_common.h"
+#include "q35hip.h"
+
+namespace q35 {
+
+constexpr int kConvMaxK = 8;
+constexpr int kConvCh = 64;    // channels per conv block (16 quads)
+constexpr int kConvTl = 16;    // time lanes per conv block
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+
+template <typename T> __device__ __forceinline__ void store4(T* p, const f32x4& v);
+template <> __device__ __forceinline__ void store4<float>(float* p, const f32x4& v) {
+  *reinterpret_cast<f32x4*>(p) = v;
+}
+template <> __device__ __forceinline__ void store4<__bf16>(__bf16* p, const f32x4& v) {
+  bf16x4 r = {(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+  *reinterpret_cast<bf16x4*>(p) = r;
+}
+
+// grid (ceil(C / 64) + 1, B), 256 threads. Blocks x < nsl: a slice of 64 conv channels of batch row b over all T
+// tokens (thread = channel quad cq x time lane tl, tokens tl, tl + 16, ...), then the slice's conv state. Block
+// x == nsl: the gate terms of row b. Each (b, channel) has a single owner block, so the state is read, and after a
+// barrier rewritten, in place.
+template <typename Tout>
+__global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__ y, int64_t ldy,
+                                                       const float* __restrict__ cw, const float* __restrict__ cbias,
+                                                       float* __restrict__ cstate, const float* __restrict__ A_log,
+                                                       const float* __restrict__ dt_bias, int b_off, int a_off,
+                                                       Tout* __restrict__ qo, Tout* __restrict__ ko,
+                                                       Tout* __restrict__ vo, float* __restrict__ go,
+                                                       float* __restrict__ betao, int T, int C, int Kd, int Vd,
+                                                       int Hv, int K) {
+  const int b = blockIdx.y, tid = threadIdx.x;
+  const int nsl = (C + kConvCh - 1) / kConvCh;
+  if ((int)blockIdx.x == nsl) {
+    for (int i = tid; i < T * Hv; i += 256) {
+      const int t = i / Hv, h = i - t * Hv;
+      const float* row = y + ((int64_t)b * T + t) * ldy;
+      const size_t oi = ((size_t)b * T + t) * Hv + h;
+      betao[oi] = 1.f / (1.f + __expf(-row[b_off + h]));
+      go[oi] = -__expf(A_log[h]) * softplus_f(row[a_off + h] + dt_bias[h]);
+    }
+    return;
+  }
+  const int cq = tid & 15, tl = tid >> 4;
+  const int c = kConvCh * blockIdx.x + 4 * cq;
+  const bool cvalid = c < C;
+  const int cc = cvalid ? c : C - 4;
+  float w[4][kConvMaxK];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int i = 0; i < kConvMaxK; ++i) w[e][i] = i < K ? cw[(size_t)(cc + e) * K + i] : 0.f;
+  f32x4 bias = zero4();
+  if (cbias) bias = *reinterpret_cast<const f32x4*>(cbias + cc);
+  float* st = cstate + (size_t)b * (K - 1) * C;
+  // output destination of this quad: q, k or v (a quad never straddles a boundary: Kd, Vd are multiples of 4)
+  Tout* dst;
+  int dstride, dcol;
+  if (cc < Kd) { dst = qo; dstride = Kd; dcol = cc; }
+  else if (cc < 2 * Kd) { dst = ko; dstride = Kd; dcol = cc - Kd; }
+  else { dst = vo; dstride = Vd; dcol = cc - 2 * Kd; }
+  for (int t = tl; t < T; t += kConvTl) {
+    f32x4 acc = bias;
+#pragma unroll
+    for (int i = 0; i < kConvMaxK; ++i) {
+      if (i >= K) break;
+      const int ts = t - (K - 1) + i;  // input time of tap i
+      const f32x4 x = ts >= 0 ? *reinterpret_cast<const f32x4*>(y + ((int64_t)b * T + ts) * ldy + cc)
+                              : *reinterpret_cast<const f32x4*>(st + (size_t)(K - 1 + ts) * C + cc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += w[e][i] * x[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = silu_f(acc[e]);
+    if (cvalid) store4<Tout>(dst + ((size_t)b * T + t) * dstride + dcol, acc);
+  }
+  __syncthreads();
+  // state <- the last K-1 entries of [old state | this call's inputs]; one thread per quad reads all its sources
+  // before writing any slot
+  if (tl == 0 && cvalid) {
+    f32x4 nv[kConvMaxK - 1];
+#pragma unroll
+    for (int j = 0; j < kConvMaxK - 1; ++j) {
+      if (j >= K - 1) break;
+      const int src = T + j;  // index into [old (K-1) | inputs (T)]
+      nv[j] = src >= K - 1 ? *reinterpret_cast<const f32x4*>(y + ((int64_t)b * T + src - (K - 1)) * ldy + c)
+                           : *reinterpret_cast<const f32x4*>(st + (size_t)src * C + c);
+    }
+#pragma unroll
+    for (int j = 0; j < kConvMaxK - 1; ++j) {
+      if (j >= K - 1) break;
+      *reinterpret_cast<f32x4*>(st + (size_t)j * C + c) = nv[j];
+    }
+  }
+}
+
+// One wave per (token m, head h) of o [M, Hv, dv]; dv = 128 (two values per lane). Four waves per block.
+template <typename T>
+__global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict__ o, const float* __restrict__ z,
+                                                            int64_t ldz, const float* __restrict__ w,
+                                                            const float* __restrict__ head_scale, T* __restrict__ out,
+                                                            int64_t M, int Hv, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t job = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (job >= M * Hv) return;
+  const int64_t m = job / Hv;
+  const int h = (int)(job - m * Hv);
+  const T* orow = o + job * 128;
+  const float x0 = to_f32(orow[2 * lane]), x1 = to_f32(orow[2 * lane + 1]);
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
+  const float r = rsqrtf(ss * (1.f / 128.f) + eps);
+  const float* zr = z + m * ldz + h * 128;
+  const float hs = head_scale ? head_scale[h] : 1.f;
+  // HF rounds the normalised value to the input dtype before the weight multiply
+  const float n0 = to_f32(from_f32<T>(x0 * r)), n1 = to_f32(from_f32<T>(x1 * r));
+  T* orw = out + job * 128;
+  orw[2 * lane] = from_f32<T>(w[2 * lane] * n0 * silu_f(zr[2 * lane]) * hs);
+  orw[2 * lane + 1] = from_f32<T>(w[2 * lane + 1] * n1 * silu_f(zr[2 * lane + 1]) * hs);
+}
+
+// One wave per (token m, job j) with j < Hq: query head j; Hq <= j < Hq + Hkv: key head; then value heads.
+// D = 256: four values per lane (dims 4 l .. 4 l + 3). Four waves per block.
+__global__ __launch_bounds__(256) void attn_prep_kernel(const float* __restrict__ y, int64_t ldy,
+                                                        const float* __restrict__ qw, const float* __restrict__ kw,
+                                                        float eps, const float* __restrict__ cos_t,
+                                                        const float* __restrict__ sin_t, int rot,
+                                                        const int32_t* __restrict__ pos, __bf16* __restrict__ q_out,
+                                                        __bf16* __restrict__ gate_out, __bf16* __restrict__ k_out,
+                                                        __bf16* __restrict__ v_out, __bf16* __restrict__ k_cache,
+                                                        __bf16* __restrict__ v_cache, int max_len, int T, int Hq,
+                                                        int Hkv, int64_t M) {
+  constexpr int D = 256;
+  const int lane = threadIdx.x & 63;
+  const int jobs = Hq + 2 * Hkv;
+  const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (g >= M * jobs) return;
+  const int64_t m = g / jobs;
+  const int j = (int)(g - m * jobs);
+  const int b = (int)(m / T), t = (int)(m - (int64_t)b * T);
+  const float* row = y + m * ldy;
+  const int d0 = 4 * lane;
+  if (j < Hq) {  // query head j: normalise q, copy the gate half
+    const f32x4 x = *reinterpret_cast<const f32x4*>(row + (size_t)j * 2 * D + d0);
+    const f32x4 gt = *reinterpret_cast<const f32x4*>(row + (size_t)j * 2 * D + D + d0);
+    const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+    const float r = rsqrtf(ss * (1.f / D) + eps);
+    const f32x4 wv = *reinterpret_cast<const f32x4*>(qw + d0);
+    f32x4 qn;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qn[e] = x[e] * r * (1.f + wv[e]);
+    store4<__bf16>(q_out + (m * Hq + j) * D + d0, qn);
+    store4<__bf16>(gate_out + (m * Hq + j) * D + d0, gt);
+    return;
+  }
+  const int p = min(max(pos[b], 0), max_len) + t;  // absolute position of this token
+  if (j < Hq + Hkv) {  // key head
+    const int kh = j - Hq;
+    const f32x4 x = *reinterpret_cast<const f32x4*>(row + (size_t)Hq * 2 * D + (size_t)kh * D + d0);
+    const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+    const float r = rsqrtf(ss * (1.f / D) + eps);
+    const f32x4 wv = *reinterpret_cast<const f32x4*>(kw + d0);
+    f32x4 kn;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) kn[e] = x[e] * r * (1.f + wv[e]);
+    if (k_out) store4<__bf16>(k_out + (m * Hkv + kh) * D + d0, kn);
+    // rotate-half partner of dims d0..d0+3 (d < rot): d +- rot/2, held by lane l +- rot/8
+    const int half = rot >> 1;
+    const int pl = d0 < half ? lane + half / 4 : lane - half / 4;
+    f32x4 pn;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pn[e] = __shfl(kn[e], d0 < rot ? pl : lane, 64);
+    if (p < max_len) {
+      f32x4 kr = kn;
+      if (d0 < rot) {
+        const int j0 = d0 < half ? d0 : d0 - half;
+        const f32x4 cv = *reinterpret_cast<const f32x4*>(cos_t + (size_t)p * half + j0);
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(sin_t + (size_t)p * half + j0);
+        const float sg = d0 < half ? -1.f : 1.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kr[e] = kn[e] * cv[e] + sg * pn[e] * sv[e];
+      }
+      store4<__bf16>(k_cache + (((size_t)b * Hkv + kh) * max_len + p) * D + d0, kr);
+    }
+    return;
+  }
+  const int vh = j - Hq - Hkv;  // value head
+  const f32x4 x = *reinterpret_cast<const f32x4*>(row + (size_t)Hq * 2 * D + (size_t)(Hkv + vh) * D + d0);
+  if (v_out) store4<__bf16>(v_out + (m * Hkv + vh) * D + d0, x);
+  if (p < max_len) store4<__bf16>(v_cache + (((size_t)b * Hkv + vh) * max_len + p) * D + d0, x);
+}
+
+}  // namespace q35
+
+extern "C" int q35_gdn_conv(const float* y, int64_t ldy, const float* conv_w, const float* conv_bias,
+                            float* conv_state, const float* A_log, const float* dt_bias, int64_t b_off, int64_t a_off,
+                            void* q, void* k, void* v, float* g, float* beta, int64_t B, int64_t T, int64_t Hk,
+                            int64_t dk, int64_t Hv, int64_t dv, int64_t K, int dtype, q35_stream_t stream) {
+  using namespace q35;
+  if (!y || !conv_w || !conv_state || !A_log || !dt_bias || !q || !k || !v || !g || !beta) return Q35_EINVAL;
+  if (B <= 0 || T <= 0 || Hk <= 0 || dk <= 0 || Hv <= 0 || dv <= 0 || K < 2) return Q35_EINVAL;
+  const int64_t Kd = Hk * dk, Vd = Hv * dv, C = 2 * Kd + Vd;
+  if (ldy < C || b_off < 0 || a_off < 0 || b_off + Hv > ldy || a_off + Hv > ldy) return Q35_EINVAL;
+  if (K > kConvMaxK || (Kd & 3) || (Vd & 3) || (ldy & 3) || ((uintptr_t)y & 15) || ((uintptr_t)conv_state & 15))
+    return Q35_EUNSUPPORTED;
+  if (conv_bias && ((uintptr_t)conv_bias & 15)) return Q35_EUNSUPPORTED;
+  if (B > 65535 || B * T * ldy > ((int64_t)1 << 40) || T * Hv > 0x7fffffff || C > 0x7fffffff)
+    return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((C + kConvCh - 1) / kConvCh + 1), (unsigned)B);
+  if (dtype == Q35_F32)
+    hipLaunchKernelGGL(gdn_conv_kernel<float>, grid, dim3(256), 0, st, y, ldy, conv_w, conv_bias, conv_state, A_log,
+                       dt_bias, (int)b_off, (int)a_off, (float*)q, (float*)k, (float*)v, g, beta, (int)T, (int)C,
+                       (int)Kd, (int)Vd, (int)Hv, (int)K);
+  else if (dtype == Q35_BF16)
+    hipLaunchKernelGGL(gdn_conv_kernel<__bf16>, grid, dim3(256), 0, st, y, ldy, conv_w, conv_bias, conv_state,
+                       A_log, dt_bias, (int)b_off, (int)a_off, (__bf16*)q, (__bf16*)k, (__bf16*)v, g, beta, (int)T,
+                       (int)C, (int)Kd, (int)Vd, (int)Hv, (int)K);
+  else
+    return Q35_EUNSUPPORTED;
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+extern "C" int q35_gated_rmsnorm(const void* o, const float* z, int64_t ldz, const float* w, const float* head_scale,
+                                 void* out, int64_t M, int64_t Hv, int64_t dv, float eps, int dtype,
+                                 q35_stream_t stream) {
+  using namespace q35;
+  if (!o || !z || !w || !out || M <= 0 || Hv <= 0 || dv <= 0 || ldz < Hv * dv) return Q35_EINVAL;
+  if (dv != 128) return Q35_EUNSUPPORTED;
+  const int64_t blocks = (M * Hv + 3) / 4;
+  if (blocks > 0x7fffffff) return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == Q35_F32)
+    hipLaunchKernelGGL(gated_rmsnorm_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)o, z,
+                       ldz, w, head_scale, (float*)out, M, (int)Hv, eps);
+  else if (dtype == Q35_BF16)
+    hipLaunchKernelGGL(gated_rmsnorm_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st, (const __bf16*)o, z,
+                       ldz, w, head_scale, (__bf16*)out, M, (int)Hv, eps);
+  else
+    return Q35_EUNSUPPORTED;
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+extern "C" int q35_attn_prep(const float* y, int64_t ldy, const float* q_norm_w, const float* k_norm_w, float eps,
+                             const float* cos, const float* sin, int64_t rot, const int32_t* pos, void* q_out,
+                             void* gate_out, void* k_out, void* v_out, void* k_cache, void* v_cache, int64_t max_len,
+                             int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, q35_stream_t stream) {
+  using namespace q35;
+  if (!y || !q_norm_w || !k_norm_w || !pos || !q_out || !gate_out || !k_cache || !v_cache) return Q35_EINVAL;
+  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0 || rot < 0 || rot > D) return Q35_EINVAL;
+  if (ldy < 2 * Hq * D + 2 * Hkv * D) return Q35_EINVAL;
+  if (rot > 0 && (!cos || !sin)) return Q35_EINVAL;
+  if (D != 256 || (rot % 8) != 0 || (ldy & 3) || ((uintptr_t)y & 15)) return Q35_EUNSUPPORTED;
+  const int64_t M = B * T;
+  const int64_t blocks = (M * (Hq + 2 * Hkv) + 3) / 4;
+  if (blocks > 0x7fffffff || max_len > 0x7fffffff || T > 0x7fffffff) return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)blocks), dim3(256), 0, st, y, ldy, q_norm_w, k_norm_w, eps, cos,
+                     sin, (int)rot, pos, (__bf16*)q_out, (__bf16*)gate_out, (__bf16*)k_out, (__bf16*)v_out,
+                     (__bf16*)k_cache, (__bf16*)v_cache, (int)max_len, (int)T, (int)Hq, (int)Hkv, M);
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}

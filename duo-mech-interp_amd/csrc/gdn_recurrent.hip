@@ -77,14 +77,16 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(const Tin* __restric
 
   __shared__ f32x4 red[2][4][8][2];  // [token parity][wave][column quad][S^T k | S^T q]
 
+  // The first token's inputs are loaded before the state: issued after it, they would queue behind every block's
+  // state reads at the memory controllers, and nothing can be computed without them.
+  RecIn cur, nxt;
+  rec_load(cur, q, k, v, g, beta, (size_t)b * T, Hk, kh, H, h, rg, j0, lane);
+  asm volatile("" ::: "memory");
   const size_t sbase = ((size_t)b * H + h) * kGdnD * kGdnD;
   f32x4 s[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     s[i] = s_in ? *reinterpret_cast<const f32x4*>(s_in + sbase + (size_t)(rg + 32 * i) * kGdnD + j0) : zero4();
-
-  RecIn cur, nxt;
-  rec_load(cur, q, k, v, g, beta, (size_t)b * T, Hk, kh, H, h, rg, j0, lane);
   for (int t = 0; t < T; ++t) {
     const int par = t & 1;
     const size_t tok = (size_t)b * T + t;

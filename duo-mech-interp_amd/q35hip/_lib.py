@@ -16,7 +16,7 @@ EXPORTS = [
     "q35_gdn_recurrent", "q35_gdn_chunk_workspace_bytes", "q35_gdn_chunk_prefill",
     "q35_gated_attn_prefill_workspace_bytes", "q35_gated_attn_prefill", "q35_gated_attn_decode_workspace_bytes",
     "q35_gated_attn_decode",
-    "q35_resid_add_rows",
+    "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep",
 ]
 
 Q35_F32, Q35_BF16 = 0, 1
@@ -41,6 +41,9 @@ _SIGS = {
     "q35_gated_attn_decode_workspace_bytes": ([I64, I64, I64, I64, I64, I64], SZ),
     "q35_gated_attn_decode": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, F32, I64, P, SZ, P], I32),
     "q35_resid_add_rows": ([P, P, P, I64, I64, I64, I64, I32, P], I32),
+    "q35_gdn_conv": ([P, I64, P, P, P, P, P, I64, I64, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, P], I32),
+    "q35_gated_rmsnorm": ([P, P, I64, P, P, P, I64, I64, I64, F32, I32, P], I32),
+    "q35_attn_prep": ([P, I64, P, P, F32, P, P, I64, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I32),
 }
 
 

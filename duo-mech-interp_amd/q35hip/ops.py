@@ -63,6 +63,13 @@ _LIB.define("gated_attn_prefill(Tensor q, Tensor k, Tensor v, Tensor gate, Tenso
 _LIB.define("gated_attn_decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor gate, Tensor cache_len, "
             "Tensor cos, Tensor sin, float scale, int splits) -> Tensor")
 _LIB.define("resid_add_rows_(Tensor(a!) x, Tensor vecs, Tensor? vec_of_row) -> ()")
+_LIB.define("gdn_conv(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
+            "Tensor dt_bias, int b_off, int a_off, int Hk, int dk, int Hv, int dv, bool bf16_out) "
+            "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
+_LIB.define("gated_rmsnorm(Tensor o, Tensor z, Tensor w, Tensor? head_scale, float eps) -> Tensor")
+_LIB.define("attn_prep(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, Tensor cos, Tensor sin, Tensor pos, "
+            "Tensor(a!) k_cache, Tensor(b!) v_cache, int Hq, int Hkv, bool want_kv) "
+            "-> (Tensor, Tensor, Tensor, Tensor)")
 
 
 # ---------------------------------------------------------------- gated delta rule
@@ -182,6 +189,87 @@ def _resid_add_impl(x, vecs, vec_of_row):
     check(st, "q35_resid_add_rows")
 
 
+# ---------------------------------------------------------------- layer front ends
+def _rows_view(t, width, what):
+    """A [..., width] fp32 view whose rows are evenly strided and whose last dim is dense: (rows, row stride)."""
+    _require(t.is_cuda and t.dtype == torch.float32, f"{what} must be an fp32 HIP tensor")
+    _require(t.shape[-1] == width and t.stride(-1) == 1, f"{what}: last dim {width}, dense")
+    rows = t.numel() // max(width, 1)
+    if t.dim() == 1:
+        return rows, width
+    flat = t.reshape(-1, width) if t.dim() > 2 else t
+    _require(flat.data_ptr() == t.data_ptr() and (rows <= 1 or flat.stride(0) >= width),
+             f"{what}: rows must be evenly strided")
+    return rows, flat.stride(0)
+
+
+def _gdn_conv_impl(y, conv_w, conv_bias, conv_state, A_log, dt_bias, b_off, a_off, Hk, dk, Hv, dv, bf16_out):
+    _on_gpu(conv_w, conv_bias, conv_state, A_log, dt_bias)
+    _require(y.is_cuda and y.dtype == torch.float32 and y.dim() == 3 and y.is_contiguous(),
+             "y: [B, T, W] fp32 dense (the fused projection output)")
+    B, T, W = y.shape
+    C = 2 * Hk * dk + Hv * dv
+    _require(conv_w.dim() == 2 and conv_w.shape[0] == C and conv_w.dtype == torch.float32, "conv_w: [C, K] fp32")
+    K = conv_w.shape[1]
+    _require(conv_state.dtype == torch.float32 and tuple(conv_state.shape) == (B, K - 1, C),
+             "conv_state: [B, K - 1, C] fp32")
+    _require(A_log.numel() == Hv and dt_bias.numel() == Hv, "A_log, dt_bias: [Hv]")
+    dt = torch.bfloat16 if bf16_out else torch.float32
+    q = torch.empty(B, T, Hk, dk, dtype=dt, device=y.device)
+    k = torch.empty_like(q)
+    v = torch.empty(B, T, Hv, dv, dtype=dt, device=y.device)
+    g = torch.empty(B, T, Hv, dtype=torch.float32, device=y.device)
+    beta = torch.empty_like(g)
+    st = _lib.lib().q35_gdn_conv(_ptr(y), W, _ptr(conv_w), _ptr(conv_bias), _ptr(conv_state), _ptr(A_log),
+                                 _ptr(dt_bias), int(b_off), int(a_off), _ptr(q), _ptr(k), _ptr(v), _ptr(g),
+                                 _ptr(beta), B, T, Hk, dk, Hv, dv, K, _DT[dt], _stream(y))
+    check(st, "q35_gdn_conv")
+    return q, k, v, g, beta
+
+
+def _gated_rmsnorm_impl(o, z, w, head_scale, eps):
+    _on_gpu(o, w, head_scale)
+    _require(o.dtype in _DT and o.dim() >= 2, "o: [..., Hv, dv] fp32 or bf16")
+    Hv, dv = o.shape[-2], o.shape[-1]
+    M = o.numel() // (Hv * dv)
+    rows, ldz = _rows_view(z, Hv * dv, "z")
+    _require(rows == M, "z must have one row per token of o")
+    _require(w.numel() == dv and w.dtype == torch.float32, "w: [dv] fp32")
+    if head_scale is not None:
+        _require(head_scale.numel() == Hv and head_scale.dtype == torch.float32, "head_scale: [Hv] fp32")
+    out = torch.empty(*o.shape[:-2], Hv * dv, dtype=o.dtype, device=o.device)
+    st = _lib.lib().q35_gated_rmsnorm(_ptr(o), _ptr(z), ldz, _ptr(w), _ptr(head_scale), _ptr(out), M, Hv, dv,
+                                      float(eps), _DT[o.dtype], _stream(o))
+    check(st, "q35_gated_rmsnorm")
+    return out
+
+
+def _attn_prep_impl(y, q_norm_w, k_norm_w, eps, cos, sin, pos, k_cache, v_cache, Hq, Hkv, want_kv):
+    _on_gpu(q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_cache)
+    _require(y.is_cuda and y.dtype == torch.float32 and y.dim() == 3 and y.is_contiguous(),
+             "y: [B, T, W] fp32 dense (the fused projection output)")
+    B, T, W = y.shape
+    _require(k_cache.dtype == torch.bfloat16 and v_cache.shape == k_cache.shape and k_cache.dim() == 4,
+             "caches: [B, Hkv, max_len, D] bf16")
+    _require(k_cache.shape[0] == B and k_cache.shape[1] == Hkv, "caches must match the batch and kv heads")
+    D, max_len = k_cache.shape[3], k_cache.shape[2]
+    _require(pos.dtype == torch.int32 and tuple(pos.shape) == (B,), "pos: [B] int32")
+    rot = _tables_check(cos, sin, max_len)
+    q = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=y.device)
+    gate = torch.empty(B, T, Hq * D, dtype=torch.bfloat16, device=y.device)
+    if want_kv:
+        k = torch.empty(B, T, Hkv, D, dtype=torch.bfloat16, device=y.device)
+        v = torch.empty_like(k)
+    else:
+        k = v = torch.empty(0, dtype=torch.bfloat16, device=y.device)
+    st = _lib.lib().q35_attn_prep(_ptr(y), W, _ptr(q_norm_w), _ptr(k_norm_w), float(eps), _ptr(cos), _ptr(sin), rot,
+                                  _ptr(pos), _ptr(q), _ptr(gate), _ptr(k) if want_kv else None,
+                                  _ptr(v) if want_kv else None, _ptr(k_cache), _ptr(v_cache), max_len, B, T, Hq, Hkv,
+                                  D, _stream(y))
+    check(st, "q35_attn_prep")
+    return q, gate, k, v
+
+
 def _no_cpu(name):
     def f(*args, **kwargs):
         raise Q35Error(f"q35hip: q35::{name} needs HIP device tensors; the product has no CPU path")
@@ -190,7 +278,9 @@ def _no_cpu(name):
 
 for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_", _gdn_decode_step_impl),
                      ("gdn_chunk_prefill", _gdn_chunk_impl), ("gated_attn_prefill", _attn_prefill_impl),
-                     ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl)]:
+                     ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
+                     ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl),
+                     ("attn_prep", _attn_prep_impl)]:
     _LIB.impl(_name, _impl, "CUDA")
     _LIB.impl(_name, _no_cpu(_name), "CPU")
 
@@ -271,3 +361,29 @@ def residual_steer_add_(x, vecs, vec_of_row=None):
     """x[r, t, :] += vecs[vec_of_row[r]] in place (negative index: no vector; None: min(r, nvec - 1))."""
     torch.ops.q35.resid_add_rows_(x, vecs, vec_of_row)
     return x
+
+
+def gdn_conv(y, conv_w, conv_state, A_log, dt_bias, *, num_k_heads, head_k_dim, num_v_heads, head_v_dim, b_off, a_off,
+             conv_bias=None, out_dtype=torch.float32):
+    """Gated DeltaNet front end (HF:454-499; engine/kernels_qwen35.js:127-178, :226-229) over the fused projection
+    output y [B, T, W]: returns (q, k [B, T, Hk, dk], v [B, T, Hv, dv] in out_dtype, g, beta [B, T, Hv] fp32) and
+    advances conv_state [B, K - 1, C] in place."""
+    w = conv_w.reshape(conv_w.shape[0], conv_w.shape[-1])
+    return torch.ops.q35.gdn_conv(y, w.float().contiguous(), conv_bias, conv_state, A_log.float().contiguous(),
+                                  dt_bias.float().contiguous(), int(b_off), int(a_off), int(num_k_heads),
+                                  int(head_k_dim), int(num_v_heads), int(head_v_dim), out_dtype == torch.bfloat16)
+
+
+def gated_rmsnorm(o, z, w, head_scale=None, eps=1e-6):
+    """Qwen3_5RMSNormGated (HF:168-184) per (token, head) with the engine's optional per-head scale
+    (engine/kernels_qwen35.js:243): o [..., Hv, dv], z [..., Hv * dv] fp32 (rows may be strided) -> [..., Hv * dv]."""
+    return torch.ops.q35.gated_rmsnorm(o, z, w.float().contiguous(), head_scale, float(eps))
+
+
+def attn_prep(y, q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_cache, *, num_heads, num_kv_heads, eps=1e-6,
+              want_kv=True):
+    """Attention front end (HF:667-680; engine/kernels_qwen35.js:18-69) over the fused projection output y: returns
+    (q [B, T, Hq, D], gate [B, T, Hq * D], k, v [B, T, Hkv, D]) in bf16, q and k RMS-normalised with (1 + w) and not
+    rotated, and writes rotated keys and values into the caches at positions pos[b] + t (pos: [B] int32 device)."""
+    return torch.ops.q35.attn_prep(y, q_norm_w.float().contiguous(), k_norm_w.float().contiguous(), float(eps), cos,
+                                   sin, pos, k_cache, v_cache, int(num_heads), int(num_kv_heads), bool(want_kv))

@@ -16,6 +16,11 @@
  *   q35_gated_attn_decode    same as above for one new token per row over a KV cache (engine/kernels_qwen35.js:73-123
  *                            with T = 1; HF decode through DynamicCache)
  *   q35_resid_add_rows       tests/engine_ref.py:49-53 residual vector hook; engine/kernels.js:190-203 `resAdd`
+ *   q35_gdn_conv             HF:454-499 (causal_conv1d_fn / causal_conv1d_update + SiLU, split, beta, g);
+ *                            engine/kernels_qwen35.js:127-178 `conv` + `convState`, :226-229 (gate terms of `delta`)
+ *   q35_gated_rmsnorm        HF:168-184 Qwen3_5RMSNormGated; engine/kernels_qwen35.js:237-243 (epilogue of `delta`)
+ *   q35_attn_prep            HF:667-680 (q / gate split, q_norm / k_norm, partial RoPE of k, cache update);
+ *                            engine/kernels_qwen35.js:18-69 `attnPrep`
  */
 #ifndef Q35HIP_H
 #define Q35HIP_H
@@ -123,6 +128,47 @@ int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cach
  */
 int q35_resid_add_rows(void* x, const float* vecs, const int32_t* vec_of_row, int64_t rows, int64_t T, int64_t H,
                        int64_t nvec, int dtype, q35_stream_t stream);
+
+/*
+ * Gated DeltaNet front end over the fused projection output y (one row per token):
+ *   y: [B, T, ldy] fp32, columns [0, C) the q|k|v channels (C = 2 Hk dk + Hv dv), columns b_off .. b_off + Hv the
+ *      beta logits b, a_off .. a_off + Hv the decay inputs a
+ *   conv_w: [C, K] fp32, conv_bias: [C] fp32 or NULL; conv_state: [B, K - 1, C] fp32, the previous K - 1 inputs
+ *      (oldest first), advanced in place by the call's T inputs
+ *   A_log, dt_bias: [Hv] fp32
+ *   out: q, k [B, T, Hk, dk] and v [B, T, Hv, dv] in dtype (silu(causal conv)), g, beta [B, T, Hv] fp32 with
+ *      beta = sigmoid(b), g = -exp(A_log) * softplus(a + dt_bias) (softplus threshold 20)
+ *   K <= 8; y, conv_state (and conv_bias) 16-byte aligned, ldy, dk * Hk and dv * Hv multiples of 4.
+ */
+int q35_gdn_conv(const float* y, int64_t ldy, const float* conv_w, const float* conv_bias, float* conv_state,
+                 const float* A_log, const float* dt_bias, int64_t b_off, int64_t a_off, void* q, void* k, void* v,
+                 float* g, float* beta, int64_t B, int64_t T, int64_t Hk, int64_t dk, int64_t Hv, int64_t dv,
+                 int64_t K, int dtype, q35_stream_t stream);
+
+/*
+ * Gated RMSNorm per (token, head): out = w * (o * rsqrt(mean(o^2) + eps)) * silu(z) * head_scale[h], the
+ * normalised o rounded to dtype before the weight multiply as HF does (plain w, not 1 + w).
+ *   o, out: [M, Hv, dv] dtype (may alias); z: [M, ldz] fp32, head h's gate at columns h dv .. h dv + dv - 1;
+ *   w: [dv] fp32; head_scale: [Hv] fp32 or NULL (ones). dv = 128.
+ */
+int q35_gated_rmsnorm(const void* o, const float* z, int64_t ldz, const float* w, const float* head_scale, void* out,
+                      int64_t M, int64_t Hv, int64_t dv, float eps, int dtype, q35_stream_t stream);
+
+/*
+ * Gated-attention front end over the fused projection output y: [B, T, ldy] fp32 holding per token
+ * [q_proj (Hq heads of [q (D) | gate (D)]) | k_proj (Hkv x D) | v_proj (Hkv x D)].
+ *   q_norm_w, k_norm_w: [D] fp32, RMSNorm with (1 + w) in fp32; cos, sin: [P, rot / 2] fp32 by absolute position
+ *   pos: [B] int32 on the device, the position of each row's first token of this call
+ *   out: q_out [B, T, Hq, D] bf16 (normalised, not rotated), gate_out [B, T, Hq * D] bf16, k_out / v_out
+ *        [B, T, Hkv, D] bf16 (normalised unrotated keys / values; either may be NULL), and the caches
+ *        k_cache, v_cache [B, Hkv, max_len, D] bf16 receive the rotated keys and the values at positions pos[b] + t
+ *        (positions at or past max_len are not written)
+ *   D = 256, rot a multiple of 8; y 16-byte aligned, ldy a multiple of 4.
+ */
+int q35_attn_prep(const float* y, int64_t ldy, const float* q_norm_w, const float* k_norm_w, float eps,
+                  const float* cos, const float* sin, int64_t rot, const int32_t* pos, void* q_out, void* gate_out,
+                  void* k_out, void* v_out, void* k_cache, void* v_cache, int64_t max_len, int64_t B, int64_t T,
+                  int64_t Hq, int64_t Hkv, int64_t D, q35_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -23,7 +23,7 @@ def declared_functions():
 def test_header_declares_the_boundary():
     names = declared_functions()
     for n in ["q35_gdn_recurrent", "q35_gdn_chunk_prefill", "q35_gated_attn_prefill", "q35_gated_attn_decode",
-              "q35_resid_add_rows"]:
+              "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep"]:
         assert n in names
 
 
@@ -37,7 +37,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 3
+    assert L.q35_abi_version() == 4
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -83,6 +83,19 @@ def test_validation_rejects_without_launching():
     assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 8, 2, 256, 128, 64, 0.1, 0,
                                    fake, 8, None) == 3
     assert L.q35_resid_add_rows(None, fake, None, 1, 1, 8, 1, 0, None) == 1
+    # front-end kernels: null pointers, inconsistent widths, unsupported sizes
+    assert L.q35_gdn_conv(None, 6144, fake, None, fake, fake, fake, 0, 0, fake, fake, fake, fake, fake, 1, 1, 16,
+                          128, 16, 128, 4, 0, None) == 1
+    assert L.q35_gdn_conv(fake, 100, fake, None, fake, fake, fake, 0, 0, fake, fake, fake, fake, fake, 1, 1, 16, 128,
+                          16, 128, 4, 0, None) == 1
+    assert L.q35_gdn_conv(fake, 6176, fake, None, fake, fake, fake, 6144, 6160, fake, fake, fake, fake, fake, 1, 1,
+                          16, 128, 16, 128, 9, 0, None) == 2
+    assert L.q35_gated_rmsnorm(fake, fake, 2048, fake, None, fake, 4, 16, 64, 1e-6, 0, None) == 2
+    assert L.q35_gated_rmsnorm(fake, fake, 100, fake, None, fake, 4, 16, 128, 1e-6, 0, None) == 1
+    assert L.q35_attn_prep(fake, 5120, fake, fake, 1e-6, fake, fake, 64, None, fake, fake, None, None, fake, fake, 16,
+                           1, 1, 8, 2, 256, None) == 1
+    assert L.q35_attn_prep(fake, 5120, fake, fake, 1e-6, fake, fake, 60, fake, fake, fake, None, None, fake, fake,
+                           16, 1, 1, 8, 2, 256, None) == 2
 
 
 def test_decode_workspace_scales_with_splits():

@@ -1,0 +1,127 @@
+"""Layer front ends on the GPU (conv + gates, gated RMSNorm, attention prep) against the CPU oracle.
+
+Tolerances (relative error, tests/engine.mjs:17): fp32 outputs <= 1e-5 (the kernels compute in fp32; only the
+summation order differs); bf16 outputs <= 4e-3 (one rounding to bf16, 2^-9 relative, on top of fp32 arithmetic).
+"""
+import pytest
+import torch
+
+import oracle
+import q35hip
+from oracle import frontend as of
+from oracle.attention import rope_inv_freq, rope_tables
+from q35hip import ops
+from gpu_util import announce, device
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+TOL_BF16 = 4e-3
+
+
+def _gdn_case(B, T, seed, Hk=16, dk=128, Hv=16, dv=128, K=4):
+    g = torch.Generator().manual_seed(seed)
+    C = 2 * Hk * dk + Hv * dv
+    W = C + Hv * dv + 2 * Hv          # [qkv | z | b | a], the fused projection row
+    y = torch.randn(B, T, W, generator=g)
+    conv_w = 0.5 * torch.randn(C, K, generator=g)
+    state = torch.randn(B, K - 1, C, generator=g)
+    A_log = torch.log(torch.rand(Hv, generator=g) * 16)
+    dt_bias = torch.ones(Hv) + 0.1 * torch.randn(Hv, generator=g)
+    return y, conv_w, state, A_log, dt_bias, C, W
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 37])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gdn_conv_matches_oracle(T, dtype):
+    dev = device()
+    B, Hk, dk, Hv, dv = 3, 16, 128, 16, 128
+    y, conv_w, state, A_log, dt_bias, C, W = _gdn_case(B, T, seed=T)
+    b_off, a_off = C + Hv * dv, C + Hv * dv + Hv
+    ref = of.gdn_conv(y, conv_w, state, A_log, dt_bias, Hk, dk, Hv, dv, b_off, a_off)
+    announce(f"gdn_conv T{T} {dtype}")
+    st = state.to(dev)
+    out = ops.gdn_conv(y.to(dev), conv_w.to(dev), st, A_log.to(dev), dt_bias.to(dev), num_k_heads=Hk, head_k_dim=dk,
+                       num_v_heads=Hv, head_v_dim=dv, b_off=b_off, a_off=a_off, out_dtype=dtype)
+    torch.cuda.synchronize()
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    for got, exp in zip(out[:3], ref[:3]):
+        assert got.dtype == dtype and got.is_contiguous()
+        assert oracle.rel_err(got.float().cpu(), exp) <= tol
+    for got, exp in zip(out[3:], ref[3:5]):
+        assert oracle.rel_err(got.cpu(), exp) <= TOL_F32
+    assert torch.equal(st.cpu(), ref[5])   # the state is a copy of inputs: exact
+
+
+def test_gdn_conv_bias_and_split_calls():
+    """Optional conv bias; a 37-token call equals 5 + 32 tokens with the state carried on the device."""
+    dev = device()
+    B, Hk, dk, Hv, dv = 2, 16, 128, 16, 128
+    y, conv_w, state, A_log, dt_bias, C, W = _gdn_case(B, 37, seed=40)
+    bias = torch.randn(C, generator=torch.Generator().manual_seed(41))
+    b_off, a_off = C + Hv * dv, C + Hv * dv + Hv
+    ref = of.gdn_conv(y, conv_w, state, A_log, dt_bias, Hk, dk, Hv, dv, b_off, a_off, conv_bias=bias)
+    announce("gdn_conv bias + split calls")
+    kw = dict(num_k_heads=Hk, head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=b_off, a_off=a_off)
+    st = state.to(dev)
+    yd = y.to(dev)
+    args = (conv_w.to(dev), st, A_log.to(dev), dt_bias.to(dev))
+    a = ops.gdn_conv(yd[:, :5].contiguous(), *args, conv_bias=bias.to(dev), **kw)
+    b = ops.gdn_conv(yd[:, 5:].contiguous(), *args, conv_bias=bias.to(dev), **kw)
+    torch.cuda.synchronize()
+    for i in range(5):
+        got = torch.cat([a[i], b[i]], dim=1).cpu()
+        assert oracle.rel_err(got, ref[i]) <= TOL_F32
+    assert torch.equal(st.cpu(), ref[5])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_scale", [False, True])
+def test_gated_rmsnorm_matches_oracle(dtype, with_scale):
+    dev = device()
+    g = torch.Generator().manual_seed(50)
+    B, T, Hv, dv = 3, 7, 16, 128
+    o = torch.randn(B, T, Hv, dv, generator=g).to(dtype)
+    y = torch.randn(B, T, 3 * Hv * dv, generator=g)            # z is a strided column range of a wider row
+    z = y[..., Hv * dv:2 * Hv * dv]
+    w = torch.randn(dv, generator=g)
+    hs = torch.rand(Hv, generator=g) + 0.5 if with_scale else None
+    ref = of.gated_rmsnorm(o, z, w, hs)
+    announce(f"gated_rmsnorm {dtype} scale={with_scale}")
+    yd = y.to(dev)
+    out = ops.gated_rmsnorm(o.to(dev), yd[..., Hv * dv:2 * Hv * dv], w.to(dev),
+                            None if hs is None else hs.to(dev))
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and tuple(out.shape) == (B, T, Hv * dv)
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    assert oracle.rel_err(out.float().cpu(), ref.float()) <= tol
+
+
+@pytest.mark.parametrize("T", [1, 6])
+def test_attn_prep_matches_oracle_and_writes_cache_rows(T):
+    dev = device()
+    g = torch.Generator().manual_seed(60 + T)
+    B, Hq, Hkv, D, max_len = 3, 8, 2, 256, 128
+    y = torch.randn(B, T, Hq * 2 * D + 2 * Hkv * D, generator=g)
+    qw, kw = 0.1 * torch.randn(D, generator=g), 0.1 * torch.randn(D, generator=g)
+    cos, sin = rope_tables(max_len, rope_inv_freq(D, 0.25, 1e7))
+    pos = torch.tensor([0, 10, max_len - T], dtype=torch.int32)
+    q, gate, k, v, k_rot = of.attn_prep(y, qw, kw, cos, sin, pos, Hq, Hkv, D)
+    announce(f"attn_prep T{T}")
+    sentinel = torch.full((B, Hkv, max_len, D), 7.0, dtype=torch.bfloat16)
+    kc, vc = sentinel.to(dev), sentinel.to(dev)
+    out = ops.attn_prep(y.to(dev), qw.to(dev), kw.to(dev), cos.to(dev), sin.to(dev), pos.to(dev), kc, vc,
+                        num_heads=Hq, num_kv_heads=Hkv)
+    torch.cuda.synchronize()
+    for got, exp in zip(out, (q, gate, k, v)):
+        assert got.dtype == torch.bfloat16
+        assert oracle.rel_err(got.float().cpu(), exp) <= TOL_BF16
+    kc, vc = kc.cpu(), vc.cpu()
+    written = torch.zeros(B, max_len, dtype=torch.bool)
+    for b in range(B):
+        p0 = int(pos[b])
+        written[b, p0:p0 + T] = True
+        assert oracle.rel_err(kc[b, :, p0:p0 + T].float(), k_rot[b].transpose(0, 1)) <= TOL_BF16
+        assert oracle.rel_err(vc[b, :, p0:p0 + T].float(), v[b].transpose(0, 1)) <= TOL_BF16
+    # every other cache row is untouched
+    assert bool((kc.transpose(1, 2)[~written] == 7.0).all()) and bool((vc.transpose(1, 2)[~written] == 7.0).all())
