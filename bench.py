@@ -193,8 +193,9 @@ def bench_copy(torch, dev, mb=256, reps=5):
 
 def bench_stack(torch, q35hip, workloads, dev, steps=256):
     """The Qwen3.5-0.8B-shaped hybrid stack (24 layers, int8 SwiGLU, tied 151,936 embedding), batch 3 steered rows:
-    2048-token prefill, then `steps` greedy decode steps, host-driven (no graph capture). Reported end to end. The
-    prefill is timed with each Gated DeltaNet prefill kernel (the fp32 token-serial default and the chunked one)."""
+    2048-token prefill, then `steps` greedy decode steps. The prefill is timed with each Gated DeltaNet prefill
+    kernel (the fp32 token-serial default and the chunked one); decode is timed host-driven (eager) and as replays of
+    one captured decode step (HIP graph)."""
     from q35hip import model as gm
     cfg = workloads.Q35Config()
     W = workloads.init_weights(cfg, seed=0)
@@ -204,7 +205,8 @@ def bench_stack(torch, q35hip, workloads, dev, steps=256):
     v = torch.randn(cfg.hidden, generator=torch.Generator().manual_seed(0))
     g.set_vectors(torch.stack([v, -v]) * 0.1, [0, -1, 1])
     out = {"rows": 3, "prompt": 2048, "steps": steps}
-    for mode in ("chunk", "recurrent"):  # the default ("recurrent") last: its states feed the decode loop
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    for mode in ("chunk", "recurrent"):  # the default ("recurrent") last: its states feed the decode loops
         g.gdn_prefill = mode
         for _ in range(2):  # warm: allocator, library handles
             g.reset()
@@ -212,7 +214,7 @@ def bench_stack(torch, q35hip, workloads, dev, steps=256):
             g.forward(torch.zeros(3, 1, dtype=torch.long))
         torch.cuda.synchronize()
         g.reset()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0, e1 = ev(), ev()
         e0.record()
         logits, _ = g.forward(prompt)
         e1.record()
@@ -220,16 +222,26 @@ def bench_stack(torch, q35hip, workloads, dev, steps=256):
         tp = e0.elapsed_time(e1) * 1e-3
         out[f"prefill_{mode}_tok_s"] = 3 * 2048 / tp
         out[f"prefill_{mode}_ms"] = tp * 1e3
-    e1, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_eager = 32
+    e1, e2 = ev(), ev()
     e1.record()
-    for _ in range(steps):
-        nxt = logits.argmax(-1, keepdim=True)
-        logits, _ = g.forward(nxt)
+    for _ in range(n_eager):
+        logits = g.decode_step(logits.argmax(-1))
     e2.record()
     torch.cuda.synchronize()
-    td = e1.elapsed_time(e2) * 1e-3
-    out.update({"decode_tok_s": 3 * steps / td, "decode_ms_per_step": td / steps * 1e3,
-                "note": "host-driven decode loop (torch glue between the HIP ops), no graph capture"})
+    td = e1.elapsed_time(e2) * 1e-3 / n_eager
+    out.update({"decode_eager_tok_s": 3 / td, "decode_eager_ms_per_step": td * 1e3})
+    g.enable_decode_graph()
+    logits, _ = g.forward(prompt)
+    e1, e2 = ev(), ev()
+    e1.record()
+    for _ in range(steps):
+        logits = g.decode_step(logits.argmax(-1))
+    e2.record()
+    torch.cuda.synchronize()
+    td = e1.elapsed_time(e2) * 1e-3 / steps
+    out.update({"decode_tok_s": 3 / td, "decode_ms_per_step": td * 1e3,
+                "note": "decode_tok_s: each step one HIP-graph replay of the 24-layer step plus the host argmax"})
     return out
 
 

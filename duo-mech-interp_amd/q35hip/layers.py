@@ -14,14 +14,14 @@ States are caller-owned device tensors mutated in place, as the engine's buffers
 conv_state [B, K-1, C] fp32 (the last K-1 conv inputs, oldest first, engine/model.js:333), rec_state [B, Hv, dk, dv]
 fp32, k_cache / v_cache [B, Hkv, max_len, D] bf16 holding rotated keys and values by position.
 
-The glue (projections, depthwise causal conv, norms, gates) is torch on the device; the delta rule, the attention
-and the steering add are the HIP kernels. Nothing here falls back to a CPU path: the ops raise on CPU tensors and
-when the library is missing.
+The projections are one torch GEMM per mixer over the stacked input weights (cached in p under "_in_fused"); every
+other step is a HIP kernel: the GDN front end (causal conv + SiLU + gate terms), the delta rule, the gated RMSNorm,
+the attention front end (q/k norms, q/gate split, KV-cache update), the attention itself and the steering add.
+Nothing here falls back to a CPU path: the ops raise on CPU tensors and when the library is missing.
 """
 import math
 
 import torch
-import torch.nn.functional as F
 
 from . import ops
 
@@ -47,16 +47,6 @@ def rmsnorm_1p(x, w, eps=1e-6):
     return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * (1.0 + w.float())).to(x.dtype)
 
 
-def _rotate_rows(x, cos_rows, sin_rows):
-    """Partial RoPE with rotate-half pairs (i, i + rot/2) on dims [0, rot) of x [B, T, H, D] (HF:546-589); the
-    KV-cache writer's glue (the attention kernels rotate q and k themselves)."""
-    half = cos_rows.shape[-1]
-    rot = 2 * half
-    c, s = cos_rows[None, :, None, :], sin_rows[None, :, None, :]
-    x1, x2 = x[..., :half].float(), x[..., half:rot].float()
-    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s, x[..., rot:].float()], dim=-1)
-
-
 def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_heads=None, head_k_dim=None,
                          eps=1e-6, prefill="chunk"):
     """Gated DeltaNet mixer of one decoder layer (Qwen3_5GatedDeltaNet.forward, HF:432-543; the WGSL conv + delta
@@ -74,26 +64,13 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     dv = p["norm"].numel()
     Hk = Hv if num_k_heads is None else num_k_heads
     dk = dv if head_k_dim is None else head_k_dim
-    kd = Hk * dk
-    w = p["conv1d"]
-    w = w.reshape(w.shape[0], w.shape[-1])
-    K = w.shape[1]
-    mixed = x @ p["in_proj_qkv"].T
-    z = x @ p["in_proj_z"].T
-    b = x @ p["in_proj_b"].T
-    a = x @ p["in_proj_a"].T
-    # depthwise causal conv over [carried K-1 inputs | this call's inputs], then SiLU (HF:199-240)
-    full = torch.cat([conv_state.to(mixed.dtype), mixed], dim=1)
-    conv = full[:, 0:T] * w[:, 0]
-    for i in range(1, K):
-        conv = conv + full[:, i:i + T] * w[:, i]
-    conv = F.silu(conv)
-    conv_state.copy_(full[:, T:T + K - 1])
-    q = conv[..., :kd].reshape(B, T, Hk, dk).contiguous()
-    k = conv[..., kd:2 * kd].reshape(B, T, Hk, dk).contiguous()
-    v = conv[..., 2 * kd:].reshape(B, T, Hv, dv).contiguous()
-    beta = torch.sigmoid(b).contiguous()
-    g = (-p["A_log"].float().exp() * F.softplus(a.float() + p["dt_bias"].float())).contiguous()
+    C, Vd = 2 * Hk * dk + Hv * dv, Hv * dv
+    # one GEMM for every projection of the token: y row = [qkv (C) | z (Vd) | b (Hv) | a (Hv)], the engine's fused
+    # layout (engine/kernels_qwen35.js:129-131)
+    y = x @ gdn_in_weight(p).T
+    q, k, v, g, beta = ops.gdn_conv(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], num_k_heads=Hk,
+                                    head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=C + Vd, a_off=C + Vd + Hv,
+                                    out_dtype=x.dtype)
     if T == 1 or prefill == "recurrent":
         o = ops.gdn_decode_step_(q, k, v, g, beta, rec_state, use_qk_l2norm_in_kernel=True)
     else:
@@ -101,20 +78,36 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
                                           use_qk_l2norm_in_kernel=True)
         rec_state.copy_(S)
     # gated RMSNorm: plain w, norm before the silu(z) gate (HF:168-184; engine/kernels_qwen35.js:237-243)
-    o = o.reshape(B, T, Hv, dv)
-    on = o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + eps)
-    o = (p["norm"] * on) * F.silu(z.reshape(B, T, Hv, dv))
-    if head_scale is not None:
-        o = o * head_scale.to(o.dtype)[:, None]
-    return o.reshape(B, T, Hv * dv) @ p["out_proj"].T
+    o = ops.gated_rmsnorm(o, y[..., C:C + Vd], p["norm"], head_scale, eps)
+    return o @ p["out_proj"].T
+
+
+def gdn_in_weight(p):
+    """The four input projections of a Gated DeltaNet layer stacked into one [C + Vd + 2 Hv, H] weight (cached in p
+    under "_in_fused")."""
+    w = p.get("_in_fused")
+    if w is None:
+        w = torch.cat([p["in_proj_qkv"], p["in_proj_z"], p["in_proj_b"], p["in_proj_a"]], dim=0).contiguous()
+        p["_in_fused"] = w
+    return w
+
+
+def attn_in_weight(p):
+    """q_proj, k_proj and v_proj stacked into one [Hq 2D + 2 Hkv D, H] weight (cached in p under "_in_fused")."""
+    w = p.get("_in_fused")
+    if w is None:
+        w = torch.cat([p["q_proj"], p["k_proj"], p["v_proj"]], dim=0).contiguous()
+        p["_in_fused"] = w
+    return w
 
 
 def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partial_rotary_factor=0.25, eps=1e-6,
                           cache_len=None):
     """Gated softmax attention mixer of one decoder layer (Qwen3_5Attention.forward, HF:656-701; WGSL attnPrep +
-    attention, engine/kernels_qwen35.js:18-123). x: [B, T, H] fp32; the T tokens sit at positions pos..pos+T-1.
-    Their rotated keys and values are written into the caches at those positions. T > 1 requires pos == 0 and runs
-    the causal flash prefill over the call's own tokens; T == 1 runs the split-K decode over cache positions
+    attention, engine/kernels_qwen35.js:18-123). x: [B, T, H] fp32; the T tokens sit at positions pos..pos+T-1,
+    pos a Python int or a [B] int32 device tensor (per row; a device tensor keeps the call capturable in a HIP
+    graph). Their rotated keys and values are written into the caches at those positions. T > 1 requires pos == 0
+    and runs the causal flash prefill over the call's own tokens; T == 1 runs the split-K decode over cache positions
     0..pos (cache_len: optional [B] int32 per-row lengths, default pos + 1). Returns y [B, T, H]."""
     B, T, _ = x.shape
     D = p["q_norm"].numel()
@@ -122,27 +115,23 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     Hkv = p["k_proj"].shape[0] // D
     rot = int(D * partial_rotary_factor)
     max_len = k_cache.shape[2]
-    if pos + T > max_len:
-        raise ValueError(f"gated_attention_layer: positions {pos}..{pos + T - 1} exceed the cache ({max_len})")
-    cos, sin = rope_tables(max_len, rot, rope_theta, x.device)
-    qg = (x @ p["q_proj"].T).view(B, T, Hq, 2 * D)
-    q = rmsnorm_1p(qg[..., :D], p["q_norm"], eps)
-    gate = qg[..., D:].reshape(B, T, Hq * D)
-    k = rmsnorm_1p((x @ p["k_proj"].T).view(B, T, Hkv, D), p["k_norm"], eps)
-    v = (x @ p["v_proj"].T).view(B, T, Hkv, D)
-    k_cache[:, :, pos:pos + T] = _rotate_rows(k, cos[pos:pos + T], sin[pos:pos + T]).transpose(1, 2).to(k_cache.dtype)
-    v_cache[:, :, pos:pos + T] = v.transpose(1, 2).to(v_cache.dtype)
-    if T > 1:
-        if pos != 0:
-            raise ValueError("gated_attention_layer: a multi-token call must start at position 0")
-        o = ops.gated_attention_prefill(q.to(torch.bfloat16).contiguous(), k.to(torch.bfloat16).contiguous(),
-                                        v.to(torch.bfloat16).contiguous(), gate.to(torch.bfloat16).contiguous(),
-                                        cos, sin, pos0=0, scale=1.0 / math.sqrt(D))
+    if torch.is_tensor(pos):
+        pos_t = pos
     else:
-        cl = (torch.full((B,), pos + 1, dtype=torch.int32, device=x.device) if cache_len is None
-              else cache_len.to(device=x.device, dtype=torch.int32))
-        o = ops.gated_attention_decode(q[:, 0].to(torch.bfloat16).contiguous(), k_cache, v_cache,
-                                       gate[:, 0].to(torch.bfloat16).contiguous(), cl, cos, sin,
+        if pos + T > max_len:
+            raise ValueError(f"gated_attention_layer: positions {pos}..{pos + T - 1} exceed the cache ({max_len})")
+        if T > 1 and pos != 0:
+            raise ValueError("gated_attention_layer: a multi-token call must start at position 0")
+        pos_t = torch.full((B,), int(pos), dtype=torch.int32, device=x.device)
+    cos, sin = rope_tables(max_len, rot, rope_theta, x.device)
+    y = x @ attn_in_weight(p).T
+    q, gate, k, v = ops.attn_prep(y, p["q_norm"], p["k_norm"], cos, sin, pos_t, k_cache, v_cache, num_heads=Hq,
+                                  num_kv_heads=Hkv, eps=eps, want_kv=T > 1)
+    if T > 1:
+        o = ops.gated_attention_prefill(q, k, v, gate, cos, sin, pos0=0, scale=1.0 / math.sqrt(D))
+    else:
+        cl = (pos_t + 1 if cache_len is None else cache_len.to(device=x.device, dtype=torch.int32))
+        o = ops.gated_attention_decode(q[:, 0], k_cache, v_cache, gate[:, 0], cl, cos, sin,
                                        scale=1.0 / math.sqrt(D)).view(B, 1, Hq * D)
     return o.float() @ p["o_proj"].T
 

@@ -44,7 +44,13 @@ class HybridModel:
     gdn_prefill selects the Gated DeltaNet prefill kernel: "recurrent" (default) runs the fp32 token-serial kernel,
     whose outputs agree with the fp32 CPU recurrence to about 1e-6, so greedy tokens follow the fp32 reference even
     through near ties of a few 1e-3 in the logits; "chunk" runs the chunked bf16-MFMA kernel (faster prefill,
-    relative error a few 1e-3 per layer)."""
+    relative error a few 1e-3 per layer).
+
+    Positions live on the device (pos_dev, [rows] int32) and the steering vectors in fixed buffers, so a decode step
+    has no host-dependent arguments: enable_decode_graph() captures one step in a HIP graph that decode_step()
+    replays."""
+
+    MAX_VECS = 4  # vector rows of the steering buffer (the WGSL resAdd clamps its row index to 3, engine/kernels.js:201)
 
     def __init__(self, cfg, W, device, max_len=4096, rows=3, steer_layer=12, gdn_prefill="recurrent"):
         if gdn_prefill not in ("chunk", "recurrent"):
@@ -53,10 +59,16 @@ class HybridModel:
         self.gdn_prefill = gdn_prefill
         self.W = W if isinstance(W, Q35Weights) else Q35Weights(W, device)
         self.max_len, self.rows = max_len, rows
-        self.vecs = None
-        self.vec_rows = None
+        self.vec_buf = torch.zeros(self.MAX_VECS, cfg.hidden, device=device)
+        self.vec_rows = torch.full((rows,), -1, dtype=torch.int32, device=device)
+        self.steering = False
         self.params = [{n[len(f"layers.{l}."):]: t for n, t in self.W.t.items() if n.startswith(f"layers.{l}.")}
                        for l in range(cfg.layers)]
+        for l, p in enumerate(self.params):  # stacked input projections, built once
+            if cfg.is_attention(l):
+                layers.attn_in_weight(p)
+            else:
+                layers.gdn_in_weight(p)
         self.states = []
         for l in range(cfg.layers):
             if cfg.is_attention(l):
@@ -67,51 +79,114 @@ class HybridModel:
                 self.states.append({
                     "conv": torch.zeros(rows, cfg.conv_k - 1, cfg.conv_dim, device=device),
                     "rec": torch.zeros(rows, cfg.lin_v_heads, cfg.lin_dk, cfg.lin_dv, device=device)})
+        self.pos_dev = torch.zeros(rows, dtype=torch.int32, device=device)
+        self.graph = None
         self.reset()
 
     def reset(self):
-        """Start a new sequence: zero the recurrent and conv states (KV caches are overwritten by position)."""
+        """Start a new sequence: zero the recurrent and conv states and the positions (KV caches are overwritten by
+        position)."""
         for st in self.states:
             if "rec" in st:
                 st["rec"].zero_()
                 st["conv"].zero_()
+        self.pos_dev.zero_()
         self.pos = 0
 
     def set_vectors(self, vecs, vec_of_row):
-        """vecs: [n, H] fp32; vec_of_row: [rows] int (-1 = no vector)."""
-        self.vecs = vecs.to(self.device, torch.float32).contiguous()
-        self.vec_rows = torch.as_tensor(vec_of_row, dtype=torch.int32).to(self.device)
+        """vecs: [n, H] fp32 (n <= MAX_VECS), copied into the model's buffer; vec_of_row: [rows] int (-1 = no vector).
+        None clears the steering."""
+        if vecs is None:
+            self.vec_rows.fill_(-1)
+            self.steering = False
+            return
+        vecs = vecs.to(self.device, torch.float32)
+        if vecs.shape[0] > self.MAX_VECS:
+            raise ValueError(f"HybridModel: at most {self.MAX_VECS} steering vectors")
+        self.vec_buf[:vecs.shape[0]].copy_(vecs)
+        self.vec_rows.copy_(torch.as_tensor(vec_of_row, dtype=torch.int32))
+        self.steering = True
 
-    @torch.no_grad()
-    def forward(self, ids, stop_after=None, collect_layer=None):
-        cfg, W = self.cfg, self.W
-        T = ids.shape[1]
-        if self.pos + T > self.max_len:
-            raise ValueError("context exceeds the KV cache")
-        x = W["embed"][ids.to(self.device)]
+    def _layers(self, x, T, last, collect_layer, steer):
+        cfg = self.cfg
         collected = None
-        last = cfg.layers - 1 if stop_after is None else stop_after
         for l in range(last + 1):
             p, st = self.params[l], self.states[l]
             h = rmsnorm_1p(x, p["input_layernorm"], cfg.eps)
             if cfg.is_attention(l):
-                y = layers.gated_attention_layer(h, p, st["k"], st["v"], self.pos, rope_theta=cfg.rope_theta,
+                y = layers.gated_attention_layer(h, p, st["k"], st["v"], self.pos_dev, rope_theta=cfg.rope_theta,
                                                  partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps)
             else:
                 y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
                                                 head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill)
             x = x + y
             x = x + mlp(p, rmsnorm_1p(x, p["post_attention_layernorm"], cfg.eps))
-            if l == self.steer_layer and self.vecs is not None:
+            if l == self.steer_layer and steer:
                 x = x.contiguous()
-                layers.residual_steer_add(x, self.vecs, self.vec_rows)
+                layers.residual_steer_add(x, self.vec_buf, self.vec_rows)
             if l == collect_layer:
                 collected = x.clone()
+        return x, collected
+
+    @torch.no_grad()
+    def forward(self, ids, stop_after=None, collect_layer=None):
+        """ids: [rows, T] token ids continuing the sequence (a multi-token call must start it). Returns
+        (last-position logits [rows, V] or None with stop_after, residual after collect_layer or None)."""
+        cfg, W = self.cfg, self.W
+        T = ids.shape[1]
+        if self.pos + T > self.max_len:
+            raise ValueError("context exceeds the KV cache")
+        if T > 1 and self.pos != 0:
+            raise ValueError("HybridModel: a multi-token call must start the sequence (positions 0..T-1)")
+        x = W["embed"][ids.to(self.device)]
+        last = cfg.layers - 1 if stop_after is None else stop_after
+        x, collected = self._layers(x, T, last, collect_layer, self.steering)
+        self.pos_dev.add_(T)
         self.pos += T
         if stop_after is not None:
             return None, collected
         hN = rmsnorm_1p(x[:, -1], W["norm"], cfg.eps)
         return hN @ W["embed"].T, collected
+
+    @torch.no_grad()
+    def enable_decode_graph(self):
+        """Capture one decode step (ids [rows, 1] -> logits) in a HIP graph; decode_step() then replays it. Must be
+        called at the start of a sequence: the warm-up runs real steps, and the states are reset afterwards. The
+        steering add is always part of the graph (rows without a vector are skipped by the kernel)."""
+        cfg = self.cfg
+        self.reset()
+        self._g_ids = torch.zeros(self.rows, 1, dtype=torch.long, device=self.device)
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):  # warm-up outside capture: library handles, allocator pools
+            for _ in range(2):
+                x, _ = self._layers(self.W["embed"][self._g_ids], 1, cfg.layers - 1, None, True)
+                self.pos_dev.add_(1)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            x, _ = self._layers(self.W["embed"][self._g_ids], 1, cfg.layers - 1, None, True)
+            self.pos_dev.add_(1)
+            hN = rmsnorm_1p(x[:, -1], self.W["norm"], cfg.eps)
+            self._g_logits = hN @ self.W["embed"].T
+        self.graph = g
+        torch.cuda.synchronize(self.device)
+        self.reset()
+
+    @torch.no_grad()
+    def decode_step(self, ids):
+        """One greedy step for every row: ids [rows] or [rows, 1]. Replays the captured graph when there is one (the
+        returned logits then live in the graph's output buffer, overwritten by the next step), else runs forward."""
+        ids = ids.reshape(self.rows, 1)
+        if self.graph is None:
+            return self.forward(ids)[0]
+        if self.pos + 1 > self.max_len:
+            raise ValueError("context exceeds the KV cache")
+        self._g_ids.copy_(ids)
+        self.graph.replay()
+        self.pos += 1
+        return self._g_logits
 
 
 @torch.no_grad()
@@ -125,7 +200,7 @@ def greedy(model, prompt_ids, steps):
         nxt = logits.argmax(dim=-1)
         toks.append(nxt)
         margins.append(top2.values[:, 0] - top2.values[:, 1])
-        logits, _ = model.forward(nxt[:, None])
+        logits = model.decode_step(nxt)
     return torch.stack(toks, 1).cpu(), torch.stack(margins, 1).cpu()
 
 
@@ -143,7 +218,7 @@ def steered_greedy(model, prompt_ids, steps, steer_layer=12, dose=0.8, seed=0):
     [+v, none, -v] as tests/engine.html:84 sets them). Returns (tokens, margins, vector)."""
     cfg = model.cfg
     model.reset()
-    model.vecs = None
+    model.set_vectors(None, None)
     # the states are sized for every row, so the unsteered calibration pass runs the whole batch and reads row 0
     _, resid = model.forward(prompt_ids, stop_after=steer_layer, collect_layer=steer_layer)
     med = median_resid_norm(resid[0])

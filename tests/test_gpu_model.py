@@ -39,11 +39,37 @@ def test_tiny_stack_prefill_decode_and_steering(gdn_prefill):
         assert oracle.rel_err(lg.cpu(), lr) <= 2e-2
 
 
+def test_tiny_stack_decode_graph_replays_match_eager():
+    """The captured decode step, replayed over 10 steps, gives the eager path's logits at every step (same kernels,
+    same buffers), with eager work and synchronisations between the replays."""
+    dev = device()
+    cfg = tiny_config()
+    W = tiny_weights(cfg)
+    ids, vec = tiny_inputs(cfg)
+    announce("model tiny decode graph vs eager")
+    eager = gm.HybridModel(cfg, W, dev, max_len=256, rows=2, steer_layer=STEER_LAYER)
+    graph = gm.HybridModel(cfg, W, dev, max_len=256, rows=2, steer_layer=STEER_LAYER)
+    graph.enable_decode_graph()
+    for m in (eager, graph):
+        m.set_vectors(torch.stack([vec, -vec]), [0, 1])
+    le, _ = eager.forward(ids)
+    lg, _ = graph.forward(ids)
+    assert torch.equal(le, lg)
+    for step in range(10):
+        nxt = le.argmax(-1)
+        le = eager.decode_step(nxt).clone()
+        lg = graph.decode_step(nxt).clone()
+        torch.cuda.synchronize()
+        assert graph.pos == eager.pos
+        assert oracle.rel_err(lg.cpu(), le.cpu()) <= 1e-6, f"replay {step} differs from eager"
+
+
 @pytest.mark.timeout(1800)
 def test_full_stack_steered_greedy_64_steps():
     """Qwen3.5-0.8B shape (24 layers, hidden 1024, int8 SwiGLU 3584, tied 151,936 embedding), seed 0; batch 3,
     2048-token prompt (seed 0) on every row, vector after layer 12 scaled to 0.8 x the median residual norm: +v on
-    row 0, none on row 1, -v on row 2; greedy tokens must be identical to the fp32 CPU path for 64 steps."""
+    row 0, none on row 1, -v on row 2; greedy tokens must be identical to the fp32 CPU path for 64 steps (decode
+    steps replayed from a captured HIP graph)."""
     dev = device()
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     cfg = workloads.Q35Config()
@@ -52,6 +78,7 @@ def test_full_stack_steered_greedy_64_steps():
     steps = 64
     announce("model full stack: GPU (fp32 token-serial GDN prefill)")
     g = gm.HybridModel(cfg, W, dev, max_len=2048 + steps + 8, rows=3, gdn_prefill="recurrent")
+    g.enable_decode_graph()  # the 64 greedy steps replay one captured decode step
     toks_g, marg_g, v = gm.steered_greedy(g, prompt, steps)
     announce("model full stack: CPU oracle")
     ref = om.OracleModel(cfg, W, steer_layer=12)
