@@ -16,10 +16,10 @@ EXPORTS = [
     "q35_gdn_recurrent", "q35_gdn_chunk_workspace_bytes", "q35_gdn_chunk_prefill",
     "q35_gated_attn_prefill_workspace_bytes", "q35_gated_attn_prefill", "q35_gated_attn_decode_workspace_bytes",
     "q35_gated_attn_decode",
-    "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep",
+    "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv", "q35_swiglu_push",
 ]
 
-Q35_F32, Q35_BF16 = 0, 1
+Q35_F32, Q35_BF16, Q35_I8 = 0, 1, 2
 
 _lib = None
 
@@ -44,6 +44,8 @@ _SIGS = {
     "q35_gdn_conv": ([P, I64, P, P, P, P, P, I64, I64, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, P], I32),
     "q35_gated_rmsnorm": ([P, P, I64, P, P, P, I64, I64, I64, F32, I32, P], I32),
     "q35_attn_prep": ([P, I64, P, P, F32, P, P, I64, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I32),
+    "q35_gemv": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
+    "q35_swiglu_push": ([P, P, I64, I64, P, I64, I64, P], I32),
 }
 
 

@@ -67,6 +67,8 @@ _LIB.define("gdn_conv(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) con
             "Tensor dt_bias, int b_off, int a_off, int Hk, int dk, int Hv, int dv, bool bf16_out) "
             "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
 _LIB.define("gated_rmsnorm(Tensor o, Tensor z, Tensor w, Tensor? head_scale, float eps) -> Tensor")
+_LIB.define("gemv_(Tensor x, Tensor W, Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
+_LIB.define("swiglu_push(Tensor gu, Tensor? pushes, int T) -> Tensor")
 _LIB.define("attn_prep(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, Tensor cos, Tensor sin, Tensor pos, "
             "Tensor(a!) k_cache, Tensor(b!) v_cache, int Hq, int Hkv, bool want_kv) "
             "-> (Tensor, Tensor, Tensor, Tensor)")
@@ -270,6 +272,48 @@ def _attn_prep_impl(y, q_norm_w, k_norm_w, eps, cos, sin, pos, k_cache, v_cache,
     return q, gate, k, v
 
 
+# ---------------------------------------------------------------- decode matrix-vector products, SwiGLU hook
+_EPI = {"store": 0, "add": 1, "swiglu": 2}
+
+
+def _pushes_check(pushes):
+    if pushes is None:
+        return 0
+    _require(pushes.dtype == torch.int32 and pushes.dim() == 2 and pushes.shape[1] == 6 and pushes.is_contiguous(),
+             "pushes: [n, 6] int32 records (see pack_pushes)")
+    return pushes.shape[0]
+
+
+def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T):
+    _on_gpu(x, W, w_scale, y, pushes)
+    _require(x.dtype == torch.float32 and x.dim() == 2 and y.dtype == torch.float32 and y.dim() == 2,
+             "x: [M, K] fp32; y: [M, N or N/2] fp32")
+    _require(W.dim() == 2 and W.dtype in (torch.int8, torch.float32), "W: [N, K] int8 or fp32")
+    M, K = x.shape
+    N = W.shape[0]
+    _require(W.shape[1] == K and y.shape[0] == M, "x, W, y shapes disagree")
+    _require(y.shape[1] == (N // 2 if epilogue == 2 else N), "y: [M, N] ([M, N / 2] for the SwiGLU epilogue)")
+    if W.dtype == torch.int8:
+        _require(w_scale is not None and w_scale.dtype == torch.float32 and w_scale.numel() == N,
+                 "int8 W needs w_scale [N] fp32")
+    npush = _pushes_check(pushes)
+    st = _lib.lib().q35_gemv(_ptr(x), K, _ptr(W), 2 if W.dtype == torch.int8 else Q35_F32, _ptr(w_scale), _ptr(y),
+                             y.shape[1], M, N, K, int(epilogue), _ptr(pushes), npush, int(T), _stream(x))
+    check(st, "q35_gemv")
+
+
+def _swiglu_push_impl(gu, pushes, T):
+    _on_gpu(gu, pushes)
+    _require(gu.dtype == torch.float32 and gu.shape[-1] % 2 == 0, "gu: [..., 2 I] fp32")
+    I = gu.shape[-1] // 2
+    M = gu.numel() // (2 * I)
+    a = torch.empty(*gu.shape[:-1], I, dtype=torch.float32, device=gu.device)
+    st = _lib.lib().q35_swiglu_push(_ptr(gu), _ptr(a), M, I, _ptr(pushes), _pushes_check(pushes), int(T),
+                                    _stream(gu))
+    check(st, "q35_swiglu_push")
+    return a
+
+
 def _no_cpu(name):
     def f(*args, **kwargs):
         raise Q35Error(f"q35hip: q35::{name} needs HIP device tensors; the product has no CPU path")
@@ -280,7 +324,7 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gdn_chunk_prefill", _gdn_chunk_impl), ("gated_attn_prefill", _attn_prefill_impl),
                      ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
                      ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl),
-                     ("attn_prep", _attn_prep_impl)]:
+                     ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl)]:
     _LIB.impl(_name, _impl, "CUDA")
     _LIB.impl(_name, _no_cpu(_name), "CPU")
 
@@ -387,3 +431,34 @@ def attn_prep(y, q_norm_w, k_norm_w, cos, sin, pos, k_cache, v_cache, *, num_hea
     rotated, and writes rotated keys and values into the caches at positions pos[b] + t (pos: [B] int32 device)."""
     return torch.ops.q35.attn_prep(y, q_norm_w.float().contiguous(), k_norm_w.float().contiguous(), float(eps), cos,
                                    sin, pos, k_cache, v_cache, int(num_heads), int(num_kv_heads), bool(want_kv))
+
+
+def pack_pushes(pushes, device):
+    """Neuron pushes [(neuron or None for every neuron, "add" | "mul", [value per row, up to 4])] as the [n, 6] int32
+    records of the C ABI (engine/model.js:412-423: missing row values are 0 for add and 1 for mul)."""
+    import struct
+    rec = []
+    for neuron, mode, vals in pushes:
+        m = {"add": 0, "mul": 1}[mode]
+        v = [float(x) for x in vals] + [1.0 if m else 0.0] * (4 - len(vals))
+        rec.append([-1 if neuron is None else int(neuron), m] + [struct.unpack("<i", struct.pack("<f", x))[0]
+                                                                 for x in v[:4]])
+    return torch.tensor(rec, dtype=torch.int32).reshape(-1, 6).to(device)
+
+
+def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1):
+    """y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k] for M <= 8 rows (decode): W int8 with per-row scales or fp32.
+    epilogue "store" writes out, "add" accumulates into out (a residual add), "swiglu" treats W's rows as
+    interleaved (gate, up) pairs and writes silu(gate) * up with the neuron pushes (pack_pushes) applied."""
+    e = _EPI[epilogue]
+    if out is None:
+        N = W.shape[0] // 2 if e == 2 else W.shape[0]
+        out = torch.empty(x.shape[0], N, dtype=torch.float32, device=x.device)
+    torch.ops.q35.gemv_(x, W, w_scale, out, e, pushes, int(T))
+    return out
+
+
+def swiglu_push(gu, pushes=None, T=1):
+    """silu(gate) * up over a [..., 2 I] ([gate | up]) projection with the neuron pushes applied (the hook point of
+    engine/kernels_qwen35.js:250-279)."""
+    return torch.ops.q35.swiglu_push(gu, pushes, int(T))

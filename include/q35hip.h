@@ -21,6 +21,10 @@
  *   q35_gated_rmsnorm        HF:168-184 Qwen3_5RMSNormGated; engine/kernels_qwen35.js:237-243 (epilogue of `delta`)
  *   q35_attn_prep            HF:667-680 (q / gate split, q_norm / k_norm, partial RoPE of k, cache update);
  *                            engine/kernels_qwen35.js:18-69 `attnPrep`
+ *   q35_gemv                 engine/kernels.js:57-90 `matvec` (int8 weights; per output channel here) and, with the
+ *                            SwiGLU epilogue, engine/kernels_qwen35.js:250-279 `swiglu` with the neuron pushes;
+ *                            HF:704-717 Qwen3_5MLP for the decode step
+ *   q35_swiglu_push          engine/kernels_qwen35.js:250-279 `swiglu` over a [gate | up] projection (prefill form)
  */
 #ifndef Q35HIP_H
 #define Q35HIP_H
@@ -43,7 +47,16 @@ enum q35_status {
   Q35_ELAUNCH = 4       /* the HIP runtime refused a kernel launch */
 };
 
-enum q35_dtype { Q35_F32 = 0, Q35_BF16 = 1 };
+enum q35_dtype { Q35_F32 = 0, Q35_BF16 = 1, Q35_I8 = 2 };
+
+/* One neuron push of the MLP hook (engine/model.js:8, :412-423): neuron -1 applies to every neuron of the layer;
+ * mode 0 adds vals[row], mode 1 multiplies by it; row = min(m / T, 3) for input row m of a call with T tokens per
+ * sequence row. */
+typedef struct q35_push {
+  int32_t neuron;
+  int32_t mode;
+  float vals[4];
+} q35_push;
 
 /* Human-readable name of a status code (static storage). */
 const char* q35_status_string(int status);
@@ -169,6 +182,26 @@ int q35_attn_prep(const float* y, int64_t ldy, const float* q_norm_w, const floa
                   const float* cos, const float* sin, int64_t rot, const int32_t* pos, void* q_out, void* gate_out,
                   void* k_out, void* v_out, void* k_cache, void* v_cache, int64_t max_len, int64_t B, int64_t T,
                   int64_t Hq, int64_t Hkv, int64_t D, q35_stream_t stream);
+
+/*
+ * Small-M matrix-vector product for the decode step: y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k], m < M <= 8.
+ *   x: [M, ldx] fp32 (16-byte aligned, ldx a multiple of 4); W: [N, K] row-major, w_dtype Q35_I8 (int8, with
+ *   w_scale [N] fp32) or Q35_F32 (w_scale NULL for 1); K a multiple of 256, M * K * 4 <= 64 KiB.
+ *   epilogue 0: y[m, n] = v; 1: y[m, n] += v (a residual add); 2: SwiGLU over interleaved row pairs (row 2 j the
+ *   gate, row 2 j + 1 the up projection of neuron j): y[m, j] = silu(v_2j) * v_2j+1, then the pushes in order.
+ *   y: [M, ldy] fp32 (ldy >= N, or >= N / 2 for epilogue 2). pushes: npush <= 64 records on the device (or NULL
+ *   with npush 0); T: tokens per sequence row (the push row is min(m / T, 3)).
+ */
+int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
+             int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T,
+             q35_stream_t stream);
+
+/*
+ * a[m, n] = silu(gu[m, n]) * gu[m, I + n] with the pushes applied, gu: [M, 2 I] fp32 ([gate | up] per row),
+ * a: [M, I] fp32; pushes and T as for q35_gemv.
+ */
+int q35_swiglu_push(const float* gu, float* a, int64_t M, int64_t I, const q35_push* pushes, int64_t npush,
+                    int64_t T, q35_stream_t stream);
 
 #ifdef __cplusplus
 }

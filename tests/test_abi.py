@@ -23,7 +23,8 @@ def declared_functions():
 def test_header_declares_the_boundary():
     names = declared_functions()
     for n in ["q35_gdn_recurrent", "q35_gdn_chunk_prefill", "q35_gated_attn_prefill", "q35_gated_attn_decode",
-              "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep"]:
+              "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
+              "q35_swiglu_push"]:
         assert n in names
 
 
@@ -96,6 +97,12 @@ def test_validation_rejects_without_launching():
                            1, 1, 8, 2, 256, None) == 1
     assert L.q35_attn_prep(fake, 5120, fake, fake, 1e-6, fake, fake, 60, fake, fake, fake, None, None, fake, fake,
                            16, 1, 1, 8, 2, 256, None) == 2
+    # decode GEMV: K not a multiple of 256, too many rows, odd N for the SwiGLU epilogue, unknown weight type
+    assert L.q35_gemv(fake, 1000, fake, 2, fake, fake, 64, 3, 64, 1000, 0, None, 0, 1, None) == 2
+    assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 9, 64, 1024, 0, None, 0, 1, None) == 2
+    assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 63, 1024, 2, None, 0, 1, None) == 1
+    assert L.q35_gemv(fake, 1024, fake, 1, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1, None) == 2
+    assert L.q35_swiglu_push(fake, fake, 3, 64, None, 2, 1, None) == 1
 
 
 def test_decode_workspace_scales_with_splits():

@@ -1,0 +1,63 @@
+"""Decode matrix-vector products (int8 per-output-channel and fp32 weights) and the SwiGLU neuron hook on the GPU,
+against the CPU oracle. fp32 arithmetic throughout: relative error <= 1e-5 (summation order only)."""
+import pytest
+import torch
+
+import oracle
+from oracle import mlp as omlp
+from q35hip import ops
+from gpu_util import announce, device
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def _weights(N, K, wdt, seed):
+    g = torch.Generator().manual_seed(seed)
+    if wdt == torch.int8:
+        return torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8), torch.rand(N, generator=g) * 0.01
+    return torch.randn(N, K, generator=g) * 0.05, None
+
+
+@pytest.mark.parametrize("wdt", [torch.int8, torch.float32])
+@pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (3, 7168, 1024), (3, 1024, 3584), (8, 1000, 2048),
+                                   (5, 2048, 256)])
+def test_gemv_store_and_add(wdt, M, N, K):
+    dev = device()
+    W, s = _weights(N, K, wdt, seed=N + K)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M))
+    ref = omlp.q8_linear(x, W, s) if wdt == torch.int8 else x @ W.T
+    announce(f"gemv {wdt} M{M} N{N} K{K}")
+    Wd, sd, xd = W.to(dev), None if s is None else s.to(dev), x.to(dev)
+    y = ops.gemv(xd, Wd, sd)
+    base = torch.randn(M, N, generator=torch.Generator().manual_seed(9))
+    acc = base.to(dev)
+    ops.gemv(xd, Wd, sd, out=acc, epilogue="add")
+    torch.cuda.synchronize()
+    assert oracle.rel_err(y.cpu(), ref) <= TOL
+    assert oracle.rel_err(acc.cpu(), base + ref) <= TOL
+
+
+@pytest.mark.parametrize("M,T", [(3, 1), (6, 2)])
+def test_gemv_swiglu_with_pushes_and_prefill_form(M, T):
+    """Interleaved (gate, up) int8 rows through the SwiGLU epilogue, with add / mul / all-neuron pushes; the prefill
+    form (swiglu_push over a [gate | up] projection) gives the same activations."""
+    dev = device()
+    I, H = 3584, 1024
+    Wg, sg = _weights(I, H, torch.int8, 1)
+    Wu, su = _weights(I, H, torch.int8, 2)
+    x = torch.randn(M, H, generator=torch.Generator().manual_seed(3))
+    pushes = [(17, "add", [1.5, -2.0, 0.25]), (17, "mul", [3.0, 0.5]), (None, "mul", [1.0, 0.75, 1.25]),
+              (3583, "add", [4.0])]
+    ref = omlp.swiglu_push(omlp.q8_linear(x, Wg, sg), omlp.q8_linear(x, Wu, su), pushes, T=T)
+    Wi = torch.stack([Wg, Wu], dim=1).reshape(2 * I, H)          # row 2 j gate j, row 2 j + 1 up j
+    si = torch.stack([sg, su], dim=1).reshape(2 * I)
+    announce(f"gemv swiglu M{M} T{T}")
+    pk = ops.pack_pushes(pushes, dev)
+    a = ops.gemv(x.to(dev), Wi.to(dev), si.to(dev), epilogue="swiglu", pushes=pk, T=T)
+    gu = torch.cat([omlp.q8_linear(x, Wg, sg), omlp.q8_linear(x, Wu, su)], dim=-1)
+    a2 = ops.swiglu_push(gu.to(dev), pk, T=T)
+    torch.cuda.synchronize()
+    assert oracle.rel_err(a.cpu(), ref) <= TOL
+    assert oracle.rel_err(a2.cpu(), ref) <= TOL
