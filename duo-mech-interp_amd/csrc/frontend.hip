@@ -14,6 +14,7 @@
 //                          dense bf16 q, gate, k, v for the prefill kernel, and the rotated keys and the values
 //                          written into the bf16 KV cache at positions pos[b] + t (pos read on the device, so that a
 //                          captured decode step replays at the right position).
+//   add_rmsnorm_kernel     the decoder layer's residual add + RMSNorm with (1 + w) (HF:720-734, :753-793).
 #include "q35_common.h"
 #include "q35hip.h"
 
@@ -208,7 +209,67 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const float* __restrict_
   if (p < max_len) store4<__bf16>(v_cache + (((size_t)b * Hkv + vh) * max_len + p) * D + d0, x);
 }
 
+// Residual add + RMSNorm with (1 + w) (HF:720-734 Qwen3_5RMSNorm, applied around every mixer and MLP at HF:753-793;
+// engine/kernels.js:226-246 `rmsnorm` with OFFSET and `addInto`): x[m] += y[m] (when y is given) in place, then
+// h[m] = x[m] * rsqrt(mean(x[m]^2) + eps) * (1 + w), all fp32. One block of 256 threads per row; H a multiple of 4.
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float* __restrict__ x, int64_t ldx,
+                                                          const float* __restrict__ y, int64_t ldy,
+                                                          const float* __restrict__ w, float* __restrict__ h,
+                                                          int64_t ldh, int H, float eps) {
+  const int64_t m = blockIdx.x;
+  const int tid = threadIdx.x;
+  float* xr = x + m * ldx;
+  const float* yr = y ? y + m * ldy : nullptr;
+  constexpr int kMaxPer = 8;  // float4s per thread held in registers (H <= 8192)
+  f32x4 v[kMaxPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPer; ++i) {
+    const int c = 4 * (tid + 256 * i);
+    if (c < H) {
+      v[i] = *reinterpret_cast<const f32x4*>(xr + c);
+      if (yr) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(yr + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[i][e] += a[e];
+        *reinterpret_cast<f32x4*>(xr + c) = v[i];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss += v[i][e] * v[i][e];
+    }
+  }
+  __shared__ float red[4];
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float r = rsqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
+  float* hr = h + m * ldh;
+#pragma unroll
+  for (int i = 0; i < kMaxPer; ++i) {
+    const int c = 4 * (tid + 256 * i);
+    if (c < H) {
+      const f32x4 wv = *reinterpret_cast<const f32x4*>(w + c);
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = v[i][e] * r * (1.f + wv[e]);
+      *reinterpret_cast<f32x4*>(hr + c) = o;
+    }
+  }
+}
+
 }  // namespace q35
+
+extern "C" int q35_add_rmsnorm(float* x, int64_t ldx, const float* y, int64_t ldy, const float* w, float* h,
+                               int64_t ldh, int64_t M, int64_t H, float eps, q35_stream_t stream) {
+  using namespace q35;
+  if (!x || !w || !h || M <= 0 || H <= 0 || ldx < H || ldh < H || (y && ldy < H)) return Q35_EINVAL;
+  if ((H & 3) || H > 8192 || (ldx & 3) || (ldh & 3) || (y && (ldy & 3)) || M > 0x7fffffff) return Q35_EUNSUPPORTED;
+  if (((uintptr_t)x & 15) || ((uintptr_t)h & 15) || ((uintptr_t)w & 15) || (y && ((uintptr_t)y & 15)))
+    return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)M), dim3(256), 0, st, x, ldx, y, ldy, w, h, ldh, (int)H, eps);
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
 
 extern "C" int q35_gdn_conv(const float* y, int64_t ldy, const float* conv_w, const float* conv_bias,
                             float* conv_state, const float* A_log, const float* dt_bias, int64_t b_off, int64_t a_off,

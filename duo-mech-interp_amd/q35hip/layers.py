@@ -67,7 +67,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     C, Vd = 2 * Hk * dk + Hv * dv, Hv * dv
     # one GEMM for every projection of the token: y row = [qkv (C) | z (Vd) | b (Hv) | a (Hv)], the engine's fused
     # layout (engine/kernels_qwen35.js:129-131)
-    y = x @ gdn_in_weight(p).T
+    y = linear(x, gdn_in_weight(p))
     q, k, v, g, beta = ops.gdn_conv(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], num_k_heads=Hk,
                                     head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=C + Vd, a_off=C + Vd + Hv,
                                     out_dtype=x.dtype)
@@ -79,7 +79,16 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
         rec_state.copy_(S)
     # gated RMSNorm: plain w, norm before the silu(z) gate (HF:168-184; engine/kernels_qwen35.js:237-243)
     o = ops.gated_rmsnorm(o, y[..., C:C + Vd], p["norm"], head_scale, eps)
-    return o @ p["out_proj"].T
+    return linear(o, p["out_proj"])
+
+
+def linear(x, w):
+    """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), a torch GEMM otherwise."""
+    K = x.shape[-1]
+    M = x.numel() // K
+    if M <= 8 and K % 256 == 0 and x.dtype == torch.float32 and w.dtype == torch.float32:
+        return ops.gemv(x.reshape(M, K).contiguous(), w).view(*x.shape[:-1], w.shape[0])
+    return x @ w.T
 
 
 def gdn_in_weight(p):
@@ -124,7 +133,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
             raise ValueError("gated_attention_layer: a multi-token call must start at position 0")
         pos_t = torch.full((B,), int(pos), dtype=torch.int32, device=x.device)
     cos, sin = rope_tables(max_len, rot, rope_theta, x.device)
-    y = x @ attn_in_weight(p).T
+    y = linear(x, attn_in_weight(p))
     q, gate, k, v = ops.attn_prep(y, p["q_norm"], p["k_norm"], cos, sin, pos_t, k_cache, v_cache, num_heads=Hq,
                                   num_kv_heads=Hkv, eps=eps, want_kv=T > 1)
     if T > 1:
@@ -133,7 +142,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
         cl = (pos_t + 1 if cache_len is None else cache_len.to(device=x.device, dtype=torch.int32))
         o = ops.gated_attention_decode(q[:, 0], k_cache, v_cache, gate[:, 0], cl, cos, sin,
                                        scale=1.0 / math.sqrt(D)).view(B, 1, Hq * D)
-    return o.float() @ p["o_proj"].T
+    return linear(o.float(), p["o_proj"])
 
 
 def residual_steer_add(x, vecs, rows=None):

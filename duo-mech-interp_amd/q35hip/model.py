@@ -8,14 +8,14 @@ q35hip.layers; the model owns their states (GDN conv / recurrent states, bf16 KV
 (engine/model.js:308-342).
 """
 import torch
-import torch.nn.functional as F
 
-from . import layers
-from .layers import rmsnorm_1p
+from . import layers, ops
 
 
 class Q35Weights:
-    """Device copy of a weight dict (fp32; int8 MLP weights dequantised once, per output channel)."""
+    """Device copy of a weight dict: fp32 tensors as given; each int8 per-output-channel weight (keys "<name>.q" int8
+    [N, K] and "<name>.s" fp32 [N]) both kept as int8 + scales (for the decode GEMVs) and dequantised once to fp32
+    under "<name>" (for the prefill GEMMs)."""
 
     def __init__(self, W, device):
         self.t = {}
@@ -23,8 +23,7 @@ class Q35Weights:
             if k.endswith(".q"):
                 base = k[:-2]
                 self.t[base] = (v.float() * W[base + ".s"][:, None]).to(device)
-            elif k.endswith(".s"):
-                continue
+                self.t[k] = v.to(device).contiguous()
             else:
                 self.t[k] = v.to(device)
 
@@ -32,9 +31,41 @@ class Q35Weights:
         return self.t[k]
 
 
-def mlp(p, h):
-    """SwiGLU MLP (HF:704-717) with the int8 per-output-channel weights dequantised once at load."""
-    return (F.silu(h @ p["gate_proj"].T) * (h @ p["up_proj"].T)) @ p["down_proj"].T
+MAX_PUSHES = 8  # neuron pushes per layer (engine/model.js:415)
+_NO_PUSH = (1 << 30, 0, 0, 0, 0, 0)  # a record that matches no neuron (neuron index past any layer width)
+
+
+def mlp_weights(p):
+    """Per-layer MLP buffers (cached in p): "_gu" the [gate | up] fp32 weight of the prefill GEMM, "_gu_q8" / "_gu_s"
+    the int8 rows interleaved (gate j, up j) for the decode GEMV's SwiGLU epilogue, "_pushes" the layer's push
+    records."""
+    if "_gu" not in p:
+        p["_gu"] = torch.cat([p["gate_proj"], p["up_proj"]], dim=0).contiguous()
+        if "gate_proj.q" in p:
+            I, H = p["gate_proj.q"].shape
+            p["_gu_q8"] = torch.stack([p["gate_proj.q"], p["up_proj.q"]], dim=1).reshape(2 * I, H).contiguous()
+            p["_gu_s"] = torch.stack([p["gate_proj.s"], p["up_proj.s"]], dim=1).reshape(2 * I).contiguous()
+        p["_pushes"] = torch.tensor([_NO_PUSH] * MAX_PUSHES, dtype=torch.int32, device=p["_gu"].device)
+    return p
+
+
+def mlp(p, h, x):
+    """x += SwiGLU MLP (HF:704-717) of h, in place, with the layer's neuron pushes at the down_proj input
+    (engine/model.js:7-9, engine/kernels_qwen35.js:250-279). Decode (at most 8 rows, int8 weights present): one GEMV
+    over the interleaved int8 gate/up rows with the SwiGLU + push epilogue, and one int8 GEMV accumulating down_proj
+    into x. Otherwise a [gate | up] GEMM on the dequantised weights, the SwiGLU push kernel and a down_proj GEMM
+    accumulating into x. Returns x."""
+    mlp_weights(p)
+    H = h.shape[-1]
+    M = h.numel() // H
+    T = h.shape[1] if h.dim() == 3 else 1
+    if M <= 8 and "_gu_q8" in p and H % 256 == 0 and p["down_proj.q"].shape[1] % 256 == 0:
+        a = ops.gemv(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T)
+        ops.gemv(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H), epilogue="add")
+        return x
+    a = ops.swiglu_push(h @ p["_gu"].T, p["_pushes"], T=T)
+    x.view(M, H).addmm_(a.view(M, -1), p["down_proj"].T)
+    return x
 
 
 class HybridModel:
@@ -64,11 +95,12 @@ class HybridModel:
         self.steering = False
         self.params = [{n[len(f"layers.{l}."):]: t for n, t in self.W.t.items() if n.startswith(f"layers.{l}.")}
                        for l in range(cfg.layers)]
-        for l, p in enumerate(self.params):  # stacked input projections, built once
+        for l, p in enumerate(self.params):  # stacked input projections and MLP buffers, built once
             if cfg.is_attention(l):
                 layers.attn_in_weight(p)
             else:
                 layers.gdn_in_weight(p)
+            mlp_weights(p)
         self.states = []
         for l in range(cfg.layers):
             if cfg.is_attention(l):
@@ -107,22 +139,39 @@ class HybridModel:
         self.vec_rows.copy_(torch.as_tensor(vec_of_row, dtype=torch.int32))
         self.steering = True
 
+    def set_pushes(self, pushes):
+        """Neuron pushes per layer, {layer: [(neuron or None for every neuron, "add" | "mul", [value per row])]}, at
+        most 8 per layer (engine/model.js:412-423); layers not named have none. Written into fixed per-layer buffers,
+        so a captured decode step picks them up."""
+        for l, p in enumerate(self.params):
+            recs = pushes.get(l, []) if pushes else []
+            if len(recs) > MAX_PUSHES:
+                raise ValueError(f"HybridModel: at most {MAX_PUSHES} pushes per layer")
+            buf = torch.tensor([_NO_PUSH] * MAX_PUSHES, dtype=torch.int32)
+            if recs:
+                buf[:len(recs)] = ops.pack_pushes(recs, "cpu")
+            p["_pushes"].copy_(buf)
+
     def _layers(self, x, T, last, collect_layer, steer):
+        """The decoder layers 0..last over the residual stream x [rows, T, H] (dense fp32, updated in place): each
+        layer adds its mixer output in the fused residual-add + RMSNorm kernel and its MLP output in the MLP's last
+        product (HF:753-793; engine/model.js:436-462)."""
         cfg = self.cfg
         collected = None
+        y = None  # the previous mixer's output, added to x by the next norm
         for l in range(last + 1):
             p, st = self.params[l], self.states[l]
-            h = rmsnorm_1p(x, p["input_layernorm"], cfg.eps)
+            h = ops.add_rmsnorm_(x, y, p["input_layernorm"], cfg.eps)
             if cfg.is_attention(l):
                 y = layers.gated_attention_layer(h, p, st["k"], st["v"], self.pos_dev, rope_theta=cfg.rope_theta,
                                                  partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps)
             else:
                 y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
                                                 head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill)
-            x = x + y
-            x = x + mlp(p, rmsnorm_1p(x, p["post_attention_layernorm"], cfg.eps))
+            h = ops.add_rmsnorm_(x, y, p["post_attention_layernorm"], cfg.eps)
+            y = None
+            mlp(p, h, x)
             if l == self.steer_layer and steer:
-                x = x.contiguous()
                 layers.residual_steer_add(x, self.vec_buf, self.vec_rows)
             if l == collect_layer:
                 collected = x.clone()
@@ -138,15 +187,21 @@ class HybridModel:
             raise ValueError("context exceeds the KV cache")
         if T > 1 and self.pos != 0:
             raise ValueError("HybridModel: a multi-token call must start the sequence (positions 0..T-1)")
-        x = W["embed"][ids.to(self.device)]
+        x = W["embed"][ids.to(self.device)].contiguous()
         last = cfg.layers - 1 if stop_after is None else stop_after
         x, collected = self._layers(x, T, last, collect_layer, self.steering)
         self.pos_dev.add_(T)
         self.pos += T
         if stop_after is not None:
             return None, collected
-        hN = rmsnorm_1p(x[:, -1], W["norm"], cfg.eps)
-        return hN @ W["embed"].T, collected
+        return self._lm_head(x[:, -1]), collected
+
+    def _lm_head(self, xl):
+        """Final RMSNorm and the tied-embedding logits of the last positions xl [rows, H] (a GEMV for few rows)."""
+        hN = ops.add_rmsnorm_(xl.contiguous(), None, self.W["norm"], self.cfg.eps)
+        if hN.shape[0] <= 8 and hN.shape[1] % 256 == 0:
+            return ops.gemv(hN.contiguous(), self.W["embed"])
+        return hN @ self.W["embed"].T
 
     @torch.no_grad()
     def enable_decode_graph(self):
@@ -160,16 +215,15 @@ class HybridModel:
         side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side):  # warm-up outside capture: library handles, allocator pools
             for _ in range(2):
-                x, _ = self._layers(self.W["embed"][self._g_ids], 1, cfg.layers - 1, None, True)
+                x, _ = self._layers(self.W["embed"][self._g_ids].contiguous(), 1, cfg.layers - 1, None, True)
                 self.pos_dev.add_(1)
         torch.cuda.current_stream(self.device).wait_stream(side)
         torch.cuda.synchronize(self.device)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            x, _ = self._layers(self.W["embed"][self._g_ids], 1, cfg.layers - 1, None, True)
+            x, _ = self._layers(self.W["embed"][self._g_ids].contiguous(), 1, cfg.layers - 1, None, True)
             self.pos_dev.add_(1)
-            hN = rmsnorm_1p(x[:, -1], self.W["norm"], cfg.eps)
-            self._g_logits = hN @ self.W["embed"].T
+            self._g_logits = self._lm_head(x[:, -1])
         self.graph = g
         torch.cuda.synchronize(self.device)
         self.reset()

@@ -69,6 +69,7 @@ _LIB.define("gdn_conv(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) con
 _LIB.define("gated_rmsnorm(Tensor o, Tensor z, Tensor w, Tensor? head_scale, float eps) -> Tensor")
 _LIB.define("gemv_(Tensor x, Tensor W, Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
 _LIB.define("swiglu_push(Tensor gu, Tensor? pushes, int T) -> Tensor")
+_LIB.define("add_rmsnorm_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tensor")
 _LIB.define("attn_prep(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, Tensor cos, Tensor sin, Tensor pos, "
             "Tensor(a!) k_cache, Tensor(b!) v_cache, int Hq, int Hkv, bool want_kv) "
             "-> (Tensor, Tensor, Tensor, Tensor)")
@@ -314,6 +315,19 @@ def _swiglu_push_impl(gu, pushes, T):
     return a
 
 
+def _add_rmsnorm_impl(x, y, w, eps):
+    _on_gpu(x, y, w)
+    _require(x.dtype == torch.float32 and w.dtype == torch.float32, "x, w fp32")
+    H = x.shape[-1]
+    _require(w.numel() == H and (y is None or (y.shape == x.shape and y.dtype == torch.float32)),
+             "w: [H]; y like x")
+    M = x.numel() // H
+    h = torch.empty_like(x)
+    st = _lib.lib().q35_add_rmsnorm(_ptr(x), H, _ptr(y), H, _ptr(w), _ptr(h), H, M, H, float(eps), _stream(x))
+    check(st, "q35_add_rmsnorm")
+    return h
+
+
 def _no_cpu(name):
     def f(*args, **kwargs):
         raise Q35Error(f"q35hip: q35::{name} needs HIP device tensors; the product has no CPU path")
@@ -324,7 +338,8 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gdn_chunk_prefill", _gdn_chunk_impl), ("gated_attn_prefill", _attn_prefill_impl),
                      ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
                      ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl),
-                     ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl)]:
+                     ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
+                     ("add_rmsnorm_", _add_rmsnorm_impl)]:
     _LIB.impl(_name, _impl, "CUDA")
     _LIB.impl(_name, _no_cpu(_name), "CPU")
 
@@ -462,3 +477,9 @@ def swiglu_push(gu, pushes=None, T=1):
     """silu(gate) * up over a [..., 2 I] ([gate | up]) projection with the neuron pushes applied (the hook point of
     engine/kernels_qwen35.js:250-279)."""
     return torch.ops.q35.swiglu_push(gu, pushes, int(T))
+
+
+def add_rmsnorm_(x, y, w, eps=1e-6):
+    """x += y in place (y None: no add), then return x * rsqrt(mean x^2 + eps) * (1 + w) (Qwen3_5RMSNorm, HF:720-734),
+    fp32, x and y dense [..., H]."""
+    return torch.ops.q35.add_rmsnorm_(x, y, w.float().contiguous(), float(eps))

@@ -25,6 +25,8 @@
  *                            SwiGLU epilogue, engine/kernels_qwen35.js:250-279 `swiglu` with the neuron pushes;
  *                            HF:704-717 Qwen3_5MLP for the decode step
  *   q35_swiglu_push          engine/kernels_qwen35.js:250-279 `swiglu` over a [gate | up] projection (prefill form)
+ *   q35_add_rmsnorm          HF:720-734 Qwen3_5RMSNorm (1 + w) with the residual add before it (HF:753-793);
+ *                            engine/kernels.js:226-246 `rmsnorm` (OFFSET) and `addInto`
  */
 #ifndef Q35HIP_H
 #define Q35HIP_H
@@ -182,6 +184,14 @@ int q35_attn_prep(const float* y, int64_t ldy, const float* q_norm_w, const floa
                   const float* cos, const float* sin, int64_t rot, const int32_t* pos, void* q_out, void* gate_out,
                   void* k_out, void* v_out, void* k_cache, void* v_cache, int64_t max_len, int64_t B, int64_t T,
                   int64_t Hq, int64_t Hkv, int64_t D, q35_stream_t stream);
+
+/*
+ * Residual add + RMSNorm with (1 + w) per row: x[m] += y[m] in place (y may be NULL: no add), then
+ * h[m] = x[m] * rsqrt(mean(x[m]^2) + eps) * (1 + w), all fp32. x: [M, ldx], y: [M, ldy], h: [M, ldh], w: [H];
+ * H a multiple of 4 and at most 8192; pointers 16-byte aligned, leading dimensions multiples of 4.
+ */
+int q35_add_rmsnorm(float* x, int64_t ldx, const float* y, int64_t ldy, const float* w, float* h, int64_t ldh,
+                    int64_t M, int64_t H, float eps, q35_stream_t stream);
 
 /*
  * Small-M matrix-vector product for the decode step: y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k], m < M <= 8.

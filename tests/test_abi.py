@@ -24,7 +24,7 @@ def test_header_declares_the_boundary():
     names = declared_functions()
     for n in ["q35_gdn_recurrent", "q35_gdn_chunk_prefill", "q35_gated_attn_prefill", "q35_gated_attn_decode",
               "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
-              "q35_swiglu_push"]:
+              "q35_swiglu_push", "q35_add_rmsnorm"]:
         assert n in names
 
 
@@ -103,6 +103,8 @@ def test_validation_rejects_without_launching():
     assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 63, 1024, 2, None, 0, 1, None) == 1
     assert L.q35_gemv(fake, 1024, fake, 1, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1, None) == 2
     assert L.q35_swiglu_push(fake, fake, 3, 64, None, 2, 1, None) == 1
+    assert L.q35_add_rmsnorm(fake, 1024, None, 0, fake, fake, 1024, 3, 1022, 1e-6, None) == 2
+    assert L.q35_add_rmsnorm(fake, 512, None, 0, fake, fake, 1024, 3, 1024, 1e-6, None) == 1
 
 
 def test_decode_workspace_scales_with_splits():

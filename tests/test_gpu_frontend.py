@@ -125,3 +125,22 @@ def test_attn_prep_matches_oracle_and_writes_cache_rows(T):
         assert oracle.rel_err(vc[b, :, p0:p0 + T].float(), v[b].transpose(0, 1)) <= TOL_BF16
     # every other cache row is untouched
     assert bool((kc.transpose(1, 2)[~written] == 7.0).all()) and bool((vc.transpose(1, 2)[~written] == 7.0).all())
+
+
+@pytest.mark.parametrize("with_add", [False, True])
+def test_add_rmsnorm_matches_oracle(with_add):
+    """Residual add + RMSNorm(1 + w) (HF:720-734): x updated in place, h returned."""
+    from oracle import model as om
+    dev = device()
+    g = torch.Generator().manual_seed(70)
+    x = torch.randn(3, 5, 1024, generator=g)
+    y = torch.randn(3, 5, 1024, generator=g) if with_add else None
+    w = 0.1 * torch.randn(1024, generator=g)
+    xs = x + y if with_add else x
+    ref = om.rmsnorm_1p(xs, w, 1e-6)
+    announce(f"add_rmsnorm add={with_add}")
+    xd = x.to(dev)
+    h = ops.add_rmsnorm_(xd, None if y is None else y.to(dev), w.to(dev))
+    torch.cuda.synchronize()
+    assert oracle.rel_err(h.cpu(), ref) <= TOL_F32
+    assert oracle.rel_err(xd.cpu(), xs) <= TOL_F32
