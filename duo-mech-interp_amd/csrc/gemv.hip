@@ -51,17 +51,32 @@ template <> struct WChunk<float> {
   __device__ __forceinline__ float at(int i) const { return r[i]; }
 };
 
-template <typename TW, int MP, int EPI>
+template <typename TW, int MP, int EPI, int U>
 __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, int64_t ldx, const TW* __restrict__ W,
                                                    const float* __restrict__ wscale, float* __restrict__ y,
                                                    int64_t ldy, int M, int N, int K,
                                                    const q35_push* __restrict__ pushes, int npush, int T) {
   constexpr int E = WChunk<TW>::kElems;  // weights per lane per 16-byte load
   constexpr int STEP = 4 * E;            // inputs per step of a row (4 lanes)
-  constexpr int U = 4;                   // steps in flight
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [MP][K]
   __shared__ float red[4][16][MP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane >> 2, qd = lane & 3;
+  const int n = blockIdx.x * 16 + r;
+  const TW* wrow = W + (size_t)min(n, N - 1) * K;
+  const int kq = K / 4, kb = wave * kq;
+  // U steps (U 16-byte loads per lane) in flight per iteration; the first iteration's weight loads are issued before
+  // x is staged, so that their latency covers the staging
+  WChunk<TW> wc[U];
+  auto issue = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = min(k0 + u * STEP, kb + kq - STEP) + qd * E;
+      wc[u].load(wrow + k);
+    }
+  };
+  issue(kb);
+  asm volatile("" ::: "memory");
   for (int i = tid; i < MP * K / 4; i += 256) {
     const int m = (4 * i) / K, k = 4 * i - m * K;
     f32x4 v = zero4();
@@ -69,20 +84,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, 
     *reinterpret_cast<f32x4*>(xs + m * K + k) = v;
   }
   __syncthreads();
-  const int r = lane >> 2, qd = lane & 3;
-  const int n = blockIdx.x * 16 + r;
-  const TW* wrow = W + (size_t)min(n, N - 1) * K;
-  const int kq = K / 4, kb = wave * kq;
   float acc[MP];
 #pragma unroll
   for (int m = 0; m < MP; ++m) acc[m] = 0.f;
   for (int k0 = kb; k0 < kb + kq; k0 += U * STEP) {
-    WChunk<TW> wc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = min(k0 + u * STEP, kb + kq - STEP) + qd * E;
-      wc[u].load(wrow + k);
-    }
+    if (k0 != kb) issue(k0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (k0 + u * STEP >= kb + kq) break;
@@ -159,16 +165,16 @@ __global__ __launch_bounds__(256) void swiglu_push_kernel(const float* __restric
 }  // namespace q35
 
 namespace {
-template <typename TW, int EPI>
-int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
-                int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, hipStream_t st) {
+template <typename TW, int EPI, int U>
+void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
+                   int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, hipStream_t st) {
   using namespace q35;
   const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
   const size_t lds = (size_t)mp * K * sizeof(float);
   const dim3 grid((unsigned)((N + 15) / 16)), block(256);
 #define Q35_GEMV(MP)                                                                                                  \
-  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI>), grid, block, lds, st, x, ldx, W, wscale, y, ldy, (int)M, (int)N, \
-                     (int)K, pushes, npush, (int)T)
+  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U>), grid, block, lds, st, x, ldx, W, wscale, y, ldy, (int)M,      \
+                     (int)N, (int)K, pushes, npush, (int)T)
   switch (mp) {
     case 1: Q35_GEMV(1); break;
     case 2: Q35_GEMV(2); break;
@@ -176,6 +182,20 @@ int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, f
     default: Q35_GEMV(8); break;
   }
 #undef Q35_GEMV
+}
+
+// steps of a wave's K quarter: all in flight at once up to 16
+template <typename TW, int EPI>
+int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
+                int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, hipStream_t st) {
+  using namespace q35;
+  const int64_t steps = K / 4 / (4 * WChunk<TW>::kElems);
+  if (steps <= 4)
+    gemv_launch_u<TW, EPI, 4>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, st);
+  else if (steps <= 8)
+    gemv_launch_u<TW, EPI, 8>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, st);
+  else
+    gemv_launch_u<TW, EPI, 16>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, st);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 }  // namespace
