@@ -36,6 +36,16 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds_dst) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
 }
+// the same with a uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset (the base is moved to SGPRs
+// explicitly: the compiler cannot always prove it uniform)
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+  const uint64_t a = reinterpret_cast<uint64_t>(sbase);
+  const uint64_t u = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_dst), "v"(voff),
+               "s"(reinterpret_cast<const void*>(u))
+               : "memory", "m0");
+}
 
 // key order inside a group of 16 keys in V^T (an involution: swaps bits 2 and 3)
 __device__ __forceinline__ int vperm(int p) { return (p & 3) | ((p & 4) << 1) | ((p & 8) >> 1); }
@@ -48,16 +58,10 @@ __global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restr
                                                            const float* __restrict__ cos_t,
                                                            const float* __restrict__ sin_t, int pos0,
                                                            __bf16* __restrict__ kr, __bf16* __restrict__ vt, int T,
-                                                           int Tp, int Hkv, int* __restrict__ cnt, int ncnt) {
+                                                           int Tp, int Hkv) {
   static_assert(ROT % 16 == 0 && ROT <= kRotMax, "rotary dims");
   constexpr int half = ROT / 2;
   const int tid = threadIdx.x;
-  // the attention kernel's split-block arrival counters start every launch at zero
-  {
-    const int lb = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    const int nb = gridDim.x * gridDim.y * gridDim.z;
-    for (int i = lb * 256 + tid; i < ncnt; i += nb * 256) cnt[i] = 0;
-  }
   const int key0 = blockIdx.x * kBN, kvh = blockIdx.y, b = blockIdx.z;
   const size_t head = (size_t)b * Hkv + kvh;
   // K: thread = (row r, quarter cq of the dims); the rotary dims [0, rot) all sit in quarter 0
@@ -148,7 +152,7 @@ struct PfStage {
 
 // Work items. Query block qb needs key tiles 0 .. nkt(qb) - 1, so the causal blocks range from 1 to ~T/64 tiles. With
 // a split length Ls > 0, every block with more than Ls tiles (qb >= 2 Ls) is run as two items, tiles [0, Ls) and
-// [Ls, nkt), whose (O, m, l) are merged by whichever finishes second; the others run whole. Items are numbered
+// [Ls, nkt), whose (O, m, l) are combined by attn_prefill_merge_kernel; the others run whole. Items are numbered
 // longest first: all first halves (Ls tiles each), then second halves and whole blocks alternately, each in
 // decreasing length, so that the hardware's in-order dispatch to free CUs balances the CUs' total tiles.
 constexpr int kPartFloats = 8192 + 128;  // one wave's partial: O^T [32 x 256] fp32 in accumulator order, m[64], l[64]
@@ -196,9 +200,8 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ kr, const __bf16* __restrict__ vt,
     const __bf16* __restrict__ gate, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos0,
     __bf16* __restrict__ out, int T, int Tp, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb, int B,
-    int Ls, float* __restrict__ part, int* __restrict__ cnt) {
+    int Ls, float* __restrict__ part) {
   __shared__ PfStage stage[2];
-  __shared__ int merge_here;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -218,55 +221,81 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
   const char* kbase = reinterpret_cast<const char*>(kr + head * Tp * kPD);
   const char* vbase = reinterpret_cast<const char*>(vt + head * kPD * Tp);
 
-  // this wave's share of the copies of tile kt into stage s: CPW of the 32 K copies (2 rows each) and CPW of the
-  // 32 V^T copies (8 rows each)
+  // This wave's share of the copies of tile kt into stage s: CPW of the 32 K copies (2 rows each) and CPW of the
+  // 32 V^T copies (8 rows each). Copy c of K fills LDS rows 2c, 2c + 1; lane i fetches the 16 bytes that belong at
+  // LDS position i: row 2c + hl (hl = i >> 5), logical segment (i & 31) ^ ((2c + hl) & 15). Its source offset is
+  // 1024 c + (512 hl + 16 ((i & 31) ^ hl)) ^ 16 ((2c) & 15): one lane constant XOR-ed with a per-copy constant (the
+  // XOR only touches bits 5-7). Copy c of V^T fills rows d = 8c + (i >> 3) with logical segment
+  // (i & 7) ^ ((d >> 1) & 7) = (i & 7) ^ (i >> 4) ^ 4 (c & 1); its source offset is d 2Tp + 16 segment. The uniform
+  // parts go into the scalar base address, so a copy costs one vector XOR.
   constexpr int CPW = 32 / GW;
+  const uint32_t kcl = 512 * (lane >> 5) + 16 * ((lane & 31) ^ (lane >> 5));
+  const uint32_t vcl = (uint32_t)(lane >> 3) * (uint32_t)(2 * Tp) + 16 * ((lane & 7) ^ (lane >> 4));
   auto copy_tile = [&](int kt, int s) {
-    int lane = threadIdx.x & 63;
-    asm volatile("" : "+v"(lane));  // keep the per-lane source offsets out of registers between tiles
     const int key0 = kt * kBN;
     const uint32_t kl = lds_u32(&stage[s].k[0]), vl = lds_u32(&stage[s].v[0]);
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
       const int c = CPW * wave + i;  // copy index 0..31
-      const int r = 2 * c + (lane >> 5), ps = lane & 31;
-      const int ls = ps ^ (r & 15);
-      dma16(kbase + (size_t)(key0 + r) * (kPD * 2) + 16 * ls, __builtin_amdgcn_readfirstlane(kl + 1024 * c));
+      dma16s(kbase + (size_t)key0 * (kPD * 2) + 1024 * c, kcl ^ (16u * ((2 * c) & 15)),
+             __builtin_amdgcn_readfirstlane(kl + 1024 * c));
     }
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
       const int c = CPW * wave + i;
-      const int d = 8 * c + (lane >> 3), ps = lane & 7;
-      const int ls = ps ^ ((d >> 1) & 7);
-      dma16(vbase + (size_t)d * (Tp * 2) + (size_t)key0 * 2 + 16 * ls, __builtin_amdgcn_readfirstlane(vl + 1024 * c));
+      dma16s(vbase + (size_t)8 * c * (Tp * 2) + (size_t)key0 * 2, vcl ^ (64u * (c & 1)),
+             __builtin_amdgcn_readfirstlane(vl + 1024 * c));
     }
   };
 
-  copy_tile(it.kt0, it.kt0 & 1);
-  // ---- Q^T operand (B of S^T = K Q^T): lane holds query q0 + ln, dims 16 ks + 8 hh + j, rotated ----
+  // ---- Q^T operand (B of S^T = K Q^T): lane holds query q0 + ln, dims 16 ks + 8 hh + j, rotated. Every load (the
+  //      query row, the rotation partners and the cos / sin rows) is issued before the first tile's copies and before
+  //      any of them is used, so the prologue costs one memory round trip.
   bf16x8 qop[16];
   {
     const int t = q0 + ln;
     const bool tv = t < T;
-    const __bf16* qrow = q + (((size_t)b * T + (tv ? t : 0)) * Hq + h) * kPD;
-    const int pos = pos0 + t;
+    const __bf16* qrow = q + (((size_t)b * T + (tv ? t : T - 1)) * Hq + h) * kPD;
+    const int pos = pos0 + (tv ? t : T - 1);
+    u32x4 raw[16];
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
+    const int nrk = rot >> 4;  // K steps holding rotary dims (rot is a multiple of 16, at most 64)
+    u32x4 praw[4];
+    f32x4 cs[4][2], sn[4][2];
+    if (nrk > 0) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks < nrk) {
+          const int d = 16 * ks + 8 * hh;
+          const int pd = d < half ? d + half : d - half;
+          const int j0 = d < half ? d : d - half;
+          praw[ks] = *reinterpret_cast<const u32x4*>(qrow + pd);
+          const float* cp = cos_t + (size_t)pos * half + j0;
+          const float* sp = sin_t + (size_t)pos * half + j0;
+          cs[ks][0] = *reinterpret_cast<const f32x4*>(cp);
+          cs[ks][1] = *reinterpret_cast<const f32x4*>(cp + 4);
+          sn[ks][0] = *reinterpret_cast<const f32x4*>(sp);
+          sn[ks][1] = *reinterpret_cast<const f32x4*>(sp + 4);
+        }
+      }
+    }
+    copy_tile(it.kt0, it.kt0 & 1);
 #pragma unroll
     for (int ks = 0; ks < 16; ++ks) {
-      const int d = 16 * ks + 8 * hh;
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(qrow + d);
-      float x[8] = {bf16lo(raw[0]), bf16hi(raw[0]), bf16lo(raw[1]), bf16hi(raw[1]),
-                    bf16lo(raw[2]), bf16hi(raw[2]), bf16lo(raw[3]), bf16hi(raw[3])};
-      if (tv && d < rot) {
-        const int pd = d < half ? d + half : d - half;
-        const u32x4 pr = *reinterpret_cast<const u32x4*>(qrow + pd);
+      const u32x4 r = raw[ks];
+      float x[8] = {bf16lo(r[0]), bf16hi(r[0]), bf16lo(r[1]), bf16hi(r[1]),
+                    bf16lo(r[2]), bf16hi(r[2]), bf16lo(r[3]), bf16hi(r[3])};
+      if (ks < 4 && ks < nrk) {
+        const int d = 16 * ks + 8 * hh;
+        const u32x4 pr = praw[ks];
         const float y[8] = {bf16lo(pr[0]), bf16hi(pr[0]), bf16lo(pr[1]), bf16hi(pr[1]),
                             bf16lo(pr[2]), bf16hi(pr[2]), bf16lo(pr[3]), bf16hi(pr[3])};
-        const int j0 = d < half ? d : d - half;
         const float sg = d < half ? -1.f : 1.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float c = cos_t[(size_t)pos * half + j0 + j], sn = sin_t[(size_t)pos * half + j0 + j];
-          x[j] = x[j] * c + sg * y[j] * sn;
+          const float c = cs[ks][j >> 2][j & 3], sv = sn[ks][j >> 2][j & 3];
+          x[j] = x[j] * c + sg * y[j] * sv;
         }
       }
 #pragma unroll
@@ -277,11 +306,27 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
   f32x16 o[8];
 #pragma unroll
   for (int mt = 0; mt < 8; ++mt) o[mt] = zero16();
+  // Scores are kept unscaled; the softmax works in base 2 on scaled scores: p = 2^(s c - m) with c = scale log2(e),
+  // m_run the running max of s c.
+  const float csc = scale * 1.44269504088896341f;
   float m_run = -INFINITY, l_run = 0.f;
   const int tq = q0 + ln;  // this lane's query
   const int full_tiles = q0 / kBN;  // tiles entirely below this block's first query: no mask
 
-  // Scores of tile kt (scaled and causally masked) into sc; returns this lane's query's max over the tile's keys.
+  // Per-lane LDS read offsets inside a stage. K: row 32 ksub + ln, logical segment 2 ks + hh, stored at segment
+  // (2 ks + hh) ^ (ln & 15): for ks = 8 a + j the offset is ka[j] + 256 a + 16384 ksub. V^T: row 32 mt + ln, logical
+  // segment 2 kk + hh stored at (2 kk + hh) ^ ((ln >> 1) & 7): offset va[kk] + 4096 mt.
+  int ka[8], va[4];
+  {
+    const int c2 = (ln >> 1) & 7;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ka[j] = 512 * ln + 16 * (hh ^ (ln & 1)) + 32 * (j ^ c2);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) va[kk] = 128 * ln + 16 * ((2 * kk + hh) ^ c2);
+  }
+
+  // Raw scores of tile kt into sc (S^T = K Q^T, causally masked with -inf); returns this lane's query's max of the
+  // raw scores over the tile's keys.
   auto tile_scores = [&](int kt, f32x16 (&sc)[2]) -> float {
     const int s = kt & 1;
     // this wave's copies of tile kt are its only ones in flight; after the barrier every wave's have landed and
@@ -290,91 +335,112 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     __syncthreads();
     if (kt + 1 < it.kt1) copy_tile(kt + 1, s ^ 1);
     const char* kl = reinterpret_cast<const char*>(&stage[s].k[0]);
-    // the operand addresses below are recomputed every tile from an opaque copy of the lane id: hoisted out of the
-    // loop they would occupy some 60 registers, and the kernel is register-bound
-    int lo_ = threadIdx.x & 63;
-    asm volatile("" : "+v"(lo_));
-    const int ln = lo_ & 31, hh = lo_ >> 5;
-    // S^T = K Q^T for the two 32-key halves of the tile (rows = keys, cols = this wave's 32 queries): four
-    // independent accumulation chains, K fragments read four K steps at a time
-    f32x16 acc[2][2];
+    // four accumulation chains (two per 32-key half: even and odd K steps) over four groups of four K steps; the K
+    // fragments of group g + 1 are read while the MFMAs of group g run, so LDS latency is hidden behind the matrix
+    // core
+    f32x16 acc[2][2] = {{zero16(), zero16()}, {zero16(), zero16()}};
+    auto kread = [&](int g, bf16x8 (&kf)[2][4]) {
 #pragma unroll
-    for (int ksub = 0; ksub < 2; ++ksub) { acc[ksub][0] = zero16(); acc[ksub][1] = zero16(); }
+      for (int ksub = 0; ksub < 2; ++ksub)
 #pragma unroll
-    for (int ks0 = 0; ks0 < 16; ks0 += 4) {
-      bf16x8 kf[2][4];
+        for (int j = 0; j < 4; ++j) {
+          const int ks = 4 * g + j;
+          kf[ksub][j] = *reinterpret_cast<const bf16x8*>(kl + ka[ks & 7] + 256 * (ks >> 3) + 16384 * ksub);
+        }
+    };
+    bf16x8 kfa[2][4], kfb[2][4];
+    kread(0, kfa);
 #pragma unroll
-      for (int ksub = 0; ksub < 2; ++ksub) {
-        const int r = 32 * ksub + ln;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          kf[ksub][j] = *reinterpret_cast<const bf16x8*>(kl + r * 512 + 16 * ((2 * (ks0 + j) + hh) ^ (r & 15)));
-      }
+    for (int g = 0; g < 4; ++g) {
+      bf16x8 (&cur)[2][4] = (g & 1) ? kfb : kfa;
+      bf16x8 (&nxt)[2][4] = (g & 1) ? kfa : kfb;
+      if (g < 3) kread(g + 1, nxt);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int ksub = 0; ksub < 2; ++ksub) acc[ksub][j & 1] = mfma32(kf[ksub][j], qop[ks0 + j], acc[ksub][j & 1]);
-      // all eight reads first, then the eight MFMAs (the default schedule waits on each read pair in turn)
+        for (int ksub = 0; ksub < 2; ++ksub)
+          acc[ksub][j & 1] = mfma32(cur[ksub][j], qop[4 * g + j], acc[ksub][j & 1]);
+    }
+    // order: reads of group 0; then (reads of g + 1, MFMAs of g) for g = 0..2; then the MFMAs of group 3
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     float mx = -INFINITY;
-    const bool masked = kt >= full_tiles;
+    if (__builtin_amdgcn_readfirstlane(kt) >= full_tiles) {
+      // lane (ln, hh) holds keys 64 kt + 32 ksub + 8 (i >> 2) + 4 hh + (i & 3) of query tq
+      const int kl0 = kt * kBN + 4 * hh;
 #pragma unroll
-    for (int ksub = 0; ksub < 2; ++ksub)
+      for (int ksub = 0; ksub < 2; ++ksub)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = kt * kBN + 32 * ksub + 8 * (i >> 2) + 4 * hh + (i & 3);
-        float x = (acc[ksub][0][i] + acc[ksub][1][i]) * scale;
-        if (masked) x = (key <= tq && key < T) ? x : -INFINITY;
-        sc[ksub][i] = x;
-        mx = fmaxf(mx, x);
-      }
-    return fmaxf(mx, __shfl_xor(mx, 32, 64));
+        for (int i = 0; i < 16; ++i) {
+          const int key = kl0 + 32 * ksub + 8 * (i >> 2) + (i & 3);
+          const float x = (key <= tq && key < T) ? acc[ksub][0][i] + acc[ksub][1][i] : -INFINITY;
+          sc[ksub][i] = x;
+          mx = fmaxf(mx, x);
+        }
+    } else {
+#pragma unroll
+      for (int ksub = 0; ksub < 2; ++ksub)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          sc[ksub][i] = acc[ksub][0][i] + acc[ksub][1][i];
+          mx = fmaxf(mx, sc[ksub][i]);
+        }
+    }
+    return fmaxf(mx, __shfl_xor(mx, 32, 64)) * csc;
   };
-  // P = exp(S - m_run) of tile kt into the row sum, then O^T += V^T P^T: rows = 256 dims (8 tiles of 32),
-  // k = 64 keys (4 steps of 16); V^T fragments read two dim tiles at a time
+  // P = 2^(s c - m_run) of tile kt into the row sum, then O^T += V^T P^T: rows = 256 dims (8 tiles of 32), k = 64
+  // keys (4 steps of 16). The MFMAs run K step by K step, so those of step kk need only P's group kk: the
+  // exponentials of later groups overlap the matrix core.
   auto tile_accumulate = [&](int kt, const f32x16 (&sc)[2]) {
     const char* vl = reinterpret_cast<const char*>(&stage[kt & 1].v[0]);
-    int lo_ = threadIdx.x & 63;
-    asm volatile("" : "+v"(lo_));
-    const int ln = lo_ & 31, hh = lo_ >> 5;
+    auto vread = [&](int kk, bf16x8 (&vf)[8]) {
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt) vf[mt] = *reinterpret_cast<const bf16x8*>(vl + va[kk] + 4096 * mt);
+    };
+    bf16x8 vfa[8], vfb[8];
+    vread(0, vfa);
+    const float nm = -m_run;
     float ps = 0.f;
     bf16x8 pb[4];
 #pragma unroll
     for (int ksub = 0; ksub < 2; ++ksub)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = __expf(sc[ksub][i] - m_run);
+        const float p = __builtin_amdgcn_exp2f(fmaf(sc[ksub][i], csc, nm));
         ps += p;
         pb[2 * ksub + (i >> 3)][i & 7] = (__bf16)p;
       }
     ps += __shfl_xor(ps, 32, 64);
     l_run += ps;
 #pragma unroll
-    for (int mt0 = 0; mt0 < 8; mt0 += 2) {
-      bf16x8 vf[2][4];
+    for (int kk = 0; kk < 4; ++kk) {
+      bf16x8 (&cur)[8] = (kk & 1) ? vfb : vfa;
+      bf16x8 (&nxt)[8] = (kk & 1) ? vfa : vfb;
+      if (kk < 3) vread(kk + 1, nxt);
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int d = 32 * (mt0 + u) + ln;
+      for (int mt = 0; mt < 8; ++mt) o[mt] = mfma32(cur[mt], pb[kk], o[mt]);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-          vf[u][kk] = *reinterpret_cast<const bf16x8*>(vl + d * 128 + 16 * ((2 * kk + hh) ^ ((d >> 1) & 7)));
-      }
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) o[mt0 + u] = mfma32(vf[u][kk], pb[kk], o[mt0 + u]);
+    for (int g = 0; g < 3; ++g) {
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
   };
 
   // Online softmax along the keys of each lane's query (lane pair l, l ^ 32 holds all 64 keys of a tile). The
-  // running max only moves (and O, l are rescaled) when a tile max exceeds it by more than 8: p = exp(s - m) <= e^8
+  // running max only moves (and O, l are rescaled) when a tile max exceeds it by more than 8 (base 2): p <= 2^8
   // stays exact enough in fp32 and in the bf16 P operand. The inner loop runs the tiles that need no rescale, so O
   // never leaves the MFMA accumulators there; the rescale (a read, multiply and write-back of all 128 accumulator
-  // registers) sits outside it and runs a few times per block (always at tile 0).
+  // registers) sits outside it and runs a few times per block (always at tile 0). Every lane has a finite score in
+  // the first tile of its item (key 0, or a split block's first key, is at or before its query), so m_run is finite
+  // from then on.
   int kt = it.kt0;
   while (kt < it.kt1) {
     f32x16 sc[2];
@@ -386,7 +452,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     }
     if (kt == it.kt1) break;
     const float mn = fmaxf(m_run, mx);
-    const float corr = __expf(m_run - mn);
+    const float corr = __builtin_amdgcn_exp2f(m_run - mn);
     l_run *= corr;
     m_run = mn;
 #pragma unroll
@@ -397,11 +463,10 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     ++kt;
   }
 
-  // ---- a split query block: both halves publish (O, m, l); the second to finish merges and stores ----
+  // ---- a split query block: each half publishes its (O, m, l); attn_prefill_merge_kernel combines them ----
   if (it.half >= 0) {
     const int pair = (qb - 2 * Ls) * n_other + rem;
     float* mine = part + ((size_t)(2 * pair + it.half) * GW + wave) * kPartFloats;
-    const float* other = part + ((size_t)(2 * pair + (it.half ^ 1)) * GW + wave) * kPartFloats;
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
@@ -411,33 +476,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
       }
     mine[8192 + lane] = m_run;
     mine[8192 + 64 + lane] = l_run;
-    // release: this block's partial is visible device-wide before its arrival is counted
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) merge_here = atomicAdd(cnt + pair, 1);
-    __syncthreads();
-    if (merge_here == 0) return;  // the other half is still running and will merge
-    __threadfence();              // acquire: the other half's partial was published before its count
-    // O = O0 e^(m0 - m) + O1 e^(m1 - m), l likewise, always in half order so that the result does not depend on
-    // which half finished last. Neither half has a fully masked query: the second half starts at key 64 Ls and every
-    // query of a split block is at or past it.
-    const float m_o = other[8192 + lane], l_o = other[8192 + 64 + lane];
-    const float m0 = it.half ? m_o : m_run, m1 = it.half ? m_run : m_o;
-    const float l0 = it.half ? l_o : l_run, l1 = it.half ? l_run : l_o;
-    const float mm = fmaxf(m0, m1);
-    const float c0 = __expf(m0 - mm), c1 = __expf(m1 - mm);
-    l_run = fmaf(l0, c0, l1 * c1);
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const f32x4 w = *reinterpret_cast<const f32x4*>(other + ((mt * 4 + c) * 64 + lane) * 4);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a = o[mt][4 * c + e];
-          o[mt][4 * c + e] = it.half ? fmaf(w[e], c0, a * c1) : fmaf(a, c0, w[e] * c1);
-        }
-      }
+    return;
   }
 
   // ---- epilogue: normalise, gate, store ----
@@ -460,13 +499,57 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
   }
 }
 
+// Kernel 3: the two halves of every split query block. One wave per (pair, query head of the group): lane (ln, hh)
+// reads the accumulator-order partials of both halves exactly as the main kernel's lanes wrote them and combines them
+// in half order, O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise (so the result does not depend on which half ran
+// first), then normalises, gates and stores as the main kernel's epilogue does. Neither half has a fully masked
+// query: the second half starts at key 64 Ls and every query of a split block is at or past it.
+template <int GW>
+__global__ __launch_bounds__(64) void attn_prefill_merge_kernel(const float* __restrict__ part,
+                                                                const __bf16* __restrict__ gate,
+                                                                __bf16* __restrict__ out, int T, int Hq, int Hkv,
+                                                                int ngroups, int B, int Ls) {
+  const int pair = blockIdx.x, wave = blockIdx.y, lane = threadIdx.x;
+  const int n_other = B * Hkv * ngroups;
+  const int qb = 2 * Ls + pair / n_other, rem = pair % n_other;
+  const int b = rem / (Hkv * ngroups), kvh = (rem / ngroups) % Hkv, hg = rem % ngroups;
+  const int h = kvh * (Hq / Hkv) + hg * GW + wave;
+  const int ln = lane & 31, hh = lane >> 5;
+  const int tq = qb * kBQ + ln;
+  const float* p0 = part + ((size_t)(2 * pair) * GW + wave) * kPartFloats;
+  const float* p1 = part + ((size_t)(2 * pair + 1) * GW + wave) * kPartFloats;
+  const float m0 = p0[8192 + lane], l0 = p0[8192 + 64 + lane];
+  const float m1 = p1[8192 + lane], l1 = p1[8192 + 64 + lane];
+  const float mm = fmaxf(m0, m1);
+  const float c0 = __builtin_amdgcn_exp2f(m0 - mm), c1 = __builtin_amdgcn_exp2f(m1 - mm);
+  const float l = fmaf(l0, c0, l1 * c1);
+  if (tq >= T) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const size_t rowo = ((size_t)b * T + tq) * (size_t)Hq * kPD + (size_t)h * kPD;
+#pragma unroll 4
+  for (int mt = 0; mt < 8; ++mt) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d = 32 * mt + 8 * c + 4 * hh;
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(p0 + ((mt * 4 + c) * 64 + lane) * 4);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(p1 + ((mt * 4 + c) * 64 + lane) * 4);
+      const u32x2 gr = *reinterpret_cast<const u32x2*>(gate + rowo + d);
+      const float gv[4] = {bf16lo(gr[0]), bf16hi(gr[0]), bf16lo(gr[1]), bf16hi(gr[1])};
+      bf16x4 ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[e] = (__bf16)(fmaf(w0[e], c0, w1[e] * c1) * inv * sigmoidf_(gv[e]));
+      *reinterpret_cast<bf16x4*>(out + rowo + d) = ov;
+    }
+  }
+}
+
 static int64_t padded_T(int64_t T) { return (T + kBN - 1) / kBN * kBN; }
 
 // Workspace: K rotated and V transposed ([B, Hkv, Tp, D] bf16 each), then the split blocks' partials
-// ([pairs][2 halves][wave] x kPartFloats fp32), then one int arrival counter per pair.
+// ([pairs][2 halves][wave] x kPartFloats fp32).
 struct PfLayout {
-  size_t part_off, cnt_off, total;
-  int64_t ncnt;
+  size_t part_off, total;
+  int64_t npairs;
 };
 static PfLayout pf_layout(int64_t B, int64_t T, int64_t Hq, int64_t Hkv) {
   const int64_t Tp = padded_T(T);
@@ -476,10 +559,9 @@ static PfLayout pf_layout(int64_t B, int64_t T, int64_t Hq, int64_t Hkv) {
   const int Ls = pf_split_len((int)nqb);
   const int64_t nsq = Ls ? nqb - 2 * Ls : 0;
   PfLayout l;
-  l.ncnt = nsq * B * Hkv * (G / GW);
+  l.npairs = nsq * B * Hkv * (G / GW);
   l.part_off = (size_t)2 * B * Hkv * Tp * kPD * sizeof(__bf16);
-  l.cnt_off = l.part_off + (size_t)2 * l.ncnt * GW * kPartFloats * sizeof(float);
-  l.total = (l.cnt_off + (size_t)l.ncnt * sizeof(int) + 255) / 256 * 256;
+  l.total = (l.part_off + (size_t)2 * l.npairs * GW * kPartFloats * sizeof(float) + 255) / 256 * 256;
   return l;
 }
 
@@ -517,18 +599,17 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
   // V^T rows are addressed with 32-bit byte offsets inside a head's [D, Tp] block
   if (Tp * kPD * 2 >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
   const PfLayout lay = pf_layout(B, T, Hq, Hkv);
-  if (lay.ncnt > 0x7fffffff) return Q35_EUNSUPPORTED;
+  if (lay.npairs > 0x7fffffff) return Q35_EUNSUPPORTED;
   if (!workspace || workspace_bytes < lay.total || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   __bf16* kr = reinterpret_cast<__bf16*>(ws);
   __bf16* vt = kr + (size_t)B * Hkv * Tp * kPD;
   float* part = reinterpret_cast<float*>(ws + lay.part_off);
-  int* cnt = reinterpret_cast<int*>(ws + lay.cnt_off);
   const dim3 gp((unsigned)(Tp / kBN), (unsigned)Hkv, (unsigned)B);
 #define Q35_KV_LAUNCH(R)                                                                                         \
   hipLaunchKernelGGL(attn_kv_prep_kernel<R>, gp, dim3(256), 0, st, (const __bf16*)k, (const __bf16*)v, cos, sin, \
-                     (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv, cnt, (int)lay.ncnt)
+                     (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv)
   switch (rot) {
     case 0: Q35_KV_LAUNCH(0); break;
     case 16: Q35_KV_LAUNCH(16); break;
@@ -540,7 +621,10 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
 #define Q35_PF_LAUNCH(GG)                                                                                         \
   hipLaunchKernelGGL(attn_prefill_kernel<GG>, dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q,    \
                      kr, vt, (const __bf16*)gate, cos, sin, (int)pos0, (__bf16*)out, (int)T, (int)Tp, (int)Hq,     \
-                     (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B, Ls, part, cnt)
+                     (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B, Ls, part);                             \
+  if (lay.npairs > 0)                                                                                             \
+    hipLaunchKernelGGL(attn_prefill_merge_kernel<GG>, dim3((unsigned)lay.npairs, GG), dim3(64), 0, st, part,       \
+                       (const __bf16*)gate, (__bf16*)out, (int)T, (int)Hq, (int)Hkv, ngroups, (int)B, Ls)
   switch (GW) {
     case 1: Q35_PF_LAUNCH(1); break;
     case 2: Q35_PF_LAUNCH(2); break;
