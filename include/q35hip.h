@@ -106,8 +106,8 @@ int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v, const flo
  *   scale is the softmax scale (HF: head_dim ** -0.5). D = 256, Hq / Hkv in {1, 2, 4, 8}.
  *   Needs q35_gated_attn_prefill_workspace_bytes(B, T, Hq, Hkv, D) bytes of workspace (256-byte aligned): the
  *   keys rotated once and the values transposed once ([B, Hkv, T rounded up to 64, D] bf16 each) and, for long
- *   sequences, the fp32 partial results and arrival counters of the query blocks whose keys are split over two
- *   work items. The workspace is overwritten by every call; calls that share one workspace must not overlap.
+ *   sequences, the fp32 partial results of the query blocks whose keys are split over two work items (combined by
+ *   a third kernel). The workspace is overwritten by every call; calls that share one workspace must not overlap.
  */
 size_t q35_gated_attn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D);
 int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const void* gate,

@@ -73,10 +73,10 @@ def test_validation_rejects_without_launching():
     # short sequence: rotated keys and transposed values only
     assert L.q35_gated_attn_prefill_workspace_bytes(1, 100, 8, 2, 256) == 2 * 2 * 128 * 256 * 2
     # T 4096: 128 query blocks, those with more than 32 key tiles (64 of them) split in two; per split block and
-    # kv head, 2 halves x 4 waves x (32 x 256 + 128) fp32 partials and one counter
+    # kv head, 2 halves x 4 waves x (32 x 256 + 128) fp32 partials
     kv = 2 * 2 * 4096 * 256 * 2
     parts = 64 * 2 * 2 * 4 * (8192 + 128) * 4
-    assert L.q35_gated_attn_prefill_workspace_bytes(1, 4096, 8, 2, 256) == kv + parts + 64 * 2 * 4
+    assert L.q35_gated_attn_prefill_workspace_bytes(1, 4096, 8, 2, 256) == kv + parts
     assert L.q35_gated_attn_prefill(fake, fake, fake, fake, fake, fake, 0, fake, 1, 100, 8, 2, 256, 64, 0.1,
                                     fake, 16, None) == 3
     assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 8, 2, 256, 128, 63, 0.1, 0,
