@@ -14,8 +14,11 @@ States are caller-owned device tensors mutated in place, as the engine's buffers
 conv_state [B, K-1, C] fp32 (the last K-1 conv inputs, oldest first, engine/model.js:333), rec_state [B, Hv, dk, dv]
 fp32, k_cache / v_cache [B, Hkv, max_len, D] bf16 holding rotated keys and values by position.
 
-The projections are one torch GEMM per mixer over the stacked input weights (cached in p under "_in_fused"); every
-other step is a HIP kernel: the GDN front end (causal conv + SiLU + gate terms), the delta rule, the gated RMSNorm,
+Any weight may also come as int8 rows with per-row scales ("<name>.q" / "<name>.s", "<name>" then holding the
+dequantised values), as the engine stores every linear (engine/model.js:3-5). The input projections are stacked into
+one weight per mixer (cached in p under "_in_fused", with "_in_fused.q" / ".s"). A projection over at most 8 rows
+(decode) is a HIP GEMV, on the int8 rows when present; over more rows a torch GEMM on the fp32 weight. Every other
+step is a HIP kernel: the GDN front end (causal conv + SiLU + gate terms), the delta rule, the gated RMSNorm,
 the attention front end (q/k norms, q/gate split, KV-cache update), the attention itself and the steering add.
 Nothing here falls back to a CPU path: the ops raise on CPU tensors and when the library is missing.
 """
@@ -67,7 +70,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     C, Vd = 2 * Hk * dk + Hv * dv, Hv * dv
     # one GEMM for every projection of the token: y row = [qkv (C) | z (Vd) | b (Hv) | a (Hv)], the engine's fused
     # layout (engine/kernels_qwen35.js:129-131)
-    y = linear(x, gdn_in_weight(p))
+    y = linear(x, gdn_in_weight(p), *_q8(p, "_in_fused"))
     q, k, v, g, beta = ops.gdn_conv(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], num_k_heads=Hk,
                                     head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=C + Vd, a_off=C + Vd + Hv,
                                     out_dtype=x.dtype)
@@ -79,35 +82,49 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
         rec_state.copy_(S)
     # gated RMSNorm: plain w, norm before the silu(z) gate (HF:168-184; engine/kernels_qwen35.js:237-243)
     o = ops.gated_rmsnorm(o, y[..., C:C + Vd], p["norm"], head_scale, eps)
-    return linear(o, p["out_proj"])
+    return linear(o, p["out_proj"], *_q8(p, "out_proj"))
 
 
-def linear(x, w):
-    """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), a torch GEMM otherwise."""
+def linear(x, w, wq=None, ws=None):
+    """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), on the int8 rows wq with per-row scales
+    ws when given (w = wq * ws, dequantised), else on w; a torch GEMM on w otherwise."""
     K = x.shape[-1]
     M = x.numel() // K
-    if M <= 8 and K % 256 == 0 and x.dtype == torch.float32 and w.dtype == torch.float32:
-        return ops.gemv(x.reshape(M, K).contiguous(), w).view(*x.shape[:-1], w.shape[0])
+    if M <= 8 and K % 256 == 0 and x.dtype == torch.float32:
+        xm = x.reshape(M, K).contiguous()
+        if wq is not None:
+            return ops.gemv(xm, wq, ws).view(*x.shape[:-1], wq.shape[0])
+        if w.dtype == torch.float32:
+            return ops.gemv(xm, w).view(*x.shape[:-1], w.shape[0])
     return x @ w.T
+
+
+def _fused(p, names):
+    """The weights `names` of p stacked into one [sum N, H] weight (cached in p under "_in_fused"), with the stacked
+    int8 rows and scales under "_in_fused.q" / "_in_fused.s" when every one has an int8 form."""
+    w = p.get("_in_fused")
+    if w is None:
+        w = torch.cat([p[n] for n in names], dim=0).contiguous()
+        p["_in_fused"] = w
+        if all(n + ".q" in p for n in names):
+            p["_in_fused.q"] = torch.cat([p[n + ".q"] for n in names], dim=0).contiguous()
+            p["_in_fused.s"] = torch.cat([p[n + ".s"] for n in names], dim=0).contiguous()
+    return w
+
+
+def _q8(p, name):
+    return p.get(name + ".q"), p.get(name + ".s")
 
 
 def gdn_in_weight(p):
     """The four input projections of a Gated DeltaNet layer stacked into one [C + Vd + 2 Hv, H] weight (cached in p
     under "_in_fused")."""
-    w = p.get("_in_fused")
-    if w is None:
-        w = torch.cat([p["in_proj_qkv"], p["in_proj_z"], p["in_proj_b"], p["in_proj_a"]], dim=0).contiguous()
-        p["_in_fused"] = w
-    return w
+    return _fused(p, ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a"))
 
 
 def attn_in_weight(p):
     """q_proj, k_proj and v_proj stacked into one [Hq 2D + 2 Hkv D, H] weight (cached in p under "_in_fused")."""
-    w = p.get("_in_fused")
-    if w is None:
-        w = torch.cat([p["q_proj"], p["k_proj"], p["v_proj"]], dim=0).contiguous()
-        p["_in_fused"] = w
-    return w
+    return _fused(p, ("q_proj", "k_proj", "v_proj"))
 
 
 def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partial_rotary_factor=0.25, eps=1e-6,
@@ -133,7 +150,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
             raise ValueError("gated_attention_layer: a multi-token call must start at position 0")
         pos_t = torch.full((B,), int(pos), dtype=torch.int32, device=x.device)
     cos, sin = rope_tables(max_len, rot, rope_theta, x.device)
-    y = linear(x, attn_in_weight(p))
+    y = linear(x, attn_in_weight(p), *_q8(p, "_in_fused"))
     q, gate, k, v = ops.attn_prep(y, p["q_norm"], p["k_norm"], cos, sin, pos_t, k_cache, v_cache, num_heads=Hq,
                                   num_kv_heads=Hkv, eps=eps, want_kv=T > 1)
     if T > 1:
@@ -142,7 +159,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
         cl = (pos_t + 1 if cache_len is None else cache_len.to(device=x.device, dtype=torch.int32))
         o = ops.gated_attention_decode(q[:, 0], k_cache, v_cache, gate[:, 0], cl, cos, sin,
                                        scale=1.0 / math.sqrt(D)).view(B, 1, Hq * D)
-    return linear(o.float(), p["o_proj"])
+    return linear(o.float(), p["o_proj"], *_q8(p, "o_proj"))
 
 
 def residual_steer_add(x, vecs, rows=None):

@@ -15,7 +15,7 @@ from . import layers, ops
 class Q35Weights:
     """Device copy of a weight dict: fp32 tensors as given; each int8 per-output-channel weight (keys "<name>.q" int8
     [N, K] and "<name>.s" fp32 [N]) both kept as int8 + scales (for the decode GEMVs) and dequantised once to fp32
-    under "<name>" (for the prefill GEMMs)."""
+    under "<name>" (for the prefill GEMMs and the embedding lookup)."""
 
     def __init__(self, W, device):
         self.t = {}
@@ -24,7 +24,7 @@ class Q35Weights:
                 base = k[:-2]
                 self.t[base] = (v.float() * W[base + ".s"][:, None]).to(device)
                 self.t[k] = v.to(device).contiguous()
-            else:
+            elif k + ".q" not in W:  # a dequantised copy given beside its int8 form is rebuilt from the int8 above
                 self.t[k] = v.to(device)
 
     def __getitem__(self, k):
@@ -199,9 +199,8 @@ class HybridModel:
     def _lm_head(self, xl):
         """Final RMSNorm and the tied-embedding logits of the last positions xl [rows, H] (a GEMV for few rows)."""
         hN = ops.add_rmsnorm_(xl.contiguous(), None, self.W["norm"], self.cfg.eps)
-        if hN.shape[0] <= 8 and hN.shape[1] % 256 == 0:
-            return ops.gemv(hN.contiguous(), self.W["embed"])
-        return hN @ self.W["embed"].T
+        wq = self.W.t.get("embed.q")
+        return layers.linear(hN.contiguous(), self.W["embed"], wq, None if wq is None else self.W["embed.s"])
 
     @torch.no_grad()
     def enable_decode_graph(self):

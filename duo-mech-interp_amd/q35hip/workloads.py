@@ -5,7 +5,8 @@
   attn_prefill:    B = 1, T = 4096, causal, 8 query / 2 kv heads, head dim 256, RoPE theta 1e7 on dims 0..63,
                    gate [T, 8 * 256].
   attn_decode:     B in {3, 32}, context 8192, same heads, bf16 KV cache, one query per row, split-K.
-  hybrid stack:    Qwen3.5-0.8B shape (Q35Config), seeded random weights (init_weights), int8 per-output-channel MLP.
+  hybrid stack:    Qwen3.5-0.8B shape (Q35Config), seeded random weights (init_weights), every linear and the
+                   tied embedding int8 per output channel as the engine quantizes them.
 q and k are L2-normalised per head, beta = sigmoid(randn), g = -softplus(randn) (log decay, alpha = exp(g)).
 """
 from dataclasses import dataclass
@@ -105,40 +106,54 @@ def quantize_rows_int8(w):
     return q, s.squeeze(1).float()
 
 
-def init_weights(cfg: Q35Config, seed=0):
+def init_weights(cfg: Q35Config, seed=0, int8_all=True):
     """Deterministic random init (seeded): normal(0, init_std) for every linear, the conv and the tied embedding;
     decoder / q / k RMSNorm weights 0 (gain 1 + w = 1) and the gated norm weight 1 (HF:171, HF:813-820);
-    dt_bias = 1; A_log = log U(0, 16). MLP weights are stored int8 per output channel with fp32 scales."""
+    dt_bias = 1; A_log = log U(0, 16).
+
+    Every linear layer and the tied embedding are int8 per output row with fp32 scales, as the engine quantizes the
+    checkpoint on load (engine/model.js:3-5, :70-100). MLP weights are stored as "<name>.q" / "<name>.s" only; the
+    other linears and the embedding (int8_all) keep "<name>.q" / "<name>.s" beside "<name>" = the dequantised fp32
+    values, so a consumer that reads "<name>" (the CPU oracle, torch GEMMs) computes with exactly the numbers the int8
+    decode GEMVs use."""
     g = torch.Generator().manual_seed(seed)
     std = cfg.init_std
 
     def lin(o, i):
         return torch.randn(o, i, generator=g) * std
 
+    def put(W, key, w):
+        if int8_all:
+            q, s = quantize_rows_int8(w)
+            W[key + ".q"], W[key + ".s"] = q, s
+            w = q.float() * s[:, None]
+        W[key] = w
+
     H = cfg.hidden
-    W = {"embed": torch.randn(cfg.vocab, H, generator=g) * std, "norm": torch.zeros(H)}
+    W = {"norm": torch.zeros(H)}
+    put(W, "embed", torch.randn(cfg.vocab, H, generator=g) * std)
     for l in range(cfg.layers):
         p = f"layers.{l}."
         W[p + "input_layernorm"] = torch.zeros(H)
         W[p + "post_attention_layernorm"] = torch.zeros(H)
         if cfg.is_attention(l):
-            W[p + "q_proj"] = lin(cfg.n_heads * cfg.head_dim * 2, H)
-            W[p + "k_proj"] = lin(cfg.n_kv * cfg.head_dim, H)
-            W[p + "v_proj"] = lin(cfg.n_kv * cfg.head_dim, H)
-            W[p + "o_proj"] = lin(H, cfg.n_heads * cfg.head_dim)
+            put(W, p + "q_proj", lin(cfg.n_heads * cfg.head_dim * 2, H))
+            put(W, p + "k_proj", lin(cfg.n_kv * cfg.head_dim, H))
+            put(W, p + "v_proj", lin(cfg.n_kv * cfg.head_dim, H))
+            put(W, p + "o_proj", lin(H, cfg.n_heads * cfg.head_dim))
             W[p + "q_norm"] = torch.zeros(cfg.head_dim)
             W[p + "k_norm"] = torch.zeros(cfg.head_dim)
         else:
             vd = cfg.lin_v_heads * cfg.lin_dv
-            W[p + "in_proj_qkv"] = lin(cfg.conv_dim, H)
-            W[p + "in_proj_z"] = lin(vd, H)
-            W[p + "in_proj_b"] = lin(cfg.lin_v_heads, H)
-            W[p + "in_proj_a"] = lin(cfg.lin_v_heads, H)
+            put(W, p + "in_proj_qkv", lin(cfg.conv_dim, H))
+            put(W, p + "in_proj_z", lin(vd, H))
+            put(W, p + "in_proj_b", lin(cfg.lin_v_heads, H))
+            put(W, p + "in_proj_a", lin(cfg.lin_v_heads, H))
             W[p + "conv1d"] = torch.randn(cfg.conv_dim, cfg.conv_k, generator=g) * std
             W[p + "dt_bias"] = torch.ones(cfg.lin_v_heads)
             W[p + "A_log"] = torch.empty(cfg.lin_v_heads).uniform_(0, 16, generator=g).log()
             W[p + "norm"] = torch.ones(cfg.lin_dv)
-            W[p + "out_proj"] = lin(H, vd)
+            put(W, p + "out_proj", lin(H, vd))
         for name, (o, i) in (("gate_proj", (cfg.inter, H)), ("up_proj", (cfg.inter, H)), ("down_proj", (H, cfg.inter))):
             q, s = quantize_rows_int8(lin(o, i))
             W[p + name + ".q"] = q
