@@ -142,7 +142,6 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     }
     __builtin_amdgcn_wave_barrier();
   };
-  // the first tile's K and V loads go out before the q prologue (they do not depend on q)
   // 1. the G query heads of this kv head, rotated at position pos, in fp32. Thread t takes quads of 4 dims
   // (qi = t, t + 256, ...); every load is unconditional (clamped indices, results selected afterwards) so that all
   // of them are issued together. rot is a multiple of 8, so no quad straddles rot or rot / 2.
@@ -166,6 +165,14 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
       }
     }
   }
+  // K / V tile registers, two sets used alternately (indices are compile-time after unrolling). Loads are issued
+  // for every tile of the span, with rows clamped into the cache, so that none sits behind a branch. The first
+  // tile's loads go out right behind the query's (which are older in the queue and return first), so that they
+  // travel while the query is rotated and laid out.
+  const int key_w = k_begin + kDecTile * wave;
+  bf16x8 kt[2][8];
+  u32x4 vt[2][kDecTile / 2];
+  tile_load(key_w, kt[0], vt[0]);
 #pragma unroll
   for (int u = 0; u < NQ; ++u) {
     const int qi = tid + 256 * u, hh = qi >> 6, d0 = 4 * (qi & 63);
@@ -198,14 +205,6 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   }
   __syncthreads();
 
-  // K / V tile registers, two sets used alternately (indices are compile-time after unrolling). Loads are issued
-  // for every tile of the span, with rows clamped into the cache, so that none sits behind a branch. The first
-  // tile's loads go out only once the query is in: issued earlier, they (and every other block's) would queue ahead
-  // of the query's loads at the memory controllers, and nothing can be computed before the query arrives.
-  const int key_w = k_begin + kDecTile * wave;
-  bf16x8 kt[2][8];
-  u32x4 vt[2][kDecTile / 2];
-  tile_load(key_w, kt[0], vt[0]);
 
   // 3. tiles key_w + 64 t, t < NT, fully unrolled: tile t + 1's loads are issued before tile t is computed. A
   // tile wholly past the span is loaded (clamped rows) but not computed: its keys carry no weight, and the rows it

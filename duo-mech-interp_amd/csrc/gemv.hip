@@ -7,11 +7,13 @@
 // silu(gate) * up, then for each push of the layer whose neuron is n or every neuron, add or multiply by the push's
 // value for the row; the row index is clamped to 3).
 //
-// Layout: a block of 4 waves takes 16 output rows; lane l works on row l / 4 and, per 64-input step (int8; 16 for
-// fp32), the 16 bytes at l % 4, so a wave load covers 16 rows x 64 contiguous bytes. The four waves split K in
-// quarters; x (M x K fp32) is staged in LDS once per block and read as broadcasts. Per-row sums: two DPP steps across
-// the 4 lanes of a row, then across the 4 waves in LDS. Epilogues: store, accumulate into y (the residual add after
-// down_proj), or SwiGLU over interleaved (gate, up) row pairs with the neuron pushes applied (gate_up_proj).
+// Layout: a block takes 16 output rows and NW = 4 or 8 waves. Lane (g, j) = (lane / 16, lane % 16) works on rows
+// g, g + 4, g + 8, g + 12 of the block and on input slot j of every K step: a K step is 16 slots of 16 weight bytes
+// (256 int8 inputs, 64 fp32), so one wave load covers 4 rows x 256 contiguous bytes, and the x values of a slot (read
+// from LDS, where x is staged once per block) serve the lane's four rows. The waves take the K steps round robin,
+// each with all of its weight loads in flight at once. Per-row sums: a 16-lane DPP row reduction, then across the
+// waves in LDS. Epilogues: store, accumulate into y (the residual add after down_proj), or SwiGLU over interleaved
+// (gate, up) row pairs with the neuron pushes applied (gate_up_proj).
 #include "q35_common.h"
 #include "q35hip.h"
 
@@ -51,95 +53,117 @@ template <> struct WChunk<float> {
   __device__ __forceinline__ float at(int i) const { return r[i]; }
 };
 
+// sum over the 16 lanes of a DPP row (lanes 16 r .. 16 r + 15), result in every lane of the row
+__device__ __forceinline__ float row16_sum_f(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  return v + dpp_f<0x140>(v);  // row_mirror
+}
+
 template <typename TW, int MP, int EPI, int U>
-__global__ __launch_bounds__(256) void gemv_kernel(const float* __restrict__ x, int64_t ldx, const TW* __restrict__ W,
+__global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, int64_t ldx, const TW* __restrict__ W,
                                                    const float* __restrict__ wscale, float* __restrict__ y,
                                                    int64_t ldy, int M, int N, int K,
                                                    const q35_push* __restrict__ pushes, int npush, int T) {
   constexpr int E = WChunk<TW>::kElems;  // weights per lane per 16-byte load
-  constexpr int STEP = 4 * E;            // inputs per step of a row (4 lanes)
+  constexpr int KS = 16 * E;             // inputs per K step
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [MP][K]
-  __shared__ float red[4][16][MP];
+  __shared__ float red[8][16][MP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane >> 2, qd = lane & 3;
-  const int n = blockIdx.x * 16 + r;
-  const TW* wrow = W + (size_t)min(n, N - 1) * K;
-  const int kq = K / 4, kb = wave * kq;
-  // U steps (U 16-byte loads per lane) in flight per iteration; the first iteration's weight loads are issued before
-  // x is staged, so that their latency covers the staging
-  WChunk<TW> wc[U];
-  auto issue = [&](int k0) {
+  const int NW = blockDim.x >> 6;
+  const int g = lane >> 4, j = lane & 15;
+  const int n0 = blockIdx.x * 16;
+  const TW* wr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) wr[r] = W + (size_t)min(n0 + g + 4 * r, N - 1) * K + j * E;
+  const int nsteps = K / KS;
+  // this wave's K steps: wave, wave + NW, ...; U of them in flight per round, the first round issued before x is
+  // staged so that its latency covers the staging
+  WChunk<TW> wc[U][4];
+  auto issue = [&](int s0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = min(k0 + u * STEP, kb + kq - STEP) + qd * E;
-      wc[u].load(wrow + k);
+      const int st = min(s0 + u * NW, nsteps - 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) wc[u][r].load(wr[r] + st * KS);
     }
   };
-  issue(kb);
+  issue(wave);
   asm volatile("" ::: "memory");
-  for (int i = tid; i < MP * K / 4; i += 256) {
+  for (int i = tid; i < MP * K / 4; i += blockDim.x) {
     const int m = (4 * i) / K, k = 4 * i - m * K;
     f32x4 v = zero4();
     if (m < M) v = *reinterpret_cast<const f32x4*>(x + m * ldx + k);
     *reinterpret_cast<f32x4*>(xs + m * K + k) = v;
   }
   __syncthreads();
-  float acc[MP];
+  float acc[4][MP];
 #pragma unroll
-  for (int m = 0; m < MP; ++m) acc[m] = 0.f;
-  for (int k0 = kb; k0 < kb + kq; k0 += U * STEP) {
-    if (k0 != kb) issue(k0);
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int m = 0; m < MP; ++m) acc[r][m] = 0.f;
+  for (int s0 = wave; s0 < nsteps; s0 += U * NW) {
+    if (s0 != wave) issue(s0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (k0 + u * STEP >= kb + kq) break;
-      const int k = k0 + u * STEP + qd * E;
+      const int st = s0 + u * NW;
+      if (st >= nsteps) break;
+      const int k = st * KS + j * E;
 #pragma unroll
-      for (int m = 0; m < MP; ++m) {
-        const float* xr = xs + m * K + k;
-        float s = 0.f;
+      for (int c = 0; c < E; c += 4) {
+        f32x4 xv[MP];
 #pragma unroll
-        for (int c = 0; c < E; c += 4) {
-          const f32x4 xv = *reinterpret_cast<const f32x4*>(xr + c);
+        for (int m = 0; m < MP; ++m) xv[m] = *reinterpret_cast<const f32x4*>(xs + m * K + k + c);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s += wc[u].at(c + e) * xv[e];
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float wv = wc[u][r].at(c + e);
+#pragma unroll
+            for (int m = 0; m < MP; ++m) acc[r][m] += wv * xv[m][e];
+          }
         }
-        acc[m] += s;
       }
     }
   }
-  // the 4 lanes of a row (a quad): quad_perm [1,0,3,2] then [2,3,0,1]
 #pragma unroll
-  for (int m = 0; m < MP; ++m) {
-    acc[m] += dpp_f<0xB1>(acc[m]);
-    acc[m] += dpp_f<0x4E>(acc[m]);
-  }
-  if (qd == 0) {
+  for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int m = 0; m < MP; ++m) red[wave][r][m] = acc[m];
+    for (int m = 0; m < MP; ++m) acc[r][m] = row16_sum_f(acc[r][m]);
+  if (j == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int m = 0; m < MP; ++m) red[wave][g + 4 * r][m] = acc[r][m];
   }
   __syncthreads();
+  auto rowsum = [&](int rr, int m) {
+    float v = 0.f;
+    for (int w = 0; w < NW; ++w) v += red[w][rr][m];
+    return v;
+  };
   if (EPI != kEpiSwiglu) {
     if (tid < 16 * MP) {
       const int rr = tid / MP, m = tid - rr * MP;
-      const int nn = blockIdx.x * 16 + rr;
+      const int nn = n0 + rr;
       if (m < M && nn < N) {
-        float v = red[0][rr][m] + red[1][rr][m] + red[2][rr][m] + red[3][rr][m];
+        float v = rowsum(rr, m);
         if (wscale) v *= wscale[nn];
         float* dst = y + m * ldy + nn;
         *dst = EPI == kEpiAccumulate ? *dst + v : v;
       }
     }
   } else {
-    // rows 2 j and 2 j + 1 of the block are gate and up of neuron blockIdx.x * 8 + j
+    // rows 2 q and 2 q + 1 of the block are gate and up of neuron blockIdx.x * 8 + q
     if (tid < 8 * MP) {
-      const int j = tid / MP, m = tid - j * MP;
-      const int ng = blockIdx.x * 16 + 2 * j;
+      const int qn = tid / MP, m = tid - qn * MP;
+      const int ng = n0 + 2 * qn;
       const int neuron = ng >> 1;
       if (m < M && ng + 1 < N) {
-        float g = red[0][2 * j][m] + red[1][2 * j][m] + red[2][2 * j][m] + red[3][2 * j][m];
-        float u = red[0][2 * j + 1][m] + red[1][2 * j + 1][m] + red[2][2 * j + 1][m] + red[3][2 * j + 1][m];
-        if (wscale) { g *= wscale[ng]; u *= wscale[ng + 1]; }
-        float a = gsilu(g) * u;
+        float gt = rowsum(2 * qn, m), up = rowsum(2 * qn + 1, m);
+        if (wscale) { gt *= wscale[ng]; up *= wscale[ng + 1]; }
+        float a = gsilu(gt) * up;
         const int row = min(m / T, 3);
         for (int p = 0; p < npush; ++p) a = apply_push(pushes + p, neuron, row, a);
         y[m * ldy + neuron] = a;
@@ -167,35 +191,38 @@ __global__ __launch_bounds__(256) void swiglu_push_kernel(const float* __restric
 namespace {
 template <typename TW, int EPI, int U>
 void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
-                   int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, hipStream_t st) {
+                   int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, int nw, hipStream_t st) {
   using namespace q35;
-  const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 3 ? 3 : M <= 4 ? 4 : 8;
   const size_t lds = (size_t)mp * K * sizeof(float);
-  const dim3 grid((unsigned)((N + 15) / 16)), block(256);
+  const dim3 grid((unsigned)((N + 15) / 16)), block(64 * nw);
 #define Q35_GEMV(MP)                                                                                                  \
   hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U>), grid, block, lds, st, x, ldx, W, wscale, y, ldy, (int)M,      \
                      (int)N, (int)K, pushes, npush, (int)T)
   switch (mp) {
     case 1: Q35_GEMV(1); break;
     case 2: Q35_GEMV(2); break;
+    case 3: Q35_GEMV(3); break;
     case 4: Q35_GEMV(4); break;
     default: Q35_GEMV(8); break;
   }
 #undef Q35_GEMV
 }
 
-// steps of a wave's K quarter: all in flight at once up to 16
+// 4 waves when K has at most 4 steps, else 8; each wave's steps all in flight at once up to 4
 template <typename TW, int EPI>
 int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
                 int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, hipStream_t st) {
   using namespace q35;
-  const int64_t steps = K / 4 / (4 * WChunk<TW>::kElems);
-  if (steps <= 4)
-    gemv_launch_u<TW, EPI, 4>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, st);
-  else if (steps <= 8)
-    gemv_launch_u<TW, EPI, 8>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, st);
+  const int64_t steps = K / (16 * WChunk<TW>::kElems);
+  const int nw = steps <= 4 ? 4 : 8;
+  const int64_t per_wave = (steps + nw - 1) / nw;
+  if (per_wave <= 1)
+    gemv_launch_u<TW, EPI, 1>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, st);
+  else if (per_wave <= 2)
+    gemv_launch_u<TW, EPI, 2>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, st);
   else
-    gemv_launch_u<TW, EPI, 16>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, st);
+    gemv_launch_u<TW, EPI, 4>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, st);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 }  // namespace
@@ -210,7 +237,7 @@ extern "C" int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype,
   if (epilogue != kEpiStore && epilogue != kEpiAccumulate && epilogue != kEpiSwiglu) return Q35_EINVAL;
   if (w_dtype != Q35_I8 && w_dtype != Q35_F32) return Q35_EUNSUPPORTED;
   if (M > 8 || (K % 256) != 0 || (ldx & 3) || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return Q35_EUNSUPPORTED;
-  const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 3 ? 3 : M <= 4 ? 4 : 8;
   if ((int64_t)mp * K * 4 > 64 * 1024 || N > 0x7fffffff || npush > 64) return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int np = (int)npush;
