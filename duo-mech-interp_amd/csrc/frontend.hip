@@ -1,7 +1,7 @@
 // The per-layer work around the two mixers, as HBM-bound passes over the fused projection output y (one GEMM per
 // layer produces every projection of a token as one row of y):
 //
-//   gdn_conv_kernel        Gated DeltaNet front end (HF:454-499; WGSL conv / convState, engine/kernels_qwen35.js
+//   gdn_conv_kernel        (and gdn_conv1_kernel, its T = 1 form) Gated DeltaNet front end (HF:454-499; WGSL conv / convState, engine/kernels_qwen35.js
 //                          :127-178, and the gate terms of `delta`, :226-229): causal depthwise conv (K taps, carried
 //                          state of the previous K-1 inputs) + SiLU over the q|k|v channels of y, split into dense
 //                          q, k [B, T, Hk, dk] and v [B, T, Hv, dv]; beta = sigmoid(b), g = -exp(A_log) *
@@ -111,6 +111,67 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__
       if (j >= K - 1) break;
       *reinterpret_cast<f32x4*>(st + (size_t)j * C + c) = nv[j];
     }
+  }
+}
+
+// T = 1 (the decode step): one thread per (row b, quad of 4 channels). Every load of the thread (taps, bias, the
+// K-1 state rows, the input) is issued before any is used, and the thread owns its quad's state, so there is no
+// barrier: one memory round trip. Block x == nb computes the gate terms of row b.
+template <typename Tout>
+__global__ __launch_bounds__(256) void gdn_conv1_kernel(const float* __restrict__ y, int64_t ldy,
+                                                        const float* __restrict__ cw, const float* __restrict__ cbias,
+                                                        float* __restrict__ cstate, const float* __restrict__ A_log,
+                                                        const float* __restrict__ dt_bias, int b_off, int a_off,
+                                                        Tout* __restrict__ qo, Tout* __restrict__ ko,
+                                                        Tout* __restrict__ vo, float* __restrict__ go,
+                                                        float* __restrict__ betao, int C, int Kd, int Vd, int Hv,
+                                                        int K) {
+  const int b = blockIdx.y, tid = threadIdx.x;
+  const int nb = (C / 4 + 255) / 256;
+  const float* row = y + (int64_t)b * ldy;
+  if ((int)blockIdx.x == nb) {
+    for (int h = tid; h < Hv; h += 256) {
+      betao[(size_t)b * Hv + h] = 1.f / (1.f + __expf(-row[b_off + h]));
+      go[(size_t)b * Hv + h] = -__expf(A_log[h]) * softplus_f(row[a_off + h] + dt_bias[h]);
+    }
+    return;
+  }
+  const int c = 4 * (blockIdx.x * 256 + tid);
+  if (c >= C) return;
+  float w[4][kConvMaxK];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int i = 0; i < kConvMaxK; ++i) w[e][i] = i < K ? cw[(size_t)(c + e) * K + i] : 0.f;
+  const f32x4 bias = cbias ? *reinterpret_cast<const f32x4*>(cbias + c) : zero4();
+  float* st = cstate + (size_t)b * (K - 1) * C;
+  f32x4 sx[kConvMaxK - 1];
+#pragma unroll
+  for (int j = 0; j < kConvMaxK - 1; ++j) sx[j] = j < K - 1 ? *reinterpret_cast<const f32x4*>(st + (size_t)j * C + c)
+                                                           : zero4();
+  const f32x4 xin = *reinterpret_cast<const f32x4*>(row + c);
+  // tap i reads state row i for i < K - 1 and the input for i = K - 1
+  f32x4 acc = bias;
+#pragma unroll
+  for (int i = 0; i < kConvMaxK; ++i) {
+    if (i >= K) break;
+    const f32x4 x = i < K - 1 ? sx[i] : xin;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += w[e][i] * x[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = silu_f(acc[e]);
+  Tout* dst;
+  int dstride, dcol;
+  if (c < Kd) { dst = qo; dstride = Kd; dcol = c; }
+  else if (c < 2 * Kd) { dst = ko; dstride = Kd; dcol = c - Kd; }
+  else { dst = vo; dstride = Vd; dcol = c - 2 * Kd; }
+  store4<Tout>(dst + (size_t)b * dstride + dcol, acc);
+  // state <- [old rows 1 .. K-2 | input]
+#pragma unroll
+  for (int j = 0; j < kConvMaxK - 1; ++j) {
+    if (j >= K - 1) break;
+    *reinterpret_cast<f32x4*>(st + (size_t)j * C + c) = j + 1 < K - 1 ? sx[j + 1] : xin;
   }
 }
 
@@ -286,6 +347,20 @@ extern "C" int q35_gdn_conv(const float* y, int64_t ldy, const float* conv_w, co
   if (B > 65535 || B * T * ldy > ((int64_t)1 << 40) || T * Hv > 0x7fffffff || C > 0x7fffffff)
     return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (T == 1) {  // decode: one thread per channel quad
+    const dim3 g1((unsigned)((C / 4 + 255) / 256 + 1), (unsigned)B);
+    if (dtype == Q35_F32)
+      hipLaunchKernelGGL(gdn_conv1_kernel<float>, g1, dim3(256), 0, st, y, ldy, conv_w, conv_bias, conv_state, A_log,
+                         dt_bias, (int)b_off, (int)a_off, (float*)q, (float*)k, (float*)v, g, beta, (int)C, (int)Kd,
+                         (int)Vd, (int)Hv, (int)K);
+    else if (dtype == Q35_BF16)
+      hipLaunchKernelGGL(gdn_conv1_kernel<__bf16>, g1, dim3(256), 0, st, y, ldy, conv_w, conv_bias, conv_state,
+                         A_log, dt_bias, (int)b_off, (int)a_off, (__bf16*)q, (__bf16*)k, (__bf16*)v, g, beta, (int)C,
+                         (int)Kd, (int)Vd, (int)Hv, (int)K);
+    else
+      return Q35_EUNSUPPORTED;
+    return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+  }
   const dim3 grid((unsigned)((C + kConvCh - 1) / kConvCh + 1), (unsigned)B);
   if (dtype == Q35_F32)
     hipLaunchKernelGGL(gdn_conv_kernel<float>, grid, dim3(256), 0, st, y, ldy, conv_w, conv_bias, conv_state, A_log,

@@ -156,7 +156,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     if T > 1:
         o = ops.gated_attention_prefill(q, k, v, gate, cos, sin, pos0=0, scale=1.0 / math.sqrt(D))
     else:
-        cl = (pos_t + 1 if cache_len is None else cache_len.to(device=x.device, dtype=torch.int32))
+        cl = pos_t + 1 if cache_len is None else cache_len
         o = ops.gated_attention_decode(q[:, 0], k_cache, v_cache, gate[:, 0], cl, cos, sin,
                                        scale=1.0 / math.sqrt(D)).view(B, 1, Hq * D)
     return linear(o.float(), p["o_proj"], *_q8(p, "o_proj"))

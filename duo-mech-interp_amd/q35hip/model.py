@@ -159,12 +159,14 @@ class HybridModel:
         cfg = self.cfg
         collected = None
         y = None  # the previous mixer's output, added to x by the next norm
+        cache_len = self.pos_dev + 1 if T == 1 else None  # decode: once per step, shared by the attention layers
         for l in range(last + 1):
             p, st = self.params[l], self.states[l]
             h = ops.add_rmsnorm_(x, y, p["input_layernorm"], cfg.eps)
             if cfg.is_attention(l):
                 y = layers.gated_attention_layer(h, p, st["k"], st["v"], self.pos_dev, rope_theta=cfg.rope_theta,
-                                                 partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps)
+                                                 partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps,
+                                                 cache_len=cache_len)
             else:
                 y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
                                                 head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill)
@@ -187,7 +189,7 @@ class HybridModel:
             raise ValueError("context exceeds the KV cache")
         if T > 1 and self.pos != 0:
             raise ValueError("HybridModel: a multi-token call must start the sequence (positions 0..T-1)")
-        x = W["embed"][ids.to(self.device)].contiguous()
+        x = W["embed"][ids.to(self.device).long()].contiguous()
         last = cfg.layers - 1 if stop_after is None else stop_after
         x, collected = self._layers(x, T, last, collect_layer, self.steering)
         self.pos_dev.add_(T)
@@ -204,36 +206,44 @@ class HybridModel:
 
     @torch.no_grad()
     def enable_decode_graph(self):
-        """Capture one decode step (ids [rows, 1] -> logits) in a HIP graph; decode_step() then replays it. Must be
-        called at the start of a sequence: the warm-up runs real steps, and the states are reset afterwards. The
-        steering add is always part of the graph (rows without a vector are skipped by the kernel)."""
+        """Capture one decode step in a HIP graph: ids [rows] int32 (self._g_ids) -> logits, then the device argmax of
+        the logits written back into self._g_ids, so that replaying the graph again continues greedy decoding with no
+        host work (the engine's decode loop, engine/model.js:494-497). decode_step() and decode_greedy() replay it.
+        Must be called at the start of a sequence: the warm-up runs real steps, and the states are reset afterwards.
+        The steering add is always part of the graph (rows without a vector are skipped by the kernel)."""
         cfg = self.cfg
         self.reset()
-        self._g_ids = torch.zeros(self.rows, 1, dtype=torch.long, device=self.device)
+        self._g_ids = torch.zeros(self.rows, dtype=torch.int32, device=self.device)
+
+        def step():
+            x, _ = self._layers(self.W["embed"].index_select(0, self._g_ids).unsqueeze(1), 1, cfg.layers - 1, None,
+                                True)
+            self.pos_dev.add_(1)
+            logits = self._lm_head(x[:, -1])
+            ops.argmax_rows(logits, out=self._g_ids)
+            return logits
         side = torch.cuda.Stream(device=self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side):  # warm-up outside capture: library handles, allocator pools
             for _ in range(2):
-                x, _ = self._layers(self.W["embed"][self._g_ids].contiguous(), 1, cfg.layers - 1, None, True)
-                self.pos_dev.add_(1)
+                step()
         torch.cuda.current_stream(self.device).wait_stream(side)
         torch.cuda.synchronize(self.device)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            x, _ = self._layers(self.W["embed"][self._g_ids].contiguous(), 1, cfg.layers - 1, None, True)
-            self.pos_dev.add_(1)
-            self._g_logits = self._lm_head(x[:, -1])
+            self._g_logits = step()
         self.graph = g
         torch.cuda.synchronize(self.device)
         self.reset()
+        self._g_ids.zero_()
 
     @torch.no_grad()
     def decode_step(self, ids):
-        """One greedy step for every row: ids [rows] or [rows, 1]. Replays the captured graph when there is one (the
-        returned logits then live in the graph's output buffer, overwritten by the next step), else runs forward."""
-        ids = ids.reshape(self.rows, 1)
+        """One step for every row: ids [rows] or [rows, 1]. Replays the captured graph when there is one (the returned
+        logits then live in the graph's output buffer, overwritten by the next step), else runs forward."""
+        ids = ids.reshape(self.rows)
         if self.graph is None:
-            return self.forward(ids)[0]
+            return self.forward(ids.reshape(self.rows, 1))[0]
         if self.pos + 1 > self.max_len:
             raise ValueError("context exceeds the KV cache")
         self._g_ids.copy_(ids)
@@ -241,17 +251,30 @@ class HybridModel:
         self.pos += 1
         return self._g_logits
 
+    @torch.no_grad()
+    def decode_greedy(self):
+        """One greedy step continuing from the last one (graph mode): replays the graph on the token ids the previous
+        step's device argmax left in self._g_ids. Returns (logits, next ids [rows] int32), both graph buffers."""
+        if self.graph is None:
+            raise ValueError("decode_greedy needs enable_decode_graph()")
+        if self.pos + 1 > self.max_len:
+            raise ValueError("context exceeds the KV cache")
+        self.graph.replay()
+        self.pos += 1
+        return self._g_logits, self._g_ids
+
 
 @torch.no_grad()
 def greedy(model, prompt_ids, steps):
-    """Prefill prompt_ids [B, T], then `steps` greedy tokens (argmax, lowest index on ties, as torch.argmax and the
-    WGSL argmax of engine/kernels.js:261-284). Returns (tokens [B, steps], top-2 margins [B, steps]) on the CPU."""
+    """Prefill prompt_ids [B, T], then `steps` greedy tokens (the device argmax: lowest index on ties, as torch.argmax
+    and the WGSL argmax of engine/kernels.js:260-283). Returns (tokens [B, steps], top-2 margins [B, steps]) on the
+    CPU."""
     logits, _ = model.forward(prompt_ids)
     toks, margins = [], []
     for _ in range(steps):
         top2 = logits.topk(2, dim=-1)
-        nxt = logits.argmax(dim=-1)
-        toks.append(nxt)
+        nxt = ops.argmax_rows(logits)
+        toks.append(nxt.long())
         margins.append(top2.values[:, 0] - top2.values[:, 1])
         logits = model.decode_step(nxt)
     return torch.stack(toks, 1).cpu(), torch.stack(margins, 1).cpu()

@@ -70,6 +70,7 @@ _LIB.define("gated_rmsnorm(Tensor o, Tensor z, Tensor w, Tensor? head_scale, flo
 _LIB.define("gemv_(Tensor x, Tensor W, Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
 _LIB.define("swiglu_push(Tensor gu, Tensor? pushes, int T) -> Tensor")
 _LIB.define("add_rmsnorm_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tensor")
+_LIB.define("argmax_rows_(Tensor x, Tensor(a!) idx) -> ()")
 _LIB.define("attn_prep(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, Tensor cos, Tensor sin, Tensor pos, "
             "Tensor(a!) k_cache, Tensor(b!) v_cache, int Hq, int Hkv, bool want_kv) "
             "-> (Tensor, Tensor, Tensor, Tensor)")
@@ -328,6 +329,14 @@ def _add_rmsnorm_impl(x, y, w, eps):
     return h
 
 
+def _argmax_rows_impl(x, idx):
+    _on_gpu(x, idx)
+    _require(x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1, "x: [rows, n] fp32, rows dense")
+    _require(idx.dtype == torch.int32 and idx.is_contiguous() and idx.numel() == x.shape[0], "idx: [rows] int32")
+    st = _lib.lib().q35_argmax_rows(_ptr(x), x.stride(0), x.shape[0], x.shape[1], _ptr(idx), None, _stream(x))
+    check(st, "q35_argmax_rows")
+
+
 def _no_cpu(name):
     def f(*args, **kwargs):
         raise Q35Error(f"q35hip: q35::{name} needs HIP device tensors; the product has no CPU path")
@@ -339,7 +348,7 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
                      ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl),
                      ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
-                     ("add_rmsnorm_", _add_rmsnorm_impl)]:
+                     ("add_rmsnorm_", _add_rmsnorm_impl), ("argmax_rows_", _argmax_rows_impl)]:
     _LIB.impl(_name, _impl, "CUDA")
     _LIB.impl(_name, _no_cpu(_name), "CPU")
 
@@ -361,6 +370,7 @@ _LIB.impl("gated_attn_decode",
           lambda q, kc, vc, gate, cl, cos, sin, scale, splits: q.new_empty(q.shape[0], q.shape[1] * q.shape[2]),
           "Meta")
 _LIB.impl("resid_add_rows_", lambda x, vecs, vor: None, "Meta")
+_LIB.impl("argmax_rows_", lambda x, idx: None, "Meta")
 
 
 # ---------------------------------------------------------------- Python entry points (reference signatures)
@@ -477,6 +487,16 @@ def swiglu_push(gu, pushes=None, T=1):
     """silu(gate) * up over a [..., 2 I] ([gate | up]) projection with the neuron pushes applied (the hook point of
     engine/kernels_qwen35.js:250-279)."""
     return torch.ops.q35.swiglu_push(gu, pushes, int(T))
+
+
+def argmax_rows(x, out=None):
+    """Per-row argmax of x [rows, n] fp32 (lowest index on ties, as torch.argmax and the engine's WGSL argmax,
+    engine/kernels.js:260-283) into out ([rows] int32, allocated when None). Returns out."""
+    x = x if x.stride(-1) == 1 else x.contiguous()
+    if out is None:
+        out = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)
+    torch.ops.q35.argmax_rows_(x, out)
+    return out
 
 
 def add_rmsnorm_(x, y, w, eps=1e-6):

@@ -27,6 +27,7 @@
  *   q35_swiglu_push          engine/kernels_qwen35.js:250-279 `swiglu` over a [gate | up] projection (prefill form)
  *   q35_add_rmsnorm          HF:720-734 Qwen3_5RMSNorm (1 + w) with the residual add before it (HF:753-793);
  *                            engine/kernels.js:226-246 `rmsnorm` (OFFSET) and `addInto`
+ *   q35_argmax_rows          engine/kernels.js:260-283 `argmax` (greedy token of each row, engine/model.js:494-497)
  */
 #ifndef Q35HIP_H
 #define Q35HIP_H
@@ -212,6 +213,14 @@ int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const floa
  */
 int q35_swiglu_push(const float* gu, float* a, int64_t M, int64_t I, const q35_push* pushes, int64_t npush,
                     int64_t T, q35_stream_t stream);
+
+/*
+ * Per-row argmax (greedy sampling): idx[r] = the lowest index of the largest value of x[r, 0:n] (the WGSL `argmax`,
+ * engine/kernels.js:260-283; torch.argmax's rule), val[r] that value (val may be NULL). A row of -inf gives index 0.
+ *   x: [rows, ldx] fp32 (rows need no alignment beyond 4 bytes). idx: [rows] int32.
+ */
+int q35_argmax_rows(const float* x, int64_t ldx, int64_t rows, int64_t n, int32_t* idx, float* val,
+                    q35_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,7 @@ def test_header_declares_the_boundary():
     names = declared_functions()
     for n in ["q35_gdn_recurrent", "q35_gdn_chunk_prefill", "q35_gated_attn_prefill", "q35_gated_attn_decode",
               "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
-              "q35_swiglu_push", "q35_add_rmsnorm"]:
+              "q35_swiglu_push", "q35_add_rmsnorm", "q35_argmax_rows"]:
         assert n in names
 
 
@@ -105,6 +105,9 @@ def test_validation_rejects_without_launching():
     assert L.q35_swiglu_push(fake, fake, 3, 64, None, 2, 1, None) == 1
     assert L.q35_add_rmsnorm(fake, 1024, None, 0, fake, fake, 1024, 3, 1022, 1e-6, None) == 2
     assert L.q35_add_rmsnorm(fake, 512, None, 0, fake, fake, 1024, 3, 1024, 1e-6, None) == 1
+    # argmax: ld shorter than the row, no rows
+    assert L.q35_argmax_rows(fake, 100, 3, 101, fake, None, None) == 1
+    assert L.q35_argmax_rows(fake, 100, 0, 100, fake, None, None) == 1
 
 
 def test_decode_workspace_scales_with_splits():

@@ -75,6 +75,30 @@ def test_gdn_conv_bias_and_split_calls():
     assert torch.equal(st.cpu(), ref[5])
 
 
+def test_gdn_conv_single_token_steps_carry_the_state():
+    """Six one-token calls (the decode form, its own kernel) equal one six-token call, bias included, for both
+    output dtypes; the carried state ends identical."""
+    dev = device()
+    B, Hk, dk, Hv, dv = 3, 16, 128, 16, 128
+    y, conv_w, state, A_log, dt_bias, C, W = _gdn_case(B, 6, seed=44)
+    bias = torch.randn(C, generator=torch.Generator().manual_seed(45))
+    b_off, a_off = C + Hv * dv, C + Hv * dv + Hv
+    ref = of.gdn_conv(y, conv_w, state, A_log, dt_bias, Hk, dk, Hv, dv, b_off, a_off, conv_bias=bias)
+    kw = dict(num_k_heads=Hk, head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=b_off, a_off=a_off)
+    for dtype in (torch.float32, torch.bfloat16):
+        announce(f"gdn_conv one-token steps {dtype}")
+        st = state.to(dev)
+        yd = y.to(dev)
+        outs = [ops.gdn_conv(yd[:, t:t + 1].contiguous(), conv_w.to(dev), st, A_log.to(dev), dt_bias.to(dev),
+                             conv_bias=bias.to(dev), out_dtype=dtype, **kw) for t in range(6)]
+        torch.cuda.synchronize()
+        tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+        for i in range(5):
+            got = torch.cat([o[i] for o in outs], dim=1).float().cpu()
+            assert oracle.rel_err(got, ref[i]) <= (tol if i < 3 else TOL_F32)
+        assert torch.equal(st.cpu(), ref[5])
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("with_scale", [False, True])
 def test_gated_rmsnorm_matches_oracle(dtype, with_scale):

@@ -61,3 +61,22 @@ def test_gemv_swiglu_with_pushes_and_prefill_form(M, T):
     torch.cuda.synchronize()
     assert oracle.rel_err(a.cpu(), ref) <= TOL
     assert oracle.rel_err(a2.cpu(), ref) <= TOL
+
+
+@pytest.mark.parametrize("rows,n", [(1, 151936), (3, 151936), (2, 1000), (5, 4099)])
+def test_argmax_rows_matches_torch(rows, n):
+    """Device argmax (engine/kernels.js:260-283) against torch.argmax, with planted ties (the lowest index wins) and
+    rows of -inf."""
+    dev = device()
+    g = torch.Generator().manual_seed(n + rows)
+    x = torch.randn(rows, n, generator=g)
+    x[0, 7] = x[0, n - 2] = x[0].max() + 1.0          # a tie: index 7 must win
+    if rows > 1:
+        x[1] = -float("inf")                          # all -inf: index 0
+    if rows > 2:
+        x[2, n - 1] = 1e30                            # the last element (a tail element when n % 4 != 0)
+    announce(f"argmax rows{rows} n{n}")
+    got = ops.argmax_rows(x.to(dev))
+    torch.cuda.synchronize()
+    assert got.dtype == torch.int32
+    assert torch.equal(got.cpu().long(), x.argmax(-1))
