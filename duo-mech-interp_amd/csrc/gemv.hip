@@ -61,11 +61,15 @@ __device__ __forceinline__ float row16_sum_f(float v) {
   return v + dpp_f<0x140>(v);  // row_mirror
 }
 
-template <typename TW, int MP, int EPI, int U>
+// NORM: x is a residual row; the kernel adds xadd (may be NULL), writes the sum to xout from block 0 (may be NULL),
+// and multiplies the RMSNorm of the sum, s * rsqrt(mean s^2 + eps) * (1 + nw), instead of x (HF:720-734).
+template <typename TW, int MP, int EPI, int U, bool NORM>
 __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, int64_t ldx, const TW* __restrict__ W,
                                                    const float* __restrict__ wscale, float* __restrict__ y,
                                                    int64_t ldy, int M, int N, int K,
-                                                   const q35_push* __restrict__ pushes, int npush, int T) {
+                                                   const q35_push* __restrict__ pushes, int npush, int T,
+                                                   const float* __restrict__ xadd, const float* __restrict__ nw,
+                                                   float eps, float* __restrict__ xout) {
   constexpr int E = WChunk<TW>::kElems;  // weights per lane per 16-byte load
   constexpr int KS = 16 * E;             // inputs per K step
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [MP][K]
@@ -94,10 +98,42 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
   for (int i = tid; i < MP * K / 4; i += blockDim.x) {
     const int m = (4 * i) / K, k = 4 * i - m * K;
     f32x4 v = zero4();
-    if (m < M) v = *reinterpret_cast<const f32x4*>(x + m * ldx + k);
+    if (m < M) {
+      v = *reinterpret_cast<const f32x4*>(x + m * ldx + k);
+      if (NORM && xadd) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(xadd + m * ldx + k);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += a[e];
+      }
+      if (NORM && xout && blockIdx.x == 0) *reinterpret_cast<f32x4*>(xout + m * ldx + k) = v;
+    }
     *reinterpret_cast<f32x4*>(xs + m * K + k) = v;
   }
   __syncthreads();
+  if (NORM) {
+    // mean of squares per row m: wave w sums rows w, w + NW, ... over K, then every thread rescales its elements
+    __shared__ float rs[MP];
+    for (int m = wave; m < MP; m += NW) {
+      float ss = 0.f;
+      for (int k = 4 * lane; k < K; k += 256) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(xs + m * K + k);
+        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      if (lane == 0) rs[m] = rsqrtf(ss / (float)K + eps);
+    }
+    __syncthreads();
+    for (int i = tid; i < MP * K / 4; i += blockDim.x) {
+      const int m = (4 * i) / K, k = 4 * i - m * K;
+      f32x4 v = *reinterpret_cast<const f32x4*>(xs + m * K + k);
+      const f32x4 w = *reinterpret_cast<const f32x4*>(nw + k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = v[e] * rs[m] * (1.f + w[e]);
+      *reinterpret_cast<f32x4*>(xs + m * K + k) = v;
+    }
+    __syncthreads();
+  }
   float acc[4][MP];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
@@ -189,16 +225,24 @@ __global__ __launch_bounds__(256) void swiglu_push_kernel(const float* __restric
 }  // namespace q35
 
 namespace {
-template <typename TW, int EPI, int U>
+struct NormArgs {
+  const float* xadd;
+  const float* nw;
+  float eps;
+  float* xout;
+};
+
+template <typename TW, int EPI, int U, bool NORM>
 void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
-                   int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, int nw, hipStream_t st) {
+                   int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, int nw, const NormArgs& na,
+                   hipStream_t st) {
   using namespace q35;
   const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 3 ? 3 : M <= 4 ? 4 : 8;
   const size_t lds = (size_t)mp * K * sizeof(float);
   const dim3 grid((unsigned)((N + 15) / 16)), block(64 * nw);
-#define Q35_GEMV(MP)                                                                                                  \
-  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U>), grid, block, lds, st, x, ldx, W, wscale, y, ldy, (int)M,      \
-                     (int)N, (int)K, pushes, npush, (int)T)
+#define Q35_GEMV(MP)                                                                                                 \
+  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM>), grid, block, lds, st, x, ldx, W, wscale, y, ldy, (int)M, \
+                     (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps, na.xout)
   switch (mp) {
     case 1: Q35_GEMV(1); break;
     case 2: Q35_GEMV(2); break;
@@ -210,26 +254,43 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
 }
 
 // 4 waves when K has at most 4 steps, else 8; each wave's steps all in flight at once up to 4
-template <typename TW, int EPI>
+template <typename TW, int EPI, bool NORM>
 int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
-                int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, hipStream_t st) {
+                int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, const NormArgs& na,
+                hipStream_t st) {
   using namespace q35;
   const int64_t steps = K / (16 * WChunk<TW>::kElems);
   const int nw = steps <= 4 ? 4 : 8;
   const int64_t per_wave = (steps + nw - 1) / nw;
   if (per_wave <= 1)
-    gemv_launch_u<TW, EPI, 1>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, st);
+    gemv_launch_u<TW, EPI, 1, NORM>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
   else if (per_wave <= 2)
-    gemv_launch_u<TW, EPI, 2>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, st);
+    gemv_launch_u<TW, EPI, 2, NORM>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
   else
-    gemv_launch_u<TW, EPI, 4>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, st);
+    gemv_launch_u<TW, EPI, 4, NORM>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
-}  // namespace
 
-extern "C" int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y,
-                        int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
-                        int64_t npush, int64_t T, q35_stream_t stream) {
+template <bool NORM>
+int gemv_dispatch(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y,
+                  int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int np,
+                  int64_t T, const NormArgs& na, hipStream_t st) {
+  using namespace q35;
+  if (w_dtype == Q35_I8) {
+    const int8_t* w8 = (const int8_t*)W;
+    if (epilogue == kEpiStore) return gemv_launch<int8_t, kEpiStore, NORM>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+    if (epilogue == kEpiAccumulate) return gemv_launch<int8_t, kEpiAccumulate, NORM>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+    return gemv_launch<int8_t, kEpiSwiglu, NORM>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+  }
+  const float* wf = (const float*)W;
+  if (epilogue == kEpiStore) return gemv_launch<float, kEpiStore, NORM>(x, ldx, wf, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+  if (epilogue == kEpiAccumulate) return gemv_launch<float, kEpiAccumulate, NORM>(x, ldx, wf, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+  return gemv_launch<float, kEpiSwiglu, NORM>(x, ldx, wf, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+}
+
+// argument checks shared by the two entry points
+int gemv_check(const float* x, int64_t ldx, const void* W, int w_dtype, float* y, int64_t ldy, int64_t M, int64_t N,
+               int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T) {
   using namespace q35;
   if (!x || !W || !y || M <= 0 || N <= 0 || K <= 0 || ldx < K || T <= 0) return Q35_EINVAL;
   if (npush < 0 || (npush > 0 && !pushes)) return Q35_EINVAL;
@@ -239,16 +300,37 @@ extern "C" int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype,
   if (M > 8 || (K % 256) != 0 || (ldx & 3) || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return Q35_EUNSUPPORTED;
   const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 3 ? 3 : M <= 4 ? 4 : 8;
   if ((int64_t)mp * K * 4 > 64 * 1024 || N > 0x7fffffff || npush > 64) return Q35_EUNSUPPORTED;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int np = (int)npush;
-  if (w_dtype == Q35_I8) {
-    if (epilogue == kEpiStore) return gemv_launch<int8_t, kEpiStore>(x, ldx, (const int8_t*)W, w_scale, y, ldy, M, N, K, pushes, np, T, st);
-    if (epilogue == kEpiAccumulate) return gemv_launch<int8_t, kEpiAccumulate>(x, ldx, (const int8_t*)W, w_scale, y, ldy, M, N, K, pushes, np, T, st);
-    return gemv_launch<int8_t, kEpiSwiglu>(x, ldx, (const int8_t*)W, w_scale, y, ldy, M, N, K, pushes, np, T, st);
-  }
-  if (epilogue == kEpiStore) return gemv_launch<float, kEpiStore>(x, ldx, (const float*)W, w_scale, y, ldy, M, N, K, pushes, np, T, st);
-  if (epilogue == kEpiAccumulate) return gemv_launch<float, kEpiAccumulate>(x, ldx, (const float*)W, w_scale, y, ldy, M, N, K, pushes, np, T, st);
-  return gemv_launch<float, kEpiSwiglu>(x, ldx, (const float*)W, w_scale, y, ldy, M, N, K, pushes, np, T, st);
+  return Q35_OK;
+}
+}  // namespace
+
+extern "C" int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y,
+                        int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
+                        int64_t npush, int64_t T, q35_stream_t stream) {
+  const int chk = gemv_check(x, ldx, W, w_dtype, y, ldy, M, N, K, epilogue, pushes, npush, T);
+  if (chk != Q35_OK) return chk;
+  const NormArgs na = {nullptr, nullptr, 0.f, nullptr};
+  return gemv_dispatch<false>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, (int)npush, T, na,
+                              reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int q35_gemv_norm(const float* x, const float* x_add, float* x_out, int64_t ldx, const float* norm_w,
+                             float eps, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
+                             int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush,
+                             int64_t T, q35_stream_t stream) {
+  const int chk = gemv_check(x, ldx, W, w_dtype, y, ldy, M, N, K, epilogue, pushes, npush, T);
+  if (chk != Q35_OK) return chk;
+  if (!norm_w) return Q35_EINVAL;
+  if (((uintptr_t)norm_w & 15) || (x_add && ((uintptr_t)x_add & 15)) || (x_out && ((uintptr_t)x_out & 15)))
+    return Q35_EUNSUPPORTED;
+  // x_out is written while other blocks still read x and x_add: it must not overlap them
+  auto overlap = [&](const float* a) {
+    return a && x_out && a < x_out + (M - 1) * ldx + K && x_out < a + (M - 1) * ldx + K;
+  };
+  if (overlap(x) || overlap(x_add)) return Q35_EINVAL;
+  const NormArgs na = {x_add, norm_w, eps, x_out};
+  return gemv_dispatch<true>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, (int)npush, T, na,
+                             reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int q35_swiglu_push(const float* gu, float* a, int64_t M, int64_t I, const q35_push* pushes,

@@ -51,7 +51,7 @@ def rmsnorm_1p(x, w, eps=1e-6):
 
 
 def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_heads=None, head_k_dim=None,
-                         eps=1e-6, prefill="chunk"):
+                         eps=1e-6, prefill="chunk", prenorm=None):
     """Gated DeltaNet mixer of one decoder layer (Qwen3_5GatedDeltaNet.forward, HF:432-543; the WGSL conv + delta
     kernels, engine/kernels_qwen35.js:127-247). x: [B, T, H] fp32 (the input-normed residual). A call with T == 1
     is one recurrent decode step (HF:505-517). T > 1 runs from rec_state either the chunked prefill (HF:518-530;
@@ -59,7 +59,8 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     (prefill="recurrent": fp32 throughout, as the WGSL engine runs prefill token by token,
     engine/kernels_qwen35.js:183-247). Both states are updated in place. head_scale: optional [Hv] per-head output
     scale applied after the gated norm (engine/kernels_qwen35.js:243). num_k_heads / head_k_dim default to the
-    value heads / value head dim (the Qwen3.5 text models use Hk = Hv and dk = dv). Returns y [B, T, H]."""
+    value heads / value head dim (the Qwen3.5 text models use Hk = Hv and dk = dv). prenorm: see linear() (x is then
+    the residual and the layer's input norm runs inside the input projection). Returns y [B, T, H]."""
     if prefill not in ("chunk", "recurrent"):
         raise ValueError(f"gated_deltanet_layer: prefill must be 'chunk' or 'recurrent', not {prefill!r}")
     B, T, _ = x.shape
@@ -70,7 +71,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     C, Vd = 2 * Hk * dk + Hv * dv, Hv * dv
     # one GEMM for every projection of the token: y row = [qkv (C) | z (Vd) | b (Hv) | a (Hv)], the engine's fused
     # layout (engine/kernels_qwen35.js:129-131)
-    y = linear(x, gdn_in_weight(p), *_q8(p, "_in_fused"))
+    y = linear(x, gdn_in_weight(p), *_q8(p, "_in_fused"), prenorm=prenorm)
     q, k, v, g, beta = ops.gdn_conv(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], num_k_heads=Hk,
                                     head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=C + Vd, a_off=C + Vd + Hv,
                                     out_dtype=x.dtype)
@@ -85,17 +86,34 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     return linear(o, p["out_proj"], *_q8(p, "out_proj"))
 
 
-def linear(x, w, wq=None, ws=None):
+def prenorm_torch(x, prenorm):
+    """The prenorm of linear() on torch ops: s = x + x_add (x_add may be None), copied to x_out when given; returns
+    s * rsqrt(mean s^2 + eps) * (1 + w)."""
+    x_add, nw, eps, x_out = prenorm
+    s = x + x_add if x_add is not None else x.clone()
+    if x_out is not None:
+        x_out.copy_(s)
+    return ops.add_rmsnorm_(s, None, nw, eps)
+
+
+def linear(x, w, wq=None, ws=None, prenorm=None):
     """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), on the int8 rows wq with per-row scales
-    ws when given (w = wq * ws, dequantised), else on w; a torch GEMM on w otherwise."""
+    ws when given (w = wq * ws, dequantised), else on w; a torch GEMM on w otherwise. prenorm = (x_add, norm_w, eps,
+    x_out): x is a residual and the product takes the RMSNorm (1 + norm_w) of x + x_add (x_add may be None), the sum
+    being written to x_out when given (the decoder layer's add + norm, fused into the GEMV)."""
     K = x.shape[-1]
     M = x.numel() // K
-    if M <= 8 and K % 256 == 0 and x.dtype == torch.float32:
+    if M <= 8 and K % 256 == 0 and x.dtype == torch.float32 and (wq is not None or w.dtype == torch.float32):
         xm = x.reshape(M, K).contiguous()
-        if wq is not None:
-            return ops.gemv(xm, wq, ws).view(*x.shape[:-1], wq.shape[0])
-        if w.dtype == torch.float32:
-            return ops.gemv(xm, w).view(*x.shape[:-1], w.shape[0])
+        pn = None
+        if prenorm is not None:
+            x_add, nw, eps, x_out = prenorm
+            pn = (None if x_add is None else x_add.reshape(M, K), nw, eps,
+                  None if x_out is None else x_out.view(M, K))
+        Wd, sd = (wq, ws) if wq is not None else (w, None)
+        return ops.gemv(xm, Wd, sd, prenorm=pn).view(*x.shape[:-1], Wd.shape[0])
+    if prenorm is not None:
+        x = prenorm_torch(x, prenorm)
     return x @ w.T
 
 
@@ -128,13 +146,14 @@ def attn_in_weight(p):
 
 
 def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partial_rotary_factor=0.25, eps=1e-6,
-                          cache_len=None):
+                          cache_len=None, prenorm=None):
     """Gated softmax attention mixer of one decoder layer (Qwen3_5Attention.forward, HF:656-701; WGSL attnPrep +
     attention, engine/kernels_qwen35.js:18-123). x: [B, T, H] fp32; the T tokens sit at positions pos..pos+T-1,
     pos a Python int or a [B] int32 device tensor (per row; a device tensor keeps the call capturable in a HIP
     graph). Their rotated keys and values are written into the caches at those positions. T > 1 requires pos == 0
     and runs the causal flash prefill over the call's own tokens; T == 1 runs the split-K decode over cache positions
-    0..pos (cache_len: optional [B] int32 per-row lengths, default pos + 1). Returns y [B, T, H]."""
+    0..pos (cache_len: optional [B] int32 per-row lengths, default pos + 1). prenorm: see linear(). Returns
+    y [B, T, H]."""
     B, T, _ = x.shape
     D = p["q_norm"].numel()
     Hq = p["q_proj"].shape[0] // (2 * D)
@@ -150,7 +169,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
             raise ValueError("gated_attention_layer: a multi-token call must start at position 0")
         pos_t = torch.full((B,), int(pos), dtype=torch.int32, device=x.device)
     cos, sin = rope_tables(max_len, rot, rope_theta, x.device)
-    y = linear(x, attn_in_weight(p), *_q8(p, "_in_fused"))
+    y = linear(x, attn_in_weight(p), *_q8(p, "_in_fused"), prenorm=prenorm)
     q, gate, k, v = ops.attn_prep(y, p["q_norm"], p["k_norm"], cos, sin, pos_t, k_cache, v_cache, num_heads=Hq,
                                   num_kv_heads=Hkv, eps=eps, want_kv=T > 1)
     if T > 1:

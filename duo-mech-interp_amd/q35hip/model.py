@@ -49,20 +49,27 @@ def mlp_weights(p):
     return p
 
 
-def mlp(p, h, x):
+def mlp(p, h, x, prenorm=None):
     """x += SwiGLU MLP (HF:704-717) of h, in place, with the layer's neuron pushes at the down_proj input
     (engine/model.js:7-9, engine/kernels_qwen35.js:250-279). Decode (at most 8 rows, int8 weights present): one GEMV
     over the interleaved int8 gate/up rows with the SwiGLU + push epilogue, and one int8 GEMV accumulating down_proj
     into x. Otherwise a [gate | up] GEMM on the dequantised weights, the SwiGLU push kernel and a down_proj GEMM
-    accumulating into x. Returns x."""
+    accumulating into x. prenorm = (y_add, norm_w, eps): h is then the residual; x receives h + y_add and the MLP
+    reads the RMSNorm (1 + norm_w) of that sum (the layer's second add + norm, fused into the first GEMV on the
+    decode path). Returns x."""
     mlp_weights(p)
     H = h.shape[-1]
     M = h.numel() // H
     T = h.shape[1] if h.dim() == 3 else 1
+    pn = None if prenorm is None else (prenorm[0], prenorm[1], prenorm[2], x)
     if M <= 8 and "_gu_q8" in p and H % 256 == 0 and p["down_proj.q"].shape[1] % 256 == 0:
-        a = ops.gemv(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T)
+        pn2 = None if pn is None else (None if pn[0] is None else pn[0].reshape(M, H), pn[1], pn[2], x.view(M, H))
+        a = ops.gemv(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T,
+                     prenorm=pn2)
         ops.gemv(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H), epilogue="add")
         return x
+    if pn is not None:
+        h = layers.prenorm_torch(h, pn)
     a = ops.swiglu_push(h @ p["_gu"].T, p["_pushes"], T=T)
     x.view(M, H).addmm_(a.view(M, -1), p["down_proj"].T)
     return x
@@ -153,20 +160,45 @@ class HybridModel:
             p["_pushes"].copy_(buf)
 
     def _layers(self, x, T, last, collect_layer, steer):
-        """The decoder layers 0..last over the residual stream x [rows, T, H] (dense fp32, updated in place): each
-        layer adds its mixer output in the fused residual-add + RMSNorm kernel and its MLP output in the MLP's last
-        product (HF:753-793; engine/model.js:436-462)."""
+        """The decoder layers 0..last over the residual stream x [rows, T, H] (dense fp32); returns (the residual
+        after layer `last`, the residual after collect_layer or None) (HF:753-793; engine/model.js:436-462).
+
+        Prefill (T > 1): x is updated in place; each layer adds its mixer output in the fused residual-add + RMSNorm
+        kernel and its MLP output in the MLP's last product. Decode (T == 1): the adds and norms run inside the
+        GEMVs (q35_gemv_norm): the mixer's input projection normalises the residual, the MLP's first GEMV writes
+        residual + mixer output into a second buffer and normalises it, and down_proj accumulates into that buffer;
+        the two buffers alternate by layer."""
         cfg = self.cfg
         collected = None
+        if T == 1:
+            cache_len = self.pos_dev + 1  # once per step, shared by the attention layers
+            cur, alt = x, torch.empty_like(x)
+            for l in range(last + 1):
+                p, st = self.params[l], self.states[l]
+                pre = (None, p["input_layernorm"], cfg.eps, None)
+                if cfg.is_attention(l):
+                    y = layers.gated_attention_layer(cur, p, st["k"], st["v"], self.pos_dev,
+                                                     rope_theta=cfg.rope_theta,
+                                                     partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps,
+                                                     cache_len=cache_len, prenorm=pre)
+                else:
+                    y = layers.gated_deltanet_layer(cur, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
+                                                    head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill,
+                                                    prenorm=pre)
+                mlp(p, cur, alt, prenorm=(y, p["post_attention_layernorm"], cfg.eps))
+                cur, alt = alt, cur
+                if l == self.steer_layer and steer:
+                    layers.residual_steer_add(cur, self.vec_buf, self.vec_rows)
+                if l == collect_layer:
+                    collected = cur.clone()
+            return cur, collected
         y = None  # the previous mixer's output, added to x by the next norm
-        cache_len = self.pos_dev + 1 if T == 1 else None  # decode: once per step, shared by the attention layers
         for l in range(last + 1):
             p, st = self.params[l], self.states[l]
             h = ops.add_rmsnorm_(x, y, p["input_layernorm"], cfg.eps)
             if cfg.is_attention(l):
                 y = layers.gated_attention_layer(h, p, st["k"], st["v"], self.pos_dev, rope_theta=cfg.rope_theta,
-                                                 partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps,
-                                                 cache_len=cache_len)
+                                                 partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps)
             else:
                 y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
                                                 head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill)
@@ -200,9 +232,9 @@ class HybridModel:
 
     def _lm_head(self, xl):
         """Final RMSNorm and the tied-embedding logits of the last positions xl [rows, H] (a GEMV for few rows)."""
-        hN = ops.add_rmsnorm_(xl.contiguous(), None, self.W["norm"], self.cfg.eps)
         wq = self.W.t.get("embed.q")
-        return layers.linear(hN.contiguous(), self.W["embed"], wq, None if wq is None else self.W["embed.s"])
+        return layers.linear(xl.contiguous(), self.W["embed"], wq, None if wq is None else self.W["embed.s"],
+                             prenorm=(None, self.W["norm"], self.cfg.eps, None))
 
     @torch.no_grad()
     def enable_decode_graph(self):

@@ -71,6 +71,8 @@ _LIB.define("gemv_(Tensor x, Tensor W, Tensor? w_scale, Tensor(a!) y, int epilog
 _LIB.define("swiglu_push(Tensor gu, Tensor? pushes, int T) -> Tensor")
 _LIB.define("add_rmsnorm_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tensor")
 _LIB.define("argmax_rows_(Tensor x, Tensor(a!) idx) -> ()")
+_LIB.define("gemv_norm_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
+            "Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
 _LIB.define("attn_prep(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, Tensor cos, Tensor sin, Tensor pos, "
             "Tensor(a!) k_cache, Tensor(b!) v_cache, int Hq, int Hkv, bool want_kv) "
             "-> (Tensor, Tensor, Tensor, Tensor)")
@@ -304,6 +306,27 @@ def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T):
     check(st, "q35_gemv")
 
 
+def _gemv_norm_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, epilogue, pushes, T):
+    _on_gpu(x, x_add, x_out, norm_w, W, w_scale, y, pushes)
+    _require(x.dtype == torch.float32 and x.dim() == 2 and y.dtype == torch.float32 and y.dim() == 2,
+             "x: [M, K] fp32; y: [M, N or N/2] fp32")
+    M, K = x.shape
+    for t in (x_add, x_out):
+        _require(t is None or (t.dtype == torch.float32 and tuple(t.shape) == (M, K) and t.stride(0) == x.stride(0)
+                               and t.stride(1) == 1), "x_add / x_out: like x")
+    _require(norm_w.dtype == torch.float32 and norm_w.numel() == K and norm_w.is_contiguous(), "norm_w: [K] fp32")
+    _require(W.dim() == 2 and W.dtype in (torch.int8, torch.float32) and W.shape[1] == K, "W: [N, K] int8 or fp32")
+    N = W.shape[0]
+    _require(y.shape[0] == M and y.shape[1] == (N // 2 if epilogue == 2 else N), "y: [M, N] ([M, N / 2] SwiGLU)")
+    if W.dtype == torch.int8:
+        _require(w_scale is not None and w_scale.dtype == torch.float32 and w_scale.numel() == N,
+                 "int8 W needs w_scale [N] fp32")
+    st = _lib.lib().q35_gemv_norm(_ptr(x), _ptr(x_add), _ptr(x_out), x.stride(0), _ptr(norm_w), float(eps), _ptr(W),
+                                  2 if W.dtype == torch.int8 else Q35_F32, _ptr(w_scale), _ptr(y), y.shape[1], M, N, K,
+                                  int(epilogue), _ptr(pushes), _pushes_check(pushes), int(T), _stream(x))
+    check(st, "q35_gemv_norm")
+
+
 def _swiglu_push_impl(gu, pushes, T):
     _on_gpu(gu, pushes)
     _require(gu.dtype == torch.float32 and gu.shape[-1] % 2 == 0, "gu: [..., 2 I] fp32")
@@ -348,7 +371,8 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
                      ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl),
                      ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
-                     ("add_rmsnorm_", _add_rmsnorm_impl), ("argmax_rows_", _argmax_rows_impl)]:
+                     ("add_rmsnorm_", _add_rmsnorm_impl), ("argmax_rows_", _argmax_rows_impl),
+                     ("gemv_norm_", _gemv_norm_impl)]:
     _LIB.impl(_name, _impl, "CUDA")
     _LIB.impl(_name, _no_cpu(_name), "CPU")
 
@@ -371,6 +395,7 @@ _LIB.impl("gated_attn_decode",
           "Meta")
 _LIB.impl("resid_add_rows_", lambda x, vecs, vor: None, "Meta")
 _LIB.impl("argmax_rows_", lambda x, idx: None, "Meta")
+_LIB.impl("gemv_norm_", lambda x, xa, xo, nw, eps, W, ws, y, e, pushes, T: None, "Meta")
 
 
 # ---------------------------------------------------------------- Python entry points (reference signatures)
@@ -471,15 +496,21 @@ def pack_pushes(pushes, device):
     return torch.tensor(rec, dtype=torch.int32).reshape(-1, 6).to(device)
 
 
-def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1):
+def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, prenorm=None):
     """y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k] for M <= 8 rows (decode): W int8 with per-row scales or fp32.
     epilogue "store" writes out, "add" accumulates into out (a residual add), "swiglu" treats W's rows as
-    interleaved (gate, up) pairs and writes silu(gate) * up with the neuron pushes (pack_pushes) applied."""
+    interleaved (gate, up) pairs and writes silu(gate) * up with the neuron pushes (pack_pushes) applied.
+    prenorm = (x_add, norm_w, eps, x_out): x is then a residual; the product takes the RMSNorm (1 + w) of
+    s = x + x_add (x_add may be None), and s is written to x_out when it is not None (q35_gemv_norm)."""
     e = _EPI[epilogue]
     if out is None:
         N = W.shape[0] // 2 if e == 2 else W.shape[0]
         out = torch.empty(x.shape[0], N, dtype=torch.float32, device=x.device)
-    torch.ops.q35.gemv_(x, W, w_scale, out, e, pushes, int(T))
+    if prenorm is None:
+        torch.ops.q35.gemv_(x, W, w_scale, out, e, pushes, int(T))
+    else:
+        x_add, norm_w, eps, x_out = prenorm
+        torch.ops.q35.gemv_norm_(x, x_add, x_out, norm_w, float(eps), W, w_scale, out, e, pushes, int(T))
     return out
 
 

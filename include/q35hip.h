@@ -24,6 +24,8 @@
  *   q35_gemv                 engine/kernels.js:57-90 `matvec` (int8 weights; per output channel here) and, with the
  *                            SwiGLU epilogue, engine/kernels_qwen35.js:250-279 `swiglu` with the neuron pushes;
  *                            HF:704-717 Qwen3_5MLP for the decode step
+ *   q35_gemv_norm            q35_gemv behind the layer's residual add + RMSNorm (HF:753-793, :720-734;
+ *                            engine/kernels.js:226-246 `addInto` + `rmsnorm` ahead of the matvec)
  *   q35_swiglu_push          engine/kernels_qwen35.js:250-279 `swiglu` over a [gate | up] projection (prefill form)
  *   q35_add_rmsnorm          HF:720-734 Qwen3_5RMSNorm (1 + w) with the residual add before it (HF:753-793);
  *                            engine/kernels.js:226-246 `rmsnorm` (OFFSET) and `addInto`
@@ -206,6 +208,17 @@ int q35_add_rmsnorm(float* x, int64_t ldx, const float* y, int64_t ldy, const fl
 int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
              int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T,
              q35_stream_t stream);
+
+/*
+ * q35_gemv with the decoder layer's residual add + RMSNorm in front (HF:753-793 then HF:720-734; the engine's
+ * addInto + rmsnorm, engine/kernels.js:226-246, fused into its matvec): s = x + x_add (x_add may be NULL), written to
+ * x_out when x_out is not NULL, and the product takes h = s * rsqrt(mean(s^2) + eps) * (1 + norm_w) in place of x.
+ *   x, x_add, x_out: [M, ldx] fp32, 16-byte aligned; x_out must not overlap x or x_add (Q35_EINVAL); norm_w: [K]
+ *   fp32. Everything else as q35_gemv.
+ */
+int q35_gemv_norm(const float* x, const float* x_add, float* x_out, int64_t ldx, const float* norm_w, float eps,
+                  const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy, int64_t M, int64_t N,
+                  int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream);
 
 /*
  * a[m, n] = silu(gu[m, n]) * gu[m, I + n] with the pushes applied, gu: [M, 2 I] fp32 ([gate | up] per row),

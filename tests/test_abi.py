@@ -24,7 +24,7 @@ def test_header_declares_the_boundary():
     names = declared_functions()
     for n in ["q35_gdn_recurrent", "q35_gdn_chunk_prefill", "q35_gated_attn_prefill", "q35_gated_attn_decode",
               "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
-              "q35_swiglu_push", "q35_add_rmsnorm", "q35_argmax_rows"]:
+              "q35_swiglu_push", "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm"]:
         assert n in names
 
 
@@ -108,6 +108,11 @@ def test_validation_rejects_without_launching():
     # argmax: ld shorter than the row, no rows
     assert L.q35_argmax_rows(fake, 100, 3, 101, fake, None, None) == 1
     assert L.q35_argmax_rows(fake, 100, 0, 100, fake, None, None) == 1
+    # gemv_norm: no norm weight; x_out overlapping x (the other blocks would read it while it is written)
+    assert L.q35_gemv_norm(fake, None, None, 1024, None, 1e-6, fake, 2, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1,
+                           None) == 1
+    assert L.q35_gemv_norm(fake, None, fake, 1024, fake, 1e-6, fake, 2, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1,
+                           None) == 1
 
 
 def test_decode_workspace_scales_with_splits():

@@ -80,3 +80,39 @@ def test_argmax_rows_matches_torch(rows, n):
     torch.cuda.synchronize()
     assert got.dtype == torch.int32
     assert torch.equal(got.cpu().long(), x.argmax(-1))
+
+
+@pytest.mark.parametrize("epilogue", ["store", "add", "swiglu"])
+@pytest.mark.parametrize("with_add,with_out", [(False, False), (True, True), (True, False)])
+def test_gemv_with_fused_residual_add_and_rmsnorm(epilogue, with_add, with_out):
+    """q35_gemv_norm: the product of RMSNorm(1 + w) of x + x_add (HF:720-734 after the residual add) equals the oracle's
+    norm followed by the plain product; x + x_add lands in x_out."""
+    from oracle import model as om
+    dev = device()
+    M, H = 3, 1024
+    N = 2048 if epilogue == "swiglu" else 1536
+    W, s = _weights(N, H, torch.int8, 77)
+    g = torch.Generator().manual_seed(78)
+    x = torch.randn(M, H, generator=g)
+    xa = torch.randn(M, H, generator=g) if with_add else None
+    nw = 0.3 * torch.randn(H, generator=g)
+    ssum = x + xa if with_add else x
+    h = om.rmsnorm_1p(ssum, nw, 1e-6)
+    lin = omlp.q8_linear(h, W, s)
+    if epilogue == "swiglu":
+        ref = torch.nn.functional.silu(lin[:, 0::2]) * lin[:, 1::2]
+    else:
+        ref = lin
+    base = torch.randn(ref.shape, generator=g)
+    announce(f"gemv_norm {epilogue} add={with_add} out={with_out}")
+    xd = x.to(dev)
+    xo = torch.full((M, H), 5.0, device=dev) if with_out else None
+    out = base.to(dev) if epilogue == "add" else None
+    y = ops.gemv(xd, W.to(dev), s.to(dev), out=out, epilogue=epilogue,
+                 prenorm=(None if xa is None else xa.to(dev), nw.to(dev), 1e-6, xo))
+    torch.cuda.synchronize()
+    exp = base + ref if epilogue == "add" else ref
+    assert oracle.rel_err(y.cpu(), exp) <= TOL
+    assert torch.equal(xd.cpu(), x)  # the residual itself is only read
+    if with_out:
+        assert oracle.rel_err(xo.cpu(), ssum) <= 1e-7
