@@ -95,45 +95,57 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
   };
   issue(wave);
   asm volatile("" ::: "memory");
-  for (int i = tid; i < MP * K / 4; i += blockDim.x) {
-    const int m = (4 * i) / K, k = 4 * i - m * K;
-    f32x4 v = zero4();
-    if (m < M) {
-      v = *reinterpret_cast<const f32x4*>(x + m * ldx + k);
-      if (NORM && xadd) {
-        const f32x4 a = *reinterpret_cast<const f32x4*>(xadd + m * ldx + k);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += a[e];
-      }
-      if (NORM && xout && blockIdx.x == 0) *reinterpret_cast<f32x4*>(xout + m * ldx + k) = v;
-    }
-    *reinterpret_cast<f32x4*>(xs + m * K + k) = v;
-  }
-  __syncthreads();
+  // x (or, with NORM, s = x + xadd times (1 + nw)) into LDS; with NORM each wave also sums the squares of s per row
+  // (all loads of a thread go out together: one round trip), the rows' rsqrt factors applied in the epilogue
+  __shared__ float ssw[8][MP];
   if (NORM) {
-    // mean of squares per row m: wave w sums rows w, w + NW, ... over K, then every thread rescales its elements
-    __shared__ float rs[MP];
-    for (int m = wave; m < MP; m += NW) {
-      float ss = 0.f;
-      for (int k = 4 * lane; k < K; k += 256) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(xs + m * K + k);
-        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    float ss[MP];
+#pragma unroll
+    for (int m = 0; m < MP; ++m) ss[m] = 0.f;
+    for (int k = 4 * tid; k < K; k += 4 * (int)blockDim.x) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(nw + k);
+      f32x4 v[MP];
+#pragma unroll
+      for (int m = 0; m < MP; ++m) {
+        v[m] = zero4();
+        if (m < M) v[m] = *reinterpret_cast<const f32x4*>(x + m * ldx + k);
+      }
+      if (xadd) {
+#pragma unroll
+        for (int m = 0; m < MP; ++m) {
+          if (m < M) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(xadd + m * ldx + k);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[m][e] += a[e];
+          }
+        }
       }
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-      if (lane == 0) rs[m] = rsqrtf(ss / (float)K + eps);
+      for (int m = 0; m < MP; ++m) {
+        if (xout && blockIdx.x == 0 && m < M) *reinterpret_cast<f32x4*>(xout + m * ldx + k) = v[m];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ss[m] += v[m][e] * v[m][e];
+          v[m][e] *= 1.f + w[e];
+        }
+        *reinterpret_cast<f32x4*>(xs + m * K + k) = v[m];
+      }
     }
-    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MP; ++m) {
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) ss[m] += __shfl_xor(ss[m], off, 64);
+      if (lane == 0) ssw[wave][m] = ss[m];
+    }
+  } else {
     for (int i = tid; i < MP * K / 4; i += blockDim.x) {
       const int m = (4 * i) / K, k = 4 * i - m * K;
-      f32x4 v = *reinterpret_cast<const f32x4*>(xs + m * K + k);
-      const f32x4 w = *reinterpret_cast<const f32x4*>(nw + k);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = v[e] * rs[m] * (1.f + w[e]);
+      f32x4 v = zero4();
+      if (m < M) v = *reinterpret_cast<const f32x4*>(x + m * ldx + k);
       *reinterpret_cast<f32x4*>(xs + m * K + k) = v;
     }
-    __syncthreads();
   }
+  __syncthreads();
   float acc[4][MP];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
@@ -177,6 +189,11 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
   auto rowsum = [&](int rr, int m) {
     float v = 0.f;
     for (int w = 0; w < NW; ++w) v += red[w][rr][m];
+    if (NORM) {
+      float ss = 0.f;
+      for (int w = 0; w < NW; ++w) ss += ssw[w][m];
+      v *= rsqrtf(ss / (float)K + eps);
+    }
     return v;
   };
   if (EPI != kEpiSwiglu) {
