@@ -51,8 +51,8 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
 __device__ __forceinline__ int vperm(int p) { return (p & 3) | ((p & 4) << 1) | ((p & 8) >> 1); }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Kernel 1: one block of 256 threads per (64 keys, kv head, row). ROT (rotary dims) is a template parameter so that
-// the rotation pairs are compile-time register indices.
+// Kernel 1: one block of 256 threads per (64 keys, kv head, row) for the keys and another for the values. ROT
+// (rotary dims) is a template parameter so that the rotation pairs are compile-time register indices.
 template <int ROT>
 __global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restrict__ k, const __bf16* __restrict__ v,
                                                            const float* __restrict__ cos_t,
@@ -62,55 +62,60 @@ __global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restr
   static_assert(ROT % 16 == 0 && ROT <= kRotMax, "rotary dims");
   constexpr int half = ROT / 2;
   const int tid = threadIdx.x;
-  const int key0 = blockIdx.x * kBN, kvh = blockIdx.y, b = blockIdx.z;
+  // blocks x < Tp / 64 prepare the keys of tile x, blocks x >= Tp / 64 the values of tile x - Tp / 64
+  const int ntile = Tp / kBN;
+  const bool doK = (int)blockIdx.x < ntile;
+  const int key0 = (doK ? blockIdx.x : blockIdx.x - ntile) * kBN, kvh = blockIdx.y, b = blockIdx.z;
   const size_t head = (size_t)b * Hkv + kvh;
-  // K: thread = (row r, quarter cq of the dims); the rotary dims [0, rot) all sit in quarter 0
-  {
-    const int r = tid >> 2, cq = tid & 3;
+  // K: thread = (row r, lane q of 4); a row is 32 segments of 8 dims and thread q takes segments q, q + 4, ...
+  // A rotary segment (s < ROT / 8) pairs with the segment half / 8 away; its cos / sin rows are loaded as vectors.
+  // Every load of the thread is issued before any is used (one memory round trip per block).
+  if (doK) {
+    constexpr int NSEG = kPD / 8, RS = ROT / 8, HS = half / 8;
+    const int r = tid >> 2, q = tid & 3;
     const int key = key0 + r;
     const bool valid = key < T;
-    const __bf16* src = k + (((size_t)b * T + min(key, T - 1)) * Hkv + kvh) * kPD + 64 * cq;
-    u32x4 w[8];
+    const __bf16* src = k + (((size_t)b * T + min(key, T - 1)) * Hkv + kvh) * kPD;
+    u32x4 w[NSEG / 4], pw[NSEG / 4];
+    f32x4 cs[NSEG / 4][2], sn[NSEG / 4][2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = *reinterpret_cast<const u32x4*>(src + 8 * i);
-    if (ROT > 0 && cq == 0 && valid) {
-      float x[64];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          x[8 * i + 2 * e] = bf16lo(w[i][e]);
-          x[8 * i + 2 * e + 1] = bf16hi(w[i][e]);
-        }
-      const float* cr = cos_t + (size_t)(pos0 + key) * half;
-      const float* sr = sin_t + (size_t)(pos0 + key) * half;
-      float y[64];
-#pragma unroll
-      for (int d = 0; d < 64; ++d) {
-        if (d < ROT) {
-          const int j = d < half ? d : d - half;
-          const float pr = d < half ? -x[(d + half) & 63] : x[(d + 64 - half) & 63];
-          y[d] = x[d] * cr[j] + pr * sr[j];
-        } else {
-          y[d] = x[d];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        bf16x8 o8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o8[e] = (__bf16)y[8 * i + e];
-        w[i] = __builtin_bit_cast(u32x4, o8);
+    for (int i = 0; i < NSEG / 4; ++i) {
+      const int sg = q + 4 * i;
+      w[i] = *reinterpret_cast<const u32x4*>(src + 8 * sg);
+      if (4 * i < RS) {  // segments 4 i .. 4 i + 3 may be rotary (compile-time bound)
+        const int ps = sg < HS ? sg + HS : sg - HS;
+        const int j0 = 8 * (sg < HS ? sg : sg - HS);
+        const size_t crow = (size_t)(pos0 + min(key, T - 1)) * half + (sg < RS ? j0 : 0);
+        pw[i] = *reinterpret_cast<const u32x4*>(src + 8 * (sg < RS ? ps : sg));
+        cs[i][0] = *reinterpret_cast<const f32x4*>(cos_t + crow);
+        cs[i][1] = *reinterpret_cast<const f32x4*>(cos_t + crow + 4);
+        sn[i][0] = *reinterpret_cast<const f32x4*>(sin_t + crow);
+        sn[i][1] = *reinterpret_cast<const f32x4*>(sin_t + crow + 4);
       }
     }
     const u32x4 z = {0u, 0u, 0u, 0u};
-    __bf16* dst = kr + (head * Tp + key) * kPD + 64 * cq;
+    __bf16* dst = kr + (head * Tp + key) * kPD;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(dst + 8 * i) = valid ? w[i] : z;
+    for (int i = 0; i < NSEG / 4; ++i) {
+      const int sg = q + 4 * i;
+      u32x4 o = w[i];
+      if (4 * i < RS && sg < RS) {
+        const float sgn = sg < HS ? -1.f : 1.f;
+        bf16x8 o8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t xw = w[i][e >> 1], pwv = pw[i][e >> 1];
+          const float x = (e & 1) ? bf16hi(xw) : bf16lo(xw), y = (e & 1) ? bf16hi(pwv) : bf16lo(pwv);
+          o8[e] = (__bf16)(x * cs[i][e >> 2][e & 3] + sgn * y * sn[i][e >> 2][e & 3]);
+        }
+        o = __builtin_bit_cast(u32x4, o8);
+      }
+      *reinterpret_cast<u32x4*>(dst + 8 * sg) = valid ? o : z;
+    }
   }
   // V^T: thread = (8 keys kg, 8 dims dg); an 8 x 8 transpose in registers, each dim row written as two 8-byte
   // pieces (keys kg*8 .. +3 and +4 .. +7 land 8 positions apart after the in-group permutation)
-  {
+  else {
     const int kg = tid >> 5, dg = tid & 31;
     u32x4 w[8];
     const u32x4 z = {0u, 0u, 0u, 0u};
@@ -499,47 +504,55 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
   }
 }
 
-// Kernel 3: the two halves of every split query block. One wave per (pair, query head of the group): lane (ln, hh)
-// reads the accumulator-order partials of both halves exactly as the main kernel's lanes wrote them and combines them
-// in half order, O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise (so the result does not depend on which half ran
-// first), then normalises, gates and stores as the main kernel's epilogue does. Neither half has a fully masked
-// query: the second half starts at key 64 Ls and every query of a split block is at or past it.
+// Kernel 3: the two halves of every split query block. One block of 256 threads per (pair, query head of the group):
+// the wave partial is 2048 16-byte chunks in accumulator order (chunk e = (4 mt + c) 64 + l holds dims
+// 32 mt + 8 c + 4 (l >> 5) .. + 3 of query q0 + (l & 31)); thread t takes chunks t + 256 j, j < 8, of both halves,
+// all loads issued before any is used. The halves are combined in half order, O = O0 2^(m0 - m) + O1 2^(m1 - m), l
+// likewise (the result does not depend on which half ran first), then normalised, gated and stored as the main
+// kernel's epilogue does. Neither half has a fully masked query: the second half starts at key 64 Ls and every
+// query of a split block is at or past it.
 template <int GW>
-__global__ __launch_bounds__(64) void attn_prefill_merge_kernel(const float* __restrict__ part,
-                                                                const __bf16* __restrict__ gate,
-                                                                __bf16* __restrict__ out, int T, int Hq, int Hkv,
-                                                                int ngroups, int B, int Ls) {
-  const int pair = blockIdx.x, wave = blockIdx.y, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __restrict__ part,
+                                                                 const __bf16* __restrict__ gate,
+                                                                 __bf16* __restrict__ out, int T, int Hq, int Hkv,
+                                                                 int ngroups, int B, int Ls) {
+  const int pair = blockIdx.x, wave = blockIdx.y, tid = threadIdx.x;
   const int n_other = B * Hkv * ngroups;
   const int qb = 2 * Ls + pair / n_other, rem = pair % n_other;
   const int b = rem / (Hkv * ngroups), kvh = (rem / ngroups) % Hkv, hg = rem % ngroups;
   const int h = kvh * (Hq / Hkv) + hg * GW + wave;
-  const int ln = lane & 31, hh = lane >> 5;
-  const int tq = qb * kBQ + ln;
   const float* p0 = part + ((size_t)(2 * pair) * GW + wave) * kPartFloats;
   const float* p1 = part + ((size_t)(2 * pair + 1) * GW + wave) * kPartFloats;
-  const float m0 = p0[8192 + lane], l0 = p0[8192 + 64 + lane];
-  const float m1 = p1[8192 + lane], l1 = p1[8192 + 64 + lane];
+  f32x4 w0[8], w1[8];
+  u32x2 gr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = tid + 256 * j, l = e & 63, mtc = e >> 6;
+    const int tq = min(qb * kBQ + (l & 31), T - 1);
+    const int d = 8 * mtc + 4 * (l >> 5);  // 32 mt + 8 c + 4 hh with mtc = 4 mt + c
+    w0[j] = *reinterpret_cast<const f32x4*>(p0 + (size_t)e * 4);
+    w1[j] = *reinterpret_cast<const f32x4*>(p1 + (size_t)e * 4);
+    gr[j] = *reinterpret_cast<const u32x2*>(gate + ((size_t)b * T + tq) * (size_t)Hq * kPD + (size_t)h * kPD + d);
+  }
+  // every chunk of thread t has lane l = t & 63 (256 j is a multiple of 64)
+  const int l = tid & 63;
+  const float m0 = p0[8192 + l], l0 = p0[8192 + 64 + l];
+  const float m1 = p1[8192 + l], l1 = p1[8192 + 64 + l];
   const float mm = fmaxf(m0, m1);
   const float c0 = __builtin_amdgcn_exp2f(m0 - mm), c1 = __builtin_amdgcn_exp2f(m1 - mm);
-  const float l = fmaf(l0, c0, l1 * c1);
+  const float lt = fmaf(l0, c0, l1 * c1);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  const int tq = qb * kBQ + (l & 31);
   if (tq >= T) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  const size_t rowo = ((size_t)b * T + tq) * (size_t)Hq * kPD + (size_t)h * kPD;
-#pragma unroll 4
-  for (int mt = 0; mt < 8; ++mt) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d = 32 * mt + 8 * c + 4 * hh;
-      const f32x4 w0 = *reinterpret_cast<const f32x4*>(p0 + ((mt * 4 + c) * 64 + lane) * 4);
-      const f32x4 w1 = *reinterpret_cast<const f32x4*>(p1 + ((mt * 4 + c) * 64 + lane) * 4);
-      const u32x2 gr = *reinterpret_cast<const u32x2*>(gate + rowo + d);
-      const float gv[4] = {bf16lo(gr[0]), bf16hi(gr[0]), bf16lo(gr[1]), bf16hi(gr[1])};
-      bf16x4 ov;
+  for (int j = 0; j < 8; ++j) {
+    const int e = tid + 256 * j, mtc = e >> 6;
+    const int d = 8 * mtc + 4 * (l >> 5);
+    const float gv[4] = {bf16lo(gr[j][0]), bf16hi(gr[j][0]), bf16lo(gr[j][1]), bf16hi(gr[j][1])};
+    bf16x4 ov;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ov[e] = (__bf16)(fmaf(w0[e], c0, w1[e] * c1) * inv * sigmoidf_(gv[e]));
-      *reinterpret_cast<bf16x4*>(out + rowo + d) = ov;
-    }
+    for (int q = 0; q < 4; ++q) ov[q] = (__bf16)(fmaf(w0[j][q], c0, w1[j][q] * c1) * inv * sigmoidf_(gv[q]));
+    *reinterpret_cast<bf16x4*>(out + ((size_t)b * T + tq) * (size_t)Hq * kPD + (size_t)h * kPD + d) = ov;
   }
 }
 
@@ -606,7 +619,7 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
   __bf16* kr = reinterpret_cast<__bf16*>(ws);
   __bf16* vt = kr + (size_t)B * Hkv * Tp * kPD;
   float* part = reinterpret_cast<float*>(ws + lay.part_off);
-  const dim3 gp((unsigned)(Tp / kBN), (unsigned)Hkv, (unsigned)B);
+  const dim3 gp((unsigned)(2 * (Tp / kBN)), (unsigned)Hkv, (unsigned)B);
 #define Q35_KV_LAUNCH(R)                                                                                         \
   hipLaunchKernelGGL(attn_kv_prep_kernel<R>, gp, dim3(256), 0, st, (const __bf16*)k, (const __bf16*)v, cos, sin, \
                      (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv)
@@ -623,7 +636,7 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
                      kr, vt, (const __bf16*)gate, cos, sin, (int)pos0, (__bf16*)out, (int)T, (int)Tp, (int)Hq,     \
                      (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B, Ls, part);                             \
   if (lay.npairs > 0)                                                                                             \
-    hipLaunchKernelGGL(attn_prefill_merge_kernel<GG>, dim3((unsigned)lay.npairs, GG), dim3(64), 0, st, part,       \
+    hipLaunchKernelGGL(attn_prefill_merge_kernel<GG>, dim3((unsigned)lay.npairs, GG), dim3(256), 0, st, part,       \
                        (const __bf16*)gate, (__bf16*)out, (int)T, (int)Hq, (int)Hkv, ngroups, (int)B, Ls)
   switch (GW) {
     case 1: Q35_PF_LAUNCH(1); break;
