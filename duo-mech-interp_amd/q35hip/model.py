@@ -232,8 +232,9 @@ class HybridModel:
 
     def _lm_head(self, xl):
         """Final RMSNorm and the tied-embedding logits of the last positions xl [rows, H] (a GEMV for few rows)."""
-        wq = self.W.t.get("embed.q")
-        return layers.linear(xl.contiguous(), self.W["embed"], wq, None if wq is None else self.W["embed.s"],
+        head = "lm_head" if "lm_head" in self.W.t else "embed"  # untied checkpoints carry their own head
+        wq = self.W.t.get(head + ".q")
+        return layers.linear(xl.contiguous(), self.W[head], wq, None if wq is None else self.W[head + ".s"],
                              prenorm=(None, self.W["norm"], self.cfg.eps, None))
 
     @torch.no_grad()

@@ -85,9 +85,14 @@ class Q35Config:
     eps: float = 1e-6
     full_attention_interval: int = 4
     init_std: float = 0.02
+    layer_types: tuple = None  # per layer "linear_attention" / "full_attention" (a checkpoint's config); None: interval
+    tie_embeddings: bool = True
 
     def is_attention(self, layer):
-        """Layer pattern of HFcfg:113-115: every full_attention_interval-th layer is full attention."""
+        """The checkpoint's layer_types when given, else the pattern of HFcfg:113-115: every
+        full_attention_interval-th layer is full attention."""
+        if self.layer_types is not None:
+            return self.layer_types[layer] == "full_attention"
         return (layer + 1) % self.full_attention_interval == 0
 
     @property

@@ -162,7 +162,7 @@ class OracleModel:
         if stop_after is not None:
             return None, collected
         hN = rmsnorm_1p(x[:, -1], W["norm"], cfg.eps)
-        return hN @ W["embed"].T, collected
+        return hN @ W.get("lm_head", W["embed"]).T, collected
 
 
 def median_resid_norm(resid):

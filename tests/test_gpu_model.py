@@ -94,3 +94,26 @@ def test_full_stack_steered_greedy_64_steps():
     first_diff = [int((~same[r]).nonzero()[0]) if not bool(same[r].all()) else -1 for r in range(3)]
     print(f"min top-2 margin (CPU) {float(marg_r.min()):.4g}; first differing step per row {first_diff}")
     assert bool(same.all()), f"greedy tokens differ; first differing step per row {first_diff}"
+
+
+def test_loaded_int8_checkpoint_runs_on_the_stack(tmp_path):
+    """A tiny HF-layout checkpoint loaded with every linear in int8 (q35hip.checkpoint) runs prefill and decode on
+    the GPU stack in agreement with the oracle on the same loaded weights."""
+    import test_checkpoint as tc
+    from q35hip import checkpoint as ck
+    dev = device()
+    cfg0 = tiny_config()
+    tc._write(str(tmp_path / "ckpt"), cfg0, tiny_weights(cfg0), shards=2)
+    cfg, W = ck.load_checkpoint(str(tmp_path / "ckpt"))
+    ids, _ = tiny_inputs(cfg)
+    announce("model tiny loaded int8 checkpoint")
+    ref = om.OracleModel(cfg, W)
+    g = gm.HybridModel(cfg, W, dev, max_len=256, rows=2)
+    lr, _ = ref.forward(ids)
+    lg, _ = g.forward(ids)
+    assert oracle.rel_err(lg.cpu(), lr) <= 2e-2
+    for _ in range(4):
+        nxt = lr.argmax(-1, keepdim=True)
+        lr, _ = ref.forward(nxt)
+        lg, _ = g.forward(nxt.to(dev))
+        assert oracle.rel_err(lg.cpu(), lr) <= 2e-2
