@@ -18,6 +18,8 @@
 // online softmax in registers, then O^T += V^T P^T with P^T's accumulator tiles used directly as B operands. Tiles
 // arrive by global_load_lds DMA into XOR-swizzled LDS (conflict-free 16-byte operand reads), two stages and one
 // barrier per tile (tile kt + 1 is copied while tile kt is computed), each wave copying a quarter of every tile.
+#include <atomic>
+
 #include "q35_common.h"
 #include "q35hip.h"
 
@@ -157,24 +159,37 @@ struct PfStage {
 
 // Work items. Query block qb needs key tiles 0 .. nkt(qb) - 1, so the causal blocks range from 1 to ~T/64 tiles. With
 // a split length Ls > 0, every block with more than Ls tiles (qb >= 2 Ls) is run as two items, tiles [0, Ls) and
-// [Ls, nkt), whose (O, m, l) are combined by attn_prefill_merge_kernel; the others run whole. Items are numbered
-// longest first: all first halves (Ls tiles each), then second halves and whole blocks alternately, each in
-// decreasing length, so that the hardware's in-order dispatch to free CUs balances the CUs' total tiles.
+// [Ls, nkt), whose (O, m, l) are combined by attn_prefill_merge_kernel; the others run whole. Two orders:
+// - Independent items, numbered longest first: all first halves (Ls tiles each), then second halves and whole blocks
+//   alternately, each in decreasing length, so that the hardware's in-order dispatch to free CUs balances the CUs'
+//   total tiles. Used when the items outnumber the CUs.
+// - Paired items, used when they fit the device in one wave (one block per CU): the second half of the j-th longest
+//   split block (about Ls - j / 2 tiles) and whole block j (about j / 2 + 1 tiles) run one after the other in one
+//   block, so every block holds Ls or Ls + 1 tiles. Independent items would leave the short items to a second wave,
+//   each paying its query prologue (a memory round trip of several microseconds) on the critical path.
 constexpr int kPartFloats = 8192 + 128;  // one wave's partial: O^T [32 x 256] fp32 in accumulator order, m[64], l[64]
 
 struct PfItem {
   int qb, kt0, kt1, half;  // half: -1 for a whole block, else 0 / 1
+  int qb2;                 // paired items: the whole block run after this one, else -1
 };
 
 __host__ __device__ inline int pf_tiles(int qb) { return (qb * kBQ + kBQ - 1) / kBN + 1; }
 
-__host__ __device__ inline PfItem pf_item(int idx, int nqb, int Ls) {
+__host__ __device__ inline PfItem pf_item(int idx, int nqb, int Ls, bool paired) {
   if (Ls == 0) {
     const int qb = nqb - 1 - idx;
-    return {qb, 0, pf_tiles(qb), -1};
+    return {qb, 0, pf_tiles(qb), -1, -1};
   }
   const int qs = 2 * Ls, nsq = nqb - qs;  // blocks qs .. nqb-1 are split
-  if (idx < nsq) return {nqb - 1 - idx, 0, Ls, 0};
+  if (idx < nsq) return {nqb - 1 - idx, 0, Ls, 0, -1};
+  if (paired) {
+    // j < min(nsq, qs): second half of block nqb-1-j, then whole block j; past that the unpaired remainder (second
+    // halves when nsq > qs, else whole blocks nsq .. qs-1)
+    const int j = idx - nsq;
+    if (j < nsq) return {nqb - 1 - j, Ls, pf_tiles(nqb - 1 - j), 1, j < qs ? j : -1};
+    return {j, 0, pf_tiles(j), -1, -1};
+  }
   const int j = idx - nsq, m2 = nsq < qs ? nsq : qs;
   bool second;
   int p;
@@ -187,10 +202,10 @@ __host__ __device__ inline PfItem pf_item(int idx, int nqb, int Ls) {
   }
   if (second) {
     const int qb = nqb - 1 - p;
-    return {qb, Ls, pf_tiles(qb), 1};
+    return {qb, Ls, pf_tiles(qb), 1, -1};
   }
   const int qb = qs - 1 - p;
-  return {qb, 0, pf_tiles(qb), -1};
+  return {qb, 0, pf_tiles(qb), -1, -1};
 }
 
 // split length for a launch: none for short sequences, else half of the longest block's tiles
@@ -198,9 +213,13 @@ inline int pf_split_len(int nqb) {
   const int nmax = pf_tiles(nqb - 1);
   return nmax >= 8 ? (nmax + 1) / 2 : 0;
 }
-inline int pf_items(int nqb, int Ls) { return Ls == 0 ? nqb : 2 * (nqb - 2 * Ls) + 2 * Ls; }
+inline int pf_items(int nqb, int Ls, bool paired) {
+  if (Ls == 0) return nqb;
+  const int nsq = nqb - 2 * Ls, qs = 2 * Ls;
+  return paired ? nsq + (nsq > qs ? nsq : qs) : 2 * nsq + qs;
+}
 
-template <int GW>
+template <int GW, bool PAIRED>
 __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ kr, const __bf16* __restrict__ vt,
     const __bf16* __restrict__ gate, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos0,
@@ -211,15 +230,13 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_other = B * Hkv * ngroups;
-  const PfItem it = pf_item((int)(blockIdx.x / n_other), nqb, Ls);
-  const int qb = it.qb;
+  const PfItem it0 = pf_item((int)(blockIdx.x / n_other), nqb, Ls, PAIRED);
   const int rem = blockIdx.x % n_other;
   const int b = rem / (Hkv * ngroups);
   const int kvh = (rem / ngroups) % Hkv;
   const int hg = rem % ngroups;
   const int G = Hq / Hkv;
   const int h = kvh * G + hg * GW + wave;
-  const int q0 = qb * kBQ;
   const int half = rot >> 1;
   const int ln = lane & 31, hh = lane >> 5;
   const size_t head = (size_t)b * Hkv + kvh;
@@ -253,254 +270,307 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     }
   };
 
-  // ---- Q^T operand (B of S^T = K Q^T): lane holds query q0 + ln, dims 16 ks + 8 hh + j, rotated. Every load (the
-  //      query row, the rotation partners and the cos / sin rows) is issued before the first tile's copies and before
-  //      any of them is used, so the prologue costs one memory round trip.
-  bf16x8 qop[16];
-  {
-    const int t = q0 + ln;
-    const bool tv = t < T;
-    const __bf16* qrow = q + (((size_t)b * T + (tv ? t : T - 1)) * Hq + h) * kPD;
-    const int pos = pos0 + (tv ? t : T - 1);
-    u32x4 raw[16];
+  // One item (or one segment of a paired item): its query block's tiles kt0 .. kt1 - 1. Inlined once per segment,
+  // so each copy is straight-line code with its own register allocation.
+  auto run = [&](const PfItem it) {
+    const int qb = it.qb;
+    const int q0 = qb * kBQ;
+
+    // ---- Q^T operand (B of S^T = K Q^T): lane holds query q0 + ln, dims 16 ks + 8 hh + j, rotated. Every load (the
+    //      query row, the rotation partners and the cos / sin rows) is issued before the first tile's copies and before
+    //      any of them is used, so the prologue costs one memory round trip.
+    bf16x8 qop[16];
+    {
+      const int t = q0 + ln;
+      const bool tv = t < T;
+      const __bf16* qrow = q + (((size_t)b * T + (tv ? t : T - 1)) * Hq + h) * kPD;
+      const int pos = pos0 + (tv ? t : T - 1);
+      u32x4 raw[16];
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
-    const int nrk = rot >> 4;  // K steps holding rotary dims (rot is a multiple of 16, at most 64)
-    u32x4 praw[4];
-    f32x4 cs[4][2], sn[4][2];
-    if (nrk > 0) {
+      for (int ks = 0; ks < 16; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
+      const int nrk = rot >> 4;  // K steps holding rotary dims (rot is a multiple of 16, at most 64)
+      u32x4 praw[4];
+      f32x4 cs[4][2], sn[4][2];
+      if (nrk > 0) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (ks < nrk) {
+        for (int ks = 0; ks < 4; ++ks) {
+          if (ks < nrk) {
+            const int d = 16 * ks + 8 * hh;
+            const int pd = d < half ? d + half : d - half;
+            const int j0 = d < half ? d : d - half;
+            praw[ks] = *reinterpret_cast<const u32x4*>(qrow + pd);
+            const float* cp = cos_t + (size_t)pos * half + j0;
+            const float* sp = sin_t + (size_t)pos * half + j0;
+            cs[ks][0] = *reinterpret_cast<const f32x4*>(cp);
+            cs[ks][1] = *reinterpret_cast<const f32x4*>(cp + 4);
+            sn[ks][0] = *reinterpret_cast<const f32x4*>(sp);
+            sn[ks][1] = *reinterpret_cast<const f32x4*>(sp + 4);
+          }
+        }
+      }
+      copy_tile(it.kt0, it.kt0 & 1);
+#pragma unroll
+      for (int ks = 0; ks < 16; ++ks) {
+        const u32x4 r = raw[ks];
+        float x[8] = {bf16lo(r[0]), bf16hi(r[0]), bf16lo(r[1]), bf16hi(r[1]),
+                      bf16lo(r[2]), bf16hi(r[2]), bf16lo(r[3]), bf16hi(r[3])};
+        if (ks < 4 && ks < nrk) {
           const int d = 16 * ks + 8 * hh;
-          const int pd = d < half ? d + half : d - half;
-          const int j0 = d < half ? d : d - half;
-          praw[ks] = *reinterpret_cast<const u32x4*>(qrow + pd);
-          const float* cp = cos_t + (size_t)pos * half + j0;
-          const float* sp = sin_t + (size_t)pos * half + j0;
-          cs[ks][0] = *reinterpret_cast<const f32x4*>(cp);
-          cs[ks][1] = *reinterpret_cast<const f32x4*>(cp + 4);
-          sn[ks][0] = *reinterpret_cast<const f32x4*>(sp);
-          sn[ks][1] = *reinterpret_cast<const f32x4*>(sp + 4);
+          const u32x4 pr = praw[ks];
+          const float y[8] = {bf16lo(pr[0]), bf16hi(pr[0]), bf16lo(pr[1]), bf16hi(pr[1]),
+                              bf16lo(pr[2]), bf16hi(pr[2]), bf16lo(pr[3]), bf16hi(pr[3])};
+          const float sg = d < half ? -1.f : 1.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float c = cs[ks][j >> 2][j & 3], sv = sn[ks][j >> 2][j & 3];
+            x[j] = x[j] * c + sg * y[j] * sv;
+          }
         }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qop[ks][j] = (__bf16)(tv ? x[j] : 0.f);
       }
     }
-    copy_tile(it.kt0, it.kt0 & 1);
+
+    f32x16 o[8];
 #pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {
-      const u32x4 r = raw[ks];
-      float x[8] = {bf16lo(r[0]), bf16hi(r[0]), bf16lo(r[1]), bf16hi(r[1]),
-                    bf16lo(r[2]), bf16hi(r[2]), bf16lo(r[3]), bf16hi(r[3])};
-      if (ks < 4 && ks < nrk) {
-        const int d = 16 * ks + 8 * hh;
-        const u32x4 pr = praw[ks];
-        const float y[8] = {bf16lo(pr[0]), bf16hi(pr[0]), bf16lo(pr[1]), bf16hi(pr[1]),
-                            bf16lo(pr[2]), bf16hi(pr[2]), bf16lo(pr[3]), bf16hi(pr[3])};
-        const float sg = d < half ? -1.f : 1.f;
+    for (int mt = 0; mt < 8; ++mt) o[mt] = zero16();
+    // Scores are kept unscaled; the softmax works in base 2 on scaled scores: p = 2^(s c - m) with c = scale log2(e),
+    // m_run the running max of s c.
+    const float csc = scale * 1.44269504088896341f;
+    float m_run = -INFINITY, l_run = 0.f;
+    const int tq = q0 + ln;  // this lane's query
+    const int full_tiles = q0 / kBN;  // tiles entirely below this block's first query: no mask
+
+    // Per-lane LDS read offsets inside a stage. K: row 32 ksub + ln, logical segment 2 ks + hh, stored at segment
+    // (2 ks + hh) ^ (ln & 15): for ks = 8 a + j the offset is ka[j] + 256 a + 16384 ksub. V^T: row 32 mt + ln, logical
+    // segment 2 kk + hh stored at (2 kk + hh) ^ ((ln >> 1) & 7): offset va[kk] + 4096 mt.
+    int ka[8], va[4];
+    {
+      const int c2 = (ln >> 1) & 7;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float c = cs[ks][j >> 2][j & 3], sv = sn[ks][j >> 2][j & 3];
-          x[j] = x[j] * c + sg * y[j] * sv;
-        }
-      }
+      for (int j = 0; j < 8; ++j) ka[j] = 512 * ln + 16 * (hh ^ (ln & 1)) + 32 * (j ^ c2);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qop[ks][j] = (__bf16)(tv ? x[j] : 0.f);
+      for (int kk = 0; kk < 4; ++kk) va[kk] = 128 * ln + 16 * ((2 * kk + hh) ^ c2);
     }
-  }
 
-  f32x16 o[8];
-#pragma unroll
-  for (int mt = 0; mt < 8; ++mt) o[mt] = zero16();
-  // Scores are kept unscaled; the softmax works in base 2 on scaled scores: p = 2^(s c - m) with c = scale log2(e),
-  // m_run the running max of s c.
-  const float csc = scale * 1.44269504088896341f;
-  float m_run = -INFINITY, l_run = 0.f;
-  const int tq = q0 + ln;  // this lane's query
-  const int full_tiles = q0 / kBN;  // tiles entirely below this block's first query: no mask
-
-  // Per-lane LDS read offsets inside a stage. K: row 32 ksub + ln, logical segment 2 ks + hh, stored at segment
-  // (2 ks + hh) ^ (ln & 15): for ks = 8 a + j the offset is ka[j] + 256 a + 16384 ksub. V^T: row 32 mt + ln, logical
-  // segment 2 kk + hh stored at (2 kk + hh) ^ ((ln >> 1) & 7): offset va[kk] + 4096 mt.
-  int ka[8], va[4];
-  {
-    const int c2 = (ln >> 1) & 7;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ka[j] = 512 * ln + 16 * (hh ^ (ln & 1)) + 32 * (j ^ c2);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) va[kk] = 128 * ln + 16 * ((2 * kk + hh) ^ c2);
-  }
-
-  // Raw scores of tile kt into sc (S^T = K Q^T, causally masked with -inf); returns this lane's query's max of the
-  // raw scores over the tile's keys.
-  auto tile_scores = [&](int kt, f32x16 (&sc)[2]) -> float {
-    const int s = kt & 1;
-    // this wave's copies of tile kt are its only ones in flight; after the barrier every wave's have landed and
-    // every wave is done with tile kt - 1, whose stage then receives tile kt + 1
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (kt + 1 < it.kt1) copy_tile(kt + 1, s ^ 1);
-    const char* kl = reinterpret_cast<const char*>(&stage[s].k[0]);
-    // four accumulation chains (two per 32-key half: even and odd K steps) over four groups of four K steps; the K
-    // fragments of group g + 1 are read while the MFMAs of group g run, so LDS latency is hidden behind the matrix
-    // core
-    f32x16 acc[2][2] = {{zero16(), zero16()}, {zero16(), zero16()}};
-    auto kread = [&](int g, bf16x8 (&kf)[2][4]) {
-#pragma unroll
-      for (int ksub = 0; ksub < 2; ++ksub)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int ks = 4 * g + j;
-          kf[ksub][j] = *reinterpret_cast<const bf16x8*>(kl + ka[ks & 7] + 256 * (ks >> 3) + 16384 * ksub);
-        }
-    };
-    bf16x8 kfa[2][4], kfb[2][4];
-    kread(0, kfa);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      bf16x8 (&cur)[2][4] = (g & 1) ? kfb : kfa;
-      bf16x8 (&nxt)[2][4] = (g & 1) ? kfa : kfb;
-      if (g < 3) kread(g + 1, nxt);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
+    // Raw scores of tile kt into sc (S^T = K Q^T, causally masked with -inf); returns this lane's query's max of the
+    // raw scores over the tile's keys.
+    auto tile_scores = [&](int kt, f32x16 (&sc)[2]) -> float {
+      const int s = kt & 1;
+      // this wave's copies of tile kt are its only ones in flight; after the barrier every wave's have landed and
+      // every wave is done with tile kt - 1, whose stage then receives tile kt + 1
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (kt + 1 < it.kt1) copy_tile(kt + 1, s ^ 1);
+      const char* kl = reinterpret_cast<const char*>(&stage[s].k[0]);
+      // four accumulation chains (two per 32-key half: even and odd K steps) over four groups of four K steps; the K
+      // fragments of group g + 1 are read while the MFMAs of group g run, so LDS latency is hidden behind the matrix
+      // core
+      f32x16 acc[2][2] = {{zero16(), zero16()}, {zero16(), zero16()}};
+      auto kread = [&](int g, bf16x8 (&kf)[2][4]) {
 #pragma unroll
         for (int ksub = 0; ksub < 2; ++ksub)
-          acc[ksub][j & 1] = mfma32(cur[ksub][j], qop[4 * g + j], acc[ksub][j & 1]);
-    }
-    // order: reads of group 0; then (reads of g + 1, MFMAs of g) for g = 0..2; then the MFMAs of group 3
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-    for (int g = 0; g < 3; ++g) {
+          for (int j = 0; j < 4; ++j) {
+            const int ks = 4 * g + j;
+            kf[ksub][j] = *reinterpret_cast<const bf16x8*>(kl + ka[ks & 7] + 256 * (ks >> 3) + 16384 * ksub);
+          }
+      };
+      bf16x8 kfa[2][4], kfb[2][4];
+      kread(0, kfa);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        bf16x8 (&cur)[2][4] = (g & 1) ? kfb : kfa;
+        bf16x8 (&nxt)[2][4] = (g & 1) ? kfa : kfb;
+        if (g < 3) kread(g + 1, nxt);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int ksub = 0; ksub < 2; ++ksub)
+            acc[ksub][j & 1] = mfma32(cur[ksub][j], qop[4 * g + j], acc[ksub][j & 1]);
+      }
+      // order: reads of group 0; then (reads of g + 1, MFMAs of g) for g = 0..2; then the MFMAs of group 3
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int g = 0; g < 3; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      }
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    float mx = -INFINITY;
-    if (__builtin_amdgcn_readfirstlane(kt) >= full_tiles) {
-      // lane (ln, hh) holds keys 64 kt + 32 ksub + 8 (i >> 2) + 4 hh + (i & 3) of query tq
-      const int kl0 = kt * kBN + 4 * hh;
+      float mx = -INFINITY;
+      if (__builtin_amdgcn_readfirstlane(kt) >= full_tiles) {
+        // lane (ln, hh) holds keys 64 kt + 32 ksub + 8 (i >> 2) + 4 hh + (i & 3) of query tq
+        const int kl0 = kt * kBN + 4 * hh;
 #pragma unroll
-      for (int ksub = 0; ksub < 2; ++ksub)
+        for (int ksub = 0; ksub < 2; ++ksub)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = kl0 + 32 * ksub + 8 * (i >> 2) + (i & 3);
-          const float x = (key <= tq && key < T) ? acc[ksub][0][i] + acc[ksub][1][i] : -INFINITY;
-          sc[ksub][i] = x;
-          mx = fmaxf(mx, x);
-        }
-    } else {
+          for (int i = 0; i < 16; ++i) {
+            const int key = kl0 + 32 * ksub + 8 * (i >> 2) + (i & 3);
+            const float x = (key <= tq && key < T) ? acc[ksub][0][i] + acc[ksub][1][i] : -INFINITY;
+            sc[ksub][i] = x;
+            mx = fmaxf(mx, x);
+          }
+      } else {
 #pragma unroll
-      for (int ksub = 0; ksub < 2; ++ksub)
+        for (int ksub = 0; ksub < 2; ++ksub)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          sc[ksub][i] = acc[ksub][0][i] + acc[ksub][1][i];
-          mx = fmaxf(mx, sc[ksub][i]);
-        }
-    }
-    return fmaxf(mx, __shfl_xor(mx, 32, 64)) * csc;
-  };
-  // P = 2^(s c - m_run) of tile kt into the row sum, then O^T += V^T P^T: rows = 256 dims (8 tiles of 32), k = 64
-  // keys (4 steps of 16). The MFMAs run K step by K step, so those of step kk need only P's group kk: the
-  // exponentials of later groups overlap the matrix core.
-  auto tile_accumulate = [&](int kt, const f32x16 (&sc)[2]) {
-    const char* vl = reinterpret_cast<const char*>(&stage[kt & 1].v[0]);
-    auto vread = [&](int kk, bf16x8 (&vf)[8]) {
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) vf[mt] = *reinterpret_cast<const bf16x8*>(vl + va[kk] + 4096 * mt);
+          for (int i = 0; i < 16; ++i) {
+            sc[ksub][i] = acc[ksub][0][i] + acc[ksub][1][i];
+            mx = fmaxf(mx, sc[ksub][i]);
+          }
+      }
+      return fmaxf(mx, __shfl_xor(mx, 32, 64)) * csc;
     };
-    bf16x8 vfa[8], vfb[8];
-    vread(0, vfa);
-    const float nm = -m_run;
-    float ps = 0.f;
-    bf16x8 pb[4];
+    // P = 2^(s c - m_run) of tile kt into the row sum, then O^T += V^T P^T: rows = 256 dims (8 tiles of 32), k = 64
+    // keys (4 steps of 16). The MFMAs run K step by K step, so those of step kk need only P's group kk: the
+    // exponentials of later groups overlap the matrix core.
+    auto tile_accumulate = [&](int kt, const f32x16 (&sc)[2]) {
+      const char* vl = reinterpret_cast<const char*>(&stage[kt & 1].v[0]);
+      auto vread = [&](int kk, bf16x8 (&vf)[8]) {
 #pragma unroll
-    for (int ksub = 0; ksub < 2; ++ksub)
+        for (int mt = 0; mt < 8; ++mt) vf[mt] = *reinterpret_cast<const bf16x8*>(vl + va[kk] + 4096 * mt);
+      };
+      bf16x8 vfa[8], vfb[8];
+      vread(0, vfa);
+      const float nm = -m_run;
+      float ps = 0.f;
+      bf16x8 pb[4];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(sc[ksub][i], csc, nm));
-        ps += p;
-        pb[2 * ksub + (i >> 3)][i & 7] = (__bf16)p;
+      for (int ksub = 0; ksub < 2; ++ksub)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(sc[ksub][i], csc, nm));
+          ps += p;
+          pb[2 * ksub + (i >> 3)][i & 7] = (__bf16)p;
+        }
+      ps += __shfl_xor(ps, 32, 64);
+      l_run += ps;
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        bf16x8 (&cur)[8] = (kk & 1) ? vfb : vfa;
+        bf16x8 (&nxt)[8] = (kk & 1) ? vfa : vfb;
+        if (kk < 3) vread(kk + 1, nxt);
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) o[mt] = mfma32(cur[mt], pb[kk], o[mt]);
       }
-    ps += __shfl_xor(ps, 32, 64);
-    l_run += ps;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      bf16x8 (&cur)[8] = (kk & 1) ? vfb : vfa;
-      bf16x8 (&nxt)[8] = (kk & 1) ? vfa : vfb;
-      if (kk < 3) vread(kk + 1, nxt);
-#pragma unroll
-      for (int mt = 0; mt < 8; ++mt) o[mt] = mfma32(cur[mt], pb[kk], o[mt]);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-    for (int g = 0; g < 3; ++g) {
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int g = 0; g < 3; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      }
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    };
+
+    // Online softmax along the keys of each lane's query (lane pair l, l ^ 32 holds all 64 keys of a tile). The
+    // running max only moves (and O, l are rescaled) when a tile max exceeds it by more than 8 (base 2): p <= 2^8
+    // stays exact enough in fp32 and in the bf16 P operand. The inner loop runs the tiles that need no rescale, so O
+    // never leaves the MFMA accumulators there; the rescale (a read, multiply and write-back of all 128 accumulator
+    // registers) sits outside it and runs a few times per block (always at tile 0). Every lane has a finite score in
+    // the first tile of its item (key 0, or a split block's first key, is at or before its query), so m_run is finite
+    // from then on.
+    int kt = it.kt0;
+    while (kt < it.kt1) {
+      f32x16 sc[2];
+      float mx = tile_scores(kt, sc);
+      while (!__any(mx > m_run + 8.f)) {
+        tile_accumulate(kt, sc);
+        if (++kt == it.kt1) break;
+        mx = tile_scores(kt, sc);
+      }
+      if (kt == it.kt1) break;
+      const float mn = fmaxf(m_run, mx);
+      const float corr = __builtin_amdgcn_exp2f(m_run - mn);
+      l_run *= corr;
+      m_run = mn;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
+      tile_accumulate(kt, sc);
+      ++kt;
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+
+    // ---- a split query block: each half publishes its (O, m, l); attn_prefill_merge_kernel combines them ----
+    if (it.half >= 0) {
+      const int pair = (qb - 2 * Ls) * n_other + rem;
+      float* mine = part + ((size_t)(2 * pair + it.half) * GW + wave) * kPartFloats;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 w = {o[mt][4 * c], o[mt][4 * c + 1], o[mt][4 * c + 2], o[mt][4 * c + 3]};
+          *reinterpret_cast<f32x4*>(mine + ((mt * 4 + c) * 64 + lane) * 4) = w;
+        }
+      mine[8192 + lane] = m_run;
+      mine[8192 + 64 + lane] = l_run;
+      return;
+    }
+
+    // ---- epilogue: normalise, then gate and store whole rows through LDS ----
+    // The accumulators hold 16-byte pieces of 32 different query rows; written straight out, every gate load and
+    // output store would touch 32 rows. Instead wave w parks its normalised O (32 queries x 256 dims fp32, 32 KB) in
+    // bytes 32768 w .. of the stages (free once every wave has left the tile loop), 16-byte segment s of row r at
+    // s ^ r, and reads it back by rows: 16 lanes per 512-byte row of gate and output.
+    __syncthreads();
+    char* ob = reinterpret_cast<char*>(&stage[0]) + 32768 * wave;
+    {
+      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f32x4 w = {o[mt][4 * c] * inv, o[mt][4 * c + 1] * inv, o[mt][4 * c + 2] * inv,
+                           o[mt][4 * c + 3] * inv};
+          *reinterpret_cast<f32x4*>(ob + 1024 * ln + 16 * ((8 * mt + 2 * c + hh) ^ ln)) = w;
+        }
+    }
+    __syncthreads();
+    {
+      const int rs = lane >> 4, g16 = lane & 15;  // row 4 i + rs, dims 16 g16 .. + 15
+      u32x4 gr[8][2];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int tr = min(q0 + 4 * i + rs, T - 1);
+        const __bf16* gp = gate + ((size_t)b * T + tr) * (size_t)Hq * kPD + (size_t)h * kPD + 16 * g16;
+        gr[i][0] = *reinterpret_cast<const u32x4*>(gp);
+        gr[i][1] = *reinterpret_cast<const u32x4*>(gp + 8);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 4 * i + rs, tr = q0 + r;
+        float x[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 w = *reinterpret_cast<const f32x4*>(ob + 1024 * r + 16 * ((4 * g16 + j) ^ r));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[4 * j + e] = w[e];
+        }
+        u32x4 ov[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const u32x4 gw = gr[i][hf];
+          const float gv[8] = {bf16lo(gw[0]), bf16hi(gw[0]), bf16lo(gw[1]), bf16hi(gw[1]),
+                               bf16lo(gw[2]), bf16hi(gw[2]), bf16lo(gw[3]), bf16hi(gw[3])};
+          bf16x8 pk;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) pk[e] = (__bf16)(x[8 * hf + e] * sigmoidf_(gv[e]));
+          ov[hf] = __builtin_bit_cast(u32x4, pk);
+        }
+        if (tr < T) {
+          __bf16* op = out + ((size_t)b * T + tr) * (size_t)Hq * kPD + (size_t)h * kPD + 16 * g16;
+          *reinterpret_cast<u32x4*>(op) = ov[0];
+          *reinterpret_cast<u32x4*>(op + 8) = ov[1];
+        }
+      }
+    }
   };
 
-  // Online softmax along the keys of each lane's query (lane pair l, l ^ 32 holds all 64 keys of a tile). The
-  // running max only moves (and O, l are rescaled) when a tile max exceeds it by more than 8 (base 2): p <= 2^8
-  // stays exact enough in fp32 and in the bf16 P operand. The inner loop runs the tiles that need no rescale, so O
-  // never leaves the MFMA accumulators there; the rescale (a read, multiply and write-back of all 128 accumulator
-  // registers) sits outside it and runs a few times per block (always at tile 0). Every lane has a finite score in
-  // the first tile of its item (key 0, or a split block's first key, is at or before its query), so m_run is finite
-  // from then on.
-  int kt = it.kt0;
-  while (kt < it.kt1) {
-    f32x16 sc[2];
-    float mx = tile_scores(kt, sc);
-    while (!__any(mx > m_run + 8.f)) {
-      tile_accumulate(kt, sc);
-      if (++kt == it.kt1) break;
-      mx = tile_scores(kt, sc);
-    }
-    if (kt == it.kt1) break;
-    const float mn = fmaxf(m_run, mx);
-    const float corr = __builtin_amdgcn_exp2f(m_run - mn);
-    l_run *= corr;
-    m_run = mn;
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[mt][i] *= corr;
-    tile_accumulate(kt, sc);
-    ++kt;
-  }
-
-  // ---- a split query block: each half publishes its (O, m, l); attn_prefill_merge_kernel combines them ----
-  if (it.half >= 0) {
-    const int pair = (qb - 2 * Ls) * n_other + rem;
-    float* mine = part + ((size_t)(2 * pair + it.half) * GW + wave) * kPartFloats;
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const f32x4 w = {o[mt][4 * c], o[mt][4 * c + 1], o[mt][4 * c + 2], o[mt][4 * c + 3]};
-        *reinterpret_cast<f32x4*>(mine + ((mt * 4 + c) * 64 + lane) * 4) = w;
-      }
-    mine[8192 + lane] = m_run;
-    mine[8192 + 64 + lane] = l_run;
-    return;
-  }
-
-  // ---- epilogue: normalise, gate, store ----
-  if (tq < T) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-    const size_t rowo = ((size_t)b * T + tq) * (size_t)Hq * kPD + (size_t)h * kPD;
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int d = 32 * mt + 8 * c + 4 * hh;
-        const u32x2 gr = *reinterpret_cast<const u32x2*>(gate + rowo + d);
-        const float gv[4] = {bf16lo(gr[0]), bf16hi(gr[0]), bf16lo(gr[1]), bf16hi(gr[1])};
-        bf16x4 ov;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = (__bf16)(o[mt][4 * c + e] * inv * sigmoidf_(gv[e]));
-        *reinterpret_cast<bf16x4*>(out + rowo + d) = ov;
-      }
-    }
+  run(it0);
+  if (PAIRED && it0.qb2 >= 0) {
+    // every wave is done with the first segment's stages before the second segment's first tile is copied
+    __syncthreads();
+    run(PfItem{it0.qb2, 0, pf_tiles(it0.qb2), -1, -1});
   }
 }
 
@@ -558,6 +628,19 @@ __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __
 
 static int64_t padded_T(int64_t T) { return (T + kBN - 1) / kBN * kBN; }
 
+// Compute units of the current device, queried once per device (the paired work order needs every block resident).
+static int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 // Workspace: K rotated and V transposed ([B, Hkv, Tp, D] bf16 each), then the split blocks' partials
 // ([pairs][2 halves][wave] x kPartFloats fp32).
 struct PfLayout {
@@ -607,7 +690,9 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
   if (T > ((int64_t)1 << 30) || B > 65535 || Hkv > 65535 || T * Hq * D > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
   const int64_t nqb = (T + kBQ - 1) / kBQ;
   const int Ls = pf_split_len((int)nqb);
-  const int64_t nblocks = (int64_t)pf_items((int)nqb, Ls) * B * Hkv * ngroups;
+  const int64_t n_other = B * Hkv * ngroups;
+  const bool paired = Ls > 0 && (int64_t)pf_items((int)nqb, Ls, true) * n_other <= device_cus();
+  const int64_t nblocks = (int64_t)pf_items((int)nqb, Ls, paired) * n_other;
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
   // V^T rows are addressed with 32-bit byte offsets inside a head's [D, Tp] block
   if (Tp * kPD * 2 >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
@@ -632,9 +717,10 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
   }
 #undef Q35_KV_LAUNCH
 #define Q35_PF_LAUNCH(GG)                                                                                         \
-  hipLaunchKernelGGL(attn_prefill_kernel<GG>, dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q,    \
-                     kr, vt, (const __bf16*)gate, cos, sin, (int)pos0, (__bf16*)out, (int)T, (int)Tp, (int)Hq,     \
-                     (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B, Ls, part);                             \
+  hipLaunchKernelGGL((paired ? attn_prefill_kernel<GG, true> : attn_prefill_kernel<GG, false>),                \
+                     dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q, kr, vt, (const __bf16*)gate, \
+                     cos, sin, (int)pos0, (__bf16*)out, (int)T, (int)Tp, (int)Hq, (int)Hkv, ngroups, (int)rot,     \
+                     scale, (int)nqb, (int)B, Ls, part);                                                           \
   if (lay.npairs > 0)                                                                                             \
     hipLaunchKernelGGL(attn_prefill_merge_kernel<GG>, dim3((unsigned)lay.npairs, GG), dim3(256), 0, st, part,       \
                        (const __bf16*)gate, (__bf16*)out, (int)T, (int)Hq, (int)Hkv, ngroups, (int)B, Ls)

@@ -247,17 +247,30 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
 
   // ---- 0. stage. Threads 0-255 hold an 8 x 8 unit of k (rows 8 rg.., dims 8 cc..), threads 256-511 one of v; the
   //         units stay in registers for the transposed copies written after the K K^T phase. q goes row-major.
+  //         Every global load of the phase (k or v, q, and the gates of wave 0) is issued before any is used, so
+  //         the phase costs one memory round trip.
   const int u = tid & 255, rg = u >> 4, cc = u & 15;
   const bool isK = tid < 256;
   u32x4 raw[8];
-  {
-    const Tin* src[8];
+  const Tin* src[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const size_t tok = (size_t)b * T + t0 + min(8 * rg + i, nvalid - 1);
-      src[i] = isK ? k + (tok * Hk + kh) * kD + 8 * cc : v + (tok * H + h) * kD + 8 * cc;
-      raw[i] = raw8(src[i]);
-    }
+  for (int i = 0; i < 8; ++i) {
+    const size_t tok = (size_t)b * T + t0 + min(8 * rg + i, nvalid - 1);
+    src[i] = isK ? k + (tok * Hk + kh) * kD + 8 * cc : v + (tok * H + h) * kD + 8 * cc;
+    raw[i] = raw8(src[i]);
+  }
+  const int qrow = tid >> 2, qs0 = 4 * (tid & 3);
+  const Tin* qsrc = q + (((size_t)b * T + t0 + min(qrow, nvalid - 1)) * Hk + kh) * kD;
+  u32x4 rq[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) rq[j] = raw8(qsrc + 8 * (qs0 + j));
+  float g0 = 0.f, g1 = 0.f, b0 = 0.f, b1 = 0.f;
+  if (wave == 0) {
+    const size_t base = ((size_t)b * T + t0) * H + h;
+    if (lane < nvalid) { g0 = g[base + (size_t)lane * H]; b0 = beta[base + (size_t)lane * H]; }
+    if (64 + lane < nvalid) { g1 = g[base + (size_t)(64 + lane) * H]; b1 = beta[base + (size_t)(64 + lane) * H]; }
+  }
+  {
     float ss[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -280,26 +293,17 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
     }
   }
   {
-    const int row = tid >> 2, s0 = 4 * (tid & 3);
-    const Tin* qs = q + (((size_t)b * T + t0 + min(row, nvalid - 1)) * Hk + kh) * kD;
-    u32x4 rq[4];
     float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      rq[j] = raw8(qs + 8 * (s0 + j));
-      ss += sumsq8_in(qs + 8 * (s0 + j), rq[j]);
-    }
+    for (int j = 0; j < 4; ++j) ss += sumsq8_in(qsrc + 8 * (qs0 + j), rq[j]);
     ss += __shfl_xor(ss, 1, 64);
     ss += __shfl_xor(ss, 2, 64);
-    if ((tid & 3) == 0) rqn[row] = l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
+    if ((tid & 3) == 0) rqn[qrow] = l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(R2 + t128(row, 8 * (s0 + j))) = mask8(rq[j], row < nvalid);
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4*>(R2 + t128(qrow, 8 * (qs0 + j))) = mask8(rq[j], qrow < nvalid);
   }
   if (wave == 0) {  // gates: gamma = cumsum(g) over the pair, beta; zero past the sequence end (HF pads with 0)
-    float g0 = 0.f, g1 = 0.f, b0 = 0.f, b1 = 0.f;
-    const size_t base = ((size_t)b * T + t0) * H + h;
-    if (lane < nvalid) { g0 = g[base + (size_t)lane * H]; b0 = beta[base + (size_t)lane * H]; }
-    if (64 + lane < nvalid) { g1 = g[base + (size_t)(64 + lane) * H]; b1 = beta[base + (size_t)(64 + lane) * H]; }
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float y0 = __shfl_up(g0, off, 64), y1 = __shfl_up(g1, off, 64);
