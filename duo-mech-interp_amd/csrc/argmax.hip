@@ -16,6 +16,7 @@ __device__ __forceinline__ void amax_take(float& bv, int& bi, float v, int i) {
 
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ x, int64_t ldx, int n,
                                                            int32_t* __restrict__ idx, float* __restrict__ val) {
+  Q35_ARGS_UPFRONT(x, ldx, n, idx, val);
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* xr = x + (int64_t)row * ldx;
   float bv = -INFINITY;

@@ -56,8 +56,30 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   constexpr int NG = (G + 3) / 4;  // lane groups of the MFMA D tile that hold real heads
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  // cache_len lives on the device, so it is clamped here rather than trusted: 0 <= len <= max_len
-  const int len = min(max(cache_len[b], 0), max_len);
+  Q35_ARGS_UPFRONT(q, kc, vc, cache_len, cos_t, sin_t, rot, part, Hq, Hkv, max_len, S, scale);
+
+  // cache_len lives on the device: its read is issued here and waited for after the query loads below
+  const int len_raw = cache_len[b];
+  // 0. the raw query loads go out next: they do not depend on the cache length, whose read from device memory
+  // is a round trip of its own. Thread t takes quads of 4 dims (qi = t, t + 256, ...), with the rotation partner
+  // of each rotary quad; every load is unconditional (clamped indices, results selected afterwards).
+  const int half = rot >> 1;
+  constexpr int NQ = (G * 64 + 255) / 256;
+  u32x2 xq[NQ], pq[NQ];
+  {
+    const __bf16* qb = q + ((size_t)b * Hq + (size_t)kvh * G) * kDecD;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int qi = min(tid + 256 * u, G * 64 - 1), hh = qi >> 6, d0 = 4 * (qi & 63);
+      const int pd0 = d0 < rot ? (d0 < half ? d0 + half : d0 - half) : d0;
+      xq[u] = *reinterpret_cast<const u32x2*>(qb + hh * kDecD + d0);
+      pq[u] = *reinterpret_cast<const u32x2*>(qb + hh * kDecD + pd0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // the cache length is clamped rather than trusted: 0 <= len <= max_len
+  const int len = min(max(len_raw, 0), max_len);
   constexpr int L = 4 * kDecTile * NT;  // keys of the block's span: NT tiles per wave
   const int k_begin = s * L;
   const int k_end = min(k_begin + L, len);
@@ -142,27 +164,16 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     }
     __builtin_amdgcn_wave_barrier();
   };
-  // 1. the G query heads of this kv head, rotated at position pos, in fp32. Thread t takes quads of 4 dims
-  // (qi = t, t + 256, ...); every load is unconditional (clamped indices, results selected afterwards) so that all
-  // of them are issued together. rot is a multiple of 8, so no quad straddles rot or rot / 2.
-  const int half = rot >> 1;
-  constexpr int NQ = (G * 64 + 255) / 256;
-  u32x2 xq[NQ], pq[NQ];
+  // 1. the G query heads of this kv head, rotated at position pos, in fp32: the cos / sin rows of pos (all loads
+  // issued together). rot is a multiple of 8, so no quad straddles rot or rot / 2.
   f32x4 cq[NQ], sq[NQ];
-  {
-    const __bf16* qb = q + ((size_t)b * Hq + (size_t)kvh * G) * kDecD;
+  if (rot > 0) {
 #pragma unroll
     for (int u = 0; u < NQ; ++u) {
-      const int qi = min(tid + 256 * u, G * 64 - 1), hh = qi >> 6, d0 = 4 * (qi & 63);
-      const bool rotd = d0 < rot;
-      const int pd0 = rotd ? (d0 < half ? d0 + half : d0 - half) : d0;
-      xq[u] = *reinterpret_cast<const u32x2*>(qb + hh * kDecD + d0);
-      pq[u] = *reinterpret_cast<const u32x2*>(qb + hh * kDecD + pd0);
-      if (rot > 0) {
-        const int j0 = rotd ? (d0 < half ? d0 : d0 - half) : 0;
-        cq[u] = *reinterpret_cast<const f32x4*>(cos_t + (size_t)pos * half + j0);
-        sq[u] = *reinterpret_cast<const f32x4*>(sin_t + (size_t)pos * half + j0);
-      }
+      const int qi = min(tid + 256 * u, G * 64 - 1), d0 = 4 * (qi & 63);
+      const int j0 = d0 < rot ? (d0 < half ? d0 : d0 - half) : 0;
+      cq[u] = *reinterpret_cast<const f32x4*>(cos_t + (size_t)pos * half + j0);
+      sq[u] = *reinterpret_cast<const f32x4*>(sin_t + (size_t)pos * half + j0);
     }
   }
   // K / V tile registers, two sets used alternately (indices are compile-time after unrolling). Loads are issued
@@ -264,6 +275,7 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __restrict__ part,
                                                                 const __bf16* __restrict__ gate,
                                                                 __bf16* __restrict__ out, int Hq, int Hkv, int S) {
+  Q35_ARGS_UPFRONT(part, gate, out, Hq, Hkv, S);
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int G = Hq / Hkv, kvh = h / G, hh = h % G;
   const int grp = tid >> 5, d = 32 * blockIdx.z + (tid & 31);

@@ -225,6 +225,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     const __bf16* __restrict__ gate, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos0,
     __bf16* __restrict__ out, int T, int Tp, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb, int B,
     int Ls, float* __restrict__ part) {
+  Q35_ARGS_UPFRONT(q, kr, vt, gate, cos_t, sin_t, pos0, out, T, Tp, Hq, Hkv, ngroups, rot, scale, nqb, B, Ls, part);
   __shared__ PfStage stage[2];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -586,6 +587,7 @@ __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __
                                                                  const __bf16* __restrict__ gate,
                                                                  __bf16* __restrict__ out, int T, int Hq, int Hkv,
                                                                  int ngroups, int B, int Ls) {
+  Q35_ARGS_UPFRONT(part, gate, out, T, Hq, Hkv, ngroups, B, Ls);
   const int pair = blockIdx.x, wave = blockIdx.y, tid = threadIdx.x;
   const int n_other = B * Hkv * ngroups;
   const int qb = 2 * Ls + pair / n_other, rem = pair % n_other;

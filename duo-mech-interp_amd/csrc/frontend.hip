@@ -126,6 +126,7 @@ __global__ __launch_bounds__(256) void gdn_conv1_kernel(const float* __restrict_
                                                         Tout* __restrict__ vo, float* __restrict__ go,
                                                         float* __restrict__ betao, int C, int Kd, int Vd, int Hv,
                                                         int K) {
+  Q35_ARGS_UPFRONT(y, ldy, cw, cbias, cstate, A_log, dt_bias, b_off, a_off, qo, ko, vo, go, betao, C, Kd, Vd, Hv, K);
   const int b = blockIdx.y, tid = threadIdx.x;
   const int nb = (C / 4 + 255) / 256;
   const float* row = y + (int64_t)b * ldy;
@@ -181,6 +182,7 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict_
                                                             int64_t ldz, const float* __restrict__ w,
                                                             const float* __restrict__ head_scale, T* __restrict__ out,
                                                             int64_t M, int Hv, float eps) {
+  Q35_ARGS_UPFRONT(o, z, ldz, w, head_scale, out, M, Hv, eps);
   const int lane = threadIdx.x & 63;
   const int64_t job = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (job >= M * Hv) return;
@@ -210,6 +212,8 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const float* __restrict_
                                                         __bf16* __restrict__ v_out, __bf16* __restrict__ k_cache,
                                                         __bf16* __restrict__ v_cache, int max_len, int T, int Hq,
                                                         int Hkv, int64_t M) {
+  Q35_ARGS_UPFRONT(y, ldy, qw, kw, eps, cos_t, sin_t, rot, pos, q_out, gate_out, k_out, v_out, k_cache, v_cache,
+                   max_len, T, Hq, Hkv, M);
   constexpr int D = 256;
   const int lane = threadIdx.x & 63;
   const int jobs = Hq + 2 * Hkv;
@@ -277,6 +281,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float* __restrict__ x,
                                                           const float* __restrict__ y, int64_t ldy,
                                                           const float* __restrict__ w, float* __restrict__ h,
                                                           int64_t ldh, int H, float eps) {
+  Q35_ARGS_UPFRONT(x, ldx, y, ldy, w, h, ldh, H, eps);
   const int64_t m = blockIdx.x;
   const int tid = threadIdx.x;
   float* xr = x + m * ldx;

@@ -67,6 +67,7 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(const Tin* __restric
                                                             const float* __restrict__ beta, const float* s_in,
                                                             float* s_out, Tin* __restrict__ o, int T, int Hk, int H,
                                                             float scale, int l2norm) {
+  Q35_ARGS_UPFRONT(q, k, v, g, beta, s_in, s_out, o, T, Hk, H, scale, l2norm);
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int cq = tid & 7;   // column quad of this thread

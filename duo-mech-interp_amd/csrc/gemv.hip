@@ -70,6 +70,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
                                                    const q35_push* __restrict__ pushes, int npush, int T,
                                                    const float* __restrict__ xadd, const float* __restrict__ nw,
                                                    float eps, float* __restrict__ xout) {
+  Q35_ARGS_UPFRONT(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, xadd, nw, eps, xout);
   constexpr int E = WChunk<TW>::kElems;  // weights per lane per 16-byte load
   constexpr int KS = 16 * E;             // inputs per K step
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [MP][K]

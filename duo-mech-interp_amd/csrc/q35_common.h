@@ -23,6 +23,39 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
+// Kernel entry: fetch the listed kernel arguments into scalar registers in one batch. Scalar loads complete out of
+// order, so every wait for one of them waits for all of them. An argument the compiler would fetch later (behind a
+// branch, or after a value read from device memory) costs one more memory round trip before the kernel's first
+// load; an empty asm that takes them all as scalar operands makes the compiler fetch them together.
+#define Q35_SGPR_OPERAND(a) "s"(a)
+#define Q35_FE_1(m, a) m(a)
+#define Q35_FE_2(m, a, ...) m(a), Q35_FE_1(m, __VA_ARGS__)
+#define Q35_FE_3(m, a, ...) m(a), Q35_FE_2(m, __VA_ARGS__)
+#define Q35_FE_4(m, a, ...) m(a), Q35_FE_3(m, __VA_ARGS__)
+#define Q35_FE_5(m, a, ...) m(a), Q35_FE_4(m, __VA_ARGS__)
+#define Q35_FE_6(m, a, ...) m(a), Q35_FE_5(m, __VA_ARGS__)
+#define Q35_FE_7(m, a, ...) m(a), Q35_FE_6(m, __VA_ARGS__)
+#define Q35_FE_8(m, a, ...) m(a), Q35_FE_7(m, __VA_ARGS__)
+#define Q35_FE_9(m, a, ...) m(a), Q35_FE_8(m, __VA_ARGS__)
+#define Q35_FE_10(m, a, ...) m(a), Q35_FE_9(m, __VA_ARGS__)
+#define Q35_FE_11(m, a, ...) m(a), Q35_FE_10(m, __VA_ARGS__)
+#define Q35_FE_12(m, a, ...) m(a), Q35_FE_11(m, __VA_ARGS__)
+#define Q35_FE_13(m, a, ...) m(a), Q35_FE_12(m, __VA_ARGS__)
+#define Q35_FE_14(m, a, ...) m(a), Q35_FE_13(m, __VA_ARGS__)
+#define Q35_FE_15(m, a, ...) m(a), Q35_FE_14(m, __VA_ARGS__)
+#define Q35_FE_16(m, a, ...) m(a), Q35_FE_15(m, __VA_ARGS__)
+#define Q35_FE_17(m, a, ...) m(a), Q35_FE_16(m, __VA_ARGS__)
+#define Q35_FE_18(m, a, ...) m(a), Q35_FE_17(m, __VA_ARGS__)
+#define Q35_FE_19(m, a, ...) m(a), Q35_FE_18(m, __VA_ARGS__)
+#define Q35_FE_20(m, a, ...) m(a), Q35_FE_19(m, __VA_ARGS__)
+#define Q35_FE_21(m, a, ...) m(a), Q35_FE_20(m, __VA_ARGS__)
+#define Q35_FE_22(m, a, ...) m(a), Q35_FE_21(m, __VA_ARGS__)
+#define Q35_FE_23(m, a, ...) m(a), Q35_FE_22(m, __VA_ARGS__)
+#define Q35_FE_24(m, a, ...) m(a), Q35_FE_23(m, __VA_ARGS__)
+#define Q35_FE_PICK(_1, _2, _3, _4, _5, _6, _7, _8, _9, _10, _11, _12, _13, _14, _15, _16, _17, _18, _19, _20, _21, _22, _23, _24, NAME, ...) NAME
+#define Q35_FOR_EACH(m, ...) Q35_FE_PICK(__VA_ARGS__, Q35_FE_24, Q35_FE_23, Q35_FE_22, Q35_FE_21, Q35_FE_20, Q35_FE_19, Q35_FE_18, Q35_FE_17, Q35_FE_16, Q35_FE_15, Q35_FE_14, Q35_FE_13, Q35_FE_12, Q35_FE_11, Q35_FE_10, Q35_FE_9, Q35_FE_8, Q35_FE_7, Q35_FE_6, Q35_FE_5, Q35_FE_4, Q35_FE_3, Q35_FE_2, Q35_FE_1)(m, __VA_ARGS__)
+#define Q35_ARGS_UPFRONT(...) asm volatile("" ::Q35_FOR_EACH(Q35_SGPR_OPERAND, __VA_ARGS__))
+
 namespace q35 {
 
 // Element types the kernels accept for activations (q, k, v, o, gate).

@@ -10,6 +10,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void resid_add_rows_kernel(T* __restrict__ x, const float* __restrict__ vecs,
                                                              const int32_t* __restrict__ vec_of_row, int64_t rows,
                                                              int64_t Tlen, int H, int nvec) {
+  Q35_ARGS_UPFRONT(x, vecs, vec_of_row, rows, Tlen, H, nvec);
   // one block per (row, position); 4 elements per thread per step
   const int64_t m = blockIdx.x;  // flattened (row, position)
   const int64_t r = m / Tlen;

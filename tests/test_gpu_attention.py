@@ -17,10 +17,14 @@ def _tables(n):
 
 
 # T >= 449 (at least 8 key tiles in the last query block) runs the long query blocks as two key-split halves that
-# are merged in the kernel: T 1000, 600 and 777 cover that with GQA 4, 8 (two head groups per kv head) and 1.
+# are merged in a third kernel: T 1000, 600 and 777 cover that with GQA 4, 8 (two head groups per kv head) and 1.
+# Those fit 256 CUs as paired items (the second half of a long block, then a short whole block, in one block; 600
+# and 777 leave whole blocks unpaired); B 4 T 1000 GQA 1 and B 5 T 1000 GQA 2 exceed it and run as independent
+# items in longest-first order.
 @pytest.mark.parametrize("B,T,Hq,Hkv,pos0", [(1, 1, 8, 2, 0), (2, 100, 8, 2, 0), (1, 257, 8, 2, 5),
                                              (1, 96, 4, 4, 0), (1, 70, 8, 1, 3), (1, 64, 16, 2, 0),
-                                             (1, 1000, 8, 2, 3), (2, 600, 16, 2, 0), (1, 777, 4, 4, 0)])
+                                             (1, 1000, 8, 2, 3), (2, 600, 16, 2, 0), (1, 777, 4, 4, 0),
+                                             (4, 1000, 8, 8, 0), (5, 1000, 4, 2, 1)])
 def test_prefill_small(B, T, Hq, Hkv, pos0):
     dev = device()
     inp = workloads.attn_prefill_inputs(B=B, T=T, Hq=Hq, Hkv=Hkv, seed=T)
