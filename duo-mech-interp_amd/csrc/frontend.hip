@@ -176,6 +176,174 @@ __global__ __launch_bounds__(256) void gdn_conv1_kernel(const float* __restrict_
   }
 }
 
+// One decode step (T = 1) of a Gated DeltaNet layer after its input projection, in one block of 1024 threads per
+// (head h, row b), for Hk = Hv and dk = dv = 128: the q / k / v channels of head h through the causal conv + SiLU
+// (their conv state advanced), beta and g, the recurrent update of the head's 128 x 128 fp32 state, and the gated
+// RMSNorm of its output. The arithmetic and its reduction order are those of gdn_conv1_kernel, gdn_recurrent_kernel
+// (T = 1) and gated_rmsnorm_kernel in fp32 (the results agree to rounding; a multiply-add may be contracted
+// differently), and the conv state is advanced identically. The step saves two launches and the round trips of
+// q, k, v, g, beta and o through memory.
+// Threads 0..95 own one channel quad of the conv each (q, k, v: 32 quads each), thread 96 the gate terms. For the
+// state, the block is four copies of gdn_recurrent_kernel's 256-thread layout, one per 32-column slice: thread t
+// holds the float4 of columns 32 (t / 256) + 4 (t % 8) .. + 3 in rows (t % 256) / 8 + 32 i.
+constexpr int kFD = 128;
+__global__ __launch_bounds__(1024) void gdn_decode_fused_kernel(
+    const float* __restrict__ y, int64_t ldy, const float* __restrict__ cw, const float* __restrict__ cbias,
+    float* __restrict__ cstate, const float* __restrict__ A_log, const float* __restrict__ dt_bias, int b_off,
+    int a_off, int z_off, float* __restrict__ S, const float* __restrict__ nw, const float* __restrict__ head_scale,
+    float eps, float scale, float* __restrict__ out, int H, int C, int K) {
+  Q35_ARGS_UPFRONT(y, ldy, cw, cbias, cstate, A_log, dt_bias, b_off, a_off, z_off, S, nw, head_scale, eps, scale, out,
+                   H, C, K);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const float* row = y + (int64_t)b * ldy;
+  __shared__ f32x4 vecs[3][kFD / 4];  // q, k, v of head h after the conv + SiLU
+  __shared__ f32x4 red[16][8][2];     // [wave][column quad][S^T k | S^T q]
+  __shared__ float ob[kFD];
+  __shared__ float gates[2];          // beta, g
+
+  // ---- 0. every load first: conv operands (threads 0..95), gate inputs (thread 96), the state slice, and the
+  //         gated norm's z, w (wave 0)
+  const bool conv_t = tid < 96;
+  const int cr = tid >> 5, c4 = 4 * (tid & 31);
+  const int ch = cr * H * kFD + h * kFD + c4;  // q: h D + c4, k: H D + h D + c4, v: 2 H D + h D + c4
+  float w[4][kConvMaxK];
+  f32x4 bias = zero4(), xin = zero4();
+  f32x4 sx[kConvMaxK - 1];
+  float* st = cstate + (size_t)b * (K - 1) * C;
+  if (conv_t) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int i = 0; i < kConvMaxK; ++i) w[e][i] = i < K ? cw[(size_t)(ch + e) * K + i] : 0.f;
+    if (cbias) bias = *reinterpret_cast<const f32x4*>(cbias + ch);
+#pragma unroll
+    for (int j = 0; j < kConvMaxK - 1; ++j)
+      sx[j] = j < K - 1 ? *reinterpret_cast<const f32x4*>(st + (size_t)j * C + ch) : zero4();
+    xin = *reinterpret_cast<const f32x4*>(row + ch);
+  }
+  float gb = 0.f, ga = 0.f, gA = 0.f, gdt = 0.f;
+  if (tid == 96) {
+    gb = row[b_off + h];
+    ga = row[a_off + h];
+    gA = A_log[h];
+    gdt = dt_bias[h];
+  }
+  const int sl = tid >> 8, tp = tid & 255, cq = tp & 7, rg = tp >> 3;
+  const int j0 = 32 * sl + 4 * cq;
+  float* sb = S + ((size_t)b * H + h) * kFD * kFD;
+  f32x4 s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = *reinterpret_cast<const f32x4*>(sb + (size_t)(rg + 32 * i) * kFD + j0);
+  float z0 = 0.f, z1 = 0.f, w0 = 0.f, w1 = 0.f, hs = 1.f;
+  if (wave == 0) {
+    z0 = row[z_off + h * kFD + 2 * lane];
+    z1 = row[z_off + h * kFD + 2 * lane + 1];
+    w0 = nw[2 * lane];
+    w1 = nw[2 * lane + 1];
+    if (head_scale) hs = head_scale[h];
+  }
+
+  // ---- 1. conv + SiLU (gdn_conv1_kernel's order), conv state <- [old rows 1 .. K-2 | input]; gate terms
+  if (conv_t) {
+    f32x4 acc = bias;
+#pragma unroll
+    for (int i = 0; i < kConvMaxK; ++i) {
+      if (i >= K) break;
+      const f32x4 x = i < K - 1 ? sx[i] : xin;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] += w[e][i] * x[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = silu_f(acc[e]);
+    vecs[cr][tid & 31] = acc;
+#pragma unroll
+    for (int j = 0; j < kConvMaxK - 1; ++j) {
+      if (j >= K - 1) break;
+      *reinterpret_cast<f32x4*>(st + (size_t)j * C + ch) = j + 1 < K - 1 ? sx[j + 1] : xin;
+    }
+  }
+  if (tid == 96) {
+    gates[0] = 1.f / (1.f + __expf(-gb));
+    gates[1] = -__expf(gA) * softplus_f(ga + gdt);
+  }
+  __syncthreads();
+
+  // ---- 2. the recurrent step (gdn_recurrent_kernel's order): column sums of S k and S q over the slice's rows
+  const float* qv = reinterpret_cast<const float*>(&vecs[0][0]);
+  const float* kv = reinterpret_cast<const float*>(&vecs[1][0]);
+  const float* vv = reinterpret_cast<const float*>(&vecs[2][0]);
+  float kr[4], qr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kr[i] = kv[rg + 32 * i];
+    qr[i] = qv[rg + 32 * i];
+  }
+  f32x4 a, c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = s[0][e] * kr[0] + s[1][e] * kr[1] + s[2][e] * kr[2] + s[3][e] * kr[3];
+    c[e] = s[0][e] * qr[0] + s[1][e] * qr[1] + s[2][e] * qr[2] + s[3][e] * qr[3];
+  }
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[e] += __shfl_xor(a[e], off, 64);
+      c[e] += __shfl_xor(c[e], off, 64);
+    }
+  }
+  if (lane < 8) {
+    red[wave][lane][0] = a;
+    red[wave][lane][1] = c;
+  }
+  const float q20 = qv[2 * lane], q21 = qv[2 * lane + 1], k20 = kv[2 * lane], k21 = kv[2 * lane + 1];
+  float sq = q20 * q20 + q21 * q21;
+  float sk = k20 * k20 + k21 * k21;
+  float sqk = q20 * k20 + q21 * k21;
+  sq = wave_sum(sq);
+  sk = wave_sum(sk);
+  sqk = wave_sum(sqk);
+  __syncthreads();
+  f32x4 A = red[4 * sl][cq][0], Cs = red[4 * sl][cq][1];
+#pragma unroll
+  for (int w2 = 1; w2 < 4; ++w2) {
+    const f32x4 a2 = red[4 * sl + w2][cq][0], c2 = red[4 * sl + w2][cq][1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { A[e] += a2[e]; Cs[e] += c2[e]; }
+  }
+  const float rk = rsqrtf(sk + 1e-6f);
+  const float rqs = rsqrtf(sq + 1e-6f) * scale;
+  const float qk = sqk * rqs * rk;
+  const float beta = gates[0], alpha = expf(gates[1]);
+  float kk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kk[i] = kr[i] * rk;
+  f32x4 o4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float d = beta * (vv[j0 + e] - alpha * rk * A[e]);
+    o4[e] = alpha * rqs * Cs[e] + qk * d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i][e] = alpha * s[i][e] + kk[i] * d;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<f32x4*>(sb + (size_t)(rg + 32 * i) * kFD + j0) = s[i];
+  if (rg == 0) *reinterpret_cast<f32x4*>(&ob[j0]) = o4;
+  __syncthreads();
+
+  // ---- 3. gated RMSNorm of the head's output (gated_rmsnorm_kernel's order)
+  if (wave == 0) {
+    const float x0 = ob[2 * lane], x1 = ob[2 * lane + 1];
+    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float r = rsqrtf(ss * (1.f / 128.f) + eps);
+    const float n0 = x0 * r, n1 = x1 * r;
+    float* orw = out + ((size_t)b * H + h) * kFD;
+    orw[2 * lane] = w0 * n0 * silu_f(z0) * hs;
+    orw[2 * lane + 1] = w1 * n1 * silu_f(z1) * hs;
+  }
+}
+
 // One wave per (token m, head h) of o [M, Hv, dv]; dv = 128 (two values per lane). Four waves per block.
 template <typename T>
 __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict__ o, const float* __restrict__ z,
@@ -334,6 +502,28 @@ extern "C" int q35_add_rmsnorm(float* x, int64_t ldx, const float* y, int64_t ld
     return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)M), dim3(256), 0, st, x, ldx, y, ldy, w, h, ldh, (int)H, eps);
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+extern "C" int q35_gdn_decode_fused(const float* y, int64_t ldy, const float* conv_w, const float* conv_bias,
+                                    float* conv_state, const float* A_log, const float* dt_bias, int64_t b_off,
+                                    int64_t a_off, int64_t z_off, float* state, const float* norm_w,
+                                    const float* head_scale, float eps, float scale, float* out, int64_t B, int64_t H,
+                                    int64_t d, int64_t K, q35_stream_t stream) {
+  using namespace q35;
+  if (!y || !conv_w || !conv_state || !A_log || !dt_bias || !state || !norm_w || !out) return Q35_EINVAL;
+  if (B <= 0 || H <= 0 || d <= 0 || K < 2) return Q35_EINVAL;
+  const int64_t C = 3 * H * d, Vd = H * d;
+  if (ldy < C || b_off < 0 || a_off < 0 || z_off < 0 || b_off + H > ldy || a_off + H > ldy || z_off + Vd > ldy)
+    return Q35_EINVAL;
+  if (d != kFD || K > kConvMaxK || (ldy & 3) || ((uintptr_t)y & 15) || ((uintptr_t)conv_state & 15))
+    return Q35_EUNSUPPORTED;
+  if (conv_bias && ((uintptr_t)conv_bias & 15)) return Q35_EUNSUPPORTED;
+  if (B > 65535 || H > 65535 || B * ldy > ((int64_t)1 << 40) || C > 0x7fffffff) return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(gdn_decode_fused_kernel, dim3((unsigned)H, (unsigned)B), dim3(1024), 0, st, y, ldy, conv_w,
+                     conv_bias, conv_state, A_log, dt_bias, (int)b_off, (int)a_off, (int)z_off, state, norm_w,
+                     head_scale, eps, scale, out, (int)H, (int)C, (int)K);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 

@@ -16,7 +16,8 @@ EXPORTS = [
     "q35_gdn_recurrent", "q35_gdn_chunk_workspace_bytes", "q35_gdn_chunk_prefill",
     "q35_gated_attn_prefill_workspace_bytes", "q35_gated_attn_prefill", "q35_gated_attn_decode_workspace_bytes",
     "q35_gated_attn_decode",
-    "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv", "q35_swiglu_push",
+    "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
+    "q35_swiglu_push",
     "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm",
 ]
 
@@ -44,6 +45,8 @@ _SIGS = {
     "q35_resid_add_rows": ([P, P, P, I64, I64, I64, I64, I32, P], I32),
     "q35_gdn_conv": ([P, I64, P, P, P, P, P, I64, I64, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, P], I32),
     "q35_gated_rmsnorm": ([P, P, I64, P, P, P, I64, I64, I64, F32, I32, P], I32),
+    "q35_gdn_decode_fused": ([P, I64, P, P, P, P, P, I64, I64, I64, P, P, P, F32, F32, P, I64, I64, I64, I64, P],
+                             I32),
     "q35_attn_prep": ([P, I64, P, P, F32, P, P, I64, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I32),
     "q35_gemv": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
     "q35_swiglu_push": ([P, P, I64, I64, P, I64, I64, P], I32),

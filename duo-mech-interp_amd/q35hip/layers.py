@@ -72,6 +72,13 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     # one GEMM for every projection of the token: y row = [qkv (C) | z (Vd) | b (Hv) | a (Hv)], the engine's fused
     # layout (engine/kernels_qwen35.js:129-131)
     y = linear(x, gdn_in_weight(p), *_q8(p, "_in_fused"), prenorm=prenorm)
+    if T == 1 and Hk == Hv and dk == dv == 128 and x.dtype == torch.float32:
+        # the decode step's conv, recurrent rule and gated norm in one launch (the same arithmetic as the three
+        # kernels below)
+        o = ops.gdn_decode_fused_(y.view(B, y.shape[-1]), p["conv1d"], conv_state, p["A_log"], p["dt_bias"],
+                                  rec_state, p["norm"], b_off=C + Vd, a_off=C + Vd + Hv, z_off=C,
+                                  head_scale=head_scale, eps=eps)
+        return linear(o.view(B, 1, Vd), p["out_proj"], *_q8(p, "out_proj"))
     q, k, v, g, beta = ops.gdn_conv(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], num_k_heads=Hk,
                                     head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=C + Vd, a_off=C + Vd + Hv,
                                     out_dtype=x.dtype)

@@ -67,6 +67,9 @@ _LIB.define("gdn_conv(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) con
             "Tensor dt_bias, int b_off, int a_off, int Hk, int dk, int Hv, int dv, bool bf16_out) "
             "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
 _LIB.define("gated_rmsnorm(Tensor o, Tensor z, Tensor w, Tensor? head_scale, float eps) -> Tensor")
+_LIB.define("gdn_decode_fused_(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
+            "Tensor dt_bias, int b_off, int a_off, int z_off, Tensor(b!) state, Tensor norm_w, Tensor? head_scale, "
+            "float eps, float scale) -> Tensor")
 _LIB.define("gemv_(Tensor x, Tensor W, Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
 _LIB.define("swiglu_push(Tensor gu, Tensor? pushes, int T) -> Tensor")
 _LIB.define("add_rmsnorm_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tensor")
@@ -233,6 +236,35 @@ def _gdn_conv_impl(y, conv_w, conv_bias, conv_state, A_log, dt_bias, b_off, a_of
     return q, k, v, g, beta
 
 
+def _gdn_decode_fused_impl(y, conv_w, conv_bias, conv_state, A_log, dt_bias, b_off, a_off, z_off, state, norm_w,
+                           head_scale, eps, scale):
+    _on_gpu(conv_w, conv_bias, conv_state, A_log, dt_bias, state, norm_w, head_scale)
+    _require(y.is_cuda and y.dtype == torch.float32 and y.dim() == 2 and y.stride(1) == 1,
+             "y: [B, W] fp32 with unit column stride (one projection row per sequence)")
+    B, W = y.shape
+    _require(state.dtype == torch.float32 and state.dim() == 4 and state.is_contiguous()
+             and state.shape[0] == B and state.shape[2] == state.shape[3], "state: [B, H, d, d] fp32 dense")
+    H, d = state.shape[1], state.shape[2]
+    C = 3 * H * d
+    _require(conv_w.dim() == 2 and conv_w.shape[0] == C and conv_w.dtype == torch.float32 and conv_w.is_contiguous(),
+             "conv_w: [C, K] fp32 dense")
+    K = conv_w.shape[1]
+    _require(conv_state.dtype == torch.float32 and tuple(conv_state.shape) == (B, K - 1, C)
+             and conv_state.is_contiguous(), "conv_state: [B, K - 1, C] fp32 dense")
+    _require(A_log.numel() == H and dt_bias.numel() == H and norm_w.numel() == d, "A_log, dt_bias: [H]; norm_w: [d]")
+    for t in (A_log, dt_bias, norm_w, head_scale):
+        _require(t is None or (t.dtype == torch.float32 and t.is_contiguous()), "gate and norm tensors: fp32 dense")
+    if head_scale is not None:
+        _require(head_scale.numel() == H, "head_scale: [H]")
+    out = torch.empty(B, H * d, dtype=torch.float32, device=y.device)
+    st = _lib.lib().q35_gdn_decode_fused(_ptr(y), y.stride(0), _ptr(conv_w), _ptr(conv_bias), _ptr(conv_state),
+                                         _ptr(A_log), _ptr(dt_bias), int(b_off), int(a_off), int(z_off), _ptr(state),
+                                         _ptr(norm_w), _ptr(head_scale), float(eps), float(scale), _ptr(out), B, H, d,
+                                         K, _stream(y))
+    check(st, "q35_gdn_decode_fused")
+    return out
+
+
 def _gated_rmsnorm_impl(o, z, w, head_scale, eps):
     _on_gpu(o, w, head_scale)
     _require(o.dtype in _DT and o.dim() >= 2, "o: [..., Hv, dv] fp32 or bf16")
@@ -370,6 +402,7 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gdn_chunk_prefill", _gdn_chunk_impl), ("gated_attn_prefill", _attn_prefill_impl),
                      ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
                      ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl),
+                     ("gdn_decode_fused_", _gdn_decode_fused_impl),
                      ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
                      ("add_rmsnorm_", _add_rmsnorm_impl), ("argmax_rows_", _argmax_rows_impl),
                      ("gemv_norm_", _gemv_norm_impl)]:
@@ -394,6 +427,8 @@ _LIB.impl("gated_attn_decode",
           lambda q, kc, vc, gate, cl, cos, sin, scale, splits: q.new_empty(q.shape[0], q.shape[1] * q.shape[2]),
           "Meta")
 _LIB.impl("resid_add_rows_", lambda x, vecs, vor: None, "Meta")
+_LIB.impl("gdn_decode_fused_", lambda y, cw, cb, cs, Al, dt, bo, ao, zo, st, nw, hs, eps, sc:
+          y.new_empty(y.shape[0], st.shape[1] * st.shape[2]), "Meta")
 _LIB.impl("argmax_rows_", lambda x, idx: None, "Meta")
 _LIB.impl("gemv_norm_", lambda x, xa, xo, nw, eps, W, ws, y, e, pushes, T: None, "Meta")
 
@@ -466,6 +501,20 @@ def gdn_conv(y, conv_w, conv_state, A_log, dt_bias, *, num_k_heads, head_k_dim, 
     return torch.ops.q35.gdn_conv(y, w.float().contiguous(), conv_bias, conv_state, A_log.float().contiguous(),
                                   dt_bias.float().contiguous(), int(b_off), int(a_off), int(num_k_heads),
                                   int(head_k_dim), int(num_v_heads), int(head_v_dim), out_dtype == torch.bfloat16)
+
+
+def gdn_decode_fused_(y, conv_w, conv_state, A_log, dt_bias, state, norm_w, *, b_off, a_off, z_off, head_scale=None,
+                      conv_bias=None, eps=1e-6, scale=None):
+    """One Gated DeltaNet decode step after the input projection, in one launch (gdn_conv for one token, the
+    recurrent rule with l2norm on the state, gated_rmsnorm; HF:454-543 for a cached token): y [B, W] fp32 rows of
+    the fused projection, conv_state [B, K - 1, C] and state [B, H, d, d] advanced in place (Hk = Hv = H,
+    dk = dv = d = 128). Returns the gated-normed output [B, H * d] fp32."""
+    H, d = state.shape[1], state.shape[2]
+    w = conv_w.reshape(conv_w.shape[0], conv_w.shape[-1])
+    return torch.ops.q35.gdn_decode_fused_(y, w.float().contiguous(), conv_bias, conv_state,
+                                           A_log.float().contiguous(), dt_bias.float().contiguous(), int(b_off),
+                                           int(a_off), int(z_off), state, norm_w.float().contiguous(), head_scale,
+                                           float(eps), float(d ** -0.5 if scale is None else scale))
 
 
 def gated_rmsnorm(o, z, w, head_scale=None, eps=1e-6):

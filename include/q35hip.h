@@ -19,6 +19,8 @@
  *   q35_gdn_conv             HF:454-499 (causal_conv1d_fn / causal_conv1d_update + SiLU, split, beta, g);
  *                            engine/kernels_qwen35.js:127-178 `conv` + `convState`, :226-229 (gate terms of `delta`)
  *   q35_gated_rmsnorm        HF:168-184 Qwen3_5RMSNormGated; engine/kernels_qwen35.js:237-243 (epilogue of `delta`)
+ *   q35_gdn_decode_fused     HF:454-543 for one cached token: q35_gdn_conv + q35_gdn_recurrent +
+ *                            q35_gated_rmsnorm in one launch; engine/kernels_qwen35.js:127-247
  *   q35_attn_prep            HF:667-680 (q / gate split, q_norm / k_norm, partial RoPE of k, cache update);
  *                            engine/kernels_qwen35.js:18-69 `attnPrep`
  *   q35_gemv                 engine/kernels.js:57-90 `matvec` (int8 weights; per output channel here) and, with the
@@ -162,6 +164,23 @@ int q35_gdn_conv(const float* y, int64_t ldy, const float* conv_w, const float* 
                  const float* A_log, const float* dt_bias, int64_t b_off, int64_t a_off, void* q, void* k, void* v,
                  float* g, float* beta, int64_t B, int64_t T, int64_t Hk, int64_t dk, int64_t Hv, int64_t dv,
                  int64_t K, int dtype, q35_stream_t stream);
+
+/*
+ * One decode step of a Gated DeltaNet layer after its input projection, fused: q35_gdn_conv (T = 1), then
+ * q35_gdn_recurrent (one token, l2norm on, fp32) on the head's state, then q35_gated_rmsnorm, with the same
+ * arithmetic in the same reduction order (results equal to fp32 rounding). HF:454-543 for one cached token
+ * (causal_conv1d_update, torch_recurrent_gated_delta_rule, Qwen3_5RMSNormGated); engine/kernels_qwen35.js:127-247
+ * (`conv`, `convState`, `delta`).
+ *   y: [B, ldy] fp32 with the q|k|v channels at [0, C), C = 3 H d (Hk = Hv = H, dk = dv = d), z at z_off, b at b_off,
+ *      a at a_off; conv_w [C, K], conv_bias [C] or NULL, conv_state [B, K - 1, C] (advanced in place);
+ *   A_log, dt_bias, head_scale (or NULL): [H]; norm_w: [d]; state: [B, H, d, d] fp32 (updated in place);
+ *   scale: the q scale (1 / sqrt(d)); out: [B, H d] fp32, the gated-normed output.
+ *   d = 128, K <= 8; y, conv_state (and conv_bias) 16-byte aligned, ldy a multiple of 4.
+ */
+int q35_gdn_decode_fused(const float* y, int64_t ldy, const float* conv_w, const float* conv_bias,
+                         float* conv_state, const float* A_log, const float* dt_bias, int64_t b_off, int64_t a_off, int64_t z_off,
+                         float* state, const float* norm_w, const float* head_scale, float eps, float scale,
+                         float* out, int64_t B, int64_t H, int64_t d, int64_t K, q35_stream_t stream);
 
 /*
  * Gated RMSNorm per (token, head): out = w * (o * rsqrt(mean(o^2) + eps)) * silu(z) * head_scale[h], the

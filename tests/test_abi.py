@@ -23,7 +23,8 @@ def declared_functions():
 def test_header_declares_the_boundary():
     names = declared_functions()
     for n in ["q35_gdn_recurrent", "q35_gdn_chunk_prefill", "q35_gated_attn_prefill", "q35_gated_attn_decode",
-              "q35_resid_add_rows", "q35_gdn_conv", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
+              "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep",
+              "q35_gemv",
               "q35_swiglu_push", "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm"]:
         assert n in names
 
@@ -92,6 +93,13 @@ def test_validation_rejects_without_launching():
     assert L.q35_gdn_conv(fake, 6176, fake, None, fake, fake, fake, 6144, 6160, fake, fake, fake, fake, fake, 1, 1,
                           16, 128, 16, 128, 9, 0, None) == 2
     assert L.q35_gated_rmsnorm(fake, fake, 2048, fake, None, fake, 4, 16, 64, 1e-6, 0, None) == 2
+    # fused GDN decode step: null pointers, a z window past the row, d != 128 (H 16, d 128: C 6144, ldy 8224)
+    assert L.q35_gdn_decode_fused(None, 8224, fake, None, fake, fake, fake, 8192, 8208, 6144, fake, fake, None, 1e-6,
+                                  0.088, fake, 1, 16, 128, 4, None) == 1
+    assert L.q35_gdn_decode_fused(fake, 8224, fake, None, fake, fake, fake, 8192, 8208, 7000, fake, fake, None, 1e-6,
+                                  0.088, fake, 1, 16, 128, 4, None) == 1
+    assert L.q35_gdn_decode_fused(fake, 4128, fake, None, fake, fake, fake, 4096, 4112, 3072, fake, fake, None, 1e-6,
+                                  0.125, fake, 1, 16, 64, 4, None) == 2
     assert L.q35_gated_rmsnorm(fake, fake, 100, fake, None, fake, 4, 16, 128, 1e-6, 0, None) == 1
     assert L.q35_attn_prep(fake, 5120, fake, fake, 1e-6, fake, fake, 64, None, fake, fake, None, None, fake, fake, 16,
                            1, 1, 8, 2, 256, None) == 1

@@ -168,3 +168,49 @@ def test_add_rmsnorm_matches_oracle(with_add):
     torch.cuda.synchronize()
     assert oracle.rel_err(h.cpu(), ref) <= TOL_F32
     assert oracle.rel_err(xd.cpu(), xs) <= TOL_F32
+
+
+@pytest.mark.parametrize("with_bias,with_scale", [(False, False), (True, True)])
+def test_gdn_decode_fused_equals_the_three_kernels(with_bias, with_scale):
+    """Five decode steps through q35_gdn_decode_fused (conv + recurrent rule + gated norm in one launch) against the
+    same steps through gdn_conv, gdn_decode_step_ and gated_rmsnorm: the conv state is bitwise equal at every step,
+    the outputs and the recurrent state agree to fp32 rounding (relative error <= 1e-6: the same arithmetic with the
+    same reduction order; the compiler may contract a multiply-add differently in the two builds), and the fused
+    output matches the CPU oracle's conv + recurrence + gated norm within the fp32 tolerance."""
+    dev = device()
+    B, H, d, K = 3, 16, 128, 4
+    y, conv_w, cstate, A_log, dt_bias, C, W = _gdn_case(B, 5, seed=61)
+    gen = torch.Generator().manual_seed(62)
+    bias = torch.randn(C, generator=gen) if with_bias else None
+    hs = (0.5 + torch.rand(H, generator=gen)) if with_scale else None
+    nw = 1.0 + 0.1 * torch.randn(d, generator=gen)
+    S0 = 0.1 * torch.randn(B, H, d, d, generator=gen)
+    Vd = H * d
+    b_off, a_off, z_off = C + Vd, C + Vd + H, C
+    todev = (lambda t: None if t is None else t.to(dev))
+    cs_f, cs_u = cstate.to(dev), cstate.to(dev)
+    S_f, S_u = S0.to(dev), S0.to(dev)
+    cw, Al, dt, nwd, hsd, bd = conv_w.to(dev), A_log.to(dev), dt_bias.to(dev), nw.to(dev), todev(hs), todev(bias)
+    # CPU oracle of the same steps
+    cs_r, S_r = cstate.clone(), S0.clone()
+    for t in range(5):
+        announce(f"gdn_decode_fused step {t} bias {with_bias} head_scale {with_scale}")
+        yt = y[:, t:t + 1].contiguous()
+        ytd = yt.to(dev)
+        out_f = ops.gdn_decode_fused_(ytd.view(B, W), cw, cs_f, Al, dt, S_f, nwd, b_off=b_off, a_off=a_off,
+                                      z_off=z_off, head_scale=hsd, conv_bias=bd)
+        q, k, v, g, beta = ops.gdn_conv(ytd, cw, cs_u, Al, dt, num_k_heads=H, head_k_dim=d, num_v_heads=H,
+                                        head_v_dim=d, b_off=b_off, a_off=a_off, conv_bias=bd)
+        o = ops.gdn_decode_step_(q, k, v, g, beta, S_u, use_qk_l2norm_in_kernel=True)
+        out_u = ops.gated_rmsnorm(o, ytd[..., z_off:z_off + Vd], nwd, hsd, 1e-6)
+        torch.cuda.synchronize()
+        assert oracle.rel_err(out_f.cpu(), out_u.view(B, Vd).cpu()) <= 1e-6, f"step {t}: output"
+        assert torch.equal(cs_f.cpu(), cs_u.cpu()), f"step {t}: conv state differs"
+        assert oracle.rel_err(S_f.cpu(), S_u.cpu()) <= 1e-6, f"step {t}: recurrent state"
+        qr, kr, vr, gr, br, cs_r = of.gdn_conv(yt, conv_w, cs_r, A_log, dt_bias, H, d, H, d, b_off, a_off,
+                                               conv_bias=bias)
+        o_r, S_r = oracle.recurrent_gated_delta_rule(qr, kr, vr, gr, br, initial_state=S_r,
+                                                     output_final_state=True, use_qk_l2norm_in_kernel=True)
+        ref = of.gated_rmsnorm(o_r, yt[..., z_off:z_off + Vd], nw, hs, 1e-6)
+        assert oracle.rel_err(out_f.cpu(), ref.reshape(B, Vd)) <= TOL_F32
+    assert oracle.rel_err(S_f.cpu(), S_r) <= TOL_F32
