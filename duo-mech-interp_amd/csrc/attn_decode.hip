@@ -272,9 +272,10 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
 // Merge over splits, gate, store. One block per (query head, row, slice of 32 head dims): thread (g, d) folds the
 // splits g, g + 8, ... of dim d with an online log-sum-exp, loading eight splits' (max, sum, acc) at a time before
 // using any of them; the eight groups are combined in LDS.
+template <typename Tout>
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __restrict__ part,
                                                                 const __bf16* __restrict__ gate,
-                                                                __bf16* __restrict__ out, int Hq, int Hkv, int S) {
+                                                                Tout* __restrict__ out, int Hq, int Hkv, int S) {
   Q35_ARGS_UPFRONT(part, gate, out, Hq, Hkv, S);
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int G = Hq / Hkv, kvh = h / G, hh = h % G;
@@ -323,7 +324,7 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __r
     }
     const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + d;
     const float res = Lt > 0.f ? Ot / Lt : 0.f;
-    out[oi] = (__bf16)(res * sigmoidf_((float)gate[oi]));
+    out[oi] = from_f32<Tout>(res * sigmoidf_((float)gate[oi]));
   }
 }
 
@@ -357,11 +358,13 @@ extern "C" size_t q35_gated_attn_decode_workspace_bytes(int64_t B, int64_t Hq, i
 
 extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* gate,
                                      const int32_t* cache_len, const float* cos, const float* sin, void* out,
+                                     int out_dtype,
                                      int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
                                      float scale, int64_t splits, void* workspace, size_t workspace_bytes,
                                      q35_stream_t stream) {
   using namespace q35;
   if (!q || !k_cache || !v_cache || !gate || !cache_len || !out) return Q35_EINVAL;
+  if (out_dtype != Q35_BF16 && out_dtype != Q35_F32) return Q35_EUNSUPPORTED;
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D || (rot & 1))
     return Q35_EINVAL;
   if (rot % 8 != 0) return Q35_EUNSUPPORTED;
@@ -397,7 +400,12 @@ extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const v
   }
 #undef Q35_DEC_NT
 #undef Q35_DEC_LAUNCH
-  hipLaunchKernelGGL(attn_decode_merge_kernel, dim3((unsigned)Hq, (unsigned)B, kDecD / 32), dim3(256), 0, st, part,
-                     (const __bf16*)gate, (__bf16*)out, (int)Hq, (int)Hkv, S);
+  const dim3 mgrid((unsigned)Hq, (unsigned)B, kDecD / 32);
+  if (out_dtype == Q35_F32)
+    hipLaunchKernelGGL(attn_decode_merge_kernel<float>, mgrid, dim3(256), 0, st, part, (const __bf16*)gate,
+                       (float*)out, (int)Hq, (int)Hkv, S);
+  else
+    hipLaunchKernelGGL(attn_decode_merge_kernel<__bf16>, mgrid, dim3(256), 0, st, part, (const __bf16*)gate,
+                       (__bf16*)out, (int)Hq, (int)Hkv, S);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }

@@ -41,7 +41,7 @@ _SIGS = {
     "q35_gated_attn_prefill_workspace_bytes": ([I64, I64, I64, I64, I64], SZ),
     "q35_gated_attn_prefill": ([P, P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, F32, P, SZ, P], I32),
     "q35_gated_attn_decode_workspace_bytes": ([I64, I64, I64, I64, I64, I64], SZ),
-    "q35_gated_attn_decode": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, F32, I64, P, SZ, P], I32),
+    "q35_gated_attn_decode": ([P, P, P, P, P, P, P, P, I32, I64, I64, I64, I64, I64, I64, F32, I64, P, SZ, P], I32),
     "q35_resid_add_rows": ([P, P, P, I64, I64, I64, I64, I32, P], I32),
     "q35_gdn_conv": ([P, I64, P, P, P, P, P, I64, I64, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, P], I32),
     "q35_gated_rmsnorm": ([P, P, I64, P, P, P, I64, I64, I64, F32, I32, P], I32),

@@ -183,8 +183,9 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
         o = ops.gated_attention_prefill(q, k, v, gate, cos, sin, pos0=0, scale=1.0 / math.sqrt(D))
     else:
         cl = pos_t + 1 if cache_len is None else cache_len
+        # fp32 straight from the merge kernel: the o_proj GEMV reads fp32 (no conversion kernel in the step)
         o = ops.gated_attention_decode(q[:, 0], k_cache, v_cache, gate[:, 0], cl, cos, sin,
-                                       scale=1.0 / math.sqrt(D)).view(B, 1, Hq * D)
+                                       scale=1.0 / math.sqrt(D), out_dtype=torch.float32).view(B, 1, Hq * D)
     return linear(o.float(), p["o_proj"], *_q8(p, "o_proj"))
 
 

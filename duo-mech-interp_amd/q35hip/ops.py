@@ -61,7 +61,7 @@ _LIB.define("gdn_chunk_prefill(Tensor q, Tensor k, Tensor v, Tensor g, Tensor be
 _LIB.define("gated_attn_prefill(Tensor q, Tensor k, Tensor v, Tensor gate, Tensor cos, Tensor sin, int pos0, "
             "float scale) -> Tensor")
 _LIB.define("gated_attn_decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor gate, Tensor cache_len, "
-            "Tensor cos, Tensor sin, float scale, int splits) -> Tensor")
+            "Tensor cos, Tensor sin, float scale, int splits, bool f32_out=False) -> Tensor")
 _LIB.define("resid_add_rows_(Tensor(a!) x, Tensor vecs, Tensor? vec_of_row) -> ()")
 _LIB.define("gdn_conv(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
             "Tensor dt_bias, int b_off, int a_off, int Hk, int dk, int Hv, int dv, bool bf16_out) "
@@ -162,7 +162,7 @@ def _attn_prefill_impl(q, k, v, gate, cos, sin, pos0, scale):
     return out
 
 
-def _attn_decode_impl(q, k_cache, v_cache, gate, cache_len, cos, sin, scale, splits):
+def _attn_decode_impl(q, k_cache, v_cache, gate, cache_len, cos, sin, scale, splits, f32_out=False):
     _on_gpu(q, k_cache, v_cache, gate, cache_len, cos, sin)
     _require(q.dtype == torch.bfloat16 and k_cache.dtype == q.dtype and v_cache.dtype == q.dtype
              and gate.dtype == q.dtype, "q, caches, gate must be bf16")
@@ -177,9 +177,10 @@ def _attn_decode_impl(q, k_cache, v_cache, gate, cache_len, cos, sin, scale, spl
     L = _lib.lib()
     nbytes = L.q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits)
     ws = _workspace(nbytes, q.device)
-    out = torch.empty(B, Hq * D, dtype=q.dtype, device=q.device)
+    odt = torch.float32 if f32_out else q.dtype
+    out = torch.empty(B, Hq * D, dtype=odt, device=q.device)
     st = L.q35_gated_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(gate), _ptr(cache_len), _ptr(cos),
-                                 _ptr(sin), _ptr(out), B, Hq, Hkv, D, max_len, rot, float(scale), int(splits),
+                                 _ptr(sin), _ptr(out), _DT[odt], B, Hq, Hkv, D, max_len, rot, float(scale), int(splits),
                                  _ptr(ws), ws.numel(), _stream(q))
     check(st, "q35_gated_attn_decode")
     return out
@@ -424,7 +425,8 @@ _LIB.impl("gated_attn_prefill",
           lambda q, k, v, gate, cos, sin, pos0, scale: q.new_empty(q.shape[0], q.shape[1], q.shape[2] * q.shape[3]),
           "Meta")
 _LIB.impl("gated_attn_decode",
-          lambda q, kc, vc, gate, cl, cos, sin, scale, splits: q.new_empty(q.shape[0], q.shape[1] * q.shape[2]),
+          lambda q, kc, vc, gate, cl, cos, sin, scale, splits, f32_out=False:
+          q.new_empty(q.shape[0], q.shape[1] * q.shape[2], dtype=torch.float32 if f32_out else q.dtype),
           "Meta")
 _LIB.impl("resid_add_rows_", lambda x, vecs, vor: None, "Meta")
 _LIB.impl("gdn_decode_fused_", lambda y, cw, cb, cs, Al, dt, bo, ao, zo, st, nw, hs, eps, sc:
@@ -480,10 +482,13 @@ def gated_attention_prefill(q, k, v, gate, cos, sin, pos0=0, scale=None):
     return torch.ops.q35.gated_attn_prefill(q, k, v, gate, cos, sin, int(pos0), float(scale))
 
 
-def gated_attention_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, scale=None, splits=0):
-    """One new token per row over a bf16 KV cache [B, Hkv, max_len, D]; q rotated at position cache_len - 1."""
+def gated_attention_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, scale=None, splits=0,
+                           out_dtype=torch.bfloat16):
+    """One new token per row over a bf16 KV cache [B, Hkv, max_len, D]; q rotated at position cache_len - 1. The
+    output [B, Hq * D] is bf16, or fp32 with out_dtype=torch.float32 (written so by the merge kernel itself)."""
     scale = q.shape[-1] ** -0.5 if scale is None else scale
-    return torch.ops.q35.gated_attn_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, float(scale), int(splits))
+    return torch.ops.q35.gated_attn_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, float(scale), int(splits),
+                                           out_dtype == torch.float32)
 
 
 def residual_steer_add_(x, vecs, vec_of_row=None):

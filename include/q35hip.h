@@ -125,7 +125,7 @@ int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const vo
  *   q: [B, Hq, D] bf16 (not yet rotated; rotated here at position cache_len[b] - 1)
  *   k_cache, v_cache: [B, Hkv, max_len, D] bf16, keys already rotated; row b uses keys 0 .. cache_len[b] - 1
  *   cache_len: [B] int32 on the device (1 <= cache_len[b] <= max_len)
- *   gate: [B, Hq * D] bf16    out: [B, Hq * D] bf16
+ *   gate: [B, Hq * D] bf16    out: [B, Hq * D] in out_dtype (Q35_BF16, or Q35_F32 for an fp32 consumer)
  *   cos, sin: [P, rot / 2] fp32 by position (P >= max_len); rot a multiple of 8 (Q35_EUNSUPPORTED otherwise)
  *   splits <= 0 lets the library choose the split count (a request is rounded to whole 64-key multiples of a
  *   power-of-two span, so the count used may be lower). Needs
@@ -134,7 +134,7 @@ int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const vo
 size_t q35_gated_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
                                              int64_t splits);
 int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* gate,
-                          const int32_t* cache_len, const float* cos, const float* sin, void* out,
+                          const int32_t* cache_len, const float* cos, const float* sin, void* out, int out_dtype,
                           int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
                           float scale, int64_t splits, void* workspace, size_t workspace_bytes,
                           q35_stream_t stream);

@@ -39,7 +39,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 4
+    assert L.q35_abi_version() == 5
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -80,10 +80,12 @@ def test_validation_rejects_without_launching():
     assert L.q35_gated_attn_prefill_workspace_bytes(1, 4096, 8, 2, 256) == kv + parts
     assert L.q35_gated_attn_prefill(fake, fake, fake, fake, fake, fake, 0, fake, 1, 100, 8, 2, 256, 64, 0.1,
                                     fake, 16, None) == 3
-    assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 8, 2, 256, 128, 63, 0.1, 0,
-                                   fake, 1 << 20, None) == 1
-    assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 8, 2, 256, 128, 64, 0.1, 0,
-                                   fake, 8, None) == 3
+    assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 1, 8, 2, 256, 128, 63, 0.1,
+                                   0, fake, 1 << 20, None) == 1
+    assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 1, 1, 8, 2, 256, 128, 64, 0.1,
+                                   0, fake, 8, None) == 3
+    assert L.q35_gated_attn_decode(fake, fake, fake, fake, fake, fake, fake, fake, 2, 1, 8, 2, 256, 128, 64, 0.1,
+                                   0, fake, 1 << 20, None) == 2
     assert L.q35_resid_add_rows(None, fake, None, 1, 1, 8, 1, 0, None) == 1
     # front-end kernels: null pointers, inconsistent widths, unsupported sizes
     assert L.q35_gdn_conv(None, 6144, fake, None, fake, fake, fake, 0, 0, fake, fake, fake, fake, fake, 1, 1, 16,

@@ -103,3 +103,21 @@ def test_decode_matches_last_prefill_row():
     cl = torch.tensor([T], dtype=torch.int32, device=dev)
     dec = q35hip.gated_attention_decode(q_last, k_cache, v_cache, gate_last, cl, cos.to(dev), sin.to(dev))
     assert oracle.rel_err(dec.float().cpu(), full[:, T - 1].float().cpu()) <= TOL
+
+
+def test_decode_fp32_output_is_the_unrounded_bf16_output():
+    """out_dtype=float32 writes the merge kernel's fp32 result (the stack's o_proj input); rounded to bf16 it is the
+    bf16 output bit for bit, and it matches the oracle within the fp32 arithmetic's error."""
+    dev = device()
+    inp = workloads.attn_decode_inputs(B=3, N=777, max_len=1024, seed=8, lens=[777, 1, 300])
+    cos, sin = _tables(1024)
+    ref = oracle.gated_attention_decode(inp["q"], inp["k_cache"], inp["v_cache"], inp["gate"], inp["cache_len"],
+                                        cos, sin)
+    d = workloads.to_device(inp, dev)
+    announce("attn decode fp32 output")
+    args = (d["q"], d["k_cache"], d["v_cache"], d["gate"], d["cache_len"], cos.to(dev), sin.to(dev))
+    o16 = q35hip.gated_attention_decode(*args)
+    o32 = q35hip.gated_attention_decode(*args, out_dtype=torch.float32)
+    assert o32.dtype == torch.float32 and o16.dtype == torch.bfloat16
+    assert torch.equal(o32.to(torch.bfloat16).cpu(), o16.cpu())
+    assert oracle.rel_err(o32.cpu(), ref) <= TOL
