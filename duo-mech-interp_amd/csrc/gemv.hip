@@ -83,8 +83,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
 #pragma unroll
   for (int r = 0; r < 4; ++r) wr[r] = W + (size_t)min(n0 + g + 4 * r, N - 1) * K + j * E;
   const int nsteps = K / KS;
-  // this wave's K steps: wave, wave + NW, ...; U of them in flight per round, the first round issued before x is
-  // staged so that its latency covers the staging
+  // this wave's K steps: wave, wave + NW, ...; U of them in flight per round. Loads complete in issue order, so the
+  // thread's first x chunk (L2) is issued ahead of the first round of weights (HBM): the staging then waits for x
+  // only, and its work overlaps the weights' flight
   WChunk<TW> wc[U][4];
   auto issue = [&](int s0) {
 #pragma unroll
@@ -94,28 +95,51 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
       for (int r = 0; r < 4; ++r) wc[u][r].load(wr[r] + st * KS);
     }
   };
-  issue(wave);
-  asm volatile("" ::: "memory");
   // x (or, with NORM, s = x + xadd times (1 + nw)) into LDS; with NORM each wave also sums the squares of s per row
   // (all loads of a thread go out together: one round trip), the rows' rsqrt factors applied in the epilogue
   __shared__ float ssw[8][MP];
+  // the first chunk's operands (k = 4 tid; zero past K), loaded before the weights
+  const int kf = 4 * tid;
+  f32x4 fv[MP], fa[MP], fw = zero4();
+#pragma unroll
+  for (int m = 0; m < MP; ++m) {
+    fv[m] = zero4();
+    fa[m] = zero4();
+  }
+  if (NORM) {
+    if (kf < K) {
+      fw = *reinterpret_cast<const f32x4*>(nw + kf);
+#pragma unroll
+      for (int m = 0; m < MP; ++m) {
+        if (m < M) fv[m] = *reinterpret_cast<const f32x4*>(x + m * ldx + kf);
+        if (m < M && xadd) fa[m] = *reinterpret_cast<const f32x4*>(xadd + m * ldx + kf);
+      }
+    }
+  } else {
+    // the non-NORM staging takes element quads i = tid, tid + blockDim ... of the flattened [MP][K]
+    const int m0 = kf / K, k0 = kf - m0 * K;
+    if (m0 < M && kf < MP * K) fv[0] = *reinterpret_cast<const f32x4*>(x + m0 * ldx + k0);
+  }
+  issue(wave);
+  asm volatile("" ::: "memory");
   if (NORM) {
     float ss[MP];
 #pragma unroll
     for (int m = 0; m < MP; ++m) ss[m] = 0.f;
-    for (int k = 4 * tid; k < K; k += 4 * (int)blockDim.x) {
-      const f32x4 w = *reinterpret_cast<const f32x4*>(nw + k);
+    for (int k = kf; k < K; k += 4 * (int)blockDim.x) {
+      const bool first = k == kf;
+      const f32x4 w = first ? fw : *reinterpret_cast<const f32x4*>(nw + k);
       f32x4 v[MP];
 #pragma unroll
       for (int m = 0; m < MP; ++m) {
         v[m] = zero4();
-        if (m < M) v[m] = *reinterpret_cast<const f32x4*>(x + m * ldx + k);
+        if (m < M) v[m] = first ? fv[m] : *reinterpret_cast<const f32x4*>(x + m * ldx + k);
       }
       if (xadd) {
 #pragma unroll
         for (int m = 0; m < MP; ++m) {
           if (m < M) {
-            const f32x4 a = *reinterpret_cast<const f32x4*>(xadd + m * ldx + k);
+            const f32x4 a = first ? fa[m] : *reinterpret_cast<const f32x4*>(xadd + m * ldx + k);
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[m][e] += a[e];
           }
@@ -142,7 +166,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
     for (int i = tid; i < MP * K / 4; i += blockDim.x) {
       const int m = (4 * i) / K, k = 4 * i - m * K;
       f32x4 v = zero4();
-      if (m < M) v = *reinterpret_cast<const f32x4*>(x + m * ldx + k);
+      if (m < M) v = i == tid ? fv[0] : *reinterpret_cast<const f32x4*>(x + m * ldx + k);
       *reinterpret_cast<f32x4*>(xs + m * K + k) = v;
     }
   }
