@@ -142,3 +142,20 @@ def test_ops_refuse_cpu_tensors():
         q35hip.chunk_gated_delta_rule(x, x, x, g, g)
     with pytest.raises(Exception, match="no CPU|HIP device"):
         q35hip.recurrent_gated_delta_rule(x, x, x, g, g, None, True)
+
+
+def test_fused_gdn_step_and_fp32_decode_refuse_cpu_tensors():
+    """The fused GDN decode step and the fp32-output attention decode have no CPU path either."""
+    B, H, d, K = 1, 2, 128, 4
+    C = 3 * H * d
+    y = torch.zeros(B, C + H * d + 2 * H)
+    with pytest.raises(Exception, match="no CPU|HIP device"):
+        q35hip.ops.gdn_decode_fused_(y, torch.zeros(C, 1, K), torch.zeros(B, K - 1, C), torch.zeros(H), torch.zeros(H),
+                                     torch.zeros(B, H, d, d), torch.ones(d), b_off=C + H * d, a_off=C + H * d + H,
+                                     z_off=C)
+    q = torch.zeros(1, 8, 256, dtype=torch.bfloat16)
+    kc = torch.zeros(1, 2, 64, 256, dtype=torch.bfloat16)
+    with pytest.raises(Exception, match="no CPU|HIP device"):
+        q35hip.ops.gated_attention_decode(q, kc, kc, torch.zeros(1, 2048, dtype=torch.bfloat16),
+                                          torch.ones(1, dtype=torch.int32), torch.zeros(64, 32), torch.zeros(64, 32),
+                                          out_dtype=torch.float32)
