@@ -118,7 +118,10 @@ class HybridModel:
                 self.states.append({
                     "conv": torch.zeros(rows, cfg.conv_k - 1, cfg.conv_dim, device=device),
                     "rec": torch.zeros(rows, cfg.lin_v_heads, cfg.lin_dk, cfg.lin_dv, device=device)})
-        self.pos_dev = torch.zeros(rows, dtype=torch.int32, device=device)
+        # row 0: each row's next position; row 1: its cache length after that token (position + 1). One add per
+        # step advances both, so the decode step computes no length of its own.
+        self._pos_len = torch.zeros(2, rows, dtype=torch.int32, device=device)
+        self.pos_dev, self.len_dev = self._pos_len[0], self._pos_len[1]
         self.graph = None
         self.reset()
 
@@ -130,6 +133,7 @@ class HybridModel:
                 st["rec"].zero_()
                 st["conv"].zero_()
         self.pos_dev.zero_()
+        self.len_dev.fill_(1)
         self.pos = 0
 
     def set_vectors(self, vecs, vec_of_row):
@@ -171,7 +175,7 @@ class HybridModel:
         cfg = self.cfg
         collected = None
         if T == 1:
-            cache_len = self.pos_dev + 1  # once per step, shared by the attention layers
+            cache_len = self.len_dev  # shared by the attention layers
             cur, alt = x, torch.empty_like(x)
             for l in range(last + 1):
                 p, st = self.params[l], self.states[l]
@@ -224,7 +228,7 @@ class HybridModel:
         x = W["embed"][ids.to(self.device).long()].contiguous()
         last = cfg.layers - 1 if stop_after is None else stop_after
         x, collected = self._layers(x, T, last, collect_layer, self.steering)
-        self.pos_dev.add_(T)
+        self._pos_len.add_(T)
         self.pos += T
         if stop_after is not None:
             return None, collected
@@ -251,7 +255,7 @@ class HybridModel:
         def step():
             x, _ = self._layers(self.W["embed"].index_select(0, self._g_ids).unsqueeze(1), 1, cfg.layers - 1, None,
                                 True)
-            self.pos_dev.add_(1)
+            self._pos_len.add_(1)
             logits = self._lm_head(x[:, -1])
             ops.argmax_rows(logits, out=self._g_ids)
             return logits
