@@ -1,4 +1,6 @@
 // Gated DeltaNet, chunked form (prefill): chunk-64 UT/WY transform, fp32 state carried across the sequence.
+// Two kernel pairs, chosen by the input dtype: bf16 q/k/v run the pair-record kernels below (bf16 MFMA products,
+// fp32 accumulation); fp32 q/k/v run the fp32 WY kernels at the end of this file (every product in fp32).
 //
 // Math (HF:249-327 torch_chunk_gated_delta_rule; decay masks and the 63-row forward substitution at HF:288-298).
 // Per (b, h), with q^ = l2norm(q) * scale, k^ = l2norm(k) and, inside a span of positions, gamma = cumsum(g):
@@ -62,42 +64,19 @@ __device__ __forceinline__ bf16x8 frag(const char* tile, int r, int c) {
   return *reinterpret_cast<const bf16x8*>(tile + t128(r, c));
 }
 
-__device__ __forceinline__ bf16x8 load8b(const float* p) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
-  bf16x8 r;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) { r[e] = (__bf16)a[e]; r[4 + e] = (__bf16)b[e]; }
-  return r;
-}
-// Raw loads as packed bf16 bits (fp32 input rounded to bf16), issued unconditionally from clamped addresses; rows
-// outside the sequence are zeroed afterwards with a select.
+// Raw loads as packed bf16 bits, issued unconditionally from clamped addresses; rows outside the sequence are
+// zeroed afterwards with a select.
 __device__ __forceinline__ u32x4 raw8(const __bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
-__device__ __forceinline__ u32x4 raw8(const float* p) {
-  const bf16x8 r = load8b(p);
-  return __builtin_bit_cast(u32x4, r);
-}
 __device__ __forceinline__ f32x4 unpack_bf16x4(const u32x2& r) {
   f32x4 o = {bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y)};
   return o;
 }
-__device__ __forceinline__ f32x4 load4f(const __bf16* p) {
-  const u32x2 r = *reinterpret_cast<const u32x2*>(p);
-  f32x4 o = {bf16lo(r.x), bf16hi(r.x), bf16lo(r.y), bf16hi(r.y)};
-  return o;
-}
-__device__ __forceinline__ f32x4 load4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
-// Four consecutive inputs as loaded (bf16 bits or fp32), converted to fp32 only when used: a raw load can be issued
-// long before its use while holding half the registers for bf16.
-template <typename Tin> struct Raw4;
-template <> struct Raw4<__bf16> {
+// Four consecutive bf16 inputs as loaded, converted to fp32 only when used: a raw load can be issued long before its
+// use while holding half the registers.
+struct Raw4 {
   u32x2 r;
   __device__ __forceinline__ void load(const __bf16* p) { r = *reinterpret_cast<const u32x2*>(p); }
   __device__ __forceinline__ f32x4 f() const { return unpack_bf16x4(r); }
-};
-template <> struct Raw4<float> {
-  f32x4 r;
-  __device__ __forceinline__ void load(const float* p) { r = *reinterpret_cast<const f32x4*>(p); }
-  __device__ __forceinline__ f32x4 f() const { return r; }
 };
 __device__ __forceinline__ u32x4 mask8(u32x4 r, bool keep) {
   const u32x4 z = {0u, 0u, 0u, 0u};
@@ -109,15 +88,6 @@ __device__ __forceinline__ float sumsq8(const u32x4& r) {
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-  return ss;
-}
-// sum of squares in the input precision (fp32 input: of the unrounded values)
-__device__ __forceinline__ float sumsq8_in(const __bf16*, const u32x4& r) { return sumsq8(r); }
-__device__ __forceinline__ float sumsq8_in(const float* p, const u32x4&) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) ss += a[e] * a[e] + b[e] * b[e];
   return ss;
 }
 __device__ __forceinline__ uint32_t half16(const u32x4& r, int e) {
@@ -217,9 +187,9 @@ __device__ __forceinline__ float tinv(const float* Am, int t, int s) {
   return 0.f;
 }
 
-template <typename Tin>
-__global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __restrict__ q, const Tin* __restrict__ k,
-                                                               const Tin* __restrict__ v, const float* __restrict__ g,
+__global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const __bf16* __restrict__ q,
+                                                               const __bf16* __restrict__ k,
+                                                               const __bf16* __restrict__ v, const float* __restrict__ g,
                                                                const float* __restrict__ beta, char* __restrict__ ws,
                                                                int T, int NP, int Hk, int H, float scale, int l2norm) {
   __shared__ __attribute__((aligned(16))) char R1[32768];           // k row-major -> k transposed
@@ -252,7 +222,7 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
   const int u = tid & 255, rg = u >> 4, cc = u & 15;
   const bool isK = tid < 256;
   u32x4 raw[8];
-  const Tin* src[8];
+  const __bf16* src[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const size_t tok = (size_t)b * T + t0 + min(8 * rg + i, nvalid - 1);
@@ -260,7 +230,7 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
     raw[i] = raw8(src[i]);
   }
   const int qrow = tid >> 2, qs0 = 4 * (tid & 3);
-  const Tin* qsrc = q + (((size_t)b * T + t0 + min(qrow, nvalid - 1)) * Hk + kh) * kD;
+  const __bf16* qsrc = q + (((size_t)b * T + t0 + min(qrow, nvalid - 1)) * Hk + kh) * kD;
   u32x4 rq[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) rq[j] = raw8(qsrc + 8 * (qs0 + j));
@@ -275,7 +245,7 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const bool valid = 8 * rg + i < nvalid;
-      ss[i] = valid && isK ? sumsq8_in(src[i], raw[i]) : 0.f;
+      ss[i] = valid && isK ? sumsq8(raw[i]) : 0.f;
       raw[i] = mask8(raw[i], valid);
     }
     if (isK) {
@@ -295,7 +265,7 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
   {
     float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ss += sumsq8_in(qsrc + 8 * (qs0 + j), rq[j]);
+    for (int j = 0; j < 4; ++j) ss += sumsq8(rq[j]);
     ss += __shfl_xor(ss, 1, 64);
     ss += __shfl_xor(ss, 2, 64);
     if ((tid & 3) == 0) rqn[qrow] = l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
@@ -553,11 +523,11 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const Tin* __rest
   const float gl = gam[kP - 1];
   const int dq = 4 * (wv >> 2), kq = wv & 3;
   // q rows of the Q' products of step 7, loaded now so that their latency is covered by step 6
-  Raw4<Tin> qraw[4][2];
+  Raw4 qraw[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = 16 * (dq + i) + li;
-    const Tin* qr = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
+    const __bf16* qr = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
 #pragma unroll
     for (int a = 0; a < 2; ++a) qraw[i][a].load(qr + 16 * (2 * kq + a) + 4 * lg);
   }
@@ -681,11 +651,8 @@ __device__ __forceinline__ void scan_coords(int L, int nunits, int& idx, int& un
   }
 }
 
-__device__ __forceinline__ void store_out(__amdgpu_buffer_rsrc_t rc, int off_elems, float x, __bf16*) {
+__device__ __forceinline__ void store_out(__amdgpu_buffer_rsrc_t rc, int off_elems, float x) {
   __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (__bf16)x), rc, off_elems * 2, 0, 0);
-}
-__device__ __forceinline__ void store_out(__amdgpu_buffer_rsrc_t rc, int off_elems, float x, float*) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, x), rc, off_elems * 4, 0, 0);
 }
 
 // Operands of one pair for one wave of the scan kernel.
@@ -697,9 +664,8 @@ struct PairOps {
   float eg;
 };
 
-template <typename Tout>
 __global__ __launch_bounds__(320, 1) void gdn_pair_scan_kernel(const char* __restrict__ ws, const float* s_in,
-                                                               float* s_out, Tout* __restrict__ o, int T, int NP,
+                                                               float* s_out, __bf16* __restrict__ o, int T, int NP,
                                                                int H, int B) {
   __shared__ bf16x8 slot[2][4][64];
   __shared__ int dummy[64];
@@ -755,7 +721,7 @@ __global__ __launch_bounds__(320, 1) void gdn_pair_scan_kernel(const char* __res
   // Outputs go through a buffer resource spanning row b's [T, H, 128] block: stores past the sequence end fall
   // outside it and are dropped by the hardware.
   const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
-      o + (size_t)b * T * H * kD, 0, (int)((size_t)T * H * kD * sizeof(Tout)), 0x00020000);
+      o + (size_t)b * T * H * kD, 0, (int)((size_t)T * H * kD * sizeof(__bf16)), 0x00020000);
 
   auto step = [&](int pp, const PairOps& op) {
     const bf16x8 own = pack8(S[0], S[1]);
@@ -770,7 +736,7 @@ __global__ __launch_bounds__(320, 1) void gdn_pair_scan_kernel(const char* __res
     for (int ks = 0; ks < 4; ++ks) acc = mfma16(op.qf[ks], sb[ks], acc);
     const int tb = kP * pp + 64 * half + 16 * w + 4 * lg;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) store_out(orc, ((tb + r) * H + h) * kD + col, acc[r], (Tout*)nullptr);
+    for (int r = 0; r < 4; ++r) store_out(orc, ((tb + r) * H + h) * kD + col, acc[r]);
     // state: S <- e^G S + Bm + M S
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -806,12 +772,370 @@ __global__ __launch_bounds__(320, 1) void gdn_pair_scan_kernel(const char* __res
   }
 }
 
+// ================================================================================================================
+// fp32 path (fp32 q, k, v): the chunk-64 WY form of HF:281-327 with every product in fp32
+// (v_mfma_f32_16x16x4_f32), so that outputs and state agree with the fp32 recurrence to fp32 rounding.
+//
+// Kernel F1, gdn_f32_prep_kernel: one 256-thread block per (chunk, head, row), all chunks in parallel. With
+// k^ = l2norm(k), q^ = l2norm(q) * scale and gamma = cumsum(g) inside the chunk it writes one record of
+//   W   [64 pos][128 d]  = T diag(beta e^gamma) K^          U  [64 pos][128 dv] = T diag(beta) V
+//   Qe  [64 pos][128 d]  = Q^ e^gamma (0 past the end)      Kt [128 d][64 pos]  = (K^ e^(gamma_last - gamma))^T
+//   P   [64 t][64 s]     = (q^_t . k^_s) e^(gamma_t - gamma_s) for s <= t (lower triangle only)
+//   e^gamma_last,  with T = (I - L)^-1, L[t][s] = -beta_t (k^_t . k^_s) e^(gamma_t - gamma_s) (s < t).
+// Kernel F2, gdn_f32_scan_kernel: 8 blocks per (row, head), one per 16 value columns; each carries its 128 x 16 fp32
+// state slice in registers (wave w: state rows 32 w .. 32 w + 31) and per chunk computes
+//   V = U - W S,   O = Qe S + P V,   S <- e^gamma_last S + Kt V
+// (wave w: positions 16 w .. 16 w + 15 of V and O). The state and V tiles are exchanged through LDS.
+//
+// Product layout: an operand X[m][k] held row-major feeds the A (or B) side of a 16 x 16 x 4 MFMA group over one
+// 16-wide k chunk as one float4 per lane (X[m][16 c + 4 g .. + 3], m = lane % 16, g = lane / 16), step s using
+// element s, i.e. k index 16 c + 4 g + s. A 16 x 16 accumulator tile in D layout (lane: column lane % 16, rows
+// 4 g + r in element r) supplies the other side of the same four steps directly: element s of lane l is row
+// 4 g + s. The k permutation is the same on both sides, so the sum is unchanged.
+constexpr int kFX = 132;                 // row stride (floats) of the fp32 [64][128] staging tiles
+constexpr size_t kFRecW = 0;             // W   [64][128]
+constexpr size_t kFRecU = 32768;         // U   [64][128]
+constexpr size_t kFRecQ = 65536;         // Qe  [64][128]
+constexpr size_t kFRecK = 98304;         // Kt  [128][64]
+constexpr size_t kFRecP = 131072;        // P   [64][64]
+constexpr size_t kFRecE = 147456;        // e^gamma_last
+constexpr size_t kFRecBytes = 147712;    // 256-byte aligned
+
+// acc += X Y over one 16-wide k chunk (layouts above): x = X[m][16 c + 4 g ..], y = element s at k = 16 c + 4 g + s
+__device__ __forceinline__ f32x4 mm_k16(const f32x4& x, const f32x4& y, f32x4 acc) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = mfma_f32_16x16x4(x[s], y[s], acc);
+  return acc;
+}
+
+__global__ __launch_bounds__(256, 1) void gdn_f32_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                              const float* __restrict__ v, const float* __restrict__ g,
+                                                              const float* __restrict__ beta, char* __restrict__ ws,
+                                                              int T, int NC, int Hk, int H, float scale, int l2norm) {
+  __shared__ __attribute__((aligned(16))) float Ks[kC * kFX];   // k rows (unnormalised)
+  __shared__ __attribute__((aligned(16))) float Xs[kC * kFX];   // q rows, then v rows
+  __shared__ __attribute__((aligned(16))) float Am[kC * kFS];   // L -> T (invert64 layout) -> T dense
+  __shared__ float scr[4][16 * 17];
+  __shared__ float gam[kC], bet[kC], rkn[kC], rqn[kC];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int kh = h / (H / Hk);
+  const int t0 = c * kC;
+  const int nvalid = min(kC, T - t0);
+  char* rec = ws + (((size_t)b * H + h) * NC + c) * kFRecBytes;
+  float* recf = reinterpret_cast<float*>(rec);
+
+  // ---- stage k and q (thread: row tid / 4, columns 32 (tid % 4) .. + 31), the gates, the l2 norms
+  const int row = tid >> 2, c0 = (tid & 3) * 32;
+  const bool valid = row < nvalid;
+  const size_t tok = (size_t)b * T + t0 + min(row, nvalid - 1);
+  f32x4 kr[8], xr[8];
+  {
+    const float* kp = k + (tok * Hk + kh) * kD + c0;
+    const float* qp = q + (tok * Hk + kh) * kD + c0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      kr[j] = *reinterpret_cast<const f32x4*>(kp + 4 * j);
+      xr[j] = *reinterpret_cast<const f32x4*>(qp + 4 * j);
+    }
+  }
+  float g0 = 0.f, b0 = 0.f;
+  if (wave == 0 && lane < nvalid) {
+    const size_t gi = ((size_t)b * T + t0 + lane) * H + h;
+    g0 = g[gi];
+    b0 = beta[gi];
+  }
+  {
+    float ssk = 0.f, ssq = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { ssk += kr[j][e] * kr[j][e]; ssq += xr[j][e] * xr[j][e]; }
+    ssk += __shfl_xor(ssk, 1, 64);
+    ssk += __shfl_xor(ssk, 2, 64);
+    ssq += __shfl_xor(ssq, 1, 64);
+    ssq += __shfl_xor(ssq, 2, 64);
+    if ((tid & 3) == 0) {
+      rkn[row] = l2norm ? rsqrtf(ssk + 1e-6f) : 1.f;
+      rqn[row] = l2norm ? rsqrtf(ssq + 1e-6f) : 1.f;
+    }
+    const f32x4 z = zero4();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      *reinterpret_cast<f32x4*>(Ks + row * kFX + c0 + 4 * j) = valid ? kr[j] : z;
+      *reinterpret_cast<f32x4*>(Xs + row * kFX + c0 + 4 * j) = valid ? xr[j] : z;
+    }
+  }
+  if (wave == 0) {  // gamma = cumsum(g) over the chunk; g = beta = 0 past the sequence end (HF pads with zeros)
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_up(g0, off, 64);
+      if (lane >= off) g0 += y;
+    }
+    gam[lane] = g0;
+    bet[lane] = b0;
+  }
+  // v rows, loaded now and staged once q is no longer needed
+  {
+    const float* vp = v + (tok * H + h) * kD + c0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(vp + 4 * j);
+      kr[j] = valid ? t : zero4();  // kr is free: k is in LDS
+    }
+  }
+  __syncthreads();
+
+  // ---- K K^T -> L (strictly lower, into Am) and Q K^T -> P (lower triangle incl. the diagonal, to the record). Wave
+  //      w takes the L row tile w (w + 1 tiles) and the P row tile 3 - w (4 - w tiles).
+  {
+    auto tile = [&](const float* X, int i, int j) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kc = 0; kc < 8; ++kc) {
+        const f32x4 xa = *reinterpret_cast<const f32x4*>(X + (16 * i + li) * kFX + 16 * kc + 4 * lg);
+        const f32x4 yb = *reinterpret_cast<const f32x4*>(Ks + (16 * j + li) * kFX + 16 * kc + 4 * lg);
+        acc = mm_k16(xa, yb, acc);
+      }
+      return acc;
+    };
+    const int iL = wv, iP = 3 - wv;
+    for (int j = 0; j <= iL; ++j) {
+      const f32x4 acc = tile(Ks, iL, j);
+      const int s = 16 * j + li;
+      const float ps = rkn[s], gs = gam[s];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * iL + 4 * lg + r;
+        Am[t * kFS + s] = s < t ? -bet[t] * rkn[t] * ps * acc[r] * __expf(gam[t] - gs) : 0.f;
+      }
+    }
+    for (int j = 0; j <= iP; ++j) {
+      const f32x4 acc = tile(Xs, iP, j);
+      const int s = 16 * j + li;
+      const float ps = rkn[s], gs = gam[s];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * iP + 4 * lg + r;
+        recf[kFRecP / 4 + t * kC + s] = s <= t ? rqn[t] * scale * ps * acc[r] * __expf(gam[t] - gs) : 0.f;
+      }
+    }
+  }
+  // ---- Qe = Q^ e^gamma (thread: its staged row and columns)
+  {
+    const float f = valid ? rqn[row] * scale * __expf(gam[row]) : 0.f;
+    float* dst = recf + kFRecQ / 4 + row * kD + c0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(Xs + row * kFX + c0 + 4 * j);
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = x[e] * f;
+      *reinterpret_cast<f32x4*>(dst + 4 * j) = y;
+    }
+  }
+  __syncthreads();
+
+  // ---- T = (I - L)^-1, then dense (zeros above the diagonal) in place; v replaces q in Xs
+  invert64(Am, wv, lane, scr[wave], [] { __syncthreads(); });
+  __syncthreads();
+  {
+    float tv[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int idx = tid + 256 * e;
+      tv[e] = tinv(Am, idx >> 6, idx & 63);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<f32x4*>(Xs + row * kFX + c0 + 4 * j) = kr[j];
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int idx = tid + 256 * e;
+      Am[(idx >> 6) * kFS + (idx & 63)] = tv[e];
+    }
+  }
+  __syncthreads();
+
+  // ---- W = T diag(beta e^gamma rk) K, U = T diag(beta) V. Wave w: column tiles 2 w, 2 w + 1 of both, all four row
+  //      tiles (T is lower triangular: row tile i sums k chunks 0..i).
+  {
+    f32x4 ta[4][4];  // T[16 i + li][16 kc + 4 lg ..]
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc)
+        ta[i][kc] = kc <= i ? *reinterpret_cast<const f32x4*>(Am + (16 * i + li) * kFS + 16 * kc + 4 * lg) : zero4();
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {  // 0: W from k, 1: U from v
+      const float* src = m == 0 ? Ks : Xs;
+      float* dst = recf + (m == 0 ? kFRecW : kFRecU) / 4;
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int d = 16 * (2 * wv + a) + li;
+        f32x4 yb[4];  // scaled operand rows s = 16 kc + 4 lg + e at column d
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int s = 16 * kc + 4 * lg + e;
+            const float f = m == 0 ? bet[s] * __expf(gam[s]) * rkn[s] : bet[s];
+            yb[kc][e] = src[s * kFX + d] * f;
+          }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int kc = 0; kc <= i; ++kc) acc = mm_k16(ta[i][kc], yb[kc], acc);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[(16 * i + 4 * lg + r) * kD + d] = acc[r];
+        }
+      }
+    }
+  }
+  // ---- Kt = (K^ e^(gamma_last - gamma))^T: thread writes Kt[d][s] for s = tid % 64, d = tid / 64 + 4 e
+  {
+    const int s = tid & 63;
+    const float f = rkn[s] * __expf(gam[kC - 1] - gam[s]);
+    float* dst = recf + kFRecK / 4;
+#pragma unroll 8
+    for (int e = 0; e < 32; ++e) {
+      const int d = (tid >> 6) + 4 * e;
+      dst[d * kC + s] = Ks[s * kFX + d] * f;
+    }
+  }
+  if (tid == 0) recf[kFRecE / 4] = __expf(gam[kC - 1]);
+}
+
+// Operands of one chunk for one wave of the fp32 scan.
+struct F32Ops {
+  f32x4 w[8];      // W rows 16 w + li, k chunks 0..7
+  f32x4 qe[8];     // Qe rows 16 w + li
+  f32x4 p[4];      // P row 16 w + li, position chunks 0..3 (chunks past w unused)
+  f32x4 kt[2][4];  // Kt rows 32 w + 16 i + li, position chunks 0..3
+  float u[4];      // U rows 16 w + 4 lg + r, the block's column
+  float eg;
+};
+
+__global__ __launch_bounds__(256, 1) void gdn_f32_scan_kernel(const char* __restrict__ ws, const float* s_in,
+                                                              float* s_out, float* __restrict__ o, int T, int NC,
+                                                              int H, int B) {
+  __shared__ f32x4 sS[8][64];  // state row tiles (D layout) of the four waves
+  __shared__ f32x4 sV[4][64];  // V row tiles
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int li = lane & 15, lg = lane >> 4;
+  // the 8 blocks of one (row, head) read the same records: place them on one XCD (block i runs on XCD i % 8)
+  const int nunits = H * B, L = blockIdx.x;
+  int sl, unit;
+  if ((nunits & 7) == 0) {
+    sl = (L >> 3) & 7;
+    unit = 8 * (L >> 6) + (L & 7);
+  } else {
+    sl = L & 7;
+    unit = L >> 3;
+  }
+  const int h = unit % H, b = unit / H;
+  const int col = 16 * sl + li;
+  const char* rec0 = ws + (size_t)unit * NC * kFRecBytes;
+  const size_t sbase = (size_t)unit * kD * kD;
+
+  f32x4 S[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[i][r] = s_in ? s_in[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col] : 0.f;
+
+  auto load = [&](int c, F32Ops& op) {
+    const char* rec = rec0 + (size_t)min(c, NC - 1) * kFRecBytes;
+    const float* rf = reinterpret_cast<const float*>(rec);
+#pragma unroll
+    for (int kc = 0; kc < 8; ++kc) {
+      op.w[kc] = *reinterpret_cast<const f32x4*>(rf + kFRecW / 4 + (16 * w + li) * kD + 16 * kc + 4 * lg);
+      op.qe[kc] = *reinterpret_cast<const f32x4*>(rf + kFRecQ / 4 + (16 * w + li) * kD + 16 * kc + 4 * lg);
+    }
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+      op.p[kc] = *reinterpret_cast<const f32x4*>(rf + kFRecP / 4 + (16 * w + li) * kC + 16 * kc + 4 * lg);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc)
+        op.kt[i][kc] = *reinterpret_cast<const f32x4*>(rf + kFRecK / 4 + (32 * w + 16 * i + li) * kC + 16 * kc + 4 * lg);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) op.u[r] = rf[kFRecU / 4 + (16 * w + 4 * lg + r) * kD + col];
+    op.eg = rf[kFRecE / 4];
+  };
+
+  auto step = [&](int c, const F32Ops& op) {
+    sS[2 * w][lane] = S[0];
+    sS[2 * w + 1][lane] = S[1];
+    lds_barrier();
+    f32x4 Sb[8];
+#pragma unroll
+    for (int kc = 0; kc < 8; ++kc) Sb[kc] = (kc >> 1) == w ? S[kc & 1] : sS[kc][lane];
+    f32x4 ws_ = zero4(), oacc = zero4();
+#pragma unroll
+    for (int kc = 0; kc < 8; ++kc) {
+      ws_ = mm_k16(op.w[kc], Sb[kc], ws_);
+      oacc = mm_k16(op.qe[kc], Sb[kc], oacc);
+    }
+    f32x4 vn;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vn[r] = op.u[r] - ws_[r];
+    sV[w][lane] = vn;
+    lds_barrier();
+    f32x4 Vb[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) Vb[kc] = kc == w ? vn : sV[kc][lane];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+      if (kc <= w) oacc = mm_k16(op.p[kc], Vb[kc], oacc);
+    const int tb = kC * c + 16 * w + 4 * lg;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (tb + r < T) o[(((size_t)b * T + tb + r) * H + h) * kD + col] = oacc[r];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      f32x4 s;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = op.eg * S[i][r];
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) s = mm_k16(op.kt[i][kc], Vb[kc], s);
+      S[i] = s;
+    }
+  };
+
+  F32Ops o0, o1;
+  load(0, o0);
+  for (int c = 0; c < NC; c += 2) {
+    load(c + 1, o1);
+    step(c, o0);
+    if (c + 1 < NC) {
+      load(c + 2, o0);
+      step(c + 1, o1);
+    }
+  }
+  if (s_out) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_out[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col] = S[i][r];
+  }
+}
+
 }  // namespace q35
 
 extern "C" size_t q35_gdn_chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t Dk, int64_t Dv,
-                                                int64_t chunk_size) {
+                                                int64_t chunk_size, int dtype) {
   using namespace q35;
   if (B <= 0 || T <= 0 || H <= 0 || Dk != kD || Dv != kD || chunk_size != kC) return 0;
+  if (dtype == Q35_F32) return (size_t)B * H * (size_t)((T + kC - 1) / kC) * kFRecBytes;
+  if (dtype != Q35_BF16) return 0;
   const size_t NP = (size_t)((T + kP - 1) / kP);
   return (size_t)B * H * NP * kRecBytes;
 }
@@ -828,25 +1152,29 @@ extern "C" int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v
   if (Dk != kD || Dv != kD || chunk_size != kC) return Q35_EUNSUPPORTED;
   if (B > 65535 || H > 65535 || H * B > (1 << 26) || T > ((int64_t)1 << 30) / (H > Hk ? H : Hk))
     return Q35_EUNSUPPORTED;
-  // the output buffer resource spans one row's [T, H, 128] block and is addressed with 32-bit byte offsets
-  if (T * H * kD * (dtype == Q35_F32 ? 4 : 2) >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
+  // the bf16 scan's output buffer resource spans one row's [T, H, 128] block, addressed with 32-bit byte offsets
+  if (dtype == Q35_BF16 && T * H * kD * 2 >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
   if (dtype != Q35_F32 && dtype != Q35_BF16) return Q35_EUNSUPPORTED;
-  const int64_t NP = (T + kP - 1) / kP;
-  if (NP > 65535) return Q35_EUNSUPPORTED;
-  const size_t need = q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, chunk_size);
+  const size_t need = q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, chunk_size, dtype);
   if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  dim3 g1((unsigned)H, (unsigned)NP, (unsigned)B), g2((unsigned)(16 * H * B));
   if (dtype == Q35_F32) {
-    hipLaunchKernelGGL(gdn_pair_prep_kernel<float>, g1, dim3(512), 0, st, (const float*)q, (const float*)k,
-                       (const float*)v, g, beta, ws, (int)T, (int)NP, (int)Hk, (int)H, scale, use_qk_l2norm);
-    hipLaunchKernelGGL(gdn_pair_scan_kernel<float>, g2, dim3(320), 0, st, ws, initial_state, final_state,
-                       (float*)out, (int)T, (int)NP, (int)H, (int)B);
+    // fp32 inputs: the fp32 WY path (chunk records, then the per-slice scan)
+    const int64_t NC = (T + kC - 1) / kC;
+    if (NC > 65535) return Q35_EUNSUPPORTED;
+    hipLaunchKernelGGL(gdn_f32_prep_kernel, dim3((unsigned)NC, (unsigned)H, (unsigned)B), dim3(256), 0, st,
+                       (const float*)q, (const float*)k, (const float*)v, g, beta, ws, (int)T, (int)NC, (int)Hk,
+                       (int)H, scale, use_qk_l2norm);
+    hipLaunchKernelGGL(gdn_f32_scan_kernel, dim3((unsigned)(8 * H * B)), dim3(256), 0, st, ws, initial_state,
+                       final_state, (float*)out, (int)T, (int)NC, (int)H, (int)B);
   } else {
-    hipLaunchKernelGGL(gdn_pair_prep_kernel<__bf16>, g1, dim3(512), 0, st, (const __bf16*)q, (const __bf16*)k,
+    const int64_t NP = (T + kP - 1) / kP;
+    if (NP > 65535) return Q35_EUNSUPPORTED;
+    dim3 g1((unsigned)H, (unsigned)NP, (unsigned)B), g2((unsigned)(16 * H * B));
+    hipLaunchKernelGGL(gdn_pair_prep_kernel, g1, dim3(512), 0, st, (const __bf16*)q, (const __bf16*)k,
                        (const __bf16*)v, g, beta, ws, (int)T, (int)NP, (int)Hk, (int)H, scale, use_qk_l2norm);
-    hipLaunchKernelGGL(gdn_pair_scan_kernel<__bf16>, g2, dim3(320), 0, st, ws, initial_state, final_state,
+    hipLaunchKernelGGL(gdn_pair_scan_kernel, g2, dim3(320), 0, st, ws, initial_state, final_state,
                        (__bf16*)out, (int)T, (int)NP, (int)H, (int)B);
   }
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;

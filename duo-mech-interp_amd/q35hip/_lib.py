@@ -35,7 +35,7 @@ _SIGS = {
     "q35_status_string": ([I32], ctypes.c_char_p),
     "q35_abi_version": ([], I32),
     "q35_gdn_recurrent": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I32, F32, I32, P], I32),
-    "q35_gdn_chunk_workspace_bytes": ([I64, I64, I64, I64, I64, I64], SZ),
+    "q35_gdn_chunk_workspace_bytes": ([I64, I64, I64, I64, I64, I64, I32], SZ),
     "q35_gdn_chunk_prefill": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I32, F32, I32, I64, P, SZ, P],
                               I32),
     "q35_gated_attn_prefill_workspace_bytes": ([I64, I64, I64, I64, I64], SZ),

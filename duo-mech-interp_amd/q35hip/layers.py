@@ -55,9 +55,8 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     """Gated DeltaNet mixer of one decoder layer (Qwen3_5GatedDeltaNet.forward, HF:432-543; the WGSL conv + delta
     kernels, engine/kernels_qwen35.js:127-247). x: [B, T, H] fp32 (the input-normed residual). A call with T == 1
     is one recurrent decode step (HF:505-517). T > 1 runs from rec_state either the chunked prefill (HF:518-530;
-    prefill="chunk": bf16 MFMA products, relative error a few 1e-3) or the token-serial fp32 recurrence
-    (prefill="recurrent": fp32 throughout, as the WGSL engine runs prefill token by token,
-    engine/kernels_qwen35.js:183-247). Both states are updated in place. head_scale: optional [Hv] per-head output
+    prefill="chunk": products at the precision of x, fp32 for fp32 x) or the token-serial fp32 recurrence
+    (prefill="recurrent": as the WGSL engine runs prefill token by token, engine/kernels_qwen35.js:183-247). Both states are updated in place. head_scale: optional [Hv] per-head output
     scale applied after the gated norm (engine/kernels_qwen35.js:243). num_k_heads / head_k_dim default to the
     value heads / value head dim (the Qwen3.5 text models use Hk = Hv and dk = dv). prenorm: see linear() (x is then
     the residual and the layer's input norm runs inside the input projection). Returns y [B, T, H]."""

@@ -79,10 +79,10 @@ class HybridModel:
     """B independent rows decoded together (the boosted / as-is / suppressed rows of the reference's steer loop,
     engine/analysis.js:117-145). fp32 residual stream; vectors added after steer_layer at every position.
 
-    gdn_prefill selects the Gated DeltaNet prefill kernel: "recurrent" (default) runs the fp32 token-serial kernel,
-    whose outputs agree with the fp32 CPU recurrence to about 1e-6, so greedy tokens follow the fp32 reference even
-    through near ties of a few 1e-3 in the logits; "chunk" runs the chunked bf16-MFMA kernel (faster prefill,
-    relative error a few 1e-3 per layer).
+    gdn_prefill selects the Gated DeltaNet prefill kernel: "chunk" (default) runs the chunked form, which on the
+    stack's fp32 activations computes every product in fp32 (agreement with the fp32 CPU recurrence to about 1e-6,
+    so greedy tokens follow the fp32 reference through near ties of a few 1e-3 in the logits); "recurrent" runs the
+    token-serial fp32 kernel (the WGSL engine's order, token by token; slower).
 
     Positions live on the device (pos_dev, [rows] int32) and the steering vectors in fixed buffers, so a decode step
     has no host-dependent arguments: enable_decode_graph() captures one step in a HIP graph that decode_step()
@@ -90,7 +90,7 @@ class HybridModel:
 
     MAX_VECS = 4  # vector rows of the steering buffer (the WGSL resAdd clamps its row index to 3, engine/kernels.js:201)
 
-    def __init__(self, cfg, W, device, max_len=4096, rows=3, steer_layer=12, gdn_prefill="recurrent"):
+    def __init__(self, cfg, W, device, max_len=4096, rows=3, steer_layer=12, gdn_prefill="chunk"):
         if gdn_prefill not in ("chunk", "recurrent"):
             raise ValueError(f"HybridModel: gdn_prefill must be 'chunk' or 'recurrent', not {gdn_prefill!r}")
         self.cfg, self.device, self.steer_layer = cfg, device, steer_layer

@@ -121,7 +121,7 @@ def _gdn_decode_step_impl(q, k, v, g, beta, state, scale, use_qk_l2norm):
 def _gdn_chunk_impl(q, k, v, g, beta, initial_state, chunk_size, scale, use_qk_l2norm):
     B, T, Hk, H, Dk, Dv = _gdn_check(q, k, v, g, beta, initial_state)
     L = _lib.lib()
-    nbytes = L.q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, chunk_size)
+    nbytes = L.q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, chunk_size, _DT[q.dtype])
     _require(nbytes > 0, f"unsupported chunk prefill shape (Dk={Dk}, Dv={Dv}, chunk={chunk_size})")
     ws = _workspace(nbytes, q.device)
     o = torch.empty_like(v)

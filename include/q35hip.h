@@ -91,9 +91,13 @@ int q35_gdn_recurrent(const void* q, const void* k, const void* v, const float* 
  * Gated delta rule, chunked form (prefill). Replaces torch_chunk_gated_delta_rule at HF:249-327: the same
  * arguments and layouts as q35_gdn_recurrent, chunk_size 64 (the only size this build supports). T need not be a
  * multiple of 64 (the tail chunk is zero-padded as HF:271-277 does). Needs a workspace of
- * q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, 64) bytes (256-byte aligned).
+ * q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, 64, dtype) bytes (256-byte aligned).
+ * The arithmetic follows the input dtype: bf16 q/k/v use bf16 MFMA products with fp32 accumulation (relative error
+ * a few 1e-3 against the fp32 recurrence); fp32 q/k/v compute every product in fp32 (agreement with the fp32
+ * recurrence to fp32 rounding, about 1e-6). The state is fp32 in both.
  */
-size_t q35_gdn_chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t Dk, int64_t Dv, int64_t chunk_size);
+size_t q35_gdn_chunk_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t Dk, int64_t Dv, int64_t chunk_size,
+                                     int dtype);
 int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v, const float* g, const float* beta,
                           const float* initial_state, float* final_state, void* out,
                           int64_t B, int64_t T, int64_t Hk, int64_t H, int64_t Dk, int64_t Dv,

@@ -39,7 +39,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 5
+    assert L.q35_abi_version() == 6
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -57,7 +57,11 @@ def test_validation_rejects_without_launching():
     assert L.q35_gdn_recurrent(fake, fake, fake, fake, fake, None, fake, fake, 1, 1, 3, 4, 128, 128, 1, 1.0, 1,
                                None) == 1
     # chunk size other than 64
-    assert L.q35_gdn_chunk_workspace_bytes(1, 128, 16, 128, 128, 32) == 0
+    assert L.q35_gdn_chunk_workspace_bytes(1, 128, 16, 128, 128, 32, 1) == 0
+    # the workspace follows the input dtype: bf16 pair records (128 positions) and fp32 chunk records (64)
+    assert L.q35_gdn_chunk_workspace_bytes(1, 130, 2, 128, 128, 64, 1) == 2 * 2 * 131328
+    assert L.q35_gdn_chunk_workspace_bytes(1, 130, 2, 128, 128, 64, 0) == 2 * 3 * 147712
+    assert L.q35_gdn_chunk_workspace_bytes(1, 130, 2, 128, 128, 64, 2) == 0
     assert L.q35_gdn_chunk_prefill(fake, fake, fake, fake, fake, None, fake, fake, 1, 128, 16, 16, 128, 128, 1, 1.0,
                                    1, 32, fake, 1 << 30, None) == 2
     # workspace too small

@@ -64,32 +64,47 @@ def test_tiny_stack_decode_graph_replays_match_eager():
         assert oracle.rel_err(lg.cpu(), le.cpu()) <= 1e-6, f"replay {step} differs from eager"
 
 
+_FULL_REF = {}
+
+
+def _full_stack_reference(cfg, W, prompt, steps):
+    """The fp32 CPU oracle's steered greedy run of the full stack (computed once per test module)."""
+    if "toks" not in _FULL_REF:
+        announce("model full stack: CPU oracle")
+        ref = om.OracleModel(cfg, W, steer_layer=12)
+        _, resid = ref.forward(prompt[:1], collect_layer=12, stop_after=12)
+        med = om.median_resid_norm(resid[0])
+        v_ref = torch.randn(cfg.hidden, generator=torch.Generator().manual_seed(0))
+        v_ref = v_ref / v_ref.norm() * (0.8 * med)
+        ref.reset()
+        ref.set_vectors(torch.stack([v_ref, torch.zeros_like(v_ref), -v_ref]))
+        toks_r, marg_r = om.greedy(ref, prompt, steps)
+        _FULL_REF.update(toks=toks_r, margins=marg_r, v=v_ref)
+    return _FULL_REF["toks"], _FULL_REF["margins"], _FULL_REF["v"]
+
+
 @pytest.mark.timeout(1800)
-def test_full_stack_steered_greedy_64_steps():
+@pytest.mark.parametrize("gdn_prefill", ["chunk", "recurrent"])
+def test_full_stack_steered_greedy_64_steps(gdn_prefill):
     """Qwen3.5-0.8B shape (24 layers, hidden 1024, int8 SwiGLU 3584, tied 151,936 embedding), seed 0; batch 3,
     2048-token prompt (seed 0) on every row, vector after layer 12 scaled to 0.8 x the median residual norm: +v on
     row 0, none on row 1, -v on row 2; greedy tokens must be identical to the fp32 CPU path for 64 steps (decode
-    steps replayed from a captured HIP graph)."""
+    steps replayed from a captured HIP graph). Run with each Gated DeltaNet prefill kernel: the chunked one (fp32
+    inputs: fp32 products) and the token-serial one."""
     dev = device()
     torch.set_num_threads(min(16, os.cpu_count() or 1))
     cfg = workloads.Q35Config()
     W = workloads.init_weights(cfg, seed=0)
     prompt = torch.randint(0, cfg.vocab, (1, 2048), generator=torch.Generator().manual_seed(0)).repeat(3, 1)
     steps = 64
-    announce("model full stack: GPU (fp32 token-serial GDN prefill)")
-    g = gm.HybridModel(cfg, W, dev, max_len=2048 + steps + 8, rows=3, gdn_prefill="recurrent")
+    announce(f"model full stack: GPU (GDN prefill {gdn_prefill})")
+    g = gm.HybridModel(cfg, W, dev, max_len=2048 + steps + 8, rows=3, gdn_prefill=gdn_prefill)
     g.enable_decode_graph()  # the 64 greedy steps replay one captured decode step
     toks_g, marg_g, v = gm.steered_greedy(g, prompt, steps)
-    announce("model full stack: CPU oracle")
-    ref = om.OracleModel(cfg, W, steer_layer=12)
-    _, resid = ref.forward(prompt[:1], collect_layer=12, stop_after=12)
-    med = om.median_resid_norm(resid[0])
-    v_ref = torch.randn(cfg.hidden, generator=torch.Generator().manual_seed(0))
-    v_ref = v_ref / v_ref.norm() * (0.8 * med)
+    del g
+    torch.cuda.empty_cache()
+    toks_r, marg_r, v_ref = _full_stack_reference(cfg, W, prompt, steps)
     assert oracle.rel_err(v, v_ref) <= 1e-3
-    ref.reset()
-    ref.set_vectors(torch.stack([v_ref, torch.zeros_like(v_ref), -v_ref]))
-    toks_r, marg_r = om.greedy(ref, prompt, steps)
     same = (toks_g == toks_r)
     first_diff = [int((~same[r]).nonzero()[0]) if not bool(same[r].all()) else -1 for r in range(3)]
     print(f"min top-2 margin (CPU) {float(marg_r.min()):.4g}; first differing step per row {first_diff}")
