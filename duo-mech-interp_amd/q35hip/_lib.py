@@ -22,6 +22,7 @@ EXPORTS = [
 ]
 
 Q35_F32, Q35_BF16, Q35_I8 = 0, 1, 2
+ABI_VERSION = 6  # the signatures below; q35_abi_version() of the loaded library must match
 
 _lib = None
 
@@ -68,6 +69,11 @@ def lib():
             raise Q35Error(f"q35hip: {LIB_PATH} is missing; build it with __graft_entry__.build() "
                            "(python -m q35hip.build). There is no CPU fallback.")
         L = ctypes.CDLL(LIB_PATH)
+        L.q35_abi_version.restype = I32
+        found = L.q35_abi_version()
+        if found != ABI_VERSION:
+            raise Q35Error(f"q35hip: {LIB_PATH} has ABI version {found}, this package binds version {ABI_VERSION}; "
+                           "rebuild it with __graft_entry__.build() (python -m q35hip.build)")
         for name, (argt, rest) in _SIGS.items():
             fn = getattr(L, name)
             fn.argtypes = argt
