@@ -15,6 +15,9 @@
 // Pass 2 (attn_decode_merge_kernel): log-sum-exp merge over splits, sigmoid gate, bf16 store; every load of a
 // thread is issued before the first is used (one memory round trip).
 // HBM traffic is the K and V spans once (AI ~ 4 flop/byte): the kernel is bandwidth bound by design.
+#include <atomic>
+#include <mutex>
+
 #include "q35_common.h"
 #include "q35hip.h"
 
@@ -356,13 +359,11 @@ extern "C" size_t q35_gated_attn_decode_workspace_bytes(int64_t B, int64_t Hq, i
   return (size_t)B * Hq * S * (size_t)(D + 2) * sizeof(float);
 }
 
-extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* gate,
-                                     const int32_t* cache_len, const float* cos, const float* sin, void* out,
-                                     int out_dtype,
-                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
-                                     float scale, int64_t splits, void* workspace, size_t workspace_bytes,
-                                     q35_stream_t stream) {
-  using namespace q35;
+namespace q35 {
+// Argument checks shared by both decode entry points (no HIP call).
+static int decode_check(const void* q, const void* k_cache, const void* v_cache, const void* gate,
+                        const int32_t* cache_len, const float* cos, const float* sin, const void* out, int out_dtype,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot, int64_t splits) {
   if (!q || !k_cache || !v_cache || !gate || !cache_len || !out) return Q35_EINVAL;
   if (out_dtype != Q35_BF16 && out_dtype != Q35_F32) return Q35_EUNSUPPORTED;
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D || (rot & 1))
@@ -375,6 +376,23 @@ extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const v
   int nt;
   const int S = decode_splits(B, Hkv, max_len, splits, &nt);
   if ((int64_t)S * 64 * nt > ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
+  return Q35_OK;
+}
+}  // namespace q35
+
+extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* gate,
+                                     const int32_t* cache_len, const float* cos, const float* sin, void* out,
+                                     int out_dtype,
+                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
+                                     float scale, int64_t splits, void* workspace, size_t workspace_bytes,
+                                     q35_stream_t stream) {
+  using namespace q35;
+  const int chk = decode_check(q, k_cache, v_cache, gate, cache_len, cos, sin, out, out_dtype, B, Hq, Hkv, D,
+                               max_len, rot, splits);
+  if (chk != Q35_OK) return chk;
+  const int64_t G = Hq / Hkv;
+  int nt;
+  const int S = decode_splits(B, Hkv, max_len, splits, &nt);
   const size_t need = q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits);
   if (!workspace || workspace_bytes < need) return Q35_EWORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -408,4 +426,57 @@ extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const v
     hipLaunchKernelGGL(attn_decode_merge_kernel<__bf16>, mgrid, dim3(256), 0, st, part, (const __bf16*)gate,
                        (__bf16*)out, (int)Hq, (int)Hkv, S);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+// ---- Allocation-free variant. The split-K partials live in a fixed device array of this file instead of a caller
+// workspace. Each device holds its own copy of the array (for the life of the process); its address on a device is
+// resolved once, on the first call with that device current, and kept per device. Every call on a device shares the
+// array: calls that overlap on one device race. Nothing in it needs clearing between calls: every partial the merge
+// reads is written by the same call's first kernel (an empty split writes max -inf, sum 0).
+namespace q35 {
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+}  // namespace q35
+
+static __device__ __align__(256) unsigned char scratch[q35::kNoAllocScratchBytes];
+
+namespace q35 {
+// The device address of `scratch` on the current device (the host-side name is only a stand-in for the symbol).
+static int scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return Q35_ELAUNCH;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return Q35_ELAUNCH;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return Q35_OK;
+}
+}  // namespace q35
+
+extern "C" size_t q35_gated_attn_decode_noalloc_max_bytes(void) { return q35::kNoAllocScratchBytes; }
+
+extern "C" int q35_gated_attn_decode_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                             const void* gate, const int32_t* cache_len, const float* cos,
+                                             const float* sin, void* out, int out_dtype, int64_t B, int64_t Hq,
+                                             int64_t Hkv, int64_t D, int64_t max_len, int64_t rot, float scale,
+                                             int64_t splits, q35_stream_t stream) {
+  using namespace q35;
+  const int chk = decode_check(q, k_cache, v_cache, gate, cache_len, cos, sin, out, out_dtype, B, Hq, Hkv, D,
+                               max_len, rot, splits);
+  if (chk != Q35_OK) return chk;
+  if (q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits) > kNoAllocScratchBytes)
+    return Q35_ESCRATCH;
+  void* ws = nullptr;
+  const int st = scratch_on_current_device(&ws);
+  if (st != Q35_OK) return st;
+  return q35_gated_attn_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, out, out_dtype, B, Hq, Hkv, D,
+                               max_len, rot, scale, splits, ws, kNoAllocScratchBytes, stream);
 }

@@ -8,6 +8,7 @@ extern "C" const char* q35_status_string(int status) {
     case Q35_EUNSUPPORTED: return "unsupported size or dtype for this build";
     case Q35_EWORKSPACE: return "workspace missing or too small";
     case Q35_ELAUNCH: return "kernel launch failed";
+    case Q35_ESCRATCH: return "request exceeds the fixed scratch of an allocation-free entry point";
     default: return "unknown status";
   }
 }

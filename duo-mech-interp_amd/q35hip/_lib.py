@@ -15,13 +15,14 @@ EXPORTS = [
     "q35_status_string", "q35_abi_version",
     "q35_gdn_recurrent", "q35_gdn_chunk_workspace_bytes", "q35_gdn_chunk_prefill",
     "q35_gated_attn_prefill_workspace_bytes", "q35_gated_attn_prefill", "q35_gated_attn_decode_workspace_bytes",
-    "q35_gated_attn_decode",
+    "q35_gated_attn_decode", "q35_gated_attn_decode_noalloc_max_bytes", "q35_gated_attn_decode_noalloc",
     "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
     "q35_swiglu_push",
     "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm",
 ]
 
 Q35_F32, Q35_BF16, Q35_I8 = 0, 1, 2
+Q35_ESCRATCH = 5
 ABI_VERSION = 6  # the signatures below; q35_abi_version() of the loaded library must match
 
 _lib = None
@@ -43,6 +44,8 @@ _SIGS = {
     "q35_gated_attn_prefill": ([P, P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, F32, P, SZ, P], I32),
     "q35_gated_attn_decode_workspace_bytes": ([I64, I64, I64, I64, I64, I64], SZ),
     "q35_gated_attn_decode": ([P, P, P, P, P, P, P, P, I32, I64, I64, I64, I64, I64, I64, F32, I64, P, SZ, P], I32),
+    "q35_gated_attn_decode_noalloc_max_bytes": ([], SZ),
+    "q35_gated_attn_decode_noalloc": ([P, P, P, P, P, P, P, P, I32, I64, I64, I64, I64, I64, I64, F32, I64, P], I32),
     "q35_resid_add_rows": ([P, P, P, I64, I64, I64, I64, I32, P], I32),
     "q35_gdn_conv": ([P, I64, P, P, P, P, P, I64, I64, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, P], I32),
     "q35_gated_rmsnorm": ([P, P, I64, P, P, P, I64, I64, I64, F32, I32, P], I32),

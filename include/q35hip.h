@@ -51,7 +51,8 @@ enum q35_status {
   Q35_EINVAL = 1,       /* null pointer, non-positive size, or inconsistent sizes */
   Q35_EUNSUPPORTED = 2, /* a size or dtype this build has no kernel for (e.g. head dim other than 128 / 256) */
   Q35_EWORKSPACE = 3,   /* workspace pointer null or smaller than *_workspace_bytes */
-  Q35_ELAUNCH = 4       /* the HIP runtime refused a kernel launch */
+  Q35_ELAUNCH = 4,      /* the HIP runtime refused a kernel launch */
+  Q35_ESCRATCH = 5      /* an allocation-free entry point's fixed scratch is too small for the request */
 };
 
 enum q35_dtype { Q35_F32 = 0, Q35_BF16 = 1, Q35_I8 = 2 };
@@ -142,6 +143,22 @@ int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cach
                           int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
                           float scale, int64_t splits, void* workspace, size_t workspace_bytes,
                           q35_stream_t stream);
+
+/*
+ * q35_gated_attn_decode without a workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation). This entry point has no counterpart in the
+ * reference. The split-K partials go to a fixed device array of q35_gated_attn_decode_noalloc_max_bytes() bytes
+ * (8 MiB; one copy per device, held until the process ends); a call whose q35_gated_attn_decode_workspace_bytes(...)
+ * exceeds it returns Q35_ESCRATCH without launching (8 MiB covers B <= 128 at an 8192-token cache with Hq 8).
+ * The stream's device must be the current device. Calls that overlap on one device race for the array. No memory
+ * is allocated or freed; the array's device address is looked up on the first call per device. Arguments and
+ * results are otherwise exactly those of q35_gated_attn_decode (same kernels, bitwise identical outputs).
+ */
+size_t q35_gated_attn_decode_noalloc_max_bytes(void);
+int q35_gated_attn_decode_noalloc(const void* q, const void* k_cache, const void* v_cache, const void* gate,
+                                  const int32_t* cache_len, const float* cos, const float* sin, void* out,
+                                  int out_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
+                                  int64_t rot, float scale, int64_t splits, q35_stream_t stream);
 
 /*
  * Residual steering add: x[r, t, :] += vecs[vec_of_row[r], :] for every row r and position t; rows whose index is
