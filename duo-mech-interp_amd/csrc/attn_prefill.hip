@@ -53,6 +53,41 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
 __device__ __forceinline__ int vperm(int p) { return (p & 3) | ((p & 4) << 1) | ((p & 8) >> 1); }
 
 // ---------------------------------------------------------------------------------------------------------------
+// V^T of one 64-key tile: keys key0 .. key0 + 63 of the rows vrow0 + key * rstride (zero for keys >= nk) into the
+// head's V^T block vth [256 dims][Tp keys]. Thread = (8 keys kg, 8 dims dg): an 8 x 8 transpose in registers, each
+// dim row written as two 8-byte pieces (keys kg*8 .. +3 and +4 .. +7 land 8 positions apart after the in-group
+// permutation).
+__device__ __forceinline__ void vt_tile(const __bf16* __restrict__ vrow0, size_t rstride, int key0, int nk,
+                                        __bf16* __restrict__ vth, int Tp, int tid) {
+  const int kg = tid >> 5, dg = tid & 31;
+  u32x4 w[8];
+  const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int key = key0 + 8 * kg + i;
+    const u32x4 ld = *reinterpret_cast<const u32x4*>(vrow0 + (size_t)min(key, nk - 1) * rstride + 8 * dg);
+    w[i] = key < nk ? ld : z;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    auto h16 = [&](const u32x4& r) -> uint32_t {
+      const uint32_t x = r[e >> 1];
+      return (e & 1) ? (x >> 16) : (x & 0xffffu);
+    };
+    u32x2 lo, hi;
+    lo[0] = h16(w[0]) | (h16(w[1]) << 16);
+    lo[1] = h16(w[2]) | (h16(w[3]) << 16);
+    hi[0] = h16(w[4]) | (h16(w[5]) << 16);
+    hi[1] = h16(w[6]) | (h16(w[7]) << 16);
+    const int d = 8 * dg + e;
+    const int p0 = 8 * kg;  // first key of this unit inside the tile
+    __bf16* row = vth + (size_t)d * Tp + key0 + (p0 & ~15);
+    *reinterpret_cast<u32x2*>(row + vperm(p0 & 15)) = lo;
+    *reinterpret_cast<u32x2*>(row + vperm((p0 & 15) + 4)) = hi;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // Kernel 1: one block of 256 threads per (64 keys, kv head, row) for the keys and another for the values. ROT
 // (rotary dims) is a template parameter so that the rotation pairs are compile-time register indices.
 template <int ROT>
@@ -115,37 +150,21 @@ __global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restr
       *reinterpret_cast<u32x4*>(dst + 8 * sg) = valid ? o : z;
     }
   }
-  // V^T: thread = (8 keys kg, 8 dims dg); an 8 x 8 transpose in registers, each dim row written as two 8-byte
-  // pieces (keys kg*8 .. +3 and +4 .. +7 land 8 positions apart after the in-group permutation)
   else {
-    const int kg = tid >> 5, dg = tid & 31;
-    u32x4 w[8];
-    const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = key0 + 8 * kg + i;
-      const u32x4 ld = *reinterpret_cast<const u32x4*>(v + (((size_t)b * T + min(key, T - 1)) * Hkv + kvh) * kPD +
-                                                      8 * dg);
-      w[i] = key < T ? ld : z;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      auto h16 = [&](const u32x4& r) -> uint32_t {
-        const uint32_t x = r[e >> 1];
-        return (e & 1) ? (x >> 16) : (x & 0xffffu);
-      };
-      u32x2 lo, hi;
-      lo[0] = h16(w[0]) | (h16(w[1]) << 16);
-      lo[1] = h16(w[2]) | (h16(w[3]) << 16);
-      hi[0] = h16(w[4]) | (h16(w[5]) << 16);
-      hi[1] = h16(w[6]) | (h16(w[7]) << 16);
-      const int d = 8 * dg + e;
-      const int p0 = 8 * kg;  // first key of this unit inside the tile
-      __bf16* row = vt + (head * kPD + d) * Tp + key0 + (p0 & ~15);
-      *reinterpret_cast<u32x2*>(row + vperm(p0 & 15)) = lo;
-      *reinterpret_cast<u32x2*>(row + vperm((p0 & 15) + 4)) = hi;
-    }
+    vt_tile(v + ((size_t)b * T * Hkv + kvh) * kPD, (size_t)Hkv * kPD, key0, T, vt + head * kPD * Tp, Tp, tid);
   }
+}
+
+// Cached prefill: V^T of the cache rows a row's queries attend to (keys 0 .. P_b + T - 1, P_b = pos[b]; zero past
+// them within the last tile) into the workspace [B, Hkv, D, Tp], Tp the cache length; tiles past them are skipped.
+__global__ __launch_bounds__(256) void attn_vcache_prep_kernel(const __bf16* __restrict__ v_cache,
+                                                               const int32_t* __restrict__ pos,
+                                                               __bf16* __restrict__ vt, int T, int Tp, int Hkv) {
+  const int key0 = blockIdx.x * kBN, kvh = blockIdx.y, b = blockIdx.z;
+  const int nk = min(max(pos[b], 0), Tp - T) + T;
+  if (key0 >= nk) return;
+  const size_t head = (size_t)b * Hkv + kvh;
+  vt_tile(v_cache + head * Tp * kPD, kPD, key0, nk, vt + head * kPD * Tp, Tp, threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -224,8 +243,9 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ kr, const __bf16* __restrict__ vt,
     const __bf16* __restrict__ gate, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos0,
     __bf16* __restrict__ out, int T, int Tp, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb, int B,
-    int Ls, float* __restrict__ part) {
-  Q35_ARGS_UPFRONT(q, kr, vt, gate, cos_t, sin_t, pos0, out, T, Tp, Hq, Hkv, ngroups, rot, scale, nqb, B, Ls, part);
+    int Ls, float* __restrict__ part, const int32_t* __restrict__ pos_dev) {
+  Q35_ARGS_UPFRONT(q, kr, vt, gate, cos_t, sin_t, pos0, out, T, Tp, Hq, Hkv, ngroups, rot, scale, nqb, B, Ls, part,
+                   pos_dev);
   __shared__ PfStage stage[2];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -243,6 +263,11 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
   const size_t head = (size_t)b * Hkv + kvh;
   const char* kbase = reinterpret_cast<const char*>(kr + head * Tp * kPD);
   const char* vbase = reinterpret_cast<const char*>(vt + head * kPD * Tp);
+  // Cached mode (pos_dev set): the keys are the KV-cache rows 0 .. P + T - 1 of this row, P = pos_dev[b] the
+  // position of the call's first token (kr is the cache itself, Tp its length); query t sits at position P + t and
+  // attends to keys 0 .. P + t. Otherwise the keys are the call's own T tokens at positions pos0 .. pos0 + T - 1.
+  const int qshift = pos_dev ? min(max(pos_dev[b], 0), Tp - T) : 0;
+  const int rpos0 = pos_dev ? qshift : pos0;
 
   // This wave's share of the copies of tile kt into stage s: CPW of the 32 K copies (2 rows each) and CPW of the
   // 32 V^T copies (8 rows each). Copy c of K fills LDS rows 2c, 2c + 1; lane i fetches the 16 bytes that belong at
@@ -273,9 +298,11 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
 
   // One item (or one segment of a paired item): its query block's tiles kt0 .. kt1 - 1. Inlined once per segment,
   // so each copy is straight-line code with its own register allocation.
-  auto run = [&](const PfItem it) {
+  auto run = [&](PfItem it) {
     const int qb = it.qb;
     const int q0 = qb * kBQ;
+    // cached mode: the block's key tiles end at its last query's position
+    if (pos_dev) it.kt1 = (qshift + min(q0 + kBQ - 1, T - 1)) / kBN + 1;
 
     // ---- Q^T operand (B of S^T = K Q^T): lane holds query q0 + ln, dims 16 ks + 8 hh + j, rotated. Every load (the
     //      query row, the rotation partners and the cos / sin rows) is issued before the first tile's copies and before
@@ -285,7 +312,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
       const int t = q0 + ln;
       const bool tv = t < T;
       const __bf16* qrow = q + (((size_t)b * T + (tv ? t : T - 1)) * Hq + h) * kPD;
-      const int pos = pos0 + (tv ? t : T - 1);
+      const int pos = rpos0 + (tv ? t : T - 1);
       u32x4 raw[16];
 #pragma unroll
       for (int ks = 0; ks < 16; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * hh);
@@ -340,7 +367,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     const float csc = scale * 1.44269504088896341f;
     float m_run = -INFINITY, l_run = 0.f;
     const int tq = q0 + ln;  // this lane's query
-    const int full_tiles = q0 / kBN;  // tiles entirely below this block's first query: no mask
+    const int full_tiles = (qshift + q0) / kBN;  // tiles entirely below this block's first query: no mask
 
     // Per-lane LDS read offsets inside a stage. K: row 32 ksub + ln, logical segment 2 ks + hh, stored at segment
     // (2 ks + hh) ^ (ln & 15): for ks = 8 a + j the offset is ka[j] + 256 a + 16384 ksub. V^T: row 32 mt + ln, logical
@@ -407,7 +434,8 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int key = kl0 + 32 * ksub + 8 * (i >> 2) + (i & 3);
-            const float x = (key <= tq && key < T) ? acc[ksub][0][i] + acc[ksub][1][i] : -INFINITY;
+            const float x = (key <= tq + qshift && key < T + qshift) ? acc[ksub][0][i] + acc[ksub][1][i]
+                                                                          : -INFINITY;
             sc[ksub][i] = x;
             mx = fmaxf(mx, x);
           }
@@ -722,7 +750,7 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
   hipLaunchKernelGGL((paired ? attn_prefill_kernel<GG, true> : attn_prefill_kernel<GG, false>),                \
                      dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q, kr, vt, (const __bf16*)gate, \
                      cos, sin, (int)pos0, (__bf16*)out, (int)T, (int)Tp, (int)Hq, (int)Hkv, ngroups, (int)rot,     \
-                     scale, (int)nqb, (int)B, Ls, part);                                                           \
+                     scale, (int)nqb, (int)B, Ls, part, (const int32_t*)nullptr);                                 \
   if (lay.npairs > 0)                                                                                             \
     hipLaunchKernelGGL(attn_prefill_merge_kernel<GG>, dim3((unsigned)lay.npairs, GG), dim3(256), 0, st, part,       \
                        (const __bf16*)gate, (__bf16*)out, (int)T, (int)Hq, (int)Hkv, ngroups, (int)B, Ls)
@@ -732,5 +760,55 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
     default: Q35_PF_LAUNCH(4); break;
   }
 #undef Q35_PF_LAUNCH
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+extern "C" size_t q35_gated_attn_prefill_cached_workspace_bytes(int64_t B, int64_t Hkv, int64_t D, int64_t max_len) {
+  using namespace q35;
+  if (B <= 0 || Hkv <= 0 || D != kPD || max_len <= 0 || max_len % kBN != 0) return 0;
+  return ((size_t)B * Hkv * kPD * max_len * sizeof(__bf16) + 255) / 256 * 256;
+}
+
+extern "C" int q35_gated_attn_prefill_cached(const void* q, const void* k_cache, const void* v_cache,
+                                             const void* gate, const int32_t* pos, const float* cos,
+                                             const float* sin, void* out, int64_t B, int64_t T, int64_t Hq,
+                                             int64_t Hkv, int64_t D, int64_t max_len, int64_t rot, float scale,
+                                             void* workspace, size_t workspace_bytes, q35_stream_t stream) {
+  using namespace q35;
+  if (!q || !k_cache || !v_cache || !gate || !pos || !out) return Q35_EINVAL;
+  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D ||
+      T > max_len)
+    return Q35_EINVAL;
+  if (rot > 0 && (!cos || !sin)) return Q35_EINVAL;
+  if (D != kPD || (rot % 16) != 0 || rot > kRotMax || max_len % kBN != 0) return Q35_EUNSUPPORTED;
+  const int64_t G = Hq / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return Q35_EUNSUPPORTED;
+  const int GW = G > 4 ? 4 : (int)G;
+  const int ngroups = (int)(G / GW);
+  if (max_len > ((int64_t)1 << 30) || B > 65535 || Hkv > 65535 || T * Hq * D > ((int64_t)1 << 40))
+    return Q35_EUNSUPPORTED;
+  // V^T rows and cache key rows are addressed with 32-bit byte offsets inside a head's block
+  if (max_len * kPD * 2 >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
+  const int64_t nqb = (T + kBQ - 1) / kBQ;
+  const int64_t nblocks = nqb * B * Hkv * ngroups;
+  if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
+  const size_t need = q35_gated_attn_prefill_cached_workspace_bytes(B, Hkv, D, max_len);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  __bf16* vt = static_cast<__bf16*>(workspace);
+  hipLaunchKernelGGL(attn_vcache_prep_kernel, dim3((unsigned)(max_len / kBN), (unsigned)Hkv, (unsigned)B), dim3(256),
+                     0, st, (const __bf16*)v_cache, pos, vt, (int)T, (int)max_len, (int)Hkv);
+  // one item per query block (no key split: the key range depends on the device positions), latest block first
+#define Q35_PFC_LAUNCH(GG)                                                                                        \
+  hipLaunchKernelGGL((attn_prefill_kernel<GG, false>), dim3((unsigned)nblocks), dim3(64 * GG), 0, st,            \
+                     (const __bf16*)q, (const __bf16*)k_cache, vt, (const __bf16*)gate, cos, sin, 0, (__bf16*)out, \
+                     (int)T, (int)max_len, (int)Hq, (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B, 0,        \
+                     (float*)nullptr, pos)
+  switch (GW) {
+    case 1: Q35_PFC_LAUNCH(1); break;
+    case 2: Q35_PFC_LAUNCH(2); break;
+    default: Q35_PFC_LAUNCH(4); break;
+  }
+#undef Q35_PFC_LAUNCH
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }

@@ -14,7 +14,8 @@ from .build import LIB_PATH
 EXPORTS = [
     "q35_status_string", "q35_abi_version",
     "q35_gdn_recurrent", "q35_gdn_chunk_workspace_bytes", "q35_gdn_chunk_prefill",
-    "q35_gated_attn_prefill_workspace_bytes", "q35_gated_attn_prefill", "q35_gated_attn_decode_workspace_bytes",
+    "q35_gated_attn_prefill_workspace_bytes", "q35_gated_attn_prefill",
+    "q35_gated_attn_prefill_cached_workspace_bytes", "q35_gated_attn_prefill_cached", "q35_gated_attn_decode_workspace_bytes",
     "q35_gated_attn_decode", "q35_gated_attn_decode_noalloc_max_bytes", "q35_gated_attn_decode_noalloc",
     "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
     "q35_swiglu_push",
@@ -42,6 +43,9 @@ _SIGS = {
                               I32),
     "q35_gated_attn_prefill_workspace_bytes": ([I64, I64, I64, I64, I64], SZ),
     "q35_gated_attn_prefill": ([P, P, P, P, P, P, I64, P, I64, I64, I64, I64, I64, I64, F32, P, SZ, P], I32),
+    "q35_gated_attn_prefill_cached_workspace_bytes": ([I64, I64, I64, I64], SZ),
+    "q35_gated_attn_prefill_cached": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, F32, P, SZ, P],
+                                      I32),
     "q35_gated_attn_decode_workspace_bytes": ([I64, I64, I64, I64, I64, I64], SZ),
     "q35_gated_attn_decode": ([P, P, P, P, P, P, P, P, I32, I64, I64, I64, I64, I64, I64, F32, I64, P, SZ, P], I32),
     "q35_gated_attn_decode_noalloc_max_bytes": ([], SZ),

@@ -156,10 +156,11 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     """Gated softmax attention mixer of one decoder layer (Qwen3_5Attention.forward, HF:656-701; WGSL attnPrep +
     attention, engine/kernels_qwen35.js:18-123). x: [B, T, H] fp32; the T tokens sit at positions pos..pos+T-1,
     pos a Python int or a [B] int32 device tensor (per row; a device tensor keeps the call capturable in a HIP
-    graph). Their rotated keys and values are written into the caches at those positions. T > 1 requires pos == 0
-    and runs the causal flash prefill over the call's own tokens; T == 1 runs the split-K decode over cache positions
-    0..pos (cache_len: optional [B] int32 per-row lengths, default pos + 1). prenorm: see linear(). Returns
-    y [B, T, H]."""
+    graph). Their rotated keys and values are written into the caches at those positions, and token t attends to
+    cache positions 0..pos+t (engine/kernels_qwen35.js:90). T > 1 at the int position 0 runs the flash prefill over
+    the call's own tokens; T > 1 at any other position (or a device pos) the same kernel over the cache (the caches'
+    max_len must then be a multiple of 64); T == 1 the split-K decode over cache positions 0..pos (cache_len:
+    optional [B] int32 per-row lengths, default pos + 1). prenorm: see linear(). Returns y [B, T, H]."""
     B, T, _ = x.shape
     D = p["q_norm"].numel()
     Hq = p["q_proj"].shape[0] // (2 * D)
@@ -168,18 +169,20 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     max_len = k_cache.shape[2]
     if torch.is_tensor(pos):
         pos_t = pos
+        own_keys = False
     else:
-        if pos + T > max_len:
+        if pos < 0 or pos + T > max_len:
             raise ValueError(f"gated_attention_layer: positions {pos}..{pos + T - 1} exceed the cache ({max_len})")
-        if T > 1 and pos != 0:
-            raise ValueError("gated_attention_layer: a multi-token call must start at position 0")
         pos_t = torch.full((B,), int(pos), dtype=torch.int32, device=x.device)
+        own_keys = pos == 0
     cos, sin = rope_tables(max_len, rot, rope_theta, x.device)
     y = linear(x, attn_in_weight(p), *_q8(p, "_in_fused"), prenorm=prenorm)
     q, gate, k, v = ops.attn_prep(y, p["q_norm"], p["k_norm"], cos, sin, pos_t, k_cache, v_cache, num_heads=Hq,
-                                  num_kv_heads=Hkv, eps=eps, want_kv=T > 1)
-    if T > 1:
+                                  num_kv_heads=Hkv, eps=eps, want_kv=T > 1 and own_keys)
+    if T > 1 and own_keys:
         o = ops.gated_attention_prefill(q, k, v, gate, cos, sin, pos0=0, scale=1.0 / math.sqrt(D))
+    elif T > 1:
+        o = ops.gated_attention_prefill_cached(q, k_cache, v_cache, gate, pos_t, cos, sin, scale=1.0 / math.sqrt(D))
     else:
         cl = pos_t + 1 if cache_len is None else cache_len
         # fp32 straight from the merge kernel: the o_proj GEMV reads fp32 (no conversion kernel in the step)

@@ -84,9 +84,12 @@ class HybridModel:
     so greedy tokens follow the fp32 reference through near ties of a few 1e-3 in the logits); "recurrent" runs the
     token-serial fp32 kernel (the WGSL engine's order, token by token; slower).
 
-    Positions live on the device (pos_dev, [rows] int32) and the steering vectors in fixed buffers, so a decode step
-    has no host-dependent arguments: enable_decode_graph() captures one step in a HIP graph that decode_step()
-    replays."""
+    Each row has its own position (rows may hold prompts of different lengths, prefilled one row at a time as the
+    reference's steer loop does: reset(r); forward(ids_r, row=r), engine/analysis.js:125), and a prompt may be
+    prefilled in several calls (engine/model.js:486-491): a multi-token call past position 0 attends over the KV
+    cache. Positions live on the device (pos_dev, [rows] int32) and the steering vectors in fixed buffers, so a
+    decode step has no host-dependent arguments: enable_decode_graph() captures one step in a HIP graph that
+    decode_step() replays."""
 
     MAX_VECS = 4  # vector rows of the steering buffer (the WGSL resAdd clamps its row index to 3, engine/kernels.js:201)
 
@@ -96,7 +99,8 @@ class HybridModel:
         self.cfg, self.device, self.steer_layer = cfg, device, steer_layer
         self.gdn_prefill = gdn_prefill
         self.W = W if isinstance(W, Q35Weights) else Q35Weights(W, device)
-        self.max_len, self.rows = max_len, rows
+        # the KV caches hold a multiple of 64 positions (the multi-token attention over the cache reads 64-key tiles)
+        self.max_len, self.rows = (max_len + 63) // 64 * 64, rows
         self.vec_buf = torch.zeros(self.MAX_VECS, cfg.hidden, device=device)
         self.vec_rows = torch.full((rows,), -1, dtype=torch.int32, device=device)
         self.steering = False
@@ -111,7 +115,7 @@ class HybridModel:
         self.states = []
         for l in range(cfg.layers):
             if cfg.is_attention(l):
-                shape = (rows, cfg.n_kv, max_len, cfg.head_dim)
+                shape = (rows, cfg.n_kv, self.max_len, cfg.head_dim)
                 self.states.append({"k": torch.zeros(shape, dtype=torch.bfloat16, device=device),
                                     "v": torch.zeros(shape, dtype=torch.bfloat16, device=device)})
             else:
@@ -123,18 +127,26 @@ class HybridModel:
         self._pos_len = torch.zeros(2, rows, dtype=torch.int32, device=device)
         self.pos_dev, self.len_dev = self._pos_len[0], self._pos_len[1]
         self.graph = None
+        self.row_pos = [0] * rows  # host mirror of pos_dev
         self.reset()
 
-    def reset(self):
-        """Start a new sequence: zero the recurrent and conv states and the positions (KV caches are overwritten by
-        position)."""
+    def reset(self, row=None):
+        """Start a new sequence on every row, or on row `row` only: zero its recurrent and conv states and its
+        position (KV caches are overwritten by position)."""
+        rs = slice(None) if row is None else slice(row, row + 1)
         for st in self.states:
             if "rec" in st:
-                st["rec"].zero_()
-                st["conv"].zero_()
-        self.pos_dev.zero_()
-        self.len_dev.fill_(1)
-        self.pos = 0
+                st["rec"][rs].zero_()
+                st["conv"][rs].zero_()
+        self.pos_dev[rs].zero_()
+        self.len_dev[rs].fill_(1)
+        for r in range(self.rows)[rs]:
+            self.row_pos[r] = 0
+
+    @property
+    def pos(self):
+        """The furthest row's next position (all rows share it unless rows were prefilled separately)."""
+        return max(self.row_pos)
 
     def set_vectors(self, vecs, vec_of_row):
         """vecs: [n, H] fp32 (n <= MAX_VECS), copied into the model's buffer; vec_of_row: [rows] int (-1 = no vector).
@@ -163,9 +175,11 @@ class HybridModel:
                 buf[:len(recs)] = ops.pack_pushes(recs, "cpu")
             p["_pushes"].copy_(buf)
 
-    def _layers(self, x, T, last, collect_layer, steer):
-        """The decoder layers 0..last over the residual stream x [rows, T, H] (dense fp32); returns (the residual
-        after layer `last`, the residual after collect_layer or None) (HF:753-793; engine/model.js:436-462).
+    def _layers(self, x, T, last, collect_layer, steer, rs=slice(None), attn_pos=None):
+        """The decoder layers 0..last over the residual stream x [n, T, H] (dense fp32) of the rows rs; returns (the
+        residual after layer `last`, the residual after collect_layer or None) (HF:753-793; engine/model.js:436-462).
+        attn_pos: the attention layers' position argument for T > 1 (0 when every row starts its sequence: the
+        prefill over the call's own keys; else the rows' device positions: the prefill over the KV cache).
 
         Prefill (T > 1): x is updated in place; each layer adds its mixer output in the fused residual-add + RMSNorm
         kernel and its MLP output in the MLP's last product. Decode (T == 1): the adds and norms run inside the
@@ -174,14 +188,16 @@ class HybridModel:
         the two buffers alternate by layer."""
         cfg = self.cfg
         collected = None
+        pos_dev, vec_rows = self.pos_dev[rs], self.vec_rows[rs]
         if T == 1:
-            cache_len = self.len_dev  # shared by the attention layers
+            cache_len = self.len_dev[rs]  # shared by the attention layers
             cur, alt = x, torch.empty_like(x)
             for l in range(last + 1):
-                p, st = self.params[l], self.states[l]
+                p = self.params[l]
+                st = {n: t[rs] for n, t in self.states[l].items()}
                 pre = (None, p["input_layernorm"], cfg.eps, None)
                 if cfg.is_attention(l):
-                    y = layers.gated_attention_layer(cur, p, st["k"], st["v"], self.pos_dev,
+                    y = layers.gated_attention_layer(cur, p, st["k"], st["v"], pos_dev,
                                                      rope_theta=cfg.rope_theta,
                                                      partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps,
                                                      cache_len=cache_len, prenorm=pre)
@@ -192,16 +208,17 @@ class HybridModel:
                 mlp(p, cur, alt, prenorm=(y, p["post_attention_layernorm"], cfg.eps))
                 cur, alt = alt, cur
                 if l == self.steer_layer and steer:
-                    layers.residual_steer_add(cur, self.vec_buf, self.vec_rows)
+                    layers.residual_steer_add(cur, self.vec_buf, vec_rows)
                 if l == collect_layer:
                     collected = cur.clone()
             return cur, collected
         y = None  # the previous mixer's output, added to x by the next norm
         for l in range(last + 1):
-            p, st = self.params[l], self.states[l]
+            p = self.params[l]
+            st = {n: t[rs] for n, t in self.states[l].items()}
             h = ops.add_rmsnorm_(x, y, p["input_layernorm"], cfg.eps)
             if cfg.is_attention(l):
-                y = layers.gated_attention_layer(h, p, st["k"], st["v"], self.pos_dev, rope_theta=cfg.rope_theta,
+                y = layers.gated_attention_layer(h, p, st["k"], st["v"], attn_pos, rope_theta=cfg.rope_theta,
                                                  partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps)
             else:
                 y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
@@ -210,26 +227,35 @@ class HybridModel:
             y = None
             mlp(p, h, x)
             if l == self.steer_layer and steer:
-                layers.residual_steer_add(x, self.vec_buf, self.vec_rows)
+                layers.residual_steer_add(x, self.vec_buf, vec_rows)
             if l == collect_layer:
                 collected = x.clone()
         return x, collected
 
     @torch.no_grad()
-    def forward(self, ids, stop_after=None, collect_layer=None):
-        """ids: [rows, T] token ids continuing the sequence (a multi-token call must start it). Returns
-        (last-position logits [rows, V] or None with stop_after, residual after collect_layer or None)."""
+    def forward(self, ids, stop_after=None, collect_layer=None, row=None):
+        """ids: [rows, T] token ids continuing every row's sequence, or with row=r [1, T] (or [T]) continuing row r
+        only (its states and position; the other rows are untouched). A multi-token call may start anywhere: past
+        position 0 its attention runs over the KV cache. Returns (last-position logits [n, V] or None with
+        stop_after, residual after collect_layer or None) for the rows called."""
         cfg, W = self.cfg, self.W
+        if row is None:
+            rs, rows = slice(None), list(range(self.rows))
+        else:
+            if not 0 <= row < self.rows:
+                raise ValueError(f"HybridModel: row {row} out of range ({self.rows} rows)")
+            rs, rows = slice(row, row + 1), [row]
+            ids = ids.reshape(1, -1)
         T = ids.shape[1]
-        if self.pos + T > self.max_len:
+        if max(self.row_pos[r] for r in rows) + T > self.max_len:
             raise ValueError("context exceeds the KV cache")
-        if T > 1 and self.pos != 0:
-            raise ValueError("HybridModel: a multi-token call must start the sequence (positions 0..T-1)")
+        attn_pos = 0 if all(self.row_pos[r] == 0 for r in rows) else self.pos_dev[rs]
         x = W["embed"][ids.to(self.device).long()].contiguous()
         last = cfg.layers - 1 if stop_after is None else stop_after
-        x, collected = self._layers(x, T, last, collect_layer, self.steering)
-        self._pos_len.add_(T)
-        self.pos += T
+        x, collected = self._layers(x, T, last, collect_layer, self.steering, rs, attn_pos)
+        self._pos_len[:, rs].add_(T)
+        for r in rows:
+            self.row_pos[r] += T
         if stop_after is not None:
             return None, collected
         return self._lm_head(x[:, -1]), collected
@@ -285,7 +311,7 @@ class HybridModel:
             raise ValueError("context exceeds the KV cache")
         self._g_ids.copy_(ids)
         self.graph.replay()
-        self.pos += 1
+        self.row_pos = [p + 1 for p in self.row_pos]
         return self._g_logits
 
     @torch.no_grad()
@@ -297,7 +323,7 @@ class HybridModel:
         if self.pos + 1 > self.max_len:
             raise ValueError("context exceeds the KV cache")
         self.graph.replay()
-        self.pos += 1
+        self.row_pos = [p + 1 for p in self.row_pos]
         return self._g_logits, self._g_ids
 
 

@@ -60,6 +60,8 @@ _LIB.define("gdn_chunk_prefill(Tensor q, Tensor k, Tensor v, Tensor g, Tensor be
             "int chunk_size, float scale, bool use_qk_l2norm) -> (Tensor, Tensor)")
 _LIB.define("gated_attn_prefill(Tensor q, Tensor k, Tensor v, Tensor gate, Tensor cos, Tensor sin, int pos0, "
             "float scale) -> Tensor")
+_LIB.define("gated_attn_prefill_cached(Tensor q, Tensor k_cache, Tensor v_cache, Tensor gate, Tensor pos, "
+            "Tensor cos, Tensor sin, float scale) -> Tensor")
 _LIB.define("gated_attn_decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor gate, Tensor cache_len, "
             "Tensor cos, Tensor sin, float scale, int splits, bool f32_out=False) -> Tensor")
 _LIB.define("resid_add_rows_(Tensor(a!) x, Tensor vecs, Tensor? vec_of_row) -> ()")
@@ -159,6 +161,32 @@ def _attn_prefill_impl(q, k, v, gate, cos, sin, pos0, scale):
     st = L.q35_gated_attn_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(cos), _ptr(sin), int(pos0),
                                   _ptr(out), B, T, Hq, Hkv, D, rot, float(scale), _ptr(ws), ws.numel(), _stream(q))
     check(st, "q35_gated_attn_prefill")
+    return out
+
+
+def _attn_prefill_cached_impl(q, k_cache, v_cache, gate, pos, cos, sin, scale):
+    _on_gpu(q, k_cache, v_cache, gate, pos, cos, sin)
+    _require(q.dtype == torch.bfloat16 and k_cache.dtype == q.dtype and v_cache.dtype == q.dtype
+             and gate.dtype == q.dtype, "q, caches, gate must be bf16")
+    _require(q.dim() == 4 and k_cache.dim() == 4 and v_cache.shape == k_cache.shape,
+             "q: [B, T, Hq, D]; caches: [B, Hkv, max_len, D]")
+    B, T, Hq, D = q.shape
+    Hkv, max_len = k_cache.shape[1], k_cache.shape[2]
+    _require(k_cache.shape[0] == B and k_cache.shape[3] == D, "caches must match q in batch and head dim")
+    _require(tuple(gate.shape) == (B, T, Hq * D), "gate: [B, T, Hq * D]")
+    _require(pos.dtype == torch.int32 and tuple(pos.shape) == (B,), "pos: [B] int32")
+    _require(max_len % 64 == 0, "the cache length must be a multiple of 64 for a multi-token call over the cache")
+    _require(T <= max_len, "more tokens than the cache holds")
+    rot = _tables_check(cos, sin, max_len)
+    L = _lib.lib()
+    nbytes = L.q35_gated_attn_prefill_cached_workspace_bytes(B, Hkv, D, max_len)
+    _require(nbytes > 0, "unsupported attention shape")
+    ws = _workspace(nbytes, q.device)
+    out = torch.empty(B, T, Hq * D, dtype=q.dtype, device=q.device)
+    st = L.q35_gated_attn_prefill_cached(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(gate), _ptr(pos), _ptr(cos),
+                                         _ptr(sin), _ptr(out), B, T, Hq, Hkv, D, max_len, rot, float(scale),
+                                         _ptr(ws), ws.numel(), _stream(q))
+    check(st, "q35_gated_attn_prefill_cached")
     return out
 
 
@@ -401,6 +429,7 @@ def _no_cpu(name):
 
 for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_", _gdn_decode_step_impl),
                      ("gdn_chunk_prefill", _gdn_chunk_impl), ("gated_attn_prefill", _attn_prefill_impl),
+                     ("gated_attn_prefill_cached", _attn_prefill_cached_impl),
                      ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
                      ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl),
                      ("gdn_decode_fused_", _gdn_decode_fused_impl),
@@ -431,8 +460,36 @@ _LIB.impl("gated_attn_decode",
 _LIB.impl("resid_add_rows_", lambda x, vecs, vor: None, "Meta")
 _LIB.impl("gdn_decode_fused_", lambda y, cw, cb, cs, Al, dt, bo, ao, zo, st, nw, hs, eps, sc:
           y.new_empty(y.shape[0], st.shape[1] * st.shape[2]), "Meta")
+_LIB.impl("gated_attn_prefill_cached",
+          lambda q, kc, vc, gate, pos, cos, sin, scale: q.new_empty(q.shape[0], q.shape[1], q.shape[2] * q.shape[3]),
+          "Meta")
 _LIB.impl("argmax_rows_", lambda x, idx: None, "Meta")
 _LIB.impl("gemv_norm_", lambda x, xa, xo, nw, eps, W, ws, y, e, pushes, T: None, "Meta")
+_LIB.impl("gemv_", lambda x, W, ws, y, e, pushes, T: None, "Meta")
+_LIB.impl("swiglu_push", lambda gu, pushes, T: gu.new_empty(*gu.shape[:-1], gu.shape[-1] // 2), "Meta")
+_LIB.impl("add_rmsnorm_", lambda x, y, w, eps: torch.empty_like(x), "Meta")
+_LIB.impl("gated_rmsnorm", lambda o, z, w, hs, eps: o.new_empty(*o.shape[:-2], o.shape[-2] * o.shape[-1]), "Meta")
+
+
+def _meta_gdn_conv(y, conv_w, conv_bias, conv_state, A_log, dt_bias, b_off, a_off, Hk, dk, Hv, dv, bf16_out):
+    B, T = y.shape[0], y.shape[1]
+    dt = torch.bfloat16 if bf16_out else torch.float32
+    q = y.new_empty(B, T, Hk, dk, dtype=dt)
+    g = y.new_empty(B, T, Hv, dtype=torch.float32)
+    return q, torch.empty_like(q), y.new_empty(B, T, Hv, dv, dtype=dt), g, torch.empty_like(g)
+
+
+def _meta_attn_prep(y, q_norm_w, k_norm_w, eps, cos, sin, pos, k_cache, v_cache, Hq, Hkv, want_kv):
+    B, T = y.shape[0], y.shape[1]
+    D = k_cache.shape[3]
+    q = y.new_empty(B, T, Hq, D, dtype=torch.bfloat16)
+    gate = y.new_empty(B, T, Hq * D, dtype=torch.bfloat16)
+    k = y.new_empty(B, T, Hkv, D, dtype=torch.bfloat16) if want_kv else y.new_empty(0, dtype=torch.bfloat16)
+    return q, gate, k, torch.empty_like(k)
+
+
+_LIB.impl("gdn_conv", _meta_gdn_conv, "Meta")
+_LIB.impl("attn_prep", _meta_attn_prep, "Meta")
 
 
 # ---------------------------------------------------------------- Python entry points (reference signatures)
@@ -480,6 +537,16 @@ def gated_attention_prefill(q, k, v, gate, cos, sin, pos0=0, scale=None):
     cos/sin: [P, rot/2] fp32 by position). Returns [B, T, Hq*D] bf16."""
     scale = q.shape[-1] ** -0.5 if scale is None else scale
     return torch.ops.q35.gated_attn_prefill(q, k, v, gate, cos, sin, int(pos0), float(scale))
+
+
+def gated_attention_prefill_cached(q, k_cache, v_cache, gate, pos, cos, sin, scale=None):
+    """Causal gated GQA attention of T new tokens per row over a bf16 KV cache that already holds them (the
+    reference's multi-token attention, engine/kernels_qwen35.js:90: token t of row b sits at position pos[b] + t and
+    attends to cache keys 0 .. pos[b] + t). q: [B, T, Hq, D] bf16, not rotated (rotated here at its position);
+    caches [B, Hkv, max_len, D] with rotated keys, max_len a multiple of 64; pos: [B] int32 on the device (clamped to
+    0 .. max_len - T); gate [B, T, Hq * D]. Returns [B, T, Hq * D] bf16."""
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    return torch.ops.q35.gated_attn_prefill_cached(q, k_cache, v_cache, gate, pos, cos, sin, float(scale))
 
 
 def gated_attention_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, scale=None, splits=0,

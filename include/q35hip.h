@@ -13,6 +13,8 @@
  *   q35_gdn_chunk_prefill    HF:249-327 torch_chunk_gated_delta_rule (chunk_size 64)
  *   q35_gated_attn_prefill   HF:554-589 apply_rotary_pos_emb (partial) + HF:604-626 eager_attention_forward (causal)
  *                            + HF:698 sigmoid gate; engine/kernels_qwen35.js:73-123 `attention`
+ *   q35_gated_attn_prefill_cached  the same for T new tokens per row over a KV cache at per-row positions
+ *                            (engine/kernels_qwen35.js:90; engine/model.js:486-491 chunked prefill)
  *   q35_gated_attn_decode    same as above for one new token per row over a KV cache (engine/kernels_qwen35.js:73-123
  *                            with T = 1; HF decode through DynamicCache)
  *   q35_resid_add_rows       tests/engine_ref.py:49-53 residual vector hook; engine/kernels.js:190-203 `resAdd`
@@ -124,6 +126,24 @@ int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const vo
                            const float* cos, const float* sin, int64_t pos0, void* out,
                            int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t rot,
                            float scale, void* workspace, size_t workspace_bytes, q35_stream_t stream);
+
+/*
+ * Gated causal GQA attention of T new tokens per row over a bf16 KV cache that already holds their keys and values
+ * (written by q35_attn_prep): the reference's multi-token attention, where token t of a call at position pos[r]
+ * attends to cache keys 0 .. pos[r] + t (engine/kernels_qwen35.js:90, n = pos + t + 1; prefill in chunks,
+ * engine/model.js:486-491), and HF:656-698 over a DynamicCache. Rows may sit at different positions.
+ *   q: [B, T, Hq, D] bf16, not rotated (rotated here at position pos[b] + t)   gate: [B, T, Hq * D] bf16
+ *   k_cache, v_cache: [B, Hkv, max_len, D] bf16, keys rotated; max_len a multiple of 64 (Q35_EUNSUPPORTED otherwise)
+ *   pos: [B] int32 on the device, clamped to 0 .. max_len - T; cos, sin: [P, rot / 2] fp32, P >= max_len
+ *   out: [B, T, Hq * D] bf16. D = 256, Hq / Hkv in {1, 2, 4, 8}, rot a multiple of 16 (at most 64).
+ *   Needs q35_gated_attn_prefill_cached_workspace_bytes(B, Hkv, D, max_len) bytes of workspace (256-byte aligned:
+ *   the values of the rows' key ranges, transposed). Calls that share one workspace must not overlap.
+ */
+size_t q35_gated_attn_prefill_cached_workspace_bytes(int64_t B, int64_t Hkv, int64_t D, int64_t max_len);
+int q35_gated_attn_prefill_cached(const void* q, const void* k_cache, const void* v_cache, const void* gate,
+                                  const int32_t* pos, const float* cos, const float* sin, void* out, int64_t B,
+                                  int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
+                                  float scale, void* workspace, size_t workspace_bytes, q35_stream_t stream);
 
 /*
  * Gated GQA attention for one new token per row over a bf16 KV cache (split-K over the context, then a merge).

@@ -10,6 +10,6 @@ Pinning status of every function is recorded in its module docstring; the checks
 """
 from .gdn import l2norm, recurrent_gated_delta_rule, chunk_gated_delta_rule  # noqa: F401
 from .attention import (rope_inv_freq, rope_tables, apply_partial_rope, gated_attention,  # noqa: F401
-                        gated_attention_decode)
+                        gated_attention_decode, gated_attention_cached)
 from .steer import residual_steer_add  # noqa: F401
 from .metrics import rel_err  # noqa: F401

@@ -7,12 +7,15 @@ Restates, from transformers 5.15.0 models/qwen3_5/modeling_qwen3_5.py:
   apply_partial_rope HF:546-589 rotate_half + apply_rotary_pos_emb on the first rot dims
   gated_attention    HF:656-698 (q/gate split left to the caller), eager_attention_forward HF:604-626 with the causal
                      mask, softmax in fp32, then * sigmoid(gate) (HF:698)
+  gated_attention_cached  the same for T new tokens per row over a KV cache at per-row positions (HF:656-698 through
+                     DynamicCache.update; the WGSL attention's key count n = pos + t + 1, engine/kernels_qwen35.js:90)
 and the WGSL equivalents engine/kernels_qwen35.js:50-59 (rotation) and :73-123 (attention, gate).
 
 Pinned (tests/test_oracle_attention.py): against torch.nn.functional.scaled_dot_product_attention (a library
 routine) in fp64, against a brute-force per-query loop, RoPE closed forms (position 0 is the identity, each pair keeps
 its norm, q.k after rotation depends only on the position difference, hand-computed pair rotation), decode equal to
-the last prefill row, invariance of decode to how the context is split.
+the last prefill row, invariance of decode to how the context is split; the cached form against the self form
+(position 0, cache = the call's rotated keys), against decode (T = 1), and a prompt split into two calls against one.
 """
 import math
 
@@ -93,4 +96,32 @@ def gated_attention_decode(q, k_cache, v_cache, gate, cache_len, cos_tab, sin_ta
         w = torch.einsum("hd,hnd->hn", qb[0], kb) * scale
         w = torch.softmax(w, dim=-1, dtype=dtype)
         out[b] = torch.einsum("hn,hnd->hd", w, vb).reshape(-1)
+    return out * torch.sigmoid(gate)
+
+
+def gated_attention_cached(q, k_cache, v_cache, gate, pos, cos_tab, sin_tab, scale=None, dtype=torch.float32):
+    """T new query tokens per row over a KV cache of already-rotated keys that holds them: token t of row b sits at
+    position pos[b] + t (rotated there) and attends to cache keys 0 .. pos[b] + t.
+
+    q: [B, T, Hq, D]; k_cache, v_cache: [B, Hkv, max_len, D]; gate: [B, T, Hq * D]; pos: [B] ints.
+    Returns [B, T, Hq * D] in `dtype`.
+    """
+    q, k_cache, v_cache, gate = [x.to(dtype) for x in (q, k_cache, v_cache, gate)]
+    B, T, Hq, D = q.shape
+    Hkv = k_cache.shape[1]
+    scale = D ** -0.5 if scale is None else scale
+    out = torch.empty(B, T, Hq * D, dtype=dtype)
+    for b in range(B):
+        P = int(pos[b])
+        qb = q[b:b + 1]
+        if cos_tab is not None and cos_tab.shape[-1] > 0:
+            qb = apply_partial_rope(qb, cos_tab[P:P + T].to(dtype), sin_tab[P:P + T].to(dtype))
+        n = P + T
+        kb = k_cache[b, :, :n].repeat_interleave(Hq // Hkv, dim=0)  # [Hq, n, D]
+        vb = v_cache[b, :, :n].repeat_interleave(Hq // Hkv, dim=0)
+        w = torch.matmul(qb[0].transpose(0, 1), kb.transpose(1, 2)) * scale  # [Hq, T, n]
+        qpos = torch.arange(P, P + T)[:, None]
+        w = w.masked_fill(torch.arange(n)[None, :] > qpos, float("-inf"))
+        w = torch.softmax(w, dim=-1, dtype=dtype)
+        out[b] = torch.matmul(w, vb).transpose(0, 1).reshape(T, Hq * D)
     return out * torch.sigmoid(gate)

@@ -121,3 +121,45 @@ def test_decode_fp32_output_is_the_unrounded_bf16_output():
     assert o32.dtype == torch.float32 and o16.dtype == torch.bfloat16
     assert torch.equal(o32.to(torch.bfloat16).cpu(), o16.cpu())
     assert oracle.rel_err(o32.cpu(), ref) <= TOL
+
+
+# Multi-token calls over a KV cache at per-row positions: token t of row b attends to cache keys 0 .. pos[b] + t.
+# Cases: rows at different positions, one token, a query length past 256 with the keys filling the cache exactly,
+# GQA 8 with a row at position 0, two head groups per kv head.
+@pytest.mark.parametrize("B,T,Hq,Hkv,max_len,pos", [(3, 100, 8, 2, 448, [0, 37, 300]), (2, 1, 8, 2, 256, [5, 200]),
+                                                     (1, 257, 4, 4, 640, [383]), (2, 64, 8, 1, 192, [128, 0]),
+                                                     (1, 130, 16, 2, 320, [64])])
+def test_prefill_over_cache(B, T, Hq, Hkv, max_len, pos):
+    dev = device()
+    inp = workloads.attn_prefill_inputs(B=B, T=T, Hq=Hq, Hkv=Hkv, seed=T + max_len)
+    g = torch.Generator().manual_seed(max_len)
+    kc = torch.randn(B, Hkv, max_len, 256, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, Hkv, max_len, 256, generator=g).to(torch.bfloat16)
+    cos, sin = _tables(max_len)
+    pos_t = torch.tensor(pos, dtype=torch.int32)
+    ref = oracle.gated_attention_cached(inp["q"], kc, vc, inp["gate"], pos_t, cos, sin)
+    announce(f"attn prefill over cache B{B} T{T} Hq{Hq} Hkv{Hkv} max_len {max_len} pos {pos}")
+    out = q35hip.ops.gated_attention_prefill_cached(inp["q"].to(dev), kc.to(dev), vc.to(dev), inp["gate"].to(dev),
+                                                    pos_t.to(dev), cos.to(dev), sin.to(dev))
+    e = oracle.rel_err(out.float().cpu(), ref)
+    print(f"cached prefill rel err {e:.3e}")
+    assert e <= TOL
+
+
+def test_prefill_over_cache_equals_own_keys_at_position_zero():
+    """At position 0 with the cache holding the call's rotated keys, the cached path gives the own-keys path's
+    result (same tiles and arithmetic: bitwise)."""
+    dev = device()
+    B, T, max_len = 2, 200, 256
+    inp = workloads.to_device(workloads.attn_prefill_inputs(B=B, T=T, seed=9), dev)
+    cos, sin = [t.to(dev) for t in _tables(max_len)]
+    kr = oracle.apply_partial_rope(inp["k"].float().cpu(), cos[:T].cpu(), sin[:T].cpu()).to(torch.bfloat16)
+    kc = torch.zeros(B, 2, max_len, 256, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    kc[:, :, :T] = kr.transpose(1, 2).to(dev)
+    vc[:, :, :T] = inp["v"].transpose(1, 2)
+    announce("attn prefill over cache at position 0 vs own keys")
+    own = q35hip.gated_attention_prefill(inp["q"], inp["k"], inp["v"], inp["gate"], cos, sin)
+    cached = q35hip.ops.gated_attention_prefill_cached(inp["q"], kc, vc, inp["gate"],
+                                                       torch.zeros(B, dtype=torch.int32, device=dev), cos, sin)
+    assert oracle.rel_err(cached.float().cpu(), own.float().cpu()) <= 1e-2

@@ -6,6 +6,7 @@ import pytest
 import torch
 
 import oracle
+import q35hip
 from oracle import model as om
 from q35hip import model as gm
 from q35hip import workloads
@@ -37,6 +38,42 @@ def test_tiny_stack_prefill_decode_and_steering(gdn_prefill):
         lr, _ = ref.forward(nxt)
         lg, _ = g.forward(nxt.to(dev))
         assert oracle.rel_err(lg.cpu(), lr) <= 2e-2
+
+
+def test_tiny_stack_rows_of_different_lengths_and_chunked_prefill():
+    """The reference's steer loop prefills each row from its own prompt (reset(r); prefill(r, ...),
+    engine/analysis.js:125) in chunks (engine/model.js:486-491), then decodes all rows together: rows of 37, 70 and 13
+    tokens, row 1's prompt in chunks of 16, 32 and 22 tokens (multi-token calls over the KV cache), then 6 decode
+    steps of all rows, each against its own single-row oracle."""
+    dev = device()
+    cfg = tiny_config()
+    W = tiny_weights(cfg)
+    ids, vec = tiny_inputs(cfg)
+    prompts = [ids[0, :37], ids[1, :70], ids[0, 40:53]]
+    announce("model tiny: rows of different lengths, chunked prefill")
+    g = gm.HybridModel(cfg, W, dev, max_len=130, rows=3, steer_layer=STEER_LAYER)
+    assert g.max_len % 64 == 0
+    g.set_vectors(torch.stack([vec, -vec]), [0, -1, 1])
+    refs, lr = [], []
+    for r, pr in enumerate(prompts):
+        ref = om.OracleModel(cfg, W, steer_layer=STEER_LAYER)
+        ref.set_vectors([vec[None], None, -vec[None]][r] if r != 1 else torch.zeros(1, cfg.hidden))
+        lr.append(ref.forward(pr[None])[0])
+        refs.append(ref)
+        g.reset(r)
+        if r == 1:
+            for a, b in ((0, 16), (16, 48), (48, 70)):
+                lg, _ = g.forward(pr[a:b], row=r)
+        else:
+            lg, _ = g.forward(pr, row=r)
+        assert oracle.rel_err(lg.cpu(), lr[r]) <= 2e-2, f"row {r} prefill"
+    assert g.row_pos == [37, 70, 13]
+    for step in range(6):
+        nxt = torch.stack([l.argmax(-1) for l in lr])  # [3, 1]
+        lg = g.decode_step(nxt.to(dev).reshape(3))
+        lr = [refs[r].forward(nxt[r:r + 1])[0] for r in range(3)]
+        for r in range(3):
+            assert oracle.rel_err(lg[r:r + 1].cpu(), lr[r]) <= 2e-2, f"row {r} decode step {step}"
 
 
 def test_tiny_stack_decode_graph_replays_match_eager():
@@ -78,8 +115,16 @@ def _full_stack_reference(cfg, W, prompt, steps):
         v_ref = v_ref / v_ref.norm() * (0.8 * med)
         ref.reset()
         ref.set_vectors(torch.stack([v_ref, torch.zeros_like(v_ref), -v_ref]))
-        toks_r, marg_r = om.greedy(ref, prompt, steps)
-        _FULL_REF.update(toks=toks_r, margins=marg_r, v=v_ref)
+        logits0, _ = ref.forward(prompt)
+        toks, margins = [], []
+        logits = logits0
+        for _ in range(steps):
+            top2 = logits.topk(2, dim=-1)
+            nxt = logits.argmax(dim=-1)
+            toks.append(nxt)
+            margins.append(top2.values[:, 0] - top2.values[:, 1])
+            logits, _ = ref.forward(nxt[:, None])
+        _FULL_REF.update(toks=torch.stack(toks, 1), margins=torch.stack(margins, 1), v=v_ref, prefill=logits0)
     return _FULL_REF["toks"], _FULL_REF["margins"], _FULL_REF["v"]
 
 
@@ -108,6 +153,38 @@ def test_full_stack_steered_greedy_64_steps(gdn_prefill):
     same = (toks_g == toks_r)
     first_diff = [int((~same[r]).nonzero()[0]) if not bool(same[r].all()) else -1 for r in range(3)]
     print(f"min top-2 margin (CPU) {float(marg_r.min()):.4g}; first differing step per row {first_diff}")
+    assert bool(same.all()), f"greedy tokens differ; first differing step per row {first_diff}"
+
+
+@pytest.mark.timeout(1800)
+def test_full_stack_prompt_prefilled_in_128_token_chunks():
+    """The config-5 workload with the 2048-token prompt prefilled in 16 calls of 128 tokens (the engine's chunked
+    prefill, engine/model.js:486-491: every call after the first attends over the KV cache): prefill logits within
+    the bf16 tolerance of the fp32 CPU path and the 64 greedy tokens of all three rows identical to it."""
+    dev = device()
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    cfg = workloads.Q35Config()
+    W = workloads.init_weights(cfg, seed=0)
+    prompt = torch.randint(0, cfg.vocab, (1, 2048), generator=torch.Generator().manual_seed(0)).repeat(3, 1)
+    steps = 64
+    toks_r, marg_r, v_ref = _full_stack_reference(cfg, W, prompt, steps)
+    announce("model full stack: prompt in 128-token chunks")
+    g = gm.HybridModel(cfg, W, dev, max_len=2048 + steps + 8, rows=3)
+    g.enable_decode_graph()
+    g.set_vectors(torch.stack([v_ref, -v_ref]), [0, -1, 1])
+    for c in range(0, 2048, 128):
+        logits, _ = g.forward(prompt[:, c:c + 128])
+    e = oracle.rel_err(logits.cpu(), _FULL_REF["prefill"])
+    toks = []
+    for _ in range(steps):
+        nxt = q35hip.ops.argmax_rows(logits)
+        toks.append(nxt.long().cpu())
+        logits = g.decode_step(nxt)
+    toks_g = torch.stack(toks, 1)
+    same = toks_g == toks_r
+    first_diff = [int((~same[r]).nonzero()[0]) if not bool(same[r].all()) else -1 for r in range(3)]
+    print(f"chunked prefill logits rel err {e:.3e}; first differing step per row {first_diff}")
+    assert e <= 2e-2
     assert bool(same.all()), f"greedy tokens differ; first differing step per row {first_diff}"
 
 

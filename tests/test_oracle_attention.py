@@ -75,3 +75,54 @@ def test_decode_equals_last_prefill_row():
     dec = oracle.gated_attention_decode(inp["q"][:, T - 1], k_rot.transpose(1, 2), inp["v"].transpose(1, 2),
                                         inp["gate"][:, T - 1], [T], cos, sin, dtype=torch.float64)
     assert oracle.rel_err(dec, full[:, T - 1]) < 1e-6
+
+
+def _rotated_cache(k, v, cos, sin, max_len):
+    """Caches [B, Hkv, max_len, D] holding k (rotated at positions 0..T-1) and v, the rest random."""
+    B, T, Hkv, D = k.shape
+    kr = oracle.apply_partial_rope(k.double(), cos[:T].double(), sin[:T].double())
+    g = torch.Generator().manual_seed(7)
+    kc = torch.randn(B, Hkv, max_len, D, generator=g, dtype=torch.float64)
+    vc = torch.randn(B, Hkv, max_len, D, generator=g, dtype=torch.float64)
+    kc[:, :, :T] = kr.transpose(1, 2)
+    vc[:, :, :T] = v.double().transpose(1, 2)
+    return kc, vc
+
+
+def test_cached_form_equals_self_form_decode_and_split_prompt():
+    """The cached form reduces to the self form at position 0 (cache = the call's rotated keys), to decode for
+    T = 1, and a prompt attended in two calls (positions 0..P-1, then P..T-1 over the cache) equals one call."""
+    inp = workloads.attn_prefill_inputs(B=2, T=50, Hq=8, Hkv=2, seed=4)
+    cos, sin = workloads.rope_tables(64)
+    q, k, v, gate = inp["q"], inp["k"], inp["v"], inp["gate"]
+    kc, vc = _rotated_cache(k, v, cos, sin, 64)
+    whole = oracle.gated_attention(q, k, v, gate, cos, sin, dtype=torch.float64)
+    z = torch.zeros(2, dtype=torch.int64)
+    got = oracle.gated_attention_cached(q, kc, vc, gate, z, cos, sin, dtype=torch.float64)
+    assert oracle.rel_err(got, whole) < 1e-12
+    P = 37
+    tail = oracle.gated_attention_cached(q[:, P:], kc, vc, gate[:, P:], z + P, cos, sin, dtype=torch.float64)
+    assert oracle.rel_err(tail, whole[:, P:]) < 1e-12
+    dec = oracle.gated_attention_decode(q[:, P], kc, vc, gate[:, P], z + P + 1, cos, sin, dtype=torch.float64)
+    one = oracle.gated_attention_cached(q[:, P:P + 1], kc, vc, gate[:, P:P + 1], z + P, cos, sin,
+                                        dtype=torch.float64)
+    assert oracle.rel_err(one[:, 0], dec) < 1e-12
+    # a planted off-by-one in the key range must be caught by the split-prompt identity
+    bad = oracle.gated_attention_cached(q[:, P:], kc, vc, gate[:, P:], z + P + 1, cos, sin, dtype=torch.float64)
+    assert oracle.rel_err(bad, whole[:, P:]) > 1e-3
+
+
+def test_cached_form_rows_at_different_positions():
+    """Each row of a cached call depends only on its own position and cache: rows computed together equal rows
+    computed alone."""
+    inp = workloads.attn_prefill_inputs(B=3, T=20, Hq=4, Hkv=1, seed=5)
+    cos, sin = workloads.rope_tables(128)
+    g = torch.Generator().manual_seed(8)
+    kc = torch.randn(3, 1, 128, 256, generator=g, dtype=torch.float64)
+    vc = torch.randn(3, 1, 128, 256, generator=g, dtype=torch.float64)
+    pos = torch.tensor([0, 13, 100])
+    both = oracle.gated_attention_cached(inp["q"], kc, vc, inp["gate"], pos, cos, sin, dtype=torch.float64)
+    for b in range(3):
+        one = oracle.gated_attention_cached(inp["q"][b:b + 1], kc[b:b + 1], vc[b:b + 1], inp["gate"][b:b + 1],
+                                            pos[b:b + 1], cos, sin, dtype=torch.float64)
+        assert torch.equal(one[0], both[b])
