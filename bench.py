@@ -32,8 +32,9 @@ ROTATE_BYTES = 640 << 20     # distinct bytes cycled through between two uses of
 GDN_PREFILL_BYTES = 68_681_728      # q,k,v bf16 + g,beta fp32 + o bf16 + final S fp32 (T 4096, H 16, d 128)
 GDN_PREFILL_FLOPS = 1.190e10
 # HBM bytes one GDN prefill launch (prep + scan kernels) actually moves: rocprofv3 FETCH_SIZE / WRITE_SIZE per
-# dispatch, each scaled by what the counter reads for a 256 MiB device copy (profiles/gdn_prefill_b1_t4096_h16_traffic.md)
-GDN_PREFILL_TRAFFIC_BYTES = 213_100_000
+# dispatch, each scaled by what the counter reads for a 256 MiB device copy
+# (profiles/counters_gdn_attn_decode_kernels.md)
+GDN_PREFILL_TRAFFIC_BYTES = 208_700_000
 GDN_DECODE_STEP_BYTES = 2_130_048   # S read + write fp32 + q,k,v,o,g,beta (B 1, H 16, d 128)
 ATTN_PREFILL_FLOPS = 6.874e10       # 4 * D * Hq * T (T + 1) / 2, T 4096, Hq 8, D 256
 ATTN_PREFILL_BYTES = 58_720_256
@@ -47,7 +48,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="", help="comma list of workloads to run")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the headline CPU baseline sample")
+    ap.add_argument("--cpu-case-seconds", type=float, default=2.0,
+                    help="budget of each per-workload CPU baseline sample (all threads and one thread)")
     return ap.parse_args()
 
 
@@ -194,19 +197,24 @@ def bench_copy(torch, dev, mb=256, reps=5):
 def bench_stack(torch, q35hip, workloads, dev, steps=256):
     """The Qwen3.5-0.8B-shaped hybrid stack (24 layers, int8 SwiGLU, tied 151,936 embedding), batch 3 steered rows:
     2048-token prefill, then `steps` greedy decode steps. The prefill is timed with each Gated DeltaNet prefill
-    kernel (the fp32 token-serial default and the chunked one); decode is timed host-driven (eager) and as replays of
-    one captured decode step (HIP graph)."""
+    kernel (the chunked default, fp32 products on the stack's fp32 activations, and the token-serial one); decode is
+    timed host-driven (eager) and as replays of one captured decode step (HIP graph)."""
     from q35hip import model as gm
     cfg = workloads.Q35Config()
     W = workloads.init_weights(cfg, seed=0)
     g = gm.HybridModel(cfg, W, dev, max_len=2048 + steps + 8, rows=3)
     del W
     prompt = torch.randint(0, cfg.vocab, (1, 2048), generator=torch.Generator().manual_seed(0)).repeat(3, 1)
+    # the workload's steering vector: randn (seed 0) scaled to 0.8 x the median residual norm after layer 12 of the
+    # unsteered prompt (tokens 1..2047), +v on row 0, none on row 1, -v on row 2
+    _, resid = g.forward(prompt, stop_after=12, collect_layer=12)
+    med = gm.median_resid_norm(resid[0])
     v = torch.randn(cfg.hidden, generator=torch.Generator().manual_seed(0))
-    g.set_vectors(torch.stack([v, -v]) * 0.1, [0, -1, 1])
-    out = {"rows": 3, "prompt": 2048, "steps": steps}
+    v = v / v.norm() * (0.8 * med)
+    g.set_vectors(torch.stack([v, -v]), [0, -1, 1])
+    out = {"rows": 3, "prompt": 2048, "steps": steps, "steer_norm": round(float(v.norm()), 4)}
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    for mode in ("chunk", "recurrent"):  # the default ("recurrent") last: its states feed the decode loops
+    for mode in ("recurrent", "chunk"):  # the default ("chunk") last: its states feed the decode loops
         g.gdn_prefill = mode
         for _ in range(2):  # warm: allocator, library handles
             g.reset()
@@ -247,30 +255,114 @@ def bench_stack(torch, q35hip, workloads, dev, steps=256):
     return out
 
 
+def host_cpu():
+    """The host CPU model (from /proc/cpuinfo) and the logical CPUs this process may run on."""
+    model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count()
+    return model, n
+
+
+def _time_calls(fn, budget_s, min_calls=2):
+    """Median seconds per call of fn() over about budget_s (at least min_calls calls)."""
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or len(times) < min_calls:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times), sum(times)
+
+
 def cpu_baseline(budget_s):
-    """The CPU oracle (a PyTorch-CPU restatement of the reference's fp32 path) timed on this host: the chunked gated
-    delta rule over the same T = 4096, 16-head workload, fp32, all threads torch uses, called repeatedly for about
-    budget_s seconds; the median call time is reported."""
+    """The headline's CPU baseline: the oracle's chunked gated delta rule (a PyTorch-CPU restatement of the reference's
+    fp32 path, HF:249-327) on the full B=1 T=4096 H=16 workload, fp32, all the threads torch uses, called repeatedly
+    for about budget_s seconds; the median call is reported."""
     import torch
     sys.path.insert(0, REPO)
     import oracle
     from q35hip import workloads
     inp = workloads.gdn_inputs(B=1, T=4096, H=16, D=128, seed=0, dtype=torch.bfloat16)
     threads = torch.get_num_threads()
-    times = []
-    t_start = time.perf_counter()
-    while time.perf_counter() - t_start < budget_s or len(times) < 3:
-        t0 = time.perf_counter()
-        oracle.chunk_gated_delta_rule(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"],
-                                      use_qk_l2norm_in_kernel=True)
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    t = times[len(times) // 2]
-    total = sum(times)
+    t, n, total = _time_calls(lambda: oracle.chunk_gated_delta_rule(inp["q"], inp["k"], inp["v"], inp["g"],
+                                                                   inp["beta"], use_qk_l2norm_in_kernel=True),
+                              budget_s, 3)
+    model, ncpu = host_cpu()
     return {"value": round(4096 / t, 1), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"oracle chunk_gated_delta_rule (fp32) on the full B=1 T=4096 H=16 d=128 workload, "
-                      f"{len(times)} calls in {total:.1f} s, median {t * 1e3:.1f} ms per call; host "
-                      f"{platform.processor() or platform.machine()}, {os.cpu_count()} logical CPUs visible"}
+                      f"{n} calls in {total:.1f} s, median {t * 1e3:.1f} ms per call; host {model}, "
+                      f"{ncpu} logical CPUs available"}
+
+
+def cpu_baselines(per_case_s):
+    """The oracle (PyTorch-CPU fp32 restatement of the reference path) on every workload, at all threads and at one
+    thread, each a bounded sample of about per_case_s seconds: config 1 one decode step (B 1, H 16) from a state
+    carried over 64 steps; config 2 the chunked rule at full size; config 3 the gated attention prefill at T 4096;
+    config 4 one decode step over 8192 keys at B 3 and B 32; config 5 the 24-layer stack at B 3: a 128-token prefill
+    (a bounded sample of the 2048-token prompt) and 4 decode steps. Returns tok/s per case."""
+    import torch
+    sys.path.insert(0, REPO)
+    import oracle
+    from oracle import model as om
+    from q35hip import workloads
+    model, ncpu = host_cpu()
+    all_threads = torch.get_num_threads()
+    out = {"host": model, "logical_cpus": ncpu, "kind": "port", "unit": "tok/s", "threads": {}}
+    g1 = workloads.gdn_inputs(B=1, T=64, H=16, D=128, seed=0)
+    g2 = workloads.gdn_inputs(B=1, T=4096, H=16, D=128, seed=0, dtype=torch.bfloat16)
+    a3 = workloads.attn_prefill_inputs(B=1, T=4096, seed=0)
+    cos3, sin3 = workloads.rope_tables(8192)
+    a4 = {B: workloads.attn_decode_inputs(B=B, N=8192, seed=0) for B in (3, 32)}
+    cfg = workloads.Q35Config()
+    W = workloads.init_weights(cfg, seed=0)
+    prompt = torch.randint(0, cfg.vocab, (3, 128), generator=torch.Generator().manual_seed(0))
+    for threads in sorted({all_threads, 1}, reverse=True):
+        torch.set_num_threads(threads)
+        r = {}
+        S = [torch.zeros(1, 16, 128, 128)]
+
+        def dec1():
+            t = len(S) % 64
+            sl = {k: v[:, t:t + 1] for k, v in g1.items()}
+            _, S[0] = oracle.recurrent_gated_delta_rule(sl["q"], sl["k"], sl["v"], sl["g"], sl["beta"],
+                                                        initial_state=S[0], use_qk_l2norm_in_kernel=True)
+        t, n, _ = _time_calls(dec1, per_case_s / 2, 8)
+        r["cfg1_gdn_decode_b1"] = {"tok_s": 1 / t, "ms_per_step": t * 1e3, "calls": n}
+        t, n, _ = _time_calls(lambda: oracle.chunk_gated_delta_rule(g2["q"], g2["k"], g2["v"], g2["g"], g2["beta"],
+                                                                    use_qk_l2norm_in_kernel=True), per_case_s, 1)
+        r["cfg2_gdn_prefill_t4096"] = {"tok_s": 4096 / t, "ms": t * 1e3, "calls": n}
+        t, n, _ = _time_calls(lambda: oracle.gated_attention(a3["q"], a3["k"], a3["v"], a3["gate"], cos3, sin3),
+                              per_case_s, 1)
+        r["cfg3_attn_prefill_t4096"] = {"tok_s": 4096 / t, "ms": t * 1e3, "calls": n}
+        for B, d in a4.items():
+            t, n, _ = _time_calls(lambda d=d: oracle.gated_attention_decode(d["q"], d["k_cache"], d["v_cache"],
+                                                                            d["gate"], d["cache_len"], cos3, sin3),
+                                  per_case_s / 2, 1)
+            r[f"cfg4_attn_decode_b{B}"] = {"tok_s": B / t, "ms": t * 1e3, "calls": n}
+        ref = om.OracleModel(cfg, W, steer_layer=12)
+        t0 = time.perf_counter()
+        logits, _ = ref.forward(prompt)
+        tp = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for _ in range(4):
+            logits, _ = ref.forward(logits.argmax(-1, keepdim=True))
+        td = (time.perf_counter() - t0) / 4
+        r["cfg5_stack_b3"] = {"prefill_tok_s": 3 * 128 / tp, "decode_tok_s": 3 / td, "prefill_ms_128": tp * 1e3,
+                              "decode_ms_per_step": td * 1e3}
+        out["threads"][str(threads)] = r
+    torch.set_num_threads(all_threads)
+    return out
 
 
 def main():
@@ -310,6 +402,9 @@ def main():
         print(f"# stack {res['stack']}", file=sys.stderr, flush=True)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    if not args.no_cpu and not only:
+        res["cpu"] = cpu_baselines(args.cpu_case_seconds)
+        print(f"# cpu {res['cpu']}", file=sys.stderr, flush=True)
     gp = res.get("gdn_prefill")
     line = {
         "metric": "GDN prefill tok/s + gated-attn decode tok/s @1 GPU; % of HBM/MFMA roofline",
