@@ -19,7 +19,7 @@ EXPORTS = [
     "q35_gated_attn_decode", "q35_gated_attn_decode_noalloc_max_bytes", "q35_gated_attn_decode_noalloc",
     "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
     "q35_swiglu_push",
-    "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm",
+    "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm", "q35_gemm_q8",
 ]
 
 Q35_F32, Q35_BF16, Q35_I8 = 0, 1, 2
@@ -60,6 +60,7 @@ _SIGS = {
     "q35_swiglu_push": ([P, P, I64, I64, P, I64, I64, P], I32),
     "q35_add_rmsnorm": ([P, I64, P, I64, P, P, I64, I64, I64, F32, P], I32),
     "q35_argmax_rows": ([P, I64, I64, I64, P, P, P], I32),
+    "q35_gemm_q8": ([P, I64, P, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
     "q35_gemv_norm": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
 }
 

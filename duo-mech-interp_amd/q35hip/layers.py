@@ -104,9 +104,10 @@ def prenorm_torch(x, prenorm):
 
 def linear(x, w, wq=None, ws=None, prenorm=None):
     """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), on the int8 rows wq with per-row scales
-    ws when given (w = wq * ws, dequantised), else on w; a torch GEMM on w otherwise. prenorm = (x_add, norm_w, eps,
-    x_out): x is a residual and the product takes the RMSNorm (1 + norm_w) of x + x_add (x_add may be None), the sum
-    being written to x_out when given (the decoder layer's add + norm, fused into the GEMV)."""
+    ws when given (w = wq * ws, dequantised), else on w; for more rows the HIP int8 GEMM on wq (fp32-accurate) when
+    given, else a torch GEMM on w. prenorm = (x_add, norm_w, eps, x_out): x is a residual and the product takes the
+    RMSNorm (1 + norm_w) of x + x_add (x_add may be None), the sum being written to x_out when given (the decoder
+    layer's add + norm, fused into the GEMV)."""
     K = x.shape[-1]
     M = x.numel() // K
     if M <= 8 and K % 256 == 0 and x.dtype == torch.float32 and (wq is not None or w.dtype == torch.float32):
@@ -120,6 +121,8 @@ def linear(x, w, wq=None, ws=None, prenorm=None):
         return ops.gemv(xm, Wd, sd, prenorm=pn).view(*x.shape[:-1], Wd.shape[0])
     if prenorm is not None:
         x = prenorm_torch(x, prenorm)
+    if wq is not None and K % 64 == 0 and x.dtype == torch.float32:
+        return ops.gemm_q8(x.reshape(M, K), wq, ws).view(*x.shape[:-1], wq.shape[0])
     return x @ w.T
 
 

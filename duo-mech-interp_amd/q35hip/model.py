@@ -36,9 +36,9 @@ _NO_PUSH = (1 << 30, 0, 0, 0, 0, 0)  # a record that matches no neuron (neuron i
 
 
 def mlp_weights(p):
-    """Per-layer MLP buffers (cached in p): "_gu" the [gate | up] fp32 weight of the prefill GEMM, "_gu_q8" / "_gu_s"
-    the int8 rows interleaved (gate j, up j) for the decode GEMV's SwiGLU epilogue, "_pushes" the layer's push
-    records."""
+    """Per-layer MLP buffers (cached in p): "_gu" the [gate | up] fp32 weight (the torch path without int8 weights),
+    "_gu_q8" / "_gu_s" the int8 rows interleaved (gate j, up j) for the SwiGLU epilogues of the decode GEMV and the
+    prefill GEMM, "_pushes" the layer's push records."""
     if "_gu" not in p:
         p["_gu"] = torch.cat([p["gate_proj"], p["up_proj"]], dim=0).contiguous()
         if "gate_proj.q" in p:
@@ -53,10 +53,11 @@ def mlp(p, h, x, prenorm=None):
     """x += SwiGLU MLP (HF:704-717) of h, in place, with the layer's neuron pushes at the down_proj input
     (engine/model.js:7-9, engine/kernels_qwen35.js:250-279). Decode (at most 8 rows, int8 weights present): one GEMV
     over the interleaved int8 gate/up rows with the SwiGLU + push epilogue, and one int8 GEMV accumulating down_proj
-    into x. Otherwise a [gate | up] GEMM on the dequantised weights, the SwiGLU push kernel and a down_proj GEMM
-    accumulating into x. prenorm = (y_add, norm_w, eps): h is then the residual; x receives h + y_add and the MLP
-    reads the RMSNorm (1 + norm_w) of that sum (the layer's second add + norm, fused into the first GEMV on the
-    decode path). Returns x."""
+    into x. Prefill (more rows): the int8 GEMM with the same SwiGLU + push epilogue over the interleaved rows, then an
+    int8 GEMM accumulating down_proj into x; without int8 weights a [gate | up] torch GEMM on the fp32 weights, the
+    SwiGLU push kernel and a down_proj GEMM. prenorm = (y_add, norm_w, eps): h is then the residual; x receives
+    h + y_add and the MLP reads the RMSNorm (1 + norm_w) of that sum (the layer's second add + norm, fused into the
+    first GEMV on the decode path). Returns x."""
     mlp_weights(p)
     H = h.shape[-1]
     M = h.numel() // H
@@ -70,6 +71,11 @@ def mlp(p, h, x, prenorm=None):
         return x
     if pn is not None:
         h = layers.prenorm_torch(h, pn)
+    if "_gu_q8" in p and H % 64 == 0 and p["down_proj.q"].shape[1] % 64 == 0:
+        # int8 GEMMs: [gate | up] interleaved with the SwiGLU + push epilogue, then down_proj accumulating into x
+        a = ops.gemm_q8(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T)
+        ops.gemm_q8(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H), epilogue="add")
+        return x
     a = ops.swiglu_push(h @ p["_gu"].T, p["_pushes"], T=T)
     x.view(M, H).addmm_(a.view(M, -1), p["down_proj"].T)
     return x

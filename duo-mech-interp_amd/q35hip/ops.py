@@ -74,6 +74,7 @@ _LIB.define("gdn_decode_fused_(Tensor y, Tensor conv_w, Tensor? conv_bias, Tenso
             "float eps, float scale) -> Tensor")
 _LIB.define("gemv_(Tensor x, Tensor W, Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
 _LIB.define("swiglu_push(Tensor gu, Tensor? pushes, int T) -> Tensor")
+_LIB.define("gemm_q8_(Tensor x, Tensor W, Tensor w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
 _LIB.define("add_rmsnorm_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tensor")
 _LIB.define("argmax_rows_(Tensor x, Tensor(a!) idx) -> ()")
 _LIB.define("gemv_norm_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
@@ -367,6 +368,24 @@ def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T):
     check(st, "q35_gemv")
 
 
+def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T):
+    _on_gpu(W, w_scale, pushes)
+    _require(x.is_cuda and x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1,
+             "x: [M, K] fp32 with unit column stride")
+    _require(y.is_cuda and y.dtype == torch.float32 and y.dim() == 2 and y.stride(1) == 1, "y: [M, N] fp32")
+    _require(W.dim() == 2 and W.dtype == torch.int8, "W: [N, K] int8")
+    M, K = x.shape
+    N = W.shape[0]
+    _require(W.shape[1] == K and y.shape[0] == M, "x, W, y shapes disagree")
+    _require(y.shape[1] == (N // 2 if epilogue == 2 else N), "y: [M, N] ([M, N / 2] for the SwiGLU epilogue)")
+    _require(w_scale.dtype == torch.float32 and w_scale.numel() == N, "w_scale: [N] fp32")
+    _require(K % 64 == 0, "K must be a multiple of 64")
+    npush = _pushes_check(pushes)
+    st = _lib.lib().q35_gemm_q8(_ptr(x), x.stride(0), _ptr(W), _ptr(w_scale), _ptr(y), y.stride(0), M, N, K,
+                                int(epilogue), _ptr(pushes), npush, int(T), _stream(x))
+    check(st, "q35_gemm_q8")
+
+
 def _gemv_norm_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, epilogue, pushes, T):
     _on_gpu(x, x_add, x_out, norm_w, W, w_scale, y, pushes)
     _require(x.dtype == torch.float32 and x.dim() == 2 and y.dtype == torch.float32 and y.dim() == 2,
@@ -434,6 +453,7 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl),
                      ("gdn_decode_fused_", _gdn_decode_fused_impl),
                      ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
+                     ("gemm_q8_", _gemm_q8_impl),
                      ("add_rmsnorm_", _add_rmsnorm_impl), ("argmax_rows_", _argmax_rows_impl),
                      ("gemv_norm_", _gemv_norm_impl)]:
     _LIB.impl(_name, _impl, "CUDA")
@@ -466,6 +486,7 @@ _LIB.impl("gated_attn_prefill_cached",
 _LIB.impl("argmax_rows_", lambda x, idx: None, "Meta")
 _LIB.impl("gemv_norm_", lambda x, xa, xo, nw, eps, W, ws, y, e, pushes, T: None, "Meta")
 _LIB.impl("gemv_", lambda x, W, ws, y, e, pushes, T: None, "Meta")
+_LIB.impl("gemm_q8_", lambda x, W, ws, y, e, pushes, T: None, "Meta")
 _LIB.impl("swiglu_push", lambda gu, pushes, T: gu.new_empty(*gu.shape[:-1], gu.shape[-1] // 2), "Meta")
 _LIB.impl("add_rmsnorm_", lambda x, y, w, eps: torch.empty_like(x), "Meta")
 _LIB.impl("gated_rmsnorm", lambda o, z, w, hs, eps: o.new_empty(*o.shape[:-2], o.shape[-2] * o.shape[-1]), "Meta")
@@ -632,6 +653,20 @@ def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, preno
     else:
         x_add, norm_w, eps, x_out = prenorm
         torch.ops.q35.gemv_norm_(x, x_add, x_out, norm_w, float(eps), W, w_scale, out, e, pushes, int(T))
+    return out
+
+
+def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1):
+    """y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k] over many rows (the prefill projections): x [M, K] fp32, W [N, K]
+    int8, K a multiple of 64; fp32-accurate (bf16 MFMA on a hi + lo split of x). epilogue "store" writes out, "add"
+    accumulates into out, "swiglu" treats W's rows as interleaved (gate, up) pairs and writes
+    silu(gate) * up with the neuron pushes (pack_pushes) applied, out [M, N / 2]. Returns out."""
+    e = _EPI[epilogue]
+    x = x if x.stride(-1) == 1 else x.contiguous()
+    if out is None:
+        N = W.shape[0] // 2 if e == 2 else W.shape[0]
+        out = torch.empty(x.shape[0], N, dtype=torch.float32, device=x.device)
+    torch.ops.q35.gemm_q8_(x, W, w_scale, out, e, pushes, int(T))
     return out
 
 

@@ -31,6 +31,8 @@
  *   q35_gemv_norm            q35_gemv behind the layer's residual add + RMSNorm (HF:753-793, :720-734;
  *                            engine/kernels.js:226-246 `addInto` + `rmsnorm` ahead of the matvec)
  *   q35_swiglu_push          engine/kernels_qwen35.js:250-279 `swiglu` over a [gate | up] projection (prefill form)
+ *   q35_gemm_q8              engine/kernels.js:97-151 `matmul` (int8 weights, many rows: the prefill projections),
+ *                            with the SwiGLU + push epilogue of `swiglu` (engine/kernels_qwen35.js:250-279)
  *   q35_add_rmsnorm          HF:720-734 Qwen3_5RMSNorm (1 + w) with the residual add before it (HF:753-793);
  *                            engine/kernels.js:226-246 `rmsnorm` (OFFSET) and `addInto`
  *   q35_argmax_rows          engine/kernels.js:260-283 `argmax` (greedy token of each row, engine/model.js:494-497)
@@ -279,6 +281,21 @@ int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const floa
 int q35_gemv_norm(const float* x, const float* x_add, float* x_out, int64_t ldx, const float* norm_w, float eps,
                   const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy, int64_t M, int64_t N,
                   int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream);
+
+/*
+ * Many-row int8 GEMM for the prefill projections: y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k]. Replaces the
+ * engine's int8 `matmul` (engine/kernels.js:97-151, used when M > 32) and, with the SwiGLU epilogue, its `swiglu`
+ * with the neuron pushes (engine/kernels_qwen35.js:250-279); HF:704-717 and the mixers' projections in fp32.
+ *   x: [M, ldx] fp32 (16-byte aligned, ldx a multiple of 4); W: [N, K] int8 row-major (16-byte aligned), K a multiple
+ *   of 64; w_scale: [N] fp32; y: [M, ldy] fp32. fp32-accurate: bf16 MFMA products of W (exact in bf16) with a hi + lo
+ *   split of x (relative error about 1e-5).
+ *   epilogue 0: y = v; 1: y += v; 2: SwiGLU over interleaved row pairs (row 2 j gate, 2 j + 1 up of neuron j):
+ *   y[m, j] = silu(v_2j) * v_2j+1 then the pushes in order (N even, ldy >= N / 2). pushes, npush <= 64 and T as
+ *   for q35_gemv.
+ */
+int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
+                int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T,
+                q35_stream_t stream);
 
 /*
  * a[m, n] = silu(gu[m, n]) * gu[m, I + n] with the pushes applied, gu: [M, 2 I] fp32 ([gate | up] per row),

@@ -1,0 +1,71 @@
+"""The int8 prefill GEMM (q35_gemm_q8) on the GPU against the oracle's int8 product (oracle.mlp.q8_linear, fp32 on
+the dequantised weights) and the oracle's SwiGLU + push semantics. The GEMM computes bf16 MFMA products on a hi + lo
+split of x, so it agrees with the fp32 product to about 1e-5 (tolerance 1e-4 here)."""
+import pytest
+import torch
+
+import oracle
+from oracle import mlp as omlp
+from q35hip import ops
+from gpu_util import announce, device
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _q8(N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * 0.02
+    s = w.abs().amax(dim=1) / 127.0
+    q = torch.clamp(torch.round(w / s[:, None]), -127, 127).to(torch.int8)
+    return q, s
+
+
+# shapes: the stack's projections at small M, ragged M and N (masked edges), M past the 128-row tile threshold
+@pytest.mark.parametrize("M,N,K", [(9, 8224, 1024), (100, 1024, 2048), (300, 130, 64), (2048, 5120, 1024),
+                                   (1500, 1024, 3584)])
+def test_gemm_q8_store_and_accumulate(M, N, K):
+    dev = device()
+    q, s = _q8(N, K, M + N)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(K)) * 3.0
+    ref = omlp.q8_linear(x, q, s)
+    announce(f"gemm_q8 store M{M} N{N} K{K}")
+    y = ops.gemm_q8(x.to(dev), q.to(dev), s.to(dev))
+    e = oracle.rel_err(y.cpu(), ref)
+    print(f"gemm_q8 M{M} N{N} K{K}: rel err {e:.2e}")
+    assert e <= TOL
+    base = torch.randn(M, N)
+    out = base.to(dev)
+    ops.gemm_q8(x.to(dev), q.to(dev), s.to(dev), out=out, epilogue="add")
+    assert oracle.rel_err(out.cpu() - base, ref) <= TOL
+
+
+def test_gemm_q8_strided_rows_of_x():
+    """x rows with a leading dimension past K (a column slice of a wider buffer)."""
+    dev = device()
+    q, s = _q8(256, 128, 3)
+    wide = torch.randn(70, 200, generator=torch.Generator().manual_seed(4))
+    ref = omlp.q8_linear(wide[:, :128], q, s)
+    announce("gemm_q8 strided x")
+    y = ops.gemm_q8(wide.to(dev)[:, :128], q.to(dev), s.to(dev))
+    assert oracle.rel_err(y.cpu(), ref) <= TOL
+
+
+@pytest.mark.parametrize("M,T", [(40, 20), (2048, 2048), (6144, 2048)])
+def test_gemm_q8_swiglu_with_pushes(M, T):
+    """Interleaved (gate, up) rows, SwiGLU epilogue, pushes in order (add then mul on one neuron, an all-neuron add),
+    push rows min(m / T, 3)."""
+    dev = device()
+    I, H = 3584, 1024
+    qg, sg = _q8(I, H, 5)
+    qu, su = _q8(I, H, 6)
+    q = torch.stack([qg, qu], dim=1).reshape(2 * I, H).contiguous()
+    s = torch.stack([sg, su], dim=1).reshape(2 * I).contiguous()
+    x = torch.randn(M, H, generator=torch.Generator().manual_seed(M))
+    pushes = [(7, "add", [1.0, 2.0, -1.0]), (7, "mul", [2.0, 0.5, 3.0]), (None, "add", [0.25, 0.0, -0.25])]
+    ref = omlp.swiglu_push(omlp.q8_linear(x, qg, sg), omlp.q8_linear(x, qu, su), pushes, T=T)
+    announce(f"gemm_q8 swiglu M{M} T{T}")
+    a = ops.gemm_q8(x.to(dev), q.to(dev), s.to(dev), epilogue="swiglu", pushes=ops.pack_pushes(pushes, dev), T=T)
+    e = oracle.rel_err(a.cpu(), ref)
+    print(f"gemm_q8 swiglu M{M}: rel err {e:.2e}")
+    assert e <= TOL
