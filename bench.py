@@ -177,6 +177,37 @@ def bench_attn_decode(torch, q35hip, workloads, steps, warmup, dev):
     return out
 
 
+GEMM_SHAPES = (("gdn_in_proj", 8224, 1024, "store"), ("mlp_gate_up", 7168, 1024, "swiglu"),
+               ("mlp_down", 1024, 3584, "add"), ("attn_in_proj", 5120, 1024, "store"),
+               ("out_proj", 1024, 2048, "add"))
+
+
+def bench_gemm(torch, q35hip, steps, warmup, dev, M=6144):
+    """The int8 prefill GEMM on the stack's projection shapes at M = 3 rows x 2048 tokens (x fp32, W int8 per output
+    channel), and torch's fp32 GEMM on the dequantised weights for comparison. TFLOP/s count the nominal 2 M N K
+    (the kernel executes twice that: the hi and lo parts of x)."""
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, N, K, epi in GEMM_SHAPES:
+        x = torch.randn(M, K, device=dev, generator=g)
+        q = torch.randint(-127, 128, (N, K), device=dev, generator=g, dtype=torch.int8)
+        sc = torch.rand(N, device=dev, generator=g) * 1e-3
+        y = torch.zeros(M, N // 2 if epi == "swiglu" else N, device=dev)
+        pushes = q35hip.ops.pack_pushes([(0, "add", [0.0])], dev) if epi == "swiglu" else None
+
+        def make_call(i):
+            return lambda: q35hip.ops.gemm_q8(x, q, sc, out=y, epilogue=epi, pushes=pushes, T=2048)
+        r = Timer(torch, make_call, 1, reps=8).run(steps, warmup)
+        wf = (q.float() * sc[:, None]).contiguous()
+        r2 = Timer(torch, lambda i: (lambda: torch.mm(x, wf.T)), 1, reps=8).run(steps, warmup)
+        fl = 2.0 * M * N * K
+        out[name] = {"M": M, "N": N, "K": K, "us": r["step_s"] * 1e6, "tflops": fl / r["step_s"] / 1e12,
+                     "frac_bf16_peak": fl / r["step_s"] / 1e12 / PEAK_BF16_TFLOPS,
+                     "torch_fp32_us": r2["step_s"] * 1e6}
+        del x, q, wf, y
+    return out
+
+
 def bench_copy(torch, dev, mb=256, reps=5):
     """A plain device copy of known size (mb MiB read + mb MiB written per launch): the calibration point for the
     FETCH_SIZE / WRITE_SIZE counters of a profiler run."""
@@ -394,6 +425,9 @@ def main():
         res["gdn_decode"] = bench_gdn_decode(torch, q35hip, workloads, args.steps, args.warmup, dev)
         print(f"# gdn_decode {res['gdn_decode']}", file=sys.stderr, flush=True)
 
+    if want("gemm"):
+        res["gemm"] = bench_gemm(torch, q35hip, args.steps, args.warmup, dev)
+        print(f"# gemm {res['gemm']}", file=sys.stderr, flush=True)
     if only and "copy" in only:
         res["copy"] = bench_copy(torch, dev)
         print(f"# copy {res['copy']}", file=sys.stderr, flush=True)
