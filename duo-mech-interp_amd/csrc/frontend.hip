@@ -516,7 +516,8 @@ extern "C" int q35_gdn_decode_fused(const float* y, int64_t ldy, const float* co
   const int64_t C = 3 * H * d, Vd = H * d;
   if (ldy < C || b_off < 0 || a_off < 0 || z_off < 0 || b_off + H > ldy || a_off + H > ldy || z_off + Vd > ldy)
     return Q35_EINVAL;
-  if (d != kFD || K > kConvMaxK || (ldy & 3) || ((uintptr_t)y & 15) || ((uintptr_t)conv_state & 15))
+  if (d != kFD || K > kConvMaxK || (ldy & 3) || ((uintptr_t)y & 15) || ((uintptr_t)conv_state & 15) ||
+      ((uintptr_t)state & 15))
     return Q35_EUNSUPPORTED;
   if (conv_bias && ((uintptr_t)conv_bias & 15)) return Q35_EUNSUPPORTED;
   if (B > 65535 || H > 65535 || B * ldy > ((int64_t)1 << 40) || C > 0x7fffffff) return Q35_EUNSUPPORTED;

@@ -164,6 +164,8 @@ extern "C" int q35_gdn_recurrent(const void* q, const void* k, const void* v, co
   if (B <= 0 || T <= 0 || Hk <= 0 || H <= 0 || Dk <= 0 || Dv <= 0 || H % Hk != 0) return Q35_EINVAL;
   if (Dk != kGdnD || Dv != kGdnD) return Q35_EUNSUPPORTED;
   if (B > 65535 || H > 65535 || T > 0x7fffffff / (H > Hk ? H : Hk) / kGdnD) return Q35_EUNSUPPORTED;
+  // the state is read and written as 16-byte vectors
+  if (((uintptr_t)final_state & 15) || (initial_state && ((uintptr_t)initial_state & 15))) return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   dim3 grid(kGdnD / kGdnJS, (unsigned)H, (unsigned)B), block(256);
   if (dtype == Q35_F32)

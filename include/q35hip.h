@@ -82,7 +82,8 @@ int q35_abi_version(void);
  * (engine/kernels_qwen35.js:229-236).
  *   q, k:  [B, T, Hk, Dk]   dtype           v, out: [B, T, H, Dv]   dtype
  *   g, beta: [B, T, H] fp32 (g is the log decay, alpha = exp(g))
- *   initial_state: [B, H, Dk, Dv] fp32 or NULL (zeros); final_state: [B, H, Dk, Dv] fp32 (may alias initial_state)
+ *   initial_state: [B, H, Dk, Dv] fp32 or NULL (zeros); final_state: [B, H, Dk, Dv] fp32 (may alias initial_state);
+ *   both 16-byte aligned (Q35_EUNSUPPORTED otherwise)
  *   H must be a multiple of Hk (q/k head h / (H / Hk) serves value head h, as repeat_interleave at HF:500-502).
  *   Dk = Dv = 128 (the reference engine requires it: engine/model.js:52).
  *   scale multiplies q after the optional l2 normalisation (HF uses 1/sqrt(Dk)).
@@ -218,7 +219,7 @@ int q35_gdn_conv(const float* y, int64_t ldy, const float* conv_w, const float* 
  *      a at a_off; conv_w [C, K], conv_bias [C] or NULL, conv_state [B, K - 1, C] (advanced in place);
  *   A_log, dt_bias, head_scale (or NULL): [H]; norm_w: [d]; state: [B, H, d, d] fp32 (updated in place);
  *   scale: the q scale (1 / sqrt(d)); out: [B, H d] fp32, the gated-normed output.
- *   d = 128, K <= 8; y, conv_state (and conv_bias) 16-byte aligned, ldy a multiple of 4.
+ *   d = 128, K <= 8; y, conv_state, state (and conv_bias) 16-byte aligned, ldy a multiple of 4.
  */
 int q35_gdn_decode_fused(const float* y, int64_t ldy, const float* conv_w, const float* conv_bias,
                          float* conv_state, const float* A_log, const float* dt_bias, int64_t b_off, int64_t a_off, int64_t z_off,

@@ -67,7 +67,6 @@ def test_decode_continues_prefill_and_rows_are_independent(tiny):
     assert oracle.rel_err(step, ref) <= 1e-5
     m3 = om.OracleModel(cfg, W)
     row1, _ = m3.forward(ids[1:])
-    assert oracle.rel_err(row1[0], ref[1]) <= 1e-5 or True  # ref includes one more token; compare prefill below
     m4 = om.OracleModel(cfg, W)
     both, _ = m4.forward(ids)
     assert oracle.rel_err(row1[0], both[1]) <= 1e-5
