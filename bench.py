@@ -6,8 +6,9 @@ q/k/v, chunk 64, fp32 state -> tokens per second. The same line carries a breakd
 decode step, gated-attention prefill T = 4096, gated-attention decode B = 3 and 32 over an 8192 context), each as
 tok/s and as a fraction of its roofline, plus the CPU oracle timed on the host cores.
 
-Method: every step is one call of the op on fresh device-resident inputs. Steps are captured once per input set in a
-HIP graph and replayed; HIP events recorded on the launch stream around each replay give the per-step GPU time.
+Method: every step is one call of the op on fresh device-resident inputs. The calls over all input sets are captured
+back to back in one HIP graph and replayed (as a model's layers run); HIP events recorded on the launch stream around
+each replay, divided by the calls it holds, give the per-step GPU time.
 Input sets rotate so that the bytes touched between two uses of one set exceed the 256 MB Infinity Cache: the GB/s
 figures are HBM figures, not cache figures.
 
@@ -114,7 +115,7 @@ def bench_gdn_prefill(torch, q35hip, workloads, steps, warmup, dev):
         d = sets[i]
         return lambda: q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"],
                                                      output_final_state=True, use_qk_l2norm_in_kernel=True)
-    r = Timer(torch, make_call, n).run(steps, warmup)
+    r = Timer(torch, make_call, n, reps=n).run(steps, warmup)
     t = r["step_s"]
     gbs = GDN_PREFILL_BYTES / t / 1e9
     return {"tok_s": T * B / t, "ms": t * 1e3, "achieved_gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
@@ -149,7 +150,7 @@ def bench_attn_prefill(torch, q35hip, workloads, steps, warmup, dev):
     def make_call(i):
         d = sets[i]
         return lambda: q35hip.gated_attention_prefill(d["q"], d["k"], d["v"], d["gate"], cos, sin)
-    r = Timer(torch, make_call, n).run(steps, warmup)
+    r = Timer(torch, make_call, n, reps=n).run(steps, warmup)
     t = r["step_s"]
     tf = ATTN_PREFILL_FLOPS / t / 1e12
     return {"tok_s": T / t, "ms": t * 1e3, "achieved_tflops": tf, "frac": tf / PEAK_BF16_TFLOPS, "sets": n}
