@@ -34,7 +34,7 @@ GDN_PREFILL_BYTES = 68_681_728      # q,k,v bf16 + g,beta fp32 + o bf16 + final 
 GDN_PREFILL_FLOPS = 1.190e10
 # HBM bytes one GDN prefill launch (prep + scan kernels) actually moves: rocprofv3 FETCH_SIZE / WRITE_SIZE per
 # dispatch, each scaled by what the counter reads for a 256 MiB device copy
-# (profiles/counters_gdn_attn_decode_kernels.md)
+# (profiles/counters_gdn_attn_gemm_kernels.md)
 GDN_PREFILL_TRAFFIC_BYTES = 208_700_000
 GDN_DECODE_STEP_BYTES = 2_130_048   # S read + write fp32 + q,k,v,o,g,beta (B 1, H 16, d 128)
 ATTN_PREFILL_FLOPS = 6.874e10       # 4 * D * Hq * T (T + 1) / 2, T 4096, Hq 8, D 256
@@ -120,6 +120,24 @@ def bench_gdn_prefill(torch, q35hip, workloads, steps, warmup, dev):
     gbs = GDN_PREFILL_BYTES / t / 1e9
     return {"tok_s": T * B / t, "ms": t * 1e3, "achieved_gbs": gbs, "frac": gbs / PEAK_HBM_GBS,
             "tflops": GDN_PREFILL_FLOPS / t / 1e12, "wall_ms_per_step": r["wall_s"] / steps * 1e3, "sets": n}
+
+
+def bench_gdn_prefill_f32(torch, q35hip, workloads, steps, warmup, dev):
+    """The chunked rule on fp32 inputs (the fp32 path: every product in fp32) at the hybrid stack's GDN prefill
+    shape, B = 3, T = 2048, 16 heads, from a carried state."""
+    B, T, H, D = 3, 2048, 16, 128
+    n = 4
+    sets = [workloads.to_device(workloads.gdn_inputs(B=B, T=T, H=H, D=D, seed=i, dtype=torch.float32), dev)
+            for i in range(n)]
+    s0 = torch.zeros(B, H, D, D, device=dev)
+
+    def make_call(i):
+        d = sets[i]
+        return lambda: q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=s0,
+                                                     output_final_state=True, use_qk_l2norm_in_kernel=True)
+    r = Timer(torch, make_call, n, reps=n).run(steps, warmup)
+    t = r["step_s"]
+    return {"tok_s": B * T / t, "us": t * 1e6, "shape": "B3 T2048 H16 d128 fp32"}
 
 
 def bench_gdn_decode(torch, q35hip, workloads, steps, warmup, dev):
@@ -422,6 +440,9 @@ def main():
     if want("attn_prefill"):
         res["attn_prefill"] = bench_attn_prefill(torch, q35hip, workloads, args.steps, args.warmup, dev)
         print(f"# attn_prefill {res['attn_prefill']}", file=sys.stderr, flush=True)
+    if want("gdn_prefill_f32"):
+        res["gdn_prefill_f32"] = bench_gdn_prefill_f32(torch, q35hip, workloads, args.steps, args.warmup, dev)
+        print(f"# gdn_prefill_f32 {res['gdn_prefill_f32']}", file=sys.stderr, flush=True)
     if want("gdn_decode"):
         res["gdn_decode"] = bench_gdn_decode(torch, q35hip, workloads, args.steps, args.warmup, dev)
         print(f"# gdn_decode {res['gdn_decode']}", file=sys.stderr, flush=True)
