@@ -202,22 +202,22 @@ GEMM_SHAPES = (("gdn_in_proj", 8224, 1024, "store"), ("mlp_gate_up", 7168, 1024,
 
 
 def bench_gemm(torch, q35hip, steps, warmup, dev, M=6144):
-    """The int8 prefill GEMM on the stack's projection shapes at M = 3 rows x 2048 tokens (x fp32, W int8 per output
-    channel), and torch's fp32 GEMM on the dequantised weights for comparison. TFLOP/s count the nominal 2 M N K
-    (the kernel executes twice that: the hi and lo parts of x)."""
+    """The int8 prefill GEMM on the stack's projection shapes at M = 3 rows x 2048 tokens (x fp32, W int8 with one
+    scale per group of 128 inputs, the stack's format), and torch's fp32 GEMM on the dequantised weights for
+    comparison. TFLOP/s count the nominal 2 M N K (the kernel executes twice that: the hi and lo parts of x)."""
     out = {}
     g = torch.Generator(device=dev).manual_seed(0)
     for name, N, K, epi in GEMM_SHAPES:
         x = torch.randn(M, K, device=dev, generator=g)
         q = torch.randint(-127, 128, (N, K), device=dev, generator=g, dtype=torch.int8)
-        sc = torch.rand(N, device=dev, generator=g) * 1e-3
+        sc = torch.rand(N, K // 128, device=dev, generator=g) * 1e-3
         y = torch.zeros(M, N // 2 if epi == "swiglu" else N, device=dev)
         pushes = q35hip.ops.pack_pushes([(0, "add", [0.0])], dev) if epi == "swiglu" else None
 
         def make_call(i):
             return lambda: q35hip.ops.gemm_q8(x, q, sc, out=y, epilogue=epi, pushes=pushes, T=2048)
         r = Timer(torch, make_call, 1, reps=8).run(steps, warmup)
-        wf = (q.float() * sc[:, None]).contiguous()
+        wf = (q.float().reshape(N, K // 128, 128) * sc[:, :, None]).reshape(N, K).contiguous()
         r2 = Timer(torch, lambda i: (lambda: torch.mm(x, wf.T)), 1, reps=8).run(steps, warmup)
         fl = 2.0 * M * N * K
         out[name] = {"M": M, "N": N, "K": K, "us": r["step_s"] * 1e6, "tflops": fl / r["step_s"] / 1e12,

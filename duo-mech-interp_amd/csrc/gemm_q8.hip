@@ -1,10 +1,9 @@
-// Int8 per-output-channel GEMM for the prefill projections: y[m, n] = s[n] * sum_k x[m, k] W[n, k] for many rows of
-// x (the decode step's few rows use gemv.hip). x fp32 [M, K], W int8 [N, K] row-major with one fp32 scale per
-// output row, y fp32.
+// Int8 GEMM for the prefill projections: y[m, n] = sum_k x[m, k] W[n, k] s(n, k) for many rows of x (the decode
+// step's few rows use gemv.hip). x fp32 [M, K], W int8 [N, K] row-major with one fp32 scale per group of 128 inputs
+// of a row (s(n, k) = scale[n][k / 128], the engine's q8 format) or per output row (s(n, k) = scale[n]), y fp32.
 //
-// Reference: the engine's int8 `matmul` (engine/kernels.js:97-151: 64 x 64 tiles, used when M > 32; it quantizes
-// per group of 128 inputs, this build per output channel) and the MLP path with the neuron hook (`swiglu`,
-// engine/kernels_qwen35.js:250-279).
+// Reference: the engine's int8 `matmul` (engine/kernels.js:97-151: 64 x 64 tiles, used when M > 32; q8 weights of
+// engine/kernels.js:15-47) and the MLP path with the neuron hook (`swiglu`, engine/kernels_qwen35.js:250-279).
 //
 // Arithmetic: bf16 MFMA (v_mfma_f32_32x32x16_bf16) with fp32 accumulation. Each x is split into hi = bf16(x) and
 // lo = bf16(x - hi), so x = hi + lo up to 2^-17 |x|; the int8 weights are exact in bf16. Two products per tile
@@ -16,6 +15,8 @@
 // 16 bytes, segment s of row r at s ^ (r & 7) (the 32 rows an MFMA operand read touches hit 8 distinct segments).
 // The next step's global loads are issued before the current step's MFMAs, so they are in flight during them.
 // Blocks run n-fastest inside an m panel: the panel's rows of x stay in L2 while its column tiles pass.
+// Group scales (GS): the MFMAs of one group (two K steps) accumulate into a second register set, which is then added
+// to the result scaled by the group's scale of the lane's column (one fp32 FMA per accumulator per 128 inputs).
 // Epilogues: store, accumulate into y (the residual add after down_proj / out_proj), or SwiGLU over interleaved
 // (gate, up) row pairs with the neuron pushes applied, writing y[m, n / 2].
 #include "q35_common.h"
@@ -59,7 +60,7 @@ __device__ __forceinline__ bf16x8 i8tobf(uint32_t w0, uint32_t w1) {
   return r;
 }
 
-template <int BM, int EPI>
+template <int BM, int EPI, bool GS>
 __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const float* __restrict__ X, int64_t ldx,
                                                          const int8_t* __restrict__ W, const float* __restrict__ ws,
                                                          float* __restrict__ Y, int64_t ldy, int M, int N, int K,
@@ -114,18 +115,30 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const float* __restrict
     }
   };
 
-  f32x16 acc[MT][2];
+  f32x16 acc[MT][2], gacc[MT][2];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = zero16();
+    for (int nt = 0; nt < 2; ++nt) {
+      acc[mt][nt] = zero16();
+      gacc[mt][nt] = zero16();
+    }
 
   const int l32 = lane & 31, lh = lane >> 5;
+  // GS: the lane's two columns' scale rows (column n = n0 + wn 64 + 32 nt + l32)
+  const float* srow[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) srow[nt] = ws + (size_t)min(n0 + wn * 64 + 32 * nt + l32, N - 1) * (K >> 7);
+  float gsc[2] = {0.f, 0.f};
   load(0);
   for (int k0 = 0; k0 < K; k0 += kGK) {
     __syncthreads();  // every wave is done reading the previous step's tiles
     stage();
     if (k0 + kGK < K) load(k0 + kGK);  // next step's loads fly during this step's MFMAs
+    if (GS && (k0 & 127) == 0) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) gsc[nt] = srow[nt][k0 >> 7];
+    }
     __syncthreads();
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -146,8 +159,19 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const float* __restrict
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-          acc[mt][nt] = mfma32(ah[mt], b[nt], acc[mt][nt]);
-          acc[mt][nt] = mfma32(al[mt], b[nt], acc[mt][nt]);
+          f32x16& d = GS ? gacc[mt][nt] : acc[mt][nt];
+          d = mfma32(ah[mt], b[nt], d);
+          d = mfma32(al[mt], b[nt], d);
+        }
+    }
+    if (GS && ((k0 + kGK) & 127) == 0) {  // end of a group: fold it in with its scale
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[mt][nt][r] += gsc[nt] * gacc[mt][nt][r];
+          gacc[mt][nt] = zero16();
         }
     }
   }
@@ -156,7 +180,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const float* __restrict
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int n = n0 + wn * 64 + 32 * nt + l32;
-    const float s = ws[min(n, N - 1)];
+    const float s = GS ? 1.f : ws[min(n, N - 1)];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -182,11 +206,14 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const float* __restrict
 
 }  // namespace q35
 
-extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y,
-                           int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
-                           int64_t npush, int64_t T, q35_stream_t stream) {
+extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
+                           float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
+                           const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
   using namespace q35;
   if (!x || !W || !w_scale || !y || M <= 0 || N <= 0 || K <= 0 || T <= 0) return Q35_EINVAL;
+  if (w_dtype != Q35_I8 && w_dtype != Q35_I8_G128) return Q35_EUNSUPPORTED;
+  const bool gs = w_dtype == Q35_I8_G128;
+  if (gs && K % 128 != 0) return Q35_EUNSUPPORTED;
   if (epilogue < kGemmStore || epilogue > kGemmSwiglu) return Q35_EINVAL;
   if (npush < 0 || (npush > 0 && !pushes) || npush > 64) return Q35_EINVAL;
   if (epilogue == kGemmSwiglu ? (N % 2 != 0 || ldy < N / 2) : ldy < N) return Q35_EINVAL;
@@ -200,18 +227,19 @@ extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, const f
   const int64_t nblocks = ((M + BM - 1) / BM) * nbn;
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define Q35_GEMM_LAUNCH(BMV, E)                                                                                  \
-  hipLaunchKernelGGL((gemm_q8_kernel<BMV, E>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W, w_scale, y, \
-                     ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T)
+#define Q35_GEMM_LAUNCH(BMV, E, G)                                                                               \
+  hipLaunchKernelGGL((gemm_q8_kernel<BMV, E, G>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W, w_scale, \
+                     y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T)
+#define Q35_GEMM_EPI(BMV, G)                                              \
+  if (epilogue == kGemmStore) Q35_GEMM_LAUNCH(BMV, kGemmStore, G);        \
+  else if (epilogue == kGemmAccumulate) Q35_GEMM_LAUNCH(BMV, kGemmAccumulate, G); \
+  else Q35_GEMM_LAUNCH(BMV, kGemmSwiglu, G);
   if (big) {
-    if (epilogue == kGemmStore) Q35_GEMM_LAUNCH(128, kGemmStore);
-    else if (epilogue == kGemmAccumulate) Q35_GEMM_LAUNCH(128, kGemmAccumulate);
-    else Q35_GEMM_LAUNCH(128, kGemmSwiglu);
+    if (gs) { Q35_GEMM_EPI(128, true) } else { Q35_GEMM_EPI(128, false) }
   } else {
-    if (epilogue == kGemmStore) Q35_GEMM_LAUNCH(64, kGemmStore);
-    else if (epilogue == kGemmAccumulate) Q35_GEMM_LAUNCH(64, kGemmAccumulate);
-    else Q35_GEMM_LAUNCH(64, kGemmSwiglu);
+    if (gs) { Q35_GEMM_EPI(64, true) } else { Q35_GEMM_EPI(64, false) }
   }
+#undef Q35_GEMM_EPI
 #undef Q35_GEMM_LAUNCH
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }

@@ -1,11 +1,12 @@
-// Small-M matrix-vector products for the decode step: y[m, n] = s[n] * sum_k x[m, k] W[n, k] for M <= 8 rows of x,
-// W row-major [N, K] in int8 with one fp32 scale per output row (the int8 per-output-channel MLP weights), or fp32
-// (scale 1). HBM-bound on W: every weight byte is read once.
+// Small-M matrix-vector products for the decode step: y[m, n] = sum_k x[m, k] W[n, k] s(n, k) for M <= 8 rows of x,
+// W row-major [N, K] in int8 with one fp32 scale per group of 128 inputs of a row (s(n, k) = scale[n][k / 128], the
+// engine's q8 format) or per output row (s(n, k) = scale[n]), or fp32 (scale 1). HBM-bound on W: every weight byte is
+// read once (group scales add 4 bytes per 128).
 //
-// Reference: the engine's int8 `matvec` (engine/kernels.js:57-90; it quantizes per group of 128 inputs, this build
-// per output channel) and its MLP path with the neuron hook (`swiglu`, engine/kernels_qwen35.js:250-279: a[m, n] =
-// silu(gate) * up, then for each push of the layer whose neuron is n or every neuron, add or multiply by the push's
-// value for the row; the row index is clamped to 3).
+// Reference: the engine's int8 `matvec` (engine/kernels.js:57-90, q8 weights of engine/kernels.js:15-47) and its MLP
+// path with the neuron hook (`swiglu`, engine/kernels_qwen35.js:250-279: a[m, n] = silu(gate) * up, then for each
+// push of the layer whose neuron is n or every neuron, add or multiply by the push's value for the row; the row index
+// is clamped to 3).
 //
 // Layout: a block takes 16 output rows and NW = 4 or 8 waves. Lane (g, j) = (lane / 16, lane % 16) works on rows
 // g, g + 4, g + 8, g + 12 of the block and on input slot j of every K step: a K step is 16 slots of 16 weight bytes
@@ -13,7 +14,8 @@
 // from LDS, where x is staged once per block) serve the lane's four rows. The waves take the K steps round robin,
 // each with all of its weight loads in flight at once. Per-row sums: a 16-lane DPP row reduction, then across the
 // waves in LDS. Epilogues: store, accumulate into y (the residual add after down_proj), or SwiGLU over interleaved
-// (gate, up) row pairs with the neuron pushes applied (gate_up_proj).
+// (gate, up) row pairs with the neuron pushes applied (gate_up_proj). With group scales a lane's 16 weights of a K step
+// lie in one group (group 2 step + slot / 8), so the lane scales its partial sum of the step once.
 #include "q35_common.h"
 #include "q35hip.h"
 
@@ -63,7 +65,7 @@ __device__ __forceinline__ float row16_sum_f(float v) {
 
 // NORM: x is a residual row; the kernel adds xadd (may be NULL), writes the sum to xout from block 0 (may be NULL),
 // and multiplies the RMSNorm of the sum, s * rsqrt(mean s^2 + eps) * (1 + nw), instead of x (HF:720-734).
-template <typename TW, int MP, int EPI, int U, bool NORM>
+template <typename TW, int MP, int EPI, int U, bool NORM, bool GS>
 __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, int64_t ldx, const TW* __restrict__ W,
                                                    const float* __restrict__ wscale, float* __restrict__ y,
                                                    int64_t ldy, int M, int N, int K,
@@ -79,20 +81,30 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
   const int NW = blockDim.x >> 6;
   const int g = lane >> 4, j = lane & 15;
   const int n0 = blockIdx.x * 16;
+  static_assert(!GS || E == 16, "group scales are for int8 weights");
   const TW* wr[4];
+  const float* sr[4];  // GS: the lane's scale of step 0 in each of its rows (groups of 128 inputs: 2 per K step)
 #pragma unroll
-  for (int r = 0; r < 4; ++r) wr[r] = W + (size_t)min(n0 + g + 4 * r, N - 1) * K + j * E;
+  for (int r = 0; r < 4; ++r) {
+    const int nr = min(n0 + g + 4 * r, N - 1);
+    wr[r] = W + (size_t)nr * K + j * E;
+    sr[r] = GS ? wscale + (size_t)nr * (K >> 7) + (j >> 3) : nullptr;
+  }
   const int nsteps = K / KS;
   // this wave's K steps: wave, wave + NW, ...; U of them in flight per round. Loads complete in issue order, so the
   // thread's first x chunk (L2) is issued ahead of the first round of weights (HBM): the staging then waits for x
   // only, and its work overlaps the weights' flight
   WChunk<TW> wc[U][4];
+  float wsc[U][4];
   auto issue = [&](int s0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int st = min(s0 + u * NW, nsteps - 1);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) wc[u][r].load(wr[r] + st * KS);
+      for (int r = 0; r < 4; ++r) {
+        wc[u][r].load(wr[r] + st * KS);
+        if (GS) wsc[u][r] = sr[r][2 * st];
+      }
     }
   };
   // x (or, with NORM, s = x + xadd times (1 + nw)) into LDS; with NORM each wave also sums the squares of s per row
@@ -183,6 +195,11 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
       const int st = s0 + u * NW;
       if (st >= nsteps) break;
       const int k = st * KS + j * E;
+      float part[4][MP];  // GS: this step's sums, scaled once by the group's scale
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int m = 0; m < MP; ++m) part[r][m] = 0.f;
 #pragma unroll
       for (int c = 0; c < E; c += 4) {
         f32x4 xv[MP];
@@ -194,9 +211,18 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
           for (int r = 0; r < 4; ++r) {
             const float wv = wc[u][r].at(c + e);
 #pragma unroll
-            for (int m = 0; m < MP; ++m) acc[r][m] += wv * xv[m][e];
+            for (int m = 0; m < MP; ++m) {
+              if (GS) part[r][m] += wv * xv[m][e];
+              else acc[r][m] += wv * xv[m][e];
+            }
           }
         }
+      }
+      if (GS) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int m = 0; m < MP; ++m) acc[r][m] += wsc[u][r] * part[r][m];
       }
     }
   }
@@ -227,7 +253,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
       const int nn = n0 + rr;
       if (m < M && nn < N) {
         float v = rowsum(rr, m);
-        if (wscale) v *= wscale[nn];
+        if (wscale && !GS) v *= wscale[nn];
         float* dst = y + m * ldy + nn;
         *dst = EPI == kEpiAccumulate ? *dst + v : v;
       }
@@ -240,7 +266,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
       const int neuron = ng >> 1;
       if (m < M && ng + 1 < N) {
         float gt = rowsum(2 * qn, m), up = rowsum(2 * qn + 1, m);
-        if (wscale) { gt *= wscale[ng]; up *= wscale[ng + 1]; }
+        if (wscale && !GS) { gt *= wscale[ng]; up *= wscale[ng + 1]; }
         float a = gsilu(gt) * up;
         const int row = min(m / T, 3);
         for (int p = 0; p < npush; ++p) a = apply_push(pushes + p, neuron, row, a);
@@ -274,7 +300,7 @@ struct NormArgs {
   float* xout;
 };
 
-template <typename TW, int EPI, int U, bool NORM>
+template <typename TW, int EPI, int U, bool NORM, bool GS>
 void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
                    int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, int nw, const NormArgs& na,
                    hipStream_t st) {
@@ -283,8 +309,8 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
   const size_t lds = (size_t)mp * K * sizeof(float);
   const dim3 grid((unsigned)((N + 15) / 16)), block(64 * nw);
 #define Q35_GEMV(MP)                                                                                                 \
-  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM>), grid, block, lds, st, x, ldx, W, wscale, y, ldy, (int)M, \
-                     (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps, na.xout)
+  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS>), grid, block, lds, st, x, ldx, W, wscale, y, ldy,    \
+                     (int)M, (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps, na.xout)
   switch (mp) {
     case 1: Q35_GEMV(1); break;
     case 2: Q35_GEMV(2); break;
@@ -296,7 +322,7 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
 }
 
 // 4 waves when K has at most 4 steps, else 8; each wave's steps all in flight at once up to 4
-template <typename TW, int EPI, bool NORM>
+template <typename TW, int EPI, bool NORM, bool GS = false>
 int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
                 int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, const NormArgs& na,
                 hipStream_t st) {
@@ -305,11 +331,11 @@ int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, f
   const int nw = steps <= 4 ? 4 : 8;
   const int64_t per_wave = (steps + nw - 1) / nw;
   if (per_wave <= 1)
-    gemv_launch_u<TW, EPI, 1, NORM>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
+    gemv_launch_u<TW, EPI, 1, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
   else if (per_wave <= 2)
-    gemv_launch_u<TW, EPI, 2, NORM>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
+    gemv_launch_u<TW, EPI, 2, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
   else
-    gemv_launch_u<TW, EPI, 4, NORM>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
+    gemv_launch_u<TW, EPI, 4, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 
@@ -318,6 +344,12 @@ int gemv_dispatch(const float* x, int64_t ldx, const void* W, int w_dtype, const
                   int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int np,
                   int64_t T, const NormArgs& na, hipStream_t st) {
   using namespace q35;
+  if (w_dtype == Q35_I8_G128) {
+    const int8_t* w8 = (const int8_t*)W;
+    if (epilogue == kEpiStore) return gemv_launch<int8_t, kEpiStore, NORM, true>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+    if (epilogue == kEpiAccumulate) return gemv_launch<int8_t, kEpiAccumulate, NORM, true>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+    return gemv_launch<int8_t, kEpiSwiglu, NORM, true>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+  }
   if (w_dtype == Q35_I8) {
     const int8_t* w8 = (const int8_t*)W;
     if (epilogue == kEpiStore) return gemv_launch<int8_t, kEpiStore, NORM>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
@@ -331,14 +363,15 @@ int gemv_dispatch(const float* x, int64_t ldx, const void* W, int w_dtype, const
 }
 
 // argument checks shared by the two entry points
-int gemv_check(const float* x, int64_t ldx, const void* W, int w_dtype, float* y, int64_t ldy, int64_t M, int64_t N,
-               int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T) {
+int gemv_check(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
+               int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T) {
   using namespace q35;
   if (!x || !W || !y || M <= 0 || N <= 0 || K <= 0 || ldx < K || T <= 0) return Q35_EINVAL;
+  if (w_dtype == Q35_I8_G128 && !w_scale) return Q35_EINVAL;
   if (npush < 0 || (npush > 0 && !pushes)) return Q35_EINVAL;
   if (epilogue == kEpiSwiglu ? (N & 1) || ldy < N / 2 : ldy < N) return Q35_EINVAL;
   if (epilogue != kEpiStore && epilogue != kEpiAccumulate && epilogue != kEpiSwiglu) return Q35_EINVAL;
-  if (w_dtype != Q35_I8 && w_dtype != Q35_F32) return Q35_EUNSUPPORTED;
+  if (w_dtype != Q35_I8 && w_dtype != Q35_I8_G128 && w_dtype != Q35_F32) return Q35_EUNSUPPORTED;
   if (M > 8 || (K % 256) != 0 || (ldx & 3) || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return Q35_EUNSUPPORTED;
   const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 3 ? 3 : M <= 4 ? 4 : 8;
   if ((int64_t)mp * K * 4 > 64 * 1024 || N > 0x7fffffff || npush > 64) return Q35_EUNSUPPORTED;
@@ -349,7 +382,7 @@ int gemv_check(const float* x, int64_t ldx, const void* W, int w_dtype, float* y
 extern "C" int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y,
                         int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
                         int64_t npush, int64_t T, q35_stream_t stream) {
-  const int chk = gemv_check(x, ldx, W, w_dtype, y, ldy, M, N, K, epilogue, pushes, npush, T);
+  const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T);
   if (chk != Q35_OK) return chk;
   const NormArgs na = {nullptr, nullptr, 0.f, nullptr};
   return gemv_dispatch<false>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, (int)npush, T, na,
@@ -360,7 +393,7 @@ extern "C" int q35_gemv_norm(const float* x, const float* x_add, float* x_out, i
                              float eps, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
                              int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush,
                              int64_t T, q35_stream_t stream) {
-  const int chk = gemv_check(x, ldx, W, w_dtype, y, ldy, M, N, K, epilogue, pushes, npush, T);
+  const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T);
   if (chk != Q35_OK) return chk;
   if (!norm_w) return Q35_EINVAL;
   if (((uintptr_t)norm_w & 15) || (x_add && ((uintptr_t)x_add & 15)) || (x_out && ((uintptr_t)x_out & 15)))

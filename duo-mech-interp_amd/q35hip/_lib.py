@@ -22,9 +22,9 @@ EXPORTS = [
     "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm", "q35_gemm_q8",
 ]
 
-Q35_F32, Q35_BF16, Q35_I8 = 0, 1, 2
+Q35_F32, Q35_BF16, Q35_I8, Q35_I8_G128 = 0, 1, 2, 3
 Q35_ESCRATCH = 5
-ABI_VERSION = 6  # the signatures below; q35_abi_version() of the loaded library must match
+ABI_VERSION = 7  # the signatures below; q35_abi_version() of the loaded library must match
 
 _lib = None
 
@@ -60,7 +60,7 @@ _SIGS = {
     "q35_swiglu_push": ([P, P, I64, I64, P, I64, I64, P], I32),
     "q35_add_rmsnorm": ([P, I64, P, I64, P, P, I64, I64, I64, F32, P], I32),
     "q35_argmax_rows": ([P, I64, I64, I64, P, P, P], I32),
-    "q35_gemm_q8": ([P, I64, P, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
+    "q35_gemm_q8": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
     "q35_gemv_norm": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
 }
 

@@ -1,10 +1,12 @@
 """Qwen3.5 checkpoints from a local directory: the HF layout the engine streams (config.json plus one or more
 *.safetensors files, engine/model.js:21-23, :70-116, :153-280) turned into the weight dict of HybridModel.
 
-Every linear layer and the embedding are quantized to int8 on load, as the engine does (engine/model.js:3-5). The
-engine quantizes per group of 128 inputs (engine/kernels.js:15-47); this build quantizes per output row, the form its
-GEMVs read (q35hip.workloads.quantize_rows_int8). The quantized dict is cached on disk, like the engine's q8 cache in
-Cache Storage (engine/model.js:140, :280), so a second load reads int8 directly.
+Every linear layer and the embedding are quantized to int8 on load, as the engine does (engine/model.js:3-5), in the
+engine's format: one fp32 scale per group of 128 inputs of a row (engine/kernels.js:15-47,
+q35hip.workloads.quantize_groups_int8). A layer whose input width is not a multiple of 128 is refused, as the
+engine's _allocQ refuses it (engine/model.js:118-120); group=0 quantizes per output row instead. The quantized dict
+is cached on disk, like the engine's q8 cache in Cache Storage (engine/model.js:140, :280), so a second load reads
+int8 directly.
 
 Tensors are read with safetensors (no pickle). Names: the multimodal checkpoints keep the text decoder under
 "model.language_model." (engine/model.js:22), text-only ones under "model."; HF's per-layer names follow HF:426-429
@@ -18,10 +20,10 @@ import torch
 from safetensors import safe_open
 from safetensors.torch import save_file
 
-from .workloads import Q35Config, quantize_rows_int8
+from .workloads import QG, Q35Config, dequantize_int8, quantize_int8
 
 _PREFIXES = ("model.language_model.", "model.")
-_CACHE_VERSION = "q35-q8-rows-v1"
+_CACHE_VERSION = "q35-q8-v2"
 
 
 def config_from_hf(cfg):
@@ -83,10 +85,11 @@ def _layer_names(cfg, l):
     return [(f"layers.{l}.{k}", hp + n, kind) for k, n, kind in out]
 
 
-def _cache_key(path, shard_files, int8):
+def _cache_key(path, shard_files, int8, group):
     h = hashlib.sha1(_CACHE_VERSION.encode())
     h.update(os.path.abspath(path).encode())
     h.update(b"int8" if int8 else b"fp32")
+    h.update(f"group{group}".encode())
     for f in sorted(set(shard_files)):
         st = os.stat(f)
         h.update(f"{os.path.basename(f)}:{st.st_size}:{int(st.st_mtime)}".encode())
@@ -99,22 +102,22 @@ def _expand(W):
     for k in [k for k in W if k.endswith(".q")]:
         base = k[:-2]
         if not any(base.endswith(n) for n in ("gate_proj", "up_proj", "down_proj")):
-            W[base] = W[k].float() * W[base + ".s"][:, None]
+            W[base] = dequantize_int8(W[k], W[base + ".s"])
     return W
 
 
-def load_checkpoint(path, *, int8=True, cache_dir=None):
+def load_checkpoint(path, *, int8=True, cache_dir=None, group=QG):
     """(Q35Config, weight dict) of the Qwen3.5 checkpoint in directory `path`. int8: every linear and the embedding
-    int8 per output row with fp32 scales ("<name>.q", "<name>.s", plus the dequantised "<name>" except for the MLP);
-    otherwise fp32 throughout (the MLP still int8, the form the stack's MLP reads). cache_dir (default
-    <path>/.q35cache; None-able by passing False) keeps the quantized tensors for the next load."""
+    int8 with fp32 scales per group of `group` inputs, or per row with group 0 ("<name>.q", "<name>.s", plus the
+    dequantised "<name>" except for the MLP); otherwise fp32 throughout (the MLP still int8, the form the stack's MLP
+    reads). cache_dir (default <path>/.q35cache; False for none) keeps the quantized tensors for the next load."""
     cfg = config_from_hf(json.load(open(os.path.join(path, "config.json"))))
     shards = _shards(path)
     if cache_dir is None:
         cache_dir = os.path.join(path, ".q35cache")
     cache_file = None
     if cache_dir:
-        cache_file = os.path.join(cache_dir, _cache_key(path, shards.values(), int8) + ".safetensors")
+        cache_file = os.path.join(cache_dir, _cache_key(path, shards.values(), int8, group) + ".safetensors")
         if os.path.exists(cache_file):
             W = {}
             with safe_open(cache_file, framework="pt") as sf:
@@ -136,7 +139,7 @@ def load_checkpoint(path, *, int8=True, cache_dir=None):
 
     def put_linear(key, w, force_q=False):
         if int8 or force_q:
-            q, s = quantize_rows_int8(w)
+            q, s = quantize_int8(w, group)
             W[key + ".q"], W[key + ".s"] = q, s
         else:
             W[key] = w.contiguous()

@@ -14,10 +14,11 @@ States are caller-owned device tensors mutated in place, as the engine's buffers
 conv_state [B, K-1, C] fp32 (the last K-1 conv inputs, oldest first, engine/model.js:333), rec_state [B, Hv, dk, dv]
 fp32, k_cache / v_cache [B, Hkv, max_len, D] bf16 holding rotated keys and values by position.
 
-Any weight may also come as int8 rows with per-row scales ("<name>.q" / "<name>.s", "<name>" then holding the
-dequantised values), as the engine stores every linear (engine/model.js:3-5). The input projections are stacked into
-one weight per mixer (cached in p under "_in_fused", with "_in_fused.q" / ".s"). A projection over at most 8 rows
-(decode) is a HIP GEMV, on the int8 rows when present; over more rows a torch GEMM on the fp32 weight. Every other
+Any weight may also come as int8 with fp32 scales ("<name>.q" / "<name>.s", one scale per group of 128 inputs as the
+engine stores every linear, engine/model.js:3-5 and engine/kernels.js:15-47, or one per row; "<name>" then holds the
+dequantised values). The input projections are stacked into one weight per mixer (cached in p under "_in_fused", with
+"_in_fused.q" / ".s"). A projection over at most 8 rows (decode) is a HIP GEMV, over more rows the HIP int8 GEMM, on
+the int8 weights when present; without them a torch GEMM on the fp32 weight. Every other
 step is a HIP kernel: the GDN front end (causal conv + SiLU + gate terms), the delta rule, the gated RMSNorm,
 the attention front end (q/k norms, q/gate split, KV-cache update), the attention itself and the steering add.
 Nothing here falls back to a CPU path: the ops raise on CPU tensors and when the library is missing.
@@ -103,9 +104,9 @@ def prenorm_torch(x, prenorm):
 
 
 def linear(x, w, wq=None, ws=None, prenorm=None):
-    """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), on the int8 rows wq with per-row scales
-    ws when given (w = wq * ws, dequantised), else on w; for more rows the HIP int8 GEMM on wq (fp32-accurate) when
-    given, else a torch GEMM on w. prenorm = (x_add, norm_w, eps, x_out): x is a residual and the product takes the
+    """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), on the int8 weights wq with scales ws
+    ([N, K / 128] per group or [N] per row; w their dequantised values) when given, else on w; for more rows the HIP
+    int8 GEMM on wq (fp32-accurate) when given, else a torch GEMM on w. prenorm = (x_add, norm_w, eps, x_out): x is a residual and the product takes the
     RMSNorm (1 + norm_w) of x + x_add (x_add may be None), the sum being written to x_out when given (the decoder
     layer's add + norm, fused into the GEMV)."""
     K = x.shape[-1]

@@ -10,19 +10,21 @@ q35hip.layers; the model owns their states (GDN conv / recurrent states, bf16 KV
 import torch
 
 from . import layers, ops
+from .workloads import dequantize_int8
 
 
 class Q35Weights:
-    """Device copy of a weight dict: fp32 tensors as given; each int8 per-output-channel weight (keys "<name>.q" int8
-    [N, K] and "<name>.s" fp32 [N]) both kept as int8 + scales (for the decode GEMVs) and dequantised once to fp32
-    under "<name>" (for the prefill GEMMs and the embedding lookup)."""
+    """Device copy of a weight dict: fp32 tensors as given; each int8 weight (keys "<name>.q" int8 [N, K] and
+    "<name>.s" fp32 [N, K / 128] per group of 128 inputs, or [N] per row) both kept as int8 + scales (for the GEMVs
+    and GEMMs) and dequantised once to fp32 under "<name>" (for the embedding lookup and torch fallbacks of shapes the
+    kernels do not take)."""
 
     def __init__(self, W, device):
         self.t = {}
         for k, v in W.items():
             if k.endswith(".q"):
                 base = k[:-2]
-                self.t[base] = (v.float() * W[base + ".s"][:, None]).to(device)
+                self.t[base] = dequantize_int8(v, W[base + ".s"]).to(device)
                 self.t[k] = v.to(device).contiguous()
             elif k + ".q" not in W:  # a dequantised copy given beside its int8 form is rebuilt from the int8 above
                 self.t[k] = v.to(device)
@@ -44,7 +46,8 @@ def mlp_weights(p):
         if "gate_proj.q" in p:
             I, H = p["gate_proj.q"].shape
             p["_gu_q8"] = torch.stack([p["gate_proj.q"], p["up_proj.q"]], dim=1).reshape(2 * I, H).contiguous()
-            p["_gu_s"] = torch.stack([p["gate_proj.s"], p["up_proj.s"]], dim=1).reshape(2 * I).contiguous()
+            gs = p["gate_proj.s"]
+            p["_gu_s"] = torch.stack([gs, p["up_proj.s"]], dim=1).reshape(2 * I, *gs.shape[1:]).contiguous()
         p["_pushes"] = torch.tensor([_NO_PUSH] * MAX_PUSHES, dtype=torch.int32, device=p["_gu"].device)
     return p
 

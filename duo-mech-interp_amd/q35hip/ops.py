@@ -17,7 +17,7 @@ import math
 import torch
 
 from . import _lib
-from ._lib import Q35_BF16, Q35_F32, Q35Error, check
+from ._lib import Q35_BF16, Q35_F32, Q35_I8, Q35_I8_G128, Q35Error, check
 
 _DT = {torch.float32: Q35_F32, torch.bfloat16: Q35_BF16}
 
@@ -350,6 +350,23 @@ def _pushes_check(pushes):
     return pushes.shape[0]
 
 
+def _weight_format(W, w_scale, N, K):
+    """The C ABI's weight format code of (W, w_scale): fp32 W (no scale) -> Q35_F32; int8 W with w_scale [N] fp32 ->
+    Q35_I8 (one scale per output row); int8 W with w_scale [N, K / 128] fp32 -> Q35_I8_G128 (one scale per group of
+    128 inputs, the engine's q8 format)."""
+    if W.dtype == torch.float32:
+        _require(w_scale is None, "fp32 W takes no w_scale")
+        return Q35_F32
+    _require(w_scale is not None and w_scale.dtype == torch.float32 and w_scale.is_contiguous(),
+             "int8 W needs a contiguous fp32 w_scale")
+    if w_scale.dim() == 2:
+        _require(K % 128 == 0 and tuple(w_scale.shape) == (N, K // 128),
+                 "group scales: w_scale [N, K / 128] fp32 (K a multiple of 128)")
+        return Q35_I8_G128
+    _require(w_scale.dim() == 1 and w_scale.numel() == N, "per-row scales: w_scale [N] fp32")
+    return Q35_I8
+
+
 def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T):
     _on_gpu(x, W, w_scale, y, pushes)
     _require(x.dtype == torch.float32 and x.dim() == 2 and y.dtype == torch.float32 and y.dim() == 2,
@@ -359,12 +376,10 @@ def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T):
     N = W.shape[0]
     _require(W.shape[1] == K and y.shape[0] == M, "x, W, y shapes disagree")
     _require(y.shape[1] == (N // 2 if epilogue == 2 else N), "y: [M, N] ([M, N / 2] for the SwiGLU epilogue)")
-    if W.dtype == torch.int8:
-        _require(w_scale is not None and w_scale.dtype == torch.float32 and w_scale.numel() == N,
-                 "int8 W needs w_scale [N] fp32")
+    fmt = _weight_format(W, w_scale, N, K)
     npush = _pushes_check(pushes)
-    st = _lib.lib().q35_gemv(_ptr(x), K, _ptr(W), 2 if W.dtype == torch.int8 else Q35_F32, _ptr(w_scale), _ptr(y),
-                             y.shape[1], M, N, K, int(epilogue), _ptr(pushes), npush, int(T), _stream(x))
+    st = _lib.lib().q35_gemv(_ptr(x), K, _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.shape[1], M, N, K, int(epilogue),
+                             _ptr(pushes), npush, int(T), _stream(x))
     check(st, "q35_gemv")
 
 
@@ -378,10 +393,10 @@ def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T):
     N = W.shape[0]
     _require(W.shape[1] == K and y.shape[0] == M, "x, W, y shapes disagree")
     _require(y.shape[1] == (N // 2 if epilogue == 2 else N), "y: [M, N] ([M, N / 2] for the SwiGLU epilogue)")
-    _require(w_scale.dtype == torch.float32 and w_scale.numel() == N, "w_scale: [N] fp32")
+    fmt = _weight_format(W, w_scale, N, K)
     _require(K % 64 == 0, "K must be a multiple of 64")
     npush = _pushes_check(pushes)
-    st = _lib.lib().q35_gemm_q8(_ptr(x), x.stride(0), _ptr(W), _ptr(w_scale), _ptr(y), y.stride(0), M, N, K,
+    st = _lib.lib().q35_gemm_q8(_ptr(x), x.stride(0), _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.stride(0), M, N, K,
                                 int(epilogue), _ptr(pushes), npush, int(T), _stream(x))
     check(st, "q35_gemm_q8")
 
@@ -398,12 +413,10 @@ def _gemv_norm_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, epilogue, pushe
     _require(W.dim() == 2 and W.dtype in (torch.int8, torch.float32) and W.shape[1] == K, "W: [N, K] int8 or fp32")
     N = W.shape[0]
     _require(y.shape[0] == M and y.shape[1] == (N // 2 if epilogue == 2 else N), "y: [M, N] ([M, N / 2] SwiGLU)")
-    if W.dtype == torch.int8:
-        _require(w_scale is not None and w_scale.dtype == torch.float32 and w_scale.numel() == N,
-                 "int8 W needs w_scale [N] fp32")
+    fmt = _weight_format(W, w_scale, N, K)
     st = _lib.lib().q35_gemv_norm(_ptr(x), _ptr(x_add), _ptr(x_out), x.stride(0), _ptr(norm_w), float(eps), _ptr(W),
-                                  2 if W.dtype == torch.int8 else Q35_F32, _ptr(w_scale), _ptr(y), y.shape[1], M, N, K,
-                                  int(epilogue), _ptr(pushes), _pushes_check(pushes), int(T), _stream(x))
+                                  fmt, _ptr(w_scale), _ptr(y), y.shape[1], M, N, K, int(epilogue), _ptr(pushes),
+                                  _pushes_check(pushes), int(T), _stream(x))
     check(st, "q35_gemv_norm")
 
 
@@ -639,7 +652,8 @@ def pack_pushes(pushes, device):
 
 
 def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, prenorm=None):
-    """y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k] for M <= 8 rows (decode): W int8 with per-row scales or fp32.
+    """y[m, n] = sum_k x[m, k] W[n, k] s(n, k) for M <= 8 rows (decode): W int8 with scales w_scale [N, K / 128]
+    (one per group of 128 inputs, the engine's q8 format) or [N] (one per row), or fp32 W (w_scale None).
     epilogue "store" writes out, "add" accumulates into out (a residual add), "swiglu" treats W's rows as
     interleaved (gate, up) pairs and writes silu(gate) * up with the neuron pushes (pack_pushes) applied.
     prenorm = (x_add, norm_w, eps, x_out): x is then a residual; the product takes the RMSNorm (1 + w) of
@@ -657,8 +671,9 @@ def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, preno
 
 
 def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1):
-    """y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k] over many rows (the prefill projections): x [M, K] fp32, W [N, K]
-    int8, K a multiple of 64; fp32-accurate (bf16 MFMA on a hi + lo split of x). epilogue "store" writes out, "add"
+    """y[m, n] = sum_k x[m, k] W[n, k] s(n, k) over many rows (the prefill projections): x [M, K] fp32, W [N, K]
+    int8 with scales w_scale [N, K / 128] (per group of 128 inputs) or [N] (per row), K a multiple of 64 (128 with
+    group scales); fp32-accurate (bf16 MFMA on a hi + lo split of x). epilogue "store" writes out, "add"
     accumulates into out, "swiglu" treats W's rows as interleaved (gate, up) pairs and writes
     silu(gate) * up with the neuron pushes (pack_pushes) applied, out [M, N / 2]. Returns out."""
     e = _EPI[epilogue]

@@ -6,7 +6,7 @@
                    gate [T, 8 * 256].
   attn_decode:     B in {3, 32}, context 8192, same heads, bf16 KV cache, one query per row, split-K.
   hybrid stack:    Qwen3.5-0.8B shape (Q35Config), seeded random weights (init_weights), every linear and the
-                   tied embedding int8 per output channel as the engine quantizes them.
+                   tied embedding int8 with one scale per group of 128 inputs, as the engine quantizes them.
 q and k are L2-normalised per head, beta = sigmoid(randn), g = -softplus(randn) (log decay, alpha = exp(g)).
 """
 from dataclasses import dataclass
@@ -111,13 +111,44 @@ def quantize_rows_int8(w):
     return q, s.squeeze(1).float()
 
 
-def init_weights(cfg: Q35Config, seed=0, int8_all=True):
+QG = 128  # inputs per quantization group (engine/kernels.js:5)
+
+
+def quantize_groups_int8(w, group=QG):
+    """The engine's q8 format (engine/kernels.js:15-47 `quantize`): symmetric int8 with one fp32 scale per group of
+    `group` consecutive inputs of a row, s = max|w_group| / 127 (1 for an all-zero group), q = round(w / s) (round
+    half to even, as WGSL round and torch.round). w [N, K], K a multiple of group -> (q [N, K] int8, s [N, K / group])."""
+    N, K = w.shape
+    if K % group:
+        raise ValueError(f"{K} inputs are not a multiple of the quantization group {group}")
+    wg = w.float().reshape(N, K // group, group)
+    m = wg.abs().amax(dim=2)
+    s = torch.where(m == 0, torch.ones_like(m), m / 127.0)
+    q = torch.round(wg / s[:, :, None]).clamp(-127, 127).to(torch.int8).reshape(N, K)
+    return q, s.float()
+
+
+def quantize_int8(w, group=QG):
+    """int8 weights of w: per group of `group` inputs (the engine's format), or per output row when group is 0."""
+    return quantize_groups_int8(w, group) if group else quantize_rows_int8(w)
+
+
+def dequantize_int8(q, s):
+    """fp32 values of int8 q [N, K] with scales s [N] (per row) or [N, K / g] (per group of g inputs)."""
+    if s.dim() == 1:
+        return q.float() * s.float()[:, None]
+    N, K = q.shape
+    return (q.float().reshape(N, s.shape[1], -1) * s.float()[:, :, None]).reshape(N, K)
+
+
+def init_weights(cfg: Q35Config, seed=0, int8_all=True, group=QG):
     """Deterministic random init (seeded): normal(0, init_std) for every linear, the conv and the tied embedding;
     decoder / q / k RMSNorm weights 0 (gain 1 + w = 1) and the gated norm weight 1 (HF:171, HF:813-820);
     dt_bias = 1; A_log = log U(0, 16).
 
-    Every linear layer and the tied embedding are int8 per output row with fp32 scales, as the engine quantizes the
-    checkpoint on load (engine/model.js:3-5, :70-100). MLP weights are stored as "<name>.q" / "<name>.s" only; the
+    Every linear layer and the tied embedding are int8 with fp32 scales, as the engine quantizes the checkpoint on
+    load (engine/model.js:3-5, :70-100): one scale per group of `group` inputs (the engine's 128), or per output row
+    with group 0. MLP weights are stored as "<name>.q" / "<name>.s" only; the
     other linears and the embedding (int8_all) keep "<name>.q" / "<name>.s" beside "<name>" = the dequantised fp32
     values, so a consumer that reads "<name>" (the CPU oracle, torch GEMMs) computes with exactly the numbers the int8
     decode GEMVs use."""
@@ -129,9 +160,9 @@ def init_weights(cfg: Q35Config, seed=0, int8_all=True):
 
     def put(W, key, w):
         if int8_all:
-            q, s = quantize_rows_int8(w)
+            q, s = quantize_int8(w, group)
             W[key + ".q"], W[key + ".s"] = q, s
-            w = q.float() * s[:, None]
+            w = dequantize_int8(q, s)
         W[key] = w
 
     H = cfg.hidden
@@ -160,7 +191,7 @@ def init_weights(cfg: Q35Config, seed=0, int8_all=True):
             W[p + "norm"] = torch.ones(cfg.lin_dv)
             put(W, p + "out_proj", lin(H, vd))
         for name, (o, i) in (("gate_proj", (cfg.inter, H)), ("up_proj", (cfg.inter, H)), ("down_proj", (H, cfg.inter))):
-            q, s = quantize_rows_int8(lin(o, i))
+            q, s = quantize_int8(lin(o, i), group)
             W[p + name + ".q"] = q
             W[p + name + ".s"] = s
     return W

@@ -25,9 +25,9 @@
  *                            q35_gated_rmsnorm in one launch; engine/kernels_qwen35.js:127-247
  *   q35_attn_prep            HF:667-680 (q / gate split, q_norm / k_norm, partial RoPE of k, cache update);
  *                            engine/kernels_qwen35.js:18-69 `attnPrep`
- *   q35_gemv                 engine/kernels.js:57-90 `matvec` (int8 weights; per output channel here) and, with the
- *                            SwiGLU epilogue, engine/kernels_qwen35.js:250-279 `swiglu` with the neuron pushes;
- *                            HF:704-717 Qwen3_5MLP for the decode step
+ *   q35_gemv                 engine/kernels.js:57-90 `matvec` (int8 weights per 128-input group, or per row)
+ *                            and, with the SwiGLU epilogue, engine/kernels_qwen35.js:250-279 `swiglu` with the
+ *                            neuron pushes; HF:704-717 Qwen3_5MLP for the decode step
  *   q35_gemv_norm            q35_gemv behind the layer's residual add + RMSNorm (HF:753-793, :720-734;
  *                            engine/kernels.js:226-246 `addInto` + `rmsnorm` ahead of the matvec)
  *   q35_swiglu_push          engine/kernels_qwen35.js:250-279 `swiglu` over a [gate | up] projection (prefill form)
@@ -59,7 +59,10 @@ enum q35_status {
   Q35_ESCRATCH = 5      /* an allocation-free entry point's fixed scratch is too small for the request */
 };
 
-enum q35_dtype { Q35_F32 = 0, Q35_BF16 = 1, Q35_I8 = 2 };
+/* Weight formats of the GEMV / GEMM entry points: Q35_I8 is int8 with one fp32 scale per output row (w_scale [N]);
+ * Q35_I8_G128 is the engine's q8 format, int8 with one fp32 scale per group of 128 consecutive inputs of a row
+ * (w_scale [N, K / 128] row-major; engine/kernels.js:1-5, :15-47). */
+enum q35_dtype { Q35_F32 = 0, Q35_BF16 = 1, Q35_I8 = 2, Q35_I8_G128 = 3 };
 
 /* One neuron push of the MLP hook (engine/model.js:8, :412-423): neuron -1 applies to every neuron of the layer;
  * mode 0 adds vals[row], mode 1 multiplies by it; row = min(m / T, 3) for input row m of a call with T tokens per
@@ -260,9 +263,10 @@ int q35_add_rmsnorm(float* x, int64_t ldx, const float* y, int64_t ldy, const fl
                     int64_t M, int64_t H, float eps, q35_stream_t stream);
 
 /*
- * Small-M matrix-vector product for the decode step: y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k], m < M <= 8.
- *   x: [M, ldx] fp32 (16-byte aligned, ldx a multiple of 4); W: [N, K] row-major, w_dtype Q35_I8 (int8, with
- *   w_scale [N] fp32) or Q35_F32 (w_scale NULL for 1); K a multiple of 256, M * K * 4 <= 64 KiB.
+ * Small-M matrix-vector product for the decode step: y[m, n] = sum_k x[m, k] W[n, k] s(n, k), m < M <= 8, with
+ * s(n, k) = w_scale[n] for Q35_I8, w_scale[n, k / 128] for Q35_I8_G128, 1 for Q35_F32 (w_scale NULL).
+ *   x: [M, ldx] fp32 (16-byte aligned, ldx a multiple of 4); W: [N, K] row-major int8 or fp32 (w_dtype);
+ *   K a multiple of 256, M * K * 4 <= 64 KiB.
  *   epilogue 0: y[m, n] = v; 1: y[m, n] += v (a residual add); 2: SwiGLU over interleaved row pairs (row 2 j the
  *   gate, row 2 j + 1 the up projection of neuron j): y[m, j] = silu(v_2j) * v_2j+1, then the pushes in order.
  *   y: [M, ldy] fp32 (ldy >= N, or >= N / 2 for epilogue 2). pushes: npush <= 64 records on the device (or NULL
@@ -284,19 +288,20 @@ int q35_gemv_norm(const float* x, const float* x_add, float* x_out, int64_t ldx,
                   int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream);
 
 /*
- * Many-row int8 GEMM for the prefill projections: y[m, n] = w_scale[n] * sum_k x[m, k] W[n, k]. Replaces the
- * engine's int8 `matmul` (engine/kernels.js:97-151, used when M > 32) and, with the SwiGLU epilogue, its `swiglu`
- * with the neuron pushes (engine/kernels_qwen35.js:250-279); HF:704-717 and the mixers' projections in fp32.
+ * Many-row int8 GEMM for the prefill projections: y[m, n] = sum_k x[m, k] W[n, k] s(n, k), s as for q35_gemv
+ * (w_dtype Q35_I8: w_scale [N]; Q35_I8_G128: w_scale [N, K / 128], K a multiple of 128). Replaces the engine's int8
+ * `matmul` (engine/kernels.js:97-151, used when M > 32) and, with the SwiGLU epilogue, its `swiglu` with the neuron
+ * pushes (engine/kernels_qwen35.js:250-279); HF:704-717 and the mixers' projections in fp32.
  *   x: [M, ldx] fp32 (16-byte aligned, ldx a multiple of 4); W: [N, K] int8 row-major (16-byte aligned), K a multiple
- *   of 64; w_scale: [N] fp32; y: [M, ldy] fp32. fp32-accurate: bf16 MFMA products of W (exact in bf16) with a hi + lo
- *   split of x (relative error about 1e-5).
+ *   of 64; y: [M, ldy] fp32. fp32-accurate: bf16 MFMA products of W (exact in bf16) with a hi + lo split of x
+ *   (relative error about 1e-5); with group scales each group's partial product is scaled in fp32.
  *   epilogue 0: y = v; 1: y += v; 2: SwiGLU over interleaved row pairs (row 2 j gate, 2 j + 1 up of neuron j):
  *   y[m, j] = silu(v_2j) * v_2j+1 then the pushes in order (N even, ldy >= N / 2). pushes, npush <= 64 and T as
  *   for q35_gemv.
  */
-int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
-                int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T,
-                q35_stream_t stream);
+int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
+                int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush,
+                int64_t T, q35_stream_t stream);
 
 /*
  * a[m, n] = silu(gu[m, n]) * gu[m, I + n] with the pushes applied, gu: [M, 2 I] fp32 ([gate | up] per row),

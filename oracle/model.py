@@ -7,8 +7,8 @@ Restates the layer compositions that the reference's PyTorch mirror (tests/engin
   causal_conv          HF:199-239 depthwise causal conv (kernel 4) with carried state, then SiLU
   gdn_layer            HF:432-543 (in_proj_qkv / z / b / a, conv, split, beta, g, delta rule, gated norm, out_proj)
   attn_layer           HF:656-701 (q/gate interleave per head, q/k norm, partial RoPE, causal GQA, sigmoid gate)
-  mlp                  HF:704-717 SwiGLU, here with int8 per-output-channel weights (dequantised identically on
-                       the GPU path)
+  mlp                  HF:704-717 SwiGLU, here with int8 weights (per 128-input group or per row, dequantised
+                       identically on the GPU path)
   decoder layer        HF:753-793 (pre-norm mixer + residual, pre-norm MLP + residual), plus the residual steering
                        add after one layer at every position (tests/engine_ref.py:49-53, engine/model.js:460)
   median residual norm engine/analysis.js:52-77 (median over tokens 1..T-1 of |x| after the layer)
@@ -24,10 +24,11 @@ import torch.nn.functional as F
 
 from .attention import apply_partial_rope, rope_inv_freq, rope_tables
 from .gdn import chunk_gated_delta_rule, recurrent_gated_delta_rule
+from .mlp import q8_dequant
 
 
 def dequant(W, key):
-    return W[key + ".q"].float() * W[key + ".s"][:, None]
+    return q8_dequant(W[key + ".q"], W[key + ".s"])
 
 
 # ------------------------------------------------------------------ pieces

@@ -16,7 +16,8 @@ def tiny_config():
 def tiny_weights(cfg):
     """init_weights(seed 1) with random norm gains (seed 2): the decoder / q / k RMSNorms use (1 + w), the gated
     norm plain w, and both must show up in the outputs."""
-    W = init_weights(cfg, seed=1, int8_all=False)  # the weights the golden vectors were written with
+    # the weights the golden vectors were written with: fp32 mixers, MLP int8 with one scale per row
+    W = init_weights(cfg, seed=1, int8_all=False, group=0)
     g = torch.Generator().manual_seed(2)
     for k in sorted(W):
         if k.endswith("layernorm") or k.endswith("q_norm") or k.endswith("k_norm") or k == "norm":

@@ -39,7 +39,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 6
+    assert L.q35_abi_version() == 7
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -116,6 +116,12 @@ def test_validation_rejects_without_launching():
     assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 9, 64, 1024, 0, None, 0, 1, None) == 2
     assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 63, 1024, 2, None, 0, 1, None) == 1
     assert L.q35_gemv(fake, 1024, fake, 1, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1, None) == 2
+    # group-128 int8 weights need their scales
+    assert L.q35_gemv(fake, 1024, fake, 3, None, fake, 64, 3, 64, 1024, 0, None, 0, 1, None) == 1
+    # prefill GEMM: weight formats other than int8, group scales over K not a multiple of 128, no scales
+    assert L.q35_gemm_q8(fake, 1024, fake, 1, fake, fake, 64, 100, 64, 1024, 0, None, 0, 1, None) == 2
+    assert L.q35_gemm_q8(fake, 192, fake, 3, fake, fake, 64, 100, 64, 192, 0, None, 0, 1, None) == 2
+    assert L.q35_gemm_q8(fake, 1024, fake, 3, None, fake, 64, 100, 64, 1024, 0, None, 0, 1, None) == 1
     assert L.q35_swiglu_push(fake, fake, 3, 64, None, 2, 1, None) == 1
     assert L.q35_add_rmsnorm(fake, 1024, None, 0, fake, fake, 1024, 3, 1022, 1e-6, None) == 2
     assert L.q35_add_rmsnorm(fake, 512, None, 0, fake, fake, 1024, 3, 1024, 1e-6, None) == 1

@@ -10,7 +10,7 @@ from safetensors.torch import save_file
 
 from oracle import model as om
 from q35hip import checkpoint as ck
-from q35hip.workloads import Q35Config, quantize_rows_int8
+from q35hip.workloads import Q35Config, quantize_groups_int8, quantize_rows_int8
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "golden"))
@@ -100,7 +100,7 @@ def test_load_fp32_matches_the_bf16_tensors(tmp_path):
     assert torch.equal(W[p + "in_proj_qkv"], sd[PREFIX + p + "linear_attn.in_proj_qkv.weight"].float())
     assert tuple(W[p + "conv1d"].shape) == (W0[p + "conv1d"].shape[0], cfg.conv_k)
     assert torch.equal(W[p + "conv1d"], _bf(W0[p + "conv1d"]))
-    q, s = quantize_rows_int8(sd[PREFIX + p + "mlp.down_proj.weight"].float())
+    q, s = quantize_groups_int8(sd[PREFIX + p + "mlp.down_proj.weight"].float())
     assert torch.equal(W[p + "down_proj.q"], q) and torch.equal(W[p + "down_proj.s"], s)
     l_att = next(l for l in range(cfg.layers) if cfg.is_attention(l))
     assert torch.equal(W[f"layers.{l_att}.q_norm"], _bf(W0[f"layers.{l_att}.q_norm"]))
@@ -119,11 +119,19 @@ def test_load_int8_sharded_and_cached_gives_one_dict(tmp_path):
     for k in Wa:
         assert torch.equal(Wa[k], Wb[k]) and torch.equal(Wb[k], Wc[k]), k
     p = "layers.0."
-    q, s = quantize_rows_int8(sd[PREFIX + p + "linear_attn.out_proj.weight"].float())
+    w = sd[PREFIX + p + "linear_attn.out_proj.weight"].float()
+    q, s = quantize_groups_int8(w)                                   # the engine's q8: a scale per 128 inputs
     assert torch.equal(Wa[p + "out_proj.q"], q) and torch.equal(Wa[p + "out_proj.s"], s)
-    assert torch.equal(Wa[p + "out_proj"], q.float() * s[:, None])   # the dequantised copy beside it
+    assert tuple(s.shape) == (w.shape[0], w.shape[1] // 128)
+    exp = (q.float().reshape(w.shape[0], -1, 128) * s[:, :, None]).reshape(w.shape)
+    assert torch.equal(Wa[p + "out_proj"], exp)                       # the dequantised copy beside it
     assert "layers.0.gate_proj" not in Wa                            # the MLP stays int8 only
     assert Wa["embed.q"].dtype == torch.int8
+    # per-row scales on request, cached apart from the per-group form
+    _, Wr = ck.load_checkpoint(str(tmp_path / "three"), group=0)
+    q, s = quantize_rows_int8(w)
+    assert torch.equal(Wr[p + "out_proj.q"], q) and torch.equal(Wr[p + "out_proj.s"], s)
+    assert len(os.listdir(str(tmp_path / "three" / ".q35cache"))) == 2
 
 
 def test_oracle_runs_the_loaded_checkpoint(tmp_path):
@@ -140,7 +148,7 @@ def test_oracle_runs_the_loaded_checkpoint(tmp_path):
     for l in range(cfg.layers):
         for n in ("gate_proj", "up_proj", "down_proj"):
             b = f"layers.{l}.{n}"
-            q, s = quantize_rows_int8(_bf(W0[b + ".q"].float() * W0[b + ".s"][:, None]))
+            q, s = quantize_groups_int8(_bf(W0[b + ".q"].float() * W0[b + ".s"][:, None]))
             Wr[b + ".q"], Wr[b + ".s"] = q, s
     ids, _ = tiny_inputs(cfg)
     la, _ = om.OracleModel(c2, W).forward(ids[:, :20])

@@ -69,3 +69,45 @@ def test_gemm_q8_swiglu_with_pushes(M, T):
     e = oracle.rel_err(a.cpu(), ref)
     print(f"gemm_q8 swiglu M{M}: rel err {e:.2e}")
     assert e <= TOL
+
+
+def _q8g(N, K, seed):
+    """The engine's q8 format: one scale per group of 128 inputs of a row (oracle.mlp.q8_quantize)."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * 0.02 * (1.0 + 9.0 * (torch.arange(K) // 128 % 2))[None, :]
+    return omlp.q8_quantize(w)
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 8224, 1024), (300, 130, 128), (2048, 5120, 1024), (1500, 1024, 3584),
+                                   (6144, 1024, 2048)])
+def test_gemm_q8_group_scales_store_and_accumulate(M, N, K):
+    """Q35_I8_G128 weights (scales of neighbouring groups about a decade apart) against the oracle's per-group
+    product, 64- and 128-row tiles."""
+    dev = device()
+    q, s = _q8g(N, K, M + N)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(K)) * 3.0
+    ref = omlp.q8_linear(x, q, s)
+    announce(f"gemm_q8 g128 M{M} N{N} K{K}")
+    y = ops.gemm_q8(x.to(dev), q.to(dev), s.to(dev))
+    e = oracle.rel_err(y.cpu(), ref)
+    print(f"gemm_q8 g128 M{M} N{N} K{K}: rel err {e:.2e}")
+    assert e <= TOL
+    base = torch.randn(M, N)
+    out = base.to(dev)
+    ops.gemm_q8(x.to(dev), q.to(dev), s.to(dev), out=out, epilogue="add")
+    assert oracle.rel_err(out.cpu() - base, ref) <= TOL
+
+
+def test_gemm_q8_group_scales_swiglu_with_pushes():
+    dev = device()
+    I, H, M, T = 3584, 1024, 2048, 2048
+    qg, sg = _q8g(I, H, 31)
+    qu, su = _q8g(I, H, 32)
+    q = torch.stack([qg, qu], dim=1).reshape(2 * I, H).contiguous()
+    s = torch.stack([sg, su], dim=1).reshape(2 * I, H // 128).contiguous()
+    x = torch.randn(M, H, generator=torch.Generator().manual_seed(33))
+    pushes = [(11, "mul", [2.0]), (None, "add", [0.5])]
+    ref = omlp.swiglu_push(omlp.q8_linear(x, qg, sg), omlp.q8_linear(x, qu, su), pushes, T=T)
+    announce("gemm_q8 g128 swiglu")
+    a = ops.gemm_q8(x.to(dev), q.to(dev), s.to(dev), epilogue="swiglu", pushes=ops.pack_pushes(pushes, dev), T=T)
+    assert oracle.rel_err(a.cpu(), ref) <= TOL

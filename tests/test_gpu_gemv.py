@@ -116,3 +116,57 @@ def test_gemv_with_fused_residual_add_and_rmsnorm(epilogue, with_add, with_out):
     assert torch.equal(xd.cpu(), x)  # the residual itself is only read
     if with_out:
         assert oracle.rel_err(xo.cpu(), ssum) <= 1e-7
+
+
+def _weights_g128(N, K, seed):
+    """int8 weights with one scale per group of 128 inputs (the engine's q8 format), the scales of neighbouring groups
+    a decade apart so that a scale applied to the wrong group shows."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    s = torch.rand(N, K // 128, generator=g) * 0.01 * (10.0 ** (torch.arange(K // 128) % 2))[None, :]
+    return q, s
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8224, 1024), (3, 1024, 3584), (3, 1024, 2048), (8, 1000, 2048),
+                                   (2, 4096, 4352)])
+def test_gemv_group_scales_store_add_and_norm(M, N, K):
+    """Q35_I8_G128 weights: store, accumulate, and the fused residual add + RMSNorm prologue, against the oracle's
+    per-group dequantised product (K 4352 takes the four-steps-per-wave form)."""
+    dev = device()
+    W, s = _weights_g128(N, K, seed=N + K)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M))
+    ref = omlp.q8_linear(x, W, s)
+    announce(f"gemv g128 M{M} N{N} K{K}")
+    Wd, sd, xd = W.to(dev), s.to(dev), x.to(dev)
+    y = ops.gemv(xd, Wd, sd)
+    base = torch.randn(M, N, generator=torch.Generator().manual_seed(9))
+    acc = base.to(dev)
+    ops.gemv(xd, Wd, sd, out=acc, epilogue="add")
+    xa = torch.randn(M, K, generator=torch.Generator().manual_seed(10))
+    nw = torch.randn(K, generator=torch.Generator().manual_seed(11)) * 0.1
+    xs = torch.empty(M, K, device=dev)
+    yn = ops.gemv(xd, Wd, sd, prenorm=(xa.to(dev), nw.to(dev), 1e-6, xs))
+    hs = x + xa
+    hn = hs * torch.rsqrt(hs.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + nw)
+    torch.cuda.synchronize()
+    assert oracle.rel_err(y.cpu(), ref) <= TOL
+    assert oracle.rel_err(acc.cpu(), base + ref) <= TOL
+    assert oracle.rel_err(yn.cpu(), omlp.q8_linear(hn, W, s)) <= TOL
+    assert torch.equal(xs.cpu(), hs)
+
+
+def test_gemv_group_scales_swiglu_with_pushes():
+    """Interleaved (gate, up) rows with interleaved group scales through the SwiGLU + push epilogue."""
+    dev = device()
+    I, H, M = 3584, 1024, 3
+    Wg, sg = _weights_g128(I, H, 21)
+    Wu, su = _weights_g128(I, H, 22)
+    x = torch.randn(M, H, generator=torch.Generator().manual_seed(23))
+    pushes = [(5, "add", [1.0, -1.0, 2.0]), (None, "mul", [1.0, 0.5, 2.0])]
+    ref = omlp.swiglu_push(omlp.q8_linear(x, Wg, sg), omlp.q8_linear(x, Wu, su), pushes, T=1)
+    Wi = torch.stack([Wg, Wu], dim=1).reshape(2 * I, H)
+    si = torch.stack([sg, su], dim=1).reshape(2 * I, H // 128)
+    announce("gemv g128 swiglu")
+    a = ops.gemv(x.to(dev), Wi.to(dev), si.to(dev), epilogue="swiglu", pushes=ops.pack_pushes(pushes, dev))
+    torch.cuda.synchronize()
+    assert oracle.rel_err(a.cpu(), ref) <= TOL

@@ -38,3 +38,39 @@ def test_push_semantics_by_hand():
     # the row index is clamped to 3
     a = omlp.swiglu_push(torch.zeros(6, 1), torch.ones(6, 1), [(0, "add", [0.0, 1.0, 2.0, 3.0])], T=1)
     assert a[:, 0].tolist() == [0.0, 1.0, 2.0, 3.0, 3.0, 3.0]
+
+
+def test_q8_quantize_closed_forms():
+    """engine/kernels.js:15-47: a zero group gets scale 1 and zeros; a group holding integer multiples of c with
+    max 127 c is reproduced exactly (scale c); a value at half a step rounds to the even neighbour."""
+    N, K = 3, 256
+    w = torch.zeros(N, K)
+    c = 0.01
+    w[1, 128:] = c * torch.arange(-127, 129)[:128].float().clamp(-127, 127)  # integer multiples, |max| 127 c
+    w[2, :128] = torch.tensor([127.0] + [2.5] * 127)                      # scale 1: 2.5 -> 2 (half to even)
+    q, s = omlp.q8_quantize(w)
+    assert s.shape == (N, 2)
+    assert s[0].tolist() == [1.0, 1.0] and int(q[0].abs().max()) == 0
+    assert torch.allclose(s[1, 1], torch.tensor(c)) and torch.equal(q[1, 128:].float(), torch.round(w[1, 128:] / c))
+    assert float(s[2, 0]) == 1.0 and q[2, 0] == 127 and bool((q[2, 1:128] == 2).all())
+
+
+def test_q8_group_linear_matches_a_loop_over_groups():
+    """q8_linear with group scales equals the sum over groups of (x_g . q_g) s_g, and the product quantizer is the
+    oracle's restatement."""
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(5, 384, generator=g) * 0.05
+    q, s = omlp.q8_quantize(w)
+    from q35hip.workloads import quantize_groups_int8
+    q2, s2 = quantize_groups_int8(w)
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+    x = torch.randn(4, 384, generator=g, dtype=torch.float64)
+    ref = torch.zeros(4, 5, dtype=torch.float64)
+    for n in range(5):
+        for gi in range(3):
+            ref[:, n] += (x[:, 128 * gi:128 * gi + 128] @ q[n, 128 * gi:128 * gi + 128].double()) * float(s[n, gi])
+    got = omlp.q8_linear(x.float(), q, s).double()
+    assert float((got - ref).abs().max()) < 1e-5
+    # quantization error is at most half a step of the group's scale
+    err = (omlp.q8_dequant(q, s) - w).abs().reshape(5, 3, 128).amax(dim=2)
+    assert bool((err <= s / 2 + 1e-7).all())
