@@ -25,10 +25,11 @@
 // The products are oriented so that their accumulator tiles pack straight into the scan kernel's MFMA operand order,
 // and the records are written with 16- or 8-byte coalesced stores.
 // Kernel 2, gdn_pair_scan_kernel: 16 blocks per (row, head): 8 slices of 16 value columns x 2 halves of the output
-// rows. Each block carries its 128 x 16 fp32 state slice in registers (4 waves x 32 rows) and, per pair, does
-// 8 + 4 MFMAs per wave; the bf16 state is exchanged through LDS once per pair. Operands stream straight from L2 into
-// registers three pairs ahead; a fifth wave touches the records several pairs further ahead so that the first of the
-// 16 blocks to need a line finds it in L2. The 16 blocks of a head are placed on one XCD (they share its L2).
+// rows. Each block carries its 128 x 16 fp32 state slice in registers (8 waves x 16 rows) while 4 more waves form the
+// 64 output rows of its half, 4 MFMAs per wave and pair; the bf16 state is exchanged through LDS once per pair.
+// Operands stream straight from L2 into registers three pairs ahead (12 waves keep about 40 KB of loads in flight per
+// CU); a thirteenth wave touches the records several pairs further ahead so that the first of the 16 blocks to need a
+// line finds it in L2. The 16 blocks of a head are placed on one XCD (they share its L2).
 #include "q35_common.h"
 #include "q35hip.h"
 
@@ -655,29 +656,40 @@ __device__ __forceinline__ void store_out(__amdgpu_buffer_rsrc_t rc, int off_ele
   __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (__bf16)x), rc, off_elems * 2, 0, 0);
 }
 
-// Operands of one pair for one wave of the scan kernel.
-struct PairOps {
-  bf16x8 m[2][4];  // M fragments of the wave's two state row tiles
-  bf16x8 qf[4];    // Q' fragments of the wave's output row tile
-  u32x2 bv[2];     // Bm (D order) of the two state row tiles
-  u32x2 rv;        // R (D order) of the output row tile
+// Operands of one pair for one wave of the scan kernel: a state-row-tile wave takes the M fragments and the Bm piece
+// of its tile, an output-tile wave the Q' fragments and the R piece of its tile.
+struct StateOps {
+  bf16x8 m[4];
+  u32x2 bv;
   float eg;
 };
+struct OutOps {
+  bf16x8 qf[4];
+  u32x2 rv;
+};
 
-__global__ __launch_bounds__(320, 1) void gdn_pair_scan_kernel(const char* __restrict__ ws, const float* s_in,
-                                                               float* s_out, __bf16* __restrict__ o, int T, int NP,
-                                                               int H, int B) {
-  __shared__ bf16x8 slot[2][4][64];
+constexpr int kScanThreads = 13 * 64;
+
+// Waves 0-7: state row tile w (rows 16 w .. 16 w + 15 of the block's 128 x 16 slice), S <- e^G S + Bm + M S.
+// Waves 8-11: output row tile 4 half + (w - 8) of the pair, O = Q' S + R. Wave 12: L2 warm-up.
+// Each state wave publishes its tile as bf16 once per pair (LDS, double-buffered by pair parity); after the pair's
+// barrier every wave reads the whole bf16 slice as its B operands. A wave holds the operands of three pairs ahead.
+__global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const char* __restrict__ ws, const float* s_in,
+                                                                        float* s_out, __bf16* __restrict__ o, int T,
+                                                                        int NP, int H, int B) {
+  __shared__ u32x2 slot[2][8][64];
   __shared__ int dummy[64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int idx, unit;
   scan_coords(blockIdx.x, H * B, idx, unit);
   const int sl = idx & 7, half = idx >> 3;
   const int h = unit % H, b = unit / H;
   const int li = lane & 15, lg = lane >> 4;
   const char* rec0 = ws + (size_t)unit * NP * kRecBytes;
+  const int col = 16 * sl + li;
 
-  if (wave == 4) {
+  if (w == 12) {
     // ---------------- L2 warm-up wave: 64 of the 1024 record lines per pair, kTouchAhead pairs ahead ------------
     const uint32_t d = lds_addr(dummy);
     const size_t line = (size_t)(64 * idx + lane) * 128;
@@ -691,67 +703,88 @@ __global__ __launch_bounds__(320, 1) void gdn_pair_scan_kernel(const char* __res
     return;
   }
 
-  const int w = wave;
-  const int col = 16 * sl + li;
-  const size_t sbase = (size_t)unit * kD * kD;
-  f32x4 S[2];
+  static_assert(kScanAhead == 3, "the pair loops below are unrolled by three");
+  auto gather = [&](int pp, bf16x8 (&sb)[4]) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      S[i][r] = s_in ? s_in[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col] : 0.f;
-
-  auto load = [&](int pp, PairOps& op) {
-    const char* rec = rec0 + (size_t)min(pp, NP - 1) * kRecBytes;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        op.m[i][ks] = *reinterpret_cast<const bf16x8*>(rec + kRecM + ((size_t)((2 * w + i) * 4 + ks) * 64 + lane) * 16);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      op.qf[ks] = *reinterpret_cast<const bf16x8*>(rec + kRecQ + ((size_t)((4 * half + w) * 4 + ks) * 64 + lane) * 16);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      op.bv[i] = *reinterpret_cast<const u32x2*>(rec + kRecB + ((size_t)((2 * w + i) * 8 + sl) * 64 + lane) * 8);
-    op.rv = *reinterpret_cast<const u32x2*>(rec + kRecR + ((size_t)((4 * half + w) * 8 + sl) * 64 + lane) * 8);
-    op.eg = *reinterpret_cast<const float*>(rec + kRecE);
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x2 lo = slot[pp & 1][2 * ks][lane], hi = slot[pp & 1][2 * ks + 1][lane];
+      const u32x4 v = {lo.x, lo.y, hi.x, hi.y};
+      sb[ks] = __builtin_bit_cast(bf16x8, v);
+    }
   };
 
+  if (w < 8) {
+    // ---------------- state row tile w ----------------
+    const size_t sbase = (size_t)unit * kD * kD;
+    f32x4 S;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) S[r] = s_in ? s_in[sbase + (size_t)(16 * w + 4 * lg + r) * kD + col] : 0.f;
+    auto load = [&](int pp, StateOps& op) {
+      const char* rec = rec0 + (size_t)min(pp, NP - 1) * kRecBytes;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        op.m[ks] = *reinterpret_cast<const bf16x8*>(rec + kRecM + ((size_t)(w * 4 + ks) * 64 + lane) * 16);
+      op.bv = *reinterpret_cast<const u32x2*>(rec + kRecB + ((size_t)(w * 8 + sl) * 64 + lane) * 8);
+      op.eg = *reinterpret_cast<const float*>(rec + kRecE);
+    };
+    auto step = [&](int pp, const StateOps& op) {
+      slot[pp & 1][w][lane] = pack4(S[0], S[1], S[2], S[3]);
+      lds_barrier();
+      bf16x8 sb[4];
+      gather(pp, sb);
+      const f32x4 bm = unpack4(op.bv);
+      f32x4 s;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = op.eg * S[r] + bm[r];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) s = mfma16(op.m[ks], sb[ks], s);
+      S = s;
+    };
+    StateOps o0, o1, o2;
+    load(0, o0);
+    load(1, o1);
+    load(2, o2);
+    for (int pp = 0; pp < NP; pp += 3) {
+      step(pp, o0);
+      load(pp + 3, o0);
+      if (pp + 1 < NP) step(pp + 1, o1);
+      load(pp + 4, o1);
+      if (pp + 2 < NP) step(pp + 2, o2);
+      load(pp + 5, o2);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (s_out && half == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_out[sbase + (size_t)(16 * w + 4 * lg + r) * kD + col] = S[r];
+    }
+    return;
+  }
+
+  // ---------------- output row tile 4 half + j ----------------
+  const int ot = 4 * half + (w - 8);
   // Outputs go through a buffer resource spanning row b's [T, H, 128] block: stores past the sequence end fall
   // outside it and are dropped by the hardware.
   const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
       o + (size_t)b * T * H * kD, 0, (int)((size_t)T * H * kD * sizeof(__bf16)), 0x00020000);
-
-  auto step = [&](int pp, const PairOps& op) {
-    const bf16x8 own = pack8(S[0], S[1]);
-    slot[pp & 1][w][lane] = own;
+  auto load = [&](int pp, OutOps& op) {
+    const char* rec = rec0 + (size_t)min(pp, NP - 1) * kRecBytes;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      op.qf[ks] = *reinterpret_cast<const bf16x8*>(rec + kRecQ + ((size_t)(ot * 4 + ks) * 64 + lane) * 16);
+    op.rv = *reinterpret_cast<const u32x2*>(rec + kRecR + ((size_t)(ot * 8 + sl) * 64 + lane) * 8);
+  };
+  auto step = [&](int pp, const OutOps& op) {
     lds_barrier();
     bf16x8 sb[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) sb[ks] = ks == w ? own : slot[pp & 1][ks][lane];
-    // outputs of this pair's half: O = Q' S + R
+    gather(pp, sb);
     f32x4 acc = unpack4(op.rv);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc = mfma16(op.qf[ks], sb[ks], acc);
-    const int tb = kP * pp + 64 * half + 16 * w + 4 * lg;
+    const int tb = kP * pp + 16 * ot + 4 * lg;
 #pragma unroll
     for (int r = 0; r < 4; ++r) store_out(orc, ((tb + r) * H + h) * kD + col, acc[r]);
-    // state: S <- e^G S + Bm + M S
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const f32x4 bm = unpack4(op.bv[i]);
-      f32x4 s;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[r] = op.eg * S[i][r] + bm[r];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) s = mfma16(op.m[i][ks], sb[ks], s);
-      S[i] = s;
-    }
   };
-
-  static_assert(kScanAhead == 3, "the pair loop below is unrolled by three");
-  PairOps o0, o1, o2;
+  OutOps o0, o1, o2;
   load(0, o0);
   load(1, o1);
   load(2, o2);
@@ -764,12 +797,6 @@ __global__ __launch_bounds__(320, 1) void gdn_pair_scan_kernel(const char* __res
     load(pp + 5, o2);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (s_out && half == 0) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_out[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col] = S[i][r];
-  }
 }
 
 // ================================================================================================================
@@ -1174,7 +1201,7 @@ extern "C" int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v
     dim3 g1((unsigned)H, (unsigned)NP, (unsigned)B), g2((unsigned)(16 * H * B));
     hipLaunchKernelGGL(gdn_pair_prep_kernel, g1, dim3(512), 0, st, (const __bf16*)q, (const __bf16*)k,
                        (const __bf16*)v, g, beta, ws, (int)T, (int)NP, (int)Hk, (int)H, scale, use_qk_l2norm);
-    hipLaunchKernelGGL(gdn_pair_scan_kernel, g2, dim3(320), 0, st, ws, initial_state, final_state,
+    hipLaunchKernelGGL(gdn_pair_scan_kernel, g2, dim3(kScanThreads), 0, st, ws, initial_state, final_state,
                        (__bf16*)out, (int)T, (int)NP, (int)H, (int)B);
   }
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
