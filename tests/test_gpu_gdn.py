@@ -60,6 +60,28 @@ def test_recurrent_long_prefill_fp32():
     assert oracle.rel_err(state.cpu(), s_ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("B,H,Hk", [(16, 16, 16), (32, 8, 4)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_step_many_states(B, H, Hk, dtype):
+    """One token over B x H states (at least 1024 units of 32 value columns: the two-units-per-block decode kernel),
+    in place, from a non-zero state; the second shape has 8 value heads over 4 q/k heads."""
+    dev = device()
+    inp = workloads.gdn_inputs(B=B, T=1, H=H, Hk=Hk, D=128, seed=7, dtype=dtype, normalize=False)
+    s0 = 0.1 * torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(8))
+    o_ref, s_ref = _oracle_rec(inp, s0)
+    d = workloads.to_device(inp, dev)
+    announce(f"gdn decode step B{B} H{H}/{Hk} {dtype}")
+    state = s0.to(dev)
+    o = q35hip.gdn_decode_step_(d["q"], d["k"], d["v"], d["g"], d["beta"], state)
+    torch.cuda.synchronize()
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    assert oracle.rel_err(o.float().cpu(), o_ref) <= tol
+    assert oracle.rel_err(state.cpu(), s_ref) <= tol
+    # every (row, head) checked on its own, so that a unit written to the wrong place cannot hide in the norm
+    err = ((state.cpu() - s_ref).flatten(2).norm(dim=2) / s_ref.flatten(2).norm(dim=2)).max().item()
+    assert err <= tol
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_recurrent_multi_token_gqa_initial_state(dtype):
     """T = 37 in one launch, B = 2, 8 value heads over 4 q/k heads, a non-zero initial state."""
