@@ -156,6 +156,18 @@ def bench_gdn_decode(torch, q35hip, workloads, steps, warmup, dev):
         by = B * GDN_DECODE_STEP_BYTES
         out[name] = {"tok_s": B / t, "us": t * 1e6, "achieved_gbs": by / t / 1e9, "frac": by / t / 1e9 / PEAK_HBM_GBS,
                      "state_mb_cycled": nstate * B * H * D * D * 4 / 1e6}
+    # The 64 sequential tokens of the decode configuration as one launch of the token-serial kernel (the state stays
+    # in registers across tokens; each token still waits for the previous one): a decode loop whose inputs are all
+    # known, as a prompt replayed token by token is. The per-step figures above are one launch per token.
+    B, T, H, D, nstate = 1, 64, 16, 128, 16
+    inp = workloads.to_device(workloads.gdn_inputs(B=B, T=T, H=H, D=D, seed=0, dtype=torch.float32), dev)
+    states = [torch.zeros(B, H, D, D, device=dev) for _ in range(nstate)]
+
+    def make_seq(i):
+        return lambda: q35hip.gdn_decode_step_(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"], states[i])
+    r = Timer(torch, make_seq, nstate, reps=nstate).run(steps, warmup)
+    t = r["step_s"]
+    out["b1_t64_one_launch"] = {"tok_s": T / t, "us_per_token": t * 1e6 / T, "us_per_launch": t * 1e6}
     return out
 
 

@@ -216,19 +216,20 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const __bf16* __r
   char* rec = ws + (((size_t)b * H + h) * NP + p) * kRecBytes;
   char* WT = reinterpret_cast<char*>(R3);
 
-  // ---- 0. stage. Threads 0-255 hold an 8 x 8 unit of k (rows 8 rg.., dims 8 cc..), threads 256-511 one of v; the
-  //         units stay in registers for the transposed copies written after the K K^T phase. q goes row-major.
-  //         Every global load of the phase (k or v, q, and the gates of wave 0) is issued before any is used, so
-  //         the phase costs one memory round trip.
+  // ---- 0. stage. Threads 0-255 hold an 8 x 8 unit of k (rows 8 rg.., dims 8 cc..), which stays in registers for
+  //         the transposed copy written after the K K^T phase; q goes row-major. Every global load of the phase
+  //         (k, q, and the gates of wave 0) is issued before any is used, so the phase costs one memory round trip.
+  //         v is first needed after the inverses: threads 256-511 load their 8 x 8 unit of it at the start of
+  //         phase 2, so that its bytes travel while the inverses run instead of lengthening this phase's burst.
   const int u = tid & 255, rg = u >> 4, cc = u & 15;
-  const bool isK = tid < 256;
+  const bool isK = wv < 4;
   u32x4 raw[8];
-  const __bf16* src[8];
+  if (isK) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const size_t tok = (size_t)b * T + t0 + min(8 * rg + i, nvalid - 1);
-    src[i] = isK ? k + (tok * Hk + kh) * kD + 8 * cc : v + (tok * H + h) * kD + 8 * cc;
-    raw[i] = raw8(src[i]);
+    for (int i = 0; i < 8; ++i) {
+      const size_t tok = (size_t)b * T + t0 + min(8 * rg + i, nvalid - 1);
+      raw[i] = raw8(k + (tok * Hk + kh) * kD + 8 * cc);
+    }
   }
   const int qrow = tid >> 2, qs0 = 4 * (tid & 3);
   const __bf16* qsrc = q + (((size_t)b * T + t0 + min(qrow, nvalid - 1)) * Hk + kh) * kD;
@@ -241,15 +242,15 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const __bf16* __r
     if (lane < nvalid) { g0 = g[base + (size_t)lane * H]; b0 = beta[base + (size_t)lane * H]; }
     if (64 + lane < nvalid) { g1 = g[base + (size_t)(64 + lane) * H]; b1 = beta[base + (size_t)(64 + lane) * H]; }
   }
-  {
+  if (isK) {
     float ss[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const bool valid = 8 * rg + i < nvalid;
-      ss[i] = valid && isK ? sumsq8(raw[i]) : 0.f;
+      ss[i] = valid ? sumsq8(raw[i]) : 0.f;
       raw[i] = mask8(raw[i], valid);
     }
-    if (isK) {
+    {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
 #pragma unroll
@@ -409,13 +410,28 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const __bf16* __r
   }
   __syncthreads();
 
-  // ---- 2. transposed k and v from the registers; the two chunk inverses T00, T11 (waves 0-3, 4-7)
+  // ---- 2. the two chunk inverses T00, T11 (waves 0-3, 4-7); transposed k from the registers meanwhile, and the v
+  //         units (loaded here, written transposed once the inverses are done; the barriers in between order LDS
+  //         traffic only, so the v loads stay in flight through the inverses)
+  if (isK) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
-    *reinterpret_cast<u32x4*>((isK ? R1 : R2) + t128(8 * cc + e, 8 * rg)) = column8(raw, e);
+    for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(R1 + t128(8 * cc + e, 8 * rg)) = column8(raw, e);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const size_t tok = (size_t)b * T + t0 + min(8 * rg + i, nvalid - 1);
+      raw[i] = raw8(v + (tok * H + h) * kD + 8 * cc);
+    }
+  }
   {
     float* Am = R3 + (wave >> 2) * 64 * kFS;
-    invert64(Am, wave & 3, lane, scr[wave], [] { __syncthreads(); });
+    invert64(Am, wave & 3, lane, scr[wave], [] { lds_barrier(); });
+  }
+  if (!isK) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) raw[i] = mask8(raw[i], 8 * rg + i < nvalid);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(R2 + t128(8 * cc + e, 8 * rg)) = column8(raw, e);
   }
   __syncthreads();
   // A operands held in registers: rows 16 rt .. of T00 scaled for W0 (waves 0-3) or U0 (waves 4-7), and of T11.
