@@ -16,6 +16,10 @@
 // waves in LDS. Epilogues: store, accumulate into y (the residual add after down_proj), or SwiGLU over interleaved
 // (gate, up) row pairs with the neuron pushes applied (gate_up_proj). With group scales a lane's 16 weights of a K step
 // lie in one group (group 2 step + slot / 8), so the lane scales its partial sum of the step once.
+// Split K: an accumulating product without the norm prologue may split its K steps over gridDim.y blocks per 16 rows
+// (a product with few output rows, e.g. N = 1024, has too few blocks to draw bandwidth from every CU); each block
+// stages and reads only its share of x and W and adds its sums into y with fp32 atomics, so the order of the
+// additions, and the last bits of y, may differ between runs.
 #include "q35_common.h"
 #include "q35hip.h"
 
@@ -81,6 +85,12 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
   const int NW = blockDim.x >> 6;
   const int g = lane >> 4, j = lane & 15;
   const int n0 = blockIdx.x * 16;
+  // this block's K steps [sb, se) (split K: gridDim.y > 1 only for accumulating products without the norm)
+  const int nsplit = gridDim.y;
+  const int spb = (K / KS + nsplit - 1) / nsplit;
+  const int sb = (int)blockIdx.y * spb, se = min(K / KS, sb + spb);
+  if (sb >= se) return;
+  const int kb0 = sb * KS, Kb = (se - sb) * KS;  // x columns staged: [kb0, kb0 + Kb)
   static_assert(!GS || E == 16, "group scales are for int8 weights");
   const TW* wr[4];
   const float* sr[4];  // GS: the lane's scale of step 0 in each of its rows (groups of 128 inputs: 2 per K step)
@@ -90,8 +100,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
     wr[r] = W + (size_t)nr * K + j * E;
     sr[r] = GS ? wscale + (size_t)nr * (K >> 7) + (j >> 3) : nullptr;
   }
-  const int nsteps = K / KS;
-  // this wave's K steps: wave, wave + NW, ...; U of them in flight per round. Loads complete in issue order, so the
+  // this wave's K steps: sb + wave, sb + wave + NW, ...; U of them in flight per round. Loads complete in issue order, so the
   // thread's first x chunk (L2) is issued ahead of the first round of weights (HBM): the staging then waits for x
   // only, and its work overlaps the weights' flight
   WChunk<TW> wc[U][4];
@@ -99,7 +108,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
   auto issue = [&](int s0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int st = min(s0 + u * NW, nsteps - 1);
+      const int st = min(s0 + u * NW, se - 1);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         wc[u][r].load(wr[r] + st * KS);
@@ -128,11 +137,11 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
       }
     }
   } else {
-    // the non-NORM staging takes element quads i = tid, tid + blockDim ... of the flattened [MP][K]
-    const int m0 = kf / K, k0 = kf - m0 * K;
-    if (m0 < M && kf < MP * K) fv[0] = *reinterpret_cast<const f32x4*>(x + m0 * ldx + k0);
+    // the non-NORM staging takes element quads i = tid, tid + blockDim ... of the flattened [MP][Kb]
+    const int m0 = kf / Kb, k0 = kf - m0 * Kb;
+    if (m0 < M && kf < MP * Kb) fv[0] = *reinterpret_cast<const f32x4*>(x + m0 * ldx + kb0 + k0);
   }
-  issue(wave);
+  issue(sb + wave);
   asm volatile("" ::: "memory");
   if (NORM) {
     float ss[MP];
@@ -175,11 +184,11 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
       if (lane == 0) ssw[wave][m] = ss[m];
     }
   } else {
-    for (int i = tid; i < MP * K / 4; i += blockDim.x) {
-      const int m = (4 * i) / K, k = 4 * i - m * K;
+    for (int i = tid; i < MP * Kb / 4; i += blockDim.x) {
+      const int m = (4 * i) / Kb, k = 4 * i - m * Kb;
       f32x4 v = zero4();
-      if (m < M) v = i == tid ? fv[0] : *reinterpret_cast<const f32x4*>(x + m * ldx + k);
-      *reinterpret_cast<f32x4*>(xs + m * K + k) = v;
+      if (m < M) v = i == tid ? fv[0] : *reinterpret_cast<const f32x4*>(x + m * ldx + kb0 + k);
+      *reinterpret_cast<f32x4*>(xs + m * Kb + k) = v;
     }
   }
   __syncthreads();
@@ -188,13 +197,13 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int m = 0; m < MP; ++m) acc[r][m] = 0.f;
-  for (int s0 = wave; s0 < nsteps; s0 += U * NW) {
-    if (s0 != wave) issue(s0);
+  for (int s0 = sb + wave; s0 < se; s0 += U * NW) {
+    if (s0 != sb + wave) issue(s0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int st = s0 + u * NW;
-      if (st >= nsteps) break;
-      const int k = st * KS + j * E;
+      if (st >= se) break;
+      const int k = (st - sb) * KS + j * E;  // column in the staged x (Kb == K without a split)
       float part[4][MP];  // GS: this step's sums, scaled once by the group's scale
 #pragma unroll
       for (int r = 0; r < 4; ++r)
@@ -204,7 +213,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
       for (int c = 0; c < E; c += 4) {
         f32x4 xv[MP];
 #pragma unroll
-        for (int m = 0; m < MP; ++m) xv[m] = *reinterpret_cast<const f32x4*>(xs + m * K + k + c);
+        for (int m = 0; m < MP; ++m) xv[m] = *reinterpret_cast<const f32x4*>(xs + m * Kb + k + c);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
 #pragma unroll
@@ -255,7 +264,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
         float v = rowsum(rr, m);
         if (wscale && !GS) v *= wscale[nn];
         float* dst = y + m * ldy + nn;
-        *dst = EPI == kEpiAccumulate ? *dst + v : v;
+        if (EPI == kEpiAccumulate && nsplit > 1)
+          __hip_atomic_fetch_add(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          *dst = EPI == kEpiAccumulate ? *dst + v : v;
       }
     }
   } else {
@@ -302,12 +314,14 @@ struct NormArgs {
 
 template <typename TW, int EPI, int U, bool NORM, bool GS>
 void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
-                   int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, int nw, const NormArgs& na,
-                   hipStream_t st) {
+                   int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, int nw, int nsplit,
+                   const NormArgs& na, hipStream_t st) {
   using namespace q35;
   const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 3 ? 3 : M <= 4 ? 4 : 8;
-  const size_t lds = (size_t)mp * K * sizeof(float);
-  const dim3 grid((unsigned)((N + 15) / 16)), block(64 * nw);
+  constexpr int KS = 16 * WChunk<TW>::kElems;
+  const int64_t spb = (K / KS + nsplit - 1) / nsplit;
+  const size_t lds = (size_t)mp * spb * KS * sizeof(float);
+  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)nsplit), block(64 * nw);
 #define Q35_GEMV(MP)                                                                                                 \
   hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS>), grid, block, lds, st, x, ldx, W, wscale, y, ldy,    \
                      (int)M, (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps, na.xout)
@@ -321,21 +335,35 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
 #undef Q35_GEMV
 }
 
-// 4 waves when K has at most 4 steps, else 8; each wave's steps all in flight at once up to 4
+// Blocks of output rows at which a product is split over K: below this many, an accumulating product without the norm
+// splits its K steps so that blocks x splits reaches it (one block per CU of the MI355X).
+constexpr int64_t kGemvSplitTarget = 256;
+
+// 4 waves when a block has at most 4 K steps, else 8; each wave's steps all in flight at once up to 4
 template <typename TW, int EPI, bool NORM, bool GS = false>
 int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
                 int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, const NormArgs& na,
                 hipStream_t st) {
   using namespace q35;
   const int64_t steps = K / (16 * WChunk<TW>::kElems);
-  const int nw = steps <= 4 ? 4 : 8;
-  const int64_t per_wave = (steps + nw - 1) / nw;
+  const int64_t nblk = (N + 15) / 16;
+  int64_t nsplit = 1;
+  if (EPI == kEpiAccumulate && !NORM && nblk < kGemvSplitTarget) {
+    nsplit = (kGemvSplitTarget + nblk - 1) / nblk;
+    if (nsplit > steps) nsplit = steps;
+    if (nsplit > 65535) nsplit = 65535;
+    const int64_t spb = (steps + nsplit - 1) / nsplit;
+    nsplit = (steps + spb - 1) / spb;  // no empty split
+  }
+  const int64_t bsteps = (steps + nsplit - 1) / nsplit;
+  const int nw = bsteps <= 4 ? 4 : 8;
+  const int64_t per_wave = (bsteps + nw - 1) / nw;
   if (per_wave <= 1)
-    gemv_launch_u<TW, EPI, 1, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
+    gemv_launch_u<TW, EPI, 1, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
   else if (per_wave <= 2)
-    gemv_launch_u<TW, EPI, 2, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
+    gemv_launch_u<TW, EPI, 2, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
   else
-    gemv_launch_u<TW, EPI, 4, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, na, st);
+    gemv_launch_u<TW, EPI, 4, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 

@@ -52,7 +52,7 @@ def rmsnorm_1p(x, w, eps=1e-6):
 
 
 def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_heads=None, head_k_dim=None,
-                         eps=1e-6, prefill="chunk", prenorm=None):
+                         eps=1e-6, prefill="chunk", prenorm=None, residual=None):
     """Gated DeltaNet mixer of one decoder layer (Qwen3_5GatedDeltaNet.forward, HF:432-543; the WGSL conv + delta
     kernels, engine/kernels_qwen35.js:127-247). x: [B, T, H] fp32 (the input-normed residual). A call with T == 1
     is one recurrent decode step (HF:505-517). T > 1 runs from rec_state either the chunked prefill (HF:518-530;
@@ -60,7 +60,8 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     (prefill="recurrent": as the WGSL engine runs prefill token by token, engine/kernels_qwen35.js:183-247). Both states are updated in place. head_scale: optional [Hv] per-head output
     scale applied after the gated norm (engine/kernels_qwen35.js:243). num_k_heads / head_k_dim default to the
     value heads / value head dim (the Qwen3.5 text models use Hk = Hv and dk = dv). prenorm: see linear() (x is then
-    the residual and the layer's input norm runs inside the input projection). Returns y [B, T, H]."""
+    the residual and the layer's input norm runs inside the input projection). Returns y [B, T, H], or with
+    residual [B, T, H] given, residual + y computed in place by the output projection (then returned)."""
     if prefill not in ("chunk", "recurrent"):
         raise ValueError(f"gated_deltanet_layer: prefill must be 'chunk' or 'recurrent', not {prefill!r}")
     B, T, _ = x.shape
@@ -78,7 +79,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
         o = ops.gdn_decode_fused_(y.view(B, y.shape[-1]), p["conv1d"], conv_state, p["A_log"], p["dt_bias"],
                                   rec_state, p["norm"], b_off=C + Vd, a_off=C + Vd + Hv, z_off=C,
                                   head_scale=head_scale, eps=eps)
-        return linear(o.view(B, 1, Vd), p["out_proj"], *_q8(p, "out_proj"))
+        return linear(o.view(B, 1, Vd), p["out_proj"], *_q8(p, "out_proj"), residual=residual)
     q, k, v, g, beta = ops.gdn_conv(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], num_k_heads=Hk,
                                     head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=C + Vd, a_off=C + Vd + Hv,
                                     out_dtype=x.dtype)
@@ -90,7 +91,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
         rec_state.copy_(S)
     # gated RMSNorm: plain w, norm before the silu(z) gate (HF:168-184; engine/kernels_qwen35.js:237-243)
     o = ops.gated_rmsnorm(o, y[..., C:C + Vd], p["norm"], head_scale, eps)
-    return linear(o, p["out_proj"], *_q8(p, "out_proj"))
+    return linear(o, p["out_proj"], *_q8(p, "out_proj"), residual=residual)
 
 
 def prenorm_torch(x, prenorm):
@@ -103,14 +104,17 @@ def prenorm_torch(x, prenorm):
     return ops.add_rmsnorm_(s, None, nw, eps)
 
 
-def linear(x, w, wq=None, ws=None, prenorm=None):
+def linear(x, w, wq=None, ws=None, prenorm=None, residual=None):
     """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), on the int8 weights wq with scales ws
     ([N, K / 128] per group or [N] per row; w their dequantised values) when given, else on w; for more rows the HIP
-    int8 GEMM on wq (fp32-accurate) when given, else a torch GEMM on w. prenorm = (x_add, norm_w, eps, x_out): x is a residual and the product takes the
-    RMSNorm (1 + norm_w) of x + x_add (x_add may be None), the sum being written to x_out when given (the decoder
-    layer's add + norm, fused into the GEMV)."""
+    int8 GEMM on wq (fp32-accurate) when given, else a torch GEMM on w. prenorm = (x_add, norm_w, eps, x_out): x is
+    a residual and the product takes the RMSNorm (1 + norm_w) of x + x_add (x_add may be None), the sum being written
+    to x_out when given (the decoder layer's add + norm, fused into the GEMV). residual [..., N]: the product is added
+    into it in place (the decoder layer's residual add after its mixer) and residual is returned."""
     K = x.shape[-1]
     M = x.numel() // K
+    N = (wq if wq is not None else w).shape[0]
+    out, epi = (None, "store") if residual is None else (residual.view(M, N), "add")
     if M <= 8 and K % 256 == 0 and x.dtype == torch.float32 and (wq is not None or w.dtype == torch.float32):
         xm = x.reshape(M, K).contiguous()
         pn = None
@@ -119,11 +123,16 @@ def linear(x, w, wq=None, ws=None, prenorm=None):
             pn = (None if x_add is None else x_add.reshape(M, K), nw, eps,
                   None if x_out is None else x_out.view(M, K))
         Wd, sd = (wq, ws) if wq is not None else (w, None)
-        return ops.gemv(xm, Wd, sd, prenorm=pn).view(*x.shape[:-1], Wd.shape[0])
+        y = ops.gemv(xm, Wd, sd, out=out, epilogue=epi, prenorm=pn)
+        return residual if residual is not None else y.view(*x.shape[:-1], N)
     if prenorm is not None:
         x = prenorm_torch(x, prenorm)
     if wq is not None and K % 64 == 0 and x.dtype == torch.float32:
-        return ops.gemm_q8(x.reshape(M, K), wq, ws).view(*x.shape[:-1], wq.shape[0])
+        y = ops.gemm_q8(x.reshape(M, K), wq, ws, out=out, epilogue=epi)
+        return residual if residual is not None else y.view(*x.shape[:-1], N)
+    if residual is not None:
+        residual.view(M, N).addmm_(x.reshape(M, K), w.T)
+        return residual
     return x @ w.T
 
 
@@ -156,7 +165,7 @@ def attn_in_weight(p):
 
 
 def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partial_rotary_factor=0.25, eps=1e-6,
-                          cache_len=None, prenorm=None):
+                          cache_len=None, prenorm=None, residual=None):
     """Gated softmax attention mixer of one decoder layer (Qwen3_5Attention.forward, HF:656-701; WGSL attnPrep +
     attention, engine/kernels_qwen35.js:18-123). x: [B, T, H] fp32; the T tokens sit at positions pos..pos+T-1,
     pos a Python int or a [B] int32 device tensor (per row; a device tensor keeps the call capturable in a HIP
@@ -164,7 +173,8 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     cache positions 0..pos+t (engine/kernels_qwen35.js:90). T > 1 at the int position 0 runs the flash prefill over
     the call's own tokens; T > 1 at any other position (or a device pos) the same kernel over the cache (the caches'
     max_len must then be a multiple of 64); T == 1 the split-K decode over cache positions 0..pos (cache_len:
-    optional [B] int32 per-row lengths, default pos + 1). prenorm: see linear(). Returns y [B, T, H]."""
+    optional [B] int32 per-row lengths, default pos + 1). prenorm: see linear(). Returns y [B, T, H], or with
+    residual [B, T, H] given, residual + y computed in place by o_proj (then returned)."""
     B, T, _ = x.shape
     D = p["q_norm"].numel()
     Hq = p["q_proj"].shape[0] // (2 * D)
@@ -192,7 +202,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
         # fp32 straight from the merge kernel: the o_proj GEMV reads fp32 (no conversion kernel in the step)
         o = ops.gated_attention_decode(q[:, 0], k_cache, v_cache, gate[:, 0], cl, cos, sin,
                                        scale=1.0 / math.sqrt(D), out_dtype=torch.float32).view(B, 1, Hq * D)
-    return linear(o.float(), p["o_proj"], *_q8(p, "o_proj"))
+    return linear(o.float(), p["o_proj"], *_q8(p, "o_proj"), residual=residual)
 
 
 def residual_steer_add(x, vecs, rows=None):

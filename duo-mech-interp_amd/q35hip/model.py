@@ -65,9 +65,11 @@ def mlp(p, h, x, prenorm=None):
     H = h.shape[-1]
     M = h.numel() // H
     T = h.shape[1] if h.dim() == 3 else 1
-    pn = None if prenorm is None else (prenorm[0], prenorm[1], prenorm[2], x)
+    # h + y_add is written to x when x is another buffer; with x = h and no y_add the norm reads h as it is
+    pn = None if prenorm is None else (prenorm[0], prenorm[1], prenorm[2], None if x is h else x)
     if M <= 8 and "_gu_q8" in p and H % 256 == 0 and p["down_proj.q"].shape[1] % 256 == 0:
-        pn2 = None if pn is None else (None if pn[0] is None else pn[0].reshape(M, H), pn[1], pn[2], x.view(M, H))
+        pn2 = None if pn is None else (None if pn[0] is None else pn[0].reshape(M, H), pn[1], pn[2],
+                                       None if pn[3] is None else x.view(M, H))
         a = ops.gemv(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T,
                      prenorm=pn2)
         ops.gemv(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H), epilogue="add")
@@ -191,36 +193,33 @@ class HybridModel:
         prefill over the call's own keys; else the rows' device positions: the prefill over the KV cache).
 
         Prefill (T > 1): x is updated in place; each layer adds its mixer output in the fused residual-add + RMSNorm
-        kernel and its MLP output in the MLP's last product. Decode (T == 1): the adds and norms run inside the
-        GEMVs (q35_gemv_norm): the mixer's input projection normalises the residual, the MLP's first GEMV writes
-        residual + mixer output into a second buffer and normalises it, and down_proj accumulates into that buffer;
-        the two buffers alternate by layer."""
+        kernel and its MLP output in the MLP's last product. Decode (T == 1): x is updated in place by the GEMVs:
+        the mixer's input projection and the MLP's first GEMV normalise the residual in their prologue
+        (q35_gemv_norm), and the mixer's output projection and down_proj accumulate into it (split over K, so that
+        these N = hidden products draw bandwidth from every CU)."""
         cfg = self.cfg
         collected = None
         pos_dev, vec_rows = self.pos_dev[rs], self.vec_rows[rs]
         if T == 1:
             cache_len = self.len_dev[rs]  # shared by the attention layers
-            cur, alt = x, torch.empty_like(x)
             for l in range(last + 1):
                 p = self.params[l]
                 st = {n: t[rs] for n, t in self.states[l].items()}
                 pre = (None, p["input_layernorm"], cfg.eps, None)
                 if cfg.is_attention(l):
-                    y = layers.gated_attention_layer(cur, p, st["k"], st["v"], pos_dev,
-                                                     rope_theta=cfg.rope_theta,
-                                                     partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps,
-                                                     cache_len=cache_len, prenorm=pre)
+                    layers.gated_attention_layer(x, p, st["k"], st["v"], pos_dev, rope_theta=cfg.rope_theta,
+                                                 partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps,
+                                                 cache_len=cache_len, prenorm=pre, residual=x)
                 else:
-                    y = layers.gated_deltanet_layer(cur, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
-                                                    head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill,
-                                                    prenorm=pre)
-                mlp(p, cur, alt, prenorm=(y, p["post_attention_layernorm"], cfg.eps))
-                cur, alt = alt, cur
+                    layers.gated_deltanet_layer(x, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
+                                                head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill,
+                                                prenorm=pre, residual=x)
+                mlp(p, x, x, prenorm=(None, p["post_attention_layernorm"], cfg.eps))
                 if l == self.steer_layer and steer:
-                    layers.residual_steer_add(cur, self.vec_buf, vec_rows)
+                    layers.residual_steer_add(x, self.vec_buf, vec_rows)
                 if l == collect_layer:
-                    collected = cur.clone()
-            return cur, collected
+                    collected = x.clone()
+            return x, collected
         y = None  # the previous mixer's output, added to x by the next norm
         for l in range(last + 1):
             p = self.params[l]

@@ -271,6 +271,8 @@ int q35_add_rmsnorm(float* x, int64_t ldx, const float* y, int64_t ldy, const fl
  *   gate, row 2 j + 1 the up projection of neuron j): y[m, j] = silu(v_2j) * v_2j+1, then the pushes in order.
  *   y: [M, ldy] fp32 (ldy >= N, or >= N / 2 for epilogue 2). pushes: npush <= 64 records on the device (or NULL
  *   with npush 0); T: tokens per sequence row (the push row is min(m / T, 3)).
+ *   Epilogue 1 with fewer than 256 blocks of 16 output rows splits K over several blocks that add their sums into
+ *   y with fp32 atomics: the order of those additions, and so the last bits of y, may differ between calls.
  */
 int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
              int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T,

@@ -78,7 +78,9 @@ def test_tiny_stack_rows_of_different_lengths_and_chunked_prefill():
 
 def test_tiny_stack_decode_graph_replays_match_eager():
     """The captured decode step, replayed over 10 steps, gives the eager path's logits at every step (same kernels,
-    same buffers), with eager work and synchronisations between the replays."""
+    same buffers), with eager work and synchronisations between the replays. The step's hidden-sized products split K
+    and add their partial sums into the residual with fp32 atomics, so two runs of the same kernels agree to rounding
+    (measured 2.4e-5 relative on these logits), not bit for bit: the bound is 1e-4."""
     dev = device()
     cfg = tiny_config()
     W = tiny_weights(cfg)
@@ -98,7 +100,7 @@ def test_tiny_stack_decode_graph_replays_match_eager():
         lg = graph.decode_step(nxt).clone()
         torch.cuda.synchronize()
         assert graph.pos == eager.pos
-        assert oracle.rel_err(lg.cpu(), le.cpu()) <= 1e-6, f"replay {step} differs from eager"
+        assert oracle.rel_err(lg.cpu(), le.cpu()) <= 1e-4, f"replay {step} differs from eager"
 
 
 _FULL_REF = {}
