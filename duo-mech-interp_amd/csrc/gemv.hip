@@ -8,14 +8,18 @@
 // push of the layer whose neuron is n or every neuron, add or multiply by the push's value for the row; the row index
 // is clamped to 3).
 //
-// Layout: a block takes 16 output rows and NW = 4 or 8 waves. Lane (g, j) = (lane / 16, lane % 16) works on rows
-// g, g + 4, g + 8, g + 12 of the block and on input slot j of every K step: a K step is 16 slots of 16 weight bytes
-// (256 int8 inputs, 64 fp32), so one wave load covers 4 rows x 256 contiguous bytes, and the x values of a slot (read
-// from LDS, where x is staged once per block) serve the lane's four rows. The waves take the K steps round robin,
-// each with all of its weight loads in flight at once. Per-row sums: a 16-lane DPP row reduction, then across the
-// waves in LDS. Epilogues: store, accumulate into y (the residual add after down_proj), or SwiGLU over interleaved
+// Layout: a tile is 4 R output rows (the launcher takes R = 4: 32-row tiles measured slower in the decode step) and a
+// block NW = 4 or 8 waves. Lane (g, j) = (lane / 16, lane % 16) works on rows g, g + 4, ..., g + 4 (R - 1) of the
+// tile and on input slot j of every K step: a K step is 16 slots of 16 weight bytes (256 int8 inputs, 64 fp32), so
+// one wave load covers 4 rows x 256 contiguous bytes, and the x values of a slot (read from LDS, where x is staged
+// once per block) serve the lane's R rows. The waves take the K steps round
+// robin, each with all of its weight loads in flight at once. Per-row sums: a 16-lane DPP row reduction, then across
+// the waves in LDS. Epilogues: store, accumulate into y (the residual add after down_proj), or SwiGLU over interleaved
 // (gate, up) row pairs with the neuron pushes applied (gate_up_proj). With group scales a lane's 16 weights of a K step
 // lie in one group (group 2 step + slot / 8), so the lane scales its partial sum of the step once.
+// TL: a block takes tiles blockIdx.x, blockIdx.x + gridDim.x, ... (the LM head's 9496 tiles run on a capped grid);
+// the next tile's weights are issued before the current tile's products when a wave has one K step per tile (two
+// register sets), else before its reduction.
 // Split K: an accumulating product without the norm prologue may split its K steps over gridDim.y blocks per 16 rows
 // (a product with few output rows, e.g. N = 1024, has too few blocks to draw bandwidth from every CU); each block
 // stages and reads only its share of x and W and adds its sums into y with fp32 atomics, so the order of the
@@ -69,7 +73,7 @@ __device__ __forceinline__ float row16_sum_f(float v) {
 
 // NORM: x is a residual row; the kernel adds xadd (may be NULL), writes the sum to xout from block 0 (may be NULL),
 // and multiplies the RMSNorm of the sum, s * rsqrt(mean s^2 + eps) * (1 + nw), instead of x (HF:720-734).
-template <typename TW, int MP, int EPI, int U, bool NORM, bool GS>
+template <typename TW, int MP, int EPI, int U, bool NORM, bool GS, bool TL, int R = 4>
 __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, int64_t ldx, const TW* __restrict__ W,
                                                    const float* __restrict__ wscale, float* __restrict__ y,
                                                    int64_t ldy, int M, int N, int K,
@@ -80,11 +84,13 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
   constexpr int E = WChunk<TW>::kElems;  // weights per lane per 16-byte load
   constexpr int KS = 16 * E;             // inputs per K step
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [MP][K]
-  __shared__ float red[8][16][MP];
+  __shared__ float red[TL ? 2 : 1][8][4 * R][MP];  // per-row wave sums (TL: double-buffered over the block's tiles)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int NW = blockDim.x >> 6;
   const int g = lane >> 4, j = lane & 15;
-  const int n0 = blockIdx.x * 16;
+  // tiles of 4 R output rows: this block takes tiles blockIdx.x, blockIdx.x + gridDim.x, ...
+  const int ntiles = (N + 4 * R - 1) / (4 * R);
+  int tile = blockIdx.x;
   // this block's K steps [sb, se) (split K: gridDim.y > 1 only for accumulating products without the norm)
   const int nsplit = gridDim.y;
   const int spb = (K / KS + nsplit - 1) / nsplit;
@@ -92,25 +98,28 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
   if (sb >= se) return;
   const int kb0 = sb * KS, Kb = (se - sb) * KS;  // x columns staged: [kb0, kb0 + Kb)
   static_assert(!GS || E == 16, "group scales are for int8 weights");
-  const TW* wr[4];
-  const float* sr[4];  // GS: the lane's scale of step 0 in each of its rows (groups of 128 inputs: 2 per K step)
+  const TW* wr[R];
+  const float* sr[R];  // GS: the lane's scale of step 0 in each of its rows (groups of 128 inputs: 2 per K step)
+  auto set_rows = [&](int t) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int nr = min(n0 + g + 4 * r, N - 1);
-    wr[r] = W + (size_t)nr * K + j * E;
-    sr[r] = GS ? wscale + (size_t)nr * (K >> 7) + (j >> 3) : nullptr;
-  }
+    for (int r = 0; r < R; ++r) {
+      const int nr = min(t * 4 * R + g + 4 * r, N - 1);
+      wr[r] = W + (size_t)nr * K + j * E;
+      sr[r] = GS ? wscale + (size_t)nr * (K >> 7) + (j >> 3) : nullptr;
+    }
+  };
+  set_rows(tile);
   // this wave's K steps: sb + wave, sb + wave + NW, ...; U of them in flight per round. Loads complete in issue order, so the
   // thread's first x chunk (L2) is issued ahead of the first round of weights (HBM): the staging then waits for x
   // only, and its work overlaps the weights' flight
-  WChunk<TW> wc[U][4];
-  float wsc[U][4];
+  WChunk<TW> wc[U][R];
+  float wsc[U][R];
   auto issue = [&](int s0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int st = min(s0 + u * NW, se - 1);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < R; ++r) {
         wc[u][r].load(wr[r] + st * KS);
         if (GS) wsc[u][r] = sr[r][2 * st];
       }
@@ -192,98 +201,177 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
     }
   }
   __syncthreads();
-  float acc[4][MP];
+  // NORM: row m's rsqrt(mean s^2 + eps) factor (TL: once per block, else in the epilogue)
+  auto rs = [&](int m) {
+    float ss = 0.f;
+    for (int w = 0; w < NW; ++w) ss += ssw[w][m];
+    return rsqrtf(ss / (float)K + eps);
+  };
+  float rsf[MP];
+  if (NORM && TL) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+    for (int m = 0; m < MP; ++m) rsf[m] = rs(m);
+  }
+  // acc += this wave's K step st over the lane's rows, weights (and group scales) from w (ws)
+  auto mac = [&](const WChunk<TW>(&w)[R], const float(&ws)[R], int st, float(&acc)[R][MP]) {
+    const int k = (st - sb) * KS + j * E;  // column in the staged x (Kb == K without a split)
+    float part[R][MP];                     // GS: this step's sums, scaled once by the group's scale
 #pragma unroll
-    for (int m = 0; m < MP; ++m) acc[r][m] = 0.f;
-  for (int s0 = sb + wave; s0 < se; s0 += U * NW) {
-    if (s0 != sb + wave) issue(s0);
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int st = s0 + u * NW;
-      if (st >= se) break;
-      const int k = (st - sb) * KS + j * E;  // column in the staged x (Kb == K without a split)
-      float part[4][MP];  // GS: this step's sums, scaled once by the group's scale
+      for (int m = 0; m < MP; ++m) part[r][m] = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+    for (int c = 0; c < E; c += 4) {
+      f32x4 xv[MP];
 #pragma unroll
-        for (int m = 0; m < MP; ++m) part[r][m] = 0.f;
+      for (int m = 0; m < MP; ++m) xv[m] = *reinterpret_cast<const f32x4*>(xs + m * Kb + k + c);
 #pragma unroll
-      for (int c = 0; c < E; c += 4) {
-        f32x4 xv[MP];
+      for (int e = 0; e < 4; ++e) {
 #pragma unroll
-        for (int m = 0; m < MP; ++m) xv[m] = *reinterpret_cast<const f32x4*>(xs + m * Kb + k + c);
+        for (int r = 0; r < R; ++r) {
+          const float wv = w[r].at(c + e);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float wv = wc[u][r].at(c + e);
-#pragma unroll
-            for (int m = 0; m < MP; ++m) {
-              if (GS) part[r][m] += wv * xv[m][e];
-              else acc[r][m] += wv * xv[m][e];
-            }
+          for (int m = 0; m < MP; ++m) {
+            if (GS) part[r][m] += wv * xv[m][e];
+            else acc[r][m] += wv * xv[m][e];
           }
         }
       }
-      if (GS) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int m = 0; m < MP; ++m) acc[r][m] += wsc[u][r] * part[r][m];
-      }
     }
-  }
+    if (GS) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int m = 0; m < MP; ++m) acc[r][m] = row16_sum_f(acc[r][m]);
-  if (j == 0) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int m = 0; m < MP; ++m) red[wave][g + 4 * r][m] = acc[r][m];
-  }
-  __syncthreads();
-  auto rowsum = [&](int rr, int m) {
-    float v = 0.f;
-    for (int w = 0; w < NW; ++w) v += red[w][rr][m];
-    if (NORM) {
-      float ss = 0.f;
-      for (int w = 0; w < NW; ++w) ss += ssw[w][m];
-      v *= rsqrtf(ss / (float)K + eps);
+        for (int m = 0; m < MP; ++m) acc[r][m] += ws[r] * part[r][m];
     }
-    return v;
   };
-  if (EPI != kEpiSwiglu) {
-    if (tid < 16 * MP) {
-      const int rr = tid / MP, m = tid - rr * MP;
-      const int nn = n0 + rr;
-      if (m < M && nn < N) {
-        float v = rowsum(rr, m);
-        if (wscale && !GS) v *= wscale[nn];
-        float* dst = y + m * ldy + nn;
-        if (EPI == kEpiAccumulate && nsplit > 1)
-          __hip_atomic_fetch_add(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-          *dst = EPI == kEpiAccumulate ? *dst + v : v;
+  // the tile's row sums across the waves and its epilogue. red[it & 1] is rewritten two tiles later, after a barrier
+  // that every thread reaches only past this tile's epilogue
+  auto finish = [&](int it, int n0, float(&acc)[R][MP]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MP; ++m) acc[r][m] = row16_sum_f(acc[r][m]);
+    float(*rd)[4 * R][MP] = red[TL ? it & 1 : 0];
+    if (j == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MP; ++m) rd[wave][g + 4 * r][m] = acc[r][m];
+    }
+    __syncthreads();
+    auto rowsum = [&](int rr, int m) {
+      float p[8];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) p[w] = w < NW ? rd[w][rr][m] : 0.f;
+      float v = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      return NORM ? v * (TL ? rsf[m] : rs(m)) : v;
+    };
+    if (EPI != kEpiSwiglu) {
+      if (tid < 4 * R * MP) {
+        const int rr = tid / MP, m = tid - rr * MP;
+        const int nn = n0 + rr;
+        if (m < M && nn < N) {
+          float v = rowsum(rr, m);
+          if (wscale && !GS) v *= wscale[nn];
+          float* dst = y + m * ldy + nn;
+          if (EPI == kEpiAccumulate && nsplit > 1)
+            __hip_atomic_fetch_add(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          else
+            *dst = EPI == kEpiAccumulate ? *dst + v : v;
+        }
       }
+    } else {
+      // rows 2 q and 2 q + 1 of the tile are gate and up of neuron n0 / 2 + q
+      if (tid < 2 * R * MP) {
+        const int qn = tid / MP, m = tid - qn * MP;
+        const int ng = n0 + 2 * qn;
+        const int neuron = ng >> 1;
+        if (m < M && ng + 1 < N) {
+          float gt = rowsum(2 * qn, m), up = rowsum(2 * qn + 1, m);
+          if (wscale && !GS) { gt *= wscale[ng]; up *= wscale[ng + 1]; }
+          float a = gsilu(gt) * up;
+          const int row = min(m / T, 3);
+          for (int p = 0; p < npush; ++p) a = apply_push(pushes + p, neuron, row, a);
+          y[m * ldy + neuron] = a;
+        }
+      }
+    }
+  };
+  if constexpr (!TL) {
+    // one tile per block
+    float acc[R][MP];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MP; ++m) acc[r][m] = 0.f;
+    for (int s0 = sb + wave; s0 < se; s0 += U * NW) {
+      if (s0 != sb + wave) issue(s0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int st = s0 + u * NW;
+        if (st >= se) break;
+        mac(wc[u], wsc[u], st, acc);
+      }
+    }
+    finish(0, tile * 4 * R, acc);
+  } else if constexpr (U == 1) {
+    // at most one K step per wave and tile: the next tile's weights go out before this tile's products, into the
+    // other of two register sets, so two tiles' loads are in flight while the wave computes
+    const int st = sb + wave;
+    const bool has = st < se;
+    WChunk<TW> wb[R];
+    float wbs[R];
+    auto one = [&](int it, const WChunk<TW>(&cur)[R], const float(&cs)[R], WChunk<TW>(&nx)[R], float(&ns)[R]) {
+      const int next = tile + (int)gridDim.x;
+      if (next < ntiles) {
+        set_rows(next);
+        const int sl = min(st, se - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          nx[r].load(wr[r] + sl * KS);
+          if (GS) ns[r] = sr[r][2 * sl];
+        }
+      }
+      float acc[R][MP];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MP; ++m) acc[r][m] = 0.f;
+      if (has) mac(cur, cs, st, acc);
+      finish(it, tile * 4 * R, acc);
+      tile = next;
+      return next < ntiles;
+    };
+    for (int it = 0;; it += 2) {
+      if (!one(it, wc[0], wsc[0], wb, wbs)) break;
+      if (!one(it + 1, wb, wbs, wc[0], wsc[0])) break;
     }
   } else {
-    // rows 2 q and 2 q + 1 of the block are gate and up of neuron blockIdx.x * 8 + q
-    if (tid < 8 * MP) {
-      const int qn = tid / MP, m = tid - qn * MP;
-      const int ng = n0 + 2 * qn;
-      const int neuron = ng >> 1;
-      if (m < M && ng + 1 < N) {
-        float gt = rowsum(2 * qn, m), up = rowsum(2 * qn + 1, m);
-        if (wscale && !GS) { gt *= wscale[ng]; up *= wscale[ng + 1]; }
-        float a = gsilu(gt) * up;
-        const int row = min(m / T, 3);
-        for (int p = 0; p < npush; ++p) a = apply_push(pushes + p, neuron, row, a);
-        y[m * ldy + neuron] = a;
+    for (int it = 0;; ++it) {
+      float acc[R][MP];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MP; ++m) acc[r][m] = 0.f;
+      for (int s0 = sb + wave; s0 < se; s0 += U * NW) {
+        if (s0 != sb + wave) issue(s0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int st = s0 + u * NW;
+          if (st >= se) break;
+          mac(wc[u], wsc[u], st, acc);
+        }
       }
+      // the next tile's first round of weights goes out before this tile's reduction and epilogue
+      const int next = tile + (int)gridDim.x;
+      if (next < ntiles) {
+        set_rows(next);
+        issue(sb + wave);
+      }
+      finish(it, tile * 4 * R, acc);
+      if (next >= ntiles) break;
+      tile = next;
     }
   }
 }
@@ -305,6 +393,14 @@ __global__ __launch_bounds__(256) void swiglu_push_kernel(const float* __restric
 }  // namespace q35
 
 namespace {
+// Blocks of 16 output rows at which a product is split over K: below this many, an accumulating product without the
+// norm splits its K steps so that blocks x splits reaches it (one block per CU of the MI355X).
+constexpr int64_t kGemvSplitTarget = 256;
+// Grid cap: a product with more 16-row tiles (the LM head: 9496) loops each block over tiles blockIdx.x,
+// + gridDim.x, ... (x staged once per block; four 4-wave blocks per CU at 128 VGPRs). The products with fewer tiles
+// take one tile per block, in a kernel without the loop (measured faster for them).
+constexpr int64_t kGemvMaxBlocks = 1024;
+
 struct NormArgs {
   const float* xadd;
   const float* nw;
@@ -321,23 +417,31 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
   constexpr int KS = 16 * WChunk<TW>::kElems;
   const int64_t spb = (K / KS + nsplit - 1) / nsplit;
   const size_t lds = (size_t)mp * spb * KS * sizeof(float);
-  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)nsplit), block(64 * nw);
-#define Q35_GEMV(MP)                                                                                                 \
-  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS>), grid, block, lds, st, x, ldx, W, wscale, y, ldy,    \
+  const int64_t ntiles = (N + 15) / 16;
+  const dim3 grid((unsigned)(ntiles < kGemvMaxBlocks ? ntiles : kGemvMaxBlocks), (unsigned)nsplit), block(64 * nw);
+#define Q35_GEMV(MP, TL)                                                                                             \
+  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS, TL>), grid, block, lds, st, x, ldx, W, wscale, y, ldy, \
                      (int)M, (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps, na.xout)
-  switch (mp) {
-    case 1: Q35_GEMV(1); break;
-    case 2: Q35_GEMV(2); break;
-    case 3: Q35_GEMV(3); break;
-    case 4: Q35_GEMV(4); break;
-    default: Q35_GEMV(8); break;
+  if (ntiles > kGemvMaxBlocks) {
+    switch (mp) {
+      case 1: Q35_GEMV(1, true); break;
+      case 2: Q35_GEMV(2, true); break;
+      case 3: Q35_GEMV(3, true); break;
+      case 4: Q35_GEMV(4, true); break;
+      default: Q35_GEMV(8, true); break;
+    }
+  } else {
+    switch (mp) {
+      case 1: Q35_GEMV(1, false); break;
+      case 2: Q35_GEMV(2, false); break;
+      case 3: Q35_GEMV(3, false); break;
+      case 4: Q35_GEMV(4, false); break;
+      default: Q35_GEMV(8, false); break;
+    }
   }
 #undef Q35_GEMV
 }
 
-// Blocks of output rows at which a product is split over K: below this many, an accumulating product without the norm
-// splits its K steps so that blocks x splits reaches it (one block per CU of the MI355X).
-constexpr int64_t kGemvSplitTarget = 256;
 
 // 4 waves when a block has at most 4 K steps, else 8; each wave's steps all in flight at once up to 4
 template <typename TW, int EPI, bool NORM, bool GS = false>

@@ -128,10 +128,11 @@ def _weights_g128(N, K, seed):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 8224, 1024), (3, 1024, 3584), (3, 1024, 2048), (8, 1000, 2048),
-                                   (2, 4096, 4352)])
+                                   (2, 4096, 4352), (3, 5000, 1024), (3, 40008, 1024), (2, 17000, 3584)])
 def test_gemv_group_scales_store_add_and_norm(M, N, K):
     """Q35_I8_G128 weights: store, accumulate, and the fused residual add + RMSNorm prologue, against the oracle's
-    per-group dequantised product (K 4352 takes the four-steps-per-wave form)."""
+    per-group dequantised product (K 4352 takes the four-steps-per-wave form; N 5000 a ragged last tile; N 40008 and
+    17000 more 16-row tiles than blocks, so blocks loop over tiles, with one and two K steps per wave)."""
     dev = device()
     W, s = _weights_g128(N, K, seed=N + K)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(M))
@@ -155,10 +156,12 @@ def test_gemv_group_scales_store_add_and_norm(M, N, K):
     assert torch.equal(xs.cpu(), hs)
 
 
-def test_gemv_group_scales_swiglu_with_pushes():
-    """Interleaved (gate, up) rows with interleaved group scales through the SwiGLU + push epilogue."""
+@pytest.mark.parametrize("I", [3584, 12000])
+def test_gemv_group_scales_swiglu_with_pushes(I):
+    """Interleaved (gate, up) rows with interleaved group scales through the SwiGLU + push epilogue (I 12000: 1500
+    16-row tiles looped over the blocks)."""
     dev = device()
-    I, H, M = 3584, 1024, 3
+    H, M = 1024, 3
     Wg, sg = _weights_g128(I, H, 21)
     Wu, su = _weights_g128(I, H, 22)
     x = torch.randn(M, H, generator=torch.Generator().manual_seed(23))
@@ -166,7 +169,7 @@ def test_gemv_group_scales_swiglu_with_pushes():
     ref = omlp.swiglu_push(omlp.q8_linear(x, Wg, sg), omlp.q8_linear(x, Wu, su), pushes, T=1)
     Wi = torch.stack([Wg, Wu], dim=1).reshape(2 * I, H)
     si = torch.stack([sg, su], dim=1).reshape(2 * I, H // 128)
-    announce("gemv g128 swiglu")
+    announce(f"gemv g128 swiglu I{I}")
     a = ops.gemv(x.to(dev), Wi.to(dev), si.to(dev), epilogue="swiglu", pushes=ops.pack_pushes(pushes, dev))
     torch.cuda.synchronize()
     assert oracle.rel_err(a.cpu(), ref) <= TOL
