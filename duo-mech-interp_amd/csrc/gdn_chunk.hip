@@ -26,7 +26,9 @@
 // and the records are written with 16- or 8-byte coalesced stores.
 // Kernel 2, gdn_pair_scan_kernel: 16 blocks per (row, head): 8 slices of 16 value columns x 2 halves of the output
 // rows. Each block carries its 128 x 16 fp32 state slice in registers (8 waves x 16 rows) while 4 more waves form the
-// 64 output rows of its half, 4 MFMAs per wave and pair; the bf16 state is exchanged through LDS once per pair.
+// 64 output rows of its half, 4 MFMAs per wave and pair (computed transposed, so that a lane holds 4 consecutive
+// value columns of one position and writes them with one 8-byte store); the bf16 state is exchanged through LDS once
+// per pair.
 // Operands stream straight from L2 into registers three pairs ahead (12 waves keep about 40 KB of loads in flight per
 // CU); a thirteenth wave touches the records several pairs further ahead so that the first of the 16 blocks to need a
 // line finds it in L2. The 16 blocks of a head are placed on one XCD (they share its L2).
@@ -42,11 +44,12 @@ constexpr int kFS = kC + 4;   // row stride (floats) of the fp32 64 x 64 inversi
 
 // Record of one (b, h, pair), bytes. Fragment order: [row tile][k step][lane][8] bf16, lane l holding row
 // 16 rt + l % 16 and columns 32 ks + kmap(l / 16, j) (kmap below); D order: [row tile][slice][lane][4] bf16, lane l
-// holding rows 16 rt + 4 (l / 16) + r of column 16 slice + l % 16 (the MFMA accumulator layout).
+// holding rows 16 rt + 4 (l / 16) + r of column 16 slice + l % 16 (the MFMA accumulator layout); transposed D order:
+// the same tiles with lane l holding row 16 rt + l % 16 and columns 16 slice + 4 (l / 16) + r.
 constexpr size_t kRecM = 0;           // M  = -K~^T W   [128 d][128 d]   fragment order
 constexpr size_t kRecQ = 32768;       // Q'             [128 pos][128 d] fragment order
 constexpr size_t kRecB = 65536;       // Bm = K~^T U    [128 d][128 dv]  D order
-constexpr size_t kRecR = 98304;       // R  = P U       [128 pos][128 dv] D order
+constexpr size_t kRecR = 98304;       // R  = P U       [128 pos][128 dv] transposed D order
 constexpr size_t kRecE = 131072;      // exp(gamma_last) fp32
 constexpr size_t kRecBytes = 131328;  // 256-byte aligned
 
@@ -596,7 +599,8 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const __bf16* __r
 
   // ---- 7. Q' = Q^ e^gamma - P W (as its transpose) and R = P U. Wave w: position tiles 4 (w / 4) .. + 3 (P is zero
   //         above the diagonal: row tile b has b / 2 + 1 k steps), the d' tile pair 2 (w % 4) .. + 1 for Q'^T, the
-  //         value-slice pair 2 (w % 4) .. + 1 for R.
+  //         value-slice pair 2 (w % 4) .. + 1 for R (as its transpose, so that the scan's output tiles come out
+  //         with four consecutive value columns per lane).
   {
     bf16x8 wf[2][4], uf[2][4];
 #pragma unroll
@@ -625,7 +629,7 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const __bf16* __r
 #pragma unroll
           for (int a = 0; a < 2; ++a) {
             qp[a] = mfma16(wf[a][ks], pf[ks], qp[a]);
-            rr[a] = mfma16(pf[ks], uf[a][ks], rr[a]);
+            rr[a] = mfma16(uf[a][ks], pf[ks], rr[a]);  // R^T = U^T P^T: the tile in transposed D order
           }
         }
       }
@@ -668,9 +672,6 @@ __device__ __forceinline__ void scan_coords(int L, int nunits, int& idx, int& un
   }
 }
 
-__device__ __forceinline__ void store_out(__amdgpu_buffer_rsrc_t rc, int off_elems, float x) {
-  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (__bf16)x), rc, off_elems * 2, 0, 0);
-}
 
 // Operands of one pair for one wave of the scan kernel: a state-row-tile wave takes the M fragments and the Bm piece
 // of its tile, an output-tile wave the Q' fragments and the R piece of its tile.
@@ -694,6 +695,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
                                                                         float* s_out, __bf16* __restrict__ o, int T,
                                                                         int NP, int H, int B) {
   __shared__ u32x2 slot[2][8][64];
+  __shared__ u32x2 ostage[2][4][64];  // the output waves' tiles of a pair, stored to memory by wave 12 a pair later
   __shared__ int dummy[64];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -705,8 +707,18 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
   const char* rec0 = ws + (size_t)unit * NP * kRecBytes;
   const int col = 16 * sl + li;
 
+  // Outputs go through a buffer resource spanning row b's [T, H, 128] block: stores past the sequence end fall
+  // outside it and are dropped by the hardware. Lane (li, lg) of output tile ot holds value columns
+  // 16 sl + 4 lg .. + 3 of position 16 ot + li (byte offset below).
+  const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
+      o + (size_t)b * T * H * kD, 0, (int)((size_t)T * H * kD * sizeof(__bf16)), 0x00020000);
+  auto out_off = [&](int pp, int ot) { return ((kP * pp + 16 * ot + li) * H + h) * kD * 2 + (16 * sl + 4 * lg) * 2; };
+
   if (w == 12) {
     // ---------------- L2 warm-up wave: 64 of the 1024 record lines per pair, kTouchAhead pairs ahead ------------
+    // It also stores the output tiles of pair pp - 1 once every wave has met at pair pp's barrier, so that the
+    // output waves' memory counters carry their loads only (a store ahead of a load in a wave's counter holds up
+    // the wait for that load).
     const uint32_t d = lds_addr(dummy);
     const size_t line = (size_t)(64 * idx + lane) * 128;
     for (int pt = kScanAhead; pt < kTouchAhead && pt < NP; ++pt) touch_line(rec0 + (size_t)pt * kRecBytes + line, d);
@@ -714,6 +726,12 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
       const int pt = pp + kTouchAhead;
       if (pt < NP) touch_line(rec0 + (size_t)pt * kRecBytes + line, d);
       lds_barrier();
+      if (pp > 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          __builtin_amdgcn_raw_buffer_store_b64(ostage[(pp - 1) & 1][j][lane], orc, out_off(pp - 1, 4 * half + j), 0,
+                                                0);
+      }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     return;
@@ -778,10 +796,6 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
 
   // ---------------- output row tile 4 half + j ----------------
   const int ot = 4 * half + (w - 8);
-  // Outputs go through a buffer resource spanning row b's [T, H, 128] block: stores past the sequence end fall
-  // outside it and are dropped by the hardware.
-  const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
-      o + (size_t)b * T * H * kD, 0, (int)((size_t)T * H * kD * sizeof(__bf16)), 0x00020000);
   auto load = [&](int pp, OutOps& op) {
     const char* rec = rec0 + (size_t)min(pp, NP - 1) * kRecBytes;
 #pragma unroll
@@ -789,16 +803,21 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
       op.qf[ks] = *reinterpret_cast<const bf16x8*>(rec + kRecQ + ((size_t)(ot * 4 + ks) * 64 + lane) * 16);
     op.rv = *reinterpret_cast<const u32x2*>(rec + kRecR + ((size_t)(ot * 8 + sl) * 64 + lane) * 8);
   };
+  // O^T = S^T Q'^T + R^T: the state fragments as the A operand and Q' as B, so that lane (li, lg) holds value
+  // columns 16 sl + 4 lg .. + 3 of position 16 ot + li (8 bytes). The tile goes to LDS for wave 12 to store, except
+  // the last pair's, which is stored here (no barrier follows it).
   auto step = [&](int pp, const OutOps& op) {
     lds_barrier();
     bf16x8 sb[4];
     gather(pp, sb);
     f32x4 acc = unpack4(op.rv);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = mfma16(op.qf[ks], sb[ks], acc);
-    const int tb = kP * pp + 16 * ot + 4 * lg;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) store_out(orc, ((tb + r) * H + h) * kD + col, acc[r]);
+    for (int ks = 0; ks < 4; ++ks) acc = mfma16(sb[ks], op.qf[ks], acc);
+    const u32x2 pk = pack4(acc[0], acc[1], acc[2], acc[3]);
+    if (pp + 1 < NP)
+      ostage[pp & 1][w - 8][lane] = pk;
+    else
+      __builtin_amdgcn_raw_buffer_store_b64(pk, orc, out_off(pp, ot), 0, 0);
   };
   OutOps o0, o1, o2;
   load(0, o0);
