@@ -49,6 +49,13 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
                : "memory", "m0");
 }
 
+// a pointer the compiler cannot prove uniform, moved to scalar registers
+template <typename T> __device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  return reinterpret_cast<T*>(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                              (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a));
+}
+
 // key order inside a group of 16 keys in V^T (an involution: swaps bits 2 and 3)
 __device__ __forceinline__ int vperm(int p) { return (p & 3) | ((p & 4) << 1) | ((p & 8) >> 1); }
 
@@ -261,8 +268,9 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
   const int half = rot >> 1;
   const int ln = lane & 31, hh = lane >> 5;
   const size_t head = (size_t)b * Hkv + kvh;
-  const char* kbase = reinterpret_cast<const char*>(kr + head * Tp * kPD);
-  const char* vbase = reinterpret_cast<const char*>(vt + head * kPD * Tp);
+  // uniform bases (scalar registers): the tile copies' addresses are then scalar arithmetic
+  const char* kbase = uniform_ptr(reinterpret_cast<const char*>(kr + head * Tp * kPD));
+  const char* vbase = uniform_ptr(reinterpret_cast<const char*>(vt + head * kPD * Tp));
   // Cached mode (pos_dev set): the keys are the KV-cache rows 0 .. P + T - 1 of this row, P = pos_dev[b] the
   // position of the call's first token (kr is the cache itself, Tp its length); query t sits at position P + t and
   // attends to keys 0 .. P + t. Otherwise the keys are the call's own T tokens at positions pos0 .. pos0 + T - 1.
@@ -384,6 +392,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     // Raw scores of tile kt into sc (S^T = K Q^T, causally masked with -inf); returns this lane's query's max of the
     // raw scores over the tile's keys.
     auto tile_scores = [&](int kt, f32x16 (&sc)[2]) -> float {
+      kt = __builtin_amdgcn_readfirstlane(kt);  // uniform: the tile copies' addresses stay scalar
       const int s = kt & 1;
       // this wave's copies of tile kt are its only ones in flight; after the barrier every wave's have landed and
       // every wave is done with tile kt - 1, whose stage then receives tile kt + 1
@@ -454,6 +463,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     // keys (4 steps of 16). The MFMAs run K step by K step, so those of step kk need only P's group kk: the
     // exponentials of later groups overlap the matrix core.
     auto tile_accumulate = [&](int kt, const f32x16 (&sc)[2]) {
+      kt = __builtin_amdgcn_readfirstlane(kt);
       const char* vl = reinterpret_cast<const char*>(&stage[kt & 1].v[0]);
       auto vread = [&](int kk, bf16x8 (&vf)[8]) {
 #pragma unroll
