@@ -400,10 +400,10 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
       __syncthreads();
       if (kt + 1 < it.kt1) copy_tile(kt + 1, s ^ 1);
       const char* kl = reinterpret_cast<const char*>(&stage[s].k[0]);
-      // four accumulation chains (two per 32-key half: even and odd K steps) over four groups of four K steps; the K
+      // two accumulation chains (one per 32-key half, issued alternately) over four groups of four K steps; the K
       // fragments of group g + 1 are read while the MFMAs of group g run, so LDS latency is hidden behind the matrix
       // core
-      f32x16 acc[2][2] = {{zero16(), zero16()}, {zero16(), zero16()}};
+      f32x16 acc[2] = {zero16(), zero16()};
       auto kread = [&](int g, bf16x8 (&kf)[2][4]) {
 #pragma unroll
         for (int ksub = 0; ksub < 2; ++ksub)
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int ksub = 0; ksub < 2; ++ksub)
-            acc[ksub][j & 1] = mfma32(cur[ksub][j], qop[4 * g + j], acc[ksub][j & 1]);
+            acc[ksub] = mfma32(cur[ksub][j], qop[4 * g + j], acc[ksub]);
       }
       // order: reads of group 0; then (reads of g + 1, MFMAs of g) for g = 0..2; then the MFMAs of group 3
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
@@ -443,8 +443,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int key = kl0 + 32 * ksub + 8 * (i >> 2) + (i & 3);
-            const float x = (key <= tq + qshift && key < T + qshift) ? acc[ksub][0][i] + acc[ksub][1][i]
-                                                                          : -INFINITY;
+            const float x = (key <= tq + qshift && key < T + qshift) ? acc[ksub][i] : -INFINITY;
             sc[ksub][i] = x;
             mx = fmaxf(mx, x);
           }
@@ -453,7 +452,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
         for (int ksub = 0; ksub < 2; ++ksub)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            sc[ksub][i] = acc[ksub][0][i] + acc[ksub][1][i];
+            sc[ksub][i] = acc[ksub][i];
             mx = fmaxf(mx, sc[ksub][i]);
           }
       }
