@@ -287,20 +287,25 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
   constexpr int CPW = 32 / GW;
   const uint32_t kcl = 512 * (lane >> 5) + 16 * ((lane & 31) ^ (lane >> 5));
   const uint32_t vcl = (uint32_t)(lane >> 3) * (uint32_t)(2 * Tp) + 16 * ((lane & 7) ^ (lane >> 4));
-  auto copy_tile = [&](int kt, int s) {
+  // parts: 1 the K tile, 2 the V^T tile
+  auto copy_tile = [&](int kt, int s, int parts) {
     const int key0 = kt * kBN;
     const uint32_t kl = lds_u32(&stage[s].k[0]), vl = lds_u32(&stage[s].v[0]);
+    if (parts & 1) {
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) {
-      const int c = CPW * wave + i;  // copy index 0..31
-      dma16s(kbase + (size_t)key0 * (kPD * 2) + 1024 * c, kcl ^ (16u * ((2 * c) & 15)),
-             __builtin_amdgcn_readfirstlane(kl + 1024 * c));
+      for (int i = 0; i < CPW; ++i) {
+        const int c = CPW * wave + i;  // copy index 0..31
+        dma16s(kbase + (size_t)key0 * (kPD * 2) + 1024 * c, kcl ^ (16u * ((2 * c) & 15)),
+               __builtin_amdgcn_readfirstlane(kl + 1024 * c));
+      }
     }
+    if (parts & 2) {
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) {
-      const int c = CPW * wave + i;
-      dma16s(vbase + (size_t)8 * c * (Tp * 2) + (size_t)key0 * 2, vcl ^ (64u * (c & 1)),
-             __builtin_amdgcn_readfirstlane(vl + 1024 * c));
+      for (int i = 0; i < CPW; ++i) {
+        const int c = CPW * wave + i;
+        dma16s(vbase + (size_t)8 * c * (Tp * 2) + (size_t)key0 * 2, vcl ^ (64u * (c & 1)),
+               __builtin_amdgcn_readfirstlane(vl + 1024 * c));
+      }
     }
   };
 
@@ -344,7 +349,7 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
           }
         }
       }
-      copy_tile(it.kt0, it.kt0 & 1);
+      copy_tile(it.kt0, it.kt0 & 1, 3);
 #pragma unroll
       for (int ks = 0; ks < 16; ++ks) {
         const u32x4 r = raw[ks];
@@ -398,7 +403,9 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
       // every wave is done with tile kt - 1, whose stage then receives tile kt + 1
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if (kt + 1 < it.kt1) copy_tile(kt + 1, s ^ 1);
+      // tile kt + 1: its K now, its V^T during this tile's accumulation (the two halves of the copy traffic into LDS
+      // go with the two phases of the tile)
+      if (kt + 1 < it.kt1) copy_tile(kt + 1, s ^ 1, 1);
       const char* kl = reinterpret_cast<const char*>(&stage[s].k[0]);
       // two accumulation chains (one per 32-key half, issued alternately) over four groups of four K steps; the K
       // fragments of group g + 1 are read while the MFMAs of group g run, so LDS latency is hidden behind the matrix
@@ -463,6 +470,8 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     // exponentials of later groups overlap the matrix core.
     auto tile_accumulate = [&](int kt, const f32x16 (&sc)[2]) {
       kt = __builtin_amdgcn_readfirstlane(kt);
+      // stage kt + 1 held tile kt - 1, which every wave finished before this tile's barrier
+      if (kt + 1 < it.kt1) copy_tile(kt + 1, (kt & 1) ^ 1, 2);
       const char* vl = reinterpret_cast<const char*>(&stage[kt & 1].v[0]);
       auto vread = [&](int kk, bf16x8 (&vf)[8]) {
 #pragma unroll
