@@ -35,7 +35,7 @@ GDN_PREFILL_FLOPS = 1.190e10
 # HBM bytes one GDN prefill launch (prep + scan kernels) actually moves: rocprofv3 FETCH_SIZE / WRITE_SIZE per
 # dispatch, each scaled by what the counter reads for a 256 MiB device copy
 # (profiles/counters_gdn_attn_gemm_kernels.md)
-GDN_PREFILL_TRAFFIC_BYTES = 208_700_000
+GDN_PREFILL_TRAFFIC_BYTES = 208_100_000
 GDN_DECODE_STEP_BYTES = 2_130_048   # S read + write fp32 + q,k,v,o,g,beta (B 1, H 16, d 128)
 ATTN_PREFILL_FLOPS = 6.874e10       # 4 * D * Hq * T (T + 1) / 2, T 4096, Hq 8, D 256
 ATTN_PREFILL_BYTES = 58_720_256
