@@ -344,6 +344,109 @@ __global__ __launch_bounds__(1024) void gdn_decode_fused_kernel(
   }
 }
 
+// The recurrent part of a GDN decode step (T = 1), split over four blocks of 256 threads per (head h, row b), for
+// Hk = Hv and dk = dv = 128, after an input projection whose epilogue already ran the causal conv + SiLU
+// (q35_gemv_norm_conv): q, k, v of head h are read straight from the projection row y. Block (j, h, b) updates
+// state columns 32 j .. 32 j + 31 with gdn_recurrent_kernel's thread layout (slice j of the fused kernel, so the
+// column sums are formed in the same order), computes beta and g from the row's b and a columns, and writes those
+// 32 columns of the head's raw output o; the gated RMSNorm is left to the output projection (q35_gemv_gated_norm).
+// 192 blocks at B 3, H 16 against the fused kernel's 48: a quarter of the state bytes per CU.
+__global__ __launch_bounds__(256) void gdn_decode_sliced_kernel(
+    const float* __restrict__ y, int64_t ldy, const float* __restrict__ A_log, const float* __restrict__ dt_bias,
+    int b_off, int a_off, float* __restrict__ S, float scale, float* __restrict__ out, int H) {
+  Q35_ARGS_UPFRONT(y, ldy, A_log, dt_bias, b_off, a_off, S, scale, out, H);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sj = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const float* row = y + (int64_t)b * ldy;
+  __shared__ f32x4 red[4][8][2];  // [wave][column quad][S^T k | S^T q]
+  __shared__ float gates[2];      // beta, g
+
+  // ---- 0. every load first: the state slice, this thread's q and k rows, the lane pairs of q and k for the norms,
+  //         the column quad of v, the gate inputs (thread 0)
+  const int cq = tid & 7, rg = tid >> 3;
+  const int j0 = 32 * sj + 4 * cq;
+  float* sb = S + ((size_t)b * H + h) * kFD * kFD;
+  f32x4 s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = *reinterpret_cast<const f32x4*>(sb + (size_t)(rg + 32 * i) * kFD + j0);
+  const float* qv = row + (size_t)h * kFD;
+  const float* kv = row + (size_t)(H + h) * kFD;
+  const float* vv = row + (size_t)(2 * H + h) * kFD;
+  float kr[4], qr[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kr[i] = kv[rg + 32 * i];
+    qr[i] = qv[rg + 32 * i];
+  }
+  const float q20 = qv[2 * lane], q21 = qv[2 * lane + 1], k20 = kv[2 * lane], k21 = kv[2 * lane + 1];
+  const f32x4 v4 = *reinterpret_cast<const f32x4*>(vv + j0);
+  float gb = 0.f, ga = 0.f, gA = 0.f, gdt = 0.f;
+  if (tid == 0) {
+    gb = row[b_off + h];
+    ga = row[a_off + h];
+    gA = A_log[h];
+    gdt = dt_bias[h];
+  }
+
+  // ---- 1. column sums of S k and S q over the slice's rows (the fused kernel's order), the norms, the gates
+  f32x4 a, c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = s[0][e] * kr[0] + s[1][e] * kr[1] + s[2][e] * kr[2] + s[3][e] * kr[3];
+    c[e] = s[0][e] * qr[0] + s[1][e] * qr[1] + s[2][e] * qr[2] + s[3][e] * qr[3];
+  }
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a[e] += __shfl_xor(a[e], off, 64);
+      c[e] += __shfl_xor(c[e], off, 64);
+    }
+  }
+  if (lane < 8) {
+    red[wave][lane][0] = a;
+    red[wave][lane][1] = c;
+  }
+  if (tid == 0) {
+    gates[0] = 1.f / (1.f + __expf(-gb));
+    gates[1] = -__expf(gA) * softplus_f(ga + gdt);
+  }
+  float sq = q20 * q20 + q21 * q21;
+  float sk = k20 * k20 + k21 * k21;
+  float sqk = q20 * k20 + q21 * k21;
+  sq = wave_sum(sq);
+  sk = wave_sum(sk);
+  sqk = wave_sum(sqk);
+  __syncthreads();
+
+  // ---- 2. the update of the slice and its 32 output columns
+  f32x4 A = red[0][cq][0], Cs = red[0][cq][1];
+#pragma unroll
+  for (int w2 = 1; w2 < 4; ++w2) {
+    const f32x4 a2 = red[w2][cq][0], c2 = red[w2][cq][1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { A[e] += a2[e]; Cs[e] += c2[e]; }
+  }
+  const float rk = rsqrtf(sk + 1e-6f);
+  const float rqs = rsqrtf(sq + 1e-6f) * scale;
+  const float qk = sqk * rqs * rk;
+  const float beta = gates[0], alpha = expf(gates[1]);
+  float kk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kk[i] = kr[i] * rk;
+  f32x4 o4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float d = beta * (v4[e] - alpha * rk * A[e]);
+    o4[e] = alpha * rqs * Cs[e] + qk * d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i][e] = alpha * s[i][e] + kk[i] * d;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *reinterpret_cast<f32x4*>(sb + (size_t)(rg + 32 * i) * kFD + j0) = s[i];
+  if (rg == 0) *reinterpret_cast<f32x4*>(out + ((size_t)b * H + h) * kFD + j0) = o4;
+}
+
 // One wave per (token m, head h) of o [M, Hv, dv]; dv = 128 (two values per lane). Four waves per block.
 template <typename T>
 __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict__ o, const float* __restrict__ z,
@@ -525,6 +628,23 @@ extern "C" int q35_gdn_decode_fused(const float* y, int64_t ldy, const float* co
   hipLaunchKernelGGL(gdn_decode_fused_kernel, dim3((unsigned)H, (unsigned)B), dim3(1024), 0, st, y, ldy, conv_w,
                      conv_bias, conv_state, A_log, dt_bias, (int)b_off, (int)a_off, (int)z_off, state, norm_w,
                      head_scale, eps, scale, out, (int)H, (int)C, (int)K);
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+extern "C" int q35_gdn_decode_sliced(const float* y, int64_t ldy, const float* A_log, const float* dt_bias,
+                                     int64_t b_off, int64_t a_off, float* state, float scale, float* out, int64_t B,
+                                     int64_t H, int64_t d, q35_stream_t stream) {
+  using namespace q35;
+  if (!y || !A_log || !dt_bias || !state || !out) return Q35_EINVAL;
+  if (B <= 0 || H <= 0 || d <= 0) return Q35_EINVAL;
+  const int64_t C = 3 * H * d;
+  if (ldy < C || b_off < 0 || a_off < 0 || b_off + H > ldy || a_off + H > ldy) return Q35_EINVAL;
+  if (d != kFD || (ldy & 3) || ((uintptr_t)y & 15) || ((uintptr_t)state & 15) || ((uintptr_t)out & 15))
+    return Q35_EUNSUPPORTED;
+  if (B > 65535 || H > 65535 || B * ldy > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(gdn_decode_sliced_kernel, dim3(4, (unsigned)H, (unsigned)B), dim3(256), 0, st, y, ldy, A_log,
+                     dt_bias, (int)b_off, (int)a_off, state, scale, out, (int)H);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 

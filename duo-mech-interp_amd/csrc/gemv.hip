@@ -29,7 +29,20 @@
 
 namespace q35 {
 
-enum GemvEpi : int { kEpiStore = 0, kEpiAccumulate = 1, kEpiSwiglu = 2 };
+enum GemvEpi : int { kEpiStore = 0, kEpiAccumulate = 1, kEpiSwiglu = 2, kEpiConv = 3 };
+constexpr int kGemvConvMaxK = 8;  // conv taps supported by the conv epilogue
+constexpr int kGemvHead = 128;    // head size of the gated-norm prologue
+
+// Operands of the gated-norm prologue (GN) and of the conv epilogue (kEpiConv); unused by the other forms.
+struct GemvAux {
+  const float* z;    // GN: gate rows z[m * ldz + k]
+  int64_t ldz;
+  const float* hs;   // GN: per-head scale (may be NULL)
+  const float* cw;   // conv: weights [cc][ck]
+  const float* cb;   // conv: bias [cc] (may be NULL)
+  float* cst;        // conv: state [M][ck - 1][cc]
+  int cc, ck;        // conv: channels (outputs 0 .. cc - 1 are convolved), taps
+};
 
 __device__ __forceinline__ float gsilu(float x) { return x / (1.f + __expf(-x)); }
 
@@ -73,14 +86,16 @@ __device__ __forceinline__ float row16_sum_f(float v) {
 
 // NORM: x is a residual row; the kernel adds xadd (may be NULL), writes the sum to xout from block 0 (may be NULL),
 // and multiplies the RMSNorm of the sum, s * rsqrt(mean s^2 + eps) * (1 + nw), instead of x (HF:720-734).
-template <typename TW, int MP, int EPI, int U, bool NORM, bool GS, bool TL, int R = 4>
+template <typename TW, int MP, int EPI, int U, bool NORM, bool GS, bool TL, int R = 4, bool GN = false>
 __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, int64_t ldx, const TW* __restrict__ W,
                                                    const float* __restrict__ wscale, float* __restrict__ y,
                                                    int64_t ldy, int M, int N, int K,
                                                    const q35_push* __restrict__ pushes, int npush, int T,
                                                    const float* __restrict__ xadd, const float* __restrict__ nw,
-                                                   float eps, float* __restrict__ xout) {
+                                                   float eps, float* __restrict__ xout, GemvAux aux) {
   Q35_ARGS_UPFRONT(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, xadd, nw, eps, xout);
+  static_assert(!(GN && NORM), "one prologue");
+  static_assert(EPI != kEpiConv || !TL, "the conv epilogue takes one tile per block");
   constexpr int E = WChunk<TW>::kElems;  // weights per lane per 16-byte load
   constexpr int KS = 16 * E;             // inputs per K step
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [MP][K]
@@ -150,7 +165,45 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
     const int m0 = kf / Kb, k0 = kf - m0 * Kb;
     if (m0 < M && kf < MP * Kb) fv[0] = *reinterpret_cast<const f32x4*>(x + m0 * ldx + kb0 + k0);
   }
+  // GN: the gated norm's operands of the thread's first kGnPre chunks (o, z, the norm weight, the head scale), all
+  // loaded before the weights, so that the staging does not wait behind them
+  constexpr int kGnPre = GN ? 2 : 1;
+  f32x4 go[kGnPre], gz[kGnPre], gw[kGnPre];
+  float gh[kGnPre];
+  if constexpr (GN) {
+#pragma unroll
+    for (int j = 0; j < kGnPre; ++j) {
+      go[j] = zero4(); gz[j] = zero4(); gw[j] = zero4(); gh[j] = 1.f;
+      const int i = tid + j * (int)blockDim.x;
+      const int m = (4 * i) / Kb, kk = kb0 + 4 * i - m * Kb;
+      if (i < MP * Kb / 4 && m < M) {
+        go[j] = *reinterpret_cast<const f32x4*>(x + m * ldx + kk);
+        gz[j] = *reinterpret_cast<const f32x4*>(aux.z + m * aux.ldz + kk);
+        gw[j] = *reinterpret_cast<const f32x4*>(nw + (kk & (kGemvHead - 1)));
+        if (aux.hs) gh[j] = aux.hs[kk / kGemvHead];
+      }
+    }
+  }
   issue(sb + wave);
+  // kEpiConv: the epilogue thread of (output row rr, row m) holds its channel's taps, bias and conv state, loaded
+  // behind the weights (the epilogue needs the weights' products first anyway)
+  float cvw[kGemvConvMaxK], cvs[kGemvConvMaxK - 1], cvb = 0.f;
+  if constexpr (EPI == kEpiConv) {
+#pragma unroll
+    for (int i = 0; i < kGemvConvMaxK; ++i) cvw[i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kGemvConvMaxK - 1; ++i) cvs[i] = 0.f;
+    const int rr = tid / MP, m = tid - rr * MP, nn = blockIdx.x * 4 * R + rr;
+    if (tid < 4 * R * MP && m < M && nn < aux.cc) {
+#pragma unroll
+      for (int i = 0; i < kGemvConvMaxK; ++i)
+        if (i < aux.ck) cvw[i] = aux.cw[(size_t)nn * aux.ck + i];
+#pragma unroll
+      for (int i = 0; i < kGemvConvMaxK - 1; ++i)
+        if (i < aux.ck - 1) cvs[i] = aux.cst[((size_t)m * (aux.ck - 1) + i) * aux.cc + nn];
+      if (aux.cb) cvb = aux.cb[nn];
+    }
+  }
   asm volatile("" ::: "memory");
   if (NORM) {
     float ss[MP];
@@ -191,6 +244,33 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
 #pragma unroll
       for (int off = 32; off > 0; off >>= 1) ss[m] += __shfl_xor(ss[m], off, 64);
       if (lane == 0) ssw[wave][m] = ss[m];
+    }
+  } else if (GN) {
+    // gated RMSNorm per head of 128 inputs (the fused GDN decode step's order): x * r * w * silu(z) * hs, with
+    // r = rsqrt(mean x^2 + eps) over the head. Kb and kb0 are multiples of 128, so the 32 quads of a head are 32
+    // consecutive i: one half wave, reduced with shuffles inside it (a half wave is wholly in or out of the loop)
+    for (int j = 0, i = tid; i < MP * Kb / 4; ++j, i += blockDim.x) {
+      const int m = (4 * i) / Kb, k = 4 * i - m * Kb, kk = kb0 + k;
+      f32x4 o = zero4(), zz = zero4(), w = zero4();
+      float hsc = 1.f;
+      if (j < kGnPre) {
+#pragma unroll
+        for (int jj = 0; jj < kGnPre; ++jj)
+          if (jj == j) { o = go[jj]; zz = gz[jj]; w = gw[jj]; hsc = gh[jj]; }
+      } else if (m < M) {
+        o = *reinterpret_cast<const f32x4*>(x + m * ldx + kk);
+        zz = *reinterpret_cast<const f32x4*>(aux.z + m * aux.ldz + kk);
+        w = *reinterpret_cast<const f32x4*>(nw + (kk & (kGemvHead - 1)));
+        if (aux.hs) hsc = aux.hs[kk / kGemvHead];
+      }
+      float ss = o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3];
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off, 64);
+      const float r = rsqrtf(ss * (1.f / kGemvHead) + eps);
+      f32x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = w[e] * (o[e] * r) * gsilu(zz[e]) * hsc;
+      *reinterpret_cast<f32x4*>(xs + m * Kb + k) = v;
     }
   } else {
     for (int i = tid; i < MP * Kb / 4; i += blockDim.x) {
@@ -275,10 +355,26 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
           float v = rowsum(rr, m);
           if (wscale && !GS) v *= wscale[nn];
           float* dst = y + m * ldy + nn;
-          if (EPI == kEpiAccumulate && nsplit > 1)
+          if (EPI == kEpiConv && nn < aux.cc) {
+            // causal conv over the channel's last ck inputs (the conv state, then v) + SiLU; state <- [rows 1.. | v]
+            float a = cvb;
+#pragma unroll
+            for (int i = 0; i < kGemvConvMaxK; ++i) {
+              if (i >= aux.ck) break;
+              a += cvw[i] * (i < aux.ck - 1 ? cvs[i] : v);
+            }
+            float* cs = aux.cst + (size_t)m * (aux.ck - 1) * aux.cc + nn;
+#pragma unroll
+            for (int i = 0; i < kGemvConvMaxK - 1; ++i) {
+              if (i >= aux.ck - 1) break;
+              cs[(size_t)i * aux.cc] = i + 1 < aux.ck - 1 ? cvs[i + 1] : v;
+            }
+            *dst = a / (1.f + __expf(-a));
+          } else if (EPI == kEpiAccumulate && nsplit > 1) {
             __hip_atomic_fetch_add(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          else
+          } else {
             *dst = EPI == kEpiAccumulate ? *dst + v : v;
+          }
         }
       }
     } else {
@@ -406,9 +502,10 @@ struct NormArgs {
   const float* nw;
   float eps;
   float* xout;
+  q35::GemvAux aux;
 };
 
-template <typename TW, int EPI, int U, bool NORM, bool GS>
+template <typename TW, int EPI, int U, bool NORM, bool GS, bool GN>
 void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
                    int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, int nw, int nsplit,
                    const NormArgs& na, hipStream_t st) {
@@ -419,10 +516,18 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
   const size_t lds = (size_t)mp * spb * KS * sizeof(float);
   const int64_t ntiles = (N + 15) / 16;
   const dim3 grid((unsigned)(ntiles < kGemvMaxBlocks ? ntiles : kGemvMaxBlocks), (unsigned)nsplit), block(64 * nw);
-#define Q35_GEMV(MP, TL)                                                                                             \
-  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS, TL>), grid, block, lds, st, x, ldx, W, wscale, y, ldy, \
-                     (int)M, (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps, na.xout)
-  if (ntiles > kGemvMaxBlocks) {
+#define Q35_GEMV(MP, TL)                                                                                           \
+  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS, TL, 4, GN>), grid, block, lds, st, x, ldx, W, wscale, \
+                     y, ldy, (int)M, (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps, na.xout, na.aux)
+  if constexpr (EPI == kEpiConv) {  // one tile per block (the entry point bounds N)
+    switch (mp) {
+      case 1: Q35_GEMV(1, false); break;
+      case 2: Q35_GEMV(2, false); break;
+      case 3: Q35_GEMV(3, false); break;
+      case 4: Q35_GEMV(4, false); break;
+      default: Q35_GEMV(8, false); break;
+    }
+  } else if (ntiles > kGemvMaxBlocks) {
     switch (mp) {
       case 1: Q35_GEMV(1, true); break;
       case 2: Q35_GEMV(2, true); break;
@@ -444,7 +549,7 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
 
 
 // 4 waves when a block has at most 4 K steps, else 8; each wave's steps all in flight at once up to 4
-template <typename TW, int EPI, bool NORM, bool GS = false>
+template <typename TW, int EPI, bool NORM, bool GS = false, bool GN = false>
 int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
                 int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, const NormArgs& na,
                 hipStream_t st) {
@@ -463,11 +568,11 @@ int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, f
   const int nw = bsteps <= 4 ? 4 : 8;
   const int64_t per_wave = (bsteps + nw - 1) / nw;
   if (per_wave <= 1)
-    gemv_launch_u<TW, EPI, 1, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
+    gemv_launch_u<TW, EPI, 1, NORM, GS, GN>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
   else if (per_wave <= 2)
-    gemv_launch_u<TW, EPI, 2, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
+    gemv_launch_u<TW, EPI, 2, NORM, GS, GN>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
   else
-    gemv_launch_u<TW, EPI, 4, NORM, GS>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
+    gemv_launch_u<TW, EPI, 4, NORM, GS, GN>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 
@@ -516,7 +621,7 @@ extern "C" int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype,
                         int64_t npush, int64_t T, q35_stream_t stream) {
   const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T);
   if (chk != Q35_OK) return chk;
-  const NormArgs na = {nullptr, nullptr, 0.f, nullptr};
+  const NormArgs na = {nullptr, nullptr, 0.f, nullptr, {}};
   return gemv_dispatch<false>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, (int)npush, T, na,
                               reinterpret_cast<hipStream_t>(stream));
 }
@@ -535,9 +640,73 @@ extern "C" int q35_gemv_norm(const float* x, const float* x_add, float* x_out, i
     return a && x_out && a < x_out + (M - 1) * ldx + K && x_out < a + (M - 1) * ldx + K;
   };
   if (overlap(x) || overlap(x_add)) return Q35_EINVAL;
-  const NormArgs na = {x_add, norm_w, eps, x_out};
+  const NormArgs na = {x_add, norm_w, eps, x_out, {}};
   return gemv_dispatch<true>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, (int)npush, T, na,
                              reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int q35_gemv_norm_conv(const float* x, const float* x_add, float* x_out, int64_t ldx,
+                                  const float* norm_w, float eps, const void* W, int w_dtype, const float* w_scale,
+                                  float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, const float* conv_w,
+                                  const float* conv_bias, float* conv_state, int64_t conv_channels, int64_t conv_k,
+                                  q35_stream_t stream) {
+  using namespace q35;
+  const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, kEpiStore, nullptr, 0, 1);
+  if (chk != Q35_OK) return chk;
+  if (!norm_w || !conv_w || !conv_state || conv_channels <= 0 || conv_channels > N || conv_k < 2) return Q35_EINVAL;
+  if (conv_k > kGemvConvMaxK || (N + 15) / 16 > kGemvMaxBlocks || conv_channels * conv_k > 0x7fffffff)
+    return Q35_EUNSUPPORTED;
+  if (((uintptr_t)norm_w & 15) || (x_add && ((uintptr_t)x_add & 15)) || (x_out && ((uintptr_t)x_out & 15)))
+    return Q35_EUNSUPPORTED;
+  auto overlap = [&](const float* a) {
+    return a && x_out && a < x_out + (M - 1) * ldx + K && x_out < a + (M - 1) * ldx + K;
+  };
+  if (overlap(x) || overlap(x_add)) return Q35_EINVAL;
+  NormArgs na = {x_add, norm_w, eps, x_out, {}};
+  na.aux.cw = conv_w;
+  na.aux.cb = conv_bias;
+  na.aux.cst = conv_state;
+  na.aux.cc = (int)conv_channels;
+  na.aux.ck = (int)conv_k;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (w_dtype == Q35_I8_G128)
+    return gemv_launch<int8_t, kEpiConv, true, true>(x, ldx, (const int8_t*)W, w_scale, y, ldy, M, N, K, nullptr, 0,
+                                                      1, na, st);
+  if (w_dtype == Q35_I8)
+    return gemv_launch<int8_t, kEpiConv, true>(x, ldx, (const int8_t*)W, w_scale, y, ldy, M, N, K, nullptr, 0, 1, na,
+                                               st);
+  return gemv_launch<float, kEpiConv, true>(x, ldx, (const float*)W, w_scale, y, ldy, M, N, K, nullptr, 0, 1, na, st);
+}
+
+extern "C" int q35_gemv_gated_norm(const float* o, int64_t ldo, const float* z, int64_t ldz, const float* norm_w,
+                                   const float* head_scale, float eps, const void* W, int w_dtype,
+                                   const float* w_scale, float* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                                   int epilogue, q35_stream_t stream) {
+  using namespace q35;
+  const int chk = gemv_check(o, ldo, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, nullptr, 0, 1);
+  if (chk != Q35_OK) return chk;
+  if (!z || !norm_w || ldz < K || (epilogue != kEpiStore && epilogue != kEpiAccumulate)) return Q35_EINVAL;
+  // the prologue normalises whole heads of 128 inputs: int8 weights (K steps of 256) keep every split head-aligned
+  if (w_dtype == Q35_F32) return Q35_EUNSUPPORTED;
+  if ((ldz & 3) || ((uintptr_t)z & 15) || ((uintptr_t)norm_w & 15)) return Q35_EUNSUPPORTED;
+  NormArgs na = {nullptr, norm_w, eps, nullptr, {}};
+  na.aux.z = z;
+  na.aux.ldz = ldz;
+  na.aux.hs = head_scale;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int8_t* w8 = (const int8_t*)W;
+  if (w_dtype == Q35_I8_G128) {
+    if (epilogue == kEpiStore)
+      return gemv_launch<int8_t, kEpiStore, false, true, true>(o, ldo, w8, w_scale, y, ldy, M, N, K, nullptr, 0, 1,
+                                                               na, st);
+    return gemv_launch<int8_t, kEpiAccumulate, false, true, true>(o, ldo, w8, w_scale, y, ldy, M, N, K, nullptr, 0, 1,
+                                                                  na, st);
+  }
+  if (epilogue == kEpiStore)
+    return gemv_launch<int8_t, kEpiStore, false, false, true>(o, ldo, w8, w_scale, y, ldy, M, N, K, nullptr, 0, 1, na,
+                                                              st);
+  return gemv_launch<int8_t, kEpiAccumulate, false, false, true>(o, ldo, w8, w_scale, y, ldy, M, N, K, nullptr, 0, 1,
+                                                                 na, st);
 }
 
 extern "C" int q35_swiglu_push(const float* gu, float* a, int64_t M, int64_t I, const q35_push* pushes,

@@ -72,7 +72,23 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     C, Vd = 2 * Hk * dk + Hv * dv, Hv * dv
     # one GEMM for every projection of the token: y row = [qkv (C) | z (Vd) | b (Hv) | a (Hv)], the engine's fused
     # layout (engine/kernels_qwen35.js:129-131)
-    y = linear(x, gdn_in_weight(p), *_q8(p, "_in_fused"), prenorm=prenorm)
+    w_in = gdn_in_weight(p)
+    wq_in, ws_in = _q8(p, "_in_fused")
+    wq_out, ws_out = _q8(p, "out_proj")
+    if (T == 1 and Hk == Hv and dk == dv == 128 and x.dtype == torch.float32 and B <= 8 and x.shape[-1] % 256 == 0
+            and Vd % 256 == 0 and wq_in is not None and wq_out is not None):
+        # decode step on int8 projections: the causal conv + SiLU in the input projection's epilogue (each channel
+        # has one owner there, so its conv state advances in place), the recurrent rule over four blocks per head,
+        # and the gated RMSNorm in the output projection's staging (the same arithmetic as the fused step below)
+        y = linear(x, w_in, wq_in, ws_in, prenorm=prenorm, conv=(p["conv1d"], None, conv_state))
+        y2 = y.view(B, y.shape[-1])
+        o = ops.gdn_decode_sliced_(y2, p["A_log"], p["dt_bias"], rec_state, b_off=C + Vd, a_off=C + Vd + Hv)
+        N = wq_out.shape[0]
+        out = residual.view(B, N) if residual is not None else torch.empty(B, N, dtype=torch.float32, device=x.device)
+        ops.gemv_gated_norm(o, y2[:, C:], p["norm"], wq_out, ws_out, out, head_scale=head_scale, eps=eps,
+                            epilogue="store" if residual is None else "add")
+        return residual if residual is not None else out.view(B, 1, N)
+    y = linear(x, w_in, wq_in, ws_in, prenorm=prenorm)
     if T == 1 and Hk == Hv and dk == dv == 128 and x.dtype == torch.float32:
         # the decode step's conv, recurrent rule and gated norm in one launch (the same arithmetic as the three
         # kernels below)
@@ -104,13 +120,15 @@ def prenorm_torch(x, prenorm):
     return ops.add_rmsnorm_(s, None, nw, eps)
 
 
-def linear(x, w, wq=None, ws=None, prenorm=None, residual=None):
+def linear(x, w, wq=None, ws=None, prenorm=None, residual=None, conv=None):
     """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), on the int8 weights wq with scales ws
     ([N, K / 128] per group or [N] per row; w their dequantised values) when given, else on w; for more rows the HIP
     int8 GEMM on wq (fp32-accurate) when given, else a torch GEMM on w. prenorm = (x_add, norm_w, eps, x_out): x is
     a residual and the product takes the RMSNorm (1 + norm_w) of x + x_add (x_add may be None), the sum being written
     to x_out when given (the decoder layer's add + norm, fused into the GEMV). residual [..., N]: the product is added
-    into it in place (the decoder layer's residual add after its mixer) and residual is returned."""
+    into it in place (the decoder layer's residual add after its mixer) and residual is returned. conv =
+    (conv_w, conv_bias, conv_state): the GEMV with prenorm runs the GDN causal conv + SiLU on the first
+    conv_w.shape[0] outputs and advances conv_state (decode only: raises when the product is not a GEMV)."""
     K = x.shape[-1]
     M = x.numel() // K
     N = (wq if wq is not None else w).shape[0]
@@ -123,8 +141,10 @@ def linear(x, w, wq=None, ws=None, prenorm=None, residual=None):
             pn = (None if x_add is None else x_add.reshape(M, K), nw, eps,
                   None if x_out is None else x_out.view(M, K))
         Wd, sd = (wq, ws) if wq is not None else (w, None)
-        y = ops.gemv(xm, Wd, sd, out=out, epilogue=epi, prenorm=pn)
+        y = ops.gemv(xm, Wd, sd, out=out, epilogue=epi, prenorm=pn, conv=conv)
         return residual if residual is not None else y.view(*x.shape[:-1], N)
+    if conv is not None:
+        raise ValueError("linear: the conv epilogue is a decode GEMV form (at most 8 fp32 rows, K a multiple of 256)")
     if prenorm is not None:
         x = prenorm_torch(x, prenorm)
     if wq is not None and K % 64 == 0 and x.dtype == torch.float32:

@@ -79,6 +79,12 @@ _LIB.define("add_rmsnorm_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tenso
 _LIB.define("argmax_rows_(Tensor x, Tensor(a!) idx) -> ()")
 _LIB.define("gemv_norm_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
             "Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
+_LIB.define("gdn_decode_sliced_(Tensor y, Tensor A_log, Tensor dt_bias, int b_off, int a_off, Tensor(a!) state, "
+            "float scale) -> Tensor")
+_LIB.define("gemv_norm_conv_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
+            "Tensor? w_scale, Tensor(a!) y, Tensor conv_w, Tensor? conv_bias, Tensor(c!) conv_state) -> ()")
+_LIB.define("gemv_gated_norm_(Tensor o, Tensor z, Tensor norm_w, Tensor? head_scale, float eps, Tensor W, "
+            "Tensor w_scale, Tensor(a!) y, int epilogue) -> ()")
 _LIB.define("attn_prep(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, Tensor cos, Tensor sin, Tensor pos, "
             "Tensor(a!) k_cache, Tensor(b!) v_cache, int Hq, int Hkv, bool want_kv) "
             "-> (Tensor, Tensor, Tensor, Tensor)")
@@ -295,6 +301,24 @@ def _gdn_decode_fused_impl(y, conv_w, conv_bias, conv_state, A_log, dt_bias, b_o
     return out
 
 
+def _gdn_decode_sliced_impl(y, A_log, dt_bias, b_off, a_off, state, scale):
+    _on_gpu(A_log, dt_bias, state)
+    _require(y.is_cuda and y.dtype == torch.float32 and y.dim() == 2 and y.stride(1) == 1,
+             "y: [B, W] fp32 with unit column stride (one projection row per sequence)")
+    B = y.shape[0]
+    _require(state.dtype == torch.float32 and state.dim() == 4 and state.is_contiguous()
+             and state.shape[0] == B and state.shape[2] == state.shape[3], "state: [B, H, d, d] fp32 dense")
+    H, d = state.shape[1], state.shape[2]
+    _require(A_log.numel() == H and dt_bias.numel() == H and A_log.dtype == torch.float32
+             and dt_bias.dtype == torch.float32 and A_log.is_contiguous() and dt_bias.is_contiguous(),
+             "A_log, dt_bias: [H] fp32 dense")
+    out = torch.empty(B, H * d, dtype=torch.float32, device=y.device)
+    st = _lib.lib().q35_gdn_decode_sliced(_ptr(y), y.stride(0), _ptr(A_log), _ptr(dt_bias), int(b_off), int(a_off),
+                                          _ptr(state), float(scale), _ptr(out), B, H, d, _stream(y))
+    check(st, "q35_gdn_decode_sliced")
+    return out
+
+
 def _gated_rmsnorm_impl(o, z, w, head_scale, eps):
     _on_gpu(o, w, head_scale)
     _require(o.dtype in _DT and o.dim() >= 2, "o: [..., Hv, dv] fp32 or bf16")
@@ -420,6 +444,51 @@ def _gemv_norm_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, epilogue, pushe
     check(st, "q35_gemv_norm")
 
 
+def _gemv_norm_conv_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, conv_w, conv_bias, conv_state):
+    _on_gpu(x, x_add, x_out, norm_w, W, w_scale, y, conv_w, conv_bias, conv_state)
+    _require(x.dtype == torch.float32 and x.dim() == 2 and y.dtype == torch.float32 and y.dim() == 2,
+             "x: [M, K] fp32; y: [M, N] fp32")
+    M, K = x.shape
+    for t in (x_add, x_out):
+        _require(t is None or (t.dtype == torch.float32 and tuple(t.shape) == (M, K) and t.stride(0) == x.stride(0)
+                               and t.stride(1) == 1), "x_add / x_out: like x")
+    _require(norm_w.dtype == torch.float32 and norm_w.numel() == K and norm_w.is_contiguous(), "norm_w: [K] fp32")
+    _require(W.dim() == 2 and W.dtype in (torch.int8, torch.float32) and W.shape[1] == K, "W: [N, K] int8 or fp32")
+    N = W.shape[0]
+    _require(y.shape[0] == M and y.shape[1] == N and y.stride(1) == 1, "y: [M, N] with unit column stride")
+    _require(conv_w.dtype == torch.float32 and conv_w.dim() == 2 and conv_w.is_contiguous(), "conv_w: [C, K] fp32")
+    C, Kc = conv_w.shape
+    _require(conv_bias is None or (conv_bias.dtype == torch.float32 and conv_bias.numel() == C), "conv_bias: [C]")
+    _require(conv_state.dtype == torch.float32 and tuple(conv_state.shape) == (M, Kc - 1, C)
+             and conv_state.is_contiguous(), "conv_state: [M, K - 1, C] fp32 dense")
+    fmt = _weight_format(W, w_scale, N, K)
+    st = _lib.lib().q35_gemv_norm_conv(_ptr(x), _ptr(x_add), _ptr(x_out), x.stride(0), _ptr(norm_w), float(eps),
+                                       _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.stride(0), M, N, K, _ptr(conv_w),
+                                       _ptr(conv_bias), _ptr(conv_state), C, Kc, _stream(x))
+    check(st, "q35_gemv_norm_conv")
+
+
+def _gemv_gated_norm_impl(o, z, norm_w, head_scale, eps, W, w_scale, y, epilogue):
+    _on_gpu(o, norm_w, head_scale, W, w_scale, y)
+    _require(z.is_cuda and z.device == o.device, "z must be on o's device (rows may be strided)")
+    _require(o.dtype == torch.float32 and o.dim() == 2 and o.stride(1) == 1 and z.dtype == torch.float32
+             and z.dim() == 2 and z.stride(1) == 1 and z.shape[0] == o.shape[0] and z.shape[1] >= o.shape[1],
+             "o: [M, K] fp32; z: [M, >= K] fp32, unit column strides")
+    M, K = o.shape
+    _require(norm_w.dtype == torch.float32 and norm_w.numel() == 128 and norm_w.is_contiguous(), "norm_w: [128] fp32")
+    _require(head_scale is None or (head_scale.dtype == torch.float32 and head_scale.numel() == K // 128),
+             "head_scale: [K / 128] fp32")
+    _require(W.dim() == 2 and W.dtype == torch.int8 and W.shape[1] == K, "W: [N, K] int8")
+    N = W.shape[0]
+    _require(y.dtype == torch.float32 and y.dim() == 2 and y.shape[0] == M and y.shape[1] == N and y.stride(1) == 1,
+             "y: [M, N] fp32")
+    fmt = _weight_format(W, w_scale, N, K)
+    st = _lib.lib().q35_gemv_gated_norm(_ptr(o), o.stride(0), _ptr(z), z.stride(0), _ptr(norm_w), _ptr(head_scale),
+                                        float(eps), _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.stride(0), M, N, K,
+                                        int(epilogue), _stream(o))
+    check(st, "q35_gemv_gated_norm")
+
+
 def _swiglu_push_impl(gu, pushes, T):
     _on_gpu(gu, pushes)
     _require(gu.dtype == torch.float32 and gu.shape[-1] % 2 == 0, "gu: [..., 2 I] fp32")
@@ -468,7 +537,8 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
                      ("gemm_q8_", _gemm_q8_impl),
                      ("add_rmsnorm_", _add_rmsnorm_impl), ("argmax_rows_", _argmax_rows_impl),
-                     ("gemv_norm_", _gemv_norm_impl)]:
+                     ("gemv_norm_", _gemv_norm_impl), ("gdn_decode_sliced_", _gdn_decode_sliced_impl),
+                     ("gemv_norm_conv_", _gemv_norm_conv_impl), ("gemv_gated_norm_", _gemv_gated_norm_impl)]:
     _LIB.impl(_name, _impl, "CUDA")
     _LIB.impl(_name, _no_cpu(_name), "CPU")
 
@@ -498,6 +568,10 @@ _LIB.impl("gated_attn_prefill_cached",
           "Meta")
 _LIB.impl("argmax_rows_", lambda x, idx: None, "Meta")
 _LIB.impl("gemv_norm_", lambda x, xa, xo, nw, eps, W, ws, y, e, pushes, T: None, "Meta")
+_LIB.impl("gdn_decode_sliced_", lambda y, Al, dt, bo, ao, st, sc: y.new_empty(y.shape[0], st.shape[1] * st.shape[2]),
+          "Meta")
+_LIB.impl("gemv_norm_conv_", lambda x, xa, xo, nw, eps, W, ws, y, cw, cb, cs: None, "Meta")
+_LIB.impl("gemv_gated_norm_", lambda o, z, nw, hs, eps, W, ws, y, e: None, "Meta")
 _LIB.impl("gemv_", lambda x, W, ws, y, e, pushes, T: None, "Meta")
 _LIB.impl("gemm_q8_", lambda x, W, ws, y, e, pushes, T: None, "Meta")
 _LIB.impl("swiglu_push", lambda gu, pushes, T: gu.new_empty(*gu.shape[:-1], gu.shape[-1] // 2), "Meta")
@@ -623,6 +697,25 @@ def gdn_decode_fused_(y, conv_w, conv_state, A_log, dt_bias, state, norm_w, *, b
                                            float(eps), float(d ** -0.5 if scale is None else scale))
 
 
+def gdn_decode_sliced_(y, A_log, dt_bias, state, *, b_off, a_off, scale=None):
+    """The recurrent part of a Gated DeltaNet decode step (HF:454-543 for a cached token, from the recurrent rule on)
+    over projection rows y [B, W] fp32 whose q|k|v channels already went through the causal conv + SiLU
+    (gemv(..., conv=...)): state [B, H, d, d] advanced in place (Hk = Hv = H, d = 128). Returns the raw output
+    o [B, H * d] fp32, before the gated RMSNorm (gemv_gated_norm applies it)."""
+    d = state.shape[2]
+    return torch.ops.q35.gdn_decode_sliced_(y, A_log.float().contiguous(), dt_bias.float().contiguous(), int(b_off),
+                                            int(a_off), state, float(d ** -0.5 if scale is None else scale))
+
+
+def gemv_gated_norm(o, z, norm_w, W, w_scale, out, *, head_scale=None, eps=1e-6, epilogue="store"):
+    """out (=, or += for epilogue "add") gated_rmsnorm(o, z) @ W^T s for M <= 8 rows: the GDN layer's output norm
+    (HF:168-184) applied per head of 128 while the product stages o (q35_gemv_gated_norm). W int8 [N, K] with
+    w_scale [N, K / 128] or [N]; o [M, K], z [M, >= K] fp32."""
+    torch.ops.q35.gemv_gated_norm_(o, z, norm_w.float().contiguous(), head_scale, float(eps), W, w_scale, out,
+                                   _EPI[epilogue])
+    return out
+
+
 def gated_rmsnorm(o, z, w, head_scale=None, eps=1e-6):
     """Qwen3_5RMSNormGated (HF:168-184) per (token, head) with the engine's optional per-head scale
     (engine/kernels_qwen35.js:243): o [..., Hv, dv], z [..., Hv * dv] fp32 (rows may be strided) -> [..., Hv * dv]."""
@@ -651,17 +744,26 @@ def pack_pushes(pushes, device):
     return torch.tensor(rec, dtype=torch.int32).reshape(-1, 6).to(device)
 
 
-def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, prenorm=None):
+def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, prenorm=None, conv=None):
     """y[m, n] = sum_k x[m, k] W[n, k] s(n, k) for M <= 8 rows (decode): W int8 with scales w_scale [N, K / 128]
     (one per group of 128 inputs, the engine's q8 format) or [N] (one per row), or fp32 W (w_scale None).
     epilogue "store" writes out, "add" accumulates into out (a residual add), "swiglu" treats W's rows as
     interleaved (gate, up) pairs and writes silu(gate) * up with the neuron pushes (pack_pushes) applied.
     prenorm = (x_add, norm_w, eps, x_out): x is then a residual; the product takes the RMSNorm (1 + w) of
-    s = x + x_add (x_add may be None), and s is written to x_out when it is not None (q35_gemv_norm)."""
+    s = x + x_add (x_add may be None), and s is written to x_out when it is not None (q35_gemv_norm).
+    conv = (conv_w [C, K], conv_bias or None, conv_state [M, K - 1, C]), with prenorm and the store epilogue: outputs
+    0 .. C - 1 go through the GDN causal conv + SiLU and conv_state advances in place (q35_gemv_norm_conv)."""
     e = _EPI[epilogue]
     if out is None:
         N = W.shape[0] // 2 if e == 2 else W.shape[0]
         out = torch.empty(x.shape[0], N, dtype=torch.float32, device=x.device)
+    if conv is not None:
+        _require(prenorm is not None and e == 0, "the conv epilogue runs with prenorm and the store epilogue")
+        x_add, norm_w, eps, x_out = prenorm
+        cw, cb, cs = conv
+        torch.ops.q35.gemv_norm_conv_(x, x_add, x_out, norm_w, float(eps), W, w_scale, out,
+                                      cw.reshape(cw.shape[0], cw.shape[-1]).float().contiguous(), cb, cs)
+        return out
     if prenorm is None:
         torch.ops.q35.gemv_(x, W, w_scale, out, e, pushes, int(T))
     else:

@@ -230,6 +230,21 @@ int q35_gdn_decode_fused(const float* y, int64_t ldy, const float* conv_w, const
                          float* out, int64_t B, int64_t H, int64_t d, int64_t K, q35_stream_t stream);
 
 /*
+ * The recurrent part of one GDN decode step, for a projection row whose q|k|v channels already went through the
+ * causal conv + SiLU (q35_gemv_norm_conv): q35_gdn_recurrent (one token, l2norm on, fp32) on the head's state with
+ * beta = sigmoid(b) and g = -exp(A_log) softplus(a + dt_bias) from the row, leaving out the gated RMSNorm (the
+ * output projection applies it: q35_gemv_gated_norm). HF:454-543 for one cached token from the recurrent rule on;
+ * engine/kernels_qwen35.js:183-236 (`delta` before its gated norm). The column sums are formed in the order of
+ * q35_gdn_decode_fused, over four blocks per (head, row).
+ *   y: [B, ldy] fp32, q|k|v (convolved) at [0, 3 H d), b at b_off, a at a_off; A_log, dt_bias: [H];
+ *   state: [B, H, d, d] fp32 (updated in place); out: [B, H d] fp32, the raw output o.
+ *   d = 128; y, state, out 16-byte aligned, ldy a multiple of 4.
+ */
+int q35_gdn_decode_sliced(const float* y, int64_t ldy, const float* A_log, const float* dt_bias, int64_t b_off,
+                          int64_t a_off, float* state, float scale, float* out, int64_t B, int64_t H, int64_t d,
+                          q35_stream_t stream);
+
+/*
  * Gated RMSNorm per (token, head): out = w * (o * rsqrt(mean(o^2) + eps)) * silu(z) * head_scale[h], the
  * normalised o rounded to dtype before the weight multiply as HF does (plain w, not 1 + w).
  *   o, out: [M, Hv, dv] dtype (may alias); z: [M, ldz] fp32, head h's gate at columns h dv .. h dv + dv - 1;
@@ -288,6 +303,32 @@ int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const floa
 int q35_gemv_norm(const float* x, const float* x_add, float* x_out, int64_t ldx, const float* norm_w, float eps,
                   const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy, int64_t M, int64_t N,
                   int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream);
+
+/*
+ * q35_gemv_norm (store epilogue) whose outputs 0 .. conv_channels - 1 go through the GDN layer's causal conv + SiLU
+ * before they are stored: for output channel c of row m, silu(conv_bias[c] + sum_i conv_w[c, i] x_i) over the
+ * channel's last conv_k inputs (the conv_k - 1 of conv_state[m, :, c], then this product), and conv_state[m, :, c]
+ * advanced by one input. The same arithmetic as q35_gdn_conv at T = 1 (HF:454-475 causal_conv1d_update;
+ * engine/kernels_qwen35.js:127-178). Each channel belongs to one block, so the state is updated in place.
+ *   conv_w: [conv_channels, conv_k] fp32, conv_bias: [conv_channels] or NULL, conv_state: [M, conv_k - 1,
+ *   conv_channels] fp32; 2 <= conv_k <= 8, N at most 16384. Everything else as q35_gemv_norm.
+ */
+int q35_gemv_norm_conv(const float* x, const float* x_add, float* x_out, int64_t ldx, const float* norm_w, float eps,
+                       const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy, int64_t M, int64_t N,
+                       int64_t K, const float* conv_w, const float* conv_bias, float* conv_state,
+                       int64_t conv_channels, int64_t conv_k, q35_stream_t stream);
+
+/*
+ * q35_gemv of the gated RMSNorm of o (the GDN layer's output norm, HF:168-184; engine/kernels_qwen35.js:237-243),
+ * computed per head of 128 inputs while x is staged: x = norm_w * (o * rsqrt(mean(o^2) + eps)) * silu(z) *
+ * head_scale[h], in the order of q35_gdn_decode_fused's norm, then y (epilogue 0) = or (epilogue 1) += x W^T s.
+ *   o: [M, ldo] fp32 (16-byte aligned), K = H 128 inputs; z: [M, ldz] fp32 (16-byte aligned, ldz a multiple of 4),
+ *   head h's gate at columns 128 h .. 128 h + 127; norm_w: [128] fp32; head_scale: [H] or NULL. int8 weights only
+ *   (Q35_I8 or Q35_I8_G128). Everything else as q35_gemv (including the split-K accumulation of epilogue 1).
+ */
+int q35_gemv_gated_norm(const float* o, int64_t ldo, const float* z, int64_t ldz, const float* norm_w,
+                        const float* head_scale, float eps, const void* W, int w_dtype, const float* w_scale,
+                        float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, q35_stream_t stream);
 
 /*
  * Many-row int8 GEMM for the prefill projections: y[m, n] = sum_k x[m, k] W[n, k] s(n, k), s as for q35_gemv
