@@ -24,9 +24,6 @@ constexpr int kConvMaxK = 8;
 constexpr int kConvCh = 64;    // channels per conv block (16 quads)
 constexpr int kConvTl = 16;    // time lanes per conv block
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
-
 template <typename T> __device__ __forceinline__ void store4(T* p, const f32x4& v);
 template <> __device__ __forceinline__ void store4<float>(float* p, const f32x4& v) {
   *reinterpret_cast<f32x4*>(p) = v;

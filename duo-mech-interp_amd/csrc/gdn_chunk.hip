@@ -870,10 +870,30 @@ __device__ __forceinline__ f32x4 mm_k16(const f32x4& x, const f32x4& y, f32x4 ac
   return acc;
 }
 
+// Front-end form (the Gated DeltaNet layer's conv + SiLU and gate terms run in the prep kernel's load phase, so q, k,
+// v, g and beta never reach HBM): the fused projection output y [B, T, ldy] with the q | k | v channels (C = 2 Kd +
+// Vd, K = 4 taps, weights [C][4], optional bias [C]) from column 0 and the b, a columns of head h at b_off + h,
+// a_off + h; the carried conv state [B, 3, C] holds the 3 inputs before y's first token. Only the first chunk's prep
+// blocks read the state; the scan kernel, which starts after every prep block has ended, advances it to the last 3
+// inputs of [old state | y]: no block reads a state entry that another block of the same launch writes.
+constexpr int kFrontK = 4;
+struct GdnFront {
+  const float* y;
+  int64_t ldy;
+  const float* cw;      // [C][kFrontK]
+  const float* cb;      // [C] or null
+  float* cst;           // [B][kFrontK - 1][C]
+  const float* A_log;   // [H]
+  const float* dt_bias; // [H]
+  int b_off, a_off, C, Kd;
+};
+
+template <bool FE>
 __global__ __launch_bounds__(256, 1) void gdn_f32_prep_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                               const float* __restrict__ v, const float* __restrict__ g,
                                                               const float* __restrict__ beta, char* __restrict__ ws,
-                                                              int T, int NC, int Hk, int H, float scale, int l2norm) {
+                                                              int T, int NC, int Hk, int H, float scale, int l2norm,
+                                                              GdnFront fe) {
   __shared__ __attribute__((aligned(16))) float Ks[kC * kFX];   // k rows (unnormalised)
   __shared__ __attribute__((aligned(16))) float Xs[kC * kFX];   // q rows, then v rows
   __shared__ __attribute__((aligned(16))) float Am[kC * kFS];   // L -> T (invert64 layout) -> T dense
@@ -894,28 +914,14 @@ __global__ __launch_bounds__(256, 1) void gdn_f32_prep_kernel(const float* __res
   const int row = tid >> 2, c0 = (tid & 3) * 32;
   const bool valid = row < nvalid;
   const size_t tok = (size_t)b * T + t0 + min(row, nvalid - 1);
-  f32x4 kr[8], xr[8];
-  {
-    const float* kp = k + (tok * Hk + kh) * kD + c0;
-    const float* qp = q + (tok * Hk + kh) * kD + c0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      kr[j] = *reinterpret_cast<const f32x4*>(kp + 4 * j);
-      xr[j] = *reinterpret_cast<const f32x4*>(qp + 4 * j);
-    }
-  }
+  f32x4 kr[8];  // the thread's k row; then v, held until q is no longer needed
   float g0 = 0.f, b0 = 0.f;
-  if (wave == 0 && lane < nvalid) {
-    const size_t gi = ((size_t)b * T + t0 + lane) * H + h;
-    g0 = g[gi];
-    b0 = beta[gi];
-  }
-  {
+  auto norms = [&](const f32x4(&kk)[8], const f32x4(&qq)[8]) {  // l2 norms of the thread's row (4 threads a row)
     float ssk = 0.f, ssq = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) { ssk += kr[j][e] * kr[j][e]; ssq += xr[j][e] * xr[j][e]; }
+      for (int e = 0; e < 4; ++e) { ssk += kk[j][e] * kk[j][e]; ssq += qq[j][e] * qq[j][e]; }
     ssk += __shfl_xor(ssk, 1, 64);
     ssk += __shfl_xor(ssk, 2, 64);
     ssq += __shfl_xor(ssq, 1, 64);
@@ -924,6 +930,96 @@ __global__ __launch_bounds__(256, 1) void gdn_f32_prep_kernel(const float* __res
       rkn[row] = l2norm ? rsqrtf(ssk + 1e-6f) : 1.f;
       rqn[row] = l2norm ? rsqrtf(ssq + 1e-6f) : 1.f;
     }
+  };
+  if constexpr (FE) {
+    // causal conv + SiLU of the head's k, q and v channels of y (thread: channel quad cq, tokens 8 tg .. 8 tg + 7 of
+    // the chunk; the 3 inputs before the chunk from y, or for the first chunk from the carried state), zero past the
+    // sequence end; the gate terms from the b and a columns. The front-end kernel's arithmetic in its order; the
+    // norms are then taken over the staged rows in the order of the other form.
+    const int cq = tid & 31, tg = tid >> 5;
+    constexpr int kWin = 8 + kFrontK - 1;  // inputs of tokens t0 + 8 tg - 3 .. t0 + 8 tg + 7
+    // every load of the three windows is issued before any is used: one memory round trip. Offsets are 32-bit
+    // relative to the row's first token of the chunk (the launcher bounds ldy) and to the row's conv state.
+    const float* ybase = fe.y + ((size_t)b * T + t0) * fe.ldy;
+    const float* sbase = fe.cst + (size_t)b * (kFrontK - 1) * fe.C;
+    auto window = [&](int ch, f32x4(&win)[kWin]) {
+#pragma unroll
+      for (int j = 0; j < kWin; ++j) {
+        const int r = t0 + 8 * tg + j - (kFrontK - 1);
+        const float* py = ybase + ((min(r, T - 1) - t0) * (int)fe.ldy + ch);
+        const float* ps = sbase + ((kFrontK - 1 + min(r, -1)) * fe.C + ch);
+        win[j] = *reinterpret_cast<const f32x4*>(r >= 0 ? py : ps);
+      }
+    };
+    auto taps = [&](int ch, f32x4(&tw)[4], f32x4& bias) {  // tw[e][i]: tap i of channel ch + e
+      const f32x4* cw4 = reinterpret_cast<const f32x4*>(fe.cw + (size_t)ch * kFrontK);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tw[e] = cw4[e];
+      bias = fe.cb ? *reinterpret_cast<const f32x4*>(fe.cb + ch) : zero4();
+    };
+    auto conv = [&](const f32x4(&win)[kWin], const f32x4(&tw)[4], const f32x4& bias, f32x4(&res)[8]) {
+#pragma unroll
+      for (int o = 0; o < 8; ++o) {
+        f32x4 acc = bias;
+#pragma unroll
+        for (int i = 0; i < kFrontK; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] += tw[e][i] * win[o + i][e];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = silu_f(acc[e]);
+        res[o] = 8 * tg + o < nvalid ? acc : zero4();
+      }
+    };
+    const int chk = fe.Kd + kh * kD + 4 * cq, chq = kh * kD + 4 * cq, chv = 2 * fe.Kd + h * kD + 4 * cq;
+    f32x4 wk[kWin], wq[kWin], wv[kWin], tk[4], tq[4], tv[4], bk, bq, bv;
+    window(chk, wk);
+    taps(chk, tk, bk);
+    window(chq, wq);
+    taps(chq, tq, bq);
+    window(chv, wv);
+    taps(chv, tv, bv);
+    // the gate inputs of the chunk's tokens (lane = token; used by wave 0, loaded by every wave), issued with the
+    // windows
+    const float* yr = ybase + min(lane, nvalid - 1) * (int)fe.ldy;
+    const float gin_b = yr[fe.b_off + h], gin_a = yr[fe.a_off + h], gin_A = fe.A_log[h], gin_dt = fe.dt_bias[h];
+    f32x4 cr[8];
+    conv(wk, tk, bk, cr);
+#pragma unroll
+    for (int o = 0; o < 8; ++o) *reinterpret_cast<f32x4*>(Ks + (8 * tg + o) * kFX + 4 * cq) = cr[o];
+    conv(wq, tq, bq, cr);
+#pragma unroll
+    for (int o = 0; o < 8; ++o) *reinterpret_cast<f32x4*>(Xs + (8 * tg + o) * kFX + 4 * cq) = cr[o];
+    conv(wv, tv, bv, kr);
+    // the gate inputs are consumed here, so that the compiler keeps their loads with the windows rather than
+    // sinking them into the branch below (a second memory round trip for wave 0)
+    asm volatile("" ::"v"(gin_b), "v"(gin_a));
+    if (wave == 0 && lane < nvalid) {
+      b0 = sigmoidf_(gin_b);
+      g0 = -__expf(gin_A) * softplus_f(gin_a + gin_dt);
+    }
+    __syncthreads();
+    f32x4 ka[8], qa[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ka[j] = *reinterpret_cast<const f32x4*>(Ks + row * kFX + c0 + 4 * j);
+      qa[j] = *reinterpret_cast<const f32x4*>(Xs + row * kFX + c0 + 4 * j);
+    }
+    norms(ka, qa);
+  } else {
+    f32x4 xr[8];
+    const float* kp = k + (tok * Hk + kh) * kD + c0;
+    const float* qp = q + (tok * Hk + kh) * kD + c0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      kr[j] = *reinterpret_cast<const f32x4*>(kp + 4 * j);
+      xr[j] = *reinterpret_cast<const f32x4*>(qp + 4 * j);
+    }
+    if (wave == 0 && lane < nvalid) {
+      const size_t gi = ((size_t)b * T + t0 + lane) * H + h;
+      g0 = g[gi];
+      b0 = beta[gi];
+    }
+    norms(kr, xr);
     const f32x4 z = zero4();
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -940,8 +1036,7 @@ __global__ __launch_bounds__(256, 1) void gdn_f32_prep_kernel(const float* __res
     gam[lane] = g0;
     bet[lane] = b0;
   }
-  // v rows, loaded now and staged once q is no longer needed
-  {
+  if constexpr (!FE) {  // v rows, loaded now and staged once q is no longer needed
     const float* vp = v + (tok * H + h) * kD + c0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -1011,8 +1106,12 @@ __global__ __launch_bounds__(256, 1) void gdn_f32_prep_kernel(const float* __res
       const int idx = tid + 256 * e;
       tv[e] = tinv(Am, idx >> 6, idx & 63);
     }
+    // v: the thread's row (or in the front-end form its channel quad and tokens)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<f32x4*>(Xs + row * kFX + c0 + 4 * j) = kr[j];
+    for (int j = 0; j < 8; ++j) {
+      float* dst = FE ? Xs + (8 * (tid >> 5) + j) * kFX + 4 * (tid & 31) : Xs + row * kFX + c0 + 4 * j;
+      *reinterpret_cast<f32x4*>(dst) = kr[j];
+    }
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
@@ -1084,7 +1183,7 @@ struct F32Ops {
 
 __global__ __launch_bounds__(256, 1) void gdn_f32_scan_kernel(const char* __restrict__ ws, const float* s_in,
                                                               float* s_out, float* __restrict__ o, int T, int NC,
-                                                              int H, int B) {
+                                                              int H, int B, int Hk, GdnFront fe) {
   __shared__ f32x4 sS[8][64];  // state row tiles (D layout) of the four waves
   __shared__ f32x4 sV[4][64];  // V row tiles
   const int lane = threadIdx.x & 63;
@@ -1172,8 +1271,29 @@ __global__ __launch_bounds__(256, 1) void gdn_f32_scan_kernel(const char* __rest
     }
   };
 
+  // front-end form: the carried conv state of this block's channels (16 of the head's v channels, and for the first
+  // head of a k group 16 of its q and k channels) <- the last 3 inputs of [old state | y]; one lane per channel reads
+  // its sources before writing, and no other block touches the channel
+  const bool fstate = fe.cst && threadIdx.x < 48 && ((threadIdx.x >> 4) == 2 || h % (H / Hk) == 0);
+  int fch = 0;
+  float fnv[kFrontK - 1];
+  if (fstate) {
+    const int m = threadIdx.x >> 4, kh = h / (H / Hk);
+    fch = (m == 0 ? kh * kD : m == 1 ? fe.Kd + kh * kD : 2 * fe.Kd + h * kD) + 16 * sl + (threadIdx.x & 15);
+#pragma unroll
+    for (int j = 0; j < kFrontK - 1; ++j) {
+      const int src = T + j;  // index into [old state (3) | inputs (T)]
+      fnv[j] = src >= kFrontK - 1 ? fe.y[((size_t)b * T + src - (kFrontK - 1)) * fe.ldy + fch]
+                                  : fe.cst[((size_t)b * (kFrontK - 1) + src) * fe.C + fch];
+    }
+  }
+
   F32Ops o0, o1;
   load(0, o0);
+  if (fstate) {
+#pragma unroll
+    for (int j = 0; j < kFrontK - 1; ++j) fe.cst[((size_t)b * (kFrontK - 1) + j) * fe.C + fch] = fnv[j];
+  }
   for (int c = 0; c < NC; c += 2) {
     load(c + 1, o1);
     step(c, o0);
@@ -1225,11 +1345,12 @@ extern "C" int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v
     // fp32 inputs: the fp32 WY path (chunk records, then the per-slice scan)
     const int64_t NC = (T + kC - 1) / kC;
     if (NC > 65535) return Q35_EUNSUPPORTED;
-    hipLaunchKernelGGL(gdn_f32_prep_kernel, dim3((unsigned)NC, (unsigned)H, (unsigned)B), dim3(256), 0, st,
+    const GdnFront none{};
+    hipLaunchKernelGGL(gdn_f32_prep_kernel<false>, dim3((unsigned)NC, (unsigned)H, (unsigned)B), dim3(256), 0, st,
                        (const float*)q, (const float*)k, (const float*)v, g, beta, ws, (int)T, (int)NC, (int)Hk,
-                       (int)H, scale, use_qk_l2norm);
+                       (int)H, scale, use_qk_l2norm, none);
     hipLaunchKernelGGL(gdn_f32_scan_kernel, dim3((unsigned)(8 * H * B)), dim3(256), 0, st, ws, initial_state,
-                       final_state, (float*)out, (int)T, (int)NC, (int)H, (int)B);
+                       final_state, (float*)out, (int)T, (int)NC, (int)H, (int)B, (int)Hk, none);
   } else {
     const int64_t NP = (T + kP - 1) / kP;
     if (NP > 65535) return Q35_EUNSUPPORTED;
@@ -1239,5 +1360,39 @@ extern "C" int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v
     hipLaunchKernelGGL(gdn_pair_scan_kernel, g2, dim3(kScanThreads), 0, st, ws, initial_state, final_state,
                        (__bf16*)out, (int)T, (int)NP, (int)H, (int)B);
   }
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+extern "C" int q35_gdn_chunk_prefill_conv(const float* y, int64_t ldy, const float* conv_w, const float* conv_bias,
+                                          float* conv_state, const float* A_log, const float* dt_bias, int64_t b_off,
+                                          int64_t a_off, const float* initial_state, float* final_state, float* out,
+                                          int64_t B, int64_t T, int64_t Hk, int64_t H, int64_t Dk, int64_t Dv,
+                                          int64_t conv_k, float scale, void* workspace, size_t workspace_bytes,
+                                          q35_stream_t stream) {
+  using namespace q35;
+  if (!y || !conv_w || !conv_state || !A_log || !dt_bias || !out) return Q35_EINVAL;
+  if (B <= 0 || T <= 0 || Hk <= 0 || H <= 0 || Dk <= 0 || Dv <= 0 || H % Hk != 0 || conv_k < 2) return Q35_EINVAL;
+  if (Dk != kD || Dv != kD || conv_k != kFrontK) return Q35_EUNSUPPORTED;
+  const int64_t Kd = Hk * kD, C = 2 * Kd + H * kD;
+  if (ldy < C || b_off < 0 || a_off < 0 || b_off + H > ldy || a_off + H > ldy) return Q35_EINVAL;
+  if ((ldy & 3) || ((uintptr_t)y & 15) || ((uintptr_t)conv_w & 15) || ((uintptr_t)conv_state & 15) ||
+      (conv_bias && ((uintptr_t)conv_bias & 15)))
+    return Q35_EUNSUPPORTED;
+  // the prep kernel addresses a chunk's rows of y with 32-bit offsets: 67 ldy must fit
+  if (B > 65535 || H > 65535 || H * B > (1 << 26) || T > ((int64_t)1 << 30) / H || ldy > (1 << 24) ||
+      C > (1 << 28))
+    return Q35_EUNSUPPORTED;
+  const int64_t NC = (T + kC - 1) / kC;
+  if (NC > 65535) return Q35_EUNSUPPORTED;
+  const size_t need = q35_gdn_chunk_workspace_bytes(B, T, H, Dk, Dv, kC, Q35_F32);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const GdnFront fe{y, ldy, conv_w, conv_bias, conv_state, A_log, dt_bias, (int)b_off, (int)a_off, (int)C, (int)Kd};
+  hipLaunchKernelGGL(gdn_f32_prep_kernel<true>, dim3((unsigned)NC, (unsigned)H, (unsigned)B), dim3(256), 0, st,
+                     (const float*)nullptr, (const float*)nullptr, (const float*)nullptr, (const float*)nullptr,
+                     (const float*)nullptr, ws, (int)T, (int)NC, (int)Hk, (int)H, scale, 1, fe);
+  hipLaunchKernelGGL(gdn_f32_scan_kernel, dim3((unsigned)(8 * H * B)), dim3(256), 0, st, ws, initial_state,
+                     final_state, out, (int)T, (int)NC, (int)H, (int)B, (int)Hk, fe);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }

@@ -96,6 +96,8 @@ __device__ __forceinline__ bf16x8 pack8(const f32x4& lo, const f32x4& hi) {
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }  // threshold 20
 
 // Block barrier that orders LDS traffic only. __syncthreads() also waits for every outstanding global load of the
 // calling wave (its fence has release semantics), which would drain register prefetches issued for the next

@@ -20,12 +20,12 @@ EXPORTS = [
     "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
     "q35_swiglu_push",
     "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm", "q35_gemm_q8",
-    "q35_gdn_decode_sliced", "q35_gemv_norm_conv", "q35_gemv_gated_norm",
+    "q35_gdn_decode_sliced", "q35_gemv_norm_conv", "q35_gemv_gated_norm", "q35_gdn_chunk_prefill_conv",
 ]
 
 Q35_F32, Q35_BF16, Q35_I8, Q35_I8_G128 = 0, 1, 2, 3
 Q35_ESCRATCH = 5
-ABI_VERSION = 8  # the signatures below; q35_abi_version() of the loaded library must match
+ABI_VERSION = 9  # the signatures below; q35_abi_version() of the loaded library must match
 
 _lib = None
 
@@ -53,6 +53,8 @@ _SIGS = {
     "q35_gated_attn_decode_noalloc": ([P, P, P, P, P, P, P, P, I32, I64, I64, I64, I64, I64, I64, F32, I64, P], I32),
     "q35_resid_add_rows": ([P, P, P, I64, I64, I64, I64, I32, P], I32),
     "q35_gdn_conv": ([P, I64, P, P, P, P, P, I64, I64, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, I32, P], I32),
+    "q35_gdn_chunk_prefill_conv": ([P, I64, P, P, P, P, P, I64, I64, P, P, P, I64, I64, I64, I64, I64, I64, I64, F32,
+                                    P, SZ, P], I32),
     "q35_gated_rmsnorm": ([P, P, I64, P, P, P, I64, I64, I64, F32, I32, P], I32),
     "q35_gdn_decode_fused": ([P, I64, P, P, P, P, P, I64, I64, I64, P, P, P, F32, F32, P, I64, I64, I64, I64, P],
                              I32),

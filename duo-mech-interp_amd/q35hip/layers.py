@@ -96,15 +96,22 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
                                   rec_state, p["norm"], b_off=C + Vd, a_off=C + Vd + Hv, z_off=C,
                                   head_scale=head_scale, eps=eps)
         return linear(o.view(B, 1, Vd), p["out_proj"], *_q8(p, "out_proj"), residual=residual)
-    q, k, v, g, beta = ops.gdn_conv(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], num_k_heads=Hk,
-                                    head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=C + Vd, a_off=C + Vd + Hv,
-                                    out_dtype=x.dtype)
-    if T == 1 or prefill == "recurrent":
-        o = ops.gdn_decode_step_(q, k, v, g, beta, rec_state, use_qk_l2norm_in_kernel=True)
+    if (T > 1 and prefill == "chunk" and x.dtype == torch.float32 and dk == dv == 128
+            and p["conv1d"].shape[-1] == 4 and rec_state.is_contiguous()):
+        # the conv + SiLU, l2 norms and gate terms in the chunk kernel's load phase (q, k, v, g, beta never written
+        # out), the recurrent state advanced in place: the arithmetic of gdn_conv + chunk_gated_delta_rule below
+        o = ops.gdn_chunk_prefill_conv_(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], rec_state,
+                                        num_k_heads=Hk, b_off=C + Vd, a_off=C + Vd + Hv)
     else:
-        o, S = ops.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=rec_state, output_final_state=True,
-                                          use_qk_l2norm_in_kernel=True)
-        rec_state.copy_(S)
+        q, k, v, g, beta = ops.gdn_conv(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], num_k_heads=Hk,
+                                        head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=C + Vd,
+                                        a_off=C + Vd + Hv, out_dtype=x.dtype)
+        if T == 1 or prefill == "recurrent":
+            o = ops.gdn_decode_step_(q, k, v, g, beta, rec_state, use_qk_l2norm_in_kernel=True)
+        else:
+            o, S = ops.chunk_gated_delta_rule(q, k, v, g, beta, initial_state=rec_state, output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+            rec_state.copy_(S)
     # gated RMSNorm: plain w, norm before the silu(z) gate (HF:168-184; engine/kernels_qwen35.js:237-243)
     o = ops.gated_rmsnorm(o, y[..., C:C + Vd], p["norm"], head_scale, eps)
     return linear(o, p["out_proj"], *_q8(p, "out_proj"), residual=residual)

@@ -79,6 +79,8 @@ _LIB.define("add_rmsnorm_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tenso
 _LIB.define("argmax_rows_(Tensor x, Tensor(a!) idx) -> ()")
 _LIB.define("gemv_norm_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
             "Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
+_LIB.define("gdn_chunk_prefill_conv_(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
+            "Tensor dt_bias, int b_off, int a_off, Tensor(b!) state, int Hk, float scale) -> Tensor")
 _LIB.define("gdn_decode_sliced_(Tensor y, Tensor A_log, Tensor dt_bias, int b_off, int a_off, Tensor(a!) state, "
             "float scale) -> Tensor")
 _LIB.define("gemv_norm_conv_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
@@ -299,6 +301,32 @@ def _gdn_decode_fused_impl(y, conv_w, conv_bias, conv_state, A_log, dt_bias, b_o
                                          K, _stream(y))
     check(st, "q35_gdn_decode_fused")
     return out
+
+
+def _gdn_chunk_prefill_conv_impl(y, conv_w, conv_bias, conv_state, A_log, dt_bias, b_off, a_off, state, Hk, scale):
+    _on_gpu(conv_w, conv_bias, conv_state, A_log, dt_bias, state)
+    _require(y.is_cuda and y.dtype == torch.float32 and y.dim() == 3 and y.is_contiguous(),
+             "y: [B, T, W] fp32 dense (the fused projection output)")
+    B, T, W = y.shape
+    _require(state.dtype == torch.float32 and state.dim() == 4 and state.is_contiguous() and state.shape[0] == B
+             and state.shape[2] == state.shape[3], "state: [B, H, d, d] fp32 dense")
+    H, d = state.shape[1], state.shape[2]
+    C = (2 * Hk + H) * d
+    _require(conv_w.dim() == 2 and conv_w.shape[0] == C and conv_w.dtype == torch.float32, "conv_w: [C, K] fp32")
+    K = conv_w.shape[1]
+    _require(conv_state.dtype == torch.float32 and tuple(conv_state.shape) == (B, K - 1, C),
+             "conv_state: [B, K - 1, C] fp32")
+    _require(A_log.numel() == H and dt_bias.numel() == H, "A_log, dt_bias: [H]")
+    L = _lib.lib()
+    nbytes = L.q35_gdn_chunk_workspace_bytes(B, T, H, d, d, 64, _DT[torch.float32])
+    _require(nbytes > 0, f"unsupported chunk prefill shape (d={d})")
+    ws = _workspace(nbytes, y.device)
+    o = torch.empty(B, T, H, d, dtype=torch.float32, device=y.device)
+    st = L.q35_gdn_chunk_prefill_conv(_ptr(y), W, _ptr(conv_w), _ptr(conv_bias), _ptr(conv_state), _ptr(A_log),
+                                      _ptr(dt_bias), int(b_off), int(a_off), _ptr(state), _ptr(state), _ptr(o), B, T,
+                                      int(Hk), H, d, d, K, float(scale), _ptr(ws), ws.numel(), _stream(y))
+    check(st, "q35_gdn_chunk_prefill_conv")
+    return o
 
 
 def _gdn_decode_sliced_impl(y, A_log, dt_bias, b_off, a_off, state, scale):
@@ -538,6 +566,7 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gemm_q8_", _gemm_q8_impl),
                      ("add_rmsnorm_", _add_rmsnorm_impl), ("argmax_rows_", _argmax_rows_impl),
                      ("gemv_norm_", _gemv_norm_impl), ("gdn_decode_sliced_", _gdn_decode_sliced_impl),
+                     ("gdn_chunk_prefill_conv_", _gdn_chunk_prefill_conv_impl),
                      ("gemv_norm_conv_", _gemv_norm_conv_impl), ("gemv_gated_norm_", _gemv_gated_norm_impl)]:
     _LIB.impl(_name, _impl, "CUDA")
     _LIB.impl(_name, _no_cpu(_name), "CPU")
@@ -568,6 +597,8 @@ _LIB.impl("gated_attn_prefill_cached",
           "Meta")
 _LIB.impl("argmax_rows_", lambda x, idx: None, "Meta")
 _LIB.impl("gemv_norm_", lambda x, xa, xo, nw, eps, W, ws, y, e, pushes, T: None, "Meta")
+_LIB.impl("gdn_chunk_prefill_conv_", lambda y, cw, cb, cs, Al, dt, bo, ao, st, Hk, sc:
+          y.new_empty(y.shape[0], y.shape[1], st.shape[1], st.shape[3]), "Meta")
 _LIB.impl("gdn_decode_sliced_", lambda y, Al, dt, bo, ao, st, sc: y.new_empty(y.shape[0], st.shape[1] * st.shape[2]),
           "Meta")
 _LIB.impl("gemv_norm_conv_", lambda x, xa, xo, nw, eps, W, ws, y, cw, cb, cs: None, "Meta")
@@ -695,6 +726,21 @@ def gdn_decode_fused_(y, conv_w, conv_state, A_log, dt_bias, state, norm_w, *, b
                                            A_log.float().contiguous(), dt_bias.float().contiguous(), int(b_off),
                                            int(a_off), int(z_off), state, norm_w.float().contiguous(), head_scale,
                                            float(eps), float(d ** -0.5 if scale is None else scale))
+
+
+def gdn_chunk_prefill_conv_(y, conv_w, conv_state, A_log, dt_bias, state, *, num_k_heads, b_off, a_off,
+                            conv_bias=None, scale=None):
+    """A Gated DeltaNet layer's multi-token call from its fused projection output y [B, T, W] fp32 up to the gated
+    norm: gdn_conv (fp32) then chunk_gated_delta_rule (l2norm on) in one kernel pair, the conv + SiLU and the gate
+    terms in the chunk kernel's load phase (HF:454-530). conv_state [B, 3, C] and state [B, H, d, d] (d = 128; the
+    initial state, then the final one) are advanced in place; returns o [B, T, H, d] fp32. The conv kernel size must
+    be 4."""
+    d = state.shape[-1]
+    w = conv_w.reshape(conv_w.shape[0], conv_w.shape[-1])
+    return torch.ops.q35.gdn_chunk_prefill_conv_(y, w.float().contiguous(), conv_bias, conv_state,
+                                                 A_log.float().contiguous(), dt_bias.float().contiguous(), int(b_off),
+                                                 int(a_off), state, int(num_k_heads),
+                                                 float(d ** -0.5 if scale is None else scale))
 
 
 def gdn_decode_sliced_(y, A_log, dt_bias, state, *, b_off, a_off, scale=None):

@@ -21,6 +21,9 @@
  *   q35_gdn_conv             HF:454-499 (causal_conv1d_fn / causal_conv1d_update + SiLU, split, beta, g);
  *                            engine/kernels_qwen35.js:127-178 `conv` + `convState`, :226-229 (gate terms of `delta`)
  *   q35_gated_rmsnorm        HF:168-184 Qwen3_5RMSNormGated; engine/kernels_qwen35.js:237-243 (epilogue of `delta`)
+ *   q35_gdn_chunk_prefill_conv  HF:454-530 for a multi-token call: q35_gdn_conv (fp32) + q35_gdn_chunk_prefill
+ *                            (fp32, l2norm on) with the front end in the chunk kernel's load phase;
+ *                            engine/kernels_qwen35.js:127-247
  *   q35_gdn_decode_fused     HF:454-543 for one cached token: q35_gdn_conv + q35_gdn_recurrent +
  *                            q35_gated_rmsnorm in one launch; engine/kernels_qwen35.js:127-247
  *   q35_attn_prep            HF:667-680 (q / gate split, q_norm / k_norm, partial RoPE of k, cache update);
@@ -211,6 +214,25 @@ int q35_gdn_conv(const float* y, int64_t ldy, const float* conv_w, const float* 
                  const float* A_log, const float* dt_bias, int64_t b_off, int64_t a_off, void* q, void* k, void* v,
                  float* g, float* beta, int64_t B, int64_t T, int64_t Hk, int64_t dk, int64_t Hv, int64_t dv,
                  int64_t K, int dtype, q35_stream_t stream);
+
+/*
+ * A Gated DeltaNet layer's multi-token call after its input projection, up to the gated norm: q35_gdn_conv with fp32
+ * outputs followed by q35_gdn_chunk_prefill on them (fp32 path, use_qk_l2norm on, chunk 64), with the conv + SiLU,
+ * the l2 norms and the gate terms computed in the chunk kernel's load phase, so that q, k, v, g and beta are never
+ * written out. The same arithmetic in the same order as that pair of calls (the same results, bit for bit).
+ * HF:454-530 (causal_conv1d_fn + SiLU, split, beta / g, torch_chunk_gated_delta_rule); engine/kernels_qwen35.js
+ * :127-247 (`conv`, `convState`, `delta`).
+ *   y, conv_w [C, conv_k], conv_bias, conv_state [B, conv_k - 1, C], A_log, dt_bias, b_off, a_off: as q35_gdn_conv,
+ *      conv_state advanced in place; conv_k must be 4 (Qwen3.5's conv kernel size); conv_w 16-byte aligned too
+ *   initial_state (or NULL: zeros), final_state [B, H, 128, 128] fp32 (they may be the same buffer: the state is
+ *      then advanced in place); out [B, T, H, 128] fp32; Hk k heads, H v heads (H % Hk == 0), Dk = Dv = 128
+ *   workspace: q35_gdn_chunk_workspace_bytes(B, T, H, 128, 128, 64, Q35_F32) bytes, 256-byte aligned
+ */
+int q35_gdn_chunk_prefill_conv(const float* y, int64_t ldy, const float* conv_w, const float* conv_bias,
+                               float* conv_state, const float* A_log, const float* dt_bias, int64_t b_off,
+                               int64_t a_off, const float* initial_state, float* final_state, float* out,
+                               int64_t B, int64_t T, int64_t Hk, int64_t H, int64_t Dk, int64_t Dv, int64_t conv_k,
+                               float scale, void* workspace, size_t workspace_bytes, q35_stream_t stream);
 
 /*
  * One decode step of a Gated DeltaNet layer after its input projection, fused: q35_gdn_conv (T = 1), then
