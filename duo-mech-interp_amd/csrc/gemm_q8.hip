@@ -8,24 +8,35 @@
 // Arithmetic: bf16 MFMA (v_mfma_f32_32x32x16_bf16) with fp32 accumulation. Each x is split into hi = bf16(x) and
 // lo = bf16(x - hi), so x = hi + lo up to 2^-17 |x|; the int8 weights are exact in bf16. Two products per tile
 // (hi W + lo W) therefore give the fp32 product to about 1e-5 relative, which keeps the prefill on the fp32 numerics
-// of the reference path (HF runs these projections in fp32).
-//
-// Layout: 256 threads = 2 x 2 waves over a BM x 128 output tile (BM 64 or 128), K in steps of 64. Per K step the
-// block stages x[BM, 64] (split into hi and lo) and W[128, 64] (int8 -> bf16) in LDS, rows of 64 bf16 = 8 segments of
-// 16 bytes, segment s of row r at s ^ (r & 7) (the 32 rows an MFMA operand read touches hit 8 distinct segments).
-// The next step's global loads are issued before the current step's MFMAs, so they are in flight during them.
-// Blocks run n-fastest inside an m panel: the panel's rows of x stay in L2 while its column tiles pass.
-// Group scales (GS): the MFMAs of one group (two K steps) accumulate into a second register set, which is then added
-// to the result scaled by the group's scale of the lane's column (one fp32 FMA per accumulator per 128 inputs).
+// of the reference path (HF runs these projections in fp32). Group scales (GS): the products of one 128-input group
+// accumulate into a second register set, which is added to the result scaled by the group's scale of the column.
 // Epilogues: store, accumulate into y (the residual add after down_proj / out_proj), or SwiGLU over interleaved
 // (gate, up) row pairs with the neuron pushes applied, writing y[m, n / 2].
+//
+// Two kernels:
+//   gemm_q8_dma_kernel (N >= 2048, K <= 2048: the gate/up and input projections): 128 x 256 tiles, one block of 8
+//     waves per CU, each wave a 64 x 64 output tile. x (fp32) and W (int8) go global -> LDS by DMA (global_load_lds,
+//     no registers) in four stages of 32 K, three in flight while one is consumed. What bounds this product on
+//     MI355X is VALU issue, not the matrix core (a 64-lane VALU instruction takes 4 cycles): so each stage's x is
+//     split into bf16 hi / lo planes once per block (every element converted once, not once per wave that reads
+//     it), W stays int8 in LDS and each wave widens only its own fragments. Per stage: MFMAs of stage s first; while
+//     the matrix core runs them, the wait for stage s + 1, a barrier, the next DMA into the freed buffer, the split
+//     of stage s + 1, a second barrier. The tiles of one XCD are consecutive (n fastest inside an m panel), so a
+//     panel's x stays in that XCD's L2. LDS rows are XOR-swizzled so that the 16-byte accesses of 16 consecutive
+//     lanes hit distinct banks.
+//   gemm_q8_rs_kernel (the rest: the N = 1024 output and down projections): 2 x 2 waves over BM x 128 tiles, x and W
+//     staged through registers into LDS (split and widened on the way), the next K step's loads issued before the
+//     current step's MFMAs; two blocks per CU.
+#include <type_traits>
+
 #include "q35_common.h"
 #include "q35hip.h"
 
 namespace q35 {
 
-constexpr int kGN = 128;  // output columns per block
-constexpr int kGK = 64;   // K step
+constexpr int kGN = 128;  // output columns per block (register-staged kernel)
+constexpr int kGK = 64;   // K step (register-staged kernel)
+constexpr int kQK = 32;   // K per pipeline stage (DMA kernel)
 
 enum GemmEpi : int { kGemmStore = 0, kGemmAccumulate = 1, kGemmSwiglu = 2 };
 
@@ -60,8 +71,252 @@ __device__ __forceinline__ bf16x8 i8tobf(uint32_t w0, uint32_t w1) {
   return r;
 }
 
+__device__ __forceinline__ uint32_t gemm_lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// 16 bytes per lane from global memory to LDS (lane i's bytes land at M0 + 16 i), from a uniform 64-bit base (moved
+// to scalar registers) and a 32-bit per-lane byte offset; no registers hold the data. Inline asm, so that the
+// compiler neither moves LDS accesses across it nor waits for it: completion is awaited with explicit vmcnt counts,
+// and the K loop issues no other vector memory load.
+__device__ __forceinline__ void gemm_dma16s(const void* sbase, uint32_t voff, uint32_t lds_dst) {
+  const uint64_t a = reinterpret_cast<uint64_t>(sbase);
+  const uint64_t u = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_dst), "v"(voff),
+               "s"(reinterpret_cast<const void*>(u))
+               : "memory", "m0");
+}
+template <int N> __device__ __forceinline__ void gemm_wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// DMA kernel: 128 x 256 tiles, 512 threads (wave w: rows 64 (w / 4), columns 64 (w % 4)), four DMA stages.
+constexpr int kDBM = 128, kDBN = 256, kDNS = 4;
+constexpr int kDGS = 16;               // groups of 128 inputs whose scales the block holds (K <= 2048)
+// LDS layouts (a 16-byte access by 16 consecutive lanes is conflict-free when the 16 addresses fall in distinct
+// 16-byte slots of a 256-byte window; the swizzles below are chosen for the patterns that read each area):
+constexpr int kDXB = kDBM * kQK * 4;   // x bytes per stage: fp32 rows of 128 B, 16-byte chunk c at c ^ ((row >> 1) & 1)
+constexpr int kDWB = kDBN * kQK;       // W bytes per stage: int8 rows of 32 B, 16-byte half h at h ^ ((row >> 3) & 1)
+constexpr int kDSB = kDXB + kDWB;
+constexpr int kDXC = kDBM * kQK * 2;   // one bf16 plane (hi or lo) of a stage's x: rows of 64 B, 16-byte chunk c at
+                                       // c ^ ((row >> 2) & 3)
+// DMA instructions (1 KB) per wave and stage: two of x (rows 8 q .. 8 q + 7, q = w, w + 8) and one of W (rows
+// 32 w .. 32 w + 31)
+
+template <int EPI, bool GS>
+__global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __restrict__ X, int64_t ldx,
+                                                             const int8_t* __restrict__ W,
+                                                             const float* __restrict__ ws, float* __restrict__ Y,
+                                                             int64_t ldy, int M, int N, int K,
+                                                             const q35_push* __restrict__ pushes, int npush, int T) {
+  __shared__ __attribute__((aligned(16))) char smem[kDNS * kDSB];
+  __shared__ __attribute__((aligned(16))) char xc[2][2][kDXC];  // [buffer][hi, lo]
+  __shared__ float gscale[GS ? kDGS * kDBN : 1];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv >> 2, wn = wv & 3;
+  const int l32 = lane & 31, lh = lane >> 5;
+  // tile order: block b runs on XCD b % 8; with the tile count a multiple of 8, XCD j takes the consecutive tiles
+  // j * ntiles / 8 .. (n fastest inside an m panel)
+  const int nbn = (N + kDBN - 1) / kDBN;
+  const int ntiles = nbn * ((M + kDBM - 1) / kDBM);
+  const int tile = (ntiles & 7) == 0 ? (int)(blockIdx.x & 7) * (ntiles >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int bm = tile / nbn, bn = tile - bm * nbn;
+  const int m0 = bm * kDBM, n0 = bn * kDBN;
+  const int G = K >> 7;
+  const int KT = K / kQK;
+
+  // DMA sources of this lane (32-bit byte offsets from x and W; the launcher keeps both under 4 GB)
+  uint32_t xsrc[2], xoff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = wv + 8 * i;
+    const int row = 8 * q + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 1);
+    xsrc[i] = (uint32_t)(((size_t)min(m0 + row, M - 1) * ldx + 4 * c) * 4);
+    xoff[i] = (uint32_t)(q * 1024);
+  }
+  uint32_t wsrc, woff;
+  {
+    const int row = 32 * wv + (lane >> 1);
+    const int h = (lane & 1) ^ ((row >> 3) & 1);
+    wsrc = (uint32_t)((size_t)min(n0 + row, N - 1) * K + 16 * h);
+    woff = (uint32_t)(kDXB + wv * 1024);
+  }
+  const uint32_t lds0 = gemm_lds_u32(smem);
+  auto issue = [&](int s, int buf) {
+    const uint32_t base = lds0 + buf * kDSB;
+    gemm_dma16s(X, xsrc[0] + (uint32_t)(s * kQK * 4), base + xoff[0]);
+    gemm_dma16s(X, xsrc[1] + (uint32_t)(s * kQK * 4), base + xoff[1]);
+    gemm_dma16s(W, wsrc + (uint32_t)(s * kQK), base + woff);
+  };
+  auto wait_stage = [&](int s) {  // stage s has landed in every wave's part; every wave is past its earlier reads
+    const int ahead = min(KT - 1 - s, kDNS - 2);  // stages issued after s that may still be in flight
+    if (ahead >= 2) gemm_wait_vm<6>();
+    else if (ahead == 1) gemm_wait_vm<3>();
+    else gemm_wait_vm<0>();
+    lds_barrier();
+  };
+  // the split of a stage's x: thread -> row tid / 4, k 8 (tid % 4) .. + 7
+  const int cr = tid >> 2, c8 = tid & 3;
+  const uint32_t cv0 = (uint32_t)(cr * 128 + (((2 * c8) ^ ((cr >> 1) & 1)) << 4));
+  const uint32_t cv1 = (uint32_t)(cr * 128 + (((2 * c8 + 1) ^ ((cr >> 1) & 1)) << 4));
+  const uint32_t cvw = (uint32_t)(cr * 64 + ((c8 ^ ((cr >> 2) & 3)) << 4));
+  auto convert = [&](int s, int xb) {
+    const char* st = smem + (s % kDNS) * kDSB;
+    bf16x8 hi, lo;
+    split8(*reinterpret_cast<const f32x4*>(st + cv0), *reinterpret_cast<const f32x4*>(st + cv1), hi, lo);
+    *reinterpret_cast<bf16x8*>(xc[xb][0] + cvw) = hi;
+    *reinterpret_cast<bf16x8*>(xc[xb][1] + cvw) = lo;
+  };
+  // fragment offsets: A rows wm 64 + 32 mt + l32 in the bf16 planes, chunk 2 lh + j (k = 16 lh + 8 j .. + 7); B rows
+  // wn 64 + 32 nt + l32 of the stage's W, half lh (k = 16 lh .. + 15: fragment j is its bytes 8 j .. 8 j + 7). The
+  // mt = 1 and nt = 1 rows are 32 rows further with the same swizzle (offsets + 2048 and + 1024).
+  uint32_t aoff[2];
+  {
+    const int r = wm * 64 + l32;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) aoff[j] = (uint32_t)(r * 64 + (((2 * lh + j) ^ ((r >> 2) & 3)) << 4));
+  }
+  const uint32_t boff = (uint32_t)(kDXB + (wn * 64 + l32) * 32 + ((lh ^ ((l32 >> 3) & 1)) << 4));
+
+  f32x16 acc[2][2], gacc[2][2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      acc[mt][nt] = zero16();
+      gacc[mt][nt] = zero16();  // (overwritten: a group's first MFMAs start from zero)
+    }
+
+#pragma unroll
+  for (int s = 0; s < kDNS - 1; ++s)
+    if (s < KT) issue(s, s);
+  if constexpr (GS) {
+    // the block's group scales, [group][column]: loaded behind the first stages (the wait for them ends about when
+    // stage 0 lands, which the loop waits for anyway), so that no register load waits inside the K loop
+    for (int i = tid; i < G * kDBN; i += 512) {
+      const int g = i / kDBN, c = i - g * kDBN;
+      gscale[i] = ws[(size_t)min(n0 + c, N - 1) * G + g];
+    }
+  }
+  wait_stage(0);
+  if (kDNS - 1 < KT) issue(kDNS - 1, kDNS - 1);
+  convert(0, 0);
+  lds_barrier();
+
+  // one stage; ph = s % 4 when the group scales are on (a group of 128 inputs is four stages): the group's first
+  // MFMAs start from zero and its last stage folds it in, with no per-stage test
+  auto stage = [&](int s, auto ph_c) {
+    constexpr int ph = decltype(ph_c)::value;
+    const char* st = smem + (s % kDNS) * kDSB;
+    const char* xh = xc[s & 1][0];
+    const char* xl = xc[s & 1][1];
+    // every fragment read of the stage is issued before the first MFMA (left to itself the scheduler interleaves
+    // read -> wait -> MFMA and serialises the LDS round trips)
+    u32x4 wr[2];
+    bf16x8 ah[2][2], al[2][2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) wr[nt] = *reinterpret_cast<const u32x4*>(st + boff + nt * 1024);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        ah[j][mt] = *reinterpret_cast<const bf16x8*>(xh + aoff[j] + mt * 2048);
+        al[j][mt] = *reinterpret_cast<const bf16x8*>(xl + aoff[j] + mt * 2048);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bf16x8 b[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) b[nt] = i8tobf(wr[nt][2 * j], wr[nt][2 * j + 1]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          if constexpr (GS) gacc[mt][nt] = mfma32(ah[j][mt], b[nt], (ph == 0 && j == 0) ? zero16() : gacc[mt][nt]);
+          else acc[mt][nt] = mfma32(ah[j][mt], b[nt], acc[mt][nt]);
+        }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          f32x16& d = GS ? gacc[mt][nt] : acc[mt][nt];
+          d = mfma32(al[j][mt], b[nt], d);
+        }
+    }
+    if (s + 1 < KT) {
+      wait_stage(s + 1);  // also: every wave has read stage s's W and the other x buffer
+      if (s + kDNS < KT) issue(s + kDNS, s % kDNS);
+      convert(s + 1, (s + 1) & 1);
+    }
+    if constexpr (GS && ph == 3) {  // end of a group of 128 inputs: fold it in with its scale
+      const int g = s >> 2;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const float sc = gscale[g * kDBN + wn * 64 + 32 * nt + l32];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[mt][nt][r] += sc * gacc[mt][nt][r];
+      }
+    }
+    if (s + 1 < KT) lds_barrier();  // stage s + 1's split is complete
+  };
+  if constexpr (GS) {
+    for (int s = 0; s < KT; s += 4) {  // K is a multiple of 128
+      stage(s, std::integral_constant<int, 0>{});
+      stage(s + 1, std::integral_constant<int, 1>{});
+      stage(s + 2, std::integral_constant<int, 2>{});
+      stage(s + 3, std::integral_constant<int, 3>{});
+    }
+  } else {
+    for (int s = 0; s < KT; ++s) stage(s, std::integral_constant<int, 0>{});
+  }
+
+  // epilogue: lane holds column n = n0 + wn 64 + 32 nt + l32, rows m0 + wm 64 + 32 mt + 8 (r / 4) + 4 lh + r % 4
+  const int mb = m0 + wm * 64 + 4 * lh;
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int n = n0 + wn * 64 + 32 * nt + l32;
+    const float sc = GS ? 1.f : ws[min(n, N - 1)];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dm = 32 * mt + 8 * (r >> 2) + (r & 3);
+        const int m = mb + dm;
+        const float v = acc[mt][nt][r] * sc;
+        if (EPI == kGemmSwiglu) {
+          const float up = __shfl_xor(v, 1, 64);  // the odd column of the pair sits in the neighbouring lane
+          if ((l32 & 1) == 0 && m < M && n + 1 < N) {
+            const int neuron = n >> 1;
+            float a = gemm_silu(v) * up;
+            if (npush > 0) {
+              const int row = min(m / T, 3);
+              for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
+            }
+            Y[(size_t)m * ldy + neuron] = a;
+          }
+        } else if (m < M && n < N) {
+          float* dst = Y + (size_t)m * ldy + n;
+          *dst = EPI == kGemmAccumulate ? *dst + v : v;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Register-staged kernel: 2 x 2 waves over BM x 128 tiles (BM 64 or 128), K in steps of 64. Per K step the block
+// stages x[BM, 64] (split into hi and lo) and W[128, 64] (int8 -> bf16) in LDS, rows of 64 bf16 = 8 segments of 16
+// bytes, segment s of row r at s ^ (r & 7). The next step's global loads are issued before the current step's MFMAs,
+// so they are in flight during them. Blocks run n-fastest inside an m panel.
 template <int BM, int EPI, bool GS>
-__global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const float* __restrict__ X, int64_t ldx,
+__global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restrict__ X, int64_t ldx,
                                                          const int8_t* __restrict__ W, const float* __restrict__ ws,
                                                          float* __restrict__ Y, int64_t ldy, int M, int N, int K,
                                                          const q35_push* __restrict__ pushes, int npush, int T) {
@@ -220,15 +475,34 @@ extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_d
   if (ldx < K) return Q35_EINVAL;
   if (K % kGK != 0 || ldx % 4 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return Q35_EUNSUPPORTED;
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // wide products with K <= 2048 (and x, W addressable with 32-bit byte offsets): the DMA kernel
+  if (N >= 2048 && K <= 128 * kDGS && ((M - 1) * ldx + K) * 4 <= 0xffffffffLL && N * K <= 0xffffffffLL) {
+    const int64_t nblocks = ((M + kDBM - 1) / kDBM) * ((N + kDBN - 1) / kDBN);
+    if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
+#define Q35_GEMM_DMA(E, G_)                                                                                       \
+  hipLaunchKernelGGL((gemm_q8_dma_kernel<E, G_>), dim3((unsigned)nblocks), dim3(512), 0, st, x, ldx, W, w_scale, y, \
+                     ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T)
+    if (gs) {
+      if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, true);
+      else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, true);
+      else Q35_GEMM_DMA(kGemmSwiglu, true);
+    } else {
+      if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, false);
+      else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, false);
+      else Q35_GEMM_DMA(kGemmSwiglu, false);
+    }
+#undef Q35_GEMM_DMA
+    return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+  }
   const int64_t nbn = (N + kGN - 1) / kGN;
   // 128-row tiles when they still give at least two blocks per compute unit, else 64-row tiles
   const bool big = ((M + 127) / 128) * nbn >= 512;
   const int BM = big ? 128 : 64;
   const int64_t nblocks = ((M + BM - 1) / BM) * nbn;
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 #define Q35_GEMM_LAUNCH(BMV, E, G)                                                                               \
-  hipLaunchKernelGGL((gemm_q8_kernel<BMV, E, G>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W, w_scale, \
+  hipLaunchKernelGGL((gemm_q8_rs_kernel<BMV, E, G>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W, w_scale, \
                      y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T)
 #define Q35_GEMM_EPI(BMV, G)                                              \
   if (epilogue == kGemmStore) Q35_GEMM_LAUNCH(BMV, kGemmStore, G);        \
