@@ -16,14 +16,16 @@
 // Two kernels:
 //   gemm_q8_dma_kernel (N >= 2048, K <= 2048: the gate/up and input projections): 128 x 256 tiles, one block of 8
 //     waves per CU, each wave a 64 x 64 output tile. x (fp32) and W (int8) go global -> LDS by DMA (global_load_lds,
-//     no registers) in four stages of 32 K, three in flight while one is consumed. What bounds this product on
-//     MI355X is VALU issue, not the matrix core (a 64-lane VALU instruction takes 4 cycles): so each stage's x is
-//     split into bf16 hi / lo planes once per block (every element converted once, not once per wave that reads
-//     it), W stays int8 in LDS and each wave widens only its own fragments. Per stage: MFMAs of stage s first; while
-//     the matrix core runs them, the wait for stage s + 1, a barrier, the next DMA into the freed buffer, the split
-//     of stage s + 1, a second barrier. The tiles of one XCD are consecutive (n fastest inside an m panel), so a
-//     panel's x stays in that XCD's L2. LDS rows are XOR-swizzled so that the 16-byte accesses of 16 consecutive
-//     lanes hit distinct banks.
+//     no registers) in four stages of 32 K. What bounds this product on MI355X is VALU issue and the matrix core's
+//     idle time around barriers, not bandwidth (a 64-lane VALU instruction takes 4 cycles): each stage's x is split
+//     into bf16 hi / lo planes once per block (every element converted once, not once per wave that reads it), W
+//     stays int8 in LDS and each wave widens only its own fragments, and there is one barrier per stage: iteration s
+//     waits for stage s + 1, crosses the barrier, hands stage s's DMA buffer to stage s + 4, reads its A fragments,
+//     splits stage s + 1's x while the other waves' MFMAs run, issues its MFMAs and reads stage s + 1's W fragments
+//     (so that stage s's buffer is free at the next barrier). The tiles of one XCD are consecutive (n fastest inside
+//     an m panel), so a panel's x stays in that XCD's L2. LDS rows are XOR-swizzled so that the 16-byte accesses of
+//     16 consecutive lanes hit distinct banks. The SwiGLU epilogue splits each (gate, up) lane pair's rows between
+//     the two lanes.
 //   gemm_q8_rs_kernel (the rest: the N = 1024 output and down projections): 2 x 2 waves over BM x 128 tiles, x and W
 //     staged through registers into LDS (split and widened on the way), the next K step's loads issued before the
 //     current step's MFMAs; two blocks per CU.
@@ -116,6 +118,8 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // wave w owns rows 64 (w / 4) .. + 63 and columns 64 (w % 4) .. + 63: 2 x 2 MFMA tiles of 32 x 32
+  constexpr int MT = 2, NT = 2;
   const int wm = wv >> 2, wn = wv & 3;
   const int l32 = lane & 31, lh = lane >> 5;
   // tile order: block b runs on XCD b % 8; with the tile count a multiple of 8, XCD j takes the consecutive tiles
@@ -171,9 +175,9 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
     *reinterpret_cast<bf16x8*>(xc[xb][0] + cvw) = hi;
     *reinterpret_cast<bf16x8*>(xc[xb][1] + cvw) = lo;
   };
-  // fragment offsets: A rows wm 64 + 32 mt + l32 in the bf16 planes, chunk 2 lh + j (k = 16 lh + 8 j .. + 7); B rows
-  // wn 64 + 32 nt + l32 of the stage's W, half lh (k = 16 lh .. + 15: fragment j is its bytes 8 j .. 8 j + 7). The
-  // mt = 1 and nt = 1 rows are 32 rows further with the same swizzle (offsets + 2048 and + 1024).
+  // fragment offsets: A rows 64 wm + 32 mt + l32 in the bf16 planes, chunk 2 lh + j (k = 16 lh + 8 j .. + 7); B rows
+  // 64 wn + 32 nt + l32 of the stage's W, half lh (k = 16 lh .. + 15: fragment j is its bytes 8 j .. 8 j + 7). Rows
+  // 32 apart have the same swizzle (A offsets step by 2048, B offsets by 1024).
   uint32_t aoff[2];
   {
     const int r = wm * 64 + l32;
@@ -182,11 +186,11 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
   }
   const uint32_t boff = (uint32_t)(kDXB + (wn * 64 + l32) * 32 + ((lh ^ ((l32 >> 3) & 1)) << 4));
 
-  f32x16 acc[2][2], gacc[2][2];
+  f32x16 acc[MT][NT], gacc[MT][NT];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
       acc[mt][nt] = zero16();
       gacc[mt][nt] = zero16();  // (overwritten: a group's first MFMAs start from zero)
     }
@@ -202,69 +206,70 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
       gscale[i] = ws[(size_t)min(n0 + c, N - 1) * G + g];
     }
   }
+  // one barrier per stage. Iteration s: wait for stage s + 1 and cross the barrier (after it: stage s's split is
+  // complete, every wave has read stage s's W and is done with the other x buffer); hand stage s's DMA buffer to
+  // stage s + 4; read stage s's A fragments; split stage s + 1's x (its VALU work overlaps the other waves' MFMAs);
+  // issue stage s's MFMAs; read stage s + 1's W fragments for the next iteration.
+  u32x4 wr[NT];
+  auto read_w = [&](int s) {
+    const char* st = smem + (s % kDNS) * kDSB;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) wr[nt] = *reinterpret_cast<const u32x4*>(st + boff + nt * 1024);
+  };
   wait_stage(0);
   if (kDNS - 1 < KT) issue(kDNS - 1, kDNS - 1);
   convert(0, 0);
-  lds_barrier();
+  read_w(0);
 
-  // one stage; ph = s % 4 when the group scales are on (a group of 128 inputs is four stages): the group's first
-  // MFMAs start from zero and its last stage folds it in, with no per-stage test
   auto stage = [&](int s, auto ph_c) {
     constexpr int ph = decltype(ph_c)::value;
-    const char* st = smem + (s % kDNS) * kDSB;
+    if (s + 1 < KT) wait_stage(s + 1);
+    else lds_barrier();
+    if (s + kDNS < KT) issue(s + kDNS, s % kDNS);
     const char* xh = xc[s & 1][0];
     const char* xl = xc[s & 1][1];
-    // every fragment read of the stage is issued before the first MFMA (left to itself the scheduler interleaves
-    // read -> wait -> MFMA and serialises the LDS round trips)
-    u32x4 wr[2];
-    bf16x8 ah[2][2], al[2][2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) wr[nt] = *reinterpret_cast<const u32x4*>(st + boff + nt * 1024);
+    bf16x8 ah[2][MT], al[2][MT];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < MT; ++mt) {
         ah[j][mt] = *reinterpret_cast<const bf16x8*>(xh + aoff[j] + mt * 2048);
         al[j][mt] = *reinterpret_cast<const bf16x8*>(xl + aoff[j] + mt * 2048);
       }
+    if (s + 1 < KT) convert(s + 1, (s + 1) & 1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      bf16x8 b[2];
+      bf16x8 b[NT];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) b[nt] = i8tobf(wr[nt][2 * j], wr[nt][2 * j + 1]);
+      for (int nt = 0; nt < NT; ++nt) b[nt] = i8tobf(wr[nt][2 * j], wr[nt][2 * j + 1]);
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
           if constexpr (GS) gacc[mt][nt] = mfma32(ah[j][mt], b[nt], (ph == 0 && j == 0) ? zero16() : gacc[mt][nt]);
           else acc[mt][nt] = mfma32(ah[j][mt], b[nt], acc[mt][nt]);
         }
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
           f32x16& d = GS ? gacc[mt][nt] : acc[mt][nt];
           d = mfma32(al[j][mt], b[nt], d);
         }
     }
-    if (s + 1 < KT) {
-      wait_stage(s + 1);  // also: every wave has read stage s's W and the other x buffer
-      if (s + kDNS < KT) issue(s + kDNS, s % kDNS);
-      convert(s + 1, (s + 1) & 1);
-    }
+    if (s + 1 < KT) read_w(s + 1);
     if constexpr (GS && ph == 3) {  // end of a group of 128 inputs: fold it in with its scale
       const int g = s >> 2;
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < NT; ++nt) {
         const float sc = gscale[g * kDBN + wn * 64 + 32 * nt + l32];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[mt][nt][r] += sc * gacc[mt][nt][r];
       }
     }
-    if (s + 1 < KT) lds_barrier();  // stage s + 1's split is complete
   };
   if constexpr (GS) {
     for (int s = 0; s < KT; s += 4) {  // K is a multiple of 128
@@ -277,24 +282,27 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
     for (int s = 0; s < KT; ++s) stage(s, std::integral_constant<int, 0>{});
   }
 
-  // epilogue: lane holds column n = n0 + wn 64 + 32 nt + l32, rows m0 + wm 64 + 32 mt + 8 (r / 4) + 4 lh + r % 4
+  // epilogue: lane holds column n = n0 + 64 wn + 32 nt + l32, rows m0 + 64 wm + 32 mt + 8 (r / 4) + 4 lh + r % 4
   const int mb = m0 + wm * 64 + 4 * lh;
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
+  for (int nt = 0; nt < NT; ++nt) {
     const int n = n0 + wn * 64 + 32 * nt + l32;
     const float sc = GS ? 1.f : ws[min(n, N - 1)];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int dm = 32 * mt + 8 * (r >> 2) + (r & 3);
-        const int m = mb + dm;
+        const int m = mb + 32 * mt + 8 * (r >> 2) + (r & 3);
         const float v = acc[mt][nt][r] * sc;
         if (EPI == kGemmSwiglu) {
-          const float up = __shfl_xor(v, 1, 64);  // the odd column of the pair sits in the neighbouring lane
-          if ((l32 & 1) == 0 && m < M && n + 1 < N) {
+          // columns n (gate, even lane) and n + 1 (up, odd lane) of a neuron: the even lane finishes the rows with
+          // r < 8, the odd lane those with r >= 8
+          const float o = __shfl_xor(v, 1, 64);
+          const bool odd = (l32 & 1) != 0;
+          if (odd == (r >= 8) && m < M && (n | 1) < N) {
             const int neuron = n >> 1;
-            float a = gemm_silu(v) * up;
+            const float gate = odd ? o : v, up = odd ? v : o;
+            float a = gemm_silu(gate) * up;
             if (npush > 0) {
               const int row = min(m / T, 3);
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
