@@ -45,6 +45,22 @@ enum GemmEpi : int { kGemmStore = 0, kGemmAccumulate = 1, kGemmSwiglu = 2 };
 __device__ __forceinline__ int gsw(int r, int s) { return s ^ (r & 7); }
 __device__ __forceinline__ float gemm_silu(float x) { return x / (1.f + __expf(-x)); }
 
+// Whether any of the push records can touch neurons nlo .. nhi - 1 (a record for every neuron, or for one in the
+// range): a block whose neurons no record touches skips the per-output push loop (the model passes a fixed number of
+// records, unused ones matching no neuron). Uniform: the records are read with scalar loads.
+__device__ __forceinline__ bool gemm_pushes_touch(const q35_push* ps, int npush, int nlo, int nhi) {
+  bool any = false;
+  for (int p = 0; p < npush; ++p) {
+    const int pn = ps[p].neuron;
+    any |= pn < 0 || (pn >= nlo && pn < nhi);
+  }
+  return any;
+}
+// the batch row of token row m (rows of T tokens each), min(m / T, 3), without a division
+__device__ __forceinline__ int gemm_push_row(int m, int T) {
+  return (int)(m >= T) + (int)((int64_t)m >= 2 * (int64_t)T) + (int)((int64_t)m >= 3 * (int64_t)T);
+}
+
 __device__ __forceinline__ float gemm_push(const q35_push* ps, int n, int row, float a) {
   const int pn = ps->neuron;
   if (pn != n && pn >= 0) return a;
@@ -284,6 +300,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
 
   // epilogue: lane holds column n = n0 + 64 wn + 32 nt + l32, rows m0 + 64 wm + 32 mt + 8 (r / 4) + 4 lh + r % 4
   const int mb = m0 + wm * 64 + 4 * lh;
+  const bool pushes_here = EPI == kGemmSwiglu && gemm_pushes_touch(pushes, npush, n0 >> 1, (n0 + kDBN) >> 1);
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int n = n0 + wn * 64 + 32 * nt + l32;
@@ -303,8 +320,8 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
             const int neuron = n >> 1;
             const float gate = odd ? o : v, up = odd ? v : o;
             float a = gemm_silu(gate) * up;
-            if (npush > 0) {
-              const int row = min(m / T, 3);
+            if (pushes_here) {
+              const int row = gemm_push_row(m, T);
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
             }
             Y[(size_t)m * ldy + neuron] = a;
@@ -440,6 +457,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
   }
 
   // epilogue: lane holds column n = n0 + wn 64 + 32 nt + l32, rows m0 + wm BM/2 + 32 mt + 8 (r / 4) + 4 lh + r % 4
+  const bool pushes_here = EPI == kGemmSwiglu && gemm_pushes_touch(pushes, npush, n0 >> 1, (n0 + kGN) >> 1);
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int n = n0 + wn * 64 + 32 * nt + l32;
@@ -453,9 +471,12 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
         if (EPI == kGemmSwiglu) {
           const float up = __shfl_xor(v, 1, 64);  // the odd column of the pair sits in the neighbouring lane
           if ((l32 & 1) == 0 && m < M && n + 1 < N) {
-            const int neuron = n >> 1, row = min(m / T, 3);
+            const int neuron = n >> 1;
             float a = gemm_silu(v) * up;
-            for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
+            if (pushes_here) {
+              const int row = gemm_push_row(m, T);
+              for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
+            }
             Y[(size_t)m * ldy + neuron] = a;
           }
         } else if (m < M && n < N) {

@@ -111,3 +111,26 @@ def test_gemm_q8_group_scales_swiglu_with_pushes():
     announce("gemm_q8 g128 swiglu")
     a = ops.gemm_q8(x.to(dev), q.to(dev), s.to(dev), epilogue="swiglu", pushes=ops.pack_pushes(pushes, dev), T=T)
     assert oracle.rel_err(a.cpu(), ref) <= TOL
+
+
+def test_gemm_q8_swiglu_placeholder_push_records():
+    """Eight push records as the model passes them: real pushes on a few neurons (two on either side of a 128-neuron
+    block boundary, one further on), the rest placeholders whose neuron index matches no neuron; batch rows of
+    T = 200 tokens (push rows 0..2). Blocks that no record touches skip the push loop; the result equals the
+    oracle's in-order pushes."""
+    dev = device()
+    I, H, M, T = 3584, 1024, 600, 200
+    qg, sg = _q8g(I, H, 41)
+    qu, su = _q8g(I, H, 42)
+    q = torch.stack([qg, qu], dim=1).reshape(2 * I, H).contiguous()
+    s = torch.stack([sg, su], dim=1).reshape(2 * I, H // 128).contiguous()
+    x = torch.randn(M, H, generator=torch.Generator().manual_seed(43))
+    none = (1 << 30, "add", [0.0])
+    pushes = [(127, "add", [1.0, -2.0, 0.5]), none, (128, "mul", [2.0, 3.0, 0.5]), none, none,
+              (3000, "add", [0.25, 0.5, 0.75]), none, (3000, "mul", [-1.0, 2.0, 1.5])]
+    ref = omlp.swiglu_push(omlp.q8_linear(x, qg, sg), omlp.q8_linear(x, qu, su), pushes, T=T)
+    announce("gemm_q8 g128 swiglu placeholder pushes")
+    a = ops.gemm_q8(x.to(dev), q.to(dev), s.to(dev), epilogue="swiglu", pushes=ops.pack_pushes(pushes, dev), T=T)
+    assert oracle.rel_err(a.cpu(), ref) <= TOL
+    cols = [127, 128, 3000]  # the pushed neurons alone, at the GEMM's own error (an unapplied push would be O(1) off)
+    assert oracle.rel_err(a.cpu()[:, cols], ref[:, cols]) <= TOL
