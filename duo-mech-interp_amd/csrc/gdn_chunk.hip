@@ -844,7 +844,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
 //   Qe  [64 pos][128 d]  = Q^ e^gamma (0 past the end)      Kt [128 d][64 pos]  = (K^ e^(gamma_last - gamma))^T
 //   P   [64 t][64 s]     = (q^_t . k^_s) e^(gamma_t - gamma_s) for s <= t (lower triangle only)
 //   e^gamma_last,  with T = (I - L)^-1, L[t][s] = -beta_t (k^_t . k^_s) e^(gamma_t - gamma_s) (s < t).
-// Kernel F2, gdn_f32_scan_kernel: 8 blocks per (row, head), one per 16 value columns; each carries its 128 x 16 fp32
+// Kernel F2, gdn_f32_scan_kernel: 8 blocks per (row, head), one per 16 value columns (4 blocks of 32 columns when 8
+// per (row, head) would exceed the 256 blocks that are resident at once); each carries its 128 x 16 (or 32) fp32
 // state slice in registers (wave w: state rows 32 w .. 32 w + 31) and per chunk computes
 //   V = U - W S,   O = Qe S + P V,   S <- e^gamma_last S + Kt V
 // (wave w: positions 16 w .. 16 w + 15 of V and O). The state and V tiles are exchanged through LDS.
@@ -1171,47 +1172,57 @@ __global__ __launch_bounds__(256, 1) void gdn_f32_prep_kernel(const float* __res
   if (tid == 0) recf[kFRecE / 4] = __expf(gam[kC - 1]);
 }
 
-// Operands of one chunk for one wave of the fp32 scan.
+// Operands of one chunk for one wave of the fp32 scan (CT column tiles of 16 per block).
+template <int CT>
 struct F32Ops {
   f32x4 w[8];      // W rows 16 w + li, k chunks 0..7
   f32x4 qe[8];     // Qe rows 16 w + li
   f32x4 p[4];      // P row 16 w + li, position chunks 0..3 (chunks past w unused)
   f32x4 kt[2][4];  // Kt rows 32 w + 16 i + li, position chunks 0..3
-  float u[4];      // U rows 16 w + 4 lg + r, the block's column
+  float u[CT][4];  // U rows 16 w + 4 lg + r, the block's columns
   float eg;
 };
 
+// CT column tiles of 16 per block: 8 / CT blocks per (row, head). The launcher takes CT = 2 when 8 blocks per (row,
+// head) would not all be resident at once (one block per CU: 316 VGPRs); the W, Qe, P, Kt operands are then loaded
+// once for two column tiles.
+template <int CT>
 __global__ __launch_bounds__(256, 1) void gdn_f32_scan_kernel(const char* __restrict__ ws, const float* s_in,
                                                               float* s_out, float* __restrict__ o, int T, int NC,
                                                               int H, int B, int Hk, GdnFront fe) {
-  __shared__ f32x4 sS[8][64];  // state row tiles (D layout) of the four waves
-  __shared__ f32x4 sV[4][64];  // V row tiles
+  constexpr int NSL = 8 / CT;      // blocks (slices) per (row, head)
+  __shared__ f32x4 sS[8][CT][64];  // state row tiles (D layout) of the four waves
+  __shared__ f32x4 sV[4][CT][64];  // V row tiles
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int li = lane & 15, lg = lane >> 4;
-  // the 8 blocks of one (row, head) read the same records: place them on one XCD (block i runs on XCD i % 8)
+  // the blocks of one (row, head) read the same records: place them on one XCD (block i runs on XCD i % 8)
   const int nunits = H * B, L = blockIdx.x;
   int sl, unit;
   if ((nunits & 7) == 0) {
-    sl = (L >> 3) & 7;
-    unit = 8 * (L >> 6) + (L & 7);
+    sl = (L >> 3) % NSL;
+    unit = 8 * (L / (8 * NSL)) + (L & 7);
   } else {
-    sl = L & 7;
-    unit = L >> 3;
+    sl = L % NSL;
+    unit = L / NSL;
   }
   const int h = unit % H, b = unit / H;
-  const int col = 16 * sl + li;
+  int col[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) col[ct] = 16 * (CT * sl + ct) + li;
   const char* rec0 = ws + (size_t)unit * NC * kFRecBytes;
   const size_t sbase = (size_t)unit * kD * kD;
 
-  f32x4 S[2];
+  f32x4 S[CT][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      S[i][r] = s_in ? s_in[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col] : 0.f;
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        S[ct][i][r] = s_in ? s_in[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col[ct]] : 0.f;
 
-  auto load = [&](int c, F32Ops& op) {
+  auto load = [&](int c, F32Ops<CT>& op) {
     const char* rec = rec0 + (size_t)min(c, NC - 1) * kFRecBytes;
     const float* rf = reinterpret_cast<const float*>(rec);
 #pragma unroll
@@ -1228,58 +1239,84 @@ __global__ __launch_bounds__(256, 1) void gdn_f32_scan_kernel(const char* __rest
       for (int kc = 0; kc < 4; ++kc)
         op.kt[i][kc] = *reinterpret_cast<const f32x4*>(rf + kFRecK / 4 + (32 * w + 16 * i + li) * kC + 16 * kc + 4 * lg);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) op.u[r] = rf[kFRecU / 4 + (16 * w + 4 * lg + r) * kD + col];
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) op.u[ct][r] = rf[kFRecU / 4 + (16 * w + 4 * lg + r) * kD + col[ct]];
     op.eg = rf[kFRecE / 4];
   };
 
-  auto step = [&](int c, const F32Ops& op) {
-    sS[2 * w][lane] = S[0];
-    sS[2 * w + 1][lane] = S[1];
-    lds_barrier();
-    f32x4 Sb[8];
+  auto step = [&](int c, const F32Ops<CT>& op) {
 #pragma unroll
-    for (int kc = 0; kc < 8; ++kc) Sb[kc] = (kc >> 1) == w ? S[kc & 1] : sS[kc][lane];
-    f32x4 ws_ = zero4(), oacc = zero4();
-#pragma unroll
-    for (int kc = 0; kc < 8; ++kc) {
-      ws_ = mm_k16(op.w[kc], Sb[kc], ws_);
-      oacc = mm_k16(op.qe[kc], Sb[kc], oacc);
+    for (int ct = 0; ct < CT; ++ct) {
+      sS[2 * w][ct][lane] = S[ct][0];
+      sS[2 * w + 1][ct][lane] = S[ct][1];
     }
-    f32x4 vn;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) vn[r] = op.u[r] - ws_[r];
-    sV[w][lane] = vn;
     lds_barrier();
-    f32x4 Vb[4];
+    f32x4 ws_[CT], oacc[CT];
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) Vb[kc] = kc == w ? vn : sV[kc][lane];
+    for (int ct = 0; ct < CT; ++ct) {
+      ws_[ct] = zero4();
+      oacc[ct] = zero4();
+    }
+#pragma unroll
+    for (int kc = 0; kc < 8; ++kc)
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const f32x4 sb = (kc >> 1) == w ? S[ct][kc & 1] : sS[kc][ct][lane];
+        ws_[ct] = mm_k16(op.w[kc], sb, ws_[ct]);
+        oacc[ct] = mm_k16(op.qe[kc], sb, oacc[ct]);
+      }
+    f32x4 vn[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vn[ct][r] = op.u[ct][r] - ws_[ct][r];
+      sV[w][ct][lane] = vn[ct];
+    }
+    lds_barrier();
+    f32x4 Vb[CT][4];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) Vb[ct][kc] = kc == w ? vn[ct] : sV[kc][ct][lane];
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc)
-      if (kc <= w) oacc = mm_k16(op.p[kc], Vb[kc], oacc);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct)
+        if (kc <= w) oacc[ct] = mm_k16(op.p[kc], Vb[ct][kc], oacc[ct]);
     const int tb = kC * c + 16 * w + 4 * lg;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (tb + r < T) o[(((size_t)b * T + tb + r) * H + h) * kD + col] = oacc[r];
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (tb + r < T) o[(((size_t)b * T + tb + r) * H + h) * kD + col[ct]] = oacc[ct][r];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      f32x4 s;
+      f32x4 sn[CT];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[r] = op.eg * S[i][r];
+      for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) s = mm_k16(op.kt[i][kc], Vb[kc], s);
-      S[i] = s;
+        for (int r = 0; r < 4; ++r) sn[ct][r] = op.eg * S[ct][i][r];
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) sn[ct] = mm_k16(op.kt[i][kc], Vb[ct][kc], sn[ct]);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) S[ct][i] = sn[ct];
     }
   };
 
-  // front-end form: the carried conv state of this block's channels (16 of the head's v channels, and for the first
-  // head of a k group 16 of its q and k channels) <- the last 3 inputs of [old state | y]; one lane per channel reads
-  // its sources before writing, and no other block touches the channel
-  const bool fstate = fe.cst && threadIdx.x < 48 && ((threadIdx.x >> 4) == 2 || h % (H / Hk) == 0);
+  // front-end form: the carried conv state of this block's channels (16 CT of the head's v channels, and for the first
+  // head of a k group 16 CT of its q and k channels) <- the last 3 inputs of [old state | y]; one lane per channel
+  // reads its sources before writing, and no other block touches the channel
+  constexpr int FCH = 16 * CT;
+  const int fm = (int)threadIdx.x / FCH;
+  const bool fstate = fe.cst && (int)threadIdx.x < 3 * FCH && (fm == 2 || h % (H / Hk) == 0);
   int fch = 0;
   float fnv[kFrontK - 1];
   if (fstate) {
-    const int m = threadIdx.x >> 4, kh = h / (H / Hk);
-    fch = (m == 0 ? kh * kD : m == 1 ? fe.Kd + kh * kD : 2 * fe.Kd + h * kD) + 16 * sl + (threadIdx.x & 15);
+    const int kh = h / (H / Hk);
+    fch = (fm == 0 ? kh * kD : fm == 1 ? fe.Kd + kh * kD : 2 * fe.Kd + h * kD) + FCH * sl + ((int)threadIdx.x % FCH);
 #pragma unroll
     for (int j = 0; j < kFrontK - 1; ++j) {
       const int src = T + j;  // index into [old state (3) | inputs (T)]
@@ -1288,7 +1325,7 @@ __global__ __launch_bounds__(256, 1) void gdn_f32_scan_kernel(const char* __rest
     }
   }
 
-  F32Ops o0, o1;
+  F32Ops<CT> o0, o1;
   load(0, o0);
   if (fstate) {
 #pragma unroll
@@ -1304,10 +1341,24 @@ __global__ __launch_bounds__(256, 1) void gdn_f32_scan_kernel(const char* __rest
   }
   if (s_out) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s_out[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col] = S[i][r];
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          s_out[sbase + (size_t)(32 * w + 16 * i + 4 * lg + r) * kD + col[ct]] = S[ct][i][r];
   }
+}
+
+// fp32 scan launch: 8 blocks per (row, head) while they fit one per CU (256 CUs), else 4 of two column tiles each
+static void gdn_f32_scan_launch(const char* ws, const float* s_in, float* s_out, float* o, int T, int NC, int H,
+                                int B, int Hk, const GdnFront& fe, hipStream_t st) {
+  if (8 * H * B <= 256)
+    hipLaunchKernelGGL(gdn_f32_scan_kernel<1>, dim3((unsigned)(8 * H * B)), dim3(256), 0, st, ws, s_in, s_out, o, T,
+                       NC, H, B, Hk, fe);
+  else
+    hipLaunchKernelGGL(gdn_f32_scan_kernel<2>, dim3((unsigned)(4 * H * B)), dim3(256), 0, st, ws, s_in, s_out, o, T,
+                       NC, H, B, Hk, fe);
 }
 
 }  // namespace q35
@@ -1349,8 +1400,8 @@ extern "C" int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v
     hipLaunchKernelGGL(gdn_f32_prep_kernel<false>, dim3((unsigned)NC, (unsigned)H, (unsigned)B), dim3(256), 0, st,
                        (const float*)q, (const float*)k, (const float*)v, g, beta, ws, (int)T, (int)NC, (int)Hk,
                        (int)H, scale, use_qk_l2norm, none);
-    hipLaunchKernelGGL(gdn_f32_scan_kernel, dim3((unsigned)(8 * H * B)), dim3(256), 0, st, ws, initial_state,
-                       final_state, (float*)out, (int)T, (int)NC, (int)H, (int)B, (int)Hk, none);
+    gdn_f32_scan_launch(ws, initial_state, final_state, (float*)out, (int)T, (int)NC, (int)H, (int)B, (int)Hk, none,
+                        st);
   } else {
     const int64_t NP = (T + kP - 1) / kP;
     if (NP > 65535) return Q35_EUNSUPPORTED;
@@ -1392,7 +1443,6 @@ extern "C" int q35_gdn_chunk_prefill_conv(const float* y, int64_t ldy, const flo
   hipLaunchKernelGGL(gdn_f32_prep_kernel<true>, dim3((unsigned)NC, (unsigned)H, (unsigned)B), dim3(256), 0, st,
                      (const float*)nullptr, (const float*)nullptr, (const float*)nullptr, (const float*)nullptr,
                      (const float*)nullptr, ws, (int)T, (int)NC, (int)Hk, (int)H, scale, 1, fe);
-  hipLaunchKernelGGL(gdn_f32_scan_kernel, dim3((unsigned)(8 * H * B)), dim3(256), 0, st, ws, initial_state,
-                     final_state, out, (int)T, (int)NC, (int)H, (int)B, (int)Hk, fe);
+  gdn_f32_scan_launch(ws, initial_state, final_state, out, (int)T, (int)NC, (int)H, (int)B, (int)Hk, fe, st);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
