@@ -490,40 +490,11 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
 
 }  // namespace q35
 
-extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
-                           float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
-                           const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
-  using namespace q35;
-  if (!x || !W || !w_scale || !y || M <= 0 || N <= 0 || K <= 0 || T <= 0) return Q35_EINVAL;
-  if (w_dtype != Q35_I8 && w_dtype != Q35_I8_G128) return Q35_EUNSUPPORTED;
-  const bool gs = w_dtype == Q35_I8_G128;
-  if (gs && K % 128 != 0) return Q35_EUNSUPPORTED;
-  if (epilogue < kGemmStore || epilogue > kGemmSwiglu) return Q35_EINVAL;
-  if (npush < 0 || (npush > 0 && !pushes) || npush > 64) return Q35_EINVAL;
-  if (epilogue == kGemmSwiglu ? (N % 2 != 0 || ldy < N / 2) : ldy < N) return Q35_EINVAL;
-  if (ldx < K) return Q35_EINVAL;
-  if (K % kGK != 0 || ldx % 4 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return Q35_EUNSUPPORTED;
-  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return Q35_EUNSUPPORTED;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // wide products with K <= 2048 (and x, W addressable with 32-bit byte offsets): the DMA kernel
-  if (N >= 2048 && K <= 128 * kDGS && ((M - 1) * ldx + K) * 4 <= 0xffffffffLL && N * K <= 0xffffffffLL) {
-    const int64_t nblocks = ((M + kDBM - 1) / kDBM) * ((N + kDBN - 1) / kDBN);
-    if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
-#define Q35_GEMM_DMA(E, G_)                                                                                       \
-  hipLaunchKernelGGL((gemm_q8_dma_kernel<E, G_>), dim3((unsigned)nblocks), dim3(512), 0, st, x, ldx, W, w_scale, y, \
-                     ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T)
-    if (gs) {
-      if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, true);
-      else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, true);
-      else Q35_GEMM_DMA(kGemmSwiglu, true);
-    } else {
-      if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, false);
-      else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, false);
-      else Q35_GEMM_DMA(kGemmSwiglu, false);
-    }
-#undef Q35_GEMM_DMA
-    return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
-  }
+namespace q35 {
+
+static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
+                          int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes, int64_t npush,
+                          int64_t T, hipStream_t st) {
   const int64_t nbn = (N + kGN - 1) / kGN;
   // 128-row tiles when they still give at least two blocks per compute unit, else 64-row tiles
   const bool big = ((M + 127) / 128) * nbn >= 512;
@@ -545,4 +516,72 @@ extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_d
 #undef Q35_GEMM_EPI
 #undef Q35_GEMM_LAUNCH
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+static int gemm_dma_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
+                           int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes,
+                           int64_t npush, int64_t T, hipStream_t st) {
+  const int64_t nblocks = ((M + kDBM - 1) / kDBM) * ((N + kDBN - 1) / kDBN);
+  if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
+#define Q35_GEMM_DMA(E, G_)                                                                                       \
+  hipLaunchKernelGGL((gemm_q8_dma_kernel<E, G_>), dim3((unsigned)nblocks), dim3(512), 0, st, x, ldx, W, w_scale, y, \
+                     ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T)
+  if (gs) {
+    if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, true);
+    else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, true);
+    else Q35_GEMM_DMA(kGemmSwiglu, true);
+  } else {
+    if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, false);
+    else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, false);
+    else Q35_GEMM_DMA(kGemmSwiglu, false);
+  }
+#undef Q35_GEMM_DMA
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+// compute units of the current device (the DMA kernel runs one block per CU)
+static int64_t gemm_cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+}  // namespace q35
+
+extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
+                           float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
+                           const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
+  using namespace q35;
+  if (!x || !W || !w_scale || !y || M <= 0 || N <= 0 || K <= 0 || T <= 0) return Q35_EINVAL;
+  if (w_dtype != Q35_I8 && w_dtype != Q35_I8_G128) return Q35_EUNSUPPORTED;
+  const bool gs = w_dtype == Q35_I8_G128;
+  if (gs && K % 128 != 0) return Q35_EUNSUPPORTED;
+  if (epilogue < kGemmStore || epilogue > kGemmSwiglu) return Q35_EINVAL;
+  if (npush < 0 || (npush > 0 && !pushes) || npush > 64) return Q35_EINVAL;
+  if (epilogue == kGemmSwiglu ? (N % 2 != 0 || ldy < N / 2) : ldy < N) return Q35_EINVAL;
+  if (ldx < K) return Q35_EINVAL;
+  if (K % kGK != 0 || ldx % 4 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return Q35_EUNSUPPORTED;
+  if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // wide products with K <= 2048 (and x, W addressable with 32-bit byte offsets): the DMA kernel
+  if (N >= 2048 && K <= 128 * kDGS && ((M - 1) * ldx + K) * 4 <= 0xffffffffLL && N * K <= 0xffffffffLL) {
+    // A partial last column tile that costs a whole extra round of blocks (one block per CU; the GDN input
+    // projection: 8192 + 32 columns) runs on the register-staged kernel after the full tiles (store and accumulate
+    // epilogues: their columns are independent).
+    const int64_t mt = (M + kDBM - 1) / kDBM, nfull = N / kDBN * kDBN;
+    if (epilogue != kGemmSwiglu && nfull > 0 && nfull < N) {
+      const int64_t cus = gemm_cu_count();
+      const int64_t rounds_all = (mt * (N / kDBN + 1) + cus - 1) / cus, rounds_full = (mt * (N / kDBN) + cus - 1) / cus;
+      if (rounds_full < rounds_all) {
+        const int r = gemm_dma_launch(x, ldx, W, w_scale, y, ldy, M, nfull, K, epilogue, gs, pushes, npush, T, st);
+        if (r != Q35_OK) return r;
+        return gemm_rs_launch(x, ldx, W + nfull * K, w_scale + (gs ? nfull * (K / 128) : nfull), y + nfull, ldy, M,
+                              N - nfull, K, epilogue, gs, pushes, npush, T, st);
+      }
+    }
+    return gemm_dma_launch(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, st);
+  }
+  return gemm_rs_launch(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, st);
 }

@@ -79,10 +79,12 @@ def _q8g(N, K, seed):
 
 
 @pytest.mark.parametrize("M,N,K", [(9, 8224, 1024), (300, 130, 128), (2048, 5120, 1024), (1500, 1024, 3584),
-                                   (6144, 1024, 2048)])
+                                   (6144, 1024, 2048), (6144, 8224, 1024)])
 def test_gemm_q8_group_scales_store_and_accumulate(M, N, K):
     """Q35_I8_G128 weights (scales of neighbouring groups about a decade apart) against the oracle's per-group
-    product, 64- and 128-row tiles."""
+    product: 64- and 128-row tiles of the register-staged kernel, the DMA-staged kernel, and at M 6144 N 8224 (the
+    stack's GDN input projection) the DMA kernel on the first 8192 columns with the last 32 on the register-staged
+    one."""
     dev = device()
     q, s = _q8g(N, K, M + N)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(K)) * 3.0
