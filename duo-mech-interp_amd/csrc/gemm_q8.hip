@@ -127,7 +127,8 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
                                                              const int8_t* __restrict__ W,
                                                              const float* __restrict__ ws, float* __restrict__ Y,
                                                              int64_t ldy, int M, int N, int K,
-                                                             const q35_push* __restrict__ pushes, int npush, int T) {
+                                                             const q35_push* __restrict__ pushes, int npush, int T,
+                                                             int moff) {
   __shared__ __attribute__((aligned(16))) char smem[kDNS * kDSB];
   __shared__ __attribute__((aligned(16))) char xc[2][2][kDXC];  // [buffer][hi, lo]
   __shared__ float gscale[GS ? kDGS * kDBN : 1];
@@ -138,11 +139,12 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
   constexpr int MT = 2, NT = 2;
   const int wm = wv >> 2, wn = wv & 3;
   const int l32 = lane & 31, lh = lane >> 5;
-  // tile order: block b runs on XCD b % 8; with the tile count a multiple of 8, XCD j takes the consecutive tiles
-  // j * ntiles / 8 .. (n fastest inside an m panel)
+  // tile order: block b runs on XCD b % 8, which gets ceil((ntiles - j) / 8) blocks; XCD j takes that many
+  // consecutive tiles from j q + min(j, r) (ntiles = 8 q + r), n fastest inside an m panel
   const int nbn = (N + kDBN - 1) / kDBN;
   const int ntiles = nbn * ((M + kDBM - 1) / kDBM);
-  const int tile = (ntiles & 7) == 0 ? (int)(blockIdx.x & 7) * (ntiles >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+  const int xj = (int)(blockIdx.x & 7), xq = ntiles >> 3, xr = ntiles & 7;
+  const int tile = xj * xq + min(xj, xr) + (int)(blockIdx.x >> 3);
   const int bm = tile / nbn, bn = tile - bm * nbn;
   const int m0 = bm * kDBM, n0 = bn * kDBN;
   const int G = K >> 7;
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
             const float gate = odd ? o : v, up = odd ? v : o;
             float a = gemm_silu(gate) * up;
             if (pushes_here) {
-              const int row = gemm_push_row(m, T);
+              const int row = gemm_push_row(moff + m, T);
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
             }
             Y[(size_t)m * ldy + neuron] = a;
@@ -344,7 +346,8 @@ template <int BM, int EPI, bool GS>
 __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restrict__ X, int64_t ldx,
                                                          const int8_t* __restrict__ W, const float* __restrict__ ws,
                                                          float* __restrict__ Y, int64_t ldy, int M, int N, int K,
-                                                         const q35_push* __restrict__ pushes, int npush, int T) {
+                                                         const q35_push* __restrict__ pushes, int npush, int T,
+                                                         int moff) {
   static_assert(BM == 64 || BM == 128, "rows per block");
   constexpr int MT = BM / 64;         // 32-row MFMA tiles per wave along M (a wave covers BM / 2 rows)
   constexpr int TPR = 256 / BM;       // threads per staged row of x
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
             const int neuron = n >> 1;
             float a = gemm_silu(v) * up;
             if (pushes_here) {
-              const int row = gemm_push_row(m, T);
+              const int row = gemm_push_row(moff + m, T);
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
             }
             Y[(size_t)m * ldy + neuron] = a;
@@ -494,7 +497,7 @@ namespace q35 {
 
 static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
                           int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes, int64_t npush,
-                          int64_t T, hipStream_t st) {
+                          int64_t T, int64_t moff, hipStream_t st) {
   const int64_t nbn = (N + kGN - 1) / kGN;
   // 128-row tiles when they still give at least two blocks per compute unit, else 64-row tiles
   const bool big = ((M + 127) / 128) * nbn >= 512;
@@ -503,7 +506,7 @@ static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const fl
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
 #define Q35_GEMM_LAUNCH(BMV, E, G)                                                                               \
   hipLaunchKernelGGL((gemm_q8_rs_kernel<BMV, E, G>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W, w_scale, \
-                     y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T)
+                     y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, (int)moff)
 #define Q35_GEMM_EPI(BMV, G)                                              \
   if (epilogue == kGemmStore) Q35_GEMM_LAUNCH(BMV, kGemmStore, G);        \
   else if (epilogue == kGemmAccumulate) Q35_GEMM_LAUNCH(BMV, kGemmAccumulate, G); \
@@ -521,11 +524,12 @@ static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const fl
 static int gemm_dma_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
                            int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes,
                            int64_t npush, int64_t T, hipStream_t st) {
+  const int moff = 0;
   const int64_t nblocks = ((M + kDBM - 1) / kDBM) * ((N + kDBN - 1) / kDBN);
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
 #define Q35_GEMM_DMA(E, G_)                                                                                       \
   hipLaunchKernelGGL((gemm_q8_dma_kernel<E, G_>), dim3((unsigned)nblocks), dim3(512), 0, st, x, ldx, W, w_scale, y, \
-                     ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T)
+                     ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, moff)
   if (gs) {
     if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, true);
     else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, true);
@@ -567,21 +571,37 @@ extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_d
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // wide products with K <= 2048 (and x, W addressable with 32-bit byte offsets): the DMA kernel
   if (N >= 2048 && K <= 128 * kDGS && ((M - 1) * ldx + K) * 4 <= 0xffffffffLL && N * K <= 0xffffffffLL) {
-    // A partial last column tile that costs a whole extra round of blocks (one block per CU; the GDN input
-    // projection: 8192 + 32 columns) runs on the register-staged kernel after the full tiles (store and accumulate
-    // epilogues: their columns are independent).
-    const int64_t mt = (M + kDBM - 1) / kDBM, nfull = N / kDBN * kDBN;
+    // One block per CU, so a last round of blocks that is mostly empty costs as much as a full one. A partial last
+    // column tile that costs a whole extra round (the GDN input projection: 8192 + 32 columns) runs on the
+    // register-staged kernel after the full tiles (store and accumulate epilogues: their columns are independent);
+    // when the last round is less than half full, the rows past the m panels that fill one round fewer run on the
+    // register-staged kernel too (gate/up: 1,344 tiles, 5.25 rounds -> 45 m panels on the DMA kernel, 384 rows).
+    const int64_t cus = gemm_cu_count();
+    const int64_t mt = (M + kDBM - 1) / kDBM;
+    int64_t Nd = N, Md = M;
+    const int64_t nfull = N / kDBN * kDBN;
     if (epilogue != kGemmSwiglu && nfull > 0 && nfull < N) {
-      const int64_t cus = gemm_cu_count();
       const int64_t rounds_all = (mt * (N / kDBN + 1) + cus - 1) / cus, rounds_full = (mt * (N / kDBN) + cus - 1) / cus;
-      if (rounds_full < rounds_all) {
-        const int r = gemm_dma_launch(x, ldx, W, w_scale, y, ldy, M, nfull, K, epilogue, gs, pushes, npush, T, st);
-        if (r != Q35_OK) return r;
-        return gemm_rs_launch(x, ldx, W + nfull * K, w_scale + (gs ? nfull * (K / 128) : nfull), y + nfull, ldy, M,
-                              N - nfull, K, epilogue, gs, pushes, npush, T, st);
+      if (rounds_full < rounds_all) Nd = nfull;
+    }
+    {
+      const int64_t nbd = (Nd + kDBN - 1) / kDBN, tiles = mt * nbd, R = (tiles + cus - 1) / cus;
+      if (R >= 2 && 2 * (tiles - (R - 1) * cus) < cus) {
+        const int64_t M1 = ((R - 1) * cus / nbd) * kDBM;
+        if (M1 > 0 && M1 < M) Md = M1;
       }
     }
-    return gemm_dma_launch(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, st);
+    int r = gemm_dma_launch(x, ldx, W, w_scale, y, ldy, Md, Nd, K, epilogue, gs, pushes, npush, T, st);
+    if (r != Q35_OK) return r;
+    if (Md < M) {
+      r = gemm_rs_launch(x + Md * ldx, ldx, W, w_scale, y + Md * ldy, ldy, M - Md, Nd, K, epilogue, gs, pushes, npush,
+                         T, Md, st);
+      if (r != Q35_OK) return r;
+    }
+    if (Nd < N)
+      r = gemm_rs_launch(x, ldx, W + Nd * K, w_scale + (gs ? Nd * (K / 128) : Nd), y + Nd, ldy, M, N - Nd, K,
+                         epilogue, gs, pushes, npush, T, 0, st);
+    return r;
   }
-  return gemm_rs_launch(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, st);
+  return gemm_rs_launch(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, st);
 }
