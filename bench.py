@@ -216,7 +216,9 @@ GEMM_SHAPES = (("gdn_in_proj", 8224, 1024, "store"), ("mlp_gate_up", 7168, 1024,
 def bench_gemm(torch, q35hip, steps, warmup, dev, M=6144):
     """The int8 prefill GEMM on the stack's projection shapes at M = 3 rows x 2048 tokens (x fp32, W int8 with one
     scale per group of 128 inputs, the stack's format), and torch's fp32 GEMM on the dequantised weights for
-    comparison. TFLOP/s count the nominal 2 M N K (the kernel executes twice that: the hi and lo parts of x)."""
+    comparison. TFLOP/s count the nominal 2 M N K (the kernel executes twice that: the hi and lo parts of x).
+    us_split: the same product on x handed over already split into bf16 hi + lo (the stack's norm writes the inputs
+    of the mixers' input projections and of gate/up that way)."""
     out = {}
     g = torch.Generator(device=dev).manual_seed(0)
     for name, N, K, epi in GEMM_SHAPES:
@@ -229,13 +231,18 @@ def bench_gemm(torch, q35hip, steps, warmup, dev, M=6144):
         def make_call(i):
             return lambda: q35hip.ops.gemm_q8(x, q, sc, out=y, epilogue=epi, pushes=pushes, T=2048)
         r = Timer(torch, make_call, 1, reps=8).run(steps, warmup)
+        xs = q35hip.ops.split_activations(x)
+
+        def make_split(i):
+            return lambda: q35hip.ops.gemm_q8(xs, q, sc, out=y, epilogue=epi, pushes=pushes, T=2048)
+        r3 = Timer(torch, make_split, 1, reps=8).run(steps, warmup)
         wf = (q.float().reshape(N, K // 128, 128) * sc[:, :, None]).reshape(N, K).contiguous()
         r2 = Timer(torch, lambda i: (lambda: torch.mm(x, wf.T)), 1, reps=8).run(steps, warmup)
         fl = 2.0 * M * N * K
         out[name] = {"M": M, "N": N, "K": K, "us": r["step_s"] * 1e6, "tflops": fl / r["step_s"] / 1e12,
                      "frac_bf16_peak": fl / r["step_s"] / 1e12 / PEAK_BF16_TFLOPS,
-                     "torch_fp32_us": r2["step_s"] * 1e6}
-        del x, q, wf, y
+                     "us_split": r3["step_s"] * 1e6, "torch_fp32_us": r2["step_s"] * 1e6}
+        del x, xs, q, wf, y
     return out
 
 

@@ -545,6 +545,9 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const float* __restrict_
 // Residual add + RMSNorm with (1 + w) (HF:720-734 Qwen3_5RMSNorm, applied around every mixer and MLP at HF:753-793;
 // engine/kernels.js:226-246 `rmsnorm` with OFFSET and `addInto`): x[m] += y[m] (when y is given) in place, then
 // h[m] = x[m] * rsqrt(mean(x[m]^2) + eps) * (1 + w), all fp32. One block of 256 threads per row; H a multiple of 4.
+// XS: h in the int8 GEMM's split layout instead (each group of 8 inputs as 8 bf16 hi parts, then 8 bf16 lo parts,
+// hi = bf16(h), lo = bf16(h - hi); H a multiple of 8), the form q35_gemm_q8_split reads without splitting.
+template <bool XS>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float* __restrict__ x, int64_t ldx,
                                                           const float* __restrict__ y, int64_t ldy,
                                                           const float* __restrict__ w, float* __restrict__ h,
@@ -586,23 +589,52 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(float* __restrict__ x,
       f32x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = v[i][e] * r * (1.f + wv[e]);
-      *reinterpret_cast<f32x4*>(hr + c) = o;
+      if constexpr (XS) {  // inputs c .. c + 3: half (c / 4) % 2 of group c / 8 (8 bytes of its hi and of its lo part)
+        bf16x4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bf16_hl t = bf16_split(o[e]);
+          hi[e] = t.hi;
+          lo[e] = t.lo;
+        }
+        float* gp = hr + 8 * (c >> 3) + 2 * ((c >> 2) & 1);
+        *reinterpret_cast<bf16x4*>(gp) = hi;
+        *reinterpret_cast<bf16x4*>(gp + 4) = lo;
+      } else {
+        *reinterpret_cast<f32x4*>(hr + c) = o;
+      }
     }
   }
 }
 
 }  // namespace q35
 
-extern "C" int q35_add_rmsnorm(float* x, int64_t ldx, const float* y, int64_t ldy, const float* w, float* h,
-                               int64_t ldh, int64_t M, int64_t H, float eps, q35_stream_t stream) {
-  using namespace q35;
+namespace q35 {
+
+template <bool XS>
+static int add_rmsnorm_run(float* x, int64_t ldx, const float* y, int64_t ldy, const float* w, float* h, int64_t ldh,
+                           int64_t M, int64_t H, float eps, q35_stream_t stream) {
   if (!x || !w || !h || M <= 0 || H <= 0 || ldx < H || ldh < H || (y && ldy < H)) return Q35_EINVAL;
   if ((H & 3) || H > 8192 || (ldx & 3) || (ldh & 3) || (y && (ldy & 3)) || M > 0x7fffffff) return Q35_EUNSUPPORTED;
+  if (XS && (H & 7)) return Q35_EUNSUPPORTED;
   if (((uintptr_t)x & 15) || ((uintptr_t)h & 15) || ((uintptr_t)w & 15) || (y && ((uintptr_t)y & 15)))
     return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)M), dim3(256), 0, st, x, ldx, y, ldy, w, h, ldh, (int)H, eps);
+  hipLaunchKernelGGL(add_rmsnorm_kernel<XS>, dim3((unsigned)M), dim3(256), 0, st, x, ldx, y, ldy, w, h, ldh, (int)H,
+                     eps);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+}  // namespace q35
+
+extern "C" int q35_add_rmsnorm(float* x, int64_t ldx, const float* y, int64_t ldy, const float* w, float* h,
+                               int64_t ldh, int64_t M, int64_t H, float eps, q35_stream_t stream) {
+  return q35::add_rmsnorm_run<false>(x, ldx, y, ldy, w, h, ldh, M, H, eps, stream);
+}
+
+extern "C" int q35_add_rmsnorm_split(float* x, int64_t ldx, const float* y, int64_t ldy, const float* w, void* hs,
+                                     int64_t ldh, int64_t M, int64_t H, float eps, q35_stream_t stream) {
+  return q35::add_rmsnorm_run<true>(x, ldx, y, ldy, w, static_cast<float*>(hs), ldh, M, H, eps, stream);
 }
 
 extern "C" int q35_gdn_decode_fused(const float* y, int64_t ldy, const float* conv_w, const float* conv_bias,

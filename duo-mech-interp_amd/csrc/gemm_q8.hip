@@ -29,6 +29,11 @@
 //   gemm_q8_rs_kernel (the rest: the N = 1024 output and down projections): 2 x 2 waves over BM x 128 tiles, x and W
 //     staged through registers into LDS (split and widened on the way), the next K step's loads issued before the
 //     current step's MFMAs; two blocks per CU.
+// Split input (XS, q35_gemm_q8_split): x arrives already split by its producer, in the same bytes as fp32 x: each
+// group of 8 consecutive inputs of a row is 32 bytes, the 8 bf16 hi parts then the 8 bf16 lo parts (the split above,
+// rounded the same way). Both kernels then skip the split: the DMA kernel copies the 16-byte hi and lo pieces
+// straight into the planes its A fragments are read from (no fp32 stage, no conversion pass), the register-staged
+// kernel stores the loaded pieces as they are. The products, and so y, are bitwise those of the fp32 input.
 #include <type_traits>
 
 #include "q35_common.h"
@@ -72,10 +77,9 @@ __device__ __forceinline__ float gemm_push(const q35_push* ps, int n, int row, f
 __device__ __forceinline__ void split8(const f32x4& a, const f32x4& b, bf16x8& hi, bf16x8& lo) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float x = e < 4 ? a[e] : b[e - 4];
-    const __bf16 h = (__bf16)x;
-    hi[e] = h;
-    lo[e] = (__bf16)(x - (float)h);
+    const bf16_hl t = bf16_split(e < 4 ? a[e] : b[e - 4]);
+    hi[e] = t.hi;
+    lo[e] = t.lo;
   }
 }
 // 8 int8 values (two 32-bit words) as bf16 (exact)
@@ -122,7 +126,7 @@ constexpr int kDXC = kDBM * kQK * 2;   // one bf16 plane (hi or lo) of a stage's
 // DMA instructions (1 KB) per wave and stage: two of x (rows 8 q .. 8 q + 7, q = w, w + 8) and one of W (rows
 // 32 w .. 32 w + 31)
 
-template <int EPI, bool GS>
+template <int EPI, bool GS, bool XS>
 __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __restrict__ X, int64_t ldx,
                                                              const int8_t* __restrict__ W,
                                                              const float* __restrict__ ws, float* __restrict__ Y,
@@ -130,7 +134,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
                                                              const q35_push* __restrict__ pushes, int npush, int T,
                                                              int moff) {
   __shared__ __attribute__((aligned(16))) char smem[kDNS * kDSB];
-  __shared__ __attribute__((aligned(16))) char xc[2][2][kDXC];  // [buffer][hi, lo]
+  __shared__ __attribute__((aligned(16))) char xc[XS ? 1 : 2][2][XS ? 16 : kDXC];  // [buffer][hi, lo] (fp32 x)
   __shared__ float gscale[GS ? kDGS * kDBN : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -154,11 +158,21 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
   uint32_t xsrc[2], xoff[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int q = wv + 8 * i;
-    const int row = 8 * q + (lane >> 3);
-    const int c = (lane & 7) ^ ((row >> 1) & 1);
-    xsrc[i] = (uint32_t)(((size_t)min(m0 + row, M - 1) * ldx + 4 * c) * 4);
-    xoff[i] = (uint32_t)(q * 1024);
+    if constexpr (XS) {
+      // split x: instruction i fills rows 16 w .. 16 w + 15 of the stage's plane i (hi, lo), laid out as the fp32
+      // path's converted planes; lane -> row 16 w + lane / 4, slot lane % 4 of the row, which holds the group of 8
+      // inputs c = slot ^ ((row >> 2) & 3) (the group's 16 bytes of plane i)
+      const int row = 16 * wv + (lane >> 2);
+      const int c = (lane & 3) ^ ((row >> 2) & 3);
+      xsrc[i] = (uint32_t)(((size_t)min(m0 + row, M - 1) * ldx + 8 * c) * 4 + 16 * i);
+      xoff[i] = (uint32_t)(i * kDXC + wv * 1024);
+    } else {
+      const int q = wv + 8 * i;
+      const int row = 8 * q + (lane >> 3);
+      const int c = (lane & 7) ^ ((row >> 1) & 1);
+      xsrc[i] = (uint32_t)(((size_t)min(m0 + row, M - 1) * ldx + 4 * c) * 4);
+      xoff[i] = (uint32_t)(q * 1024);
+    }
   }
   uint32_t wsrc, woff;
   {
@@ -203,6 +217,23 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
     for (int j = 0; j < 2; ++j) aoff[j] = (uint32_t)(r * 64 + (((2 * lh + j) ^ ((r >> 2) & 3)) << 4));
   }
   const uint32_t boff = (uint32_t)(kDXB + (wn * 64 + l32) * 32 + ((lh ^ ((l32 >> 3) & 1)) << 4));
+  // A fragments of one stage: from the converted planes (fp32 x, read at the start of the stage's iteration) or,
+  // for split x, from the stage's DMA buffer (read at the end of the previous iteration, like W, so that the buffer
+  // is free for the stage issued after the next barrier)
+  bf16x8 ah[2][MT], al[2][MT];
+  auto read_a = [&](const char* xh, const char* xl) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        ah[j][mt] = *reinterpret_cast<const bf16x8*>(xh + aoff[j] + mt * 2048);
+        al[j][mt] = *reinterpret_cast<const bf16x8*>(xl + aoff[j] + mt * 2048);
+      }
+  };
+  auto read_a_stage = [&](int s) {
+    const char* st = smem + (s % kDNS) * kDSB;
+    read_a(st, st + kDXC);
+  };
 
   f32x16 acc[MT][NT], gacc[MT][NT];
 #pragma unroll
@@ -236,7 +267,8 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
   };
   wait_stage(0);
   if (kDNS - 1 < KT) issue(kDNS - 1, kDNS - 1);
-  convert(0, 0);
+  if constexpr (XS) read_a_stage(0);
+  else convert(0, 0);
   read_w(0);
 
   auto stage = [&](int s, auto ph_c) {
@@ -244,17 +276,10 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
     if (s + 1 < KT) wait_stage(s + 1);
     else lds_barrier();
     if (s + kDNS < KT) issue(s + kDNS, s % kDNS);
-    const char* xh = xc[s & 1][0];
-    const char* xl = xc[s & 1][1];
-    bf16x8 ah[2][MT], al[2][MT];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        ah[j][mt] = *reinterpret_cast<const bf16x8*>(xh + aoff[j] + mt * 2048);
-        al[j][mt] = *reinterpret_cast<const bf16x8*>(xl + aoff[j] + mt * 2048);
-      }
-    if (s + 1 < KT) convert(s + 1, (s + 1) & 1);
+    if constexpr (!XS) {
+      read_a(xc[s & 1][0], xc[s & 1][1]);
+      if (s + 1 < KT) convert(s + 1, (s + 1) & 1);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -276,7 +301,10 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
           d = mfma32(al[j][mt], b[nt], d);
         }
     }
-    if (s + 1 < KT) read_w(s + 1);
+    if (s + 1 < KT) {
+      read_w(s + 1);
+      if constexpr (XS) read_a_stage(s + 1);
+    }
     if constexpr (GS && ph == 3) {  // end of a group of 128 inputs: fold it in with its scale
       const int g = s >> 2;
 #pragma unroll
@@ -342,7 +370,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
 // stages x[BM, 64] (split into hi and lo) and W[128, 64] (int8 -> bf16) in LDS, rows of 64 bf16 = 8 segments of 16
 // bytes, segment s of row r at s ^ (r & 7). The next step's global loads are issued before the current step's MFMAs,
 // so they are in flight during them. Blocks run n-fastest inside an m panel.
-template <int BM, int EPI, bool GS>
+template <int BM, int EPI, bool GS, bool XS>
 __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restrict__ X, int64_t ldx,
                                                          const int8_t* __restrict__ W, const float* __restrict__ ws,
                                                          float* __restrict__ Y, int64_t ldy, int M, int N, int K,
@@ -385,7 +413,12 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       bf16x8 hi, lo;
-      split8(xa[s][0], xa[s][1], hi, lo);
+      if constexpr (XS) {  // split x: the group's 16 bytes of hi parts, then its 16 bytes of lo parts
+        hi = __builtin_bit_cast(bf16x8, xa[s][0]);
+        lo = __builtin_bit_cast(bf16x8, xa[s][1]);
+      } else {
+        split8(xa[s][0], xa[s][1], hi, lo);
+      }
       const int idx = ar * 8 + gsw(ar, as0 + s);
       Ah[idx] = av ? hi : z;
       Al[idx] = av ? lo : z;
@@ -495,6 +528,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
 
 namespace q35 {
 
+template <bool XS>
 static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
                           int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes, int64_t npush,
                           int64_t T, int64_t moff, hipStream_t st) {
@@ -504,9 +538,9 @@ static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const fl
   const int BM = big ? 128 : 64;
   const int64_t nblocks = ((M + BM - 1) / BM) * nbn;
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
-#define Q35_GEMM_LAUNCH(BMV, E, G)                                                                               \
-  hipLaunchKernelGGL((gemm_q8_rs_kernel<BMV, E, G>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W, w_scale, \
-                     y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, (int)moff)
+#define Q35_GEMM_LAUNCH(BMV, E, G)                                                                                   \
+  hipLaunchKernelGGL((gemm_q8_rs_kernel<BMV, E, G, XS>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W,       \
+                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, (int)moff)
 #define Q35_GEMM_EPI(BMV, G)                                              \
   if (epilogue == kGemmStore) Q35_GEMM_LAUNCH(BMV, kGemmStore, G);        \
   else if (epilogue == kGemmAccumulate) Q35_GEMM_LAUNCH(BMV, kGemmAccumulate, G); \
@@ -521,6 +555,7 @@ static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const fl
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 
+template <bool XS>
 static int gemm_dma_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
                            int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes,
                            int64_t npush, int64_t T, hipStream_t st) {
@@ -528,8 +563,8 @@ static int gemm_dma_launch(const float* x, int64_t ldx, const int8_t* W, const f
   const int64_t nblocks = ((M + kDBM - 1) / kDBM) * ((N + kDBN - 1) / kDBN);
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
 #define Q35_GEMM_DMA(E, G_)                                                                                       \
-  hipLaunchKernelGGL((gemm_q8_dma_kernel<E, G_>), dim3((unsigned)nblocks), dim3(512), 0, st, x, ldx, W, w_scale, y, \
-                     ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, moff)
+  hipLaunchKernelGGL((gemm_q8_dma_kernel<E, G_, XS>), dim3((unsigned)nblocks), dim3(512), 0, st, x, ldx, W,        \
+                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, moff)
   if (gs) {
     if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, true);
     else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, true);
@@ -554,10 +589,13 @@ static int64_t gemm_cu_count() {
 
 }  // namespace q35
 
-extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
-                           float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
-                           const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
-  using namespace q35;
+namespace q35 {
+
+// x: fp32 rows, or for XS rows in the split layout (the same bytes and leading dimension as fp32 rows)
+template <bool XS>
+static int gemm_q8_run(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
+                       int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
+                       int64_t npush, int64_t T, q35_stream_t stream) {
   if (!x || !W || !w_scale || !y || M <= 0 || N <= 0 || K <= 0 || T <= 0) return Q35_EINVAL;
   if (w_dtype != Q35_I8 && w_dtype != Q35_I8_G128) return Q35_EUNSUPPORTED;
   const bool gs = w_dtype == Q35_I8_G128;
@@ -591,17 +629,32 @@ extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_d
         if (M1 > 0 && M1 < M) Md = M1;
       }
     }
-    int r = gemm_dma_launch(x, ldx, W, w_scale, y, ldy, Md, Nd, K, epilogue, gs, pushes, npush, T, st);
+    int r = gemm_dma_launch<XS>(x, ldx, W, w_scale, y, ldy, Md, Nd, K, epilogue, gs, pushes, npush, T, st);
     if (r != Q35_OK) return r;
     if (Md < M) {
-      r = gemm_rs_launch(x + Md * ldx, ldx, W, w_scale, y + Md * ldy, ldy, M - Md, Nd, K, epilogue, gs, pushes, npush,
+      r = gemm_rs_launch<XS>(x + Md * ldx, ldx, W, w_scale, y + Md * ldy, ldy, M - Md, Nd, K, epilogue, gs, pushes, npush,
                          T, Md, st);
       if (r != Q35_OK) return r;
     }
     if (Nd < N)
-      r = gemm_rs_launch(x, ldx, W + Nd * K, w_scale + (gs ? Nd * (K / 128) : Nd), y + Nd, ldy, M, N - Nd, K,
+      r = gemm_rs_launch<XS>(x, ldx, W + Nd * K, w_scale + (gs ? Nd * (K / 128) : Nd), y + Nd, ldy, M, N - Nd, K,
                          epilogue, gs, pushes, npush, T, 0, st);
     return r;
   }
-  return gemm_rs_launch(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, st);
+  return gemm_rs_launch<XS>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, st);
+}
+
+}  // namespace q35
+
+extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
+                           float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
+                           const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
+  return q35::gemm_q8_run<false>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T, stream);
+}
+
+extern "C" int q35_gemm_q8_split(const void* xs, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
+                                 float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
+                                 const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
+  return q35::gemm_q8_run<true>(static_cast<const float*>(xs), ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue,
+                                pushes, npush, T, stream);
 }

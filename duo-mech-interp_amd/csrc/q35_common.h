@@ -96,6 +96,17 @@ __device__ __forceinline__ bf16x8 pack8(const f32x4& lo, const f32x4& hi) {
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+// x = hi + lo up to 2^-17 |x|: hi = bf16(x), lo = bf16(x - hi), both rounded to nearest even (the split of fp32
+// activations for the int8 GEMM's bf16 products). The subtraction is never contracted into the product that made x
+// (an FMA would form lo from the unrounded product): every producer of split values rounds the same way.
+struct bf16_hl {
+  __bf16 hi, lo;
+};
+__device__ __forceinline__ bf16_hl bf16_split(float x) {
+#pragma clang fp contract(off)
+  const __bf16 h = (__bf16)x;
+  return {h, (__bf16)(x - (float)h)};
+}
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }  // threshold 20
 

@@ -61,7 +61,9 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     scale applied after the gated norm (engine/kernels_qwen35.js:243). num_k_heads / head_k_dim default to the
     value heads / value head dim (the Qwen3.5 text models use Hk = Hv and dk = dv). prenorm: see linear() (x is then
     the residual and the layer's input norm runs inside the input projection). Returns y [B, T, H], or with
-    residual [B, T, H] given, residual + y computed in place by the output projection (then returned)."""
+    residual [B, T, H] given, residual + y computed in place by the output projection (then returned). For T > 1,
+    x may be the int32 words of the normed rows already split for the int8 GEMM (add_rmsnorm_(..., split=True);
+    the layer must then have int8 input projections)."""
     if prefill not in ("chunk", "recurrent"):
         raise ValueError(f"gated_deltanet_layer: prefill must be 'chunk' or 'recurrent', not {prefill!r}")
     B, T, _ = x.shape
@@ -96,7 +98,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
                                   rec_state, p["norm"], b_off=C + Vd, a_off=C + Vd + Hv, z_off=C,
                                   head_scale=head_scale, eps=eps)
         return linear(o.view(B, 1, Vd), p["out_proj"], *_q8(p, "out_proj"), residual=residual)
-    if (T > 1 and prefill == "chunk" and x.dtype == torch.float32 and dk == dv == 128
+    if (T > 1 and prefill == "chunk" and _act_dtype(x) == torch.float32 and dk == dv == 128
             and p["conv1d"].shape[-1] == 4 and rec_state.is_contiguous()):
         # the conv + SiLU, l2 norms and gate terms in the chunk kernel's load phase (q, k, v, g, beta never written
         # out), the recurrent state advanced in place: the arithmetic of gdn_conv + chunk_gated_delta_rule below
@@ -105,7 +107,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     else:
         q, k, v, g, beta = ops.gdn_conv(y, p["conv1d"], conv_state, p["A_log"], p["dt_bias"], num_k_heads=Hk,
                                         head_k_dim=dk, num_v_heads=Hv, head_v_dim=dv, b_off=C + Vd,
-                                        a_off=C + Vd + Hv, out_dtype=x.dtype)
+                                        a_off=C + Vd + Hv, out_dtype=_act_dtype(x))
         if T == 1 or prefill == "recurrent":
             o = ops.gdn_decode_step_(q, k, v, g, beta, rec_state, use_qk_l2norm_in_kernel=True)
         else:
@@ -115,6 +117,11 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     # gated RMSNorm: plain w, norm before the silu(z) gate (HF:168-184; engine/kernels_qwen35.js:237-243)
     o = ops.gated_rmsnorm(o, y[..., C:C + Vd], p["norm"], head_scale, eps)
     return linear(o, p["out_proj"], *_q8(p, "out_proj"), residual=residual)
+
+
+def _act_dtype(x):
+    """The value dtype of a layer input: fp32 for the int32 words of split activations."""
+    return torch.float32 if x.dtype == torch.int32 else x.dtype
 
 
 def prenorm_torch(x, prenorm):
@@ -135,7 +142,8 @@ def linear(x, w, wq=None, ws=None, prenorm=None, residual=None, conv=None):
     to x_out when given (the decoder layer's add + norm, fused into the GEMV). residual [..., N]: the product is added
     into it in place (the decoder layer's residual add after its mixer) and residual is returned. conv =
     (conv_w, conv_bias, conv_state): the GEMV with prenorm runs the GDN causal conv + SiLU on the first
-    conv_w.shape[0] outputs and advances conv_state (decode only: raises when the product is not a GEMV)."""
+    conv_w.shape[0] outputs and advances conv_state (decode only: raises when the product is not a GEMV). x may be the
+    int32 words of split activations (ops.split_activations) when wq is given: the int8 GEMM reads them as they are."""
     K = x.shape[-1]
     M = x.numel() // K
     N = (wq if wq is not None else w).shape[0]
@@ -154,9 +162,11 @@ def linear(x, w, wq=None, ws=None, prenorm=None, residual=None, conv=None):
         raise ValueError("linear: the conv epilogue is a decode GEMV form (at most 8 fp32 rows, K a multiple of 256)")
     if prenorm is not None:
         x = prenorm_torch(x, prenorm)
-    if wq is not None and K % 64 == 0 and x.dtype == torch.float32:
+    if wq is not None and K % 64 == 0 and x.dtype in (torch.float32, torch.int32):
         y = ops.gemm_q8(x.reshape(M, K), wq, ws, out=out, epilogue=epi)
         return residual if residual is not None else y.view(*x.shape[:-1], N)
+    if x.dtype == torch.int32:
+        raise ValueError("linear: split activations need the int8 GEMM (int8 weights, K a multiple of 64)")
     if residual is not None:
         residual.view(M, N).addmm_(x.reshape(M, K), w.T)
         return residual
@@ -200,8 +210,9 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     cache positions 0..pos+t (engine/kernels_qwen35.js:90). T > 1 at the int position 0 runs the flash prefill over
     the call's own tokens; T > 1 at any other position (or a device pos) the same kernel over the cache (the caches'
     max_len must then be a multiple of 64); T == 1 the split-K decode over cache positions 0..pos (cache_len:
-    optional [B] int32 per-row lengths, default pos + 1). prenorm: see linear(). Returns y [B, T, H], or with
-    residual [B, T, H] given, residual + y computed in place by o_proj (then returned)."""
+    optional [B] int32 per-row lengths, default pos + 1). prenorm: see linear(). For T > 1, x may be the int32 words
+    of split activations (see gated_deltanet_layer). Returns y [B, T, H], or with residual [B, T, H] given,
+    residual + y computed in place by o_proj (then returned)."""
     B, T, _ = x.shape
     D = p["q_norm"].numel()
     Hq = p["q_proj"].shape[0] // (2 * D)

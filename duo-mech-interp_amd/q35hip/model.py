@@ -52,6 +52,17 @@ def mlp_weights(p):
     return p
 
 
+_GDN_IN = ("in_proj_qkv", "in_proj_z", "in_proj_b", "in_proj_a")
+_ATTN_IN = ("q_proj", "k_proj", "v_proj")
+_MLP_IN = ("gate_proj", "up_proj")
+
+
+def _split_ok(p, names, x):
+    """Whether the products that read a norm's output all run on the int8 GEMM (int8 weights, 64 | H), which then
+    takes the rows already split."""
+    return x.shape[-1] % 64 == 0 and all(n + ".q" in p for n in names)
+
+
 def mlp(p, h, x, prenorm=None):
     """x += SwiGLU MLP (HF:704-717) of h, in place, with the layer's neuron pushes at the down_proj input
     (engine/model.js:7-9, engine/kernels_qwen35.js:250-279). Decode (at most 8 rows, int8 weights present): one GEMV
@@ -60,14 +71,16 @@ def mlp(p, h, x, prenorm=None):
     int8 GEMM accumulating down_proj into x; without int8 weights a [gate | up] torch GEMM on the fp32 weights, the
     SwiGLU push kernel and a down_proj GEMM. prenorm = (y_add, norm_w, eps): h is then the residual; x receives
     h + y_add and the MLP reads the RMSNorm (1 + norm_w) of that sum (the layer's second add + norm, fused into the
-    first GEMV on the decode path). Returns x."""
+    first GEMV on the decode path). h may be the int32 words of split activations (add_rmsnorm_(..., split=True)) when
+    the layer has int8 weights: the gate/up GEMM reads them as they are. Returns x."""
     mlp_weights(p)
     H = h.shape[-1]
     M = h.numel() // H
     T = h.shape[1] if h.dim() == 3 else 1
     # h + y_add is written to x when x is another buffer; with x = h and no y_add the norm reads h as it is
     pn = None if prenorm is None else (prenorm[0], prenorm[1], prenorm[2], None if x is h else x)
-    if M <= 8 and "_gu_q8" in p and H % 256 == 0 and p["down_proj.q"].shape[1] % 256 == 0:
+    if M <= 8 and "_gu_q8" in p and H % 256 == 0 and p["down_proj.q"].shape[1] % 256 == 0 and \
+            h.dtype == torch.float32:
         pn2 = None if pn is None else (None if pn[0] is None else pn[0].reshape(M, H), pn[1], pn[2],
                                        None if pn[3] is None else x.view(M, H))
         a = ops.gemv(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T,
@@ -81,6 +94,8 @@ def mlp(p, h, x, prenorm=None):
         a = ops.gemm_q8(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T)
         ops.gemm_q8(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H), epilogue="add")
         return x
+    if h.dtype == torch.int32:
+        raise ValueError("mlp: split activations need the int8 GEMM (int8 weights, H a multiple of 64)")
     a = ops.swiglu_push(h @ p["_gu"].T, p["_pushes"], T=T)
     x.view(M, H).addmm_(a.view(M, -1), p["down_proj"].T)
     return x
@@ -224,14 +239,16 @@ class HybridModel:
         for l in range(last + 1):
             p = self.params[l]
             st = {n: t[rs] for n, t in self.states[l].items()}
-            h = ops.add_rmsnorm_(x, y, p["input_layernorm"], cfg.eps)
+            # the norms hand the int8 GEMMs their rows already split (bf16 hi + lo) when the layer's products are int8
+            mixer = _ATTN_IN if cfg.is_attention(l) else _GDN_IN
+            h = ops.add_rmsnorm_(x, y, p["input_layernorm"], cfg.eps, split=_split_ok(p, mixer, x))
             if cfg.is_attention(l):
                 y = layers.gated_attention_layer(h, p, st["k"], st["v"], attn_pos, rope_theta=cfg.rope_theta,
                                                  partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps)
             else:
                 y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
                                                 head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill)
-            h = ops.add_rmsnorm_(x, y, p["post_attention_layernorm"], cfg.eps)
+            h = ops.add_rmsnorm_(x, y, p["post_attention_layernorm"], cfg.eps, split=_split_ok(p, _MLP_IN, x))
             y = None
             mlp(p, h, x)
             if l == self.steer_layer and steer:

@@ -76,6 +76,7 @@ _LIB.define("gemv_(Tensor x, Tensor W, Tensor? w_scale, Tensor(a!) y, int epilog
 _LIB.define("swiglu_push(Tensor gu, Tensor? pushes, int T) -> Tensor")
 _LIB.define("gemm_q8_(Tensor x, Tensor W, Tensor w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
 _LIB.define("add_rmsnorm_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tensor")
+_LIB.define("add_rmsnorm_split_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tensor")
 _LIB.define("argmax_rows_(Tensor x, Tensor(a!) idx) -> ()")
 _LIB.define("gemv_norm_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
             "Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
@@ -437,8 +438,8 @@ def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T):
 
 def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T):
     _on_gpu(W, w_scale, pushes)
-    _require(x.is_cuda and x.dtype == torch.float32 and x.dim() == 2 and x.stride(1) == 1,
-             "x: [M, K] fp32 with unit column stride")
+    _require(x.is_cuda and x.dtype in (torch.float32, torch.int32) and x.dim() == 2 and x.stride(1) == 1,
+             "x: [M, K] fp32 (or int32 words of split activations) with unit column stride")
     _require(y.is_cuda and y.dtype == torch.float32 and y.dim() == 2 and y.stride(1) == 1, "y: [M, N] fp32")
     _require(W.dim() == 2 and W.dtype == torch.int8, "W: [N, K] int8")
     M, K = x.shape
@@ -448,9 +449,10 @@ def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T):
     fmt = _weight_format(W, w_scale, N, K)
     _require(K % 64 == 0, "K must be a multiple of 64")
     npush = _pushes_check(pushes)
-    st = _lib.lib().q35_gemm_q8(_ptr(x), x.stride(0), _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.stride(0), M, N, K,
-                                int(epilogue), _ptr(pushes), npush, int(T), _stream(x))
-    check(st, "q35_gemm_q8")
+    fn = "q35_gemm_q8_split" if x.dtype == torch.int32 else "q35_gemm_q8"
+    st = getattr(_lib.lib(), fn)(_ptr(x), x.stride(0), _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.stride(0), M, N, K,
+                                 int(epilogue), _ptr(pushes), npush, int(T), _stream(x))
+    check(st, fn)
 
 
 def _gemv_norm_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, epilogue, pushes, T):
@@ -529,17 +531,22 @@ def _swiglu_push_impl(gu, pushes, T):
     return a
 
 
-def _add_rmsnorm_impl(x, y, w, eps):
+def _add_rmsnorm_impl(x, y, w, eps, split=False):
     _on_gpu(x, y, w)
     _require(x.dtype == torch.float32 and w.dtype == torch.float32, "x, w fp32")
     H = x.shape[-1]
     _require(w.numel() == H and (y is None or (y.shape == x.shape and y.dtype == torch.float32)),
              "w: [H]; y like x")
     M = x.numel() // H
-    h = torch.empty_like(x)
-    st = _lib.lib().q35_add_rmsnorm(_ptr(x), H, _ptr(y), H, _ptr(w), _ptr(h), H, M, H, float(eps), _stream(x))
-    check(st, "q35_add_rmsnorm")
+    h = torch.empty_like(x, dtype=torch.int32 if split else torch.float32)
+    fn = "q35_add_rmsnorm_split" if split else "q35_add_rmsnorm"
+    st = getattr(_lib.lib(), fn)(_ptr(x), H, _ptr(y), H, _ptr(w), _ptr(h), H, M, H, float(eps), _stream(x))
+    check(st, fn)
     return h
+
+
+def _add_rmsnorm_split_impl(x, y, w, eps):
+    return _add_rmsnorm_impl(x, y, w, eps, split=True)
 
 
 def _argmax_rows_impl(x, idx):
@@ -564,7 +571,8 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gdn_decode_fused_", _gdn_decode_fused_impl),
                      ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
                      ("gemm_q8_", _gemm_q8_impl),
-                     ("add_rmsnorm_", _add_rmsnorm_impl), ("argmax_rows_", _argmax_rows_impl),
+                     ("add_rmsnorm_", _add_rmsnorm_impl), ("add_rmsnorm_split_", _add_rmsnorm_split_impl),
+                     ("argmax_rows_", _argmax_rows_impl),
                      ("gemv_norm_", _gemv_norm_impl), ("gdn_decode_sliced_", _gdn_decode_sliced_impl),
                      ("gdn_chunk_prefill_conv_", _gdn_chunk_prefill_conv_impl),
                      ("gemv_norm_conv_", _gemv_norm_conv_impl), ("gemv_gated_norm_", _gemv_gated_norm_impl)]:
@@ -607,6 +615,7 @@ _LIB.impl("gemv_", lambda x, W, ws, y, e, pushes, T: None, "Meta")
 _LIB.impl("gemm_q8_", lambda x, W, ws, y, e, pushes, T: None, "Meta")
 _LIB.impl("swiglu_push", lambda gu, pushes, T: gu.new_empty(*gu.shape[:-1], gu.shape[-1] // 2), "Meta")
 _LIB.impl("add_rmsnorm_", lambda x, y, w, eps: torch.empty_like(x), "Meta")
+_LIB.impl("add_rmsnorm_split_", lambda x, y, w, eps: torch.empty_like(x, dtype=torch.int32), "Meta")
 _LIB.impl("gated_rmsnorm", lambda o, z, w, hs, eps: o.new_empty(*o.shape[:-2], o.shape[-2] * o.shape[-1]), "Meta")
 
 
@@ -823,7 +832,9 @@ def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1):
     int8 with scales w_scale [N, K / 128] (per group of 128 inputs) or [N] (per row), K a multiple of 64 (128 with
     group scales); fp32-accurate (bf16 MFMA on a hi + lo split of x). epilogue "store" writes out, "add"
     accumulates into out, "swiglu" treats W's rows as interleaved (gate, up) pairs and writes
-    silu(gate) * up with the neuron pushes (pack_pushes) applied, out [M, N / 2]. Returns out."""
+    silu(gate) * up with the neuron pushes (pack_pushes) applied, out [M, N / 2]. x may also be the int32 words of
+    activations already split (add_rmsnorm_(..., split=True), split_activations): the same product, bitwise, without
+    the split in the kernel. Returns out."""
     e = _EPI[epilogue]
     x = x if x.stride(-1) == 1 else x.contiguous()
     if out is None:
@@ -849,7 +860,24 @@ def argmax_rows(x, out=None):
     return out
 
 
-def add_rmsnorm_(x, y, w, eps=1e-6):
+def add_rmsnorm_(x, y, w, eps=1e-6, split=False):
     """x += y in place (y None: no add), then return x * rsqrt(mean x^2 + eps) * (1 + w) (Qwen3_5RMSNorm, HF:720-734),
-    fp32, x and y dense [..., H]."""
+    fp32, x and y dense [..., H]. split=True returns the normed rows as int32 words in the int8 GEMM's split layout
+    (split_activations of the fp32 result, H a multiple of 8), which gemm_q8 reads without splitting them again."""
+    if split:
+        return torch.ops.q35.add_rmsnorm_split_(x, y, w.float().contiguous(), float(eps))
     return torch.ops.q35.add_rmsnorm_(x, y, w.float().contiguous(), float(eps))
+
+
+def split_activations(x):
+    """fp32 rows [..., K] (K a multiple of 8) in the int8 GEMM's split layout, as int32 words of the same shape: each
+    value as hi = bf16(x) and lo = bf16(x - hi) (round to nearest even), each group of 8 inputs as its 8 hi parts
+    followed by its 8 lo parts. Torch ops on any device (the layout's definition; the product path produces it in
+    add_rmsnorm_(..., split=True))."""
+    if x.dtype != torch.float32 or x.shape[-1] % 8:
+        raise ValueError("split_activations: fp32 rows with a multiple of 8 inputs")
+    hi = x.to(torch.bfloat16)
+    lo = (x - hi.float()).to(torch.bfloat16)
+    g = x.shape[:-1] + (x.shape[-1] // 8, 8)
+    return torch.cat([hi.reshape(g), lo.reshape(g)], dim=-1).reshape(x.shape[:-1] + (2 * x.shape[-1],)).contiguous() \
+        .view(torch.int32)

@@ -38,6 +38,8 @@
  *                            with the SwiGLU + push epilogue of `swiglu` (engine/kernels_qwen35.js:250-279)
  *   q35_add_rmsnorm          HF:720-734 Qwen3_5RMSNorm (1 + w) with the residual add before it (HF:753-793);
  *                            engine/kernels.js:226-246 `rmsnorm` (OFFSET) and `addInto`
+ *   q35_gemm_q8_split,       the same two on activations handed over already split into bf16 hi + lo parts (no
+ *   q35_add_rmsnorm_split    counterpart in the reference's interface: a layout between the norm and the GEMM)
  *   q35_argmax_rows          engine/kernels.js:260-283 `argmax` (greedy token of each row, engine/model.js:494-497)
  */
 #ifndef Q35HIP_H
@@ -300,6 +302,15 @@ int q35_add_rmsnorm(float* x, int64_t ldx, const float* y, int64_t ldy, const fl
                     int64_t M, int64_t H, float eps, q35_stream_t stream);
 
 /*
+ * q35_add_rmsnorm with h written in the split layout that q35_gemm_q8_split reads (the same norm, then each value
+ * as hi = bf16(h), lo = bf16(h - hi), rounded to nearest even; per row, each group of 8 inputs is 32 bytes: the 8
+ * hi parts, then the 8 lo parts). hs: [M, ldh] 4-byte words (the bytes of an fp32 [M, ldh] array), H a multiple
+ * of 8; everything else as q35_add_rmsnorm. Same reference lines (the norm before the prefill projections).
+ */
+int q35_add_rmsnorm_split(float* x, int64_t ldx, const float* y, int64_t ldy, const float* w, void* hs, int64_t ldh,
+                          int64_t M, int64_t H, float eps, q35_stream_t stream);
+
+/*
  * Small-M matrix-vector product for the decode step: y[m, n] = sum_k x[m, k] W[n, k] s(n, k), m < M <= 8, with
  * s(n, k) = w_scale[n] for Q35_I8, w_scale[n, k / 128] for Q35_I8_G128, 1 for Q35_F32 (w_scale NULL).
  *   x: [M, ldx] fp32 (16-byte aligned, ldx a multiple of 4); W: [N, K] row-major int8 or fp32 (w_dtype);
@@ -367,6 +378,16 @@ int q35_gemv_gated_norm(const float* o, int64_t ldo, const float* z, int64_t ldz
 int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush,
                 int64_t T, q35_stream_t stream);
+
+/*
+ * q35_gemm_q8 on x already split by its producer (q35_add_rmsnorm_split): xs [M, ldx] 4-byte words in the split
+ * layout (per row, each group of 8 inputs as 8 bf16 hi parts then 8 bf16 lo parts; ldx counted in inputs, a multiple
+ * of 4). The product skips the split and is bitwise that of q35_gemm_q8 on the fp32 values hi + lo was made from.
+ * Same reference lines as q35_gemm_q8.
+ */
+int q35_gemm_q8_split(const void* xs, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
+                      int64_t npush, int64_t T, q35_stream_t stream);
 
 /*
  * a[m, n] = silu(gu[m, n]) * gu[m, I + n] with the pushes applied, gu: [M, 2 I] fp32 ([gate | up] per row),

@@ -39,7 +39,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 9
+    assert L.q35_abi_version() == 10
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -125,6 +125,10 @@ def test_validation_rejects_without_launching():
     assert L.q35_swiglu_push(fake, fake, 3, 64, None, 2, 1, None) == 1
     assert L.q35_add_rmsnorm(fake, 1024, None, 0, fake, fake, 1024, 3, 1022, 1e-6, None) == 2
     assert L.q35_add_rmsnorm(fake, 512, None, 0, fake, fake, 1024, 3, 1024, 1e-6, None) == 1
+    # split forms: the norm's split output needs H a multiple of 8; the split GEMM validates as q35_gemm_q8
+    assert L.q35_add_rmsnorm_split(fake, 1028, None, 0, fake, fake, 1028, 3, 1028, 1e-6, None) == 2
+    assert L.q35_gemm_q8_split(fake, 192, fake, 3, fake, fake, 64, 100, 64, 192, 0, None, 0, 1, None) == 2
+    assert L.q35_gemm_q8_split(None, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 0, None, 0, 1, None) == 1
     # argmax: ld shorter than the row, no rows
     assert L.q35_argmax_rows(fake, 100, 3, 101, fake, None, None) == 1
     assert L.q35_argmax_rows(fake, 100, 0, 100, fake, None, None) == 1
@@ -169,3 +173,29 @@ def test_fused_gdn_step_and_fp32_decode_refuse_cpu_tensors():
         q35hip.ops.gated_attention_decode(q, kc, kc, torch.zeros(1, 2048, dtype=torch.bfloat16),
                                           torch.ones(1, dtype=torch.int32), torch.zeros(64, 32), torch.zeros(64, 32),
                                           out_dtype=torch.float32)
+
+
+def test_split_activation_layout():
+    """The int8 GEMM's split layout (ops.split_activations, which the norm's split output and the split GEMM follow):
+    per row, each group of 8 inputs is 32 bytes, the 8 bf16 hi parts then the 8 bf16 lo parts; hi is x rounded to
+    bf16 (nearest even), hi + lo recovers x to 2^-16 relative (lo is the rounded remainder), exactly when x has at
+    most 16 significant bits."""
+    from q35hip import ops
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 40, generator=g) * torch.logspace(-3, 3, 40)
+    w = ops.split_activations(x)
+    assert w.dtype == torch.int32 and w.shape == x.shape
+    parts = w.view(torch.bfloat16).view(3, 5, 16)
+    hi, lo = parts[..., :8].reshape(3, 40), parts[..., 8:].reshape(3, 40)
+    assert torch.equal(hi, x.to(torch.bfloat16))
+    assert torch.equal(lo, (x - hi.float()).to(torch.bfloat16))
+    assert bool(((hi.float() + lo.float() - x).abs() <= x.abs() * 2.0 ** -16).all())
+    exact = torch.tensor([[1.0, -3.0, 0.5, 1 + 2.0 ** -10, 0.0, 1024.0, -2.0 ** -20, 3 * 2.0 ** -9]])
+    e = ops.split_activations(exact).view(torch.bfloat16).view(1, 1, 16)
+    assert torch.equal(e[..., :8].float() + e[..., 8:].float(), exact.view(1, 1, 8))
+    # a planted layout mistake (hi and lo interleaved per value) reads back as different words
+    wrong = torch.stack([x.to(torch.bfloat16), (x - hi.float()).to(torch.bfloat16)], -1).reshape(3, 80)
+    assert not torch.equal(wrong.view(torch.int32), w)
+    with pytest.raises(ValueError):
+        ops.split_activations(torch.zeros(2, 12))
+

@@ -170,6 +170,25 @@ def test_add_rmsnorm_matches_oracle(with_add):
     assert oracle.rel_err(xd.cpu(), xs) <= TOL_F32
 
 
+@pytest.mark.parametrize("with_add,H", [(False, 1024), (True, 1024), (True, 1000)])
+def test_add_rmsnorm_split_output(with_add, H):
+    """The norm with its output in the int8 GEMM's split layout: the words equal ops.split_activations of the fp32
+    output (the same norm, then hi = bf16(h), lo = bf16(h - hi)), and x is updated as by the fp32 form."""
+    dev = device()
+    g = torch.Generator().manual_seed(71)
+    x = torch.randn(3, 7, H, generator=g).to(dev)
+    y = torch.randn(3, 7, H, generator=g).to(dev) if with_add else None
+    w = (0.1 * torch.randn(H, generator=g)).to(dev)
+    announce(f"add_rmsnorm split add={with_add} H{H}")
+    xa, xb = x.clone(), x.clone()
+    h = ops.add_rmsnorm_(xa, y, w)
+    hs = ops.add_rmsnorm_(xb, y, w, split=True)
+    torch.cuda.synchronize()
+    assert hs.dtype == torch.int32 and hs.shape == h.shape
+    assert torch.equal(hs, ops.split_activations(h))
+    assert torch.equal(xa, xb)
+
+
 @pytest.mark.parametrize("with_bias,with_scale", [(False, False), (True, True)])
 def test_gdn_decode_fused_equals_the_three_kernels(with_bias, with_scale):
     """Five decode steps through q35_gdn_decode_fused (conv + recurrent rule + gated norm in one launch) against the

@@ -136,3 +136,34 @@ def test_gemm_q8_swiglu_placeholder_push_records():
     assert oracle.rel_err(a.cpu(), ref) <= TOL
     cols = [127, 128, 3000]  # the pushed neurons alone, at the GEMM's own error (an unapplied push would be O(1) off)
     assert oracle.rel_err(a.cpu()[:, cols], ref[:, cols]) <= TOL
+
+
+@pytest.mark.parametrize("M,N,K,gs,epi", [(9, 8224, 1024, True, "store"), (300, 130, 128, False, "add"),
+                                          (2048, 5120, 1024, True, "store"), (1500, 1024, 3584, True, "add"),
+                                          (6144, 8224, 1024, True, "store"), (6144, 7168, 1024, True, "swiglu"),
+                                          (2100, 4096, 512, False, "swiglu")])
+def test_gemm_q8_split_input_equals_fp32_input(M, N, K, gs, epi):
+    """x handed over already split (ops.split_activations: bf16 hi + lo per value, the GEMM's own split) gives the
+    same product, bitwise, as fp32 x: both kernels (the DMA-staged one copies the split pieces straight into its
+    fragment planes, the register-staged one stores them as loaded), with the DMA kernel's column and row tails
+    (M 6144 N 8224; the SwiGLU rows past 45 panels at M 6144 N 7168) and ragged M, N."""
+    dev = device()
+    q, s = (_q8g if gs else _q8)(N, K, M + 7 * N)
+    x = (torch.randn(M, K, generator=torch.Generator().manual_seed(M + K)) * 3.0).to(dev)
+    qd, sd = q.to(dev), s.to(dev)
+    pushes = None
+    if epi == "swiglu":
+        pushes = ops.pack_pushes([(5, "add", [1.0, -1.0, 2.0]), (None, "mul", [0.5, 2.0, 1.0])], dev)
+    announce(f"gemm_q8 split input M{M} N{N} K{K} gs {gs} {epi}")
+    xs = ops.split_activations(x)
+    if epi == "add":
+        base = torch.randn(M, N, generator=torch.Generator().manual_seed(1)).to(dev)
+        a, b = base.clone(), base.clone()
+        ops.gemm_q8(x, qd, sd, out=a, epilogue="add")
+        ops.gemm_q8(xs, qd, sd, out=b, epilogue="add")
+    else:
+        a = ops.gemm_q8(x, qd, sd, epilogue=epi, pushes=pushes, T=max(1, M // 3))
+        b = ops.gemm_q8(xs, qd, sd, epilogue=epi, pushes=pushes, T=max(1, M // 3))
+    torch.cuda.synchronize()
+    assert torch.equal(a, b), f"max diff {(a - b).abs().max().item():.3e}"
+
