@@ -445,7 +445,9 @@ __global__ __launch_bounds__(256) void gdn_decode_sliced_kernel(
 }
 
 // One wave per (token m, head h) of o [M, Hv, dv]; dv = 128 (two values per lane). Four waves per block.
-template <typename T>
+// XS (fp32 o): out in the int8 GEMM's split layout (each group of 8 values as 8 bf16 hi parts, then 8 bf16 lo parts),
+// the output projection's input read without splitting.
+template <typename T, bool XS>
 __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict__ o, const float* __restrict__ z,
                                                             int64_t ldz, const float* __restrict__ w,
                                                             const float* __restrict__ head_scale, T* __restrict__ out,
@@ -465,8 +467,20 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict_
   // HF rounds the normalised value to the input dtype before the weight multiply
   const float n0 = to_f32(from_f32<T>(x0 * r)), n1 = to_f32(from_f32<T>(x1 * r));
   T* orw = out + job * 128;
-  orw[2 * lane] = from_f32<T>(w[2 * lane] * n0 * silu_f(zr[2 * lane]) * hs);
-  orw[2 * lane + 1] = from_f32<T>(w[2 * lane + 1] * n1 * silu_f(zr[2 * lane + 1]) * hs);
+  const float y0 = w[2 * lane] * n0 * silu_f(zr[2 * lane]) * hs;
+  const float y1 = w[2 * lane + 1] * n1 * silu_f(zr[2 * lane + 1]) * hs;
+  if constexpr (XS) {  // values 2 l, 2 l + 1: positions 2 (l % 4) .. + 1 of group l / 4
+    __bf16* g = reinterpret_cast<__bf16*>(orw + 8 * (lane >> 2));
+    const bf16_hl a = bf16_split(y0), c = bf16_split(y1);
+    const int e = 2 * (lane & 3);
+    g[e] = a.hi;
+    g[e + 1] = c.hi;
+    g[8 + e] = a.lo;
+    g[9 + e] = c.lo;
+  } else {
+    orw[2 * lane] = from_f32<T>(y0);
+    orw[2 * lane + 1] = from_f32<T>(y1);
+  }
 }
 
 // One wave per (token m, job j) with j < Hq: query head j; Hq <= j < Hq + Hkv: key head; then value heads.
@@ -730,13 +744,27 @@ extern "C" int q35_gated_rmsnorm(const void* o, const float* z, int64_t ldz, con
   if (blocks > 0x7fffffff) return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (dtype == Q35_F32)
-    hipLaunchKernelGGL(gated_rmsnorm_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)o, z,
+    hipLaunchKernelGGL((gated_rmsnorm_kernel<float, false>), dim3((unsigned)blocks), dim3(256), 0, st, (const float*)o, z,
                        ldz, w, head_scale, (float*)out, M, (int)Hv, eps);
   else if (dtype == Q35_BF16)
-    hipLaunchKernelGGL(gated_rmsnorm_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, st, (const __bf16*)o, z,
+    hipLaunchKernelGGL((gated_rmsnorm_kernel<__bf16, false>), dim3((unsigned)blocks), dim3(256), 0, st, (const __bf16*)o, z,
                        ldz, w, head_scale, (__bf16*)out, M, (int)Hv, eps);
   else
     return Q35_EUNSUPPORTED;
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+extern "C" int q35_gated_rmsnorm_split(const float* o, const float* z, int64_t ldz, const float* w,
+                                       const float* head_scale, void* out, int64_t M, int64_t Hv, int64_t dv, float eps,
+                                       q35_stream_t stream) {
+  using namespace q35;
+  if (!o || !z || !w || !out || M <= 0 || Hv <= 0 || dv <= 0 || ldz < Hv * dv) return Q35_EINVAL;
+  if (dv != 128 || ((uintptr_t)out & 15)) return Q35_EUNSUPPORTED;
+  const int64_t blocks = (M * Hv + 3) / 4;
+  if (blocks > 0x7fffffff) return Q35_EUNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL((gated_rmsnorm_kernel<float, true>), dim3((unsigned)blocks), dim3(256), 0, st, o, z, ldz, w,
+                     head_scale, static_cast<float*>(out), M, (int)Hv, eps);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 

@@ -11,7 +11,8 @@
 // of the reference path (HF runs these projections in fp32). Group scales (GS): the products of one 128-input group
 // accumulate into a second register set, which is added to the result scaled by the group's scale of the column.
 // Epilogues: store, accumulate into y (the residual add after down_proj / out_proj), or SwiGLU over interleaved
-// (gate, up) row pairs with the neuron pushes applied, writing y[m, n / 2].
+// (gate, up) row pairs with the neuron pushes applied, writing y[m, n / 2] (fp32, or in the split layout below for
+// down_proj to read without splitting).
 //
 // Two kernels:
 //   gemm_q8_dma_kernel (N >= 2048, K <= 2048: the gate/up and input projections): 128 x 256 tiles, one block of 8
@@ -45,7 +46,7 @@ constexpr int kGN = 128;  // output columns per block (register-staged kernel)
 constexpr int kGK = 64;   // K step (register-staged kernel)
 constexpr int kQK = 32;   // K per pipeline stage (DMA kernel)
 
-enum GemmEpi : int { kGemmStore = 0, kGemmAccumulate = 1, kGemmSwiglu = 2 };
+enum GemmEpi : int { kGemmStore = 0, kGemmAccumulate = 1, kGemmSwiglu = 2, kGemmSwigluSplit = 3 };
 
 __device__ __forceinline__ int gsw(int r, int s) { return s ^ (r & 7); }
 __device__ __forceinline__ float gemm_silu(float x) { return x / (1.f + __expf(-x)); }
@@ -64,6 +65,18 @@ __device__ __forceinline__ bool gemm_pushes_touch(const q35_push* ps, int npush,
 // the batch row of token row m (rows of T tokens each), min(m / T, 3), without a division
 __device__ __forceinline__ int gemm_push_row(int m, int T) {
   return (int)(m >= T) + (int)((int64_t)m >= 2 * (int64_t)T) + (int)((int64_t)m >= 3 * (int64_t)T);
+}
+
+// y[n] of an activation row: fp32, or (ys) in the split layout (n's bf16 hi and lo parts in its group of 8)
+__device__ __forceinline__ void gemm_store_act(float* yrow, int n, float a, int ys) {
+  if (ys) {
+    __bf16* g = reinterpret_cast<__bf16*>(yrow + 8 * (n >> 3));
+    const bf16_hl t = bf16_split(a);
+    g[n & 7] = t.hi;
+    g[8 + (n & 7)] = t.lo;
+  } else {
+    yrow[n] = a;
+  }
 }
 
 __device__ __forceinline__ float gemm_push(const q35_push* ps, int n, int row, float a) {
@@ -132,7 +145,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
                                                              const float* __restrict__ ws, float* __restrict__ Y,
                                                              int64_t ldy, int M, int N, int K,
                                                              const q35_push* __restrict__ pushes, int npush, int T,
-                                                             int moff) {
+                                                             int moff, int ys) {
   __shared__ __attribute__((aligned(16))) char smem[kDNS * kDSB];
   __shared__ __attribute__((aligned(16))) char xc[XS ? 1 : 2][2][XS ? 16 : kDXC];  // [buffer][hi, lo] (fp32 x)
   __shared__ float gscale[GS ? kDGS * kDBN : 1];
@@ -354,7 +367,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
               const int row = gemm_push_row(moff + m, T);
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
             }
-            Y[(size_t)m * ldy + neuron] = a;
+            gemm_store_act(Y + (size_t)m * ldy, neuron, a, ys);
           }
         } else if (m < M && n < N) {
           float* dst = Y + (size_t)m * ldy + n;
@@ -375,7 +388,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
                                                          const int8_t* __restrict__ W, const float* __restrict__ ws,
                                                          float* __restrict__ Y, int64_t ldy, int M, int N, int K,
                                                          const q35_push* __restrict__ pushes, int npush, int T,
-                                                         int moff) {
+                                                         int moff, int ys) {
   static_assert(BM == 64 || BM == 128, "rows per block");
   constexpr int MT = BM / 64;         // 32-row MFMA tiles per wave along M (a wave covers BM / 2 rows)
   constexpr int TPR = 256 / BM;       // threads per staged row of x
@@ -513,7 +526,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
               const int row = gemm_push_row(moff + m, T);
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
             }
-            Y[(size_t)m * ldy + neuron] = a;
+            gemm_store_act(Y + (size_t)m * ldy, neuron, a, ys);
           }
         } else if (m < M && n < N) {
           float* dst = Y + (size_t)m * ldy + n;
@@ -531,7 +544,7 @@ namespace q35 {
 template <bool XS>
 static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
                           int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes, int64_t npush,
-                          int64_t T, int64_t moff, hipStream_t st) {
+                          int64_t T, int64_t moff, int ys, hipStream_t st) {
   const int64_t nbn = (N + kGN - 1) / kGN;
   // 128-row tiles when they still give at least two blocks per compute unit, else 64-row tiles
   const bool big = ((M + 127) / 128) * nbn >= 512;
@@ -540,7 +553,7 @@ static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const fl
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
 #define Q35_GEMM_LAUNCH(BMV, E, G)                                                                                   \
   hipLaunchKernelGGL((gemm_q8_rs_kernel<BMV, E, G, XS>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W,       \
-                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, (int)moff)
+                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, (int)moff, ys)
 #define Q35_GEMM_EPI(BMV, G)                                              \
   if (epilogue == kGemmStore) Q35_GEMM_LAUNCH(BMV, kGemmStore, G);        \
   else if (epilogue == kGemmAccumulate) Q35_GEMM_LAUNCH(BMV, kGemmAccumulate, G); \
@@ -558,13 +571,13 @@ static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const fl
 template <bool XS>
 static int gemm_dma_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
                            int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes,
-                           int64_t npush, int64_t T, hipStream_t st) {
+                           int64_t npush, int64_t T, int ys, hipStream_t st) {
   const int moff = 0;
   const int64_t nblocks = ((M + kDBM - 1) / kDBM) * ((N + kDBN - 1) / kDBN);
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
 #define Q35_GEMM_DMA(E, G_)                                                                                       \
   hipLaunchKernelGGL((gemm_q8_dma_kernel<E, G_, XS>), dim3((unsigned)nblocks), dim3(512), 0, st, x, ldx, W,        \
-                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, moff)
+                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, moff, ys)
   if (gs) {
     if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, true);
     else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, true);
@@ -600,7 +613,13 @@ static int gemm_q8_run(const float* x, int64_t ldx, const int8_t* W, int w_dtype
   if (w_dtype != Q35_I8 && w_dtype != Q35_I8_G128) return Q35_EUNSUPPORTED;
   const bool gs = w_dtype == Q35_I8_G128;
   if (gs && K % 128 != 0) return Q35_EUNSUPPORTED;
-  if (epilogue < kGemmStore || epilogue > kGemmSwiglu) return Q35_EINVAL;
+  if (epilogue < kGemmStore || epilogue > kGemmSwigluSplit) return Q35_EINVAL;
+  // epilogue 3: SwiGLU with y in the split layout (the next product's input, read without splitting)
+  const int ys = epilogue == kGemmSwigluSplit;
+  if (ys) {
+    epilogue = kGemmSwiglu;
+    if ((N / 2) % 8 != 0 || ldy % 4 != 0 || ((uintptr_t)y & 15)) return Q35_EUNSUPPORTED;
+  }
   if (npush < 0 || (npush > 0 && !pushes) || npush > 64) return Q35_EINVAL;
   if (epilogue == kGemmSwiglu ? (N % 2 != 0 || ldy < N / 2) : ldy < N) return Q35_EINVAL;
   if (ldx < K) return Q35_EINVAL;
@@ -629,19 +648,19 @@ static int gemm_q8_run(const float* x, int64_t ldx, const int8_t* W, int w_dtype
         if (M1 > 0 && M1 < M) Md = M1;
       }
     }
-    int r = gemm_dma_launch<XS>(x, ldx, W, w_scale, y, ldy, Md, Nd, K, epilogue, gs, pushes, npush, T, st);
+    int r = gemm_dma_launch<XS>(x, ldx, W, w_scale, y, ldy, Md, Nd, K, epilogue, gs, pushes, npush, T, ys, st);
     if (r != Q35_OK) return r;
     if (Md < M) {
-      r = gemm_rs_launch<XS>(x + Md * ldx, ldx, W, w_scale, y + Md * ldy, ldy, M - Md, Nd, K, epilogue, gs, pushes, npush,
-                         T, Md, st);
+      r = gemm_rs_launch<XS>(x + Md * ldx, ldx, W, w_scale, y + Md * ldy, ldy, M - Md, Nd, K, epilogue, gs, pushes,
+                             npush, T, Md, ys, st);
       if (r != Q35_OK) return r;
     }
     if (Nd < N)
       r = gemm_rs_launch<XS>(x, ldx, W + Nd * K, w_scale + (gs ? Nd * (K / 128) : Nd), y + Nd, ldy, M, N - Nd, K,
-                         epilogue, gs, pushes, npush, T, 0, st);
+                             epilogue, gs, pushes, npush, T, 0, ys, st);
     return r;
   }
-  return gemm_rs_launch<XS>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, st);
+  return gemm_rs_launch<XS>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, ys, st);
 }
 
 }  // namespace q35

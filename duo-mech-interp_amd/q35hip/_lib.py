@@ -20,7 +20,7 @@ EXPORTS = [
     "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
     "q35_swiglu_push",
     "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm", "q35_gemm_q8", "q35_gemm_q8_split",
-    "q35_add_rmsnorm_split",
+    "q35_add_rmsnorm_split", "q35_gated_rmsnorm_split",
     "q35_gdn_decode_sliced", "q35_gemv_norm_conv", "q35_gemv_gated_norm", "q35_gdn_chunk_prefill_conv",
 ]
 
@@ -57,6 +57,7 @@ _SIGS = {
     "q35_gdn_chunk_prefill_conv": ([P, I64, P, P, P, P, P, I64, I64, P, P, P, I64, I64, I64, I64, I64, I64, I64, F32,
                                     P, SZ, P], I32),
     "q35_gated_rmsnorm": ([P, P, I64, P, P, P, I64, I64, I64, F32, I32, P], I32),
+    "q35_gated_rmsnorm_split": ([P, P, I64, P, P, P, I64, I64, I64, F32, P], I32),
     "q35_gdn_decode_fused": ([P, I64, P, P, P, P, P, I64, I64, I64, P, P, P, F32, F32, P, I64, I64, I64, I64, P],
                              I32),
     "q35_attn_prep": ([P, I64, P, P, F32, P, P, I64, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I32),

@@ -115,8 +115,10 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
                                               use_qk_l2norm_in_kernel=True)
             rec_state.copy_(S)
     # gated RMSNorm: plain w, norm before the silu(z) gate (HF:168-184; engine/kernels_qwen35.js:237-243)
-    o = ops.gated_rmsnorm(o, y[..., C:C + Vd], p["norm"], head_scale, eps)
-    return linear(o, p["out_proj"], *_q8(p, "out_proj"), residual=residual)
+    # (fp32 o before an int8 output projection: the result already split for the int8 GEMM)
+    split = T > 1 and o.dtype == torch.float32 and wq_out is not None and Vd % 64 == 0
+    o = ops.gated_rmsnorm(o, y[..., C:C + Vd], p["norm"], head_scale, eps, split=split)
+    return linear(o, p["out_proj"], wq_out, ws_out, residual=residual)
 
 
 def _act_dtype(x):

@@ -90,8 +90,10 @@ def mlp(p, h, x, prenorm=None):
     if pn is not None:
         h = layers.prenorm_torch(h, pn)
     if "_gu_q8" in p and H % 64 == 0 and p["down_proj.q"].shape[1] % 64 == 0:
-        # int8 GEMMs: [gate | up] interleaved with the SwiGLU + push epilogue, then down_proj accumulating into x
-        a = ops.gemm_q8(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T)
+        # int8 GEMMs: [gate | up] interleaved with the SwiGLU + push epilogue (its output already split for the next
+        # product), then down_proj accumulating into x
+        a = ops.gemm_q8(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T,
+                        split_out=p["_gu_q8"].shape[0] % 16 == 0)
         ops.gemm_q8(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H), epilogue="add")
         return x
     if h.dtype == torch.int32:

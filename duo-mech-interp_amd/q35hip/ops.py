@@ -69,6 +69,7 @@ _LIB.define("gdn_conv(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) con
             "Tensor dt_bias, int b_off, int a_off, int Hk, int dk, int Hv, int dv, bool bf16_out) "
             "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
 _LIB.define("gated_rmsnorm(Tensor o, Tensor z, Tensor w, Tensor? head_scale, float eps) -> Tensor")
+_LIB.define("gated_rmsnorm_split(Tensor o, Tensor z, Tensor w, Tensor? head_scale, float eps) -> Tensor")
 _LIB.define("gdn_decode_fused_(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
             "Tensor dt_bias, int b_off, int a_off, int z_off, Tensor(b!) state, Tensor norm_w, Tensor? head_scale, "
             "float eps, float scale) -> Tensor")
@@ -348,9 +349,10 @@ def _gdn_decode_sliced_impl(y, A_log, dt_bias, b_off, a_off, state, scale):
     return out
 
 
-def _gated_rmsnorm_impl(o, z, w, head_scale, eps):
+def _gated_rmsnorm_impl(o, z, w, head_scale, eps, split=False):
     _on_gpu(o, w, head_scale)
     _require(o.dtype in _DT and o.dim() >= 2, "o: [..., Hv, dv] fp32 or bf16")
+    _require(not split or o.dtype == torch.float32, "the split output form takes fp32 o")
     Hv, dv = o.shape[-2], o.shape[-1]
     M = o.numel() // (Hv * dv)
     rows, ldz = _rows_view(z, Hv * dv, "z")
@@ -358,11 +360,20 @@ def _gated_rmsnorm_impl(o, z, w, head_scale, eps):
     _require(w.numel() == dv and w.dtype == torch.float32, "w: [dv] fp32")
     if head_scale is not None:
         _require(head_scale.numel() == Hv and head_scale.dtype == torch.float32, "head_scale: [Hv] fp32")
-    out = torch.empty(*o.shape[:-2], Hv * dv, dtype=o.dtype, device=o.device)
+    out = torch.empty(*o.shape[:-2], Hv * dv, dtype=torch.int32 if split else o.dtype, device=o.device)
+    if split:
+        st = _lib.lib().q35_gated_rmsnorm_split(_ptr(o), _ptr(z), ldz, _ptr(w), _ptr(head_scale), _ptr(out), M, Hv,
+                                                dv, float(eps), _stream(o))
+        check(st, "q35_gated_rmsnorm_split")
+        return out
     st = _lib.lib().q35_gated_rmsnorm(_ptr(o), _ptr(z), ldz, _ptr(w), _ptr(head_scale), _ptr(out), M, Hv, dv,
                                       float(eps), _DT[o.dtype], _stream(o))
     check(st, "q35_gated_rmsnorm")
     return out
+
+
+def _gated_rmsnorm_split_impl(o, z, w, head_scale, eps):
+    return _gated_rmsnorm_impl(o, z, w, head_scale, eps, split=True)
 
 
 def _attn_prep_impl(y, q_norm_w, k_norm_w, eps, cos, sin, pos, k_cache, v_cache, Hq, Hkv, want_kv):
@@ -440,12 +451,13 @@ def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T):
     _on_gpu(W, w_scale, pushes)
     _require(x.is_cuda and x.dtype in (torch.float32, torch.int32) and x.dim() == 2 and x.stride(1) == 1,
              "x: [M, K] fp32 (or int32 words of split activations) with unit column stride")
-    _require(y.is_cuda and y.dtype == torch.float32 and y.dim() == 2 and y.stride(1) == 1, "y: [M, N] fp32")
+    _require(y.is_cuda and y.dtype == (torch.int32 if epilogue == 3 else torch.float32) and y.dim() == 2
+             and y.stride(1) == 1, "y: [M, N] fp32 (int32 words of split activations for epilogue 3)")
     _require(W.dim() == 2 and W.dtype == torch.int8, "W: [N, K] int8")
     M, K = x.shape
     N = W.shape[0]
     _require(W.shape[1] == K and y.shape[0] == M, "x, W, y shapes disagree")
-    _require(y.shape[1] == (N // 2 if epilogue == 2 else N), "y: [M, N] ([M, N / 2] for the SwiGLU epilogue)")
+    _require(y.shape[1] == (N // 2 if epilogue in (2, 3) else N), "y: [M, N] ([M, N / 2] for the SwiGLU epilogue)")
     fmt = _weight_format(W, w_scale, N, K)
     _require(K % 64 == 0, "K must be a multiple of 64")
     npush = _pushes_check(pushes)
@@ -567,7 +579,7 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gdn_chunk_prefill", _gdn_chunk_impl), ("gated_attn_prefill", _attn_prefill_impl),
                      ("gated_attn_prefill_cached", _attn_prefill_cached_impl),
                      ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
-                     ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl),
+                     ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl), ("gated_rmsnorm_split", _gated_rmsnorm_split_impl),
                      ("gdn_decode_fused_", _gdn_decode_fused_impl),
                      ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
                      ("gemm_q8_", _gemm_q8_impl),
@@ -617,6 +629,8 @@ _LIB.impl("swiglu_push", lambda gu, pushes, T: gu.new_empty(*gu.shape[:-1], gu.s
 _LIB.impl("add_rmsnorm_", lambda x, y, w, eps: torch.empty_like(x), "Meta")
 _LIB.impl("add_rmsnorm_split_", lambda x, y, w, eps: torch.empty_like(x, dtype=torch.int32), "Meta")
 _LIB.impl("gated_rmsnorm", lambda o, z, w, hs, eps: o.new_empty(*o.shape[:-2], o.shape[-2] * o.shape[-1]), "Meta")
+_LIB.impl("gated_rmsnorm_split", lambda o, z, w, hs, eps: o.new_empty(*o.shape[:-2], o.shape[-2] * o.shape[-1],
+                                                                      dtype=torch.int32), "Meta")
 
 
 def _meta_gdn_conv(y, conv_w, conv_bias, conv_state, A_log, dt_bias, b_off, a_off, Hk, dk, Hv, dv, bf16_out):
@@ -771,9 +785,12 @@ def gemv_gated_norm(o, z, norm_w, W, w_scale, out, *, head_scale=None, eps=1e-6,
     return out
 
 
-def gated_rmsnorm(o, z, w, head_scale=None, eps=1e-6):
+def gated_rmsnorm(o, z, w, head_scale=None, eps=1e-6, split=False):
     """Qwen3_5RMSNormGated (HF:168-184) per (token, head) with the engine's optional per-head scale
-    (engine/kernels_qwen35.js:243): o [..., Hv, dv], z [..., Hv * dv] fp32 (rows may be strided) -> [..., Hv * dv]."""
+    (engine/kernels_qwen35.js:243): o [..., Hv, dv], z [..., Hv * dv] fp32 (rows may be strided) -> [..., Hv * dv].
+    split=True (fp32 o): the int32 words of the result in the int8 GEMM's split layout (split_activations)."""
+    if split:
+        return torch.ops.q35.gated_rmsnorm_split(o, z, w.float().contiguous(), head_scale, float(eps))
     return torch.ops.q35.gated_rmsnorm(o, z, w.float().contiguous(), head_scale, float(eps))
 
 
@@ -827,19 +844,24 @@ def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, preno
     return out
 
 
-def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1):
+def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1, split_out=False):
     """y[m, n] = sum_k x[m, k] W[n, k] s(n, k) over many rows (the prefill projections): x [M, K] fp32, W [N, K]
     int8 with scales w_scale [N, K / 128] (per group of 128 inputs) or [N] (per row), K a multiple of 64 (128 with
     group scales); fp32-accurate (bf16 MFMA on a hi + lo split of x). epilogue "store" writes out, "add"
     accumulates into out, "swiglu" treats W's rows as interleaved (gate, up) pairs and writes
     silu(gate) * up with the neuron pushes (pack_pushes) applied, out [M, N / 2]. x may also be the int32 words of
     activations already split (add_rmsnorm_(..., split=True), split_activations): the same product, bitwise, without
-    the split in the kernel. Returns out."""
+    the split in the kernel. split_out=True (SwiGLU only) writes out as the int32 words of the split layout, the
+    input of the next gemm_q8. Returns out."""
     e = _EPI[epilogue]
+    if split_out:
+        if e != 2:
+            raise ValueError("gemm_q8: split_out is a form of the SwiGLU epilogue")
+        e = 3
     x = x if x.stride(-1) == 1 else x.contiguous()
     if out is None:
-        N = W.shape[0] // 2 if e == 2 else W.shape[0]
-        out = torch.empty(x.shape[0], N, dtype=torch.float32, device=x.device)
+        N = W.shape[0] // 2 if e in (2, 3) else W.shape[0]
+        out = torch.empty(x.shape[0], N, dtype=torch.int32 if e == 3 else torch.float32, device=x.device)
     torch.ops.q35.gemm_q8_(x, W, w_scale, out, e, pushes, int(T))
     return out
 

@@ -38,8 +38,9 @@
  *                            with the SwiGLU + push epilogue of `swiglu` (engine/kernels_qwen35.js:250-279)
  *   q35_add_rmsnorm          HF:720-734 Qwen3_5RMSNorm (1 + w) with the residual add before it (HF:753-793);
  *                            engine/kernels.js:226-246 `rmsnorm` (OFFSET) and `addInto`
- *   q35_gemm_q8_split,       the same two on activations handed over already split into bf16 hi + lo parts (no
- *   q35_add_rmsnorm_split    counterpart in the reference's interface: a layout between the norm and the GEMM)
+ *   q35_gemm_q8_split,       the same on activations handed over already split into bf16 hi + lo parts (no
+ *   q35_add_rmsnorm_split,   counterpart in the reference's interface: a layout between the producers and the
+ *   q35_gated_rmsnorm_split  GEMM)
  *   q35_argmax_rows          engine/kernels.js:260-283 `argmax` (greedy token of each row, engine/model.js:494-497)
  */
 #ifndef Q35HIP_H
@@ -278,6 +279,14 @@ int q35_gated_rmsnorm(const void* o, const float* z, int64_t ldz, const float* w
                       int64_t M, int64_t Hv, int64_t dv, float eps, int dtype, q35_stream_t stream);
 
 /*
+ * q35_gated_rmsnorm on fp32 o with out written in the int8 GEMM's split layout (each value as hi = bf16(v),
+ * lo = bf16(v - hi); per row of Hv dv values, each group of 8 as its 8 hi parts then its 8 lo parts): the input of
+ * the output projection's q35_gemm_q8_split. out: [M, Hv dv] 4-byte words, 16-byte aligned. Same reference lines.
+ */
+int q35_gated_rmsnorm_split(const float* o, const float* z, int64_t ldz, const float* w, const float* head_scale,
+                            void* out, int64_t M, int64_t Hv, int64_t dv, float eps, q35_stream_t stream);
+
+/*
  * Gated-attention front end over the fused projection output y: [B, T, ldy] fp32 holding per token
  * [q_proj (Hq heads of [q (D) | gate (D)]) | k_proj (Hkv x D) | v_proj (Hkv x D)].
  *   q_norm_w, k_norm_w: [D] fp32, RMSNorm with (1 + w) in fp32; cos, sin: [P, rot / 2] fp32 by absolute position
@@ -372,8 +381,9 @@ int q35_gemv_gated_norm(const float* o, int64_t ldo, const float* z, int64_t ldz
  *   of 64; y: [M, ldy] fp32. fp32-accurate: bf16 MFMA products of W (exact in bf16) with a hi + lo split of x
  *   (relative error about 1e-5); with group scales each group's partial product is scaled in fp32.
  *   epilogue 0: y = v; 1: y += v; 2: SwiGLU over interleaved row pairs (row 2 j gate, 2 j + 1 up of neuron j):
- *   y[m, j] = silu(v_2j) * v_2j+1 then the pushes in order (N even, ldy >= N / 2). pushes, npush <= 64 and T as
- *   for q35_gemv.
+ *   y[m, j] = silu(v_2j) * v_2j+1 then the pushes in order (N even, ldy >= N / 2); 3: as 2 with y written in the
+ *   split layout of q35_gemm_q8_split's input (N / 2 a multiple of 8, ldy a multiple of 4, y 16-byte aligned), the
+ *   down projection's input. pushes, npush <= 64 and T as for q35_gemv.
  */
 int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush,

@@ -129,6 +129,10 @@ def test_validation_rejects_without_launching():
     assert L.q35_add_rmsnorm_split(fake, 1028, None, 0, fake, fake, 1028, 3, 1028, 1e-6, None) == 2
     assert L.q35_gemm_q8_split(fake, 192, fake, 3, fake, fake, 64, 100, 64, 192, 0, None, 0, 1, None) == 2
     assert L.q35_gemm_q8_split(None, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 0, None, 0, 1, None) == 1
+    # SwiGLU with split output (epilogue 3): N / 2 must be a multiple of 8; epilogue 4 does not exist
+    assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 36, 1024, 3, None, 0, 1, None) == 2
+    assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 4, None, 0, 1, None) == 1
+    assert L.q35_gated_rmsnorm_split(fake, fake, 2048, fake, None, fake, 3, 16, 64, 1e-6, None) == 2
     # argmax: ld shorter than the row, no rows
     assert L.q35_argmax_rows(fake, 100, 3, 101, fake, None, None) == 1
     assert L.q35_argmax_rows(fake, 100, 0, 100, fake, None, None) == 1

@@ -170,6 +170,25 @@ def test_add_rmsnorm_matches_oracle(with_add):
     assert oracle.rel_err(xd.cpu(), xs) <= TOL_F32
 
 
+@pytest.mark.parametrize("with_scale", [False, True])
+def test_gated_rmsnorm_split_output(with_scale):
+    """The gated norm with its output in the int8 GEMM's split layout (the GDN output projection's input): equal to
+    ops.split_activations of the fp32 form's output, bitwise, z rows strided as in the fused projection output."""
+    dev = device()
+    g = torch.Generator().manual_seed(72)
+    M, Hv = 70, 16
+    o = torch.randn(M, Hv, 128, generator=g).to(dev)
+    zw = torch.randn(M, Hv * 128 + 40, generator=g).to(dev)
+    w = (1.0 + 0.1 * torch.randn(128, generator=g)).to(dev)
+    hs = (1.0 + 0.1 * torch.randn(Hv, generator=g)).to(dev) if with_scale else None
+    announce(f"gated_rmsnorm split scale={with_scale}")
+    a = ops.gated_rmsnorm(o, zw[:, 8:8 + Hv * 128], w, hs)
+    b = ops.gated_rmsnorm(o, zw[:, 8:8 + Hv * 128], w, hs, split=True)
+    torch.cuda.synchronize()
+    assert b.dtype == torch.int32 and b.shape == a.shape
+    assert torch.equal(b, ops.split_activations(a))
+
+
 @pytest.mark.parametrize("with_add,H", [(False, 1024), (True, 1024), (True, 1000)])
 def test_add_rmsnorm_split_output(with_add, H):
     """The norm with its output in the int8 GEMM's split layout: the words equal ops.split_activations of the fp32

@@ -167,3 +167,24 @@ def test_gemm_q8_split_input_equals_fp32_input(M, N, K, gs, epi):
     torch.cuda.synchronize()
     assert torch.equal(a, b), f"max diff {(a - b).abs().max().item():.3e}"
 
+
+@pytest.mark.parametrize("M,N,K", [(6144, 7168, 1024), (300, 512, 256)])
+def test_gemm_q8_swiglu_split_output(M, N, K):
+    """The SwiGLU epilogue writing its output in the split layout (split_out, the down projection's input) equals
+    ops.split_activations of the fp32 output bitwise, with pushes: the DMA kernel with its row tail (M 6144) and the
+    register-staged kernel (N 512); down_proj on that output equals down_proj on the fp32 output bitwise."""
+    dev = device()
+    q, s = _q8g(N, K, 17 + M)
+    x = (torch.randn(M, K, generator=torch.Generator().manual_seed(M)) * 2.0).to(dev)
+    pushes = ops.pack_pushes([(3, "mul", [2.0, -1.0, 0.5]), (None, "add", [0.25, 0.0, -0.25])], dev)
+    announce(f"gemm_q8 swiglu split output M{M} N{N} K{K}")
+    a = ops.gemm_q8(x, q.to(dev), s.to(dev), epilogue="swiglu", pushes=pushes, T=max(1, M // 3))
+    b = ops.gemm_q8(x, q.to(dev), s.to(dev), epilogue="swiglu", pushes=pushes, T=max(1, M // 3), split_out=True)
+    torch.cuda.synchronize()
+    assert b.dtype == torch.int32 and b.shape == a.shape
+    assert torch.equal(b, ops.split_activations(a))
+    qd, sd = _q8g(256, N // 2, 19)
+    ya = ops.gemm_q8(a, qd.to(dev), sd.to(dev))
+    yb = ops.gemm_q8(b, qd.to(dev), sd.to(dev))
+    assert torch.equal(ya, yb)
+
