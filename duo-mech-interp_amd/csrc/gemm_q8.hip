@@ -49,7 +49,9 @@ constexpr int kQK = 32;   // K per pipeline stage (DMA kernel)
 enum GemmEpi : int { kGemmStore = 0, kGemmAccumulate = 1, kGemmSwiglu = 2, kGemmSwigluSplit = 3 };
 
 __device__ __forceinline__ int gsw(int r, int s) { return s ^ (r & 7); }
-__device__ __forceinline__ float gemm_silu(float x) { return x / (1.f + __expf(-x)); }
+// silu with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE division (about ten VALU instructions
+// per output of the SwiGLU epilogue); x = -inf gives NaN and large negative x gives -0, as the division does
+__device__ __forceinline__ float gemm_silu(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 // Whether any of the push records can touch neurons nlo .. nhi - 1 (a record for every neuron, or for one in the
 // range): a block whose neurons no record touches skips the per-output push loop (the model passes a fixed number of
@@ -67,15 +69,17 @@ __device__ __forceinline__ int gemm_push_row(int m, int T) {
   return (int)(m >= T) + (int)((int64_t)m >= 2 * (int64_t)T) + (int)((int64_t)m >= 3 * (int64_t)T);
 }
 
-// y[n] of an activation row: fp32, or (ys) in the split layout (n's bf16 hi and lo parts in its group of 8)
-__device__ __forceinline__ void gemm_store_act(float* yrow, int n, float a, int ys) {
+// y[n] of an activation row, given p = the row + gemm_act_col(n, ys): fp32, or (ys) in the split layout (n's bf16
+// hi and lo parts in its group of 8)
+__device__ __forceinline__ int gemm_act_col(int n, int ys) { return ys ? 8 * (n >> 3) : n; }
+__device__ __forceinline__ void gemm_store_act(float* p, int n, float a, int ys) {
   if (ys) {
-    __bf16* g = reinterpret_cast<__bf16*>(yrow + 8 * (n >> 3));
+    __bf16* g = reinterpret_cast<__bf16*>(p);
     const bf16_hl t = bf16_split(a);
     g[n & 7] = t.hi;
     g[8 + (n & 7)] = t.lo;
   } else {
-    yrow[n] = a;
+    *p = a;
   }
 }
 
@@ -344,12 +348,17 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
   // epilogue: lane holds column n = n0 + 64 wn + 32 nt + l32, rows m0 + 64 wm + 32 mt + 8 (r / 4) + 4 lh + r % 4
   const int mb = m0 + wm * 64 + 4 * lh;
   const bool pushes_here = EPI == kGemmSwiglu && gemm_pushes_touch(pushes, npush, n0 >> 1, (n0 + kDBN) >> 1);
+  int64_t roff[16];  // element offsets of a tile's 16 accumulator rows from its first (uniform): one add per output
+#pragma unroll
+  for (int r = 0; r < 16; ++r) roff[r] = (int64_t)(8 * (r >> 2) + (r & 3)) * ldy;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int n = n0 + wn * 64 + 32 * nt + l32;
     const float sc = GS ? 1.f : ws[min(n, N - 1)];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+      float* yt = Y + (int64_t)(mb + 32 * mt) * ldy;
+      float* ytn = yt + (EPI == kGemmSwiglu ? gemm_act_col(n >> 1, ys) : n);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = mb + 32 * mt + 8 * (r >> 2) + (r & 3);
@@ -367,10 +376,10 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
               const int row = gemm_push_row(moff + m, T);
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
             }
-            gemm_store_act(Y + (size_t)m * ldy, neuron, a, ys);
+            gemm_store_act(ytn + roff[r], neuron, a, ys);
           }
         } else if (m < M && n < N) {
-          float* dst = Y + (size_t)m * ldy + n;
+          float* dst = ytn + roff[r];
           *dst = EPI == kGemmAccumulate ? *dst + v : v;
         }
       }
@@ -507,15 +516,20 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
 
   // epilogue: lane holds column n = n0 + wn 64 + 32 nt + l32, rows m0 + wm BM/2 + 32 mt + 8 (r / 4) + 4 lh + r % 4
   const bool pushes_here = EPI == kGemmSwiglu && gemm_pushes_touch(pushes, npush, n0 >> 1, (n0 + kGN) >> 1);
+  int64_t roff[16];  // element offsets of a tile's 16 accumulator rows from its first (uniform): one add per output
+#pragma unroll
+  for (int r = 0; r < 16; ++r) roff[r] = (int64_t)(8 * (r >> 2) + (r & 3)) * ldy;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int n = n0 + wn * 64 + 32 * nt + l32;
     const float s = GS ? 1.f : ws[min(n, N - 1)];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+      const int mt0 = m0 + wm * (BM / 2) + 32 * mt + 4 * lh;
+      float* ytn = Y + (int64_t)mt0 * ldy + (EPI == kGemmSwiglu ? gemm_act_col(n >> 1, ys) : n);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * (BM / 2) + 32 * mt + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const int m = mt0 + 8 * (r >> 2) + (r & 3);
         const float v = acc[mt][nt][r] * s;
         if (EPI == kGemmSwiglu) {
           const float up = __shfl_xor(v, 1, 64);  // the odd column of the pair sits in the neighbouring lane
@@ -526,10 +540,10 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
               const int row = gemm_push_row(moff + m, T);
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
             }
-            gemm_store_act(Y + (size_t)m * ldy, neuron, a, ys);
+            gemm_store_act(ytn + roff[r], neuron, a, ys);
           }
         } else if (m < M && n < N) {
-          float* dst = Y + (size_t)m * ldy + n;
+          float* dst = ytn + roff[r];
           *dst = EPI == kGemmAccumulate ? *dst + v : v;
         }
       }
