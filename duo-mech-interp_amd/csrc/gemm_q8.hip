@@ -49,9 +49,7 @@ constexpr int kQK = 32;   // K per pipeline stage (DMA kernel)
 enum GemmEpi : int { kGemmStore = 0, kGemmAccumulate = 1, kGemmSwiglu = 2, kGemmSwigluSplit = 3 };
 
 __device__ __forceinline__ int gsw(int r, int s) { return s ^ (r & 7); }
-// silu with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE division (about ten VALU instructions
-// per output of the SwiGLU epilogue); x = -inf gives NaN and large negative x gives -0, as the division does
-__device__ __forceinline__ float gemm_silu(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+__device__ __forceinline__ float gemm_silu(float x) { return silu_f(x); }
 
 // Whether any of the push records can touch neurons nlo .. nhi - 1 (a record for every neuron, or for one in the
 // range): a block whose neurons no record touches skips the per-output push loop (the model passes a fixed number of

@@ -44,7 +44,7 @@ struct GemvAux {
   int cc, ck;        // conv: channels (outputs 0 .. cc - 1 are convolved), taps
 };
 
-__device__ __forceinline__ float gsilu(float x) { return x / (1.f + __expf(-x)); }
+__device__ __forceinline__ float gsilu(float x) { return silu_f(x); }
 
 // one push applied to activation a of neuron n (fields read straight from the record: no copy of the value array)
 __device__ __forceinline__ float apply_push(const q35_push* ps, int n, int row, float a) {
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
               if (i >= aux.ck - 1) break;
               cs[(size_t)i * aux.cc] = i + 1 < aux.ck - 1 ? cvs[i + 1] : v;
             }
-            *dst = a / (1.f + __expf(-a));
+            *dst = silu_f(a);
           } else if (EPI == kEpiAccumulate && nsplit > 1) {
             __hip_atomic_fetch_add(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           } else {

@@ -107,7 +107,10 @@ __device__ __forceinline__ bf16_hl bf16_split(float x) {
   const __bf16 h = (__bf16)x;
   return {h, (__bf16)(x - (float)h)};
 }
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
+// silu(x) = x / (1 + e^-x) with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE division (about ten
+// VALU instructions); large negative x gives -0 and x = -inf NaN, as the division does. Every kernel uses this one
+// form, so kernels that are compared bit for bit (a fused form against its parts) round alike.
+__device__ __forceinline__ float silu_f(float x) { return x * __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }  // threshold 20
 
 // Block barrier that orders LDS traffic only. __syncthreads() also waits for every outstanding global load of the
