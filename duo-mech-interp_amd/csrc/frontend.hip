@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const float* __restrict__
       const int t = i / Hv, h = i - t * Hv;
       const float* row = y + ((int64_t)b * T + t) * ldy;
       const size_t oi = ((size_t)b * T + t) * Hv + h;
-      betao[oi] = 1.f / (1.f + __expf(-row[b_off + h]));
+      betao[oi] = sigmoidf_(row[b_off + h]);
       go[oi] = -__expf(A_log[h]) * softplus_f(row[a_off + h] + dt_bias[h]);
     }
     return;
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void gdn_conv1_kernel(const float* __restrict_
   const float* row = y + (int64_t)b * ldy;
   if ((int)blockIdx.x == nb) {
     for (int h = tid; h < Hv; h += 256) {
-      betao[(size_t)b * Hv + h] = 1.f / (1.f + __expf(-row[b_off + h]));
+      betao[(size_t)b * Hv + h] = sigmoidf_(row[b_off + h]);
       go[(size_t)b * Hv + h] = -__expf(A_log[h]) * softplus_f(row[a_off + h] + dt_bias[h]);
     }
     return;
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(1024) void gdn_decode_fused_kernel(
     }
   }
   if (tid == 96) {
-    gates[0] = 1.f / (1.f + __expf(-gb));
+    gates[0] = sigmoidf_(gb);
     gates[1] = -__expf(gA) * softplus_f(ga + gdt);
   }
   __syncthreads();
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(256) void gdn_decode_sliced_kernel(
     red[wave][lane][1] = c;
   }
   if (tid == 0) {
-    gates[0] = 1.f / (1.f + __expf(-gb));
+    gates[0] = sigmoidf_(gb);
     gates[1] = -__expf(gA) * softplus_f(ga + gdt);
   }
   float sq = q20 * q20 + q21 * q21;

@@ -95,8 +95,8 @@ __device__ __forceinline__ bf16x8 pack8(const f32x4& lo, const f32x4& hi) {
   return r;
 }
 
-// sigmoid with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE division: the attention output gate,
-// one per output value
+// sigmoid with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE division (the attention output gate,
+// one per output value, and the GDN beta). Every kernel uses this one form, so fused forms round as their parts.
 __device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 // x = hi + lo up to 2^-17 |x|: hi = bf16(x), lo = bf16(x - hi), both rounded to nearest even (the split of fp32
 // activations for the int8 GEMM's bf16 products). The subtraction is never contracted into the product that made x
