@@ -15,6 +15,8 @@
 //                          written into the bf16 KV cache at positions pos[b] + t (pos read on the device, so that a
 //                          captured decode step replays at the right position).
 //   add_rmsnorm_kernel     the decoder layer's residual add + RMSNorm with (1 + w) (HF:720-734, :753-793).
+#include <type_traits>
+
 #include "q35_common.h"
 #include "q35hip.h"
 
@@ -483,6 +485,65 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const T* __restrict_
   }
 }
 
+// The same norm with 16-byte accesses (o, z, w, out 16-byte aligned, ldz a multiple of 4): two (token, head) jobs per
+// wave, 32 lanes per job, four values per lane; the squares are summed over the 32 lanes with xor shuffles. The
+// arithmetic per value is gated_rmsnorm_kernel's (only the summation order of the squares differs).
+template <typename T, bool XS>
+__global__ __launch_bounds__(256) void gated_rmsnorm4_kernel(const T* __restrict__ o, const float* __restrict__ z,
+                                                             int64_t ldz, const float* __restrict__ w,
+                                                             const float* __restrict__ head_scale,
+                                                             T* __restrict__ out, int64_t M, int Hv, float eps) {
+  Q35_ARGS_UPFRONT(o, z, ldz, w, head_scale, out, M, Hv, eps);
+  const int lane = threadIdx.x & 63, hl = lane & 31;
+  const int64_t job = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
+  if (job >= M * Hv) return;  // whole halves only: the shuffles below stay inside a half
+  const int64_t m = job / Hv;
+  const int h = (int)(job - m * Hv);
+  float x[4];
+  if constexpr (std::is_same<T, float>::value) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(o + job * 128 + 4 * hl);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = t[e];
+  } else {
+    const bf16x4 t = *reinterpret_cast<const bf16x4*>(o + job * 128 + 4 * hl);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = (float)t[e];
+  }
+  float ss = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off, 64);
+  const float r = rsqrtf(ss * (1.f / 128.f) + eps);
+  const f32x4 zz = *reinterpret_cast<const f32x4*>(z + m * ldz + h * 128 + 4 * hl);
+  const f32x4 ww = *reinterpret_cast<const f32x4*>(w + 4 * hl);
+  const float hs = head_scale ? head_scale[h] : 1.f;
+  float y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float n = to_f32(from_f32<T>(x[e] * r));  // HF rounds the normalised value to the input dtype
+    y[e] = ww[e] * n * silu_f(zz[e]) * hs;
+  }
+  T* orw = out + job * 128;
+  if constexpr (XS) {  // values 4 l .. 4 l + 3: half l % 2 of group l / 2 (8 bytes of its hi and of its lo part)
+    bf16x4 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bf16_hl t = bf16_split(y[e]);
+      hi[e] = t.hi;
+      lo[e] = t.lo;
+    }
+    float* gp = reinterpret_cast<float*>(orw) + 8 * (hl >> 1) + 2 * (hl & 1);
+    *reinterpret_cast<bf16x4*>(gp) = hi;
+    *reinterpret_cast<bf16x4*>(gp + 4) = lo;
+  } else if constexpr (std::is_same<T, float>::value) {
+    *reinterpret_cast<f32x4*>(orw + 4 * hl) = f32x4{y[0], y[1], y[2], y[3]};
+  } else {
+    bf16x4 t;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[e] = (__bf16)y[e];
+    *reinterpret_cast<bf16x4*>(orw + 4 * hl) = t;
+  }
+}
+
 // One wave per (token m, job j) with j < Hq: query head j; Hq <= j < Hq + Hkv: key head; then value heads.
 // D = 256: four values per lane (dims 4 l .. 4 l + 3). Four waves per block.
 __global__ __launch_bounds__(256) void attn_prep_kernel(const float* __restrict__ y, int64_t ldy,
@@ -743,7 +804,15 @@ extern "C" int q35_gated_rmsnorm(const void* o, const float* z, int64_t ldz, con
   const int64_t blocks = (M * Hv + 3) / 4;
   if (blocks > 0x7fffffff) return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == Q35_F32)
+  const bool v4 = !(((uintptr_t)o | (uintptr_t)z | (uintptr_t)w | (uintptr_t)out) & 15) && ldz % 4 == 0;
+  const unsigned blocks4 = (unsigned)((M * Hv + 7) / 8);
+  if (v4 && dtype == Q35_F32)
+    hipLaunchKernelGGL((gated_rmsnorm4_kernel<float, false>), dim3(blocks4), dim3(256), 0, st, (const float*)o, z, ldz,
+                       w, head_scale, (float*)out, M, (int)Hv, eps);
+  else if (v4 && dtype == Q35_BF16)
+    hipLaunchKernelGGL((gated_rmsnorm4_kernel<__bf16, false>), dim3(blocks4), dim3(256), 0, st, (const __bf16*)o, z,
+                       ldz, w, head_scale, (__bf16*)out, M, (int)Hv, eps);
+  else if (dtype == Q35_F32)
     hipLaunchKernelGGL((gated_rmsnorm_kernel<float, false>), dim3((unsigned)blocks), dim3(256), 0, st, (const float*)o, z,
                        ldz, w, head_scale, (float*)out, M, (int)Hv, eps);
   else if (dtype == Q35_BF16)
@@ -763,8 +832,12 @@ extern "C" int q35_gated_rmsnorm_split(const float* o, const float* z, int64_t l
   const int64_t blocks = (M * Hv + 3) / 4;
   if (blocks > 0x7fffffff) return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL((gated_rmsnorm_kernel<float, true>), dim3((unsigned)blocks), dim3(256), 0, st, o, z, ldz, w,
-                     head_scale, static_cast<float*>(out), M, (int)Hv, eps);
+  if (!(((uintptr_t)o | (uintptr_t)z | (uintptr_t)w) & 15) && ldz % 4 == 0)
+    hipLaunchKernelGGL((gated_rmsnorm4_kernel<float, true>), dim3((unsigned)((M * Hv + 7) / 8)), dim3(256), 0, st, o, z,
+                       ldz, w, head_scale, static_cast<float*>(out), M, (int)Hv, eps);
+  else
+    hipLaunchKernelGGL((gated_rmsnorm_kernel<float, true>), dim3((unsigned)blocks), dim3(256), 0, st, o, z, ldz, w,
+                       head_scale, static_cast<float*>(out), M, (int)Hv, eps);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 

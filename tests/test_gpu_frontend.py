@@ -189,6 +189,28 @@ def test_gated_rmsnorm_split_output(with_scale):
     assert torch.equal(b, ops.split_activations(a))
 
 
+def test_gated_rmsnorm_aligned_and_unaligned_forms():
+    """16-byte-aligned o and z take the two-heads-per-wave form, a z one float off alignment the one-head form: the
+    two agree to fp32 rounding (only the summation order of the squares differs), fp32 and bf16, and each one's split
+    output equals ops.split_activations of its fp32 output."""
+    dev = device()
+    g = torch.Generator().manual_seed(73)
+    M, Hv = 37, 16
+    o = torch.randn(M, Hv, 128, generator=g).to(dev)
+    zw = torch.randn(M, Hv * 128 + 12, generator=g).to(dev)
+    w = (1.0 + 0.1 * torch.randn(128, generator=g)).to(dev)
+    announce("gated_rmsnorm aligned / unaligned z")
+    za, zu = zw[:, 8:8 + Hv * 128], zw[:, 9:9 + Hv * 128]
+    for dt in (torch.float32, torch.bfloat16):
+        a = ops.gated_rmsnorm(o.to(dt), zu, w).float()
+        b = ops.gated_rmsnorm(o.to(dt), zu.contiguous(), w).float()
+        torch.cuda.synchronize()
+        assert oracle.rel_err(a.cpu(), b.cpu()) <= (1e-6 if dt == torch.float32 else 1e-2)
+    for z in (za, zu):
+        f = ops.gated_rmsnorm(o, z, w)
+        assert torch.equal(ops.gated_rmsnorm(o, z, w, split=True), ops.split_activations(f))
+
+
 @pytest.mark.parametrize("with_add,H", [(False, 1024), (True, 1024), (True, 1000)])
 def test_add_rmsnorm_split_output(with_add, H):
     """The norm with its output in the int8 GEMM's split layout: the words equal ops.split_activations of the fp32
