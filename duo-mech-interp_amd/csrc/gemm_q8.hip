@@ -35,6 +35,8 @@
 // rounded the same way). Both kernels then skip the split: the DMA kernel copies the 16-byte hi and lo pieces
 // straight into the planes its A fragments are read from (no fp32 stage, no conversion pass), the register-staged
 // kernel stores the loaded pieces as they are. The products, and so y, are bitwise those of the fp32 input.
+// bf16 input (q35_gemm_q8_bf16, the attention output): hi = x exactly and lo = 0, so the register-staged kernel
+// issues only the hi products (bitwise those of the fp32 input x.float(): the skipped products are exact zeros).
 #include <type_traits>
 
 #include "q35_common.h"
@@ -390,7 +392,8 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
 // stages x[BM, 64] (split into hi and lo) and W[128, 64] (int8 -> bf16) in LDS, rows of 64 bf16 = 8 segments of 16
 // bytes, segment s of row r at s ^ (r & 7). The next step's global loads are issued before the current step's MFMAs,
 // so they are in flight during them. Blocks run n-fastest inside an m panel.
-template <int BM, int EPI, bool GS, bool XS>
+// XF: x fp32 (0), in the split layout (1), or bf16 (2: hi = x exactly, lo = 0, so the lo products are skipped)
+template <int BM, int EPI, bool GS, int XF>
 __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restrict__ X, int64_t ldx,
                                                          const int8_t* __restrict__ W, const float* __restrict__ ws,
                                                          float* __restrict__ Y, int64_t ldy, int M, int N, int K,
@@ -414,7 +417,10 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
   const int ar = tid / TPR, as0 = (tid % TPR) * SPT;
   const int br = tid >> 1, bh = tid & 1;
   const bool av = m0 + ar < M, bv = n0 + br < N;
-  const float* xrow = X + (size_t)min(m0 + ar, M - 1) * ldx + 8 * as0;
+  // (bf16 x: element offsets count 2-byte values; xa[s][0] then holds the segment's 8 values)
+  const float* xrow = XF == 2 ? reinterpret_cast<const float*>(reinterpret_cast<const __bf16*>(X) +
+                                                               (size_t)min(m0 + ar, M - 1) * ldx + 8 * as0)
+                              : X + (size_t)min(m0 + ar, M - 1) * ldx + 8 * as0;
   const int8_t* wrow = W + (size_t)min(n0 + br, N - 1) * K + 32 * bh;
 
   f32x4 xa[SPT][2];
@@ -422,8 +428,12 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
   auto load = [&](int k0) {
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
-      xa[s][0] = *reinterpret_cast<const f32x4*>(xrow + k0 + 8 * s);
-      xa[s][1] = *reinterpret_cast<const f32x4*>(xrow + k0 + 8 * s + 4);
+      if constexpr (XF == 2) {
+        xa[s][0] = *reinterpret_cast<const f32x4*>(xrow + (k0 + 8 * s) / 2);
+      } else {
+        xa[s][0] = *reinterpret_cast<const f32x4*>(xrow + k0 + 8 * s);
+        xa[s][1] = *reinterpret_cast<const f32x4*>(xrow + k0 + 8 * s + 4);
+      }
     }
     wb[0] = *reinterpret_cast<const u32x4*>(wrow + k0);
     wb[1] = *reinterpret_cast<const u32x4*>(wrow + k0 + 16);
@@ -433,15 +443,17 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
 #pragma unroll
     for (int s = 0; s < SPT; ++s) {
       bf16x8 hi, lo;
-      if constexpr (XS) {  // split x: the group's 16 bytes of hi parts, then its 16 bytes of lo parts
+      if constexpr (XF == 1) {  // split x: the group's 16 bytes of hi parts, then its 16 bytes of lo parts
         hi = __builtin_bit_cast(bf16x8, xa[s][0]);
         lo = __builtin_bit_cast(bf16x8, xa[s][1]);
+      } else if constexpr (XF == 2) {
+        hi = __builtin_bit_cast(bf16x8, xa[s][0]);
       } else {
         split8(xa[s][0], xa[s][1], hi, lo);
       }
       const int idx = ar * 8 + gsw(ar, as0 + s);
       Ah[idx] = av ? hi : z;
-      Al[idx] = av ? lo : z;
+      if constexpr (XF != 2) Al[idx] = av ? lo : z;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -484,7 +496,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
       for (int mt = 0; mt < MT; ++mt) {
         const int r = wm * (BM / 2) + 32 * mt + l32;
         ah[mt] = Ah[r * 8 + gsw(r, sg)];
-        al[mt] = Al[r * 8 + gsw(r, sg)];
+        if constexpr (XF != 2) al[mt] = Al[r * 8 + gsw(r, sg)];
       }
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
@@ -497,7 +509,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
         for (int nt = 0; nt < 2; ++nt) {
           f32x16& d = GS ? gacc[mt][nt] : acc[mt][nt];
           d = mfma32(ah[mt], b[nt], d);
-          d = mfma32(al[mt], b[nt], d);
+          if constexpr (XF != 2) d = mfma32(al[mt], b[nt], d);
         }
     }
     if (GS && ((k0 + kGK) & 127) == 0) {  // end of a group: fold it in with its scale
@@ -553,7 +565,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
 
 namespace q35 {
 
-template <bool XS>
+template <int XF>
 static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
                           int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes, int64_t npush,
                           int64_t T, int64_t moff, int ys, hipStream_t st) {
@@ -564,7 +576,7 @@ static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const fl
   const int64_t nblocks = ((M + BM - 1) / BM) * nbn;
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
 #define Q35_GEMM_LAUNCH(BMV, E, G)                                                                                   \
-  hipLaunchKernelGGL((gemm_q8_rs_kernel<BMV, E, G, XS>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W,       \
+  hipLaunchKernelGGL((gemm_q8_rs_kernel<BMV, E, G, XF>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W,       \
                      w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, (int)moff, ys)
 #define Q35_GEMM_EPI(BMV, G)                                              \
   if (epilogue == kGemmStore) Q35_GEMM_LAUNCH(BMV, kGemmStore, G);        \
@@ -617,7 +629,7 @@ static int64_t gemm_cu_count() {
 namespace q35 {
 
 // x: fp32 rows, or for XS rows in the split layout (the same bytes and leading dimension as fp32 rows)
-template <bool XS>
+template <bool XS, bool XB = false>
 static int gemm_q8_run(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
                        int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
                        int64_t npush, int64_t T, q35_stream_t stream) {
@@ -635,9 +647,12 @@ static int gemm_q8_run(const float* x, int64_t ldx, const int8_t* W, int w_dtype
   if (npush < 0 || (npush > 0 && !pushes) || npush > 64) return Q35_EINVAL;
   if (epilogue == kGemmSwiglu ? (N % 2 != 0 || ldy < N / 2) : ldy < N) return Q35_EINVAL;
   if (ldx < K) return Q35_EINVAL;
-  if (K % kGK != 0 || ldx % 4 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return Q35_EUNSUPPORTED;
+  if (K % kGK != 0 || ldx % (XB ? 8 : 4) != 0 || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return Q35_EUNSUPPORTED;
   if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff) return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // bf16 x: the register-staged kernel (one product per tile: the lo parts are zero)
+  if constexpr (XB)
+    return gemm_rs_launch<2>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, ys, st);
   // wide products with K <= 2048 (and x, W addressable with 32-bit byte offsets): the DMA kernel
   if (N >= 2048 && K <= 128 * kDGS && ((M - 1) * ldx + K) * 4 <= 0xffffffffLL && N * K <= 0xffffffffLL) {
     // One block per CU, so a last round of blocks that is mostly empty costs as much as a full one. A partial last
@@ -663,16 +678,16 @@ static int gemm_q8_run(const float* x, int64_t ldx, const int8_t* W, int w_dtype
     int r = gemm_dma_launch<XS>(x, ldx, W, w_scale, y, ldy, Md, Nd, K, epilogue, gs, pushes, npush, T, ys, st);
     if (r != Q35_OK) return r;
     if (Md < M) {
-      r = gemm_rs_launch<XS>(x + Md * ldx, ldx, W, w_scale, y + Md * ldy, ldy, M - Md, Nd, K, epilogue, gs, pushes,
-                             npush, T, Md, ys, st);
+      r = gemm_rs_launch<(XS ? 1 : 0)>(x + Md * ldx, ldx, W, w_scale, y + Md * ldy, ldy, M - Md, Nd, K, epilogue, gs,
+                                       pushes, npush, T, Md, ys, st);
       if (r != Q35_OK) return r;
     }
     if (Nd < N)
-      r = gemm_rs_launch<XS>(x, ldx, W + Nd * K, w_scale + (gs ? Nd * (K / 128) : Nd), y + Nd, ldy, M, N - Nd, K,
-                             epilogue, gs, pushes, npush, T, 0, ys, st);
+      r = gemm_rs_launch<(XS ? 1 : 0)>(x, ldx, W + Nd * K, w_scale + (gs ? Nd * (K / 128) : Nd), y + Nd, ldy, M,
+                                       N - Nd, K, epilogue, gs, pushes, npush, T, 0, ys, st);
     return r;
   }
-  return gemm_rs_launch<XS>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, ys, st);
+  return gemm_rs_launch<(XS ? 1 : 0)>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, ys, st);
 }
 
 }  // namespace q35
@@ -688,4 +703,11 @@ extern "C" int q35_gemm_q8_split(const void* xs, int64_t ldx, const int8_t* W, i
                                  const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
   return q35::gemm_q8_run<true>(static_cast<const float*>(xs), ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue,
                                 pushes, npush, T, stream);
+}
+
+extern "C" int q35_gemm_q8_bf16(const void* xb, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
+                                float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
+                                const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
+  return q35::gemm_q8_run<false, true>(static_cast<const float*>(xb), ldx, W, w_dtype, w_scale, y, ldy, M, N, K,
+                                       epilogue, pushes, npush, T, stream);
 }

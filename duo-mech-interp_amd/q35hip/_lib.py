@@ -20,7 +20,7 @@ EXPORTS = [
     "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
     "q35_swiglu_push",
     "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm", "q35_gemm_q8", "q35_gemm_q8_split",
-    "q35_add_rmsnorm_split", "q35_gated_rmsnorm_split",
+    "q35_add_rmsnorm_split", "q35_gated_rmsnorm_split", "q35_gemm_q8_bf16",
     "q35_gdn_decode_sliced", "q35_gemv_norm_conv", "q35_gemv_gated_norm", "q35_gdn_chunk_prefill_conv",
 ]
 
@@ -68,6 +68,7 @@ _SIGS = {
     "q35_argmax_rows": ([P, I64, I64, I64, P, P, P], I32),
     "q35_gemm_q8": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
     "q35_gemm_q8_split": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
+    "q35_gemm_q8_bf16": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
     "q35_gemv_norm": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
     "q35_gdn_decode_sliced": ([P, I64, P, P, I64, I64, P, F32, P, I64, I64, I64, P], I32),
     "q35_gemv_norm_conv": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P], I32),

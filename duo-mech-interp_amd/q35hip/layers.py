@@ -164,7 +164,7 @@ def linear(x, w, wq=None, ws=None, prenorm=None, residual=None, conv=None):
         raise ValueError("linear: the conv epilogue is a decode GEMV form (at most 8 fp32 rows, K a multiple of 256)")
     if prenorm is not None:
         x = prenorm_torch(x, prenorm)
-    if wq is not None and K % 64 == 0 and x.dtype in (torch.float32, torch.int32):
+    if wq is not None and K % 64 == 0 and x.dtype in (torch.float32, torch.int32, torch.bfloat16):
         y = ops.gemm_q8(x.reshape(M, K), wq, ws, out=out, epilogue=epi)
         return residual if residual is not None else y.view(*x.shape[:-1], N)
     if x.dtype == torch.int32:
@@ -242,7 +242,10 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
         # fp32 straight from the merge kernel: the o_proj GEMV reads fp32 (no conversion kernel in the step)
         o = ops.gated_attention_decode(q[:, 0], k_cache, v_cache, gate[:, 0], cl, cos, sin,
                                        scale=1.0 / math.sqrt(D), out_dtype=torch.float32).view(B, 1, Hq * D)
-    return linear(o.float(), p["o_proj"], *_q8(p, "o_proj"), residual=residual)
+    wq_o, ws_o = _q8(p, "o_proj")
+    # bf16 o straight into the int8 GEMM (the product of o.float(), bitwise); fp32 for the other forms
+    xo = o if (T > 1 and wq_o is not None and o.shape[-1] % 64 == 0) else o.float()
+    return linear(xo, p["o_proj"], wq_o, ws_o, residual=residual)
 
 
 def residual_steer_add(x, vecs, rows=None):

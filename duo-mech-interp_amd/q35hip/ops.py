@@ -449,8 +449,8 @@ def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T):
 
 def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T):
     _on_gpu(W, w_scale, pushes)
-    _require(x.is_cuda and x.dtype in (torch.float32, torch.int32) and x.dim() == 2 and x.stride(1) == 1,
-             "x: [M, K] fp32 (or int32 words of split activations) with unit column stride")
+    _require(x.is_cuda and x.dtype in (torch.float32, torch.int32, torch.bfloat16) and x.dim() == 2
+             and x.stride(1) == 1, "x: [M, K] fp32, bf16 or int32 words of split activations, unit column stride")
     _require(y.is_cuda and y.dtype == (torch.int32 if epilogue == 3 else torch.float32) and y.dim() == 2
              and y.stride(1) == 1, "y: [M, N] fp32 (int32 words of split activations for epilogue 3)")
     _require(W.dim() == 2 and W.dtype == torch.int8, "W: [N, K] int8")
@@ -461,7 +461,7 @@ def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T):
     fmt = _weight_format(W, w_scale, N, K)
     _require(K % 64 == 0, "K must be a multiple of 64")
     npush = _pushes_check(pushes)
-    fn = "q35_gemm_q8_split" if x.dtype == torch.int32 else "q35_gemm_q8"
+    fn = {torch.int32: "q35_gemm_q8_split", torch.bfloat16: "q35_gemm_q8_bf16"}.get(x.dtype, "q35_gemm_q8")
     st = getattr(_lib.lib(), fn)(_ptr(x), x.stride(0), _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.stride(0), M, N, K,
                                  int(epilogue), _ptr(pushes), npush, int(T), _stream(x))
     check(st, fn)
@@ -851,7 +851,7 @@ def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1, split_o
     accumulates into out, "swiglu" treats W's rows as interleaved (gate, up) pairs and writes
     silu(gate) * up with the neuron pushes (pack_pushes) applied, out [M, N / 2]. x may also be the int32 words of
     activations already split (add_rmsnorm_(..., split=True), split_activations): the same product, bitwise, without
-    the split in the kernel. split_out=True (SwiGLU only) writes out as the int32 words of the split layout, the
+    the split in the kernel; or bf16 (the product of x.float(), bitwise, with the lo products skipped). split_out=True (SwiGLU only) writes out as the int32 words of the split layout, the
     input of the next gemm_q8. Returns out."""
     e = _EPI[epilogue]
     if split_out:

@@ -38,6 +38,7 @@
  *                            with the SwiGLU + push epilogue of `swiglu` (engine/kernels_qwen35.js:250-279)
  *   q35_add_rmsnorm          HF:720-734 Qwen3_5RMSNorm (1 + w) with the residual add before it (HF:753-793);
  *                            engine/kernels.js:226-246 `rmsnorm` (OFFSET) and `addInto`
+ *   q35_gemm_q8_bf16,        q35_gemm_q8 on bf16 activations (the attention output; no counterpart either)
  *   q35_gemm_q8_split,       the same on activations handed over already split into bf16 hi + lo parts (no
  *   q35_add_rmsnorm_split,   counterpart in the reference's interface: a layout between the producers and the
  *   q35_gated_rmsnorm_split  GEMM)
@@ -398,6 +399,15 @@ int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const
 int q35_gemm_q8_split(const void* xs, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
                       int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
                       int64_t npush, int64_t T, q35_stream_t stream);
+
+/*
+ * q35_gemm_q8 on bf16 x (the attention output, read without a conversion to fp32): xb [M, ldx] bf16, 16-byte
+ * aligned, ldx a multiple of 8; bitwise q35_gemm_q8 on the fp32 values of x (their hi parts are x, their lo parts
+ * zero, and only the hi products are issued). Runs on the register-staged kernel. Same reference lines.
+ */
+int q35_gemm_q8_bf16(const void* xb, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
+                     int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
+                     int64_t npush, int64_t T, q35_stream_t stream);
 
 /*
  * a[m, n] = silu(gu[m, n]) * gu[m, I + n] with the pushes applied, gu: [M, 2 I] fp32 ([gate | up] per row),

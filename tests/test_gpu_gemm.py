@@ -188,3 +188,20 @@ def test_gemm_q8_swiglu_split_output(M, N, K):
     yb = ops.gemm_q8(b, qd.to(dev), sd.to(dev))
     assert torch.equal(ya, yb)
 
+
+@pytest.mark.parametrize("M,N,K", [(6144, 1024, 2048), (70, 300, 512)])
+def test_gemm_q8_bf16_input_equals_fp32_input(M, N, K):
+    """bf16 x (the attention output) gives bitwise the product of its fp32 values, store and accumulate."""
+    dev = device()
+    q, s = _q8g(N, K, 23 + M)
+    xb = (torch.randn(M, K, generator=torch.Generator().manual_seed(M)) * 2.0).to(torch.bfloat16).to(dev)
+    announce(f"gemm_q8 bf16 input M{M} N{N} K{K}")
+    a = ops.gemm_q8(xb.float(), q.to(dev), s.to(dev))
+    b = ops.gemm_q8(xb, q.to(dev), s.to(dev))
+    base = torch.randn(M, N, generator=torch.Generator().manual_seed(2)).to(dev)
+    c, d = base.clone(), base.clone()
+    ops.gemm_q8(xb.float(), q.to(dev), s.to(dev), out=c, epilogue="add")
+    ops.gemm_q8(xb, q.to(dev), s.to(dev), out=d, epilogue="add")
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(c, d)
+
