@@ -83,6 +83,16 @@ __device__ __forceinline__ void gemm_store_act(float* p, int n, float a, int ys)
   }
 }
 
+// SwiGLU activation capture (p may be NULL): the activation of neuron n of global row m goes to
+// p[(m / T) ldcr + (m % T) ldc + n], fp32, whatever the layout of y
+struct GemmCap {
+  float* p;
+  int64_t ldc, ldcr;
+};
+__device__ __forceinline__ void gemm_capture(const GemmCap& c, int m, int T, int n, float a) {
+  if (c.p) c.p[(int64_t)(m / T) * c.ldcr + (int64_t)(m % T) * c.ldc + n] = a;
+}
+
 __device__ __forceinline__ float gemm_push(const q35_push* ps, int n, int row, float a) {
   const int pn = ps->neuron;
   if (pn != n && pn >= 0) return a;
@@ -149,7 +159,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
                                                              const float* __restrict__ ws, float* __restrict__ Y,
                                                              int64_t ldy, int M, int N, int K,
                                                              const q35_push* __restrict__ pushes, int npush, int T,
-                                                             int moff, int ys) {
+                                                             int moff, int ys, GemmCap cap) {
   __shared__ __attribute__((aligned(16))) char smem[kDNS * kDSB];
   __shared__ __attribute__((aligned(16))) char xc[XS ? 1 : 2][2][XS ? 16 : kDXC];  // [buffer][hi, lo] (fp32 x)
   __shared__ float gscale[GS ? kDGS * kDBN : 1];
@@ -377,6 +387,7 @@ __global__ __launch_bounds__(512, 1) void gemm_q8_dma_kernel(const float* __rest
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
             }
             gemm_store_act(ytn + roff[r], neuron, a, ys);
+            gemm_capture(cap, moff + m, T, neuron, a);
           }
         } else if (m < M && n < N) {
           float* dst = ytn + roff[r];
@@ -398,7 +409,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
                                                          const int8_t* __restrict__ W, const float* __restrict__ ws,
                                                          float* __restrict__ Y, int64_t ldy, int M, int N, int K,
                                                          const q35_push* __restrict__ pushes, int npush, int T,
-                                                         int moff, int ys) {
+                                                         int moff, int ys, GemmCap cap) {
   static_assert(BM == 64 || BM == 128, "rows per block");
   constexpr int MT = BM / 64;         // 32-row MFMA tiles per wave along M (a wave covers BM / 2 rows)
   constexpr int TPR = 256 / BM;       // threads per staged row of x
@@ -551,6 +562,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_rs_kernel(const float* __restr
               for (int p = 0; p < npush; ++p) a = gemm_push(pushes + p, neuron, row, a);
             }
             gemm_store_act(ytn + roff[r], neuron, a, ys);
+            gemm_capture(cap, moff + m, T, neuron, a);
           }
         } else if (m < M && n < N) {
           float* dst = ytn + roff[r];
@@ -568,7 +580,7 @@ namespace q35 {
 template <int XF>
 static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
                           int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes, int64_t npush,
-                          int64_t T, int64_t moff, int ys, hipStream_t st) {
+                          int64_t T, int64_t moff, int ys, const GemmCap& cap, hipStream_t st) {
   const int64_t nbn = (N + kGN - 1) / kGN;
   // 128-row tiles when they still give at least two blocks per compute unit, else 64-row tiles
   const bool big = ((M + 127) / 128) * nbn >= 512;
@@ -577,7 +589,7 @@ static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const fl
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
 #define Q35_GEMM_LAUNCH(BMV, E, G)                                                                                   \
   hipLaunchKernelGGL((gemm_q8_rs_kernel<BMV, E, G, XF>), dim3((unsigned)nblocks), dim3(256), 0, st, x, ldx, W,       \
-                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, (int)moff, ys)
+                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, (int)moff, ys, cap)
 #define Q35_GEMM_EPI(BMV, G)                                              \
   if (epilogue == kGemmStore) Q35_GEMM_LAUNCH(BMV, kGemmStore, G);        \
   else if (epilogue == kGemmAccumulate) Q35_GEMM_LAUNCH(BMV, kGemmAccumulate, G); \
@@ -595,13 +607,13 @@ static int gemm_rs_launch(const float* x, int64_t ldx, const int8_t* W, const fl
 template <bool XS>
 static int gemm_dma_launch(const float* x, int64_t ldx, const int8_t* W, const float* w_scale, float* y, int64_t ldy,
                            int64_t M, int64_t N, int64_t K, int epilogue, bool gs, const q35_push* pushes,
-                           int64_t npush, int64_t T, int ys, hipStream_t st) {
+                           int64_t npush, int64_t T, int ys, const GemmCap& cap, hipStream_t st) {
   const int moff = 0;
   const int64_t nblocks = ((M + kDBM - 1) / kDBM) * ((N + kDBN - 1) / kDBN);
   if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
 #define Q35_GEMM_DMA(E, G_)                                                                                       \
   hipLaunchKernelGGL((gemm_q8_dma_kernel<E, G_, XS>), dim3((unsigned)nblocks), dim3(512), 0, st, x, ldx, W,        \
-                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, moff, ys)
+                     w_scale, y, ldy, (int)M, (int)N, (int)K, pushes, (int)npush, (int)T, moff, ys, cap)
   if (gs) {
     if (epilogue == kGemmStore) Q35_GEMM_DMA(kGemmStore, true);
     else if (epilogue == kGemmAccumulate) Q35_GEMM_DMA(kGemmAccumulate, true);
@@ -632,8 +644,12 @@ namespace q35 {
 template <bool XS, bool XB = false>
 static int gemm_q8_run(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
                        int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
-                       int64_t npush, int64_t T, q35_stream_t stream) {
+                       int64_t npush, int64_t T, float* cap_p, int64_t ld_cap, int64_t ld_cap_row,
+                       q35_stream_t stream) {
   if (!x || !W || !w_scale || !y || M <= 0 || N <= 0 || K <= 0 || T <= 0) return Q35_EINVAL;
+  if (cap_p && (epilogue < kGemmSwiglu || ld_cap < N / 2 || ld_cap_row < N / 2 || ((uintptr_t)cap_p & 3)))
+    return Q35_EINVAL;
+  const GemmCap cap = {cap_p, ld_cap, ld_cap_row};
   if (w_dtype != Q35_I8 && w_dtype != Q35_I8_G128) return Q35_EUNSUPPORTED;
   const bool gs = w_dtype == Q35_I8_G128;
   if (gs && K % 128 != 0) return Q35_EUNSUPPORTED;
@@ -652,7 +668,7 @@ static int gemm_q8_run(const float* x, int64_t ldx, const int8_t* W, int w_dtype
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // bf16 x: the register-staged kernel (one product per tile: the lo parts are zero)
   if constexpr (XB)
-    return gemm_rs_launch<2>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, ys, st);
+    return gemm_rs_launch<2>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, ys, cap, st);
   // wide products with K <= 2048 (and x, W addressable with 32-bit byte offsets): the DMA kernel
   if (N >= 2048 && K <= 128 * kDGS && ((M - 1) * ldx + K) * 4 <= 0xffffffffLL && N * K <= 0xffffffffLL) {
     // One block per CU, so a last round of blocks that is mostly empty costs as much as a full one. A partial last
@@ -675,39 +691,44 @@ static int gemm_q8_run(const float* x, int64_t ldx, const int8_t* W, int w_dtype
         if (M1 > 0 && M1 < M) Md = M1;
       }
     }
-    int r = gemm_dma_launch<XS>(x, ldx, W, w_scale, y, ldy, Md, Nd, K, epilogue, gs, pushes, npush, T, ys, st);
+    int r = gemm_dma_launch<XS>(x, ldx, W, w_scale, y, ldy, Md, Nd, K, epilogue, gs, pushes, npush, T, ys, cap, st);
     if (r != Q35_OK) return r;
     if (Md < M) {
       r = gemm_rs_launch<(XS ? 1 : 0)>(x + Md * ldx, ldx, W, w_scale, y + Md * ldy, ldy, M - Md, Nd, K, epilogue, gs,
-                                       pushes, npush, T, Md, ys, st);
+                                       pushes, npush, T, Md, ys, cap, st);
       if (r != Q35_OK) return r;
     }
     if (Nd < N)
       r = gemm_rs_launch<(XS ? 1 : 0)>(x, ldx, W + Nd * K, w_scale + (gs ? Nd * (K / 128) : Nd), y + Nd, ldy, M,
-                                       N - Nd, K, epilogue, gs, pushes, npush, T, 0, ys, st);
+                                       N - Nd, K, epilogue, gs, pushes, npush, T, 0, ys, cap, st);
     return r;
   }
-  return gemm_rs_launch<(XS ? 1 : 0)>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, ys, st);
+  return gemm_rs_launch<(XS ? 1 : 0)>(x, ldx, W, w_scale, y, ldy, M, N, K, epilogue, gs, pushes, npush, T, 0, ys, cap,
+                                      st);
 }
 
 }  // namespace q35
 
 extern "C" int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
                            float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
-                           const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
-  return q35::gemm_q8_run<false>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T, stream);
+                           const q35_push* pushes, int64_t npush, int64_t T, float* cap, int64_t ld_cap,
+                           int64_t ld_cap_row, q35_stream_t stream) {
+  return q35::gemm_q8_run<false>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T, cap, ld_cap,
+                                 ld_cap_row, stream);
 }
 
 extern "C" int q35_gemm_q8_split(const void* xs, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
                                  float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
-                                 const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
+                                 const q35_push* pushes, int64_t npush, int64_t T, float* cap, int64_t ld_cap,
+                                 int64_t ld_cap_row, q35_stream_t stream) {
   return q35::gemm_q8_run<true>(static_cast<const float*>(xs), ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue,
-                                pushes, npush, T, stream);
+                                pushes, npush, T, cap, ld_cap, ld_cap_row, stream);
 }
 
 extern "C" int q35_gemm_q8_bf16(const void* xb, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale,
                                 float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue,
-                                const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream) {
+                                const q35_push* pushes, int64_t npush, int64_t T, float* cap, int64_t ld_cap,
+                                int64_t ld_cap_row, q35_stream_t stream) {
   return q35::gemm_q8_run<false, true>(static_cast<const float*>(xb), ldx, W, w_dtype, w_scale, y, ldy, M, N, K,
-                                       epilogue, pushes, npush, T, stream);
+                                       epilogue, pushes, npush, T, cap, ld_cap, ld_cap_row, stream);
 }

@@ -42,6 +42,8 @@ struct GemvAux {
   const float* cb;   // conv: bias [cc] (may be NULL)
   float* cst;        // conv: state [M][ck - 1][cc]
   int cc, ck;        // conv: channels (outputs 0 .. cc - 1 are convolved), taps
+  float* cap;        // SwiGLU: activation capture (may be NULL): row m, neuron n at
+  int64_t ldc, ldcr; //   cap[(m / T) ldcr + (m % T) ldc + n]
 };
 
 __device__ __forceinline__ float gsilu(float x) { return silu_f(x); }
@@ -390,6 +392,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
           const int row = min(m / T, 3);
           for (int p = 0; p < npush; ++p) a = apply_push(pushes + p, neuron, row, a);
           y[m * ldy + neuron] = a;
+          if (aux.cap) aux.cap[(int64_t)(m / T) * aux.ldcr + (int64_t)(m % T) * aux.ldc + neuron] = a;
         }
       }
     }
@@ -475,7 +478,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
 // a[m, n] = silu(gu[m, n]) * gu[m, I + n] with the pushes applied (the prefill form over a [gate | up] projection)
 __global__ __launch_bounds__(256) void swiglu_push_kernel(const float* __restrict__ gu, float* __restrict__ a,
                                                           int64_t M, int I, const q35_push* __restrict__ pushes,
-                                                          int npush, int T) {
+                                                          int npush, int T, float* __restrict__ cap, int64_t ldc,
+                                                          int64_t ldcr) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= M * I) return;
   const int64_t m = i / I;
@@ -484,6 +488,7 @@ __global__ __launch_bounds__(256) void swiglu_push_kernel(const float* __restric
   const int row = (int)min(m / T, (int64_t)3);
   for (int p = 0; p < npush; ++p) v = apply_push(pushes + p, n, row, v);
   a[i] = v;
+  if (cap) cap[(m / T) * ldcr + (m % T) * ldc + n] = v;
 }
 
 }  // namespace q35
@@ -601,9 +606,11 @@ int gemv_dispatch(const float* x, int64_t ldx, const void* W, int w_dtype, const
 
 // argument checks shared by the two entry points
 int gemv_check(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
-               int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T) {
+               int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T,
+               const float* cap = nullptr, int64_t ldc = 0, int64_t ldcr = 0) {
   using namespace q35;
   if (!x || !W || !y || M <= 0 || N <= 0 || K <= 0 || ldx < K || T <= 0) return Q35_EINVAL;
+  if (cap && (epilogue != kEpiSwiglu || ldc < N / 2 || ldcr < N / 2 || ((uintptr_t)cap & 3))) return Q35_EINVAL;
   if (w_dtype == Q35_I8_G128 && !w_scale) return Q35_EINVAL;
   if (npush < 0 || (npush > 0 && !pushes)) return Q35_EINVAL;
   if (epilogue == kEpiSwiglu ? (N & 1) || ldy < N / 2 : ldy < N) return Q35_EINVAL;
@@ -618,10 +625,15 @@ int gemv_check(const float* x, int64_t ldx, const void* W, int w_dtype, const fl
 
 extern "C" int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y,
                         int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
-                        int64_t npush, int64_t T, q35_stream_t stream) {
-  const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T);
+                        int64_t npush, int64_t T, float* cap, int64_t ld_cap, int64_t ld_cap_row,
+                        q35_stream_t stream) {
+  const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T, cap, ld_cap,
+                             ld_cap_row);
   if (chk != Q35_OK) return chk;
-  const NormArgs na = {nullptr, nullptr, 0.f, nullptr, {}};
+  NormArgs na = {nullptr, nullptr, 0.f, nullptr, {}};
+  na.aux.cap = cap;
+  na.aux.ldc = ld_cap;
+  na.aux.ldcr = ld_cap_row;
   return gemv_dispatch<false>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, (int)npush, T, na,
                               reinterpret_cast<hipStream_t>(stream));
 }
@@ -629,8 +641,9 @@ extern "C" int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype,
 extern "C" int q35_gemv_norm(const float* x, const float* x_add, float* x_out, int64_t ldx, const float* norm_w,
                              float eps, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
                              int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush,
-                             int64_t T, q35_stream_t stream) {
-  const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T);
+                             int64_t T, float* cap, int64_t ld_cap, int64_t ld_cap_row, q35_stream_t stream) {
+  const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, npush, T, cap, ld_cap,
+                             ld_cap_row);
   if (chk != Q35_OK) return chk;
   if (!norm_w) return Q35_EINVAL;
   if (((uintptr_t)norm_w & 15) || (x_add && ((uintptr_t)x_add & 15)) || (x_out && ((uintptr_t)x_out & 15)))
@@ -640,7 +653,10 @@ extern "C" int q35_gemv_norm(const float* x, const float* x_add, float* x_out, i
     return a && x_out && a < x_out + (M - 1) * ldx + K && x_out < a + (M - 1) * ldx + K;
   };
   if (overlap(x) || overlap(x_add)) return Q35_EINVAL;
-  const NormArgs na = {x_add, norm_w, eps, x_out, {}};
+  NormArgs na = {x_add, norm_w, eps, x_out, {}};
+  na.aux.cap = cap;
+  na.aux.ldc = ld_cap;
+  na.aux.ldcr = ld_cap_row;
   return gemv_dispatch<true>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, (int)npush, T, na,
                              reinterpret_cast<hipStream_t>(stream));
 }
@@ -710,13 +726,15 @@ extern "C" int q35_gemv_gated_norm(const float* o, int64_t ldo, const float* z, 
 }
 
 extern "C" int q35_swiglu_push(const float* gu, float* a, int64_t M, int64_t I, const q35_push* pushes,
-                               int64_t npush, int64_t T, q35_stream_t stream) {
+                               int64_t npush, int64_t T, float* cap, int64_t ld_cap, int64_t ld_cap_row,
+                               q35_stream_t stream) {
   using namespace q35;
   if (!gu || !a || M <= 0 || I <= 0 || T <= 0 || npush < 0 || (npush > 0 && !pushes)) return Q35_EINVAL;
+  if (cap && (ld_cap < I || ld_cap_row < I || ((uintptr_t)cap & 3))) return Q35_EINVAL;
   if (M * I > ((int64_t)1 << 40) || (M * I + 255) / 256 > 0x7fffffff || npush > 64 || I > 0x7fffffff)
     return Q35_EUNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(swiglu_push_kernel, dim3((unsigned)((M * I + 255) / 256)), dim3(256), 0, st, gu, a, M, (int)I,
-                     pushes, (int)npush, (int)T);
+                     pushes, (int)npush, (int)T, cap, ld_cap, ld_cap_row);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }

@@ -26,7 +26,7 @@ EXPORTS = [
 
 Q35_F32, Q35_BF16, Q35_I8, Q35_I8_G128 = 0, 1, 2, 3
 Q35_ESCRATCH = 5
-ABI_VERSION = 10  # the signatures below; q35_abi_version() of the loaded library must match
+ABI_VERSION = 11  # the signatures below; q35_abi_version() of the loaded library must match
 
 _lib = None
 
@@ -61,15 +61,16 @@ _SIGS = {
     "q35_gdn_decode_fused": ([P, I64, P, P, P, P, P, I64, I64, I64, P, P, P, F32, F32, P, I64, I64, I64, I64, P],
                              I32),
     "q35_attn_prep": ([P, I64, P, P, F32, P, P, I64, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P], I32),
-    "q35_gemv": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
-    "q35_swiglu_push": ([P, P, I64, I64, P, I64, I64, P], I32),
+    "q35_gemv": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P, I64, I64, P], I32),
+    "q35_swiglu_push": ([P, P, I64, I64, P, I64, I64, P, I64, I64, P], I32),
     "q35_add_rmsnorm": ([P, I64, P, I64, P, P, I64, I64, I64, F32, P], I32),
     "q35_add_rmsnorm_split": ([P, I64, P, I64, P, P, I64, I64, I64, F32, P], I32),
     "q35_argmax_rows": ([P, I64, I64, I64, P, P, P], I32),
-    "q35_gemm_q8": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
-    "q35_gemm_q8_split": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
-    "q35_gemm_q8_bf16": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
-    "q35_gemv_norm": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P], I32),
+    "q35_gemm_q8": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P, I64, I64, P], I32),
+    "q35_gemm_q8_split": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P, I64, I64, P], I32),
+    "q35_gemm_q8_bf16": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P, I64, I64, P], I32),
+    "q35_gemv_norm": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P, I64, I64, P],
+                      I32),
     "q35_gdn_decode_sliced": ([P, I64, P, P, I64, I64, P, F32, P, I64, I64, I64, P], I32),
     "q35_gemv_norm_conv": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P], I32),
     "q35_gemv_gated_norm": ([P, I64, P, I64, P, P, F32, P, I32, P, P, I64, I64, I64, I64, I32, P], I32),

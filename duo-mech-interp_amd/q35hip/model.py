@@ -63,7 +63,7 @@ def _split_ok(p, names, x):
     return x.shape[-1] % 64 == 0 and all(n + ".q" in p for n in names)
 
 
-def mlp(p, h, x, prenorm=None):
+def mlp(p, h, x, prenorm=None, capture=None):
     """x += SwiGLU MLP (HF:704-717) of h, in place, with the layer's neuron pushes at the down_proj input
     (engine/model.js:7-9, engine/kernels_qwen35.js:250-279). Decode (at most 8 rows, int8 weights present): one GEMV
     over the interleaved int8 gate/up rows with the SwiGLU + push epilogue, and one int8 GEMV accumulating down_proj
@@ -72,7 +72,9 @@ def mlp(p, h, x, prenorm=None):
     SwiGLU push kernel and a down_proj GEMM. prenorm = (y_add, norm_w, eps): h is then the residual; x receives
     h + y_add and the MLP reads the RMSNorm (1 + norm_w) of that sum (the layer's second add + norm, fused into the
     first GEMV on the decode path). h may be the int32 words of split activations (add_rmsnorm_(..., split=True)) when
-    the layer has int8 weights: the gate/up GEMM reads them as they are. Returns x."""
+    the layer has int8 weights: the gate/up GEMM reads them as they are. capture: an fp32 view [rows, T, I] (unit
+    neuron stride) that receives the post-push activations, the down_proj input (the engine's capture hook,
+    engine/model.js:9, :451-453), written by the SwiGLU epilogue itself. Returns x."""
     mlp_weights(p)
     H = h.shape[-1]
     M = h.numel() // H
@@ -84,7 +86,7 @@ def mlp(p, h, x, prenorm=None):
         pn2 = None if pn is None else (None if pn[0] is None else pn[0].reshape(M, H), pn[1], pn[2],
                                        None if pn[3] is None else x.view(M, H))
         a = ops.gemv(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T,
-                     prenorm=pn2)
+                     prenorm=pn2, capture=capture)
         ops.gemv(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H), epilogue="add")
         return x
     if pn is not None:
@@ -93,12 +95,12 @@ def mlp(p, h, x, prenorm=None):
         # int8 GEMMs: [gate | up] interleaved with the SwiGLU + push epilogue (its output already split for the next
         # product), then down_proj accumulating into x
         a = ops.gemm_q8(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T,
-                        split_out=p["_gu_q8"].shape[0] % 16 == 0)
+                        split_out=p["_gu_q8"].shape[0] % 16 == 0, capture=capture)
         ops.gemm_q8(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H), epilogue="add")
         return x
     if h.dtype == torch.int32:
         raise ValueError("mlp: split activations need the int8 GEMM (int8 weights, H a multiple of 64)")
-    a = ops.swiglu_push(h @ p["_gu"].T, p["_pushes"], T=T)
+    a = ops.swiglu_push(h @ p["_gu"].T, p["_pushes"], T=T, capture=capture)
     x.view(M, H).addmm_(a.view(M, -1), p["down_proj"].T)
     return x
 
@@ -139,6 +141,8 @@ class HybridModel:
                 layers.attn_in_weight(p)
             else:
                 layers.gdn_in_weight(p)
+                # the engine's per-head output scale (engine/model.js:362-368): 1 for every head until set
+                p["_head_scale"] = torch.ones(cfg.lin_v_heads, device=device)
             mlp_weights(p)
         self.states = []
         for l in range(cfg.layers):
@@ -155,6 +159,7 @@ class HybridModel:
         self._pos_len = torch.zeros(2, rows, dtype=torch.int32, device=device)
         self.pos_dev, self.len_dev = self._pos_len[0], self._pos_len[1]
         self.graph = None
+        self.step_capture, self._step_cap_idx = None, {}
         self.row_pos = [0] * rows  # host mirror of pos_dev
         self.reset()
 
@@ -190,6 +195,25 @@ class HybridModel:
         self.vec_rows.copy_(torch.as_tensor(vec_of_row, dtype=torch.int32))
         self.steering = True
 
+    def set_head_scales(self, scales):
+        """Per-head output scales of the Gated DeltaNet layers, {layer: [Hv] values} (the engine's `heads` ablation
+        hook, engine/model.js:10, :362-368): applied after the gated norm (engine/kernels_qwen35.js:243); heads of
+        layers not named (or scales None) get 1. Written into fixed per-layer buffers, so a captured decode step picks
+        them up."""
+        for l, p in enumerate(self.params):
+            if "_head_scale" not in p:
+                if scales and l in scales:
+                    raise ValueError(f"HybridModel: layer {l} is not a Gated DeltaNet layer")
+                continue
+            s = scales.get(l) if scales else None
+            if s is None:
+                p["_head_scale"].fill_(1.0)
+            else:
+                s = torch.as_tensor(s, dtype=torch.float32).reshape(-1)
+                if s.numel() != p["_head_scale"].numel():
+                    raise ValueError(f"HybridModel: layer {l} takes {p['_head_scale'].numel()} head scales")
+                p["_head_scale"].copy_(s)
+
     def set_pushes(self, pushes):
         """Neuron pushes per layer, {layer: [(neuron or None for every neuron, "add" | "mul", [value per row])]}, at
         most 8 per layer (engine/model.js:412-423); layers not named have none. Written into fixed per-layer buffers,
@@ -203,7 +227,7 @@ class HybridModel:
                 buf[:len(recs)] = ops.pack_pushes(recs, "cpu")
             p["_pushes"].copy_(buf)
 
-    def _layers(self, x, T, last, collect_layer, steer, rs=slice(None), attn_pos=None):
+    def _layers(self, x, T, last, collect_layer, steer, rs=slice(None), attn_pos=None, hooks=None):
         """The decoder layers 0..last over the residual stream x [n, T, H] (dense fp32) of the rows rs; returns (the
         residual after layer `last`, the residual after collect_layer or None) (HF:753-793; engine/model.js:436-462).
         attn_pos: the attention layers' position argument for T > 1 (0 when every row starts its sequence: the
@@ -213,9 +237,26 @@ class HybridModel:
         kernel and its MLP output in the MLP's last product. Decode (T == 1): x is updated in place by the GEMVs:
         the mixer's input projection and the MLP's first GEMV normalise the residual in their prologue
         (q35_gemv_norm), and the mixer's output projection and down_proj accumulate into it (split over K, so that
-        these N = hidden products draw bandwidth from every CU)."""
+        these N = hidden products draw bandwidth from every CU).
+
+        hooks (the engine's forward options, engine/model.js:9-11, :446-461): "cap" = (buffer [nL, n, capT, I],
+        {layer: index}, t0): the MLP activations of the listed layers written by the SwiGLU epilogues at tokens
+        t0 .. t0 + T - 1; "resid" = (buffer [last + 1, n, capT, H], mode, t0): the residual after every layer
+        (mode "layer", after the steering add) or after the mixer's residual add (mode "mixer", the engine's
+        resid "attn")."""
         cfg = self.cfg
         collected = None
+        hooks = hooks or {}
+        cap_buf, cap_idx, cap_t0 = hooks.get("cap", (None, {}, 0))
+        res_buf, res_mode, res_t0 = hooks.get("resid", (None, "layer", 0))
+
+        def cap_view(l):
+            i = cap_idx.get(l)
+            return None if i is None else cap_buf[i, :, cap_t0:cap_t0 + T]
+
+        def snap(l, mode):
+            if res_buf is not None and res_mode == mode:
+                res_buf[l, :, res_t0:res_t0 + T].copy_(x.view(res_buf.shape[1], T, -1))
         pos_dev, vec_rows = self.pos_dev[rs], self.vec_rows[rs]
         if T == 1:
             cache_len = self.len_dev[rs]  # shared by the attention layers
@@ -228,12 +269,14 @@ class HybridModel:
                                                  partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps,
                                                  cache_len=cache_len, prenorm=pre, residual=x)
                 else:
-                    layers.gated_deltanet_layer(x, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
-                                                head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill,
-                                                prenorm=pre, residual=x)
-                mlp(p, x, x, prenorm=(None, p["post_attention_layernorm"], cfg.eps))
+                    layers.gated_deltanet_layer(x, p, st["conv"], st["rec"], p["_head_scale"],
+                                                num_k_heads=cfg.lin_k_heads, head_k_dim=cfg.lin_dk, eps=cfg.eps,
+                                                prefill=self.gdn_prefill, prenorm=pre, residual=x)
+                snap(l, "mixer")
+                mlp(p, x, x, prenorm=(None, p["post_attention_layernorm"], cfg.eps), capture=cap_view(l))
                 if l == self.steer_layer and steer:
                     layers.residual_steer_add(x, self.vec_buf, vec_rows)
+                snap(l, "layer")
                 if l == collect_layer:
                     collected = x.clone()
             return x, collected
@@ -248,23 +291,34 @@ class HybridModel:
                 y = layers.gated_attention_layer(h, p, st["k"], st["v"], attn_pos, rope_theta=cfg.rope_theta,
                                                  partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps)
             else:
-                y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], num_k_heads=cfg.lin_k_heads,
-                                                head_k_dim=cfg.lin_dk, eps=cfg.eps, prefill=self.gdn_prefill)
+                y = layers.gated_deltanet_layer(h, p, st["conv"], st["rec"], p["_head_scale"],
+                                                num_k_heads=cfg.lin_k_heads, head_k_dim=cfg.lin_dk, eps=cfg.eps,
+                                                prefill=self.gdn_prefill)
             h = ops.add_rmsnorm_(x, y, p["post_attention_layernorm"], cfg.eps, split=_split_ok(p, _MLP_IN, x))
             y = None
-            mlp(p, h, x)
+            snap(l, "mixer")
+            mlp(p, h, x, capture=cap_view(l))
             if l == self.steer_layer and steer:
                 layers.residual_steer_add(x, self.vec_buf, vec_rows)
+            snap(l, "layer")
             if l == collect_layer:
                 collected = x.clone()
         return x, collected
 
     @torch.no_grad()
-    def forward(self, ids, stop_after=None, collect_layer=None, row=None):
+    def forward(self, ids, stop_after=None, collect_layer=None, row=None, *, capture=None, capture_layers=None,
+                resid=None, resid_mode="layer", t0=0):
         """ids: [rows, T] token ids continuing every row's sequence, or with row=r [1, T] (or [T]) continuing row r
         only (its states and position; the other rows are untouched). A multi-token call may start anywhere: past
         position 0 its attention runs over the KV cache. Returns (last-position logits [n, V] or None with
-        stop_after, residual after collect_layer or None) for the rows called."""
+        stop_after, residual after collect_layer or None) for the rows called.
+
+        The engine's forward hooks (engine/model.js:9-11, :446-461; device buffers owned by the caller, n = rows
+        called, capT >= t0 + T, so a prompt given in several calls fills one buffer through t0, as the engine's capT0):
+          capture  fp32 [len(capture_layers), n, capT, I]: the MLP activations (the down_proj input, after the
+                   pushes) of every token, written by the SwiGLU epilogues; capture_layers defaults to every layer
+          resid    fp32 [layers run, n, capT, H]: the residual stream after each layer (resid_mode "layer", after
+                   the steering add) or after each mixer's residual add (resid_mode "mixer", the engine's "attn")"""
         cfg, W = self.cfg, self.W
         if row is None:
             rs, rows = slice(None), list(range(self.rows))
@@ -279,13 +333,38 @@ class HybridModel:
         attn_pos = 0 if all(self.row_pos[r] == 0 for r in rows) else self.pos_dev[rs]
         x = W["embed"][ids.to(self.device).long()].contiguous()
         last = cfg.layers - 1 if stop_after is None else stop_after
-        x, collected = self._layers(x, T, last, collect_layer, self.steering, rs, attn_pos)
+        hooks = self._hooks(len(rows), T, last, capture, capture_layers, resid, resid_mode, t0)
+        x, collected = self._layers(x, T, last, collect_layer, self.steering, rs, attn_pos, hooks)
         self._pos_len[:, rs].add_(T)
         for r in rows:
             self.row_pos[r] += T
         if stop_after is not None:
             return None, collected
         return self._lm_head(x[:, -1]), collected
+
+    def _hooks(self, n, T, last, capture, capture_layers, resid, resid_mode, t0):
+        """Validated hook buffers of a forward call (see forward)."""
+        cfg, hooks = self.cfg, {}
+        if capture is not None:
+            lays = list(range(cfg.layers)) if capture_layers is None else [int(l) for l in capture_layers]
+            if any(not 0 <= l < cfg.layers for l in lays) or len(set(lays)) != len(lays):
+                raise ValueError("HybridModel: capture_layers must be distinct layer indices")
+            if (capture.dtype != torch.float32 or capture.device != self.device or capture.dim() != 4
+                    or tuple(capture.shape[:2]) != (len(lays), n) or capture.shape[3] != cfg.inter
+                    or not 0 <= t0 <= capture.shape[2] - T or capture.stride(3) != 1):
+                raise ValueError(f"HybridModel: capture must be fp32 [{len(lays)}, {n}, >= t0 + {T}, {cfg.inter}] "
+                                 "on the model's device")
+            hooks["cap"] = (capture, {l: i for i, l in enumerate(lays)}, int(t0))
+        if resid is not None:
+            if resid_mode not in ("layer", "mixer"):
+                raise ValueError(f"HybridModel: resid_mode must be 'layer' or 'mixer', not {resid_mode!r}")
+            if (resid.dtype != torch.float32 or resid.device != self.device or resid.dim() != 4
+                    or resid.shape[0] < last + 1 or resid.shape[1] != n or resid.shape[3] != cfg.hidden
+                    or not 0 <= t0 <= resid.shape[2] - T):
+                raise ValueError(f"HybridModel: resid must be fp32 [>= {last + 1}, {n}, >= t0 + {T}, {cfg.hidden}] "
+                                 "on the model's device")
+            hooks["resid"] = (resid, resid_mode, int(t0))
+        return hooks
 
     def _lm_head(self, xl):
         """Final RMSNorm and the tied-embedding logits of the last positions xl [rows, H] (a GEMV for few rows)."""
@@ -294,20 +373,39 @@ class HybridModel:
         return layers.linear(xl.contiguous(), self.W[head], wq, None if wq is None else self.W[head + ".s"],
                              prenorm=(None, self.W["norm"], self.cfg.eps, None))
 
+    def set_step_capture(self, capture_layers):
+        """Capture the MLP activations of `capture_layers` (None: stop) at every decode step (decode_step,
+        decode_greedy, graph or eager) into self.step_capture [len(layers), rows, 1, I] fp32, overwritten by each step.
+        Call before enable_decode_graph(): the graph records the buffer it finds."""
+        if capture_layers is None:
+            self.step_capture, self._step_cap_idx = None, {}
+            return
+        lays = [int(l) for l in capture_layers]
+        if any(not 0 <= l < self.cfg.layers for l in lays) or len(set(lays)) != len(lays):
+            raise ValueError("HybridModel: capture_layers must be distinct layer indices")
+        self.step_capture = torch.zeros(len(lays), self.rows, 1, self.cfg.inter, device=self.device)
+        self._step_cap_idx = {l: i for i, l in enumerate(lays)}
+
+    def _step_hooks(self):
+        cap = self.step_capture
+        return {} if cap is None else {"cap": (cap, self._step_cap_idx, 0)}
+
     @torch.no_grad()
     def enable_decode_graph(self):
         """Capture one decode step in a HIP graph: ids [rows] int32 (self._g_ids) -> logits, then the device argmax of
         the logits written back into self._g_ids, so that replaying the graph again continues greedy decoding with no
         host work (the engine's decode loop, engine/model.js:494-497). decode_step() and decode_greedy() replay it.
         Must be called at the start of a sequence: the warm-up runs real steps, and the states are reset afterwards.
-        The steering add is always part of the graph (rows without a vector are skipped by the kernel)."""
+        The steering add is always part of the graph (rows without a vector are skipped by the kernel), and so are the
+        neuron pushes, the head scales and the step capture (set_step_capture) in their fixed buffers."""
         cfg = self.cfg
         self.reset()
         self._g_ids = torch.zeros(self.rows, dtype=torch.int32, device=self.device)
+        hooks = self._step_hooks()
 
         def step():
             x, _ = self._layers(self.W["embed"].index_select(0, self._g_ids).unsqueeze(1), 1, cfg.layers - 1, None,
-                                True)
+                                True, hooks=hooks)
             self._pos_len.add_(1)
             logits = self._lm_head(x[:, -1])
             ops.argmax_rows(logits, out=self._g_ids)
@@ -333,7 +431,9 @@ class HybridModel:
         logits then live in the graph's output buffer, overwritten by the next step), else runs forward."""
         ids = ids.reshape(self.rows)
         if self.graph is None:
-            return self.forward(ids.reshape(self.rows, 1))[0]
+            cap = self.step_capture
+            lays = None if cap is None else sorted(self._step_cap_idx, key=self._step_cap_idx.get)
+            return self.forward(ids.reshape(self.rows, 1), capture=cap, capture_layers=lays)[0]
         if self.pos + 1 > self.max_len:
             raise ValueError("context exceeds the KV cache")
         self._g_ids.copy_(ids)

@@ -73,14 +73,16 @@ _LIB.define("gated_rmsnorm_split(Tensor o, Tensor z, Tensor w, Tensor? head_scal
 _LIB.define("gdn_decode_fused_(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
             "Tensor dt_bias, int b_off, int a_off, int z_off, Tensor(b!) state, Tensor norm_w, Tensor? head_scale, "
             "float eps, float scale) -> Tensor")
-_LIB.define("gemv_(Tensor x, Tensor W, Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
-_LIB.define("swiglu_push(Tensor gu, Tensor? pushes, int T) -> Tensor")
-_LIB.define("gemm_q8_(Tensor x, Tensor W, Tensor w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
+_LIB.define("gemv_(Tensor x, Tensor W, Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T, "
+            "Tensor(b!)? cap=None) -> ()")
+_LIB.define("swiglu_push(Tensor gu, Tensor? pushes, int T, Tensor(a!)? cap=None) -> Tensor")
+_LIB.define("gemm_q8_(Tensor x, Tensor W, Tensor w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T, "
+            "Tensor(b!)? cap=None) -> ()")
 _LIB.define("add_rmsnorm_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tensor")
 _LIB.define("add_rmsnorm_split_(Tensor(a!) x, Tensor? y, Tensor w, float eps) -> Tensor")
 _LIB.define("argmax_rows_(Tensor x, Tensor(a!) idx) -> ()")
 _LIB.define("gemv_norm_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
-            "Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T) -> ()")
+            "Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T, Tensor(c!)? cap=None) -> ()")
 _LIB.define("gdn_chunk_prefill_conv_(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
             "Tensor dt_bias, int b_off, int a_off, Tensor(b!) state, int Hk, float scale) -> Tensor")
 _LIB.define("gdn_decode_sliced_(Tensor y, Tensor A_log, Tensor dt_bias, int b_off, int a_off, Tensor(a!) state, "
@@ -414,6 +416,21 @@ def _pushes_check(pushes):
     return pushes.shape[0]
 
 
+def _cap_args(cap, M, T, I, device):
+    """(pointer, ld_cap, ld_cap_row) of a capture destination: a view [R, T, I] (R * T = M rows; any row and token
+    strides, unit neuron stride) or [M, I] (unit neuron stride) fp32 on the product's device; None -> no capture."""
+    if cap is None:
+        return None, 0, 0
+    _require(cap.is_cuda and cap.device == device and cap.dtype == torch.float32 and cap.stride(-1) == 1,
+             "capture: fp32 view on the product's device with unit neuron stride")
+    if cap.dim() == 3:
+        _require(cap.shape[0] * cap.shape[1] == M and cap.shape[1] == T and cap.shape[2] == I,
+                 "capture: [rows, T, I] with rows * T = M")
+        return cap.data_ptr(), cap.stride(1), cap.stride(0)
+    _require(cap.dim() == 2 and cap.shape[0] == M and cap.shape[1] == I, "capture: [M, I] or [rows, T, I]")
+    return cap.data_ptr(), cap.stride(0), cap.stride(0) * T
+
+
 def _weight_format(W, w_scale, N, K):
     """The C ABI's weight format code of (W, w_scale): fp32 W (no scale) -> Q35_F32; int8 W with w_scale [N] fp32 ->
     Q35_I8 (one scale per output row); int8 W with w_scale [N, K / 128] fp32 -> Q35_I8_G128 (one scale per group of
@@ -431,7 +448,7 @@ def _weight_format(W, w_scale, N, K):
     return Q35_I8
 
 
-def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T):
+def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T, cap=None):
     _on_gpu(x, W, w_scale, y, pushes)
     _require(x.dtype == torch.float32 and x.dim() == 2 and y.dtype == torch.float32 and y.dim() == 2,
              "x: [M, K] fp32; y: [M, N or N/2] fp32")
@@ -442,12 +459,14 @@ def _gemv_impl(x, W, w_scale, y, epilogue, pushes, T):
     _require(y.shape[1] == (N // 2 if epilogue == 2 else N), "y: [M, N] ([M, N / 2] for the SwiGLU epilogue)")
     fmt = _weight_format(W, w_scale, N, K)
     npush = _pushes_check(pushes)
+    _require(cap is None or epilogue == 2, "capture: SwiGLU epilogue only")
+    cp, ldc, ldcr = _cap_args(cap, M, int(T), N // 2, x.device)
     st = _lib.lib().q35_gemv(_ptr(x), K, _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.shape[1], M, N, K, int(epilogue),
-                             _ptr(pushes), npush, int(T), _stream(x))
+                             _ptr(pushes), npush, int(T), cp, ldc, ldcr, _stream(x))
     check(st, "q35_gemv")
 
 
-def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T):
+def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T, cap=None):
     _on_gpu(W, w_scale, pushes)
     _require(x.is_cuda and x.dtype in (torch.float32, torch.int32, torch.bfloat16) and x.dim() == 2
              and x.stride(1) == 1, "x: [M, K] fp32, bf16 or int32 words of split activations, unit column stride")
@@ -462,12 +481,14 @@ def _gemm_q8_impl(x, W, w_scale, y, epilogue, pushes, T):
     _require(K % 64 == 0, "K must be a multiple of 64")
     npush = _pushes_check(pushes)
     fn = {torch.int32: "q35_gemm_q8_split", torch.bfloat16: "q35_gemm_q8_bf16"}.get(x.dtype, "q35_gemm_q8")
+    _require(cap is None or epilogue in (2, 3), "capture: SwiGLU epilogues only")
+    cp, ldc, ldcr = _cap_args(cap, M, int(T), N // 2, x.device)
     st = getattr(_lib.lib(), fn)(_ptr(x), x.stride(0), _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.stride(0), M, N, K,
-                                 int(epilogue), _ptr(pushes), npush, int(T), _stream(x))
+                                 int(epilogue), _ptr(pushes), npush, int(T), cp, ldc, ldcr, _stream(x))
     check(st, fn)
 
 
-def _gemv_norm_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, epilogue, pushes, T):
+def _gemv_norm_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, epilogue, pushes, T, cap=None):
     _on_gpu(x, x_add, x_out, norm_w, W, w_scale, y, pushes)
     _require(x.dtype == torch.float32 and x.dim() == 2 and y.dtype == torch.float32 and y.dim() == 2,
              "x: [M, K] fp32; y: [M, N or N/2] fp32")
@@ -480,9 +501,11 @@ def _gemv_norm_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, epilogue, pushe
     N = W.shape[0]
     _require(y.shape[0] == M and y.shape[1] == (N // 2 if epilogue == 2 else N), "y: [M, N] ([M, N / 2] SwiGLU)")
     fmt = _weight_format(W, w_scale, N, K)
+    _require(cap is None or epilogue == 2, "capture: SwiGLU epilogue only")
+    cp, ldc, ldcr = _cap_args(cap, M, int(T), N // 2, x.device)
     st = _lib.lib().q35_gemv_norm(_ptr(x), _ptr(x_add), _ptr(x_out), x.stride(0), _ptr(norm_w), float(eps), _ptr(W),
                                   fmt, _ptr(w_scale), _ptr(y), y.shape[1], M, N, K, int(epilogue), _ptr(pushes),
-                                  _pushes_check(pushes), int(T), _stream(x))
+                                  _pushes_check(pushes), int(T), cp, ldc, ldcr, _stream(x))
     check(st, "q35_gemv_norm")
 
 
@@ -531,14 +554,15 @@ def _gemv_gated_norm_impl(o, z, norm_w, head_scale, eps, W, w_scale, y, epilogue
     check(st, "q35_gemv_gated_norm")
 
 
-def _swiglu_push_impl(gu, pushes, T):
+def _swiglu_push_impl(gu, pushes, T, cap=None):
     _on_gpu(gu, pushes)
     _require(gu.dtype == torch.float32 and gu.shape[-1] % 2 == 0, "gu: [..., 2 I] fp32")
     I = gu.shape[-1] // 2
     M = gu.numel() // (2 * I)
     a = torch.empty(*gu.shape[:-1], I, dtype=torch.float32, device=gu.device)
-    st = _lib.lib().q35_swiglu_push(_ptr(gu), _ptr(a), M, I, _ptr(pushes), _pushes_check(pushes), int(T),
-                                    _stream(gu))
+    cp, ldc, ldcr = _cap_args(cap, M, int(T), I, gu.device)
+    st = _lib.lib().q35_swiglu_push(_ptr(gu), _ptr(a), M, I, _ptr(pushes), _pushes_check(pushes), int(T), cp, ldc,
+                                    ldcr, _stream(gu))
     check(st, "q35_swiglu_push")
     return a
 
@@ -616,16 +640,17 @@ _LIB.impl("gated_attn_prefill_cached",
           lambda q, kc, vc, gate, pos, cos, sin, scale: q.new_empty(q.shape[0], q.shape[1], q.shape[2] * q.shape[3]),
           "Meta")
 _LIB.impl("argmax_rows_", lambda x, idx: None, "Meta")
-_LIB.impl("gemv_norm_", lambda x, xa, xo, nw, eps, W, ws, y, e, pushes, T: None, "Meta")
+_LIB.impl("gemv_norm_", lambda x, xa, xo, nw, eps, W, ws, y, e, pushes, T, cap=None: None, "Meta")
 _LIB.impl("gdn_chunk_prefill_conv_", lambda y, cw, cb, cs, Al, dt, bo, ao, st, Hk, sc:
           y.new_empty(y.shape[0], y.shape[1], st.shape[1], st.shape[3]), "Meta")
 _LIB.impl("gdn_decode_sliced_", lambda y, Al, dt, bo, ao, st, sc: y.new_empty(y.shape[0], st.shape[1] * st.shape[2]),
           "Meta")
 _LIB.impl("gemv_norm_conv_", lambda x, xa, xo, nw, eps, W, ws, y, cw, cb, cs: None, "Meta")
 _LIB.impl("gemv_gated_norm_", lambda o, z, nw, hs, eps, W, ws, y, e: None, "Meta")
-_LIB.impl("gemv_", lambda x, W, ws, y, e, pushes, T: None, "Meta")
-_LIB.impl("gemm_q8_", lambda x, W, ws, y, e, pushes, T: None, "Meta")
-_LIB.impl("swiglu_push", lambda gu, pushes, T: gu.new_empty(*gu.shape[:-1], gu.shape[-1] // 2), "Meta")
+_LIB.impl("gemv_", lambda x, W, ws, y, e, pushes, T, cap=None: None, "Meta")
+_LIB.impl("gemm_q8_", lambda x, W, ws, y, e, pushes, T, cap=None: None, "Meta")
+_LIB.impl("swiglu_push", lambda gu, pushes, T, cap=None: gu.new_empty(*gu.shape[:-1], gu.shape[-1] // 2),
+          "Meta")
 _LIB.impl("add_rmsnorm_", lambda x, y, w, eps: torch.empty_like(x), "Meta")
 _LIB.impl("add_rmsnorm_split_", lambda x, y, w, eps: torch.empty_like(x, dtype=torch.int32), "Meta")
 _LIB.impl("gated_rmsnorm", lambda o, z, w, hs, eps: o.new_empty(*o.shape[:-2], o.shape[-2] * o.shape[-1]), "Meta")
@@ -816,7 +841,7 @@ def pack_pushes(pushes, device):
     return torch.tensor(rec, dtype=torch.int32).reshape(-1, 6).to(device)
 
 
-def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, prenorm=None, conv=None):
+def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, prenorm=None, conv=None, capture=None):
     """y[m, n] = sum_k x[m, k] W[n, k] s(n, k) for M <= 8 rows (decode): W int8 with scales w_scale [N, K / 128]
     (one per group of 128 inputs, the engine's q8 format) or [N] (one per row), or fp32 W (w_scale None).
     epilogue "store" writes out, "add" accumulates into out (a residual add), "swiglu" treats W's rows as
@@ -824,7 +849,9 @@ def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, preno
     prenorm = (x_add, norm_w, eps, x_out): x is then a residual; the product takes the RMSNorm (1 + w) of
     s = x + x_add (x_add may be None), and s is written to x_out when it is not None (q35_gemv_norm).
     conv = (conv_w [C, K], conv_bias or None, conv_state [M, K - 1, C]), with prenorm and the store epilogue: outputs
-    0 .. C - 1 go through the GDN causal conv + SiLU and conv_state advances in place (q35_gemv_norm_conv)."""
+    0 .. C - 1 go through the GDN causal conv + SiLU and conv_state advances in place (q35_gemv_norm_conv).
+    capture (SwiGLU only): an fp32 view [rows, T, I] or [M, I] (unit neuron stride) that also receives the
+    activations after the pushes (the engine's MLP capture hook, engine/model.js:9, :451-453)."""
     e = _EPI[epilogue]
     if out is None:
         N = W.shape[0] // 2 if e == 2 else W.shape[0]
@@ -837,14 +864,14 @@ def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, preno
                                       cw.reshape(cw.shape[0], cw.shape[-1]).float().contiguous(), cb, cs)
         return out
     if prenorm is None:
-        torch.ops.q35.gemv_(x, W, w_scale, out, e, pushes, int(T))
+        torch.ops.q35.gemv_(x, W, w_scale, out, e, pushes, int(T), capture)
     else:
         x_add, norm_w, eps, x_out = prenorm
-        torch.ops.q35.gemv_norm_(x, x_add, x_out, norm_w, float(eps), W, w_scale, out, e, pushes, int(T))
+        torch.ops.q35.gemv_norm_(x, x_add, x_out, norm_w, float(eps), W, w_scale, out, e, pushes, int(T), capture)
     return out
 
 
-def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1, split_out=False):
+def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1, split_out=False, capture=None):
     """y[m, n] = sum_k x[m, k] W[n, k] s(n, k) over many rows (the prefill projections): x [M, K] fp32, W [N, K]
     int8 with scales w_scale [N, K / 128] (per group of 128 inputs) or [N] (per row), K a multiple of 64 (128 with
     group scales); fp32-accurate (bf16 MFMA on a hi + lo split of x). epilogue "store" writes out, "add"
@@ -852,7 +879,7 @@ def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1, split_o
     silu(gate) * up with the neuron pushes (pack_pushes) applied, out [M, N / 2]. x may also be the int32 words of
     activations already split (add_rmsnorm_(..., split=True), split_activations): the same product, bitwise, without
     the split in the kernel; or bf16 (the product of x.float(), bitwise, with the lo products skipped). split_out=True (SwiGLU only) writes out as the int32 words of the split layout, the
-    input of the next gemm_q8. Returns out."""
+    input of the next gemm_q8. capture: as for gemv (the fp32 activations, whatever the layout of out). Returns out."""
     e = _EPI[epilogue]
     if split_out:
         if e != 2:
@@ -862,14 +889,14 @@ def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1, split_o
     if out is None:
         N = W.shape[0] // 2 if e in (2, 3) else W.shape[0]
         out = torch.empty(x.shape[0], N, dtype=torch.int32 if e == 3 else torch.float32, device=x.device)
-    torch.ops.q35.gemm_q8_(x, W, w_scale, out, e, pushes, int(T))
+    torch.ops.q35.gemm_q8_(x, W, w_scale, out, e, pushes, int(T), capture)
     return out
 
 
-def swiglu_push(gu, pushes=None, T=1):
+def swiglu_push(gu, pushes=None, T=1, capture=None):
     """silu(gate) * up over a [..., 2 I] ([gate | up]) projection with the neuron pushes applied (the hook point of
-    engine/kernels_qwen35.js:250-279)."""
-    return torch.ops.q35.swiglu_push(gu, pushes, int(T))
+    engine/kernels_qwen35.js:250-279); capture as for gemv."""
+    return torch.ops.q35.swiglu_push(gu, pushes, int(T), capture)
 
 
 def argmax_rows(x, out=None):

@@ -331,10 +331,15 @@ int q35_add_rmsnorm_split(float* x, int64_t ldx, const float* y, int64_t ldy, co
  *   with npush 0); T: tokens per sequence row (the push row is min(m / T, 3)).
  *   Epilogue 1 with fewer than 256 blocks of 16 output rows splits K over several blocks that add their sums into
  *   y with fp32 atomics: the order of those additions, and so the last bits of y, may differ between calls.
+ *   cap: the neuron activation capture of the MLP hook (engine/model.js:9, :451-453; the `cap` binding of
+ *   engine/kernels_qwen35.js:251-279, its capOff folded into the pointer), NULL for none, epilogue 2 only: the
+ *   activation of neuron j of row m (after the pushes, as y holds it) is also written to
+ *   cap[(m / T) ld_cap_row + (m % T) ld_cap + j] in fp32 (ld_cap, ld_cap_row >= N / 2; 4-byte aligned), e.g.
+ *   [sequence row][token][neuron] slices of a [layers, rows, tokens, neurons] buffer.
  */
 int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
              int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T,
-             q35_stream_t stream);
+             float* cap, int64_t ld_cap, int64_t ld_cap_row, q35_stream_t stream);
 
 /*
  * q35_gemv with the decoder layer's residual add + RMSNorm in front (HF:753-793 then HF:720-734; the engine's
@@ -345,7 +350,8 @@ int q35_gemv(const float* x, int64_t ldx, const void* W, int w_dtype, const floa
  */
 int q35_gemv_norm(const float* x, const float* x_add, float* x_out, int64_t ldx, const float* norm_w, float eps,
                   const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy, int64_t M, int64_t N,
-                  int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T, q35_stream_t stream);
+                  int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T, float* cap,
+                  int64_t ld_cap, int64_t ld_cap_row, q35_stream_t stream);
 
 /*
  * q35_gemv_norm (store epilogue) whose outputs 0 .. conv_channels - 1 go through the GDN layer's causal conv + SiLU
@@ -384,11 +390,12 @@ int q35_gemv_gated_norm(const float* o, int64_t ldo, const float* z, int64_t ldz
  *   epilogue 0: y = v; 1: y += v; 2: SwiGLU over interleaved row pairs (row 2 j gate, 2 j + 1 up of neuron j):
  *   y[m, j] = silu(v_2j) * v_2j+1 then the pushes in order (N even, ldy >= N / 2); 3: as 2 with y written in the
  *   split layout of q35_gemm_q8_split's input (N / 2 a multiple of 8, ldy a multiple of 4, y 16-byte aligned), the
- *   down projection's input. pushes, npush <= 64 and T as for q35_gemv.
+ *   down projection's input. pushes, npush <= 64 and T as for q35_gemv; cap, ld_cap, ld_cap_row (epilogues 2 and 3:
+ *   the fp32 activations whatever the layout of y) as for q35_gemv.
  */
 int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int64_t npush,
-                int64_t T, q35_stream_t stream);
+                int64_t T, float* cap, int64_t ld_cap, int64_t ld_cap_row, q35_stream_t stream);
 
 /*
  * q35_gemm_q8 on x already split by its producer (q35_add_rmsnorm_split): xs [M, ldx] 4-byte words in the split
@@ -398,7 +405,8 @@ int q35_gemm_q8(const float* x, int64_t ldx, const int8_t* W, int w_dtype, const
  */
 int q35_gemm_q8_split(const void* xs, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
                       int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
-                      int64_t npush, int64_t T, q35_stream_t stream);
+                      int64_t npush, int64_t T, float* cap, int64_t ld_cap, int64_t ld_cap_row,
+                      q35_stream_t stream);
 
 /*
  * q35_gemm_q8 on bf16 x (the attention output, read without a conversion to fp32): xb [M, ldx] bf16, 16-byte
@@ -407,14 +415,14 @@ int q35_gemm_q8_split(const void* xs, int64_t ldx, const int8_t* W, int w_dtype,
  */
 int q35_gemm_q8_bf16(const void* xb, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
                      int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,
-                     int64_t npush, int64_t T, q35_stream_t stream);
+                     int64_t npush, int64_t T, float* cap, int64_t ld_cap, int64_t ld_cap_row, q35_stream_t stream);
 
 /*
  * a[m, n] = silu(gu[m, n]) * gu[m, I + n] with the pushes applied, gu: [M, 2 I] fp32 ([gate | up] per row),
- * a: [M, I] fp32; pushes and T as for q35_gemv.
+ * a: [M, I] fp32; pushes, T and the capture (cap, ld_cap, ld_cap_row >= I) as for q35_gemv.
  */
 int q35_swiglu_push(const float* gu, float* a, int64_t M, int64_t I, const q35_push* pushes, int64_t npush,
-                    int64_t T, q35_stream_t stream);
+                    int64_t T, float* cap, int64_t ld_cap, int64_t ld_cap_row, q35_stream_t stream);
 
 /*
  * Per-row argmax (greedy sampling): idx[r] = the lowest index of the largest value of x[r, 0:n] (the WGSL `argmax`,

@@ -24,7 +24,7 @@ import torch.nn.functional as F
 
 from .attention import apply_partial_rope, rope_inv_freq, rope_tables
 from .gdn import chunk_gated_delta_rule, recurrent_gated_delta_rule
-from .mlp import q8_dequant
+from .mlp import q8_dequant, swiglu_push
 
 
 def dequant(W, key):
@@ -56,9 +56,10 @@ def causal_conv(x, w, state):
     return F.silu(out), full[:, -(K - 1):, :].clone()
 
 
-def gdn_layer(cfg, W, l, h, state, decode):
+def gdn_layer(cfg, W, l, h, state, decode, head_scale=None):
     """Gated DeltaNet mixer (HF:432-543). state: dict with 'conv' [B, K-1, C] and 'rec' [B, Hv, dk, dv] (or None).
-    Prefill uses the chunked rule, decode (T == 1 with a state) the recurrent one, as HF:505-530 does."""
+    Prefill uses the chunked rule, decode (T == 1 with a state) the recurrent one, as HF:505-530 does. head_scale:
+    optional [Hv] per-head output scale after the gated norm (engine/kernels_qwen35.js:243)."""
     p = f"layers.{l}."
     B, T, _ = h.shape
     mixed = h @ W[p + "in_proj_qkv"].T
@@ -80,6 +81,8 @@ def gdn_layer(cfg, W, l, h, state, decode):
         o, rec = chunk_gated_delta_rule(q, k, v, g, beta, initial_state=rec0, output_final_state=True,
                                         use_qk_l2norm_in_kernel=True)
     o = rmsnorm_gated(o.reshape(-1, cfg.lin_dv), z.reshape(-1, cfg.lin_dv), W[p + "norm"], cfg.eps)
+    if head_scale is not None:
+        o = o.reshape(B, T, cfg.lin_v_heads, cfg.lin_dv) * head_scale.float()[:, None]
     y = o.reshape(B, T, -1) @ W[p + "out_proj"].T
     return y, {"conv": conv_state, "rec": rec}
 
@@ -115,9 +118,19 @@ def attn_layer(cfg, W, l, h, cache, pos, cos_t, sin_t):
     return o @ W[p + "o_proj"].T, {"k": kh, "v": vh}
 
 
-def mlp(W, l, h):
+def mlp_act(W, l, h, pushes=()):
+    """The MLP activations silu(gate) * up (the down_proj input, where the engine's neuron hook sits) of h [B, T, H]
+    (or [M, H], one token per row), with the layer's pushes applied (oracle.mlp.swiglu_push: the push row of token t
+    of batch row b is min(b, 3))."""
     p = f"layers.{l}."
-    return (F.silu(h @ dequant(W, p + "gate_proj").T) * (h @ dequant(W, p + "up_proj").T)) @ dequant(W, p + "down_proj").T
+    T = h.shape[1] if h.dim() == 3 else 1
+    g = (h @ dequant(W, p + "gate_proj").T).reshape(-1, W[p + "gate_proj.q"].shape[0])
+    u = (h @ dequant(W, p + "up_proj").T).reshape(g.shape)
+    return swiglu_push(g, u, pushes, T=T).reshape(*h.shape[:-1], -1)
+
+
+def mlp(W, l, h, pushes=()):
+    return mlp_act(W, l, h, pushes) @ dequant(W, f"layers.{l}.down_proj").T
 
 
 class OracleModel:
@@ -127,6 +140,7 @@ class OracleModel:
         self.cfg, self.W, self.steer_layer = cfg, W, steer_layer
         self.cos, self.sin = rope_tables(1 << 15, rope_inv_freq(cfg.head_dim, cfg.partial_rotary, cfg.rope_theta))
         self.vecs = None
+        self.pushes, self.head_scales = {}, {}
         self.reset()
 
     def reset(self):
@@ -137,10 +151,23 @@ class OracleModel:
         """vecs: [B, H] fp32 (zero rows for no vector), added after steer_layer at every position."""
         self.vecs = vecs
 
-    def forward(self, ids, collect_layer=None, stop_after=None):
+    def set_pushes(self, pushes):
+        """{layer: [(neuron or None, "add" | "mul", [value per row])]}: the engine's neuron pushes
+        (engine/model.js:412-423) at the down_proj input."""
+        self.pushes = dict(pushes or {})
+
+    def set_head_scales(self, scales):
+        """{layer: [Hv] values}: per-head output scales of Gated DeltaNet layers (engine/model.js:362-368)."""
+        self.head_scales = {l: torch.as_tensor(v, dtype=torch.float32) for l, v in (scales or {}).items()}
+
+    def forward(self, ids, collect_layer=None, stop_after=None, capture_layers=()):
         """ids: [B, T] token ids continuing from self.pos. Returns (last-position logits [B, V] or None when
-        stopping after layer stop_after, optional residual after collect_layer [B, T, H])."""
+        stopping after layer stop_after, optional residual after collect_layer [B, T, H]). Also leaves, for the
+        engine's hooks (engine/model.js:9-11): self.acts {layer: [B, T, I]} the MLP activations of capture_layers,
+        self.resid_mixer / self.resid_layer [layers run] of [B, T, H] the residual after each mixer's residual add and
+        after each layer."""
         cfg, W = self.cfg, self.W
+        self.acts, self.resid_mixer, self.resid_layer = {}, [], []
         x = W["embed"][ids]
         T = ids.shape[1]
         decode = self.pos > 0 and T == 1
@@ -152,11 +179,16 @@ class OracleModel:
             if cfg.is_attention(l):
                 y, self.states[l] = attn_layer(cfg, W, l, h, self.states[l], self.pos, self.cos, self.sin)
             else:
-                y, self.states[l] = gdn_layer(cfg, W, l, h, self.states[l], decode)
+                y, self.states[l] = gdn_layer(cfg, W, l, h, self.states[l], decode, self.head_scales.get(l))
             x = x + y
-            x = x + mlp(W, l, rmsnorm_1p(x, W[p + "post_attention_layernorm"], cfg.eps))
+            self.resid_mixer.append(x)
+            a = mlp_act(W, l, rmsnorm_1p(x, W[p + "post_attention_layernorm"], cfg.eps), self.pushes.get(l, ()))
+            if l in capture_layers:
+                self.acts[l] = a
+            x = x + a @ dequant(W, p + "down_proj").T
             if l == self.steer_layer and self.vecs is not None:
                 x = x + self.vecs[:, None, :]
+            self.resid_layer.append(x)
             if l == collect_layer:
                 collected = x.clone()
         self.pos += T

@@ -13,6 +13,12 @@ Recorded (all fp32):
   next_ids, logits_decode  one cached decode step (recurrent delta rule, KV cache) with the prefill's argmax
   logits_steered           prefill with a residual vector added after layer 1 on every position: +v on row 0,
                            -v on row 1 (the forward-hook form of tests/engine_ref.py:49-53)
+  acts_l{0..3}             MLP activations (the input of down_proj, recorded by a forward pre-hook as
+                           tests/engine_ref.py:11-20 does) of the prefill, every 7th position
+  acts_decode_l{0..3}      the same for the cached decode step
+  acts_push_l{0..3},       prefill with a neuron push on layer PUSH_LAYER (neuron PUSH_NEURON += PUSH_VALUE on every
+  logits_pushed            row and position, the hook's push form of tests/engine_ref.py:14-15): the activations of
+                           every layer and the last-position logits
 
 Run from the repository root in the build container (it imports transformers; nothing here runs on the GPU box):
     python tests/golden/make_layer_golden.py
@@ -27,7 +33,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
 sys.path.insert(0, os.path.join(HERE, "..", "..", "duo-mech-interp_amd"))
 
-from tiny_weights import STEER_LAYER, tiny_config, tiny_weights, tiny_inputs  # noqa: E402
+from tiny_weights import PUSH_LAYER, PUSH_NEURON, PUSH_VALUE, STEER_LAYER, tiny_config, tiny_weights, \
+    tiny_inputs  # noqa: E402
 
 from transformers import Qwen3_5TextConfig  # noqa: E402
 from transformers.models.qwen3_5.modeling_qwen3_5 import Qwen3_5ForCausalLM  # noqa: E402
@@ -75,10 +82,23 @@ def main():
     hooks = [m.model.layers[l].register_forward_hook(
         lambda mod, inp, o, l=l: resid.__setitem__(l, (o[0] if isinstance(o, tuple) else o).detach().clone()))
         for l in range(cfg.layers)]
+    acts, push = {}, {}
+
+    def pre_hook(l):
+        def f(mod, inp):
+            h = inp[0]
+            if l in push:
+                h = h.clone()
+                n, v = push[l]
+                h[..., n] += v
+            acts[l] = h.detach().clone()
+            return (h,)
+        return f
+    hooks += [m.model.layers[l].mlp.down_proj.register_forward_pre_hook(pre_hook(l)) for l in range(cfg.layers)]
     with torch.no_grad():
         r = m(input_ids=ids, use_cache=True)
-        for h in hooks:
-            h.remove()
+        for l in range(cfg.layers):
+            out[f"acts_l{l}"] = acts[l][:, ::7].contiguous()
         for l in range(cfg.layers):
             out[f"resid_l{l}"] = resid[l][:, ::7].contiguous()
         out["logits_prefill"] = r.logits[:, -1].contiguous()
@@ -86,6 +106,16 @@ def main():
         out["next_ids"] = nxt
         r2 = m(input_ids=nxt, past_key_values=r.past_key_values, use_cache=True)
         out["logits_decode"] = r2.logits[:, -1].contiguous()
+        for l in range(cfg.layers):
+            out[f"acts_decode_l{l}"] = acts[l][:, 0].contiguous()
+        push[PUSH_LAYER] = (PUSH_NEURON, PUSH_VALUE)
+        r4 = m(input_ids=ids)
+        push.clear()
+        for l in range(cfg.layers):
+            out[f"acts_push_l{l}"] = acts[l][:, ::7].contiguous()
+        out["logits_pushed"] = r4.logits[:, -1].contiguous()
+        for h in hooks:
+            h.remove()
         signs = torch.tensor([1.0, -1.0])[:, None, None]
         hv = m.model.layers[STEER_LAYER].register_forward_hook(
             lambda mod, inp, o: ((o[0] + signs * vec,) + tuple(o[1:])) if isinstance(o, tuple) else o + signs * vec)

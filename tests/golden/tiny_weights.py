@@ -6,6 +6,7 @@ import torch
 from q35hip.workloads import Q35Config, init_weights
 
 STEER_LAYER = 1
+PUSH_LAYER, PUSH_NEURON, PUSH_VALUE = 2, 5, 0.75  # the neuron push of the fixture's pushed prefill
 
 
 def tiny_config():

@@ -39,7 +39,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 10
+    assert L.q35_abi_version() == 11
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -112,35 +112,43 @@ def test_validation_rejects_without_launching():
     assert L.q35_attn_prep(fake, 5120, fake, fake, 1e-6, fake, fake, 60, fake, fake, fake, None, None, fake, fake,
                            16, 1, 1, 8, 2, 256, None) == 2
     # decode GEMV: K not a multiple of 256, too many rows, odd N for the SwiGLU epilogue, unknown weight type
-    assert L.q35_gemv(fake, 1000, fake, 2, fake, fake, 64, 3, 64, 1000, 0, None, 0, 1, None) == 2
-    assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 9, 64, 1024, 0, None, 0, 1, None) == 2
-    assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 63, 1024, 2, None, 0, 1, None) == 1
-    assert L.q35_gemv(fake, 1024, fake, 1, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1, None) == 2
+    assert L.q35_gemv(fake, 1000, fake, 2, fake, fake, 64, 3, 64, 1000, 0, None, 0, 1, None, 0, 0, None) == 2
+    assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 9, 64, 1024, 0, None, 0, 1, None, 0, 0, None) == 2
+    assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 63, 1024, 2, None, 0, 1, None, 0, 0, None) == 1
+    assert L.q35_gemv(fake, 1024, fake, 1, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1, None, 0, 0, None) == 2
     # group-128 int8 weights need their scales
-    assert L.q35_gemv(fake, 1024, fake, 3, None, fake, 64, 3, 64, 1024, 0, None, 0, 1, None) == 1
+    assert L.q35_gemv(fake, 1024, fake, 3, None, fake, 64, 3, 64, 1024, 0, None, 0, 1, None, 0, 0, None) == 1
     # prefill GEMM: weight formats other than int8, group scales over K not a multiple of 128, no scales
-    assert L.q35_gemm_q8(fake, 1024, fake, 1, fake, fake, 64, 100, 64, 1024, 0, None, 0, 1, None) == 2
-    assert L.q35_gemm_q8(fake, 192, fake, 3, fake, fake, 64, 100, 64, 192, 0, None, 0, 1, None) == 2
-    assert L.q35_gemm_q8(fake, 1024, fake, 3, None, fake, 64, 100, 64, 1024, 0, None, 0, 1, None) == 1
-    assert L.q35_swiglu_push(fake, fake, 3, 64, None, 2, 1, None) == 1
+    assert L.q35_gemm_q8(fake, 1024, fake, 1, fake, fake, 64, 100, 64, 1024, 0, None, 0, 1, None, 0, 0, None) == 2
+    assert L.q35_gemm_q8(fake, 192, fake, 3, fake, fake, 64, 100, 64, 192, 0, None, 0, 1, None, 0, 0, None) == 2
+    assert L.q35_gemm_q8(fake, 1024, fake, 3, None, fake, 64, 100, 64, 1024, 0, None, 0, 1, None, 0, 0, None) == 1
+    assert L.q35_swiglu_push(fake, fake, 3, 64, None, 2, 1, None, 0, 0, None) == 1
     assert L.q35_add_rmsnorm(fake, 1024, None, 0, fake, fake, 1024, 3, 1022, 1e-6, None) == 2
     assert L.q35_add_rmsnorm(fake, 512, None, 0, fake, fake, 1024, 3, 1024, 1e-6, None) == 1
     # split forms: the norm's split output needs H a multiple of 8; the split GEMM validates as q35_gemm_q8
     assert L.q35_add_rmsnorm_split(fake, 1028, None, 0, fake, fake, 1028, 3, 1028, 1e-6, None) == 2
-    assert L.q35_gemm_q8_split(fake, 192, fake, 3, fake, fake, 64, 100, 64, 192, 0, None, 0, 1, None) == 2
-    assert L.q35_gemm_q8_split(None, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 0, None, 0, 1, None) == 1
+    assert L.q35_gemm_q8_split(fake, 192, fake, 3, fake, fake, 64, 100, 64, 192, 0, None, 0, 1, None, 0, 0, None) == 2
+    assert L.q35_gemm_q8_split(None, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 0, None, 0, 1, None, 0, 0, None) == 1
     # SwiGLU with split output (epilogue 3): N / 2 must be a multiple of 8; epilogue 4 does not exist
-    assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 36, 1024, 3, None, 0, 1, None) == 2
-    assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 4, None, 0, 1, None) == 1
+    assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 36, 1024, 3, None, 0, 1, None, 0, 0, None) == 2
+    assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 4, None, 0, 1, None, 0, 0, None) == 1
     assert L.q35_gated_rmsnorm_split(fake, fake, 2048, fake, None, fake, 3, 16, 64, 1e-6, None) == 2
+    # activation capture: only with the SwiGLU epilogues, neuron strides of at least N / 2, 4-byte aligned
+    assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1, fake, 64, 64, None) == 1
+    assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 64, 1024, 2, None, 0, 1, fake, 31, 64, None) == 1
+    assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 1, None, 0, 1, fake, 64, 64, None) == 1
+    assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 2, None, 0, 1, fake, 32, 31, None) == 1
+    assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 3, None, 0, 1, fake + 2, 32, 32,
+                         None) == 1
+    assert L.q35_swiglu_push(fake, fake, 3, 64, None, 0, 1, fake, 63, 64, None) == 1
     # argmax: ld shorter than the row, no rows
     assert L.q35_argmax_rows(fake, 100, 3, 101, fake, None, None) == 1
     assert L.q35_argmax_rows(fake, 100, 0, 100, fake, None, None) == 1
     # gemv_norm: no norm weight; x_out overlapping x (the other blocks would read it while it is written)
     assert L.q35_gemv_norm(fake, None, None, 1024, None, 1e-6, fake, 2, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1,
-                           None) == 1
+                           None, 0, 0, None) == 1
     assert L.q35_gemv_norm(fake, None, fake, 1024, fake, 1e-6, fake, 2, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1,
-                           None) == 1
+                           None, 0, 0, None) == 1
 
 
 def test_decode_workspace_scales_with_splits():

@@ -12,7 +12,8 @@ from oracle import model as om
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "golden"))
-from tiny_weights import STEER_LAYER, tiny_config, tiny_inputs, tiny_weights  # noqa: E402
+from tiny_weights import PUSH_LAYER, PUSH_NEURON, PUSH_VALUE, STEER_LAYER, tiny_config, tiny_inputs, \
+    tiny_weights  # noqa: E402
 
 GOLD = load_file(os.path.join(HERE, "golden", "qwen35_tiny_golden.safetensors"))
 TOL = 2e-4
@@ -70,6 +71,67 @@ def test_decode_continues_prefill_and_rows_are_independent(tiny):
     m4 = om.OracleModel(cfg, W)
     both, _ = m4.forward(ids)
     assert oracle.rel_err(row1[0], both[1]) <= 1e-5
+
+
+def test_mlp_activation_capture_and_push_against_hf_hooks(tiny):
+    """The oracle's captured MLP activations (the down_proj input) equal HF's forward pre-hook on down_proj
+    (tests/engine_ref.py:11-20) for the prefill and the cached decode step, and with a neuron push on one layer the
+    activations of every layer and the logits follow HF's pushed run."""
+    cfg, W = tiny
+    layers = tuple(range(cfg.layers))
+    m = om.OracleModel(cfg, W)
+    m.forward(GOLD["ids"], capture_layers=layers)
+    for l in layers:
+        assert oracle.rel_err(m.acts[l][:, ::7], GOLD[f"acts_l{l}"]) <= TOL, l
+    m.forward(GOLD["next_ids"], capture_layers=layers)
+    for l in layers:
+        assert oracle.rel_err(m.acts[l][:, 0], GOLD[f"acts_decode_l{l}"]) <= TOL, l
+    m = om.OracleModel(cfg, W)
+    m.set_pushes({PUSH_LAYER: [(PUSH_NEURON, "add", [PUSH_VALUE] * 2)]})
+    logits, _ = m.forward(GOLD["ids"], capture_layers=layers)
+    for l in layers:
+        assert oracle.rel_err(m.acts[l][:, ::7], GOLD[f"acts_push_l{l}"]) <= TOL, l
+    assert oracle.rel_err(logits, GOLD["logits_pushed"]) <= TOL
+    # the push must show: the unpushed run differs from the pushed fixture
+    assert oracle.rel_err(GOLD["acts_l3"], GOLD["acts_push_l3"]) > 10 * TOL
+
+
+def test_residual_snapshots_and_activations_compose(tiny):
+    """The hook outputs fit the layer's algebra: resid after layer l = resid after its mixer + acts_l @ down_proj^T
+    (+ the steering vector after the steer layer), and the last snapshot is the collected residual."""
+    cfg, W = tiny
+    ids, vec = tiny_inputs(cfg)
+    m = om.OracleModel(cfg, W, steer_layer=STEER_LAYER)
+    m.set_vectors(torch.stack([vec, -vec]))
+    _, collected = m.forward(ids[:, :20], collect_layer=cfg.layers - 1, capture_layers=range(cfg.layers))
+    assert len(m.resid_layer) == len(m.resid_mixer) == cfg.layers
+    assert torch.equal(m.resid_layer[-1], collected)
+    for l in range(cfg.layers):
+        x = m.resid_mixer[l] + m.acts[l] @ om.dequant(W, f"layers.{l}.down_proj").T
+        if l == STEER_LAYER:
+            x = x + torch.stack([vec, -vec])[:, None, :]
+        assert torch.allclose(x, m.resid_layer[l], rtol=0, atol=0), l
+
+
+def test_head_scales_scale_each_heads_contribution(tiny):
+    """Per-head output scales (engine/model.js:362-368) act linearly on the GDN mixer output: scales of 1 change
+    nothing (bitwise), 0 on every head silences the mixer, the one-hot scales of the heads sum to the unscaled
+    output, and mixed scales give the matching combination of the one-hot outputs."""
+    cfg, W = tiny
+    ids = GOLD["ids"][:, :24]
+    B, T = ids.shape
+    h = W["embed"][ids]
+
+    def y_of(hs):
+        y, _ = om.gdn_layer(cfg, W, 0, h, None, False, hs)
+        return y
+    y0 = y_of(None)
+    assert torch.equal(y_of(torch.ones(cfg.lin_v_heads)), y0)
+    assert torch.count_nonzero(y_of(torch.zeros(cfg.lin_v_heads))) == 0
+    parts = sum(y_of(torch.eye(cfg.lin_v_heads)[i]) for i in range(cfg.lin_v_heads))
+    assert oracle.rel_err(parts, y0) <= 1e-6
+    y2 = y_of(torch.tensor([2.0, 0.5]))
+    assert oracle.rel_err(y2, 2.0 * y_of(torch.tensor([1.0, 0.0])) + 0.5 * y_of(torch.tensor([0.0, 1.0]))) <= 1e-6
 
 
 def test_median_residual_norm_convention():
