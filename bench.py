@@ -263,14 +263,23 @@ def bench_copy(torch, dev, mb=256, reps=5):
     return {"bytes_per_launch": 2 * (mb << 20), "us": t * 1e6, "gbs": 2 * (mb << 20) / t / 1e9}
 
 
-def bench_stack(torch, q35hip, workloads, dev, steps=256):
-    """The Qwen3.5-0.8B-shaped hybrid stack (24 layers, int8 SwiGLU, tied 151,936 embedding), batch 3 steered rows:
-    2048-token prefill, then `steps` greedy decode steps. The prefill is timed with each Gated DeltaNet prefill
+def stack_quantization(mlp_group):
+    """The weight format of every linear of the config-5 stack as bench_stack builds it."""
+    mlp = "int8, one fp32 scale per output channel" if mlp_group == 0 else \
+        f"int8, one fp32 scale per group of {mlp_group} inputs"
+    eng = "int8, one fp32 scale per group of 128 inputs (the engine's q8 format)"
+    return {"mlp_gate_up_down": mlp, "gdn_in_out_proj": eng, "attn_qkv_o_proj": eng, "embedding_lm_head_tied": eng}
+
+
+def bench_stack(torch, q35hip, workloads, dev, steps=256, mlp_group=0, both_prefills=True):
+    """The Qwen3.5-0.8B-shaped hybrid stack (24 layers, SwiGLU 3584, tied 151,936 embedding), batch 3 steered rows:
+    2048-token prefill, then `steps` greedy decode steps. mlp_group 0: the MLP int8 per output channel (the stated
+    config-5 workload); 128: the engine's per-group format. The prefill is timed with each Gated DeltaNet prefill
     kernel (the chunked default, fp32 products on the stack's fp32 activations, and the token-serial one); decode is
     timed host-driven (eager) and as replays of one captured decode step (HIP graph)."""
     from q35hip import model as gm
     cfg = workloads.Q35Config()
-    W = workloads.init_weights(cfg, seed=0)
+    W = workloads.init_weights(cfg, seed=0, mlp_group=mlp_group)
     g = gm.HybridModel(cfg, W, dev, max_len=2048 + steps + 8, rows=3)
     del W
     prompt = torch.randint(0, cfg.vocab, (1, 2048), generator=torch.Generator().manual_seed(0)).repeat(3, 1)
@@ -281,9 +290,11 @@ def bench_stack(torch, q35hip, workloads, dev, steps=256):
     v = torch.randn(cfg.hidden, generator=torch.Generator().manual_seed(0))
     v = v / v.norm() * (0.8 * med)
     g.set_vectors(torch.stack([v, -v]), [0, -1, 1])
-    out = {"rows": 3, "prompt": 2048, "steps": steps, "steer_norm": round(float(v.norm()), 4)}
+    out = {"rows": 3, "prompt": 2048, "steps": steps, "steer_norm": round(float(v.norm()), 4),
+           "quantization": stack_quantization(mlp_group)}
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    for mode in ("recurrent", "chunk"):  # the default ("chunk") last: its states feed the decode loops
+    # the default ("chunk") last: its states feed the decode loops
+    for mode in (("recurrent", "chunk") if both_prefills else ("chunk",)):
         g.gdn_prefill = mode
         for _ in range(2):  # warm: allocator, library handles
             g.reset()
@@ -378,8 +389,9 @@ def cpu_baselines(per_case_s):
     """The oracle (PyTorch-CPU fp32 restatement of the reference path) on every workload, at all threads and at one
     thread, each a bounded sample of about per_case_s seconds: config 1 one decode step (B 1, H 16) from a state
     carried over 64 steps; config 2 the chunked rule at full size; config 3 the gated attention prefill at T 4096;
-    config 4 one decode step over 8192 keys at B 3 and B 32; config 5 the 24-layer stack at B 3: a 128-token prefill
-    (a bounded sample of the 2048-token prompt) and 4 decode steps. Returns tok/s per case."""
+    config 4 one decode step over 8192 keys at B 3 and B 32; config 5 the 24-layer stack at B 3 (MLP int8 per output
+    channel): at all threads the full workload (the 2048-token prefill and 256 greedy decode steps), at one thread a
+    bounded sample of it (a 128-token prefill and 4 decode steps). Returns tok/s per case."""
     import torch
     sys.path.insert(0, REPO)
     import oracle
@@ -394,8 +406,8 @@ def cpu_baselines(per_case_s):
     cos3, sin3 = workloads.rope_tables(8192)
     a4 = {B: workloads.attn_decode_inputs(B=B, N=8192, seed=0) for B in (3, 32)}
     cfg = workloads.Q35Config()
-    W = workloads.init_weights(cfg, seed=0)
-    prompt = torch.randint(0, cfg.vocab, (3, 128), generator=torch.Generator().manual_seed(0))
+    W = workloads.init_weights(cfg, seed=0, mlp_group=0)
+    prompt_full = torch.randint(0, cfg.vocab, (1, 2048), generator=torch.Generator().manual_seed(0)).repeat(3, 1)
     for threads in sorted({all_threads, 1}, reverse=True):
         torch.set_num_threads(threads)
         r = {}
@@ -420,15 +432,18 @@ def cpu_baselines(per_case_s):
                                   per_case_s / 2, 1)
             r[f"cfg4_attn_decode_b{B}"] = {"tok_s": B / t, "ms": t * 1e3, "calls": n}
         ref = om.OracleModel(cfg, W, steer_layer=12)
+        full = threads == all_threads
+        T, n_dec = (2048, 256) if full else (128, 4)
         t0 = time.perf_counter()
-        logits, _ = ref.forward(prompt)
+        logits, _ = ref.forward(prompt_full[:, :T])
         tp = time.perf_counter() - t0
         t0 = time.perf_counter()
-        for _ in range(4):
+        for _ in range(n_dec):
             logits, _ = ref.forward(logits.argmax(-1, keepdim=True))
-        td = (time.perf_counter() - t0) / 4
-        r["cfg5_stack_b3"] = {"prefill_tok_s": 3 * 128 / tp, "decode_tok_s": 3 / td, "prefill_ms_128": tp * 1e3,
-                              "decode_ms_per_step": td * 1e3}
+        td = (time.perf_counter() - t0) / n_dec
+        r["cfg5_stack_b3"] = {"prefill_tok_s": 3 * T / tp, "decode_tok_s": 3 / td, "prefill_tokens": T,
+                              "prefill_ms": tp * 1e3, "decode_steps": n_dec, "decode_ms_per_step": td * 1e3,
+                              "sample": "full workload" if full else "bounded sample"}
         out["threads"][str(threads)] = r
     torch.set_num_threads(all_threads)
     return out
@@ -473,8 +488,10 @@ def main():
         res["copy"] = bench_copy(torch, dev)
         print(f"# copy {res['copy']}", file=sys.stderr, flush=True)
     if want("stack"):
-        res["stack"] = bench_stack(torch, q35hip, workloads, dev)
+        res["stack"] = bench_stack(torch, q35hip, workloads, dev, mlp_group=0)
         print(f"# stack {res['stack']}", file=sys.stderr, flush=True)
+        res["stack_mlp_g128"] = bench_stack(torch, q35hip, workloads, dev, mlp_group=128, both_prefills=False)
+        print(f"# stack_mlp_g128 {res['stack_mlp_g128']}", file=sys.stderr, flush=True)
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     if not args.no_cpu and not only:

@@ -30,6 +30,7 @@
 namespace q35 {
 
 enum GemvEpi : int { kEpiStore = 0, kEpiAccumulate = 1, kEpiSwiglu = 2, kEpiConv = 3 };
+constexpr int kEpiAccumulateFixed = 4;  // entry-point code: accumulate, every output summed in one fixed order
 constexpr int kGemvConvMaxK = 8;  // conv taps supported by the conv epilogue
 constexpr int kGemvHead = 128;    // head size of the gated-norm prologue
 
@@ -510,7 +511,7 @@ struct NormArgs {
   q35::GemvAux aux;
 };
 
-template <typename TW, int EPI, int U, bool NORM, bool GS, bool GN>
+template <typename TW, int EPI, int U, bool NORM, bool GS, bool GN, int R = 4>
 void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
                    int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, int nw, int nsplit,
                    const NormArgs& na, hipStream_t st) {
@@ -519,10 +520,10 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
   constexpr int KS = 16 * WChunk<TW>::kElems;
   const int64_t spb = (K / KS + nsplit - 1) / nsplit;
   const size_t lds = (size_t)mp * spb * KS * sizeof(float);
-  const int64_t ntiles = (N + 15) / 16;
+  const int64_t ntiles = (N + 4 * R - 1) / (4 * R);
   const dim3 grid((unsigned)(ntiles < kGemvMaxBlocks ? ntiles : kGemvMaxBlocks), (unsigned)nsplit), block(64 * nw);
 #define Q35_GEMV(MP, TL)                                                                                           \
-  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS, TL, 4, GN>), grid, block, lds, st, x, ldx, W, wscale, \
+  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS, TL, R, GN>), grid, block, lds, st, x, ldx, W, wscale, \
                      y, ldy, (int)M, (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps, na.xout, na.aux)
   if constexpr (EPI == kEpiConv) {  // one tile per block (the entry point bounds N)
     switch (mp) {
@@ -554,15 +555,29 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
 
 
 // 4 waves when a block has at most 4 K steps, else 8; each wave's steps all in flight at once up to 4
+// fixed (epilogue 4, accumulate in a fixed order): no split over K; a product with too few 16-row tiles to occupy the
+// device takes 4-row tiles instead (the stack's N = 1024 products: 256 blocks), each block over all of K, so every
+// output is summed in one order whatever the run (0.6-1.4 us slower per call than the split at N = 1024, M = 3)
 template <typename TW, int EPI, bool NORM, bool GS = false, bool GN = false>
 int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, float* y, int64_t ldy, int64_t M,
                 int64_t N, int64_t K, const q35_push* pushes, int npush, int64_t T, const NormArgs& na,
-                hipStream_t st) {
+                hipStream_t st, bool fixed = false) {
   using namespace q35;
   const int64_t steps = K / (16 * WChunk<TW>::kElems);
   const int64_t nblk = (N + 15) / 16;
   int64_t nsplit = 1;
-  if (EPI == kEpiAccumulate && !NORM && nblk < kGemvSplitTarget) {
+  if (EPI == kEpiAccumulate && !NORM && fixed && nblk < kGemvSplitTarget && (N + 3) / 4 <= kGemvMaxBlocks) {
+    const int nw = steps <= 4 ? 4 : 8;
+    const int64_t per_wave = (steps + nw - 1) / nw;
+    if (per_wave <= 1)
+      gemv_launch_u<TW, EPI, 1, NORM, GS, GN, 1>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, 1, na, st);
+    else if (per_wave <= 2)
+      gemv_launch_u<TW, EPI, 2, NORM, GS, GN, 1>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, 1, na, st);
+    else
+      gemv_launch_u<TW, EPI, 4, NORM, GS, GN, 1>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, 1, na, st);
+    return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+  }
+  if (EPI == kEpiAccumulate && !NORM && !fixed && nblk < kGemvSplitTarget) {
     nsplit = (kGemvSplitTarget + nblk - 1) / nblk;
     if (nsplit > steps) nsplit = steps;
     if (nsplit > 65535) nsplit = 65535;
@@ -586,21 +601,23 @@ int gemv_dispatch(const float* x, int64_t ldx, const void* W, int w_dtype, const
                   int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes, int np,
                   int64_t T, const NormArgs& na, hipStream_t st) {
   using namespace q35;
+  const bool fx = epilogue == kEpiAccumulateFixed;
+  const bool acc = epilogue == kEpiAccumulate || fx;
   if (w_dtype == Q35_I8_G128) {
     const int8_t* w8 = (const int8_t*)W;
     if (epilogue == kEpiStore) return gemv_launch<int8_t, kEpiStore, NORM, true>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
-    if (epilogue == kEpiAccumulate) return gemv_launch<int8_t, kEpiAccumulate, NORM, true>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+    if (acc) return gemv_launch<int8_t, kEpiAccumulate, NORM, true>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st, fx);
     return gemv_launch<int8_t, kEpiSwiglu, NORM, true>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
   }
   if (w_dtype == Q35_I8) {
     const int8_t* w8 = (const int8_t*)W;
     if (epilogue == kEpiStore) return gemv_launch<int8_t, kEpiStore, NORM>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
-    if (epilogue == kEpiAccumulate) return gemv_launch<int8_t, kEpiAccumulate, NORM>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+    if (acc) return gemv_launch<int8_t, kEpiAccumulate, NORM>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st, fx);
     return gemv_launch<int8_t, kEpiSwiglu, NORM>(x, ldx, w8, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
   }
   const float* wf = (const float*)W;
   if (epilogue == kEpiStore) return gemv_launch<float, kEpiStore, NORM>(x, ldx, wf, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
-  if (epilogue == kEpiAccumulate) return gemv_launch<float, kEpiAccumulate, NORM>(x, ldx, wf, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
+  if (acc) return gemv_launch<float, kEpiAccumulate, NORM>(x, ldx, wf, w_scale, y, ldy, M, N, K, pushes, np, T, na, st, fx);
   return gemv_launch<float, kEpiSwiglu, NORM>(x, ldx, wf, w_scale, y, ldy, M, N, K, pushes, np, T, na, st);
 }
 
@@ -614,7 +631,9 @@ int gemv_check(const float* x, int64_t ldx, const void* W, int w_dtype, const fl
   if (w_dtype == Q35_I8_G128 && !w_scale) return Q35_EINVAL;
   if (npush < 0 || (npush > 0 && !pushes)) return Q35_EINVAL;
   if (epilogue == kEpiSwiglu ? (N & 1) || ldy < N / 2 : ldy < N) return Q35_EINVAL;
-  if (epilogue != kEpiStore && epilogue != kEpiAccumulate && epilogue != kEpiSwiglu) return Q35_EINVAL;
+  if (epilogue != kEpiStore && epilogue != kEpiAccumulate && epilogue != kEpiSwiglu &&
+      epilogue != kEpiAccumulateFixed)
+    return Q35_EINVAL;
   if (w_dtype != Q35_I8 && w_dtype != Q35_I8_G128 && w_dtype != Q35_F32) return Q35_EUNSUPPORTED;
   if (M > 8 || (K % 256) != 0 || (ldx & 3) || ((uintptr_t)x & 15) || ((uintptr_t)W & 15)) return Q35_EUNSUPPORTED;
   const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 3 ? 3 : M <= 4 ? 4 : 8;
@@ -701,7 +720,10 @@ extern "C" int q35_gemv_gated_norm(const float* o, int64_t ldo, const float* z, 
   using namespace q35;
   const int chk = gemv_check(o, ldo, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, nullptr, 0, 1);
   if (chk != Q35_OK) return chk;
-  if (!z || !norm_w || ldz < K || (epilogue != kEpiStore && epilogue != kEpiAccumulate)) return Q35_EINVAL;
+  if (!z || !norm_w || ldz < K ||
+      (epilogue != kEpiStore && epilogue != kEpiAccumulate && epilogue != kEpiAccumulateFixed))
+    return Q35_EINVAL;
+  const bool fx = epilogue == kEpiAccumulateFixed;
   // the prologue normalises whole heads of 128 inputs: int8 weights (K steps of 256) keep every split head-aligned
   if (w_dtype == Q35_F32) return Q35_EUNSUPPORTED;
   if ((ldz & 3) || ((uintptr_t)z & 15) || ((uintptr_t)norm_w & 15)) return Q35_EUNSUPPORTED;
@@ -716,13 +738,13 @@ extern "C" int q35_gemv_gated_norm(const float* o, int64_t ldo, const float* z, 
       return gemv_launch<int8_t, kEpiStore, false, true, true>(o, ldo, w8, w_scale, y, ldy, M, N, K, nullptr, 0, 1,
                                                                na, st);
     return gemv_launch<int8_t, kEpiAccumulate, false, true, true>(o, ldo, w8, w_scale, y, ldy, M, N, K, nullptr, 0, 1,
-                                                                  na, st);
+                                                                  na, st, fx);
   }
   if (epilogue == kEpiStore)
     return gemv_launch<int8_t, kEpiStore, false, false, true>(o, ldo, w8, w_scale, y, ldy, M, N, K, nullptr, 0, 1, na,
                                                               st);
   return gemv_launch<int8_t, kEpiAccumulate, false, false, true>(o, ldo, w8, w_scale, y, ldy, M, N, K, nullptr, 0, 1,
-                                                                 na, st);
+                                                                 na, st, fx);
 }
 
 extern "C" int q35_swiglu_push(const float* gu, float* a, int64_t M, int64_t I, const q35_push* pushes,

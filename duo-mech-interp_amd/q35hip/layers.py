@@ -52,7 +52,7 @@ def rmsnorm_1p(x, w, eps=1e-6):
 
 
 def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_heads=None, head_k_dim=None,
-                         eps=1e-6, prefill="chunk", prenorm=None, residual=None):
+                         eps=1e-6, prefill="chunk", prenorm=None, residual=None, fixed_order=False):
     """Gated DeltaNet mixer of one decoder layer (Qwen3_5GatedDeltaNet.forward, HF:432-543; the WGSL conv + delta
     kernels, engine/kernels_qwen35.js:127-247). x: [B, T, H] fp32 (the input-normed residual). A call with T == 1
     is one recurrent decode step (HF:505-517). T > 1 runs from rec_state either the chunked prefill (HF:518-530;
@@ -63,7 +63,8 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     the residual and the layer's input norm runs inside the input projection). Returns y [B, T, H], or with
     residual [B, T, H] given, residual + y computed in place by the output projection (then returned). For T > 1,
     x may be the int32 words of the normed rows already split for the int8 GEMM (add_rmsnorm_(..., split=True);
-    the layer must then have int8 input projections)."""
+    the layer must then have int8 input projections). fixed_order: the decode step's residual add sums every output
+    in one fixed order (repeatable bits; see linear())."""
     if prefill not in ("chunk", "recurrent"):
         raise ValueError(f"gated_deltanet_layer: prefill must be 'chunk' or 'recurrent', not {prefill!r}")
     B, T, _ = x.shape
@@ -78,7 +79,8 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     wq_in, ws_in = _q8(p, "_in_fused")
     wq_out, ws_out = _q8(p, "out_proj")
     if (T == 1 and Hk == Hv and dk == dv == 128 and x.dtype == torch.float32 and B <= 8 and x.shape[-1] % 256 == 0
-            and Vd % 256 == 0 and wq_in is not None and wq_out is not None):
+            and Vd % 256 == 0 and wq_in is not None and wq_out is not None
+            and wq_in.shape[0] <= ops.GEMV_CONV_MAX_N and p["conv1d"].shape[-1] <= ops.GEMV_CONV_MAX_K):
         # decode step on int8 projections: the causal conv + SiLU in the input projection's epilogue (each channel
         # has one owner there, so its conv state advances in place), the recurrent rule over four blocks per head,
         # and the gated RMSNorm in the output projection's staging (the same arithmetic as the fused step below)
@@ -88,7 +90,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
         N = wq_out.shape[0]
         out = residual.view(B, N) if residual is not None else torch.empty(B, N, dtype=torch.float32, device=x.device)
         ops.gemv_gated_norm(o, y2[:, C:], p["norm"], wq_out, ws_out, out, head_scale=head_scale, eps=eps,
-                            epilogue="store" if residual is None else "add")
+                            epilogue="store" if residual is None else ("add_fixed" if fixed_order else "add"))
         return residual if residual is not None else out.view(B, 1, N)
     y = linear(x, w_in, wq_in, ws_in, prenorm=prenorm)
     if T == 1 and Hk == Hv and dk == dv == 128 and x.dtype == torch.float32:
@@ -97,7 +99,8 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
         o = ops.gdn_decode_fused_(y.view(B, y.shape[-1]), p["conv1d"], conv_state, p["A_log"], p["dt_bias"],
                                   rec_state, p["norm"], b_off=C + Vd, a_off=C + Vd + Hv, z_off=C,
                                   head_scale=head_scale, eps=eps)
-        return linear(o.view(B, 1, Vd), p["out_proj"], *_q8(p, "out_proj"), residual=residual)
+        return linear(o.view(B, 1, Vd), p["out_proj"], *_q8(p, "out_proj"), residual=residual,
+                      fixed_order=fixed_order)
     if (T > 1 and prefill == "chunk" and _act_dtype(x) == torch.float32 and dk == dv == 128
             and p["conv1d"].shape[-1] == 4 and rec_state.is_contiguous()):
         # the conv + SiLU, l2 norms and gate terms in the chunk kernel's load phase (q, k, v, g, beta never written
@@ -136,7 +139,7 @@ def prenorm_torch(x, prenorm):
     return ops.add_rmsnorm_(s, None, nw, eps)
 
 
-def linear(x, w, wq=None, ws=None, prenorm=None, residual=None, conv=None):
+def linear(x, w, wq=None, ws=None, prenorm=None, residual=None, conv=None, fixed_order=False):
     """x [..., K] @ w[N, K]^T in fp32: the HIP GEMV for a few rows (decode), on the int8 weights wq with scales ws
     ([N, K / 128] per group or [N] per row; w their dequantised values) when given, else on w; for more rows the HIP
     int8 GEMM on wq (fp32-accurate) when given, else a torch GEMM on w. prenorm = (x_add, norm_w, eps, x_out): x is
@@ -145,11 +148,14 @@ def linear(x, w, wq=None, ws=None, prenorm=None, residual=None, conv=None):
     into it in place (the decoder layer's residual add after its mixer) and residual is returned. conv =
     (conv_w, conv_bias, conv_state): the GEMV with prenorm runs the GDN causal conv + SiLU on the first
     conv_w.shape[0] outputs and advances conv_state (decode only: raises when the product is not a GEMV). x may be the
-    int32 words of split activations (ops.split_activations) when wq is given: the int8 GEMM reads them as they are."""
+    int32 words of split activations (ops.split_activations) when wq is given: the int8 GEMM reads them as they are.
+    fixed_order (with residual): the decode GEMV sums every output in one fixed order (the "add_fixed" epilogue:
+    repeatable bits) instead of splitting K over blocks that add with atomics; the GEMM's sums are always in a fixed
+    order."""
     K = x.shape[-1]
     M = x.numel() // K
     N = (wq if wq is not None else w).shape[0]
-    out, epi = (None, "store") if residual is None else (residual.view(M, N), "add")
+    out, epi = (None, "store") if residual is None else (residual.view(M, N), "add_fixed" if fixed_order else "add")
     if M <= 8 and K % 256 == 0 and x.dtype == torch.float32 and (wq is not None or w.dtype == torch.float32):
         xm = x.reshape(M, K).contiguous()
         pn = None
@@ -165,7 +171,7 @@ def linear(x, w, wq=None, ws=None, prenorm=None, residual=None, conv=None):
     if prenorm is not None:
         x = prenorm_torch(x, prenorm)
     if wq is not None and K % 64 == 0 and x.dtype in (torch.float32, torch.int32, torch.bfloat16):
-        y = ops.gemm_q8(x.reshape(M, K), wq, ws, out=out, epilogue=epi)
+        y = ops.gemm_q8(x.reshape(M, K), wq, ws, out=out, epilogue="add" if epi == "add_fixed" else epi)
         return residual if residual is not None else y.view(*x.shape[:-1], N)
     if x.dtype == torch.int32:
         raise ValueError("linear: split activations need the int8 GEMM (int8 weights, K a multiple of 64)")
@@ -204,7 +210,7 @@ def attn_in_weight(p):
 
 
 def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partial_rotary_factor=0.25, eps=1e-6,
-                          cache_len=None, prenorm=None, residual=None):
+                          cache_len=None, prenorm=None, residual=None, fixed_order=False):
     """Gated softmax attention mixer of one decoder layer (Qwen3_5Attention.forward, HF:656-701; WGSL attnPrep +
     attention, engine/kernels_qwen35.js:18-123). x: [B, T, H] fp32; the T tokens sit at positions pos..pos+T-1,
     pos a Python int or a [B] int32 device tensor (per row; a device tensor keeps the call capturable in a HIP
@@ -214,7 +220,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     max_len must then be a multiple of 64); T == 1 the split-K decode over cache positions 0..pos (cache_len:
     optional [B] int32 per-row lengths, default pos + 1). prenorm: see linear(). For T > 1, x may be the int32 words
     of split activations (see gated_deltanet_layer). Returns y [B, T, H], or with residual [B, T, H] given,
-    residual + y computed in place by o_proj (then returned)."""
+    residual + y computed in place by o_proj (then returned). fixed_order: see linear()."""
     B, T, _ = x.shape
     D = p["q_norm"].numel()
     Hq = p["q_proj"].shape[0] // (2 * D)
@@ -245,7 +251,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     wq_o, ws_o = _q8(p, "o_proj")
     # bf16 o straight into the int8 GEMM (the product of o.float(), bitwise); fp32 for the other forms
     xo = o if (T > 1 and wq_o is not None and o.shape[-1] % 64 == 0) else o.float()
-    return linear(xo, p["o_proj"], wq_o, ws_o, residual=residual)
+    return linear(xo, p["o_proj"], wq_o, ws_o, residual=residual, fixed_order=fixed_order)
 
 
 def residual_steer_add(x, vecs, rows=None):

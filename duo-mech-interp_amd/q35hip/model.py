@@ -63,7 +63,7 @@ def _split_ok(p, names, x):
     return x.shape[-1] % 64 == 0 and all(n + ".q" in p for n in names)
 
 
-def mlp(p, h, x, prenorm=None, capture=None):
+def mlp(p, h, x, prenorm=None, capture=None, fixed_order=False):
     """x += SwiGLU MLP (HF:704-717) of h, in place, with the layer's neuron pushes at the down_proj input
     (engine/model.js:7-9, engine/kernels_qwen35.js:250-279). Decode (at most 8 rows, int8 weights present): one GEMV
     over the interleaved int8 gate/up rows with the SwiGLU + push epilogue, and one int8 GEMV accumulating down_proj
@@ -74,7 +74,8 @@ def mlp(p, h, x, prenorm=None, capture=None):
     first GEMV on the decode path). h may be the int32 words of split activations (add_rmsnorm_(..., split=True)) when
     the layer has int8 weights: the gate/up GEMM reads them as they are. capture: an fp32 view [rows, T, I] (unit
     neuron stride) that receives the post-push activations, the down_proj input (the engine's capture hook,
-    engine/model.js:9, :451-453), written by the SwiGLU epilogue itself. Returns x."""
+    engine/model.js:9, :451-453), written by the SwiGLU epilogue itself. fixed_order: the decode down_proj sums
+    every output in one fixed order (repeatable bits; layers.linear). Returns x."""
     mlp_weights(p)
     H = h.shape[-1]
     M = h.numel() // H
@@ -87,7 +88,8 @@ def mlp(p, h, x, prenorm=None, capture=None):
                                        None if pn[3] is None else x.view(M, H))
         a = ops.gemv(h.reshape(M, H), p["_gu_q8"], p["_gu_s"], epilogue="swiglu", pushes=p["_pushes"], T=T,
                      prenorm=pn2, capture=capture)
-        ops.gemv(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H), epilogue="add")
+        ops.gemv(a, p["down_proj.q"], p["down_proj.s"], out=x.view(M, H),
+                 epilogue="add_fixed" if fixed_order else "add")
         return x
     if pn is not None:
         h = layers.prenorm_torch(h, pn)
@@ -119,15 +121,22 @@ class HybridModel:
     prefilled in several calls (engine/model.js:486-491): a multi-token call past position 0 attends over the KV
     cache. Positions live on the device (pos_dev, [rows] int32) and the steering vectors in fixed buffers, so a
     decode step has no host-dependent arguments: enable_decode_graph() captures one step in a HIP graph that
-    decode_step() replays."""
+    decode_step() replays.
+
+    deterministic: the decode step's residual adds (the mixers' output projections and down_proj) sum every output
+    in one fixed order, so that two runs give identical logits bit for bit; by default these N = hidden products
+    split K over four blocks that add with fp32 atomics (faster; the last bits of a step may vary between runs).
+    Prefill is deterministic either way."""
 
     MAX_VECS = 4  # vector rows of the steering buffer (the WGSL resAdd clamps its row index to 3, engine/kernels.js:201)
 
-    def __init__(self, cfg, W, device, max_len=4096, rows=3, steer_layer=12, gdn_prefill="chunk"):
+    def __init__(self, cfg, W, device, max_len=4096, rows=3, steer_layer=12, gdn_prefill="chunk",
+                 deterministic=False):
         if gdn_prefill not in ("chunk", "recurrent"):
             raise ValueError(f"HybridModel: gdn_prefill must be 'chunk' or 'recurrent', not {gdn_prefill!r}")
         self.cfg, self.device, self.steer_layer = cfg, device, steer_layer
         self.gdn_prefill = gdn_prefill
+        self.deterministic = bool(deterministic)
         self.W = W if isinstance(W, Q35Weights) else Q35Weights(W, device)
         # the KV caches hold a multiple of 64 positions (the multi-token attention over the cache reads 64-key tiles)
         self.max_len, self.rows = (max_len + 63) // 64 * 64, rows
@@ -259,6 +268,7 @@ class HybridModel:
                 res_buf[l, :, res_t0:res_t0 + T].copy_(x.view(res_buf.shape[1], T, -1))
         pos_dev, vec_rows = self.pos_dev[rs], self.vec_rows[rs]
         if T == 1:
+            fx = self.deterministic
             cache_len = self.len_dev[rs]  # shared by the attention layers
             for l in range(last + 1):
                 p = self.params[l]
@@ -267,13 +277,14 @@ class HybridModel:
                 if cfg.is_attention(l):
                     layers.gated_attention_layer(x, p, st["k"], st["v"], pos_dev, rope_theta=cfg.rope_theta,
                                                  partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps,
-                                                 cache_len=cache_len, prenorm=pre, residual=x)
+                                                 cache_len=cache_len, prenorm=pre, residual=x, fixed_order=fx)
                 else:
                     layers.gated_deltanet_layer(x, p, st["conv"], st["rec"], p["_head_scale"],
                                                 num_k_heads=cfg.lin_k_heads, head_k_dim=cfg.lin_dk, eps=cfg.eps,
-                                                prefill=self.gdn_prefill, prenorm=pre, residual=x)
+                                                prefill=self.gdn_prefill, prenorm=pre, residual=x, fixed_order=fx)
                 snap(l, "mixer")
-                mlp(p, x, x, prenorm=(None, p["post_attention_layernorm"], cfg.eps), capture=cap_view(l))
+                mlp(p, x, x, prenorm=(None, p["post_attention_layernorm"], cfg.eps), capture=cap_view(l),
+                    fixed_order=fx)
                 if l == self.steer_layer and steer:
                     layers.residual_steer_add(x, self.vec_buf, vec_rows)
                 snap(l, "layer")

@@ -405,7 +405,10 @@ def _attn_prep_impl(y, q_norm_w, k_norm_w, eps, cos, sin, pos, k_cache, v_cache,
 
 
 # ---------------------------------------------------------------- decode matrix-vector products, SwiGLU hook
-_EPI = {"store": 0, "add": 1, "swiglu": 2}
+# limits of the conv epilogue of the decode GEMV (q35_gemv_norm_conv): output rows and conv taps
+GEMV_CONV_MAX_N, GEMV_CONV_MAX_K = 16384, 8
+# "add_fixed": accumulate with every output summed in one fixed order (repeatable bits; no split over K)
+_EPI = {"store": 0, "add": 1, "swiglu": 2, "add_fixed": 4}
 
 
 def _pushes_check(pushes):
@@ -844,8 +847,10 @@ def pack_pushes(pushes, device):
 def gemv(x, W, w_scale=None, out=None, epilogue="store", pushes=None, T=1, prenorm=None, conv=None, capture=None):
     """y[m, n] = sum_k x[m, k] W[n, k] s(n, k) for M <= 8 rows (decode): W int8 with scales w_scale [N, K / 128]
     (one per group of 128 inputs, the engine's q8 format) or [N] (one per row), or fp32 W (w_scale None).
-    epilogue "store" writes out, "add" accumulates into out (a residual add), "swiglu" treats W's rows as
-    interleaved (gate, up) pairs and writes silu(gate) * up with the neuron pushes (pack_pushes) applied.
+    epilogue "store" writes out, "add" accumulates into out (a residual add; products with few output rows split K
+    and add with fp32 atomics, so the last bits may vary between runs), "add_fixed" accumulates with every output
+    summed in one fixed order (repeatable bits), "swiglu" treats W's rows as interleaved (gate, up) pairs and writes
+    silu(gate) * up with the neuron pushes (pack_pushes) applied.
     prenorm = (x_add, norm_w, eps, x_out): x is then a residual; the product takes the RMSNorm (1 + w) of
     s = x + x_add (x_add may be None), and s is written to x_out when it is not None (q35_gemv_norm).
     conv = (conv_w [C, K], conv_bias or None, conv_state [M, K - 1, C]), with prenorm and the store epilogue: outputs

@@ -141,14 +141,16 @@ def dequantize_int8(q, s):
     return (q.float().reshape(N, s.shape[1], -1) * s.float()[:, :, None]).reshape(N, K)
 
 
-def init_weights(cfg: Q35Config, seed=0, int8_all=True, group=QG):
+def init_weights(cfg: Q35Config, seed=0, int8_all=True, group=QG, mlp_group=None):
     """Deterministic random init (seeded): normal(0, init_std) for every linear, the conv and the tied embedding;
     decoder / q / k RMSNorm weights 0 (gain 1 + w = 1) and the gated norm weight 1 (HF:171, HF:813-820);
     dt_bias = 1; A_log = log U(0, 16).
 
     Every linear layer and the tied embedding are int8 with fp32 scales, as the engine quantizes the checkpoint on
     load (engine/model.js:3-5, :70-100): one scale per group of `group` inputs (the engine's 128), or per output row
-    with group 0. MLP weights are stored as "<name>.q" / "<name>.s" only; the
+    with group 0. The MLP weights take `mlp_group` instead when it is given (0: int8 per output channel, the MLP
+    format the config-5 workload states, with the other linears in the engine's format). MLP weights are stored as
+    "<name>.q" / "<name>.s" only; the
     other linears and the embedding (int8_all) keep "<name>.q" / "<name>.s" beside "<name>" = the dequantised fp32
     values, so a consumer that reads "<name>" (the CPU oracle, torch GEMMs) computes with exactly the numbers the int8
     decode GEMVs use."""
@@ -191,7 +193,7 @@ def init_weights(cfg: Q35Config, seed=0, int8_all=True, group=QG):
             W[p + "norm"] = torch.ones(cfg.lin_dv)
             put(W, p + "out_proj", lin(H, vd))
         for name, (o, i) in (("gate_proj", (cfg.inter, H)), ("up_proj", (cfg.inter, H)), ("down_proj", (H, cfg.inter))):
-            q, s = quantize_int8(lin(o, i), group)
+            q, s = quantize_int8(lin(o, i), group if mlp_group is None else mlp_group)
             W[p + name + ".q"] = q
             W[p + name + ".s"] = s
     return W

@@ -331,6 +331,9 @@ int q35_add_rmsnorm_split(float* x, int64_t ldx, const float* y, int64_t ldy, co
  *   with npush 0); T: tokens per sequence row (the push row is min(m / T, 3)).
  *   Epilogue 1 with fewer than 256 blocks of 16 output rows splits K over several blocks that add their sums into
  *   y with fp32 atomics: the order of those additions, and so the last bits of y, may differ between calls.
+ *   Epilogue 4 is epilogue 1 with every output summed in one fixed order (no split over K: a product with fewer
+ *   than 256 blocks of 16 rows takes blocks of 4 rows instead), so that repeated calls give identical bits; it is
+ *   the deterministic form of the decode step's residual adds (the engine's matvec sums in a fixed order).
  *   cap: the neuron activation capture of the MLP hook (engine/model.js:9, :451-453; the `cap` binding of
  *   engine/kernels_qwen35.js:251-279, its capOff folded into the pointer), NULL for none, epilogue 2 only: the
  *   activation of neuron j of row m (after the pushes, as y holds it) is also written to
@@ -373,7 +376,8 @@ int q35_gemv_norm_conv(const float* x, const float* x_add, float* x_out, int64_t
  * head_scale[h], in the order of q35_gdn_decode_fused's norm, then y (epilogue 0) = or (epilogue 1) += x W^T s.
  *   o: [M, ldo] fp32 (16-byte aligned), K = H 128 inputs; z: [M, ldz] fp32 (16-byte aligned, ldz a multiple of 4),
  *   head h's gate at columns 128 h .. 128 h + 127; norm_w: [128] fp32; head_scale: [H] or NULL. int8 weights only
- *   (Q35_I8 or Q35_I8_G128). Everything else as q35_gemv (including the split-K accumulation of epilogue 1).
+ *   (Q35_I8 or Q35_I8_G128). epilogue 0, 1 or 4; everything else as q35_gemv (including the split-K accumulation
+ *   of epilogue 1 and the fixed order of epilogue 4).
  */
 int q35_gemv_gated_norm(const float* o, int64_t ldo, const float* z, int64_t ldz, const float* norm_w,
                         const float* head_scale, float eps, const void* W, int w_dtype, const float* w_scale,

@@ -135,6 +135,7 @@ def test_validation_rejects_without_launching():
     assert L.q35_gated_rmsnorm_split(fake, fake, 2048, fake, None, fake, 3, 16, 64, 1e-6, None) == 2
     # activation capture: only with the SwiGLU epilogues, neuron strides of at least N / 2, 4-byte aligned
     assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 64, 1024, 0, None, 0, 1, fake, 64, 64, None) == 1
+    assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 64, 1024, 5, None, 0, 1, None, 0, 0, None) == 1
     assert L.q35_gemv(fake, 1024, fake, 2, fake, fake, 64, 3, 64, 1024, 2, None, 0, 1, fake, 31, 64, None) == 1
     assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 1, None, 0, 1, fake, 64, 64, None) == 1
     assert L.q35_gemm_q8(fake, 1024, fake, 3, fake, fake, 64, 100, 64, 1024, 2, None, 0, 1, fake, 32, 31, None) == 1

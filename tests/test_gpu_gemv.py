@@ -173,3 +173,52 @@ def test_gemv_group_scales_swiglu_with_pushes(I):
     a = ops.gemv(x.to(dev), Wi.to(dev), si.to(dev), epilogue="swiglu", pushes=ops.pack_pushes(pushes, dev))
     torch.cuda.synchronize()
     assert oracle.rel_err(a.cpu(), ref) <= TOL
+
+
+@pytest.mark.parametrize("gs", [True, False])
+@pytest.mark.parametrize("M,N,K", [(3, 1024, 3584), (1, 1024, 2048), (8, 1000, 2048), (3, 4096, 1024)])
+def test_gemv_fixed_order_accumulate_is_repeatable(gs, M, N, K):
+    """The "add_fixed" epilogue (every output summed in one order: 4-row blocks over all of K where the split-K form
+    would split) agrees with the oracle's int8 product and with the split "add" form to fp32 rounding, and two calls
+    from the same residual give bitwise the same result."""
+    dev = device()
+    g = torch.Generator().manual_seed(N + K + M)
+    w = torch.randn(N, K, generator=g) * 0.02
+    W, s = omlp.q8_quantize(w) if gs else _weights(N, K, torch.int8, seed=N + K)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)) * 2.0
+    base = torch.randn(M, N, generator=torch.Generator().manual_seed(9))
+    ref = base + omlp.q8_linear(x, W, s)
+    announce(f"gemv add_fixed M{M} N{N} K{K} gs {gs}")
+    Wd, sd, xd = W.to(dev), s.to(dev), x.to(dev)
+    outs = []
+    for epi in ("add_fixed", "add_fixed", "add"):
+        acc = base.to(dev)
+        ops.gemv(xd, Wd, sd, out=acc, epilogue=epi)
+        outs.append(acc)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert oracle.rel_err(outs[0].cpu(), ref) <= TOL
+    assert oracle.rel_err(outs[2].cpu(), outs[0].cpu()) <= TOL
+
+
+def test_gemv_gated_norm_fixed_order_is_repeatable():
+    """The GDN output projection with its gated-norm prologue, "add_fixed" against "add" (rounding) and itself
+    (bitwise)."""
+    dev = device()
+    M, K, N = 3, 2048, 1024
+    g = torch.Generator().manual_seed(3)
+    W, s = omlp.q8_quantize(torch.randn(N, K, generator=g) * 0.02)
+    o = torch.randn(M, K, generator=g).to(dev)
+    z = torch.randn(M, K, generator=g).to(dev)
+    nw = (1.0 + 0.1 * torch.randn(128, generator=g)).to(dev)
+    hs = torch.rand(K // 128, generator=g).to(dev)
+    base = torch.randn(M, N, generator=g).to(dev)
+    announce("gemv_gated_norm add_fixed")
+    outs = []
+    for epi in ("add_fixed", "add_fixed", "add"):
+        acc = base.clone()
+        ops.gemv_gated_norm(o, z, nw, W.to(dev), s.to(dev), acc, head_scale=hs, epilogue=epi)
+        outs.append(acc)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert oracle.rel_err(outs[2].cpu(), outs[0].cpu()) <= TOL
