@@ -246,6 +246,40 @@ def bench_gemm(torch, q35hip, steps, warmup, dev, M=6144):
     return out
 
 
+GEMV_SHAPES = (("mlp_gate_up_norm_swiglu", 7168, 1024, "swiglu", True), ("mlp_down_add", 1024, 3584, "add", False),
+               ("gdn_in_proj_norm", 8224, 1024, "store", True), ("lm_head_norm", 151936, 1024, "store", True))
+
+
+def bench_gemv(torch, q35hip, steps, warmup, dev):
+    """The decode GEMV (int8 weights with one scale per group of 128 inputs) on the stack's decode shapes at 1, 3 and
+    8 rows of x: weights rotated over enough copies to leave the Infinity Cache, so GB/s is HBM; 'add' is the split-K
+    residual accumulation, the norm forms read the residual and apply the RMSNorm prologue."""
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, N, K, epi, norm in GEMV_SHAPES:
+        wbytes = N * K + N * (K // 128) * 4
+        n = n_sets_for(wbytes, cap=24)
+        qs = [torch.randint(-127, 128, (N, K), device=dev, generator=g, dtype=torch.int8) for _ in range(n)]
+        ss = [torch.rand(N, K // 128, device=dev, generator=g) * 1e-3 for _ in range(n)]
+        nw = torch.rand(K, device=dev, generator=g) * 0.1
+        pushes = q35hip.ops.pack_pushes([(0, "add", [0.0])], dev) if epi == "swiglu" else None
+        for M in (1, 3, 8):
+            if M * K * 4 > 64 * 1024:  # x is staged in 64 KiB of LDS (q35_gemv's limit)
+                continue
+            x = torch.randn(M, K, device=dev, generator=g)
+            y = torch.zeros(M, N // 2 if epi == "swiglu" else N, device=dev)
+            pn = (None, nw, 1e-6, None) if norm else None
+
+            def make_call(i, x=x, y=y, pn=pn):
+                return lambda: q35hip.ops.gemv(x, qs[i], ss[i], out=y, epilogue=epi, pushes=pushes, prenorm=pn)
+            r = Timer(torch, make_call, n, reps=n).run(steps, warmup)
+            t = r["step_s"]
+            out[f"{name}_m{M}"] = {"M": M, "N": N, "K": K, "us": t * 1e6, "gbs": wbytes / t / 1e9,
+                                   "frac_hbm": wbytes / t / 1e9 / PEAK_HBM_GBS}
+        del qs, ss
+    return out
+
+
 def bench_copy(torch, dev, mb=256, reps=5):
     """A plain device copy of known size (mb MiB read + mb MiB written per launch): the calibration point for the
     FETCH_SIZE / WRITE_SIZE counters of a profiler run."""
@@ -484,6 +518,9 @@ def main():
     if want("gemm"):
         res["gemm"] = bench_gemm(torch, q35hip, args.steps, args.warmup, dev)
         print(f"# gemm {res['gemm']}", file=sys.stderr, flush=True)
+    if want("gemv"):
+        res["gemv"] = bench_gemv(torch, q35hip, args.steps, args.warmup, dev)
+        print(f"# gemv {res['gemv']}", file=sys.stderr, flush=True)
     if only and "copy" in only:
         res["copy"] = bench_copy(torch, dev)
         print(f"# copy {res['copy']}", file=sys.stderr, flush=True)

@@ -437,7 +437,7 @@ extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const v
 // array: calls that overlap on one device race. Nothing in it needs clearing between calls: every partial the merge
 // reads is written by the same call's first kernel (an empty split writes max -inf, sum 0).
 namespace q35 {
-constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+constexpr size_t kNoAllocScratchBytes = (size_t)9 << 20;
 constexpr int kMaxDevices = 64;
 static std::atomic<void*> g_scratch_ptr[kMaxDevices];
 static std::mutex g_scratch_mu;

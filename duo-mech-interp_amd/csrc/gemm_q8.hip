@@ -36,7 +36,9 @@
 // straight into the planes its A fragments are read from (no fp32 stage, no conversion pass), the register-staged
 // kernel stores the loaded pieces as they are. The products, and so y, are bitwise those of the fp32 input.
 // bf16 input (q35_gemm_q8_bf16, the attention output): hi = x exactly and lo = 0, so the register-staged kernel
-// issues only the hi products (bitwise those of the fp32 input x.float(): the skipped products are exact zeros).
+// issues only the hi products (the skipped products are exact zeros): bitwise the product of x.float() wherever the
+// fp32 input also runs the register-staged kernel (N < 2048 or K > 2048); for the wide shapes the fp32 input runs the
+// DMA kernel, whose MFMAs group K differently, and the two agree to fp32 rounding.
 #include <type_traits>
 
 #include "q35_common.h"

@@ -520,18 +520,22 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
   constexpr int KS = 16 * WChunk<TW>::kElems;
   const int64_t spb = (K / KS + nsplit - 1) / nsplit;
   const size_t lds = (size_t)mp * spb * KS * sizeof(float);
-  const int64_t ntiles = (N + 4 * R - 1) / (4 * R);
+  // 8 rows of x: tiles of 8 output rows (R 2), so that the accumulators and weight registers fit without spilling
+  constexpr int R8 = R > 2 ? 2 : R;
+  const int re = mp == 8 ? R8 : R;
+  const int64_t ntiles = (N + 4 * re - 1) / (4 * re);
   const dim3 grid((unsigned)(ntiles < kGemvMaxBlocks ? ntiles : kGemvMaxBlocks), (unsigned)nsplit), block(64 * nw);
 #define Q35_GEMV(MP, TL)                                                                                           \
-  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS, TL, R, GN>), grid, block, lds, st, x, ldx, W, wscale, \
-                     y, ldy, (int)M, (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps, na.xout, na.aux)
+  hipLaunchKernelGGL((gemv_kernel<TW, MP, EPI, U, NORM, GS, TL, (MP == 8 ? R8 : R), GN>), grid, block, lds, st, x, \
+                     ldx, W, wscale, y, ldy, (int)M, (int)N, (int)K, pushes, npush, (int)T, na.xadd, na.nw, na.eps,   \
+                     na.xout, na.aux)
   if constexpr (EPI == kEpiConv) {  // one tile per block (the entry point bounds N)
     switch (mp) {
       case 1: Q35_GEMV(1, false); break;
       case 2: Q35_GEMV(2, false); break;
       case 3: Q35_GEMV(3, false); break;
       case 4: Q35_GEMV(4, false); break;
-      default: Q35_GEMV(8, false); break;
+      default: if constexpr (U <= 2) Q35_GEMV(8, false); break;  // 8 rows: U <= 2 (gemv_launch)
     }
   } else if (ntiles > kGemvMaxBlocks) {
     switch (mp) {
@@ -539,7 +543,7 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
       case 2: Q35_GEMV(2, true); break;
       case 3: Q35_GEMV(3, true); break;
       case 4: Q35_GEMV(4, true); break;
-      default: Q35_GEMV(8, true); break;
+      default: if constexpr (U <= 2) Q35_GEMV(8, true); break;  // 8 rows: U <= 2 (gemv_launch)
     }
   } else {
     switch (mp) {
@@ -547,7 +551,7 @@ void gemv_launch_u(const float* x, int64_t ldx, const TW* W, const float* wscale
       case 2: Q35_GEMV(2, false); break;
       case 3: Q35_GEMV(3, false); break;
       case 4: Q35_GEMV(4, false); break;
-      default: Q35_GEMV(8, false); break;
+      default: if constexpr (U <= 2) Q35_GEMV(8, false); break;  // 8 rows: U <= 2 (gemv_launch)
     }
   }
 #undef Q35_GEMV
@@ -566,12 +570,12 @@ int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, f
   const int64_t steps = K / (16 * WChunk<TW>::kElems);
   const int64_t nblk = (N + 15) / 16;
   int64_t nsplit = 1;
-  if (EPI == kEpiAccumulate && !NORM && fixed && nblk < kGemvSplitTarget && (N + 3) / 4 <= kGemvMaxBlocks) {
+  if constexpr (EPI == kEpiAccumulate && !NORM) if (fixed && nblk < kGemvSplitTarget && (N + 3) / 4 <= kGemvMaxBlocks) {
     const int nw = steps <= 4 ? 4 : 8;
     const int64_t per_wave = (steps + nw - 1) / nw;
     if (per_wave <= 1)
       gemv_launch_u<TW, EPI, 1, NORM, GS, GN, 1>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, 1, na, st);
-    else if (per_wave <= 2)
+    else if (per_wave <= 2 || M > 4)
       gemv_launch_u<TW, EPI, 2, NORM, GS, GN, 1>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, 1, na, st);
     else
       gemv_launch_u<TW, EPI, 4, NORM, GS, GN, 1>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, 1, na, st);
@@ -587,9 +591,12 @@ int gemv_launch(const float* x, int64_t ldx, const TW* W, const float* wscale, f
   const int64_t bsteps = (steps + nsplit - 1) / nsplit;
   const int nw = bsteps <= 4 ? 4 : 8;
   const int64_t per_wave = (bsteps + nw - 1) / nw;
+  // more than 4 rows of x: at most two K steps per wave in flight (four spill the registers of 8 rows)
   if (per_wave <= 1)
     gemv_launch_u<TW, EPI, 1, NORM, GS, GN>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
   else if (per_wave <= 2)
+    gemv_launch_u<TW, EPI, 2, NORM, GS, GN>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
+  else if (M > 4)
     gemv_launch_u<TW, EPI, 2, NORM, GS, GN>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
   else
     gemv_launch_u<TW, EPI, 4, NORM, GS, GN>(x, ldx, W, wscale, y, ldy, M, N, K, pushes, npush, T, nw, (int)nsplit, na, st);
@@ -689,7 +696,9 @@ extern "C" int q35_gemv_norm_conv(const float* x, const float* x_add, float* x_o
   const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, kEpiStore, nullptr, 0, 1);
   if (chk != Q35_OK) return chk;
   if (!norm_w || !conv_w || !conv_state || conv_channels <= 0 || conv_channels > N || conv_k < 2) return Q35_EINVAL;
-  if (conv_k > kGemvConvMaxK || (N + 15) / 16 > kGemvMaxBlocks || conv_channels * conv_k > 0x7fffffff)
+  // one tile per block: 16 output rows, or 8 for more than 4 rows of x
+  if (conv_k > kGemvConvMaxK || (N + (M > 4 ? 7 : 15)) / (M > 4 ? 8 : 16) > kGemvMaxBlocks ||
+      conv_channels * conv_k > 0x7fffffff)
     return Q35_EUNSUPPORTED;
   if (((uintptr_t)norm_w & 15) || (x_add && ((uintptr_t)x_add & 15)) || (x_out && ((uintptr_t)x_out & 15)))
     return Q35_EUNSUPPORTED;

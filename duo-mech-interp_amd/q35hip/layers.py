@@ -80,7 +80,7 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     wq_out, ws_out = _q8(p, "out_proj")
     if (T == 1 and Hk == Hv and dk == dv == 128 and x.dtype == torch.float32 and B <= 8 and x.shape[-1] % 256 == 0
             and Vd % 256 == 0 and wq_in is not None and wq_out is not None
-            and wq_in.shape[0] <= ops.GEMV_CONV_MAX_N and p["conv1d"].shape[-1] <= ops.GEMV_CONV_MAX_K):
+            and wq_in.shape[0] <= ops.gemv_conv_max_n(B) and p["conv1d"].shape[-1] <= ops.GEMV_CONV_MAX_K):
         # decode step on int8 projections: the causal conv + SiLU in the input projection's epilogue (each channel
         # has one owner there, so its conv state advances in place), the recurrent rule over four blocks per head,
         # and the gated RMSNorm in the output projection's staging (the same arithmetic as the fused step below)

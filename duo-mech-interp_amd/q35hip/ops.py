@@ -405,8 +405,13 @@ def _attn_prep_impl(y, q_norm_w, k_norm_w, eps, cos, sin, pos, k_cache, v_cache,
 
 
 # ---------------------------------------------------------------- decode matrix-vector products, SwiGLU hook
-# limits of the conv epilogue of the decode GEMV (q35_gemv_norm_conv): output rows and conv taps
-GEMV_CONV_MAX_N, GEMV_CONV_MAX_K = 16384, 8
+# limits of the conv epilogue of the decode GEMV (q35_gemv_norm_conv): conv taps, and output rows (1024 tiles of 16
+# rows, or of 8 rows for more than 4 rows of x)
+GEMV_CONV_MAX_K = 8
+
+
+def gemv_conv_max_n(M):
+    return 1024 * (8 if M > 4 else 16)
 # "add_fixed": accumulate with every output summed in one fixed order (repeatable bits; no split over K)
 _EPI = {"store": 0, "add": 1, "swiglu": 2, "add_fixed": 4}
 
@@ -883,7 +888,8 @@ def gemm_q8(x, W, w_scale, out=None, epilogue="store", pushes=None, T=1, split_o
     accumulates into out, "swiglu" treats W's rows as interleaved (gate, up) pairs and writes
     silu(gate) * up with the neuron pushes (pack_pushes) applied, out [M, N / 2]. x may also be the int32 words of
     activations already split (add_rmsnorm_(..., split=True), split_activations): the same product, bitwise, without
-    the split in the kernel; or bf16 (the product of x.float(), bitwise, with the lo products skipped). split_out=True (SwiGLU only) writes out as the int32 words of the split layout, the
+    the split in the kernel; or bf16 (the lo products skipped: the product of x.float() bitwise where that runs the register-staged
+    kernel, N < 2048 or K > 2048, and to fp32 rounding on the wide shapes). split_out=True (SwiGLU only) writes out as the int32 words of the split layout, the
     input of the next gemm_q8. capture: as for gemv (the fp32 activations, whatever the layout of out). Returns out."""
     e = _EPI[epilogue]
     if split_out:

@@ -181,8 +181,9 @@ int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cach
  * q35_gated_attn_decode without a workspace argument, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid allocation). This entry point has no counterpart in the
  * reference. The split-K partials go to a fixed device array of q35_gated_attn_decode_noalloc_max_bytes() bytes
- * (8 MiB; one copy per device, held until the process ends); a call whose q35_gated_attn_decode_workspace_bytes(...)
- * exceeds it returns Q35_ESCRATCH without launching (8 MiB covers B <= 128 at an 8192-token cache with Hq 8).
+ * (9 MiB; one copy per device, held until the process ends); a call whose q35_gated_attn_decode_workspace_bytes(...)
+ * exceeds it returns Q35_ESCRATCH without launching (9 MiB covers B <= 142 at an 8192-token cache with Hq 8, Hkv 2,
+ * D 256 and the default splits: 66,048 bytes of partials per row).
  * The stream's device must be the current device. Calls that overlap on one device race for the array. No memory
  * is allocated or freed; the array's device address is looked up on the first call per device. Arguments and
  * results are otherwise exactly those of q35_gated_attn_decode (same kernels, bitwise identical outputs).
@@ -363,7 +364,7 @@ int q35_gemv_norm(const float* x, const float* x_add, float* x_out, int64_t ldx,
  * advanced by one input. The same arithmetic as q35_gdn_conv at T = 1 (HF:454-475 causal_conv1d_update;
  * engine/kernels_qwen35.js:127-178). Each channel belongs to one block, so the state is updated in place.
  *   conv_w: [conv_channels, conv_k] fp32, conv_bias: [conv_channels] or NULL, conv_state: [M, conv_k - 1,
- *   conv_channels] fp32; 2 <= conv_k <= 8, N at most 16384. Everything else as q35_gemv_norm.
+ *   conv_channels] fp32; 2 <= conv_k <= 8, N at most 16384 (8192 for M > 4). Everything else as q35_gemv_norm.
  */
 int q35_gemv_norm_conv(const float* x, const float* x_add, float* x_out, int64_t ldx, const float* norm_w, float eps,
                        const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy, int64_t M, int64_t N,
@@ -414,8 +415,10 @@ int q35_gemm_q8_split(const void* xs, int64_t ldx, const int8_t* W, int w_dtype,
 
 /*
  * q35_gemm_q8 on bf16 x (the attention output, read without a conversion to fp32): xb [M, ldx] bf16, 16-byte
- * aligned, ldx a multiple of 8; bitwise q35_gemm_q8 on the fp32 values of x (their hi parts are x, their lo parts
- * zero, and only the hi products are issued). Runs on the register-staged kernel. Same reference lines.
+ * aligned, ldx a multiple of 8. Runs on the register-staged kernel with only the hi products issued (the hi parts are
+ * x, the lo parts zero): bitwise q35_gemm_q8 on the fp32 values of x where that also runs the register-staged kernel
+ * (N < 2048 or K > 2048), equal to fp32 rounding elsewhere (the DMA kernel sums K in another grouping). Same
+ * reference lines.
  */
 int q35_gemm_q8_bf16(const void* xb, int64_t ldx, const int8_t* W, int w_dtype, const float* w_scale, float* y,
                      int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const q35_push* pushes,

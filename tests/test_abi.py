@@ -162,6 +162,30 @@ def test_decode_workspace_scales_with_splits():
     assert a > 0 and b == 2 * a and c == a
 
 
+def test_no_kernel_spills_registers_or_uses_scratch():
+    """Every gfx950 kernel of the built library (read from its code objects' metadata) keeps its values in registers:
+    no VGPR spills and no private (scratch) segment, in particular the decode GEMV at 1 and 8 rows of x. (SGPR spills
+    go to VGPR lanes, not to memory, and are allowed.)"""
+    from kernel_meta import kernel_metadata
+    md = kernel_metadata(LIB_PATH)
+    assert len(md) > 100
+    assert any("gemv_kernelIaLi1E" in k["name"] for k in md) and any("gemv_kernelIaLi8E" in k["name"] for k in md)
+    bad = [(k["name"], k.get(".vgpr_spill_count"), k.get(".private_segment_fixed_size"))
+           for k in md if k.get(".vgpr_spill_count", 0) or k.get(".private_segment_fixed_size", 0)]
+    assert not bad, bad[:5]
+
+
+def test_noalloc_scratch_capacity_boundary():
+    """The allocation-free decode's fixed scratch (9 MiB) holds the partials of B <= 142 rows at an 8192-token cache
+    (Hq 8, Hkv 2, D 256, default splits) and not of 143: host-side sizes only."""
+    L = q35hip.lib()
+    cap = L.q35_gated_attn_decode_noalloc_max_bytes()
+    assert cap == 9 << 20
+    assert L.q35_gated_attn_decode_workspace_bytes(128, 8, 2, 256, 8192, 0) <= cap
+    assert L.q35_gated_attn_decode_workspace_bytes(142, 8, 2, 256, 8192, 0) <= cap
+    assert L.q35_gated_attn_decode_workspace_bytes(143, 8, 2, 256, 8192, 0) > cap
+
+
 def test_ops_refuse_cpu_tensors():
     x = torch.zeros(1, 4, 16, 128)
     g = torch.zeros(1, 4, 16)

@@ -148,7 +148,9 @@ def test_prefill_over_cache(B, T, Hq, Hkv, max_len, pos):
 
 def test_prefill_over_cache_equals_own_keys_at_position_zero():
     """At position 0 with the cache holding the call's rotated keys, the cached path gives the own-keys path's
-    result (same tiles and arithmetic: bitwise)."""
+    result to bf16 rounding. Not bitwise: the cache's keys are rotated on the host here (the own-keys path rotates
+    them on the GPU, each rounded to bf16), and the own-keys path splits long query blocks into two key ranges merged
+    afterwards (another summation order); both differences are at bf16 rounding, well inside the bound."""
     dev = device()
     B, T, max_len = 2, 200, 256
     inp = workloads.to_device(workloads.attn_prefill_inputs(B=B, T=T, seed=9), dev)
@@ -162,4 +164,6 @@ def test_prefill_over_cache_equals_own_keys_at_position_zero():
     own = q35hip.gated_attention_prefill(inp["q"], inp["k"], inp["v"], inp["gate"], cos, sin)
     cached = q35hip.ops.gated_attention_prefill_cached(inp["q"], kc, vc, inp["gate"],
                                                        torch.zeros(B, dtype=torch.int32, device=dev), cos, sin)
-    assert oracle.rel_err(cached.float().cpu(), own.float().cpu()) <= 1e-2
+    e = oracle.rel_err(cached.float().cpu(), own.float().cpu())
+    print(f"cached vs own keys at position 0: rel err {e:.2e}")
+    assert e <= 1e-2

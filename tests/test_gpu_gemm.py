@@ -189,9 +189,11 @@ def test_gemm_q8_swiglu_split_output(M, N, K):
     assert torch.equal(ya, yb)
 
 
-@pytest.mark.parametrize("M,N,K", [(6144, 1024, 2048), (70, 300, 512)])
+@pytest.mark.parametrize("M,N,K", [(6144, 1024, 2048), (70, 300, 512), (2048, 4096, 1024)])
 def test_gemm_q8_bf16_input_equals_fp32_input(M, N, K):
-    """bf16 x (the attention output) gives bitwise the product of its fp32 values, store and accumulate."""
+    """bf16 x (the attention output) gives bitwise the product of its fp32 values, store and accumulate, where the
+    fp32 input also runs the register-staged kernel (N < 2048); at N 4096, K 1024 the fp32 input runs the DMA kernel
+    (another K grouping) and the two agree to fp32 rounding (1e-5)."""
     dev = device()
     q, s = _q8g(N, K, 23 + M)
     xb = (torch.randn(M, K, generator=torch.Generator().manual_seed(M)) * 2.0).to(torch.bfloat16).to(dev)
@@ -203,5 +205,8 @@ def test_gemm_q8_bf16_input_equals_fp32_input(M, N, K):
     ops.gemm_q8(xb.float(), q.to(dev), s.to(dev), out=c, epilogue="add")
     ops.gemm_q8(xb, q.to(dev), s.to(dev), out=d, epilogue="add")
     torch.cuda.synchronize()
-    assert torch.equal(a, b) and torch.equal(c, d)
+    if N < 2048:
+        assert torch.equal(a, b) and torch.equal(c, d)
+    else:
+        assert oracle.rel_err(b.cpu(), a.cpu()) <= 1e-5 and oracle.rel_err(d.cpu(), c.cpu()) <= 1e-5
 

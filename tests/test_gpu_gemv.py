@@ -222,3 +222,32 @@ def test_gemv_gated_norm_fixed_order_is_repeatable():
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1])
     assert oracle.rel_err(outs[2].cpu(), outs[0].cpu()) <= TOL
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(8, 7168, 1024, "swiglu"), (8, 1024, 2048, "add"), (8, 40008, 1024, "store"),
+                                       (1, 40008, 1024, "store"), (1, 7168, 1024, "swiglu"), (5, 8224, 1024, "store")])
+def test_gemv_group_scales_one_and_eight_rows(M, N, K, epi):
+    """The decode GEMV at 1 and 8 rows of x (8 rows run tiles of 8 output rows) with the engine's q8 weights and the
+    norm prologue: SwiGLU with pushes, the split-K accumulation, and the tile loop of a wide product (N 40008)."""
+    dev = device()
+    g = torch.Generator().manual_seed(N + M)
+    W, s = omlp.q8_quantize(torch.randn(N, K, generator=g) * 0.02)
+    x = torch.randn(M, K, generator=g) * 2.0
+    nw = torch.randn(K, generator=g) * 0.1
+    h = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + nw)
+    pushes = [(17, "add", [1.0, -1.0, 0.5]), (None, "mul", [0.5, 2.0, 1.5])] if epi == "swiglu" else []
+    if epi == "swiglu":
+        y = omlp.q8_linear(h, W, s)
+        ref = omlp.swiglu_push(y[:, 0::2], y[:, 1::2], pushes, T=1)
+    else:
+        ref = omlp.q8_linear(h, W, s)
+    base = torch.randn(M, N, generator=g) if epi == "add" else None
+    announce(f"gemv g128 M{M} N{N} K{K} {epi}")
+    out = base.to(dev) if base is not None else None
+    y = ops.gemv(x.to(dev), W.to(dev), s.to(dev), out=out, epilogue=epi,
+                 pushes=ops.pack_pushes(pushes, dev) if pushes else None, prenorm=(None, nw.to(dev), 1e-6, None))
+    torch.cuda.synchronize()
+    got = y.cpu() - base if base is not None else y.cpu()
+    e = oracle.rel_err(got, ref)
+    print(f"gemv M{M} N{N} {epi}: rel err {e:.2e}")
+    assert e <= TOL
