@@ -32,6 +32,8 @@
 // Operands stream straight from L2 into registers three pairs ahead (12 waves keep about 40 KB of loads in flight per
 // CU); a thirteenth wave touches the records several pairs further ahead so that the first of the 16 blocks to need a
 // line finds it in L2. The 16 blocks of a head are placed on one XCD (they share its L2).
+#include <type_traits>
+
 #include "q35_common.h"
 #include "q35hip.h"
 
@@ -646,6 +648,575 @@ __global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const __bf16* __r
     }
   }
   if (tid == 0) *reinterpret_cast<float*>(rec + kRecE) = __expf(gl);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// gdn_pair_prep4_kernel: the records of one (pair, head, row) from a 4-wave block with at most 80 KB of LDS and 256
+// VGPRs, so that two blocks share a compute unit and every block of a T = 4096, 16-head call is resident at once (one
+// block's memory and barrier waits are covered by the other's work). Same records, same math, as laid out above.
+//
+// Dataflow. Waves 0-1 ("W waves") own value tiles D0 .. D0 + 3 (D0 = 4 (w & 1)) of W; waves 2-3 ("U waves") the same
+// tiles of U. Each wave forms its tiles for all 128 positions (W0 = T00 K'0, Z = L10 W0 + K'1, W1 = T11 Z; U alike),
+// keeps them in registers as MFMA operands (a D-layout accumulator tile is one half of a 32-wide k step: the kmap
+// order) and from them writes its part of the records: M^T = -W^T K~ and Q'^T = Q^ e^gamma - W^T P^T (W waves),
+// Bm = K~^T U and R^T = U^T P^T (U waves). LDS holds the row-major k tile (K K^T / Q K^T), then the two fp32 64 x 64
+// L blocks (inverted in place), then V^T, then P; K^T stays for the whole block. Tiles are [128][128] bf16 with
+// 272-byte rows: 16 lanes reading 16 consecutive rows at one column hit 16 distinct bank quads, and fragment
+// addresses are a per-lane row base plus immediate offsets.
+//
+// Decay factors exp(gamma_t - gamma_s) (s < t): exact per element on diagonal 16 x 16 tiles; on tiles below the
+// diagonal the product of a row factor exp(gamma_t - gamma_r) and a column factor exp(gamma_r - gamma_s) around the
+// tile's first row r, both <= 1 (gamma is non-increasing), so neither overflows whatever the size of g.
+constexpr int kRS = 272;  // bytes per row of a padded [128][128] bf16 LDS tile
+
+__device__ __forceinline__ bf16x8 ldf(const char* tile, int r, int c) {  // row r, columns c .. c + 7
+  return *reinterpret_cast<const bf16x8*>(tile + r * kRS + 2 * c);
+}
+// row r, the 8 columns of k step c0 held by lane group g in kmap order: c0 + 4 g .. + 3 and c0 + 16 + 4 g .. + 3
+__device__ __forceinline__ bf16x8 ldf_km(const char* tile, int r, int c0, int g) {
+  const u32x2 a = *reinterpret_cast<const u32x2*>(tile + r * kRS + 2 * (c0 + 4 * g));
+  const u32x2 b = *reinterpret_cast<const u32x2*>(tile + r * kRS + 2 * (c0 + 16 + 4 * g));
+  const u32x4 v = {a.x, a.y, b.x, b.y};
+  return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ f32x4 scale4(const f32x4& a, const f32x4& s) {
+  f32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = a[i] * s[i];
+  return r;
+}
+
+// Inverses T = (I - L)^-1 of the two unit lower-triangular 64 x 64 blocks of a pair, in place in Am (two [64][kFS]
+// fp32 arrays, strictly-lower L on entry with zeros on and above the diagonal of the diagonal 16 x 16 blocks; on exit
+// T row-major with the strictly-lower part of its diagonal blocks stored and the unit diagonal implicit). Wave w takes
+// matrix w / 2 and block columns c and 3 - c (c = w % 2): the two diagonal inverses (forward substitution, the two
+// chains interleaved), then the two block columns T_ij = (I + T'_ii) sum_{k=j}^{i-1} L_ik T_kj, whose blocks are kept
+// transposed in the unused upper block (j, i) while other columns still read L, and rewritten row-major in place of
+// L_ij at the end.
+__device__ __forceinline__ void invert64x2(float* Am2, int wv, int lane) {
+  const int li = lane & 15, lg = lane >> 4;
+  float* Am = Am2 + (wv >> 1) * 64 * kFS;
+  const int c0 = wv & 1, c1 = 3 - c0;
+  auto blk = [&](int bi, int bj) { return Am + (16 * bi) * kFS + 16 * bj; };
+  {
+    float ta[16], tb[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      ta[i] = blk(c0, c0)[i * kFS + li];
+      tb[i] = blk(c1, c1)[i * kFS + li];
+    }
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+      float aa = ta[i], ab = tb[i];
+#pragma unroll
+      for (int j = 0; j < i; ++j) {
+        aa += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ta[i]), j)) * ta[j];
+        ab += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tb[i]), j)) * tb[j];
+      }
+      ta[i] = aa;
+      tb[i] = ab;
+    }
+    if (lane < 16) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        blk(c0, c0)[i * kFS + lane] = ta[i];
+        blk(c1, c1)[i * kFS + lane] = tb[i];
+      }
+    }
+  }
+  lds_barrier();
+  f32x4 tfin[3];  // column c0's blocks (c0 + 1 ..), then column c1's (at most 3 in all: columns {0, 3} or {1, 2})
+  int nf = 0;
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) {
+    const int j = cc ? c1 : c0;
+    for (int i = j + 1; i < 4; ++i) {
+      f32x4 acc;
+      const float* Lij = blk(i, j);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = Lij[(4 * lg + r) * kFS + li];
+      acc = mm16_f32(Lij, kFS, blk(j, j), kFS, false, acc, lane);
+      for (int kk = j + 1; kk < i; ++kk) acc = mm16_f32(blk(i, kk), kFS, blk(j, kk), kFS, true, acc, lane);
+      // the partial sum goes into block (j, i) transposed, the final T_ij over it
+      *reinterpret_cast<f32x4*>(blk(j, i) + li * kFS + 4 * lg) = acc;
+      __builtin_amdgcn_wave_barrier();
+      acc = mm16_f32(blk(i, i), kFS, blk(j, i), kFS, true, acc, lane);
+      __builtin_amdgcn_wave_barrier();
+      *reinterpret_cast<f32x4*>(blk(j, i) + li * kFS + 4 * lg) = acc;
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+        if (q == nf) tfin[q] = acc;
+      ++nf;
+    }
+  }
+  lds_barrier();  // every column done: the L blocks below the diagonal are no longer read
+  nf = 0;
+#pragma unroll
+  for (int cc = 0; cc < 2; ++cc) {
+    const int j = cc ? c1 : c0;
+    for (int i = j + 1; i < 4; ++i) {
+      f32x4 v = tfin[0];
+#pragma unroll
+      for (int q = 1; q < 3; ++q)
+        if (q == nf) v = tfin[q];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) blk(i, j)[(4 * lg + r) * kFS + li] = v[r];
+      ++nf;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __restrict__ q,
+                                                                const __bf16* __restrict__ k,
+                                                                const __bf16* __restrict__ v,
+                                                                const float* __restrict__ g,
+                                                                const float* __restrict__ beta, char* __restrict__ ws,
+                                                                int T, int NP, int Hk, int H, float scale,
+                                                                int l2norm) {
+  __shared__ __attribute__((aligned(16))) char RA[kP * kRS];  // k rows -> L00, L11 fp32 -> T -> V^T -> P fragments
+  __shared__ __attribute__((aligned(16))) char RB[kP * kRS];  // K^T [d][pos]
+  __shared__ __attribute__((aligned(16))) bf16x8 L10f[8][64];  // L10 A fragments [c1 row tile][k step], kmap order
+  // per position: 0 gamma; 1 beta; 2 rk, then rk e^(gamma_last - gamma) (K~); 3 rq scale, then rq scale e^gamma
+  // (Q^ e^gamma, 0 past the end); 4 beta e^gamma rk (W's input scale)
+  __shared__ __attribute__((aligned(16))) float cf[5][kP];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int h = blockIdx.x, p = blockIdx.y, b = blockIdx.z;
+  const int kh = h / (H / Hk);
+  const int t0 = p * kP;
+  const int nvalid = min(kP, T - t0);
+  char* rec = ws + (((size_t)b * H + h) * NP + p) * kRecBytes;
+  float* Am = reinterpret_cast<float*>(RA);
+
+  // ---- 0. stage: each thread an 8 x 8 unit of k (positions 8 ur .., dims 8 uc ..) into the row-major tile (RA) and
+  //         transposed into K^T (RB); the wave's own q rows (row tiles X0 = w, X1 = 7 - w) as B fragments in
+  //         registers; the gates (wave 0). Every load goes out before any is used.
+  const int ur = tid >> 4, uc = tid & 15;
+  u32x4 raw[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const size_t tok = (size_t)b * T + t0 + min(8 * ur + i, nvalid - 1);
+    raw[i] = raw8(k + (tok * Hk + kh) * kD + 8 * uc);
+  }
+  const int X0 = wv, X1 = 7 - wv;
+  bf16x8 qf[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const int t = 16 * (a ? X1 : X0) + li;
+    const __bf16* src = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[a][ks] = *reinterpret_cast<const bf16x8*>(src + 32 * ks + 8 * lg);
+  }
+  float g0 = 0.f, g1 = 0.f, b0 = 0.f, b1 = 0.f;
+  if (wv == 0) {
+    const size_t base = ((size_t)b * T + t0) * H + h;
+    if (lane < nvalid) { g0 = g[base + (size_t)lane * H]; b0 = beta[base + (size_t)lane * H]; }
+    if (64 + lane < nvalid) { g1 = g[base + (size_t)(64 + lane) * H]; b1 = beta[base + (size_t)(64 + lane) * H]; }
+  }
+  {
+    float ss[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool valid = 8 * ur + i < nvalid;
+      ss[i] = valid ? sumsq8(raw[i]) : 0.f;
+      raw[i] = mask8(raw[i], valid);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) ss[i] += __shfl_xor(ss[i], off, 64);
+    }
+    if (uc == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cf[2][8 * ur + i] = l2norm ? rsqrtf(ss[i] + 1e-6f) : 1.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(RA + (8 * ur + i) * kRS + 16 * uc) = raw[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(RB + (8 * uc + e) * kRS + 16 * ur) = column8(raw, e);
+  }
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const int t = 16 * (a ? X1 : X0) + li;
+    float ss = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ss += sumsq8(__builtin_bit_cast(u32x4, qf[a][ks]));
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    if (lg == 0) cf[3][t] = t < nvalid ? (l2norm ? rsqrtf(ss + 1e-6f) : 1.f) * scale : 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[a][ks] = __builtin_bit_cast(bf16x8, mask8(__builtin_bit_cast(u32x4, qf[a][ks]), t < nvalid));
+  }
+  if (wv == 0) {  // gamma = cumsum(g) over the pair; beta; both zero past the sequence end (HF pads with 0)
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y0 = __shfl_up(g0, off, 64), y1 = __shfl_up(g1, off, 64);
+      if (lane >= off) { g0 += y0; g1 += y1; }
+    }
+    const float tot0 = __shfl(g0, 63, 64);
+    cf[0][lane] = g0;
+    cf[0][64 + lane] = tot0 + g1;
+    cf[1][lane] = b0;
+    cf[1][64 + lane] = b1;
+  }
+  lds_barrier();
+
+  // ---- 1. K K^T and Q K^T for the wave's row tiles X0 (chunk 0) and X1 (chunk 1), all products before any store
+  //         (the fp32 L blocks replace the k tile). Per column tile Y <= X1 the k rows of Y are read once and serve:
+  //         L00 (X0, Y), L11 (X1, Y >= 4) as B operands; L10 (X1, Y < 4) and P (X0 / X1, Y) as A operands of the
+  //         transposed tiles (positions s down each lane's 4 rows, t across the lanes).
+  bf16x8 kx[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kx[a][ks] = ldf(RA, 16 * (a ? X1 : X0) + li, 32 * ks + 8 * lg);
+  f32x4 lA[4], pA[4], lB[8], pB[8];
+#pragma unroll
+  for (int y = 0; y < 8; ++y) {
+    if (y > X1) break;
+    bf16x8 ky[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ky[ks] = ldf(RA, 16 * y + li, 32 * ks + 8 * lg);
+    f32x4 a1 = zero4(), a2 = zero4();
+    if (y < 4) {  // L10 (transposed)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) a1 = mfma16(ky[ks], kx[1][ks], a1);
+    } else {      // L11
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) a1 = mfma16(kx[1][ks], ky[ks], a1);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) a2 = mfma16(ky[ks], qf[1][ks], a2);
+    lB[y] = a1;
+    pB[y] = a2;
+    if (y < 4 && y <= X0) {
+      f32x4 a3 = zero4(), a4 = zero4();
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        a3 = mfma16(kx[0][ks], ky[ks], a3);
+        a4 = mfma16(ky[ks], qf[0][ks], a4);
+      }
+      lA[y] = a3;
+      pA[y] = a4;
+    }
+  }
+  lds_barrier();  // the k tile (RA) is read by every wave: now it becomes L
+
+  // epilogues. gamma is non-increasing; tile factors relative to the tile's first row r = 16 X.
+  bf16x8 pfr[2][4];  // P B-fragments of row tiles X0, X1: [k step] (kmap order), zero above the diagonal
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) pfr[a][ks] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+  auto epilogue = [&](auto aconst) {
+    constexpr int a = decltype(aconst)::value;
+    constexpr int NY = a ? 8 : 4;
+    const int X = a ? X1 : X0;
+    const float gr = cf[0][16 * X];
+    // rows t = 16 X + 4 lg + r (normal tiles) and the lane's own t = 16 X + li (transposed tiles)
+    f32x4 rowL, gtr, ltr;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * X + 4 * lg + r;
+      gtr[r] = cf[0][t];
+      ltr[r] = -cf[1][t] * cf[2][t];
+      rowL[r] = ltr[r] * __expf(gtr[r] - gr);
+    }
+    const int tl = 16 * X + li;
+    const float gt = cf[0][tl];
+    const float rowT_L = -cf[1][tl] * cf[2][tl] * __expf(gt - gr);
+    const float rowT_P = cf[3][tl] * __expf(gt - gr);
+#pragma unroll
+    for (int y = 0; y < NY; ++y) {
+      if (y > X) break;
+      const bool diag = y == X;
+      // normal-tile column s = 16 y + li; transposed-tile columns s = 16 y + 4 lg + r
+      const int sn = 16 * y + li;
+      const float colN = cf[2][sn] * __expf(gr - cf[0][sn]);
+      f32x4 colT, gsT, rkT;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int s = 16 * y + 4 * lg + r;
+        gsT[r] = cf[0][s];
+        rkT[r] = cf[2][s];
+        colT[r] = rkT[r] * __expf(gr - gsT[r]);
+      }
+      // P (transposed): rows s of tile y, column t = tl
+      {
+        f32x4 acc;
+        if constexpr (a) acc = pB[y]; else acc = pA[y];
+        float pv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int s = 16 * y + 4 * lg + r;
+          pv[r] = diag ? (s <= tl ? cf[3][tl] * rkT[r] * __expf(gt - gsT[r]) * acc[r] : 0.f)
+                       : rowT_P * colT[r] * acc[r];
+        }
+        const u32x2 pk = pack4(pv[0], pv[1], pv[2], pv[3]);
+        u32x4 cur = __builtin_bit_cast(u32x4, pfr[a][y >> 1]);
+        if (y & 1) { cur.z = pk.x; cur.w = pk.y; } else { cur.x = pk.x; cur.y = pk.y; }
+        pfr[a][y >> 1] = __builtin_bit_cast(bf16x8, cur);
+      }
+      if (a == 1 && y < 4) {
+        // L10 (transposed): rows s of tile y (chunk 0), column t = tl (chunk 1); below the diagonal, no mask
+        const f32x4 acc = lB[y];
+        float lv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lv[r] = rowT_L * colT[r] * acc[r];
+        *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(&L10f[(X1 - 4) * 2 + (y >> 1)][lane]) + 8 * (y & 1)) =
+            pack4(lv[0], lv[1], lv[2], lv[3]);
+      } else {
+        // L00 (X0, y) or L11 (X1, y >= 4), normal orientation: rows t = 16 X + 4 lg + r, column s = sn
+        f32x4 acc;
+        if constexpr (a) acc = lB[y]; else acc = lA[y];
+        float* Ac = Am + a * 64 * kFS;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * X + 4 * lg + r;
+          const float val = diag ? (sn < t ? ltr[r] * cf[2][sn] * __expf(gtr[r] - cf[0][sn]) * acc[r] : 0.f)
+                                 : rowL[r] * colN * acc[r];
+          Ac[(t - 64 * a) * kFS + (sn - 64 * a)] = val;
+        }
+      }
+    }
+  };
+  epilogue(std::integral_constant<int, 0>{});
+  epilogue(std::integral_constant<int, 1>{});
+  lds_barrier();
+
+  // ---- 2. the per-position factors of the later phases (in place, one position per thread); V loads go out; the
+  //         two inverses (fp32, in place in RA)
+  if (tid < kP) {
+    const float gt = cf[0][tid], gl = cf[0][kP - 1], bt = cf[1][tid], rk = cf[2][tid], qs = cf[3][tid];
+    cf[4][tid] = bt * __expf(gt) * rk;
+    cf[2][tid] = rk * __expf(gl - gt);
+    cf[3][tid] = qs * __expf(gt);
+    if (tid == 0) *reinterpret_cast<float*>(rec + kRecE) = __expf(gl);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const size_t tok = (size_t)b * T + t0 + min(8 * ur + i, nvalid - 1);
+    raw[i] = raw8(v + (tok * H + h) * kD + 8 * uc);
+  }
+  invert64x2(Am, wv, lane);
+  lds_barrier();
+
+  // A fragments of T00 (natural k order, columns scaled by W's or U's input factor) and of T11 (kmap order), rows
+  // 16 X + li; fragments wholly above the diagonal are zero
+  const bool isW = wv < 2;
+  const float* cin = cf[isW ? 4 : 1];
+  bf16x8 t00[4][2], t11[4][2];
+#pragma unroll
+  for (int X = 0; X < 4; ++X) {
+    const int t = 16 * X + li;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 f0, f1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { f0[j] = (__bf16)0.f; f1[j] = (__bf16)0.f; }
+      if (ks <= (X >> 1)) {
+        const int s0 = 32 * ks + 8 * lg;
+        const f32x4 u0 = *reinterpret_cast<const f32x4*>(Am + t * kFS + s0);
+        const f32x4 u1 = *reinterpret_cast<const f32x4*>(Am + t * kFS + s0 + 4);
+        const f32x4 c0 = *reinterpret_cast<const f32x4*>(cin + s0);
+        const f32x4 c1 = *reinterpret_cast<const f32x4*>(cin + s0 + 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int s = s0 + j;
+          const float tv = j < 4 ? u0[j] : u1[j - 4];
+          const float val = s < t ? tv : (s == t ? 1.f : 0.f);
+          f0[j] = (__bf16)(val * (j < 4 ? c0[j] : c1[j - 4]));
+        }
+        const float* A1 = Am + 64 * kFS;
+        const int sa = 32 * ks + 4 * lg, sb = 32 * ks + 16 + 4 * lg;
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(A1 + t * kFS + sa);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(A1 + t * kFS + sb);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int s = j < 4 ? sa + j : sb + j - 4;
+          const float tv = j < 4 ? v0[j] : v1[j - 4];
+          f1[j] = (__bf16)(s < t ? tv : (s == t ? 1.f : 0.f));
+        }
+      }
+      t00[X][ks] = f0;
+      t11[X][ks] = f1;
+    }
+  }
+  lds_barrier();  // T is read: RA becomes V^T
+#pragma unroll
+  for (int i = 0; i < 8; ++i) raw[i] = mask8(raw[i], 8 * ur + i < nvalid);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(RA + (8 * uc + e) * kRS + 16 * ur) = column8(raw, e);
+  lds_barrier();
+
+  // ---- 3-5. X0 = T00 diag(c) K0 (or V0), Z = L10 X0 + diag(c) K1, X1 = T11 Z, for this wave's value tiles D0 + D.
+  //           The results stay in registers as 32-wide k steps over positions (kmap order): xn unscaled, xk scaled by
+  //           the K~ factor rk e^(gamma_last - gamma) of each position.
+  const int D0 = 4 * (wv & 1);
+  const char* src = isW ? RB : RA;  // K^T or V^T
+  bf16x8 xn[4][4], xk[4][4];        // [D][position k step]
+  {
+    bf16x8 bs[4][2];
+#pragma unroll
+    for (int D = 0; D < 4; ++D)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) bs[D][ks] = ldf(src, 16 * (D0 + D) + li, 32 * ks + 8 * lg);
+    f32x4 x0[4][4];
+#pragma unroll
+    for (int X = 0; X < 4; ++X)
+#pragma unroll
+      for (int D = 0; D < 4; ++D) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          if (ks <= (X >> 1)) acc = mfma16(t00[X][ks], bs[D][ks], acc);
+        x0[X][D] = acc;
+      }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const f32x4 sa = *reinterpret_cast<const f32x4*>(&cf[2][32 * kt + 4 * lg]);
+      const f32x4 sb = *reinterpret_cast<const f32x4*>(&cf[2][32 * kt + 16 + 4 * lg]);
+#pragma unroll
+      for (int D = 0; D < 4; ++D) {
+        xn[D][kt] = pack8(x0[2 * kt][D], x0[2 * kt + 1][D]);
+        xk[D][kt] = pack8(scale4(x0[2 * kt][D], sa), scale4(x0[2 * kt + 1][D], sb));
+      }
+    }
+  }
+  {
+    f32x4 z[4][4];
+#pragma unroll
+    for (int X = 0; X < 4; ++X) {
+      const f32x4 c = *reinterpret_cast<const f32x4*>(&cin[64 + 16 * X + 4 * lg]);
+      bf16x8 la[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) la[ks] = L10f[X * 2 + ks][lane];
+#pragma unroll
+      for (int D = 0; D < 4; ++D) {
+        const f32x4 x = unpack4(*reinterpret_cast<const u32x2*>(src + (16 * (D0 + D) + li) * kRS +
+                                                              2 * (64 + 16 * X + 4 * lg)));
+        f32x4 acc = scale4(x, c);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) acc = mfma16(la[ks], xn[D][ks], acc);
+        z[X][D] = acc;
+      }
+    }
+    bf16x8 zf[4][2];
+#pragma unroll
+    for (int D = 0; D < 4; ++D)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) zf[D][ks] = pack8(z[2 * ks][D], z[2 * ks + 1][D]);
+    f32x4 x1[4][4];
+#pragma unroll
+    for (int X = 0; X < 4; ++X)
+#pragma unroll
+      for (int D = 0; D < 4; ++D) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          if (ks <= (X >> 1)) acc = mfma16(t11[X][ks], zf[D][ks], acc);
+        x1[X][D] = acc;
+      }
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const f32x4 sa = *reinterpret_cast<const f32x4*>(&cf[2][64 + 32 * kt + 4 * lg]);
+      const f32x4 sb = *reinterpret_cast<const f32x4*>(&cf[2][64 + 32 * kt + 16 + 4 * lg]);
+#pragma unroll
+      for (int D = 0; D < 4; ++D) {
+        xn[D][2 + kt] = pack8(x1[2 * kt][D], x1[2 * kt + 1][D]);
+        xk[D][2 + kt] = pack8(scale4(x1[2 * kt][D], sa), scale4(x1[2 * kt + 1][D], sb));
+      }
+    }
+  }
+  lds_barrier();  // V^T (RA) is read: RA takes the P fragments
+  {
+    bf16x8* Pf = reinterpret_cast<bf16x8*>(RA);
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int X = a ? X1 : X0;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        if (ks <= (X >> 1)) Pf[(pbase(X) + ks) * 64 + lane] = pfr[a][ks];
+    }
+  }
+  lds_barrier();
+
+  // ---- 6. W waves: M^T = -W^T K~ (rows d' = 16 (D0 + D) .., columns d = 16 E ..), stored as M's A fragments;
+  //         U waves: Bm = K~^T U (rows d = 16 E .., columns dv = 16 (D0 + D) ..), stored in D order.
+#pragma unroll
+  for (int E = 0; E < 8; ++E) {
+    bf16x8 kf[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) kf[kt] = ldf_km(RB, 16 * E + li, 32 * kt, lg);
+    if (isW) {
+      f32x4 acc[4];
+#pragma unroll
+      for (int D = 0; D < 4; ++D) {
+        acc[D] = zero4();
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) acc[D] = mfma16(xk[D][kt], kf[kt], acc[D]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[D][r] = -acc[D][r];
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        *reinterpret_cast<bf16x8*>(rec + kRecM + ((size_t)(E * 4 + (D0 >> 1) + hh) * 64 + lane) * 16) =
+            pack8(acc[2 * hh], acc[2 * hh + 1]);
+    } else {
+#pragma unroll
+      for (int D = 0; D < 4; ++D) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) acc = mfma16(kf[kt], xk[D][kt], acc);
+        *reinterpret_cast<u32x2*>(rec + kRecB + ((size_t)(E * 8 + D0 + D) * 64 + lane) * 8) =
+            pack4(acc[0], acc[1], acc[2], acc[3]);
+      }
+    }
+  }
+
+  // ---- 7. W waves: Q'^T = Q^ e^gamma - W^T P^T (rows d', columns t), stored as Q''s A fragments; U waves:
+  //         R^T = U^T P^T (rows dv, columns t), stored in transposed D order. P is zero above the diagonal: row tile X
+  //         has X / 2 + 1 k steps.
+  const bf16x8* Pf = reinterpret_cast<const bf16x8*>(RA);
+#pragma unroll
+  for (int X = 0; X < 8; ++X) {
+    const int t = 16 * X + li;
+    bf16x8 pf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) pf[ks] = Pf[(pbase(X) + min(ks, X >> 1)) * 64 + lane];
+    if (isW) {
+      const __bf16* qr = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
+      const float cq = cf[3][t];
+      f32x4 acc[4];
+#pragma unroll
+      for (int D = 0; D < 4; ++D) {
+        const f32x4 qv = unpack4(*reinterpret_cast<const u32x2*>(qr + 16 * (D0 + D) + 4 * lg));
+        f32x4 pw = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          if (ks <= (X >> 1)) pw = mfma16(xn[D][ks], pf[ks], pw);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[D][r] = qv[r] * cq - pw[r];
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        *reinterpret_cast<bf16x8*>(rec + kRecQ + ((size_t)(X * 4 + (D0 >> 1) + hh) * 64 + lane) * 16) =
+            pack8(acc[2 * hh], acc[2 * hh + 1]);
+    } else {
+#pragma unroll
+      for (int D = 0; D < 4; ++D) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          if (ks <= (X >> 1)) acc = mfma16(xn[D][ks], pf[ks], acc);
+        *reinterpret_cast<u32x2*>(rec + kRecR + ((size_t)(X * 8 + D0 + D) * 64 + lane) * 8) =
+            pack4(acc[0], acc[1], acc[2], acc[3]);
+      }
+    }
+  }
 }
 
 // L2 warm-up: one global_load_lds_dword of one dword per 128-byte line into a dummy LDS area (no registers held);
@@ -1406,7 +1977,7 @@ extern "C" int q35_gdn_chunk_prefill(const void* q, const void* k, const void* v
     const int64_t NP = (T + kP - 1) / kP;
     if (NP > 65535) return Q35_EUNSUPPORTED;
     dim3 g1((unsigned)H, (unsigned)NP, (unsigned)B), g2((unsigned)(16 * H * B));
-    hipLaunchKernelGGL(gdn_pair_prep_kernel, g1, dim3(512), 0, st, (const __bf16*)q, (const __bf16*)k,
+    hipLaunchKernelGGL(gdn_pair_prep4_kernel, g1, dim3(256), 0, st, (const __bf16*)q, (const __bf16*)k,
                        (const __bf16*)v, g, beta, ws, (int)T, (int)NP, (int)Hk, (int)H, scale, use_qk_l2norm);
     hipLaunchKernelGGL(gdn_pair_scan_kernel, g2, dim3(kScanThreads), 0, st, ws, initial_state, final_state,
                        (__bf16*)out, (int)T, (int)NP, (int)H, (int)B);
