@@ -18,12 +18,12 @@
 // (exact algebra: U - W S substituted into both lines). M, Bm, Q', R depend on the inputs only, so all of them come
 // out of one fully parallel kernel, and the sequential kernel streams 128 x 128 bf16 matrices per 128 positions.
 //
-// Kernel 1, gdn_pair_prep_kernel: one block of 8 waves per (pair, head, row), all pairs in parallel. k, q, v rows
-// are staged in XOR-swizzled LDS tiles (row-major for the K K^T / Q K^T products, transposed for the products that
-// contract over positions); the two 64 x 64 inverses run in fp32 (16 x 16 diagonal blocks by forward substitution,
-// off-diagonal blocks by per-column chains on fp32 MFMA); every other product is bf16 MFMA with fp32 accumulation.
-// The products are oriented so that their accumulator tiles pack straight into the scan kernel's MFMA operand order,
-// and the records are written with 16- or 8-byte coalesced stores.
+// Kernel 1, gdn_pair_prep4_kernel: one block of 4 waves per (pair, head, row), all pairs in parallel, two blocks per
+// compute unit. k, q, v rows are staged in padded LDS tiles (row-major for the K K^T / Q K^T products, transposed for
+// the products that contract over positions); the two 64 x 64 inverses run in fp32 (16 x 16 diagonal blocks by
+// forward substitution, off-diagonal blocks by per-column chains on fp32 MFMA); every other product is bf16 MFMA with
+// fp32 accumulation. The products are oriented so that their accumulator tiles pack straight into the scan kernel's
+// MFMA operand order, and the records are written with 16- or 8-byte coalesced stores.
 // Kernel 2, gdn_pair_scan_kernel: 16 blocks per (row, head): 8 slices of 16 value columns x 2 halves of the output
 // rows. Each block carries its 128 x 16 fp32 state slice in registers (8 waves x 16 rows) while 4 more waves form the
 // 64 output rows of its half, 4 MFMAs per wave and pair (computed transposed, so that a lane holds 4 consecutive
@@ -60,15 +60,6 @@ constexpr int kTouchAhead = 8;   // pairs ahead of use that the L2 warm-up wave 
 
 // k index of position j (0..7) of lane group g in a 32-wide K step fed from two 16-row accumulator tiles
 __device__ __forceinline__ int kmap(int g, int j) { return j < 4 ? 4 * g + j : 12 + 4 * g + j; }
-
-// [128][128] bf16 LDS tiles, 256-byte rows of 16 segments of 16 bytes; segment s of row r lives at s ^ swz(r).
-// Both access patterns used (16 lanes reading one segment of 16 consecutive rows; 16 lanes writing one segment of
-// rows 8 c + e, c = 0..15) touch 16 distinct segments: conflict-free.
-__device__ __forceinline__ int swz16(int r) { return (r ^ (r >> 3)) & 15; }
-__device__ __forceinline__ int t128(int r, int c) { return r * 256 + ((((c >> 3) ^ swz16(r)) << 4) | ((c & 7) << 1)); }
-__device__ __forceinline__ bf16x8 frag(const char* tile, int r, int c) {
-  return *reinterpret_cast<const bf16x8*>(tile + t128(r, c));
-}
 
 // Raw loads as packed bf16 bits, issued unconditionally from clamped addresses; rows outside the sequence are
 // zeroed afterwards with a select.
@@ -193,467 +184,10 @@ __device__ __forceinline__ float tinv(const float* Am, int t, int s) {
   return 0.f;
 }
 
-__global__ __launch_bounds__(512, 1) void gdn_pair_prep_kernel(const __bf16* __restrict__ q,
-                                                               const __bf16* __restrict__ k,
-                                                               const __bf16* __restrict__ v, const float* __restrict__ g,
-                                                               const float* __restrict__ beta, char* __restrict__ ws,
-                                                               int T, int NP, int Hk, int H, float scale, int l2norm) {
-  __shared__ __attribute__((aligned(16))) char R1[32768];           // k row-major -> k transposed
-  __shared__ __attribute__((aligned(16))) char R2[32768];           // q row-major -> v transposed -> U transposed
-  __shared__ __attribute__((aligned(16))) float R3[2 * 64 * kFS];   // L00, L11 -> T00, T11 (fp32) -> W transposed
-  __shared__ __attribute__((aligned(16))) bf16x8 L10f[8][64];       // L10 A fragments [rt 4][ks 2], natural k order
-  __shared__ __attribute__((aligned(16))) bf16x8 Pf[kPFrags][64];   // P A fragments (lower), natural k order
-  __shared__ float scr[8][16 * 17];
-  __shared__ float gam[kP], bet[kP], rkn[kP], rqn[kP];
-  // per position t: {gamma_t, -beta_t rk_t, rk_t, rq_t scale} and {beta_t e^gamma_t rk_t, beta_t,
-  // rk_t e^(gamma_last - gamma_t), rq_t scale e^gamma_t}
-  __shared__ f32x4 pa[kP], pb[kP];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int li = lane & 15, lg = lane >> 4;
-  // grid (H, NP, B): the heads of one pair are dispatched together, so concurrently running blocks read whole
-  // [H, D] rows of q, k, v
-  const int h = blockIdx.x, p = blockIdx.y, b = blockIdx.z;
-  const int wv = __builtin_amdgcn_readfirstlane(wave);
-  const int kh = h / (H / Hk);
-  const int t0 = p * kP;
-  const int nvalid = min(kP, T - t0);
-  char* rec = ws + (((size_t)b * H + h) * NP + p) * kRecBytes;
-  char* WT = reinterpret_cast<char*>(R3);
-
-  // ---- 0. stage. Threads 0-255 hold an 8 x 8 unit of k (rows 8 rg.., dims 8 cc..), which stays in registers for
-  //         the transposed copy written after the K K^T phase; q goes row-major. Every global load of the phase
-  //         (k, q, and the gates of wave 0) is issued before any is used, so the phase costs one memory round trip.
-  //         v is first needed after the inverses: threads 256-511 load their 8 x 8 unit of it at the start of
-  //         phase 2, so that its bytes travel while the inverses run instead of lengthening this phase's burst.
-  const int u = tid & 255, rg = u >> 4, cc = u & 15;
-  const bool isK = wv < 4;
-  u32x4 raw[8];
-  if (isK) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const size_t tok = (size_t)b * T + t0 + min(8 * rg + i, nvalid - 1);
-      raw[i] = raw8(k + (tok * Hk + kh) * kD + 8 * cc);
-    }
-  }
-  const int qrow = tid >> 2, qs0 = 4 * (tid & 3);
-  const __bf16* qsrc = q + (((size_t)b * T + t0 + min(qrow, nvalid - 1)) * Hk + kh) * kD;
-  u32x4 rq[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) rq[j] = raw8(qsrc + 8 * (qs0 + j));
-  float g0 = 0.f, g1 = 0.f, b0 = 0.f, b1 = 0.f;
-  if (wave == 0) {
-    const size_t base = ((size_t)b * T + t0) * H + h;
-    if (lane < nvalid) { g0 = g[base + (size_t)lane * H]; b0 = beta[base + (size_t)lane * H]; }
-    if (64 + lane < nvalid) { g1 = g[base + (size_t)(64 + lane) * H]; b1 = beta[base + (size_t)(64 + lane) * H]; }
-  }
-  if (isK) {
-    float ss[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool valid = 8 * rg + i < nvalid;
-      ss[i] = valid ? sumsq8(raw[i]) : 0.f;
-      raw[i] = mask8(raw[i], valid);
-    }
-    {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) ss[i] += __shfl_xor(ss[i], off, 64);
-      }
-      if (cc == 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) rkn[8 * rg + i] = l2norm ? rsqrtf(ss[i] + 1e-6f) : 1.f;
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(R1 + t128(8 * rg + i, 8 * cc)) = raw[i];
-    }
-  }
-  {
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) ss += sumsq8(rq[j]);
-    ss += __shfl_xor(ss, 1, 64);
-    ss += __shfl_xor(ss, 2, 64);
-    if ((tid & 3) == 0) rqn[qrow] = l2norm ? rsqrtf(ss + 1e-6f) : 1.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<u32x4*>(R2 + t128(qrow, 8 * (qs0 + j))) = mask8(rq[j], qrow < nvalid);
-  }
-  if (wave == 0) {  // gates: gamma = cumsum(g) over the pair, beta; zero past the sequence end (HF pads with 0)
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y0 = __shfl_up(g0, off, 64), y1 = __shfl_up(g1, off, 64);
-      if (lane >= off) { g0 += y0; g1 += y1; }
-    }
-    const float tot0 = __shfl(g0, 63, 64);
-    gam[lane] = g0;
-    gam[64 + lane] = tot0 + g1;
-    bet[lane] = b0;
-    bet[64 + lane] = b1;
-  }
-  for (int i = tid; i < kPFrags * 64; i += 512) {
-    const bf16x8 z = {};
-    Pf[i >> 6][i & 63] = z;
-  }
-  __syncthreads();
-  if (tid < kP) {
-    const float gt = gam[tid], gl = gam[kP - 1];
-    const f32x4 a = {gt, -bet[tid] * rkn[tid], rkn[tid], rqn[tid] * scale};
-    const f32x4 c = {bet[tid] * __expf(gt) * rkn[tid], bet[tid], rkn[tid] * __expf(gl - gt),
-                     tid < nvalid ? rqn[tid] * scale * __expf(gt) : 0.f};
-    pa[tid] = a;
-    pb[tid] = c;
-  }
-  __syncthreads();
-
-  // ---- 1. K K^T over the 8 row tiles of the pair (the 36 tiles x >= y: L00, L11 and the cross block L10) and
-  //         Q K^T (P, the 36 tiles s-tile <= t-tile). Wave w takes the K K^T row x = w (w + 1 tiles) and the
-  //         P row 7 - w (8 - w tiles), so that one operand of each row is loaded once and the waves stay balanced.
-  //         Cross and P tiles are computed transposed (positions s down each lane's 4 rows) so that every lane's 4
-  //         results are 4 consecutive k indices of a natural-order A fragment (one 8-byte store).
-  {
-    // The epilogues scale each product by per-position terms held in pa (LDS). Every pa value a tile needs is read
-    // into registers together with the tile's operand fragments, before its MFMAs, so that no LDS read latency sits
-    // between a product and its store (the epilogue stores to LDS, which the compiler will not move reads across).
-    const int x = wv, bt = 7 - wv;
-    const f32x4 pcx = pa[16 * x + li];    // cross tiles: column t of tile x
-    const f32x4 pcb = pa[16 * bt + li];   // P tiles: column t of tile bt
-    f32x4 prx[4];                         // diagonal tiles: rows t of tile x
-#pragma unroll
-    for (int r = 0; r < 4; ++r) prx[r] = pa[16 * x + 4 * lg + r];
-    auto kk_epilogue = [&](int y, const f32x4& acc, const f32x4 (&py)[4], const f32x4& pcy) {
-      if (x >= 4 && y < 4) {  // cross: rows s of tile y (py), column t of tile x (pcx)
-        const int t = 16 * x + li, s0 = 16 * y + 4 * lg;
-        float v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = pcx[1] * py[r][2] * acc[r] * __expf(pcx[0] - py[r][0]);
-        bf16x8* dst = &L10f[(x - 4) * 2 + (s0 >> 5)][(t & 15) + 16 * ((s0 & 31) >> 3)];
-        *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(dst) + 2 * (s0 & 7)) = pack4(v[0], v[1], v[2], v[3]);
-      } else {  // diagonal chunk block: rows t of tile x (prx), column s of tile y (pcy)
-        const int cb = x >= 4, s = 16 * y + li;
-        float* Am = R3 + cb * 64 * kFS;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = 16 * x + 4 * lg + r;
-          Am[(t - 64 * cb) * kFS + (s - 64 * cb)] =
-              s < t ? prx[r][1] * pcy[2] * acc[r] * __expf(prx[r][0] - pcy[0]) : 0.f;
-        }
-      }
-    };
-    auto p_epilogue = [&](int a, const f32x4& acc, const f32x4 (&pa4)[4]) {  // rows s of tile a, column t of bt
-      const int t = 16 * bt + li, s0 = 16 * a + 4 * lg;
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        v[r] = s0 + r <= t ? pcb[3] * pa4[r][2] * acc[r] * __expf(pcb[0] - pa4[r][0]) : 0.f;
-      bf16x8* dst = &Pf[pbase(bt) + (s0 >> 5)][(t & 15) + 16 * ((s0 & 31) >> 3)];
-      *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(dst) + 2 * (s0 & 7)) = pack4(v[0], v[1], v[2], v[3]);
-    };
-    bf16x8 fx[4], fq[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      fx[ks] = frag(R1, 16 * x + li, 32 * ks + 8 * lg);
-      fq[ks] = frag(R2, 16 * bt + li, 32 * ks + 8 * lg);
-    }
-#pragma unroll
-    for (int y0 = 0; y0 < 8; y0 += 2) {
-      if (y0 > x) break;
-      bf16x8 fy[2][4];
-      f32x4 py[2][4], pcy[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int yy = min(y0 + j, x);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) fy[j][ks] = frag(R1, 16 * yy + li, 32 * ks + 8 * lg);
-        pcy[j] = pa[16 * yy + li];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) py[j][r] = pa[16 * yy + 4 * lg + r];
-      }
-      f32x4 acc[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        acc[j] = zero4();
-        if (y0 + j > x) continue;
-        if (x >= 4 && y0 + j < 4) {
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) acc[j] = mfma16(fy[j][ks], fx[ks], acc[j]);
-        } else {
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) acc[j] = mfma16(fx[ks], fy[j][ks], acc[j]);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        if (y0 + j <= x) kk_epilogue(y0 + j, acc[j], py[j], pcy[j]);
-    }
-#pragma unroll
-    for (int a0 = 0; a0 < 8; a0 += 2) {
-      if (a0 > bt) break;
-      bf16x8 fa[2][4];
-      f32x4 pr[2][4];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int aa = min(a0 + j, bt);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) fa[j][ks] = frag(R1, 16 * aa + li, 32 * ks + 8 * lg);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pr[j][r] = pa[16 * aa + 4 * lg + r];
-      }
-      f32x4 acc[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        acc[j] = zero4();
-        if (a0 + j > bt) continue;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc[j] = mfma16(fa[j][ks], fq[ks], acc[j]);
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        if (a0 + j <= bt) p_epilogue(a0 + j, acc[j], pr[j]);
-    }
-  }
-  __syncthreads();
-
-  // ---- 2. the two chunk inverses T00, T11 (waves 0-3, 4-7); transposed k from the registers meanwhile, and the v
-  //         units (loaded here, written transposed once the inverses are done; the barriers in between order LDS
-  //         traffic only, so the v loads stay in flight through the inverses)
-  if (isK) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(R1 + t128(8 * cc + e, 8 * rg)) = column8(raw, e);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const size_t tok = (size_t)b * T + t0 + min(8 * rg + i, nvalid - 1);
-      raw[i] = raw8(v + (tok * H + h) * kD + 8 * cc);
-    }
-  }
-  {
-    float* Am = R3 + (wave >> 2) * 64 * kFS;
-    invert64(Am, wave & 3, lane, scr[wave], [] { lds_barrier(); });
-  }
-  if (!isK) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) raw[i] = mask8(raw[i], 8 * rg + i < nvalid);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(R2 + t128(8 * cc + e, 8 * rg)) = column8(raw, e);
-  }
-  __syncthreads();
-  // A operands held in registers: rows 16 rt .. of T00 scaled for W0 (waves 0-3) or U0 (waves 4-7), and of T11.
-  // T[t][s] (layout of invert64): diagonal block row-major with an implicit unit diagonal, the block below it stored
-  // transposed; both candidates are read and the right one selected (no divergent loads).
-  const int rt = wv & 3;
-  const bool isW = wv < 4;
-  bf16x8 a0[2], a1[2];
-  {
-    const int t = 16 * rt + li;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int s0 = 32 * ks + 8 * lg, bs = s0 >> 4;
-      float d0[8], d1[8], x0[8], x1[8];
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const f32x4 u0 = *reinterpret_cast<const f32x4*>(R3 + t * kFS + s0 + 4 * h2);
-        const f32x4 u1 = *reinterpret_cast<const f32x4*>(R3 + 64 * kFS + t * kFS + s0 + 4 * h2);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { d0[4 * h2 + e] = u0[e]; d1[4 * h2 + e] = u1[e]; }
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        x0[j] = R3[(s0 + j) * kFS + t];
-        x1[j] = R3[64 * kFS + (s0 + j) * kFS + t];
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int sj = s0 + j;
-        const float dg0 = (sj == t ? 1.f : 0.f) + (sj < t ? d0[j] : 0.f);
-        const float dg1 = (sj == t ? 1.f : 0.f) + (sj < t ? d1[j] : 0.f);
-        const float v0 = bs == rt ? dg0 : (bs < rt ? x0[j] : 0.f);
-        const float v1 = bs == rt ? dg1 : (bs < rt ? x1[j] : 0.f);
-        a0[ks][j] = (__bf16)(v0 * (isW ? pb[sj][0] : pb[sj][1]));
-        a1[ks][j] = (__bf16)v1;
-      }
-    }
-  }
-  __syncthreads();  // R3 (fp32 T) is free: it becomes W^T
-
-  // ---- 3. W0 = T00 diag(beta e^gamma rk) K0, U0 = T00 diag(beta) V0   (wave: row tile rt; W or U; 8 col tiles)
-  char* XT = isW ? WT : R2;  // this wave's destination (W^T or U^T, [d][pos])
-  {
-    const char* src = isW ? R1 : R2;
-    f32x4 acc[8];
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct) {
-      acc[ct] = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) acc[ct] = mfma16(a0[ks], frag(src, 16 * ct + li, 32 * ks + 8 * lg), acc[ct]);
-    }
-    __syncthreads();  // every wave has read chunk 0 of V^T before U0 replaces it
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct)
-      *reinterpret_cast<u32x2*>(XT + t128(16 * ct + li, 16 * rt + 4 * lg)) =
-          pack4(acc[ct][0], acc[ct][1], acc[ct][2], acc[ct][3]);
-  }
-  __syncthreads();
-
-  // ---- 4. Z = L10 [W0 | U0] + [K'1 | V'1]   (chunk-1 columns of W^T / U^T; U^T overwrites V^T in place)
-  {
-    f32x4 acc[8];
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct) {
-      acc[ct] = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        acc[ct] = mfma16(L10f[rt * 2 + ks][lane], frag(XT, 16 * ct + li, 32 * ks + 8 * lg), acc[ct]);
-    }
-    const char* raw_src = isW ? R1 : R2;
-    const int t = 64 + 16 * rt + 4 * lg;
-    float sc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = isW ? pb[t + r][0] : pb[t + r][1];
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct) {
-      const int d = 16 * ct + li;
-      const f32x4 x = unpack4(*reinterpret_cast<const u32x2*>(raw_src + t128(d, t)));
-      *reinterpret_cast<u32x2*>(XT + t128(d, t)) =
-          pack4(acc[ct][0] + x[0] * sc[0], acc[ct][1] + x[1] * sc[1], acc[ct][2] + x[2] * sc[2],
-                acc[ct][3] + x[3] * sc[3]);
-    }
-  }
-  __syncthreads();
-
-  // ---- 5. W1 = T11 Z_W, U1 = T11 Z_U
-  {
-    f32x4 acc[8];
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct) {
-      acc[ct] = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) acc[ct] = mfma16(a1[ks], frag(XT, 16 * ct + li, 64 + 32 * ks + 8 * lg), acc[ct]);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct)
-      *reinterpret_cast<u32x2*>(XT + t128(16 * ct + li, 64 + 16 * rt + 4 * lg)) =
-          pack4(acc[ct][0], acc[ct][1], acc[ct][2], acc[ct][3]);
-  }
-  __syncthreads();
-
-  // ---- 6. M = -K~^T W (computed as its transpose M^T = -W^T K~, whose 16 x 16 tiles pack straight into M's A
-  //         fragments) and Bm = K~^T U. Wave w: d tiles 4 (w / 4) .. + 3 of K~ (shared by both products), the d' tile
-  //         pair of k step w % 4 for M^T, the value-slice pair 2 (w % 4) .. + 1 for Bm.
-  const float gl = gam[kP - 1];
-  const int dq = 4 * (wv >> 2), kq = wv & 3;
-  // q rows of the Q' products of step 7, loaded now so that their latency is covered by step 6
-  Raw4 qraw[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = 16 * (dq + i) + li;
-    const __bf16* qr = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
-#pragma unroll
-    for (int a = 0; a < 2; ++a) qraw[i][a].load(qr + 16 * (2 * kq + a) + 4 * lg);
-  }
-  {
-    bf16x8 F[4][4];  // K~ [positions 32 ks + 8 lg + j][d 16 (dq + i) + li]
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) F[i][ks] = frag(R1, 16 * (dq + i) + li, 32 * ks + 8 * lg);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      float sc[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sc[j] = pb[32 * ks + 8 * lg + j][2];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) F[i][ks][j] = (__bf16)((float)F[i][ks][j] * sc[j]);
-    }
-    bf16x8 wf[2][4], uf[2][4];
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        wf[a][ks] = frag(WT, 16 * (2 * kq + a) + li, 32 * ks + 8 * lg);
-        uf[a][ks] = frag(R2, 16 * (2 * kq + a) + li, 32 * ks + 8 * lg);
-      }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 lo = zero4(), hi = zero4();
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        lo = mfma16(wf[0][ks], F[i][ks], lo);
-        hi = mfma16(wf[1][ks], F[i][ks], hi);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) { lo[r] = -lo[r]; hi[r] = -hi[r]; }
-      *reinterpret_cast<bf16x8*>(rec + kRecM + ((size_t)((dq + i) * 4 + kq) * 64 + lane) * 16) = pack8(lo, hi);
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc = mfma16(F[i][ks], uf[a][ks], acc);
-        *reinterpret_cast<u32x2*>(rec + kRecB + ((size_t)((dq + i) * 8 + 2 * kq + a) * 64 + lane) * 8) =
-            pack4(acc[0], acc[1], acc[2], acc[3]);
-      }
-    }
-  }
-
-  // ---- 7. Q' = Q^ e^gamma - P W (as its transpose) and R = P U. Wave w: position tiles 4 (w / 4) .. + 3 (P is zero
-  //         above the diagonal: row tile b has b / 2 + 1 k steps), the d' tile pair 2 (w % 4) .. + 1 for Q'^T, the
-  //         value-slice pair 2 (w % 4) .. + 1 for R (as its transpose, so that the scan's output tiles come out
-  //         with four consecutive value columns per lane).
-  {
-    bf16x8 wf[2][4], uf[2][4];
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        wf[a][ks] = frag(WT, 16 * (2 * kq + a) + li, 32 * ks + 8 * lg);
-        uf[a][ks] = frag(R2, 16 * (2 * kq + a) + li, 32 * ks + 8 * lg);
-      }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int bt = dq + i, nks = (bt >> 1) + 1;
-      const int t = 16 * bt + li;
-      f32x4 qt[2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a) qt[a] = qraw[i][a].f();
-      bf16x8 pf[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) pf[ks] = Pf[pbase(bt) + min(ks, nks - 1)][lane];
-      f32x4 qp[2], rr[2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a) { qp[a] = zero4(); rr[a] = zero4(); }
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (ks < nks) {
-#pragma unroll
-          for (int a = 0; a < 2; ++a) {
-            qp[a] = mfma16(wf[a][ks], pf[ks], qp[a]);
-            rr[a] = mfma16(uf[a][ks], pf[ks], rr[a]);  // R^T = U^T P^T: the tile in transposed D order
-          }
-        }
-      }
-      const float fq = pb[t][3];
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) qp[a][r] = qt[a][r] * fq - qp[a][r];
-      *reinterpret_cast<bf16x8*>(rec + kRecQ + ((size_t)(bt * 4 + kq) * 64 + lane) * 16) = pack8(qp[0], qp[1]);
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-        *reinterpret_cast<u32x2*>(rec + kRecR + ((size_t)(bt * 8 + 2 * kq + a) * 64 + lane) * 8) =
-            pack4(rr[a][0], rr[a][1], rr[a][2], rr[a][3]);
-    }
-  }
-  if (tid == 0) *reinterpret_cast<float*>(rec + kRecE) = __expf(gl);
-}
-
 // ---------------------------------------------------------------------------------------------------------------
 // gdn_pair_prep4_kernel: the records of one (pair, head, row) from a 4-wave block with at most 80 KB of LDS and 256
 // VGPRs, so that two blocks share a compute unit and every block of a T = 4096, 16-head call is resident at once (one
-// block's memory and barrier waits are covered by the other's work). Same records, same math, as laid out above.
+// block's memory and barrier waits are covered by the other's work).
 //
 // Dataflow. Waves 0-1 ("W waves") own value tiles D0 .. D0 + 3 (D0 = 4 (w & 1)) of W; waves 2-3 ("U waves") the same
 // tiles of U. Each wave forms its tiles for all 128 positions (W0 = T00 K'0, Z = L10 W0 + K'1, W1 = T11 Z; U alike),
@@ -672,10 +206,20 @@ constexpr int kRS = 272;  // bytes per row of a padded [128][128] bf16 LDS tile
 __device__ __forceinline__ bf16x8 ldf(const char* tile, int r, int c) {  // row r, columns c .. c + 7
   return *reinterpret_cast<const bf16x8*>(tile + r * kRS + 2 * c);
 }
-// row r, the 8 columns of k step c0 held by lane group g in kmap order: c0 + 4 g .. + 3 and c0 + 16 + 4 g .. + 3
-__device__ __forceinline__ bf16x8 ldf_km(const char* tile, int r, int c0, int g) {
-  const u32x2 a = *reinterpret_cast<const u32x2*>(tile + r * kRS + 2 * (c0 + 4 * g));
-  const u32x2 b = *reinterpret_cast<const u32x2*>(tile + r * kRS + 2 * (c0 + 16 + 4 * g));
+// The transposed tiles (K^T, V^T: rows d, columns positions) swap 16-byte column chunks by row group: chunk j of
+// row r is stored at chunk j ^ ((r / 16) % 8). A transposed write of 16 rows 8 apart then covers every bank once, while
+// the fragment reads (16 consecutive rows of one group at one column) stay conflict-free.
+__device__ __forceinline__ int tsw(int rg, int c) {  // byte offset of column c in a row of row group rg
+  return 16 * ((c >> 3) ^ (rg & 7)) + 2 * (c & 7);
+}
+__device__ __forceinline__ bf16x8 ldf_t(const char* tile, int rg, int li, int c) {  // row 16 rg + li, columns c .. + 7
+  return *reinterpret_cast<const bf16x8*>(tile + (16 * rg + li) * kRS + tsw(rg, c));
+}
+// row 16 rg + li, the 8 columns of k step c0 held by lane group g in kmap order: c0 + 4 g .. + 3, c0 + 16 + 4 g .. + 3
+__device__ __forceinline__ bf16x8 ldf_km_t(const char* tile, int rg, int li, int c0, int g) {
+  const char* row = tile + (16 * rg + li) * kRS;
+  const u32x2 a = *reinterpret_cast<const u32x2*>(row + tsw(rg, c0 + 4 * g));
+  const u32x2 b = *reinterpret_cast<const u32x2*>(row + tsw(rg, c0 + 16 + 4 * g));
   const u32x4 v = {a.x, a.y, b.x, b.y};
   return __builtin_bit_cast(bf16x8, v);
 }
@@ -699,29 +243,30 @@ __device__ __forceinline__ void invert64x2(float* Am2, int wv, int lane) {
   const int c0 = wv & 1, c1 = 3 - c0;
   auto blk = [&](int bi, int bj) { return Am + (16 * bi) * kFS + 16 * bj; };
   {
-    float ta[16], tb[16];
+    // lane groups 0-1 take diagonal block c0, groups 2-3 block c1 (groups 1 and 3 repeat 0 and 2); lane li keeps
+    // column li, T'[i][li] = L[i][li] + sum_{j < i} L[i][j] T'[j][li], with row i of L read from LDS as a broadcast
+    // (LDS keeps L until the end)
+    // (the scheduling barriers keep the compiler from hoisting every row's reads at once, which would hold 60 more
+    // registers at the kernel's register limit)
+    float* Dg = lg < 2 ? blk(c0, c0) : blk(c1, c1);
+    float tc[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      ta[i] = blk(c0, c0)[i * kFS + li];
-      tb[i] = blk(c1, c1)[i * kFS + li];
-    }
+    for (int i = 0; i < 16; ++i) tc[i] = Dg[i * kFS + li];
 #pragma unroll
     for (int i = 1; i < 16; ++i) {
-      float aa = ta[i], ab = tb[i];
+      f32x4 lr[4];
 #pragma unroll
-      for (int j = 0; j < i; ++j) {
-        aa += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ta[i]), j)) * ta[j];
-        ab += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tb[i]), j)) * tb[j];
-      }
-      ta[i] = aa;
-      tb[i] = ab;
+      for (int q = 0; q < 4; ++q)
+        if (4 * q < i) lr[q] = *reinterpret_cast<const f32x4*>(Dg + i * kFS + 4 * q);
+      float acc = tc[i];
+#pragma unroll
+      for (int j = 0; j < i; ++j) acc += lr[j >> 2][j & 3] * tc[j];
+      tc[i] = acc;
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (lane < 16) {
+    if ((lg & 1) == 0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        blk(c0, c0)[i * kFS + lane] = ta[i];
-        blk(c1, c1)[i * kFS + lane] = tb[i];
-      }
+      for (int i = 0; i < 16; ++i) Dg[i * kFS + li] = tc[i];
     }
   }
   lds_barrier();
@@ -795,18 +340,20 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
   //         transposed into K^T (RB); the wave's own q rows (row tiles X0 = w, X1 = 7 - w) as B fragments in
   //         registers; the gates (wave 0). Every load goes out before any is used.
   const int ur = tid >> 4, uc = tid & 15;
+  // per-block bases (64-bit, uniform) and 32-bit offsets inside the pair (T H 128 < 2^31 is checked by the launcher)
+  const __bf16* kb = k + (((size_t)b * T + t0) * Hk + kh) * kD;
+  const __bf16* qb = q + (((size_t)b * T + t0) * Hk + kh) * kD;
+  const __bf16* vb = v + (((size_t)b * T + t0) * H + h) * kD;
+  const int kstride = Hk * kD, vstride = H * kD;
   u32x4 raw[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const size_t tok = (size_t)b * T + t0 + min(8 * ur + i, nvalid - 1);
-    raw[i] = raw8(k + (tok * Hk + kh) * kD + 8 * uc);
-  }
+  for (int i = 0; i < 8; ++i) raw[i] = raw8(kb + min(8 * ur + i, nvalid - 1) * kstride + 8 * uc);
   const int X0 = wv, X1 = 7 - wv;
   bf16x8 qf[2][4];
 #pragma unroll
   for (int a = 0; a < 2; ++a) {
     const int t = 16 * (a ? X1 : X0) + li;
-    const __bf16* src = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
+    const __bf16* src = qb + min(t, nvalid - 1) * kstride;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) qf[a][ks] = *reinterpret_cast<const bf16x8*>(src + 32 * ks + 8 * lg);
   }
@@ -836,7 +383,8 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
 #pragma unroll
     for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(RA + (8 * ur + i) * kRS + 16 * uc) = raw[i];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(RB + (8 * uc + e) * kRS + 16 * ur) = column8(raw, e);
+    for (int e = 0; e < 8; ++e)
+      *reinterpret_cast<u32x4*>(RB + (8 * uc + e) * kRS + 16 * (ur ^ ((uc >> 1) & 7))) = column8(raw, e);
   }
 #pragma unroll
   for (int a = 0; a < 2; ++a) {
@@ -906,24 +454,29 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
   lds_barrier();  // the k tile (RA) is read by every wave: now it becomes L
 
   // epilogues. gamma is non-increasing; tile factors relative to the tile's first row r = 16 X.
-  bf16x8 pfr[2][4];  // P B-fragments of row tiles X0, X1: [k step] (kmap order), zero above the diagonal
+  // P B-fragments of row tiles X0 (<= 3: k steps 0-1) and X1 (k steps 0-3), kmap order, zero above the diagonal
+  bf16x8 pfr0[2], pfr1[4];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) pfr[a][ks] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+  for (int ks = 0; ks < 4; ++ks) {
+    if (ks < 2) pfr0[ks] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+    pfr1[ks] = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+  }
   auto epilogue = [&](auto aconst) {
     constexpr int a = decltype(aconst)::value;
     constexpr int NY = a ? 8 : 4;
     const int X = a ? X1 : X0;
     const float gr = cf[0][16 * X];
     // rows t = 16 X + 4 lg + r (normal tiles) and the lane's own t = 16 X + li (transposed tiles)
-    f32x4 rowL, gtr, ltr;
+    f32x4 rowL, ltr;
+    const f32x4 gtr = *reinterpret_cast<const f32x4*>(&cf[0][16 * X + 4 * lg]);
+    {
+      const f32x4 bt4 = *reinterpret_cast<const f32x4*>(&cf[1][16 * X + 4 * lg]);
+      const f32x4 rk4 = *reinterpret_cast<const f32x4*>(&cf[2][16 * X + 4 * lg]);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * X + 4 * lg + r;
-      gtr[r] = cf[0][t];
-      ltr[r] = -cf[1][t] * cf[2][t];
-      rowL[r] = ltr[r] * __expf(gtr[r] - gr);
+      for (int r = 0; r < 4; ++r) {
+        ltr[r] = -bt4[r] * rk4[r];
+        rowL[r] = ltr[r] * __expf(gtr[r] - gr);
+      }
     }
     const int tl = 16 * X + li;
     const float gt = cf[0][tl];
@@ -936,14 +489,11 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
       // normal-tile column s = 16 y + li; transposed-tile columns s = 16 y + 4 lg + r
       const int sn = 16 * y + li;
       const float colN = cf[2][sn] * __expf(gr - cf[0][sn]);
-      f32x4 colT, gsT, rkT;
+      f32x4 colT;
+      const f32x4 gsT = *reinterpret_cast<const f32x4*>(&cf[0][16 * y + 4 * lg]);
+      const f32x4 rkT = *reinterpret_cast<const f32x4*>(&cf[2][16 * y + 4 * lg]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int s = 16 * y + 4 * lg + r;
-        gsT[r] = cf[0][s];
-        rkT[r] = cf[2][s];
-        colT[r] = rkT[r] * __expf(gr - gsT[r]);
-      }
+      for (int r = 0; r < 4; ++r) colT[r] = rkT[r] * __expf(gr - gsT[r]);
       // P (transposed): rows s of tile y, column t = tl
       {
         f32x4 acc;
@@ -956,9 +506,10 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
                        : rowT_P * colT[r] * acc[r];
         }
         const u32x2 pk = pack4(pv[0], pv[1], pv[2], pv[3]);
-        u32x4 cur = __builtin_bit_cast(u32x4, pfr[a][y >> 1]);
+        bf16x8& slot = a ? pfr1[y >> 1] : pfr0[(y >> 1) & 1];
+        u32x4 cur = __builtin_bit_cast(u32x4, slot);
         if (y & 1) { cur.z = pk.x; cur.w = pk.y; } else { cur.x = pk.x; cur.y = pk.y; }
-        pfr[a][y >> 1] = __builtin_bit_cast(bf16x8, cur);
+        slot = __builtin_bit_cast(bf16x8, cur);
       }
       if (a == 1 && y < 4) {
         // L10 (transposed): rows s of tile y (chunk 0), column t = tl (chunk 1); below the diagonal, no mask
@@ -997,10 +548,7 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
     if (tid == 0) *reinterpret_cast<float*>(rec + kRecE) = __expf(gl);
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const size_t tok = (size_t)b * T + t0 + min(8 * ur + i, nvalid - 1);
-    raw[i] = raw8(v + (tok * H + h) * kD + 8 * uc);
-  }
+  for (int i = 0; i < 8; ++i) raw[i] = raw8(vb + min(8 * ur + i, nvalid - 1) * vstride + 8 * uc);
   invert64x2(Am, wv, lane);
   lds_barrier();
 
@@ -1049,21 +597,21 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
 #pragma unroll
   for (int i = 0; i < 8; ++i) raw[i] = mask8(raw[i], 8 * ur + i < nvalid);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(RA + (8 * uc + e) * kRS + 16 * ur) = column8(raw, e);
+  for (int e = 0; e < 8; ++e)
+    *reinterpret_cast<u32x4*>(RA + (8 * uc + e) * kRS + 16 * (ur ^ ((uc >> 1) & 7))) = column8(raw, e);
   lds_barrier();
 
   // ---- 3-5. X0 = T00 diag(c) K0 (or V0), Z = L10 X0 + diag(c) K1, X1 = T11 Z, for this wave's value tiles D0 + D.
-  //           The results stay in registers as 32-wide k steps over positions (kmap order): xn unscaled, xk scaled by
-  //           the K~ factor rk e^(gamma_last - gamma) of each position.
+  //           The results stay in registers as 32-wide k steps over positions (kmap order).
   const int D0 = 4 * (wv & 1);
   const char* src = isW ? RB : RA;  // K^T or V^T
-  bf16x8 xn[4][4], xk[4][4];        // [D][position k step]
+  bf16x8 xn[4][4];                  // [D][position k step]
   {
     bf16x8 bs[4][2];
 #pragma unroll
     for (int D = 0; D < 4; ++D)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) bs[D][ks] = ldf(src, 16 * (D0 + D) + li, 32 * ks + 8 * lg);
+      for (int ks = 0; ks < 2; ++ks) bs[D][ks] = ldf_t(src, D0 + D, li, 32 * ks + 8 * lg);
     f32x4 x0[4][4];
 #pragma unroll
     for (int X = 0; X < 4; ++X)
@@ -1076,16 +624,13 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
         x0[X][D] = acc;
       }
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const f32x4 sa = *reinterpret_cast<const f32x4*>(&cf[2][32 * kt + 4 * lg]);
-      const f32x4 sb = *reinterpret_cast<const f32x4*>(&cf[2][32 * kt + 16 + 4 * lg]);
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int D = 0; D < 4; ++D) {
-        xn[D][kt] = pack8(x0[2 * kt][D], x0[2 * kt + 1][D]);
-        xk[D][kt] = pack8(scale4(x0[2 * kt][D], sa), scale4(x0[2 * kt + 1][D], sb));
-      }
-    }
+      for (int D = 0; D < 4; ++D) xn[D][kt] = pack8(x0[2 * kt][D], x0[2 * kt + 1][D]);
   }
+  // V^T is last read by Z: the P fragments go to LDS before X1 is formed, so that they are out of registers where
+  // the most values are live
+  bf16x8 zf[4][2];
   {
     f32x4 z[4][4];
 #pragma unroll
@@ -1097,18 +642,42 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
 #pragma unroll
       for (int D = 0; D < 4; ++D) {
         const f32x4 x = unpack4(*reinterpret_cast<const u32x2*>(src + (16 * (D0 + D) + li) * kRS +
-                                                              2 * (64 + 16 * X + 4 * lg)));
+                                                              tsw(D0 + D, 64 + 16 * X + 4 * lg)));
         f32x4 acc = scale4(x, c);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) acc = mfma16(la[ks], xn[D][ks], acc);
         z[X][D] = acc;
       }
     }
-    bf16x8 zf[4][2];
 #pragma unroll
     for (int D = 0; D < 4; ++D)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) zf[D][ks] = pack8(z[2 * ks][D], z[2 * ks + 1][D]);
+  }
+  lds_barrier();  // V^T (RA) and K^T (RB) are read: RA takes the P fragments, RB becomes K~^T in place
+  {
+    bf16x8* Pf = reinterpret_cast<bf16x8*>(RA);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks < 2 && ks <= (X0 >> 1)) Pf[(pbase(X0) + ks) * 64 + lane] = pfr0[ks];
+      if (ks <= (X1 >> 1)) Pf[(pbase(X1) + ks) * 64 + lane] = pfr1[ks];
+    }
+    // K~[t][d] = k[t][d] rk_t e^(gamma_last - gamma_t): chunk j of row d holds positions 8 (j ^ (d / 16 % 8)) .. + 7
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = tid + 256 * i, d = c >> 4, j = c & 15;
+      u32x4* p = reinterpret_cast<u32x4*>(RB + d * kRS + 16 * j);
+      const int t0s = 8 * (j ^ ((d >> 4) & 7));
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(&cf[2][t0s]);
+      const f32x4 s1 = *reinterpret_cast<const f32x4*>(&cf[2][t0s + 4]);
+      const u32x4 w = *p;
+      const f32x4 a = unpack4(u32x2{w.x, w.y}), bb = unpack4(u32x2{w.z, w.w});
+      const u32x2 lo = pack4(a[0] * s0[0], a[1] * s0[1], a[2] * s0[2], a[3] * s0[3]);
+      const u32x2 hi = pack4(bb[0] * s1[0], bb[1] * s1[1], bb[2] * s1[2], bb[3] * s1[3]);
+      *p = u32x4{lo.x, lo.y, hi.x, hi.y};
+    }
+  }
+  {
     f32x4 x1[4][4];
 #pragma unroll
     for (int X = 0; X < 4; ++X)
@@ -1121,28 +690,24 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
         x1[X][D] = acc;
       }
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const f32x4 sa = *reinterpret_cast<const f32x4*>(&cf[2][64 + 32 * kt + 4 * lg]);
-      const f32x4 sb = *reinterpret_cast<const f32x4*>(&cf[2][64 + 32 * kt + 16 + 4 * lg]);
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int D = 0; D < 4; ++D) {
-        xn[D][2 + kt] = pack8(x1[2 * kt][D], x1[2 * kt + 1][D]);
-        xk[D][2 + kt] = pack8(scale4(x1[2 * kt][D], sa), scale4(x1[2 * kt + 1][D], sb));
-      }
-    }
+      for (int D = 0; D < 4; ++D) xn[D][2 + kt] = pack8(x1[2 * kt][D], x1[2 * kt + 1][D]);
   }
-  lds_barrier();  // V^T (RA) is read: RA takes the P fragments
-  {
-    bf16x8* Pf = reinterpret_cast<bf16x8*>(RA);
+  lds_barrier();  // the P fragments and K~^T are in LDS
+
+  // q values of the Q' products (W waves: rows t = 16 X + li, columns 16 (D0 + D) + 4 lg ..), loaded ahead of use:
+  // row tiles 0-1 before the M products, 2-7 after them
+  u32x2 qpre[8][4];
+  auto load_q = [&](int X) {
+    const __bf16* qr = qb + min(16 * X + li, nvalid - 1) * kstride;
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const int X = a ? X1 : X0;
+    for (int D = 0; D < 4; ++D) qpre[X][D] = *reinterpret_cast<const u32x2*>(qr + 16 * (D0 + D) + 4 * lg);
+  };
+  if (isW) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        if (ks <= (X >> 1)) Pf[(pbase(X) + ks) * 64 + lane] = pfr[a][ks];
-    }
+    for (int X = 0; X < 1; ++X) load_q(X);
   }
-  lds_barrier();
 
   // ---- 6. W waves: M^T = -W^T K~ (rows d' = 16 (D0 + D) .., columns d = 16 E ..), stored as M's A fragments;
   //         U waves: Bm = K~^T U (rows d = 16 E .., columns dv = 16 (D0 + D) ..), stored in D order.
@@ -1150,14 +715,14 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
   for (int E = 0; E < 8; ++E) {
     bf16x8 kf[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) kf[kt] = ldf_km(RB, 16 * E + li, 32 * kt, lg);
+    for (int kt = 0; kt < 4; ++kt) kf[kt] = ldf_km_t(RB, E, li, 32 * kt, lg);
     if (isW) {
       f32x4 acc[4];
 #pragma unroll
       for (int D = 0; D < 4; ++D) {
         acc[D] = zero4();
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) acc[D] = mfma16(xk[D][kt], kf[kt], acc[D]);
+        for (int kt = 0; kt < 4; ++kt) acc[D] = mfma16(xn[D][kt], kf[kt], acc[D]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[D][r] = -acc[D][r];
       }
@@ -1170,7 +735,7 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
       for (int D = 0; D < 4; ++D) {
         f32x4 acc = zero4();
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) acc = mfma16(kf[kt], xk[D][kt], acc);
+        for (int kt = 0; kt < 4; ++kt) acc = mfma16(kf[kt], xn[D][kt], acc);
         *reinterpret_cast<u32x2*>(rec + kRecB + ((size_t)(E * 8 + D0 + D) * 64 + lane) * 8) =
             pack4(acc[0], acc[1], acc[2], acc[3]);
       }
@@ -1181,6 +746,10 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
   //         R^T = U^T P^T (rows dv, columns t), stored in transposed D order. P is zero above the diagonal: row tile X
   //         has X / 2 + 1 k steps.
   const bf16x8* Pf = reinterpret_cast<const bf16x8*>(RA);
+  if (isW) {
+#pragma unroll
+    for (int X = 1; X < 8; ++X) load_q(X);
+  }
 #pragma unroll
   for (int X = 0; X < 8; ++X) {
     const int t = 16 * X + li;
@@ -1188,12 +757,11 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) pf[ks] = Pf[(pbase(X) + min(ks, X >> 1)) * 64 + lane];
     if (isW) {
-      const __bf16* qr = q + (((size_t)b * T + t0 + min(t, nvalid - 1)) * Hk + kh) * kD;
       const float cq = cf[3][t];
       f32x4 acc[4];
 #pragma unroll
       for (int D = 0; D < 4; ++D) {
-        const f32x4 qv = unpack4(*reinterpret_cast<const u32x2*>(qr + 16 * (D0 + D) + 4 * lg));
+        const f32x4 qv = unpack4(qpre[X][D]);
         f32x4 pw = zero4();
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
