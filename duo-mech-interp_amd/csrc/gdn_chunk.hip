@@ -30,8 +30,9 @@
 // value columns of one position and writes them with one 8-byte store); the bf16 state is exchanged through LDS once
 // per pair.
 // Operands stream straight from L2 into registers three pairs ahead (12 waves keep about 40 KB of loads in flight per
-// CU); a thirteenth wave touches the records several pairs further ahead so that the first of the 16 blocks to need a
-// line finds it in L2. The 16 blocks of a head are placed on one XCD (they share its L2).
+// CU). The 16 blocks of a head are placed on one XCD (they share its L2). Each pair costs about 0.9 us: the state
+// update's LDS exchange, barrier and 4 dependent MFMAs take about 0.3 us, and the rest follows the 54 KB of operands
+// each compute unit streams per pair (M alone is 32 KB, needed whole by every slice).
 #include <type_traits>
 
 #include "q35_common.h"
@@ -56,7 +57,6 @@ constexpr size_t kRecE = 131072;      // exp(gamma_last) fp32
 constexpr size_t kRecBytes = 131328;  // 256-byte aligned
 
 constexpr int kScanAhead = 3;    // pairs whose operands are held in registers ahead of use
-constexpr int kTouchAhead = 8;   // pairs ahead of use that the L2 warm-up wave touches
 
 // k index of position j (0..7) of lane group g in a 32-wide K step fed from two 16-row accumulator tiles
 __device__ __forceinline__ int kmap(int g, int j) { return j < 4 ? 4 * g + j : 12 + 4 * g + j; }
@@ -232,11 +232,14 @@ __device__ __forceinline__ f32x4 scale4(const f32x4& a, const f32x4& s) {
 
 // Inverses T = (I - L)^-1 of the two unit lower-triangular 64 x 64 blocks of a pair, in place in Am (two [64][kFS]
 // fp32 arrays, strictly-lower L on entry with zeros on and above the diagonal of the diagonal 16 x 16 blocks; on exit
-// T row-major with the strictly-lower part of its diagonal blocks stored and the unit diagonal implicit). Wave w takes
-// matrix w / 2 and block columns c and 3 - c (c = w % 2): the two diagonal inverses (forward substitution, the two
-// chains interleaved), then the two block columns T_ij = (I + T'_ii) sum_{k=j}^{i-1} L_ik T_kj, whose blocks are kept
-// transposed in the unused upper block (j, i) while other columns still read L, and rewritten row-major in place of
-// L_ij at the end.
+// T row-major with the strictly-lower part of its diagonal blocks stored and the unit diagonal implicit). Waves 2 m and
+// 2 m + 1 take matrix m. With T_ii = I + T'_ii the diagonal inverses (forward substitution, wave w the blocks c and
+// 3 - c, c = w % 2), the blocks below the diagonal follow from T_ij = T_ii sum_{k=j}^{i-1} L_ik T_kj in two levels of
+// 2 x 2 block inversion:
+//   level 1 (32 x 32 diagonal halves):  T_10 = T_11 L_10 T_00 (wave 2 m),  T_32 = T_33 L_32 T_22 (wave 2 m + 1)
+//   level 2 (block column j = w % 2):    X_2j = L_20 T_0j + L_21 T_1j,  X_3j = L_30 T_0j + L_31 T_1j,
+//                                        T_2j = T_22 X_2j,  T_3j = T_33 X_3j + T_32 X_2j
+// Operands that a product takes as its B side are also stored transposed in the free blocks above the diagonal.
 __device__ __forceinline__ void invert64x2(float* Am2, int wv, int lane) {
   const int li = lane & 15, lg = lane >> 4;
   float* Am = Am2 + (wv >> 1) * 64 * kFS;
@@ -269,46 +272,48 @@ __device__ __forceinline__ void invert64x2(float* Am2, int wv, int lane) {
       for (int i = 0; i < 16; ++i) Dg[i * kFS + li] = tc[i];
     }
   }
-  lds_barrier();
-  f32x4 tfin[3];  // column c0's blocks (c0 + 1 ..), then column c1's (at most 3 in all: columns {0, 3} or {1, 2})
-  int nf = 0;
+  lds_barrier();  // the diagonal blocks are inverted
+  const bool wa = (wv & 1) == 0;
+  auto ld_d = [&](const float* b) {  // a 16 x 16 block in the accumulator layout
+    f32x4 v;
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc) {
-    const int j = cc ? c1 : c0;
-    for (int i = j + 1; i < 4; ++i) {
-      f32x4 acc;
-      const float* Lij = blk(i, j);
+    for (int r = 0; r < 4; ++r) v[r] = b[(4 * lg + r) * kFS + li];
+    return v;
+  };
+  auto st_d = [&](float* b, const f32x4& v) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = Lij[(4 * lg + r) * kFS + li];
-      acc = mm16_f32(Lij, kFS, blk(j, j), kFS, false, acc, lane);
-      for (int kk = j + 1; kk < i; ++kk) acc = mm16_f32(blk(i, kk), kFS, blk(j, kk), kFS, true, acc, lane);
-      // the partial sum goes into block (j, i) transposed, the final T_ij over it
-      *reinterpret_cast<f32x4*>(blk(j, i) + li * kFS + 4 * lg) = acc;
-      __builtin_amdgcn_wave_barrier();
-      acc = mm16_f32(blk(i, i), kFS, blk(j, i), kFS, true, acc, lane);
-      __builtin_amdgcn_wave_barrier();
-      *reinterpret_cast<f32x4*>(blk(j, i) + li * kFS + 4 * lg) = acc;
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int q = 0; q < 3; ++q)
-        if (q == nf) tfin[q] = acc;
-      ++nf;
-    }
+    for (int r = 0; r < 4; ++r) b[(4 * lg + r) * kFS + li] = v[r];
+  };
+  auto st_t = [&](float* b, const f32x4& v) { *reinterpret_cast<f32x4*>(b + li * kFS + 4 * lg) = v; };
+  {
+    // level 1: T_hl = (I + T'_hh) (L_hl + L_hl T'_ll), (h, l) = (1, 0) or (3, 2); L_hl is read by this wave only
+    const int l = wa ? 0 : 2, h = l + 1;
+    f32x4 acc = mm16_f32(blk(h, l), kFS, blk(l, l), kFS, false, ld_d(blk(h, l)), lane);
+    st_t(blk(l, h), acc);
+    __builtin_amdgcn_wave_barrier();
+    acc = mm16_f32(blk(h, h), kFS, blk(l, h), kFS, true, acc, lane);
+    __builtin_amdgcn_wave_barrier();
+    st_d(blk(h, l), acc);
+    st_t(blk(l, h), acc);
   }
-  lds_barrier();  // every column done: the L blocks below the diagonal are no longer read
-  nf = 0;
-#pragma unroll
-  for (int cc = 0; cc < 2; ++cc) {
-    const int j = cc ? c1 : c0;
-    for (int i = j + 1; i < 4; ++i) {
-      f32x4 v = tfin[0];
-#pragma unroll
-      for (int q = 1; q < 3; ++q)
-        if (q == nf) v = tfin[q];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) blk(i, j)[(4 * lg + r) * kFS + li] = v[r];
-      ++nf;
+  lds_barrier();  // T_10 (also transposed in block (0, 1)) and T_32 are in place
+  {
+    const int j = wa ? 0 : 1;
+    f32x4 x2 = mm16_f32(blk(2, j), kFS, blk(j, j), kFS, false, ld_d(blk(2, j)), lane);
+    f32x4 x3 = mm16_f32(blk(3, j), kFS, blk(j, j), kFS, false, ld_d(blk(3, j)), lane);
+    if (wa) {  // column 0 also takes L_21 T_10, L_31 T_10
+      x2 = mm16_f32(blk(2, 1), kFS, blk(0, 1), kFS, true, x2, lane);
+      x3 = mm16_f32(blk(3, 1), kFS, blk(0, 1), kFS, true, x3, lane);
     }
+    st_t(blk(j, 2), x2);
+    st_t(blk(j, 3), x3);
+    __builtin_amdgcn_wave_barrier();
+    const f32x4 t2 = mm16_f32(blk(2, 2), kFS, blk(j, 2), kFS, true, x2, lane);
+    f32x4 t3 = mm16_f32(blk(3, 3), kFS, blk(j, 3), kFS, true, x3, lane);
+    t3 = mm16_f32(blk(3, 2), kFS, blk(j, 2), kFS, true, t3, lane);
+    lds_barrier();  // every L block below the diagonal is read
+    st_d(blk(2, j), t2);
+    st_d(blk(3, j), t3);
   }
 }
 
@@ -482,54 +487,62 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
     const float gt = cf[0][tl];
     const float rowT_L = -cf[1][tl] * cf[2][tl] * __expf(gt - gr);
     const float rowT_P = cf[3][tl] * __expf(gt - gr);
+    auto put_p = [&](int y, const float (&pv)[4]) {
+      const u32x2 pk = pack4(pv[0], pv[1], pv[2], pv[3]);
+      bf16x8& slot = a ? pfr1[y >> 1] : pfr0[(y >> 1) & 1];
+      u32x4 cur = __builtin_bit_cast(u32x4, slot);
+      if (y & 1) { cur.z = pk.x; cur.w = pk.y; } else { cur.x = pk.x; cur.y = pk.y; }
+      slot = __builtin_bit_cast(bf16x8, cur);
+    };
+    float* Ac = Am + a * 64 * kFS;
+    // one uniform branch per tile: the diagonal tile (exact per-element decay, masked) or a tile below it
 #pragma unroll
     for (int y = 0; y < NY; ++y) {
       if (y > X) break;
-      const bool diag = y == X;
-      // normal-tile column s = 16 y + li; transposed-tile columns s = 16 y + 4 lg + r
+      // normal-tile column s = 16 y + li; transposed-tile rows s = 16 y + 4 lg + r
       const int sn = 16 * y + li;
-      const float colN = cf[2][sn] * __expf(gr - cf[0][sn]);
-      f32x4 colT;
+      f32x4 accP, accL;
+      if constexpr (a) { accP = pB[y]; accL = lB[y]; } else { accP = pA[y]; accL = lA[y]; }
       const f32x4 gsT = *reinterpret_cast<const f32x4*>(&cf[0][16 * y + 4 * lg]);
       const f32x4 rkT = *reinterpret_cast<const f32x4*>(&cf[2][16 * y + 4 * lg]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) colT[r] = rkT[r] * __expf(gr - gsT[r]);
-      // P (transposed): rows s of tile y, column t = tl
-      {
-        f32x4 acc;
-        if constexpr (a) acc = pB[y]; else acc = pA[y];
+      if (y == X) {
+        // P (transposed, s <= t) and L00 / L11 (normal, s < t)
         float pv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int s = 16 * y + 4 * lg + r;
-          pv[r] = diag ? (s <= tl ? cf[3][tl] * rkT[r] * __expf(gt - gsT[r]) * acc[r] : 0.f)
-                       : rowT_P * colT[r] * acc[r];
+          const int sp = 16 * y + 4 * lg + r;
+          pv[r] = sp <= tl ? cf[3][tl] * rkT[r] * __expf(gt - gsT[r]) * accP[r] : 0.f;
         }
-        const u32x2 pk = pack4(pv[0], pv[1], pv[2], pv[3]);
-        bf16x8& slot = a ? pfr1[y >> 1] : pfr0[(y >> 1) & 1];
-        u32x4 cur = __builtin_bit_cast(u32x4, slot);
-        if (y & 1) { cur.z = pk.x; cur.w = pk.y; } else { cur.x = pk.x; cur.y = pk.y; }
-        slot = __builtin_bit_cast(bf16x8, cur);
-      }
-      if (a == 1 && y < 4) {
-        // L10 (transposed): rows s of tile y (chunk 0), column t = tl (chunk 1); below the diagonal, no mask
-        const f32x4 acc = lB[y];
-        float lv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) lv[r] = rowT_L * colT[r] * acc[r];
-        *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(&L10f[(X1 - 4) * 2 + (y >> 1)][lane]) + 8 * (y & 1)) =
-            pack4(lv[0], lv[1], lv[2], lv[3]);
-      } else {
-        // L00 (X0, y) or L11 (X1, y >= 4), normal orientation: rows t = 16 X + 4 lg + r, column s = sn
-        f32x4 acc;
-        if constexpr (a) acc = lB[y]; else acc = lA[y];
-        float* Ac = Am + a * 64 * kFS;
+        put_p(y, pv);
+        const float rks = cf[2][sn], gs = cf[0][sn];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 16 * X + 4 * lg + r;
-          const float val = diag ? (sn < t ? ltr[r] * cf[2][sn] * __expf(gtr[r] - cf[0][sn]) * acc[r] : 0.f)
-                                 : rowL[r] * colN * acc[r];
-          Ac[(t - 64 * a) * kFS + (sn - 64 * a)] = val;
+          Ac[(t - 64 * a) * kFS + (sn - 64 * a)] = sn < t ? ltr[r] * rks * __expf(gtr[r] - gs) * accL[r] : 0.f;
+        }
+      } else {
+        f32x4 colT;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) colT[r] = rkT[r] * __expf(gr - gsT[r]);
+        float pv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pv[r] = rowT_P * colT[r] * accP[r];
+        put_p(y, pv);
+        if (a == 1 && y < 4) {
+          // L10 (transposed): rows s of tile y (chunk 0), column t = tl (chunk 1)
+          float lv[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) lv[r] = rowT_L * colT[r] * accL[r];
+          *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(&L10f[(X1 - 4) * 2 + (y >> 1)][lane]) + 8 * (y & 1)) =
+              pack4(lv[0], lv[1], lv[2], lv[3]);
+        } else {
+          // L00 (X0, y) or L11 (X1, y >= 4), normal orientation: rows t = 16 X + 4 lg + r, column s = sn
+          const float colN = cf[2][sn] * __expf(gr - cf[0][sn]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 16 * X + 4 * lg + r;
+            Ac[(t - 64 * a) * kFS + (sn - 64 * a)] = rowL[r] * colN * accL[r];
+          }
         }
       }
     }
@@ -787,15 +800,6 @@ __global__ __launch_bounds__(256, 2) void gdn_pair_prep4_kernel(const __bf16* __
   }
 }
 
-// L2 warm-up: one global_load_lds_dword of one dword per 128-byte line into a dummy LDS area (no registers held);
-// the instruction is issued from inline asm so that the compiler does not order later LDS accesses behind it.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-__device__ __forceinline__ void touch_line(const char* p, uint32_t lds_dummy) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_dummy), "v"(p) : "memory", "m0");
-}
-
 // Blocks are dispatched round-robin over the 8 XCDs (block i runs on XCD i % 8). The 16 blocks of one (row, head)
 // read the same records, so they are mapped onto one XCD to share its L2: block L serves XCD x = L % 8, and the j-th
 // block of that XCD (j = L / 8) is block j % 16 of unit 8 (j / 16) + x. When the number of (row, head) units is not
@@ -824,18 +828,16 @@ struct OutOps {
   u32x2 rv;
 };
 
-constexpr int kScanThreads = 13 * 64;
+constexpr int kScanThreads = 12 * 64;
 
 // Waves 0-7: state row tile w (rows 16 w .. 16 w + 15 of the block's 128 x 16 slice), S <- e^G S + Bm + M S.
-// Waves 8-11: output row tile 4 half + (w - 8) of the pair, O = Q' S + R. Wave 12: L2 warm-up.
+// Waves 8-11: output row tile 4 half + (w - 8) of the pair, O = Q' S + R.
 // Each state wave publishes its tile as bf16 once per pair (LDS, double-buffered by pair parity); after the pair's
 // barrier every wave reads the whole bf16 slice as its B operands. A wave holds the operands of three pairs ahead.
 __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const char* __restrict__ ws, const float* s_in,
                                                                         float* s_out, __bf16* __restrict__ o, int T,
                                                                         int NP, int H, int B) {
   __shared__ u32x2 slot[2][8][64];
-  __shared__ u32x2 ostage[2][4][64];  // the output waves' tiles of a pair, stored to memory by wave 12 a pair later
-  __shared__ int dummy[64];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int idx, unit;
@@ -852,29 +854,6 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
   const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
       o + (size_t)b * T * H * kD, 0, (int)((size_t)T * H * kD * sizeof(__bf16)), 0x00020000);
   auto out_off = [&](int pp, int ot) { return ((kP * pp + 16 * ot + li) * H + h) * kD * 2 + (16 * sl + 4 * lg) * 2; };
-
-  if (w == 12) {
-    // ---------------- L2 warm-up wave: 64 of the 1024 record lines per pair, kTouchAhead pairs ahead ------------
-    // It also stores the output tiles of pair pp - 1 once every wave has met at pair pp's barrier, so that the
-    // output waves' memory counters carry their loads only (a store ahead of a load in a wave's counter holds up
-    // the wait for that load).
-    const uint32_t d = lds_addr(dummy);
-    const size_t line = (size_t)(64 * idx + lane) * 128;
-    for (int pt = kScanAhead; pt < kTouchAhead && pt < NP; ++pt) touch_line(rec0 + (size_t)pt * kRecBytes + line, d);
-    for (int pp = 0; pp < NP; ++pp) {
-      const int pt = pp + kTouchAhead;
-      if (pt < NP) touch_line(rec0 + (size_t)pt * kRecBytes + line, d);
-      lds_barrier();
-      if (pp > 0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          __builtin_amdgcn_raw_buffer_store_b64(ostage[(pp - 1) & 1][j][lane], orc, out_off(pp - 1, 4 * half + j), 0,
-                                                0);
-      }
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    return;
-  }
 
   static_assert(kScanAhead == 3, "the pair loops below are unrolled by three");
   auto gather = [&](int pp, bf16x8 (&sb)[4]) {
@@ -943,8 +922,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
     op.rv = *reinterpret_cast<const u32x2*>(rec + kRecR + ((size_t)(ot * 8 + sl) * 64 + lane) * 8);
   };
   // O^T = S^T Q'^T + R^T: the state fragments as the A operand and Q' as B, so that lane (li, lg) holds value
-  // columns 16 sl + 4 lg .. + 3 of position 16 ot + li (8 bytes). The tile goes to LDS for wave 12 to store, except
-  // the last pair's, which is stored here (no barrier follows it).
+  // columns 16 sl + 4 lg .. + 3 of position 16 ot + li (8 bytes).
   auto step = [&](int pp, const OutOps& op) {
     lds_barrier();
     bf16x8 sb[4];
@@ -952,11 +930,7 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
     f32x4 acc = unpack4(op.rv);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc = mfma16(sb[ks], op.qf[ks], acc);
-    const u32x2 pk = pack4(acc[0], acc[1], acc[2], acc[3]);
-    if (pp + 1 < NP)
-      ostage[pp & 1][w - 8][lane] = pk;
-    else
-      __builtin_amdgcn_raw_buffer_store_b64(pk, orc, out_off(pp, ot), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(pack4(acc[0], acc[1], acc[2], acc[3]), orc, out_off(pp, ot), 0, 0);
   };
   OutOps o0, o1, o2;
   load(0, o0);
