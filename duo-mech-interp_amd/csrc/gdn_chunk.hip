@@ -830,6 +830,30 @@ struct OutOps {
 
 constexpr int kScanThreads = 12 * 64;
 
+// The pair loop of a scan wave with its operands kScanAhead pairs ahead: slot i of `ops` serves the pairs i mod
+// kScanAhead. Whole groups of kScanAhead pairs run without conditions and in program order (the scheduling barriers
+// keep each pair's loads behind its step, so that the wait counts allow the full prefetch distance), then the rest.
+template <typename Ops, typename Load, typename Step>
+__device__ __forceinline__ void pipeline(int NP, Ops (&ops)[kScanAhead], Load load, Step step) {
+#pragma unroll
+  for (int i = 0; i < kScanAhead; ++i) {
+    load(i, ops[i]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int pp = 0;
+  for (; pp + kScanAhead <= NP; pp += kScanAhead) {
+#pragma unroll
+    for (int i = 0; i < kScanAhead; ++i) {
+      step(pp + i, ops[i]);
+      load(pp + i + kScanAhead, ops[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i + 1 < kScanAhead; ++i)
+    if (pp + i < NP) step(pp + i, ops[i]);
+}
+
 // Waves 0-7: state row tile w (rows 16 w .. 16 w + 15 of the block's 128 x 16 slice), S <- e^G S + Bm + M S.
 // Waves 8-11: output row tile 4 half + (w - 8) of the pair, O = Q' S + R.
 // Each state wave publishes its tile as bf16 once per pair (LDS, double-buffered by pair parity); after the pair's
@@ -855,7 +879,6 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
       o + (size_t)b * T * H * kD, 0, (int)((size_t)T * H * kD * sizeof(__bf16)), 0x00020000);
   auto out_off = [&](int pp, int ot) { return ((kP * pp + 16 * ot + li) * H + h) * kD * 2 + (16 * sl + 4 * lg) * 2; };
 
-  static_assert(kScanAhead == 3, "the pair loops below are unrolled by three");
   auto gather = [&](int pp, bf16x8 (&sb)[4]) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -892,18 +915,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
       for (int ks = 0; ks < 4; ++ks) s = mfma16(op.m[ks], sb[ks], s);
       S = s;
     };
-    StateOps o0, o1, o2;
-    load(0, o0);
-    load(1, o1);
-    load(2, o2);
-    for (int pp = 0; pp < NP; pp += 3) {
-      step(pp, o0);
-      load(pp + 3, o0);
-      if (pp + 1 < NP) step(pp + 1, o1);
-      load(pp + 4, o1);
-      if (pp + 2 < NP) step(pp + 2, o2);
-      load(pp + 5, o2);
-    }
+    StateOps ops[kScanAhead];
+    pipeline(NP, ops, load, step);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (s_out && half == 0) {
 #pragma unroll
@@ -932,18 +945,8 @@ __global__ __launch_bounds__(kScanThreads, 1) void gdn_pair_scan_kernel(const ch
     for (int ks = 0; ks < 4; ++ks) acc = mfma16(sb[ks], op.qf[ks], acc);
     __builtin_amdgcn_raw_buffer_store_b64(pack4(acc[0], acc[1], acc[2], acc[3]), orc, out_off(pp, ot), 0, 0);
   };
-  OutOps o0, o1, o2;
-  load(0, o0);
-  load(1, o1);
-  load(2, o2);
-  for (int pp = 0; pp < NP; pp += 3) {
-    step(pp, o0);
-    load(pp + 3, o0);
-    if (pp + 1 < NP) step(pp + 1, o1);
-    load(pp + 4, o1);
-    if (pp + 2 < NP) step(pp + 2, o2);
-    load(pp + 5, o2);
-  }
+  OutOps ops[kScanAhead];
+  pipeline(NP, ops, load, step);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
