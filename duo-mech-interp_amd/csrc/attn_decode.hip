@@ -286,6 +286,9 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __r
   const size_t sstride = (size_t)G * (kDecD + 2);
   const float* pb = part + ((size_t)b * Hkv + kvh) * S * sstride + (size_t)hh * (kDecD + 2);
   __shared__ float gm[8], gl[8], go[8][32];
+  // the gate value this thread's output needs is loaded first, so that its round trip overlaps the partials'
+  const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + d;
+  const float gv = tid < 32 ? (float)gate[oi] : 0.f;
   float M = -INFINITY, Lsum = 0.f, O = 0.f;
   for (int s0 = grp; s0 < S; s0 += 64) {
     float m[8], l[8], a[8];
@@ -325,18 +328,18 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __r
         Ot += go[g][tid] * w;
       }
     }
-    const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + d;
     const float res = Lt > 0.f ? Ot / Lt : 0.f;
-    out[oi] = from_f32<Tout>(res * sigmoidf_((float)gate[oi]));
+    out[oi] = from_f32<Tout>(res * sigmoidf_(gv));
   }
 }
 
 // Split of the context: a block's span is 64 NT keys (NT 16-key tiles per wave), NT a power of two <= 16. By
 // default the spans are sized so that about 256 blocks (one per CU) cover B x Hkv contexts, with at least one tile
-// per wave. Measured over an 8192-key context: at B 3 (6 contexts), 32 splits of 256 keys take 18.1 us against
-// 19.5 us for 64 splits of 128 keys (fewer partials to merge, two tiles in flight per wave); at B 32 (64 contexts)
-// 8, 16, 32 or 64 splits are within 5 % of each other.
-constexpr int kMaxNT = 16;
+// per wave. Measured over an 8192-key context at B 3 (6 contexts), op time against the span: 1024 keys (8 splits)
+// 33.8 us, 512 keys 22.6, 256 keys (32 splits, 192 blocks) 17.8, 128 keys 19.3; spans of 3 and 6 tiles per wave,
+// built for the comparison, took 21.7 us (192 keys: 258 blocks, a few CUs take two) and 20.2 us (384 keys). At B 32
+// (64 contexts) 4, 8 and 16 splits are within 3 % of each other.
+constexpr int kNTs[] = {1, 2, 4, 8, 16};
 static int decode_splits(int64_t B, int64_t Hkv, int64_t max_len, int64_t splits, int* nt_out) {
   int64_t S = splits;
   if (S <= 0) {
@@ -345,8 +348,12 @@ static int decode_splits(int64_t B, int64_t Hkv, int64_t max_len, int64_t splits
   }
   if (S < 1) S = 1;
   const int64_t L0 = (max_len + S - 1) / S;
-  int nt = 1;
-  while (nt < kMaxNT && (int64_t)64 * nt < L0) nt <<= 1;
+  int nt = 16;
+  for (int c : kNTs)
+    if ((int64_t)64 * c >= L0) {
+      nt = c;
+      break;
+    }
   *nt_out = nt;
   return (int)((max_len + 64 * nt - 1) / (64 * nt));
 }

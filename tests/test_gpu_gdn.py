@@ -63,8 +63,8 @@ def test_recurrent_long_prefill_fp32():
 @pytest.mark.parametrize("B,H,Hk", [(16, 16, 16), (32, 8, 4)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_decode_step_many_states(B, H, Hk, dtype):
-    """One token over B x H states (at least 1024 units of 32 value columns: the two-units-per-block decode kernel),
-    in place, from a non-zero state; the second shape has 8 value heads over 4 q/k heads."""
+    """One token over B x H states (1024 blocks of 32 value columns), in place, from a non-zero state; the second
+    shape has 8 value heads over 4 q/k heads."""
     dev = device()
     inp = workloads.gdn_inputs(B=B, T=1, H=H, Hk=Hk, D=128, seed=7, dtype=dtype, normalize=False)
     s0 = 0.1 * torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(8))
