@@ -36,6 +36,7 @@ GDN_PREFILL_FLOPS = 1.190e10
 # dispatch, each scaled by what the counter reads for a 256 MiB device copy, on the kernels of commit 7b4258e
 # (profiles/counters_gdn_attn_gemm_kernels.md: prep 72.0 + 67.1 MB, scan 67.3 + 17.8 MB)
 GDN_PREFILL_TRAFFIC_BYTES = 224_200_000
+GDN_PREFILL_TRAFFIC_COMMIT = "7b4258e"  # the kernels the traffic was counted on
 GDN_DECODE_STEP_BYTES = 2_130_048   # S read + write fp32 + q,k,v,o,g,beta (B 1, H 16, d 128)
 ATTN_PREFILL_FLOPS = 6.874e10       # 4 * D * Hq * T (T + 1) / 2, T 4096, Hq 8, D 256
 ATTN_PREFILL_BYTES = 58_720_256
@@ -552,7 +553,8 @@ def main():
         "config": {"workload": "gdn_chunked_prefill", "batch": 1, "seq_len": 4096, "heads": 16, "d_k": 128,
                    "d_v": 128, "chunk": 64, "state": "fp32", "activations": "bf16", "parallelism": "none (1 GPU)"},
         "roofline": ({"bound": "hbm", "achieved": round(gp["achieved_gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                      "frac": round(gp["frac"], 4), "traffic": GDN_PREFILL_TRAFFIC_BYTES} if gp else None),
+                      "frac": round(gp["frac"], 4), "traffic": GDN_PREFILL_TRAFFIC_BYTES,
+                      "traffic_profiled_at": GDN_PREFILL_TRAFFIC_COMMIT} if gp else None),
         "cpu_baseline": cpu,
         "breakdown": res,
     }
