@@ -112,6 +112,111 @@ def test_chunk_prefill_ragged_lengths(T):
     assert oracle.rel_err(S.cpu(), s_ref) <= TOL_BF16
 
 
+def _gate_regime(inp, regime, seed):
+    """Rescale the generator's gates (g = -softplus(randn), about -0.8 per token: a 128-token pair decays by
+    e^-100, so the state carried into a pair barely reaches its outputs) so that the carry matters: `zero` (no
+    decay, the state accumulates over every pair), `slow` (x 0.03: about e^-3 per pair), `extreme` (slow, plus 2 %
+    of the tokens at g = -1.2, a decay of e^-1.2 in one token), `strong` (x 10: e^gamma underflows to 0 inside a
+    chunk; nothing may overflow)."""
+    g = inp["g"]
+    if regime == "zero":
+        g = torch.zeros_like(g)
+    elif regime == "slow":
+        g = 0.03 * g
+    elif regime == "extreme":
+        hit = torch.rand(g.shape, generator=torch.Generator().manual_seed(seed)) < 0.02
+        g = torch.where(hit, torch.full_like(g, -1.2), 0.02 * g)
+    elif regime == "strong":
+        g = 10.0 * g
+    return dict(inp, g=g)
+
+
+@pytest.mark.parametrize("regime", ["zero", "slow", "extreme", "strong"])
+def test_chunk_prefill_gate_regimes_carry_across_pairs(regime):
+    """bf16 chunked prefill over 8 pairs of 128 tokens with gates that let the state carry across the pair
+    boundaries (the scan's e^G S + M S + Bm step and the output's Q' S term at full weight), and with gates strong
+    enough to underflow the decay factors. Measured 2.4e-3 to 4.5e-3 on o and S."""
+    dev = device()
+    inp = _gate_regime(workloads.gdn_inputs(B=1, T=1024, H=4, D=128, seed=31, dtype=torch.bfloat16), regime, 31)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    announce(f"gdn chunk T1024 H4 bf16 gates {regime}")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], output_final_state=True,
+                                         use_qk_l2norm_in_kernel=True)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(S).all()
+    eo, es = oracle.rel_err(o.float().cpu(), o_ref), oracle.rel_err(S.cpu(), s_ref)
+    print(f"gates {regime}: rel err o {eo:.3e} S {es:.3e}")
+    assert eo <= TOL_BF16 and es <= TOL_BF16
+
+
+def test_chunk_prefill_no_decay_full_length():
+    """No decay at all over T = 4096 (32 pairs): the final state is the whole sequence's delta-rule sum, so an error
+    in the pair-to-pair chain accumulates into it. Measured 4.7e-3 (o), 3.9e-3 (S)."""
+    dev = device()
+    inp = _gate_regime(workloads.gdn_inputs(B=1, T=4096, H=4, D=128, seed=32, dtype=torch.bfloat16), "zero", 32)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    announce("gdn chunk T4096 H4 bf16 no decay")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], output_final_state=True,
+                                         use_qk_l2norm_in_kernel=True)
+    eo, es = oracle.rel_err(o.float().cpu(), o_ref), oracle.rel_err(S.cpu(), s_ref)
+    print(f"no decay T4096: rel err o {eo:.3e} S {es:.3e}")
+    assert eo <= TOL_BF16 and es <= TOL_BF16
+
+
+@pytest.mark.parametrize("regime", ["zero", "slow"])
+def test_chunk_prefill_fp32_gate_regimes(regime):
+    """The fp32 chunk path (the stack's) with the state carried across all 16 chunks of T = 1024: fp32 tolerance.
+    Measured 3.5e-7 to 4.9e-7."""
+    dev = device()
+    inp = _gate_regime(workloads.gdn_inputs(B=1, T=1024, H=4, D=128, seed=36, dtype=torch.float32), regime, 36)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    announce(f"gdn chunk T1024 H4 fp32 gates {regime}")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], output_final_state=True,
+                                         use_qk_l2norm_in_kernel=True)
+    eo, es = oracle.rel_err(o.cpu(), o_ref), oracle.rel_err(S.cpu(), s_ref)
+    print(f"fp32 gates {regime}: rel err o {eo:.3e} S {es:.3e}")
+    assert eo <= TOL_F32 and es <= TOL_F32
+
+
+@pytest.mark.parametrize("B,T,H,Hk", [(3, 700, 5, 5), (2, 640, 8, 2)])
+def test_chunk_prefill_slow_gates_initial_state_odd_shapes(B, T, H, Hk):
+    """Slow gates with a non-zero initial state: B 3 x 5 heads (15 (row, head) units, not a multiple of 8: the scan's
+    plain block order) over a ragged 6-pair sequence, and GQA (8 value heads over 2 q/k heads)."""
+    dev = device()
+    inp = _gate_regime(workloads.gdn_inputs(B=B, T=T, H=H, Hk=Hk, D=128, seed=33 + B, dtype=torch.bfloat16),
+                       "slow", 33)
+    s0 = 0.1 * torch.randn(B, H, 128, 128, generator=torch.Generator().manual_seed(34 + B))
+    o_ref, s_ref = _oracle_rec(inp, s0)
+    d = workloads.to_device(inp, dev)
+    announce(f"gdn chunk B{B} T{T} H{H}/{Hk} bf16 slow gates, initial state")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], initial_state=s0.to(dev),
+                                         output_final_state=True, use_qk_l2norm_in_kernel=True)
+    eo, es = oracle.rel_err(o.float().cpu(), o_ref), oracle.rel_err(S.cpu(), s_ref)
+    print(f"B{B} T{T} H{H}/{Hk}: rel err o {eo:.3e} S {es:.3e}")
+    assert eo <= TOL_BF16 and es <= TOL_BF16
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_chunk_prefill_without_in_kernel_l2norm(dtype):
+    """use_qk_l2norm_in_kernel=False on unit-norm q and k (the caller normalised them): both chunk paths against the
+    recurrence without the in-kernel norm, slow gates."""
+    dev = device()
+    inp = _gate_regime(workloads.gdn_inputs(B=1, T=1024, H=4, D=128, seed=35, dtype=dtype), "slow", 35)
+    o_ref, s_ref = oracle.recurrent_gated_delta_rule(inp["q"], inp["k"], inp["v"], inp["g"], inp["beta"],
+                                                     output_final_state=True, use_qk_l2norm_in_kernel=False,
+                                                     dtype=torch.float32)
+    d = workloads.to_device(inp, dev)
+    announce(f"gdn chunk T1024 H4 {dtype} without the in-kernel l2 norm")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], output_final_state=True,
+                                         use_qk_l2norm_in_kernel=False)
+    eo, es = oracle.rel_err(o.float().cpu(), o_ref), oracle.rel_err(S.cpu(), s_ref)
+    print(f"no in-kernel l2 norm {dtype}: rel err o {eo:.3e} S {es:.3e}")
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    assert eo <= tol and es <= tol
+
+
 def test_chunk_prefill_initial_state_and_gqa():
     dev = device()
     inp = workloads.gdn_inputs(B=1, T=256, H=8, Hk=2, D=128, seed=7, dtype=torch.bfloat16, normalize=False)
