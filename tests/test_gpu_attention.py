@@ -54,6 +54,64 @@ def test_prefill_full_size():
         assert torch.equal(again, out)
 
 
+def _score_regime(q, k, regime, key_axis):
+    """Reshape the scores so that the softmax's running max moves: `rising` adds 16 u to every query and
+    60 (t / T) u to key t (u the unit vector on dims 192..255, outside the rotary dims), a score drift of 60 / sqrt(256)
+    x 16 = 60 nats over the keys, so later tiles keep beating the running max by more than the prefill kernel's
+    2^8 rescale threshold; `sharp` multiplies the queries by 8 (scores with a standard deviation of about 8: near
+    one-hot rows whose maxima jump between tiles)."""
+    if regime == "sharp":
+        return (q.float() * 8).to(torch.bfloat16), k
+    D = q.shape[-1]
+    u = torch.zeros(D)
+    u[192:] = 64 ** -0.5
+    n = k.shape[key_axis]
+    shape = [1] * k.dim()
+    shape[key_axis] = n
+    ramp = (torch.arange(n, dtype=torch.float32) / n).view(shape)
+    return (q.float() + 16 * u).to(torch.bfloat16), (k.float() + 60 * ramp * u).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("regime,T", [("rising", 1000), ("sharp", 1000), ("rising", 4096)])
+def test_prefill_running_max_moves(regime, T):
+    """Prefill with scores whose running max moves tile after tile (the rescale of O and l outside the kernel's inner
+    loop, and split halves whose maxima differ by tens of nats in the merge), against the fp32 oracle."""
+    dev = device()
+    inp = workloads.attn_prefill_inputs(B=1, T=T, seed=40 + T)
+    q, k = _score_regime(inp["q"], inp["k"], regime, key_axis=1)
+    inp = dict(inp, q=q, k=k)
+    cos, sin = _tables(T)
+    ref = oracle.gated_attention(inp["q"], inp["k"], inp["v"], inp["gate"], cos, sin)
+    d = workloads.to_device(inp, dev)
+    announce(f"attn prefill T{T} scores {regime}")
+    out = q35hip.gated_attention_prefill(d["q"], d["k"], d["v"], d["gate"], cos.to(dev), sin.to(dev))
+    e = oracle.rel_err(out.float().cpu(), ref)
+    print(f"attn prefill T{T} {regime}: rel err {e:.3e}")
+    assert torch.isfinite(out.float()).all()
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("regime", ["rising", "sharp"])
+def test_decode_running_max_moves(regime):
+    """Decode over 8192 cached keys with rising or sharp scores: the splits' partial maxima differ by tens of nats,
+    so the merge's weights 2^(m_s - m) span a wide range; rows of 8192, 5000 and 1 keys."""
+    dev = device()
+    inp = workloads.attn_decode_inputs(B=3, N=8192, seed=41, lens=[8192, 5000, 1])
+    q, kc = _score_regime(inp["q"], inp["k_cache"], regime, key_axis=2)
+    inp = dict(inp, q=q, k_cache=kc)
+    cos, sin = _tables(8192)
+    ref = oracle.gated_attention_decode(inp["q"], inp["k_cache"], inp["v_cache"], inp["gate"], inp["cache_len"],
+                                        cos, sin)
+    d = workloads.to_device(inp, dev)
+    announce(f"attn decode B3 N8192 scores {regime}")
+    out = q35hip.gated_attention_decode(d["q"], d["k_cache"], d["v_cache"], d["gate"], d["cache_len"],
+                                        cos.to(dev), sin.to(dev))
+    e = oracle.rel_err(out.float().cpu(), ref)
+    print(f"attn decode {regime}: rel err {e:.3e}")
+    assert torch.isfinite(out.float()).all()
+    assert e <= TOL
+
+
 @pytest.mark.parametrize("B", [3, 32])
 def test_decode_full_size(B):
     """Batch 3 and 32, context 8192, 8 q / 2 kv heads, head dim 256, bf16 KV cache, split-K."""
