@@ -60,6 +60,24 @@ def test_recurrent_long_prefill_fp32():
     assert oracle.rel_err(state.cpu(), s_ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("regime", ["zero", "slow", "strong"])
+def test_recurrent_gate_regimes_fp32(regime):
+    """The token-serial kernel over T = 1024 in one launch with no decay (the state sums every token's update),
+    slow decay, and decays that underflow e^g to 0: fp32 tolerance, finite outputs."""
+    dev = device()
+    inp = _gate_regime(workloads.gdn_inputs(B=1, T=1024, H=4, D=128, seed=37, dtype=torch.float32), regime, 37)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    announce(f"gdn recurrent T1024 H4 fp32 gates {regime}")
+    state = torch.zeros(1, 4, 128, 128, device=dev)
+    o = q35hip.gdn_decode_step_(d["q"], d["k"], d["v"], d["g"], d["beta"], state)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all() and torch.isfinite(state).all()
+    eo, es = oracle.rel_err(o.cpu(), o_ref), oracle.rel_err(state.cpu(), s_ref)
+    print(f"recurrent gates {regime}: rel err o {eo:.3e} S {es:.3e}")
+    assert eo <= TOL_F32 and es <= TOL_F32
+
+
 @pytest.mark.parametrize("B,H,Hk", [(16, 16, 16), (32, 8, 4)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_decode_step_many_states(B, H, Hk, dtype):
