@@ -20,7 +20,7 @@ Recorded (all fp32):
   logits_pushed            row and position, the hook's push form of tests/engine_ref.py:14-15): the activations of
                            every layer and the last-position logits
 
-Run from the repository root in the build container (it imports transformers; nothing here runs on the GPU box):
+Run from the repository root in the build container (it imports transformers; nothing here runs on a GPU):
     python tests/golden/make_layer_golden.py
 """
 import os
