@@ -50,27 +50,52 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp_mov<0x140>(v);
 }
 
-template <int G, int NT>
+// Query source of the partial kernel. FP false: bf16 q [B, Hq, D], the cache holding every key up to and including
+// the token's (cache_len[b] keys, the query at position cache_len[b] - 1). FP true: the token's fused projection
+// output, fp32 rows of y with [q | gate] per query head from column 0 (engine/kernels_qwen35.js:36-38), q
+// normalised here with (1 + w) (the WGSL attnPrep's q half, :40-47); cache_len[b] is then the token's position
+// pos, the cache holds keys 0 .. pos - 1, and the new key is folded in by the merge kernel.
+struct DecQ {
+  const void* q;
+  int64_t ldy;       // FP: row stride of y (floats)
+  const float* qnw;  // FP: q_norm weight [D]
+  float eps;
+};
+
+template <int G, int NT, bool FP>
 __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
-    const __bf16* __restrict__ q, const __bf16* __restrict__ kc, const __bf16* __restrict__ vc,
+    DecQ dq, const __bf16* __restrict__ kc, const __bf16* __restrict__ vc,
     const int32_t* __restrict__ cache_len, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int rot,
     float* __restrict__ part, int Hq, int Hkv, int max_len, int S, float scale) {
   static_assert(G == 1 || G == 2 || G == 4 || G == 8, "heads per kv head");
   constexpr int NG = (G + 3) / 4;  // lane groups of the MFMA D tile that hold real heads
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  Q35_ARGS_UPFRONT(q, kc, vc, cache_len, cos_t, sin_t, rot, part, Hq, Hkv, max_len, S, scale);
+  Q35_ARGS_UPFRONT(dq.q, dq.ldy, dq.qnw, dq.eps, kc, vc, cache_len, cos_t, sin_t, rot, part, Hq, Hkv, max_len, S, scale);
 
   // cache_len lives on the device: its read is issued here and waited for after the query loads below
   const int len_raw = cache_len[b];
   // 0. the raw query loads go out next: they do not depend on the cache length, whose read from device memory
   // is a round trip of its own. Thread t takes quads of 4 dims (qi = t, t + 256, ...), with the rotation partner
-  // of each rotary quad; every load is unconditional (clamped indices, results selected afterwards).
+  // of each rotary quad; every load is unconditional (clamped indices, results selected afterwards). A wave's 64
+  // quads are one head's 256 dims (G * 64 quads over 256 threads), so its RMS is one wave sum.
   const int half = rot >> 1;
   constexpr int NQ = (G * 64 + 255) / 256;
   u32x2 xq[NQ], pq[NQ];
-  {
-    const __bf16* qb = q + ((size_t)b * Hq + (size_t)kvh * G) * kDecD;
+  f32x4 xf[NQ], pf[NQ], wx[NQ], wp[NQ];
+  if constexpr (FP) {
+    const float* yb = static_cast<const float*>(dq.q) + (size_t)b * dq.ldy + (size_t)kvh * G * 2 * kDecD;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int qi = min(tid + 256 * u, G * 64 - 1), hh = qi >> 6, d0 = 4 * (qi & 63);
+      const int pd0 = d0 < rot ? (d0 < half ? d0 + half : d0 - half) : d0;
+      xf[u] = *reinterpret_cast<const f32x4*>(yb + hh * 2 * kDecD + d0);
+      pf[u] = *reinterpret_cast<const f32x4*>(yb + hh * 2 * kDecD + pd0);
+      wx[u] = *reinterpret_cast<const f32x4*>(dq.qnw + d0);
+      wp[u] = *reinterpret_cast<const f32x4*>(dq.qnw + pd0);
+    }
+  } else {
+    const __bf16* qb = static_cast<const __bf16*>(dq.q) + ((size_t)b * Hq + (size_t)kvh * G) * kDecD;
 #pragma unroll
     for (int u = 0; u < NQ; ++u) {
       const int qi = min(tid + 256 * u, G * 64 - 1), hh = qi >> 6, d0 = 4 * (qi & 63);
@@ -81,12 +106,12 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // the cache length is clamped rather than trusted: 0 <= len <= max_len
+  // the cache length (FP: the position) is clamped rather than trusted: 0 <= len <= max_len
   const int len = min(max(len_raw, 0), max_len);
   constexpr int L = 4 * kDecTile * NT;  // keys of the block's span: NT tiles per wave
   const int k_begin = s * L;
   const int k_end = min(k_begin + L, len);
-  const int pos = max(len - 1, 0);
+  const int pos = FP ? min(len, max_len - 1) : max(len - 1, 0);  // the query's position
 
   __shared__ __attribute__((aligned(16))) float qf[G][kDecD];
   __shared__ float pl[4][kDecTile][G];
@@ -190,8 +215,21 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
 #pragma unroll
   for (int u = 0; u < NQ; ++u) {
     const int qi = tid + 256 * u, hh = qi >> 6, d0 = 4 * (qi & 63);
+    f32x4 x, y;
+    if constexpr (FP) {
+      // q RMSNorm with (1 + w) (engine/kernels_qwen35.js:40-47); every lane takes part in the wave sum
+      const float ss = wave_sum(xf[u][0] * xf[u][0] + xf[u][1] * xf[u][1] + xf[u][2] * xf[u][2] + xf[u][3] * xf[u][3]);
+      const float rr = rsqrtf(ss * (1.f / kDecD) + dq.eps);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = xf[u][e] * rr * (1.f + wx[u][e]);
+        y[e] = pf[u][e] * rr * (1.f + wp[u][e]);
+      }
+    } else {
+      x = unpack_bf16x4(xq[u]);
+      y = unpack_bf16x4(pq[u]);
+    }
     if (qi < G * 64) {
-      const f32x4 x = unpack_bf16x4(xq[u]), y = unpack_bf16x4(pq[u]);
       f32x4 r;
       if (d0 < rot) {
         const float sg = d0 < half ? -1.f : 1.f;
@@ -275,20 +313,109 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
 // Merge over splits, gate, store. One block per (query head, row, slice of 32 head dims): thread (g, d) folds the
 // splits g, g + 8, ... of dim d with an online log-sum-exp, loading eight splits' (max, sum, acc) at a time before
 // using any of them; the eight groups are combined in LDS.
-template <typename Tout>
+// The new token of the FP form (the WGSL attnPrep's k / v half, engine/kernels_qwen35.js:40-65, for one token per
+// row): its key and value come from y (k of kv head j at column Hq 2 D + j D, v at Hq 2 D + (Hkv + j) D), k
+// normalised with (1 + w) and rotated at the token's position pos[b]. The merge folds them in as one more split of
+// one key, and one block per (row, kv head) writes them into the caches at pos[b] (when pos[b] < max_len): the
+// partial kernel of the same call reads only keys below pos[b], and the next call finds them in the cache.
+struct DecNew {
+  const float* y;
+  int64_t ldy;
+  const float* qnw;
+  const float* knw;
+  float eps;
+  const int32_t* pos;
+  const float* cos_t;
+  const float* sin_t;
+  int rot;
+  int max_len;
+  __bf16* kc;
+  __bf16* vc;
+  float scale;
+};
+
+// Normalise (RMS with (1 + w)) and rotate one 256-dim head held as a float4 per lane of a wave, exactly as the
+// attention front end does it (frontend.hip attn_prep_kernel), so that a key written here equals the one the front
+// end would have written.
+__device__ __forceinline__ f32x4 norm_rotate(const float* src, const float* nw, float eps, const float* cos_t,
+                                             const float* sin_t, int rot, int p, int lane) {
+  const int d0 = 4 * lane, half = rot >> 1;
+  const int pd0 = d0 < rot ? (d0 < half ? d0 + half : d0 - half) : d0;
+  const f32x4 x = *reinterpret_cast<const f32x4*>(src + d0);
+  const f32x4 px = *reinterpret_cast<const f32x4*>(src + pd0);
+  const f32x4 wv = *reinterpret_cast<const f32x4*>(nw + d0);
+  const f32x4 pw = *reinterpret_cast<const f32x4*>(nw + pd0);
+  const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
+  const float r = rsqrtf(ss * (1.f / kDecD) + eps);
+  f32x4 xn, pn;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    xn[e] = x[e] * r * (1.f + wv[e]);
+    pn[e] = px[e] * r * (1.f + pw[e]);
+  }
+  if (d0 >= rot) return xn;
+  const int j0 = d0 < half ? d0 : d0 - half;
+  const f32x4 cv = *reinterpret_cast<const f32x4*>(cos_t + (size_t)p * half + j0);
+  const f32x4 sv = *reinterpret_cast<const f32x4*>(sin_t + (size_t)p * half + j0);
+  const float sg = d0 < half ? -1.f : 1.f;
+  f32x4 xr;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) xr[e] = xn[e] * cv[e] + sg * pn[e] * sv[e];
+  return xr;
+}
+
+template <typename Tout, bool FP>
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __restrict__ part,
                                                                 const __bf16* __restrict__ gate,
-                                                                Tout* __restrict__ out, int Hq, int Hkv, int S) {
+                                                                Tout* __restrict__ out, int Hq, int Hkv, int S,
+                                                                DecNew nk) {
   Q35_ARGS_UPFRONT(part, gate, out, Hq, Hkv, S);
+  if constexpr (FP)
+    Q35_ARGS_UPFRONT(nk.y, nk.ldy, nk.qnw, nk.knw, nk.eps, nk.pos, nk.cos_t, nk.sin_t, nk.rot, nk.max_len, nk.kc,
+                     nk.vc, nk.scale);
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int G = Hq / Hkv, kvh = h / G, hh = h % G;
   const int grp = tid >> 5, d = 32 * blockIdx.z + (tid & 31);
   const size_t sstride = (size_t)G * (kDecD + 2);
   const float* pb = part + ((size_t)b * Hkv + kvh) * S * sstride + (size_t)hh * (kDecD + 2);
   __shared__ float gm[8], gl[8], go[8][32];
+  __shared__ __attribute__((aligned(16))) float qs[FP ? kDecD : 1], ks[FP ? kDecD : 1];
   // the gate value this thread's output needs is loaded first, so that its round trip overlaps the partials'
   const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + d;
-  const float gv = tid < 32 ? (float)gate[oi] : 0.f;
+  float gv = 0.f, vnew = 0.f;
+  if constexpr (FP) {
+    const float* yr = nk.y + (size_t)b * nk.ldy;
+    if (tid < 32) {
+      gv = yr[(size_t)h * 2 * kDecD + kDecD + d];
+      vnew = (float)(__bf16)yr[(size_t)Hq * 2 * kDecD + (size_t)(Hkv + kvh) * kDecD + d];
+    }
+    // the new key's score: wave 0 forms the query (as the partial kernel does), wave 1 the key, both rounded to
+    // bf16 as the partial kernel's MFMA operands and the cache hold them; wave 2 of the writing block the value
+    const int wv = tid >> 6, lane = tid & 63;
+    const int p = min(max(nk.pos[b], 0), nk.max_len);
+    const int pq = min(p, nk.max_len - 1);
+    const bool writer = hh == 0 && blockIdx.z == 0 && p < nk.max_len;
+    if (wv == 0) {
+      const f32x4 qr = norm_rotate(yr + (size_t)h * 2 * kDecD, nk.qnw, nk.eps, nk.cos_t, nk.sin_t, nk.rot, pq, lane);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qs[4 * lane + e] = (float)(__bf16)qr[e];
+    } else if (wv == 1) {
+      const f32x4 kr = norm_rotate(yr + (size_t)Hq * 2 * kDecD + (size_t)kvh * kDecD, nk.knw, nk.eps, nk.cos_t,
+                                   nk.sin_t, nk.rot, pq, lane);
+      bf16x4 kb = {(__bf16)kr[0], (__bf16)kr[1], (__bf16)kr[2], (__bf16)kr[3]};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ks[4 * lane + e] = (float)kb[e];
+      if (writer)
+        *reinterpret_cast<bf16x4*>(nk.kc + (((size_t)b * Hkv + kvh) * nk.max_len + p) * kDecD + 4 * lane) = kb;
+    } else if (wv == 2 && writer) {
+      const f32x4 x =
+          *reinterpret_cast<const f32x4*>(yr + (size_t)Hq * 2 * kDecD + (size_t)(Hkv + kvh) * kDecD + 4 * lane);
+      const bf16x4 vb = {(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
+      *reinterpret_cast<bf16x4*>(nk.vc + (((size_t)b * Hkv + kvh) * nk.max_len + p) * kDecD + 4 * lane) = vb;
+    }
+  } else {
+    gv = tid < 32 ? (float)gate[oi] : 0.f;
+  }
   float M = -INFINITY, Lsum = 0.f, O = 0.f;
   for (int s0 = grp; s0 < S; s0 += 64) {
     float m[8], l[8], a[8];
@@ -319,6 +446,17 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __r
     float Mx = -INFINITY;
 #pragma unroll
     for (int g = 0; g < 8; ++g) Mx = fmaxf(Mx, gm[g]);
+    float snew = 0.f;
+    if constexpr (FP) {
+      // q . k of the new token over 256 dims: 8 per lane, then across the 32 lanes
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc += qs[8 * tid + i] * ks[8 * tid + i];
+#pragma unroll
+      for (int off = 16; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+      snew = acc * nk.scale;
+      Mx = fmaxf(Mx, snew);
+    }
     float Lt = 0.f, Ot = 0.f;
     if (Mx != -INFINITY) {
 #pragma unroll
@@ -327,6 +465,11 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __r
         Lt += gl[g] * w;
         Ot += go[g][tid] * w;
       }
+    }
+    if constexpr (FP) {
+      const float e = __expf(snew - Mx);
+      Lt += e;
+      Ot += e * vnew;
     }
     const float res = Lt > 0.f ? Ot / Lt : 0.f;
     out[oi] = from_f32<Tout>(res * sigmoidf_(gv));
@@ -390,28 +533,23 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
 }
 }  // namespace q35
 
-extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* gate,
-                                     const int32_t* cache_len, const float* cos, const float* sin, void* out,
-                                     int out_dtype,
-                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
-                                     float scale, int64_t splits, void* workspace, size_t workspace_bytes,
-                                     q35_stream_t stream) {
-  using namespace q35;
-  const int chk = decode_check(q, k_cache, v_cache, gate, cache_len, cos, sin, out, out_dtype, B, Hq, Hkv, D,
-                               max_len, rot, splits);
-  if (chk != Q35_OK) return chk;
+namespace q35 {
+// The two launches of a decode call (partial over the splits, then the merge); FP: the query, the new key and value
+// and the gate from the fused projection output (DecQ / DecNew), cache_len then holding the token's position.
+template <bool FP>
+static int decode_launch(const DecQ& dq, const DecNew& nk, const void* k_cache, const void* v_cache,
+                         const void* gate, const int32_t* cache_len, const float* cos, const float* sin, void* out,
+                         int out_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t rot,
+                         float scale, int64_t splits, void* workspace, hipStream_t st) {
   const int64_t G = Hq / Hkv;
   int nt;
   const int S = decode_splits(B, Hkv, max_len, splits, &nt);
-  const size_t need = q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits);
-  if (!workspace || workspace_bytes < need) return Q35_EWORKSPACE;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   float* part = (float*)workspace;
   dim3 grid(S, (unsigned)Hkv, (unsigned)B), block(256);
 #define Q35_DEC_LAUNCH(GG, NT)                                                                                   \
-  hipLaunchKernelGGL((attn_decode_partial_kernel<GG, NT>), grid, block, 0, st, (const __bf16*)q,                \
-                     (const __bf16*)k_cache, (const __bf16*)v_cache, cache_len, cos, sin, (int)rot, part, (int)Hq, \
-                     (int)Hkv, (int)max_len, S, scale)
+  hipLaunchKernelGGL((attn_decode_partial_kernel<GG, NT, FP>), grid, block, 0, st, dq, (const __bf16*)k_cache,  \
+                     (const __bf16*)v_cache, cache_len, cos, sin, (int)rot, part, (int)Hq, (int)Hkv,             \
+                     (int)max_len, S, scale)
 #define Q35_DEC_NT(GG)                        \
   switch (nt) {                               \
     case 1: Q35_DEC_LAUNCH(GG, 1); break;     \
@@ -430,12 +568,56 @@ extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const v
 #undef Q35_DEC_LAUNCH
   const dim3 mgrid((unsigned)Hq, (unsigned)B, kDecD / 32);
   if (out_dtype == Q35_F32)
-    hipLaunchKernelGGL(attn_decode_merge_kernel<float>, mgrid, dim3(256), 0, st, part, (const __bf16*)gate,
-                       (float*)out, (int)Hq, (int)Hkv, S);
+    hipLaunchKernelGGL((attn_decode_merge_kernel<float, FP>), mgrid, dim3(256), 0, st, part, (const __bf16*)gate,
+                       (float*)out, (int)Hq, (int)Hkv, S, nk);
   else
-    hipLaunchKernelGGL(attn_decode_merge_kernel<__bf16>, mgrid, dim3(256), 0, st, part, (const __bf16*)gate,
-                       (__bf16*)out, (int)Hq, (int)Hkv, S);
+    hipLaunchKernelGGL((attn_decode_merge_kernel<__bf16, FP>), mgrid, dim3(256), 0, st, part, (const __bf16*)gate,
+                       (__bf16*)out, (int)Hq, (int)Hkv, S, nk);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+}  // namespace q35
+
+extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cache, const void* gate,
+                                     const int32_t* cache_len, const float* cos, const float* sin, void* out,
+                                     int out_dtype,
+                                     int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
+                                     float scale, int64_t splits, void* workspace, size_t workspace_bytes,
+                                     q35_stream_t stream) {
+  using namespace q35;
+  const int chk = decode_check(q, k_cache, v_cache, gate, cache_len, cos, sin, out, out_dtype, B, Hq, Hkv, D,
+                               max_len, rot, splits);
+  if (chk != Q35_OK) return chk;
+  const size_t need = q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits);
+  if (!workspace || workspace_bytes < need) return Q35_EWORKSPACE;
+  const DecQ dq{q, 0, nullptr, 0.f};
+  const DecNew nk{};
+  return decode_launch<false>(dq, nk, k_cache, v_cache, gate, cache_len, cos, sin, out, out_dtype, B, Hq, Hkv,
+                              max_len, rot, scale, splits, workspace, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int q35_gated_attn_decode_proj(const float* y, int64_t ldy, const float* q_norm_w, const float* k_norm_w,
+                                          float eps, void* k_cache, void* v_cache, const int32_t* pos,
+                                          const float* cos, const float* sin, void* out, int out_dtype, int64_t B,
+                                          int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
+                                          float scale, int64_t splits, void* workspace, size_t workspace_bytes,
+                                          q35_stream_t stream) {
+  using namespace q35;
+  if (!y || !q_norm_w || !k_norm_w) return Q35_EINVAL;
+  const int chk = decode_check(y, k_cache, v_cache, y, pos, cos, sin, out, out_dtype, B, Hq, Hkv, D, max_len, rot,
+                               splits);
+  if (chk != Q35_OK) return chk;
+  if (ldy < Hq * 2 * D + 2 * Hkv * D) return Q35_EINVAL;
+  // y, its rows and the norm weights are read as 16-byte vectors
+  if ((ldy & 3) || ((uintptr_t)y & 15) || ((uintptr_t)q_norm_w & 15) || ((uintptr_t)k_norm_w & 15))
+    return Q35_EUNSUPPORTED;
+  if (B * ldy > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
+  const size_t need = q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits);
+  if (!workspace || workspace_bytes < need) return Q35_EWORKSPACE;
+  const DecQ dq{y, ldy, q_norm_w, eps};
+  const DecNew nk{y, ldy, q_norm_w, k_norm_w, eps, pos, cos, sin, (int)rot, (int)max_len, (__bf16*)k_cache,
+                  (__bf16*)v_cache, scale};
+  return decode_launch<true>(dq, nk, k_cache, v_cache, nullptr, pos, cos, sin, out, out_dtype, B, Hq, Hkv, max_len,
+                             rot, scale, splits, workspace, reinterpret_cast<hipStream_t>(stream));
 }
 
 // ---- Allocation-free variant. The split-K partials live in a fixed device array of this file instead of a caller

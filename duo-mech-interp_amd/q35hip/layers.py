@@ -218,7 +218,8 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     cache positions 0..pos+t (engine/kernels_qwen35.js:90). T > 1 at the int position 0 runs the flash prefill over
     the call's own tokens; T > 1 at any other position (or a device pos) the same kernel over the cache (the caches'
     max_len must then be a multiple of 64); T == 1 the split-K decode over cache positions 0..pos (cache_len:
-    optional [B] int32 per-row lengths, default pos + 1). prenorm: see linear(). For T > 1, x may be the int32 words
+    optional [B] int32 per-row lengths, default pos + 1; without it the q / k norms, RoPE and the cache append run
+    inside the decode kernels, q35_gated_attn_decode_proj, instead of a front-end launch). prenorm: see linear(). For T > 1, x may be the int32 words
     of split activations (see gated_deltanet_layer). Returns y [B, T, H], or with residual [B, T, H] given,
     residual + y computed in place by o_proj (then returned). fixed_order: see linear()."""
     B, T, _ = x.shape
@@ -237,6 +238,13 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
         own_keys = pos == 0
     cos, sin = rope_tables(max_len, rot, rope_theta, x.device)
     y = linear(x, attn_in_weight(p), *_q8(p, "_in_fused"), prenorm=prenorm)
+    if T == 1 and cache_len is None and y.dtype == torch.float32 and y.shape[-1] % 4 == 0:
+        # one token: the front end (q / k norms, RoPE, cache append) runs inside the decode kernels, reading y
+        o = ops.gated_attention_decode_proj(y, p["q_norm"], p["k_norm"], k_cache, v_cache, pos_t, cos, sin,
+                                            num_heads=Hq, eps=eps, scale=1.0 / math.sqrt(D),
+                                            out_dtype=torch.float32).view(B, 1, Hq * D)
+        wq_o, ws_o = _q8(p, "o_proj")
+        return linear(o, p["o_proj"], wq_o, ws_o, residual=residual, fixed_order=fixed_order)
     q, gate, k, v = ops.attn_prep(y, p["q_norm"], p["k_norm"], cos, sin, pos_t, k_cache, v_cache, num_heads=Hq,
                                   num_kv_heads=Hkv, eps=eps, want_kv=T > 1 and own_keys)
     if T > 1 and own_keys:

@@ -163,10 +163,8 @@ class HybridModel:
                 self.states.append({
                     "conv": torch.zeros(rows, cfg.conv_k - 1, cfg.conv_dim, device=device),
                     "rec": torch.zeros(rows, cfg.lin_v_heads, cfg.lin_dk, cfg.lin_dv, device=device)})
-        # row 0: each row's next position; row 1: its cache length after that token (position + 1). One add per
-        # step advances both, so the decode step computes no length of its own.
-        self._pos_len = torch.zeros(2, rows, dtype=torch.int32, device=device)
-        self.pos_dev, self.len_dev = self._pos_len[0], self._pos_len[1]
+        # each row's next position, on the device (the decode step reads it there, so a replayed graph follows it)
+        self.pos_dev = torch.zeros(rows, dtype=torch.int32, device=device)
         self.graph = None
         self.step_capture, self._step_cap_idx = None, {}
         self.row_pos = [0] * rows  # host mirror of pos_dev
@@ -181,7 +179,6 @@ class HybridModel:
                 st["rec"][rs].zero_()
                 st["conv"][rs].zero_()
         self.pos_dev[rs].zero_()
-        self.len_dev[rs].fill_(1)
         for r in range(self.rows)[rs]:
             self.row_pos[r] = 0
 
@@ -269,7 +266,6 @@ class HybridModel:
         pos_dev, vec_rows = self.pos_dev[rs], self.vec_rows[rs]
         if T == 1:
             fx = self.deterministic
-            cache_len = self.len_dev[rs]  # shared by the attention layers
             for l in range(last + 1):
                 p = self.params[l]
                 st = {n: t[rs] for n, t in self.states[l].items()}
@@ -277,7 +273,7 @@ class HybridModel:
                 if cfg.is_attention(l):
                     layers.gated_attention_layer(x, p, st["k"], st["v"], pos_dev, rope_theta=cfg.rope_theta,
                                                  partial_rotary_factor=cfg.partial_rotary, eps=cfg.eps,
-                                                 cache_len=cache_len, prenorm=pre, residual=x, fixed_order=fx)
+                                                 prenorm=pre, residual=x, fixed_order=fx)
                 else:
                     layers.gated_deltanet_layer(x, p, st["conv"], st["rec"], p["_head_scale"],
                                                 num_k_heads=cfg.lin_k_heads, head_k_dim=cfg.lin_dk, eps=cfg.eps,
@@ -346,7 +342,7 @@ class HybridModel:
         last = cfg.layers - 1 if stop_after is None else stop_after
         hooks = self._hooks(len(rows), T, last, capture, capture_layers, resid, resid_mode, t0)
         x, collected = self._layers(x, T, last, collect_layer, self.steering, rs, attn_pos, hooks)
-        self._pos_len[:, rs].add_(T)
+        self.pos_dev[rs].add_(T)
         for r in rows:
             self.row_pos[r] += T
         if stop_after is not None:
@@ -417,7 +413,7 @@ class HybridModel:
         def step():
             x, _ = self._layers(self.W["embed"].index_select(0, self._g_ids).unsqueeze(1), 1, cfg.layers - 1, None,
                                 True, hooks=hooks)
-            self._pos_len.add_(1)
+            self.pos_dev.add_(1)
             logits = self._lm_head(x[:, -1])
             ops.argmax_rows(logits, out=self._g_ids)
             return logits

@@ -64,6 +64,9 @@ _LIB.define("gated_attn_prefill_cached(Tensor q, Tensor k_cache, Tensor v_cache,
             "Tensor cos, Tensor sin, float scale) -> Tensor")
 _LIB.define("gated_attn_decode(Tensor q, Tensor k_cache, Tensor v_cache, Tensor gate, Tensor cache_len, "
             "Tensor cos, Tensor sin, float scale, int splits, bool f32_out=False) -> Tensor")
+_LIB.define("gated_attn_decode_proj(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, Tensor(a!) k_cache, "
+            "Tensor(b!) v_cache, Tensor pos, Tensor cos, Tensor sin, int Hq, float scale, int splits, "
+            "bool f32_out=False) -> Tensor")
 _LIB.define("resid_add_rows_(Tensor(a!) x, Tensor vecs, Tensor? vec_of_row) -> ()")
 _LIB.define("gdn_conv(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
             "Tensor dt_bias, int b_off, int a_off, int Hk, int dk, int Hv, int dv, bool bf16_out) "
@@ -224,6 +227,33 @@ def _attn_decode_impl(q, k_cache, v_cache, gate, cache_len, cos, sin, scale, spl
                                  _ptr(sin), _ptr(out), _DT[odt], B, Hq, Hkv, D, max_len, rot, float(scale), int(splits),
                                  _ptr(ws), ws.numel(), _stream(q))
     check(st, "q35_gated_attn_decode")
+    return out
+
+
+def _attn_decode_proj_impl(y, q_norm_w, k_norm_w, eps, k_cache, v_cache, pos, cos, sin, Hq, scale, splits,
+                           f32_out=False):
+    _on_gpu(q_norm_w, k_norm_w, k_cache, v_cache, pos, cos, sin)
+    _require(y.is_cuda and y.dtype == torch.float32 and y.is_contiguous() and y.dim() in (2, 3)
+             and (y.dim() == 2 or y.shape[1] == 1), "y: [B, W] or [B, 1, W] fp32 dense (the fused projection output)")
+    y2 = y.view(y.shape[0], y.shape[-1])
+    B, W = y2.shape
+    _require(k_cache.dtype == torch.bfloat16 and k_cache.dim() == 4 and v_cache.shape == k_cache.shape
+             and v_cache.dtype == k_cache.dtype, "caches: [B, Hkv, max_len, D] bf16")
+    Hkv, max_len, D = k_cache.shape[1], k_cache.shape[2], k_cache.shape[3]
+    _require(k_cache.shape[0] == B, "caches must match y in batch")
+    _require(pos.dtype == torch.int32 and tuple(pos.shape) == (B,), "pos: [B] int32")
+    _require(q_norm_w.dtype == torch.float32 and k_norm_w.dtype == torch.float32 and q_norm_w.numel() == D
+             and k_norm_w.numel() == D and q_norm_w.is_contiguous() and k_norm_w.is_contiguous(),
+             "q_norm_w, k_norm_w: [D] fp32")
+    rot = _tables_check(cos, sin, max_len)
+    L = _lib.lib()
+    ws = _workspace(L.q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits), y.device)
+    odt = torch.float32 if f32_out else torch.bfloat16
+    out = torch.empty(B, Hq * D, dtype=odt, device=y.device)
+    st = L.q35_gated_attn_decode_proj(_ptr(y2), W, _ptr(q_norm_w), _ptr(k_norm_w), float(eps), _ptr(k_cache),
+                                      _ptr(v_cache), _ptr(pos), _ptr(cos), _ptr(sin), _ptr(out), _DT[odt], B, Hq, Hkv,
+                                      D, max_len, rot, float(scale), int(splits), _ptr(ws), ws.numel(), _stream(y))
+    check(st, "q35_gated_attn_decode_proj")
     return out
 
 
@@ -611,6 +641,7 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gdn_chunk_prefill", _gdn_chunk_impl), ("gated_attn_prefill", _attn_prefill_impl),
                      ("gated_attn_prefill_cached", _attn_prefill_cached_impl),
                      ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
+                     ("gated_attn_decode_proj", _attn_decode_proj_impl),
                      ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl), ("gated_rmsnorm_split", _gated_rmsnorm_split_impl),
                      ("gdn_decode_fused_", _gdn_decode_fused_impl),
                      ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
@@ -640,6 +671,10 @@ _LIB.impl("gated_attn_prefill",
 _LIB.impl("gated_attn_decode",
           lambda q, kc, vc, gate, cl, cos, sin, scale, splits, f32_out=False:
           q.new_empty(q.shape[0], q.shape[1] * q.shape[2], dtype=torch.float32 if f32_out else q.dtype),
+          "Meta")
+_LIB.impl("gated_attn_decode_proj",
+          lambda y, qn, kn, eps, kc, vc, pos, cos, sin, Hq, scale, splits, f32_out=False:
+          y.new_empty(y.shape[0], Hq * kc.shape[3], dtype=torch.float32 if f32_out else torch.bfloat16),
           "Meta")
 _LIB.impl("resid_add_rows_", lambda x, vecs, vor: None, "Meta")
 _LIB.impl("gdn_decode_fused_", lambda y, cw, cb, cs, Al, dt, bo, ao, zo, st, nw, hs, eps, sc:
@@ -751,6 +786,20 @@ def gated_attention_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, scale
     scale = q.shape[-1] ** -0.5 if scale is None else scale
     return torch.ops.q35.gated_attn_decode(q, k_cache, v_cache, gate, cache_len, cos, sin, float(scale), int(splits),
                                            out_dtype == torch.float32)
+
+
+def gated_attention_decode_proj(y, q_norm_w, k_norm_w, k_cache, v_cache, pos, cos, sin, *, num_heads, eps=1e-6,
+                                scale=None, splits=0, out_dtype=torch.bfloat16):
+    """The attention decode step from the fused projection output y [B, W] (or [B, 1, W]) fp32 of one token per row
+    ([q | gate] per head, then k, then v; engine/kernels_qwen35.js:18-123 attnPrep + attention): q and k normalised
+    with (1 + w) and rotated at position pos[b] ([B] int32 on the device), the token's key and value appended to the
+    bf16 caches at pos[b], attention over cache keys 0 .. pos[b], sigmoid gate. Returns [B, num_heads * D] bf16, or
+    fp32 with out_dtype=torch.float32."""
+    D = k_cache.shape[3]
+    scale = D ** -0.5 if scale is None else scale
+    return torch.ops.q35.gated_attn_decode_proj(y, q_norm_w.float().contiguous(), k_norm_w.float().contiguous(),
+                                                float(eps), k_cache, v_cache, pos, cos, sin, int(num_heads),
+                                                float(scale), int(splits), out_dtype == torch.float32)
 
 
 def residual_steer_add_(x, vecs, vec_of_row=None):

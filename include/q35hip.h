@@ -17,6 +17,9 @@
  *                            (engine/kernels_qwen35.js:90; engine/model.js:486-491 chunked prefill)
  *   q35_gated_attn_decode    same as above for one new token per row over a KV cache (engine/kernels_qwen35.js:73-123
  *                            with T = 1; HF decode through DynamicCache)
+ *   q35_gated_attn_decode_proj  the decode step from the fused projection output: engine/kernels_qwen35.js:18-69
+ *                            `attnPrep` (q / k RMSNorm, RoPE, cache append) and :73-123 `attention` for T = 1
+ *                            in one call (HF:667-701 for one cached token)
  *   q35_resid_add_rows       tests/engine_ref.py:49-53 residual vector hook; engine/kernels.js:190-203 `resAdd`
  *   q35_gdn_conv             HF:454-499 (causal_conv1d_fn / causal_conv1d_update + SiLU, split, beta, g);
  *                            engine/kernels_qwen35.js:127-178 `conv` + `convState`, :226-229 (gate terms of `delta`)
@@ -176,6 +179,24 @@ int q35_gated_attn_decode(const void* q, const void* k_cache, const void* v_cach
                           int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len, int64_t rot,
                           float scale, int64_t splits, void* workspace, size_t workspace_bytes,
                           q35_stream_t stream);
+
+/*
+ * The attention decode step from the fused projection output of one token per row (engine/kernels_qwen35.js:18-69
+ * `attnPrep` followed by :73-123 `attention` with T = 1; HF:667-701 with a DynamicCache): y [B, ldy] fp32 rows
+ * holding [q | gate] per query head (Hq * 2D), then k (Hkv * D), then v (Hkv * D) from column 0. q and k are
+ * normalised with (1 + q_norm_w / k_norm_w) (RMS, eps) and rotated at position pos[b] (device int32, so that a
+ * captured step replays at the row's current position); the token attends to cache keys 0 .. pos[b] - 1 and to
+ * itself; its rotated key and its value are written into k_cache / v_cache at pos[b] (bf16, when pos[b] < max_len).
+ * out = attention * sigmoid(gate), [B, Hq * D] in out_dtype. Same workspace as q35_gated_attn_decode
+ * (q35_gated_attn_decode_workspace_bytes), same limits (D 256, Hq / Hkv in 1, 2, 4, 8, rot a multiple of 8); y,
+ * ldy and the norm weights 16-byte aligned. The cached keys are those the front end (q35_attn_prep) would have
+ * written, and the key written here is bitwise the one it writes.
+ */
+int q35_gated_attn_decode_proj(const float* y, int64_t ldy, const float* q_norm_w, const float* k_norm_w, float eps,
+                               void* k_cache, void* v_cache, const int32_t* pos, const float* cos, const float* sin,
+                               void* out, int out_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                               int64_t max_len, int64_t rot, float scale, int64_t splits, void* workspace,
+                               size_t workspace_bytes, q35_stream_t stream);
 
 /*
  * q35_gated_attn_decode without a workspace argument, for callers that cannot allocate device memory (code under HIP

@@ -151,6 +151,50 @@ def test_attn_prep_matches_oracle_and_writes_cache_rows(T):
     assert bool((kc.transpose(1, 2)[~written] == 7.0).all()) and bool((vc.transpose(1, 2)[~written] == 7.0).all())
 
 
+@pytest.mark.parametrize("Hq,Hkv,splits", [(8, 2, 0), (16, 2, 0), (8, 8, 3)])
+def test_attn_decode_from_projection(Hq, Hkv, splits):
+    """The decode step from the fused projection output (q35_gated_attn_decode_proj: the front end inside the decode
+    kernels) against the oracle's front end + decode over the cache with the token's key appended, and against the
+    two-launch path (q35_attn_prep, then q35_gated_attn_decode) on the same inputs, whose caches it must leave
+    bitwise equal. Rows at positions 0 (empty cache: the token attends to itself only), 1, 300 and max_len - 1; GQA
+    4, 8 and 1 (with 3 splits)."""
+    dev = device()
+    g = torch.Generator().manual_seed(80 + Hq + Hkv)
+    B, D, max_len = 4, 256, 512
+    y = torch.randn(B, Hq * 2 * D + 2 * Hkv * D, generator=g)
+    qw, kw = 0.1 * torch.randn(D, generator=g), 0.1 * torch.randn(D, generator=g)
+    cos, sin = rope_tables(max_len, rope_inv_freq(D, 0.25, 1e7))
+    pos = torch.tensor([0, 1, 300, max_len - 1], dtype=torch.int32)
+    kc0 = torch.randn(B, Hkv, max_len, D, generator=g).to(torch.bfloat16)
+    vc0 = torch.randn(B, Hkv, max_len, D, generator=g).to(torch.bfloat16)
+    q, gate, k, v, k_rot = of.attn_prep(y[:, None], qw, kw, cos, sin, pos, Hq, Hkv, D)
+    kr, vr = kc0.clone(), vc0.clone()
+    for b in range(B):
+        kr[b, :, int(pos[b])] = k_rot[b, 0].to(torch.bfloat16)
+        vr[b, :, int(pos[b])] = v[b, 0].to(torch.bfloat16)
+    ref = oracle.gated_attention_decode(q[:, 0], kr, vr, gate[:, 0], pos + 1, cos, sin)
+    announce(f"attn decode from projection Hq{Hq} Hkv{Hkv} splits {splits}")
+    yd, qwd, kwd, posd = y.to(dev), qw.to(dev), kw.to(dev), pos.to(dev)
+    cosd, sind = cos.to(dev), sin.to(dev)
+    kcb, vcb = kc0.to(dev), vc0.to(dev)
+    out = ops.gated_attention_decode_proj(yd, qwd, kwd, kcb, vcb, posd, cosd, sind, num_heads=Hq, splits=splits)
+    kca, vca = kc0.to(dev), vc0.to(dev)
+    qa, ga, _, _ = ops.attn_prep(yd[:, None].contiguous(), qwd, kwd, cosd, sind, posd, kca, vca, num_heads=Hq,
+                                 num_kv_heads=Hkv)
+    two = q35hip.gated_attention_decode(qa[:, 0].contiguous(), kca, vca, ga[:, 0].contiguous(), posd + 1, cosd, sind,
+                                        splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(kcb.cpu(), kca.cpu()) and torch.equal(vcb.cpu(), vca.cpu())
+    e_ref, e_two = oracle.rel_err(out.float().cpu(), ref), oracle.rel_err(out.float().cpu(), two.float().cpu())
+    print(f"decode from projection: rel err {e_ref:.3e} (oracle), {e_two:.3e} (two-launch path)")
+    assert e_ref <= 2e-2 and e_two <= 1e-2
+    # fp32 output: the bf16 output before its rounding
+    kcb, vcb = kc0.to(dev), vc0.to(dev)
+    o32 = ops.gated_attention_decode_proj(yd, qwd, kwd, kcb, vcb, posd, cosd, sind, num_heads=Hq, splits=splits,
+                                          out_dtype=torch.float32)
+    assert o32.dtype == torch.float32 and torch.equal(o32.to(torch.bfloat16).cpu(), out.cpu())
+
+
 @pytest.mark.parametrize("with_add", [False, True])
 def test_add_rmsnorm_matches_oracle(with_add):
     """Residual add + RMSNorm(1 + w) (HF:720-734): x updated in place, h returned."""
