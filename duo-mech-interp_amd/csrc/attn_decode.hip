@@ -15,6 +15,12 @@
 // Pass 2 (attn_decode_merge_kernel): log-sum-exp merge over splits, sigmoid gate, bf16 store; every load of a
 // thread is issued before the first is used (one memory round trip).
 // HBM traffic is the K and V spans once (AI ~ 4 flop/byte): the kernel is bandwidth bound by design.
+//
+// From the fused projection output (q35_gated_attn_decode_proj, the WGSL attnPrep + attention for one token,
+// engine/kernels_qwen35.js:18-123): the partial kernel reads q from y and normalises it (RMS with 1 + w) before the
+// rotation; split 0's block also forms the token's own key (normalised, rotated) and value, appends them to the caches
+// at the token's position and folds that key into its partial; the merge reads the gate from y. One launch fewer
+// per decode step than the front end followed by the decode, and no q / gate round trip through memory.
 #include <atomic>
 #include <mutex>
 
@@ -52,14 +58,20 @@ __device__ __forceinline__ float row16_sum(float v) {
 
 // Query source of the partial kernel. FP false: bf16 q [B, Hq, D], the cache holding every key up to and including
 // the token's (cache_len[b] keys, the query at position cache_len[b] - 1). FP true: the token's fused projection
-// output, fp32 rows of y with [q | gate] per query head from column 0 (engine/kernels_qwen35.js:36-38), q
-// normalised here with (1 + w) (the WGSL attnPrep's q half, :40-47); cache_len[b] is then the token's position
-// pos, the cache holds keys 0 .. pos - 1, and the new key is folded in by the merge kernel.
+// output y (fp32 rows: [q | gate] per query head, then k, then v; engine/kernels_qwen35.js:36-38), the WGSL attnPrep
+// (:18-69) done here: q and the new key normalised with (1 + w) and rotated at the token's position pos =
+// cache_len[b]; the cache holds keys 0 .. pos - 1, and split 0's block appends the new key and value to the caches
+// at pos (when pos < max_len) and folds the token's own key into its partial. No block of the launch reads cache
+// row pos for a key it uses (a block's keys end below pos; rows past a span are loaded from clamped rows and masked),
+// so the append needs no ordering against the other blocks.
 struct DecQ {
   const void* q;
   int64_t ldy;       // FP: row stride of y (floats)
   const float* qnw;  // FP: q_norm weight [D]
+  const float* knw;  // FP: k_norm weight [D]
   float eps;
+  __bf16* kw;        // FP: the caches, for the append
+  __bf16* vw;
 };
 
 template <int G, int NT, bool FP>
@@ -71,7 +83,8 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   constexpr int NG = (G + 3) / 4;  // lane groups of the MFMA D tile that hold real heads
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  Q35_ARGS_UPFRONT(dq.q, dq.ldy, dq.qnw, dq.eps, kc, vc, cache_len, cos_t, sin_t, rot, part, Hq, Hkv, max_len, S, scale);
+  Q35_ARGS_UPFRONT(dq.q, dq.ldy, dq.qnw, dq.knw, dq.eps, dq.kw, dq.vw, kc, vc, cache_len, cos_t, sin_t, rot, part, Hq,
+                   Hkv, max_len, S, scale);
 
   // cache_len lives on the device: its read is issued here and waited for after the query loads below
   const int len_raw = cache_len[b];
@@ -83,8 +96,12 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   constexpr int NQ = (G * 64 + 255) / 256;
   u32x2 xq[NQ], pq[NQ];
   f32x4 xf[NQ], pf[NQ], wx[NQ], wp[NQ];
+  // FP, split 0: the new token's key quad (wave 0: dims 4 lane .., with its rotation partner) and value quad (wave 1)
+  const bool newkey = FP && s == 0;
+  f32x4 nx, npx, nw, npw;
   if constexpr (FP) {
-    const float* yb = static_cast<const float*>(dq.q) + (size_t)b * dq.ldy + (size_t)kvh * G * 2 * kDecD;
+    const float* yr = static_cast<const float*>(dq.q) + (size_t)b * dq.ldy;
+    const float* yb = yr + (size_t)kvh * G * 2 * kDecD;
 #pragma unroll
     for (int u = 0; u < NQ; ++u) {
       const int qi = min(tid + 256 * u, G * 64 - 1), hh = qi >> 6, d0 = 4 * (qi & 63);
@@ -93,6 +110,16 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
       pf[u] = *reinterpret_cast<const f32x4*>(yb + hh * 2 * kDecD + pd0);
       wx[u] = *reinterpret_cast<const f32x4*>(dq.qnw + d0);
       wp[u] = *reinterpret_cast<const f32x4*>(dq.qnw + pd0);
+    }
+    if (newkey && wave < 2) {
+      const int d0 = 4 * lane, pd0 = d0 < rot ? (d0 < half ? d0 + half : d0 - half) : d0;
+      const float* src = yr + (size_t)Hq * 2 * kDecD + (size_t)(wave == 0 ? kvh : Hkv + kvh) * kDecD;
+      nx = *reinterpret_cast<const f32x4*>(src + d0);
+      if (wave == 0) {
+        npx = *reinterpret_cast<const f32x4*>(src + pd0);
+        nw = *reinterpret_cast<const f32x4*>(dq.knw + d0);
+        npw = *reinterpret_cast<const f32x4*>(dq.knw + pd0);
+      }
     }
   } else {
     const __bf16* qb = static_cast<const __bf16*>(dq.q) + ((size_t)b * Hq + (size_t)kvh * G) * kDecD;
@@ -114,6 +141,8 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
   const int pos = FP ? min(len, max_len - 1) : max(len - 1, 0);  // the query's position
 
   __shared__ __attribute__((aligned(16))) float qf[G][kDecD];
+  __shared__ __attribute__((aligned(16))) float knew[FP ? kDecD : 1], vnew[FP ? kDecD : 1];
+  __shared__ float snew[FP ? G : 1];
   __shared__ float pl[4][kDecTile][G];
   __shared__ float comb_o[4][G][kDecD];
   __shared__ float comb_ml[4][G][2];
@@ -241,6 +270,42 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
       *reinterpret_cast<f32x4*>(&qf[hh][d0]) = r;
     }
   }
+  if constexpr (FP) {
+    // the new key (split 0, wave 0), normalised and rotated exactly as the front end does it (frontend.hip
+    // attn_prep_kernel) and rounded to bf16 as the cache holds it; the value (wave 1) likewise. Lane l holds dims
+    // 4 l .. 4 l + 3, whose cos / sin rows wave 0 loaded for its query quad above.
+    if (newkey && wave < 2) {
+      const int e0 = 4 * lane;
+      bf16x4 kb;
+      if (wave == 0) {
+        const float ss = wave_sum(nx[0] * nx[0] + nx[1] * nx[1] + nx[2] * nx[2] + nx[3] * nx[3]);
+        const float rr = rsqrtf(ss * (1.f / kDecD) + dq.eps);
+        f32x4 kn, pn, kr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kn[e] = nx[e] * rr * (1.f + nw[e]);
+          pn[e] = npx[e] * rr * (1.f + npw[e]);
+        }
+        if (e0 < rot) {
+          const float sg = e0 < half ? -1.f : 1.f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) kr[e] = kn[e] * cq[0][e] + sg * pn[e] * sq[0][e];
+        } else {
+          kr = kn;
+        }
+        kb = {(__bf16)kr[0], (__bf16)kr[1], (__bf16)kr[2], (__bf16)kr[3]};
+      } else {
+        kb = {(__bf16)nx[0], (__bf16)nx[1], (__bf16)nx[2], (__bf16)nx[3]};
+      }
+      float* dst = wave == 0 ? knew : vnew;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dst[e0 + e] = (float)kb[e];
+      if (len < max_len) {
+        __bf16* cache = wave == 0 ? dq.kw : dq.vw;
+        *reinterpret_cast<bf16x4*>(cache + (((size_t)b * Hkv + kvh) * max_len + len) * kDecD + e0) = kb;
+      }
+    }
+  }
   __syncthreads();
 
   // 2. A operand: row = head (l % 16 < G), k = dims 32 ks + 8 (l / 16) + j; wave w writes k steps 2 w, 2 w + 1
@@ -286,6 +351,18 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
       comb_ml[wave][hh][1] = l_run[r];
     }
   }
+  if constexpr (FP) {
+    // split 0: the new key's score for each head, from the query and key as the MFMA and the cache hold them (bf16)
+    if (newkey) {
+      for (int hh = wave; hh < G; hh += 4) {
+        float dot = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dot += (float)(__bf16)qf[hh][4 * lane + e] * knew[4 * lane + e];
+        dot = wave_sum(dot);
+        if (lane == 0) snew[hh] = dot * scale;
+      }
+    }
+  }
   __syncthreads();
   float* pb = part + (((size_t)b * Hkv + kvh) * S + s) * (size_t)G * (kDecD + 2);
   for (int i = tid; i < G * kDecD; i += 256) {
@@ -293,6 +370,11 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < 4; ++w) M = fmaxf(M, comb_ml[w][hh][0]);
+    float sn = -INFINITY;
+    if constexpr (FP) {
+      if (newkey) sn = snew[hh];
+    }
+    M = fmaxf(M, sn);
     float Lsum = 0.f, O = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
@@ -300,6 +382,13 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
         const float f = __expf(comb_ml[w][hh][0] - M);
         Lsum += comb_ml[w][hh][1] * f;
         O += comb_o[w][hh][d] * f;
+      }
+    }
+    if constexpr (FP) {
+      if (newkey) {
+        const float f = __expf(sn - M);
+        Lsum += f;
+        O += f * vnew[d];
       }
     }
     pb[(size_t)hh * (kDecD + 2) + d] = O;
@@ -313,109 +402,21 @@ __global__ __launch_bounds__(256) void attn_decode_partial_kernel(
 // Merge over splits, gate, store. One block per (query head, row, slice of 32 head dims): thread (g, d) folds the
 // splits g, g + 8, ... of dim d with an online log-sum-exp, loading eight splits' (max, sum, acc) at a time before
 // using any of them; the eight groups are combined in LDS.
-// The new token of the FP form (the WGSL attnPrep's k / v half, engine/kernels_qwen35.js:40-65, for one token per
-// row): its key and value come from y (k of kv head j at column Hq 2 D + j D, v at Hq 2 D + (Hkv + j) D), k
-// normalised with (1 + w) and rotated at the token's position pos[b]. The merge folds them in as one more split of
-// one key, and one block per (row, kv head) writes them into the caches at pos[b] (when pos[b] < max_len): the
-// partial kernel of the same call reads only keys below pos[b], and the next call finds them in the cache.
-struct DecNew {
-  const float* y;
-  int64_t ldy;
-  const float* qnw;
-  const float* knw;
-  float eps;
-  const int32_t* pos;
-  const float* cos_t;
-  const float* sin_t;
-  int rot;
-  int max_len;
-  __bf16* kc;
-  __bf16* vc;
-  float scale;
-};
-
-// Normalise (RMS with (1 + w)) and rotate one 256-dim head held as a float4 per lane of a wave, exactly as the
-// attention front end does it (frontend.hip attn_prep_kernel), so that a key written here equals the one the front
-// end would have written.
-__device__ __forceinline__ f32x4 norm_rotate(const float* src, const float* nw, float eps, const float* cos_t,
-                                             const float* sin_t, int rot, int p, int lane) {
-  const int d0 = 4 * lane, half = rot >> 1;
-  const int pd0 = d0 < rot ? (d0 < half ? d0 + half : d0 - half) : d0;
-  const f32x4 x = *reinterpret_cast<const f32x4*>(src + d0);
-  const f32x4 px = *reinterpret_cast<const f32x4*>(src + pd0);
-  const f32x4 wv = *reinterpret_cast<const f32x4*>(nw + d0);
-  const f32x4 pw = *reinterpret_cast<const f32x4*>(nw + pd0);
-  const float ss = wave_sum(x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3]);
-  const float r = rsqrtf(ss * (1.f / kDecD) + eps);
-  f32x4 xn, pn;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    xn[e] = x[e] * r * (1.f + wv[e]);
-    pn[e] = px[e] * r * (1.f + pw[e]);
-  }
-  if (d0 >= rot) return xn;
-  const int j0 = d0 < half ? d0 : d0 - half;
-  const f32x4 cv = *reinterpret_cast<const f32x4*>(cos_t + (size_t)p * half + j0);
-  const f32x4 sv = *reinterpret_cast<const f32x4*>(sin_t + (size_t)p * half + j0);
-  const float sg = d0 < half ? -1.f : 1.f;
-  f32x4 xr;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) xr[e] = xn[e] * cv[e] + sg * pn[e] * sv[e];
-  return xr;
-}
-
-template <typename Tout, bool FP>
+template <typename Tout, typename Tg>
 __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __restrict__ part,
-                                                                const __bf16* __restrict__ gate,
-                                                                Tout* __restrict__ out, int Hq, int Hkv, int S,
-                                                                DecNew nk) {
-  Q35_ARGS_UPFRONT(part, gate, out, Hq, Hkv, S);
-  if constexpr (FP)
-    Q35_ARGS_UPFRONT(nk.y, nk.ldy, nk.qnw, nk.knw, nk.eps, nk.pos, nk.cos_t, nk.sin_t, nk.rot, nk.max_len, nk.kc,
-                     nk.vc, nk.scale);
+                                                                const Tg* __restrict__ gate, int64_t gate_ld,
+                                                                int gate_hs, Tout* __restrict__ out, int Hq, int Hkv,
+                                                                int S) {
+  Q35_ARGS_UPFRONT(part, gate, gate_ld, gate_hs, out, Hq, Hkv, S);
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int G = Hq / Hkv, kvh = h / G, hh = h % G;
   const int grp = tid >> 5, d = 32 * blockIdx.z + (tid & 31);
   const size_t sstride = (size_t)G * (kDecD + 2);
   const float* pb = part + ((size_t)b * Hkv + kvh) * S * sstride + (size_t)hh * (kDecD + 2);
   __shared__ float gm[8], gl[8], go[8][32];
-  __shared__ __attribute__((aligned(16))) float qs[FP ? kDecD : 1], ks[FP ? kDecD : 1];
   // the gate value this thread's output needs is loaded first, so that its round trip overlaps the partials'
   const size_t oi = (size_t)b * Hq * kDecD + (size_t)h * kDecD + d;
-  float gv = 0.f, vnew = 0.f;
-  if constexpr (FP) {
-    const float* yr = nk.y + (size_t)b * nk.ldy;
-    if (tid < 32) {
-      gv = yr[(size_t)h * 2 * kDecD + kDecD + d];
-      vnew = (float)(__bf16)yr[(size_t)Hq * 2 * kDecD + (size_t)(Hkv + kvh) * kDecD + d];
-    }
-    // the new key's score: wave 0 forms the query (as the partial kernel does), wave 1 the key, both rounded to
-    // bf16 as the partial kernel's MFMA operands and the cache hold them; wave 2 of the writing block the value
-    const int wv = tid >> 6, lane = tid & 63;
-    const int p = min(max(nk.pos[b], 0), nk.max_len);
-    const int pq = min(p, nk.max_len - 1);
-    const bool writer = hh == 0 && blockIdx.z == 0 && p < nk.max_len;
-    if (wv == 0) {
-      const f32x4 qr = norm_rotate(yr + (size_t)h * 2 * kDecD, nk.qnw, nk.eps, nk.cos_t, nk.sin_t, nk.rot, pq, lane);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) qs[4 * lane + e] = (float)(__bf16)qr[e];
-    } else if (wv == 1) {
-      const f32x4 kr = norm_rotate(yr + (size_t)Hq * 2 * kDecD + (size_t)kvh * kDecD, nk.knw, nk.eps, nk.cos_t,
-                                   nk.sin_t, nk.rot, pq, lane);
-      bf16x4 kb = {(__bf16)kr[0], (__bf16)kr[1], (__bf16)kr[2], (__bf16)kr[3]};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ks[4 * lane + e] = (float)kb[e];
-      if (writer)
-        *reinterpret_cast<bf16x4*>(nk.kc + (((size_t)b * Hkv + kvh) * nk.max_len + p) * kDecD + 4 * lane) = kb;
-    } else if (wv == 2 && writer) {
-      const f32x4 x =
-          *reinterpret_cast<const f32x4*>(yr + (size_t)Hq * 2 * kDecD + (size_t)(Hkv + kvh) * kDecD + 4 * lane);
-      const bf16x4 vb = {(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
-      *reinterpret_cast<bf16x4*>(nk.vc + (((size_t)b * Hkv + kvh) * nk.max_len + p) * kDecD + 4 * lane) = vb;
-    }
-  } else {
-    gv = tid < 32 ? (float)gate[oi] : 0.f;
-  }
+  const float gv = tid < 32 ? to_f32(gate[(size_t)b * gate_ld + (size_t)h * gate_hs + d]) : 0.f;
   float M = -INFINITY, Lsum = 0.f, O = 0.f;
   for (int s0 = grp; s0 < S; s0 += 64) {
     float m[8], l[8], a[8];
@@ -446,17 +447,6 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __r
     float Mx = -INFINITY;
 #pragma unroll
     for (int g = 0; g < 8; ++g) Mx = fmaxf(Mx, gm[g]);
-    float snew = 0.f;
-    if constexpr (FP) {
-      // q . k of the new token over 256 dims: 8 per lane, then across the 32 lanes
-      float acc = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc += qs[8 * tid + i] * ks[8 * tid + i];
-#pragma unroll
-      for (int off = 16; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-      snew = acc * nk.scale;
-      Mx = fmaxf(Mx, snew);
-    }
     float Lt = 0.f, Ot = 0.f;
     if (Mx != -INFINITY) {
 #pragma unroll
@@ -465,11 +455,6 @@ __global__ __launch_bounds__(256) void attn_decode_merge_kernel(const float* __r
         Lt += gl[g] * w;
         Ot += go[g][tid] * w;
       }
-    }
-    if constexpr (FP) {
-      const float e = __expf(snew - Mx);
-      Lt += e;
-      Ot += e * vnew;
     }
     const float res = Lt > 0.f ? Ot / Lt : 0.f;
     out[oi] = from_f32<Tout>(res * sigmoidf_(gv));
@@ -534,11 +519,11 @@ static int decode_check(const void* q, const void* k_cache, const void* v_cache,
 }  // namespace q35
 
 namespace q35 {
-// The two launches of a decode call (partial over the splits, then the merge); FP: the query, the new key and value
-// and the gate from the fused projection output (DecQ / DecNew), cache_len then holding the token's position.
+// The two launches of a decode call (partial over the splits, then the merge). FP: the query, the new key and value
+// and the gate come from the fused projection output (DecQ), cache_len holding the token's position.
 template <bool FP>
-static int decode_launch(const DecQ& dq, const DecNew& nk, const void* k_cache, const void* v_cache,
-                         const void* gate, const int32_t* cache_len, const float* cos, const float* sin, void* out,
+static int decode_launch(const DecQ& dq, const void* k_cache, const void* v_cache, const void* gate, int64_t gate_ld,
+                         int gate_hs, const int32_t* cache_len, const float* cos, const float* sin, void* out,
                          int out_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t max_len, int64_t rot,
                          float scale, int64_t splits, void* workspace, hipStream_t st) {
   const int64_t G = Hq / Hkv;
@@ -566,13 +551,14 @@ static int decode_launch(const DecQ& dq, const DecNew& nk, const void* k_cache, 
   }
 #undef Q35_DEC_NT
 #undef Q35_DEC_LAUNCH
+  using Tg = typename std::conditional<FP, float, __bf16>::type;
   const dim3 mgrid((unsigned)Hq, (unsigned)B, kDecD / 32);
   if (out_dtype == Q35_F32)
-    hipLaunchKernelGGL((attn_decode_merge_kernel<float, FP>), mgrid, dim3(256), 0, st, part, (const __bf16*)gate,
-                       (float*)out, (int)Hq, (int)Hkv, S, nk);
+    hipLaunchKernelGGL((attn_decode_merge_kernel<float, Tg>), mgrid, dim3(256), 0, st, part, (const Tg*)gate, gate_ld,
+                       gate_hs, (float*)out, (int)Hq, (int)Hkv, S);
   else
-    hipLaunchKernelGGL((attn_decode_merge_kernel<__bf16, FP>), mgrid, dim3(256), 0, st, part, (const __bf16*)gate,
-                       (__bf16*)out, (int)Hq, (int)Hkv, S, nk);
+    hipLaunchKernelGGL((attn_decode_merge_kernel<__bf16, Tg>), mgrid, dim3(256), 0, st, part, (const Tg*)gate,
+                       gate_ld, gate_hs, (__bf16*)out, (int)Hq, (int)Hkv, S);
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 }  // namespace q35
@@ -589,10 +575,9 @@ extern "C" int q35_gated_attn_decode(const void* q, const void* k_cache, const v
   if (chk != Q35_OK) return chk;
   const size_t need = q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits);
   if (!workspace || workspace_bytes < need) return Q35_EWORKSPACE;
-  const DecQ dq{q, 0, nullptr, 0.f};
-  const DecNew nk{};
-  return decode_launch<false>(dq, nk, k_cache, v_cache, gate, cache_len, cos, sin, out, out_dtype, B, Hq, Hkv,
-                              max_len, rot, scale, splits, workspace, reinterpret_cast<hipStream_t>(stream));
+  const DecQ dq{q, 0, nullptr, nullptr, 0.f, nullptr, nullptr};
+  return decode_launch<false>(dq, k_cache, v_cache, gate, Hq * D, (int)D, cache_len, cos, sin, out, out_dtype, B,
+                              Hq, Hkv, max_len, rot, scale, splits, workspace, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int q35_gated_attn_decode_proj(const float* y, int64_t ldy, const float* q_norm_w, const float* k_norm_w,
@@ -613,11 +598,10 @@ extern "C" int q35_gated_attn_decode_proj(const float* y, int64_t ldy, const flo
   if (B * ldy > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
   const size_t need = q35_gated_attn_decode_workspace_bytes(B, Hq, Hkv, D, max_len, splits);
   if (!workspace || workspace_bytes < need) return Q35_EWORKSPACE;
-  const DecQ dq{y, ldy, q_norm_w, eps};
-  const DecNew nk{y, ldy, q_norm_w, k_norm_w, eps, pos, cos, sin, (int)rot, (int)max_len, (__bf16*)k_cache,
-                  (__bf16*)v_cache, scale};
-  return decode_launch<true>(dq, nk, k_cache, v_cache, nullptr, pos, cos, sin, out, out_dtype, B, Hq, Hkv, max_len,
-                             rot, scale, splits, workspace, reinterpret_cast<hipStream_t>(stream));
+  const DecQ dq{y, ldy, q_norm_w, k_norm_w, eps, (__bf16*)k_cache, (__bf16*)v_cache};
+  // the gate of head h: columns h 2 D + D .. of y
+  return decode_launch<true>(dq, k_cache, v_cache, y + D, ldy, (int)(2 * D), pos, cos, sin, out, out_dtype, B, Hq,
+                             Hkv, max_len, rot, scale, splits, workspace, reinterpret_cast<hipStream_t>(stream));
 }
 
 // ---- Allocation-free variant. The split-K partials live in a fixed device array of this file instead of a caller
