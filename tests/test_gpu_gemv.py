@@ -5,6 +5,7 @@ import torch
 
 import oracle
 from oracle import mlp as omlp
+import q35hip
 from q35hip import ops
 from gpu_util import announce, device
 
@@ -80,6 +81,18 @@ def test_argmax_rows_matches_torch(rows, n):
     torch.cuda.synchronize()
     assert got.dtype == torch.int32
     assert torch.equal(got.cpu().long(), x.argmax(-1))
+    # rows that start 4 bytes past a 16-byte boundary and have a row stride of n + 1 (every row a different head
+    # of scalar elements before the 16-byte loads)
+    # (through the C ABI, which takes the row stride)
+    base = torch.full((rows, n + 1), -5.0)
+    base[:, 1:] = x
+    based = base.to(dev)
+    got2 = torch.full((rows,), -1, dtype=torch.int32, device=dev)
+    st = q35hip.lib().q35_argmax_rows(based.data_ptr() + 4, n + 1, rows, n, got2.data_ptr(), None,
+                                      torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    assert torch.equal(got2.cpu().long(), x.argmax(-1))
 
 
 @pytest.mark.parametrize("epilogue", ["store", "add", "swiglu"])
