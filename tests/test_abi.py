@@ -212,6 +212,32 @@ def test_fused_gdn_step_and_fp32_decode_refuse_cpu_tensors():
                                           out_dtype=torch.float32)
 
 
+def test_decode_from_projection_rejects_without_launching():
+    """q35_gated_attn_decode_proj refuses bad arguments before any HIP call (Hq 8, Hkv 2, D 256: y rows of 5120
+    floats), and its torch op has no CPU path."""
+    L = q35hip.lib()
+    fake = 0x1000
+    W = 8 * 2 * 256 + 2 * 2 * 256
+
+    def call(y=fake, ldy=W, qnw=fake, knw=fake, Hq=8, Hkv=2, D=256, ws_bytes=1 << 20):
+        return L.q35_gated_attn_decode_proj(y, ldy, qnw, knw, 1e-6, fake, fake, fake, fake, fake, fake, 1, 1, Hq, Hkv,
+                                            D, 128, 64, 0.0625, 0, fake, ws_bytes, None)
+    assert call(y=None) == 1                 # null y
+    assert call(knw=None) == 1               # null norm weight
+    assert call(ldy=W - 4) == 1              # rows too short for [q | gate] x Hq, k, v
+    assert call(y=fake + 4) == 2             # y not 16-byte aligned
+    assert call(ldy=W + 2) == 2              # row stride not a multiple of 4 floats
+    assert call(Hq=6) == 2                   # 3 query heads per kv head
+    assert call(D=128, ldy=8 * 256 + 4 * 128) == 2  # head dim other than 256
+    assert call(ws_bytes=8) == 3             # workspace too small
+    y = torch.zeros(1, W)
+    kc = torch.zeros(1, 2, 64, 256, dtype=torch.bfloat16)
+    with pytest.raises(Exception, match="no CPU|HIP device"):
+        q35hip.ops.gated_attention_decode_proj(y, torch.zeros(256), torch.zeros(256), kc, kc.clone(),
+                                               torch.zeros(1, dtype=torch.int32), torch.zeros(64, 32),
+                                               torch.zeros(64, 32), num_heads=8)
+
+
 def test_split_activation_layout():
     """The int8 GEMM's split layout (ops.split_activations, which the norm's split output and the split GEMM follow):
     per row, each group of 8 inputs is 32 bytes, the 8 bf16 hi parts then the 8 bf16 lo parts; hi is x rounded to
