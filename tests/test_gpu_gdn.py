@@ -182,6 +182,21 @@ def test_chunk_prefill_no_decay_full_length():
     assert eo <= TOL_BF16 and es <= TOL_BF16
 
 
+def test_chunk_prefill_long_sequence_slow_gates():
+    """T = 32767 (256 pairs, a ragged last pair) with slow gates: the scan's pipelined pair loop over a long chain,
+    the state carried across every boundary, against the fp32 recurrence."""
+    dev = device()
+    inp = _gate_regime(workloads.gdn_inputs(B=1, T=32767, H=2, D=128, seed=38, dtype=torch.bfloat16), "slow", 38)
+    o_ref, s_ref = _oracle_rec(inp)
+    d = workloads.to_device(inp, dev)
+    announce("gdn chunk T32767 H2 bf16 slow gates")
+    o, S = q35hip.chunk_gated_delta_rule(d["q"], d["k"], d["v"], d["g"], d["beta"], output_final_state=True,
+                                         use_qk_l2norm_in_kernel=True)
+    eo, es = oracle.rel_err(o.float().cpu(), o_ref), oracle.rel_err(S.cpu(), s_ref)
+    print(f"T32767: rel err o {eo:.3e} S {es:.3e}")
+    assert eo <= TOL_BF16 and es <= TOL_BF16
+
+
 @pytest.mark.parametrize("regime", ["zero", "slow"])
 def test_chunk_prefill_fp32_gate_regimes(regime):
     """The fp32 chunk path (the stack's) with the state carried across all 16 chunks of T = 1024: fp32 tolerance.
