@@ -54,6 +54,21 @@ def test_prefill_full_size():
         assert torch.equal(again, out)
 
 
+def test_prefill_long_sequence():
+    """T = 8192 (512 (query block, kv head) items, more than the device holds at once: the independent, longest-first
+    work order) against the fp32 oracle."""
+    dev = device()
+    inp = workloads.attn_prefill_inputs(B=1, T=8192, seed=9)
+    cos, sin = _tables(8192)
+    ref = oracle.gated_attention(inp["q"], inp["k"], inp["v"], inp["gate"], cos, sin)
+    d = workloads.to_device(inp, dev)
+    announce("attn prefill T8192")
+    out = q35hip.gated_attention_prefill(d["q"], d["k"], d["v"], d["gate"], cos.to(dev), sin.to(dev))
+    e = oracle.rel_err(out.float().cpu(), ref)
+    print(f"attn prefill T8192 rel err {e:.3e}")
+    assert e <= TOL
+
+
 def _score_regime(q, k, regime, key_axis):
     """Reshape the scores so that the softmax's running max moves: `rising` adds 16 u to every query and
     60 (t / T) u to key t (u the unit vector on dims 192..255, outside the rotary dims), a score drift of 60 / sqrt(256)
