@@ -8,7 +8,8 @@
 //
 // Kernel 1, attn_kv_prep_kernel: K rotated once ([B, Hkv, Tp, D] bf16, keys padded to a multiple of 64 with zeros)
 // and V transposed once ([B, Hkv, D, Tp] bf16) into the workspace, so that the main loop stages its tiles with
-// plain global -> LDS copies. Inside each group of 16 keys, V^T stores keys in the order 0-3, 8-11, 4-7, 12-15
+// plain global -> LDS copies. From the fused projection output (q35_gated_attn_prefill_proj) it is also the front
+// end: q and k normalised and rotated, k and v appended to the KV cache, q written rotated for the main kernel. Inside each group of 16 keys, V^T stores keys in the order 0-3, 8-11, 4-7, 12-15
 // (bits 2 and 3 of the key index swapped): that is the key order in which an MFMA accumulator tile of scores is fed
 // back as a B operand, so every A fragment of V^T is one 16-byte read.
 // Kernel 2, attn_prefill_kernel: one block of 4 waves per (32-query block, group of up to 4 query heads sharing a kv
@@ -19,6 +20,7 @@
 // arrive by global_load_lds DMA into XOR-swizzled LDS (conflict-free 16-byte operand reads), two stages and one
 // barrier per tile (tile kt + 1 is copied while tile kt is computed), each wave copying a quarter of every tile.
 #include <atomic>
+#include <type_traits>
 
 #include "q35_common.h"
 #include "q35hip.h"
@@ -64,16 +66,31 @@ __device__ __forceinline__ int vperm(int p) { return (p & 3) | ((p & 4) << 1) | 
 // head's V^T block vth [256 dims][Tp keys]. Thread = (8 keys kg, 8 dims dg): an 8 x 8 transpose in registers, each
 // dim row written as two 8-byte pieces (keys kg*8 .. +3 and +4 .. +7 land 8 positions apart after the in-group
 // permutation).
-__device__ __forceinline__ void vt_tile(const __bf16* __restrict__ vrow0, size_t rstride, int key0, int nk,
-                                        __bf16* __restrict__ vth, int Tp, int tid) {
+// Tsrc float: fp32 rows (the fused projection output), rounded to bf16 here; vcache (when given): the values are also
+// written, as rows, into the cache rows crow0 + key below crows (the cache's row stride 256).
+template <typename Tsrc>
+__device__ __forceinline__ void vt_tile(const Tsrc* __restrict__ vrow0, size_t rstride, int key0, int nk,
+                                        __bf16* __restrict__ vth, int Tp, int tid, __bf16* __restrict__ vcache = nullptr,
+                                        int crow0 = 0, int crows = 0) {
   const int kg = tid >> 5, dg = tid & 31;
   u32x4 w[8];
   const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int key = key0 + 8 * kg + i;
-    const u32x4 ld = *reinterpret_cast<const u32x4*>(vrow0 + (size_t)min(key, nk - 1) * rstride + 8 * dg);
+    u32x4 ld;
+    if constexpr (std::is_same<Tsrc, float>::value) {
+      const float* src = vrow0 + (size_t)min(key, nk - 1) * rstride + 8 * dg;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(src), c = *reinterpret_cast<const f32x4*>(src + 4);
+      const bf16x8 h = {(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
+                        (__bf16)c[0], (__bf16)c[1], (__bf16)c[2], (__bf16)c[3]};
+      ld = __builtin_bit_cast(u32x4, h);
+    } else {
+      ld = *reinterpret_cast<const u32x4*>(vrow0 + (size_t)min(key, nk - 1) * rstride + 8 * dg);
+    }
     w[i] = key < nk ? ld : z;
+    if (vcache && key < nk && crow0 + key < crows)
+      *reinterpret_cast<u32x4*>(vcache + (size_t)(crow0 + key) * kPD + 8 * dg) = ld;
   }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -94,71 +111,169 @@ __device__ __forceinline__ void vt_tile(const __bf16* __restrict__ vrow0, size_t
   }
 }
 
+// The attention front end for the form that starts from the fused projection output (q35_gated_attn_prefill_proj;
+// the WGSL attnPrep, engine/kernels_qwen35.js:18-69): y [B * T, ldy] fp32 rows of [q | gate] per query head
+// (Hq 2 D), then k (Hkv D), then v (Hkv D); q and k normalised with RMS and (1 + w), then rotated. The keys and values
+// are also appended to the bf16 caches [B, Hkv, max_len, D] at rows pos0 + t; the queries go, rotated, to
+// qr [B, T, Hq, D] bf16.
+struct PfFront {
+  const float* y;
+  int64_t ldy;
+  const float* qnw;
+  const float* knw;
+  float eps;
+  __bf16* kc;
+  __bf16* vc;
+  __bf16* qr;
+  int max_len;
+};
+
 // ---------------------------------------------------------------------------------------------------------------
-// Kernel 1: one block of 256 threads per (64 keys, kv head, row) for the keys and another for the values. ROT
-// (rotary dims) is a template parameter so that the rotation pairs are compile-time register indices.
-template <int ROT>
+// Kernel 1: one block of 256 threads per (64 keys, kv head, row) for the keys and another for the values; with FP
+// (the projection-output form, PfFront) also one per (64 tokens, query head of the kv head's group, row) for the
+// queries. ROT (rotary dims) is a template parameter so that the rotation pairs are compile-time register indices.
+template <int ROT, bool FP>
 __global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restrict__ k, const __bf16* __restrict__ v,
                                                            const float* __restrict__ cos_t,
                                                            const float* __restrict__ sin_t, int pos0,
                                                            __bf16* __restrict__ kr, __bf16* __restrict__ vt, int T,
-                                                           int Tp, int Hkv) {
+                                                           int Tp, int Hkv, int Hq, PfFront fe) {
   static_assert(ROT % 16 == 0 && ROT <= kRotMax, "rotary dims");
   constexpr int half = ROT / 2;
   const int tid = threadIdx.x;
-  // blocks x < Tp / 64 prepare the keys of tile x, blocks x >= Tp / 64 the values of tile x - Tp / 64
-  const int ntile = Tp / kBN;
-  const bool doK = (int)blockIdx.x < ntile;
-  const int key0 = (doK ? blockIdx.x : blockIdx.x - ntile) * kBN, kvh = blockIdx.y, b = blockIdx.z;
+  // blocks x < Tp / 64 prepare the keys of tile x, the next Tp / 64 the values of tile x - Tp / 64, then (FP) the
+  // queries: block 2 Tp / 64 + G u + g holds tokens 64 u .. of query head kvh G + g
+  const int ntile = Tp / kBN, bx = blockIdx.x;
+  const int role = bx < ntile ? 0 : (bx < 2 * ntile ? 1 : 2);  // 0 keys, 1 values, 2 queries
+  const int kvh = blockIdx.y, b = blockIdx.z;
+  const int G = Hq / Hkv;
+  const int key0 = (role == 0 ? bx : role == 1 ? bx - ntile : (bx - 2 * ntile) / G) * kBN;
+  const int qh = role == 2 ? kvh * G + (bx - 2 * ntile) % G : 0;
   const size_t head = (size_t)b * Hkv + kvh;
-  // K: thread = (row r, lane q of 4); a row is 32 segments of 8 dims and thread q takes segments q, q + 4, ...
-  // A rotary segment (s < ROT / 8) pairs with the segment half / 8 away; its cos / sin rows are loaded as vectors.
-  // Every load of the thread is issued before any is used (one memory round trip per block).
-  if (doK) {
+  // Keys and queries: thread = (row r, lane q of 4); a row is 32 segments of 8 dims and thread q takes segments
+  // q, q + 4, ... A rotary segment (s < ROT / 8) pairs with the segment half / 8 away; its cos / sin rows are loaded
+  // as vectors. Every load of the thread is issued before any is used (one memory round trip per block).
+  if (role != 1) {
     constexpr int NSEG = kPD / 8, RS = ROT / 8, HS = half / 8;
     const int r = tid >> 2, q = tid & 3;
     const int key = key0 + r;
     const bool valid = key < T;
-    const __bf16* src = k + (((size_t)b * T + min(key, T - 1)) * Hkv + kvh) * kPD;
+    const size_t trow = (size_t)b * T + min(key, T - 1);
     u32x4 w[NSEG / 4], pw[NSEG / 4];
     f32x4 cs[NSEG / 4][2], sn[NSEG / 4][2];
+    // FP: the row in fp32 (and its rotation partners), the norm weights of the thread's segments
+    f32x4 xf[NSEG / 4][2], pxf[NSEG / 4][2], wf[NSEG / 4][2], pwf[NSEG / 4][2];
+    const __bf16* src = k + (trow * Hkv + kvh) * kPD;
+    const float* ysrc = nullptr;
+    const float* nw = nullptr;
+    if constexpr (FP) {
+      ysrc = fe.y + trow * fe.ldy + (role == 2 ? (size_t)qh * 2 * kPD : (size_t)Hq * 2 * kPD + (size_t)kvh * kPD);
+      nw = role == 2 ? fe.qnw : fe.knw;
+    }
 #pragma unroll
     for (int i = 0; i < NSEG / 4; ++i) {
       const int sg = q + 4 * i;
-      w[i] = *reinterpret_cast<const u32x4*>(src + 8 * sg);
+      if constexpr (FP) {
+        xf[i][0] = *reinterpret_cast<const f32x4*>(ysrc + 8 * sg);
+        xf[i][1] = *reinterpret_cast<const f32x4*>(ysrc + 8 * sg + 4);
+        wf[i][0] = *reinterpret_cast<const f32x4*>(nw + 8 * sg);
+        wf[i][1] = *reinterpret_cast<const f32x4*>(nw + 8 * sg + 4);
+      } else {
+        w[i] = *reinterpret_cast<const u32x4*>(src + 8 * sg);
+      }
       if (4 * i < RS) {  // segments 4 i .. 4 i + 3 may be rotary (compile-time bound)
         const int ps = sg < HS ? sg + HS : sg - HS;
         const int j0 = 8 * (sg < HS ? sg : sg - HS);
         const size_t crow = (size_t)(pos0 + min(key, T - 1)) * half + (sg < RS ? j0 : 0);
-        pw[i] = *reinterpret_cast<const u32x4*>(src + 8 * (sg < RS ? ps : sg));
+        if constexpr (FP) {
+          const int pss = sg < RS ? ps : sg;
+          pxf[i][0] = *reinterpret_cast<const f32x4*>(ysrc + 8 * pss);
+          pxf[i][1] = *reinterpret_cast<const f32x4*>(ysrc + 8 * pss + 4);
+          pwf[i][0] = *reinterpret_cast<const f32x4*>(nw + 8 * pss);
+          pwf[i][1] = *reinterpret_cast<const f32x4*>(nw + 8 * pss + 4);
+        } else {
+          pw[i] = *reinterpret_cast<const u32x4*>(src + 8 * (sg < RS ? ps : sg));
+        }
         cs[i][0] = *reinterpret_cast<const f32x4*>(cos_t + crow);
         cs[i][1] = *reinterpret_cast<const f32x4*>(cos_t + crow + 4);
         sn[i][0] = *reinterpret_cast<const f32x4*>(sin_t + crow);
         sn[i][1] = *reinterpret_cast<const f32x4*>(sin_t + crow + 4);
       }
     }
+    float rr = 1.f;
+    if constexpr (FP) {
+      // RMS over the row's 256 dims, summed in the order of the one-wave-per-head front end (q35_attn_prep: lane l
+      // sums dims 4 l .. 4 l + 3, then a butterfly over lane bits 5 .. 0), so that the cache rows match its bitwise.
+      // Here that lane is (i, q, h) = bits 5-3, 2-1, 0: the i levels are local, the q levels the row's 4 threads.
+      float s3[2];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        float p[NSEG / 4];
+#pragma unroll
+        for (int i = 0; i < NSEG / 4; ++i) {
+          const f32x4 x = xf[i][h2];
+          p[i] = x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+        }
+        const float s1[4] = {p[0] + p[4], p[1] + p[5], p[2] + p[6], p[3] + p[7]};
+        const float s2[2] = {s1[0] + s1[2], s1[1] + s1[3]};
+        s3[h2] = s2[0] + s2[1];
+        s3[h2] += __shfl_xor(s3[h2], 2, 64);
+        s3[h2] += __shfl_xor(s3[h2], 1, 64);
+      }
+      rr = rsqrtf((s3[0] + s3[1]) * (1.f / kPD) + fe.eps);
+    }
     const u32x4 z = {0u, 0u, 0u, 0u};
-    __bf16* dst = kr + (head * Tp + key) * kPD;
+    // keys: every row of the tile (zero past T); queries: the valid rows
+    __bf16* dst = role == 2 ? (valid ? fe.qr + (trow * Hq + qh) * kPD : nullptr) : kr + (head * Tp + key) * kPD;
+    __bf16* cdst = nullptr;
+    if constexpr (FP)
+      if (role == 0 && valid && pos0 + key < fe.max_len) cdst = fe.kc + (head * fe.max_len + pos0 + key) * kPD;
 #pragma unroll
     for (int i = 0; i < NSEG / 4; ++i) {
       const int sg = q + 4 * i;
-      u32x4 o = w[i];
+      // the segment's 8 values (and, rotary, the partner's), fp32
+      float xv[8], yv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (FP) {
+          xv[e] = xf[i][e >> 2][e & 3] * rr * (1.f + wf[i][e >> 2][e & 3]);
+          yv[e] = (4 * i < RS) ? pxf[i][e >> 2][e & 3] * rr * (1.f + pwf[i][e >> 2][e & 3]) : 0.f;
+        } else {
+          const uint32_t xw = w[i][e >> 1];
+          xv[e] = (e & 1) ? bf16hi(xw) : bf16lo(xw);
+          if (4 * i < RS) {
+            const uint32_t pwv = pw[i][e >> 1];
+            yv[e] = (e & 1) ? bf16hi(pwv) : bf16lo(pwv);
+          } else {
+            yv[e] = 0.f;
+          }
+        }
+      }
+      u32x4 o;
       if (4 * i < RS && sg < RS) {
         const float sgn = sg < HS ? -1.f : 1.f;
         bf16x8 o8;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t xw = w[i][e >> 1], pwv = pw[i][e >> 1];
-          const float x = (e & 1) ? bf16hi(xw) : bf16lo(xw), y = (e & 1) ? bf16hi(pwv) : bf16lo(pwv);
-          o8[e] = (__bf16)(x * cs[i][e >> 2][e & 3] + sgn * y * sn[i][e >> 2][e & 3]);
-        }
+        for (int e = 0; e < 8; ++e) o8[e] = (__bf16)(xv[e] * cs[i][e >> 2][e & 3] + sgn * yv[e] * sn[i][e >> 2][e & 3]);
         o = __builtin_bit_cast(u32x4, o8);
+      } else if constexpr (FP) {
+        bf16x8 o8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o8[e] = (__bf16)xv[e];
+        o = __builtin_bit_cast(u32x4, o8);
+      } else {
+        o = w[i];
       }
-      *reinterpret_cast<u32x4*>(dst + 8 * sg) = valid ? o : z;
+      if (dst) *reinterpret_cast<u32x4*>(dst + 8 * sg) = valid ? o : z;
+      if (cdst) *reinterpret_cast<u32x4*>(cdst + 8 * sg) = o;
     }
-  }
-  else {
-    vt_tile(v + ((size_t)b * T * Hkv + kvh) * kPD, (size_t)Hkv * kPD, key0, T, vt + head * kPD * Tp, Tp, tid);
+  } else {
+    if constexpr (FP) {
+      vt_tile(fe.y + (size_t)b * T * fe.ldy + (size_t)Hq * 2 * kPD + (size_t)(Hkv + kvh) * kPD, (size_t)fe.ldy, key0,
+              T, vt + head * kPD * Tp, Tp, tid, fe.vc + head * fe.max_len * kPD, pos0, fe.max_len);
+    } else {
+      vt_tile(v + ((size_t)b * T * Hkv + kvh) * kPD, (size_t)Hkv * kPD, key0, T, vt + head * kPD * Tp, Tp, tid);
+    }
   }
 }
 
@@ -245,14 +360,16 @@ inline int pf_items(int nqb, int Ls, bool paired) {
   return paired ? nsq + (nsq > qs ? nsq : qs) : 2 * nsq + qs;
 }
 
-template <int GW, bool PAIRED>
+// GF: the gate is read from the fused projection output (fp32 rows of stride gate_ld, query head h at 2 D h) instead
+// of a [B, T, Hq, D] bf16 tensor.
+template <int GW, bool PAIRED, bool GF>
 __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     const __bf16* __restrict__ q, const __bf16* __restrict__ kr, const __bf16* __restrict__ vt,
-    const __bf16* __restrict__ gate, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int pos0,
-    __bf16* __restrict__ out, int T, int Tp, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb, int B,
-    int Ls, float* __restrict__ part, const int32_t* __restrict__ pos_dev) {
-  Q35_ARGS_UPFRONT(q, kr, vt, gate, cos_t, sin_t, pos0, out, T, Tp, Hq, Hkv, ngroups, rot, scale, nqb, B, Ls, part,
-                   pos_dev);
+    const void* __restrict__ gate, int64_t gate_ld, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    int pos0, __bf16* __restrict__ out, int T, int Tp, int Hq, int Hkv, int ngroups, int rot, float scale, int nqb,
+    int B, int Ls, float* __restrict__ part, const int32_t* __restrict__ pos_dev) {
+  Q35_ARGS_UPFRONT(q, kr, vt, gate, gate_ld, cos_t, sin_t, pos0, out, T, Tp, Hq, Hkv, ngroups, rot, scale, nqb, B, Ls,
+                   part, pos_dev);
   __shared__ PfStage stage[2];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -576,12 +693,21 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
     {
       const int rs = lane >> 4, g16 = lane & 15;  // row 4 i + rs, dims 16 g16 .. + 15
       u32x4 gr[8][2];
+      f32x4 gf[8][4];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int tr = min(q0 + 4 * i + rs, T - 1);
-        const __bf16* gp = gate + ((size_t)b * T + tr) * (size_t)Hq * kPD + (size_t)h * kPD + 16 * g16;
-        gr[i][0] = *reinterpret_cast<const u32x4*>(gp);
-        gr[i][1] = *reinterpret_cast<const u32x4*>(gp + 8);
+        if constexpr (GF) {
+          const float* gp = static_cast<const float*>(gate) + ((size_t)b * T + tr) * gate_ld + (size_t)h * 2 * kPD +
+                            16 * g16;
+#pragma unroll
+          for (int c = 0; c < 4; ++c) gf[i][c] = *reinterpret_cast<const f32x4*>(gp + 4 * c);
+        } else {
+          const __bf16* gp = static_cast<const __bf16*>(gate) + ((size_t)b * T + tr) * (size_t)Hq * kPD +
+                             (size_t)h * kPD + 16 * g16;
+          gr[i][0] = *reinterpret_cast<const u32x4*>(gp);
+          gr[i][1] = *reinterpret_cast<const u32x4*>(gp + 8);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -596,9 +722,17 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
         u32x4 ov[2];
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
-          const u32x4 gw = gr[i][hf];
-          const float gv[8] = {bf16lo(gw[0]), bf16hi(gw[0]), bf16lo(gw[1]), bf16hi(gw[1]),
-                               bf16lo(gw[2]), bf16hi(gw[2]), bf16lo(gw[3]), bf16hi(gw[3])};
+          float gv[8];
+          if constexpr (GF) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) gv[e] = gf[i][2 * hf + (e >> 2)][e & 3];
+          } else {
+            const u32x4 gw = gr[i][hf];
+            const float gb[8] = {bf16lo(gw[0]), bf16hi(gw[0]), bf16lo(gw[1]), bf16hi(gw[1]),
+                                 bf16lo(gw[2]), bf16hi(gw[2]), bf16lo(gw[3]), bf16hi(gw[3])};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) gv[e] = gb[e];
+          }
           bf16x8 pk;
 #pragma unroll
           for (int e = 0; e < 8; ++e) pk[e] = (__bf16)(x[8 * hf + e] * sigmoidf_(gv[e]));
@@ -628,12 +762,13 @@ __global__ __launch_bounds__(64 * GW, 1) void attn_prefill_kernel(
 // likewise (the result does not depend on which half ran first), then normalised, gated and stored as the main
 // kernel's epilogue does. Neither half has a fully masked query: the second half starts at key 64 Ls and every
 // query of a split block is at or past it.
-template <int GW>
+// GF: the gate from the fused projection output, as in attn_prefill_kernel.
+template <int GW, bool GF>
 __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __restrict__ part,
-                                                                 const __bf16* __restrict__ gate,
+                                                                 const void* __restrict__ gate, int64_t gate_ld,
                                                                  __bf16* __restrict__ out, int T, int Hq, int Hkv,
                                                                  int ngroups, int B, int Ls) {
-  Q35_ARGS_UPFRONT(part, gate, out, T, Hq, Hkv, ngroups, B, Ls);
+  Q35_ARGS_UPFRONT(part, gate, gate_ld, out, T, Hq, Hkv, ngroups, B, Ls);
   const int pair = blockIdx.x, wave = blockIdx.y, tid = threadIdx.x;
   const int n_other = B * Hkv * ngroups;
   const int qb = 2 * Ls + pair / n_other, rem = pair % n_other;
@@ -641,7 +776,7 @@ __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __
   const int h = kvh * (Hq / Hkv) + hg * GW + wave;
   const float* p0 = part + ((size_t)(2 * pair) * GW + wave) * kPartFloats;
   const float* p1 = part + ((size_t)(2 * pair + 1) * GW + wave) * kPartFloats;
-  f32x4 w0[8], w1[8];
+  f32x4 w0[8], w1[8], gf[8];
   u32x2 gr[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -650,7 +785,12 @@ __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __
     const int d = 8 * mtc + 4 * (l >> 5);  // 32 mt + 8 c + 4 hh with mtc = 4 mt + c
     w0[j] = *reinterpret_cast<const f32x4*>(p0 + (size_t)e * 4);
     w1[j] = *reinterpret_cast<const f32x4*>(p1 + (size_t)e * 4);
-    gr[j] = *reinterpret_cast<const u32x2*>(gate + ((size_t)b * T + tq) * (size_t)Hq * kPD + (size_t)h * kPD + d);
+    if constexpr (GF)
+      gf[j] = *reinterpret_cast<const f32x4*>(static_cast<const float*>(gate) + ((size_t)b * T + tq) * gate_ld +
+                                              (size_t)h * 2 * kPD + d);
+    else
+      gr[j] = *reinterpret_cast<const u32x2*>(static_cast<const __bf16*>(gate) + ((size_t)b * T + tq) * (size_t)Hq * kPD +
+                                              (size_t)h * kPD + d);
   }
   // every chunk of thread t has lane l = t & 63 (256 j is a multiple of 64)
   const int l = tid & 63;
@@ -666,7 +806,16 @@ __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __
   for (int j = 0; j < 8; ++j) {
     const int e = tid + 256 * j, mtc = e >> 6;
     const int d = 8 * mtc + 4 * (l >> 5);
-    const float gv[4] = {bf16lo(gr[j][0]), bf16hi(gr[j][0]), bf16lo(gr[j][1]), bf16hi(gr[j][1])};
+    float gv[4];
+    if constexpr (GF) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) gv[q] = gf[j][q];
+    } else {
+      gv[0] = bf16lo(gr[j][0]);
+      gv[1] = bf16hi(gr[j][0]);
+      gv[2] = bf16lo(gr[j][1]);
+      gv[3] = bf16hi(gr[j][1]);
+    }
     bf16x4 ov;
 #pragma unroll
     for (int q = 0; q < 4; ++q) ov[q] = (__bf16)(fmaf(w0[j][q], c0, w1[j][q] * c1) * inv * sigmoidf_(gv[q]));
@@ -689,13 +838,13 @@ static int device_cus() {
   return n;
 }
 
-// Workspace: K rotated and V transposed ([B, Hkv, Tp, D] bf16 each), then the split blocks' partials
-// ([pairs][2 halves][wave] x kPartFloats fp32).
+// Workspace: K rotated and V transposed ([B, Hkv, Tp, D] bf16 each), for the projection-output form the rotated
+// queries ([B, T, Hq, D] bf16), then the split blocks' partials ([pairs][2 halves][wave] x kPartFloats fp32).
 struct PfLayout {
-  size_t part_off, total;
+  size_t q_off, part_off, total;
   int64_t npairs;
 };
-static PfLayout pf_layout(int64_t B, int64_t T, int64_t Hq, int64_t Hkv) {
+static PfLayout pf_layout(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, bool fp) {
   const int64_t Tp = padded_T(T);
   const int64_t G = Hq / Hkv;
   const int64_t GW = G > 4 ? 4 : G;
@@ -704,58 +853,60 @@ static PfLayout pf_layout(int64_t B, int64_t T, int64_t Hq, int64_t Hkv) {
   const int64_t nsq = Ls ? nqb - 2 * Ls : 0;
   PfLayout l;
   l.npairs = nsq * B * Hkv * (G / GW);
-  l.part_off = (size_t)2 * B * Hkv * Tp * kPD * sizeof(__bf16);
+  l.q_off = (size_t)2 * B * Hkv * Tp * kPD * sizeof(__bf16);
+  l.part_off = l.q_off + (fp ? ((size_t)B * T * Hq * kPD * sizeof(__bf16) + 255) / 256 * 256 : 0);
   l.total = (l.part_off + (size_t)2 * l.npairs * GW * kPartFloats * sizeof(float) + 255) / 256 * 256;
   return l;
 }
 
-}  // namespace q35
-
-extern "C" size_t q35_gated_attn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D) {
-  using namespace q35;
-  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D != kPD) return 0;
-  const int64_t G = Hq / Hkv;
-  if (G != 1 && G != 2 && G != 4 && G != 8) return 0;
-  if (T > ((int64_t)1 << 30) || B * Hq > ((int64_t)1 << 30)) return 0;
-  return pf_layout(B, T, Hq, Hkv).total;
-}
-
-extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const void* gate,
-                                      const float* cos, const float* sin, int64_t pos0, void* out, int64_t B,
-                                      int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t rot, float scale,
-                                      void* workspace, size_t workspace_bytes, q35_stream_t stream) {
-  using namespace q35;
-  if (!q || !k || !v || !gate || !out) return Q35_EINVAL;
-  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D || pos0 < 0)
-    return Q35_EINVAL;
-  if (rot > 0 && (!cos || !sin)) return Q35_EINVAL;
+// Size limits shared by both forms of the own-keys prefill (Q35_OK, or the status to return).
+static int pf_check(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t rot) {
+  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D) return Q35_EINVAL;
   if (D != kPD || (rot % 16) != 0 || rot > kRotMax) return Q35_EUNSUPPORTED;
   const int64_t G = Hq / Hkv;
   if (G != 1 && G != 2 && G != 4 && G != 8) return Q35_EUNSUPPORTED;
+  if (T > ((int64_t)1 << 30) || B > 65535 || Hkv > 65535 || T * Hq * D > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
+  // V^T rows are addressed with 32-bit byte offsets inside a head's [D, Tp] block
+  if (padded_T(T) * kPD * 2 >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
+  // the pre-pass grid: (2 + G) tiles of 64 per kv head in x
+  if ((2 + G) * (padded_T(T) / kBN) > 0x7fffffff) return Q35_EUNSUPPORTED;
+  return Q35_OK;
+}
+
+// The own-keys prefill (validated arguments): the pre-pass, the main kernel and, for split blocks, the merge.
+// FP: q, k and v come from the projection output (fe); gate then points at y + D with row stride gate_ld.
+template <bool FP>
+static int pf_launch(const void* q, const void* k, const void* v, const void* gate, int64_t gate_ld, const PfFront& fe0,
+                     const float* cos, const float* sin, int64_t pos0, void* out, int64_t B, int64_t T, int64_t Hq,
+                     int64_t Hkv, int64_t rot, float scale, void* workspace, size_t workspace_bytes,
+                     hipStream_t st) {
+  const int64_t G = Hq / Hkv;
   const int GW = G > 4 ? 4 : (int)G;
   const int ngroups = (int)(G / GW);
   const int64_t Tp = padded_T(T);
-  if (T > ((int64_t)1 << 30) || B > 65535 || Hkv > 65535 || T * Hq * D > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
   const int64_t nqb = (T + kBQ - 1) / kBQ;
   const int Ls = pf_split_len((int)nqb);
   const int64_t n_other = B * Hkv * ngroups;
-  const bool paired = Ls > 0 && (int64_t)pf_items((int)nqb, Ls, true) * n_other <= device_cus();
-  const int64_t nblocks = (int64_t)pf_items((int)nqb, Ls, paired) * n_other;
-  if (nblocks > 0x7fffffff) return Q35_EUNSUPPORTED;
-  // V^T rows are addressed with 32-bit byte offsets inside a head's [D, Tp] block
-  if (Tp * kPD * 2 >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
-  const PfLayout lay = pf_layout(B, T, Hq, Hkv);
+  if ((int64_t)pf_items((int)nqb, Ls, false) * n_other > 0x7fffffff) return Q35_EUNSUPPORTED;
+  const PfLayout lay = pf_layout(B, T, Hq, Hkv, FP);
   if (lay.npairs > 0x7fffffff) return Q35_EUNSUPPORTED;
   if (!workspace || workspace_bytes < lay.total || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // the first HIP call: the device's compute units decide the work order
+  const bool paired = Ls > 0 && (int64_t)pf_items((int)nqb, Ls, true) * n_other <= device_cus();
+  const int64_t nblocks = (int64_t)pf_items((int)nqb, Ls, paired) * n_other;
   char* ws = static_cast<char*>(workspace);
   __bf16* kr = reinterpret_cast<__bf16*>(ws);
   __bf16* vt = kr + (size_t)B * Hkv * Tp * kPD;
   float* part = reinterpret_cast<float*>(ws + lay.part_off);
-  const dim3 gp((unsigned)(2 * (Tp / kBN)), (unsigned)Hkv, (unsigned)B);
-#define Q35_KV_LAUNCH(R)                                                                                         \
-  hipLaunchKernelGGL(attn_kv_prep_kernel<R>, gp, dim3(256), 0, st, (const __bf16*)k, (const __bf16*)v, cos, sin, \
-                     (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv)
+  PfFront fe = fe0;
+  if constexpr (FP) {
+    fe.qr = reinterpret_cast<__bf16*>(ws + lay.q_off);
+    q = fe.qr;
+  }
+  const dim3 gp((unsigned)((FP ? 2 + G : 2) * (Tp / kBN)), (unsigned)Hkv, (unsigned)B);
+#define Q35_KV_LAUNCH(R)                                                                                        \
+  hipLaunchKernelGGL((attn_kv_prep_kernel<R, FP>), gp, dim3(256), 0, st, (const __bf16*)k, (const __bf16*)v, cos, \
+                     sin, (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv, (int)Hq, fe)
   switch (rot) {
     case 0: Q35_KV_LAUNCH(0); break;
     case 16: Q35_KV_LAUNCH(16); break;
@@ -764,14 +915,16 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
     default: Q35_KV_LAUNCH(64); break;
   }
 #undef Q35_KV_LAUNCH
-#define Q35_PF_LAUNCH(GG)                                                                                         \
-  hipLaunchKernelGGL((paired ? attn_prefill_kernel<GG, true> : attn_prefill_kernel<GG, false>),                \
-                     dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q, kr, vt, (const __bf16*)gate, \
-                     cos, sin, (int)pos0, (__bf16*)out, (int)T, (int)Tp, (int)Hq, (int)Hkv, ngroups, (int)rot,     \
-                     scale, (int)nqb, (int)B, Ls, part, (const int32_t*)nullptr);                                 \
-  if (lay.npairs > 0)                                                                                             \
-    hipLaunchKernelGGL(attn_prefill_merge_kernel<GG>, dim3((unsigned)lay.npairs, GG), dim3(256), 0, st, part,       \
-                       (const __bf16*)gate, (__bf16*)out, (int)T, (int)Hq, (int)Hkv, ngroups, (int)B, Ls)
+  // the projection-output form's queries are rotated by the pre-pass: the main kernel then rotates nothing
+  const int mrot = FP ? 0 : (int)rot;
+#define Q35_PF_LAUNCH(GG)                                                                                           \
+  hipLaunchKernelGGL((paired ? attn_prefill_kernel<GG, true, FP> : attn_prefill_kernel<GG, false, FP>),            \
+                     dim3((unsigned)nblocks), dim3(64 * GG), 0, st, (const __bf16*)q, kr, vt, gate, gate_ld, cos, sin, \
+                     (int)pos0, (__bf16*)out, (int)T, (int)Tp, (int)Hq, (int)Hkv, ngroups, mrot, scale, (int)nqb,     \
+                     (int)B, Ls, part, (const int32_t*)nullptr);                                                    \
+  if (lay.npairs > 0)                                                                                               \
+    hipLaunchKernelGGL((attn_prefill_merge_kernel<GG, FP>), dim3((unsigned)lay.npairs, GG), dim3(256), 0, st, part,  \
+                       gate, gate_ld, (__bf16*)out, (int)T, (int)Hq, (int)Hkv, ngroups, (int)B, Ls)
   switch (GW) {
     case 1: Q35_PF_LAUNCH(1); break;
     case 2: Q35_PF_LAUNCH(2); break;
@@ -779,6 +932,53 @@ extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* 
   }
 #undef Q35_PF_LAUNCH
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+}  // namespace q35
+
+extern "C" size_t q35_gated_attn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D) {
+  using namespace q35;
+  if (pf_check(B, T, Hq, Hkv, D, 0) != Q35_OK) return 0;
+  return pf_layout(B, T, Hq, Hkv, false).total;
+}
+
+extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const void* gate,
+                                      const float* cos, const float* sin, int64_t pos0, void* out, int64_t B,
+                                      int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t rot, float scale,
+                                      void* workspace, size_t workspace_bytes, q35_stream_t stream) {
+  using namespace q35;
+  if (!q || !k || !v || !gate || !out) return Q35_EINVAL;
+  if (pos0 < 0 || (rot > 0 && (!cos || !sin))) return Q35_EINVAL;
+  const int chk = pf_check(B, T, Hq, Hkv, D, rot);
+  if (chk != Q35_OK) return chk;
+  return pf_launch<false>(q, k, v, gate, Hq * kPD, PfFront{}, cos, sin, pos0, out, B, T, Hq, Hkv, rot, scale,
+                          workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t q35_gated_attn_prefill_proj_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
+                                                              int64_t D) {
+  using namespace q35;
+  if (pf_check(B, T, Hq, Hkv, D, 0) != Q35_OK) return 0;
+  return pf_layout(B, T, Hq, Hkv, true).total;
+}
+
+extern "C" int q35_gated_attn_prefill_proj(const float* y, int64_t ldy, const float* q_norm_w,
+                                           const float* k_norm_w, float eps, void* k_cache, void* v_cache,
+                                           int64_t pos0, const float* cos, const float* sin, void* out, int64_t B,
+                                           int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
+                                           int64_t rot, float scale, void* workspace, size_t workspace_bytes,
+                                           q35_stream_t stream) {
+  using namespace q35;
+  if (!y || !q_norm_w || !k_norm_w || !k_cache || !v_cache || !out) return Q35_EINVAL;
+  if (pos0 < 0 || (rot > 0 && (!cos || !sin))) return Q35_EINVAL;
+  const int chk = pf_check(B, T, Hq, Hkv, D, rot);
+  if (chk != Q35_OK) return chk;
+  if (max_len <= 0 || pos0 + T > max_len || ldy < 2 * Hq * D + 2 * Hkv * D) return Q35_EINVAL;
+  if ((ldy & 3) || (((uintptr_t)y | (uintptr_t)q_norm_w | (uintptr_t)k_norm_w) & 15)) return Q35_EUNSUPPORTED;
+  if (max_len > 0x7fffffff || B * Hkv * max_len * D > ((int64_t)1 << 40)) return Q35_EUNSUPPORTED;
+  PfFront fe{y, ldy, q_norm_w, k_norm_w, eps, (__bf16*)k_cache, (__bf16*)v_cache, nullptr, (int)max_len};
+  return pf_launch<true>(nullptr, nullptr, nullptr, y + kPD, ldy, fe, cos, sin, pos0, out, B, T, Hq, Hkv, rot, scale,
+                         workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t q35_gated_attn_prefill_cached_workspace_bytes(int64_t B, int64_t Hkv, int64_t D, int64_t max_len) {
@@ -818,8 +1018,8 @@ extern "C" int q35_gated_attn_prefill_cached(const void* q, const void* k_cache,
                      0, st, (const __bf16*)v_cache, pos, vt, (int)T, (int)max_len, (int)Hkv);
   // one item per query block (no key split: the key range depends on the device positions), latest block first
 #define Q35_PFC_LAUNCH(GG)                                                                                        \
-  hipLaunchKernelGGL((attn_prefill_kernel<GG, false>), dim3((unsigned)nblocks), dim3(64 * GG), 0, st,            \
-                     (const __bf16*)q, (const __bf16*)k_cache, vt, (const __bf16*)gate, cos, sin, 0, (__bf16*)out, \
+  hipLaunchKernelGGL((attn_prefill_kernel<GG, false, false>), dim3((unsigned)nblocks), dim3(64 * GG), 0, st,     \
+                     (const __bf16*)q, (const __bf16*)k_cache, vt, gate, Hq * kPD, cos, sin, 0, (__bf16*)out,      \
                      (int)T, (int)max_len, (int)Hq, (int)Hkv, ngroups, (int)rot, scale, (int)nqb, (int)B, 0,        \
                      (float*)nullptr, pos)
   switch (GW) {

@@ -17,7 +17,7 @@ EXPORTS = [
     "q35_gated_attn_prefill_workspace_bytes", "q35_gated_attn_prefill",
     "q35_gated_attn_prefill_cached_workspace_bytes", "q35_gated_attn_prefill_cached", "q35_gated_attn_decode_workspace_bytes",
     "q35_gated_attn_decode", "q35_gated_attn_decode_noalloc_max_bytes", "q35_gated_attn_decode_noalloc",
-    "q35_gated_attn_decode_proj",
+    "q35_gated_attn_decode_proj", "q35_gated_attn_prefill_proj_workspace_bytes", "q35_gated_attn_prefill_proj",
     "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
     "q35_swiglu_push",
     "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm", "q35_gemm_q8", "q35_gemm_q8_split",
@@ -27,7 +27,7 @@ EXPORTS = [
 
 Q35_F32, Q35_BF16, Q35_I8, Q35_I8_G128 = 0, 1, 2, 3
 Q35_ESCRATCH = 5
-ABI_VERSION = 12  # the signatures below; q35_abi_version() of the loaded library must match
+ABI_VERSION = 13  # the signatures below; q35_abi_version() of the loaded library must match
 
 _lib = None
 
@@ -53,6 +53,9 @@ _SIGS = {
     "q35_gated_attn_decode": ([P, P, P, P, P, P, P, P, I32, I64, I64, I64, I64, I64, I64, F32, I64, P, SZ, P], I32),
     "q35_gated_attn_decode_proj": ([P, I64, P, P, F32, P, P, P, P, P, P, I32, I64, I64, I64, I64, I64, I64, F32, I64,
                                     P, SZ, P], I32),
+    "q35_gated_attn_prefill_proj_workspace_bytes": ([I64, I64, I64, I64, I64], SZ),
+    "q35_gated_attn_prefill_proj": ([P, I64, P, P, F32, P, P, I64, P, P, P, I64, I64, I64, I64, I64, I64, I64, F32, P,
+                                     SZ, P], I32),
     "q35_gated_attn_decode_noalloc_max_bytes": ([], SZ),
     "q35_gated_attn_decode_noalloc": ([P, P, P, P, P, P, P, P, I32, I64, I64, I64, I64, I64, I64, F32, I64, P], I32),
     "q35_resid_add_rows": ([P, P, P, I64, I64, I64, I64, I32, P], I32),

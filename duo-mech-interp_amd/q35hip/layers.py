@@ -216,11 +216,12 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     pos a Python int or a [B] int32 device tensor (per row; a device tensor keeps the call capturable in a HIP
     graph). Their rotated keys and values are written into the caches at those positions, and token t attends to
     cache positions 0..pos+t (engine/kernels_qwen35.js:90). T > 1 at the int position 0 runs the flash prefill over
-    the call's own tokens; T > 1 at any other position (or a device pos) the same kernel over the cache (the caches'
-    max_len must then be a multiple of 64); T == 1 the split-K decode over cache positions 0..pos (cache_len:
-    optional [B] int32 per-row lengths, default pos + 1; without it the q / k norms, RoPE and the cache append run
-    inside the decode kernels, q35_gated_attn_decode_proj, instead of a front-end launch). prenorm: see linear(). For T > 1, x may be the int32 words
-    of split activations (see gated_deltanet_layer). Returns y [B, T, H], or with residual [B, T, H] given,
+    the call's own tokens (for an fp32 y with the front end in its pre-pass, q35_gated_attn_prefill_proj); T > 1 at
+    any other position (or a device pos) the same kernel over the cache (the caches' max_len must then be a multiple
+    of 64); T == 1 the split-K decode over cache positions 0..pos (cache_len: optional [B] int32 per-row lengths,
+    default pos + 1; without it the q / k norms, RoPE and the cache append run inside the decode kernels,
+    q35_gated_attn_decode_proj, instead of a front-end launch). prenorm: see linear(). For T > 1, x may be the int32
+    words of split activations (see gated_deltanet_layer). Returns y [B, T, H], or with residual [B, T, H] given,
     residual + y computed in place by o_proj (then returned). fixed_order: see linear()."""
     B, T, _ = x.shape
     D = p["q_norm"].numel()
@@ -245,6 +246,13 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
                                             out_dtype=torch.float32).view(B, 1, Hq * D)
         wq_o, ws_o = _q8(p, "o_proj")
         return linear(o, p["o_proj"], wq_o, ws_o, residual=residual, fixed_order=fixed_order)
+    if T > 1 and own_keys and y.dtype == torch.float32 and y.shape[-1] % 4 == 0:
+        # the call's own tokens: the front end runs in the prefill's pre-pass, reading y (q35_gated_attn_prefill_proj)
+        o = ops.gated_attention_prefill_proj(y, p["q_norm"], p["k_norm"], k_cache, v_cache, cos, sin, num_heads=Hq,
+                                             pos0=0, eps=eps, scale=1.0 / math.sqrt(D))
+        wq_o, ws_o = _q8(p, "o_proj")
+        xo = o if (wq_o is not None and o.shape[-1] % 64 == 0) else o.float()
+        return linear(xo, p["o_proj"], wq_o, ws_o, residual=residual, fixed_order=fixed_order)
     q, gate, k, v = ops.attn_prep(y, p["q_norm"], p["k_norm"], cos, sin, pos_t, k_cache, v_cache, num_heads=Hq,
                                   num_kv_heads=Hkv, eps=eps, want_kv=T > 1 and own_keys)
     if T > 1 and own_keys:

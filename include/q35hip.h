@@ -20,6 +20,9 @@
  *   q35_gated_attn_decode_proj  the decode step from the fused projection output: engine/kernels_qwen35.js:18-69
  *                            `attnPrep` (q / k RMSNorm, RoPE, cache append) and :73-123 `attention` for T = 1
  *                            in one call (HF:667-701 for one cached token)
+ *   q35_gated_attn_prefill_proj  the multi-token attention of a call's own tokens from the fused projection
+ *                            output: engine/kernels_qwen35.js:18-69 `attnPrep` and :73-123 `attention` in one call
+ *                            (HF:667-701 at positions pos0 .. pos0 + T - 1)
  *   q35_resid_add_rows       tests/engine_ref.py:49-53 residual vector hook; engine/kernels.js:190-203 `resAdd`
  *   q35_gdn_conv             HF:454-499 (causal_conv1d_fn / causal_conv1d_update + SiLU, split, beta, g);
  *                            engine/kernels_qwen35.js:127-178 `conv` + `convState`, :226-229 (gate terms of `delta`)
@@ -197,6 +200,26 @@ int q35_gated_attn_decode_proj(const float* y, int64_t ldy, const float* q_norm_
                                void* out, int out_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                                int64_t max_len, int64_t rot, float scale, int64_t splits, void* workspace,
                                size_t workspace_bytes, q35_stream_t stream);
+
+/*
+ * Gated causal GQA attention of the call's own T tokens per row from their fused projection output
+ * (engine/kernels_qwen35.js:18-69 `attnPrep` followed by :73-123 `attention`; HF:667-701 for a prompt at positions
+ * pos0 .. pos0 + T - 1 with nothing cached before pos0 attended to): y holds B * T rows (row b T + t, stride ldy) of
+ * fp32 [q | gate] per query head (Hq * 2D), then k (Hkv * D), then v (Hkv * D) from column 0. q and k are normalised
+ * with (1 + q_norm_w / k_norm_w) (RMS, eps) and rotated at position pos0 + t; token t attends to the call's tokens
+ * 0 .. t. The rotated keys and the values are written into k_cache / v_cache [B, Hkv, max_len, D] bf16 at rows
+ * pos0 + t (pos0 + T <= max_len), bitwise the rows q35_attn_prep writes. out = attention * sigmoid(gate),
+ * [B, T, Hq * D] bf16. Limits as q35_gated_attn_prefill (D 256, Hq / Hkv in 1, 2, 4, 8, rot a multiple of 16, at
+ * most 64); y, ldy and the norm weights 16-byte aligned; cos, sin [P, rot / 2] fp32 with P >= pos0 + T. Needs
+ * q35_gated_attn_prefill_proj_workspace_bytes(B, T, Hq, Hkv, D) bytes of workspace (256-byte aligned); calls that
+ * share one workspace must not overlap.
+ */
+size_t q35_gated_attn_prefill_proj_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D);
+int q35_gated_attn_prefill_proj(const float* y, int64_t ldy, const float* q_norm_w, const float* k_norm_w, float eps,
+                                void* k_cache, void* v_cache, int64_t pos0, const float* cos, const float* sin,
+                                void* out, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
+                                int64_t rot, float scale, void* workspace, size_t workspace_bytes,
+                                q35_stream_t stream);
 
 /*
  * q35_gated_attn_decode without a workspace argument, for callers that cannot allocate device memory (code under HIP

@@ -39,7 +39,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 12
+    assert L.q35_abi_version() == 13
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -236,6 +236,43 @@ def test_decode_from_projection_rejects_without_launching():
         q35hip.ops.gated_attention_decode_proj(y, torch.zeros(256), torch.zeros(256), kc, kc.clone(),
                                                torch.zeros(1, dtype=torch.int32), torch.zeros(64, 32),
                                                torch.zeros(64, 32), num_heads=8)
+
+
+def test_prefill_from_projection_rejects_without_launching():
+    """q35_gated_attn_prefill_proj refuses bad arguments before any HIP call (Hq 8, Hkv 2, D 256, T 130 tokens at
+    pos0 0 into a 192-row cache: y rows of 5120 floats); its workspace is the own-keys prefill's plus the rotated
+    queries, and its torch op has no CPU path."""
+    L = q35hip.lib()
+    fake = 0x1000
+    W = 8 * 2 * 256 + 2 * 2 * 256
+
+    def call(y=fake, ldy=W, qnw=fake, knw=fake, pos0=0, T=130, Hq=8, Hkv=2, D=256, max_len=192, rot=64,
+             ws_bytes=1 << 24):
+        return L.q35_gated_attn_prefill_proj(y, ldy, qnw, knw, 1e-6, fake, fake, pos0, fake, fake, fake, 1, T, Hq, Hkv,
+                                             D, max_len, rot, 0.0625, fake, ws_bytes, None)
+    assert call(y=None) == 1                 # null y
+    assert call(knw=None) == 1               # null norm weight
+    assert call(ldy=W - 4) == 1              # rows too short for [q | gate] x Hq, k, v
+    assert call(pos0=63) == 1                # positions 63 .. 192 run past the cache
+    assert call(pos0=-1) == 1
+    assert call(T=0) == 1
+    assert call(y=fake + 4) == 2             # y not 16-byte aligned
+    assert call(ldy=W + 2) == 2              # row stride not a multiple of 4 floats
+    assert call(Hq=6) == 2                   # 3 query heads per kv head
+    assert call(D=128, ldy=8 * 256 + 4 * 128) == 2  # head dim other than 256
+    assert call(rot=24) == 2                 # rotary dims not a multiple of 16
+    assert call(ws_bytes=8) == 3             # workspace too small
+    # 2 x [1, 2, 192, 256] bf16 (keys, values^T), then [1, 130, 8, 256] bf16 rotated queries; no split blocks
+    plain = L.q35_gated_attn_prefill_workspace_bytes(1, 130, 8, 2, 256)
+    assert plain == 2 * 2 * 192 * 256 * 2
+    assert L.q35_gated_attn_prefill_proj_workspace_bytes(1, 130, 8, 2, 256) == plain + 130 * 8 * 256 * 2
+    assert L.q35_gated_attn_prefill_proj_workspace_bytes(1, 130, 6, 2, 256) == 0
+    assert call(ws_bytes=plain + 130 * 8 * 256 * 2 - 256) == 3
+    y = torch.zeros(1, 4, W)
+    kc = torch.zeros(1, 2, 64, 256, dtype=torch.bfloat16)
+    with pytest.raises(Exception, match="no CPU|HIP device"):
+        q35hip.ops.gated_attention_prefill_proj(y, torch.zeros(256), torch.zeros(256), kc, kc.clone(),
+                                                torch.zeros(64, 32), torch.zeros(64, 32), num_heads=8)
 
 
 def test_split_activation_layout():

@@ -195,6 +195,42 @@ def test_attn_decode_from_projection(Hq, Hkv, splits):
     assert o32.dtype == torch.float32 and torch.equal(o32.to(torch.bfloat16).cpu(), out.cpu())
 
 
+# B 2 T 130 (a ragged last key tile), pos0 5 and 3 (cache rows on both sides of the call's), T 1000 (split query
+# blocks: the merge kernel reads the gate from y as well), GQA 8 (two head groups per kv head), GQA 1, one token.
+@pytest.mark.parametrize("B,T,Hq,Hkv,pos0,max_len", [(2, 130, 8, 2, 0, 192), (1, 70, 8, 2, 5, 128),
+                                                     (1, 1000, 8, 2, 0, 1024), (1, 300, 16, 2, 0, 320),
+                                                     (1, 96, 4, 4, 3, 128), (1, 1, 8, 2, 0, 64)])
+def test_attn_prefill_from_projection(B, T, Hq, Hkv, pos0, max_len):
+    """The own-keys prefill from the fused projection output (q35_gated_attn_prefill_proj: q / k norms, RoPE and the
+    cache append in the pre-pass, the gate read from y) against the oracle's front end + causal attention, and
+    against the two-launch path (q35_attn_prep, then q35_gated_attn_prefill) on the same inputs, whose caches it must
+    leave bitwise equal (rows outside pos0 .. pos0 + T - 1 untouched)."""
+    dev = device()
+    g = torch.Generator().manual_seed(90 + T + Hq)
+    D = 256
+    y = torch.randn(B, T, Hq * 2 * D + 2 * Hkv * D, generator=g)
+    qw, kw = 0.1 * torch.randn(D, generator=g), 0.1 * torch.randn(D, generator=g)
+    cos, sin = rope_tables(max_len, rope_inv_freq(D, 0.25, 1e7))
+    pos = torch.full((B,), pos0, dtype=torch.int32)
+    q, gate, k, v, _ = of.attn_prep(y, qw, kw, cos, sin, pos, Hq, Hkv, D)
+    ref = oracle.gated_attention(q, k, v, gate, cos, sin, pos0=pos0)
+    kc0 = torch.randn(B, Hkv, max_len, D, generator=g).to(torch.bfloat16)
+    vc0 = torch.randn(B, Hkv, max_len, D, generator=g).to(torch.bfloat16)
+    announce(f"attn prefill from projection B{B} T{T} Hq{Hq} Hkv{Hkv} pos0 {pos0}")
+    yd, qwd, kwd, posd = y.to(dev), qw.to(dev), kw.to(dev), pos.to(dev)
+    cosd, sind = cos.to(dev), sin.to(dev)
+    kcb, vcb = kc0.to(dev), vc0.to(dev)
+    out = ops.gated_attention_prefill_proj(yd, qwd, kwd, kcb, vcb, cosd, sind, num_heads=Hq, pos0=pos0)
+    kca, vca = kc0.to(dev), vc0.to(dev)
+    qa, ga, ka, va = ops.attn_prep(yd, qwd, kwd, cosd, sind, posd, kca, vca, num_heads=Hq, num_kv_heads=Hkv)
+    two = q35hip.gated_attention_prefill(qa, ka, va, ga, cosd, sind, pos0=pos0)
+    torch.cuda.synchronize()
+    assert torch.equal(kcb.cpu(), kca.cpu()) and torch.equal(vcb.cpu(), vca.cpu())
+    e_ref, e_two = oracle.rel_err(out.float().cpu(), ref), oracle.rel_err(out.float().cpu(), two.float().cpu())
+    print(f"prefill from projection: rel err {e_ref:.3e} (oracle), {e_two:.3e} (two-launch path)")
+    assert out.shape == (B, T, Hq * D) and e_ref <= 2e-2 and e_two <= 1e-2
+
+
 @pytest.mark.parametrize("with_add", [False, True])
 def test_add_rmsnorm_matches_oracle(with_add):
     """Residual add + RMSNorm(1 + w) (HF:720-734): x updated in place, h returned."""
