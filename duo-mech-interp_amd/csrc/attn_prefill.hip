@@ -66,30 +66,37 @@ __device__ __forceinline__ int vperm(int p) { return (p & 3) | ((p & 4) << 1) | 
 // head's V^T block vth [256 dims][Tp keys]. Thread = (8 keys kg, 8 dims dg): an 8 x 8 transpose in registers, each
 // dim row written as two 8-byte pieces (keys kg*8 .. +3 and +4 .. +7 land 8 positions apart after the in-group
 // permutation).
-// Tsrc float: fp32 rows (the fused projection output), rounded to bf16 here; vcache (when given): the values are also
-// written, as rows, into the cache rows crow0 + key below crows (the cache's row stride 256).
+// Tsrc float: fp32 rows (the fused projection output), rounded to bf16 here; then keys below nold come from the bf16
+// rows cold + key * 256 (a KV cache's earlier rows) and key >= nold from row key - nold of vrow0; vcache (when
+// given): the values of keys >= nold are also written, as rows, into the cache rows crow0 + key below crows (the
+// cache's row stride 256).
 template <typename Tsrc>
 __device__ __forceinline__ void vt_tile(const Tsrc* __restrict__ vrow0, size_t rstride, int key0, int nk,
-                                        __bf16* __restrict__ vth, int Tp, int tid, __bf16* __restrict__ vcache = nullptr,
-                                        int crow0 = 0, int crows = 0) {
+                                        __bf16* __restrict__ vth, int Tp, int tid, __bf16* vcache = nullptr,
+                                        int crow0 = 0, int crows = 0, const __bf16* cold = nullptr, int nold = 0) {
   const int kg = tid >> 5, dg = tid & 31;
   u32x4 w[8];
   const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int key = key0 + 8 * kg + i;
+    const int kc = min(key, nk - 1);
     u32x4 ld;
     if constexpr (std::is_same<Tsrc, float>::value) {
-      const float* src = vrow0 + (size_t)min(key, nk - 1) * rstride + 8 * dg;
-      const f32x4 a = *reinterpret_cast<const f32x4*>(src), c = *reinterpret_cast<const f32x4*>(src + 4);
-      const bf16x8 h = {(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
-                        (__bf16)c[0], (__bf16)c[1], (__bf16)c[2], (__bf16)c[3]};
-      ld = __builtin_bit_cast(u32x4, h);
+      if (kc < nold) {
+        ld = *reinterpret_cast<const u32x4*>(cold + (size_t)kc * kPD + 8 * dg);
+      } else {
+        const float* src = vrow0 + (size_t)(kc - nold) * rstride + 8 * dg;
+        const f32x4 a = *reinterpret_cast<const f32x4*>(src), c = *reinterpret_cast<const f32x4*>(src + 4);
+        const bf16x8 h = {(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
+                          (__bf16)c[0], (__bf16)c[1], (__bf16)c[2], (__bf16)c[3]};
+        ld = __builtin_bit_cast(u32x4, h);
+      }
     } else {
-      ld = *reinterpret_cast<const u32x4*>(vrow0 + (size_t)min(key, nk - 1) * rstride + 8 * dg);
+      ld = *reinterpret_cast<const u32x4*>(vrow0 + (size_t)kc * rstride + 8 * dg);
     }
     w[i] = key < nk ? ld : z;
-    if (vcache && key < nk && crow0 + key < crows)
+    if (vcache && key < nk && key >= nold && crow0 + key < crows)
       *reinterpret_cast<u32x4*>(vcache + (size_t)(crow0 + key) * kPD + 8 * dg) = ld;
   }
 #pragma unroll
@@ -132,24 +139,31 @@ struct PfFront {
 // Kernel 1: one block of 256 threads per (64 keys, kv head, row) for the keys and another for the values; with FP
 // (the projection-output form, PfFront) also one per (64 tokens, query head of the kv head's group, row) for the
 // queries. ROT (rotary dims) is a template parameter so that the rotation pairs are compile-time register indices.
-template <int ROT, bool FP>
+// CACHED (with FP): the call's T tokens sit at cache positions P .. P + T - 1, P = pos_dev[b] clamped to
+// 0 .. max_len - T as the cached main kernel clamps it; the keys go to the cache only (the main kernel reads them
+// there), and the value blocks cover the cache rows 0 .. P + T - 1 (Tp = max_len): rows below P from the cache, the
+// call's rows from y (also appended to the cache).
+template <int ROT, bool FP, bool CACHED>
 __global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restrict__ k, const __bf16* __restrict__ v,
                                                            const float* __restrict__ cos_t,
                                                            const float* __restrict__ sin_t, int pos0,
                                                            __bf16* __restrict__ kr, __bf16* __restrict__ vt, int T,
-                                                           int Tp, int Hkv, int Hq, PfFront fe) {
+                                                           int Tp, int Hkv, int Hq, PfFront fe,
+                                                           const int32_t* __restrict__ pos_dev) {
   static_assert(ROT % 16 == 0 && ROT <= kRotMax, "rotary dims");
+  static_assert(FP || !CACHED, "the cached form starts from the projection output");
   constexpr int half = ROT / 2;
   const int tid = threadIdx.x;
-  // blocks x < Tp / 64 prepare the keys of tile x, the next Tp / 64 the values of tile x - Tp / 64, then (FP) the
-  // queries: block 2 Tp / 64 + G u + g holds tokens 64 u .. of query head kvh G + g
-  const int ntile = Tp / kBN, bx = blockIdx.x;
-  const int role = bx < ntile ? 0 : (bx < 2 * ntile ? 1 : 2);  // 0 keys, 1 values, 2 queries
+  // blocks x < ntk prepare the keys of tile x (tokens 64 x ..), the next nvt the values of tile x - ntk, then (FP)
+  // the queries: block ntk + nvt + G u + g holds tokens 64 u .. of query head kvh G + g
+  const int ntk = CACHED ? (T + kBN - 1) / kBN : Tp / kBN, nvt = Tp / kBN, bx = blockIdx.x;
+  const int role = bx < ntk ? 0 : (bx < ntk + nvt ? 1 : 2);  // 0 keys, 1 values, 2 queries
   const int kvh = blockIdx.y, b = blockIdx.z;
   const int G = Hq / Hkv;
-  const int key0 = (role == 0 ? bx : role == 1 ? bx - ntile : (bx - 2 * ntile) / G) * kBN;
-  const int qh = role == 2 ? kvh * G + (bx - 2 * ntile) % G : 0;
+  const int key0 = (role == 0 ? bx : role == 1 ? bx - ntk : (bx - ntk - nvt) / G) * kBN;
+  const int qh = role == 2 ? kvh * G + (bx - ntk - nvt) % G : 0;
   const size_t head = (size_t)b * Hkv + kvh;
+  if constexpr (CACHED) pos0 = min(max(pos_dev[b], 0), Tp - T);
   // Keys and queries: thread = (row r, lane q of 4); a row is 32 segments of 8 dims and thread q takes segments
   // q, q + 4, ... A rotary segment (s < ROT / 8) pairs with the segment half / 8 away; its cos / sin rows are loaded
   // as vectors. Every load of the thread is issued before any is used (one memory round trip per block).
@@ -223,8 +237,9 @@ __global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restr
       rr = rsqrtf((s3[0] + s3[1]) * (1.f / kPD) + fe.eps);
     }
     const u32x4 z = {0u, 0u, 0u, 0u};
-    // keys: every row of the tile (zero past T); queries: the valid rows
-    __bf16* dst = role == 2 ? (valid ? fe.qr + (trow * Hq + qh) * kPD : nullptr) : kr + (head * Tp + key) * kPD;
+    // keys: every row of the tile (zero past T; the cached form writes the cache only); queries: the valid rows
+    __bf16* dst = role == 2 ? (valid ? fe.qr + (trow * Hq + qh) * kPD : nullptr)
+                            : (CACHED ? nullptr : kr + (head * Tp + key) * kPD);
     __bf16* cdst = nullptr;
     if constexpr (FP)
       if (role == 0 && valid && pos0 + key < fe.max_len) cdst = fe.kc + (head * fe.max_len + pos0 + key) * kPD;
@@ -268,9 +283,17 @@ __global__ __launch_bounds__(256) void attn_kv_prep_kernel(const __bf16* __restr
       if (cdst) *reinterpret_cast<u32x4*>(cdst + 8 * sg) = o;
     }
   } else {
-    if constexpr (FP) {
-      vt_tile(fe.y + (size_t)b * T * fe.ldy + (size_t)Hq * 2 * kPD + (size_t)(Hkv + kvh) * kPD, (size_t)fe.ldy, key0,
-              T, vt + head * kPD * Tp, Tp, tid, fe.vc + head * fe.max_len * kPD, pos0, fe.max_len);
+    const float* yv = nullptr;
+    if constexpr (FP) yv = fe.y + (size_t)b * T * fe.ldy + (size_t)Hq * 2 * kPD + (size_t)(Hkv + kvh) * kPD;
+    if constexpr (CACHED) {
+      // cache rows 0 .. pos0 + T - 1; tiles past them are not read by the main kernel
+      const int nk = pos0 + T;
+      if (key0 >= nk) return;
+      __bf16* vch = fe.vc + head * fe.max_len * kPD;
+      vt_tile(yv, (size_t)fe.ldy, key0, nk, vt + head * kPD * Tp, Tp, tid, vch, 0, fe.max_len, vch, pos0);
+    } else if constexpr (FP) {
+      vt_tile(yv, (size_t)fe.ldy, key0, T, vt + head * kPD * Tp, Tp, tid, fe.vc + head * fe.max_len * kPD, pos0,
+              fe.max_len);
     } else {
       vt_tile(v + ((size_t)b * T * Hkv + kvh) * kPD, (size_t)Hkv * kPD, key0, T, vt + head * kPD * Tp, Tp, tid);
     }
@@ -905,8 +928,8 @@ static int pf_launch(const void* q, const void* k, const void* v, const void* ga
   }
   const dim3 gp((unsigned)((FP ? 2 + G : 2) * (Tp / kBN)), (unsigned)Hkv, (unsigned)B);
 #define Q35_KV_LAUNCH(R)                                                                                        \
-  hipLaunchKernelGGL((attn_kv_prep_kernel<R, FP>), gp, dim3(256), 0, st, (const __bf16*)k, (const __bf16*)v, cos, \
-                     sin, (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv, (int)Hq, fe)
+  hipLaunchKernelGGL((attn_kv_prep_kernel<R, FP, false>), gp, dim3(256), 0, st, (const __bf16*)k, (const __bf16*)v,  \
+                     cos, sin, (int)pos0, kr, vt, (int)T, (int)Tp, (int)Hkv, (int)Hq, fe, (const int32_t*)nullptr)
   switch (rot) {
     case 0: Q35_KV_LAUNCH(0); break;
     case 16: Q35_KV_LAUNCH(16); break;
@@ -984,7 +1007,7 @@ extern "C" int q35_gated_attn_prefill_proj(const float* y, int64_t ldy, const fl
 extern "C" size_t q35_gated_attn_prefill_cached_workspace_bytes(int64_t B, int64_t Hkv, int64_t D, int64_t max_len) {
   using namespace q35;
   if (B <= 0 || Hkv <= 0 || D != kPD || max_len <= 0 || max_len % kBN != 0) return 0;
-  return ((size_t)B * Hkv * kPD * max_len * sizeof(__bf16) + 255) / 256 * 256;
+  return ((size_t)B * Hkv * q35::kPD * max_len * sizeof(__bf16) + 255) / 256 * 256;
 }
 
 extern "C" int q35_gated_attn_prefill_cached(const void* q, const void* k_cache, const void* v_cache,
@@ -1028,5 +1051,84 @@ extern "C" int q35_gated_attn_prefill_cached(const void* q, const void* k_cache,
     default: Q35_PFC_LAUNCH(4); break;
   }
 #undef Q35_PFC_LAUNCH
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
+}
+
+// The cached multi-token form from the fused projection output: workspace V^T [B, Hkv, D, max_len] bf16, then the
+// rotated queries [B, T, Hq, D] bf16.
+static size_t pfc_proj_q_off(int64_t B, int64_t Hkv, int64_t max_len) {
+  return ((size_t)B * Hkv * q35::kPD * max_len * sizeof(__bf16) + 255) / 256 * 256;
+}
+
+extern "C" size_t q35_gated_attn_prefill_cached_proj_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
+                                                                     int64_t D, int64_t max_len) {
+  using namespace q35;
+  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D != kPD || max_len <= 0 || max_len % kBN != 0 ||
+      T > max_len)
+    return 0;
+  const int64_t G = Hq / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return 0;
+  if (max_len > ((int64_t)1 << 30) || B * Hq > ((int64_t)1 << 30)) return 0;
+  return pfc_proj_q_off(B, Hkv, max_len) + ((size_t)B * T * Hq * kPD * sizeof(__bf16) + 255) / 256 * 256;
+}
+
+extern "C" int q35_gated_attn_prefill_cached_proj(const float* y, int64_t ldy, const float* q_norm_w,
+                                                  const float* k_norm_w, float eps, void* k_cache, void* v_cache,
+                                                  const int32_t* pos, const float* cos, const float* sin, void* out,
+                                                  int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                                  int64_t max_len, int64_t rot, float scale, void* workspace,
+                                                  size_t workspace_bytes, q35_stream_t stream) {
+  using namespace q35;
+  if (!y || !q_norm_w || !k_norm_w || !k_cache || !v_cache || !pos || !out) return Q35_EINVAL;
+  if (B <= 0 || T <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_len <= 0 || Hq % Hkv != 0 || rot < 0 || rot > D ||
+      T > max_len)
+    return Q35_EINVAL;
+  if (rot > 0 && (!cos || !sin)) return Q35_EINVAL;
+  if (ldy < 2 * Hq * D + 2 * Hkv * D) return Q35_EINVAL;
+  if (D != kPD || (rot % 16) != 0 || rot > kRotMax || max_len % kBN != 0) return Q35_EUNSUPPORTED;
+  if ((ldy & 3) || (((uintptr_t)y | (uintptr_t)q_norm_w | (uintptr_t)k_norm_w) & 15)) return Q35_EUNSUPPORTED;
+  const int64_t G = Hq / Hkv;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return Q35_EUNSUPPORTED;
+  const int GW = G > 4 ? 4 : (int)G;
+  const int ngroups = (int)(G / GW);
+  if (max_len > ((int64_t)1 << 30) || B > 65535 || Hkv > 65535 || T * Hq * D > ((int64_t)1 << 40) ||
+      B * Hkv * max_len * D > ((int64_t)1 << 40))
+    return Q35_EUNSUPPORTED;
+  // V^T rows and cache key rows are addressed with 32-bit byte offsets inside a head's block
+  if (max_len * kPD * 2 >= ((int64_t)1 << 31)) return Q35_EUNSUPPORTED;
+  const int64_t nqb = (T + kBQ - 1) / kBQ, ntk = (T + kBN - 1) / kBN;
+  const int64_t nblocks = nqb * B * Hkv * ngroups;
+  if (nblocks > 0x7fffffff || ntk * (1 + G) + max_len / kBN > 0x7fffffff) return Q35_EUNSUPPORTED;
+  const size_t need = q35_gated_attn_prefill_cached_proj_workspace_bytes(B, T, Hq, Hkv, D, max_len);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  __bf16* vt = static_cast<__bf16*>(workspace);
+  __bf16* qr = reinterpret_cast<__bf16*>(static_cast<char*>(workspace) + pfc_proj_q_off(B, Hkv, max_len));
+  const PfFront fe{y, ldy, q_norm_w, k_norm_w, eps, (__bf16*)k_cache, (__bf16*)v_cache, qr, (int)max_len};
+  const dim3 gp((unsigned)(ntk * (1 + G) + max_len / kBN), (unsigned)Hkv, (unsigned)B);
+#define Q35_KVC_LAUNCH(R)                                                                                        \
+  hipLaunchKernelGGL((attn_kv_prep_kernel<R, true, true>), gp, dim3(256), 0, st, (const __bf16*)nullptr,          \
+                     (const __bf16*)nullptr, cos, sin, 0, (__bf16*)nullptr, vt, (int)T, (int)max_len, (int)Hkv,   \
+                     (int)Hq, fe, pos)
+  switch (rot) {
+    case 0: Q35_KVC_LAUNCH(0); break;
+    case 16: Q35_KVC_LAUNCH(16); break;
+    case 32: Q35_KVC_LAUNCH(32); break;
+    case 48: Q35_KVC_LAUNCH(48); break;
+    default: Q35_KVC_LAUNCH(64); break;
+  }
+#undef Q35_KVC_LAUNCH
+  // the queries arrive rotated (rot 0 in the main kernel); keys from the cache, the gate from y
+#define Q35_PFCP_LAUNCH(GG)                                                                                        \
+  hipLaunchKernelGGL((attn_prefill_kernel<GG, false, true>), dim3((unsigned)nblocks), dim3(64 * GG), 0, st,        \
+                     (const __bf16*)qr, (const __bf16*)k_cache, vt, (const void*)(y + kPD), ldy, cos, sin, 0,      \
+                     (__bf16*)out, (int)T, (int)max_len, (int)Hq, (int)Hkv, ngroups, 0, scale, (int)nqb, (int)B, 0, \
+                     (float*)nullptr, pos)
+  switch (GW) {
+    case 1: Q35_PFCP_LAUNCH(1); break;
+    case 2: Q35_PFCP_LAUNCH(2); break;
+    default: Q35_PFCP_LAUNCH(4); break;
+  }
+#undef Q35_PFCP_LAUNCH
   return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }

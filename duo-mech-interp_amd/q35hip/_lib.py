@@ -18,6 +18,7 @@ EXPORTS = [
     "q35_gated_attn_prefill_cached_workspace_bytes", "q35_gated_attn_prefill_cached", "q35_gated_attn_decode_workspace_bytes",
     "q35_gated_attn_decode", "q35_gated_attn_decode_noalloc_max_bytes", "q35_gated_attn_decode_noalloc",
     "q35_gated_attn_decode_proj", "q35_gated_attn_prefill_proj_workspace_bytes", "q35_gated_attn_prefill_proj",
+    "q35_gated_attn_prefill_cached_proj_workspace_bytes", "q35_gated_attn_prefill_cached_proj",
     "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
     "q35_swiglu_push",
     "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm", "q35_gemm_q8", "q35_gemm_q8_split",
@@ -56,6 +57,9 @@ _SIGS = {
     "q35_gated_attn_prefill_proj_workspace_bytes": ([I64, I64, I64, I64, I64], SZ),
     "q35_gated_attn_prefill_proj": ([P, I64, P, P, F32, P, P, I64, P, P, P, I64, I64, I64, I64, I64, I64, I64, F32, P,
                                      SZ, P], I32),
+    "q35_gated_attn_prefill_cached_proj_workspace_bytes": ([I64, I64, I64, I64, I64, I64], SZ),
+    "q35_gated_attn_prefill_cached_proj": ([P, I64, P, P, F32, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I64, F32,
+                                            P, SZ, P], I32),
     "q35_gated_attn_decode_noalloc_max_bytes": ([], SZ),
     "q35_gated_attn_decode_noalloc": ([P, P, P, P, P, P, P, P, I32, I64, I64, I64, I64, I64, I64, F32, I64, P], I32),
     "q35_resid_add_rows": ([P, P, P, I64, I64, I64, I64, I32, P], I32),

@@ -218,7 +218,7 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     cache positions 0..pos+t (engine/kernels_qwen35.js:90). T > 1 at the int position 0 runs the flash prefill over
     the call's own tokens (for an fp32 y with the front end in its pre-pass, q35_gated_attn_prefill_proj); T > 1 at
     any other position (or a device pos) the same kernel over the cache (the caches' max_len must then be a multiple
-    of 64); T == 1 the split-K decode over cache positions 0..pos (cache_len: optional [B] int32 per-row lengths,
+    of 64; for an fp32 y with the front end in its pre-pass, q35_gated_attn_prefill_cached_proj); T == 1 the split-K decode over cache positions 0..pos (cache_len: optional [B] int32 per-row lengths,
     default pos + 1; without it the q / k norms, RoPE and the cache append run inside the decode kernels,
     q35_gated_attn_decode_proj, instead of a front-end launch). prenorm: see linear(). For T > 1, x may be the int32
     words of split activations (see gated_deltanet_layer). Returns y [B, T, H], or with residual [B, T, H] given,
@@ -250,6 +250,14 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
         # the call's own tokens: the front end runs in the prefill's pre-pass, reading y (q35_gated_attn_prefill_proj)
         o = ops.gated_attention_prefill_proj(y, p["q_norm"], p["k_norm"], k_cache, v_cache, cos, sin, num_heads=Hq,
                                              pos0=0, eps=eps, scale=1.0 / math.sqrt(D))
+        wq_o, ws_o = _q8(p, "o_proj")
+        xo = o if (wq_o is not None and o.shape[-1] % 64 == 0) else o.float()
+        return linear(xo, p["o_proj"], wq_o, ws_o, residual=residual, fixed_order=fixed_order)
+    if T > 1 and not own_keys and y.dtype == torch.float32 and y.shape[-1] % 4 == 0 and max_len % 64 == 0:
+        # the same over the cache (tokens at per-row positions), the front end in the pre-pass
+        # (q35_gated_attn_prefill_cached_proj)
+        o = ops.gated_attention_prefill_cached_proj(y, p["q_norm"], p["k_norm"], k_cache, v_cache, pos_t, cos, sin,
+                                                    num_heads=Hq, eps=eps, scale=1.0 / math.sqrt(D))
         wq_o, ws_o = _q8(p, "o_proj")
         xo = o if (wq_o is not None and o.shape[-1] % 64 == 0) else o.float()
         return linear(xo, p["o_proj"], wq_o, ws_o, residual=residual, fixed_order=fixed_order)

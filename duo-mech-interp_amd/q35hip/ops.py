@@ -69,6 +69,8 @@ _LIB.define("gated_attn_decode_proj(Tensor y, Tensor q_norm_w, Tensor k_norm_w, 
             "bool f32_out=False) -> Tensor")
 _LIB.define("gated_attn_prefill_proj(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, Tensor(a!) k_cache, "
             "Tensor(b!) v_cache, int pos0, Tensor cos, Tensor sin, int Hq, float scale) -> Tensor")
+_LIB.define("gated_attn_prefill_cached_proj(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, "
+            "Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor pos, Tensor cos, Tensor sin, int Hq, float scale) -> Tensor")
 _LIB.define("resid_add_rows_(Tensor(a!) x, Tensor vecs, Tensor? vec_of_row) -> ()")
 _LIB.define("gdn_conv(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
             "Tensor dt_bias, int b_off, int a_off, int Hk, int dk, int Hv, int dv, bool bf16_out) "
@@ -286,6 +288,39 @@ def _attn_prefill_proj_impl(y, q_norm_w, k_norm_w, eps, k_cache, v_cache, pos0, 
                                        _ptr(v_cache), int(pos0), _ptr(cos), _ptr(sin), _ptr(out), B, T, Hq, Hkv, D,
                                        max_len, rot, float(scale), _ptr(ws), ws.numel(), _stream(y))
     check(st, "q35_gated_attn_prefill_proj")
+    return out
+
+
+def _attn_prefill_cached_proj_impl(y, q_norm_w, k_norm_w, eps, k_cache, v_cache, pos, cos, sin, Hq, scale):
+    _on_gpu(q_norm_w, k_norm_w, k_cache, v_cache, pos, cos, sin)
+    _require(y.is_cuda and y.dtype == torch.float32 and y.dim() == 3 and y.stride(2) == 1
+             and y.stride(0) == y.shape[1] * y.stride(1), "y: [B, T, W] fp32 with dense rows (the fused projection "
+             "output)")
+    B, T, W = y.shape
+    ldy = y.stride(1)
+    _require(k_cache.dtype == torch.bfloat16 and k_cache.dim() == 4 and v_cache.shape == k_cache.shape
+             and v_cache.dtype == k_cache.dtype and k_cache.is_contiguous() and v_cache.is_contiguous(),
+             "caches: [B, Hkv, max_len, D] bf16 dense")
+    Hkv, max_len, D = k_cache.shape[1], k_cache.shape[2], k_cache.shape[3]
+    _require(k_cache.shape[0] == B, "caches must match y in batch")
+    _require(W >= Hq * 2 * D + 2 * Hkv * D, "y: too narrow for [q | gate] x Hq, k, v")
+    _require(q_norm_w.dtype == torch.float32 and k_norm_w.dtype == torch.float32 and q_norm_w.numel() == D
+             and k_norm_w.numel() == D and q_norm_w.is_contiguous() and k_norm_w.is_contiguous(),
+             "q_norm_w, k_norm_w: [D] fp32")
+    _require(pos.dtype == torch.int32 and tuple(pos.shape) == (B,), "pos: [B] int32")
+    _require(max_len % 64 == 0, "the cache length must be a multiple of 64 for a multi-token call over the cache")
+    _require(T <= max_len, "more tokens than the cache holds")
+    rot = _tables_check(cos, sin, max_len)
+    L = _lib.lib()
+    nbytes = L.q35_gated_attn_prefill_cached_proj_workspace_bytes(B, T, Hq, Hkv, D, max_len)
+    _require(nbytes > 0, "unsupported attention shape")
+    ws = _workspace(nbytes, y.device)
+    out = torch.empty(B, T, Hq * D, dtype=torch.bfloat16, device=y.device)
+    st = L.q35_gated_attn_prefill_cached_proj(_ptr(y), ldy, _ptr(q_norm_w), _ptr(k_norm_w), float(eps),
+                                              _ptr(k_cache), _ptr(v_cache), _ptr(pos), _ptr(cos), _ptr(sin), _ptr(out),
+                                              B, T, Hq, Hkv, D, max_len, rot, float(scale), _ptr(ws), ws.numel(),
+                                              _stream(y))
+    check(st, "q35_gated_attn_prefill_cached_proj")
     return out
 
 
@@ -675,6 +710,7 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("gated_attn_decode", _attn_decode_impl), ("resid_add_rows_", _resid_add_impl),
                      ("gated_attn_decode_proj", _attn_decode_proj_impl),
                      ("gated_attn_prefill_proj", _attn_prefill_proj_impl),
+                     ("gated_attn_prefill_cached_proj", _attn_prefill_cached_proj_impl),
                      ("gdn_conv", _gdn_conv_impl), ("gated_rmsnorm", _gated_rmsnorm_impl), ("gated_rmsnorm_split", _gated_rmsnorm_split_impl),
                      ("gdn_decode_fused_", _gdn_decode_fused_impl),
                      ("attn_prep", _attn_prep_impl), ("gemv_", _gemv_impl), ("swiglu_push", _swiglu_push_impl),
@@ -711,6 +747,10 @@ _LIB.impl("gated_attn_decode_proj",
           "Meta")
 _LIB.impl("gated_attn_prefill_proj",
           lambda y, qn, kn, eps, kc, vc, pos0, cos, sin, Hq, scale:
+          y.new_empty(y.shape[0], y.shape[1], Hq * kc.shape[3], dtype=torch.bfloat16),
+          "Meta")
+_LIB.impl("gated_attn_prefill_cached_proj",
+          lambda y, qn, kn, eps, kc, vc, pos, cos, sin, Hq, scale:
           y.new_empty(y.shape[0], y.shape[1], Hq * kc.shape[3], dtype=torch.bfloat16),
           "Meta")
 _LIB.impl("resid_add_rows_", lambda x, vecs, vor: None, "Meta")
@@ -850,6 +890,20 @@ def gated_attention_prefill_proj(y, q_norm_w, k_norm_w, k_cache, v_cache, cos, s
     return torch.ops.q35.gated_attn_prefill_proj(y, q_norm_w.float().contiguous(), k_norm_w.float().contiguous(),
                                                  float(eps), k_cache, v_cache, int(pos0), cos, sin, int(num_heads),
                                                  float(scale))
+
+
+def gated_attention_prefill_cached_proj(y, q_norm_w, k_norm_w, k_cache, v_cache, pos, cos, sin, *, num_heads,
+                                        eps=1e-6, scale=None):
+    """T new tokens per row over the bf16 KV cache from their fused projection output y [B, T, W] fp32 (the
+    reference's multi-token attention, engine/kernels_qwen35.js:18-123 attnPrep + attention, with token t of row b at
+    position pos[b] + t, pos: [B] int32 on the device, clamped to 0 .. max_len - T): q and k normalised with (1 + w)
+    and rotated, the tokens' keys and values appended to the caches, attention over cache keys 0 .. pos[b] + t,
+    sigmoid gate; max_len a multiple of 64. Returns [B, T, num_heads * D] bf16."""
+    D = k_cache.shape[3]
+    scale = D ** -0.5 if scale is None else scale
+    return torch.ops.q35.gated_attn_prefill_cached_proj(y, q_norm_w.float().contiguous(),
+                                                        k_norm_w.float().contiguous(), float(eps), k_cache, v_cache,
+                                                        pos, cos, sin, int(num_heads), float(scale))
 
 
 def residual_steer_add_(x, vecs, vec_of_row=None):

@@ -23,6 +23,8 @@
  *   q35_gated_attn_prefill_proj  the multi-token attention of a call's own tokens from the fused projection
  *                            output: engine/kernels_qwen35.js:18-69 `attnPrep` and :73-123 `attention` in one call
  *                            (HF:667-701 at positions pos0 .. pos0 + T - 1)
+ *   q35_gated_attn_prefill_cached_proj  the same over a KV cache at per-row positions (engine/model.js:486-491
+ *                            chunked prefill; HF:667-701 with a DynamicCache)
  *   q35_resid_add_rows       tests/engine_ref.py:49-53 residual vector hook; engine/kernels.js:190-203 `resAdd`
  *   q35_gdn_conv             HF:454-499 (causal_conv1d_fn / causal_conv1d_update + SiLU, split, beta, g);
  *                            engine/kernels_qwen35.js:127-178 `conv` + `convState`, :226-229 (gate terms of `delta`)
@@ -220,6 +222,25 @@ int q35_gated_attn_prefill_proj(const float* y, int64_t ldy, const float* q_norm
                                 void* out, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t max_len,
                                 int64_t rot, float scale, void* workspace, size_t workspace_bytes,
                                 q35_stream_t stream);
+
+/*
+ * The multi-token attention over a bf16 KV cache from the fused projection output (engine/kernels_qwen35.js:18-69
+ * `attnPrep` followed by :73-123 `attention`, token t of row b at position P_b + t with P_b = pos[b] clamped to
+ * 0 .. max_len - T; engine/model.js:486-491 chunked prefill; HF:667-701 with a DynamicCache): y as for
+ * q35_gated_attn_prefill_proj. q and k are normalised and rotated at P_b + t; the tokens' rotated keys and values
+ * are written into k_cache / v_cache at rows P_b + t (bitwise the rows q35_attn_prep writes for positions with
+ * pos[b] + T <= max_len), and token t attends to cache keys 0 .. P_b + t. out [B, T, Hq * D] bf16. Limits as
+ * q35_gated_attn_prefill_cached (max_len a multiple of 64); y, ldy and the norm weights 16-byte aligned. Needs
+ * q35_gated_attn_prefill_cached_proj_workspace_bytes(B, T, Hq, Hkv, D, max_len) bytes of workspace (256-byte
+ * aligned); calls that share one workspace must not overlap.
+ */
+size_t q35_gated_attn_prefill_cached_proj_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                                          int64_t max_len);
+int q35_gated_attn_prefill_cached_proj(const float* y, int64_t ldy, const float* q_norm_w, const float* k_norm_w,
+                                       float eps, void* k_cache, void* v_cache, const int32_t* pos, const float* cos,
+                                       const float* sin, void* out, int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
+                                       int64_t D, int64_t max_len, int64_t rot, float scale, void* workspace,
+                                       size_t workspace_bytes, q35_stream_t stream);
 
 /*
  * q35_gated_attn_decode without a workspace argument, for callers that cannot allocate device memory (code under HIP

@@ -275,6 +275,37 @@ def test_prefill_from_projection_rejects_without_launching():
                                                 torch.zeros(64, 32), torch.zeros(64, 32), num_heads=8)
 
 
+def test_prefill_over_cache_from_projection_rejects_without_launching():
+    """q35_gated_attn_prefill_cached_proj refuses bad arguments before any HIP call (Hq 8, Hkv 2, D 256, T 100 over a
+    448-row cache); its workspace is V^T of the cache plus the rotated queries, and its torch op has no CPU path."""
+    L = q35hip.lib()
+    fake = 0x1000
+    W = 8 * 2 * 256 + 2 * 2 * 256
+
+    def call(y=fake, ldy=W, pos=fake, T=100, Hq=8, D=256, max_len=448, rot=64, ws_bytes=1 << 24):
+        return L.q35_gated_attn_prefill_cached_proj(y, ldy, fake, fake, 1e-6, fake, fake, pos, fake, fake, fake, 1, T,
+                                                    Hq, 2, D, max_len, rot, 0.0625, fake, ws_bytes, None)
+    assert call(y=None) == 1                 # null y
+    assert call(pos=None) == 1               # null positions
+    assert call(ldy=W - 4) == 1              # rows too short for [q | gate] x Hq, k, v
+    assert call(T=449) == 1                  # more tokens than the cache holds
+    assert call(y=fake + 4) == 2             # y not 16-byte aligned
+    assert call(max_len=450, T=100) == 2     # cache length not a multiple of 64
+    assert call(Hq=6) == 2                   # 3 query heads per kv head
+    assert call(rot=24) == 2                 # rotary dims not a multiple of 16
+    assert call(ws_bytes=8) == 3             # workspace too small
+    need = 2 * 256 * 448 * 2 + 100 * 8 * 256 * 2
+    assert L.q35_gated_attn_prefill_cached_proj_workspace_bytes(1, 100, 8, 2, 256, 448) == need
+    assert L.q35_gated_attn_prefill_cached_proj_workspace_bytes(1, 100, 8, 2, 256, 450) == 0
+    assert call(ws_bytes=need - 256) == 3
+    y = torch.zeros(1, 4, W)
+    kc = torch.zeros(1, 2, 64, 256, dtype=torch.bfloat16)
+    with pytest.raises(Exception, match="no CPU|HIP device"):
+        q35hip.ops.gated_attention_prefill_cached_proj(y, torch.zeros(256), torch.zeros(256), kc, kc.clone(),
+                                                       torch.zeros(1, dtype=torch.int32), torch.zeros(64, 32),
+                                                       torch.zeros(64, 32), num_heads=8)
+
+
 def test_split_activation_layout():
     """The int8 GEMM's split layout (ops.split_activations, which the norm's split output and the split GEMM follow):
     per row, each group of 8 inputs is 32 bytes, the 8 bf16 hi parts then the 8 bf16 lo parts; hi is x rounded to

@@ -231,6 +231,49 @@ def test_attn_prefill_from_projection(B, T, Hq, Hkv, pos0, max_len):
     assert out.shape == (B, T, Hq * D) and e_ref <= 2e-2 and e_two <= 1e-2
 
 
+# Rows at different positions (0, mid-cache, the last rows), ragged key ranges, GQA 1 / 4 / 8, one token.
+@pytest.mark.parametrize("B,T,Hq,Hkv,max_len,pos", [(3, 100, 8, 2, 448, [0, 37, 300]), (2, 1, 8, 2, 256, [5, 255]),
+                                                     (1, 257, 4, 4, 640, [383]), (2, 64, 8, 1, 192, [128, 0]),
+                                                     (1, 130, 16, 2, 320, [64])])
+def test_attn_prefill_over_cache_from_projection(B, T, Hq, Hkv, max_len, pos):
+    """The multi-token call over the cache from the fused projection output (q35_gated_attn_prefill_cached_proj: the
+    front end and the cache append in the pre-pass, whose value blocks take the earlier rows from the cache and the
+    call's rows from y) against the oracle's front end + cached attention, and against q35_attn_prep +
+    q35_gated_attn_prefill_cached on the same inputs, whose caches it must leave bitwise equal."""
+    dev = device()
+    g = torch.Generator().manual_seed(70 + T + max_len)
+    D = 256
+    y = torch.randn(B, T, Hq * 2 * D + 2 * Hkv * D, generator=g)
+    qw, kw = 0.1 * torch.randn(D, generator=g), 0.1 * torch.randn(D, generator=g)
+    cos, sin = rope_tables(max_len, rope_inv_freq(D, 0.25, 1e7))
+    pos_t = torch.tensor(pos, dtype=torch.int32)
+    kc0 = torch.randn(B, Hkv, max_len, D, generator=g).to(torch.bfloat16)
+    vc0 = torch.randn(B, Hkv, max_len, D, generator=g).to(torch.bfloat16)
+    q, gate, _, v, k_rot = of.attn_prep(y, qw, kw, cos, sin, pos_t, Hq, Hkv, D)
+    kr, vr = kc0.clone(), vc0.clone()
+    for b in range(B):
+        p0 = int(pos_t[b])
+        kr[b, :, p0:p0 + T] = k_rot[b].transpose(0, 1).to(torch.bfloat16)
+        vr[b, :, p0:p0 + T] = v[b].transpose(0, 1).to(torch.bfloat16)
+    ref = oracle.gated_attention_cached(q, kr, vr, gate, pos_t, cos, sin)
+    announce(f"attn prefill over cache from projection B{B} T{T} Hq{Hq} Hkv{Hkv} max_len {max_len} pos {pos}")
+    yd, qwd, kwd, posd = y.to(dev), qw.to(dev), kw.to(dev), pos_t.to(dev)
+    cosd, sind = cos.to(dev), sin.to(dev)
+    kcb, vcb = kc0.to(dev), vc0.to(dev)
+    out = ops.gated_attention_prefill_cached_proj(yd, qwd, kwd, kcb, vcb, posd, cosd, sind, num_heads=Hq)
+    kca, vca = kc0.to(dev), vc0.to(dev)
+    qa, ga, _, _ = ops.attn_prep(yd, qwd, kwd, cosd, sind, posd, kca, vca, num_heads=Hq, num_kv_heads=Hkv,
+                                 want_kv=False)
+    two = ops.gated_attention_prefill_cached(qa, kca, vca, ga, posd, cosd, sind)
+    torch.cuda.synchronize()
+    assert torch.equal(kcb.cpu(), kca.cpu()) and torch.equal(vcb.cpu(), vca.cpu())
+    # values: the fp32 rows rounded to bf16, bitwise the oracle's; keys: one bf16 rounding of the fp32 front end
+    assert torch.equal(vcb.cpu(), vr) and oracle.rel_err(kcb.cpu().float(), kr.float()) <= TOL_BF16
+    e_ref, e_two = oracle.rel_err(out.float().cpu(), ref), oracle.rel_err(out.float().cpu(), two.float().cpu())
+    print(f"prefill over cache from projection: rel err {e_ref:.3e} (oracle), {e_two:.3e} (two-launch path)")
+    assert out.shape == (B, T, Hq * D) and e_ref <= 2e-2 and e_two <= 1e-2
+
+
 @pytest.mark.parametrize("with_add", [False, True])
 def test_add_rmsnorm_matches_oracle(with_add):
     """Residual add + RMSNorm(1 + w) (HF:720-734): x updated in place, h returned."""
