@@ -20,7 +20,11 @@
 // arrive by global_load_lds DMA into XOR-swizzled LDS (conflict-free 16-byte operand reads), two stages and one
 // barrier per tile (tile kt + 1 is copied while tile kt is computed), each wave copying a quarter of every tile.
 #include <atomic>
+#include <functional>
+#include <mutex>
+#include <queue>
 #include <type_traits>
+#include <vector>
 
 #include "q35_common.h"
 #include "q35hip.h"
@@ -323,7 +327,8 @@ struct PfStage {
 
 // Work items. Query block qb needs key tiles 0 .. nkt(qb) - 1, so the causal blocks range from 1 to ~T/64 tiles. With
 // a split length Ls > 0, every block with more than Ls tiles (qb >= 2 Ls) is run as two items, tiles [0, Ls) and
-// [Ls, nkt), whose (O, m, l) are combined by attn_prefill_merge_kernel; the others run whole. Two orders:
+// [Ls, nkt), whose (O, m, l) are combined by attn_prefill_merge_kernel; the others run whole (Ls = 0, every block
+// whole and longest first, when the estimate of pf_split_pays finds that faster). Two orders:
 // - Independent items, numbered longest first: all first halves (Ls tiles each), then second halves and whole blocks
 //   alternately, each in decreasing length, so that the hardware's in-order dispatch to free CUs balances the CUs'
 //   total tiles. Used when the items outnumber the CUs.
@@ -381,6 +386,61 @@ inline int pf_items(int nqb, int Ls, bool paired) {
   if (Ls == 0) return nqb;
   const int nsq = nqb - 2 * Ls, qs = 2 * Ls;
   return paired ? nsq + (nsq > qs ? nsq : qs) : 2 * nsq + qs;
+}
+
+// Estimated end of a launch's blocks (in units of one tile's time) under the hardware's in-order dispatch, each block
+// taken by the CU that frees first (one block per CU at a time). A block costs its tiles, 1.5 for its query prologue
+// and epilogue, and 0.5 more for a split half's partial stores.
+static double pf_dispatch_time(int nqb, int Ls, bool paired, int64_t n_other, int cus) {
+  std::priority_queue<double, std::vector<double>, std::greater<double>> free_at;
+  for (int c = 0; c < cus; ++c) free_at.push(0.0);
+  double end = 0.0;
+  const int n = pf_items(nqb, Ls, paired);
+  for (int i = 0; i < n; ++i) {
+    const PfItem it = pf_item(i, nqb, Ls, paired);
+    const double cost = (it.kt1 - it.kt0) + (it.qb2 >= 0 ? pf_tiles(it.qb2) : 0) + 1.5 + (it.half >= 0 ? 0.5 : 0.0);
+    for (int64_t o = 0; o < n_other; ++o) {
+      const double f = free_at.top() + cost;
+      free_at.pop();
+      free_at.push(f);
+      end = f > end ? f : end;
+    }
+  }
+  return end;
+}
+
+// Whether splitting the long query blocks pays on a device of cus CUs: the split schedule's estimated end plus the
+// merge kernel (1 for its launch, 0.04 per pair of halves of four waves: the partials' stores and reads) against
+// the longest-first order of whole blocks. The costs were fitted to same-box timings of both schedules over ten
+// shapes (B 1-4, T 1536-8192, 8 q / 2 kv heads), whose faster schedule they all pick. Decisions are kept per shape.
+static bool pf_split_pays(int nqb, int Ls, int64_t n_other, int gw, int cus) {
+  if (Ls == 0) return false;
+  if (cus <= 0) return true;
+  const int64_t nsq = nqb - 2 * Ls;
+  // past a few million blocks the whole blocks spread evenly however long the longest is
+  if ((int64_t)pf_items(nqb, Ls, false) * n_other > ((int64_t)1 << 22)) return false;
+  struct Key {
+    int nqb, gw, cus;
+    int64_t n_other;
+  };
+  static std::mutex mu;
+  static Key keys[32];
+  static bool vals[32];
+  static int nkeys = 0, next = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < nkeys; ++i)
+      if (keys[i].nqb == nqb && keys[i].gw == gw && keys[i].cus == cus && keys[i].n_other == n_other) return vals[i];
+  }
+  const bool paired = (int64_t)pf_items(nqb, Ls, true) * n_other <= cus;
+  const double split = pf_dispatch_time(nqb, Ls, paired, n_other, cus) + 1.0 + 0.01 * gw * (double)(nsq * n_other);
+  const bool pays = split < pf_dispatch_time(nqb, 0, false, n_other, cus);
+  std::lock_guard<std::mutex> lock(mu);
+  keys[next] = Key{nqb, gw, cus, n_other};
+  vals[next] = pays;
+  next = (next + 1) % 32;
+  nkeys = nkeys < 32 ? nkeys + 1 : 32;
+  return pays;
 }
 
 // GF: the gate is read from the fused projection output (fp32 rows of stride gate_ld, query head h at 2 D h) instead
@@ -867,12 +927,12 @@ struct PfLayout {
   size_t q_off, part_off, total;
   int64_t npairs;
 };
-static PfLayout pf_layout(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, bool fp) {
+// Ls: the split length (the workspace functions size for pf_split_len, the most a launch can use).
+static PfLayout pf_layout(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, bool fp, int Ls) {
   const int64_t Tp = padded_T(T);
   const int64_t G = Hq / Hkv;
   const int64_t GW = G > 4 ? 4 : G;
   const int64_t nqb = (T + kBQ - 1) / kBQ;
-  const int Ls = pf_split_len((int)nqb);
   const int64_t nsq = Ls ? nqb - 2 * Ls : 0;
   PfLayout l;
   l.npairs = nsq * B * Hkv * (G / GW);
@@ -908,14 +968,18 @@ static int pf_launch(const void* q, const void* k, const void* v, const void* ga
   const int ngroups = (int)(G / GW);
   const int64_t Tp = padded_T(T);
   const int64_t nqb = (T + kBQ - 1) / kBQ;
-  const int Ls = pf_split_len((int)nqb);
+  const int Lmax = pf_split_len((int)nqb);
   const int64_t n_other = B * Hkv * ngroups;
-  if ((int64_t)pf_items((int)nqb, Ls, false) * n_other > 0x7fffffff) return Q35_EUNSUPPORTED;
-  const PfLayout lay = pf_layout(B, T, Hq, Hkv, FP);
-  if (lay.npairs > 0x7fffffff) return Q35_EUNSUPPORTED;
-  if (!workspace || workspace_bytes < lay.total || ((uintptr_t)workspace & 255)) return Q35_EWORKSPACE;
-  // the first HIP call: the device's compute units decide the work order
-  const bool paired = Ls > 0 && (int64_t)pf_items((int)nqb, Ls, true) * n_other <= device_cus();
+  if ((int64_t)pf_items((int)nqb, Lmax, false) * n_other > 0x7fffffff) return Q35_EUNSUPPORTED;
+  if (pf_layout(B, T, Hq, Hkv, FP, Lmax).npairs > 0x7fffffff) return Q35_EUNSUPPORTED;
+  // the workspace as the size functions report it (the split case), checked before any HIP call
+  if (!workspace || workspace_bytes < pf_layout(B, T, Hq, Hkv, FP, Lmax).total || ((uintptr_t)workspace & 255))
+    return Q35_EWORKSPACE;
+  // the first HIP call: the device's compute units decide the split and the work order
+  const int cus = device_cus();
+  const int Ls = pf_split_pays((int)nqb, Lmax, n_other, GW, cus) ? Lmax : 0;
+  const PfLayout lay = pf_layout(B, T, Hq, Hkv, FP, Ls);
+  const bool paired = Ls > 0 && (int64_t)pf_items((int)nqb, Ls, true) * n_other <= cus;
   const int64_t nblocks = (int64_t)pf_items((int)nqb, Ls, paired) * n_other;
   char* ws = static_cast<char*>(workspace);
   __bf16* kr = reinterpret_cast<__bf16*>(ws);
@@ -962,7 +1026,7 @@ static int pf_launch(const void* q, const void* k, const void* v, const void* ga
 extern "C" size_t q35_gated_attn_prefill_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D) {
   using namespace q35;
   if (pf_check(B, T, Hq, Hkv, D, 0) != Q35_OK) return 0;
-  return pf_layout(B, T, Hq, Hkv, false).total;
+  return pf_layout(B, T, Hq, Hkv, false, pf_split_len((int)((T + kBQ - 1) / kBQ))).total;
 }
 
 extern "C" int q35_gated_attn_prefill(const void* q, const void* k, const void* v, const void* gate,
@@ -982,7 +1046,7 @@ extern "C" size_t q35_gated_attn_prefill_proj_workspace_bytes(int64_t B, int64_t
                                                               int64_t D) {
   using namespace q35;
   if (pf_check(B, T, Hq, Hkv, D, 0) != Q35_OK) return 0;
-  return pf_layout(B, T, Hq, Hkv, true).total;
+  return pf_layout(B, T, Hq, Hkv, true, pf_split_len((int)((T + kBQ - 1) / kBQ))).total;
 }
 
 extern "C" int q35_gated_attn_prefill_proj(const float* y, int64_t ldy, const float* q_norm_w,

@@ -16,15 +16,16 @@ def _tables(n):
     return workloads.rope_tables(n)
 
 
-# T >= 449 (at least 8 key tiles in the last query block) runs the long query blocks as two key-split halves that
-# are merged in a third kernel: T 1000, 600 and 777 cover that with GQA 4, 8 (two head groups per kv head) and 1.
-# Those fit 256 CUs as paired items (the second half of a long block, then a short whole block, in one block; 600
-# and 777 leave whole blocks unpaired); B 4 T 1000 GQA 1 and B 5 T 1000 GQA 2 exceed it and run as independent
-# items in longest-first order.
+# T >= 449 (at least 8 key tiles in the last query block) may run the long query blocks as two key-split halves that
+# are merged in a third kernel, when the launcher's dispatch estimate finds that faster than whole blocks on 256
+# CUs. T 1000 and 777 (GQA 4 and 1) split and fit the device as paired items (the second half of a long block, then
+# a short whole block, in one block; 777 leaves whole blocks unpaired); T 5120 splits into more items than CUs and
+# runs them independently, longest first; B 2 T 600 GQA 8 (two head groups per kv head), B 4 T 1000 GQA 1 and B 5
+# T 1000 GQA 2 run whole blocks longest first (their longest block is short against a CU's share).
 @pytest.mark.parametrize("B,T,Hq,Hkv,pos0", [(1, 1, 8, 2, 0), (2, 100, 8, 2, 0), (1, 257, 8, 2, 5),
                                              (1, 96, 4, 4, 0), (1, 70, 8, 1, 3), (1, 64, 16, 2, 0),
                                              (1, 1000, 8, 2, 3), (2, 600, 16, 2, 0), (1, 777, 4, 4, 0),
-                                             (4, 1000, 8, 8, 0), (5, 1000, 4, 2, 1)])
+                                             (4, 1000, 8, 8, 0), (5, 1000, 4, 2, 1), (1, 5120, 8, 2, 0)])
 def test_prefill_small(B, T, Hq, Hkv, pos0):
     dev = device()
     inp = workloads.attn_prefill_inputs(B=B, T=T, Hq=Hq, Hkv=Hkv, seed=T)
@@ -55,8 +56,8 @@ def test_prefill_full_size():
 
 
 def test_prefill_long_sequence():
-    """T = 8192 (512 (query block, kv head) items, more than the device holds at once: the independent, longest-first
-    work order) against the fp32 oracle."""
+    """T = 8192 (256 whole query blocks per kv head, longest first: the longest block's 128 tiles are about a CU's
+    share, so nothing is split) against the fp32 oracle."""
     dev = device()
     inp = workloads.attn_prefill_inputs(B=1, T=8192, seed=9)
     cos, sin = _tables(8192)
