@@ -33,10 +33,10 @@ ROTATE_BYTES = 640 << 20     # distinct bytes cycled through between two uses of
 GDN_PREFILL_BYTES = 68_681_728      # q,k,v bf16 + g,beta fp32 + o bf16 + final S fp32 (T 4096, H 16, d 128)
 GDN_PREFILL_FLOPS = 1.190e10
 # HBM bytes one GDN prefill launch (prep + scan kernels) actually moves: rocprofv3 FETCH_SIZE / WRITE_SIZE per
-# dispatch, each scaled by what the counter reads for a 256 MiB device copy, on the kernels of commit 7b4258e
+# dispatch, each scaled by what the counter reads for a 256 MiB device copy, on the kernels of commit cc5e284
 # (profiles/counters_gdn_attn_gemm_kernels.md: prep 72.0 + 67.1 MB, scan 67.3 + 17.8 MB)
 GDN_PREFILL_TRAFFIC_BYTES = 224_200_000
-GDN_PREFILL_TRAFFIC_COMMIT = "7b4258e"  # the kernels the traffic was counted on
+GDN_PREFILL_TRAFFIC_COMMIT = "cc5e284"  # the kernels the traffic was counted on
 GDN_DECODE_STEP_BYTES = 2_130_048   # S read + write fp32 + q,k,v,o,g,beta (B 1, H 16, d 128)
 ATTN_PREFILL_FLOPS = 6.874e10       # 4 * D * Hq * T (T + 1) / 2, T 4096, Hq 8, D 256
 ATTN_PREFILL_BYTES = 58_720_256
