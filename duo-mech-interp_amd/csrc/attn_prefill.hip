@@ -417,8 +417,8 @@ static bool pf_split_pays(int nqb, int Ls, int64_t n_other, int gw, int cus) {
   if (Ls == 0) return false;
   if (cus <= 0) return true;
   const int64_t nsq = nqb - 2 * Ls;
-  // past a few million blocks the whole blocks spread evenly however long the longest is
-  if ((int64_t)pf_items(nqb, Ls, false) * n_other > ((int64_t)1 << 22)) return false;
+  // past 256 K blocks (a simulation of about 10 ms) the whole blocks spread evenly however long the longest is
+  if ((int64_t)pf_items(nqb, Ls, false) * n_other > ((int64_t)1 << 18)) return false;
   struct Key {
     int nqb, gw, cus;
     int64_t n_other;
