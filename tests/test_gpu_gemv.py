@@ -23,8 +23,10 @@ def _weights(N, K, wdt, seed):
 
 @pytest.mark.parametrize("wdt", [torch.int8, torch.float32])
 @pytest.mark.parametrize("M,N,K", [(1, 1024, 1024), (3, 7168, 1024), (3, 1024, 3584), (8, 1000, 2048),
-                                   (5, 2048, 256)])
+                                   (5, 2048, 256), (3, 20000, 1024)])
 def test_gemv_store_and_add(wdt, M, N, K):
+    """Per-row int8 and fp32 weights, store and accumulate. N 20000 has more 16-row tiles than blocks, so blocks
+    loop over tiles (one K step per wave with int8 at K 1024, four with fp32)."""
     dev = device()
     W, s = _weights(N, K, wdt, seed=N + K)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(M))
