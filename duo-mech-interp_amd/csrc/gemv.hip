@@ -45,7 +45,19 @@ struct GemvAux {
   int cc, ck;        // conv: channels (outputs 0 .. cc - 1 are convolved), taps
   float* cap;        // SwiGLU: activation capture (may be NULL): row m, neuron n at
   int64_t ldc, ldcr; //   cap[(m / T) ldcr + (m % T) ldc + n]
+  unsigned long long* amax;  // store: per-row argmax keys (may be NULL), see amax_key
 };
+
+// Argmax key of output n with value v: the order-preserving bits of v above the complement of n, so that the largest
+// key is the largest value and, among equal values, the lowest index (as argmax_rows_kernel and torch.argmax). -0
+// ranks as +0; NaN gets 0, the empty key, and never wins (the scan's strict comparisons). A real key is never 0.
+__device__ __forceinline__ unsigned long long amax_key(float v, int n) {
+  if (!(v == v)) return 0ull;
+  if (v == 0.f) v = 0.f;
+  uint32_t b = __float_as_uint(v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((unsigned long long)b << 32) | (0xFFFFFFFFu - (uint32_t)n);
+}
 
 __device__ __forceinline__ float gsilu(float x) { return silu_f(x); }
 
@@ -328,6 +340,8 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
         for (int m = 0; m < MP; ++m) acc[r][m] += ws[r] * part[r][m];
     }
   };
+  // store with aux.amax: the best argmax key of this thread's (output row, x row) over the block's tiles
+  unsigned long long best_key = 0ull;
   // the tile's row sums across the waves and its epilogue. red[it & 1] is rewritten two tiles later, after a barrier
   // that every thread reaches only past this tile's epilogue
   auto finish = [&](int it, int n0, float(&acc)[R][MP]) {
@@ -377,6 +391,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
             __hip_atomic_fetch_add(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           } else {
             *dst = EPI == kEpiAccumulate ? *dst + v : v;
+            if (EPI == kEpiStore && aux.amax) {
+              const unsigned long long kk = amax_key(v, nn);
+              best_key = kk > best_key ? kk : best_key;
+            }
           }
         }
       }
@@ -473,6 +491,31 @@ __global__ __launch_bounds__(512) void gemv_kernel(const float* __restrict__ x, 
       if (next >= ntiles) break;
       tile = next;
     }
+  }
+  if constexpr (EPI == kEpiStore) {
+    if (aux.amax) {  // uniform: every thread reaches the barrier
+      // the block's best key per row of x, then one device-scope atomic max per row
+      __shared__ unsigned long long kbest[4 * R * MP];
+      if (tid < 4 * R * MP) kbest[tid] = best_key;
+      __syncthreads();
+      if (tid < MP && tid < M) {
+        unsigned long long k = 0ull;
+        for (int rr = 0; rr < 4 * R; ++rr) k = kbest[rr * MP + tid] > k ? kbest[rr * MP + tid] : k;
+        if (k) __hip_atomic_fetch_max(aux.amax + tid, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+// The argmax keys of q35_gemv_norm_argmax turned into indices (the empty key: index 0, as argmax_rows_kernel reports
+// for a row that nothing wins), and the slots cleared for the next call.
+__global__ __launch_bounds__(64) void amax_take_kernel(unsigned long long* __restrict__ slots, int rows,
+                                                       int32_t* __restrict__ idx) {
+  const int r = threadIdx.x;
+  if (r < rows) {
+    const unsigned long long k = slots[r];
+    idx[r] = k ? (int32_t)(0xFFFFFFFFu - (uint32_t)k) : 0;
+    slots[r] = 0ull;
   }
 }
 
@@ -685,6 +728,31 @@ extern "C" int q35_gemv_norm(const float* x, const float* x_add, float* x_out, i
   na.aux.ldcr = ld_cap_row;
   return gemv_dispatch<true>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, epilogue, pushes, (int)npush, T, na,
                              reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int q35_gemv_norm_argmax(const float* x, const float* x_add, float* x_out, int64_t ldx,
+                                    const float* norm_w, float eps, const void* W, int w_dtype, const float* w_scale,
+                                    float* y, int64_t ldy, int64_t M, int64_t N, int64_t K, uint64_t* slots,
+                                    int32_t* idx, q35_stream_t stream) {
+  using namespace q35;
+  const int chk = gemv_check(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, kEpiStore, nullptr, 0, 1);
+  if (chk != Q35_OK) return chk;
+  if (!norm_w || !slots || !idx) return Q35_EINVAL;
+  if (((uintptr_t)norm_w & 15) || (x_add && ((uintptr_t)x_add & 15)) || (x_out && ((uintptr_t)x_out & 15)) ||
+      ((uintptr_t)slots & 7) || ((uintptr_t)idx & 3))
+    return Q35_EUNSUPPORTED;
+  auto overlap = [&](const float* a) {
+    return a && x_out && a < x_out + (M - 1) * ldx + K && x_out < a + (M - 1) * ldx + K;
+  };
+  if (overlap(x) || overlap(x_add)) return Q35_EINVAL;
+  NormArgs na = {x_add, norm_w, eps, x_out, {}};
+  na.aux.amax = reinterpret_cast<unsigned long long*>(slots);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int r = gemv_dispatch<true>(x, ldx, W, w_dtype, w_scale, y, ldy, M, N, K, kEpiStore, nullptr, 0, 1, na, st);
+  if (r != Q35_OK) return r;
+  hipLaunchKernelGGL(amax_take_kernel, dim3(1), dim3(64), 0, st, reinterpret_cast<unsigned long long*>(slots),
+                     (int)M, idx);
+  return hipGetLastError() == hipSuccess ? Q35_OK : Q35_ELAUNCH;
 }
 
 extern "C" int q35_gemv_norm_conv(const float* x, const float* x_add, float* x_out, int64_t ldx,

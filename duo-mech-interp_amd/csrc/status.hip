@@ -13,4 +13,4 @@ extern "C" const char* q35_status_string(int status) {
   }
 }
 
-extern "C" int q35_abi_version(void) { return 13; }
+extern "C" int q35_abi_version(void) { return 14; }

@@ -19,6 +19,7 @@ EXPORTS = [
     "q35_gated_attn_decode", "q35_gated_attn_decode_noalloc_max_bytes", "q35_gated_attn_decode_noalloc",
     "q35_gated_attn_decode_proj", "q35_gated_attn_prefill_proj_workspace_bytes", "q35_gated_attn_prefill_proj",
     "q35_gated_attn_prefill_cached_proj_workspace_bytes", "q35_gated_attn_prefill_cached_proj",
+    "q35_gemv_norm_argmax",
     "q35_resid_add_rows", "q35_gdn_conv", "q35_gdn_decode_fused", "q35_gated_rmsnorm", "q35_attn_prep", "q35_gemv",
     "q35_swiglu_push",
     "q35_add_rmsnorm", "q35_argmax_rows", "q35_gemv_norm", "q35_gemm_q8", "q35_gemm_q8_split",
@@ -28,7 +29,7 @@ EXPORTS = [
 
 Q35_F32, Q35_BF16, Q35_I8, Q35_I8_G128 = 0, 1, 2, 3
 Q35_ESCRATCH = 5
-ABI_VERSION = 13  # the signatures below; q35_abi_version() of the loaded library must match
+ABI_VERSION = 14  # the signatures below; q35_abi_version() of the loaded library must match
 
 _lib = None
 
@@ -81,6 +82,7 @@ _SIGS = {
     "q35_gemm_q8_bf16": ([P, I64, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P, I64, I64, P], I32),
     "q35_gemv_norm": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, I32, P, I64, I64, P, I64, I64, P],
                       I32),
+    "q35_gemv_norm_argmax": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, P, P, P], I32),
     "q35_gdn_decode_sliced": ([P, I64, P, P, I64, I64, P, F32, P, I64, I64, I64, P], I32),
     "q35_gemv_norm_conv": ([P, P, P, I64, P, F32, P, I32, P, P, I64, I64, I64, I64, P, P, P, I64, I64, P], I32),
     "q35_gemv_gated_norm": ([P, I64, P, I64, P, P, F32, P, I32, P, P, I64, I64, I64, I64, I32, P], I32),

@@ -165,6 +165,8 @@ class HybridModel:
                     "rec": torch.zeros(rows, cfg.lin_v_heads, cfg.lin_dk, cfg.lin_dv, device=device)})
         # each row's next position, on the device (the decode step reads it there, so a replayed graph follows it)
         self.pos_dev = torch.zeros(rows, dtype=torch.int32, device=device)
+        # the LM head's argmax slots (q35_gemv_norm_argmax: zeros between calls)
+        self._amax_slots = torch.zeros(rows, dtype=torch.int64, device=device)
         self.graph = None
         self.step_capture, self._step_cap_idx = None, {}
         self.row_pos = [0] * rows  # host mirror of pos_dev
@@ -373,12 +375,21 @@ class HybridModel:
             hooks["resid"] = (resid, resid_mode, int(t0))
         return hooks
 
-    def _lm_head(self, xl):
-        """Final RMSNorm and the tied-embedding logits of the last positions xl [rows, H] (a GEMV for few rows)."""
+    def _lm_head(self, xl, ids_out=None):
+        """Final RMSNorm and the tied-embedding logits of the last positions xl [rows, H] (a GEMV for few rows).
+        ids_out: also each row's greedy pick (argmax of the logits) into this [rows] int32 buffer, folded into the
+        LM head's GEMV when its weights are int8 (q35_gemv_norm_argmax), else ops.argmax_rows."""
         head = "lm_head" if "lm_head" in self.W.t else "embed"  # untied checkpoints carry their own head
         wq = self.W.t.get(head + ".q")
-        return layers.linear(xl.contiguous(), self.W[head], wq, None if wq is None else self.W[head + ".s"],
-                             prenorm=(None, self.W["norm"], self.cfg.eps, None))
+        xl = xl.contiguous()
+        pre = (None, self.W["norm"], self.cfg.eps, None)
+        if (ids_out is not None and wq is not None and xl.shape[0] <= 8 and xl.shape[-1] % 256 == 0
+                and xl.dtype == torch.float32):
+            return ops.gemv_norm_argmax(xl, wq, self.W[head + ".s"], pre, self._amax_slots, idx=ids_out)[0]
+        logits = layers.linear(xl, self.W[head], wq, None if wq is None else self.W[head + ".s"], prenorm=pre)
+        if ids_out is not None:
+            ops.argmax_rows(logits, out=ids_out)
+        return logits
 
     def set_step_capture(self, capture_layers):
         """Capture the MLP activations of `capture_layers` (None: stop) at every decode step (decode_step,
@@ -414,9 +425,7 @@ class HybridModel:
             x, _ = self._layers(self.W["embed"].index_select(0, self._g_ids).unsqueeze(1), 1, cfg.layers - 1, None,
                                 True, hooks=hooks)
             self.pos_dev.add_(1)
-            logits = self._lm_head(x[:, -1])
-            ops.argmax_rows(logits, out=self._g_ids)
-            return logits
+            return self._lm_head(x[:, -1], ids_out=self._g_ids)
         side = torch.cuda.Stream(device=self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side):  # warm-up outside capture: library handles, allocator pools

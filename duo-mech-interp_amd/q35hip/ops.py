@@ -90,6 +90,8 @@ _LIB.define("add_rmsnorm_split_(Tensor(a!) x, Tensor? y, Tensor w, float eps) ->
 _LIB.define("argmax_rows_(Tensor x, Tensor(a!) idx) -> ()")
 _LIB.define("gemv_norm_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
             "Tensor? w_scale, Tensor(a!) y, int epilogue, Tensor? pushes, int T, Tensor(c!)? cap=None) -> ()")
+_LIB.define("gemv_norm_argmax_(Tensor x, Tensor? x_add, Tensor(b!)? x_out, Tensor norm_w, float eps, Tensor W, "
+            "Tensor? w_scale, Tensor(a!) y, Tensor(c!) slots, Tensor(d!) idx) -> ()")
 _LIB.define("gdn_chunk_prefill_conv_(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
             "Tensor dt_bias, int b_off, int a_off, Tensor(b!) state, int Hk, float scale) -> Tensor")
 _LIB.define("gdn_decode_sliced_(Tensor y, Tensor A_log, Tensor dt_bias, int b_off, int a_off, Tensor(a!) state, "
@@ -614,6 +616,28 @@ def _gemv_norm_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, epilogue, pushe
     check(st, "q35_gemv_norm")
 
 
+def _gemv_norm_argmax_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, slots, idx):
+    _on_gpu(x, x_add, x_out, norm_w, W, w_scale, y, slots, idx)
+    _require(x.dtype == torch.float32 and x.dim() == 2 and y.dtype == torch.float32 and y.dim() == 2,
+             "x: [M, K] fp32; y: [M, N] fp32")
+    M, K = x.shape
+    for t in (x_add, x_out):
+        _require(t is None or (t.dtype == torch.float32 and tuple(t.shape) == (M, K) and t.stride(0) == x.stride(0)
+                               and t.stride(1) == 1), "x_add / x_out: like x")
+    _require(norm_w.dtype == torch.float32 and norm_w.numel() == K and norm_w.is_contiguous(), "norm_w: [K] fp32")
+    _require(W.dim() == 2 and W.dtype in (torch.int8, torch.float32) and W.shape[1] == K, "W: [N, K] int8 or fp32")
+    N = W.shape[0]
+    _require(tuple(y.shape) == (M, N) and y.stride(1) == 1, "y: [M, N] fp32")
+    _require(slots.dtype == torch.int64 and slots.numel() == M and slots.is_contiguous(),
+             "slots: [M] int64, zeros before the first call (each call leaves them zero)")
+    _require(idx.dtype == torch.int32 and idx.numel() == M and idx.is_contiguous(), "idx: [M] int32")
+    fmt = _weight_format(W, w_scale, N, K)
+    st = _lib.lib().q35_gemv_norm_argmax(_ptr(x), _ptr(x_add), _ptr(x_out), x.stride(0), _ptr(norm_w), float(eps),
+                                         _ptr(W), fmt, _ptr(w_scale), _ptr(y), y.stride(0), M, N, K, _ptr(slots),
+                                         _ptr(idx), _stream(x))
+    check(st, "q35_gemv_norm_argmax")
+
+
 def _gemv_norm_conv_impl(x, x_add, x_out, norm_w, eps, W, w_scale, y, conv_w, conv_bias, conv_state):
     _on_gpu(x, x_add, x_out, norm_w, W, w_scale, y, conv_w, conv_bias, conv_state)
     _require(x.dtype == torch.float32 and x.dim() == 2 and y.dtype == torch.float32 and y.dim() == 2,
@@ -718,6 +742,7 @@ for _name, _impl in [("gdn_recurrent", _gdn_recurrent_impl), ("gdn_decode_step_"
                      ("add_rmsnorm_", _add_rmsnorm_impl), ("add_rmsnorm_split_", _add_rmsnorm_split_impl),
                      ("argmax_rows_", _argmax_rows_impl),
                      ("gemv_norm_", _gemv_norm_impl), ("gdn_decode_sliced_", _gdn_decode_sliced_impl),
+                     ("gemv_norm_argmax_", _gemv_norm_argmax_impl),
                      ("gdn_chunk_prefill_conv_", _gdn_chunk_prefill_conv_impl),
                      ("gemv_norm_conv_", _gemv_norm_conv_impl), ("gemv_gated_norm_", _gemv_gated_norm_impl)]:
     _LIB.impl(_name, _impl, "CUDA")
@@ -761,6 +786,7 @@ _LIB.impl("gated_attn_prefill_cached",
           "Meta")
 _LIB.impl("argmax_rows_", lambda x, idx: None, "Meta")
 _LIB.impl("gemv_norm_", lambda x, xa, xo, nw, eps, W, ws, y, e, pushes, T, cap=None: None, "Meta")
+_LIB.impl("gemv_norm_argmax_", lambda x, xa, xo, nw, eps, W, ws, y, slots, idx: None, "Meta")
 _LIB.impl("gdn_chunk_prefill_conv_", lambda y, cw, cb, cs, Al, dt, bo, ao, st, Hk, sc:
           y.new_empty(y.shape[0], y.shape[1], st.shape[1], st.shape[3]), "Meta")
 _LIB.impl("gdn_decode_sliced_", lambda y, Al, dt, bo, ao, st, sc: y.new_empty(y.shape[0], st.shape[1] * st.shape[2]),
@@ -1061,6 +1087,20 @@ def swiglu_push(gu, pushes=None, T=1, capture=None):
     """silu(gate) * up over a [..., 2 I] ([gate | up]) projection with the neuron pushes applied (the hook point of
     engine/kernels_qwen35.js:250-279); capture as for gemv."""
     return torch.ops.q35.swiglu_push(gu, pushes, int(T), capture)
+
+
+def gemv_norm_argmax(x, W, w_scale, prenorm, slots, out=None, idx=None):
+    """The store GEMV behind the RMSNorm prologue (gemv with prenorm = (x_add, norm_w, eps, x_out)) with each row's
+    argmax of the result folded in (q35_gemv_norm_argmax: the greedy pick over the LM head's logits, lowest index on
+    ties as argmax_rows). slots: [M] int64 device buffer holding zeros (each call leaves it zero). Returns (y [M, N]
+    fp32, idx [M] int32)."""
+    x_add, norm_w, eps, x_out = prenorm
+    if out is None:
+        out = torch.empty(x.shape[0], W.shape[0], dtype=torch.float32, device=x.device)
+    if idx is None:
+        idx = torch.empty(x.shape[0], dtype=torch.int32, device=x.device)
+    torch.ops.q35.gemv_norm_argmax_(x, x_add, x_out, norm_w, float(eps), W, w_scale, out, slots, idx)
+    return out, idx
 
 
 def argmax_rows(x, out=None):

@@ -39,6 +39,8 @@
  *   q35_gemv                 engine/kernels.js:57-90 `matvec` (int8 weights per 128-input group, or per row)
  *                            and, with the SwiGLU epilogue, engine/kernels_qwen35.js:250-279 `swiglu` with the
  *                            neuron pushes; HF:704-717 Qwen3_5MLP for the decode step
+ *   q35_gemv_norm_argmax     q35_gemv_norm (store) with the greedy pick of each row folded in: engine/kernels.js
+ *                            :260-283 `argmax` over the logits the LM head writes (engine/model.js:494-497)
  *   q35_gemv_norm            q35_gemv behind the layer's residual add + RMSNorm (HF:753-793, :720-734;
  *                            engine/kernels.js:226-246 `addInto` + `rmsnorm` ahead of the matvec)
  *   q35_swiglu_push          engine/kernels_qwen35.js:250-279 `swiglu` over a [gate | up] projection (prefill form)
@@ -421,6 +423,17 @@ int q35_gemv_norm(const float* x, const float* x_add, float* x_out, int64_t ldx,
                   const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy, int64_t M, int64_t N,
                   int64_t K, int epilogue, const q35_push* pushes, int64_t npush, int64_t T, float* cap,
                   int64_t ld_cap, int64_t ld_cap_row, q35_stream_t stream);
+
+/*
+ * q35_gemv_norm with the store epilogue (y = the logits, as that call writes them) and the argmax of each row of y
+ * written to idx [M] int32: the lowest index among the largest values, as q35_argmax_rows (NaN never wins; a row with
+ * no winner reports 0). The blocks fold their best (value, index) into slots [M] (uint64, 8-byte aligned) with one
+ * atomic max each, and a one-block kernel then turns the slots into indices and clears them: slots must hold zeros
+ * before the first call, and every call leaves them zero (calls sharing slots must not overlap).
+ */
+int q35_gemv_norm_argmax(const float* x, const float* x_add, float* x_out, int64_t ldx, const float* norm_w,
+                         float eps, const void* W, int w_dtype, const float* w_scale, float* y, int64_t ldy,
+                         int64_t M, int64_t N, int64_t K, uint64_t* slots, int32_t* idx, q35_stream_t stream);
 
 /*
  * q35_gemv_norm (store epilogue) whose outputs 0 .. conv_channels - 1 go through the GDN layer's causal conv + SiLU

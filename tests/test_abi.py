@@ -39,7 +39,7 @@ def test_library_built_and_exports_every_declared_symbol():
 
 def test_status_strings_and_version():
     L = q35hip.lib()
-    assert L.q35_abi_version() == 13
+    assert L.q35_abi_version() == 14
     assert L.q35_status_string(0) == b"ok"
     assert b"invalid" in L.q35_status_string(1)
 
@@ -273,6 +273,27 @@ def test_prefill_from_projection_rejects_without_launching():
     with pytest.raises(Exception, match="no CPU|HIP device"):
         q35hip.ops.gated_attention_prefill_proj(y, torch.zeros(256), torch.zeros(256), kc, kc.clone(),
                                                 torch.zeros(64, 32), torch.zeros(64, 32), num_heads=8)
+
+
+def test_gemv_norm_argmax_rejects_without_launching():
+    """q35_gemv_norm_argmax refuses bad arguments before any HIP call (3 rows, N 151936, K 1024, int8 weights with
+    group scales), and its torch op has no CPU path."""
+    L = q35hip.lib()
+    fake = 0x1000
+
+    def call(slots=fake, idx=fake, M=3, K=1024, nw=fake):
+        return L.q35_gemv_norm_argmax(fake, None, None, K, nw, 1e-6, fake, 3, fake, fake, 151936, M, 151936, K, slots,
+                                      idx, None)
+    assert call(slots=None) == 1             # no argmax slots
+    assert call(idx=None) == 1               # no index output
+    assert call(nw=None) == 1                # no norm weight
+    assert call(slots=fake + 4) == 2         # slots not 8-byte aligned
+    assert call(M=9) == 2                    # more rows than the GEMV takes
+    assert call(K=1000) == 2                 # K not a multiple of 256
+    x = torch.zeros(3, 1024)
+    with pytest.raises(Exception, match="no CPU|HIP device"):
+        q35hip.ops.gemv_norm_argmax(x, torch.zeros(8, 1024, dtype=torch.int8), torch.ones(8, 8),
+                                    (None, torch.zeros(1024), 1e-6, None), torch.zeros(3, dtype=torch.int64))
 
 
 def test_prefill_over_cache_from_projection_rejects_without_launching():

@@ -97,6 +97,44 @@ def test_argmax_rows_matches_torch(rows, n):
     assert torch.equal(got2.cpu().long(), x.argmax(-1))
 
 
+@pytest.mark.parametrize("M,N,K,fmt", [(3, 151936, 1024, "g128"), (1, 40008, 1024, "g128"), (2, 5000, 1024, "row"),
+                                       (8, 20000, 2048, "g128")])
+def test_gemv_norm_argmax_matches_torch(M, N, K, fmt):
+    """The LM head's GEMV with the greedy pick folded in (q35_gemv_norm_argmax): the logits bitwise those of the plain
+    norm GEMV, each row's index torch.argmax of them (two identical weight rows planted as the largest logit of row 0:
+    the lower index wins), and the slots left zero for the next call (second call on other inputs). The shapes run the
+    block tile loop (N 151936, 40008, 20000) and one tile per block (N 5000)."""
+    dev = device()
+    g = torch.Generator().manual_seed(N + M)
+    Wf = torch.randn(N, K, generator=g) * 0.02
+    x = torch.randn(M, K, generator=g)
+    nw = torch.randn(K, generator=g) * 0.1
+    h = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + nw)
+    lo, hi = N // 7, N - 3
+    Wf[lo] = h[0] / h[0].norm() * 0.5   # the largest logit of row 0, twice
+    Wf[hi] = Wf[lo]
+    if fmt == "g128":
+        W, s = omlp.q8_quantize(Wf)
+    else:
+        amax = Wf.abs().amax(1).clamp_min(1e-12)
+        s = amax / 127
+        W = torch.round(Wf / s[:, None]).clamp(-127, 127).to(torch.int8)
+    announce(f"gemv norm argmax M{M} N{N} K{K} {fmt}")
+    Wd, sd, nwd = W.to(dev), s.to(dev), nw.to(dev)
+    slots = torch.zeros(M, dtype=torch.int64, device=dev)
+    for call in range(2):
+        xc = x if call == 0 else torch.randn(M, K, generator=g)
+        xd = xc.to(dev)
+        y, idx = ops.gemv_norm_argmax(xd, Wd, sd, (None, nwd, 1e-6, None), slots)
+        plain = ops.gemv(xd, Wd, sd, prenorm=(None, nwd, 1e-6, None))
+        torch.cuda.synchronize()
+        assert torch.equal(y.cpu(), plain.cpu())
+        assert torch.equal(idx.cpu().long(), y.cpu().argmax(-1))
+        assert int(slots.abs().sum()) == 0
+        if call == 0:
+            assert int(idx[0]) == lo
+
+
 @pytest.mark.parametrize("epilogue", ["store", "add", "swiglu"])
 @pytest.mark.parametrize("with_add,with_out", [(False, False), (True, True), (True, False)])
 def test_gemv_with_fused_residual_add_and_rmsnorm(epilogue, with_add, with_out):
