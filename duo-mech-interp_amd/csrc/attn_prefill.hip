@@ -9,9 +9,10 @@
 // Kernel 1, attn_kv_prep_kernel: K rotated once ([B, Hkv, Tp, D] bf16, keys padded to a multiple of 64 with zeros)
 // and V transposed once ([B, Hkv, D, Tp] bf16) into the workspace, so that the main loop stages its tiles with
 // plain global -> LDS copies. From the fused projection output (q35_gated_attn_prefill_proj) it is also the front
-// end: q and k normalised and rotated, k and v appended to the KV cache, q written rotated for the main kernel. Inside each group of 16 keys, V^T stores keys in the order 0-3, 8-11, 4-7, 12-15
-// (bits 2 and 3 of the key index swapped): that is the key order in which an MFMA accumulator tile of scores is fed
-// back as a B operand, so every A fragment of V^T is one 16-byte read.
+// end: q and k normalised and rotated, k and v appended to the KV cache, q written rotated for the main kernel.
+// Inside each group of 16 keys, V^T stores keys in the order 0-3, 8-11, 4-7, 12-15 (bits 2 and 3 of the key index
+// swapped): that is the key order in which an MFMA accumulator tile of scores is fed back as a B operand, so every
+// A fragment of V^T is one 16-byte read.
 // Kernel 2, attn_prefill_kernel: one block of 4 waves per (32-query block, group of up to 4 query heads sharing a kv
 // head, batch row); wave w owns query head w of the group, so every K/V tile in LDS serves up to 4 heads. Query
 // blocks are issued longest (latest) first. Per 64-key tile each wave computes S^T = K Q^T with 32 x 32 x 16 bf16
@@ -872,8 +873,8 @@ __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __
       gf[j] = *reinterpret_cast<const f32x4*>(static_cast<const float*>(gate) + ((size_t)b * T + tq) * gate_ld +
                                               (size_t)h * 2 * kPD + d);
     else
-      gr[j] = *reinterpret_cast<const u32x2*>(static_cast<const __bf16*>(gate) + ((size_t)b * T + tq) * (size_t)Hq * kPD +
-                                              (size_t)h * kPD + d);
+      gr[j] = *reinterpret_cast<const u32x2*>(static_cast<const __bf16*>(gate) +
+                                              ((size_t)b * T + tq) * (size_t)Hq * kPD + (size_t)h * kPD + d);
   }
   // every chunk of thread t has lane l = t & 63 (256 j is a multiple of 64)
   const int l = tid & 63;

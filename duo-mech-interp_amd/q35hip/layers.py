@@ -57,8 +57,9 @@ def gated_deltanet_layer(x, p, conv_state, rec_state, head_scale=None, *, num_k_
     kernels, engine/kernels_qwen35.js:127-247). x: [B, T, H] fp32 (the input-normed residual). A call with T == 1
     is one recurrent decode step (HF:505-517). T > 1 runs from rec_state either the chunked prefill (HF:518-530;
     prefill="chunk": products at the precision of x, fp32 for fp32 x) or the token-serial fp32 recurrence
-    (prefill="recurrent": as the WGSL engine runs prefill token by token, engine/kernels_qwen35.js:183-247). Both states are updated in place. head_scale: optional [Hv] per-head output
-    scale applied after the gated norm (engine/kernels_qwen35.js:243). num_k_heads / head_k_dim default to the
+    (prefill="recurrent": as the WGSL engine runs prefill token by token, engine/kernels_qwen35.js:183-247). Both
+    states are updated in place. head_scale: optional [Hv] per-head output scale applied after the gated norm
+    (engine/kernels_qwen35.js:243). num_k_heads / head_k_dim default to the
     value heads / value head dim (the Qwen3.5 text models use Hk = Hv and dk = dv). prenorm: see linear() (x is then
     the residual and the layer's input norm runs inside the input projection). Returns y [B, T, H], or with
     residual [B, T, H] given, residual + y computed in place by the output projection (then returned). For T > 1,
@@ -218,10 +219,11 @@ def gated_attention_layer(x, p, k_cache, v_cache, pos, *, rope_theta=1e7, partia
     cache positions 0..pos+t (engine/kernels_qwen35.js:90). T > 1 at the int position 0 runs the flash prefill over
     the call's own tokens (for an fp32 y with the front end in its pre-pass, q35_gated_attn_prefill_proj); T > 1 at
     any other position (or a device pos) the same kernel over the cache (the caches' max_len must then be a multiple
-    of 64; for an fp32 y with the front end in its pre-pass, q35_gated_attn_prefill_cached_proj); T == 1 the split-K decode over cache positions 0..pos (cache_len: optional [B] int32 per-row lengths,
-    default pos + 1; without it the q / k norms, RoPE and the cache append run inside the decode kernels,
-    q35_gated_attn_decode_proj, instead of a front-end launch). prenorm: see linear(). For T > 1, x may be the int32
-    words of split activations (see gated_deltanet_layer). Returns y [B, T, H], or with residual [B, T, H] given,
+    of 64; for an fp32 y with the front end in its pre-pass, q35_gated_attn_prefill_cached_proj); T == 1 the split-K
+    decode over cache positions 0..pos (cache_len: optional [B] int32 per-row lengths, default pos + 1; without it
+    the q / k norms, RoPE and the cache append run inside the decode kernels, q35_gated_attn_decode_proj, instead of
+    a front-end launch). prenorm: see linear(). For T > 1, x may be the int32 words of split activations (see
+    gated_deltanet_layer). Returns y [B, T, H], or with residual [B, T, H] given,
     residual + y computed in place by o_proj (then returned). fixed_order: see linear()."""
     B, T, _ = x.shape
     D = p["q_norm"].numel()

@@ -70,7 +70,8 @@ _LIB.define("gated_attn_decode_proj(Tensor y, Tensor q_norm_w, Tensor k_norm_w, 
 _LIB.define("gated_attn_prefill_proj(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, Tensor(a!) k_cache, "
             "Tensor(b!) v_cache, int pos0, Tensor cos, Tensor sin, int Hq, float scale) -> Tensor")
 _LIB.define("gated_attn_prefill_cached_proj(Tensor y, Tensor q_norm_w, Tensor k_norm_w, float eps, "
-            "Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor pos, Tensor cos, Tensor sin, int Hq, float scale) -> Tensor")
+            "Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor pos, Tensor cos, Tensor sin, int Hq, "
+            "float scale) -> Tensor")
 _LIB.define("resid_add_rows_(Tensor(a!) x, Tensor vecs, Tensor? vec_of_row) -> ()")
 _LIB.define("gdn_conv(Tensor y, Tensor conv_w, Tensor? conv_bias, Tensor(a!) conv_state, Tensor A_log, "
             "Tensor dt_bias, int b_off, int a_off, int Hk, int dk, int Hv, int dv, bool bf16_out) "
