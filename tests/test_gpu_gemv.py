@@ -98,12 +98,12 @@ def test_argmax_rows_matches_torch(rows, n):
 
 
 @pytest.mark.parametrize("M,N,K,fmt", [(3, 151936, 1024, "g128"), (1, 40008, 1024, "g128"), (2, 5000, 1024, "row"),
-                                       (8, 20000, 2048, "g128")])
+                                       (8, 20000, 2048, "g128"), (2, 20000, 1024, "f32")])
 def test_gemv_norm_argmax_matches_torch(M, N, K, fmt):
     """The LM head's GEMV with the greedy pick folded in (q35_gemv_norm_argmax): the logits bitwise those of the plain
     norm GEMV, each row's index torch.argmax of them (two identical weight rows planted as the largest logit of row 0:
     the lower index wins), and the slots left zero for the next call (second call on other inputs). The shapes run the
-    block tile loop (N 151936, 40008, 20000) and one tile per block (N 5000)."""
+    block tile loop (N 151936, 40008, 20000; int8 and fp32 weights) and one tile per block (N 5000)."""
     dev = device()
     g = torch.Generator().manual_seed(N + M)
     Wf = torch.randn(N, K, generator=g) * 0.02
@@ -115,12 +115,14 @@ def test_gemv_norm_argmax_matches_torch(M, N, K, fmt):
     Wf[hi] = Wf[lo]
     if fmt == "g128":
         W, s = omlp.q8_quantize(Wf)
+    elif fmt == "f32":
+        W, s = Wf, None
     else:
         amax = Wf.abs().amax(1).clamp_min(1e-12)
         s = amax / 127
         W = torch.round(Wf / s[:, None]).clamp(-127, 127).to(torch.int8)
     announce(f"gemv norm argmax M{M} N{N} K{K} {fmt}")
-    Wd, sd, nwd = W.to(dev), s.to(dev), nw.to(dev)
+    Wd, sd, nwd = W.to(dev), None if s is None else s.to(dev), nw.to(dev)
     slots = torch.zeros(M, dtype=torch.int64, device=dev)
     for call in range(2):
         xc = x if call == 0 else torch.randn(M, K, generator=g)
