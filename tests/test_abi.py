@@ -37,6 +37,35 @@ def test_library_built_and_exports_every_declared_symbol():
     assert sorted(_lib.EXPORTS) == declared_functions()
 
 
+def _c_kind(decl):
+    """ctypes kind of one C declaration of the header (a parameter with its name, or a return type): P (any pointer
+    or the stream handle), I64, I32, F32, SZ, or STR for a returned C string."""
+    d = " ".join(decl.replace("const ", "").split())
+    if d.startswith("char") and "*" in d:
+        return "STR"
+    if "*" in d or d.startswith("q35_stream_t"):
+        return "P"
+    return {"int64_t": "I64", "int": "I32", "float": "F32", "size_t": "SZ"}[d.split()[0]]
+
+
+def test_bindings_match_the_header_prototypes():
+    """Every prototype of include/q35hip.h has the parameter count and kinds, and the return kind, that the ctypes
+    table of q35hip._lib binds (a wrong or missing argtype would pass garbage without any error)."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    protos = re.findall(r"([A-Za-z_][\w\s\*]*?)\b(q35_[a-z0-9_]+)\s*\(([^()]*)\)\s*;", text)
+    kinds = {_lib.P: "P", _lib.I64: "I64", _lib.I32: "I32", _lib.F32: "F32", _lib.SZ: "SZ", ctypes.c_char_p: "STR"}
+    seen = set()
+    for ret, name, params in protos:
+        seen.add(name)
+        args, res = _lib._SIGS[name]
+        plist = [] if params.strip() in ("", "void") else [x.strip() for x in params.split(",")]
+        want = [_c_kind(x) for x in plist]
+        got = [kinds[a] for a in args]
+        assert got == want, f"{name}: ctypes {got} against the header's {want}"
+        assert kinds[res] == _c_kind(ret.strip().split("\n")[-1]), f"{name}: return kind"
+    assert seen == set(_lib._SIGS), sorted(seen ^ set(_lib._SIGS))
+
+
 def test_status_strings_and_version():
     L = q35hip.lib()
     assert L.q35_abi_version() == 14
